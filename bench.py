@@ -1,0 +1,245 @@
+"""Benchmark of the hot path on one MI355X.
+
+Headline (BASELINE.json metric, config 2): fp32 GEMM C = A @ B at
+M = N = K = 4096, NN layout, A/B ~ N(0,1), inputs resident in HBM. A "step" is
+one GEMM. Prints ONE JSON line:
+
+  value        whole-job TFLOP/s over the timed K steps (2*M*N*K per step)
+  roofline     the GEMM kernel's algorithmic TFLOP/s from HIP-event launch times
+               on the backend's stream, against the fp32 MFMA peak (157.3 TFLOP/s)
+  cpu_baseline the CPU oracle (the C restatement of vkML's CPU matmul) on a row
+               sample of the same problem, on this host's cores
+  secondary    the other hot-path kernels at their BASELINE shapes (GB/s against
+               8 TB/s for bandwidth kernels; bandwidth cases rotate buffers larger
+               than the 256 MB Infinity Cache)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary]
+       [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+METRIC = "fp32 GEMM TFLOP/s @4096³ (% fp32 MFMA peak); im2col/softmax GB/s; steps/s"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--m", type=int, default=4096)
+    p.add_argument("--n", type=int, default=4096)
+    p.add_argument("--k", type=int, default=4096)
+    p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="target CPU work for the baseline sample")
+    return p.parse_args()
+
+
+class Timer:
+    """HIP events on the backend's own stream (torch wraps the handle)."""
+
+    def __init__(self, stream_handle: int):
+        import torch
+
+        self.torch = torch
+        self.stream = torch.cuda.ExternalStream(stream_handle)
+
+    def event(self):
+        ev = self.torch.cuda.Event(enable_timing=True)
+        ev.record(self.stream)
+        return ev
+
+
+def time_launches(fn, timer: Timer, reps: int, warmup: int = 3):
+    """Per-launch durations (ms) from event pairs around each call."""
+    for _ in range(warmup):
+        fn(0)
+    pairs = []
+    for i in range(reps):
+        s = timer.event()
+        fn(i)
+        e = timer.event()
+        pairs.append((s, e))
+    pairs[-1][1].synchronize()
+    return [s.elapsed_time(e) for s, e in pairs]
+
+
+def gemm_headline(args, hip, ops, timer):
+    from vkml_amd.device import DeviceArray
+
+    m, n, k = args.m, args.n, args.k
+    rng = np.random.default_rng(20260726)
+    a = DeviceArray.from_numpy(rng.standard_normal((m, k), dtype=np.float32))
+    b = DeviceArray.from_numpy(rng.standard_normal((k, n), dtype=np.float32))
+    c = DeviceArray((m, n), np.float32)
+    for _ in range(args.warmup):
+        ops.matmul(a, b, out=c)
+    hip.synchronize()
+    events = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        s = timer.event()
+        ops.matmul(a, b, out=c)
+        e = timer.event()
+        events.append((s, e))
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [s.elapsed_time(e) for s, e in events]
+    flop = 2.0 * m * n * k
+    value = flop * args.steps / wall / 1e12
+    avg_ms = float(np.mean(launch_ms))
+    achieved = flop / (avg_ms * 1e-3) / 1e12
+    return value, wall * 1e3 / args.steps, avg_ms, achieved, float(np.min(launch_ms))
+
+
+def cpu_baseline(args):
+    import oracle as O
+
+    m, n, k = args.m, args.n, args.k
+    threads = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(1)
+    b = rng.standard_normal((k, n), dtype=np.float32)
+    rows = 8
+    a = rng.standard_normal((rows, k), dtype=np.float32)
+    t0 = time.perf_counter()
+    O.matmul(a, b, threads=threads)
+    probe = time.perf_counter() - t0
+    rows = int(min(m, max(8, rows * args.cpu_seconds / max(probe, 1e-3))))
+    rows = max(threads, rows - rows % threads)
+    a = rng.standard_normal((rows, k), dtype=np.float32)
+    t0 = time.perf_counter()
+    O.matmul(a, b, threads=threads)
+    dt = time.perf_counter() - t0
+    tflops = 2.0 * rows * n * k / dt / 1e12
+    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle matmul (C restatement of reference kernels_matmul.cpp:34-87, "
+                      f"pairwise K-sum, -O2 -ffp-contract=off) on {rows} of {m} rows of the "
+                      f"{m}x{n}x{k} problem, {threads} threads over outputs, {dt:.1f} s"}
+
+
+def secondary(hip, ops, timer):
+    """The other hot-path kernels at BASELINE shapes; median per-launch time."""
+    from vkml_amd.device import DeviceArray
+
+    rng = np.random.default_rng(7)
+    out = {}
+
+    def rotate(shape, count, gen=lambda s: rng.standard_normal(s, dtype=np.float32)):
+        return [DeviceArray.from_numpy(gen(shape)) for _ in range(count)]
+
+    def med(ms):
+        return float(np.median(ms))
+
+    # GEMM variants (compute-bound: no rotation)
+    for name, (m, n, k), lay in [("gemm_nt_4096", (4096, 4096, 4096), "nt"),
+                                 ("gemm_tn_4096", (4096, 4096, 4096), "tn"),
+                                 ("gemm_8192x1024x4096", (8192, 1024, 4096), "nn"),
+                                 ("splitk_256x256x65536", (256, 256, 65536), "nn"),
+                                 ("wgrad_128x784x16384", (128, 784, 16384), "nn")]:
+        a = DeviceArray.from_numpy(rng.standard_normal((m, k) if lay[0] == "n" else (k, m),
+                                                       dtype=np.float32))
+        b = DeviceArray.from_numpy(rng.standard_normal((k, n) if lay[1] == "n" else (n, k),
+                                                       dtype=np.float32))
+        av = a if lay[0] == "n" else a.T
+        bv = b if lay[1] == "n" else b.T
+        ms = med(time_launches(lambda i: ops.matmul(av, bv), timer, 20))
+        splits, _ = ops.gemm_plan(1, m, n, k)
+        out[name] = {"ms": ms, "tflops": 2.0 * m * n * k / ms / 1e9,
+                     "frac_of_peak": 2.0 * m * n * k / ms / 1e9 / MFMA_FP32_PEAK_TFLOPS,
+                     "splits": splits}
+
+    # GEMV 4096x4096 . 4096 (bandwidth): rotate 8 matrices (512 MB)
+    mats = rotate((4096, 4096), 8)
+    x = DeviceArray.from_numpy(rng.standard_normal(4096, dtype=np.float32))
+    ms = med(time_launches(lambda i: ops.gemv(mats[i % 8], x), timer, 24))
+    byt = 4096 * 4096 * 4 + 4096 * 4 * 2
+    out["gemv_4096"] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+    del mats
+
+    # im2col / col2im conv2 [128,64,32,32] <-> [128,576,1024]
+    imgs = rotate((128, 64, 32, 32), 2)
+    cols = [ops.im2col(im, 3, 1, 1) for im in imgs]
+    hip.synchronize()
+    byt = 128 * 64 * 32 * 32 * 4 + 128 * 576 * 1024 * 4
+    ms = med(time_launches(lambda i: ops.im2col(imgs[i % 2], 3, 1, 1), timer, 20))
+    out["im2col_conv2"] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+    ms = med(time_launches(lambda i: ops.col2im(cols[i % 2], (32, 32), 3, 1, 1), timer, 20))
+    out["col2im_conv2"] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+    del imgs, cols
+
+    # softmax (read + write once), rotate past the MALL
+    for shape, count in [((4096, 1000), 20), ((256, 32768), 10)]:
+        xs = rotate(shape, count, lambda s: rng.standard_normal(s, dtype=np.float32) * 2)
+        byt = 2 * shape[0] * shape[1] * 4
+        ms = med(time_launches(lambda i: ops.softmax(xs[i % count], -1), timer, 40))
+        out[f"softmax_{shape[0]}x{shape[1]}"] = {"ms": ms, "gbs": byt / ms / 1e6,
+                                                 "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+        del xs
+
+    # sum / max over the last axis of [8192, 4096] (134 MB read), 4 buffers
+    xs = rotate((8192, 4096), 4)
+    byt = 8192 * 4096 * 4 + 8192 * 4
+    for name, fn in [("sum_8192x4096", ops.sum), ("max_8192x4096", ops.amax)]:
+        ms = med(time_launches(lambda i: fn(xs[i % 4], [1]), timer, 20))
+        out[name] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+    del xs
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not implemented)"}))
+        sys.exit(2)
+    from vkml_amd import ops
+    from vkml_amd.device import backend
+
+    hip = backend()
+    timer = Timer(hip.stream_handle())
+    value, ms_step, avg_ms, achieved, min_ms = gemm_headline(args, hip, ops, timer)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"gemm_nn_{args.m}x{args.n}x{args.k}_fp32", "m": args.m,
+                   "n": args.n, "k": args.k, "layout": "NN", "parallelism": "none"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "gemm_mfma_kernel<128,128,32,64,64>",
+                     "avg_launch_ms": round(avg_ms, 4), "min_launch_ms": round(min_ms, 4)},
+    }
+    if not args.no_secondary:
+        result["secondary"] = secondary(hip, ops, timer)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

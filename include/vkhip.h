@@ -1,0 +1,300 @@
+/*
+ * vkhip.h -- C ABI of the MI355X (gfx950) device backend for vkML's hot path.
+ *
+ * This is the drop-in boundary. In the reference, every graph flush reaches a
+ * device through one virtual call, `vkml::Backend::compute(span<Node* const>)`
+ * (reference: include/vkml/backend/api/backend.h:49-125), made by
+ * `dispatch::realize` (src/dispatch/executor.cpp:132). The Vulkan implementation
+ * of that call is `VulkanBackend::compute` (src/backend/vulkan/vulkan_backend.cpp:1189-2718).
+ * This header replaces that implementation with plain C entry points:
+ *
+ *   - device/memory/copy/sync entry points mirror the rest of `Backend`
+ *     (allocator(), copy_from_host, copy_to_host, copy_device_to_device,
+ *     synchronize, capabilities);
+ *   - `vkhip_compute` takes an ordered span of node records -- a C struct
+ *     rendering of `vkml::Node` (include/vkml/graph/node.h:69-157) -- and
+ *     enqueues one launch sequence on the backend's HIP stream;
+ *   - one launch entry point per op family (gemm, split-K reduce, gemv,
+ *     im2col, col2im, softmax, reduce, max-pool, elementwise) takes device
+ *     pointers plus rank-4 operand descriptors, as the reference's push-constant
+ *     blocks do (vulkan_backend.cpp:87-115 `GpuOperand`, :472-483 `GemmPush`).
+ *
+ * Conventions
+ *   - No exceptions cross this ABI. Every entry point returns an int status
+ *     (VKHIP_OK == 0); `vkhip_last_error()` gives the message of the last
+ *     failure on the calling thread. The C++ wrapper maps the codes back to
+ *     vkML's exception types (error.h:26-68).
+ *   - All pointers are device addresses unless named `host_*`.
+ *   - Work is stream-ordered and MAY RETURN BEFORE COMPLETION, exactly as the
+ *     reference contract allows (backend.h:72-79). Host reads synchronise.
+ *   - Strides are in ELEMENTS, extents are right-aligned to rank 4 and padded
+ *     with 1 (reference to_gpu_operand, vulkan_backend.cpp:99-115). A stride of
+ *     0 is a broadcast axis.
+ */
+#ifndef VKHIP_H
+#define VKHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+enum vkhip_status {
+    VKHIP_OK = 0,
+    VKHIP_ERR_DEVICE = 1,        /* HIP runtime failure      -> vkml::DeviceError */
+    VKHIP_ERR_UNSUPPORTED = 2,   /* op/dtype/layout not here -> vkml::NotImplementedError */
+    VKHIP_ERR_INVALID = 3,       /* bad argument / shape     -> vkml::InternalError */
+    VKHIP_ERR_OOM = 4,           /* allocation failed        -> vkml::OutOfMemoryError */
+    VKHIP_ERR_NOT_INITIALISED = 5
+};
+
+/* ---- dtypes: same numbering as vkml::DType (include/vkml/core/dtype.h:17-23) */
+enum vkhip_dtype {
+    VKHIP_F32 = 0,
+    VKHIP_F16 = 1, /* storage-only in the reference; not supported here */
+    VKHIP_I32 = 2,
+    VKHIP_I64 = 3,
+    VKHIP_BOOL = 4 /* one byte per element, 0 or 1 */
+};
+
+/* ---- operand descriptor (reference GpuOperand, vulkan_backend.cpp:87-115) */
+typedef struct vkhip_operand {
+    uint32_t ne[4]; /* extents, right-aligned, padded with 1 */
+    int64_t nb[4];  /* strides in elements; 0 = broadcast */
+} vkhip_operand;
+
+/* ---- op params: byte-compatible with the reference's structs ----------- */
+typedef struct vkhip_unfold { /* vkml::UnfoldParams, include/vkml/graph/op.h:300-311 */
+    int32_t kernel_h, kernel_w;
+    int32_t stride_h, stride_w;
+    int32_t pad_h, pad_w;
+    int32_t dilation_h, dilation_w;
+    int32_t image_h, image_w;
+} vkhip_unfold;
+
+/* ---- reduce op ids: same order as the reference shader's op_id
+ *      (vulkan_backend.cpp:1863-1871) */
+enum vkhip_reduce_op {
+    VKHIP_REDUCE_SUM = 0,
+    VKHIP_REDUCE_MEAN = 1,
+    VKHIP_REDUCE_MAX = 2,
+    VKHIP_REDUCE_MIN = 3,
+    VKHIP_REDUCE_ARGMAX = 4,
+    VKHIP_REDUCE_ARGMIN = 5
+};
+
+/* ---- node ops handled by vkhip_compute: the hot-path and support subset of
+ *      vkml::OpKind (include/vkml/graph/op.h:30-139), numbered with OpKind's
+ *      own ordinals so a host passes `static_cast<int>(node.op)` unchanged. */
+enum vkhip_op {
+    VKHIP_OP_FULL = 2,
+    VKHIP_OP_ARANGE = 3,
+    VKHIP_OP_CONTIGUOUS = 11,
+    VKHIP_OP_CAST = 12,
+    VKHIP_OP_ADD = 14,
+    VKHIP_OP_SUB = 15,
+    VKHIP_OP_MUL = 16,
+    VKHIP_OP_SCALED_ADD = 17,
+    VKHIP_OP_DIV = 18,
+    VKHIP_OP_MAXIMUM = 20,
+    VKHIP_OP_MINIMUM = 21,
+    VKHIP_OP_EQUAL = 22,
+    VKHIP_OP_LESS = 23,
+    VKHIP_OP_GREATER = 24,
+    VKHIP_OP_LESS_EQUAL = 25,
+    VKHIP_OP_GREATER_EQUAL = 26,
+    VKHIP_OP_NOT_EQUAL = 27,
+    VKHIP_OP_NEG = 28,
+    VKHIP_OP_EXP = 35,
+    VKHIP_OP_LOG = 36,
+    VKHIP_OP_RELU = 43,
+    VKHIP_OP_SUM = 47,
+    VKHIP_OP_MEAN = 48,
+    VKHIP_OP_MAX = 49,
+    VKHIP_OP_MIN = 50,
+    VKHIP_OP_ARGMAX = 52,
+    VKHIP_OP_ARGMIN = 53,
+    VKHIP_OP_MATMUL = 54,
+    VKHIP_OP_SOFTMAX = 55,
+    VKHIP_OP_LOG_SOFTMAX = 56,
+    VKHIP_OP_IM2COL = 57,
+    VKHIP_OP_COL2IM = 58,
+    VKHIP_OP_MAX_POOL2D = 59,
+    VKHIP_OP_MAX_POOL2D_BACKWARD = 60,
+    VKHIP_OP_WHERE = 64
+};
+
+/* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */
+typedef struct vkhip_tensor {
+    void* data;      /* device address of element 0 (Node::data()) */
+    int32_t dtype;   /* vkhip_dtype */
+    int32_t ndim;    /* 0..4 */
+    int64_t ne[4];   /* extents, first ndim used (Shape::dim) */
+    int64_t nb[4];   /* strides in ELEMENTS, first ndim used (Shape::stride / itemsize) */
+} vkhip_tensor;
+
+/* ---- one node of a flush (vkml::Node, node.h:69-157) -------------------- */
+typedef struct vkhip_node {
+    int32_t op;            /* vkhip_op */
+    int32_t n_src;         /* 0..3 */
+    vkhip_tensor out;      /* bound, contiguous */
+    vkhip_tensor src[3];   /* realised sources; views already resolved to strides */
+    uint8_t params[64];    /* vkml::OpParams::raw (op.h:199-221), same payload layout */
+} vkhip_node;
+
+/* ---- device description (vkml::DeviceCapabilities, capabilities.h:23-119) */
+typedef struct vkhip_caps {
+    char name[64];
+    int32_t device_index;
+    int32_t compute_units;        /* split-K and reduce planning use it */
+    int32_t wavefront_size;       /* 64 on CDNA */
+    int32_t max_threads_per_block;
+    int64_t max_shared_memory;    /* LDS bytes per workgroup */
+    int64_t total_memory;
+    int32_t global_float_atomics; /* present on gfx950, deliberately unused */
+    int32_t asynchronous;         /* 1: compute() returns before completion */
+} vkhip_caps;
+
+/* ---- one device-to-device copy (vkml::BufferCopy, backend.h:18-24) ------ */
+typedef struct vkhip_copy {
+    void* dst;
+    const void* src;
+    size_t nbytes;
+} vkhip_copy;
+
+/* ---- GEMM selection knobs: the reference's VKML_GEMM_* switches
+ *      (vulkan_backend.cpp:536-561, 2160-2250) as explicit arguments ------- */
+enum vkhip_gemm_kernel {
+    VKHIP_GEMM_AUTO = 0,   /* MFMA tiles, split-K / GEMV by the planner */
+    VKHIP_GEMM_MFMA = 1,   /* MFMA tiles, never GEMV */
+    VKHIP_GEMM_GEMV = 2    /* force the GEMV path (N == 1 or M == 1 only) */
+};
+typedef struct vkhip_gemm_opts {
+    int32_t kernel;        /* vkhip_gemm_kernel */
+    int32_t split_k;       /* 0 = AUTO planner, 1 = OFF, >1 = forced partition request */
+} vkhip_gemm_opts;
+
+/* ======================================================================== */
+/* Backend lifecycle / description  (Backend::name/device/capabilities)     */
+/* ======================================================================== */
+
+/* Binds the calling process to GPU `device` and creates the backend stream.
+ * Idempotent for the same device. */
+int vkhip_init(int device);
+/* Releases the stream and the backend's internal workspaces. */
+int vkhip_shutdown(void);
+/* Message of the last failure on this thread ("" if none). */
+const char* vkhip_last_error(void);
+int vkhip_caps_get(vkhip_caps* out);
+/* Makes the backend enqueue on `stream` (a hipStream_t; NULL = its own).
+ * Lets a host that owns the stream (e.g. PyTorch) share stream order. */
+int vkhip_set_stream(void* stream);
+void* vkhip_get_stream(void);
+
+/* ======================================================================== */
+/* Memory (Backend::allocator, copies, synchronize)                          */
+/* ======================================================================== */
+int vkhip_alloc(size_t nbytes, void** out_ptr);
+/* Stream-ordered: memory in use by enqueued work is not reused early
+ * (reference retirement queue, vulkan_backend.cpp:921-984). */
+int vkhip_free(void* ptr);
+int vkhip_copy_from_host(void* dst, const void* host_src, size_t nbytes);
+int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes); /* synchronises */
+/* One unit of work for several disjoint copies (backend.h:83-108). */
+int vkhip_copy_device_to_device(const vkhip_copy* copies, size_t n);
+int vkhip_synchronize(void);
+
+/* ======================================================================== */
+/* The Backend::compute boundary                                             */
+/* ======================================================================== */
+/* 1 if `node` is supported (op, dtype, rank, layout), else 0
+ * (VulkanBackend::supports, vulkan_backend.cpp:1012-1187). */
+int vkhip_supports(const vkhip_node* node);
+/* Enqueues `n` nodes in order on the backend stream (backend.h:72-79). */
+int vkhip_compute(const vkhip_node* nodes, size_t n);
+
+/* ======================================================================== */
+/* Per-op-family launch entry points (what compute() dispatches to)          */
+/* ======================================================================== */
+
+/* C[b0,b1,M,N] (contiguous) = A[b0,b1,M,K] @ B[b0,b1,K,N]; any strides
+ * (NN / NT / TN / batch-broadcast). fp32 in, fp32 MFMA accumulate.
+ * Reference: Matmul case, vulkan_backend.cpp:2056-2657; CPU oracle
+ * kernels_matmul.cpp:34-87. `opts` may be NULL (AUTO). */
+int vkhip_gemm(const float* a, const vkhip_operand* a_desc,
+               const float* b, const vkhip_operand* b_desc,
+               float* c, const vkhip_gemm_opts* opts);
+
+/* The split-K plan the AUTO path would use for this problem
+ * (reference plan_split_k, vulkan_backend.cpp:596-647). Writes splits (1 =
+ * no split) and chunk (K-tiles per partition, a power of two). */
+int vkhip_gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                    int32_t split_request, uint32_t* out_splits, uint32_t* out_chunk);
+
+/* dst[i] = carry-stack fold of ws[s*ne + i], s = 0..splits-1
+ * (reference gemm_split_k_reduce.comp:48-85). Deterministic, bit-stable. */
+int vkhip_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits);
+
+/* y[M] = A[M,K] @ x[K] with strided A (row stride lda, unit inner stride
+ * required) -- the N == 1 matmul (reference gemv.comp:105-201). Products are
+ * rounded, then summed in the CPU oracle's pairwise order: bit-exact. */
+int vkhip_gemv(const float* a, int64_t lda, const float* x, int64_t incx, float* y,
+               uint32_t m, uint32_t k);
+
+/* cols[N, C*kh*kw, out_h*out_w] from image src[N,C,H,W] (any strides).
+ * Reference: ops.cpp:485-512, kernels_movement.cpp:454-483, im2col.comp. */
+int vkhip_im2col(const float* src, const vkhip_operand* src_desc, float* dst,
+                 const vkhip_unfold* p);
+
+/* image dst[N,C,H,W] (contiguous) from cols[N, C*kh*kw, L] (contiguous);
+ * pull with ascending (ki,kj) fold from 0.0f: bit-exact.
+ * Reference: ops.cpp:514-541, kernels_movement.cpp:500-542, col2im.comp. */
+int vkhip_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
+                 const vkhip_unfold* p);
+
+/* Softmax / log-softmax of src over `axis` (0..3 of the rank-4 descriptor),
+ * out contiguous with src's extents. Reference: ops.cpp:883-900,
+ * kernels_reduce.cpp:205-259, softmax.comp. */
+int vkhip_softmax(const float* src, const vkhip_operand* src_desc, float* dst, int axis,
+                  int log_softmax);
+
+/* Reduction of src over the axes in `axes_mask` (bit i = axis i of the
+ * rank-4 descriptor). dst holds prod(kept extents) values, f32 or int64 for
+ * argmax/argmin. Reference: ops.cpp:119-130, kernels_reduce.cpp:44-176,
+ * reduce.comp. Sum/mean follow the oracle's pairwise association: bit-exact. */
+int vkhip_reduce(int op, const float* src, const vkhip_operand* src_desc, uint32_t axes_mask,
+                 void* dst);
+
+/* Max-pool forward and backward (pull, first maximum wins). Reference:
+ * ops.cpp:611-641, kernels_movement.cpp:556-680, max_pool2d.comp. */
+int vkhip_max_pool2d(const float* src, float* dst, uint32_t planes, uint32_t out_h,
+                     uint32_t out_w, const vkhip_unfold* p);
+int vkhip_max_pool2d_backward(const float* grad, const float* src, float* dst,
+                              uint32_t planes, uint32_t out_h, uint32_t out_w,
+                              const vkhip_unfold* p);
+
+/* a*alpha + b*beta with two rounded multiplies and one add
+ * (reference scaled_add.comp:41-66, kernels_elementwise.cpp:256-259). */
+int vkhip_scaled_add(const float* a, const float* b, float* out, uint64_t n, float alpha,
+                     float beta);
+
+/* ======================================================================== */
+/* Host-side planning helpers (callable without a GPU)                       */
+/* ======================================================================== */
+/* Geometry of the CPU oracle's pairwise-summation tree (reference
+ * pairwise_sum, src/backend/cpu/reduce.h:55-72) as the device kernels lay it
+ * out: depth D and the element range [begin, end) of depth-D leaf `leaf`
+ * (0 <= leaf < 2^D; empty for the non-leftmost descendants of a leaf that
+ * ended above depth D). Summing each leaf from 0.0f and combining leaves
+ * adjacent-first reproduces the oracle's additions. */
+int vkhip_pairwise_leaf(uint32_t n, uint32_t leaf, uint32_t* out_depth, uint32_t* out_begin,
+                        uint32_t* out_end);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VKHIP_H */

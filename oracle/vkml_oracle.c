@@ -1,0 +1,562 @@
+/*
+ * vkml_oracle.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of vkML's CPU backend (the parity oracle) for the hot
+ * path and the support kernels the training steps need. Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and only
+ * as the checker or as the reported CPU baseline; the product never calls it.
+ *
+ * Build: -O2 -ffp-contract=off (no FMA contraction, no fast-math), so every
+ * product and sum rounds to f32 exactly where the reference's does.
+ *
+ * Each function cites the reference source it follows. The reference is C++20
+ * (templates over a strided Node); here the same loops walk rank-4 operand
+ * descriptors (extents right-aligned, strides in elements), and the pairwise
+ * recursion is restated over a gathered array, which performs the identical
+ * sequence of f32 operations.
+ *
+ * Threads: functions taking `threads` parallelise over OUTPUT elements only
+ * (OpenMP); every output's arithmetic is unchanged, so any thread count gives
+ * bit-identical results.
+ */
+#include "vkhip.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define OR_PAIRWISE_BLOCK 32 /* reference kPairwiseBlock, src/backend/cpu/reduce.h:48 */
+
+/* ------------------------------------------------------------------------ */
+/* Pairwise summation: reference pairwise_sum, src/backend/cpu/reduce.h:55-72 */
+/* ------------------------------------------------------------------------ */
+static float pairwise(const float* v, int64_t begin, int64_t end) {
+    const int64_t n = end - begin;
+    if (n <= 0) return 0.0f;
+    if (n <= OR_PAIRWISE_BLOCK) {
+        float acc = 0.0f;
+        for (int64_t i = begin; i < end; ++i) acc += v[i];
+        return acc;
+    }
+    const int64_t mid = begin + n / 2; /* midpoint split, reduce.h:69 */
+    return pairwise(v, begin, mid) + pairwise(v, mid, end);
+}
+
+float or_pairwise_sum(const float* v, int64_t n) { return pairwise(v, 0, n); }
+
+/* Offset (elements) of the `linear`-th element in row-major order of a
+ * rank-4 descriptor: reference linear_to_offset, src/backend/cpu/iterate.h:33-42. */
+static int64_t lin_off(int64_t linear, const uint32_t ne[4], const int64_t nb[4]) {
+    int64_t off = 0;
+    for (int i = 3; i >= 0; --i) {
+        const int64_t e = ne[i];
+        off += (linear % e) * nb[i];
+        linear /= e;
+    }
+    return off;
+}
+
+static int64_t numel4(const uint32_t ne[4]) {
+    return (int64_t)ne[0] * ne[1] * ne[2] * ne[3];
+}
+
+static int nthreads(int threads) { return threads > 0 ? threads : 1; }
+
+/* ------------------------------------------------------------------------ */
+/* Matmul: reference matmul_impl<float>, src/backend/cpu/kernels_matmul.cpp:34-87
+ * out[b0,b1,M,N] contiguous; per output the K products are rounded to f32
+ * (widen(a)*widen(b)) and pairwise-summed. */
+/* ------------------------------------------------------------------------ */
+void or_matmul(const float* a, const vkhip_operand* ad, const float* b, const vkhip_operand* bd,
+               float* out, int threads) {
+    const int64_t b0 = ad->ne[0] > bd->ne[0] ? ad->ne[0] : bd->ne[0];
+    const int64_t b1 = ad->ne[1] > bd->ne[1] ? ad->ne[1] : bd->ne[1];
+    const int64_t m = ad->ne[2], k = ad->ne[3], n = bd->ne[3];
+    const int64_t total = b0 * b1 * m * n;
+#pragma omp parallel num_threads(nthreads(threads))
+    {
+        float* prod = (float*)malloc(sizeof(float) * (size_t)(k > 0 ? k : 1));
+#pragma omp for schedule(static)
+        for (int64_t o = 0; o < total; ++o) {
+            const int64_t c = o % n, r = (o / n) % m, i1 = (o / (n * m)) % b1,
+                          i0 = o / (n * m * b1);
+            const float* ap = a + i0 * ad->nb[0] + i1 * ad->nb[1] + r * ad->nb[2];
+            const float* bp = b + i0 * bd->nb[0] + i1 * bd->nb[1] + c * bd->nb[3];
+            for (int64_t t = 0; t < k; ++t) prod[t] = ap[t * ad->nb[3]] * bp[t * bd->nb[2]];
+            out[o] = pairwise(prod, 0, k);
+        }
+        free(prod);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Reductions: reference reduce_generic + k_sum/k_mean/k_max/k_min/k_argmax/
+ * k_argmin, src/backend/cpu/kernels_reduce.cpp:44-176, plan from
+ * make_reduce_plan (reduce.cpp:11-30). `mask` bit i = axis i of the rank-4
+ * descriptor. Output: kept axes, row-major; f32, or int64 for arg ops. */
+/* ------------------------------------------------------------------------ */
+static void split_plan(const vkhip_operand* d, uint32_t mask, uint32_t kne[4], int64_t knb[4],
+                       uint32_t rne[4], int64_t rnb[4]) {
+    int kc = 0, rc = 0;
+    uint32_t kn[4], rn[4];
+    int64_t ks[4], rs[4];
+    for (int i = 0; i < 4; ++i) {
+        if (mask & (1u << i)) {
+            rn[rc] = d->ne[i];
+            rs[rc++] = d->nb[i];
+        } else {
+            kn[kc] = d->ne[i];
+            ks[kc++] = d->nb[i];
+        }
+    }
+    for (int i = 0; i < 4; ++i) {
+        kne[i] = 1; knb[i] = 0; rne[i] = 1; rnb[i] = 0;
+    }
+    for (int i = 0; i < kc; ++i) { kne[4 - kc + i] = kn[i]; knb[4 - kc + i] = ks[i]; }
+    for (int i = 0; i < rc; ++i) { rne[4 - rc + i] = rn[i]; rnb[4 - rc + i] = rs[i]; }
+}
+
+void or_reduce(int op, const float* in, const vkhip_operand* d, uint32_t mask, void* out,
+               int threads) {
+    uint32_t kne[4], rne[4];
+    int64_t knb[4], rnb[4];
+    split_plan(d, mask, kne, knb, rne, rnb);
+    const int64_t n_out = numel4(kne), n_red = numel4(rne);
+#pragma omp parallel num_threads(nthreads(threads))
+    {
+        float* buf = (float*)malloc(sizeof(float) * (size_t)(n_red > 0 ? n_red : 1));
+#pragma omp for schedule(static)
+        for (int64_t o = 0; o < n_out; ++o) {
+            const float* base = in + lin_off(o, kne, knb);
+            for (int64_t i = 0; i < n_red; ++i) buf[i] = base[lin_off(i, rne, rnb)];
+            switch (op) {
+                case VKHIP_REDUCE_SUM: ((float*)out)[o] = pairwise(buf, 0, n_red); break;
+                case VKHIP_REDUCE_MEAN:
+                    ((float*)out)[o] = n_red == 0 ? NAN : pairwise(buf, 0, n_red) / (float)n_red;
+                    break;
+                case VKHIP_REDUCE_MAX:
+                case VKHIP_REDUCE_MIN: {
+                    /* sequential, NaN returned immediately (kernels_reduce.cpp:124-154) */
+                    const int is_max = op == VKHIP_REDUCE_MAX;
+                    float best = is_max ? -INFINITY : INFINITY;
+                    for (int64_t i = 0; i < n_red; ++i) {
+                        const float v = buf[i];
+                        if (isnan(v)) { best = v; break; }
+                        if (is_max ? (v > best) : (v < best)) best = v;
+                    }
+                    ((float*)out)[o] = best;
+                    break;
+                }
+                case VKHIP_REDUCE_ARGMAX:
+                case VKHIP_REDUCE_ARGMIN: {
+                    /* strict comparison keeps the FIRST extremum; NaN never
+                     * compares true so it is skipped (kernels_reduce.cpp:156-192) */
+                    const int is_max = op == VKHIP_REDUCE_ARGMAX;
+                    int64_t best_i = 0;
+                    float best = is_max ? -INFINITY : INFINITY;
+                    for (int64_t i = 0; i < n_red; ++i) {
+                        const float v = buf[i];
+                        if (is_max ? (v > best) : (v < best)) { best = v; best_i = i; }
+                    }
+                    ((int64_t*)out)[o] = best_i;
+                    break;
+                }
+                default: break;
+            }
+        }
+        free(buf);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Softmax / log-softmax: reference softmax_impl<Log,float>,
+ * src/backend/cpu/kernels_reduce.cpp:205-259. peak = running std::max
+ * (NaN-ignoring, as std::max(peak, v) is); denom = pairwise sum of
+ * exp(x - peak); out = exp(x-peak)/denom or (x-peak) - log(denom).
+ * Output contiguous with the input's extents. */
+/* ------------------------------------------------------------------------ */
+void or_softmax(const float* in, const vkhip_operand* d, float* out, int axis, int log_softmax,
+                int threads) {
+    const uint32_t mask = 1u << axis;
+    uint32_t kne[4], rne[4];
+    int64_t knb[4], rnb[4];
+    split_plan(d, mask, kne, knb, rne, rnb);
+    /* contiguous output strides */
+    vkhip_operand od;
+    int64_t s = 1;
+    for (int i = 3; i >= 0; --i) { od.ne[i] = d->ne[i]; od.nb[i] = s; s *= d->ne[i]; }
+    uint32_t okne[4], orne[4];
+    int64_t oknb[4], ornb[4];
+    split_plan(&od, mask, okne, oknb, orne, ornb);
+    const int64_t n_out = numel4(kne), n_axis = numel4(rne);
+#pragma omp parallel num_threads(nthreads(threads))
+    {
+        float* ex = (float*)malloc(sizeof(float) * (size_t)(n_axis > 0 ? n_axis : 1));
+#pragma omp for schedule(static)
+        for (int64_t o = 0; o < n_out; ++o) {
+            const float* base = in + lin_off(o, kne, knb);
+            float* obase = out + lin_off(o, okne, oknb);
+            float peak = -INFINITY;
+            for (int64_t k = 0; k < n_axis; ++k) {
+                const float v = base[lin_off(k, rne, rnb)];
+                peak = (peak < v) ? v : peak; /* std::max(peak, v) */
+            }
+            for (int64_t k = 0; k < n_axis; ++k) ex[k] = expf(base[lin_off(k, rne, rnb)] - peak);
+            const float denom = pairwise(ex, 0, n_axis);
+            const float ld = logf(denom);
+            for (int64_t k = 0; k < n_axis; ++k) {
+                const float shifted = base[lin_off(k, rne, rnb)] - peak;
+                obase[lin_off(k, orne, ornb)] = log_softmax ? shifted - ld : expf(shifted) / denom;
+            }
+        }
+        free(ex);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* im2col / col2im: reference window_of, k_im2col_impl, k_col2im_impl,
+ * src/backend/cpu/kernels_movement.cpp:438-542. */
+/* ------------------------------------------------------------------------ */
+static int64_t span_of(int64_t extent, int k, int s, int pad, int dil) {
+    return (extent + 2LL * pad - ((int64_t)dil * (k - 1) + 1)) / s + 1;
+}
+
+void or_im2col(const float* src, const vkhip_operand* sd, float* dst, const vkhip_unfold* p,
+               int threads) {
+    const int64_t nb = sd->ne[0], ch = sd->ne[1];
+    const int64_t oh_n = span_of(p->image_h, p->kernel_h, p->stride_h, p->pad_h, p->dilation_h);
+    const int64_t ow_n = span_of(p->image_w, p->kernel_w, p->stride_w, p->pad_w, p->dilation_w);
+    const int64_t patch = (int64_t)p->kernel_h * p->kernel_w;
+    const int64_t rows = ch * patch, L = oh_n * ow_n;
+#pragma omp parallel for num_threads(nthreads(threads)) schedule(static) collapse(2)
+    for (int64_t n = 0; n < nb; ++n) {
+        for (int64_t row = 0; row < rows; ++row) {
+            const int64_t c = row / patch, ki = (row % patch) / p->kernel_w,
+                          kj = (row % patch) % p->kernel_w;
+            for (int64_t pos = 0; pos < L; ++pos) {
+                const int64_t oh = pos / ow_n, ow = pos % ow_n;
+                const int64_t h = oh * p->stride_h - p->pad_h + ki * p->dilation_h;
+                const int64_t x = ow * p->stride_w - p->pad_w + kj * p->dilation_w;
+                const int inside = h >= 0 && h < p->image_h && x >= 0 && x < p->image_w;
+                dst[(n * rows + row) * L + pos] =
+                    inside ? src[n * sd->nb[0] + c * sd->nb[1] + h * sd->nb[2] + x * sd->nb[3]]
+                           : 0.0f;
+            }
+        }
+    }
+}
+
+void or_col2im(const float* cols, float* dst, uint32_t nbatch, uint32_t channels,
+               const vkhip_unfold* p, int threads) {
+    const int64_t oh_n = span_of(p->image_h, p->kernel_h, p->stride_h, p->pad_h, p->dilation_h);
+    const int64_t ow_n = span_of(p->image_w, p->kernel_w, p->stride_w, p->pad_w, p->dilation_w);
+    const int64_t patch = (int64_t)p->kernel_h * p->kernel_w;
+    const int64_t rows = (int64_t)channels * patch, L = oh_n * ow_n;
+    const int64_t total = (int64_t)nbatch * channels * p->image_h * p->image_w;
+#pragma omp parallel for num_threads(nthreads(threads)) schedule(static)
+    for (int64_t i = 0; i < total; ++i) {
+        const int64_t x = i % p->image_w, h = (i / p->image_w) % p->image_h,
+                      c = (i / ((int64_t)p->image_w * p->image_h)) % channels,
+                      n = i / ((int64_t)p->image_w * p->image_h * channels);
+        float acc = 0.0f;
+        for (int64_t ki = 0; ki < p->kernel_h; ++ki) {
+            const int64_t top = h + p->pad_h - ki * p->dilation_h;
+            if (top < 0 || top % p->stride_h != 0) continue;
+            const int64_t oh = top / p->stride_h;
+            if (oh >= oh_n) continue;
+            for (int64_t kj = 0; kj < p->kernel_w; ++kj) {
+                const int64_t left = x + p->pad_w - kj * p->dilation_w;
+                if (left < 0 || left % p->stride_w != 0) continue;
+                const int64_t ow = left / p->stride_w;
+                if (ow >= ow_n) continue;
+                const int64_t row = c * patch + ki * p->kernel_w + kj;
+                acc += cols[(n * rows + row) * L + oh * ow_n + ow];
+            }
+        }
+        dst[i] = acc;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Max-pool: reference argmax_in_window, k_max_pool2d_impl,
+ * k_max_pool2d_backward_impl, src/backend/cpu/kernels_movement.cpp:556-680.
+ * Input and output are contiguous planes [planes, H, W] / [planes, oh, ow]. */
+/* ------------------------------------------------------------------------ */
+static int64_t window_argmax(const vkhip_unfold* p, int64_t oh, int64_t ow, const float* plane) {
+    float best = -INFINITY;
+    int64_t best_off = -1;
+    for (int64_t ki = 0; ki < p->kernel_h; ++ki) {
+        const int64_t h = oh * p->stride_h - p->pad_h + ki * p->dilation_h;
+        if (h < 0 || h >= p->image_h) continue;
+        for (int64_t kj = 0; kj < p->kernel_w; ++kj) {
+            const int64_t x = ow * p->stride_w - p->pad_w + kj * p->dilation_w;
+            if (x < 0 || x >= p->image_w) continue;
+            const float v = plane[h * p->image_w + x];
+            if (v > best) { best = v; best_off = ki * p->kernel_w + kj; }
+        }
+    }
+    return best_off;
+}
+
+int or_max_pool2d(const float* src, float* dst, uint32_t planes, uint32_t out_h, uint32_t out_w,
+                  const vkhip_unfold* p, int threads) {
+    int bad = 0;
+#pragma omp parallel for num_threads(nthreads(threads)) schedule(static) reduction(| : bad)
+    for (int64_t pl = 0; pl < planes; ++pl) {
+        const float* plane = src + pl * (int64_t)p->image_h * p->image_w;
+        for (int64_t oh = 0; oh < out_h; ++oh)
+            for (int64_t ow = 0; ow < out_w; ++ow) {
+                const int64_t off = window_argmax(p, oh, ow, plane);
+                if (off < 0) { bad = 1; continue; } /* whole window in padding: VKML_ASSERT */
+                const int64_t h = oh * p->stride_h - p->pad_h + (off / p->kernel_w) * p->dilation_h;
+                const int64_t x = ow * p->stride_w - p->pad_w + (off % p->kernel_w) * p->dilation_w;
+                dst[(pl * out_h + oh) * out_w + ow] = plane[h * p->image_w + x];
+            }
+    }
+    return bad ? VKHIP_ERR_INVALID : VKHIP_OK;
+}
+
+void or_max_pool2d_backward(const float* grad, const float* src, float* dst, uint32_t planes,
+                            uint32_t out_h, uint32_t out_w, const vkhip_unfold* p, int threads) {
+#pragma omp parallel for num_threads(nthreads(threads)) schedule(static)
+    for (int64_t pl = 0; pl < planes; ++pl) {
+        const float* plane = src + pl * (int64_t)p->image_h * p->image_w;
+        for (int64_t h = 0; h < p->image_h; ++h)
+            for (int64_t x = 0; x < p->image_w; ++x) {
+                float acc = 0.0f;
+                for (int64_t ki = 0; ki < p->kernel_h; ++ki) {
+                    const int64_t top = h + p->pad_h - ki * p->dilation_h;
+                    if (top < 0 || top % p->stride_h != 0) continue;
+                    const int64_t oh = top / p->stride_h;
+                    if (oh >= out_h) continue;
+                    for (int64_t kj = 0; kj < p->kernel_w; ++kj) {
+                        const int64_t left = x + p->pad_w - kj * p->dilation_w;
+                        if (left < 0 || left % p->stride_w != 0) continue;
+                        const int64_t ow = left / p->stride_w;
+                        if (ow >= out_w) continue;
+                        if (window_argmax(p, oh, ow, plane) == ki * p->kernel_w + kj)
+                            acc += grad[(pl * out_h + oh) * out_w + ow];
+                    }
+                }
+                dst[pl * (int64_t)p->image_h * p->image_w + h * p->image_w + x] = acc;
+            }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Split-K carry-stack fold: reference gemm_split_k_reduce.comp:48-85 (the
+ * binary-counter push/drain, also restated in tests/python/test_invariants.py:90-107). */
+/* ------------------------------------------------------------------------ */
+void or_split_k_fold(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
+    for (uint64_t i = 0; i < ne; ++i) {
+        float stack[32];
+        uint32_t count = 0;
+        for (uint32_t s = 0; s < splits; ++s) {
+            float block = ws[(uint64_t)s * ne + i];
+            uint32_t c = count, level = 0;
+            while (c & 1u) { block += stack[level]; c >>= 1; ++level; }
+            stack[level] = block;
+            ++count;
+        }
+        float total = 0.0f;
+        for (uint32_t level = 0; level < 32; ++level)
+            if ((count >> level) & 1u) total += stack[level];
+        dst[i] = total;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Elementwise support ops: reference kernels_elementwise.cpp:160-300 and
+ * kernels_movement.cpp:100-200 (cast, full, arange). Output contiguous;
+ * sources already broadcast to the output extents by strides. */
+/* ------------------------------------------------------------------------ */
+static float unary_f(int op, float x) {
+    switch (op) {
+        case VKHIP_OP_NEG: return -x;
+        case VKHIP_OP_EXP: return expf(x);
+        case VKHIP_OP_LOG: return logf(x);
+        case VKHIP_OP_RELU: return x <= 0.0f ? 0.0f : x; /* NaN propagates, k_relu */
+        case VKHIP_OP_CONTIGUOUS: return x;
+        default: return NAN;
+    }
+}
+
+static float binary_f(int op, float x, float y, float alpha, float beta) {
+    switch (op) {
+        case VKHIP_OP_ADD: return x + y;
+        case VKHIP_OP_SUB: return x - y;
+        case VKHIP_OP_MUL: return x * y;
+        case VKHIP_OP_DIV: return x / y;
+        case VKHIP_OP_SCALED_ADD: { const float l = x * alpha; const float r = y * beta; return l + r; }
+        case VKHIP_OP_MAXIMUM: return (isnan(x) || isnan(y)) ? NAN : (x > y ? x : y);
+        case VKHIP_OP_MINIMUM: return (isnan(x) || isnan(y)) ? NAN : (x < y ? x : y);
+        default: return NAN;
+    }
+}
+
+static int compare_f(int op, float x, float y) {
+    switch (op) {
+        case VKHIP_OP_EQUAL: return x == y;
+        case VKHIP_OP_LESS: return x < y;
+        case VKHIP_OP_GREATER: return x > y;
+        case VKHIP_OP_LESS_EQUAL: return x <= y;
+        case VKHIP_OP_GREATER_EQUAL: return x >= y;
+        case VKHIP_OP_NOT_EQUAL: return x != y;
+        default: return 0;
+    }
+}
+
+static void to_desc(const vkhip_tensor* t, vkhip_operand* d) {
+    const int pad = 4 - t->ndim;
+    for (int i = 0; i < 4; ++i) { d->ne[i] = 1; d->nb[i] = 0; }
+    for (int i = 0; i < t->ndim; ++i) { d->ne[pad + i] = (uint32_t)t->ne[i]; d->nb[pad + i] = t->nb[i]; }
+}
+
+static int64_t tnumel(const vkhip_tensor* t) {
+    int64_t n = 1;
+    for (int i = 0; i < t->ndim; ++i) n *= t->ne[i];
+    return n;
+}
+
+/* ------------------------------------------------------------------------ */
+/* or_compute: the CPU backend's compute(span<Node*>) loop over the same node
+ * records the device backend takes (reference CpuBackend::compute,
+ * src/backend/cpu/cpu_backend.cpp, which looks each op up in its kernel table,
+ * kernels.h:15-24). Host pointers. Returns a vkhip_status. */
+/* ------------------------------------------------------------------------ */
+int or_compute(const vkhip_node* nodes, size_t count, int threads) {
+    for (size_t ni = 0; ni < count; ++ni) {
+        const vkhip_node* nd = &nodes[ni];
+        const vkhip_tensor* o = &nd->out;
+        const int64_t n = tnumel(o);
+        vkhip_operand s0, s1, s2;
+        if (nd->n_src > 0) to_desc(&nd->src[0], &s0);
+        if (nd->n_src > 1) to_desc(&nd->src[1], &s1);
+        if (nd->n_src > 2) to_desc(&nd->src[2], &s2);
+        switch (nd->op) {
+            case VKHIP_OP_FULL: {
+                double v;
+                memcpy(&v, nd->params, sizeof v);
+                if (o->dtype == VKHIP_F32) for (int64_t i = 0; i < n; ++i) ((float*)o->data)[i] = (float)v;
+                else if (o->dtype == VKHIP_I64) for (int64_t i = 0; i < n; ++i) ((int64_t*)o->data)[i] = (int64_t)v;
+                else if (o->dtype == VKHIP_BOOL) memset(o->data, v != 0.0 ? 1 : 0, (size_t)n);
+                else return VKHIP_ERR_UNSUPPORTED;
+                break;
+            }
+            case VKHIP_OP_ARANGE: {
+                double ar[2];
+                memcpy(ar, nd->params, sizeof ar);
+                if (o->dtype == VKHIP_F32) for (int64_t i = 0; i < n; ++i) ((float*)o->data)[i] = (float)(ar[0] + (double)i * ar[1]);
+                else if (o->dtype == VKHIP_I64) for (int64_t i = 0; i < n; ++i) ((int64_t*)o->data)[i] = (int64_t)(ar[0] + (double)i * ar[1]);
+                else return VKHIP_ERR_UNSUPPORTED;
+                break;
+            }
+            case VKHIP_OP_CAST: {
+                const int from = nd->src[0].dtype, to = o->dtype;
+                for (int64_t i = 0; i < n; ++i) {
+                    const int64_t off = lin_off(i, s0.ne, s0.nb);
+                    if (from == VKHIP_I64 && to == VKHIP_F32) ((float*)o->data)[i] = (float)((const int64_t*)nd->src[0].data)[off];
+                    else if (from == VKHIP_BOOL && to == VKHIP_F32) ((float*)o->data)[i] = ((const uint8_t*)nd->src[0].data)[off] != 0 ? 1.0f : 0.0f;
+                    else if (from == VKHIP_F32 && to == VKHIP_I64) ((int64_t*)o->data)[i] = (int64_t)((const float*)nd->src[0].data)[off];
+                    else if (from == to && to == VKHIP_F32) ((float*)o->data)[i] = ((const float*)nd->src[0].data)[off];
+                    else return VKHIP_ERR_UNSUPPORTED;
+                }
+                break;
+            }
+            case VKHIP_OP_CONTIGUOUS:
+                if (o->dtype == VKHIP_I64) {
+                    for (int64_t i = 0; i < n; ++i) ((int64_t*)o->data)[i] = ((const int64_t*)nd->src[0].data)[lin_off(i, s0.ne, s0.nb)];
+                    break;
+                }
+                /* fall through: f32 copy */
+            case VKHIP_OP_NEG: case VKHIP_OP_EXP: case VKHIP_OP_LOG: case VKHIP_OP_RELU: {
+                if (o->dtype != VKHIP_F32) return VKHIP_ERR_UNSUPPORTED;
+                const float* x = (const float*)nd->src[0].data;
+                for (int64_t i = 0; i < n; ++i) ((float*)o->data)[i] = unary_f(nd->op, x[lin_off(i, s0.ne, s0.nb)]);
+                break;
+            }
+            case VKHIP_OP_ADD: case VKHIP_OP_SUB: case VKHIP_OP_MUL: case VKHIP_OP_DIV:
+            case VKHIP_OP_SCALED_ADD: case VKHIP_OP_MAXIMUM: case VKHIP_OP_MINIMUM: {
+                float ab[2] = {1.0f, 1.0f};
+                memcpy(ab, nd->params, sizeof ab);
+                const float* x = (const float*)nd->src[0].data;
+                const float* y = (const float*)nd->src[1].data;
+                for (int64_t i = 0; i < n; ++i)
+                    ((float*)o->data)[i] = binary_f(nd->op, x[lin_off(i, s0.ne, s0.nb)], y[lin_off(i, s1.ne, s1.nb)], ab[0], ab[1]);
+                break;
+            }
+            case VKHIP_OP_EQUAL: case VKHIP_OP_LESS: case VKHIP_OP_GREATER: case VKHIP_OP_LESS_EQUAL:
+            case VKHIP_OP_GREATER_EQUAL: case VKHIP_OP_NOT_EQUAL: {
+                const float* x = (const float*)nd->src[0].data;
+                const float* y = (const float*)nd->src[1].data;
+                for (int64_t i = 0; i < n; ++i)
+                    ((uint8_t*)o->data)[i] = (uint8_t)compare_f(nd->op, x[lin_off(i, s0.ne, s0.nb)], y[lin_off(i, s1.ne, s1.nb)]);
+                break;
+            }
+            case VKHIP_OP_WHERE: {
+                const uint8_t* c = (const uint8_t*)nd->src[0].data;
+                const float* x = (const float*)nd->src[1].data;
+                const float* y = (const float*)nd->src[2].data;
+                for (int64_t i = 0; i < n; ++i)
+                    ((float*)o->data)[i] = c[lin_off(i, s0.ne, s0.nb)] ? x[lin_off(i, s1.ne, s1.nb)] : y[lin_off(i, s2.ne, s2.nb)];
+                break;
+            }
+            case VKHIP_OP_SUM: case VKHIP_OP_MEAN: case VKHIP_OP_MAX: case VKHIP_OP_MIN:
+            case VKHIP_OP_ARGMAX: case VKHIP_OP_ARGMIN: {
+                uint32_t mask;
+                memcpy(&mask, nd->params, sizeof mask);
+                const int nd0 = nd->src[0].ndim;
+                if (mask == 0) mask = nd0 <= 0 ? 0u : (1u << nd0) - 1u; /* all_axes_mask */
+                const uint32_t mask4 = mask << (4 - nd0);
+                static const int map[] = {VKHIP_REDUCE_SUM, VKHIP_REDUCE_MEAN, VKHIP_REDUCE_MAX, VKHIP_REDUCE_MIN, -1, VKHIP_REDUCE_ARGMAX, VKHIP_REDUCE_ARGMIN};
+                or_reduce(map[nd->op - VKHIP_OP_SUM], (const float*)nd->src[0].data, &s0, mask4, o->data, threads);
+                break;
+            }
+            case VKHIP_OP_MATMUL:
+                or_matmul((const float*)nd->src[0].data, &s0, (const float*)nd->src[1].data, &s1, (float*)o->data, threads);
+                break;
+            case VKHIP_OP_SOFTMAX: case VKHIP_OP_LOG_SOFTMAX: {
+                int32_t axis;
+                memcpy(&axis, nd->params, sizeof axis);
+                if (axis < 0) axis += nd->src[0].ndim;
+                or_softmax((const float*)nd->src[0].data, &s0, (float*)o->data, axis + 4 - nd->src[0].ndim,
+                           nd->op == VKHIP_OP_LOG_SOFTMAX, threads);
+                break;
+            }
+            case VKHIP_OP_IM2COL: {
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                or_im2col((const float*)nd->src[0].data, &s0, (float*)o->data, &p, threads);
+                break;
+            }
+            case VKHIP_OP_COL2IM: {
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                or_col2im((const float*)nd->src[0].data, (float*)o->data, (uint32_t)o->ne[0], (uint32_t)o->ne[1], &p, threads);
+                break;
+            }
+            case VKHIP_OP_MAX_POOL2D: {
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                const int st = or_max_pool2d((const float*)nd->src[0].data, (float*)o->data,
+                                             (uint32_t)(o->ne[0] * o->ne[1]), (uint32_t)o->ne[2], (uint32_t)o->ne[3], &p, threads);
+                if (st != VKHIP_OK) return st;
+                break;
+            }
+            case VKHIP_OP_MAX_POOL2D_BACKWARD: {
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                or_max_pool2d_backward((const float*)nd->src[0].data, (const float*)nd->src[1].data, (float*)o->data,
+                                       (uint32_t)(o->ne[0] * o->ne[1]), (uint32_t)nd->src[0].ne[2], (uint32_t)nd->src[0].ne[3], &p, threads);
+                break;
+            }
+            default: return VKHIP_ERR_UNSUPPORTED;
+        }
+    }
+    return VKHIP_OK;
+}

@@ -1,0 +1,73 @@
+"""Shared test configuration.
+
+Markers:
+  gpu -- needs an MI355X (gfx950) and the built libvkhip.so; the parity tests.
+Everything unmarked runs on a CPU-only machine: the oracle against the
+reference's golden vectors and closed forms, host-side planning logic, and the
+C-ABI library's symbol table (no device calls).
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+# The reference suite's session seed (tests/python/test_vulkan_kernels.py:32).
+SEED = 20260726
+FP32_EPS = float(np.finfo(np.float32).eps)
+PAIRWISE_BLOCK = 32
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU and the built HIP library")
+
+
+def pairwise_gamma(n: int) -> float:
+    """Relative error factor of pairwise summation of n terms (reference
+    tests/python/tolerance.py:310-318): (B + log2(n/B)) * eps."""
+    if n <= 1:
+        return 0.0
+    return (PAIRWISE_BLOCK + np.log2(max(n / PAIRWISE_BLOCK, 1.0))) * FP32_EPS
+
+
+def gemm_atol(a: np.ndarray, b: np.ndarray, safety: float = 16.0) -> float:
+    """Backward-error bound for a product (reference conftest.py:145-165):
+    gamma(K) * max_ij sum_k |a_ik b_kj| * safety."""
+    k = a.shape[-1]
+    abs_prod = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))
+    return float(pairwise_gamma(max(k, 32)) * abs_prod.max() * safety)
+
+
+def normwise_rel_err(got: np.ndarray, want: np.ndarray) -> float:
+    """max |got - want| / max |want|: the north-star's relative error, normwise
+    (elementwise relative error is meaningless near the zeros of C)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = float(np.max(np.abs(want))) if want.size else 0.0
+    if scale == 0.0:
+        return float(np.max(np.abs(got))) if got.size else 0.0
+    return float(np.max(np.abs(got - want)) / scale)
+
+
+def gemm_tolerance(k: int) -> float:
+    """North-star GEMM/softmax gate: max relative error 1e-5 * sqrt(K)."""
+    return 1e-5 * float(np.sqrt(max(k, 1)))
+
+
+@pytest.fixture(scope="session")
+def rng():
+    return np.random.default_rng(SEED)
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """The process-wide HIP backend; GPU tests only."""
+    from vkml_amd.device import backend
+
+    return backend()

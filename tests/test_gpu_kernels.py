@@ -1,0 +1,388 @@
+"""Device parity: every hot-path kernel through the C ABI against the CPU oracle.
+
+Bars (north star): im2col/col2im, pooling, argmax, sum/mean, GEMV and the
+split-K fold are bit-exact; GEMM and softmax are within a normwise relative
+error of 1e-5*sqrt(K) of the oracle (and inside the backward-error bound of a
+float64 product, the reference's own GEMM policy, conftest.py:145-165).
+Shapes are the reference's test geometries plus the BASELINE configs; where the
+oracle is too slow at full size, full-size runs are checked on row samples
+against float64.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import SEED, gemm_atol, gemm_tolerance, normwise_rel_err
+from vkml_amd import _lib, ops
+from vkml_amd.device import DeviceArray
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(x: np.ndarray) -> DeviceArray:
+    return DeviceArray.from_numpy(x)
+
+
+def layout_view(x: np.ndarray, transposed: bool) -> tuple[np.ndarray, DeviceArray]:
+    """Host array and a device view of the same values; `transposed` stores the
+    matrix as its transpose and hands out a strided .T view (NT / TN operands)."""
+    if transposed:
+        d = dev(np.ascontiguousarray(np.swapaxes(x, -1, -2)))
+        return x, d.transpose(-2, -1)
+    return x, dev(x)
+
+
+def check_gemm(a: np.ndarray, b: np.ndarray, got: np.ndarray, want: np.ndarray | None = None):
+    k = a.shape[-1]
+    if want is None:
+        want = O.matmul(a, b)
+    err = normwise_rel_err(got, want)
+    assert err <= gemm_tolerance(k), f"normwise rel err {err:.3g} > {gemm_tolerance(k):.3g}"
+    exact = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    assert np.max(np.abs(got - exact)) <= gemm_atol(a, b) + 1e-30
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+
+def test_gemm_known_answer(hip):
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    np.testing.assert_array_equal(ops.matmul(dev(a), dev(b)).numpy(), [[58, 64], [139, 154]])
+    bt = np.array([[7, 9, 11], [8, 10, 12]], np.float32)
+    np.testing.assert_array_equal(ops.matmul(dev(a), dev(bt).T).numpy(), [[58, 64], [139, 154]])
+
+
+def test_gemm_vector_rules(hip):
+    m = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    v = np.ones(3, np.float32)
+    u = np.ones(2, np.float32)
+    np.testing.assert_array_equal(ops.matmul(dev(m), dev(v)).numpy(), [6, 15])
+    np.testing.assert_array_equal(ops.matmul(dev(u), dev(m)).numpy(), [5, 7, 9])
+
+
+@pytest.mark.parametrize("size", [1, 2, 3, 7, 8, 15, 16, 31, 32, 63, 64, 127, 128, 255, 256, 257])
+def test_gemm_edge_sizes(hip, size):
+    rng = np.random.default_rng(SEED + 32)
+    a = rng.uniform(-2, 2, (size, size)).astype(np.float32)
+    b = rng.uniform(-2, 2, (size, size)).astype(np.float32)
+    check_gemm(a, b, ops.matmul(dev(a), dev(b)).numpy())
+
+
+def gemm_cases(count: int):
+    rng = np.random.default_rng(SEED + 30)
+    for i in range(count):
+        m, n, k = (int(v) for v in rng.integers(1, 300, 3))
+        yield i, m, n, k, bool(rng.integers(2)), bool(rng.integers(2))
+
+
+@pytest.mark.parametrize("i,m,n,k,ta,tb", list(gemm_cases(40)))
+def test_gemm_random_shapes_and_layouts(hip, i, m, n, k, ta, tb):
+    rng = np.random.default_rng(SEED + 100 + i)
+    a, da = layout_view(rng.uniform(-2, 2, (m, k)).astype(np.float32), ta)
+    b, db = layout_view(rng.uniform(-2, 2, (k, n)).astype(np.float32), tb)
+    check_gemm(a, b, ops.matmul(da, db).numpy())
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn", "tt"])
+def test_gemm_config2_512_layouts(hip, layout):
+    """BASELINE config 2 at 512^3 in every layout forward/backward emit."""
+    rng = np.random.default_rng(SEED + 2)
+    a, da = layout_view(rng.standard_normal((512, 512)).astype(np.float32), layout[0] == "t")
+    b, db = layout_view(rng.standard_normal((512, 512)).astype(np.float32), layout[1] == "t")
+    check_gemm(a, b, ops.matmul(da, db).numpy())
+
+
+def test_gemm_batched_broadcast_conv_shape(hip):
+    """conv2d's GEMM: flat weight [Cout, CK] broadcast (stride 0) over a batch
+    of cols [N, CK, L], plus the dW (NT) and dcols (TN) products of backward."""
+    rng = np.random.default_rng(SEED + 3)
+    n, cout, ck, L = 4, 64, 27, 1024
+    w = rng.uniform(-0.2, 0.2, (cout, ck)).astype(np.float32)
+    cols = rng.uniform(-1, 1, (n, ck, L)).astype(np.float32)
+    g = rng.standard_normal((n, cout, L)).astype(np.float32)
+    dw_, dc_, dg_ = dev(w), dev(cols), dev(g)
+    fwd = ops.matmul(dw_.broadcast_to((1, n, cout, ck)), dc_.reshape(1, n, ck, L)).numpy()
+    check_gemm(np.broadcast_to(w, (1, n, cout, ck)), cols[None], fwd)
+    dwt = ops.matmul(dg_.reshape(1, n, cout, L), dc_.reshape(1, n, ck, L).transpose(-2, -1)).numpy()
+    check_gemm(g[None], np.swapaxes(cols, -1, -2)[None], dwt)
+    dcols = ops.matmul(dw_.T.broadcast_to((1, n, ck, cout)), dg_.reshape(1, n, cout, L)).numpy()
+    check_gemm(np.broadcast_to(w.T, (1, n, ck, cout)), g[None], dcols)
+
+
+def test_gemm_large_k_cancellation(hip):
+    """reference test_gemm_large_k_backward_error: K=4096, sign-mixed."""
+    rng = np.random.default_rng(SEED + 34)
+    a = rng.uniform(-2, 2, (4, 4096)).astype(np.float32)
+    b = rng.uniform(-2, 2, (4096, 4)).astype(np.float32)
+    got = ops.matmul(dev(a), dev(b)).numpy()
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.max(np.abs(got - exact)) <= gemm_atol(a, b)
+
+
+def test_gemm_is_deterministic(hip):
+    rng = np.random.default_rng(SEED + 33)
+    a, b = dev(rng.uniform(-2, 2, (64, 128)).astype(np.float32)), \
+        dev(rng.uniform(-2, 2, (128, 64)).astype(np.float32))
+    first = ops.matmul(a, b).numpy()
+    for _ in range(8):
+        assert ops.matmul(a, b).numpy().tobytes() == first.tobytes()
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 65536), (128, 784, 16384), (64, 128, 784)])
+def test_split_k_config3_parity_and_bit_stability(hip, m, n, k):
+    """BASELINE config 3's split-K shapes: AUTO splits, matches the oracle
+    within tolerance, and repeats bit for bit; a forced split count is also
+    bit-stable and agrees with the unsplit product within tolerance."""
+    splits, _ = ops.gemm_plan(1, m, n, k)
+    assert splits > 1
+    rng = np.random.default_rng(SEED + 4)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    da, db = dev(a), dev(b)
+    got = ops.matmul(da, db).numpy()
+    want = O.matmul(a, b) if m * n * k <= (1 << 31) else None
+    check_gemm(a, b, got, want)
+    for _ in range(3):
+        assert ops.matmul(da, db).numpy().tobytes() == got.tobytes()
+    forced = ops.matmul(da, db, split_k=8).numpy()
+    assert ops.matmul(da, db, split_k=8).numpy().tobytes() == forced.tobytes()
+    unsplit = ops.matmul(da, db, split_k=1).numpy()
+    assert normwise_rel_err(forced, unsplit) <= gemm_tolerance(k)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 4, 7, 16, 33, 128])
+def test_split_k_reduce_bit_exact(hip, splits):
+    rng = np.random.default_rng(splits)
+    ws = (rng.standard_normal(splits * 1000 + 0) * 1e3).astype(np.float32)
+    got = ops.split_k_reduce(dev(ws), splits).numpy()
+    assert got.tobytes() == O.split_k_fold(ws, splits).tobytes()
+
+
+@pytest.mark.parametrize("m,k", [(1, 1), (7, 31), (64, 784), (129, 1000), (4096, 4096),
+                                 (300, 33)])
+def test_gemv_bit_exact(hip, m, k):
+    """GEMV rounds each product and sums in the oracle's pairwise order."""
+    rng = np.random.default_rng(SEED + m + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    x = rng.standard_normal(k).astype(np.float32)
+    got = ops.gemv(dev(a), dev(x)).numpy()
+    want = O.matmul(a, x[:, None]).ravel()
+    assert got.tobytes() == want.tobytes()
+    # the matmul entry point routes N == 1 to the same kernel
+    assert ops.matmul(dev(a), dev(x)).numpy().tobytes() == want.tobytes()
+
+
+def test_gemm_config2_full_size_row_sample(hip):
+    """4096^3 (the bench workload) and 8192x1024x4096, checked on sampled rows
+    against float64."""
+    rng = np.random.default_rng(SEED + 5)
+    for m, n, k in [(4096, 4096, 4096), (8192, 1024, 4096)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        got = ops.matmul(dev(a), dev(b)).numpy()
+        rows = rng.choice(m, 64, replace=False)
+        exact = a[rows].astype(np.float64) @ b.astype(np.float64)
+        assert normwise_rel_err(got[rows], exact) <= gemm_tolerance(k)
+        assert np.max(np.abs(got[rows] - exact)) <= gemm_atol(a[rows], b)
+
+
+# ---------------------------------------------------------------------------
+# im2col / col2im
+# ---------------------------------------------------------------------------
+
+WINDOWS = [  # reference test_vulkan_kernels.py:1303-1310
+    ((1, 1, 4, 4), (2, 2), (1, 1), (0, 0), (1, 1)),
+    ((2, 3, 5, 5), (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 2, 6, 6), (2, 2), (2, 2), (0, 0), (1, 1)),
+    ((2, 1, 7, 5), (3, 2), (2, 1), (1, 0), (1, 1)),
+    ((1, 2, 5, 5), (2, 2), (1, 1), (0, 0), (2, 2)),
+    ((1, 1, 17, 17), (3, 3), (1, 1), (1, 1), (1, 1)),
+    # BASELINE config 4 geometries at full batch
+    ((128, 3, 32, 32), (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((128, 64, 32, 32), (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((128, 64, 16, 16), (3, 3), (1, 1), (1, 1), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("shape,kernel,stride,pad,dil", WINDOWS)
+def test_im2col_col2im_bit_exact(hip, shape, kernel, stride, pad, dil):
+    x = np.random.default_rng(SEED).uniform(-1, 1, shape).astype(np.float32)
+    cols = ops.im2col(dev(x), kernel, stride, pad, dil)
+    want = O.im2col(x, kernel, stride, pad, dil)
+    assert cols.numpy().tobytes() == want.tobytes()
+    img = ops.col2im(cols, shape[2:], kernel, stride, pad, dil).numpy()
+    assert img.tobytes() == O.col2im(want, shape[2:], kernel, stride, pad, dil).tobytes()
+
+
+def test_im2col_strided_input_view(hip):
+    """The image may arrive as a strided view (here: a channel-transposed copy)."""
+    x = np.random.default_rng(SEED).uniform(-1, 1, (2, 5, 9, 7)).astype(np.float32)
+    d = dev(np.ascontiguousarray(np.transpose(x, (0, 1, 3, 2)))).transpose(2, 3)
+    got = ops.im2col(d, (3, 3), (2, 1), (1, 1), (1, 1)).numpy()
+    assert got.tobytes() == O.im2col(x, (3, 3), (2, 1), (1, 1), (1, 1)).tobytes()
+
+
+def test_col2im_fold_order_fixture(hip):
+    """reference test_col2im_fold_is_bit_reproducible (test_vulkan_kernels.py:1342-1356)."""
+    vals = np.array([1e8, 1.0, -1e8, 1e-8, 1.0, -1.0, 1e7, 1.0, -1e7], np.float32)
+    cols = np.zeros((1, 9, 16), np.float32)
+    cols[0, :, :] = vals[:, None]
+    got = ops.col2im(dev(cols), (4, 4), (3, 3), (1, 1), (1, 1)).numpy()
+    assert got.tobytes() == O.col2im(cols, (4, 4), (3, 3), (1, 1), (1, 1)).tobytes()
+    again = ops.col2im(dev(cols), (4, 4), (3, 3), (1, 1), (1, 1)).numpy()
+    assert again.tobytes() == got.tobytes()
+
+
+# ---------------------------------------------------------------------------
+# softmax
+# ---------------------------------------------------------------------------
+
+def check_softmax(got, want, n):
+    tol = gemm_tolerance(n)
+    big = np.abs(want) > 1e-30
+    rel = np.abs(got[big] - want[big]) / np.abs(want[big])
+    assert rel.size == 0 or rel.max() <= tol, f"max rel err {rel.max():.3g} > {tol:.3g}"
+    assert np.all(np.abs(got[~big] - want[~big]) <= 1e-30)
+
+
+@pytest.mark.parametrize("shape", [(4096, 1000), (256, 32768), (64, 10), (128, 100),
+                                   (3, 1), (5, 4097), (7, 2048), (2, 3000), (33, 8192)])
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax_parity(hip, shape, log):
+    x = (np.random.default_rng(SEED + shape[1]).standard_normal(shape) * 2).astype(np.float32)
+    got = ops.softmax(dev(x), -1, log).numpy()
+    want = O.softmax(x, -1, log)
+    if log:
+        assert normwise_rel_err(got, want) <= gemm_tolerance(shape[1])
+    else:
+        check_softmax(got, want, shape[1])
+
+
+STABILITY_INPUTS = {
+    "large positive": [[1000.0, 1001.0, 1002.0]],
+    "large negative": [[-1000.0, -1001.0, -1002.0]],
+    "mixed sign": [[-500.0, 0.0, 500.0]],
+    "identical": [[3.5] * 8],
+    "identical zeros": [[0.0] * 16],
+    "extreme spread": [[0.0, -300.0, -600.0, -900.0]],
+    "single element": [[42.0]],
+    "tiny magnitudes": [[1e-30, 2e-30, 3e-30]],
+}
+
+
+@pytest.mark.parametrize("name", list(STABILITY_INPUTS))
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax_stability(hip, name, log):
+    x = np.array(STABILITY_INPUTS[name], np.float32)
+    got = ops.softmax(dev(x), -1, log).numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, O.softmax(x, -1, log), rtol=1e-5, atol=1e-6)
+
+
+def test_softmax_non_last_axis(hip):
+    x = np.random.default_rng(1).standard_normal((6, 37, 5)).astype(np.float32)
+    for axis in (0, 1):
+        got = ops.softmax(dev(x), axis).numpy()
+        check_softmax(got, O.softmax(x, axis), x.shape[axis])
+
+
+# ---------------------------------------------------------------------------
+# reductions
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape,axes", [
+    ((8192, 4096), [1]),        # BASELINE config 5 standalone
+    ((64, 128), [0]),           # Linear bias gradient
+    ((128, 64 * 27), [0]),      # conv weight-gradient batch sum (outer axis)
+    ((1024, 1024), [1]),
+    ((4096, 256), [1]),
+    ((3, 100003), [1]),         # long rows, irregular tree
+    ((5, 7, 33), [0, 2]),
+    ((2, 3, 4, 5), None),
+    ((17, 9), [1]),             # below one leaf per row
+])
+def test_sum_mean_bit_exact(hip, shape, axes):
+    x = (np.random.default_rng(SEED).standard_normal(shape) * 10).astype(np.float32)
+    d = dev(x)
+    assert ops.sum(d, axes).numpy().tobytes() == O.sum(x, axes).tobytes()
+    assert ops.mean(d, axes).numpy().tobytes() == O.mean(x, axes).tobytes()
+
+
+@pytest.mark.parametrize("shape,axis", [((8192, 4096), 1), ((1024, 1024), 1), ((64, 10), 1),
+                                        ((100, 37), 0), ((3, 5000), 1)])
+def test_max_min_argmax_exact(hip, shape, axis):
+    x = np.random.default_rng(SEED).standard_normal(shape).astype(np.float32)
+    x[..., ::97] = np.float32(2.5)  # planted ties
+    d = dev(x)
+    assert ops.amax(d, [axis]).numpy().tobytes() == O.amax(x, [axis]).tobytes()
+    assert ops.amin(d, [axis]).numpy().tobytes() == O.amin(x, [axis]).tobytes()
+    np.testing.assert_array_equal(ops.argmax(d, axis).numpy(), O.argmax(x, axis))
+    np.testing.assert_array_equal(ops.argmin(d, axis).numpy(), O.argmin(x, axis))
+
+
+def test_reduce_known_answers_and_nan(hip):
+    a = np.array([[1, 5, 5], [4, 2, 4]], np.float32)
+    np.testing.assert_array_equal(ops.argmax(dev(a), 1).numpy(), [1, 0])
+    np.testing.assert_array_equal(ops.argmin(dev(a), 1).numpy(), [0, 1])
+    x = np.array([[1.0, np.nan, 3.0, 2.0] * 20, [np.nan, np.nan, -np.inf, -np.inf] * 20],
+                 np.float32)
+    np.testing.assert_array_equal(ops.argmax(dev(x), 1).numpy(), O.argmax(x, 1))
+    assert np.isnan(ops.amax(dev(x), [1]).numpy()).all()
+
+
+# ---------------------------------------------------------------------------
+# max-pool and scaled_add
+# ---------------------------------------------------------------------------
+
+POOLS = [
+    ((1, 1, 4, 4), (2, 2), (2, 2), (0, 0)),
+    ((2, 3, 6, 6), (2, 2), (2, 2), (0, 0)),
+    ((1, 2, 5, 5), (3, 3), (1, 1), (1, 1)),
+    ((2, 1, 7, 5), (3, 2), (2, 1), (1, 0)),
+    ((1, 1, 17, 17), (3, 3), (2, 2), (1, 1)),
+    ((128, 64, 32, 32), (2, 2), (2, 2), (0, 0)),  # BASELINE configs 4/5
+    ((128, 128, 16, 16), (2, 2), (2, 2), (0, 0)),
+]
+
+
+@pytest.mark.parametrize("shape,kernel,stride,pad", POOLS)
+def test_max_pool2d_forward_backward_bit_exact(hip, shape, kernel, stride, pad):
+    x = np.random.default_rng(SEED).uniform(-3, 3, shape).astype(np.float32)
+    y = ops.max_pool2d(dev(x), kernel, stride, pad).numpy()
+    assert y.tobytes() == O.max_pool2d(x, kernel, stride, pad).tobytes()
+    g = np.random.default_rng(SEED + 1).uniform(-1, 1, y.shape).astype(np.float32)
+    gx = ops.max_pool2d_backward(dev(g), dev(x), kernel, stride, pad).numpy()
+    assert gx.tobytes() == O.max_pool2d_backward(g, x, kernel, stride, pad).tobytes()
+
+
+def test_max_pool2d_tie(hip):
+    x = np.array([[[[5.0, 5.0], [1.0, 2.0]]]], np.float32)
+    g = ops.max_pool2d_backward(dev(np.ones((1, 1, 1, 1), np.float32)), dev(x), (2, 2)).numpy()
+    np.testing.assert_array_equal(g, [[[[1, 0], [0, 0]]]])
+
+
+def test_scaled_add_is_two_rounded_products(hip):
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal(10001).astype(np.float32)
+    b = rng.standard_normal(10001).astype(np.float32)
+    got = ops.scaled_add(dev(a), dev(b), 0.9, -0.1).numpy()
+    want = (a * np.float32(0.9)).astype(np.float32) + (b * np.float32(-0.1)).astype(np.float32)
+    assert got.tobytes() == want.astype(np.float32).tobytes()
+
+
+def test_errors_are_reported_not_crashed(hip):
+    a = dev(np.ones((3, 4), np.float32))
+    b = dev(np.ones((5, 6), np.float32))
+    with pytest.raises(ValueError):
+        ops.matmul(a, b)
+    lib = _lib.load()
+    d = _lib.operand((3, 4), (4, 1))
+    e = _lib.operand((5, 6), (6, 1))
+    from ctypes import byref, c_void_p
+    code = lib.vkhip_gemm(c_void_p(a.ptr), byref(d), c_void_p(b.ptr), byref(e), c_void_p(a.ptr),
+                          None)
+    assert code == _lib.ERR_INVALID and b"inner dimensions" in lib.vkhip_last_error()

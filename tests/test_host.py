@@ -1,0 +1,127 @@
+"""CPU-only checks of the device library: it loads, exports every symbol the
+C header declares, and its host-side planning (the pairwise-tree layout every
+bit-exact kernel uses, the split-K plan) agrees with the oracle and the
+reference's rules. No device calls."""
+from __future__ import annotations
+
+import re
+from ctypes import byref, c_uint32
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import ROOT
+from vkml_amd import _lib
+
+HEADER = ROOT / "include" / "vkhip.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vkhip_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared in vkhip.h but not exported: {missing}"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with vkhip.h"
+
+
+def test_calls_before_init_fail_cleanly():
+    lib = _lib.load()
+    if lib.vkhip_get_stream():
+        pytest.skip("backend already initialised in this process")
+    code = lib.vkhip_synchronize()
+    assert code == _lib.ERR_NOT_INITIALISED
+    assert b"not initialised" in lib.vkhip_last_error()
+
+
+def leaf_layout(n: int):
+    lib = _lib.load()
+    d, b, e = c_uint32(), c_uint32(), c_uint32()
+    assert lib.vkhip_pairwise_leaf(n, 0, byref(d), byref(b), byref(e)) == 0
+    leaves = []
+    for j in range(1 << d.value):
+        assert lib.vkhip_pairwise_leaf(n, j, None, byref(b), byref(e)) == 0
+        leaves.append((b.value, e.value))
+    return d.value, leaves
+
+
+def carry_fold(vals) -> np.float32:
+    stack, count = {}, 0
+    for v in vals:
+        block, c, level = np.float32(v), count, 0
+        while c & 1:
+            block = np.float32(block + stack[level])
+            c >>= 1
+            level += 1
+        stack[level] = block
+        count += 1
+    total, level = np.float32(0.0), 0
+    while (count >> level) != 0:
+        if (count >> level) & 1:
+            total = np.float32(total + stack[level])
+        level += 1
+    return total
+
+
+@pytest.mark.parametrize("n", [0, 1, 31, 32, 33, 48, 64, 65, 100, 127, 784, 1000, 1023, 1025,
+                               4096, 4097, 9999, 32768, 100003])
+def test_device_tree_layout_reproduces_the_oracle_sum(n):
+    """The device kernels sum each depth-D leaf sequentially and combine the
+    2^D leaf values adjacent-first (a balanced fold). Done here on the CPU with
+    the library's own leaf table, that must equal the oracle bit for bit."""
+    depth, leaves = leaf_layout(n)
+    # leaves tile [0, n) in order; non-leftmost descendants are empty
+    covered = [i for b, e in leaves for i in range(b, e)]
+    assert covered == list(range(n))
+    assert all(e - b <= 32 for b, e in leaves)
+    rng = np.random.default_rng(n)
+    for scale in (1.0, 1e4):
+        v = (rng.standard_normal(n) * scale).astype(np.float32)
+        v[::7] *= np.float32(1e3)
+        sums = []
+        for b, e in leaves:
+            sums.append(np.float32(0.0) if e == b else np.cumsum(v[b:e], dtype=np.float32)[-1])
+        got = carry_fold(sums) if sums else np.float32(0.0)
+        assert got.tobytes() == O.pairwise_sum(v).tobytes(), (n, depth)
+
+
+def plan(batch, m, n, k, split=0):
+    lib = _lib.load()
+    s, c = c_uint32(), c_uint32()
+    assert lib.vkhip_gemm_plan(batch, m, n, k, split, byref(s), byref(c)) == 0
+    return s.value, c.value
+
+
+def test_split_k_plan_rules():
+    """The reference's plan_split_k rules (vulkan_backend.cpp:596-647): split
+    only when K-tiles >= output tiles, power-of-two chunk of >= 4 K-tiles,
+    workspace <= 64 MiB; OFF never splits."""
+    # square 4096^3: plenty of tiles, no split
+    assert plan(1, 4096, 4096, 4096) == (1, 128)
+    # the skinny K-dominant BASELINE shapes split
+    for m, n, k in [(256, 256, 65536), (128, 784, 16384)]:
+        splits, chunk = plan(1, m, n, k)
+        ktiles = -(-k // 32)
+        assert splits > 1 and chunk >= 4 and chunk & (chunk - 1) == 0
+        assert splits == -(-ktiles // chunk)
+        assert m * n * splits * 4 <= 64 << 20
+    # OFF
+    assert plan(1, 256, 256, 65536, split=1)[0] == 1
+    # forced request: chunk is the largest power of two giving >= request splits
+    s, c = plan(1, 64, 64, 4096, split=8)
+    assert c == 16 and s == 8
+
+
+def test_unfold_and_operand_helpers():
+    d = _lib.operand((3, 5), (5, 1))
+    assert list(d.ne) == [1, 1, 3, 5] and list(d.nb) == [0, 0, 5, 1]
+    u = _lib.unfold((3, 2), (1, 2), (1, 0), (1, 1), (7, 5))
+    assert (u.kernel_h, u.kernel_w, u.stride_w, u.pad_h, u.image_h) == (3, 2, 2, 1, 7)

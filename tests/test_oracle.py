@@ -1,0 +1,378 @@
+"""Pins the CPU oracle (oracle/vkml_oracle.c) before anything is checked against it.
+
+Each oracle function is tied to something independent of its own code:
+the reference's known answers (tests/cpp/test_ops.cpp:234-293), its fixtures
+(test_vulkan_kernels.py: STABILITY_INPUTS :808-817, the col2im bit-reproducibility
+cols :1347-1352, the pool tie :1440), the carry-stack theorem the reference proves
+on the host (test_invariants.py:90-191), torch / float64 closed forms, and brute
+force on tiny inputs. Each check is chosen so that a plausible slip -- a split at a
+block boundary instead of the midpoint, a dropped term, a transposed operand, an
+off-by-one window -- fails it.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import SEED, gemm_atol, pairwise_gamma
+
+
+def seq32(v: np.ndarray) -> np.float32:
+    """Sequential float32 sum from 0 (numpy's cumsum accumulates in order)."""
+    v = np.asarray(v, np.float32)
+    return np.float32(0.0) if v.size == 0 else np.cumsum(v, dtype=np.float32)[-1]
+
+
+def carry_fold(vals) -> np.float32:
+    """The reference's binary-counter push/drain (test_invariants.py:90-107)."""
+    stack, count = {}, 0
+    for v in vals:
+        block, c, level = np.float32(v), count, 0
+        while c & 1:
+            block = np.float32(block + stack[level])
+            c >>= 1
+            level += 1
+        stack[level] = block
+        count += 1
+    total, level = np.float32(0.0), 0
+    while (count >> level) != 0:
+        if (count >> level) & 1:
+            total = np.float32(total + stack[level])
+        level += 1
+    return total
+
+
+# ---------------------------------------------------------------------------
+# pairwise summation (reference reduce.h:55-72)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [0, 1, 2, 31, 32])
+def test_pairwise_base_case_is_sequential(n):
+    v = np.random.default_rng(n).standard_normal(n).astype(np.float32) * 1e3
+    assert O.pairwise_sum(v).tobytes() == seq32(v).tobytes()
+
+
+@pytest.mark.parametrize("n", [48, 50, 63])
+def test_pairwise_splits_at_the_midpoint(n):
+    """n in (32, 64]: one split at n//2, not at the 32-element block boundary."""
+    rng = np.random.default_rng(n)
+    hits = 0
+    for _ in range(40):
+        v = (rng.standard_normal(n) * 1e4).astype(np.float32)
+        want = np.float32(seq32(v[: n // 2]) + seq32(v[n // 2:]))
+        assert O.pairwise_sum(v).tobytes() == want.tobytes()
+        block_split = np.float32(seq32(v[:32]) + seq32(v[32:]))
+        hits += block_split.tobytes() != want.tobytes()
+    assert hits > 10, "test cannot tell a midpoint split from a block split"
+
+
+@pytest.mark.parametrize("q", [1, 2, 5, 7])
+def test_pairwise_equals_carry_stack_over_32_blocks(q):
+    """For n = 32 * 2^q the recursion is a balanced tree over 32-element
+    sequential blocks, i.e. the carry stack over block sums (the N1 theorem,
+    reference test_invariants.py:117-135)."""
+    n = 32 << q
+    v = (np.random.default_rng(q).standard_normal(n) * 1e3).astype(np.float32)
+    blocks = [seq32(v[i:i + 32]) for i in range(0, n, 32)]
+    assert O.pairwise_sum(v).tobytes() == carry_fold(blocks).tobytes()
+
+
+def test_pairwise_is_not_a_flat_sum():
+    rng = np.random.default_rng(11)
+    differ = 0
+    for _ in range(40):
+        v = (rng.standard_normal(4096) * 1e3).astype(np.float32)
+        differ += O.pairwise_sum(v).tobytes() != seq32(v).tobytes()
+    assert differ > 10
+
+
+@pytest.mark.parametrize("n", [100, 784, 1000, 4096, 32768, 65537])
+def test_pairwise_within_backward_bound(n):
+    v = np.random.default_rng(n).uniform(-2, 2, n).astype(np.float32)
+    exact = float(np.sum(v.astype(np.float64)))
+    bound = pairwise_gamma(n) * float(np.sum(np.abs(v.astype(np.float64))))
+    assert abs(float(O.pairwise_sum(v)) - exact) <= bound
+
+
+# ---------------------------------------------------------------------------
+# matmul (reference kernels_matmul.cpp:34-87)
+# ---------------------------------------------------------------------------
+
+def test_matmul_known_answer():
+    """reference test_ops.cpp:266-272."""
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    np.testing.assert_array_equal(O.matmul(a, b), [[58, 64], [139, 154]])
+
+
+def test_matmul_transposed_operand_known_answer():
+    """reference test_ops.cpp:274-280: b given as a transposed (strided) view."""
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    bt = np.array([[7, 9, 11], [8, 10, 12]], np.float32)
+    np.testing.assert_array_equal(O.matmul(a, bt.T), [[58, 64], [139, 154]])
+
+
+def test_matmul_vector_known_answers():
+    """reference test_ops.cpp:282-293 (rank-1 promoted to a row / a column)."""
+    m = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    v = np.ones((3, 1), np.float32)
+    u = np.ones((1, 2), np.float32)
+    np.testing.assert_array_equal(O.matmul(m, v).ravel(), [6, 15])
+    np.testing.assert_array_equal(O.matmul(u, m).ravel(), [5, 7, 9])
+    np.testing.assert_array_equal(O.matmul(v.T, v).ravel(), [3])
+
+
+def test_matmul_products_are_rounded_then_pairwise_summed():
+    """One output = pairwise sum of the individually rounded f32 products."""
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((3, 1000)).astype(np.float32)
+    b = rng.standard_normal((1000, 4)).astype(np.float32)
+    got = O.matmul(a, b)
+    for i in range(3):
+        for j in range(4):
+            prods = (a[i] * b[:, j]).astype(np.float32)
+            assert got[i, j].tobytes() == O.pairwise_sum(prods).tobytes()
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn", "tt"])
+def test_matmul_layouts_and_batch_broadcast_vs_float64(layout):
+    rng = np.random.default_rng(SEED + 1)
+    m, k, n = 37, 130, 29
+    a = rng.uniform(-2, 2, (m, k)).astype(np.float32)
+    b = rng.uniform(-2, 2, (k, n)).astype(np.float32)
+    av = np.ascontiguousarray(a.T).T if layout[0] == "t" else a
+    bv = np.ascontiguousarray(b.T).T if layout[1] == "t" else b
+    # batch-broadcast A (stride 0) against a real batch of B, as conv2d does
+    bb = np.stack([bv, bv * 2, -bv])
+    got = O.matmul(av[None], bb)
+    want = np.einsum("mk,bkn->bmn", a.astype(np.float64), bb.astype(np.float64))
+    assert np.max(np.abs(got - want)) <= gemm_atol(a, b * 2)
+
+
+def test_matmul_threads_do_not_change_bits():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((64, 300)).astype(np.float32)
+    b = rng.standard_normal((300, 48)).astype(np.float32)
+    assert O.matmul(a, b, threads=1).tobytes() == O.matmul(a, b, threads=8).tobytes()
+
+
+# ---------------------------------------------------------------------------
+# reductions (reference kernels_reduce.cpp:44-192)
+# ---------------------------------------------------------------------------
+
+def test_argmax_argmin_first_extremum_known_answer():
+    """reference test_ops.cpp:225-231."""
+    a = np.array([[1, 5, 5], [4, 2, 4]], np.float32)
+    np.testing.assert_array_equal(O.argmax(a, 1), [1, 0])
+    np.testing.assert_array_equal(O.argmin(a, 1), [0, 1])
+
+
+def test_argmax_skips_nan_and_max_returns_it():
+    """The CPU loops: argmax's strict `>` never selects NaN; max returns the
+    first NaN it meets (kernels_reduce.cpp:124-176)."""
+    x = np.array([[1.0, np.nan, 3.0, 2.0], [np.nan, np.nan, -np.inf, -np.inf]], np.float32)
+    np.testing.assert_array_equal(O.argmax(x, 1), [2, 0])
+    mx = O.amax(x, 1)
+    assert np.isnan(mx).all()
+
+
+def test_sum_is_pairwise_over_the_reduced_axes():
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((6, 5, 40)) * 100).astype(np.float32)
+    s = O.sum(x, [0, 2])  # reduced elements in row-major order of the reduced axes
+    for j in range(5):
+        assert s[j].tobytes() == O.pairwise_sum(x[:, j, :].ravel()).tobytes()
+    np.testing.assert_array_equal(O.mean(x, [0, 2]), s / np.float32(240))
+
+
+def test_max_min_are_exact_selections():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((33, 77)).astype(np.float32)
+    np.testing.assert_array_equal(O.amax(x, 1), x.max(1))
+    np.testing.assert_array_equal(O.amin(x, 0), x.min(0))
+    np.testing.assert_array_equal(O.argmax(x, 0), x.argmax(0))
+
+
+# ---------------------------------------------------------------------------
+# softmax (reference kernels_reduce.cpp:205-259)
+# ---------------------------------------------------------------------------
+
+STABILITY_INPUTS = {  # reference test_vulkan_kernels.py:808-817
+    "large positive": np.array([[1000.0, 1001.0, 1002.0]], dtype=np.float32),
+    "large negative": np.array([[-1000.0, -1001.0, -1002.0]], dtype=np.float32),
+    "mixed sign": np.array([[-500.0, 0.0, 500.0]], dtype=np.float32),
+    "identical": np.full((1, 8), 3.5, dtype=np.float32),
+    "identical zeros": np.zeros((1, 16), dtype=np.float32),
+    "extreme spread": np.array([[0.0, -300.0, -600.0, -900.0]], dtype=np.float32),
+    "single element": np.array([[42.0]], dtype=np.float32),
+    "tiny magnitudes": np.array([[1e-30, 2e-30, 3e-30]], dtype=np.float32),
+}
+
+
+@pytest.mark.parametrize("name", list(STABILITY_INPUTS))
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax_stability_vs_torch_float64(name, log):
+    x = STABILITY_INPUTS[name]
+    got = O.softmax(x, -1, log)
+    assert np.isfinite(got).all()
+    t = torch.from_numpy(x.astype(np.float64))
+    want = (torch.log_softmax if log else torch.softmax)(t, -1).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_softmax_known_answers():
+    """reference test_ops.cpp:233-264."""
+    s = O.softmax(np.array([[1, 2, 3], [1, 2, 3]], np.float32), 1)
+    np.testing.assert_allclose(s.sum(1), 1.0, rtol=1e-6)
+    big = O.softmax(np.array([1000, 1001, 1002], np.float32), 0)
+    small = O.softmax(np.array([0, 1, 2], np.float32), 0)
+    np.testing.assert_allclose(big, small, atol=1e-6)
+    ls = O.log_softmax(np.array([0.0, -200.0, -400.0], np.float32), 0)
+    assert np.isfinite(ls).all() and abs(ls[2] + 400.0) <= 400.0 * 1e-4
+
+
+def test_softmax_denominator_is_pairwise_and_strided_axes_work():
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((4, 300)) * 2).astype(np.float32)
+    got = O.softmax(x, -1)
+    for r in range(4):
+        peak = x[r].max()
+        e = np.exp(x[r] - peak).astype(np.float32)
+        denom = O.pairwise_sum(e)
+        np.testing.assert_allclose(got[r], e / denom, rtol=3e-7)
+    # softmax over axis 0 of a transposed view == softmax over axis -1 transposed
+    np.testing.assert_array_equal(O.softmax(np.ascontiguousarray(x.T), 0).T, O.softmax(x, -1))
+
+
+# ---------------------------------------------------------------------------
+# im2col / col2im / max-pool (reference kernels_movement.cpp:438-680)
+# ---------------------------------------------------------------------------
+
+WINDOWS = [  # reference test_vulkan_kernels.py:1303-1310
+    ((1, 1, 4, 4), (2, 2), (1, 1), (0, 0), (1, 1)),
+    ((2, 3, 5, 5), (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 2, 6, 6), (2, 2), (2, 2), (0, 0), (1, 1)),
+    ((2, 1, 7, 5), (3, 2), (2, 1), (1, 0), (1, 1)),
+    ((1, 2, 5, 5), (2, 2), (1, 1), (0, 0), (2, 2)),
+    ((1, 1, 17, 17), (3, 3), (1, 1), (1, 1), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("shape,kernel,stride,pad,dil", WINDOWS)
+def test_im2col_equals_torch_unfold(shape, kernel, stride, pad, dil):
+    x = np.random.default_rng(SEED).uniform(-3, 3, shape).astype(np.float32)
+    got = O.im2col(x, kernel, stride, pad, dil)
+    want = torch.nn.functional.unfold(torch.from_numpy(x), kernel, dil, pad, stride).numpy()
+    assert got.tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("shape,kernel,stride,pad,dil", WINDOWS)
+def test_col2im_is_the_adjoint_of_im2col(shape, kernel, stride, pad, dil):
+    """<im2col(x), y> == <x, col2im(y)> exactly, with small integers so every
+    f32 sum is exact."""
+    rng = np.random.default_rng(SEED + 2)
+    x = rng.integers(-4, 5, shape).astype(np.float32)
+    cols_shape = O.im2col(x, kernel, stride, pad, dil).shape
+    y = rng.integers(-4, 5, cols_shape).astype(np.float32)
+    lhs = float(np.sum(O.im2col(x, kernel, stride, pad, dil).astype(np.float64) * y))
+    rhs = float(np.sum(x.astype(np.float64) * O.col2im(y, shape[2:], kernel, stride, pad, dil)))
+    assert lhs == rhs
+    want = torch.nn.functional.fold(torch.from_numpy(y), shape[2:], kernel, dil, pad, stride)
+    np.testing.assert_array_equal(O.col2im(y, shape[2:], kernel, stride, pad, dil), want.numpy())
+
+
+def test_col2im_fold_order_fixture():
+    """reference test_vulkan_kernels.py:1342-1356: wide magnitudes expose the
+    ascending (ki, kj) fold; interior positions get all nine contributions."""
+    vals = np.array([1e8, 1.0, -1e8, 1e-8, 1.0, -1.0, 1e7, 1.0, -1e7], np.float32)
+    cols = np.zeros((1, 9, 16), np.float32)
+    cols[0, :, :] = vals[:, None]
+    got = O.col2im(cols, (4, 4), (3, 3), (1, 1), (1, 1))
+    # Position (h, w) receives row ki*3+kj when the window at (h+1-ki, w+1-kj) exists.
+    for h in range(4):
+        for w in range(4):
+            acc = np.float32(0.0)
+            for ki in range(3):
+                for kj in range(3):
+                    if 0 <= h + 1 - ki < 4 and 0 <= w + 1 - kj < 4:
+                        acc = np.float32(acc + vals[ki * 3 + kj])
+            assert got[0, 0, h, w].tobytes() == acc.tobytes()
+    # An order-insensitive float64 sum disagrees at the interior, which is what
+    # makes this fixture a test of order.
+    assert got[0, 0, 1, 1] != np.float32(np.sum(vals.astype(np.float64)))
+
+
+POOLS = [  # reference test_vulkan_kernels.py:1386-1392
+    ((1, 1, 4, 4), (2, 2), (2, 2), (0, 0)),
+    ((2, 3, 6, 6), (2, 2), (2, 2), (0, 0)),
+    ((1, 2, 5, 5), (3, 3), (1, 1), (1, 1)),
+    ((2, 1, 7, 5), (3, 2), (2, 1), (1, 0)),
+    ((1, 1, 17, 17), (3, 3), (2, 2), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("shape,kernel,stride,pad", POOLS)
+def test_max_pool2d_and_backward_vs_torch(shape, kernel, stride, pad):
+    x = np.random.default_rng(SEED).uniform(-3, 3, shape).astype(np.float32)
+    t = torch.from_numpy(x).requires_grad_(True)
+    y = torch.nn.functional.max_pool2d(t, kernel, stride, pad)
+    got = O.max_pool2d(x, kernel, stride, pad)
+    assert got.tobytes() == y.detach().numpy().tobytes()
+    g = np.random.default_rng(SEED + 1).uniform(-1, 1, got.shape).astype(np.float32)
+    y.backward(torch.from_numpy(g))
+    np.testing.assert_allclose(O.max_pool2d_backward(g, x, kernel, stride, pad), t.grad.numpy(),
+                               rtol=1e-6, atol=1e-7)
+
+
+def test_max_pool2d_tie_goes_to_the_first_maximum():
+    """reference test_vulkan_kernels.py:1440-1452."""
+    x = np.array([[[[5.0, 5.0], [1.0, 2.0]]]], np.float32)
+    g = O.max_pool2d_backward(np.ones((1, 1, 1, 1), np.float32), x, (2, 2))
+    np.testing.assert_array_equal(g, [[[[1, 0], [0, 0]]]])
+
+
+def test_max_pool2d_pads_with_minus_infinity():
+    """reference test_vulkan_kernels.py:1425-1437."""
+    x = -np.abs(np.random.default_rng(SEED).uniform(-3, 3, (1, 2, 5, 5))).astype(np.float32) - 1
+    got = O.max_pool2d(x, (3, 3), (1, 1), (1, 1))
+    assert not np.any(got == 0.0)
+
+
+# ---------------------------------------------------------------------------
+# split-K carry-stack fold (reference gemm_split_k_reduce.comp:48-85)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tiles", [1, 2, 3, 5, 8, 12, 17, 33, 129])
+def test_split_fold_power_of_two_chunks_equal_unsplit(tiles):
+    """The alignment theorem (reference test_invariants.py:117-135), on the
+    oracle's own fold: folding power-of-two chunks, then the chunk results,
+    equals one fold over everything."""
+    vals = (np.random.default_rng(tiles).standard_normal(tiles) * 1e3).astype(np.float32)
+    whole = O.split_k_fold(vals, tiles)
+    assert whole.tobytes() == carry_fold(vals).tobytes()
+    chunk = 1
+    while chunk <= tiles:
+        parts = [O.split_k_fold(vals[i:i + chunk], len(vals[i:i + chunk]))[0]
+                 for i in range(0, tiles, chunk)]
+        assert O.split_k_fold(np.array(parts, np.float32), len(parts)).tobytes() == whole.tobytes()
+        chunk *= 2
+
+
+def test_split_fold_is_a_balanced_tree_for_four():
+    v = (np.random.default_rng(4).standard_normal(4) * 1e3).astype(np.float32)
+    want = np.float32(np.float32(v[0] + v[1]) + np.float32(v[2] + v[3]))
+    assert O.split_k_fold(v, 4)[0].tobytes() == want.tobytes()
+
+
+def test_split_fold_non_power_of_two_chunks_break_identity():
+    """Negative control (reference test_invariants.py:138-163)."""
+    rng = np.random.default_rng(12)
+    mismatches = 0
+    for _ in range(60):
+        vals = (rng.standard_normal(97) * 1e3).astype(np.float32)
+        parts = [O.split_k_fold(vals[i:i + 5], len(vals[i:i + 5]))[0] for i in range(0, 97, 5)]
+        folded = O.split_k_fold(np.array(parts, np.float32), len(parts))
+        mismatches += folded.tobytes() != O.split_k_fold(vals, 97).tobytes()
+    assert mismatches > 15

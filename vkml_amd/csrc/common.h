@@ -1,0 +1,140 @@
+// Shared runtime state and helpers for the vkhip library (gfx950 only).
+//
+// One process, one device, one HIP stream: a graph flush becomes an ordered
+// launch sequence on that stream, which replaces the Vulkan recorder's per-node
+// global barrier (reference vulkan_backend.cpp:2667) with stream order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstring>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "vkhip.h"
+
+namespace vkhip {
+
+// Last error message, per host thread (vkhip_last_error).
+void set_error_msg(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+
+struct Context {
+    bool ready = false;
+    int device = -1;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;  // where launches go: own_stream or a host-provided one
+    vkhip_caps caps{};
+    // Split-K partials workspace, grown on demand and released stream-ordered
+    // (reference grows its own the same way, vulkan_backend.cpp:899-919).
+    float* ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+Context& ctx();
+
+// Returns VKHIP_OK or a failure code with the message set.
+int require_ready();
+
+// Workspace of at least `bytes` on the current stream.
+int workspace(size_t bytes, float** out);
+
+#define VKHIP_HIP(expr)                                                                   \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return ::vkhip::fail(VKHIP_ERR_DEVICE, "%s failed: %s (%s:%d)", #expr,         \
+                                 hipGetErrorString(e_), __FILE__, __LINE__);              \
+    } while (0)
+
+#define VKHIP_LAUNCH_CHECK()                                                              \
+    do {                                                                                  \
+        hipError_t e_ = hipGetLastError();                                                \
+        if (e_ != hipSuccess)                                                             \
+            return ::vkhip::fail(VKHIP_ERR_DEVICE, "kernel launch failed: %s (%s:%d)",    \
+                                 hipGetErrorString(e_), __FILE__, __LINE__);              \
+    } while (0)
+
+inline uint32_t ceil_div(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a + b - 1) / b); }
+
+// ---- device helpers --------------------------------------------------------
+
+// Offset (elements) of the `linear`-th element, row-major, of a rank-4
+// operand (reference linear_to_offset, src/backend/cpu/iterate.h:33-42).
+__device__ __forceinline__ int64_t lin_off4(uint64_t linear, const uint32_t ne[4],
+                                            const int64_t nb[4]) {
+    int64_t off = 0;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) {
+        const uint64_t e = ne[i];
+        off += static_cast<int64_t>(linear % e) * nb[i];
+        linear /= e;
+    }
+    return off;
+}
+
+// Rank-4 operand passed by value to kernels.
+struct Op4 {
+    uint32_t ne[4];
+    int64_t nb[4];
+};
+
+inline Op4 to_op4(const vkhip_operand& d) {
+    Op4 o;
+    for (int i = 0; i < 4; ++i) {
+        o.ne[i] = d.ne[i];
+        o.nb[i] = d.nb[i];
+    }
+    return o;
+}
+
+inline uint64_t numel(const vkhip_operand& d) {
+    return static_cast<uint64_t>(d.ne[0]) * d.ne[1] * d.ne[2] * d.ne[3];
+}
+
+// Pairwise-summation geometry, shared by every kernel that reproduces the CPU
+// oracle's association (reference pairwise_sum, src/backend/cpu/reduce.h:55-72:
+// split [b,e) at b + n/2 until n <= 32, sum each leaf sequentially from 0).
+//
+// The recursion tree is laid out as a complete binary tree of depth D, where D
+// is the smallest depth at which every range has <= 32 elements. Leaf j (0..2^D-1)
+// follows the bits of j from the top; a range that became a leaf at a shallower
+// depth is carried whole by its leftmost depth-D descendant, and every other
+// descendant carries +0.0. Adding +0.0 is exact for every sum that starts from
+// +0.0 (such a sum is never -0.0), so combining the 2^D leaf values pairwise,
+// adjacent first, performs exactly the oracle's additions.
+__host__ __device__ __forceinline__ int pairwise_depth(uint32_t n) {
+    int d = 0;
+    // ceil(n / 2^d) is the largest range at depth d.
+    while (((static_cast<uint64_t>(n) + (1ull << d) - 1) >> d) > 32u) ++d;
+    return d;
+}
+
+// Range [begin, end) of depth-D leaf `j` of a length-n pairwise tree; empty
+// (begin == end) for descendants of a shallower leaf other than its leftmost.
+__host__ __device__ __forceinline__ void pairwise_leaf(uint32_t n, int depth, uint32_t j,
+                                                       uint32_t& begin, uint32_t& end) {
+    uint32_t b = 0, e = n;
+    for (int lvl = depth - 1; lvl >= 0; --lvl) {
+        const uint32_t bit = (j >> lvl) & 1u;
+        if (e - b <= 32u) {
+            // Already a leaf: only the all-zeros path below it carries it.
+            if (j & ((2u << lvl) - 1u)) {
+                b = e;
+            }
+            break;
+        }
+        const uint32_t mid = b + (e - b) / 2;
+        if (bit) {
+            b = mid;
+        } else {
+            e = mid;
+        }
+    }
+    begin = b;
+    end = e;
+}
+
+}  // namespace vkhip

@@ -1,0 +1,286 @@
+// Elementwise support ops the training steps need on the device (the
+// reference has no CPU fallback, executor.cpp:107-124): unary (neg, exp, log,
+// relu, copy), binary (add, sub, mul, div, maximum, minimum, scaled_add),
+// comparisons -> bool, where, cast, fill, arange.
+//
+// Semantics follow the CPU oracle (reference kernels_elementwise.cpp:160-300,
+// kernels_movement.cpp:100-200): relu is `x <= 0 ? 0 : x` (NaN propagates);
+// maximum/minimum return NaN if either side is NaN; scaled_add is two rounded
+// multiplies and one rounded add (never an FMA); arange computes start + i*step
+// in double and rounds once. Outputs are contiguous; sources arrive already
+// broadcast to the output extents as strides (stride 0 on broadcast axes).
+#include "common.h"
+
+namespace vkhip {
+
+struct Src {
+    const void* p;
+    int32_t dtype;
+    int32_t contig;
+    Op4 d;
+};
+
+struct EwArgs {
+    int32_t op;
+    int32_t out_dtype;
+    void* out;
+    uint64_t n;
+    Src s[3];
+    float alpha, beta;
+    double d0, d1;
+};
+
+__device__ __forceinline__ int64_t src_off(const Src& s, uint64_t i) {
+    return s.contig ? static_cast<int64_t>(i) : lin_off4(i, s.d.ne, s.d.nb);
+}
+
+__device__ __forceinline__ float load_f(const Src& s, uint64_t i) {
+    const int64_t off = src_off(s, i);
+    switch (s.dtype) {
+        case VKHIP_I64: return static_cast<float>(static_cast<const int64_t*>(s.p)[off]);
+        case VKHIP_BOOL: return static_cast<const uint8_t*>(s.p)[off] != 0 ? 1.0f : 0.0f;
+        case VKHIP_I32: return static_cast<float>(static_cast<const int32_t*>(s.p)[off]);
+        default: return static_cast<const float*>(s.p)[off];
+    }
+}
+
+__device__ __forceinline__ void store_out(const EwArgs& a, uint64_t i, float v) {
+    switch (a.out_dtype) {
+        case VKHIP_I64: static_cast<int64_t*>(a.out)[i] = static_cast<int64_t>(v); break;
+        case VKHIP_BOOL: static_cast<uint8_t*>(a.out)[i] = v != 0.0f ? 1 : 0; break;
+        default: static_cast<float*>(a.out)[i] = v; break;
+    }
+}
+
+__global__ __launch_bounds__(256) void elementwise_kernel(EwArgs a) {
+    const uint64_t base = (static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint64_t i = base + j;
+        if (i >= a.n) return;
+        switch (a.op) {
+            case VKHIP_OP_FULL:
+                if (a.out_dtype == VKHIP_I64)
+                    static_cast<int64_t*>(a.out)[i] = static_cast<int64_t>(a.d0);
+                else if (a.out_dtype == VKHIP_BOOL)
+                    static_cast<uint8_t*>(a.out)[i] = a.d0 != 0.0 ? 1 : 0;
+                else
+                    static_cast<float*>(a.out)[i] = static_cast<float>(a.d0);
+                break;
+            case VKHIP_OP_ARANGE: {
+                const double v = a.d0 + static_cast<double>(i) * a.d1;
+                if (a.out_dtype == VKHIP_I64)
+                    static_cast<int64_t*>(a.out)[i] = static_cast<int64_t>(v);
+                else
+                    static_cast<float*>(a.out)[i] = static_cast<float>(v);
+                break;
+            }
+            case VKHIP_OP_CONTIGUOUS:
+                if (a.out_dtype == VKHIP_I64)
+                    static_cast<int64_t*>(a.out)[i] =
+                        static_cast<const int64_t*>(a.s[0].p)[src_off(a.s[0], i)];
+                else if (a.out_dtype == VKHIP_BOOL)
+                    static_cast<uint8_t*>(a.out)[i] =
+                        static_cast<const uint8_t*>(a.s[0].p)[src_off(a.s[0], i)];
+                else
+                    static_cast<float*>(a.out)[i] =
+                        static_cast<const float*>(a.s[0].p)[src_off(a.s[0], i)];
+                break;
+            case VKHIP_OP_CAST:
+                if (a.s[0].dtype == VKHIP_F32 && a.out_dtype == VKHIP_I64)
+                    static_cast<int64_t*>(a.out)[i] = static_cast<int64_t>(
+                        static_cast<const float*>(a.s[0].p)[src_off(a.s[0], i)]);
+                else
+                    store_out(a, i, load_f(a.s[0], i));
+                break;
+            case VKHIP_OP_NEG: store_out(a, i, -load_f(a.s[0], i)); break;
+            case VKHIP_OP_EXP: store_out(a, i, expf(load_f(a.s[0], i))); break;
+            case VKHIP_OP_LOG: store_out(a, i, logf(load_f(a.s[0], i))); break;
+            case VKHIP_OP_RELU: {
+                const float x = load_f(a.s[0], i);
+                store_out(a, i, x <= 0.0f ? 0.0f : x);
+                break;
+            }
+            case VKHIP_OP_ADD: store_out(a, i, __fadd_rn(load_f(a.s[0], i), load_f(a.s[1], i))); break;
+            case VKHIP_OP_SUB: store_out(a, i, __fsub_rn(load_f(a.s[0], i), load_f(a.s[1], i))); break;
+            case VKHIP_OP_MUL: store_out(a, i, __fmul_rn(load_f(a.s[0], i), load_f(a.s[1], i))); break;
+            case VKHIP_OP_DIV: store_out(a, i, load_f(a.s[0], i) / load_f(a.s[1], i)); break;
+            case VKHIP_OP_SCALED_ADD:
+                store_out(a, i,
+                          __fadd_rn(__fmul_rn(load_f(a.s[0], i), a.alpha),
+                                    __fmul_rn(load_f(a.s[1], i), a.beta)));
+                break;
+            case VKHIP_OP_MAXIMUM:
+            case VKHIP_OP_MINIMUM: {
+                const float x = load_f(a.s[0], i), y = load_f(a.s[1], i);
+                float r;
+                if (x != x || y != y)
+                    r = __builtin_nanf("");
+                else if (a.op == VKHIP_OP_MAXIMUM)
+                    r = x > y ? x : y;
+                else
+                    r = x < y ? x : y;
+                store_out(a, i, r);
+                break;
+            }
+            case VKHIP_OP_EQUAL:
+            case VKHIP_OP_LESS:
+            case VKHIP_OP_GREATER:
+            case VKHIP_OP_LESS_EQUAL:
+            case VKHIP_OP_GREATER_EQUAL:
+            case VKHIP_OP_NOT_EQUAL: {
+                const float x = load_f(a.s[0], i), y = load_f(a.s[1], i);
+                bool r = false;
+                switch (a.op) {
+                    case VKHIP_OP_EQUAL: r = x == y; break;
+                    case VKHIP_OP_LESS: r = x < y; break;
+                    case VKHIP_OP_GREATER: r = x > y; break;
+                    case VKHIP_OP_LESS_EQUAL: r = x <= y; break;
+                    case VKHIP_OP_GREATER_EQUAL: r = x >= y; break;
+                    default: r = x != y; break;
+                }
+                static_cast<uint8_t*>(a.out)[i] = r ? 1 : 0;
+                break;
+            }
+            case VKHIP_OP_WHERE: {
+                const bool c = static_cast<const uint8_t*>(a.s[0].p)[src_off(a.s[0], i)] != 0;
+                store_out(a, i, c ? load_f(a.s[1], i) : load_f(a.s[2], i));
+                break;
+            }
+            default: break;
+        }
+    }
+}
+
+// Contiguous f32 fast path for the ops on the optimiser and activation paths:
+// 16-byte loads and stores, no index decoding.
+__global__ __launch_bounds__(256) void elementwise_f32_vec_kernel(int op, const float* __restrict__ x,
+                                                                  const float* __restrict__ y,
+                                                                  float* __restrict__ out,
+                                                                  uint64_t n4, float alpha,
+                                                                  float beta) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const f32x4 a = reinterpret_cast<const f32x4*>(x)[i];
+    f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (y) b = reinterpret_cast<const f32x4*>(y)[i];
+    f32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        switch (op) {
+            case VKHIP_OP_ADD: r[j] = __fadd_rn(a[j], b[j]); break;
+            case VKHIP_OP_SUB: r[j] = __fsub_rn(a[j], b[j]); break;
+            case VKHIP_OP_MUL: r[j] = __fmul_rn(a[j], b[j]); break;
+            case VKHIP_OP_SCALED_ADD:
+                r[j] = __fadd_rn(__fmul_rn(a[j], alpha), __fmul_rn(b[j], beta));
+                break;
+            case VKHIP_OP_RELU: r[j] = a[j] <= 0.0f ? 0.0f : a[j]; break;
+            case VKHIP_OP_NEG: r[j] = -a[j]; break;
+            default: r[j] = a[j]; break;  // contiguous copy
+        }
+    }
+    reinterpret_cast<f32x4*>(out)[i] = r;
+}
+
+static bool is_contig(const vkhip_tensor& t) {
+    int64_t expect = 1;
+    for (int i = t.ndim - 1; i >= 0; --i) {
+        if (t.ne[i] == 1) continue;
+        if (t.nb[i] != expect) return false;
+        expect *= t.ne[i];
+    }
+    return true;
+}
+
+static uint64_t tnumel(const vkhip_tensor& t) {
+    uint64_t n = 1;
+    for (int i = 0; i < t.ndim; ++i) n *= static_cast<uint64_t>(t.ne[i]);
+    return n;
+}
+
+static Src make_src(const vkhip_tensor& t) {
+    Src s{};
+    s.p = t.data;
+    s.dtype = t.dtype;
+    s.contig = is_contig(t) ? 1 : 0;
+    const int pad = 4 - t.ndim;
+    for (int i = 0; i < 4; ++i) {
+        s.d.ne[i] = 1;
+        s.d.nb[i] = 0;
+    }
+    for (int i = 0; i < t.ndim; ++i) {
+        s.d.ne[pad + i] = static_cast<uint32_t>(t.ne[i]);
+        s.d.nb[pad + i] = t.nb[i];
+    }
+    return s;
+}
+
+int launch_elementwise(const vkhip_node& nd) {
+    const uint64_t n = tnumel(nd.out);
+    if (n == 0) return VKHIP_OK;
+    float ab[2] = {1.0f, 1.0f};
+    double dd[2] = {0.0, 0.0};
+    memcpy(ab, nd.params, sizeof ab);
+    memcpy(dd, nd.params, sizeof dd);
+    hipStream_t st = ctx().stream;
+
+    // Vector fast path: f32, everything contiguous and 16-byte aligned.
+    const int op = nd.op;
+    const bool vec_op = op == VKHIP_OP_ADD || op == VKHIP_OP_SUB || op == VKHIP_OP_MUL ||
+                        op == VKHIP_OP_SCALED_ADD || op == VKHIP_OP_RELU || op == VKHIP_OP_NEG ||
+                        op == VKHIP_OP_CONTIGUOUS;
+    if (vec_op && n % 4 == 0 && nd.out.dtype == VKHIP_F32) {
+        bool ok = reinterpret_cast<uintptr_t>(nd.out.data) % 16 == 0;
+        for (int s = 0; s < nd.n_src && ok; ++s)
+            ok = nd.src[s].dtype == VKHIP_F32 && is_contig(nd.src[s]) && tnumel(nd.src[s]) == n &&
+                 reinterpret_cast<uintptr_t>(nd.src[s].data) % 16 == 0;
+        if (ok) {
+            const uint64_t n4 = n / 4;
+            hipLaunchKernelGGL(elementwise_f32_vec_kernel, dim3(ceil_div(n4, 256)), dim3(256), 0, st,
+                               op, static_cast<const float*>(nd.src[0].data),
+                               nd.n_src > 1 ? static_cast<const float*>(nd.src[1].data) : nullptr,
+                               static_cast<float*>(nd.out.data), n4, ab[0], ab[1]);
+            VKHIP_LAUNCH_CHECK();
+            return VKHIP_OK;
+        }
+    }
+    EwArgs a{};
+    a.op = op;
+    a.out_dtype = nd.out.dtype;
+    a.out = nd.out.data;
+    a.n = n;
+    for (int s = 0; s < nd.n_src && s < 3; ++s) a.s[s] = make_src(nd.src[s]);
+    a.alpha = ab[0];
+    a.beta = ab[1];
+    a.d0 = dd[0];
+    a.d1 = dd[1];
+    const uint64_t threads = (n + 3) / 4;
+    hipLaunchKernelGGL(elementwise_kernel, dim3(ceil_div(threads, 256)), dim3(256), 0, st, a);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+}  // namespace vkhip
+
+extern "C" int vkhip_scaled_add(const float* a, const float* b, float* out, uint64_t n, float alpha,
+                                float beta) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    vkhip_node nd{};
+    nd.op = VKHIP_OP_SCALED_ADD;
+    nd.n_src = 2;
+    auto flat = [n](vkhip_tensor& t, const void* p) {
+        t.data = const_cast<void*>(p);
+        t.dtype = VKHIP_F32;
+        t.ndim = 1;
+        t.ne[0] = static_cast<int64_t>(n);
+        t.nb[0] = 1;
+    };
+    flat(nd.out, out);
+    flat(nd.src[0], a);
+    flat(nd.src[1], b);
+    memcpy(nd.params, &alpha, sizeof alpha);
+    memcpy(nd.params + sizeof alpha, &beta, sizeof beta);
+    return vkhip::launch_elementwise(nd);
+}

@@ -1,0 +1,551 @@
+// fp32 GEMM family on CDNA4 matrix cores: MFMA tiles, split-K with a
+// deterministic carry-stack reduce, and a bandwidth GEMV.
+//
+// Replaces the reference's gemm_naive/gemm_tiled/gemm_reg/gemm_db shaders and
+// their selection (reference vulkan_backend.cpp:2056-2657). The reference folds
+// K with a per-accumulator carry stack in rounded (no-FMA) arithmetic; matrix
+// cores accumulate in hardware order, so GEMM parity with the CPU oracle is
+// tolerance-based (normwise, 1e-5*sqrt(K)), while split-K stays bit-stable for
+// a fixed split count.
+//
+// Tile scheme (v_mfma_f32_32x32x2_f32, wave64):
+//   - a 256-thread workgroup owns a BM x BN output tile, 4 waves in a 2x2
+//     grid, each wave a WM x WN sub-tile of 32x32 MFMA blocks;
+//   - both operands are staged in LDS as [row][k] (k contiguous, row pitch
+//     BK+4 floats) so every lane reads its MFMA operands as 16-byte
+//     ds_read_b128; the +4 pad spreads 8 consecutive rows over distinct banks;
+//   - A K-tile is loaded to registers while the previous one is multiplied,
+//     then stored to the other LDS buffer: one barrier per K-tile;
+//   - inside a K-tile, lane half h (lanes 32..63) supplies k in the upper half
+//     of the tile, so each lane's k values are contiguous in LDS. The sum over
+//     k is unchanged; only the order MFMA visits the k values differs.
+#include "common.h"
+
+namespace vkhip {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    const float* a;
+    const float* b;
+    float* c;
+    int64_t sa0, sa1, sam, sak;  // A strides: batch0, batch1, m, k (elements)
+    int64_t sb0, sb1, sbk, sbn;  // B strides: batch0, batch1, k, n
+    uint32_t b1;                 // extent of batch axis 1
+    uint32_t m, n, k;
+    uint32_t tiles_m, tiles_n;
+    uint32_t ktiles;             // ceil(K / BK)
+    uint32_t chunk;              // K-tiles per split partition
+    uint64_t split_stride;       // elements between partition slices of c
+    uint32_t a_vec, b_vec;       // 16-byte loads along k are legal
+};
+
+// Loads one BK-deep tile of an operand (rows x BK) into registers as groups of
+// four consecutive k. KC: the operand is k-contiguous, so lanes walk k first
+// and load 16 bytes each. Otherwise lanes walk rows, so a 4-byte load per k is
+// coalesced along the row axis (the m- or n-contiguous transposed operand).
+template <int R, int BK, bool KC>
+struct TileLoader {
+    static constexpr int kGroups = R * BK / 4;
+    static constexpr int kPer = kGroups / 256;
+    static_assert(kGroups % 256 == 0, "tile must split evenly over 256 threads");
+
+    __device__ __forceinline__ static void row_kq(int g, int& r, int& kq) {
+        if (KC) {
+            kq = g % (BK / 4);
+            r = g / (BK / 4);
+        } else {
+            r = g % R;
+            kq = g / R;
+        }
+    }
+
+    __device__ __forceinline__ static void load(f32x4 (&v)[kPer], const float* base, int64_t s_row,
+                                                int64_t s_k, uint32_t row0, uint32_t rows,
+                                                uint32_t k0, uint32_t kdim, bool vec, int tid) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            int r, kq;
+            row_kq(tid + 256 * i, r, kq);
+            const uint32_t gr = row0 + r;
+            const uint32_t gk = k0 + 4 * kq;
+            const float* p = base + static_cast<int64_t>(gr) * s_row + static_cast<int64_t>(gk) * s_k;
+            if (KC && vec && gr < rows && gk + 3 < kdim) {
+                v[i] = *reinterpret_cast<const f32x4*>(p);
+            } else {
+                f32x4 t;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    t[j] = (gr < rows && gk + j < kdim) ? p[j * s_k] : 0.0f;
+                }
+                v[i] = t;
+            }
+        }
+    }
+
+    __device__ __forceinline__ static void store(const f32x4 (&v)[kPer], float* lds, int tid) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            int r, kq;
+            row_kq(tid + 256 * i, r, kq);
+            *reinterpret_cast<f32x4*>(lds + r * (BK + 4) + 4 * kq) = v[i];
+        }
+    }
+};
+
+template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
+    static_assert((BM / WM) * (BN / WN) == 4, "four waves per workgroup");
+    constexpr int LDK = BK + 4;
+    constexpr int MI = WM / 32;
+    constexpr int NI = WN / 32;
+    using LA = TileLoader<BM, BK, AKC>;
+    using LB = TileLoader<BN, BK, BKC>;
+
+    __shared__ __attribute__((aligned(16))) float lds[2][(BM + BN) * LDK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = (wave / (BN / WN)) * WM;
+    const int wn0 = (wave % (BN / WN)) * WN;
+
+    // Tile order: contiguous tile ranges per XCD (workgroups are dealt to the
+    // 8 XCDs round-robin), and within a range, groups of 8 tile-rows so that
+    // co-resident tiles share A and B panels in that XCD's L2.
+    const uint32_t ntiles = g.tiles_m * g.tiles_n;
+    uint32_t bid = blockIdx.x;
+    if ((ntiles & 7u) == 0) bid = (bid & 7u) * (ntiles >> 3) + (bid >> 3);
+    const uint32_t group_span = 8u * g.tiles_n;
+    const uint32_t first_m = (bid / group_span) * 8u;
+    const uint32_t gsize = min(g.tiles_m - first_m, 8u);
+    const uint32_t tm = first_m + (bid % group_span) % gsize;
+    const uint32_t tn = (bid % group_span) / gsize;
+    const uint32_t row0 = tm * BM;
+    const uint32_t col0 = tn * BN;
+
+    const uint32_t z = blockIdx.z;
+    const uint32_t i0 = z / g.b1, i1 = z % g.b1;
+    const float* abase = g.a + i0 * g.sa0 + i1 * g.sa1;
+    const float* bbase = g.b + i0 * g.sb0 + i1 * g.sb1;
+    float* cbase = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride +
+                   static_cast<uint64_t>(z) * g.m * g.n;
+
+    const uint32_t kt0 = blockIdx.y * g.chunk;
+    const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
+
+    f32x16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    f32x4 ra[LA::kPer], rb[LB::kPer];
+    if (kt0 < kt1) {
+        LA::load(ra, abase, g.sam, g.sak, row0, g.m, kt0 * BK, g.k, g.a_vec, tid);
+        LB::load(rb, bbase, g.sbn, g.sbk, col0, g.n, kt0 * BK, g.k, g.b_vec, tid);
+        LA::store(ra, lds[0], tid);
+        LB::store(rb, lds[0] + BM * LDK, tid);
+    }
+    __syncthreads();
+
+    const int lrow = lane & 31;
+    const int kh = lane >> 5;
+    for (uint32_t kt = kt0; kt < kt1; ++kt) {
+        const int cur = (kt - kt0) & 1;
+        const bool more = kt + 1 < kt1;
+        if (more) {
+            LA::load(ra, abase, g.sam, g.sak, row0, g.m, (kt + 1) * BK, g.k, g.a_vec, tid);
+            LB::load(rb, bbase, g.sbn, g.sbk, col0, g.n, (kt + 1) * BK, g.k, g.b_vec, tid);
+        }
+        const float* As = lds[cur];
+        const float* Bs = lds[cur] + BM * LDK;
+#pragma unroll
+        for (int q = 0; q < BK / 8; ++q) {
+            f32x4 av[MI], bv[NI];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+                av[i] = *reinterpret_cast<const f32x4*>(As + (wm0 + 32 * i + lrow) * LDK +
+                                                        kh * (BK / 2) + 4 * q);
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+                bv[j] = *reinterpret_cast<const f32x4*>(Bs + (wn0 + 32 * j + lrow) * LDK +
+                                                        kh * (BK / 2) + 4 * q);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NI; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bv[j][s],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            LA::store(ra, lds[cur ^ 1], tid);
+            LB::store(rb, lds[cur ^ 1] + BM * LDK, tid);
+        }
+        __syncthreads();
+    }
+
+    // 32x32 accumulator layout: register r of lane l holds
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const uint32_t col = col0 + wn0 + 32 * j + lrow;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = row0 + wm0 + 32 * i + 8 * (r / 4) + 4 * kh + (r % 4);
+                if (row < g.m && col < g.n) cbase[static_cast<uint64_t>(row) * g.n + col] = acc[i][j][r];
+            }
+        }
+}
+
+// ---- split-K partial fold --------------------------------------------------
+// Per output: the binary-counter carry stack over the `splits` partial slices,
+// drained in ascending level order from 0.0 (reference
+// gemm_split_k_reduce.comp:48-85). Unrolled over a fixed number of levels so
+// the stack lives in registers.
+constexpr int kSplitLevels = 9;  // up to 511 partitions
+
+__global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __restrict__ ws,
+                                                             float* __restrict__ dst, uint64_t ne,
+                                                             uint32_t splits) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= ne) return;
+    float stack[kSplitLevels];
+#pragma unroll
+    for (int l = 0; l < kSplitLevels; ++l) stack[l] = 0.0f;
+    uint32_t count = 0;
+    for (uint32_t s = 0; s < splits; ++s) {
+        float block = ws[static_cast<uint64_t>(s) * ne + i];
+        bool carry = true;
+#pragma unroll
+        for (int l = 0; l < kSplitLevels; ++l) {
+            if (carry) {
+                if ((count >> l) & 1u) {
+                    block = block + stack[l];
+                } else {
+                    stack[l] = block;
+                    carry = false;
+                }
+            }
+        }
+        ++count;
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int l = 0; l < kSplitLevels; ++l)
+        if ((count >> l) & 1u) total = total + stack[l];
+    dst[i] = total;
+}
+
+// ---- GEMV -------------------------------------------------------------------
+// y[row] = sum_k A[row,k] * x[k]: one wave per row. The row is streamed once
+// with 16-byte loads into LDS, products are rounded to f32 separately (no FMA,
+// as the oracle's widen(a)*widen(b)), and summed in the oracle's pairwise tree:
+// lanes own depth-D leaves, then adjacent leaves combine by xor-butterfly.
+// Bit-exact against the CPU oracle.
+constexpr int kGemvMaxK = 4096;  // LDS-staged row length per wave (+1 pad per 32)
+
+__device__ __forceinline__ float wave_butterfly_sum(float v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ a, int64_t lda,
+                                                   const float* __restrict__ x, int64_t incx,
+                                                   float* __restrict__ y, uint32_t m, uint32_t k,
+                                                   int depth, int vec) {
+    __shared__ float prod[4][kGemvMaxK + kGemvMaxK / 32];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + wave;
+    const bool live = row < m;
+    float* pr = prod[wave];
+    if (live) {
+        const float* ar = a + static_cast<int64_t>(row) * lda;
+        if (vec) {
+            for (uint32_t c = 4 * lane; c < k; c += 256) {
+                const f32x4 av = *reinterpret_cast<const f32x4*>(ar + c);
+                f32x4 xv;
+                if (incx == 1) {
+                    xv = *reinterpret_cast<const f32x4*>(x + c);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) xv[j] = x[static_cast<int64_t>(c + j) * incx];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t e = c + j;
+                    pr[e + (e >> 5)] = __fmul_rn(av[j], xv[j]);
+                }
+            }
+        } else {
+            for (uint32_t e = lane; e < k; e += 64)
+                pr[e + (e >> 5)] = __fmul_rn(ar[e], x[static_cast<int64_t>(e) * incx]);
+        }
+    }
+    __syncthreads();
+    if (!live) return;
+    // Leaves: 2^depth of them; lane l owns leaves [l*per, (l+1)*per).
+    const uint32_t leaves = 1u << depth;
+    const uint32_t per = leaves > 64 ? leaves / 64 : 1;
+    float v = 0.0f;
+    if (static_cast<uint32_t>(lane) * per < leaves) {
+        // Carry stack over this lane's `per` leaves (a power of two: one
+        // balanced subtree, whose total ends at level log2(per)).
+        float stack[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) stack[l] = 0.0f;
+        for (uint32_t t = 0; t < per; ++t) {
+            uint32_t b, e;
+            pairwise_leaf(k, depth, lane * per + t, b, e);
+            float s = 0.0f;
+            for (uint32_t q = b; q < e; ++q) s = s + pr[q + (q >> 5)];
+            bool carry = true;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                if (carry) {
+                    if ((t >> l) & 1u) {
+                        s = stack[l] + s;
+                    } else {
+                        stack[l] = s;
+                        carry = false;
+                    }
+                }
+            }
+        }
+        int top = 0;
+        while ((1u << top) < per) ++top;
+#pragma unroll
+        for (int l = 0; l < 8; ++l)
+            if (l == top) v = stack[l];
+    }
+    v = wave_butterfly_sum(v);
+    if (lane == 0) y[row] = v;
+}
+
+// ---- planning ---------------------------------------------------------------
+
+// Split-K plan (reference plan_split_k, vulkan_backend.cpp:596-647), restated
+// for MI355X. Same structure: split only when K-tiles >= output tiles; chunk =
+// largest power of two of K-tiles giving at least `target` partitions, raised to
+// >= 4 K-tiles; workspace capped at 64 MiB. What changes is the target: the
+// reference aims at 8 workgroups per CU capped at 16 partitions (a 36-CU RDNA1
+// part); a 256-CU MI355X needs about two 256-thread MFMA workgroups per CU, so
+// the target is 512 resident workgroups, capped at 256 partitions.
+static void plan_split_k(uint32_t tiles, uint32_t ktiles, uint64_t out_elems, uint32_t cu,
+                         uint32_t requested, uint32_t& splits, uint32_t& chunk) {
+    splits = 1;
+    chunk = ktiles;
+    if (ktiles < 2 || tiles == 0) return;
+    uint32_t target = requested;
+    if (target == 0) {
+        if (ktiles < tiles) return;
+        const uint32_t slots = (cu ? cu : 256) * 2;
+        target = slots / (tiles ? tiles : 1);
+        if (target < 2) target = 2;
+        if (target > 256) target = 256;
+    }
+    uint32_t c = 1;
+    while (c * 2 <= ktiles / target) c *= 2;
+    if (c < 4 && requested == 0) c = 4;
+    if (c >= ktiles) return;
+    const uint32_t s = (ktiles + c - 1) / c;
+    if (s < 2 || s > 511) return;
+    constexpr uint64_t kMaxWorkspaceBytes = 64ull * 1024 * 1024;
+    if (out_elems * s * sizeof(float) > kMaxWorkspaceBytes) return;
+    splits = s;
+    chunk = c;
+}
+
+struct TileChoice {
+    int bm, bn;
+};
+
+static TileChoice choose_tile(uint32_t m, uint32_t n) {
+    // Large outputs: 128x128 tiles (64x64 per wave). Small ones: 64x64 tiles
+    // so that the grid still spreads over the CUs.
+    if (static_cast<uint64_t>(m) * n >= 512ull * 512ull) return {128, 128};
+    return {64, 64};
+}
+
+template <int BM, int BN, int WM, int WN>
+static int launch_tiles(const GemmArgs& g, uint32_t batch, uint32_t splits, bool akc, bool bkc) {
+    constexpr int BK = 32;
+    dim3 grid(g.tiles_m * g.tiles_n, splits, batch);
+    hipStream_t st = ctx().stream;
+    if (akc && bkc)
+        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, true, true>), grid, dim3(256), 0, st, g);
+    else if (akc)
+        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, true, false>), grid, dim3(256), 0, st, g);
+    else if (bkc)
+        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, false, true>), grid, dim3(256), 0, st, g);
+    else
+        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, false, false>), grid, dim3(256), 0, st, g);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
+    if (ne == 0) return VKHIP_OK;
+    hipLaunchKernelGGL(split_k_reduce_kernel, dim3(ceil_div(ne, 256)), dim3(256), 0, ctx().stream,
+                       ws, dst, ne, splits);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+int launch_gemv(const float* a, int64_t lda, const float* x, int64_t incx, float* y, uint32_t m,
+                uint32_t k) {
+    if (m == 0) return VKHIP_OK;
+    if (k > static_cast<uint32_t>(kGemvMaxK))
+        return fail(VKHIP_ERR_UNSUPPORTED, "gemv: K=%u exceeds the LDS-staged maximum %d", k,
+                    kGemvMaxK);
+    const bool vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) && (lda % 4 == 0) && (k % 4 == 0) &&
+                     (incx != 1 || reinterpret_cast<uintptr_t>(x) % 16 == 0);
+    const int depth = pairwise_depth(k);
+    hipLaunchKernelGGL(gemv_kernel, dim3(ceil_div(m, 4)), dim3(256), 0, ctx().stream, a, lda, x,
+                       incx, y, m, k, depth, vec ? 1 : 0);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_request,
+              uint32_t& splits, uint32_t& chunk, TileChoice& tile) {
+    constexpr uint32_t BK = 32;
+    tile = choose_tile(m, n);
+    const uint32_t tiles = ceil_div(m, tile.bm) * ceil_div(n, tile.bn) * batch;
+    const uint32_t ktiles = ceil_div(k, BK);
+    splits = 1;
+    chunk = ktiles > 0 ? ktiles : 1;
+    if (split_request == 1) return VKHIP_OK;  // OFF
+    const uint32_t req = split_request > 1 ? static_cast<uint32_t>(split_request) : 0u;
+    const uint32_t cu = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
+    plan_split_k(tiles, ktiles, static_cast<uint64_t>(m) * n * batch, cu, req, splits, chunk);
+    if (splits == 1) chunk = ktiles > 0 ? ktiles : 1;
+    return VKHIP_OK;
+}
+
+int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd,
+         float* c, const vkhip_gemm_opts* opts) {
+    const uint32_t b0 = ad.ne[0] > bd.ne[0] ? ad.ne[0] : bd.ne[0];
+    const uint32_t b1 = ad.ne[1] > bd.ne[1] ? ad.ne[1] : bd.ne[1];
+    const uint32_t m = ad.ne[2], k = ad.ne[3], n = bd.ne[3];
+    if (bd.ne[2] != k)
+        return fail(VKHIP_ERR_INVALID, "matmul inner dimensions disagree: %u vs %u", k, bd.ne[2]);
+    for (int i = 0; i < 2; ++i) {
+        if ((ad.ne[i] != 1 && ad.ne[i] != (i ? b1 : b0)) || (bd.ne[i] != 1 && bd.ne[i] != (i ? b1 : b0)))
+            return fail(VKHIP_ERR_INVALID, "matmul batch extents disagree");
+    }
+    const uint64_t batch = static_cast<uint64_t>(b0) * b1;
+    if (batch == 0 || m == 0 || n == 0) return VKHIP_OK;
+    if (batch > 65535) return fail(VKHIP_ERR_UNSUPPORTED, "matmul batch %llu > 65535",
+                                   static_cast<unsigned long long>(batch));
+    const int kernel = opts ? opts->kernel : VKHIP_GEMM_AUTO;
+    const int32_t split_req = opts ? opts->split_k : 0;
+    if (k == 0) {
+        VKHIP_HIP(hipMemsetAsync(c, 0, batch * m * n * sizeof(float), ctx().stream));
+        return VKHIP_OK;
+    }
+
+    // GEMV: an N == 1 product with a unit-stride K axis of A is a bandwidth
+    // problem, not a matrix-core one. AUTO takes it whenever batch == 1.
+    if ((kernel == VKHIP_GEMM_GEMV || kernel == VKHIP_GEMM_AUTO) && n == 1 && batch == 1 &&
+        ad.nb[3] == 1 && k <= static_cast<uint32_t>(kGemvMaxK)) {
+        return launch_gemv(a, ad.nb[2], b, bd.nb[2], c, m, k);
+    }
+    if (kernel == VKHIP_GEMM_GEMV)
+        return fail(VKHIP_ERR_UNSUPPORTED, "gemv requested for a %ux%ux%u problem", m, n, k);
+
+    uint32_t splits, chunk;
+    TileChoice tile;
+    gemm_plan(static_cast<uint32_t>(batch), m, n, k, split_req, splits, chunk, tile);
+
+    GemmArgs g{};
+    g.a = a;
+    g.b = b;
+    g.sa0 = ad.ne[0] == 1 ? 0 : ad.nb[0];
+    g.sa1 = ad.ne[1] == 1 ? 0 : ad.nb[1];
+    g.sam = ad.nb[2];
+    g.sak = ad.nb[3];
+    g.sb0 = bd.ne[0] == 1 ? 0 : bd.nb[0];
+    g.sb1 = bd.ne[1] == 1 ? 0 : bd.nb[1];
+    g.sbk = bd.nb[2];
+    g.sbn = bd.nb[3];
+    g.b1 = b1;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.tiles_m = ceil_div(m, tile.bm);
+    g.tiles_n = ceil_div(n, tile.bn);
+    g.ktiles = ceil_div(k, 32);
+    g.chunk = chunk;
+    const bool akc = ad.nb[3] == 1 || k == 1;
+    const bool bkc = bd.nb[2] == 1 || k == 1;
+    auto aligned = [](const float* p, int64_t s0, int64_t s1, int64_t srow) {
+        return reinterpret_cast<uintptr_t>(p) % 16 == 0 && s0 % 4 == 0 && s1 % 4 == 0 && srow % 4 == 0;
+    };
+    g.a_vec = akc && ad.nb[3] == 1 && aligned(a, g.sa0, g.sa1, g.sam);
+    g.b_vec = bkc && bd.nb[2] == 1 && aligned(b, g.sb0, g.sb1, g.sbn);
+
+    const uint64_t out_elems = batch * m * n;
+    float* target = c;
+    if (splits > 1) {
+        float* ws = nullptr;
+        int st = workspace(out_elems * splits * sizeof(float), &ws);
+        if (st != VKHIP_OK) return st;
+        target = ws;
+        g.split_stride = out_elems;
+    }
+    g.c = target;
+    int st;
+    if (tile.bm == 128)
+        st = launch_tiles<128, 128, 64, 64>(g, static_cast<uint32_t>(batch), splits, akc, bkc);
+    else
+        st = launch_tiles<64, 64, 32, 32>(g, static_cast<uint32_t>(batch), splits, akc, bkc);
+    if (st != VKHIP_OK) return st;
+    if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
+    return VKHIP_OK;
+}
+
+}  // namespace vkhip
+
+// ---- C ABI -------------------------------------------------------------------
+extern "C" int vkhip_gemm(const float* a, const vkhip_operand* a_desc, const float* b,
+                          const vkhip_operand* b_desc, float* c, const vkhip_gemm_opts* opts) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!a_desc || !b_desc) return vkhip::fail(VKHIP_ERR_INVALID, "gemm: null descriptor");
+    return vkhip::gemm(a, *a_desc, b, *b_desc, c, opts);
+}
+
+extern "C" int vkhip_gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                               int32_t split_request, uint32_t* out_splits, uint32_t* out_chunk) {
+    uint32_t s, c;
+    vkhip::TileChoice t;
+    vkhip::gemm_plan(batch, m, n, k, split_request, s, c, t);
+    if (out_splits) *out_splits = s;
+    if (out_chunk) *out_chunk = c;
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (splits == 0 || splits > 511)
+        return vkhip::fail(VKHIP_ERR_INVALID, "split_k_reduce: splits=%u outside 1..511", splits);
+    return vkhip::launch_split_k_reduce(ws, dst, ne, splits);
+}
+
+extern "C" int vkhip_gemv(const float* a, int64_t lda, const float* x, int64_t incx, float* y,
+                          uint32_t m, uint32_t k) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    return vkhip::launch_gemv(a, lda, x, incx, y, m, k);
+}

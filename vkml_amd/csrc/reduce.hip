@@ -1,0 +1,636 @@
+// Softmax / log-softmax and row/axis reductions (sum, mean, max, min, argmax,
+// argmin) for gfx950.
+//
+// Numerics follow the CPU oracle (reference kernels_reduce.cpp:44-259):
+//   - sum and mean are the oracle's pairwise tree (reduce.h:55-72) exactly. The
+//     row is staged once in LDS (coalesced 16-byte loads), each thread sums the
+//     tree's 32-element leaves sequentially, and leaves combine adjacent-first by
+//     a wave64 xor-butterfly and then across waves. Bit-identical to the oracle.
+//   - max/min/argmax/argmin are selections, merged with an explicit lowest-index
+//     tie-break, so any merge order gives the oracle's sequential answer:
+//     first maximum; max/min return the first NaN; argmax/argmin skip NaN.
+//   - softmax uses the same staged row: peak = max, denominator = the oracle's
+//     pairwise tree over exp(x - peak), out = exp(x - peak) / denom or
+//     (x - peak) - log(denom). exp/log are the device library's (OCML), so the
+//     result is within a few ulp of the oracle's libm, not bit-identical.
+//
+// Bandwidth: one HBM read and (softmax) one write per element; the row never
+// leaves the CU between passes.
+#include "common.h"
+
+namespace vkhip {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_sum_butterfly(float v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float max_ignoring_nan(float a, float b) { return (a < b) ? b : a; }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = max_ignoring_nan(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t padded(uint32_t i) { return i + (i >> 5); }
+
+// Sum of the `per` consecutive depth-D leaves starting at leaf `first`, folded
+// with the binary-counter carry stack (per is a power of two, so the result is
+// the balanced subtree over those leaves).
+__device__ __forceinline__ float leaves_subtree_sum(const float* lds, uint32_t n, int depth,
+                                                    uint32_t first, uint32_t per) {
+    float stack[9];
+#pragma unroll
+    for (int l = 0; l < 9; ++l) stack[l] = 0.0f;
+    for (uint32_t t = 0; t < per; ++t) {
+        uint32_t b, e;
+        pairwise_leaf(n, depth, first + t, b, e);
+        float s = 0.0f;
+        for (uint32_t q = b; q < e; ++q) s = s + lds[padded(q)];
+        bool carry = true;
+#pragma unroll
+        for (int l = 0; l < 9; ++l) {
+            if (carry) {
+                if ((t >> l) & 1u) {
+                    s = stack[l] + s;
+                } else {
+                    stack[l] = s;
+                    carry = false;
+                }
+            }
+        }
+    }
+    int top = 0;
+    while ((1u << top) < per) ++top;
+    float v = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 9; ++l)
+        if (l == top) v = stack[l];
+    return v;
+}
+
+// Pairwise sum of the n values staged (padded) in `lds` by a group of T threads
+// (t = index within the group). Every thread of the group gets the total.
+// `scratch` holds T/64 floats for the group. All threads of the BLOCK must call
+// this together (it contains block barriers when T > 64).
+template <int T>
+__device__ float group_pairwise_sum(const float* lds, uint32_t n, int depth, int t,
+                                    float* scratch) {
+    const uint32_t leaves = 1u << depth;
+    const uint32_t per = leaves > static_cast<uint32_t>(T) ? leaves / T : 1u;
+    float v = 0.0f;
+    if (static_cast<uint32_t>(t) * per < leaves) v = leaves_subtree_sum(lds, n, depth, t * per, per);
+    v = wave_sum_butterfly(v);
+    if constexpr (T > 64) {
+        const int lane = t & 63, wave = t >> 6;
+        if (lane == 0) scratch[wave] = v;
+        __syncthreads();
+        float u = lane < T / 64 ? scratch[lane] : 0.0f;
+        v = wave_sum_butterfly(u);
+        __syncthreads();
+    }
+    return v;
+}
+
+template <int T>
+__device__ float group_max(float v, int t, float* scratch) {
+    v = wave_max(v);
+    if constexpr (T > 64) {
+        const int lane = t & 63, wave = t >> 6;
+        if (lane == 0) scratch[wave] = v;
+        __syncthreads();
+        float u = lane < T / 64 ? scratch[lane] : -__builtin_inff();
+        v = wave_max(u);
+        __syncthreads();
+    }
+    return v;
+}
+
+// ---- softmax over contiguous rows ------------------------------------------------
+// T threads per row (64: four rows per 256-thread block), rows of n <= NMAX
+// contiguous floats at src + row*in_stride; dst rows contiguous.
+template <int T, int NMAX>
+__global__ __launch_bounds__(T >= 256 ? T : 256) void softmax_rows_kernel(
+    const float* __restrict__ src, int64_t in_stride, float* __restrict__ dst, uint32_t rows,
+    uint32_t n, int depth, int log_mode, int vec) {
+    constexpr int RPB = T >= 256 ? 1 : 256 / T;
+    constexpr int E = NMAX / T;  // elements per thread at most
+    static_assert(E % 4 == 0, "elements per thread must be a multiple of 4");
+    __shared__ float lds[RPB][NMAX + NMAX / 32];
+    __shared__ float scratch[RPB][T / 64 > 0 ? T / 64 : 1];
+
+    const int slot = threadIdx.x / T;
+    const int t = threadIdx.x % T;
+    const uint32_t row = blockIdx.x * RPB + slot;
+    const bool live = row < rows;
+    const float* rs = src + static_cast<int64_t>(live ? row : 0) * in_stride;
+    float* stage = lds[slot];
+
+    float x[E];
+    float mx = -__builtin_inff();
+    if (vec) {
+#pragma unroll
+        for (int i = 0; i < E / 4; ++i) {
+            const uint32_t e0 = 4u * (t + T * i);
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (live && e0 < n) v = *reinterpret_cast<const f32x4*>(rs + e0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x[4 * i + j] = v[j];
+                if (live && e0 < n) mx = max_ignoring_nan(mx, v[j]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const uint32_t e = t + T * i;
+            x[i] = (live && e < n) ? rs[e] : 0.0f;
+            if (live && e < n) mx = max_ignoring_nan(mx, x[i]);
+        }
+    }
+    mx = group_max<T>(mx, t, scratch[slot]);
+
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const uint32_t e = vec ? 4u * (t + T * (i / 4)) + (i % 4) : t + T * i;
+        if (live && e < n) stage[padded(e)] = expf(x[i] - mx);
+    }
+    __syncthreads();
+    const float denom = group_pairwise_sum<T>(stage, n, depth, t, scratch[slot]);
+    if (!live) return;
+    const float ld = logf(denom);
+    float* ds = dst + static_cast<uint64_t>(row) * n;
+    if (vec) {
+#pragma unroll
+        for (int i = 0; i < E / 4; ++i) {
+            const uint32_t e0 = 4u * (t + T * i);
+            if (e0 < n) {
+                f32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float sh = x[4 * i + j] - mx;
+                    o[j] = log_mode ? sh - ld : expf(sh) / denom;
+                }
+                *reinterpret_cast<f32x4*>(ds + e0) = o;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const uint32_t e = t + T * i;
+            if (e < n) {
+                const float sh = x[i] - mx;
+                ds[e] = log_mode ? sh - ld : expf(sh) / denom;
+            }
+        }
+    }
+}
+
+// ---- one thread per output: any layout ------------------------------------------------
+// The reduced elements of output o are at base(o) + lin_off(i, reduced). Sum and
+// mean walk the depth-D leaves in order and fold them with a carry stack (a
+// balanced fold over 2^D leaves is the oracle's tree); selections scan in index
+// order exactly as the oracle's loops do. Adjacent threads own adjacent outputs,
+// so the loads coalesce whenever the kept axis is the contiguous one.
+constexpr int kTallLevels = 22;  // 2^21 leaves of <= 32: n < 2^26 elements
+
+struct Reader {
+    Op4 red;
+    int single;  // the reduced elements sit on one axis with stride `step`
+    int64_t step;
+    __device__ __forceinline__ int64_t off(uint32_t i) const {
+        return single ? static_cast<int64_t>(i) * step : lin_off4(i, red.ne, red.nb);
+    }
+};
+
+__global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* __restrict__ src,
+                                                          Op4 kept, Reader rd, uint64_t n_out,
+                                                          uint32_t n_red, int depth,
+                                                          void* __restrict__ dst) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= n_out) return;
+    const float* base = src + lin_off4(o, kept.ne, kept.nb);
+    if (op == VKHIP_REDUCE_SUM || op == VKHIP_REDUCE_MEAN) {
+        float stack[kTallLevels];
+#pragma unroll
+        for (int l = 0; l < kTallLevels; ++l) stack[l] = 0.0f;
+        const uint32_t leaves = 1u << depth;
+        for (uint32_t j = 0; j < leaves; ++j) {
+            uint32_t b, e;
+            pairwise_leaf(n_red, depth, j, b, e);
+            float s = 0.0f;
+            for (uint32_t q = b; q < e; ++q) s = s + base[rd.off(q)];
+            bool carry = true;
+#pragma unroll
+            for (int l = 0; l < kTallLevels; ++l) {
+                if (carry) {
+                    if ((j >> l) & 1u) {
+                        s = stack[l] + s;
+                    } else {
+                        stack[l] = s;
+                        carry = false;
+                    }
+                }
+            }
+        }
+        float total = 0.0f;
+#pragma unroll
+        for (int l = 0; l < kTallLevels; ++l)
+            if (l == depth) total = stack[l];
+        if (op == VKHIP_REDUCE_MEAN)
+            total = n_red == 0 ? __builtin_nanf("") : total / static_cast<float>(n_red);
+        static_cast<float*>(dst)[o] = total;
+        return;
+    }
+    if (op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_MIN) {
+        const bool is_max = op == VKHIP_REDUCE_MAX;
+        float best = is_max ? -__builtin_inff() : __builtin_inff();
+        for (uint32_t i = 0; i < n_red; ++i) {
+            const float v = base[rd.off(i)];
+            if (v != v) {
+                best = v;
+                break;
+            }
+            if (is_max ? (v > best) : (v < best)) best = v;
+        }
+        static_cast<float*>(dst)[o] = best;
+        return;
+    }
+    const bool is_max = op == VKHIP_REDUCE_ARGMAX;
+    float best = is_max ? -__builtin_inff() : __builtin_inff();
+    int64_t best_i = 0;
+    for (uint32_t i = 0; i < n_red; ++i) {
+        const float v = base[rd.off(i)];
+        if (is_max ? (v > best) : (v < best)) {
+            best = v;
+            best_i = i;
+        }
+    }
+    static_cast<int64_t*>(dst)[o] = best_i;
+}
+
+// ---- one workgroup per output: contiguous reduced runs ----------------------------------
+// Sum / mean: the run is staged in LDS and summed by group_pairwise_sum.
+template <int T, int NMAX>
+__global__ __launch_bounds__(T >= 256 ? T : 256) void reduce_rows_sum_kernel(
+    const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int depth, int mean,
+    int vec, float* __restrict__ dst) {
+    constexpr int RPB = T >= 256 ? 1 : 256 / T;
+    __shared__ float lds[RPB][NMAX + NMAX / 32];
+    __shared__ float scratch[RPB][T / 64 > 0 ? T / 64 : 1];
+    const int slot = threadIdx.x / T;
+    const int t = threadIdx.x % T;
+    const uint32_t o = blockIdx.x * RPB + slot;
+    const bool live = o < n_out;
+    const float* rs = src + (live ? lin_off4(o, kept.ne, kept.nb) : 0);
+    float* stage = lds[slot];
+    if (live) {
+        if (vec) {
+            for (uint32_t e0 = 4u * t; e0 < n; e0 += 4u * T) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(rs + e0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) stage[padded(e0 + j)] = v[j];
+            }
+        } else {
+            for (uint32_t e = t; e < n; e += T) stage[padded(e)] = rs[e];
+        }
+    }
+    __syncthreads();
+    float s = group_pairwise_sum<T>(stage, n, depth, t, scratch[slot]);
+    if (live && t == 0) dst[o] = mean ? s / static_cast<float>(n) : s;
+}
+
+// Selections: thread-strided scan, then (value, index) merges with the
+// lowest-index tie-break.
+struct Sel {
+    float v;
+    uint32_t i;  // 0xffffffff = no candidate
+};
+
+__device__ __forceinline__ Sel sel_merge(int op, Sel a, Sel b) {
+    if (b.i == 0xffffffffu) return a;
+    if (a.i == 0xffffffffu) return b;
+    const bool is_max = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_ARGMAX;
+    if (op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_MIN) {
+        const bool an = a.v != a.v, bn = b.v != b.v;
+        if (an || bn) {
+            if (an && bn) return a.i < b.i ? a : b;
+            return an ? a : b;
+        }
+    }
+    const bool b_better = is_max ? (b.v > a.v) : (b.v < a.v);
+    const bool a_better = is_max ? (a.v > b.v) : (a.v < b.v);
+    if (b_better) return b;
+    if (a_better) return a;
+    return a.i < b.i ? a : b;
+}
+
+template <int T>
+__global__ __launch_bounds__(T >= 256 ? T : 256) void reduce_rows_select_kernel(
+    int op, const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n,
+    void* __restrict__ dst) {
+    constexpr int RPB = T >= 256 ? 1 : 256 / T;
+    __shared__ float sv[RPB][T / 64 > 0 ? T / 64 : 1];
+    __shared__ uint32_t si[RPB][T / 64 > 0 ? T / 64 : 1];
+    const int slot = threadIdx.x / T;
+    const int t = threadIdx.x % T;
+    const uint32_t o = blockIdx.x * RPB + slot;
+    const bool live = o < n_out;
+    const float* rs = src + (live ? lin_off4(o, kept.ne, kept.nb) : 0);
+    const bool is_max = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_ARGMAX;
+    const bool value_op = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_MIN;
+    Sel s{is_max ? -__builtin_inff() : __builtin_inff(), 0xffffffffu};
+    if (live) {
+        for (uint32_t e = t; e < n; e += T) {
+            const float v = rs[e];
+            if (v != v) {
+                if (value_op) {
+                    s = Sel{v, e};  // first NaN of this thread's subsequence
+                    break;
+                }
+                continue;
+            }
+            // Value ops take the first element as their candidate even if it is
+            // +-inf; index ops need a strict improvement on +-inf, as the
+            // oracle's loops do.
+            const bool better = is_max ? v > s.v : v < s.v;
+            if (better || (value_op && s.i == 0xffffffffu)) s = Sel{v, e};
+        }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        Sel o2{__shfl_xor(s.v, off, 64), static_cast<uint32_t>(__shfl_xor(static_cast<int>(s.i), off, 64))};
+        s = sel_merge(op, s, o2);
+    }
+    if constexpr (T > 64) {
+        const int lane = t & 63, wave = t >> 6;
+        if (lane == 0) {
+            sv[slot][wave] = s.v;
+            si[slot][wave] = s.i;
+        }
+        __syncthreads();
+        if (t == 0) {
+            for (int w = 1; w < T / 64; ++w) s = sel_merge(op, s, Sel{sv[slot][w], si[slot][w]});
+        }
+    }
+    if (!live || t != 0) return;
+    if (value_op) {
+        static_cast<float*>(dst)[o] = s.i == 0xffffffffu ? (is_max ? -__builtin_inff() : __builtin_inff()) : s.v;
+    } else {
+        static_cast<int64_t*>(dst)[o] = s.i == 0xffffffffu ? 0 : static_cast<int64_t>(s.i);
+    }
+}
+
+// ---- host side ----------------------------------------------------------------------
+
+static void split_axes(const vkhip_operand& d, uint32_t mask, Op4& kept, Op4& red) {
+    int kc = 0, rc = 0;
+    uint32_t kn[4], rn[4];
+    int64_t ks[4], rs[4];
+    for (int i = 0; i < 4; ++i) {
+        if (mask & (1u << i)) {
+            rn[rc] = d.ne[i];
+            rs[rc++] = d.nb[i];
+        } else {
+            kn[kc] = d.ne[i];
+            ks[kc++] = d.nb[i];
+        }
+    }
+    for (int i = 0; i < 4; ++i) {
+        kept.ne[i] = 1;
+        kept.nb[i] = 0;
+        red.ne[i] = 1;
+        red.nb[i] = 0;
+    }
+    for (int i = 0; i < kc; ++i) {
+        kept.ne[4 - kc + i] = kn[i];
+        kept.nb[4 - kc + i] = ks[i];
+    }
+    for (int i = 0; i < rc; ++i) {
+        red.ne[4 - rc + i] = rn[i];
+        red.nb[4 - rc + i] = rs[i];
+    }
+}
+
+static uint64_t numel_op4(const Op4& o) {
+    return static_cast<uint64_t>(o.ne[0]) * o.ne[1] * o.ne[2] * o.ne[3];
+}
+
+// True when the elements of `o` form one contiguous run, row-major, stride 1.
+static bool contiguous_run(const Op4& o) {
+    int64_t expect = 1;
+    for (int i = 3; i >= 0; --i) {
+        if (o.ne[i] == 1) continue;
+        if (o.nb[i] != expect) return false;
+        expect *= o.ne[i];
+    }
+    return true;
+}
+
+// The reduced elements lie on at most one non-unit axis: its stride.
+static bool single_axis(const Op4& o, int64_t& step) {
+    int count = 0;
+    step = 0;
+    for (int i = 0; i < 4; ++i)
+        if (o.ne[i] != 1) {
+            ++count;
+            step = o.nb[i];
+        }
+    return count <= 1;
+}
+
+constexpr uint32_t kRowsMax = 32768;  // longest run staged in LDS
+
+int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst) {
+    if (op < VKHIP_REDUCE_SUM || op > VKHIP_REDUCE_ARGMIN)
+        return fail(VKHIP_ERR_INVALID, "reduce: unknown op %d", op);
+    Op4 kept, red;
+    split_axes(d, mask & 0xfu, kept, red);
+    const uint64_t n_out64 = numel_op4(kept), n_red64 = numel_op4(red);
+    if (n_out64 == 0) return VKHIP_OK;
+    if (n_red64 >= (1ull << 26) || n_out64 > 0xffffffffull)
+        return fail(VKHIP_ERR_UNSUPPORTED, "reduce: extents too large");
+    const uint32_t n_out = static_cast<uint32_t>(n_out64), n_red = static_cast<uint32_t>(n_red64);
+    hipStream_t st = ctx().stream;
+    const bool sum_op = op == VKHIP_REDUCE_SUM || op == VKHIP_REDUCE_MEAN;
+    const bool run = contiguous_run(red);
+    // Structure rule (reference vulkan_backend.cpp:1912-1920, restated for a
+    // 256-CU part): a workgroup per output when the reduced run is contiguous
+    // and long enough to feed it; otherwise a lane per output, which coalesces
+    // when the kept axis is the contiguous one. Both give identical results.
+    const bool wide = run && n_red >= 32 && (!sum_op || n_red <= kRowsMax);
+    if (wide) {
+        const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) && (n_red % 4 == 0) &&
+                        (kept.nb[0] % 4 == 0) && (kept.nb[1] % 4 == 0) && (kept.nb[2] % 4 == 0) &&
+                        (kept.nb[3] % 4 == 0);
+        if (sum_op) {
+            const int depth = pairwise_depth(n_red);
+            const int mean = op == VKHIP_REDUCE_MEAN;
+            float* out = static_cast<float*>(dst);
+            if (n_red <= 2048) {
+                hipLaunchKernelGGL((reduce_rows_sum_kernel<64, 2048>), dim3(ceil_div(n_out, 4)),
+                                   dim3(256), 0, st, src, kept, n_out, n_red, depth, mean, vec, out);
+            } else if (n_red <= 8192) {
+                hipLaunchKernelGGL((reduce_rows_sum_kernel<256, 8192>), dim3(n_out), dim3(256), 0,
+                                   st, src, kept, n_out, n_red, depth, mean, vec, out);
+            } else {
+                hipLaunchKernelGGL((reduce_rows_sum_kernel<1024, kRowsMax>), dim3(n_out),
+                                   dim3(1024), 0, st, src, kept, n_out, n_red, depth, mean, vec,
+                                   out);
+            }
+        } else {
+            if (n_red <= 2048)
+                hipLaunchKernelGGL((reduce_rows_select_kernel<64>), dim3(ceil_div(n_out, 4)),
+                                   dim3(256), 0, st, op, src, kept, n_out, n_red, dst);
+            else
+                hipLaunchKernelGGL((reduce_rows_select_kernel<256>), dim3(n_out), dim3(256), 0,
+                                   st, op, src, kept, n_out, n_red, dst);
+        }
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
+    Reader rd;
+    rd.red = red;
+    rd.single = single_axis(red, rd.step) ? 1 : 0;
+    const int depth = pairwise_depth(n_red);
+    hipLaunchKernelGGL(reduce_tall_kernel, dim3(ceil_div(n_out, 256)), dim3(256), 0, st, op, src,
+                       kept, rd, static_cast<uint64_t>(n_out), n_red, depth, dst);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+// ---- softmax host side ------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restrict__ src, Op4 kept,
+                                                           Reader rd, Op4 okept, Reader ord,
+                                                           uint64_t n_out, uint32_t n, int depth,
+                                                           int log_mode, float* __restrict__ dst) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= n_out) return;
+    const float* base = src + lin_off4(o, kept.ne, kept.nb);
+    float* obase = dst + lin_off4(o, okept.ne, okept.nb);
+    float peak = -__builtin_inff();
+    for (uint32_t i = 0; i < n; ++i) peak = max_ignoring_nan(peak, base[rd.off(i)]);
+    float stack[kTallLevels];
+#pragma unroll
+    for (int l = 0; l < kTallLevels; ++l) stack[l] = 0.0f;
+    const uint32_t leaves = 1u << depth;
+    for (uint32_t j = 0; j < leaves; ++j) {
+        uint32_t b, e;
+        pairwise_leaf(n, depth, j, b, e);
+        float s = 0.0f;
+        for (uint32_t q = b; q < e; ++q) s = s + expf(base[rd.off(q)] - peak);
+        bool carry = true;
+#pragma unroll
+        for (int l = 0; l < kTallLevels; ++l) {
+            if (carry) {
+                if ((j >> l) & 1u) {
+                    s = stack[l] + s;
+                } else {
+                    stack[l] = s;
+                    carry = false;
+                }
+            }
+        }
+    }
+    float denom = 0.0f;
+#pragma unroll
+    for (int l = 0; l < kTallLevels; ++l)
+        if (l == depth) denom = stack[l];
+    const float ld = logf(denom);
+    for (uint32_t i = 0; i < n; ++i) {
+        const float sh = base[rd.off(i)] - peak;
+        obase[ord.off(i)] = log_mode ? sh - ld : expf(sh) / denom;
+    }
+}
+
+int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axis, int log_mode) {
+    if (axis < 0 || axis > 3) return fail(VKHIP_ERR_INVALID, "softmax: axis %d outside 0..3", axis);
+    Op4 kept, red;
+    split_axes(d, 1u << axis, kept, red);
+    const uint64_t n_out64 = numel_op4(kept);
+    const uint32_t n = d.ne[axis];
+    if (n_out64 == 0 || n == 0) return VKHIP_OK;
+    if (n_out64 > 0xffffffffull || n >= (1u << 26))
+        return fail(VKHIP_ERR_UNSUPPORTED, "softmax: extents too large");
+    const uint32_t rows = static_cast<uint32_t>(n_out64);
+    hipStream_t st = ctx().stream;
+    const int depth = pairwise_depth(n);
+    // Fast path: softmax over the innermost, unit-stride axis, rows evenly spaced.
+    int64_t row_stride = 0;
+    bool rows_regular = true;
+    {
+        // Kept offsets must be o * row_stride for a single stride.
+        int64_t expect = -1;
+        int64_t acc = 1;
+        for (int i = 3; i >= 0; --i) {
+            if (kept.ne[i] == 1) continue;
+            if (expect < 0) {
+                row_stride = kept.nb[i];
+                expect = kept.nb[i];
+            }
+            if (kept.nb[i] != row_stride * acc) rows_regular = false;
+            acc *= kept.ne[i];
+        }
+        if (expect < 0) row_stride = n;
+    }
+    if (axis == 3 && d.nb[3] == 1 && rows_regular && n <= kRowsMax) {
+        const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
+                        (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (n % 4 == 0) &&
+                        (row_stride % 4 == 0);
+        if (n <= 2048)
+            hipLaunchKernelGGL((softmax_rows_kernel<64, 2048>), dim3(ceil_div(rows, 4)), dim3(256),
+                               0, st, src, row_stride, dst, rows, n, depth, log_mode, vec);
+        else if (n <= 8192)
+            hipLaunchKernelGGL((softmax_rows_kernel<256, 8192>), dim3(rows), dim3(256), 0, st, src,
+                               row_stride, dst, rows, n, depth, log_mode, vec);
+        else
+            hipLaunchKernelGGL((softmax_rows_kernel<1024, kRowsMax>), dim3(rows), dim3(1024), 0, st,
+                               src, row_stride, dst, rows, n, depth, log_mode, vec);
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
+    // General layout: one thread per row.
+    vkhip_operand od;
+    int64_t s = 1;
+    for (int i = 3; i >= 0; --i) {
+        od.ne[i] = d.ne[i];
+        od.nb[i] = s;
+        s *= d.ne[i];
+    }
+    Op4 okept, ored;
+    split_axes(od, 1u << axis, okept, ored);
+    Reader rd, ord;
+    rd.red = red;
+    rd.single = 1;
+    rd.step = d.nb[axis];
+    ord.red = ored;
+    ord.single = 1;
+    ord.step = od.nb[axis];
+    hipLaunchKernelGGL(softmax_tall_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, st, src, kept,
+                       rd, okept, ord, n_out64, n, depth, log_mode, dst);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+}  // namespace vkhip
+
+extern "C" int vkhip_softmax(const float* src, const vkhip_operand* src_desc, float* dst, int axis,
+                             int log_softmax) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!src_desc) return vkhip::fail(VKHIP_ERR_INVALID, "softmax: null descriptor");
+    return vkhip::launch_softmax(src, *src_desc, dst, axis, log_softmax);
+}
+
+extern "C" int vkhip_reduce(int op, const float* src, const vkhip_operand* src_desc,
+                            uint32_t axes_mask, void* dst) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!src_desc) return vkhip::fail(VKHIP_ERR_INVALID, "reduce: null descriptor");
+    return vkhip::launch_reduce(op, src, *src_desc, axes_mask, dst);
+}

@@ -1,0 +1,472 @@
+// Backend runtime: device binding, stream, memory, copies, and the
+// compute(span<Node*>) dispatcher that turns one graph flush into an ordered
+// launch sequence on one HIP stream.
+//
+// Mirrors the reference Backend contract (include/vkml/backend/api/backend.h:34-125):
+// compute() orders work and may return before it completes; host reads
+// synchronise; frees are stream-ordered so memory still read by enqueued work
+// is not reused early (the reference retires frees behind its timeline,
+// vulkan_backend.cpp:921-984; hipFreeAsync gives that ordering directly).
+#include <cstring>
+#include <mutex>
+
+#include "common.h"
+
+namespace vkhip {
+
+// Launchers defined in the kernel translation units.
+int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd, float* c,
+         const vkhip_gemm_opts* opts);
+int launch_im2col(const float* src, const vkhip_operand& sd, float* dst, const vkhip_unfold& p);
+int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
+                  const vkhip_unfold& p);
+int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uint32_t out_h,
+                      uint32_t out_w, const vkhip_unfold& p);
+int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_operand& sd,
+                               float* dst, uint32_t out_h, uint32_t out_w, const vkhip_unfold& p);
+int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axis, int log_mode);
+int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst);
+int launch_elementwise(const vkhip_node& nd);
+
+static thread_local char g_last_error[512] = "";
+
+void set_error_msg(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+    va_end(ap);
+}
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+Context& ctx() {
+    static Context c;
+    return c;
+}
+
+static std::mutex g_mu;  // guards init/shutdown/workspace (reference allocation-map mutex)
+
+int require_ready() {
+    if (!ctx().ready)
+        return fail(VKHIP_ERR_NOT_INITIALISED, "vkhip: backend not initialised (call vkhip_init)");
+    return VKHIP_OK;
+}
+
+int workspace(size_t bytes, float** out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Context& c = ctx();
+    if (c.ws_bytes < bytes) {
+        if (c.ws) VKHIP_HIP(hipFreeAsync(c.ws, c.stream));
+        c.ws = nullptr;
+        c.ws_bytes = 0;
+        void* p = nullptr;
+        if (hipMallocAsync(&p, bytes, c.stream) != hipSuccess)
+            return fail(VKHIP_ERR_OOM, "split-K workspace of %zu bytes could not be allocated", bytes);
+        c.ws = static_cast<float*>(p);
+        c.ws_bytes = bytes;
+    }
+    *out = c.ws;
+    return VKHIP_OK;
+}
+
+// ---- node -> descriptor helpers ------------------------------------------------
+
+static vkhip_operand to_operand(const vkhip_tensor& t) {
+    vkhip_operand d;
+    const int pad = 4 - t.ndim;
+    for (int i = 0; i < 4; ++i) {
+        d.ne[i] = 1;
+        d.nb[i] = 0;
+    }
+    for (int i = 0; i < t.ndim; ++i) {
+        d.ne[pad + i] = static_cast<uint32_t>(t.ne[i]);
+        d.nb[pad + i] = t.nb[i];
+    }
+    return d;
+}
+
+static bool contiguous(const vkhip_tensor& t) {
+    int64_t expect = 1;
+    for (int i = t.ndim - 1; i >= 0; --i) {
+        if (t.ne[i] == 1) continue;
+        if (t.nb[i] != expect) return false;
+        expect *= t.ne[i];
+    }
+    return true;
+}
+
+static bool fits32(const vkhip_tensor& t) {
+    if (t.ndim < 0 || t.ndim > 4) return false;
+    for (int i = 0; i < t.ndim; ++i)
+        if (t.ne[i] < 0 || t.ne[i] > 0xffffffffll) return false;
+    return true;
+}
+
+static bool is_f32(const vkhip_tensor& t) { return t.dtype == VKHIP_F32; }
+
+static int supports_node(const vkhip_node& nd) {
+    if (!fits32(nd.out)) return 0;
+    for (int s = 0; s < nd.n_src; ++s)
+        if (!fits32(nd.src[s])) return 0;
+    const vkhip_tensor& o = nd.out;
+    switch (nd.op) {
+        case VKHIP_OP_FULL:
+            return o.dtype == VKHIP_F32 || o.dtype == VKHIP_I64 || o.dtype == VKHIP_BOOL;
+        case VKHIP_OP_ARANGE: return o.dtype == VKHIP_F32 || o.dtype == VKHIP_I64;
+        case VKHIP_OP_CONTIGUOUS:
+            return nd.n_src == 1 && nd.src[0].dtype == o.dtype &&
+                   (o.dtype == VKHIP_F32 || o.dtype == VKHIP_I64 || o.dtype == VKHIP_BOOL);
+        case VKHIP_OP_CAST: {
+            const int f = nd.src[0].dtype, t = o.dtype;
+            return nd.n_src == 1 && ((f == VKHIP_I64 && t == VKHIP_F32) ||
+                                     (f == VKHIP_BOOL && t == VKHIP_F32) ||
+                                     (f == VKHIP_F32 && t == VKHIP_I64) ||
+                                     (f == VKHIP_F32 && t == VKHIP_F32));
+        }
+        case VKHIP_OP_NEG:
+        case VKHIP_OP_EXP:
+        case VKHIP_OP_LOG:
+        case VKHIP_OP_RELU: return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]);
+        case VKHIP_OP_ADD:
+        case VKHIP_OP_SUB:
+        case VKHIP_OP_MUL:
+        case VKHIP_OP_DIV:
+        case VKHIP_OP_SCALED_ADD:
+        case VKHIP_OP_MAXIMUM:
+        case VKHIP_OP_MINIMUM:
+            return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]);
+        case VKHIP_OP_EQUAL:
+        case VKHIP_OP_LESS:
+        case VKHIP_OP_GREATER:
+        case VKHIP_OP_LESS_EQUAL:
+        case VKHIP_OP_GREATER_EQUAL:
+        case VKHIP_OP_NOT_EQUAL:
+            return nd.n_src == 2 && o.dtype == VKHIP_BOOL && is_f32(nd.src[0]) && is_f32(nd.src[1]);
+        case VKHIP_OP_WHERE:
+            return nd.n_src == 3 && nd.src[0].dtype == VKHIP_BOOL && is_f32(o) &&
+                   is_f32(nd.src[1]) && is_f32(nd.src[2]);
+        case VKHIP_OP_SUM:
+        case VKHIP_OP_MEAN:
+        case VKHIP_OP_MAX:
+        case VKHIP_OP_MIN: return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && contiguous(o);
+        case VKHIP_OP_ARGMAX:
+        case VKHIP_OP_ARGMIN:
+            return nd.n_src == 1 && o.dtype == VKHIP_I64 && is_f32(nd.src[0]) && contiguous(o);
+        case VKHIP_OP_MATMUL:
+            return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
+                   contiguous(o) && nd.src[0].ndim >= 2 && nd.src[1].ndim >= 2;
+        case VKHIP_OP_SOFTMAX:
+        case VKHIP_OP_LOG_SOFTMAX:
+            return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && contiguous(o) &&
+                   nd.src[0].ndim >= 1;
+        case VKHIP_OP_IM2COL:
+            return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && nd.src[0].ndim == 4 &&
+                   o.ndim == 3 && contiguous(o);
+        case VKHIP_OP_COL2IM:
+            return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && nd.src[0].ndim == 3 &&
+                   contiguous(nd.src[0]) && o.ndim == 4 && contiguous(o);
+        case VKHIP_OP_MAX_POOL2D:
+            return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && nd.src[0].ndim == 4 &&
+                   o.ndim == 4 && contiguous(o);
+        case VKHIP_OP_MAX_POOL2D_BACKWARD:
+            return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
+                   nd.src[0].ndim == 4 && contiguous(nd.src[0]) && nd.src[1].ndim == 4 &&
+                   o.ndim == 4 && contiguous(o);
+        default: return 0;
+    }
+}
+
+static const char* op_name(int op) {
+    switch (op) {
+        case VKHIP_OP_MATMUL: return "matmul";
+        case VKHIP_OP_SOFTMAX: return "softmax";
+        case VKHIP_OP_LOG_SOFTMAX: return "log_softmax";
+        case VKHIP_OP_IM2COL: return "im2col";
+        case VKHIP_OP_COL2IM: return "col2im";
+        case VKHIP_OP_SUM: return "sum";
+        case VKHIP_OP_MEAN: return "mean";
+        case VKHIP_OP_MAX: return "max";
+        case VKHIP_OP_ARGMAX: return "argmax";
+        case VKHIP_OP_MAX_POOL2D: return "max_pool2d";
+        case VKHIP_OP_MAX_POOL2D_BACKWARD: return "max_pool2d_backward";
+        default: return "op";
+    }
+}
+
+static int compute_node(const vkhip_node& nd) {
+    if (!supports_node(nd))
+        return fail(VKHIP_ERR_UNSUPPORTED, "vkhip: %s (op %d) is not supported for these dtypes/layout",
+                    op_name(nd.op), nd.op);
+    switch (nd.op) {
+        case VKHIP_OP_MATMUL: {
+            const vkhip_operand a = to_operand(nd.src[0]);
+            const vkhip_operand b = to_operand(nd.src[1]);
+            return gemm(static_cast<const float*>(nd.src[0].data), a,
+                        static_cast<const float*>(nd.src[1].data), b,
+                        static_cast<float*>(nd.out.data), nullptr);
+        }
+        case VKHIP_OP_SUM:
+        case VKHIP_OP_MEAN:
+        case VKHIP_OP_MAX:
+        case VKHIP_OP_MIN:
+        case VKHIP_OP_ARGMAX:
+        case VKHIP_OP_ARGMIN: {
+            uint32_t mask;
+            memcpy(&mask, nd.params, sizeof mask);
+            const int ndim = nd.src[0].ndim;
+            if (mask == 0) mask = ndim <= 0 ? 0u : (1u << ndim) - 1u;  // reduce-all
+            static const int map[] = {VKHIP_REDUCE_SUM, VKHIP_REDUCE_MEAN, VKHIP_REDUCE_MAX,
+                                      VKHIP_REDUCE_MIN, -1,                VKHIP_REDUCE_ARGMAX,
+                                      VKHIP_REDUCE_ARGMIN};
+            const vkhip_operand d = to_operand(nd.src[0]);
+            return launch_reduce(map[nd.op - VKHIP_OP_SUM], static_cast<const float*>(nd.src[0].data),
+                                 d, (mask << (4 - ndim)) & 0xfu, nd.out.data);
+        }
+        case VKHIP_OP_SOFTMAX:
+        case VKHIP_OP_LOG_SOFTMAX: {
+            int32_t axis;
+            memcpy(&axis, nd.params, sizeof axis);
+            const int ndim = nd.src[0].ndim;
+            if (axis < 0) axis += ndim;
+            if (axis < 0 || axis >= ndim) return fail(VKHIP_ERR_INVALID, "softmax: bad axis");
+            return launch_softmax(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
+                                  static_cast<float*>(nd.out.data), axis + 4 - ndim,
+                                  nd.op == VKHIP_OP_LOG_SOFTMAX);
+        }
+        case VKHIP_OP_IM2COL: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return launch_im2col(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
+                                 static_cast<float*>(nd.out.data), p);
+        }
+        case VKHIP_OP_COL2IM: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return launch_col2im(static_cast<const float*>(nd.src[0].data),
+                                 static_cast<float*>(nd.out.data), static_cast<uint32_t>(nd.out.ne[0]),
+                                 static_cast<uint32_t>(nd.out.ne[1]), p);
+        }
+        case VKHIP_OP_MAX_POOL2D: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return launch_max_pool2d(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
+                                     static_cast<float*>(nd.out.data),
+                                     static_cast<uint32_t>(nd.out.ne[2]),
+                                     static_cast<uint32_t>(nd.out.ne[3]), p);
+        }
+        case VKHIP_OP_MAX_POOL2D_BACKWARD: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return launch_max_pool2d_backward(
+                static_cast<const float*>(nd.src[0].data), static_cast<const float*>(nd.src[1].data),
+                to_operand(nd.src[1]), static_cast<float*>(nd.out.data),
+                static_cast<uint32_t>(nd.src[0].ne[2]), static_cast<uint32_t>(nd.src[0].ne[3]), p);
+        }
+        default: return launch_elementwise(nd);
+    }
+}
+
+}  // namespace vkhip
+
+using vkhip::ctx;
+using vkhip::fail;
+
+// ---- lifecycle ---------------------------------------------------------------------
+
+extern "C" int vkhip_init(int device) {
+    std::lock_guard<std::mutex> lk(vkhip::g_mu);
+    vkhip::Context& c = ctx();
+    if (c.ready) {
+        if (c.device == device) return VKHIP_OK;
+        return fail(VKHIP_ERR_INVALID, "vkhip: already bound to device %d", c.device);
+    }
+    int count = 0;
+    VKHIP_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count)
+        return fail(VKHIP_ERR_DEVICE, "vkhip: no device %d (%d visible)", device, count);
+    VKHIP_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    VKHIP_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(VKHIP_ERR_UNSUPPORTED, "vkhip: built for gfx950, device %d is %s", device,
+                    prop.gcnArchName);
+    VKHIP_HIP(hipStreamCreateWithFlags(&c.own_stream, hipStreamNonBlocking));
+    c.stream = c.own_stream;
+    c.device = device;
+    memset(&c.caps, 0, sizeof c.caps);
+    snprintf(c.caps.name, sizeof c.caps.name, "%s", prop.name);
+    c.caps.device_index = device;
+    c.caps.compute_units = prop.multiProcessorCount;
+    c.caps.wavefront_size = prop.warpSize;
+    c.caps.max_threads_per_block = prop.maxThreadsPerBlock;
+    c.caps.max_shared_memory = static_cast<int64_t>(prop.sharedMemPerBlock);
+    c.caps.total_memory = static_cast<int64_t>(prop.totalGlobalMem);
+    c.caps.global_float_atomics = 1;
+    c.caps.asynchronous = 1;
+    c.ready = true;
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_shutdown(void) {
+    std::lock_guard<std::mutex> lk(vkhip::g_mu);
+    vkhip::Context& c = ctx();
+    if (!c.ready) return VKHIP_OK;
+    if (c.ws) {
+        VKHIP_HIP(hipFreeAsync(c.ws, c.stream));
+        c.ws = nullptr;
+        c.ws_bytes = 0;
+    }
+    VKHIP_HIP(hipStreamSynchronize(c.stream));
+    VKHIP_HIP(hipStreamDestroy(c.own_stream));
+    c.own_stream = nullptr;
+    c.stream = nullptr;
+    c.ready = false;
+    return VKHIP_OK;
+}
+
+extern "C" const char* vkhip_last_error(void) { return vkhip::g_last_error; }
+
+extern "C" int vkhip_caps_get(vkhip_caps* out) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!out) return fail(VKHIP_ERR_INVALID, "caps: null output");
+    *out = ctx().caps;
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_set_stream(void* stream) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    ctx().stream = stream ? static_cast<hipStream_t>(stream) : ctx().own_stream;
+    return VKHIP_OK;
+}
+
+extern "C" void* vkhip_get_stream(void) { return ctx().stream; }
+
+// ---- memory ----------------------------------------------------------------------------
+
+extern "C" int vkhip_alloc(size_t nbytes, void** out_ptr) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!out_ptr) return fail(VKHIP_ERR_INVALID, "alloc: null output");
+    *out_ptr = nullptr;
+    if (nbytes == 0) return VKHIP_OK;
+    if (hipMallocAsync(out_ptr, nbytes, ctx().stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(VKHIP_ERR_OOM, "alloc: %zu bytes could not be allocated", nbytes);
+    }
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_free(void* ptr) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!ptr) return VKHIP_OK;
+    VKHIP_HIP(hipFreeAsync(ptr, ctx().stream));
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_copy_from_host(void* dst, const void* host_src, size_t nbytes) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (nbytes == 0) return VKHIP_OK;
+    VKHIP_HIP(hipMemcpyAsync(dst, host_src, nbytes, hipMemcpyHostToDevice, ctx().stream));
+    // The host buffer belongs to the caller once this returns.
+    VKHIP_HIP(hipStreamSynchronize(ctx().stream));
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (nbytes == 0) return VKHIP_OK;
+    VKHIP_HIP(hipMemcpyAsync(host_dst, src, nbytes, hipMemcpyDeviceToHost, ctx().stream));
+    VKHIP_HIP(hipStreamSynchronize(ctx().stream));
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_copy_device_to_device(const vkhip_copy* copies, size_t n) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    for (size_t i = 0; i < n; ++i) {
+        if (copies[i].nbytes == 0) continue;
+        VKHIP_HIP(hipMemcpyAsync(copies[i].dst, copies[i].src, copies[i].nbytes,
+                                 hipMemcpyDeviceToDevice, ctx().stream));
+    }
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_synchronize(void) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    VKHIP_HIP(hipStreamSynchronize(ctx().stream));
+    return VKHIP_OK;
+}
+
+// ---- compute -------------------------------------------------------------------------
+
+extern "C" int vkhip_supports(const vkhip_node* node) {
+    return node ? vkhip::supports_node(*node) : 0;
+}
+
+extern "C" int vkhip_compute(const vkhip_node* nodes, size_t n) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    for (size_t i = 0; i < n; ++i) {
+        st = vkhip::compute_node(nodes[i]);
+        if (st != VKHIP_OK) return st;
+    }
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_max_pool2d(const float* src, float* dst, uint32_t planes, uint32_t out_h,
+                                uint32_t out_w, const vkhip_unfold* p) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!p) return fail(VKHIP_ERR_INVALID, "max_pool2d: null params");
+    vkhip_operand d;
+    const uint32_t ne[4] = {1, planes, static_cast<uint32_t>(p->image_h), static_cast<uint32_t>(p->image_w)};
+    int64_t s = 1;
+    for (int i = 3; i >= 0; --i) {
+        d.ne[i] = ne[i];
+        d.nb[i] = s;
+        s *= ne[i];
+    }
+    return vkhip::launch_max_pool2d(src, d, dst, out_h, out_w, *p);
+}
+
+extern "C" int vkhip_max_pool2d_backward(const float* grad, const float* src, float* dst,
+                                         uint32_t planes, uint32_t out_h, uint32_t out_w,
+                                         const vkhip_unfold* p) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!p) return fail(VKHIP_ERR_INVALID, "max_pool2d_backward: null params");
+    vkhip_operand d;
+    const uint32_t ne[4] = {1, planes, static_cast<uint32_t>(p->image_h), static_cast<uint32_t>(p->image_w)};
+    int64_t s = 1;
+    for (int i = 3; i >= 0; --i) {
+        d.ne[i] = ne[i];
+        d.nb[i] = s;
+        s *= ne[i];
+    }
+    return vkhip::launch_max_pool2d_backward(grad, src, d, dst, out_h, out_w, *p);
+}
+
+// ---- host-side planning helpers (no device needed) -----------------------------------
+
+extern "C" int vkhip_pairwise_leaf(uint32_t n, uint32_t leaf, uint32_t* out_depth,
+                                   uint32_t* out_begin, uint32_t* out_end) {
+    const int depth = vkhip::pairwise_depth(n);
+    uint32_t b = 0, e = 0;
+    if (leaf < (1u << depth)) vkhip::pairwise_leaf(n, depth, leaf, b, e);
+    if (out_depth) *out_depth = static_cast<uint32_t>(depth);
+    if (out_begin) *out_begin = b;
+    if (out_end) *out_end = e;
+    return leaf < (1u << depth) ? VKHIP_OK : VKHIP_ERR_INVALID;
+}
