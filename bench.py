@@ -51,18 +51,12 @@ def parse():
 
 
 class Timer:
-    """HIP events on the backend's own stream (torch wraps the handle)."""
-
-    def __init__(self, stream_handle: int):
-        import torch
-
-        self.torch = torch
-        self.stream = torch.cuda.ExternalStream(stream_handle)
+    """HIP events recorded on the backend's own stream, through the C ABI."""
 
     def event(self):
-        ev = self.torch.cuda.Event(enable_timing=True)
-        ev.record(self.stream)
-        return ev
+        from vkml_amd.device import Event
+
+        return Event().record()
 
 
 def time_launches(fn, timer: Timer, reps: int, warmup: int = 3):
@@ -75,8 +69,7 @@ def time_launches(fn, timer: Timer, reps: int, warmup: int = 3):
         fn(i)
         e = timer.event()
         pairs.append((s, e))
-    pairs[-1][1].synchronize()
-    return [s.elapsed_time(e) for s, e in pairs]
+    return [s.elapsed_ms(e) for s, e in pairs]
 
 
 def gemm_headline(args, hip, ops, timer):
@@ -99,7 +92,7 @@ def gemm_headline(args, hip, ops, timer):
         events.append((s, e))
     hip.synchronize()
     wall = time.perf_counter() - t0
-    launch_ms = [s.elapsed_time(e) for s, e in events]
+    launch_ms = [s.elapsed_ms(e) for s, e in events]
     flop = 2.0 * m * n * k
     value = flop * args.steps / wall / 1e12
     avg_ms = float(np.mean(launch_ms))
@@ -211,7 +204,7 @@ def main():
     from vkml_amd.device import backend
 
     hip = backend()
-    timer = Timer(hip.stream_handle())
+    timer = Timer()
     value, ms_step, avg_ms, achieved, min_ms = gemm_headline(args, hip, ops, timer)
     result = {
         "metric": METRIC,

@@ -282,6 +282,17 @@ int vkhip_scaled_add(const float* a, const float* b, float* out, uint64_t n, flo
                      float beta);
 
 /* ======================================================================== */
+/* Timing (the reference's per-dispatch timestamp pairs, vk_command.h:185-256,
+ * exposed as HIP events on the backend stream)                              */
+/* ======================================================================== */
+int vkhip_event_create(void** out_event);
+int vkhip_event_destroy(void* event);
+/* Records `event` on the backend stream, after all work enqueued so far. */
+int vkhip_event_record(void* event);
+/* Milliseconds between two recorded events; waits for `end` to complete. */
+int vkhip_event_elapsed(void* start, void* end, float* out_ms);
+
+/* ======================================================================== */
 /* Host-side planning helpers (callable without a GPU)                       */
 /* ======================================================================== */
 /* Geometry of the CPU oracle's pairwise-summation tree (reference

@@ -98,6 +98,10 @@ SIGNATURES = {
     "vkhip_max_pool2d_backward": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32,
                                           c_uint32, POINTER(Unfold)]),
     "vkhip_scaled_add": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_float, c_float]),
+    "vkhip_event_create": (c_int, [POINTER(c_void_p)]),
+    "vkhip_event_destroy": (c_int, [c_void_p]),
+    "vkhip_event_record": (c_int, [c_void_p]),
+    "vkhip_event_elapsed": (c_int, [c_void_p, c_void_p, POINTER(c_float)]),
     "vkhip_pairwise_leaf": (c_int, [c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_uint32),
                                     POINTER(c_uint32)]),
 }

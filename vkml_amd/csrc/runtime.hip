@@ -458,6 +458,40 @@ extern "C" int vkhip_max_pool2d_backward(const float* grad, const float* src, fl
     return vkhip::launch_max_pool2d_backward(grad, src, d, dst, out_h, out_w, *p);
 }
 
+// ---- timing ------------------------------------------------------------------------------
+
+extern "C" int vkhip_event_create(void** out_event) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!out_event) return fail(VKHIP_ERR_INVALID, "event_create: null output");
+    hipEvent_t e;
+    VKHIP_HIP(hipEventCreate(&e));
+    *out_event = e;
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_event_destroy(void* event) {
+    if (!event) return VKHIP_OK;
+    VKHIP_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)));
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_event_record(void* event) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    VKHIP_HIP(hipEventRecord(static_cast<hipEvent_t>(event), ctx().stream));
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_event_elapsed(void* start, void* end, float* out_ms) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!out_ms) return fail(VKHIP_ERR_INVALID, "event_elapsed: null output");
+    VKHIP_HIP(hipEventSynchronize(static_cast<hipEvent_t>(end)));
+    VKHIP_HIP(hipEventElapsedTime(out_ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)));
+    return VKHIP_OK;
+}
+
 // ---- host-side planning helpers (no device needed) -----------------------------------
 
 extern "C" int vkhip_pairwise_leaf(uint32_t n, uint32_t leaf, uint32_t* out_depth,

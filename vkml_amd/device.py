@@ -255,6 +255,34 @@ class HipBackend:
         return self.lib.vkhip_get_stream() or 0
 
 
+class Event:
+    """A HIP event recorded on the backend stream (launch timing)."""
+
+    __slots__ = ("handle", "__weakref__")
+
+    def __init__(self):
+        h = c_void_p()
+        check(backend().lib.vkhip_event_create(byref(h)), "event_create")
+        self.handle = h.value
+        weakref.finalize(self, _destroy_event, self.handle)
+
+    def record(self) -> "Event":
+        check(backend().lib.vkhip_event_record(c_void_p(self.handle)), "event_record")
+        return self
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        check(backend().lib.vkhip_event_elapsed(c_void_p(self.handle), c_void_p(end.handle),
+                                                byref(ms)), "event_elapsed")
+        return float(ms.value)
+
+
+def _destroy_event(handle: int) -> None:
+    b = _BACKEND
+    if b is not None and b.alive:
+        b.lib.vkhip_event_destroy(c_void_p(handle))
+
+
 _BACKEND: HipBackend | None = None
 
 
