@@ -59,10 +59,29 @@ class Timer:
         return Event().record()
 
 
+_GATE = None
+
+
+def gate():
+    """Enqueues ~2 ms of GEMM so the host can queue the timed launches ahead of
+    the GPU: event pairs then bracket GPU time only, not Python launch gaps."""
+    global _GATE
+    from vkml_amd import ops
+    from vkml_amd.device import DeviceArray
+
+    if _GATE is None:
+        a = DeviceArray.from_numpy(np.ones((4096, 4096), np.float32))
+        _GATE = (a, DeviceArray((4096, 4096), np.float32))
+    a, c = _GATE
+    for _ in range(2):
+        ops.matmul(a, a, out=c)
+
+
 def time_launches(fn, timer: Timer, reps: int, warmup: int = 3):
     """Per-launch durations (ms) from event pairs around each call."""
     for _ in range(warmup):
         fn(0)
+    gate()
     pairs = []
     for i in range(reps):
         s = timer.event()
@@ -155,6 +174,14 @@ def secondary(hip, ops, timer):
         out[name] = {"ms": ms, "tflops": 2.0 * m * n * k / ms / 1e9,
                      "frac_of_peak": 2.0 * m * n * k / ms / 1e9 / MFMA_FP32_PEAK_TFLOPS,
                      "splits": splits}
+
+    # Practical HBM ceiling: the library's plain 16-byte copy, 4 x 256 MiB buffers
+    bufs = [DeviceArray((64 << 20,), np.float32) for _ in range(4)]
+    byt = 2 * (64 << 20) * 4
+    ms = med(time_launches(lambda i: hip.copy_device_to_device([(bufs[(i + 1) % 4], bufs[i % 4])]),
+                           timer, 20))
+    out["copy_256MiB"] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+    del bufs
 
     # GEMV 4096x4096 . 4096 (bandwidth): rotate 8 matrices (512 MB)
     mats = rotate((4096, 4096), 8)

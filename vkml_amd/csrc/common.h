@@ -137,4 +137,86 @@ __host__ __device__ __forceinline__ void pairwise_leaf(uint32_t n, int depth, ui
     end = e;
 }
 
+// ---- staged rows ------------------------------------------------------------
+// A row that is summed in the pairwise order is first staged in LDS with 4
+// padding floats after every 32 elements: each full 32-element leaf then starts
+// on a 16-byte boundary (read as eight 16-byte loads), and eight consecutive
+// leaves start 36 floats apart, which spreads them over distinct LDS banks.
+__host__ __device__ __forceinline__ uint32_t stage_index(uint32_t i) { return i + 4u * (i >> 5); }
+
+// Floats one staged row of n elements occupies, rounded to 16 bytes.
+__host__ __device__ __forceinline__ uint32_t stage_stride(uint32_t n) {
+    return (n + 4u * ((n + 31u) / 32u) + 3u) & ~3u;
+}
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Sequential sum from +0.0 of the leaf [b, e) (e - b <= 32) of a staged row.
+// All loads are issued before the additions; absent slots add +0.0, which is
+// exact because a sum started from +0.0 is never -0.0.
+__device__ __forceinline__ float staged_leaf_sum(const float* st, uint32_t b, uint32_t e) {
+    float s = 0.0f;
+    if (e - b == 32u && (b & 31u) == 0u) {
+        const f32x4_t* p = reinterpret_cast<const f32x4_t*>(st + stage_index(b));
+#pragma unroll
+        for (int h = 0; h < 8; h += 4) {
+            f32x4_t v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = p[h + i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s = s + v[i][j];
+        }
+        return s;
+    }
+#pragma unroll
+    for (int c = 0; c < 32; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (b + c + i < e) ? st[stage_index(b + c + i)] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = s + v[i];
+    }
+    return s;
+}
+
+// Sum of the `per` consecutive depth-D leaves starting at leaf `first` of a
+// staged row of n elements, folded with the binary-counter carry stack (per is
+// a power of two, so this is the balanced subtree over those leaves).
+__device__ __forceinline__ float staged_subtree_sum(const float* st, uint32_t n, int depth,
+                                                    uint32_t first, uint32_t per) {
+    float stack[9];
+#pragma unroll
+    for (int l = 0; l < 9; ++l) stack[l] = 0.0f;
+    for (uint32_t t = 0; t < per; ++t) {
+        uint32_t b, e;
+        pairwise_leaf(n, depth, first + t, b, e);
+        float s = staged_leaf_sum(st, b, e);
+        bool carry = true;
+#pragma unroll
+        for (int l = 0; l < 9; ++l) {
+            if (carry) {
+                if ((t >> l) & 1u) {
+                    s = stack[l] + s;
+                } else {
+                    stack[l] = s;
+                    carry = false;
+                }
+            }
+        }
+    }
+    float v = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 9; ++l)
+        if ((1u << l) == per) v = stack[l];
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_butterfly(float v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
 }  // namespace vkhip

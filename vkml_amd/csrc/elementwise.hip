@@ -261,6 +261,33 @@ int launch_elementwise(const vkhip_node& nd) {
     return VKHIP_OK;
 }
 
+// Plain 16-byte copy: the batched device-to-device copy, and the kernel whose
+// measured bandwidth and HBM byte counters calibrate every other kernel's.
+__global__ __launch_bounds__(256) void copy16_kernel(const f32x4_t* __restrict__ src,
+                                                     f32x4_t* __restrict__ dst, uint64_t n16) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16;
+         i += stride)
+        dst[i] = src[i];
+}
+
+int launch_copy_bytes(void* dst, const void* src, size_t nbytes) {
+    if (nbytes == 0) return VKHIP_OK;
+    hipStream_t st = ctx().stream;
+    if (reinterpret_cast<uintptr_t>(dst) % 16 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+        nbytes % 16 == 0) {
+        const uint64_t n16 = nbytes / 16;
+        const uint64_t want = (n16 + 255) / 256;
+        const uint32_t blocks = static_cast<uint32_t>(want < 8192 ? want : 8192);
+        hipLaunchKernelGGL(copy16_kernel, dim3(blocks), dim3(256), 0, st,
+                           static_cast<const f32x4_t*>(src), static_cast<f32x4_t*>(dst), n16);
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
+    VKHIP_HIP(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, st));
+    return VKHIP_OK;
+}
+
 }  // namespace vkhip
 
 extern "C" int vkhip_scaled_add(const float* a, const float* b, float* out, uint64_t n, float alpha,

@@ -42,17 +42,31 @@ struct GemmArgs {
 };
 
 // Loads one BK-deep tile of an operand (rows x BK) into registers as groups of
-// four consecutive k. KC: the operand is k-contiguous, so lanes walk k first
-// and load 16 bytes each. Otherwise lanes walk rows, so a 4-byte load per k is
-// coalesced along the row axis (the m- or n-contiguous transposed operand).
-template <int R, int BK, bool KC>
+// four consecutive k, then stores each group to LDS [row][k] as 16 bytes.
+//   KCV  k-contiguous and 16-byte aligned (A in NN, B in NT): lanes walk k
+//        first, one 16-byte load per group.
+//   RCV  row-contiguous and aligned (B in NN, A in TN): each thread loads a
+//        4-row x 4-k block as four 16-byte loads along the rows and transposes
+//        it in registers. Lanes walk k-blocks first, so eight lanes fill one
+//        128-byte line per k and their LDS stores land on distinct banks.
+//   KCS / RCS  any other layout: four 4-byte loads per group, lanes along k
+//        (k-contiguous) or along rows.
+// GUARD = false is the interior fast path: the whole tile is in range, so no
+// per-element bounds checks are emitted.
+enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3 };
+
+template <int R, int BK, int MODE>
 struct TileLoader {
+    static constexpr bool KMAP = MODE == KCV || MODE == KCS;  // lanes walk k first
     static constexpr int kGroups = R * BK / 4;
     static constexpr int kPer = kGroups / 256;
     static_assert(kGroups % 256 == 0, "tile must split evenly over 256 threads");
+    static constexpr int kTiles = R * BK / 16;        // 4x4 blocks
+    static constexpr int kTPT = (kTiles + 255) / 256;  // blocks per thread
+    static constexpr int kRegs = MODE == RCV ? 4 * kTPT : kPer;
 
     __device__ __forceinline__ static void row_kq(int g, int& r, int& kq) {
-        if (KC) {
+        if (KMAP) {
             kq = g % (BK / 4);
             r = g / (BK / 4);
         } else {
@@ -61,47 +75,93 @@ struct TileLoader {
         }
     }
 
-    __device__ __forceinline__ static void load(f32x4 (&v)[kPer], const float* base, int64_t s_row,
+    template <bool GUARD>
+    __device__ __forceinline__ static void load(f32x4 (&v)[kRegs], const float* base, int64_t s_row,
                                                 int64_t s_k, uint32_t row0, uint32_t rows,
-                                                uint32_t k0, uint32_t kdim, bool vec, int tid) {
+                                                uint32_t k0, uint32_t kdim, int tid) {
+        if constexpr (MODE == RCV) {
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            int r, kq;
-            row_kq(tid + 256 * i, r, kq);
-            const uint32_t gr = row0 + r;
-            const uint32_t gk = k0 + 4 * kq;
-            const float* p = base + static_cast<int64_t>(gr) * s_row + static_cast<int64_t>(gk) * s_k;
-            if (KC && vec && gr < rows && gk + 3 < kdim) {
-                v[i] = *reinterpret_cast<const f32x4*>(p);
-            } else {
-                f32x4 t;
+            for (int tt = 0; tt < kTPT; ++tt) {
+                const int tile = tid + 256 * tt;
+                const bool active = kTiles % 256 == 0 || tile < kTiles;
+                const int kg = tile % (BK / 4), mg = active ? tile / (BK / 4) : 0;
+                const uint32_t gr0 = row0 + 4 * mg;
+                const uint32_t gk0 = k0 + 4 * kg;
+                f32x4 c[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    t[j] = (gr < rows && gk + j < kdim) ? p[j * s_k] : 0.0f;
+                    const float* p = base + static_cast<int64_t>(gk0 + j) * s_k + gr0;
+                    if (!GUARD || (active && gr0 + 3 < rows && gk0 + j < kdim)) {
+                        c[j] = *reinterpret_cast<const f32x4*>(p);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            c[j][i] = (active && gr0 + i < rows && gk0 + j < kdim) ? p[i] : 0.0f;
+                    }
                 }
-                v[i] = t;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f32x4 t;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) t[j] = c[j][i];
+                    v[4 * tt + i] = t;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                int r, kq;
+                row_kq(tid + 256 * i, r, kq);
+                const uint32_t gr = row0 + r;
+                const uint32_t gk = k0 + 4 * kq;
+                const float* p =
+                    base + static_cast<int64_t>(gr) * s_row + static_cast<int64_t>(gk) * s_k;
+                if (MODE == KCV && (!GUARD || (gr < rows && gk + 3 < kdim))) {
+                    v[i] = *reinterpret_cast<const f32x4*>(p);
+                } else {
+                    f32x4 t;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        t[j] = (!GUARD || (gr < rows && gk + j < kdim)) ? p[j * s_k] : 0.0f;
+                    v[i] = t;
+                }
             }
         }
     }
 
-    __device__ __forceinline__ static void store(const f32x4 (&v)[kPer], float* lds, int tid) {
+    __device__ __forceinline__ static void store(const f32x4 (&v)[kRegs], float* lds, int tid) {
+        if constexpr (MODE == RCV) {
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            int r, kq;
-            row_kq(tid + 256 * i, r, kq);
-            *reinterpret_cast<f32x4*>(lds + r * (BK + 4) + 4 * kq) = v[i];
+            for (int tt = 0; tt < kTPT; ++tt) {
+                const int tile = tid + 256 * tt;
+                if (kTiles % 256 == 0 || tile < kTiles) {
+                    const int kg = tile % (BK / 4), mg = tile / (BK / 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        *reinterpret_cast<f32x4*>(lds + (4 * mg + i) * (BK + 4) + 4 * kg) =
+                            v[4 * tt + i];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                int r, kq;
+                row_kq(tid + 256 * i, r, kq);
+                *reinterpret_cast<f32x4*>(lds + r * (BK + 4) + 4 * kq) = v[i];
+            }
         }
     }
 };
 
-template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC>
+template <int BM, int BN, int BK, int WM, int WN, int AMODE, int BMODE>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
     static_assert((BM / WM) * (BN / WN) == 4, "four waves per workgroup");
     constexpr int LDK = BK + 4;
     constexpr int MI = WM / 32;
     constexpr int NI = WN / 32;
-    using LA = TileLoader<BM, BK, AKC>;
-    using LB = TileLoader<BN, BK, BKC>;
+    constexpr int QN = BK / 8;  // groups of four MFMA k-steps per K-tile
+    using LA = TileLoader<BM, BK, AMODE>;
+    using LB = TileLoader<BN, BK, BMODE>;
 
     __shared__ __attribute__((aligned(16))) float lds[2][(BM + BN) * LDK];
 
@@ -134,6 +194,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 
     const uint32_t kt0 = blockIdx.y * g.chunk;
     const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
+    // Whole tile inside M x N: K-tiles that are also inside K load unguarded.
+    const bool rows_in = row0 + BM <= g.m && col0 + BN <= g.n;
 
     f32x16 acc[MI][NI];
 #pragma unroll
@@ -143,10 +205,18 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    f32x4 ra[LA::kPer], rb[LB::kPer];
+    f32x4 ra[LA::kRegs], rb[LB::kRegs];
+    auto load_tile = [&](uint32_t kt) {
+        if (rows_in && (kt + 1) * BK <= g.k) {
+            LA::template load<false>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
+            LB::template load<false>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
+        } else {
+            LA::template load<true>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
+            LB::template load<true>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
+        }
+    };
     if (kt0 < kt1) {
-        LA::load(ra, abase, g.sam, g.sak, row0, g.m, kt0 * BK, g.k, g.a_vec, tid);
-        LB::load(rb, bbase, g.sbn, g.sbk, col0, g.n, kt0 * BK, g.k, g.b_vec, tid);
+        load_tile(kt0);
         LA::store(ra, lds[0], tid);
         LB::store(rb, lds[0] + BM * LDK, tid);
     }
@@ -157,31 +227,47 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
     for (uint32_t kt = kt0; kt < kt1; ++kt) {
         const int cur = (kt - kt0) & 1;
         const bool more = kt + 1 < kt1;
-        if (more) {
-            LA::load(ra, abase, g.sam, g.sak, row0, g.m, (kt + 1) * BK, g.k, g.a_vec, tid);
-            LB::load(rb, bbase, g.sbn, g.sbk, col0, g.n, (kt + 1) * BK, g.k, g.b_vec, tid);
-        }
-        const float* As = lds[cur];
-        const float* Bs = lds[cur] + BM * LDK;
+        if (more) load_tile(kt + 1);
+        const float* As = lds[cur] + (wm0 + lrow) * LDK + kh * (BK / 2);
+        const float* Bs = lds[cur] + BM * LDK + (wn0 + lrow) * LDK + kh * (BK / 2);
+        // MFMA operands for step group q+1 are read from LDS while group q's
+        // MFMAs run (two register sets).
+        f32x4 av[2][MI], bv[2][NI];
 #pragma unroll
-        for (int q = 0; q < BK / 8; ++q) {
-            f32x4 av[MI], bv[NI];
+        for (int i = 0; i < MI; ++i) av[0][i] = *reinterpret_cast<const f32x4*>(As + 32 * i * LDK);
 #pragma unroll
-            for (int i = 0; i < MI; ++i)
-                av[i] = *reinterpret_cast<const f32x4*>(As + (wm0 + 32 * i + lrow) * LDK +
-                                                        kh * (BK / 2) + 4 * q);
+        for (int j = 0; j < NI; ++j) bv[0][j] = *reinterpret_cast<const f32x4*>(Bs + 32 * j * LDK);
 #pragma unroll
-            for (int j = 0; j < NI; ++j)
-                bv[j] = *reinterpret_cast<const f32x4*>(Bs + (wn0 + 32 * j + lrow) * LDK +
-                                                        kh * (BK / 2) + 4 * q);
+        for (int q = 0; q < QN; ++q) {
+            const int cb = q & 1;
+            if (q + 1 < QN) {
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+                    av[cb ^ 1][i] = *reinterpret_cast<const f32x4*>(As + 32 * i * LDK + 4 * (q + 1));
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    bv[cb ^ 1][j] = *reinterpret_cast<const f32x4*>(Bs + 32 * j * LDK + 4 * (q + 1));
+            }
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
 #pragma unroll
                     for (int j = 0; j < NI; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bv[j][s],
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][i][s], bv[cb][j][s],
                                                                          acc[i][j], 0, 0, 0);
+            // Spread the next group's LDS reads over this group's MFMAs, one
+            // 16-byte read after every MFMA pair; left to itself the compiler
+            // bunches them, which exposes LDS latency between MFMA bursts
+            // (measured: 110 -> 116 TFLOP/s on NN 4096^3).
+            {
+                const int reads = (q + 1 < QN) ? (MI + NI) : 0;
+#pragma unroll
+                for (int r = 0; r < 4 * MI * NI / 2; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    if (r < reads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            }
         }
         if (more) {
             LA::store(ra, lds[cur ^ 1], tid);
@@ -250,19 +336,14 @@ __global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __rest
 // as the oracle's widen(a)*widen(b)), and summed in the oracle's pairwise tree:
 // lanes own depth-D leaves, then adjacent leaves combine by xor-butterfly.
 // Bit-exact against the CPU oracle.
-constexpr int kGemvMaxK = 4096;  // LDS-staged row length per wave (+1 pad per 32)
-
-__device__ __forceinline__ float wave_butterfly_sum(float v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
-}
+constexpr int kGemvMaxK = 4096;  // row length one wave stages in LDS
 
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ a, int64_t lda,
                                                    const float* __restrict__ x, int64_t incx,
                                                    float* __restrict__ y, uint32_t m, uint32_t k,
                                                    int depth, int vec) {
-    __shared__ float prod[4][kGemvMaxK + kGemvMaxK / 32];
+    constexpr uint32_t kStage = (kGemvMaxK + 4 * (kGemvMaxK / 32) + 3) & ~3u;
+    __shared__ __attribute__((aligned(16))) float prod[4][kStage];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + wave;
@@ -271,24 +352,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ a, 
     if (live) {
         const float* ar = a + static_cast<int64_t>(row) * lda;
         if (vec) {
-            for (uint32_t c = 4 * lane; c < k; c += 256) {
-                const f32x4 av = *reinterpret_cast<const f32x4*>(ar + c);
-                f32x4 xv;
-                if (incx == 1) {
-                    xv = *reinterpret_cast<const f32x4*>(x + c);
-                } else {
+            // 16 groups of 4 per lane at most (K <= 4096): issue every load first.
+            f32x4 av[kGemvMaxK / 256], xv[kGemvMaxK / 256];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) xv[j] = x[static_cast<int64_t>(c + j) * incx];
+            for (int i = 0; i < kGemvMaxK / 256; ++i) {
+                const uint32_t c = 4u * lane + 256u * i;
+                if (c < k) {
+                    av[i] = *reinterpret_cast<const f32x4*>(ar + c);
+                    if (incx == 1) {
+                        xv[i] = *reinterpret_cast<const f32x4*>(x + c);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) xv[i][j] = x[static_cast<int64_t>(c + j) * incx];
+                    }
                 }
+            }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t e = c + j;
-                    pr[e + (e >> 5)] = __fmul_rn(av[j], xv[j]);
+            for (int i = 0; i < kGemvMaxK / 256; ++i) {
+                const uint32_t c = 4u * lane + 256u * i;
+                if (c < k) {
+                    f32x4 p;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) p[j] = __fmul_rn(av[i][j], xv[i][j]);
+                    *reinterpret_cast<f32x4*>(pr + stage_index(c)) = p;
                 }
             }
         } else {
             for (uint32_t e = lane; e < k; e += 64)
-                pr[e + (e >> 5)] = __fmul_rn(ar[e], x[static_cast<int64_t>(e) * incx]);
+                pr[stage_index(e)] = __fmul_rn(ar[e], x[static_cast<int64_t>(e) * incx]);
         }
     }
     __syncthreads();
@@ -297,37 +388,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ a, 
     const uint32_t leaves = 1u << depth;
     const uint32_t per = leaves > 64 ? leaves / 64 : 1;
     float v = 0.0f;
-    if (static_cast<uint32_t>(lane) * per < leaves) {
-        // Carry stack over this lane's `per` leaves (a power of two: one
-        // balanced subtree, whose total ends at level log2(per)).
-        float stack[8];
-#pragma unroll
-        for (int l = 0; l < 8; ++l) stack[l] = 0.0f;
-        for (uint32_t t = 0; t < per; ++t) {
-            uint32_t b, e;
-            pairwise_leaf(k, depth, lane * per + t, b, e);
-            float s = 0.0f;
-            for (uint32_t q = b; q < e; ++q) s = s + pr[q + (q >> 5)];
-            bool carry = true;
-#pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                if (carry) {
-                    if ((t >> l) & 1u) {
-                        s = stack[l] + s;
-                    } else {
-                        stack[l] = s;
-                        carry = false;
-                    }
-                }
-            }
-        }
-        int top = 0;
-        while ((1u << top) < per) ++top;
-#pragma unroll
-        for (int l = 0; l < 8; ++l)
-            if (l == top) v = stack[l];
-    }
-    v = wave_butterfly_sum(v);
+    if (static_cast<uint32_t>(lane) * per < leaves) v = staged_subtree_sum(pr, k, depth, lane * per, per);
+    v = wave_sum_butterfly(v);
     if (lane == 0) y[row] = v;
 }
 
@@ -376,19 +438,27 @@ static TileChoice choose_tile(uint32_t m, uint32_t n) {
     return {64, 64};
 }
 
-template <int BM, int BN, int WM, int WN>
-static int launch_tiles(const GemmArgs& g, uint32_t batch, uint32_t splits, bool akc, bool bkc) {
+template <int BM, int BN, int WM, int WN, int AM>
+static void launch_b(const GemmArgs& g, dim3 grid, hipStream_t st, int bmode) {
     constexpr int BK = 32;
+    switch (bmode) {
+        case KCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCV>), grid, dim3(256), 0, st, g); break;
+        case RCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, RCV>), grid, dim3(256), 0, st, g); break;
+        case KCS: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCS>), grid, dim3(256), 0, st, g); break;
+        default: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, RCS>), grid, dim3(256), 0, st, g); break;
+    }
+}
+
+template <int BM, int BN, int WM, int WN>
+static int launch_tiles(const GemmArgs& g, uint32_t batch, uint32_t splits, int amode, int bmode) {
     dim3 grid(g.tiles_m * g.tiles_n, splits, batch);
     hipStream_t st = ctx().stream;
-    if (akc && bkc)
-        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, true, true>), grid, dim3(256), 0, st, g);
-    else if (akc)
-        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, true, false>), grid, dim3(256), 0, st, g);
-    else if (bkc)
-        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, false, true>), grid, dim3(256), 0, st, g);
-    else
-        hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, false, false>), grid, dim3(256), 0, st, g);
+    switch (amode) {
+        case KCV: launch_b<BM, BN, WM, WN, KCV>(g, grid, st, bmode); break;
+        case RCV: launch_b<BM, BN, WM, WN, RCV>(g, grid, st, bmode); break;
+        case KCS: launch_b<BM, BN, WM, WN, KCS>(g, grid, st, bmode); break;
+        default: launch_b<BM, BN, WM, WN, RCS>(g, grid, st, bmode); break;
+    }
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -491,8 +561,13 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     auto aligned = [](const float* p, int64_t s0, int64_t s1, int64_t srow) {
         return reinterpret_cast<uintptr_t>(p) % 16 == 0 && s0 % 4 == 0 && s1 % 4 == 0 && srow % 4 == 0;
     };
-    g.a_vec = akc && ad.nb[3] == 1 && aligned(a, g.sa0, g.sa1, g.sam);
-    g.b_vec = bkc && bd.nb[2] == 1 && aligned(b, g.sb0, g.sb1, g.sbn);
+    // 16-byte loads: along k for a k-contiguous operand, along rows for a
+    // row-contiguous one (then the k stride is the row pitch that must keep
+    // 16-byte alignment).
+    g.a_vec = akc ? (ad.nb[3] == 1 && aligned(a, g.sa0, g.sa1, g.sam))
+                  : (g.sam == 1 && aligned(a, g.sa0, g.sa1, g.sak));
+    g.b_vec = bkc ? (bd.nb[2] == 1 && aligned(b, g.sb0, g.sb1, g.sbn))
+                  : (g.sbn == 1 && aligned(b, g.sb0, g.sb1, g.sbk));
 
     const uint64_t out_elems = batch * m * n;
     float* target = c;
@@ -504,11 +579,13 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
         g.split_stride = out_elems;
     }
     g.c = target;
+    const int amode = akc ? (g.a_vec ? KCV : KCS) : (g.a_vec ? RCV : RCS);
+    const int bmode = bkc ? (g.b_vec ? KCV : KCS) : (g.b_vec ? RCV : RCS);
     int st;
     if (tile.bm == 128)
-        st = launch_tiles<128, 128, 64, 64>(g, static_cast<uint32_t>(batch), splits, akc, bkc);
+        st = launch_tiles<128, 128, 64, 64>(g, static_cast<uint32_t>(batch), splits, amode, bmode);
     else
-        st = launch_tiles<64, 64, 32, 32>(g, static_cast<uint32_t>(batch), splits, akc, bkc);
+        st = launch_tiles<64, 64, 32, 32>(g, static_cast<uint32_t>(batch), splits, amode, bmode);
     if (st != VKHIP_OK) return st;
     if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
     return VKHIP_OK;

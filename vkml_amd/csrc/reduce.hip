@@ -22,12 +22,6 @@ namespace vkhip {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float wave_sum_butterfly(float v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
-}
-
 __device__ __forceinline__ float max_ignoring_nan(float a, float b) { return (a < b) ? b : a; }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -36,54 +30,17 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-__device__ __forceinline__ uint32_t padded(uint32_t i) { return i + (i >> 5); }
-
-// Sum of the `per` consecutive depth-D leaves starting at leaf `first`, folded
-// with the binary-counter carry stack (per is a power of two, so the result is
-// the balanced subtree over those leaves).
-__device__ __forceinline__ float leaves_subtree_sum(const float* lds, uint32_t n, int depth,
-                                                    uint32_t first, uint32_t per) {
-    float stack[9];
-#pragma unroll
-    for (int l = 0; l < 9; ++l) stack[l] = 0.0f;
-    for (uint32_t t = 0; t < per; ++t) {
-        uint32_t b, e;
-        pairwise_leaf(n, depth, first + t, b, e);
-        float s = 0.0f;
-        for (uint32_t q = b; q < e; ++q) s = s + lds[padded(q)];
-        bool carry = true;
-#pragma unroll
-        for (int l = 0; l < 9; ++l) {
-            if (carry) {
-                if ((t >> l) & 1u) {
-                    s = stack[l] + s;
-                } else {
-                    stack[l] = s;
-                    carry = false;
-                }
-            }
-        }
-    }
-    int top = 0;
-    while ((1u << top) < per) ++top;
-    float v = 0.0f;
-#pragma unroll
-    for (int l = 0; l < 9; ++l)
-        if (l == top) v = stack[l];
-    return v;
-}
-
-// Pairwise sum of the n values staged (padded) in `lds` by a group of T threads
-// (t = index within the group). Every thread of the group gets the total.
-// `scratch` holds T/64 floats for the group. All threads of the BLOCK must call
-// this together (it contains block barriers when T > 64).
+// Pairwise sum of the n values staged in `st` by a group of T threads (t =
+// index within the group). Every thread of the group gets the total. `scratch`
+// holds T/64 floats for the group. All threads of the BLOCK must call this
+// together (it contains block barriers when T > 64).
 template <int T>
-__device__ float group_pairwise_sum(const float* lds, uint32_t n, int depth, int t,
+__device__ float group_pairwise_sum(const float* st, uint32_t n, int depth, int t,
                                     float* scratch) {
     const uint32_t leaves = 1u << depth;
     const uint32_t per = leaves > static_cast<uint32_t>(T) ? leaves / T : 1u;
     float v = 0.0f;
-    if (static_cast<uint32_t>(t) * per < leaves) v = leaves_subtree_sum(lds, n, depth, t * per, per);
+    if (static_cast<uint32_t>(t) * per < leaves) v = staged_subtree_sum(st, n, depth, t * per, per);
     v = wave_sum_butterfly(v);
     if constexpr (T > 64) {
         const int lane = t & 63, wave = t >> 6;
@@ -110,17 +67,52 @@ __device__ float group_max(float v, int t, float* scratch) {
     return v;
 }
 
+// Rows per 256-thread block when a group of T threads owns a row.
+template <int T>
+struct Rows {
+    static constexpr int kPerBlock = T >= 256 ? 1 : 256 / T;
+    static constexpr int kThreads = T >= 256 ? T : 256;
+};
+
+// Loads this thread's share of a contiguous row: float4 groups 4*(t + T*i)
+// (vec) or elements t + T*i (scalar), i < E4 (vec) / 4*E4 (scalar).
+template <int T, int E4>
+__device__ __forceinline__ void load_row(float (&x)[4 * E4], const float* rs, uint32_t n, int t,
+                                         bool live, int vec) {
+    if (vec) {
+#pragma unroll
+        for (int i = 0; i < E4; ++i) {
+            const uint32_t e0 = 4u * (t + T * i);
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (live && e0 < n) v = *reinterpret_cast<const f32x4*>(rs + e0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x[4 * i + j] = v[j];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4 * E4; ++i) {
+            const uint32_t e = t + T * i;
+            x[i] = (live && e < n) ? rs[e] : 0.0f;
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t elem_of(int vec, int T, int t, int i) {
+    return vec ? 4u * (t + T * (i / 4)) + (i % 4) : static_cast<uint32_t>(t + T * i);
+}
+
 // ---- softmax over contiguous rows ------------------------------------------------
-// T threads per row (64: four rows per 256-thread block), rows of n <= NMAX
-// contiguous floats at src + row*in_stride; dst rows contiguous.
-template <int T, int NMAX>
-__global__ __launch_bounds__(T >= 256 ? T : 256) void softmax_rows_kernel(
+// T threads per row (64: four rows per 256-thread block), rows of n <= 4*E4*T
+// contiguous floats at src + row*in_stride; dst rows contiguous. The row is read
+// once into registers; exp(x - peak) is computed once, staged in LDS for the
+// pairwise denominator and kept in registers for the output.
+template <int T, int E4>
+__global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
     const float* __restrict__ src, int64_t in_stride, float* __restrict__ dst, uint32_t rows,
-    uint32_t n, int depth, int log_mode, int vec) {
-    constexpr int RPB = T >= 256 ? 1 : 256 / T;
-    constexpr int E = NMAX / T;  // elements per thread at most
-    static_assert(E % 4 == 0, "elements per thread must be a multiple of 4");
-    __shared__ float lds[RPB][NMAX + NMAX / 32];
+    uint32_t n, int depth, int log_mode, int vec, uint32_t sstride) {
+    constexpr int RPB = Rows<T>::kPerBlock;
+    constexpr int E = 4 * E4;
+    extern __shared__ __attribute__((aligned(16))) float dyn[];
     __shared__ float scratch[RPB][T / 64 > 0 ? T / 64 : 1];
 
     const int slot = threadIdx.x / T;
@@ -128,36 +120,23 @@ __global__ __launch_bounds__(T >= 256 ? T : 256) void softmax_rows_kernel(
     const uint32_t row = blockIdx.x * RPB + slot;
     const bool live = row < rows;
     const float* rs = src + static_cast<int64_t>(live ? row : 0) * in_stride;
-    float* stage = lds[slot];
+    float* stage = dyn + slot * sstride;
 
     float x[E];
+    load_row<T, E4>(x, rs, n, t, live, vec);
     float mx = -__builtin_inff();
-    if (vec) {
 #pragma unroll
-        for (int i = 0; i < E / 4; ++i) {
-            const uint32_t e0 = 4u * (t + T * i);
-            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (live && e0 < n) v = *reinterpret_cast<const f32x4*>(rs + e0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                x[4 * i + j] = v[j];
-                if (live && e0 < n) mx = max_ignoring_nan(mx, v[j]);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < E; ++i) {
-            const uint32_t e = t + T * i;
-            x[i] = (live && e < n) ? rs[e] : 0.0f;
-            if (live && e < n) mx = max_ignoring_nan(mx, x[i]);
-        }
-    }
+    for (int i = 0; i < E; ++i)
+        if (live && elem_of(vec, T, t, i) < n) mx = max_ignoring_nan(mx, x[i]);
     mx = group_max<T>(mx, t, scratch[slot]);
 
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-        const uint32_t e = vec ? 4u * (t + T * (i / 4)) + (i % 4) : t + T * i;
-        if (live && e < n) stage[padded(e)] = expf(x[i] - mx);
+        const uint32_t e = elem_of(vec, T, t, i);
+        const float sh = x[i] - mx;
+        const float ex = expf(sh);
+        if (live && e < n) stage[stage_index(e)] = ex;
+        x[i] = log_mode ? sh : ex;
     }
     __syncthreads();
     const float denom = group_pairwise_sum<T>(stage, n, depth, t, scratch[slot]);
@@ -166,15 +145,12 @@ __global__ __launch_bounds__(T >= 256 ? T : 256) void softmax_rows_kernel(
     float* ds = dst + static_cast<uint64_t>(row) * n;
     if (vec) {
 #pragma unroll
-        for (int i = 0; i < E / 4; ++i) {
+        for (int i = 0; i < E4; ++i) {
             const uint32_t e0 = 4u * (t + T * i);
             if (e0 < n) {
                 f32x4 o;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float sh = x[4 * i + j] - mx;
-                    o[j] = log_mode ? sh - ld : expf(sh) / denom;
-                }
+                for (int j = 0; j < 4; ++j) o[j] = log_mode ? x[4 * i + j] - ld : x[4 * i + j] / denom;
                 *reinterpret_cast<f32x4*>(ds + e0) = o;
             }
         }
@@ -182,10 +158,7 @@ __global__ __launch_bounds__(T >= 256 ? T : 256) void softmax_rows_kernel(
 #pragma unroll
         for (int i = 0; i < E; ++i) {
             const uint32_t e = t + T * i;
-            if (e < n) {
-                const float sh = x[i] - mx;
-                ds[e] = log_mode ? sh - ld : expf(sh) / denom;
-            }
+            if (e < n) ds[e] = log_mode ? x[i] - ld : x[i] / denom;
         }
     }
 }
@@ -275,28 +248,37 @@ __global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* _
 
 // ---- one workgroup per output: contiguous reduced runs ----------------------------------
 // Sum / mean: the run is staged in LDS and summed by group_pairwise_sum.
-template <int T, int NMAX>
-__global__ __launch_bounds__(T >= 256 ? T : 256) void reduce_rows_sum_kernel(
+template <int T, int E4>
+__global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_sum_kernel(
     const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int depth, int mean,
-    int vec, float* __restrict__ dst) {
-    constexpr int RPB = T >= 256 ? 1 : 256 / T;
-    __shared__ float lds[RPB][NMAX + NMAX / 32];
+    int vec, uint32_t sstride, float* __restrict__ dst) {
+    constexpr int RPB = Rows<T>::kPerBlock;
+    extern __shared__ __attribute__((aligned(16))) float dyn[];
     __shared__ float scratch[RPB][T / 64 > 0 ? T / 64 : 1];
     const int slot = threadIdx.x / T;
     const int t = threadIdx.x % T;
     const uint32_t o = blockIdx.x * RPB + slot;
     const bool live = o < n_out;
     const float* rs = src + (live ? lin_off4(o, kept.ne, kept.nb) : 0);
-    float* stage = lds[slot];
-    if (live) {
-        if (vec) {
-            for (uint32_t e0 = 4u * t; e0 < n; e0 += 4u * T) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(rs + e0);
+    float* stage = dyn + slot * sstride;
+    float x[4 * E4];
+    load_row<T, E4>(x, rs, n, t, live, vec);
+    if (vec) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) stage[padded(e0 + j)] = v[j];
+        for (int i = 0; i < E4; ++i) {
+            const uint32_t e0 = 4u * (t + T * i);
+            if (live && e0 < n) {
+                f32x4 v;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = x[4 * i + j];
+                *reinterpret_cast<f32x4*>(stage + stage_index(e0)) = v;
             }
-        } else {
-            for (uint32_t e = t; e < n; e += T) stage[padded(e)] = rs[e];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4 * E4; ++i) {
+            const uint32_t e = t + T * i;
+            if (live && e < n) stage[stage_index(e)] = x[i];
         }
     }
     __syncthreads();
@@ -331,7 +313,7 @@ __device__ __forceinline__ Sel sel_merge(int op, Sel a, Sel b) {
 
 template <int T>
 __global__ __launch_bounds__(T >= 256 ? T : 256) void reduce_rows_select_kernel(
-    int op, const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n,
+    int op, const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int vec,
     void* __restrict__ dst) {
     constexpr int RPB = T >= 256 ? 1 : 256 / T;
     __shared__ float sv[RPB][T / 64 > 0 ? T / 64 : 1];
@@ -344,21 +326,32 @@ __global__ __launch_bounds__(T >= 256 ? T : 256) void reduce_rows_select_kernel(
     const bool is_max = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_ARGMAX;
     const bool value_op = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_MIN;
     Sel s{is_max ? -__builtin_inff() : __builtin_inff(), 0xffffffffu};
-    if (live) {
-        for (uint32_t e = t; e < n; e += T) {
-            const float v = rs[e];
-            if (v != v) {
-                if (value_op) {
-                    s = Sel{v, e};  // first NaN of this thread's subsequence
-                    break;
-                }
-                continue;
+    // Visits this thread's elements in increasing index order, four at a time.
+    auto visit = [&](float v, uint32_t e, bool& stop) {
+        if (v != v) {
+            if (value_op) {
+                s = Sel{v, e};  // first NaN of this thread's subsequence
+                stop = true;
             }
-            // Value ops take the first element as their candidate even if it is
-            // +-inf; index ops need a strict improvement on +-inf, as the
-            // oracle's loops do.
-            const bool better = is_max ? v > s.v : v < s.v;
-            if (better || (value_op && s.i == 0xffffffffu)) s = Sel{v, e};
+            return;
+        }
+        // Value ops take the first element as their candidate even if it is
+        // +-inf; index ops need a strict improvement on +-inf, as the
+        // oracle's loops do.
+        const bool better = is_max ? v > s.v : v < s.v;
+        if (better || (value_op && s.i == 0xffffffffu)) s = Sel{v, e};
+    };
+    if (live) {
+        bool stop = false;
+        if (vec) {
+            for (uint32_t e0 = 4u * t; e0 < n && !stop; e0 += 4u * T) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(rs + e0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (!stop) visit(v[j], e0 + j, stop);
+            }
+        } else {
+            for (uint32_t e = t; e < n && !stop; e += T) visit(rs[e], e, stop);
         }
     }
 #pragma unroll
@@ -445,6 +438,70 @@ static bool single_axis(const Op4& o, int64_t& step) {
 
 constexpr uint32_t kRowsMax = 32768;  // longest run staged in LDS
 
+// Row size classes: T threads per row and E4 float4 groups per thread.
+struct RowClass {
+    int T, E4;
+};
+
+static RowClass row_class(uint32_t n) {
+    if (n <= 256) return {64, 1};
+    if (n <= 1024) return {64, 4};
+    if (n <= 2048) return {64, 8};
+    if (n <= 4096) return {256, 4};
+    if (n <= 8192) return {256, 8};
+    if (n <= 16384) return {1024, 4};
+    return {1024, 8};
+}
+
+// Dynamic LDS above 64 KiB must be opted into per kernel.
+static int allow_lds(const void* fn, size_t bytes) {
+    if (bytes <= 65536) return VKHIP_OK;
+    VKHIP_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(bytes)));
+    return VKHIP_OK;
+}
+
+template <int T, int E4>
+static int launch_sum_rows(const float* src, const Op4& kept, uint32_t n_out, uint32_t n, int depth,
+                           int mean, int vec, float* out, hipStream_t st) {
+    constexpr int RPB = Rows<T>::kPerBlock;
+    const uint32_t ss = stage_stride(n);
+    const size_t lds = static_cast<size_t>(RPB) * ss * sizeof(float);
+    auto fn = reduce_rows_sum_kernel<T, E4>;
+    int rc = allow_lds(reinterpret_cast<const void*>(fn), lds);
+    if (rc != VKHIP_OK) return rc;
+    hipLaunchKernelGGL(fn, dim3(ceil_div(n_out, RPB)), dim3(Rows<T>::kThreads), lds, st, src, kept,
+                       n_out, n, depth, mean, vec, ss, out);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+template <int T, int E4>
+static int launch_softmax_rows(const float* src, int64_t stride, float* dst, uint32_t rows,
+                               uint32_t n, int depth, int log_mode, int vec, hipStream_t st) {
+    constexpr int RPB = Rows<T>::kPerBlock;
+    const uint32_t ss = stage_stride(n);
+    const size_t lds = static_cast<size_t>(RPB) * ss * sizeof(float);
+    auto fn = softmax_rows_kernel<T, E4>;
+    int rc = allow_lds(reinterpret_cast<const void*>(fn), lds);
+    if (rc != VKHIP_OK) return rc;
+    hipLaunchKernelGGL(fn, dim3(ceil_div(rows, RPB)), dim3(Rows<T>::kThreads), lds, st, src,
+                       stride, dst, rows, n, depth, log_mode, vec, ss);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+#define VKHIP_ROW_CLASSES(FN, ...)                                         \
+    switch (rc.T * 100 + rc.E4) {                                          \
+        case 6401: return FN<64, 1>(__VA_ARGS__);                          \
+        case 6404: return FN<64, 4>(__VA_ARGS__);                          \
+        case 6408: return FN<64, 8>(__VA_ARGS__);                          \
+        case 25604: return FN<256, 4>(__VA_ARGS__);                        \
+        case 25608: return FN<256, 8>(__VA_ARGS__);                        \
+        case 102404: return FN<1024, 4>(__VA_ARGS__);                      \
+        default: return FN<1024, 8>(__VA_ARGS__);                          \
+    }
+
 int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst) {
     if (op < VKHIP_REDUCE_SUM || op > VKHIP_REDUCE_ARGMIN)
         return fail(VKHIP_ERR_INVALID, "reduce: unknown op %d", op);
@@ -471,25 +528,15 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
             const int depth = pairwise_depth(n_red);
             const int mean = op == VKHIP_REDUCE_MEAN;
             float* out = static_cast<float*>(dst);
-            if (n_red <= 2048) {
-                hipLaunchKernelGGL((reduce_rows_sum_kernel<64, 2048>), dim3(ceil_div(n_out, 4)),
-                                   dim3(256), 0, st, src, kept, n_out, n_red, depth, mean, vec, out);
-            } else if (n_red <= 8192) {
-                hipLaunchKernelGGL((reduce_rows_sum_kernel<256, 8192>), dim3(n_out), dim3(256), 0,
-                                   st, src, kept, n_out, n_red, depth, mean, vec, out);
-            } else {
-                hipLaunchKernelGGL((reduce_rows_sum_kernel<1024, kRowsMax>), dim3(n_out),
-                                   dim3(1024), 0, st, src, kept, n_out, n_red, depth, mean, vec,
-                                   out);
-            }
-        } else {
-            if (n_red <= 2048)
-                hipLaunchKernelGGL((reduce_rows_select_kernel<64>), dim3(ceil_div(n_out, 4)),
-                                   dim3(256), 0, st, op, src, kept, n_out, n_red, dst);
-            else
-                hipLaunchKernelGGL((reduce_rows_select_kernel<256>), dim3(n_out), dim3(256), 0,
-                                   st, op, src, kept, n_out, n_red, dst);
+            const RowClass rc = row_class(n_red);
+            VKHIP_ROW_CLASSES(launch_sum_rows, src, kept, n_out, n_red, depth, mean, vec, out, st)
         }
+        if (n_red <= 2048)
+            hipLaunchKernelGGL((reduce_rows_select_kernel<64>), dim3(ceil_div(n_out, 4)), dim3(256),
+                               0, st, op, src, kept, n_out, n_red, vec, dst);
+        else
+            hipLaunchKernelGGL((reduce_rows_select_kernel<256>), dim3(n_out), dim3(256), 0, st, op,
+                               src, kept, n_out, n_red, vec, dst);
         VKHIP_LAUNCH_CHECK();
         return VKHIP_OK;
     }
@@ -582,17 +629,8 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
         const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
                         (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (n % 4 == 0) &&
                         (row_stride % 4 == 0);
-        if (n <= 2048)
-            hipLaunchKernelGGL((softmax_rows_kernel<64, 2048>), dim3(ceil_div(rows, 4)), dim3(256),
-                               0, st, src, row_stride, dst, rows, n, depth, log_mode, vec);
-        else if (n <= 8192)
-            hipLaunchKernelGGL((softmax_rows_kernel<256, 8192>), dim3(rows), dim3(256), 0, st, src,
-                               row_stride, dst, rows, n, depth, log_mode, vec);
-        else
-            hipLaunchKernelGGL((softmax_rows_kernel<1024, kRowsMax>), dim3(rows), dim3(1024), 0, st,
-                               src, row_stride, dst, rows, n, depth, log_mode, vec);
-        VKHIP_LAUNCH_CHECK();
-        return VKHIP_OK;
+        const RowClass rc = row_class(n);
+        VKHIP_ROW_CLASSES(launch_softmax_rows, src, row_stride, dst, rows, n, depth, log_mode, vec, st)
     }
     // General layout: one thread per row.
     vkhip_operand od;

@@ -27,6 +27,7 @@ int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_
 int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axis, int log_mode);
 int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst);
 int launch_elementwise(const vkhip_node& nd);
+int launch_copy_bytes(void* dst, const void* src, size_t nbytes);
 
 static thread_local char g_last_error[512] = "";
 
@@ -395,9 +396,8 @@ extern "C" int vkhip_copy_device_to_device(const vkhip_copy* copies, size_t n) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
     for (size_t i = 0; i < n; ++i) {
-        if (copies[i].nbytes == 0) continue;
-        VKHIP_HIP(hipMemcpyAsync(copies[i].dst, copies[i].src, copies[i].nbytes,
-                                 hipMemcpyDeviceToDevice, ctx().stream));
+        st = vkhip::launch_copy_bytes(copies[i].dst, copies[i].src, copies[i].nbytes);
+        if (st != VKHIP_OK) return st;
     }
     return VKHIP_OK;
 }
