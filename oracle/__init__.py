@@ -277,3 +277,45 @@ def split_k_fold(ws: np.ndarray, splits: int) -> np.ndarray:
 def compute(nodes, count: int, threads: int | None = None) -> int:
     """CPU backend compute() over vkhip node records whose pointers are HOST addresses."""
     return load().or_compute(ctypes.cast(nodes, c_void_p), count, threads or default_threads())
+
+
+class HostStorage:
+    """Host memory standing in for a device allocation."""
+
+    __slots__ = ("buf", "ptr", "nbytes")
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.buf = np.zeros(self.nbytes + 64, np.uint8)
+        base = self.buf.ctypes.data
+        self.ptr = base + (-base) % 64
+
+
+class OracleBackend:
+    """vkML's CPU backend for the host core's executor: the same node records,
+    evaluated by or_compute on host memory. Tests use it to run the identical
+    graph the device runs (reference CpuBackend, src/backend/cpu/cpu_backend.cpp)."""
+
+    name = "cpu-oracle"
+
+    def __init__(self, threads: int | None = None):
+        self.threads = threads or default_threads()
+        load()
+
+    def alloc(self, nbytes: int) -> HostStorage:
+        return HostStorage(max(int(nbytes), 4))
+
+    def upload(self, storage: HostStorage, offset_bytes: int, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        ctypes.memmove(storage.ptr + offset_bytes, arr.ctypes.data, arr.nbytes)
+
+    def download(self, storage: HostStorage, offset_bytes: int, out: np.ndarray) -> None:
+        ctypes.memmove(out.ctypes.data, storage.ptr + offset_bytes, out.nbytes)
+
+    def compute(self, nodes, count: int) -> None:
+        st = compute(nodes, count, self.threads)
+        if st != 0:
+            raise RuntimeError(f"oracle compute failed with status {st}")
+
+    def synchronize(self) -> None:
+        pass

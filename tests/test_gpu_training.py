@@ -1,0 +1,111 @@
+"""Whole training steps on the device against the same graph on the CPU oracle.
+
+BASELINE config 1 (MNIST-shaped MLP, 100 SGD-momentum steps) must keep every
+step's loss within 1e-4 of the oracle's; config 5 (CIFAR-100-shaped CNN) is run
+at full batch for a few steps (the oracle needs ~10 s per full step) and at a
+reduced batch for more; config 4's conv layers are checked forward, dX and dW at
+full shape. The graph, the initial weights and the data are identical on both
+sides; only the backend executing the nodes differs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import SEED, gemm_tolerance, normwise_rel_err
+from oracle import OracleBackend
+from vkml_amd import nn, optim
+from vkml_amd import tensor as T
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def backends():
+    return T.default_backend(), OracleBackend()
+
+
+def mlp(backend):
+    nn.manual_seed(SEED)
+    return nn.Sequential(nn.Flatten(), nn.Linear(784, 128, backend=backend), nn.ReLU(),
+                         nn.Linear(128, 10, backend=backend))
+
+
+def cnn(backend):
+    nn.manual_seed(SEED)
+    return nn.Sequential(
+        nn.Conv2d(3, 64, 3, padding=1, backend=backend), nn.ReLU(), nn.MaxPool2d(2),
+        nn.Conv2d(64, 128, 3, padding=1, backend=backend), nn.ReLU(), nn.MaxPool2d(2),
+        nn.Flatten(), nn.Linear(8192, 256, backend=backend), nn.ReLU(),
+        nn.Linear(256, 100, backend=backend))
+
+
+def train(model, backend, batches, lr=0.1, momentum=0.9):
+    opt = optim.SGD(model.parameters(), lr=lr, momentum=momentum)
+    losses = []
+    for x, y in batches:
+        opt.zero_grad()
+        loss = nn.cross_entropy(model(T.tensor(x, backend=backend)), T.tensor(y, backend=backend))
+        loss.backward()
+        opt.step()
+        losses.append(loss.item())
+    return np.array(losses)
+
+
+@pytest.mark.timeout(600)
+def test_config1_mlp_100_steps_loss_drift(backends):
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED)
+    batches = [(rng.uniform(0, 1, (64, 1, 28, 28)).astype(np.float32),
+                rng.integers(0, 10, 64).astype(np.int64)) for _ in range(100)]
+    got = train(mlp(dev), dev, batches)
+    want = train(mlp(cpu), cpu, batches)
+    drift = np.abs(got - want)
+    assert drift.max() <= 1e-4, f"max loss drift {drift.max():.3g} at step {drift.argmax()}"
+    assert got[-1] < got[0]
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("batch,steps", [(128, 2), (16, 10)])
+def test_config5_cnn_loss_drift(backends, batch, steps):
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED + batch)
+    batches = [(rng.uniform(-1, 1, (batch, 3, 32, 32)).astype(np.float32),
+                rng.integers(0, 100, batch).astype(np.int64)) for _ in range(steps)]
+    got = train(cnn(dev), dev, batches, lr=0.01)
+    want = train(cnn(cpu), cpu, batches, lr=0.01)
+    drift = np.abs(got - want)
+    assert drift.max() <= 1e-4, f"max loss drift {drift.max():.3g} at step {drift.argmax()}"
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("cin,cout", [(3, 64), (64, 128)])
+def test_config4_conv_forward_dx_dw(backends, cin, cout):
+    """Conv2d 3x3 s1 p1 on [128, cin, 32, 32]: output, dX (col2im of the TN
+    product) and dW (NT product + batch reduce) against the oracle."""
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED + cin)
+    x = rng.uniform(-1, 1, (128, cin, 32, 32)).astype(np.float32)
+    g = rng.standard_normal((128, cout, 32, 32)).astype(np.float32)
+    res = {}
+    for name, be in (("dev", dev), ("cpu", cpu)):
+        nn.manual_seed(SEED)
+        conv = nn.Conv2d(cin, cout, 3, padding=1, backend=be)
+        xt = T.tensor(x, requires_grad=True, backend=be)
+        y = conv(xt)
+        y.backward(T.tensor(g, backend=be))
+        res[name] = (y.numpy(), xt.grad.numpy(), conv.weight.grad.numpy(), conv.bias.grad.numpy())
+    k = cin * 9
+    assert normwise_rel_err(res["dev"][0], res["cpu"][0]) <= gemm_tolerance(k)
+    assert normwise_rel_err(res["dev"][1], res["cpu"][1]) <= gemm_tolerance(cout)
+    assert normwise_rel_err(res["dev"][2], res["cpu"][2]) <= gemm_tolerance(128 * 1024)
+    # the bias gradient is a pure pairwise sum over axes {0, 2, 3}: bit-exact
+    assert res["dev"][3].tobytes() == res["cpu"][3].tobytes()
+
+
+def test_bias_gradient_reduce_is_bit_exact(backends):
+    dev, cpu = backends
+    x = np.random.default_rng(5).standard_normal((128, 64, 32, 32)).astype(np.float32)
+    got = T.sum(T.tensor(x, backend=dev), [0, 2, 3]).numpy()
+    want = T.sum(T.tensor(x, backend=cpu), [0, 2, 3]).numpy()
+    assert got.tobytes() == want.tobytes()

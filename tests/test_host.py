@@ -101,18 +101,25 @@ def plan(batch, m, n, k, split=0):
 
 
 def test_split_k_plan_rules():
-    """The reference's plan_split_k rules (vulkan_backend.cpp:596-647): split
-    only when K-tiles >= output tiles, power-of-two chunk of >= 4 K-tiles,
-    workspace <= 64 MiB; OFF never splits."""
-    # square 4096^3: plenty of tiles, no split
+    """The split-K plan: power-of-two chunk, workspace <= 64 MiB, OFF never
+    splits, a forced request gets the largest power-of-two chunk giving at
+    least that many partitions (reference plan_split_k,
+    vulkan_backend.cpp:596-647); AUTO splits exactly when the output tiles
+    cannot fill two workgroups per CU (the rule restated for 256 CUs)."""
+    # square 4096^3 and the 8192x1024x4096 sweep case fill the machine: no split
     assert plan(1, 4096, 4096, 4096) == (1, 128)
-    # the skinny K-dominant BASELINE shapes split
-    for m, n, k in [(256, 256, 65536), (128, 784, 16384)]:
+    assert plan(1, 8192, 1024, 4096)[0] == 1
+    # the skinny K-dominant BASELINE shapes and the small MLP/conv GEMMs split
+    for m, n, k in [(256, 256, 65536), (128, 784, 16384), (64, 128, 784), (128, 1024, 576)]:
         splits, chunk = plan(1, m, n, k)
         ktiles = -(-k // 32)
-        assert splits > 1 and chunk >= 4 and chunk & (chunk - 1) == 0
+        assert splits > 1 and chunk >= 2 and chunk & (chunk - 1) == 0
         assert splits == -(-ktiles // chunk)
         assert m * n * splits * 4 <= 64 << 20
+        tiles = -(-m // 64) * -(-n // 64)
+        assert tiles * splits >= min(512, tiles * (ktiles // 2)) // 2
+    # a batched conv GEMM has tiles enough
+    assert plan(128, 128, 1024, 576)[0] == 1
     # OFF
     assert plan(1, 256, 256, 65536, split=1)[0] == 1
     # forced request: chunk is the largest power of two giving >= request splits

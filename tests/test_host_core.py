@@ -1,0 +1,101 @@
+"""The host core (lazy graph, executor, autograd, nn, SGD) on the CPU oracle
+backend, pinned against torch float64: forward values and every parameter
+gradient of the BASELINE MLP and a small CNN, and SGD-with-momentum updates.
+These check the restated graph (cross_entropy, conv2d lowering, autograd
+rules) independently of the oracle's own kernels."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import SEED
+from oracle import OracleBackend
+from vkml_amd import nn, optim
+from vkml_amd import tensor as T
+
+
+@pytest.fixture(scope="module")
+def cpu():
+    return OracleBackend()
+
+
+def torch_mlp_grads(x, y, w1, b1, w2, b2):
+    p = [torch.tensor(v.astype(np.float64), requires_grad=True) for v in (w1, b1, w2, b2)]
+    xt = torch.tensor(x.reshape(x.shape[0], -1).astype(np.float64))
+    h = torch.relu(xt @ p[0].T + p[1])
+    logits = h @ p[2].T + p[3]
+    loss = torch.nn.functional.cross_entropy(logits, torch.tensor(y))
+    loss.backward()
+    return loss.item(), [q.grad.numpy() for q in p]
+
+
+def test_mlp_forward_backward_vs_torch(cpu):
+    rng = np.random.default_rng(SEED)
+    x = rng.uniform(0, 1, (64, 1, 28, 28)).astype(np.float32)
+    y = rng.integers(0, 10, 64).astype(np.int64)
+    nn.manual_seed(SEED)
+    model = nn.Sequential(nn.Flatten(), nn.Linear(784, 128, backend=cpu), nn.ReLU(),
+                          nn.Linear(128, 10, backend=cpu))
+    loss = nn.cross_entropy(model(T.tensor(x, backend=cpu)), T.tensor(y, backend=cpu))
+    loss.backward()
+    params = model.parameters()
+    want_loss, want_grads = torch_mlp_grads(x, y, *[p.numpy() for p in params])
+    assert abs(loss.item() - want_loss) <= 1e-5 * max(1.0, abs(want_loss))
+    for p, g in zip(params, want_grads):
+        got = p.grad.numpy()
+        assert got.shape == g.shape
+        np.testing.assert_allclose(got, g, rtol=1e-4, atol=1e-6)
+
+
+def test_cnn_forward_backward_vs_torch(cpu):
+    """conv -> relu -> pool -> flatten -> linear: conv2d lowered to
+    im2col + batch-broadcast matmul, backward through col2im-free first conv,
+    the NT weight-gradient GEMM + batch reduce, and max-pool backward."""
+    rng = np.random.default_rng(SEED + 1)
+    x = rng.uniform(-1, 1, (4, 3, 8, 8)).astype(np.float32)
+    y = rng.integers(0, 5, 4).astype(np.int64)
+    nn.manual_seed(SEED)
+    conv = nn.Conv2d(3, 6, 3, padding=1, backend=cpu)
+    conv2 = nn.Conv2d(6, 4, 3, padding=1, backend=cpu)
+    fc = nn.Linear(4 * 2 * 2, 5, backend=cpu)
+    model = nn.Sequential(conv, nn.ReLU(), nn.MaxPool2d(2), conv2, nn.ReLU(), nn.MaxPool2d(2),
+                          nn.Flatten(), fc)
+    loss = nn.cross_entropy(model(T.tensor(x, backend=cpu)), T.tensor(y, backend=cpu))
+    loss.backward()
+    tp = [torch.tensor(p.numpy().astype(np.float64), requires_grad=True)
+          for p in model.parameters()]
+    F = torch.nn.functional
+    h = F.max_pool2d(F.relu(F.conv2d(torch.tensor(x, dtype=torch.float64), tp[0], tp[1], padding=1)), 2)
+    h = F.max_pool2d(F.relu(F.conv2d(h, tp[2], tp[3], padding=1)), 2)
+    logits = h.reshape(4, -1) @ tp[4].T + tp[5]
+    want = F.cross_entropy(logits, torch.tensor(y))
+    want.backward()
+    assert abs(loss.item() - want.item()) <= 1e-5
+    for p, q in zip(model.parameters(), tp):
+        np.testing.assert_allclose(p.grad.numpy(), q.grad.numpy(), rtol=1e-4, atol=1e-6)
+
+
+def test_sgd_momentum_matches_torch(cpu):
+    rng = np.random.default_rng(3)
+    w0 = rng.standard_normal((5, 3)).astype(np.float32)
+    grads = [rng.standard_normal((5, 3)).astype(np.float32) for _ in range(3)]
+    p = T.tensor(w0, requires_grad=True, backend=cpu)
+    opt = optim.SGD([p], lr=0.1, momentum=0.9)
+    tw = torch.tensor(w0, requires_grad=True)
+    topt = torch.optim.SGD([tw], lr=0.1, momentum=0.9)
+    for g in grads:
+        p.grad = T.tensor(g, backend=cpu)
+        opt.step()
+        tw.grad = torch.tensor(g)
+        topt.step()
+        np.testing.assert_allclose(p.numpy(), tw.detach().numpy(), rtol=1e-6, atol=1e-7)
+
+
+def test_views_and_broadcast_resolve_by_aliasing(cpu):
+    a = np.arange(12, dtype=np.float32).reshape(3, 4)
+    t = T.tensor(a, backend=cpu)
+    np.testing.assert_array_equal(t.T.numpy(), a.T)
+    np.testing.assert_array_equal((t + T.tensor(np.ones(4, np.float32), backend=cpu)).numpy(), a + 1)
+    np.testing.assert_array_equal(T.sum(t, [0]).numpy(), a.sum(0))
+    np.testing.assert_array_equal(T.matmul(t, t.T).numpy(), a @ a.T)

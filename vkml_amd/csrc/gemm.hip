@@ -396,28 +396,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ a, 
 // ---- planning ---------------------------------------------------------------
 
 // Split-K plan (reference plan_split_k, vulkan_backend.cpp:596-647), restated
-// for MI355X. Same structure: split only when K-tiles >= output tiles; chunk =
-// largest power of two of K-tiles giving at least `target` partitions, raised to
-// >= 4 K-tiles; workspace capped at 64 MiB. What changes is the target: the
-// reference aims at 8 workgroups per CU capped at 16 partitions (a 36-CU RDNA1
-// part); a 256-CU MI355X needs about two 256-thread MFMA workgroups per CU, so
-// the target is 512 resident workgroups, capped at 256 partitions.
+// for MI355X. Kept from the reference: the partition chunk is a power of two of
+// K-tiles, a forced request gets the largest power-of-two chunk that still
+// yields at least that many partitions, the partial workspace is capped at
+// 64 MiB, and the fold of the partials is the carry stack. Changed: the
+// reference's profitability rule (split iff K-tiles >= output tiles, at most
+// 16 partitions, chunk >= 4) was fitted on a 36-CU RDNA1 part. A 256-CU MI355X
+// runs about two 256-thread MFMA workgroups per CU, so here a product splits
+// whenever its output tiles cannot fill those 512 slots: the target is
+// ceil(512 / tiles) partitions, capped at 256, with a chunk of at least two
+// K-tiles so each partition still overlaps one tile's loads with another's
+// MFMAs.
 static void plan_split_k(uint32_t tiles, uint32_t ktiles, uint64_t out_elems, uint32_t cu,
                          uint32_t requested, uint32_t& splits, uint32_t& chunk) {
     splits = 1;
     chunk = ktiles;
     if (ktiles < 2 || tiles == 0) return;
+    const uint32_t slots = (cu ? cu : 256) * 2;
     uint32_t target = requested;
     if (target == 0) {
-        if (ktiles < tiles) return;
-        const uint32_t slots = (cu ? cu : 256) * 2;
-        target = slots / (tiles ? tiles : 1);
+        if (tiles * 2 > slots) return;  // at least one workgroup per CU already
+        target = (slots + tiles - 1) / tiles;
         if (target < 2) target = 2;
         if (target > 256) target = 256;
     }
     uint32_t c = 1;
     while (c * 2 <= ktiles / target) c *= 2;
-    if (c < 4 && requested == 0) c = 4;
+    if (c < 2 && requested == 0) c = 2;
     if (c >= ktiles) return;
     const uint32_t s = (ktiles + c - 1) / c;
     if (s < 2 || s > 511) return;

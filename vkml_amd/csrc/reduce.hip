@@ -378,6 +378,57 @@ __global__ __launch_bounds__(T >= 256 ? T : 256) void reduce_rows_select_kernel(
     }
 }
 
+// ---- one workgroup per output: any layout, many reduced elements ---------------------
+// Sum / mean over a reduced set that is not one contiguous run (e.g. a conv
+// bias gradient, axes {0, 2, 3}), with few outputs: T threads share one
+// output, each owning consecutive depth-D leaves read through the reduced
+// descriptor, combined by the same butterfly as the staged kernels.
+template <int T>
+__global__ __launch_bounds__(T) void reduce_wide_strided_kernel(
+    const float* __restrict__ src, Op4 kept, Reader rd, uint32_t n, int depth, int mean,
+    float* __restrict__ dst) {
+    __shared__ float scratch[T / 64];
+    const int t = threadIdx.x;
+    const uint32_t o = blockIdx.x;
+    const float* base = src + lin_off4(o, kept.ne, kept.nb);
+    const uint32_t leaves = 1u << depth;
+    const uint32_t per = leaves > static_cast<uint32_t>(T) ? leaves / T : 1u;
+    float v = 0.0f;
+    if (static_cast<uint32_t>(t) * per < leaves) {
+        float stack[kTallLevels];
+#pragma unroll
+        for (int l = 0; l < kTallLevels; ++l) stack[l] = 0.0f;
+        for (uint32_t j = 0; j < per; ++j) {
+            uint32_t b, e;
+            pairwise_leaf(n, depth, t * per + j, b, e);
+            float sv = 0.0f;
+            for (uint32_t q = b; q < e; ++q) sv = sv + base[rd.off(q)];
+            bool carry = true;
+#pragma unroll
+            for (int l = 0; l < kTallLevels; ++l) {
+                if (carry) {
+                    if ((j >> l) & 1u) {
+                        sv = stack[l] + sv;
+                    } else {
+                        stack[l] = sv;
+                        carry = false;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int l = 0; l < kTallLevels; ++l)
+            if ((1u << l) == per) v = stack[l];
+    }
+    v = wave_sum_butterfly(v);
+    const int lane = t & 63, wave = t >> 6;
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float u = lane < T / 64 ? scratch[lane] : 0.0f;
+    u = wave_sum_butterfly(u);
+    if (t == 0) dst[o] = mean ? u / static_cast<float>(n) : u;
+}
+
 // ---- host side ----------------------------------------------------------------------
 
 static void split_axes(const vkhip_operand& d, uint32_t mask, Op4& kept, Op4& red) {
@@ -544,6 +595,14 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
     rd.red = red;
     rd.single = single_axis(red, rd.step) ? 1 : 0;
     const int depth = pairwise_depth(n_red);
+    const uint32_t cus = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
+    if (sum_op && n_red >= 8192 && n_out < 4 * cus) {
+        hipLaunchKernelGGL(reduce_wide_strided_kernel<256>, dim3(n_out), dim3(256), 0, st, src,
+                           kept, rd, n_red, depth, op == VKHIP_REDUCE_MEAN ? 1 : 0,
+                           static_cast<float*>(dst));
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
     hipLaunchKernelGGL(reduce_tall_kernel, dim3(ceil_div(n_out, 256)), dim3(256), 0, st, op, src,
                        kept, rd, static_cast<uint64_t>(n_out), n_red, depth, dst);
     VKHIP_LAUNCH_CHECK();

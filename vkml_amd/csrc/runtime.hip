@@ -297,6 +297,13 @@ extern "C" int vkhip_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(VKHIP_ERR_UNSUPPORTED, "vkhip: built for gfx950, device %d is %s", device,
                     prop.gcnArchName);
+    // Stream-ordered allocations come from the device's default pool; keep
+    // freed blocks in it instead of returning them to the OS at every
+    // synchronisation, so a training step's per-node allocations are reused.
+    hipMemPool_t pool;
+    VKHIP_HIP(hipDeviceGetDefaultMemPool(&pool, device));
+    uint64_t keep = ~0ull;
+    VKHIP_HIP(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep));
     VKHIP_HIP(hipStreamCreateWithFlags(&c.own_stream, hipStreamNonBlocking));
     c.stream = c.own_stream;
     c.device = device;

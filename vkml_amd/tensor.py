@@ -1,0 +1,877 @@
+"""Lazy tensors, the executor and reverse-mode autograd: the host side that
+drives the device backend through `Backend.compute(span of nodes)`.
+
+This restates the parts of vkML's host core that the hot path's callers use,
+so that the BASELINE training steps (MNIST MLP, CIFAR CNN) run end to end:
+
+  graph      Node with shape/strides/dtype/params and view aliasing
+             (reference include/vkml/graph/node.h:69-157, op.h:30-139)
+  executor   realize(): topological order, view resolution by aliasing,
+             allocation, then ONE backend.compute() over the span
+             (reference src/dispatch/executor.cpp:23-154)
+  ops        torch-like constructors with the reference's lowering: rank-4
+             matmul with broadcast batch axes (src/api/ops.cpp:906-981),
+             conv2d = im2col + matmul (:662-705), cross_entropy (:417-441),
+             reductions (:119-130), scaled_add (:144-171)
+  autograd   backward() with the reference's rules
+             (src/autograd/autograd.cpp:84-116, 160-560, 588-673)
+
+A Tensor lives on a backend: the HIP device backend by default. Anything with
+the same five methods (alloc/upload/download/compute/synchronize) can stand in,
+which is how the tests run the identical graph on the CPU oracle. There is no
+implicit fallback: an op the backend does not support raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Iterable, Sequence
+
+import numpy as np
+
+from . import _lib
+
+OP = _lib.OP
+# View ops are resolved by aliasing on the host and never reach a backend
+# (reference backend.h:34-45). Numbered with the reference's OpKind ordinals.
+INPUT, FULL, ARANGE = 0, OP["FULL"], OP["ARANGE"]
+RESHAPE, PERMUTE, BROADCAST, UNSQUEEZE = 5, 6, 8, 10
+VIEW_OPS = {RESHAPE, PERMUTE, BROADCAST, UNSQUEEZE}
+LEAF_OPS = {INPUT, FULL, ARANGE}
+
+_VK_DTYPE = {np.dtype(np.float32): _lib.F32, np.dtype(np.int64): _lib.I64,
+             np.dtype(np.bool_): _lib.BOOL}
+
+_grad_enabled = True
+
+
+class no_grad:
+    """Context manager that disables graph recording of requires_grad."""
+
+    def __enter__(self):
+        global _grad_enabled
+        self.prev = _grad_enabled
+        _grad_enabled = False
+
+    def __exit__(self, *exc):
+        global _grad_enabled
+        _grad_enabled = self.prev
+
+
+def contiguous_strides(shape: Sequence[int]) -> tuple[int, ...]:
+    out, s = [], 1
+    for e in reversed(list(shape)):
+        out.append(s)
+        s *= int(e)
+    return tuple(reversed(out))
+
+
+def _numel(shape) -> int:
+    n = 1
+    for e in shape:
+        n *= int(e)
+    return n
+
+
+def broadcast_dims(a: Sequence[int], b: Sequence[int]) -> tuple[int, ...]:
+    """torch broadcasting of two shapes (reference broadcast_dims)."""
+    a, b = list(a), list(b)
+    n = max(len(a), len(b))
+    a = [1] * (n - len(a)) + a
+    b = [1] * (n - len(b)) + b
+    out = []
+    for x, y in zip(a, b):
+        if x != y and x != 1 and y != 1:
+            raise ValueError(f"shapes {a} and {b} do not broadcast")
+        out.append(max(x, y))
+    return tuple(out)
+
+
+# ---------------------------------------------------------------------------
+# Backends
+# ---------------------------------------------------------------------------
+
+class DeviceBackend:
+    """The HIP device backend (libvkhip) behind the executor."""
+
+    name = "hip"
+
+    def __init__(self, index: int = 0):
+        from .device import backend
+
+        self.hip = backend(index)
+
+    def alloc(self, nbytes: int):
+        from .device import Buffer
+
+        return Buffer(max(int(nbytes), 4))
+
+    def upload(self, storage, offset_bytes: int, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes:
+            _lib.check(self.hip.lib.vkhip_copy_from_host(
+                ctypes.c_void_p(storage.ptr + offset_bytes), arr.ctypes.data_as(ctypes.c_void_p),
+                arr.nbytes), "copy_from_host")
+
+    def download(self, storage, offset_bytes: int, out: np.ndarray) -> None:
+        if out.nbytes:
+            _lib.check(self.hip.lib.vkhip_copy_to_host(
+                out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(storage.ptr + offset_bytes),
+                out.nbytes), "copy_to_host")
+
+    def compute(self, nodes, count: int) -> None:
+        _lib.check(self.hip.lib.vkhip_compute(nodes, count), "compute")
+
+    def synchronize(self) -> None:
+        self.hip.synchronize()
+
+
+_DEFAULT_BACKEND = None
+
+
+def default_backend():
+    global _DEFAULT_BACKEND
+    if _DEFAULT_BACKEND is None:
+        _DEFAULT_BACKEND = DeviceBackend()
+    return _DEFAULT_BACKEND
+
+
+# ---------------------------------------------------------------------------
+# Graph
+# ---------------------------------------------------------------------------
+
+class Node:
+    __slots__ = ("op", "shape", "strides", "dtype", "src", "params", "view_src", "view_offset",
+                 "storage", "offset", "computed", "requires_grad", "grad", "backend", "aux",
+                 "__weakref__")
+
+    def __init__(self, op, shape, dtype, backend, src=(), params=b"", requires_grad=False,
+                 strides=None):
+        self.op = op
+        self.shape = tuple(int(e) for e in shape)
+        self.strides = tuple(strides) if strides is not None else contiguous_strides(self.shape)
+        self.dtype = np.dtype(dtype)
+        self.src = list(src)
+        self.params = params
+        self.view_src = None
+        self.view_offset = 0
+        self.storage = None
+        self.offset = 0  # elements
+        self.computed = False
+        self.requires_grad = requires_grad
+        self.grad = None
+        self.backend = backend
+        self.aux = None  # op-specific host data (permutation, axis, ...)
+
+    @property
+    def is_view(self) -> bool:
+        return self.op in VIEW_OPS
+
+    @property
+    def itemsize(self) -> int:
+        return self.dtype.itemsize
+
+    def is_contiguous(self) -> bool:
+        expect = 1
+        for e, s in zip(reversed(self.shape), reversed(self.strides)):
+            if e == 1:
+                continue
+            if s != expect:
+                return False
+            expect *= e
+        return True
+
+
+def _params(*values: tuple[str, object]) -> bytes:
+    """Packs op params like the reference's 64-byte OpParams payload."""
+    out = bytearray()
+    for fmt, v in values:
+        import struct
+
+        out += struct.pack("<" + fmt, v)
+    return bytes(out)
+
+
+class Tensor:
+    """A lazy tensor (reference include/vkml/api/tensor.h)."""
+
+    __slots__ = ("node",)
+
+    def __init__(self, node: Node):
+        self.node = node
+
+    # -- construction ------------------------------------------------------------
+    @staticmethod
+    def from_numpy(arr, requires_grad: bool = False, backend=None) -> "Tensor":
+        backend = backend or default_backend()
+        arr = np.asarray(arr)
+        if arr.dtype == np.float64:
+            arr = arr.astype(np.float32)
+        if arr.dtype not in _VK_DTYPE:
+            raise TypeError(f"unsupported dtype {arr.dtype}")
+        n = Node(INPUT, arr.shape, arr.dtype, backend, requires_grad=requires_grad)
+        n.storage = backend.alloc(arr.nbytes)
+        host = arr.view(np.uint8) if arr.dtype == np.bool_ else arr
+        backend.upload(n.storage, 0, host)
+        n.computed = True
+        return Tensor(n)
+
+    # -- properties -----------------------------------------------------------------
+    @property
+    def shape(self) -> tuple[int, ...]:
+        return self.node.shape
+
+    @property
+    def ndim(self) -> int:
+        return len(self.node.shape)
+
+    @property
+    def dtype(self):
+        return self.node.dtype
+
+    @property
+    def requires_grad(self) -> bool:
+        return self.node.requires_grad
+
+    @property
+    def grad(self):
+        return Tensor(self.node.grad) if self.node.grad is not None else None
+
+    @grad.setter
+    def grad(self, value):
+        self.node.grad = value.node if value is not None else None
+
+    def numel(self) -> int:
+        return _numel(self.shape)
+
+    def size(self, i: int) -> int:
+        return self.shape[i]
+
+    # -- evaluation -------------------------------------------------------------------
+    def realize(self) -> "Tensor":
+        realize([self])
+        return self
+
+    def numpy(self) -> np.ndarray:
+        t = self if self.node.is_contiguous() else self.contiguous()
+        t.realize()
+        n = t.node
+        host = np.empty(n.shape, np.uint8 if n.dtype == np.bool_ else n.dtype)
+        n.backend.download(n.storage, n.offset * n.itemsize, host)
+        return host.astype(np.bool_) if n.dtype == np.bool_ else host
+
+    def item(self) -> float:
+        return self.numpy().reshape(-1)[0].item()
+
+    def detach(self) -> "Tensor":
+        self.realize()
+        n = Node(INPUT, self.shape, self.dtype, self.node.backend, strides=self.node.strides)
+        n.storage, n.offset, n.computed = self.node.storage, self.node.offset, True
+        return Tensor(n)
+
+    # -- views -----------------------------------------------------------------------------
+    def reshape(self, *shape) -> "Tensor":
+        if len(shape) == 1 and isinstance(shape[0], (tuple, list)):
+            shape = tuple(shape[0])
+        shape = list(shape)
+        if -1 in shape:
+            known = _numel([e for e in shape if e != -1])
+            shape[shape.index(-1)] = self.numel() // max(known, 1)
+        if _numel(shape) != self.numel():
+            raise ValueError(f"cannot reshape {self.shape} to {tuple(shape)}")
+        if tuple(shape) == self.shape:
+            return self
+        src = self if self.node.is_contiguous() else self.contiguous()
+        return _view(RESHAPE, src, shape, contiguous_strides(shape), 0)
+
+    def permute(self, *perm) -> "Tensor":
+        if len(perm) == 1 and isinstance(perm[0], (tuple, list)):
+            perm = tuple(perm[0])
+        perm = [p % self.ndim for p in perm]
+        shape = [self.shape[p] for p in perm]
+        strides = [self.node.strides[p] for p in perm]
+        t = _view(PERMUTE, self, shape, strides, 0)
+        t.node.aux = tuple(perm)
+        return t
+
+    def transpose(self, a: int, b: int) -> "Tensor":
+        perm = list(range(self.ndim))
+        a, b = a % self.ndim, b % self.ndim
+        perm[a], perm[b] = perm[b], perm[a]
+        return self.permute(perm)
+
+    @property
+    def T(self) -> "Tensor":
+        return self.transpose(-2, -1)
+
+    def unsqueeze(self, axis: int) -> "Tensor":
+        axis = axis % (self.ndim + 1)
+        shape = list(self.shape)
+        strides = list(self.node.strides)
+        shape.insert(axis, 1)
+        strides.insert(axis, strides[axis] * shape[axis + 1] if axis < len(strides) else 1)
+        return _view(UNSQUEEZE, self, shape, strides, 0)
+
+    def broadcast_to(self, dims) -> "Tensor":
+        dims = tuple(int(e) for e in dims)
+        if dims == self.shape:
+            return self
+        pad = len(dims) - self.ndim
+        if pad < 0:
+            raise ValueError(f"cannot broadcast {self.shape} to {dims}")
+        src_shape = (1,) * pad + self.shape
+        src_str = (0,) * pad + self.node.strides
+        strides = []
+        for se, ss, te in zip(src_shape, src_str, dims):
+            if se == te:
+                strides.append(ss)
+            elif se == 1:
+                strides.append(0)
+            else:
+                raise ValueError(f"cannot broadcast {self.shape} to {dims}")
+        return _view(BROADCAST, self, dims, strides, 0)
+
+    def contiguous(self) -> "Tensor":
+        if self.node.is_contiguous() and not self.node.is_view:
+            return self
+        return _unary(OP["CONTIGUOUS"], self)
+
+    def to(self, dtype) -> "Tensor":
+        dtype = np.dtype(dtype)
+        if dtype == self.dtype:
+            return self
+        n = Node(OP["CAST"], self.shape, dtype, self.node.backend, [self.node],
+                 requires_grad=_grad_enabled and self.requires_grad and dtype == np.float32)
+        return Tensor(n)
+
+    # -- arithmetic -----------------------------------------------------------------------
+    def __add__(self, o): return add(self, o)
+    def __radd__(self, o): return add(self, o)
+    def __sub__(self, o): return sub(self, o)
+    def __rsub__(self, o): return sub(_scalar_like(self, o), self)
+    def __mul__(self, o): return mul(self, o)
+    def __rmul__(self, o): return mul(self, o)
+    def __truediv__(self, o): return div(self, o)
+    def __neg__(self): return neg(self)
+    def __matmul__(self, o): return matmul(self, o)
+
+    def backward(self, seed: "Tensor | None" = None) -> None:
+        backward(self, seed)
+
+    def __repr__(self) -> str:
+        return f"Tensor(shape={self.shape}, dtype={self.dtype}, backend={self.node.backend.name})"
+
+
+def tensor(data, requires_grad: bool = False, backend=None) -> Tensor:
+    return Tensor.from_numpy(np.asarray(data), requires_grad, backend)
+
+
+def _view(op, t: Tensor, shape, strides, offset) -> Tensor:
+    n = Node(op, shape, t.dtype, t.node.backend, [t.node], strides=strides,
+             requires_grad=_grad_enabled and t.requires_grad)
+    n.view_src = t.node
+    n.view_offset = offset
+    return Tensor(n)
+
+
+# ---------------------------------------------------------------------------
+# Creation and elementwise ops
+# ---------------------------------------------------------------------------
+
+def full(shape, value: float, dtype=np.float32, backend=None) -> Tensor:
+    return Tensor(Node(FULL, shape, dtype, backend or default_backend(),
+                       params=_params(("d", float(value)))))
+
+
+def ones(shape, dtype=np.float32, backend=None) -> Tensor:
+    return full(shape, 1.0, dtype, backend)
+
+
+def zeros_like(t: Tensor) -> Tensor:
+    return full(t.shape, 0.0, t.dtype, t.node.backend)
+
+
+def arange(start: float, stop: float, step: float = 1.0, dtype=np.float32, backend=None) -> Tensor:
+    count = max(0, math.ceil((stop - start) / step))
+    return Tensor(Node(ARANGE, (count,), dtype, backend or default_backend(),
+                       params=_params(("d", float(start)), ("d", float(step)))))
+
+
+def _scalar_like(peer: Tensor, value) -> Tensor:
+    if isinstance(value, Tensor):
+        return value
+    return full((), float(value), peer.dtype, peer.node.backend)
+
+
+def _binary(op, a: Tensor, b, out_dtype=None, params=b"") -> Tensor:
+    b = _scalar_like(a, b)
+    dims = broadcast_dims(a.shape, b.shape)
+    ba = a if a.shape == dims else a.broadcast_to(dims)
+    bb = b if b.shape == dims else b.broadcast_to(dims)
+    out_dtype = np.dtype(out_dtype or a.dtype)
+    rg = _grad_enabled and (a.requires_grad or b.requires_grad) and out_dtype == np.float32
+    return Tensor(Node(op, dims, out_dtype, a.node.backend, [ba.node, bb.node], params=params,
+                       requires_grad=rg))
+
+
+def _unary(op, a: Tensor) -> Tensor:
+    return Tensor(Node(op, a.shape, a.dtype, a.node.backend, [a.node],
+                       requires_grad=_grad_enabled and a.requires_grad))
+
+
+def add(a, b): return _binary(OP["ADD"], a, b)
+def sub(a, b): return _binary(OP["SUB"], a, b)
+def mul(a, b): return _binary(OP["MUL"], a, b)
+def div(a, b): return _binary(OP["DIV"], a, b)
+def maximum(a, b): return _binary(OP["MAXIMUM"], a, b)
+def minimum(a, b): return _binary(OP["MINIMUM"], a, b)
+def equal(a, b): return _binary(OP["EQUAL"], a, b, np.bool_)
+def less(a, b): return _binary(OP["LESS"], a, b, np.bool_)
+def greater(a, b): return _binary(OP["GREATER"], a, b, np.bool_)
+def less_equal(a, b): return _binary(OP["LESS_EQUAL"], a, b, np.bool_)
+def greater_equal(a, b): return _binary(OP["GREATER_EQUAL"], a, b, np.bool_)
+def neg(a): return _unary(OP["NEG"], a)
+def exp(a): return _unary(OP["EXP"], a)
+def log(a): return _unary(OP["LOG"], a)
+def relu(a): return _unary(OP["RELU"], a)
+
+
+def scaled_add(a: Tensor, b: Tensor, alpha: float, beta: float) -> Tensor:
+    """a*alpha + b*beta as one node (reference ops.cpp:144-171)."""
+    return _binary(OP["SCALED_ADD"], a, b, params=_params(("f", alpha), ("f", beta)))
+
+
+def where(cond: Tensor, a: Tensor, b: Tensor) -> Tensor:
+    dims = broadcast_dims(broadcast_dims(cond.shape, a.shape), b.shape)
+    c, x, y = cond.broadcast_to(dims), a.broadcast_to(dims), b.broadcast_to(dims)
+    rg = _grad_enabled and (a.requires_grad or b.requires_grad)
+    return Tensor(Node(OP["WHERE"], dims, a.dtype, a.node.backend, [c.node, x.node, y.node],
+                       requires_grad=rg))
+
+
+# ---------------------------------------------------------------------------
+# Reductions, softmax, matmul, convolution, pooling
+# ---------------------------------------------------------------------------
+
+def _axes_mask(axes, ndim: int) -> int:
+    if axes is None or (isinstance(axes, (list, tuple)) and len(axes) == 0):
+        return (1 << ndim) - 1 if ndim > 0 else 0
+    if isinstance(axes, int):
+        axes = [axes]
+    mask = 0
+    for a in axes:
+        a = a % ndim
+        if mask & (1 << a):
+            raise ValueError(f"axis {a} given more than once")
+        mask |= 1 << a
+    return mask
+
+
+def _reduction(op, a: Tensor, axes, keepdim: bool, out_dtype=None) -> Tensor:
+    mask = _axes_mask(axes, a.ndim)
+    dims = []
+    for i, e in enumerate(a.shape):
+        if not mask & (1 << i):
+            dims.append(e)
+        elif keepdim:
+            dims.append(1)
+    out_dtype = np.dtype(out_dtype or a.dtype)
+    n = Node(op, dims, out_dtype, a.node.backend, [a.node],
+             params=_params(("I", mask), ("?", keepdim)),
+             requires_grad=_grad_enabled and a.requires_grad and out_dtype == np.float32)
+    n.aux = (mask, keepdim)
+    return Tensor(n)
+
+
+def sum(a: Tensor, axes=None, keepdim: bool = False) -> Tensor:  # noqa: A001
+    return _reduction(OP["SUM"], a, axes, keepdim)
+
+
+def mean(a: Tensor, axes=None, keepdim: bool = False) -> Tensor:
+    return _reduction(OP["MEAN"], a, axes, keepdim)
+
+
+def amax(a: Tensor, axes=None, keepdim: bool = False) -> Tensor:
+    return _reduction(OP["MAX"], a, axes, keepdim)
+
+
+def argmax(a: Tensor, axis: int, keepdim: bool = False) -> Tensor:
+    return _reduction(OP["ARGMAX"], a, [axis], keepdim, np.int64)
+
+
+def _softmax_family(op, a: Tensor, axis: int) -> Tensor:
+    axis = axis % a.ndim
+    n = Node(op, a.shape, a.dtype, a.node.backend, [a.node], params=_params(("i", axis)),
+             requires_grad=_grad_enabled and a.requires_grad)
+    n.aux = axis
+    return Tensor(n)
+
+
+def softmax(a: Tensor, axis: int = -1) -> Tensor:
+    return _softmax_family(OP["SOFTMAX"], a, axis)
+
+
+def log_softmax(a: Tensor, axis: int = -1) -> Tensor:
+    return _softmax_family(OP["LOG_SOFTMAX"], a, axis)
+
+
+def matmul(a: Tensor, b: Tensor) -> Tensor:
+    """torch.matmul semantics lowered to one rank-4 Matmul node over broadcast
+    views (reference ops.cpp:906-981)."""
+    a_vec, b_vec = a.ndim == 1, b.ndim == 1
+    am = a.unsqueeze(0) if a_vec else a
+    bm = b.unsqueeze(1) if b_vec else b
+    m, k = am.shape[-2], am.shape[-1]
+    k2, n = bm.shape[-2], bm.shape[-1]
+    if k != k2:
+        raise ValueError(f"matmul inner dimensions disagree: {k} vs {k2}")
+    real_batch = broadcast_dims(am.shape[:-2], bm.shape[:-2])
+    if len(real_batch) > 2:
+        raise ValueError("matmul supports at most 2 batch axes")
+    batch = (1,) * (2 - len(real_batch)) + real_batch
+    a4 = am.broadcast_to(batch + (m, k))
+    b4 = bm.broadcast_to(batch + (k, n))
+    node = Node(OP["MATMUL"], batch + (m, n), a.dtype, a.node.backend, [a4.node, b4.node],
+                requires_grad=_grad_enabled and (a.requires_grad or b.requires_grad))
+    out = Tensor(node)
+    final = list(real_batch) + ([] if a_vec else [m]) + ([] if b_vec else [n])
+    return out.reshape(final)
+
+
+def _unfold_params(kernel, stride, pad, dil, hw) -> bytes:
+    return _params(*[("i", int(v)) for v in (*kernel, *stride, *pad, *dil, *hw)])
+
+
+def _pair(v):
+    return (int(v[0]), int(v[1])) if isinstance(v, (tuple, list)) else (int(v), int(v))
+
+
+def window_count(extent, k, s, p, d) -> int:
+    return (extent + 2 * p - (d * (k - 1) + 1)) // s + 1
+
+
+def im2col(x: Tensor, kernel, stride=1, padding=0, dilation=1) -> Tensor:
+    kernel, stride, padding, dilation = map(_pair, (kernel, stride, padding, dilation))
+    n_, c, h, w = x.shape
+    oh = window_count(h, kernel[0], stride[0], padding[0], dilation[0])
+    ow = window_count(w, kernel[1], stride[1], padding[1], dilation[1])
+    node = Node(OP["IM2COL"], (n_, c * kernel[0] * kernel[1], oh * ow), x.dtype, x.node.backend,
+                [x.node], params=_unfold_params(kernel, stride, padding, dilation, (h, w)),
+                requires_grad=_grad_enabled and x.requires_grad)
+    node.aux = (kernel, stride, padding, dilation, (h, w))
+    return Tensor(node)
+
+
+def col2im(cols: Tensor, image_hw, kernel, stride=1, padding=0, dilation=1) -> Tensor:
+    kernel, stride, padding, dilation, image_hw = map(_pair, (kernel, stride, padding, dilation,
+                                                              image_hw))
+    n_, rows, _ = cols.shape
+    c = rows // (kernel[0] * kernel[1])
+    src = cols.contiguous()
+    node = Node(OP["COL2IM"], (n_, c, image_hw[0], image_hw[1]), cols.dtype, cols.node.backend,
+                [src.node], params=_unfold_params(kernel, stride, padding, dilation, image_hw),
+                requires_grad=_grad_enabled and cols.requires_grad)
+    node.aux = (kernel, stride, padding, dilation, image_hw)
+    return Tensor(node)
+
+
+def conv2d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padding=0,
+           dilation=1) -> Tensor:
+    """im2col -> flat_weight @ cols (batch-broadcast A) -> reshape -> + bias
+    (reference ops.cpp:662-705)."""
+    stride, padding, dilation = map(_pair, (stride, padding, dilation))
+    cout = weight.shape[0]
+    kernel = (weight.shape[2], weight.shape[3])
+    cols = im2col(x, kernel, stride, padding, dilation)
+    oh = window_count(x.shape[2], kernel[0], stride[0], padding[0], dilation[0])
+    ow = window_count(x.shape[3], kernel[1], stride[1], padding[1], dilation[1])
+    flat_weight = weight.reshape(cout, cols.shape[1])
+    out = matmul(flat_weight, cols).reshape(x.shape[0], cout, oh, ow)
+    if bias is not None:
+        out = add(out, bias.reshape(cout, 1, 1))
+    return out
+
+
+def max_pool2d(x: Tensor, kernel, stride=None, padding=0) -> Tensor:
+    kernel = _pair(kernel)
+    stride = _pair(stride) if stride is not None else kernel
+    padding = _pair(padding)
+    n_, c, h, w = x.shape
+    oh = window_count(h, kernel[0], stride[0], padding[0], 1)
+    ow = window_count(w, kernel[1], stride[1], padding[1], 1)
+    node = Node(OP["MAX_POOL2D"], (n_, c, oh, ow), x.dtype, x.node.backend, [x.node],
+                params=_unfold_params(kernel, stride, padding, (1, 1), (h, w)),
+                requires_grad=_grad_enabled and x.requires_grad)
+    return Tensor(node)
+
+
+def one_hot_f32(target: Tensor, classes: int) -> Tensor:
+    """Cast(Equal(Cast(labels->F32)[:, None], arange(C))) (reference ops.cpp:347-354)."""
+    indices = arange(0.0, float(classes), 1.0, np.float32, target.node.backend)
+    return equal(target.to(np.float32).unsqueeze(-1), indices).to(np.float32)
+
+
+def cross_entropy(logits: Tensor, target: Tensor) -> Tensor:
+    """mean(-sum(log_softmax(logits) * one_hot, -1)) (reference ops.cpp:417-441)."""
+    batched = logits.unsqueeze(0) if logits.ndim == 1 else logits
+    labels = target.unsqueeze(0) if logits.ndim == 1 else target
+    picked = sum(mul(log_softmax(batched, -1), one_hot_f32(labels, batched.shape[1])), [-1])
+    return mean(neg(picked))
+
+
+# ---------------------------------------------------------------------------
+# Executor
+# ---------------------------------------------------------------------------
+
+def _fill_desc(d: _lib.TensorDesc, n: Node) -> None:
+    d.data = n.storage.ptr + n.offset * n.itemsize if n.storage is not None else 0
+    d.dtype = _VK_DTYPE[n.dtype]
+    d.ndim = len(n.shape)
+    for i, (e, s) in enumerate(zip(n.shape, n.strides)):
+        d.ne[i] = e
+        d.nb[i] = s
+
+
+def realize(tensors: Iterable[Tensor]) -> None:
+    """Evaluate every uncomputed node the tensors depend on, as ONE backend
+    compute() over the span in dependency order (reference executor.cpp:90-154)."""
+    roots = [t.node for t in tensors if t is not None and not t.node.computed]
+    if not roots:
+        return
+    order: list[Node] = []
+    seen: set[int] = set()
+    stack = [(r, 0) for r in reversed(roots)]
+    while stack:
+        node, i = stack.pop()
+        if id(node) in seen and i == 0:
+            continue
+        if node.computed:
+            seen.add(id(node))
+            continue
+        if i < len(node.src):
+            stack.append((node, i + 1))
+            child = node.src[i]
+            if child is not None and id(child) not in seen and not child.computed:
+                stack.append((child, 0))
+            continue
+        if id(node) not in seen:
+            seen.add(id(node))
+            order.append(node)
+    by_backend: dict[int, list[Node]] = {}
+    backends = {}
+    for node in order:
+        if node.is_view:
+            src = node.view_src
+            node.storage = src.storage
+            node.offset = src.offset + node.view_offset
+            node.computed = True
+            continue
+        if node.op == INPUT:
+            raise RuntimeError("an input tensor has no storage")
+        node.storage = node.backend.alloc(max(_numel(node.shape), 1) * node.itemsize)
+        node.offset = 0
+        by_backend.setdefault(id(node.backend), []).append(node)
+        backends[id(node.backend)] = node.backend
+    for key, nodes in by_backend.items():
+        arr = (_lib.NodeDesc * len(nodes))()
+        for d, node in zip(arr, nodes):
+            d.op = node.op
+            d.n_src = len(node.src)
+            _fill_desc(d.out, node)
+            for j, s in enumerate(node.src):
+                _fill_desc(d.src[j], s)
+            p = node.params
+            if p:
+                ctypes.memmove(ctypes.addressof(d.params), p, len(p))
+        backends[key].compute(arr, len(nodes))
+        for node in nodes:
+            node.computed = True
+
+
+def assign(params: Sequence[Tensor], values: Sequence[Tensor]) -> None:
+    """Rebind each parameter to its new value's storage (reference
+    python/vkml/__init__.py assign, which becomes copy_device_to_device)."""
+    realize(values)
+    for p, v in zip(params, values):
+        p.node.storage = v.node.storage
+        p.node.offset = v.node.offset
+        p.node.strides = v.node.strides
+        p.node.computed = True
+
+
+# ---------------------------------------------------------------------------
+# Autograd (reference src/autograd/autograd.cpp)
+# ---------------------------------------------------------------------------
+
+def _autograd_order(root: Node) -> list[Node]:
+    order, done = [], set()
+    stack = [(root, 0)]
+    while stack:
+        node, i = stack[-1]
+        if id(node) in done:
+            stack.pop()
+            continue
+        if i < len(node.src):
+            stack[-1] = (node, i + 1)
+            child = node.src[i]
+            if child is not None and child.requires_grad and id(child) not in done:
+                stack.append((child, 0))
+            continue
+        done.add(id(node))
+        order.append(node)
+        stack.pop()
+    return order
+
+
+def _accumulate(grads: dict, node: Node, g: Tensor) -> None:
+    if node is None or not node.requires_grad:
+        return
+    key = id(node)
+    if key in grads:
+        grads[key] = (node, grads[key][1] + g)
+    else:
+        grads[key] = (node, g)
+
+
+def reduce_to_shape(g: Tensor, target_dims) -> Tensor:
+    """Sums g down to target_dims, undoing a broadcast (autograd.cpp:84-116)."""
+    gd = list(g.shape)
+    target_dims = list(target_dims)
+    if gd == target_dims:
+        return g
+    lead = len(gd) - len(target_dims)
+    axes = []
+    for i, e in enumerate(gd):
+        if e == 1:
+            continue
+        absent = i < lead
+        stretched = not absent and target_dims[i - lead] == 1
+        if absent or stretched:
+            axes.append(i)
+    r = sum(g, axes, keepdim=True) if axes else g
+    return r.reshape(target_dims)
+
+
+def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
+    op = node.op
+    a = node.src[0] if node.src else None
+    b = node.src[1] if len(node.src) > 1 else None
+    ta = lambda: Tensor(a)  # noqa: E731
+    tb = lambda: Tensor(b)  # noqa: E731
+    out = Tensor(node)
+    if op in (OP["CONTIGUOUS"], RESHAPE, UNSQUEEZE):
+        _accumulate(grads, a, grad.reshape(a.shape))
+    elif op == PERMUTE:
+        perm = node.aux
+        inverse = [0] * len(perm)
+        for i, p in enumerate(perm):
+            inverse[p] = i
+        _accumulate(grads, a, grad.permute(inverse))
+    elif op == BROADCAST:
+        _accumulate(grads, a, reduce_to_shape(grad, a.shape))
+    elif op == OP["CAST"]:
+        _accumulate(grads, a, grad.to(a.dtype))
+    elif op == OP["ADD"]:
+        _accumulate(grads, a, grad)
+        _accumulate(grads, b, grad)
+    elif op == OP["SUB"]:
+        _accumulate(grads, a, grad)
+        _accumulate(grads, b, neg(grad))
+    elif op == OP["MUL"]:
+        if a.requires_grad:
+            _accumulate(grads, a, grad * tb())
+        if b.requires_grad:
+            _accumulate(grads, b, grad * ta())
+    elif op == OP["SCALED_ADD"]:
+        import struct
+
+        alpha, beta = struct.unpack("<ff", node.params[:8])
+        scale = lambda k: grad if k == 1.0 else scaled_add(grad, grad, k, 0.0)  # noqa: E731
+        if a.requires_grad:
+            _accumulate(grads, a, scale(alpha))
+        if b.requires_grad:
+            _accumulate(grads, b, scale(beta))
+    elif op == OP["DIV"]:
+        if a.requires_grad:
+            _accumulate(grads, a, grad / tb())
+        if b.requires_grad:
+            _accumulate(grads, b, neg(grad * out) / tb())
+    elif op == OP["NEG"]:
+        _accumulate(grads, a, neg(grad))
+    elif op == OP["EXP"]:
+        _accumulate(grads, a, grad * out)
+    elif op == OP["LOG"]:
+        _accumulate(grads, a, grad / ta())
+    elif op == OP["RELU"]:
+        _accumulate(grads, a, where(less_equal(ta(), zeros_like(ta())), zeros_like(grad), grad))
+    elif op in (OP["SUM"], OP["MEAN"]):
+        mask, keepdim = node.aux
+        src_dims = list(a.shape)
+        g = grad
+        if op == OP["MEAN"]:
+            count = 1
+            for i, e in enumerate(src_dims):
+                if mask & (1 << i):
+                    count *= e
+            g = g / float(count)
+        if not keepdim:
+            keep = [1 if mask & (1 << i) else e for i, e in enumerate(src_dims)]
+            g = g.reshape(keep)
+        _accumulate(grads, a, g.broadcast_to(src_dims).contiguous())
+    elif op == OP["SOFTMAX"]:
+        y = out
+        dot = sum(grad * y, [node.aux], keepdim=True)
+        _accumulate(grads, a, y * sub(grad, dot.broadcast_to(a.shape)))
+    elif op == OP["LOG_SOFTMAX"]:
+        total = sum(grad, [node.aux], keepdim=True)
+        _accumulate(grads, a, sub(grad, exp(out) * total.broadcast_to(a.shape)))
+    elif op == OP["MATMUL"]:
+        if a.requires_grad:
+            _accumulate(grads, a, matmul(grad, tb().transpose(-2, -1)))
+        if b.requires_grad:
+            _accumulate(grads, b, matmul(ta().transpose(-2, -1), grad))
+    elif op == OP["MAX_POOL2D"]:
+        inp = ta()
+        n = Node(OP["MAX_POOL2D_BACKWARD"], inp.shape, inp.dtype, inp.node.backend,
+                 [grad.contiguous().node, inp.contiguous().node], params=node.params)
+        _accumulate(grads, a, Tensor(n))
+    elif op == OP["IM2COL"]:
+        kernel, stride, pad, dil, hw = node.aux
+        _accumulate(grads, a, col2im(grad, hw, kernel, stride, pad, dil))
+    elif op == OP["COL2IM"]:
+        kernel, stride, pad, dil, hw = node.aux
+        _accumulate(grads, a, im2col(grad, kernel, stride, pad, dil))
+    else:
+        raise NotImplementedError(f"no gradient rule for op {op}")
+
+
+def backward(root: Tensor, seed: Tensor | None = None) -> None:
+    """Reverse-mode pass from `root`; leaf gradients are realised in ONE flush
+    (reference autograd.cpp:588-673)."""
+    if not root.requires_grad:
+        raise RuntimeError("backward() called on a tensor that does not require grad")
+    if seed is None:
+        if root.numel() != 1:
+            raise ValueError("backward() without a seed requires a scalar")
+        seed = ones(root.shape, root.dtype, root.node.backend)
+    order = _autograd_order(root.node)
+    grads = {id(root.node): (root.node, seed)}
+    with no_grad():
+        for node in reversed(order):
+            entry = grads.get(id(node))
+            if entry is None or node.op in LEAF_OPS:
+                continue
+            _apply_backward(node, entry[1], grads)
+        totals, leaves = [], []
+        for node in order:
+            if node.op not in LEAF_OPS or not node.requires_grad:
+                continue
+            entry = grads.get(id(node))
+            if entry is None:
+                continue
+            total = Tensor(node.grad) + entry[1] if node.grad is not None else entry[1]
+            totals.append(total)
+            leaves.append(node)
+    realize(totals)
+    for node, t in zip(leaves, totals):
+        node.grad = t.node
