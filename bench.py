@@ -47,6 +47,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="target CPU work for the baseline sample")
+    p.add_argument("--calibrate", action="store_true",
+                   help="also run the plain 16-byte copy kernel 5x over 256 MiB (the byte-counter "
+                        "calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -78,7 +81,8 @@ def gate():
 
 
 def time_launches(fn, timer: Timer, reps: int, warmup: int = 3):
-    """Per-launch durations (ms) from event pairs around each call."""
+    """Per-launch durations (ms) from event pairs around each call (for
+    launches long enough that event overhead is negligible)."""
     for _ in range(warmup):
         fn(0)
     gate()
@@ -89,6 +93,19 @@ def time_launches(fn, timer: Timer, reps: int, warmup: int = 3):
         e = timer.event()
         pairs.append((s, e))
     return [s.elapsed_ms(e) for s, e in pairs]
+
+
+def time_batch(fn, timer: Timer, reps: int, warmup: int = 3) -> float:
+    """Mean time (ms) of `reps` back-to-back launches between ONE event pair,
+    queued behind the gate so the GPU never waits for the host."""
+    for _ in range(warmup):
+        fn(0)
+    gate()
+    s = timer.event()
+    for i in range(reps):
+        fn(i)
+    e = timer.event()
+    return s.elapsed_ms(e) / reps
 
 
 def gemm_headline(args, hip, ops, timer):
@@ -145,7 +162,8 @@ def cpu_baseline(args):
 
 
 def secondary(hip, ops, timer):
-    """The other hot-path kernels at BASELINE shapes; median per-launch time."""
+    """The other hot-path kernels at BASELINE shapes: mean per-launch time of
+    back-to-back launches into preallocated outputs."""
     from vkml_amd.device import DeviceArray
 
     rng = np.random.default_rng(7)
@@ -154,13 +172,15 @@ def secondary(hip, ops, timer):
     def rotate(shape, count, gen=lambda s: rng.standard_normal(s, dtype=np.float32)):
         return [DeviceArray.from_numpy(gen(shape)) for _ in range(count)]
 
-    def med(ms):
-        return float(np.median(ms))
+    def bw(name, ms, byt):
+        out[name] = {"ms": round(ms, 5), "gbs": round(byt / ms / 1e6, 1),
+                     "frac_of_hbm": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4)}
 
     # GEMM variants (compute-bound: no rotation)
     for name, (m, n, k), lay in [("gemm_nt_4096", (4096, 4096, 4096), "nt"),
                                  ("gemm_tn_4096", (4096, 4096, 4096), "tn"),
                                  ("gemm_8192x1024x4096", (8192, 1024, 4096), "nn"),
+                                 ("gemm_8192", (8192, 8192, 8192), "nn"),
                                  ("splitk_256x256x65536", (256, 256, 65536), "nn"),
                                  ("wgrad_128x784x16384", (128, 784, 16384), "nn")]:
         a = DeviceArray.from_numpy(rng.standard_normal((m, k) if lay[0] == "n" else (k, m),
@@ -169,56 +189,114 @@ def secondary(hip, ops, timer):
                                                        dtype=np.float32))
         av = a if lay[0] == "n" else a.T
         bv = b if lay[1] == "n" else b.T
-        ms = med(time_launches(lambda i: ops.matmul(av, bv), timer, 20))
+        c = DeviceArray((m, n), np.float32)
+        ms = time_batch(lambda i: ops.matmul(av, bv, out=c), timer, 10 if m * n * k > 2**36 else 20)
         splits, _ = ops.gemm_plan(1, m, n, k)
-        out[name] = {"ms": ms, "tflops": 2.0 * m * n * k / ms / 1e9,
-                     "frac_of_peak": 2.0 * m * n * k / ms / 1e9 / MFMA_FP32_PEAK_TFLOPS,
-                     "splits": splits}
+        tf = 2.0 * m * n * k / ms / 1e9
+        out[name] = {"ms": round(ms, 5), "tflops": round(tf, 2),
+                     "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "splits": splits}
+        del a, b, c
 
     # Practical HBM ceiling: the library's plain 16-byte copy, 4 x 256 MiB buffers
     bufs = [DeviceArray((64 << 20,), np.float32) for _ in range(4)]
-    byt = 2 * (64 << 20) * 4
-    ms = med(time_launches(lambda i: hip.copy_device_to_device([(bufs[(i + 1) % 4], bufs[i % 4])]),
-                           timer, 20))
-    out["copy_256MiB"] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+    ms = time_batch(lambda i: hip.copy_device_to_device([(bufs[(i + 1) % 4], bufs[i % 4])]),
+                    timer, 20)
+    bw("copy_256MiB", ms, 2 * (64 << 20) * 4)
     del bufs
 
     # GEMV 4096x4096 . 4096 (bandwidth): rotate 8 matrices (512 MB)
     mats = rotate((4096, 4096), 8)
     x = DeviceArray.from_numpy(rng.standard_normal(4096, dtype=np.float32))
-    ms = med(time_launches(lambda i: ops.gemv(mats[i % 8], x), timer, 24))
-    byt = 4096 * 4096 * 4 + 4096 * 4 * 2
-    out["gemv_4096"] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+    y = DeviceArray((4096,), np.float32)
+    ms = time_batch(lambda i: ops.gemv(mats[i % 8], x, out=y), timer, 40)
+    bw("gemv_4096", ms, 4096 * 4096 * 4 + 4096 * 4 * 2)
     del mats
 
-    # im2col / col2im conv2 [128,64,32,32] <-> [128,576,1024]
+    # im2col / col2im conv2 [128,64,32,32] <-> [128,576,1024] (335.5 MB each way)
     imgs = rotate((128, 64, 32, 32), 2)
     cols = [ops.im2col(im, 3, 1, 1) for im in imgs]
+    img_out = DeviceArray((128, 64, 32, 32), np.float32)
     hip.synchronize()
     byt = 128 * 64 * 32 * 32 * 4 + 128 * 576 * 1024 * 4
-    ms = med(time_launches(lambda i: ops.im2col(imgs[i % 2], 3, 1, 1), timer, 20))
-    out["im2col_conv2"] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
-    ms = med(time_launches(lambda i: ops.col2im(cols[i % 2], (32, 32), 3, 1, 1), timer, 20))
-    out["col2im_conv2"] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
-    del imgs, cols
+    ms = time_batch(lambda i: ops.im2col(imgs[i % 2], 3, 1, 1, out=cols[(i + 1) % 2]), timer, 20)
+    bw("im2col_conv2", ms, byt)
+    ms = time_batch(lambda i: ops.col2im(cols[i % 2], (32, 32), 3, 1, 1, out=img_out), timer, 20)
+    bw("col2im_conv2", ms, byt)
+    del imgs, cols, img_out
 
     # softmax (read + write once), rotate past the MALL
     for shape, count in [((4096, 1000), 20), ((256, 32768), 10)]:
         xs = rotate(shape, count, lambda s: rng.standard_normal(s, dtype=np.float32) * 2)
-        byt = 2 * shape[0] * shape[1] * 4
-        ms = med(time_launches(lambda i: ops.softmax(xs[i % count], -1), timer, 40))
-        out[f"softmax_{shape[0]}x{shape[1]}"] = {"ms": ms, "gbs": byt / ms / 1e6,
-                                                 "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
-        del xs
+        ys = [DeviceArray(shape, np.float32) for _ in range(2)]
+        ms = time_batch(lambda i: ops.softmax(xs[i % count], -1, out=ys[i % 2]), timer, 40)
+        bw(f"softmax_{shape[0]}x{shape[1]}", ms, 2 * shape[0] * shape[1] * 4)
+        del xs, ys
 
     # sum / max over the last axis of [8192, 4096] (134 MB read), 4 buffers
     xs = rotate((8192, 4096), 4)
-    byt = 8192 * 4096 * 4 + 8192 * 4
+    r = DeviceArray((8192,), np.float32)
     for name, fn in [("sum_8192x4096", ops.sum), ("max_8192x4096", ops.amax)]:
-        ms = med(time_launches(lambda i: fn(xs[i % 4], [1]), timer, 20))
-        out[name] = {"ms": ms, "gbs": byt / ms / 1e6, "frac_of_hbm": byt / ms / 1e6 / HBM_PEAK_GBS}
+        ms = time_batch(lambda i: fn(xs[i % 4], [1], out=r), timer, 20)
+        bw(name, ms, 8192 * 4096 * 4 + 8192 * 4)
     del xs
     return out
+
+
+def training_steps(steps_mlp: int = 100, steps_cnn: int = 20):
+    """BASELINE configs 1 and 5 as training loops on the device: steps/s over
+    the timed steps (graph build + flushes + the loss read each step)."""
+    from vkml_amd import nn, optim
+    from vkml_amd import tensor as T
+
+    res = {}
+    rng = np.random.default_rng(20260726)
+    configs = {
+        "mlp_784_128_10_b64": (lambda: nn.Sequential(nn.Flatten(), nn.Linear(784, 128), nn.ReLU(),
+                                                      nn.Linear(128, 10)),
+                               (64, 1, 28, 28), 10, 0.1, steps_mlp, (0.0, 1.0)),
+        "cifar_cnn_b128": (lambda: nn.Sequential(
+            nn.Conv2d(3, 64, 3, padding=1), nn.ReLU(), nn.MaxPool2d(2),
+            nn.Conv2d(64, 128, 3, padding=1), nn.ReLU(), nn.MaxPool2d(2), nn.Flatten(),
+            nn.Linear(8192, 256), nn.ReLU(), nn.Linear(256, 100)),
+            (128, 3, 32, 32), 100, 0.01, steps_cnn, (-1.0, 1.0)),
+    }
+    for name, (make, shape, classes, lr, steps, (lo, hi)) in configs.items():
+        nn.manual_seed(20260726)
+        model = make()
+        opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
+        data = [(rng.uniform(lo, hi, shape).astype(np.float32),
+                 rng.integers(0, classes, shape[0]).astype(np.int64)) for _ in range(4)]
+
+        def step(i):
+            x, y = data[i % 4]
+            opt.zero_grad()
+            loss = nn.cross_entropy(model(T.tensor(x)), T.tensor(y))
+            loss.backward()
+            opt.step()
+            return loss.item()
+
+        for i in range(3):
+            step(i)
+        t0 = time.perf_counter()
+        for i in range(steps):
+            last = step(i)
+        dt = time.perf_counter() - t0
+        res[name] = {"steps": steps, "ms_per_step": round(dt * 1e3 / steps, 3),
+                     "steps_per_s": round(steps / dt, 2), "last_loss": round(last, 5)}
+    return res
+
+
+def read_traffic(args):
+    """HBM bytes per launch of the headline GEMM, from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
+    calibration in the same summary); None when no summary matches."""
+    path = ROOT / "profiles" / f"gemm_nn_{args.m}x{args.n}x{args.k}_pmc.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def main():
@@ -254,8 +332,19 @@ def main():
                      "kernel": "gemm_mfma_kernel<128,128,32,64,64>",
                      "avg_launch_ms": round(avg_ms, 4), "min_launch_ms": round(min_ms, 4)},
     }
+    if args.calibrate:
+        from vkml_amd.device import DeviceArray
+
+        src, dst = DeviceArray((64 << 20,), np.float32), DeviceArray((64 << 20,), np.float32)
+        for _ in range(5):
+            hip.copy_device_to_device([(dst, src)])
+        hip.synchronize()
+    traffic = read_traffic(args)
+    if traffic is not None:
+        result["roofline"]["traffic"] = traffic
     if not args.no_secondary:
         result["secondary"] = secondary(hip, ops, timer)
+        result["training"] = training_steps()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(result), flush=True)

@@ -101,13 +101,23 @@ def split_k_reduce(ws: DeviceArray, splits: int) -> DeviceArray:
     return out
 
 
-def gemv(a: DeviceArray, x: DeviceArray) -> DeviceArray:
+def _out(out: DeviceArray | None, shape, dtype=np.float32) -> DeviceArray:
+    """The result buffer: `out` if given (contiguous, right shape), else new."""
+    shape = tuple(int(e) for e in shape)
+    if out is None:
+        return DeviceArray(shape, dtype)
+    if out.shape != shape or out.dtype != np.dtype(dtype) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {np.dtype(dtype)} array of shape {shape}")
+    return out
+
+
+def gemv(a: DeviceArray, x: DeviceArray, out: DeviceArray | None = None) -> DeviceArray:
     """y = A @ x for A [M,K] with unit inner stride (the N == 1 matmul)."""
     _f32(a, "gemv")
     _f32(x, "gemv")
     if a.ndim != 2 or x.ndim != 1 or a.shape[1] != x.shape[0] or a.strides[1] != 1:
         raise ValueError("gemv: expects A [M,K] with unit inner stride and x [K]")
-    y = DeviceArray((a.shape[0],), np.float32)
+    y = _out(out, (a.shape[0],))
     check(_lib.load().vkhip_gemv(c_void_p(a.ptr), a.strides[0], c_void_p(x.ptr), x.strides[0],
                                  c_void_p(y.ptr), a.shape[0], a.shape[1]), "gemv")
     return y
@@ -120,7 +130,8 @@ def window_count(extent: int, k: int, s: int, p: int, d: int) -> int:
     return (extent + 2 * p - (d * (k - 1) + 1)) // s + 1
 
 
-def im2col(x: DeviceArray, kernel, stride=1, padding=0, dilation=1) -> DeviceArray:
+def im2col(x: DeviceArray, kernel, stride=1, padding=0, dilation=1,
+           out: DeviceArray | None = None) -> DeviceArray:
     """[N, C, H, W] -> [N, C*kh*kw, out_h*out_w] (reference ops.cpp:485-512)."""
     _f32(x, "im2col")
     if x.ndim != 4:
@@ -133,14 +144,15 @@ def im2col(x: DeviceArray, kernel, stride=1, padding=0, dilation=1) -> DeviceArr
     oh, ow = window_count(h, kh, sh, ph, dh), window_count(w, kw, sw, pw, dw)
     if oh <= 0 or ow <= 0:
         raise ValueError("im2col: kernel larger than the padded image")
-    out = DeviceArray((n, c * kh * kw, oh * ow), np.float32)
+    out = _out(out, (n, c * kh * kw, oh * ow))
     u = _lib.unfold((kh, kw), (sh, sw), (ph, pw), (dh, dw), (h, w))
     check(_lib.load().vkhip_im2col(c_void_p(x.ptr), byref(x.operand()), c_void_p(out.ptr),
                                    byref(u)), "im2col")
     return out
 
 
-def col2im(cols: DeviceArray, image_hw, kernel, stride=1, padding=0, dilation=1) -> DeviceArray:
+def col2im(cols: DeviceArray, image_hw, kernel, stride=1, padding=0, dilation=1,
+           out: DeviceArray | None = None) -> DeviceArray:
     """[N, C*kh*kw, L] -> [N, C, H, W], the adjoint of im2col (reference ops.cpp:514-541)."""
     _f32(cols, "col2im")
     if cols.ndim != 3:
@@ -159,7 +171,7 @@ def col2im(cols: DeviceArray, image_hw, kernel, stride=1, padding=0, dilation=1)
     if window_count(h, kh, sh, ph, dh) * window_count(w, kw, sw, pw, dw) != L:
         raise ValueError("col2im: column count disagrees with the image geometry")
     c = rows // (kh * kw)
-    out = DeviceArray((n, c, h, w), np.float32)
+    out = _out(out, (n, c, h, w))
     u = _lib.unfold((kh, kw), (sh, sw), (ph, pw), (dh, dw), (h, w))
     check(_lib.load().vkhip_col2im(c_void_p(cols.ptr), c_void_p(out.ptr), n, c, byref(u)),
           "col2im")
@@ -174,9 +186,10 @@ def _axis4(x: DeviceArray, axis: int) -> int:
     return (axis % x.ndim) + 4 - x.ndim
 
 
-def softmax(x: DeviceArray, axis: int = -1, log: bool = False) -> DeviceArray:
+def softmax(x: DeviceArray, axis: int = -1, log: bool = False,
+            out: DeviceArray | None = None) -> DeviceArray:
     _f32(x, "softmax")
-    out = DeviceArray(x.shape, np.float32)
+    out = _out(out, x.shape)
     check(_lib.load().vkhip_softmax(c_void_p(x.ptr), byref(x.operand()), c_void_p(out.ptr),
                                     _axis4(x, axis), 1 if log else 0), "softmax")
     return out
@@ -186,7 +199,8 @@ def log_softmax(x: DeviceArray, axis: int = -1) -> DeviceArray:
     return softmax(x, axis, log=True)
 
 
-def _reduce(op: int, x: DeviceArray, axes, keepdim: bool) -> DeviceArray:
+def _reduce(op: int, x: DeviceArray, axes, keepdim: bool,
+            out: DeviceArray | None = None) -> DeviceArray:
     _f32(x, "reduce")
     if axes is None:
         axes = list(range(x.ndim))
@@ -199,26 +213,30 @@ def _reduce(op: int, x: DeviceArray, axes, keepdim: bool) -> DeviceArray:
     kept = [e for i, e in enumerate(x.shape) if i not in axes]
     shape = [1 if i in axes else e for i, e in enumerate(x.shape)] if keepdim else kept
     dt = np.int64 if op in (_lib.REDUCE_ARGMAX, _lib.REDUCE_ARGMIN) else np.float32
-    out = DeviceArray(shape, dt)
+    out = _out(out, shape, dt)
     check(_lib.load().vkhip_reduce(op, c_void_p(x.ptr), byref(x.operand()), mask,
                                    c_void_p(out.ptr)), "reduce")
     return out
 
 
-def sum(x: DeviceArray, axes=None, keepdim: bool = False) -> DeviceArray:  # noqa: A001
-    return _reduce(_lib.REDUCE_SUM, x, axes, keepdim)
+def sum(x: DeviceArray, axes=None, keepdim: bool = False,
+        out: DeviceArray | None = None) -> DeviceArray:  # noqa: A001
+    return _reduce(_lib.REDUCE_SUM, x, axes, keepdim, out)
 
 
-def mean(x: DeviceArray, axes=None, keepdim: bool = False) -> DeviceArray:
-    return _reduce(_lib.REDUCE_MEAN, x, axes, keepdim)
+def mean(x: DeviceArray, axes=None, keepdim: bool = False,
+        out: DeviceArray | None = None) -> DeviceArray:
+    return _reduce(_lib.REDUCE_MEAN, x, axes, keepdim, out)
 
 
-def amax(x: DeviceArray, axes=None, keepdim: bool = False) -> DeviceArray:
-    return _reduce(_lib.REDUCE_MAX, x, axes, keepdim)
+def amax(x: DeviceArray, axes=None, keepdim: bool = False,
+        out: DeviceArray | None = None) -> DeviceArray:
+    return _reduce(_lib.REDUCE_MAX, x, axes, keepdim, out)
 
 
-def amin(x: DeviceArray, axes=None, keepdim: bool = False) -> DeviceArray:
-    return _reduce(_lib.REDUCE_MIN, x, axes, keepdim)
+def amin(x: DeviceArray, axes=None, keepdim: bool = False,
+        out: DeviceArray | None = None) -> DeviceArray:
+    return _reduce(_lib.REDUCE_MIN, x, axes, keepdim, out)
 
 
 def argmax(x: DeviceArray, axis: int, keepdim: bool = False) -> DeviceArray:
