@@ -303,6 +303,9 @@ int vkhip_event_elapsed(void* start, void* end, float* out_ms);
  * adjacent-first reproduces the oracle's additions. */
 int vkhip_pairwise_leaf(uint32_t n, uint32_t leaf, uint32_t* out_depth, uint32_t* out_begin,
                         uint32_t* out_end);
+/* n / d as the device kernels compute it (multiply-high by a precomputed
+ * magic number; d = 0 returns 0xffffffff). */
+uint32_t vkhip_fast_divide(uint32_t n, uint32_t d);
 
 #ifdef __cplusplus
 }

@@ -250,7 +250,8 @@ def check_softmax(got, want, n):
 
 
 @pytest.mark.parametrize("shape", [(4096, 1000), (256, 32768), (64, 10), (128, 100),
-                                   (3, 1), (5, 4097), (7, 2048), (2, 3000), (33, 8192)])
+                                   (3, 1), (5, 4097), (7, 2048), (2, 3000), (33, 8192),
+                                   (9, 4096), (5, 16384), (3000, 257), (1025, 64)])
 @pytest.mark.parametrize("log", [False, True])
 def test_softmax_parity(hip, shape, log):
     x = (np.random.default_rng(SEED + shape[1]).standard_normal(shape) * 2).astype(np.float32)

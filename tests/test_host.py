@@ -132,3 +132,19 @@ def test_unfold_and_operand_helpers():
     assert list(d.ne) == [1, 1, 3, 5] and list(d.nb) == [0, 0, 5, 1]
     u = _lib.unfold((3, 2), (1, 2), (1, 0), (1, 1), (7, 5))
     assert (u.kernel_h, u.kernel_w, u.stride_w, u.pad_h, u.image_h) == (3, 2, 2, 1, 7)
+
+
+def test_fast_divide_is_exact():
+    """The launch-time division the movement kernels use, against Python's //,
+    over small, large, boundary and random numerators and divisors."""
+    lib = _lib.load()
+    rng = np.random.default_rng(0)
+    divisors = [1, 2, 3, 5, 7, 9, 16, 17, 31, 32, 33, 100, 1000, 1024, 4095, 65535, 65536,
+                (1 << 31) - 1, 1 << 31, (1 << 31) + 1, (1 << 32) - 1]
+    divisors += [int(d) for d in rng.integers(1, 1 << 32, 40, dtype=np.uint64)]
+    for d in divisors:
+        nums = [0, 1, d - 1, d, d + 1, 2 * d - 1, (1 << 32) - 1, (1 << 32) - 2, (1 << 31)]
+        nums += [int(v) for v in rng.integers(0, 1 << 32, 200, dtype=np.uint64)]
+        for n in nums:
+            n &= 0xFFFFFFFF
+            assert lib.vkhip_fast_divide(n, d) == n // d, (n, d)

@@ -137,6 +137,33 @@ __host__ __device__ __forceinline__ void pairwise_leaf(uint32_t n, int depth, ui
     end = e;
 }
 
+// ---- division by a runtime-constant divisor -----------------------------------
+// Unsigned 32-bit division by a divisor fixed at launch, as one multiply-high,
+// a subtract, an add and two shifts (the round-up multiplier method from
+// Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994). Exact for every 32-bit numerator.
+struct FastDiv {
+    uint32_t d, m, s;
+    FastDiv() = default;
+    __host__ explicit FastDiv(uint32_t divisor) : d(divisor), m(0), s(0) {
+        if (d > 1) {
+            uint32_t l = 0;
+            while ((1ull << l) < d) ++l;  // l = ceil(log2 d)
+            s = l;
+            m = static_cast<uint32_t>(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+        }
+    }
+    __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
+        if (d == 1) return n;
+#ifdef __HIP_DEVICE_COMPILE__
+        const uint32_t t = __umulhi(m, n);
+#else
+        const uint32_t t = static_cast<uint32_t>((static_cast<uint64_t>(m) * n) >> 32);
+#endif
+        return (t + ((n - t) >> 1)) >> (s - 1);
+    }
+};
+
 // ---- staged rows ------------------------------------------------------------
 // A row that is summed in the pairwise order is first staged in LDS with 4
 // padding floats after every 32 elements: each full 32-element leaf then starts

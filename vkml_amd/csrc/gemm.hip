@@ -476,9 +476,15 @@ int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t spl
     return VKHIP_OK;
 }
 
+int launch_gemv_rows(const float* a, int64_t lda, const float* x, float* y, uint32_t m, uint32_t k);
+
 int launch_gemv(const float* a, int64_t lda, const float* x, int64_t incx, float* y, uint32_t m,
                 uint32_t k) {
     if (m == 0) return VKHIP_OK;
+    // Contiguous x and rows up to 32768: the staged row-sum kernel with
+    // products (a whole workgroup per row for long rows). Otherwise the
+    // wave-per-row kernel below, which also takes a strided x.
+    if (incx == 1 && k <= 32768) return launch_gemv_rows(a, lda, x, y, m, k);
     if (k > static_cast<uint32_t>(kGemvMaxK))
         return fail(VKHIP_ERR_UNSUPPORTED, "gemv: K=%u exceeds the LDS-staged maximum %d", k,
                     kGemvMaxK);
@@ -532,7 +538,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     // GEMV: an N == 1 product with a unit-stride K axis of A is a bandwidth
     // problem, not a matrix-core one. AUTO takes it whenever batch == 1.
     if ((kernel == VKHIP_GEMM_GEMV || kernel == VKHIP_GEMM_AUTO) && n == 1 && batch == 1 &&
-        ad.nb[3] == 1 && k <= static_cast<uint32_t>(kGemvMaxK)) {
+        ad.nb[3] == 1 && (k <= static_cast<uint32_t>(kGemvMaxK) || (bd.nb[2] == 1 && k <= 32768))) {
         return launch_gemv(a, ad.nb[2], b, bd.nb[2], c, m, k);
     }
     if (kernel == VKHIP_GEMM_GEMV)

@@ -61,7 +61,7 @@ template <bool NT>
 __global__ __launch_bounds__(256) void im2col_kernel(const float* __restrict__ src, Op4 sd,
                                                      float* __restrict__ dst, Geo g, uint32_t rows,
                                                      uint32_t nrows, uint32_t L,
-                                                     uint32_t pos_blocks, int vec) {
+                                                     uint32_t pos_blocks, int vec, FastDiv div_w) {
     const uint32_t rb = blockIdx.x / pos_blocks;
     const uint32_t pb = blockIdx.x % pos_blocks;
     const uint32_t pos0 = (pb * 256 + threadIdx.x) * 4;
@@ -72,8 +72,8 @@ __global__ __launch_bounds__(256) void im2col_kernel(const float* __restrict__ s
     for (int j = 0; j < 4; ++j) {
         const uint32_t pos = pos0 + j;
         in[j] = pos < L;
-        const int32_t oh = in[j] ? pos / g.out_w : 0;
-        const int32_t ow = in[j] ? pos - oh * g.out_w : 0;
+        const int32_t oh = in[j] ? static_cast<int32_t>(div_w.div(pos)) : 0;
+        const int32_t ow = in[j] ? static_cast<int32_t>(pos) - oh * g.out_w : 0;
         hb[j] = oh * g.sh - g.ph;
         xb[j] = ow * g.sw - g.pw;
     }
@@ -138,11 +138,13 @@ int launch_im2col(const float* src, const vkhip_operand& sd, float* dst, const v
     if (nt_stores())
         hipLaunchKernelGGL(im2col_kernel<true>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
                            ctx().stream, src, to_op4(sd), dst, g, rows,
-                           static_cast<uint32_t>(nrows), L, pos_blocks, vec);
+                           static_cast<uint32_t>(nrows), L, pos_blocks, vec,
+                           FastDiv(static_cast<uint32_t>(g.out_w)));
     else
         hipLaunchKernelGGL(im2col_kernel<false>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
                            ctx().stream, src, to_op4(sd), dst, g, rows,
-                           static_cast<uint32_t>(nrows), L, pos_blocks, vec);
+                           static_cast<uint32_t>(nrows), L, pos_blocks, vec,
+                           FastDiv(static_cast<uint32_t>(g.out_w)));
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -198,6 +200,81 @@ __global__ __launch_bounds__(256) void col2im_kernel(const float* __restrict__ c
     }
 }
 
+// Staged variant: one workgroup per (image, channel) plane. That plane's kh*kw
+// cols rows are one contiguous run of kh*kw*L floats, staged once in LDS with
+// 16-byte loads; each thread then pulls four consecutive output pixels from LDS
+// in the same ascending (ki, kj) order. Every cols byte is read from HBM
+// exactly once, fully coalesced.
+template <bool UNIT>
+__global__ __launch_bounds__(256) void col2im_staged_kernel(const float* __restrict__ cols,
+                                                            float* __restrict__ dst, Geo g,
+                                                            uint32_t plane_floats, int vec_in,
+                                                            int vec_out, FastDiv div_w) {
+    extern __shared__ __attribute__((aligned(16))) float stage[];
+    const uint64_t plane = blockIdx.x;
+    const float* src = cols + plane * plane_floats;
+    if (vec_in) {
+        const f32x4* s4 = reinterpret_cast<const f32x4*>(src);
+        f32x4* d4 = reinterpret_cast<f32x4*>(stage);
+        for (uint32_t i = threadIdx.x; i < plane_floats / 4; i += 256) d4[i] = s4[i];
+    } else {
+        for (uint32_t i = threadIdx.x; i < plane_floats; i += 256) stage[i] = src[i];
+    }
+    __syncthreads();
+    const int32_t L = g.out_h * g.out_w;
+    const uint32_t hw = static_cast<uint32_t>(g.H) * g.W;
+    float* out = dst + plane * hw;
+    for (uint32_t q = threadIdx.x; 4 * q < hw; q += 256) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t pix0 = 4 * q;
+        int32_t h = static_cast<int32_t>(div_w.div(pix0));
+        int32_t x = static_cast<int32_t>(pix0) - h * g.W;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (pix0 + j < hw) {
+                float a = 0.0f;
+                for (int32_t ki = 0; ki < g.kh; ++ki) {
+                    int32_t oh;
+                    if (UNIT) {
+                        oh = h + g.ph - ki;
+                        if (oh < 0 || oh >= g.out_h) continue;
+                    } else {
+                        const int32_t top = h + g.ph - ki * g.dh;
+                        if (top < 0 || top % g.sh != 0) continue;
+                        oh = top / g.sh;
+                        if (oh >= g.out_h) continue;
+                    }
+                    for (int32_t kj = 0; kj < g.kw; ++kj) {
+                        int32_t ow;
+                        if (UNIT) {
+                            ow = x + g.pw - kj;
+                            if (ow < 0 || ow >= g.out_w) continue;
+                        } else {
+                            const int32_t left = x + g.pw - kj * g.dw;
+                            if (left < 0 || left % g.sw != 0) continue;
+                            ow = left / g.sw;
+                            if (ow >= g.out_w) continue;
+                        }
+                        a = a + stage[(ki * g.kw + kj) * L + oh * g.out_w + ow];
+                    }
+                }
+                acc[j] = a;
+            }
+            if (++x == g.W) {
+                x = 0;
+                ++h;
+            }
+        }
+        if (vec_out && pix0 + 3 < hw) {
+            *reinterpret_cast<f32x4*>(out + pix0) = acc;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (pix0 + j < hw) out[pix0 + j] = acc[j];
+        }
+    }
+}
+
 int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
                   const vkhip_unfold& p) {
     Geo g;
@@ -205,6 +282,25 @@ int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
     if (st != VKHIP_OK) return st;
     const uint64_t planes = static_cast<uint64_t>(n) * channels;
     if (planes == 0 || g.H == 0 || g.W == 0) return VKHIP_OK;
+    const uint64_t L = static_cast<uint64_t>(g.out_h) * g.out_w;
+    const uint64_t plane_floats = L * g.kh * g.kw;
+    if (plane_floats * sizeof(float) <= 65536 && planes <= 0x7fffffffull) {
+        const int vec_in = (plane_floats % 4 == 0) && (reinterpret_cast<uintptr_t>(cols) % 16 == 0);
+        const int vec_out = (static_cast<uint64_t>(g.H) * g.W % 4 == 0) &&
+                            (reinterpret_cast<uintptr_t>(dst) % 16 == 0);
+        const bool unit = g.sh == 1 && g.sw == 1 && g.dh == 1 && g.dw == 1;
+        const FastDiv dw(static_cast<uint32_t>(g.W));
+        if (unit)
+            hipLaunchKernelGGL(col2im_staged_kernel<true>, dim3(static_cast<uint32_t>(planes)),
+                               dim3(256), plane_floats * sizeof(float), ctx().stream, cols, dst, g,
+                               static_cast<uint32_t>(plane_floats), vec_in, vec_out, dw);
+        else
+            hipLaunchKernelGGL(col2im_staged_kernel<false>, dim3(static_cast<uint32_t>(planes)),
+                               dim3(256), plane_floats * sizeof(float), ctx().stream, cols, dst, g,
+                               static_cast<uint32_t>(plane_floats), vec_in, vec_out, dw);
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
     const uint32_t xq_n = ceil_div(g.W, 4);
     const uint64_t total_q = planes * g.H * xq_n;
     const uint64_t blocks = (total_q + 255) / 256;

@@ -163,6 +163,149 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
     }
 }
 
+// ---- softmax, one wave per row, persistent with prefetch -------------------------------
+// Rows of n <= 16*E4 (E4 float4 per lane) contiguous floats. Each wave walks
+// rows row0, row0 + stride, ... and issues the next row's loads before it
+// works on the current one, so HBM reads of one row overlap the reductions
+// and the stores of the previous: the latency-bound phases of the one-shot
+// kernel (all loads, then all math, then all stores) interleave instead.
+// The wave's LDS stage is private to it; lanes exchange staged values only
+// inside the wave, whose LDS operations complete in issue order, so a
+// compiler barrier (no s_barrier) orders them.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int E4>
+__global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
+    const float* __restrict__ src, int64_t in_stride, float* __restrict__ dst, uint32_t rows,
+    uint32_t n, int depth, int log_mode, int vec, uint32_t sstride) {
+    constexpr int E = 4 * E4;
+    extern __shared__ __attribute__((aligned(16))) float dyn[];
+    const int wave = threadIdx.x >> 6;
+    const int t = threadIdx.x & 63;
+    float* stage = dyn + wave * sstride;
+    const uint32_t stride = gridDim.x * 4;
+    uint32_t row = blockIdx.x * 4 + wave;
+    float xn[E];
+    load_row<64, E4>(xn, src + static_cast<int64_t>(row < rows ? row : 0) * in_stride, n, t,
+                     row < rows, vec);
+    const uint32_t leaves = 1u << depth;
+    for (; row < rows; row += stride) {
+        float x[E];
+#pragma unroll
+        for (int i = 0; i < E; ++i) x[i] = xn[i];
+        const uint32_t next = row + stride;
+        if (next < rows) load_row<64, E4>(xn, src + static_cast<int64_t>(next) * in_stride, n, t, true, vec);
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < E; ++i)
+            if (elem_of(vec, 64, t, i) < n) mx = max_ignoring_nan(mx, x[i]);
+        mx = wave_max(mx);
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const uint32_t e = elem_of(vec, 64, t, i);
+            const float sh = x[i] - mx;
+            const float ex = expf(sh);
+            if (e < n) stage[stage_index(e)] = ex;
+            x[i] = log_mode ? sh : ex;
+        }
+        wave_lds_fence();
+        const uint32_t per = leaves > 64 ? leaves / 64 : 1u;
+        float v = 0.0f;
+        if (static_cast<uint32_t>(t) * per < leaves) v = staged_subtree_sum(stage, n, depth, t * per, per);
+        const float denom = wave_sum_butterfly(v);
+        wave_lds_fence();  // every lane's stage reads precede the next row's writes
+        const float ld = logf(denom);
+        float* ds = dst + static_cast<uint64_t>(row) * n;
+        if (vec) {
+#pragma unroll
+            for (int i = 0; i < E4; ++i) {
+                const uint32_t e0 = 4u * (t + 64 * i);
+                if (e0 < n) {
+                    f32x4 o;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) o[j] = log_mode ? x[4 * i + j] - ld : x[4 * i + j] / denom;
+                    *reinterpret_cast<f32x4*>(ds + e0) = o;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const uint32_t e = t + 64 * i;
+                if (e < n) ds[e] = log_mode ? x[i] - ld : x[i] / denom;
+            }
+        }
+    }
+}
+
+// ---- softmax over long rows of 32 * 2^q elements, leaves in registers -------------------
+// T threads per row; thread t owns the PER consecutive 32-element leaves
+// starting at leaf t*PER, i.e. one contiguous run of 32*PER floats, loaded as
+// 16-byte vectors. With every leaf exactly 32 long, the oracle's pairwise tree
+// is: a sequential sum inside each leaf, then a balanced tree over leaves,
+// which is the thread's carry fold followed by the butterfly. No LDS staging.
+template <int T, int PER>
+__global__ __launch_bounds__(T) void softmax_leaf_rows_kernel(const float* __restrict__ src,
+                                                              int64_t in_stride,
+                                                              float* __restrict__ dst,
+                                                              uint32_t rows, int log_mode) {
+    constexpr int E = 32 * PER;
+    constexpr uint32_t n = static_cast<uint32_t>(T) * E;
+    __shared__ float scratch[T / 64];
+    const int t = threadIdx.x;
+    const uint32_t row = blockIdx.x;
+    const float* rs = src + static_cast<int64_t>(row) * in_stride + static_cast<uint32_t>(t) * E;
+    float x[E];
+#pragma unroll
+    for (int i = 0; i < E / 4; ++i) {
+        const f32x4 v = reinterpret_cast<const f32x4*>(rs)[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[4 * i + j] = v[j];
+    }
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < E; ++i) mx = max_ignoring_nan(mx, x[i]);
+    mx = group_max<T>(mx, t, scratch);
+    float leaf[PER];
+#pragma unroll
+    for (int l = 0; l < PER; ++l) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const float sh = x[32 * l + i] - mx;
+            const float ex = expf(sh);
+            a = a + ex;
+            x[32 * l + i] = log_mode ? sh : ex;
+        }
+        leaf[l] = a;
+    }
+    // Balanced fold of this thread's PER leaves (PER is a power of two).
+#pragma unroll
+    for (int w = 1; w < PER; w <<= 1)
+#pragma unroll
+        for (int l = 0; l < PER; l += 2 * w) leaf[l] = leaf[l] + leaf[l + w];
+    float v = wave_sum_butterfly(leaf[0]);
+    const int lane = t & 63, wv = t >> 6;
+    if constexpr (T > 64) {
+        if (lane == 0) scratch[wv] = v;
+        __syncthreads();
+        const float u = lane < T / 64 ? scratch[lane] : 0.0f;
+        v = wave_sum_butterfly(u);
+    }
+    const float denom = v;
+    const float ld = logf(denom);
+    float* ds = dst + static_cast<uint64_t>(row) * n + static_cast<uint32_t>(t) * E;
+#pragma unroll
+    for (int i = 0; i < E / 4; ++i) {
+        f32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = log_mode ? x[4 * i + j] - ld : x[4 * i + j] / denom;
+        reinterpret_cast<f32x4*>(ds)[i] = o;
+    }
+}
+
 // ---- one thread per output: any layout ------------------------------------------------
 // The reduced elements of output o are at base(o) + lin_off(i, reduced). Sum and
 // mean walk the depth-D leaves in order and fold them with a carry stack (a
@@ -247,11 +390,14 @@ __global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* _
 }
 
 // ---- one workgroup per output: contiguous reduced runs ----------------------------------
-// Sum / mean: the run is staged in LDS and summed by group_pairwise_sum.
-template <int T, int E4>
+// Sum / mean: the run is staged in LDS and summed by group_pairwise_sum. With
+// PROD, each element is first multiplied by the matching element of a
+// contiguous vector x, rounded on its own (no FMA): that is the N == 1 matmul,
+// y[o] = sum_k A[o,k] * x[k], in the oracle's order (kernels_matmul.cpp:57-86).
+template <int T, int E4, bool PROD>
 __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_sum_kernel(
     const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int depth, int mean,
-    int vec, uint32_t sstride, float* __restrict__ dst) {
+    int vec, uint32_t sstride, float* __restrict__ dst, const float* __restrict__ xv) {
     constexpr int RPB = Rows<T>::kPerBlock;
     extern __shared__ __attribute__((aligned(16))) float dyn[];
     __shared__ float scratch[RPB][T / 64 > 0 ? T / 64 : 1];
@@ -263,6 +409,12 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_sum_kernel(
     float* stage = dyn + slot * sstride;
     float x[4 * E4];
     load_row<T, E4>(x, rs, n, t, live, vec);
+    if constexpr (PROD) {
+        float w[4 * E4];
+        load_row<T, E4>(w, xv, n, t, live, vec);
+#pragma unroll
+        for (int i = 0; i < 4 * E4; ++i) x[i] = __fmul_rn(x[i], w[i]);
+    }
     if (vec) {
 #pragma unroll
         for (int i = 0; i < E4; ++i) {
@@ -285,6 +437,14 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_sum_kernel(
     float s = group_pairwise_sum<T>(stage, n, depth, t, scratch[slot]);
     if (live && t == 0) dst[o] = mean ? s / static_cast<float>(n) : s;
 }
+
+// Selections (max/min/argmax/argmin) over contiguous runs that fit the row
+// classes: the thread's elements are loaded up front, scanned in index order,
+// then merged across threads with the lowest-index tie-break.
+template <int T, int E4>
+__global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kernel(
+    int op, const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int vec,
+    void* __restrict__ dst);
 
 // Selections: thread-strided scan, then (value, index) merges with the
 // lowest-index tie-break.
@@ -309,6 +469,66 @@ __device__ __forceinline__ Sel sel_merge(int op, Sel a, Sel b) {
     if (b_better) return b;
     if (a_better) return a;
     return a.i < b.i ? a : b;
+}
+
+template <int T, int E4>
+__global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kernel(
+    int op, const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int vec,
+    void* __restrict__ dst) {
+    constexpr int RPB = Rows<T>::kPerBlock;
+    __shared__ float sv[RPB][T / 64 > 0 ? T / 64 : 1];
+    __shared__ uint32_t si[RPB][T / 64 > 0 ? T / 64 : 1];
+    const int slot = threadIdx.x / T;
+    const int t = threadIdx.x % T;
+    const uint32_t o = blockIdx.x * RPB + slot;
+    const bool live = o < n_out;
+    const float* rs = src + (live ? lin_off4(o, kept.ne, kept.nb) : 0);
+    const bool is_max = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_ARGMAX;
+    const bool value_op = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_MIN;
+    float x[4 * E4];
+    load_row<T, E4>(x, rs, n, t, live, vec);
+    // Branch-free scan in increasing index order: the best non-NaN candidate
+    // and, for max/min, the first NaN (which wins the thread's result).
+    constexpr uint32_t kNone = 0xffffffffu;
+    float bv = is_max ? -__builtin_inff() : __builtin_inff(), nv = 0.0f;
+    uint32_t bi = kNone, ni = kNone;
+#pragma unroll
+    for (int i = 0; i < 4 * E4; ++i) {
+        const uint32_t e = elem_of(vec, T, t, i);
+        const float v = x[i];
+        const bool valid = live && e < n;
+        const bool nan = v != v;
+        const bool first_nan = valid && nan && ni == kNone;
+        nv = first_nan ? v : nv;
+        ni = first_nan ? e : ni;
+        const bool better = valid && !nan &&
+                            ((is_max ? v > bv : v < bv) || (value_op && bi == kNone));
+        bv = better ? v : bv;
+        bi = better ? e : bi;
+    }
+    Sel s = (value_op && ni != kNone) ? Sel{nv, ni} : Sel{bv, bi};
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        Sel o2{__shfl_xor(s.v, off, 64), static_cast<uint32_t>(__shfl_xor(static_cast<int>(s.i), off, 64))};
+        s = sel_merge(op, s, o2);
+    }
+    if constexpr (T > 64) {
+        const int lane = t & 63, wave = t >> 6;
+        if (lane == 0) {
+            sv[slot][wave] = s.v;
+            si[slot][wave] = s.i;
+        }
+        __syncthreads();
+        if (t == 0) {
+            for (int w = 1; w < T / 64; ++w) s = sel_merge(op, s, Sel{sv[slot][w], si[slot][w]});
+        }
+    }
+    if (!live || t != 0) return;
+    if (value_op) {
+        static_cast<float*>(dst)[o] = s.i == 0xffffffffu ? (is_max ? -__builtin_inff() : __builtin_inff()) : s.v;
+    } else {
+        static_cast<int64_t*>(dst)[o] = s.i == 0xffffffffu ? 0 : static_cast<int64_t>(s.i);
+    }
 }
 
 template <int T>
@@ -514,15 +734,33 @@ static int allow_lds(const void* fn, size_t bytes) {
 
 template <int T, int E4>
 static int launch_sum_rows(const float* src, const Op4& kept, uint32_t n_out, uint32_t n, int depth,
-                           int mean, int vec, float* out, hipStream_t st) {
+                           int mean, int vec, float* out, hipStream_t st, const float* xv) {
     constexpr int RPB = Rows<T>::kPerBlock;
     const uint32_t ss = stage_stride(n);
     const size_t lds = static_cast<size_t>(RPB) * ss * sizeof(float);
-    auto fn = reduce_rows_sum_kernel<T, E4>;
-    int rc = allow_lds(reinterpret_cast<const void*>(fn), lds);
-    if (rc != VKHIP_OK) return rc;
-    hipLaunchKernelGGL(fn, dim3(ceil_div(n_out, RPB)), dim3(Rows<T>::kThreads), lds, st, src, kept,
-                       n_out, n, depth, mean, vec, ss, out);
+    if (xv) {
+        auto fn = reduce_rows_sum_kernel<T, E4, true>;
+        int rc = allow_lds(reinterpret_cast<const void*>(fn), lds);
+        if (rc != VKHIP_OK) return rc;
+        hipLaunchKernelGGL(fn, dim3(ceil_div(n_out, RPB)), dim3(Rows<T>::kThreads), lds, st, src,
+                           kept, n_out, n, depth, mean, vec, ss, out, xv);
+    } else {
+        auto fn = reduce_rows_sum_kernel<T, E4, false>;
+        int rc = allow_lds(reinterpret_cast<const void*>(fn), lds);
+        if (rc != VKHIP_OK) return rc;
+        hipLaunchKernelGGL(fn, dim3(ceil_div(n_out, RPB)), dim3(Rows<T>::kThreads), lds, st, src,
+                           kept, n_out, n, depth, mean, vec, ss, out, xv);
+    }
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+template <int T, int E4>
+static int launch_select_rows(int op, const float* src, const Op4& kept, uint32_t n_out,
+                              uint32_t n, int vec, void* out, hipStream_t st) {
+    constexpr int RPB = Rows<T>::kPerBlock;
+    hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4>), dim3(ceil_div(n_out, RPB)),
+                       dim3(Rows<T>::kThreads), 0, st, op, src, kept, n_out, n, vec, out);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -580,14 +818,15 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
             const int mean = op == VKHIP_REDUCE_MEAN;
             float* out = static_cast<float*>(dst);
             const RowClass rc = row_class(n_red);
-            VKHIP_ROW_CLASSES(launch_sum_rows, src, kept, n_out, n_red, depth, mean, vec, out, st)
+            VKHIP_ROW_CLASSES(launch_sum_rows, src, kept, n_out, n_red, depth, mean, vec, out, st,
+                              nullptr)
         }
-        if (n_red <= 2048)
-            hipLaunchKernelGGL((reduce_rows_select_kernel<64>), dim3(ceil_div(n_out, 4)), dim3(256),
-                               0, st, op, src, kept, n_out, n_red, vec, dst);
-        else
-            hipLaunchKernelGGL((reduce_rows_select_kernel<256>), dim3(n_out), dim3(256), 0, st, op,
-                               src, kept, n_out, n_red, vec, dst);
+        if (n_red <= kRowsMax) {
+            const RowClass rc = row_class(n_red);
+            VKHIP_ROW_CLASSES(launch_select_rows, op, src, kept, n_out, n_red, vec, dst, st)
+        }
+        hipLaunchKernelGGL((reduce_rows_select_kernel<256>), dim3(n_out), dim3(256), 0, st, op,
+                           src, kept, n_out, n_red, vec, dst);
         VKHIP_LAUNCH_CHECK();
         return VKHIP_OK;
     }
@@ -688,6 +927,44 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
         const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
                         (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (n % 4 == 0) &&
                         (row_stride % 4 == 0);
+        // Long rows of exactly 32 * 2^q floats: leaves straight from registers.
+        if (vec && (n == 32768 || n == 16384 || n == 8192 || n == 4096)) {
+            if (n == 32768)
+                hipLaunchKernelGGL((softmax_leaf_rows_kernel<1024, 1>), dim3(rows), dim3(1024), 0,
+                                   st, src, row_stride, dst, rows, log_mode);
+            else if (n == 16384)
+                hipLaunchKernelGGL((softmax_leaf_rows_kernel<512, 1>), dim3(rows), dim3(512), 0,
+                                   st, src, row_stride, dst, rows, log_mode);
+            else if (n == 8192)
+                hipLaunchKernelGGL((softmax_leaf_rows_kernel<256, 1>), dim3(rows), dim3(256), 0,
+                                   st, src, row_stride, dst, rows, log_mode);
+            else
+                hipLaunchKernelGGL((softmax_leaf_rows_kernel<128, 1>), dim3(rows), dim3(128), 0,
+                                   st, src, row_stride, dst, rows, log_mode);
+            VKHIP_LAUNCH_CHECK();
+            return VKHIP_OK;
+        }
+        // Rows up to 2048: a persistent wave per row with next-row prefetch.
+        if (n <= 2048) {
+            const uint32_t ss = stage_stride(n);
+            const size_t lds = 4 * static_cast<size_t>(ss) * sizeof(float);
+            const uint32_t cus = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
+            // Two resident workgroups per CU, so a wave walks several rows and
+            // its prefetch has something to overlap with.
+            const uint32_t want = ceil_div(rows, 4);
+            const uint32_t blocks = want < cus * 2 ? want : cus * 2;
+            if (n <= 256)
+                hipLaunchKernelGGL((softmax_wave_rows_kernel<1>), dim3(blocks), dim3(256), lds, st,
+                                   src, row_stride, dst, rows, n, depth, log_mode, vec, ss);
+            else if (n <= 1024)
+                hipLaunchKernelGGL((softmax_wave_rows_kernel<4>), dim3(blocks), dim3(256), lds, st,
+                                   src, row_stride, dst, rows, n, depth, log_mode, vec, ss);
+            else
+                hipLaunchKernelGGL((softmax_wave_rows_kernel<8>), dim3(blocks), dim3(256), lds, st,
+                                   src, row_stride, dst, rows, n, depth, log_mode, vec, ss);
+            VKHIP_LAUNCH_CHECK();
+            return VKHIP_OK;
+        }
         const RowClass rc = row_class(n);
         VKHIP_ROW_CLASSES(launch_softmax_rows, src, row_stride, dst, rows, n, depth, log_mode, vec, st)
     }
@@ -712,6 +989,26 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
                        rd, okept, ord, n_out64, n, depth, log_mode, dst);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
+}
+
+// y[row] = sum_k A[row, k] * x[k] for a row-major A with unit inner stride and
+// a contiguous x: the staged pairwise row sum of rounded products.
+int launch_gemv_rows(const float* a, int64_t lda, const float* x, float* y, uint32_t m,
+                     uint32_t k) {
+    if (m == 0) return VKHIP_OK;
+    Op4 kept;
+    for (int i = 0; i < 4; ++i) {
+        kept.ne[i] = 1;
+        kept.nb[i] = 0;
+    }
+    kept.ne[3] = m;
+    kept.nb[3] = lda;
+    const int vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) &&
+                    (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (k % 4 == 0) && (lda % 4 == 0);
+    const int depth = pairwise_depth(k);
+    const RowClass rc = row_class(k);
+    hipStream_t st = ctx().stream;
+    VKHIP_ROW_CLASSES(launch_sum_rows, a, kept, m, k, depth, 0, vec, y, st, x)
 }
 
 }  // namespace vkhip

@@ -501,6 +501,10 @@ extern "C" int vkhip_event_elapsed(void* start, void* end, float* out_ms) {
 
 // ---- host-side planning helpers (no device needed) -----------------------------------
 
+extern "C" uint32_t vkhip_fast_divide(uint32_t n, uint32_t d) {
+    return d == 0 ? 0xffffffffu : vkhip::FastDiv(d).div(n);
+}
+
 extern "C" int vkhip_pairwise_leaf(uint32_t n, uint32_t leaf, uint32_t* out_depth,
                                    uint32_t* out_begin, uint32_t* out_end) {
     const int depth = vkhip::pairwise_depth(n);
