@@ -325,6 +325,40 @@ def test_max_min_argmax_exact(hip, shape, axis):
     np.testing.assert_array_equal(ops.argmin(d, axis).numpy(), O.argmin(x, axis))
 
 
+def special_rows(n: int, seed: int) -> np.ndarray:
+    """48 rows of width n: planted NaNs, signed-zero ties, infinities,
+    all -inf and all-NaN rows - the cases where selection order shows."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((48, n)).astype(np.float32)
+    for r in range(8):
+        x[r, rng.integers(0, n, 1 + r % 3)] = np.nan
+    x[8:16] = np.where(rng.integers(0, 2, (8, n)) == 1, np.float32(0.0), np.float32(-0.0))
+    x[16:24] = -np.abs(x[16:24])
+    x[16:24, rng.integers(0, n, 3)] = np.float32(-0.0)
+    x[16:24, rng.integers(0, n, 3)] = np.float32(0.0)
+    x[24:28] = -np.inf
+    x[28:32] = np.nan
+    x[32:40, rng.integers(0, n, 4)] = np.inf
+    x[32:40, rng.integers(0, n, 2)] = -np.inf
+    x[36:40, n - 1] = np.nan
+    x[40:48, rng.integers(0, n, 5)] = -np.inf
+    return x
+
+
+@pytest.mark.parametrize("n", [1, 10, 80, 300, 1000, 2500, 4096, 9000, 40000])
+def test_select_special_values_exact(hip, n):
+    """max/min (first NaN, else first extreme, which fixes a zero's sign) and
+    argmax/argmin (NaN skipped, first strict improvement) across every row
+    class the device dispatches, along the last axis and along axis 0."""
+    x = special_rows(n, SEED + n)
+    for arr, axis in ((x, 1), (np.ascontiguousarray(x.T), 0)):
+        d = dev(arr)
+        assert ops.amax(d, [axis]).numpy().tobytes() == O.amax(arr, [axis]).tobytes(), axis
+        assert ops.amin(d, [axis]).numpy().tobytes() == O.amin(arr, [axis]).tobytes(), axis
+        np.testing.assert_array_equal(ops.argmax(d, axis).numpy(), O.argmax(arr, axis))
+        np.testing.assert_array_equal(ops.argmin(d, axis).numpy(), O.argmin(arr, axis))
+
+
 def test_reduce_known_answers_and_nan(hip):
     a = np.array([[1, 5, 5], [4, 2, 4]], np.float32)
     np.testing.assert_array_equal(ops.argmax(dev(a), 1).numpy(), [1, 0])
@@ -358,6 +392,30 @@ def test_max_pool2d_forward_backward_bit_exact(hip, shape, kernel, stride, pad):
     g = np.random.default_rng(SEED + 1).uniform(-1, 1, y.shape).astype(np.float32)
     gx = ops.max_pool2d_backward(dev(g), dev(x), kernel, stride, pad).numpy()
     assert gx.tobytes() == O.max_pool2d_backward(g, x, kernel, stride, pad).tobytes()
+
+
+@pytest.mark.parametrize("shape", [(3, 5, 8, 12), (2, 4, 16, 4), (1, 2, 6, 8), (2, 3, 8, 10)])
+def test_max_pool2d_ties_nan_and_signed_zero(hip, shape):
+    """2x2/stride-2 windows (the tiled fast path where W % 4 == 0, the general
+    kernel otherwise): values from {-1, 0, 1} so most windows tie, planted
+    NaNs that the window scan skips, -0 gradients, and for the backward some
+    windows with no maximum at all (all -inf / NaN), which route nothing."""
+    rng = np.random.default_rng(SEED + sum(shape))
+    x = rng.integers(-1, 2, shape).astype(np.float32)
+    plant = rng.random(shape) < 0.05
+    plant[..., ::2, ::2] = False  # every window keeps a number for the forward
+    x[plant] = np.nan
+    x[..., 0:2, 0:2] = np.where(rng.random((2, 2)) < 0.5, np.float32(0.0), np.float32(-0.0))
+    d = dev(x)
+    y = ops.max_pool2d(d, (2, 2), (2, 2)).numpy()
+    assert y.tobytes() == O.max_pool2d(x, (2, 2), (2, 2), (0, 0)).tobytes()
+    g = rng.uniform(-1, 1, y.shape).astype(np.float32)
+    g[rng.random(g.shape) < 0.2] = np.float32(-0.0)
+    xb = x.copy()
+    xb[0, 0, 2:4, 2:4] = -np.inf
+    xb[-1, -1, -2:, -2:] = np.nan
+    gx = ops.max_pool2d_backward(dev(g), dev(xb), (2, 2), (2, 2)).numpy()
+    assert gx.tobytes() == O.max_pool2d_backward(g, xb, (2, 2), (2, 2), (0, 0)).tobytes()
 
 
 def test_max_pool2d_tie(hip):

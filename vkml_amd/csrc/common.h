@@ -240,10 +240,42 @@ __device__ __forceinline__ float staged_subtree_sum(const float* st, uint32_t n,
     return v;
 }
 
+// ---- butterflies across a wave of 64 ----------------------------------------
+// Step OFF of a butterfly pairs lane i with lane i ^ OFF. Once the steps
+// below OFF have run with a symmetric merge (merge(a, b) == merge(b, a)),
+// every aligned group of OFF lanes holds one value, and any exchange that
+// lands in the partner group gives the same result. That lets the steps use
+// register-speed DPP moves instead of LDS-routed shuffles: xor 1 and xor 2
+// are DPP quad permutations, 4 and 8 the half-row and row mirrors (lane
+// 7 - i, 15 - i), 16 a ds_swizzle xor within 32 lanes, and the last step
+// combines lanes 0 and 32 read into scalars.
+template <int OFF>
+__device__ __forceinline__ int wave_partner(int v) {
+    if constexpr (OFF == 1) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (OFF == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (OFF == 4) return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false);
+    else if constexpr (OFF == 8) return __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);
+    else if constexpr (OFF == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+    else return __shfl_xor(v, OFF, 64);
+}
+
+template <int OFF>
+__device__ __forceinline__ float wave_partner(float v) {
+    return __builtin_bit_cast(float, wave_partner<OFF>(__builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Balanced pairwise sum of the 64 lanes' values (lane order), in every lane.
 __device__ __forceinline__ float wave_sum_butterfly(float v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
+    v = v + wave_partner<1>(v);
+    v = v + wave_partner<2>(v);
+    v = v + wave_partner<4>(v);
+    v = v + wave_partner<8>(v);
+    v = v + wave_partner<16>(v);
+    return lane_value(v, 0) + lane_value(v, 32);
 }
 
 }  // namespace vkhip

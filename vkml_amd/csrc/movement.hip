@@ -399,6 +399,89 @@ __global__ __launch_bounds__(256) void max_pool2d_backward_kernel(
     dst[static_cast<uint64_t>(plane) * hw + idx] = acc;
 }
 
+// ---- 2x2 windows tiling the plane exactly (stride 2, no padding or dilation) ----
+// Each thread owns two horizontally adjacent windows: two 16-byte loads (rows
+// 2*oh and 2*oh + 1, columns 4j..4j+3) cover both. Output row r of the flat
+// [planes*out_h, out_w] output reads input rows 2r and 2r + 1 of the flat
+// [planes*H, W] input. The window scan is window_argmax's: strict '>' from
+// -inf in the order (0,0), (0,1), (1,0), (1,1); no winner (all -inf or NaN)
+// gives -1, and the forward then takes the first position, as the general
+// kernel does.
+__device__ __forceinline__ int32_t argmax4(float a, float b, float c, float d) {
+    float best = -__builtin_inff();
+    int32_t off = -1;
+    if (a > best) { best = a; off = 0; }
+    if (b > best) { best = b; off = 1; }
+    if (c > best) { best = c; off = 2; }
+    if (d > best) { best = d; off = 3; }
+    return off;
+}
+
+__device__ __forceinline__ float pick4(int32_t off, float a, float b, float c, float d) {
+    return off == 1 ? b : off == 2 ? c : off == 3 ? d : a;
+}
+
+__global__ __launch_bounds__(256) void max_pool2x2_kernel(const float* __restrict__ src,
+                                                         float* __restrict__ dst, uint32_t W,
+                                                         FastDiv pairs_per_row, uint32_t total) {
+    const uint32_t q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= total) return;
+    const uint32_t r = pairs_per_row.div(q);
+    const uint32_t j = q - r * pairs_per_row.d;
+    const float* r0 = src + static_cast<uint64_t>(2 * r) * W + 4 * j;
+    const f32x4_t t = *reinterpret_cast<const f32x4_t*>(r0);
+    const f32x4_t u = *reinterpret_cast<const f32x4_t*>(r0 + W);
+    float2 o;
+    o.x = pick4(argmax4(t[0], t[1], u[0], u[1]), t[0], t[1], u[0], u[1]);
+    o.y = pick4(argmax4(t[2], t[3], u[2], u[3]), t[2], t[3], u[2], u[3]);
+    reinterpret_cast<float2*>(dst)[q] = o;
+}
+
+// Backward of the same tiling: every input position lies in exactly one
+// window, so the pull of the general kernel reduces to 0 + g at the window's
+// first maximum and +0 elsewhere (0 + g also turns a -0 gradient into +0, as
+// the pull's accumulator does).
+__global__ __launch_bounds__(256) void max_pool2x2_backward_kernel(
+    const float* __restrict__ grad, const float* __restrict__ src, float* __restrict__ dst,
+    uint32_t W, FastDiv pairs_per_row, uint32_t total) {
+    const uint32_t q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= total) return;
+    const uint32_t r = pairs_per_row.div(q);
+    const uint32_t j = q - r * pairs_per_row.d;
+    const uint64_t base = static_cast<uint64_t>(2 * r) * W + 4 * j;
+    const f32x4_t t = *reinterpret_cast<const f32x4_t*>(src + base);
+    const f32x4_t u = *reinterpret_cast<const f32x4_t*>(src + base + W);
+    const float2 g = reinterpret_cast<const float2*>(grad)[q];
+    const int32_t a0 = argmax4(t[0], t[1], u[0], u[1]);
+    const int32_t a1 = argmax4(t[2], t[3], u[2], u[3]);
+    const float g0 = 0.0f + g.x, g1 = 0.0f + g.y;
+    f32x4_t top, bot;
+    top[0] = a0 == 0 ? g0 : 0.0f;
+    top[1] = a0 == 1 ? g0 : 0.0f;
+    bot[0] = a0 == 2 ? g0 : 0.0f;
+    bot[1] = a0 == 3 ? g0 : 0.0f;
+    top[2] = a1 == 0 ? g1 : 0.0f;
+    top[3] = a1 == 1 ? g1 : 0.0f;
+    bot[2] = a1 == 2 ? g1 : 0.0f;
+    bot[3] = a1 == 3 ? g1 : 0.0f;
+    *reinterpret_cast<f32x4_t*>(dst + base) = top;
+    *reinterpret_cast<f32x4_t*>(dst + base + W) = bot;
+}
+
+// The 2x2 fast path applies to contiguous planes whose width is a multiple of
+// 4, 16-byte aligned, pooled by 2x2 windows at stride 2 with no padding or
+// dilation over an even height.
+static bool pool2x2_tiles(const Geo& g, const vkhip_operand& sd, const void* a, const void* b,
+                          const void* c) {
+    const bool geo = g.kh == 2 && g.kw == 2 && g.sh == 2 && g.sw == 2 && g.ph == 0 && g.pw == 0 &&
+                     g.dh == 1 && g.dw == 1 && g.H % 2 == 0 && g.W % 4 == 0;
+    const bool contiguous = sd.nb[3] == 1 && sd.nb[2] == g.W &&
+                            sd.nb[1] == static_cast<int64_t>(g.H) * g.W &&
+                            (sd.ne[0] == 1 || sd.nb[0] == static_cast<int64_t>(sd.ne[1]) * g.H * g.W);
+    const auto al = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    return geo && contiguous && al(a) && al(b) && al(c);
+}
+
 // True when every pooling window has at least one position inside the image
 // (the oracle asserts this per window, kernels_movement.cpp:604-605).
 static bool windows_reach_image(const Geo& g) {
@@ -426,6 +509,9 @@ int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uin
     Geo g;
     int st = make_geo(p, g);
     if (st != VKHIP_OK) return st;
+    if (static_cast<int64_t>(sd.ne[2]) != p.image_h || static_cast<int64_t>(sd.ne[3]) != p.image_w)
+        return fail(VKHIP_ERR_INVALID, "max_pool2d: input is %ux%u but the geometry says %dx%d",
+                    sd.ne[2], sd.ne[3], p.image_h, p.image_w);
     if (static_cast<uint32_t>(g.out_h) != out_h || static_cast<uint32_t>(g.out_w) != out_w)
         return fail(VKHIP_ERR_INVALID, "max_pool2d: output %ux%u disagrees with geometry %dx%d",
                     out_h, out_w, g.out_h, g.out_w);
@@ -434,6 +520,16 @@ int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uin
     const uint64_t planes = static_cast<uint64_t>(sd.ne[0]) * sd.ne[1];
     const uint32_t ohw = out_h * out_w;
     if (planes == 0 || ohw == 0) return VKHIP_OK;
+    if (pool2x2_tiles(g, sd, src, dst, nullptr)) {
+        const uint64_t total = planes * ohw / 2;
+        if (total <= 0xffffffffull) {
+            hipLaunchKernelGGL(max_pool2x2_kernel, dim3(ceil_div(static_cast<uint32_t>(total), 256)),
+                               dim3(256), 0, ctx().stream, src, dst, static_cast<uint32_t>(g.W),
+                               FastDiv(out_w / 2), static_cast<uint32_t>(total));
+            VKHIP_LAUNCH_CHECK();
+            return VKHIP_OK;
+        }
+    }
     const uint32_t bpp = ceil_div(ohw, 256);
     hipLaunchKernelGGL(max_pool2d_kernel, dim3(static_cast<uint32_t>(planes * bpp)), dim3(256), 0,
                        ctx().stream, src, to_op4(sd), dst, g, sd.ne[1], bpp);
@@ -446,12 +542,26 @@ int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_
     Geo g;
     int st = make_geo(p, g);
     if (st != VKHIP_OK) return st;
+    if (static_cast<int64_t>(sd.ne[2]) != p.image_h || static_cast<int64_t>(sd.ne[3]) != p.image_w)
+        return fail(VKHIP_ERR_INVALID, "max_pool2d: input is %ux%u but the geometry says %dx%d",
+                    sd.ne[2], sd.ne[3], p.image_h, p.image_w);
     if (static_cast<uint32_t>(g.out_h) != out_h || static_cast<uint32_t>(g.out_w) != out_w)
         return fail(VKHIP_ERR_INVALID, "max_pool2d_backward: grad %ux%u disagrees with geometry %dx%d",
                     out_h, out_w, g.out_h, g.out_w);
     const uint64_t planes = static_cast<uint64_t>(sd.ne[0]) * sd.ne[1];
     const uint32_t hw = static_cast<uint32_t>(g.H) * g.W;
     if (planes == 0 || hw == 0) return VKHIP_OK;
+    if (pool2x2_tiles(g, sd, src, dst, grad)) {
+        const uint64_t total = planes * out_h * out_w / 2;
+        if (total <= 0xffffffffull) {
+            hipLaunchKernelGGL(max_pool2x2_backward_kernel,
+                               dim3(ceil_div(static_cast<uint32_t>(total), 256)), dim3(256), 0,
+                               ctx().stream, grad, src, dst, static_cast<uint32_t>(g.W),
+                               FastDiv(out_w / 2), static_cast<uint32_t>(total));
+            VKHIP_LAUNCH_CHECK();
+            return VKHIP_OK;
+        }
+    }
     const uint32_t bpp = ceil_div(hw, 256);
     hipLaunchKernelGGL(max_pool2d_backward_kernel, dim3(static_cast<uint32_t>(planes * bpp)),
                        dim3(256), 0, ctx().stream, grad, src, to_op4(sd), dst, g, sd.ne[1], bpp);

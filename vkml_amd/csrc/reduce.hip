@@ -24,10 +24,36 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float max_ignoring_nan(float a, float b) { return (a < b) ? b : a; }
 
-__device__ __forceinline__ float wave_max(float v) {
+// Peak of a register-held row slice for softmax, as a balanced tree of fmaxf.
+// fmaxf ignores a NaN operand and may return either zero when both signs
+// meet; neither shows in softmax outputs, so this agrees with the oracle's
+// sequential std::max: a row holding a NaN is NaN throughout whatever its
+// peak; x - peak depends on the sign of a zero peak only for a zero x, whose
+// exp is 1 either way and whose log-softmax value (x - peak) - log(denom) is
+// -log(denom) unless denom == 1, which leaves a single zero in the row, and
+// that zero is the peak under either rule. Slots with keep[i] false count as
+// -inf.
+template <int E>
+__device__ __forceinline__ float tree_peak(const float (&x)[E], const bool (&keep)[E]) {
+    float m[E];
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v = max_ignoring_nan(v, __shfl_xor(v, off, 64));
-    return v;
+    for (int i = 0; i < E; ++i) m[i] = keep[i] ? x[i] : -__builtin_inff();
+#pragma unroll
+    for (int w = 1; w < E; w <<= 1)
+#pragma unroll
+        for (int i = 0; i + w < E; i += 2 * w) m[i] = __builtin_fmaxf(m[i], m[i + w]);
+    return m[0];
+}
+
+// Wave-wide fmaxf (symmetric, NaN-ignoring); used for softmax peaks only,
+// where the sign of a zero peak is not observable.
+__device__ __forceinline__ float wave_max(float v) {
+    v = __builtin_fmaxf(v, wave_partner<1>(v));
+    v = __builtin_fmaxf(v, wave_partner<2>(v));
+    v = __builtin_fmaxf(v, wave_partner<4>(v));
+    v = __builtin_fmaxf(v, wave_partner<8>(v));
+    v = __builtin_fmaxf(v, wave_partner<16>(v));
+    return __builtin_fmaxf(lane_value(v, 0), lane_value(v, 32));
 }
 
 // Pairwise sum of the n values staged in `st` by a group of T threads (t =
@@ -102,14 +128,26 @@ __device__ __forceinline__ uint32_t elem_of(int vec, int T, int t, int i) {
 }
 
 // ---- softmax over contiguous rows ------------------------------------------------
+// Division by the row's denominator d with its reciprocal r = 1/d (correctly
+// rounded, computed once per row): q0 = x*r, then one fused correction
+// q = q0 + (x - q0*d)*r. For a normal quotient this is the correctly rounded
+// x/d (Markstein's theorem; Muller et al., Handbook of Floating-Point
+// Arithmetic, 2nd ed., sec. 4.7), so it agrees with the oracle's expf(.)/denom;
+// a subnormal quotient may differ from it by one subnormal unit.
+__device__ __forceinline__ float div_by(float x, float d, float r) {
+    const float q0 = x * r;
+    const float e = __builtin_fmaf(-q0, d, x);
+    return __builtin_fmaf(e, r, q0);
+}
+
 // T threads per row (64: four rows per 256-thread block), rows of n <= 4*E4*T
 // contiguous floats at src + row*in_stride; dst rows contiguous. The row is read
 // once into registers; exp(x - peak) is computed once, staged in LDS for the
 // pairwise denominator and kept in registers for the output.
-template <int T, int E4>
+template <int T, int E4, bool LOG>
 __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
     const float* __restrict__ src, int64_t in_stride, float* __restrict__ dst, uint32_t rows,
-    uint32_t n, int depth, int log_mode, int vec, uint32_t sstride) {
+    uint32_t n, int depth, int vec, uint32_t sstride) {
     constexpr int RPB = Rows<T>::kPerBlock;
     constexpr int E = 4 * E4;
     extern __shared__ __attribute__((aligned(16))) float dyn[];
@@ -124,10 +162,10 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
 
     float x[E];
     load_row<T, E4>(x, rs, n, t, live, vec);
-    float mx = -__builtin_inff();
+    bool keep[E];
 #pragma unroll
-    for (int i = 0; i < E; ++i)
-        if (live && elem_of(vec, T, t, i) < n) mx = max_ignoring_nan(mx, x[i]);
+    for (int i = 0; i < E; ++i) keep[i] = live && elem_of(vec, T, t, i) < n;
+    float mx = tree_peak<E>(x, keep);
     mx = group_max<T>(mx, t, scratch[slot]);
 
 #pragma unroll
@@ -136,12 +174,13 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
         const float sh = x[i] - mx;
         const float ex = expf(sh);
         if (live && e < n) stage[stage_index(e)] = ex;
-        x[i] = log_mode ? sh : ex;
+        x[i] = LOG ? sh : ex;
     }
     __syncthreads();
     const float denom = group_pairwise_sum<T>(stage, n, depth, t, scratch[slot]);
     if (!live) return;
     const float ld = logf(denom);
+        const float rinv = 1.0f / denom;
     float* ds = dst + static_cast<uint64_t>(row) * n;
     if (vec) {
 #pragma unroll
@@ -150,7 +189,7 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
             if (e0 < n) {
                 f32x4 o;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) o[j] = log_mode ? x[4 * i + j] - ld : x[4 * i + j] / denom;
+                for (int j = 0; j < 4; ++j) o[j] = LOG ? x[4 * i + j] - ld : div_by(x[4 * i + j], denom, rinv);
                 *reinterpret_cast<f32x4*>(ds + e0) = o;
             }
         }
@@ -158,7 +197,7 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
 #pragma unroll
         for (int i = 0; i < E; ++i) {
             const uint32_t e = t + T * i;
-            if (e < n) ds[e] = log_mode ? x[i] - ld : x[i] / denom;
+            if (e < n) ds[e] = LOG ? x[i] - ld : div_by(x[i], denom, rinv);
         }
     }
 }
@@ -177,10 +216,11 @@ __device__ __forceinline__ void wave_lds_fence() {
     asm volatile("" ::: "memory");
 }
 
-template <int E4>
+template <int E4, bool LOG, bool VEC>
 __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
     const float* __restrict__ src, int64_t in_stride, float* __restrict__ dst, uint32_t rows,
-    uint32_t n, int depth, int log_mode, int vec, uint32_t sstride) {
+    uint32_t n, int depth, uint32_t sstride) {
+    constexpr int vec = VEC ? 1 : 0;
     constexpr int E = 4 * E4;
     extern __shared__ __attribute__((aligned(16))) float dyn[];
     const int wave = threadIdx.x >> 6;
@@ -198,10 +238,10 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
         for (int i = 0; i < E; ++i) x[i] = xn[i];
         const uint32_t next = row + stride;
         if (next < rows) load_row<64, E4>(xn, src + static_cast<int64_t>(next) * in_stride, n, t, true, vec);
-        float mx = -__builtin_inff();
+        bool keep[E];
 #pragma unroll
-        for (int i = 0; i < E; ++i)
-            if (elem_of(vec, 64, t, i) < n) mx = max_ignoring_nan(mx, x[i]);
+        for (int i = 0; i < E; ++i) keep[i] = elem_of(vec, 64, t, i) < n;
+        float mx = tree_peak<E>(x, keep);
         mx = wave_max(mx);
 #pragma unroll
         for (int i = 0; i < E; ++i) {
@@ -209,7 +249,7 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
             const float sh = x[i] - mx;
             const float ex = expf(sh);
             if (e < n) stage[stage_index(e)] = ex;
-            x[i] = log_mode ? sh : ex;
+            x[i] = LOG ? sh : ex;
         }
         wave_lds_fence();
         const uint32_t per = leaves > 64 ? leaves / 64 : 1u;
@@ -218,6 +258,7 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
         const float denom = wave_sum_butterfly(v);
         wave_lds_fence();  // every lane's stage reads precede the next row's writes
         const float ld = logf(denom);
+        const float rinv = 1.0f / denom;
         float* ds = dst + static_cast<uint64_t>(row) * n;
         if (vec) {
 #pragma unroll
@@ -226,7 +267,7 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
                 if (e0 < n) {
                     f32x4 o;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) o[j] = log_mode ? x[4 * i + j] - ld : x[4 * i + j] / denom;
+                    for (int j = 0; j < 4; ++j) o[j] = LOG ? x[4 * i + j] - ld : div_by(x[4 * i + j], denom, rinv);
                     *reinterpret_cast<f32x4*>(ds + e0) = o;
                 }
             }
@@ -234,7 +275,7 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
 #pragma unroll
             for (int i = 0; i < E; ++i) {
                 const uint32_t e = t + 64 * i;
-                if (e < n) ds[e] = log_mode ? x[i] - ld : x[i] / denom;
+                if (e < n) ds[e] = LOG ? x[i] - ld : div_by(x[i], denom, rinv);
             }
         }
     }
@@ -246,11 +287,11 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
 // 16-byte vectors. With every leaf exactly 32 long, the oracle's pairwise tree
 // is: a sequential sum inside each leaf, then a balanced tree over leaves,
 // which is the thread's carry fold followed by the butterfly. No LDS staging.
-template <int T, int PER>
+template <int T, int PER, bool LOG>
 __global__ __launch_bounds__(T) void softmax_leaf_rows_kernel(const float* __restrict__ src,
                                                               int64_t in_stride,
                                                               float* __restrict__ dst,
-                                                              uint32_t rows, int log_mode) {
+                                                              uint32_t rows) {
     constexpr int E = 32 * PER;
     constexpr uint32_t n = static_cast<uint32_t>(T) * E;
     __shared__ float scratch[T / 64];
@@ -264,9 +305,10 @@ __global__ __launch_bounds__(T) void softmax_leaf_rows_kernel(const float* __res
 #pragma unroll
         for (int j = 0; j < 4; ++j) x[4 * i + j] = v[j];
     }
-    float mx = -__builtin_inff();
+    bool keep[E];
 #pragma unroll
-    for (int i = 0; i < E; ++i) mx = max_ignoring_nan(mx, x[i]);
+    for (int i = 0; i < E; ++i) keep[i] = true;
+    float mx = tree_peak<E>(x, keep);
     mx = group_max<T>(mx, t, scratch);
     float leaf[PER];
 #pragma unroll
@@ -277,7 +319,7 @@ __global__ __launch_bounds__(T) void softmax_leaf_rows_kernel(const float* __res
             const float sh = x[32 * l + i] - mx;
             const float ex = expf(sh);
             a = a + ex;
-            x[32 * l + i] = log_mode ? sh : ex;
+            x[32 * l + i] = LOG ? sh : ex;
         }
         leaf[l] = a;
     }
@@ -296,12 +338,13 @@ __global__ __launch_bounds__(T) void softmax_leaf_rows_kernel(const float* __res
     }
     const float denom = v;
     const float ld = logf(denom);
+        const float rinv = 1.0f / denom;
     float* ds = dst + static_cast<uint64_t>(row) * n + static_cast<uint32_t>(t) * E;
 #pragma unroll
     for (int i = 0; i < E / 4; ++i) {
         f32x4 o;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = log_mode ? x[4 * i + j] - ld : x[4 * i + j] / denom;
+        for (int j = 0; j < 4; ++j) o[j] = LOG ? x[4 * i + j] - ld : div_by(x[4 * i + j], denom, rinv);
         reinterpret_cast<f32x4*>(ds)[i] = o;
     }
 }
@@ -441,10 +484,6 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_sum_kernel(
 // Selections (max/min/argmax/argmin) over contiguous runs that fit the row
 // classes: the thread's elements are loaded up front, scanned in index order,
 // then merged across threads with the lowest-index tie-break.
-template <int T, int E4>
-__global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kernel(
-    int op, const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int vec,
-    void* __restrict__ dst);
 
 // Selections: thread-strided scan, then (value, index) merges with the
 // lowest-index tie-break.
@@ -471,11 +510,41 @@ __device__ __forceinline__ Sel sel_merge(int op, Sel a, Sel b) {
     return a.i < b.i ? a : b;
 }
 
-template <int T, int E4>
+// The same merge with the operation fixed at compile time, so that a lane's
+// merge is a handful of compares and selects rather than a branch tree.
+template <int OP>
+__device__ __forceinline__ Sel sel_merge_t(Sel a, Sel b) {
+    constexpr bool is_max = OP == VKHIP_REDUCE_MAX || OP == VKHIP_REDUCE_ARGMAX;
+    constexpr bool value_op = OP == VKHIP_REDUCE_MAX || OP == VKHIP_REDUCE_MIN;
+    const bool a_none = a.i == 0xffffffffu, b_none = b.i == 0xffffffffu;
+    const bool lower = b.i < a.i;  // "none" is the largest index
+    bool take_b;
+    if constexpr (value_op) {
+        const bool an = a.v != a.v, bn = b.v != b.v;
+        const bool b_wins = is_max ? b.v > a.v : b.v < a.v;
+        const bool tie = !(a.v > b.v) && !(a.v < b.v);
+        take_b = (an || bn) ? (bn && (!an || lower)) : (b_wins || (tie && lower));
+    } else {
+        const bool b_wins = is_max ? b.v > a.v : b.v < a.v;
+        const bool tie = a.v == b.v;
+        take_b = b_wins || (tie && lower);
+    }
+    take_b = !b_none && (a_none || take_b);
+    return take_b ? b : a;
+}
+
+// Selections over rows held in registers: max/min return the first NaN of the
+// row if there is one, else the first of the extreme values (which fixes the
+// sign of a zero maximum); argmax/argmin skip NaN and return the lowest index
+// of a strict improvement, 0 when nothing improves on the initial +-inf.
+template <int T, int E4, int OP>
 __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kernel(
-    int op, const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int vec,
+    const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int vec,
     void* __restrict__ dst) {
     constexpr int RPB = Rows<T>::kPerBlock;
+    constexpr bool is_max = OP == VKHIP_REDUCE_MAX || OP == VKHIP_REDUCE_ARGMAX;
+    constexpr bool value_op = OP == VKHIP_REDUCE_MAX || OP == VKHIP_REDUCE_MIN;
+    constexpr uint32_t kNone = 0xffffffffu;
     __shared__ float sv[RPB][T / 64 > 0 ? T / 64 : 1];
     __shared__ uint32_t si[RPB][T / 64 > 0 ? T / 64 : 1];
     const int slot = threadIdx.x / T;
@@ -483,35 +552,37 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kern
     const uint32_t o = blockIdx.x * RPB + slot;
     const bool live = o < n_out;
     const float* rs = src + (live ? lin_off4(o, kept.ne, kept.nb) : 0);
-    const bool is_max = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_ARGMAX;
-    const bool value_op = op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_MIN;
     float x[4 * E4];
     load_row<T, E4>(x, rs, n, t, live, vec);
-    // Branch-free scan in increasing index order: the best non-NaN candidate
-    // and, for max/min, the first NaN (which wins the thread's result).
-    constexpr uint32_t kNone = 0xffffffffu;
-    float bv = is_max ? -__builtin_inff() : __builtin_inff(), nv = 0.0f;
-    uint32_t bi = kNone, ni = kNone;
+    // One candidate per thread, scanned in increasing index order. For value
+    // ops a NaN outranks every number and the first one stays; the first
+    // element is taken even when it equals the initial +-inf.
+    float bv = is_max ? -__builtin_inff() : __builtin_inff();
+    uint32_t bi = kNone;
 #pragma unroll
     for (int i = 0; i < 4 * E4; ++i) {
         const uint32_t e = elem_of(vec, T, t, i);
         const float v = x[i];
         const bool valid = live && e < n;
-        const bool nan = v != v;
-        const bool first_nan = valid && nan && ni == kNone;
-        nv = first_nan ? v : nv;
-        ni = first_nan ? e : ni;
-        const bool better = valid && !nan &&
-                            ((is_max ? v > bv : v < bv) || (value_op && bi == kNone));
+        const bool improves = is_max ? v > bv : v < bv;
+        bool better;
+        if constexpr (value_op) {
+            const bool b_nan = bv != bv;
+            better = valid && (bi == kNone || (!b_nan && (v != v || improves)));
+        } else {
+            better = valid && improves;
+        }
         bv = better ? v : bv;
         bi = better ? e : bi;
     }
-    Sel s = (value_op && ni != kNone) ? Sel{nv, ni} : Sel{bv, bi};
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        Sel o2{__shfl_xor(s.v, off, 64), static_cast<uint32_t>(__shfl_xor(static_cast<int>(s.i), off, 64))};
-        s = sel_merge(op, s, o2);
-    }
+    Sel s{bv, bi};
+    s = sel_merge_t<OP>(s, Sel{wave_partner<1>(s.v), static_cast<uint32_t>(wave_partner<1>(static_cast<int>(s.i)))});
+    s = sel_merge_t<OP>(s, Sel{wave_partner<2>(s.v), static_cast<uint32_t>(wave_partner<2>(static_cast<int>(s.i)))});
+    s = sel_merge_t<OP>(s, Sel{wave_partner<4>(s.v), static_cast<uint32_t>(wave_partner<4>(static_cast<int>(s.i)))});
+    s = sel_merge_t<OP>(s, Sel{wave_partner<8>(s.v), static_cast<uint32_t>(wave_partner<8>(static_cast<int>(s.i)))});
+    s = sel_merge_t<OP>(s, Sel{wave_partner<16>(s.v), static_cast<uint32_t>(wave_partner<16>(static_cast<int>(s.i)))});
+    s = sel_merge_t<OP>(Sel{lane_value(s.v, 0), static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(s.i), 0))},
+                        Sel{lane_value(s.v, 32), static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(s.i), 32))});
     if constexpr (T > 64) {
         const int lane = t & 63, wave = t >> 6;
         if (lane == 0) {
@@ -520,14 +591,14 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kern
         }
         __syncthreads();
         if (t == 0) {
-            for (int w = 1; w < T / 64; ++w) s = sel_merge(op, s, Sel{sv[slot][w], si[slot][w]});
+            for (int w = 1; w < T / 64; ++w) s = sel_merge_t<OP>(s, Sel{sv[slot][w], si[slot][w]});
         }
     }
     if (!live || t != 0) return;
-    if (value_op) {
-        static_cast<float*>(dst)[o] = s.i == 0xffffffffu ? (is_max ? -__builtin_inff() : __builtin_inff()) : s.v;
+    if constexpr (value_op) {
+        static_cast<float*>(dst)[o] = s.i == kNone ? (is_max ? -__builtin_inff() : __builtin_inff()) : s.v;
     } else {
-        static_cast<int64_t*>(dst)[o] = s.i == 0xffffffffu ? 0 : static_cast<int64_t>(s.i);
+        static_cast<int64_t*>(dst)[o] = s.i == kNone ? 0 : static_cast<int64_t>(s.i);
     }
 }
 
@@ -759,8 +830,27 @@ template <int T, int E4>
 static int launch_select_rows(int op, const float* src, const Op4& kept, uint32_t n_out,
                               uint32_t n, int vec, void* out, hipStream_t st) {
     constexpr int RPB = Rows<T>::kPerBlock;
-    hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4>), dim3(ceil_div(n_out, RPB)),
-                       dim3(Rows<T>::kThreads), 0, st, op, src, kept, n_out, n, vec, out);
+    const dim3 grid(ceil_div(n_out, RPB)), block(Rows<T>::kThreads);
+    switch (op) {
+        case VKHIP_REDUCE_MAX:
+            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_MAX>), grid,
+                               block, 0, st, src, kept, n_out, n, vec, out);
+            break;
+        case VKHIP_REDUCE_MIN:
+            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_MIN>), grid,
+                               block, 0, st, src, kept, n_out, n, vec, out);
+            break;
+        case VKHIP_REDUCE_ARGMAX:
+            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_ARGMAX>), grid,
+                               block, 0, st, src, kept, n_out, n, vec, out);
+            break;
+        case VKHIP_REDUCE_ARGMIN:
+            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_ARGMIN>), grid,
+                               block, 0, st, src, kept, n_out, n, vec, out);
+            break;
+        default:
+            return fail(VKHIP_ERR_INVALID, "select reduce: unknown op %d", op);
+    }
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -771,11 +861,11 @@ static int launch_softmax_rows(const float* src, int64_t stride, float* dst, uin
     constexpr int RPB = Rows<T>::kPerBlock;
     const uint32_t ss = stage_stride(n);
     const size_t lds = static_cast<size_t>(RPB) * ss * sizeof(float);
-    auto fn = softmax_rows_kernel<T, E4>;
+    auto fn = log_mode ? softmax_rows_kernel<T, E4, true> : softmax_rows_kernel<T, E4, false>;
     int rc = allow_lds(reinterpret_cast<const void*>(fn), lds);
     if (rc != VKHIP_OK) return rc;
     hipLaunchKernelGGL(fn, dim3(ceil_div(rows, RPB)), dim3(Rows<T>::kThreads), lds, st, src,
-                       stride, dst, rows, n, depth, log_mode, vec, ss);
+                       stride, dst, rows, n, depth, vec, ss);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -893,6 +983,53 @@ __global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restri
     }
 }
 
+// Rows of exactly 32 * 2^q floats (4096..32768, 16-byte aligned): leaves
+// straight from registers, one workgroup per row.
+static bool leaf_rows_width(uint32_t n) {
+    return n == 32768 || n == 16384 || n == 8192 || n == 4096;
+}
+
+// Contiguous rows handled without the row classes: register-leaf rows, or,
+// up to 2048 floats, a persistent wave per row with next-row prefetch.
+template <bool LOG>
+static int launch_softmax_short(const float* src, int64_t row_stride, float* dst, uint32_t rows,
+                                uint32_t n, int depth, int vec, hipStream_t st) {
+    if (vec && leaf_rows_width(n)) {
+        if (n == 32768)
+            hipLaunchKernelGGL((softmax_leaf_rows_kernel<1024, 1, LOG>), dim3(rows), dim3(1024), 0,
+                               st, src, row_stride, dst, rows);
+        else if (n == 16384)
+            hipLaunchKernelGGL((softmax_leaf_rows_kernel<512, 1, LOG>), dim3(rows), dim3(512), 0,
+                               st, src, row_stride, dst, rows);
+        else if (n == 8192)
+            hipLaunchKernelGGL((softmax_leaf_rows_kernel<256, 1, LOG>), dim3(rows), dim3(256), 0,
+                               st, src, row_stride, dst, rows);
+        else
+            hipLaunchKernelGGL((softmax_leaf_rows_kernel<128, 1, LOG>), dim3(rows), dim3(128), 0,
+                               st, src, row_stride, dst, rows);
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
+    if (n > 2048) return fail(VKHIP_ERR_INVALID, "softmax: short-row path given n=%u", n);
+    const uint32_t ss = stage_stride(n);
+    const size_t lds = 4 * static_cast<size_t>(ss) * sizeof(float);
+    const uint32_t cus = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
+    // Two resident workgroups per CU, so a wave walks several rows and its
+    // prefetch has something to overlap with.
+    const uint32_t want = ceil_div(rows, 4);
+    const uint32_t blocks = want < cus * 2 ? want : cus * 2;
+    void (*fn)(const float*, int64_t, float*, uint32_t, uint32_t, int, uint32_t);
+    if (n <= 256)
+        fn = vec ? softmax_wave_rows_kernel<1, LOG, true> : softmax_wave_rows_kernel<1, LOG, false>;
+    else if (n <= 1024)
+        fn = vec ? softmax_wave_rows_kernel<4, LOG, true> : softmax_wave_rows_kernel<4, LOG, false>;
+    else
+        fn = vec ? softmax_wave_rows_kernel<8, LOG, true> : softmax_wave_rows_kernel<8, LOG, false>;
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, st, src, row_stride, dst, rows, n, depth, ss);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
 int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axis, int log_mode) {
     if (axis < 0 || axis > 3) return fail(VKHIP_ERR_INVALID, "softmax: axis %d outside 0..3", axis);
     Op4 kept, red;
@@ -927,44 +1064,9 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
         const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
                         (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (n % 4 == 0) &&
                         (row_stride % 4 == 0);
-        // Long rows of exactly 32 * 2^q floats: leaves straight from registers.
-        if (vec && (n == 32768 || n == 16384 || n == 8192 || n == 4096)) {
-            if (n == 32768)
-                hipLaunchKernelGGL((softmax_leaf_rows_kernel<1024, 1>), dim3(rows), dim3(1024), 0,
-                                   st, src, row_stride, dst, rows, log_mode);
-            else if (n == 16384)
-                hipLaunchKernelGGL((softmax_leaf_rows_kernel<512, 1>), dim3(rows), dim3(512), 0,
-                                   st, src, row_stride, dst, rows, log_mode);
-            else if (n == 8192)
-                hipLaunchKernelGGL((softmax_leaf_rows_kernel<256, 1>), dim3(rows), dim3(256), 0,
-                                   st, src, row_stride, dst, rows, log_mode);
-            else
-                hipLaunchKernelGGL((softmax_leaf_rows_kernel<128, 1>), dim3(rows), dim3(128), 0,
-                                   st, src, row_stride, dst, rows, log_mode);
-            VKHIP_LAUNCH_CHECK();
-            return VKHIP_OK;
-        }
-        // Rows up to 2048: a persistent wave per row with next-row prefetch.
-        if (n <= 2048) {
-            const uint32_t ss = stage_stride(n);
-            const size_t lds = 4 * static_cast<size_t>(ss) * sizeof(float);
-            const uint32_t cus = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
-            // Two resident workgroups per CU, so a wave walks several rows and
-            // its prefetch has something to overlap with.
-            const uint32_t want = ceil_div(rows, 4);
-            const uint32_t blocks = want < cus * 2 ? want : cus * 2;
-            if (n <= 256)
-                hipLaunchKernelGGL((softmax_wave_rows_kernel<1>), dim3(blocks), dim3(256), lds, st,
-                                   src, row_stride, dst, rows, n, depth, log_mode, vec, ss);
-            else if (n <= 1024)
-                hipLaunchKernelGGL((softmax_wave_rows_kernel<4>), dim3(blocks), dim3(256), lds, st,
-                                   src, row_stride, dst, rows, n, depth, log_mode, vec, ss);
-            else
-                hipLaunchKernelGGL((softmax_wave_rows_kernel<8>), dim3(blocks), dim3(256), lds, st,
-                                   src, row_stride, dst, rows, n, depth, log_mode, vec, ss);
-            VKHIP_LAUNCH_CHECK();
-            return VKHIP_OK;
-        }
+        if (n <= 2048 || (vec && leaf_rows_width(n)))
+            return log_mode ? launch_softmax_short<true>(src, row_stride, dst, rows, n, depth, vec, st)
+                            : launch_softmax_short<false>(src, row_stride, dst, rows, n, depth, vec, st);
         const RowClass rc = row_class(n);
         VKHIP_ROW_CLASSES(launch_softmax_rows, src, row_stride, dst, rows, n, depth, log_mode, vec, st)
     }

@@ -256,6 +256,8 @@ static int compute_node(const vkhip_node& nd) {
         case VKHIP_OP_MAX_POOL2D: {
             vkhip_unfold p;
             memcpy(&p, nd.params, sizeof p);
+            if (nd.out.ne[0] != nd.src[0].ne[0] || nd.out.ne[1] != nd.src[0].ne[1])
+                return fail(VKHIP_ERR_INVALID, "max_pool2d: output planes disagree with the input's");
             return launch_max_pool2d(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
                                      static_cast<float*>(nd.out.data),
                                      static_cast<uint32_t>(nd.out.ne[2]),
@@ -264,6 +266,11 @@ static int compute_node(const vkhip_node& nd) {
         case VKHIP_OP_MAX_POOL2D_BACKWARD: {
             vkhip_unfold p;
             memcpy(&p, nd.params, sizeof p);
+            for (int i = 0; i < 4; ++i)
+                if (nd.out.ne[i] != nd.src[1].ne[i])
+                    return fail(VKHIP_ERR_INVALID, "max_pool2d_backward: output shape differs from the input's");
+            if (nd.src[0].ne[0] != nd.src[1].ne[0] || nd.src[0].ne[1] != nd.src[1].ne[1])
+                return fail(VKHIP_ERR_INVALID, "max_pool2d_backward: gradient planes disagree with the input's");
             return launch_max_pool2d_backward(
                 static_cast<const float*>(nd.src[0].data), static_cast<const float*>(nd.src[1].data),
                 to_operand(nd.src[1]), static_cast<float*>(nd.out.data),
