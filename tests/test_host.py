@@ -104,11 +104,17 @@ def test_split_k_plan_rules():
     """The split-K plan: power-of-two chunk, workspace <= 64 MiB, OFF never
     splits, a forced request gets the largest power-of-two chunk giving at
     least that many partitions (reference plan_split_k,
-    vulkan_backend.cpp:596-647); AUTO splits exactly when the output tiles
-    cannot fill two workgroups per CU (the rule restated for 256 CUs)."""
-    # square 4096^3 and the 8192x1024x4096 sweep case fill the machine: no split
+    vulkan_backend.cpp:596-647); AUTO splits exactly when neither 128x128 nor
+    64x64 output tiles give each of the 256 CUs a workgroup, aiming at about
+    one workgroup per CU (the rule restated for MI355X)."""
+    # the GEMM sweep's square sizes down to 1024^3 and 8192x1024x4096 fill the
+    # machine with 128x128 or 64x64 tiles: no split
     assert plan(1, 4096, 4096, 4096) == (1, 128)
     assert plan(1, 8192, 1024, 4096)[0] == 1
+    assert plan(1, 2048, 2048, 2048)[0] == 1
+    assert plan(1, 1024, 1024, 1024)[0] == 1
+    # 512^3: 64 tiles of 64x64 -> four partitions of four K-tiles
+    assert plan(1, 512, 512, 512) == (4, 4)
     # the skinny K-dominant BASELINE shapes and the small MLP/conv GEMMs split
     for m, n, k in [(256, 256, 65536), (128, 784, 16384), (64, 128, 784), (128, 1024, 576)]:
         splits, chunk = plan(1, m, n, k)

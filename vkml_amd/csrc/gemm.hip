@@ -298,36 +298,77 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 // the stack lives in registers.
 constexpr int kSplitLevels = 9;  // up to 511 partitions
 
+// Push of one value onto a carry stack of `count` earlier pushes.
+__device__ __forceinline__ void carry_push(float (&stack)[kSplitLevels], uint32_t count, float block) {
+    bool carry = true;
+#pragma unroll
+    for (int l = 0; l < kSplitLevels; ++l) {
+        if (carry) {
+            if ((count >> l) & 1u) {
+                block = block + stack[l];
+            } else {
+                stack[l] = block;
+                carry = false;
+            }
+        }
+    }
+}
+
+// G threads per output. With G == 1 a thread folds all `splits` partials.
+// With G > 1 (splits a power of two) thread g folds the block of per =
+// splits/G consecutive partials starting at g*per, which the carry stack
+// leaves as one balanced subtree at level log2(per); the G subtrees then meet
+// in a balanced tree and the drain adds it to 0.0 - the same association as
+// one thread pushing all partials. Partials are read eight at a time so the
+// loads overlap; outputs are consecutive across lanes, so loads coalesce.
+template <int G>
 __global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __restrict__ ws,
                                                              float* __restrict__ dst, uint64_t ne,
                                                              uint32_t splits) {
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= ne) return;
+    constexpr int kOuts = 256 / G;
+    __shared__ float part[G][kOuts];
+    const int g = threadIdx.x / kOuts, o = threadIdx.x % kOuts;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * kOuts + o;
+    const bool live = i < ne;
+    const uint32_t per = splits / G;
+    const float* src = ws + static_cast<uint64_t>(g) * per * ne + (live ? i : 0);
     float stack[kSplitLevels];
 #pragma unroll
     for (int l = 0; l < kSplitLevels; ++l) stack[l] = 0.0f;
-    uint32_t count = 0;
-    for (uint32_t s = 0; s < splits; ++s) {
-        float block = ws[static_cast<uint64_t>(s) * ne + i];
-        bool carry = true;
+    if (live) {
+        for (uint32_t s0 = 0; s0 < per; s0 += 8) {
+            float v[8];
 #pragma unroll
-        for (int l = 0; l < kSplitLevels; ++l) {
-            if (carry) {
-                if ((count >> l) & 1u) {
-                    block = block + stack[l];
-                } else {
-                    stack[l] = block;
-                    carry = false;
-                }
-            }
+            for (int j = 0; j < 8; ++j)
+                v[j] = s0 + j < per ? src[static_cast<uint64_t>(s0 + j) * ne] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (s0 + j < per) carry_push(stack, s0 + j, v[j]);
         }
-        ++count;
     }
-    float total = 0.0f;
+    if constexpr (G == 1) {
+        float total = 0.0f;
 #pragma unroll
-    for (int l = 0; l < kSplitLevels; ++l)
-        if ((count >> l) & 1u) total = total + stack[l];
-    dst[i] = total;
+        for (int l = 0; l < kSplitLevels; ++l)
+            if ((per >> l) & 1u) total = total + stack[l];
+        if (live) dst[i] = total;
+    } else {
+        float mine = 0.0f;
+#pragma unroll
+        for (int l = 0; l < kSplitLevels; ++l)
+            if ((1u << l) == per) mine = stack[l];
+        part[g][o] = mine;
+        __syncthreads();
+        if (g != 0 || !live) return;
+        float v[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) v[j] = part[j][o];
+#pragma unroll
+        for (int w = 1; w < G; w <<= 1)
+#pragma unroll
+            for (int j = 0; j + w < G; j += 2 * w) v[j] = v[j] + v[j + w];
+        dst[i] = 0.0f + v[0];
+    }
 }
 
 // ---- GEMV -------------------------------------------------------------------
@@ -401,21 +442,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ a, 
 // yields at least that many partitions, the partial workspace is capped at
 // 64 MiB, and the fold of the partials is the carry stack. Changed: the
 // reference's profitability rule (split iff K-tiles >= output tiles, at most
-// 16 partitions, chunk >= 4) was fitted on a 36-CU RDNA1 part. A 256-CU MI355X
-// runs about two 256-thread MFMA workgroups per CU, so here a product splits
-// whenever its output tiles cannot fill those 512 slots: the target is
-// ceil(512 / tiles) partitions, capped at 256, with a chunk of at least two
-// K-tiles so each partition still overlaps one tile's loads with another's
-// MFMAs.
-static void plan_split_k(uint32_t tiles, uint32_t ktiles, uint64_t out_elems, uint32_t cu,
+// 16 partitions, chunk >= 4) was fitted on a 36-CU RDNA1 part. Here the caller
+// splits only products whose output tiles cannot give every one of the 256 CUs
+// a workgroup; the target is ceil(CUs / tiles) partitions, capped at 256, with
+// a chunk of at least two K-tiles.
+static void plan_split_k(uint32_t tiles, uint32_t ktiles, uint64_t out_elems, uint32_t slots,
                          uint32_t requested, uint32_t& splits, uint32_t& chunk) {
     splits = 1;
     chunk = ktiles;
     if (ktiles < 2 || tiles == 0) return;
-    const uint32_t slots = (cu ? cu : 256) * 2;
     uint32_t target = requested;
     if (target == 0) {
-        if (tiles * 2 > slots) return;  // at least one workgroup per CU already
+        if (tiles >= slots) return;
         target = (slots + tiles - 1) / tiles;
         if (target < 2) target = 2;
         if (target > 256) target = 256;
@@ -435,13 +473,6 @@ static void plan_split_k(uint32_t tiles, uint32_t ktiles, uint64_t out_elems, ui
 struct TileChoice {
     int bm, bn;
 };
-
-static TileChoice choose_tile(uint32_t m, uint32_t n) {
-    // Large outputs: 128x128 tiles (64x64 per wave). Small ones: 64x64 tiles
-    // so that the grid still spreads over the CUs.
-    if (static_cast<uint64_t>(m) * n >= 512ull * 512ull) return {128, 128};
-    return {64, 64};
-}
 
 template <int BM, int BN, int WM, int WN, int AM>
 static void launch_b(const GemmArgs& g, dim3 grid, hipStream_t st, int bmode) {
@@ -470,8 +501,19 @@ static int launch_tiles(const GemmArgs& g, uint32_t batch, uint32_t splits, int 
 
 int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
     if (ne == 0) return VKHIP_OK;
-    hipLaunchKernelGGL(split_k_reduce_kernel, dim3(ceil_div(ne, 256)), dim3(256), 0, ctx().stream,
-                       ws, dst, ne, splits);
+    if (splits == 0 || splits >= (1u << kSplitLevels))
+        return fail(VKHIP_ERR_INVALID, "split-K reduce: %u partitions outside 1..%u", splits,
+                    (1u << kSplitLevels) - 1);
+    const bool pow2 = (splits & (splits - 1)) == 0;
+    if (pow2 && splits >= 8)
+        hipLaunchKernelGGL(split_k_reduce_kernel<8>, dim3(ceil_div(ne, 32)), dim3(256), 0,
+                           ctx().stream, ws, dst, ne, splits);
+    else if (pow2 && splits >= 2)
+        hipLaunchKernelGGL(split_k_reduce_kernel<2>, dim3(ceil_div(ne, 128)), dim3(256), 0,
+                           ctx().stream, ws, dst, ne, splits);
+    else
+        hipLaunchKernelGGL(split_k_reduce_kernel<1>, dim3(ceil_div(ne, 256)), dim3(256), 0,
+                           ctx().stream, ws, dst, ne, splits);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -497,18 +539,48 @@ int launch_gemv(const float* a, int64_t lda, const float* x, int64_t incx, float
     return VKHIP_OK;
 }
 
+// Tile and split-K choice, from measurements of both tile kernels on MI355X
+// (fp32, 256 CUs):
+//  - A 128x128 tile (four 64x64 wave tiles, four independent MFMA chains per
+//    wave) keeps the matrix cores busy even at one workgroup per CU; a 64x64
+//    tile (one chain per wave) needs several workgroups per CU to do so, and
+//    wastes less on outputs narrower than 128.
+//  - So: enough 128x128 tiles for every CU -> 128x128, unsplit (2048^3 runs
+//    at 108 TFLOP/s unsplit, 101 split in two); else enough 64x64 tiles ->
+//    64x64, unsplit (1024^3: 31 us, against 34-48 us for any split).
+//  - Otherwise split K: with 128x128 tiles when each partition still gets at
+//    least 8 K-tiles (256x256x65536: 88 us as 64 partitions, 102 us as 32
+//    partitions of 64x64 tiles), else with 64x64 tiles (512^3: 11 us as 4
+//    partitions, 16 us as 8).
 int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_request,
               uint32_t& splits, uint32_t& chunk, TileChoice& tile) {
     constexpr uint32_t BK = 32;
-    tile = choose_tile(m, n);
-    const uint32_t tiles = ceil_div(m, tile.bm) * ceil_div(n, tile.bn) * batch;
+    const uint32_t cu = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
+    const uint64_t t128 = static_cast<uint64_t>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
+    const uint64_t t64 = static_cast<uint64_t>(ceil_div(m, 64)) * ceil_div(n, 64) * batch;
+    // 128x128 tiles pad the output more than 25% beyond what 64x64 tiles do
+    // (padded areas are 16384*t128 and 4096*t64).
+    const bool narrow = 16 * t128 > 5 * t64;
     const uint32_t ktiles = ceil_div(k, BK);
     splits = 1;
     chunk = ktiles > 0 ? ktiles : 1;
-    if (split_request == 1) return VKHIP_OK;  // OFF
     const uint32_t req = split_request > 1 ? static_cast<uint32_t>(split_request) : 0u;
-    const uint32_t cu = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
-    plan_split_k(tiles, ktiles, static_cast<uint64_t>(m) * n * batch, cu, req, splits, chunk);
+    bool want_split = false;
+    if (t128 >= cu && !narrow) {
+        tile = {128, 128};
+    } else if (t64 >= cu) {
+        tile = {64, 64};
+    } else {
+        const uint64_t target128 = (cu + t128 - 1) / t128;
+        tile = (!narrow && ktiles / target128 >= 8) ? TileChoice{128, 128} : TileChoice{64, 64};
+        want_split = true;
+    }
+    if (split_request == 1) return VKHIP_OK;  // OFF
+    if (!want_split && req == 0) return VKHIP_OK;
+    const uint64_t tiles = tile.bm == 128 ? t128 : t64;
+    if (tiles > 0xffffffffull) return VKHIP_OK;
+    plan_split_k(static_cast<uint32_t>(tiles), ktiles, static_cast<uint64_t>(m) * n * batch, cu,
+                 req, splits, chunk);
     if (splits == 1) chunk = ktiles > 0 ? ktiles : 1;
     return VKHIP_OK;
 }
