@@ -213,12 +213,37 @@ __global__ __launch_bounds__(256) void col2im_staged_kernel(const float* __restr
     extern __shared__ __attribute__((aligned(16))) float stage[];
     const uint64_t plane = blockIdx.x;
     const float* src = cols + plane * plane_floats;
+    // Every load of the plane is issued before the first LDS write (the plane
+    // is at most 64 KB: sixteen 16-byte loads per thread).
     if (vec_in) {
         const f32x4* s4 = reinterpret_cast<const f32x4*>(src);
         f32x4* d4 = reinterpret_cast<f32x4*>(stage);
-        for (uint32_t i = threadIdx.x; i < plane_floats / 4; i += 256) d4[i] = s4[i];
+        const uint32_t nv = plane_floats / 4;
+        f32x4 v[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t i = threadIdx.x + 256u * r;
+            if (i < nv) v[r] = s4[i];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t i = threadIdx.x + 256u * r;
+            if (i < nv) d4[i] = v[r];
+        }
     } else {
-        for (uint32_t i = threadIdx.x; i < plane_floats; i += 256) stage[i] = src[i];
+        for (uint32_t i0 = 0; i0 < plane_floats; i0 += 256u * 16) {
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t i = i0 + threadIdx.x + 256u * r;
+                if (i < plane_floats) v[r] = src[i];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t i = i0 + threadIdx.x + 256u * r;
+                if (i < plane_floats) stage[i] = v[r];
+            }
+        }
     }
     __syncthreads();
     const int32_t L = g.out_h * g.out_w;

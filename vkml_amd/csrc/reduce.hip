@@ -1014,10 +1014,11 @@ static int launch_softmax_short(const float* src, int64_t row_stride, float* dst
     const uint32_t ss = stage_stride(n);
     const size_t lds = 4 * static_cast<size_t>(ss) * sizeof(float);
     const uint32_t cus = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
-    // Two resident workgroups per CU, so a wave walks several rows and its
-    // prefetch has something to overlap with.
+    // Up to four workgroups (16 waves) per CU: on MI355X one row per wave at
+    // that occupancy beat two rows per wave at half of it (4096x1000: 10.5 vs
+    // 11.3 us); more rows than waves are walked with the next-row prefetch.
     const uint32_t want = ceil_div(rows, 4);
-    const uint32_t blocks = want < cus * 2 ? want : cus * 2;
+    const uint32_t blocks = want < cus * 4 ? want : cus * 4;
     void (*fn)(const float*, int64_t, float*, uint32_t, uint32_t, int, uint32_t);
     if (n <= 256)
         fn = vec ? softmax_wave_rows_kernel<1, LOG, true> : softmax_wave_rows_kernel<1, LOG, false>;
