@@ -190,17 +190,28 @@ int vkhip_shutdown(void);
 const char* vkhip_last_error(void);
 int vkhip_caps_get(vkhip_caps* out);
 /* Makes the backend enqueue on `stream` (a hipStream_t; NULL = its own).
- * Lets a host that owns the stream (e.g. PyTorch) share stream order. */
+ * Lets a host that owns the stream (e.g. PyTorch) share stream order. The
+ * previous stream is synchronised first (cached blocks carry no pending work
+ * across streams). */
 int vkhip_set_stream(void* stream);
 void* vkhip_get_stream(void);
 
 /* ======================================================================== */
 /* Memory (Backend::allocator, copies, synchronize)                          */
 /* ======================================================================== */
+/* Device memory (Backend::allocator; reference VulkanBackend allocation map,
+ * vulkan_backend.cpp:894-919). Served from per-size caches of blocks; the
+ * backend's one stream orders every use, so a freed block is reused by later
+ * work only (the reference's retirement queue, vulkan_backend.cpp:921-984). */
 int vkhip_alloc(size_t nbytes, void** out_ptr);
-/* Stream-ordered: memory in use by enqueued work is not reused early
- * (reference retirement queue, vulkan_backend.cpp:921-984). */
+/* Returns a block from vkhip_alloc to the cache; VKHIP_ERR_INVALID for a
+ * pointer it did not hand out. */
 int vkhip_free(void* ptr);
+/* Synchronises and returns every cached (free) block to HIP. Also done
+ * automatically when an allocation fails, then the allocation is retried. */
+int vkhip_release_cached(void);
+/* Bytes handed out and not freed, and bytes held in the caches. */
+int vkhip_memory_stats(size_t* bytes_in_use, size_t* bytes_cached);
 int vkhip_copy_from_host(void* dst, const void* host_src, size_t nbytes);
 int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes); /* synchronises */
 /* One unit of work for several disjoint copies (backend.h:83-108). */

@@ -433,6 +433,38 @@ def test_scaled_add_is_two_rounded_products(hip):
     assert got.tobytes() == want.astype(np.float32).tobytes()
 
 
+def test_caching_allocator_reuses_and_accounts(hip):
+    """vkhip_alloc/vkhip_free: a freed block of the same size is handed out
+    again, the byte counts follow, an unknown pointer is refused, and
+    release_cached empties the cache."""
+    from ctypes import byref, c_void_p
+
+    lib = _lib.load()
+    b = hip
+    b.synchronize()
+    base = b.memory_stats()
+    p = c_void_p()
+    assert lib.vkhip_alloc(3 << 20, byref(p)) == 0 and p.value
+    first = p.value
+    assert b.memory_stats()["in_use"] == base["in_use"] + (3 << 20)
+    assert lib.vkhip_free(c_void_p(first)) == 0
+    assert lib.vkhip_free(c_void_p(first)) == _lib.ERR_INVALID  # already freed
+    q = c_void_p()
+    assert lib.vkhip_alloc((3 << 20) - 100, byref(q)) == 0  # rounds to the same size
+    assert q.value == first
+    # A reused block is ordinary memory: write and read it through the stream.
+    x = np.arange(1 << 18, dtype=np.float32)
+    assert lib.vkhip_copy_from_host(q, x.ctypes.data_as(c_void_p), x.nbytes) == 0
+    y = np.empty_like(x)
+    assert lib.vkhip_copy_to_host(y.ctypes.data_as(c_void_p), q, x.nbytes) == 0
+    assert y.tobytes() == x.tobytes()
+    assert lib.vkhip_free(q) == 0
+    assert b.memory_stats()["cached"] >= 3 << 20
+    b.release_cached()
+    assert b.memory_stats()["cached"] == 0
+    assert lib.vkhip_free(c_void_p(0x1000)) == _lib.ERR_INVALID
+
+
 def test_errors_are_reported_not_crashed(hip):
     a = dev(np.ones((3, 4), np.float32))
     b = dev(np.ones((5, 6), np.float32))

@@ -77,6 +77,8 @@ SIGNATURES = {
     "vkhip_get_stream": (c_void_p, []),
     "vkhip_alloc": (c_int, [c_size_t, POINTER(c_void_p)]),
     "vkhip_free": (c_int, [c_void_p]),
+    "vkhip_release_cached": (c_int, []),
+    "vkhip_memory_stats": (c_int, [POINTER(c_size_t), POINTER(c_size_t)]),
     "vkhip_copy_from_host": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vkhip_copy_to_host": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vkhip_copy_device_to_device": (c_int, [POINTER(Copy), c_size_t]),

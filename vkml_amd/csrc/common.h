@@ -41,6 +41,12 @@ int require_ready();
 // Workspace of at least `bytes` on the current stream.
 int workspace(size_t bytes, float** out);
 
+// The caching allocator behind vkhip_alloc / vkhip_free (allocator.hip).
+int cached_alloc(size_t nbytes, void** out);
+int cached_free(void* ptr);
+int release_cached();
+void memory_stats(size_t* live, size_t* cached);
+
 #define VKHIP_HIP(expr)                                                                   \
     do {                                                                                  \
         hipError_t e_ = (expr);                                                           \

@@ -338,6 +338,10 @@ extern "C" int vkhip_shutdown(void) {
         c.ws_bytes = 0;
     }
     VKHIP_HIP(hipStreamSynchronize(c.stream));
+    {
+        const int rc = vkhip::release_cached();
+        if (rc != VKHIP_OK) return rc;
+    }
     VKHIP_HIP(hipStreamDestroy(c.own_stream));
     c.own_stream = nullptr;
     c.stream = nullptr;
@@ -358,7 +362,10 @@ extern "C" int vkhip_caps_get(vkhip_caps* out) {
 extern "C" int vkhip_set_stream(void* stream) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
-    ctx().stream = stream ? static_cast<hipStream_t>(stream) : ctx().own_stream;
+    hipStream_t next = stream ? static_cast<hipStream_t>(stream) : ctx().own_stream;
+    // Cached blocks may still be in use by work on the old stream.
+    if (next != ctx().stream) VKHIP_HIP(hipStreamSynchronize(ctx().stream));
+    ctx().stream = next;
     return VKHIP_OK;
 }
 
@@ -372,18 +379,26 @@ extern "C" int vkhip_alloc(size_t nbytes, void** out_ptr) {
     if (!out_ptr) return fail(VKHIP_ERR_INVALID, "alloc: null output");
     *out_ptr = nullptr;
     if (nbytes == 0) return VKHIP_OK;
-    if (hipMallocAsync(out_ptr, nbytes, ctx().stream) != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(VKHIP_ERR_OOM, "alloc: %zu bytes could not be allocated", nbytes);
-    }
-    return VKHIP_OK;
+    return vkhip::cached_alloc(nbytes, out_ptr);
 }
 
 extern "C" int vkhip_free(void* ptr) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
     if (!ptr) return VKHIP_OK;
-    VKHIP_HIP(hipFreeAsync(ptr, ctx().stream));
+    return vkhip::cached_free(ptr);
+}
+
+extern "C" int vkhip_release_cached(void) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    return vkhip::release_cached();
+}
+
+extern "C" int vkhip_memory_stats(size_t* bytes_in_use, size_t* bytes_cached) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    vkhip::memory_stats(bytes_in_use, bytes_cached);
     return VKHIP_OK;
 }
 

@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import weakref
-from ctypes import byref, c_uint32, c_void_p
+from ctypes import c_size_t, byref, c_uint32, c_void_p
 from typing import Sequence
 
 import numpy as np
@@ -247,6 +247,16 @@ class HipBackend:
 
     def synchronize(self) -> None:
         check(self.lib.vkhip_synchronize(), "synchronize")
+
+    def memory_stats(self) -> dict:
+        """Bytes handed out by the caching allocator and bytes it holds free."""
+        live, cached = c_size_t(), c_size_t()
+        check(self.lib.vkhip_memory_stats(byref(live), byref(cached)), "memory_stats")
+        return {"in_use": live.value, "cached": cached.value}
+
+    def release_cached(self) -> None:
+        """Returns every cached free block to HIP (synchronises)."""
+        check(self.lib.vkhip_release_cached(), "release_cached")
 
     def set_stream(self, stream_handle: int | None) -> None:
         check(self.lib.vkhip_set_stream(c_void_p(stream_handle or None)), "set_stream")
