@@ -305,6 +305,11 @@ def test_softmax_non_last_axis(hip):
     ((5, 7, 33), [0, 2]),
     ((2, 3, 4, 5), None),
     ((17, 9), [1]),             # below one leaf per row
+    ((128, 64, 32, 32), [0, 2, 3]),  # conv bias gradient: split tree over 131072
+    ((4096, 64), [0]),          # strided column sums, split tree
+    ((2, 3, 70001), [0, 2]),    # uneven tree over two strided axes
+    ((50000, 3), [0]),          # three outputs, 128 subtrees of 390-391
+    ((2, 3, 600000), [0, 2]),   # subtrees too long to stage: per-output workgroups
 ])
 def test_sum_mean_bit_exact(hip, shape, axes):
     x = (np.random.default_rng(SEED).standard_normal(shape) * 10).astype(np.float32)

@@ -13,11 +13,18 @@
 
 namespace vkhip {
 
+// How a source's offset follows the output's linear index.
+enum SrcMode : int32_t {
+    kContig = 0,  // offset == index
+    kScalar = 1,  // every stride 0 (a broadcast scalar)
+    kStrided = 2  // sum over the output's rank-4 coordinates times the strides
+};
+
 struct Src {
     const void* p;
     int32_t dtype;
-    int32_t contig;
-    Op4 d;
+    int32_t mode;
+    int64_t nb[4];
 };
 
 struct EwArgs {
@@ -28,14 +35,51 @@ struct EwArgs {
     Src s[3];
     float alpha, beta;
     double d0, d1;
+    // The output's rank-4 extents and launch-time divisions by the inner three
+    // (outputs with 2^32 elements or more decode with 64-bit division).
+    uint32_t ne[4];
+    FastDiv dv[3];  // by ne[3], ne[2], ne[1]
+    int32_t wide;
 };
 
-__device__ __forceinline__ int64_t src_off(const Src& s, uint64_t i) {
-    return s.contig ? static_cast<int64_t>(i) : lin_off4(i, s.d.ne, s.d.nb);
+// Coordinates of output element i (computed once, shared by every source).
+struct Coord {
+    uint32_t c[4];
+};
+
+__device__ __forceinline__ Coord coord_of(const EwArgs& a, uint64_t i) {
+    Coord k;
+    if (a.wide) {
+        uint64_t q = i;
+        for (int d = 3; d >= 1; --d) {
+            k.c[d] = static_cast<uint32_t>(q % a.ne[d]);
+            q /= a.ne[d];
+        }
+        k.c[0] = static_cast<uint32_t>(q);
+        return k;
+    }
+    uint32_t q = static_cast<uint32_t>(i);
+    uint32_t qn = a.dv[0].div(q);
+    k.c[3] = q - qn * a.ne[3];
+    q = qn;
+    qn = a.dv[1].div(q);
+    k.c[2] = q - qn * a.ne[2];
+    q = qn;
+    qn = a.dv[2].div(q);
+    k.c[1] = q - qn * a.ne[1];
+    k.c[0] = qn;
+    return k;
 }
 
-__device__ __forceinline__ float load_f(const Src& s, uint64_t i) {
-    const int64_t off = src_off(s, i);
+__device__ __forceinline__ int64_t src_off(const Src& s, uint64_t i, const Coord& k) {
+    if (s.mode == kContig) return static_cast<int64_t>(i);
+    if (s.mode == kScalar) return 0;
+    return static_cast<int64_t>(k.c[0]) * s.nb[0] + static_cast<int64_t>(k.c[1]) * s.nb[1] +
+           static_cast<int64_t>(k.c[2]) * s.nb[2] + static_cast<int64_t>(k.c[3]) * s.nb[3];
+}
+
+__device__ __forceinline__ float load_f(const Src& s, uint64_t i, const Coord& k) {
+    const int64_t off = src_off(s, i, k);
     switch (s.dtype) {
         case VKHIP_I64: return static_cast<float>(static_cast<const int64_t*>(s.p)[off]);
         case VKHIP_BOOL: return static_cast<const uint8_t*>(s.p)[off] != 0 ? 1.0f : 0.0f;
@@ -58,6 +102,9 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EwArgs a) {
     for (int j = 0; j < 4; ++j) {
         const uint64_t i = base + j;
         if (i >= a.n) return;
+        Coord k{};
+        if (a.s[0].mode == kStrided || a.s[1].mode == kStrided || a.s[2].mode == kStrided)
+            k = coord_of(a, i);
         switch (a.op) {
             case VKHIP_OP_FULL:
                 if (a.out_dtype == VKHIP_I64)
@@ -78,41 +125,41 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EwArgs a) {
             case VKHIP_OP_CONTIGUOUS:
                 if (a.out_dtype == VKHIP_I64)
                     static_cast<int64_t*>(a.out)[i] =
-                        static_cast<const int64_t*>(a.s[0].p)[src_off(a.s[0], i)];
+                        static_cast<const int64_t*>(a.s[0].p)[src_off(a.s[0], i, k)];
                 else if (a.out_dtype == VKHIP_BOOL)
                     static_cast<uint8_t*>(a.out)[i] =
-                        static_cast<const uint8_t*>(a.s[0].p)[src_off(a.s[0], i)];
+                        static_cast<const uint8_t*>(a.s[0].p)[src_off(a.s[0], i, k)];
                 else
                     static_cast<float*>(a.out)[i] =
-                        static_cast<const float*>(a.s[0].p)[src_off(a.s[0], i)];
+                        static_cast<const float*>(a.s[0].p)[src_off(a.s[0], i, k)];
                 break;
             case VKHIP_OP_CAST:
                 if (a.s[0].dtype == VKHIP_F32 && a.out_dtype == VKHIP_I64)
                     static_cast<int64_t*>(a.out)[i] = static_cast<int64_t>(
-                        static_cast<const float*>(a.s[0].p)[src_off(a.s[0], i)]);
+                        static_cast<const float*>(a.s[0].p)[src_off(a.s[0], i, k)]);
                 else
-                    store_out(a, i, load_f(a.s[0], i));
+                    store_out(a, i, load_f(a.s[0], i, k));
                 break;
-            case VKHIP_OP_NEG: store_out(a, i, -load_f(a.s[0], i)); break;
-            case VKHIP_OP_EXP: store_out(a, i, expf(load_f(a.s[0], i))); break;
-            case VKHIP_OP_LOG: store_out(a, i, logf(load_f(a.s[0], i))); break;
+            case VKHIP_OP_NEG: store_out(a, i, -load_f(a.s[0], i, k)); break;
+            case VKHIP_OP_EXP: store_out(a, i, expf(load_f(a.s[0], i, k))); break;
+            case VKHIP_OP_LOG: store_out(a, i, logf(load_f(a.s[0], i, k))); break;
             case VKHIP_OP_RELU: {
-                const float x = load_f(a.s[0], i);
+                const float x = load_f(a.s[0], i, k);
                 store_out(a, i, x <= 0.0f ? 0.0f : x);
                 break;
             }
-            case VKHIP_OP_ADD: store_out(a, i, __fadd_rn(load_f(a.s[0], i), load_f(a.s[1], i))); break;
-            case VKHIP_OP_SUB: store_out(a, i, __fsub_rn(load_f(a.s[0], i), load_f(a.s[1], i))); break;
-            case VKHIP_OP_MUL: store_out(a, i, __fmul_rn(load_f(a.s[0], i), load_f(a.s[1], i))); break;
-            case VKHIP_OP_DIV: store_out(a, i, load_f(a.s[0], i) / load_f(a.s[1], i)); break;
+            case VKHIP_OP_ADD: store_out(a, i, __fadd_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
+            case VKHIP_OP_SUB: store_out(a, i, __fsub_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
+            case VKHIP_OP_MUL: store_out(a, i, __fmul_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
+            case VKHIP_OP_DIV: store_out(a, i, load_f(a.s[0], i, k) / load_f(a.s[1], i, k)); break;
             case VKHIP_OP_SCALED_ADD:
                 store_out(a, i,
-                          __fadd_rn(__fmul_rn(load_f(a.s[0], i), a.alpha),
-                                    __fmul_rn(load_f(a.s[1], i), a.beta)));
+                          __fadd_rn(__fmul_rn(load_f(a.s[0], i, k), a.alpha),
+                                    __fmul_rn(load_f(a.s[1], i, k), a.beta)));
                 break;
             case VKHIP_OP_MAXIMUM:
             case VKHIP_OP_MINIMUM: {
-                const float x = load_f(a.s[0], i), y = load_f(a.s[1], i);
+                const float x = load_f(a.s[0], i, k), y = load_f(a.s[1], i, k);
                 float r;
                 if (x != x || y != y)
                     r = __builtin_nanf("");
@@ -129,7 +176,7 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EwArgs a) {
             case VKHIP_OP_LESS_EQUAL:
             case VKHIP_OP_GREATER_EQUAL:
             case VKHIP_OP_NOT_EQUAL: {
-                const float x = load_f(a.s[0], i), y = load_f(a.s[1], i);
+                const float x = load_f(a.s[0], i, k), y = load_f(a.s[1], i, k);
                 bool r = false;
                 switch (a.op) {
                     case VKHIP_OP_EQUAL: r = x == y; break;
@@ -143,8 +190,8 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EwArgs a) {
                 break;
             }
             case VKHIP_OP_WHERE: {
-                const bool c = static_cast<const uint8_t*>(a.s[0].p)[src_off(a.s[0], i)] != 0;
-                store_out(a, i, c ? load_f(a.s[1], i) : load_f(a.s[2], i));
+                const bool c = static_cast<const uint8_t*>(a.s[0].p)[src_off(a.s[0], i, k)] != 0;
+                store_out(a, i, c ? load_f(a.s[1], i, k) : load_f(a.s[2], i, k));
                 break;
             }
             default: break;
@@ -199,20 +246,18 @@ static uint64_t tnumel(const vkhip_tensor& t) {
     return n;
 }
 
+// Sources arrive with the output's extents (broadcast axes have stride 0).
 static Src make_src(const vkhip_tensor& t) {
     Src s{};
     s.p = t.data;
     s.dtype = t.dtype;
-    s.contig = is_contig(t) ? 1 : 0;
     const int pad = 4 - t.ndim;
-    for (int i = 0; i < 4; ++i) {
-        s.d.ne[i] = 1;
-        s.d.nb[i] = 0;
-    }
+    bool scalar = true;
     for (int i = 0; i < t.ndim; ++i) {
-        s.d.ne[pad + i] = static_cast<uint32_t>(t.ne[i]);
-        s.d.nb[pad + i] = t.nb[i];
+        s.nb[pad + i] = t.nb[i];
+        if (t.ne[i] != 1 && t.nb[i] != 0) scalar = false;
     }
+    s.mode = is_contig(t) ? kContig : scalar ? kScalar : kStrided;
     return s;
 }
 
@@ -251,6 +296,16 @@ int launch_elementwise(const vkhip_node& nd) {
     a.out = nd.out.data;
     a.n = n;
     for (int s = 0; s < nd.n_src && s < 3; ++s) a.s[s] = make_src(nd.src[s]);
+    for (int s = nd.n_src; s < 3; ++s) a.s[s].mode = kContig;
+    {
+        const int pad = 4 - nd.out.ndim;
+        for (int i = 0; i < 4; ++i) a.ne[i] = 1;
+        for (int i = 0; i < nd.out.ndim; ++i) a.ne[pad + i] = static_cast<uint32_t>(nd.out.ne[i]);
+        a.dv[0] = FastDiv(a.ne[3]);
+        a.dv[1] = FastDiv(a.ne[2]);
+        a.dv[2] = FastDiv(a.ne[1]);
+        a.wide = n >= (1ull << 32) ? 1 : 0;
+    }
     a.alpha = ab[0];
     a.beta = ab[1];
     a.d0 = dd[0];

@@ -357,14 +357,69 @@ __global__ __launch_bounds__(T) void softmax_leaf_rows_kernel(const float* __res
 // so the loads coalesce whenever the kept axis is the contiguous one.
 constexpr int kTallLevels = 22;  // 2^21 leaves of <= 32: n < 2^26 elements
 
+// Offset of reduced element i: the reduced axes, merged on the host wherever
+// they are contiguous with each other, innermost first; every axis but the
+// outermost is split off with a launch-time division (reduced extents are
+// below 2^26, so 32-bit quotients suffice).
 struct Reader {
-    Op4 red;
-    int single;  // the reduced elements sit on one axis with stride `step`
-    int64_t step;
+    int naxes;         // 1..4
+    uint32_t ne[3];    // extents of the inner naxes - 1 axes
+    int64_t nb[3];     // their strides
+    FastDiv div[3];    // divisions by ne[]
+    int64_t nb_outer;  // stride of the outermost axis
     __device__ __forceinline__ int64_t off(uint32_t i) const {
-        return single ? static_cast<int64_t>(i) * step : lin_off4(i, red.ne, red.nb);
+        int64_t o = 0;
+        uint32_t q = i;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            if (a + 1 < naxes) {
+                const uint32_t qn = div[a].div(q);
+                o += static_cast<int64_t>(q - qn * ne[a]) * nb[a];
+                q = qn;
+            }
+        }
+        return o + static_cast<int64_t>(q) * nb_outer;
     }
 };
+
+// Reader over the reduced axes of `red` (right-aligned rank 4).
+static Reader make_reader(const Op4& red) {
+    uint32_t ne[4];
+    int64_t nb[4];
+    int k = 0;  // axes with extent > 1, outermost first, merged when contiguous
+    for (int i = 0; i < 4; ++i) {
+        if (red.ne[i] == 1) continue;
+        if (k > 0 && nb[k - 1] == static_cast<int64_t>(red.ne[i]) * red.nb[i]) {
+            ne[k - 1] *= red.ne[i];
+            nb[k - 1] = red.nb[i];
+        } else {
+            ne[k] = red.ne[i];
+            nb[k] = red.nb[i];
+            ++k;
+        }
+    }
+    Reader r{};
+    if (k == 0) {
+        r.naxes = 1;
+        r.nb_outer = 0;
+        return r;
+    }
+    r.naxes = k;
+    for (int a = 0; a + 1 < k; ++a) {  // innermost first
+        r.ne[a] = ne[k - 1 - a];
+        r.nb[a] = nb[k - 1 - a];
+        r.div[a] = FastDiv(ne[k - 1 - a]);
+    }
+    r.nb_outer = nb[0];
+    return r;
+}
+
+static Reader single_reader(int64_t step) {
+    Reader r{};
+    r.naxes = 1;
+    r.nb_outer = step;
+    return r;
+}
 
 __global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* __restrict__ src,
                                                           Op4 kept, Reader rd, uint64_t n_out,
@@ -381,8 +436,15 @@ __global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* _
         for (uint32_t j = 0; j < leaves; ++j) {
             uint32_t b, e;
             pairwise_leaf(n_red, depth, j, b, e);
+            // All of the leaf's (at most 32) loads are issued before the
+            // sequential sum, so a leaf costs one memory round trip.
+            float v[32];
+#pragma unroll
+            for (int r = 0; r < 32; ++r) v[r] = b + r < e ? base[rd.off(b + r)] : 0.0f;
             float s = 0.0f;
-            for (uint32_t q = b; q < e; ++q) s = s + base[rd.off(q)];
+#pragma unroll
+            for (int r = 0; r < 32; ++r)
+                if (b + r < e) s = s + v[r];
             bool carry = true;
 #pragma unroll
             for (int l = 0; l < kTallLevels; ++l) {
@@ -405,16 +467,25 @@ __global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* _
         static_cast<float*>(dst)[o] = total;
         return;
     }
+    // Selections scan in index order, 32 loads in flight at a time.
     if (op == VKHIP_REDUCE_MAX || op == VKHIP_REDUCE_MIN) {
         const bool is_max = op == VKHIP_REDUCE_MAX;
         float best = is_max ? -__builtin_inff() : __builtin_inff();
-        for (uint32_t i = 0; i < n_red; ++i) {
-            const float v = base[rd.off(i)];
-            if (v != v) {
-                best = v;
-                break;
+        bool found_nan = false;
+        for (uint32_t i0 = 0; i0 < n_red && !found_nan; i0 += 32) {
+            float v[32];
+#pragma unroll
+            for (int r = 0; r < 32; ++r) v[r] = i0 + r < n_red ? base[rd.off(i0 + r)] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 32; ++r) {
+                if (found_nan || i0 + r >= n_red) continue;
+                if (v[r] != v[r]) {
+                    best = v[r];
+                    found_nan = true;
+                } else if (is_max ? (v[r] > best) : (v[r] < best)) {
+                    best = v[r];
+                }
             }
-            if (is_max ? (v > best) : (v < best)) best = v;
         }
         static_cast<float*>(dst)[o] = best;
         return;
@@ -422,11 +493,16 @@ __global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* _
     const bool is_max = op == VKHIP_REDUCE_ARGMAX;
     float best = is_max ? -__builtin_inff() : __builtin_inff();
     int64_t best_i = 0;
-    for (uint32_t i = 0; i < n_red; ++i) {
-        const float v = base[rd.off(i)];
-        if (is_max ? (v > best) : (v < best)) {
-            best = v;
-            best_i = i;
+    for (uint32_t i0 = 0; i0 < n_red; i0 += 32) {
+        float v[32];
+#pragma unroll
+        for (int r = 0; r < 32; ++r) v[r] = i0 + r < n_red ? base[rd.off(i0 + r)] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+            if (i0 + r < n_red && (is_max ? (v[r] > best) : (v[r] < best))) {
+                best = v[r];
+                best_i = i0 + r;
+            }
         }
     }
     static_cast<int64_t*>(dst)[o] = best_i;
@@ -720,6 +796,80 @@ __global__ __launch_bounds__(T) void reduce_wide_strided_kernel(
     if (t == 0) dst[o] = mean ? u / static_cast<float>(n) : u;
 }
 
+// ---- sums with few outputs over many elements: split tree ----------------------
+// The oracle's pairwise recursion is self-similar: the node reached from the
+// root by the d bits of j (MSB first, midpoint splits) is the pairwise sum of
+// its own range, and the top d levels above those nodes only add left + right.
+// So a sum over n elements splits exactly into 2^d subtree sums (one workgroup
+// each, staged in LDS from coalesced loads and summed with the same leaf
+// machinery as the row kernels, depth D - d inside the subtree) and a balanced
+// fold of the 2^d partials. A node at depth < d that is already a leaf is
+// carried by its leftmost descendant and the others contribute +0.0, which
+// leaves every sum unchanged.
+constexpr uint32_t kSubtreeMax = 8192;  // elements one workgroup stages
+
+__global__ __launch_bounds__(256) void reduce_subtree_kernel(const float* __restrict__ src,
+                                                             Op4 kept, Reader rd, uint32_t n,
+                                                             int depth, int split,
+                                                             float* __restrict__ partial) {
+    __shared__ __attribute__((aligned(16))) float stage[(kSubtreeMax + 4 * (kSubtreeMax / 32) + 3) & ~3u];
+    __shared__ float scratch[4];
+    const uint32_t j = blockIdx.x, o = blockIdx.y;
+    const float* base = src + lin_off4(o, kept.ne, kept.nb);
+    uint32_t b, e;
+    pairwise_leaf(n, split, j, b, e);
+    const uint32_t m = e - b;
+    constexpr int kBatch = kSubtreeMax / 256;
+    float v[kBatch];
+#pragma unroll
+    for (int r = 0; r < kBatch; ++r) {
+        const uint32_t i = threadIdx.x + 256u * r;
+        v[r] = i < m ? base[rd.off(b + i)] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < kBatch; ++r) {
+        const uint32_t i = threadIdx.x + 256u * r;
+        if (i < m) stage[stage_index(i)] = v[r];
+    }
+    __syncthreads();
+    const float sum = group_pairwise_sum<256>(stage, m, depth - split, threadIdx.x, scratch);
+    if (threadIdx.x == 0) partial[static_cast<uint64_t>(j) * gridDim.y + o] = sum;
+}
+
+// Balanced fold of the 2^split partials of each output (a carry stack over
+// 2^split pushes is exactly that tree).
+__global__ __launch_bounds__(256) void reduce_subtree_fold_kernel(const float* __restrict__ partial,
+                                                                  uint32_t n_out, int split,
+                                                                  uint32_t n, int mean,
+                                                                  float* __restrict__ dst) {
+    const uint32_t o = blockIdx.x * 256 + threadIdx.x;
+    if (o >= n_out) return;
+    float stack[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) stack[l] = 0.0f;
+    const uint32_t parts = 1u << split;
+    for (uint32_t j = 0; j < parts; ++j) {
+        float sv = partial[static_cast<uint64_t>(j) * n_out + o];
+        bool carry = true;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            if (carry) {
+                if ((j >> l) & 1u) {
+                    sv = stack[l] + sv;
+                } else {
+                    stack[l] = sv;
+                    carry = false;
+                }
+            }
+        }
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l)
+        if ((1u << l) == parts) total = stack[l];
+    dst[o] = mean ? total / static_cast<float>(n) : total;
+}
+
 // ---- host side ----------------------------------------------------------------------
 
 static void split_axes(const vkhip_operand& d, uint32_t mask, Op4& kept, Op4& red) {
@@ -767,17 +917,6 @@ static bool contiguous_run(const Op4& o) {
 }
 
 // The reduced elements lie on at most one non-unit axis: its stride.
-static bool single_axis(const Op4& o, int64_t& step) {
-    int count = 0;
-    step = 0;
-    for (int i = 0; i < 4; ++i)
-        if (o.ne[i] != 1) {
-            ++count;
-            step = o.nb[i];
-        }
-    return count <= 1;
-}
-
 constexpr uint32_t kRowsMax = 32768;  // longest run staged in LDS
 
 // Row size classes: T threads per row and E4 float4 groups per thread.
@@ -920,11 +1059,33 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
         VKHIP_LAUNCH_CHECK();
         return VKHIP_OK;
     }
-    Reader rd;
-    rd.red = red;
-    rd.single = single_axis(red, rd.step) ? 1 : 0;
+    const Reader rd = make_reader(red);
     const int depth = pairwise_depth(n_red);
     const uint32_t cus = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
+    if (sum_op && n_red >= 2048 && n_out < 4 * cus) {
+        // Split into 2^split subtrees of at most kSubtreeMax elements, with
+        // enough workgroups for two per CU, keeping split <= depth and the
+        // partials within 2^7 per output.
+        int split = 0;
+        while (split < depth && split < 7 &&
+               (((static_cast<uint64_t>(n_red) + (1ull << split) - 1) >> split) > kSubtreeMax ||
+                (static_cast<uint64_t>(n_out) << split) < 2ull * cus))
+            ++split;
+        if (((static_cast<uint64_t>(n_red) + (1ull << split) - 1) >> split) <= kSubtreeMax &&
+            split > 0) {
+            float* part = nullptr;
+            int rc = workspace((static_cast<size_t>(n_out) << split) * sizeof(float), &part);
+            if (rc != VKHIP_OK) return rc;
+            hipLaunchKernelGGL(reduce_subtree_kernel, dim3(1u << split, n_out), dim3(256), 0, st,
+                               src, kept, rd, n_red, depth, split, part);
+            VKHIP_LAUNCH_CHECK();
+            hipLaunchKernelGGL(reduce_subtree_fold_kernel, dim3(ceil_div(n_out, 256)), dim3(256), 0,
+                               st, part, n_out, split, n_red, op == VKHIP_REDUCE_MEAN ? 1 : 0,
+                               static_cast<float*>(dst));
+            VKHIP_LAUNCH_CHECK();
+            return VKHIP_OK;
+        }
+    }
     if (sum_op && n_red >= 8192 && n_out < 4 * cus) {
         hipLaunchKernelGGL(reduce_wide_strided_kernel<256>, dim3(n_out), dim3(256), 0, st, src,
                            kept, rd, n_red, depth, op == VKHIP_REDUCE_MEAN ? 1 : 0,
@@ -1081,13 +1242,8 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
     }
     Op4 okept, ored;
     split_axes(od, 1u << axis, okept, ored);
-    Reader rd, ord;
-    rd.red = red;
-    rd.single = 1;
-    rd.step = d.nb[axis];
-    ord.red = ored;
-    ord.single = 1;
-    ord.step = od.nb[axis];
+    const Reader rd = single_reader(d.nb[axis]);
+    const Reader ord = single_reader(od.nb[axis]);
     hipLaunchKernelGGL(softmax_tall_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, st, src, kept,
                        rd, okept, ord, n_out64, n, depth, log_mode, dst);
     VKHIP_LAUNCH_CHECK();

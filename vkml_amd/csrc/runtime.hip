@@ -111,10 +111,38 @@ static bool fits32(const vkhip_tensor& t) {
 
 static bool is_f32(const vkhip_tensor& t) { return t.dtype == VKHIP_F32; }
 
+// Elementwise nodes write a contiguous output and read sources already
+// broadcast to its extents (stride 0 on broadcast axes), as the reference's
+// executor hands them over.
+static bool elementwise_layout(const vkhip_node& nd) {
+    if (!contiguous(nd.out)) return false;
+    for (int s = 0; s < nd.n_src; ++s) {
+        if (nd.src[s].ndim != nd.out.ndim) return false;
+        for (int i = 0; i < nd.out.ndim; ++i)
+            if (nd.src[s].ne[i] != nd.out.ne[i]) return false;
+    }
+    return true;
+}
+
+static bool is_elementwise(int op) {
+    switch (op) {
+        case VKHIP_OP_FULL: case VKHIP_OP_ARANGE: case VKHIP_OP_CONTIGUOUS: case VKHIP_OP_CAST:
+        case VKHIP_OP_NEG: case VKHIP_OP_EXP: case VKHIP_OP_LOG: case VKHIP_OP_RELU:
+        case VKHIP_OP_ADD: case VKHIP_OP_SUB: case VKHIP_OP_MUL: case VKHIP_OP_DIV:
+        case VKHIP_OP_SCALED_ADD: case VKHIP_OP_MAXIMUM: case VKHIP_OP_MINIMUM:
+        case VKHIP_OP_EQUAL: case VKHIP_OP_LESS: case VKHIP_OP_GREATER: case VKHIP_OP_LESS_EQUAL:
+        case VKHIP_OP_GREATER_EQUAL: case VKHIP_OP_NOT_EQUAL: case VKHIP_OP_WHERE:
+            return true;
+        default: return false;
+    }
+}
+
 static int supports_node(const vkhip_node& nd) {
     if (!fits32(nd.out)) return 0;
+    if (nd.n_src < 0 || nd.n_src > 3) return 0;
     for (int s = 0; s < nd.n_src; ++s)
         if (!fits32(nd.src[s])) return 0;
+    if (is_elementwise(nd.op) && !elementwise_layout(nd)) return 0;
     const vkhip_tensor& o = nd.out;
     switch (nd.op) {
         case VKHIP_OP_FULL:
