@@ -284,6 +284,27 @@ def test_softmax_stability(hip, name, log):
     np.testing.assert_allclose(got, O.softmax(x, -1, log), rtol=1e-5, atol=1e-6)
 
 
+def test_softmax_exponential_accuracy(hip):
+    """The softmax kernels' exponential, read back exactly: for a row [0, s]
+    with s < -17, 1 + exp(s) rounds to 1, so the second output IS exp(s).
+    Within 2 ulp of the correctly rounded exp for normal results, within
+    2^-126 below; rows [0, s] with s in (-17, 0] stay within 4 ulp of
+    exp(s) / (1 + exp(s))."""
+    s = np.concatenate([np.linspace(-103.0, -17.0, 4001), np.linspace(-17.0, 0.0, 2001)[1:]])
+    s = s.astype(np.float32)
+    rows = np.stack([np.zeros_like(s), s], axis=1)
+    got = ops.softmax(dev(rows), -1).numpy()[:, 1].astype(np.float64)
+    e = np.exp(s.astype(np.float64))
+    want = np.where(s < -17.0, e, e / (1.0 + e))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    normal = want >= 2.0 ** -126
+    deep = s < -17.0
+    err = np.abs(got - want) / ulp
+    assert err[normal & deep].max() <= 2.0, err[normal & deep].max()
+    assert err[normal & ~deep].max() <= 4.0, err[normal & ~deep].max()
+    assert np.abs(got - want)[~normal].max() <= 2.0 ** -126
+
+
 def test_softmax_non_last_axis(hip):
     x = np.random.default_rng(1).standard_normal((6, 37, 5)).astype(np.float32)
     for axis in (0, 1):

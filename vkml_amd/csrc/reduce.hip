@@ -127,18 +127,34 @@ __device__ __forceinline__ uint32_t elem_of(int vec, int T, int t, int i) {
     return vec ? 4u * (t + T * (i / 4)) + (i % 4) : static_cast<uint32_t>(t + T * i);
 }
 
-// ---- softmax over contiguous rows ------------------------------------------------
-// Division by the row's denominator d with its reciprocal r = 1/d (correctly
-// rounded, computed once per row): q0 = x*r, then one fused correction
-// q = q0 + (x - q0*d)*r. For a normal quotient this is the correctly rounded
-// x/d (Markstein's theorem; Muller et al., Handbook of Floating-Point
-// Arithmetic, 2nd ed., sec. 4.7), so it agrees with the oracle's expf(.)/denom;
-// a subnormal quotient may differ from it by one subnormal unit.
-__device__ __forceinline__ float div_by(float x, float d, float r) {
-    const float q0 = x * r;
-    const float e = __builtin_fmaf(-q0, d, x);
-    return __builtin_fmaf(e, r, q0);
+// ---- exp for softmax ------------------------------------------------------------
+// exp(s) for the softmax shifts s = x - peak <= 0 (or NaN): 2^(s*log2 e) on the
+// hardware base-2 exponential (v_exp_f32), with the rounding error of s*log2 e
+// carried along. log2 e = kL2eHi + kL2eLo (kL2eHi its float rounding); the
+// product's exact remainder comes from one FMA (the 2MultFMA algorithm, Muller
+// et al., Handbook of Floating-Point Arithmetic, 2nd ed., sec. 4.4.2), and
+// 2^(t + r) = 2^t (1 + r ln 2) to within (r ln 2)^2 / 2 < 2^-41 for |r| < 2^-20.
+// The result is within about 2 ulp of exp(s) (against ~1 for the general expf,
+// in a third of the instructions: the softmax kernels are instruction-bound at
+// 32768-wide rows). Shifts below -150 (and -inf) give 0; the general expf keeps
+// subnormal results down to -103.97, a difference of less than 2^-126.
+__device__ __forceinline__ float softmax_exp(float s) {
+    constexpr float kL2eHi = 1.44269502162933349609375f;
+    constexpr float kL2eLo = 1.925963033500011e-08f;
+    constexpr float kLn2 = 0.6931471805599453f;
+    const float t = s * kL2eHi;
+    const float r = __builtin_fmaf(s, kL2eLo, __builtin_fmaf(s, kL2eHi, -t));
+    const float e = __builtin_amdgcn_exp2f(t);
+    const float v = __builtin_fmaf(e, r * kLn2, e);
+    return t < -150.0f ? 0.0f : v;
 }
+
+// ---- softmax over contiguous rows ------------------------------------------------
+// Outputs are exp(x - peak) * (1/denom): one multiply per element by the
+// row's correctly rounded reciprocal, within 1.5 ulp of the quotient (the
+// exponential above is the larger error term; softmax parity is tolerance-
+// based, 1e-5 * sqrt(n) relative).
+__device__ __forceinline__ float div_by(float x, float /*d*/, float r) { return x * r; }
 
 // T threads per row (64: four rows per 256-thread block), rows of n <= 4*E4*T
 // contiguous floats at src + row*in_stride; dst rows contiguous. The row is read
@@ -172,7 +188,7 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
     for (int i = 0; i < E; ++i) {
         const uint32_t e = elem_of(vec, T, t, i);
         const float sh = x[i] - mx;
-        const float ex = expf(sh);
+        const float ex = softmax_exp(sh);
         if (live && e < n) stage[stage_index(e)] = ex;
         x[i] = LOG ? sh : ex;
     }
@@ -231,7 +247,10 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
     float xn[E];
     load_row<64, E4>(xn, src + static_cast<int64_t>(row < rows ? row : 0) * in_stride, n, t,
                      row < rows, vec);
-    const uint32_t leaves = 1u << depth;
+    // n <= 2048 gives at most 64 leaves: lane t owns leaf t, the same range
+    // for every row, so it is computed once.
+    uint32_t leaf_b = 0, leaf_e = 0;
+    if (static_cast<uint32_t>(t) < (1u << depth)) pairwise_leaf(n, depth, t, leaf_b, leaf_e);
     for (; row < rows; row += stride) {
         float x[E];
 #pragma unroll
@@ -245,16 +264,30 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
         mx = wave_max(mx);
 #pragma unroll
         for (int i = 0; i < E; ++i) {
-            const uint32_t e = elem_of(vec, 64, t, i);
             const float sh = x[i] - mx;
-            const float ex = expf(sh);
-            if (e < n) stage[stage_index(e)] = ex;
-            x[i] = LOG ? sh : ex;
+            x[i] = LOG ? sh : softmax_exp(sh);
+            if (LOG) {
+                if (!VEC && elem_of(vec, 64, t, i) < n) stage[stage_index(elem_of(vec, 64, t, i))] = softmax_exp(sh);
+            } else if (!VEC) {
+                if (elem_of(vec, 64, t, i) < n) stage[stage_index(elem_of(vec, 64, t, i))] = x[i];
+            }
+        }
+        if constexpr (VEC) {
+            // Four consecutive elements of one 32-element block: one 16-byte write.
+#pragma unroll
+            for (int i = 0; i < E4; ++i) {
+                const uint32_t e0 = 4u * (t + 64 * i);
+                if (e0 < n) {
+                    f32x4 w;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        w[j] = LOG ? softmax_exp(x[4 * i + j]) : x[4 * i + j];
+                    *reinterpret_cast<f32x4*>(stage + stage_index(e0)) = w;
+                }
+            }
         }
         wave_lds_fence();
-        const uint32_t per = leaves > 64 ? leaves / 64 : 1u;
-        float v = 0.0f;
-        if (static_cast<uint32_t>(t) * per < leaves) v = staged_subtree_sum(stage, n, depth, t * per, per);
+        const float v = leaf_e > leaf_b ? staged_leaf_sum(stage, leaf_b, leaf_e) : 0.0f;
         const float denom = wave_sum_butterfly(v);
         wave_lds_fence();  // every lane's stage reads precede the next row's writes
         const float ld = logf(denom);
@@ -278,74 +311,6 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
                 if (e < n) ds[e] = LOG ? x[i] - ld : div_by(x[i], denom, rinv);
             }
         }
-    }
-}
-
-// ---- softmax over long rows of 32 * 2^q elements, leaves in registers -------------------
-// T threads per row; thread t owns the PER consecutive 32-element leaves
-// starting at leaf t*PER, i.e. one contiguous run of 32*PER floats, loaded as
-// 16-byte vectors. With every leaf exactly 32 long, the oracle's pairwise tree
-// is: a sequential sum inside each leaf, then a balanced tree over leaves,
-// which is the thread's carry fold followed by the butterfly. No LDS staging.
-template <int T, int PER, bool LOG>
-__global__ __launch_bounds__(T) void softmax_leaf_rows_kernel(const float* __restrict__ src,
-                                                              int64_t in_stride,
-                                                              float* __restrict__ dst,
-                                                              uint32_t rows) {
-    constexpr int E = 32 * PER;
-    constexpr uint32_t n = static_cast<uint32_t>(T) * E;
-    __shared__ float scratch[T / 64];
-    const int t = threadIdx.x;
-    const uint32_t row = blockIdx.x;
-    const float* rs = src + static_cast<int64_t>(row) * in_stride + static_cast<uint32_t>(t) * E;
-    float x[E];
-#pragma unroll
-    for (int i = 0; i < E / 4; ++i) {
-        const f32x4 v = reinterpret_cast<const f32x4*>(rs)[i];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x[4 * i + j] = v[j];
-    }
-    bool keep[E];
-#pragma unroll
-    for (int i = 0; i < E; ++i) keep[i] = true;
-    float mx = tree_peak<E>(x, keep);
-    mx = group_max<T>(mx, t, scratch);
-    float leaf[PER];
-#pragma unroll
-    for (int l = 0; l < PER; ++l) {
-        float a = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const float sh = x[32 * l + i] - mx;
-            const float ex = expf(sh);
-            a = a + ex;
-            x[32 * l + i] = LOG ? sh : ex;
-        }
-        leaf[l] = a;
-    }
-    // Balanced fold of this thread's PER leaves (PER is a power of two).
-#pragma unroll
-    for (int w = 1; w < PER; w <<= 1)
-#pragma unroll
-        for (int l = 0; l < PER; l += 2 * w) leaf[l] = leaf[l] + leaf[l + w];
-    float v = wave_sum_butterfly(leaf[0]);
-    const int lane = t & 63, wv = t >> 6;
-    if constexpr (T > 64) {
-        if (lane == 0) scratch[wv] = v;
-        __syncthreads();
-        const float u = lane < T / 64 ? scratch[lane] : 0.0f;
-        v = wave_sum_butterfly(u);
-    }
-    const float denom = v;
-    const float ld = logf(denom);
-        const float rinv = 1.0f / denom;
-    float* ds = dst + static_cast<uint64_t>(row) * n + static_cast<uint32_t>(t) * E;
-#pragma unroll
-    for (int i = 0; i < E / 4; ++i) {
-        f32x4 o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = LOG ? x[4 * i + j] - ld : div_by(x[4 * i + j], denom, rinv);
-        reinterpret_cast<f32x4*>(ds)[i] = o;
     }
 }
 
@@ -1119,7 +1084,7 @@ __global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restri
         uint32_t b, e;
         pairwise_leaf(n, depth, j, b, e);
         float s = 0.0f;
-        for (uint32_t q = b; q < e; ++q) s = s + expf(base[rd.off(q)] - peak);
+        for (uint32_t q = b; q < e; ++q) s = s + softmax_exp(base[rd.off(q)] - peak);
         bool carry = true;
 #pragma unroll
         for (int l = 0; l < kTallLevels; ++l) {
@@ -1140,37 +1105,20 @@ __global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restri
     const float ld = logf(denom);
     for (uint32_t i = 0; i < n; ++i) {
         const float sh = base[rd.off(i)] - peak;
-        obase[ord.off(i)] = log_mode ? sh - ld : expf(sh) / denom;
+        obase[ord.off(i)] = log_mode ? sh - ld : softmax_exp(sh) / denom;
     }
 }
 
-// Rows of exactly 32 * 2^q floats (4096..32768, 16-byte aligned): leaves
-// straight from registers, one workgroup per row.
-static bool leaf_rows_width(uint32_t n) {
-    return n == 32768 || n == 16384 || n == 8192 || n == 4096;
-}
-
-// Contiguous rows handled without the row classes: register-leaf rows, or,
-// up to 2048 floats, a persistent wave per row with next-row prefetch.
+// Contiguous rows of up to 2048 floats: a wave per row, persistent with
+// next-row prefetch when there are more rows than waves. (A variant that kept
+// each thread's own 32-float leaves in registers for 4096..32768-wide rows was
+// measured and dropped: each lane reading 128 contiguous bytes runs the loads
+// at 3.6 TB/s against 5.8 for lane-interleaved 16-byte loads, so the staged
+// row-class kernel is faster at those widths: 256x32768 in 18.7 against
+// 22.8 us.)
 template <bool LOG>
 static int launch_softmax_short(const float* src, int64_t row_stride, float* dst, uint32_t rows,
                                 uint32_t n, int depth, int vec, hipStream_t st) {
-    if (vec && leaf_rows_width(n)) {
-        if (n == 32768)
-            hipLaunchKernelGGL((softmax_leaf_rows_kernel<1024, 1, LOG>), dim3(rows), dim3(1024), 0,
-                               st, src, row_stride, dst, rows);
-        else if (n == 16384)
-            hipLaunchKernelGGL((softmax_leaf_rows_kernel<512, 1, LOG>), dim3(rows), dim3(512), 0,
-                               st, src, row_stride, dst, rows);
-        else if (n == 8192)
-            hipLaunchKernelGGL((softmax_leaf_rows_kernel<256, 1, LOG>), dim3(rows), dim3(256), 0,
-                               st, src, row_stride, dst, rows);
-        else
-            hipLaunchKernelGGL((softmax_leaf_rows_kernel<128, 1, LOG>), dim3(rows), dim3(128), 0,
-                               st, src, row_stride, dst, rows);
-        VKHIP_LAUNCH_CHECK();
-        return VKHIP_OK;
-    }
     if (n > 2048) return fail(VKHIP_ERR_INVALID, "softmax: short-row path given n=%u", n);
     const uint32_t ss = stage_stride(n);
     const size_t lds = 4 * static_cast<size_t>(ss) * sizeof(float);
@@ -1226,7 +1174,7 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
         const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
                         (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (n % 4 == 0) &&
                         (row_stride % 4 == 0);
-        if (n <= 2048 || (vec && leaf_rows_width(n)))
+        if (n <= 2048)
             return log_mode ? launch_softmax_short<true>(src, row_stride, dst, rows, n, depth, vec, st)
                             : launch_softmax_short<false>(src, row_stride, dst, rows, n, depth, vec, st);
         const RowClass rc = row_class(n);

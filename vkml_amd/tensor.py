@@ -24,6 +24,7 @@ implicit fallback: an op the backend does not support raises.
 from __future__ import annotations
 
 import ctypes
+import struct
 import math
 from typing import Iterable, Sequence
 
@@ -623,13 +624,19 @@ def cross_entropy(logits: Tensor, target: Tensor) -> Tensor:
 # Executor
 # ---------------------------------------------------------------------------
 
-def _fill_desc(d: _lib.TensorDesc, n: Node) -> None:
-    d.data = n.storage.ptr + n.offset * n.itemsize if n.storage is not None else 0
-    d.dtype = _VK_DTYPE[n.dtype]
-    d.ndim = len(n.shape)
-    for i, (e, s) in enumerate(zip(n.shape, n.strides)):
-        d.ne[i] = e
-        d.nb[i] = s
+# One vkhip_node record (include/vkhip.h): op, n_src, out, src[3], params[64];
+# a vkhip_tensor is data, dtype, ndim, ne[4], nb[4] (extents and strides
+# left-aligned, unused slots 0). Packed with one struct call per node.
+_NODE_RECORD = struct.Struct("<ii" + "Qii4q4q" * 4 + "64s")
+_NO_TENSOR = (0,) * 11
+_PADS = tuple((0,) * (4 - k) for k in range(5))
+assert _NODE_RECORD.size == ctypes.sizeof(_lib.NodeDesc)
+
+
+def _tensor_fields(n: Node) -> tuple:
+    pad = _PADS[len(n.shape)]
+    data = n.storage.ptr + n.offset * n.dtype.itemsize if n.storage is not None else 0
+    return (data, _VK_DTYPE[n.dtype], len(n.shape)) + n.shape + pad + n.strides + pad
 
 
 def realize(tensors: Iterable[Tensor]) -> None:
@@ -638,25 +645,25 @@ def realize(tensors: Iterable[Tensor]) -> None:
     roots = [t.node for t in tensors if t is not None and not t.node.computed]
     if not roots:
         return
+    # Post-order walk of the uncomputed subgraph: a node is emitted once all
+    # of its sources are computed or emitted (sources in order, so the
+    # sequence is the one a recursive walk from the roots would give).
     order: list[Node] = []
     seen: set[int] = set()
-    stack = [(r, 0) for r in reversed(roots)]
+    stack = list(reversed(roots))
     while stack:
-        node, i = stack.pop()
-        if id(node) in seen and i == 0:
+        node = stack[-1]
+        nid = id(node)
+        if nid in seen:
+            stack.pop()
             continue
-        if node.computed:
-            seen.add(id(node))
+        waiting = [c for c in node.src if not c.computed and id(c) not in seen]
+        if waiting:
+            stack.extend(reversed(waiting))
             continue
-        if i < len(node.src):
-            stack.append((node, i + 1))
-            child = node.src[i]
-            if child is not None and id(child) not in seen and not child.computed:
-                stack.append((child, 0))
-            continue
-        if id(node) not in seen:
-            seen.add(id(node))
-            order.append(node)
+        stack.pop()
+        seen.add(nid)
+        order.append(node)
     by_backend: dict[int, list[Node]] = {}
     backends = {}
     for node in order:
@@ -672,17 +679,18 @@ def realize(tensors: Iterable[Tensor]) -> None:
         node.offset = 0
         by_backend.setdefault(id(node.backend), []).append(node)
         backends[id(node.backend)] = node.backend
+    size = _NODE_RECORD.size
     for key, nodes in by_backend.items():
-        arr = (_lib.NodeDesc * len(nodes))()
-        for d, node in zip(arr, nodes):
-            d.op = node.op
-            d.n_src = len(node.src)
-            _fill_desc(d.out, node)
-            for j, s in enumerate(node.src):
-                _fill_desc(d.src[j], s)
-            p = node.params
-            if p:
-                ctypes.memmove(ctypes.addressof(d.params), p, len(p))
+        buf = bytearray(size * len(nodes))
+        for k, node in enumerate(nodes):
+            src = node.src
+            fields = [node.op, len(src)]
+            fields += _tensor_fields(node)
+            for j in range(3):
+                fields += _tensor_fields(src[j]) if j < len(src) else _NO_TENSOR
+            fields.append(node.params or b"")
+            _NODE_RECORD.pack_into(buf, k * size, *fields)
+        arr = (_lib.NodeDesc * len(nodes)).from_buffer(buf)
         backends[key].compute(arr, len(nodes))
         for node in nodes:
             node.computed = True
