@@ -304,6 +304,50 @@ int vkhip_event_record(void* event);
 int vkhip_event_elapsed(void* start, void* end, float* out_ms);
 
 /* ======================================================================== */
+/* Observability: decision facts and per-dispatch timing                     */
+/* ======================================================================== */
+/* One choice the backend made, what it rejected, why, and the numbers that
+ * forced it (reference vkml::observe::Decision, include/vkml/util/observe.h:
+ * 55-93). Sites: "matmul.kernel", "matmul.split_k", "reduce.structure",
+ * "softmax.structure", "col2im.kernel", "max_pool2d.kernel",
+ * "allocator.release". The strings live for the duration of the callback
+ * only. `dispatch` names the unit of work the choice produced: the same id the
+ * profile records carry, so a consumer joins the two to learn what a kernel
+ * choice cost (vulkan_backend.h:123-131, 174-181). */
+typedef struct vkhip_decision {
+    const char* site;
+    const char* op;          /* the operation in the user's vocabulary */
+    const char* chose;
+    const char* instead_of;  /* "" when nothing was rejected */
+    const char* because;
+    int64_t required;        /* the numbers behind the choice; 0 when none */
+    int64_t available;
+    uint64_t dispatch;
+} vkhip_decision;
+typedef void (*vkhip_decision_fn)(const vkhip_decision* decision, void* user);
+/* Installs the one subscriber (NULL removes it), like observe::subscribe
+ * (observe.h:108-119). Decisions are published synchronously on the calling
+ * thread, before the work they choose is enqueued. */
+int vkhip_subscribe_decisions(vkhip_decision_fn fn, void* user);
+
+/* One measured unit of work: a node of vkhip_compute or one call of a
+ * per-op entry point (reference ProfileRecord, vulkan_backend.h:123-131). */
+typedef struct vkhip_profile_record {
+    char label[48];    /* the op ("matmul", "softmax", ...) */
+    double gpu_ms;     /* HIP-event time of the unit's launches on the stream */
+    uint64_t dispatch; /* joins with vkhip_decision.dispatch */
+} vkhip_profile_record;
+/* Enables per-unit event timing (set_profiling, vulkan_backend.h:165-166);
+ * zero cost when off. Records accumulate until read (at most 65536 pending;
+ * older ones are dropped and counted). */
+int vkhip_set_profiling(int enabled);
+/* Waits for the recorded work, moves up to `capacity` of the oldest pending
+ * records to `out` and sets *count; *dropped (may be NULL) gets the number
+ * of records dropped since the last read. */
+int vkhip_profile_read(vkhip_profile_record* out, size_t capacity, size_t* count,
+                       uint64_t* dropped);
+
+/* ======================================================================== */
 /* Host-side planning helpers (callable without a GPU)                       */
 /* ======================================================================== */
 /* Geometry of the CPU oracle's pairwise-summation tree (reference

@@ -491,6 +491,46 @@ def test_caching_allocator_reuses_and_accounts(hip):
     assert lib.vkhip_free(c_void_p(0x1000)) == _lib.ERR_INVALID
 
 
+def test_decision_facts_join_profile_records(hip):
+    """Decision facts name the kernel each op chose with the numbers behind it,
+    and their dispatch ids join with the per-unit timing records (reference
+    observe::Decision and ProfileRecord)."""
+    from vkml_amd.device import DecisionRecorder
+
+    rng = np.random.default_rng(SEED + 77)
+    a = dev(rng.standard_normal((256, 65536)).astype(np.float32))
+    b = dev(rng.standard_normal((65536, 256)).astype(np.float32))
+    x = dev(rng.standard_normal((4096, 1000)).astype(np.float32))
+    g = dev(rng.standard_normal((16, 64, 32, 32)).astype(np.float32))
+    hip.set_profiling(True)
+    hip.profile_records()
+    with DecisionRecorder() as rec:
+        ops.matmul(a, b)
+        ops.softmax(x, -1)
+        ops.sum(g, [0, 2, 3])
+    records = hip.profile_records()
+    hip.set_profiling(False)
+    by_site = {}
+    for d in rec.decisions:
+        by_site.setdefault(d["site"], []).append(d)
+    splits, _ = ops.gemm_plan(1, 256, 256, 65536)
+    kern = by_site["matmul.kernel"][-1]
+    assert kern["chose"] == "gemm_mfma_128x128" and kern["required"] == 4
+    assert kern["available"] == hip.capabilities().compute_units
+    split = by_site["matmul.split_k"][-1]
+    assert split["chose"] == f"split_k_{splits}" and split["dispatch"] == kern["dispatch"]
+    soft = by_site["softmax.structure"][-1]
+    assert soft["chose"] == "softmax_wave_per_row" and (soft["required"], soft["available"]) == (1000, 4096)
+    red = by_site["reduce.structure"][-1]
+    assert red["chose"] == "reduce_split_tree" and (red["required"], red["available"]) == (16 * 1024, 64)
+    timed = {r["dispatch"]: r for r in records}
+    for d, label in ((kern, "matmul"), (soft, "softmax"), (red, "reduce")):
+        assert timed[d["dispatch"]]["label"] == label and timed[d["dispatch"]]["gpu_ms"] > 0
+    assert len({kern["dispatch"], soft["dispatch"], red["dispatch"]}) == 3
+    ops.matmul(a, b)
+    assert hip.profile_records() == []  # profiling off again
+
+
 def test_errors_are_reported_not_crashed(hip):
     a = dev(np.ones((3, 4), np.float32))
     b = dev(np.ones((5, 6), np.float32))

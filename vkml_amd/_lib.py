@@ -63,6 +63,19 @@ class Copy(ctypes.Structure):
     _fields_ = [("dst", c_void_p), ("src", c_void_p), ("nbytes", c_size_t)]
 
 
+class Decision(ctypes.Structure):
+    _fields_ = [("site", c_char_p), ("op", c_char_p), ("chose", c_char_p),
+                ("instead_of", c_char_p), ("because", c_char_p), ("required", c_int64),
+                ("available", c_int64), ("dispatch", c_uint64)]
+
+
+DECISION_FN = ctypes.CFUNCTYPE(None, POINTER(Decision), c_void_p)
+
+
+class ProfileRecord(ctypes.Structure):
+    _fields_ = [("label", c_char * 48), ("gpu_ms", ctypes.c_double), ("dispatch", c_uint64)]
+
+
 class GemmOpts(ctypes.Structure):
     _fields_ = [("kernel", c_int32), ("split_k", c_int32)]
 
@@ -79,6 +92,10 @@ SIGNATURES = {
     "vkhip_free": (c_int, [c_void_p]),
     "vkhip_release_cached": (c_int, []),
     "vkhip_memory_stats": (c_int, [POINTER(c_size_t), POINTER(c_size_t)]),
+    "vkhip_subscribe_decisions": (c_int, [DECISION_FN, c_void_p]),
+    "vkhip_set_profiling": (c_int, [c_int]),
+    "vkhip_profile_read": (c_int, [POINTER(ProfileRecord), c_size_t, POINTER(c_size_t),
+                                   POINTER(c_uint64)]),
     "vkhip_copy_from_host": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vkhip_copy_to_host": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vkhip_copy_device_to_device": (c_int, [POINTER(Copy), c_size_t]),

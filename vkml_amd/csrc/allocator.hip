@@ -73,6 +73,9 @@ int cached_alloc(size_t nbytes, void** out) {
         void* p = nullptr;
         if (hipMalloc(&p, sz) != hipSuccess) {
             (void)hipGetLastError();
+            publish("allocator.release", "alloc", "release_cached", "",
+                    "an allocation failed: cached blocks go back to HIP and it is retried",
+                    static_cast<int64_t>(sz), static_cast<int64_t>(c.bytes_cached));
             int st = release_locked(c);
             if (st != VKHIP_OK) return st;
             if (hipMalloc(&p, sz) != hipSuccess) {

@@ -41,6 +41,20 @@ int require_ready();
 // Workspace of at least `bytes` on the current stream.
 int workspace(size_t bytes, float** out);
 
+// Decision facts and units of work (observe.hip). A unit is a node of
+// vkhip_compute or one per-op entry call; decisions published inside it carry
+// its dispatch id.
+void publish(const char* site, const char* op, const char* chose, const char* instead_of,
+             const char* because, int64_t required, int64_t available);
+void unit_begin(const char* label);
+void unit_end();
+struct Unit {
+    explicit Unit(const char* label) { unit_begin(label); }
+    ~Unit() { unit_end(); }
+    Unit(const Unit&) = delete;
+    Unit& operator=(const Unit&) = delete;
+};
+
 // The caching allocator behind vkhip_alloc / vkhip_free (allocator.hip).
 int cached_alloc(size_t nbytes, void** out);
 int cached_free(void* ptr);

@@ -352,6 +352,7 @@ extern "C" int vkhip_scaled_add(const float* a, const float* b, float* out, uint
                                 float beta) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("scaled_add");
     vkhip_node nd{};
     nd.op = VKHIP_OP_SCALED_ADD;
     nd.n_src = 2;

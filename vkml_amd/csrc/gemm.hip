@@ -472,6 +472,8 @@ static void plan_split_k(uint32_t tiles, uint32_t ktiles, uint64_t out_elems, ui
 
 struct TileChoice {
     int bm, bn;
+    const char* why = "";   // the reason, for the matmul.kernel decision fact
+    uint64_t tiles = 0;     // output tiles of this tiling
 };
 
 template <int BM, int BN, int WM, int WN, int AM>
@@ -567,14 +569,18 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
     const uint32_t req = split_request > 1 ? static_cast<uint32_t>(split_request) : 0u;
     bool want_split = false;
     if (t128 >= cu && !narrow) {
-        tile = {128, 128};
+        tile = {128, 128, "128x128 tiles give every CU a workgroup"};
     } else if (t64 >= cu) {
-        tile = {64, 64};
+        tile = {64, 64, narrow ? "128x128 tiles would pad the output by more than 25%"
+                               : "only 64x64 tiles give every CU a workgroup"};
     } else {
         const uint64_t target128 = (cu + t128 - 1) / t128;
-        tile = (!narrow && ktiles / target128 >= 8) ? TileChoice{128, 128} : TileChoice{64, 64};
+        tile = (!narrow && ktiles / target128 >= 8)
+                   ? TileChoice{128, 128, "too few output tiles: K split over 128x128 tiles"}
+                   : TileChoice{64, 64, "too few output tiles: K split over 64x64 tiles"};
         want_split = true;
     }
+    tile.tiles = tile.bm == 128 ? t128 : t64;
     if (split_request == 1) return VKHIP_OK;  // OFF
     if (!want_split && req == 0) return VKHIP_OK;
     const uint64_t tiles = tile.bm == 128 ? t128 : t64;
@@ -611,6 +617,9 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     // problem, not a matrix-core one. AUTO takes it whenever batch == 1.
     if ((kernel == VKHIP_GEMM_GEMV || kernel == VKHIP_GEMM_AUTO) && n == 1 && batch == 1 &&
         ad.nb[3] == 1 && (k <= static_cast<uint32_t>(kGemvMaxK) || (bd.nb[2] == 1 && k <= 32768))) {
+        publish("matmul.kernel", "matmul", "gemv", "gemm_mfma",
+                kernel == VKHIP_GEMM_GEMV ? "GEMV requested" : "an N == 1 product is bandwidth-bound",
+                static_cast<int64_t>(k), static_cast<int64_t>(m));
         return launch_gemv(a, ad.nb[2], b, bd.nb[2], c, m, k);
     }
     if (kernel == VKHIP_GEMM_GEMV)
@@ -619,6 +628,20 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     uint32_t splits, chunk;
     TileChoice tile;
     gemm_plan(static_cast<uint32_t>(batch), m, n, k, split_req, splits, chunk, tile);
+    {
+        const int64_t cus = ctx().ready ? ctx().caps.compute_units : 256;
+        publish("matmul.kernel", "matmul", tile.bm == 128 ? "gemm_mfma_128x128" : "gemm_mfma_64x64",
+                tile.bm == 128 ? "gemm_mfma_64x64" : "gemm_mfma_128x128", tile.why,
+                static_cast<int64_t>(tile.tiles), cus);
+        char chose[32] = "unsplit";
+        if (splits > 1) snprintf(chose, sizeof chose, "split_k_%u", splits);
+        publish("matmul.split_k", "matmul", chose, splits > 1 ? "unsplit" : "split_k",
+                split_req > 1    ? "partition count requested"
+                : split_req == 1 ? "split-K turned off"
+                : splits > 1     ? "output tiles below one workgroup per CU"
+                                 : "output tiles fill the CUs",
+                static_cast<int64_t>(tile.tiles) * splits, cus);
+    }
 
     GemmArgs g{};
     g.a = a;
@@ -681,6 +704,7 @@ extern "C" int vkhip_gemm(const float* a, const vkhip_operand* a_desc, const flo
                           const vkhip_operand* b_desc, float* c, const vkhip_gemm_opts* opts) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("matmul");
     if (!a_desc || !b_desc) return vkhip::fail(VKHIP_ERR_INVALID, "gemm: null descriptor");
     return vkhip::gemm(a, *a_desc, b, *b_desc, c, opts);
 }
@@ -698,6 +722,7 @@ extern "C" int vkhip_gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t 
 extern "C" int vkhip_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("split_k_reduce");
     if (splits == 0 || splits > 511)
         return vkhip::fail(VKHIP_ERR_INVALID, "split_k_reduce: splits=%u outside 1..511", splits);
     return vkhip::launch_split_k_reduce(ws, dst, ne, splits);
@@ -707,5 +732,6 @@ extern "C" int vkhip_gemv(const float* a, int64_t lda, const float* x, int64_t i
                           uint32_t m, uint32_t k) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("gemv");
     return vkhip::launch_gemv(a, lda, x, incx, y, m, k);
 }

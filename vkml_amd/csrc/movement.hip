@@ -309,7 +309,12 @@ int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
     if (planes == 0 || g.H == 0 || g.W == 0) return VKHIP_OK;
     const uint64_t L = static_cast<uint64_t>(g.out_h) * g.out_w;
     const uint64_t plane_floats = L * g.kh * g.kw;
-    if (plane_floats * sizeof(float) <= 65536 && planes <= 0x7fffffffull) {
+    const bool staged = plane_floats * sizeof(float) <= 65536 && planes <= 0x7fffffffull;
+    publish("col2im.kernel", "col2im", staged ? "col2im_staged" : "col2im_direct",
+            staged ? "col2im_direct" : "col2im_staged",
+            staged ? "an image plane's columns fit in 64 KB of LDS" : "a plane's columns exceed 64 KB",
+            static_cast<int64_t>(plane_floats * sizeof(float)), 65536);
+    if (staged) {
         const int vec_in = (plane_floats % 4 == 0) && (reinterpret_cast<uintptr_t>(cols) % 16 == 0);
         const int vec_out = (static_cast<uint64_t>(g.H) * g.W % 4 == 0) &&
                             (reinterpret_cast<uintptr_t>(dst) % 16 == 0);
@@ -545,7 +550,12 @@ int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uin
     const uint64_t planes = static_cast<uint64_t>(sd.ne[0]) * sd.ne[1];
     const uint32_t ohw = out_h * out_w;
     if (planes == 0 || ohw == 0) return VKHIP_OK;
-    if (pool2x2_tiles(g, sd, src, dst, nullptr)) {
+    const bool tiled = pool2x2_tiles(g, sd, src, dst, nullptr);
+    publish("max_pool2d.kernel", "max_pool2d", tiled ? "max_pool2x2_tiled" : "max_pool2d_general",
+            tiled ? "max_pool2d_general" : "max_pool2x2_tiled",
+            tiled ? "2x2 windows at stride 2 tile the plane" : "windows overlap, pad or dilate",
+            g.kh * g.kw, g.sh * g.sw);
+    if (tiled) {
         const uint64_t total = planes * ohw / 2;
         if (total <= 0xffffffffull) {
             hipLaunchKernelGGL(max_pool2x2_kernel, dim3(ceil_div(static_cast<uint32_t>(total), 256)),
@@ -576,7 +586,13 @@ int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_
     const uint64_t planes = static_cast<uint64_t>(sd.ne[0]) * sd.ne[1];
     const uint32_t hw = static_cast<uint32_t>(g.H) * g.W;
     if (planes == 0 || hw == 0) return VKHIP_OK;
-    if (pool2x2_tiles(g, sd, src, dst, grad)) {
+    const bool tiled = pool2x2_tiles(g, sd, src, dst, grad);
+    publish("max_pool2d.kernel", "max_pool2d_backward",
+            tiled ? "max_pool2x2_tiled" : "max_pool2d_general",
+            tiled ? "max_pool2d_general" : "max_pool2x2_tiled",
+            tiled ? "2x2 windows at stride 2 tile the plane" : "windows overlap, pad or dilate",
+            g.kh * g.kw, g.sh * g.sw);
+    if (tiled) {
         const uint64_t total = planes * out_h * out_w / 2;
         if (total <= 0xffffffffull) {
             hipLaunchKernelGGL(max_pool2x2_backward_kernel,
@@ -600,6 +616,7 @@ extern "C" int vkhip_im2col(const float* src, const vkhip_operand* src_desc, flo
                             const vkhip_unfold* p) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("im2col");
     if (!src_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "im2col: null argument");
     return vkhip::launch_im2col(src, *src_desc, dst, *p);
 }
@@ -608,6 +625,7 @@ extern "C" int vkhip_col2im(const float* cols, float* dst, uint32_t n, uint32_t 
                             const vkhip_unfold* p) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("col2im");
     if (!p) return vkhip::fail(VKHIP_ERR_INVALID, "col2im: null params");
     return vkhip::launch_col2im(cols, dst, n, channels, *p);
 }

@@ -985,6 +985,17 @@ static int launch_softmax_rows(const float* src, int64_t stride, float* dst, uin
         default: return FN<1024, 8>(__VA_ARGS__);                          \
     }
 
+static const char* reduce_name(int op) {
+    switch (op) {
+        case VKHIP_REDUCE_SUM: return "sum";
+        case VKHIP_REDUCE_MEAN: return "mean";
+        case VKHIP_REDUCE_MAX: return "max";
+        case VKHIP_REDUCE_MIN: return "min";
+        case VKHIP_REDUCE_ARGMAX: return "argmax";
+        default: return "argmin";
+    }
+}
+
 int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst) {
     if (op < VKHIP_REDUCE_SUM || op > VKHIP_REDUCE_ARGMIN)
         return fail(VKHIP_ERR_INVALID, "reduce: unknown op %d", op);
@@ -1003,7 +1014,10 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
     // and long enough to feed it; otherwise a lane per output, which coalesces
     // when the kept axis is the contiguous one. Both give identical results.
     const bool wide = run && n_red >= 32 && (!sum_op || n_red <= kRowsMax);
+    const char* rname = reduce_name(op);
     if (wide) {
+        publish("reduce.structure", rname, "reduce_workgroup_tree", "reduce_lane_per_output",
+                "the reduced elements form one contiguous run per output", n_red, n_out);
         const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) && (n_red % 4 == 0) &&
                         (kept.nb[0] % 4 == 0) && (kept.nb[1] % 4 == 0) && (kept.nb[2] % 4 == 0) &&
                         (kept.nb[3] % 4 == 0);
@@ -1038,6 +1052,9 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
             ++split;
         if (((static_cast<uint64_t>(n_red) + (1ull << split) - 1) >> split) <= kSubtreeMax &&
             split > 0) {
+            publish("reduce.structure", rname, "reduce_split_tree", "reduce_lane_per_output",
+                    "few outputs over many strided elements: one workgroup per subtree",
+                    n_red, n_out);
             float* part = nullptr;
             int rc = workspace((static_cast<size_t>(n_out) << split) * sizeof(float), &part);
             if (rc != VKHIP_OK) return rc;
@@ -1052,12 +1069,16 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
         }
     }
     if (sum_op && n_red >= 8192 && n_out < 4 * cus) {
+        publish("reduce.structure", rname, "reduce_workgroup_strided", "reduce_split_tree",
+                "subtrees too long to stage in LDS", n_red, n_out);
         hipLaunchKernelGGL(reduce_wide_strided_kernel<256>, dim3(n_out), dim3(256), 0, st, src,
                            kept, rd, n_red, depth, op == VKHIP_REDUCE_MEAN ? 1 : 0,
                            static_cast<float*>(dst));
         VKHIP_LAUNCH_CHECK();
         return VKHIP_OK;
     }
+    publish("reduce.structure", rname, "reduce_lane_per_output", "reduce_workgroup_tree",
+            "the reduced elements are strided", n_red, n_out);
     hipLaunchKernelGGL(reduce_tall_kernel, dim3(ceil_div(n_out, 256)), dim3(256), 0, st, op, src,
                        kept, rd, static_cast<uint64_t>(n_out), n_red, depth, dst);
     VKHIP_LAUNCH_CHECK();
@@ -1174,6 +1195,11 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
         const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
                         (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (n % 4 == 0) &&
                         (row_stride % 4 == 0);
+        publish("softmax.structure", log_mode ? "log_softmax" : "softmax",
+                n <= 2048 ? "softmax_wave_per_row" : "softmax_workgroup_per_row",
+                "softmax_lane_per_row", n <= 2048 ? "rows of at most 2048 fit one wave's registers"
+                                                  : "long contiguous rows",
+                n, rows);
         if (n <= 2048)
             return log_mode ? launch_softmax_short<true>(src, row_stride, dst, rows, n, depth, vec, st)
                             : launch_softmax_short<false>(src, row_stride, dst, rows, n, depth, vec, st);
@@ -1181,6 +1207,8 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
         VKHIP_ROW_CLASSES(launch_softmax_rows, src, row_stride, dst, rows, n, depth, log_mode, vec, st)
     }
     // General layout: one thread per row.
+    publish("softmax.structure", log_mode ? "log_softmax" : "softmax", "softmax_lane_per_row",
+            "softmax_workgroup_per_row", "the softmax axis is not the contiguous one", n, rows);
     vkhip_operand od;
     int64_t s = 1;
     for (int i = 3; i >= 0; --i) {
@@ -1224,6 +1252,7 @@ extern "C" int vkhip_softmax(const float* src, const vkhip_operand* src_desc, fl
                              int log_softmax) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("softmax");
     if (!src_desc) return vkhip::fail(VKHIP_ERR_INVALID, "softmax: null descriptor");
     return vkhip::launch_softmax(src, *src_desc, dst, axis, log_softmax);
 }
@@ -1232,6 +1261,7 @@ extern "C" int vkhip_reduce(int op, const float* src, const vkhip_operand* src_d
                             uint32_t axes_mask, void* dst) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("reduce");
     if (!src_desc) return vkhip::fail(VKHIP_ERR_INVALID, "reduce: null descriptor");
     return vkhip::launch_reduce(op, src, *src_desc, axes_mask, dst);
 }

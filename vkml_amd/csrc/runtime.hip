@@ -224,11 +224,36 @@ static const char* op_name(int op) {
         case VKHIP_OP_ARGMAX: return "argmax";
         case VKHIP_OP_MAX_POOL2D: return "max_pool2d";
         case VKHIP_OP_MAX_POOL2D_BACKWARD: return "max_pool2d_backward";
+        case VKHIP_OP_MIN: return "min";
+        case VKHIP_OP_ARGMIN: return "argmin";
+        case VKHIP_OP_FULL: return "full";
+        case VKHIP_OP_ARANGE: return "arange";
+        case VKHIP_OP_CONTIGUOUS: return "contiguous";
+        case VKHIP_OP_CAST: return "cast";
+        case VKHIP_OP_NEG: return "neg";
+        case VKHIP_OP_EXP: return "exp";
+        case VKHIP_OP_LOG: return "log";
+        case VKHIP_OP_RELU: return "relu";
+        case VKHIP_OP_ADD: return "add";
+        case VKHIP_OP_SUB: return "sub";
+        case VKHIP_OP_MUL: return "mul";
+        case VKHIP_OP_DIV: return "div";
+        case VKHIP_OP_SCALED_ADD: return "scaled_add";
+        case VKHIP_OP_MAXIMUM: return "maximum";
+        case VKHIP_OP_MINIMUM: return "minimum";
+        case VKHIP_OP_EQUAL: return "equal";
+        case VKHIP_OP_LESS: return "less";
+        case VKHIP_OP_GREATER: return "greater";
+        case VKHIP_OP_LESS_EQUAL: return "less_equal";
+        case VKHIP_OP_GREATER_EQUAL: return "greater_equal";
+        case VKHIP_OP_NOT_EQUAL: return "not_equal";
+        case VKHIP_OP_WHERE: return "where";
         default: return "op";
     }
 }
 
 static int compute_node(const vkhip_node& nd) {
+    Unit unit(op_name(nd.op));
     if (!supports_node(nd))
         return fail(VKHIP_ERR_UNSUPPORTED, "vkhip: %s (op %d) is not supported for these dtypes/layout",
                     op_name(nd.op), nd.op);
@@ -452,6 +477,7 @@ extern "C" int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes
 extern "C" int vkhip_copy_device_to_device(const vkhip_copy* copies, size_t n) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("copy_device_to_device");
     for (size_t i = 0; i < n; ++i) {
         st = vkhip::launch_copy_bytes(copies[i].dst, copies[i].src, copies[i].nbytes);
         if (st != VKHIP_OK) return st;
@@ -486,6 +512,7 @@ extern "C" int vkhip_max_pool2d(const float* src, float* dst, uint32_t planes, u
                                 uint32_t out_w, const vkhip_unfold* p) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("max_pool2d");
     if (!p) return fail(VKHIP_ERR_INVALID, "max_pool2d: null params");
     vkhip_operand d;
     const uint32_t ne[4] = {1, planes, static_cast<uint32_t>(p->image_h), static_cast<uint32_t>(p->image_w)};
@@ -503,6 +530,7 @@ extern "C" int vkhip_max_pool2d_backward(const float* grad, const float* src, fl
                                          const vkhip_unfold* p) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("max_pool2d_backward");
     if (!p) return fail(VKHIP_ERR_INVALID, "max_pool2d_backward: null params");
     vkhip_operand d;
     const uint32_t ne[4] = {1, planes, static_cast<uint32_t>(p->image_h), static_cast<uint32_t>(p->image_w)};

@@ -258,6 +258,53 @@ class HipBackend:
         """Returns every cached free block to HIP (synchronises)."""
         check(self.lib.vkhip_release_cached(), "release_cached")
 
+    # -- observability (reference VulkanBackend::set_profiling /
+    #    last_profile_records, vulkan_backend.h:123-198; observe::subscribe) --
+    def set_profiling(self, enabled: bool) -> None:
+        check(self.lib.vkhip_set_profiling(1 if enabled else 0), "set_profiling")
+
+    def profile_records(self) -> list[dict]:
+        """Drains the pending per-unit timing records (waits for their work)."""
+        out = []
+        buf = (_lib.ProfileRecord * 1024)()
+        while True:
+            n, dropped = c_size_t(), ctypes.c_uint64()
+            check(self.lib.vkhip_profile_read(buf, 1024, byref(n), byref(dropped)), "profile_read")
+            out += [{"label": r.label.decode(), "gpu_ms": r.gpu_ms, "dispatch": r.dispatch}
+                    for r in buf[:n.value]]
+            if n.value < 1024:
+                return out
+
+
+class DecisionRecorder:
+    """Collects the backend's decision facts while active:
+
+        with DecisionRecorder() as rec:
+            ops.matmul(a, b)
+        rec.decisions  # [{"site": "matmul.kernel", "chose": ..., "dispatch": ...}, ...]
+
+    One subscriber at a time, as in the reference (observe.h:108-119)."""
+
+    def __init__(self):
+        self.decisions: list[dict] = []
+
+        def on_decision(d, _user):
+            x = d.contents
+            self.decisions.append({
+                "site": x.site.decode(), "op": x.op.decode(), "chose": x.chose.decode(),
+                "instead_of": x.instead_of.decode(), "because": x.because.decode(),
+                "required": x.required, "available": x.available, "dispatch": x.dispatch})
+
+        self._fn = _lib.DECISION_FN(on_decision)
+
+    def __enter__(self):
+        check(backend().lib.vkhip_subscribe_decisions(self._fn, None), "subscribe_decisions")
+        return self
+
+    def __exit__(self, *exc):
+        backend().lib.vkhip_subscribe_decisions(_lib.DECISION_FN(0), None)
+        return False
+
     def set_stream(self, stream_handle: int | None) -> None:
         check(self.lib.vkhip_set_stream(c_void_p(stream_handle or None)), "set_stream")
 
