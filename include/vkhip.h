@@ -124,7 +124,15 @@ enum vkhip_op {
     VKHIP_OP_COL2IM = 58,
     VKHIP_OP_MAX_POOL2D = 59,
     VKHIP_OP_MAX_POOL2D_BACKWARD = 60,
-    VKHIP_OP_WHERE = 64
+    VKHIP_OP_WHERE = 64,
+    /* Backend extensions (not vkML OpKind ordinals): the reference's
+     * cross_entropy composition (ops.cpp:417-441: mean(-sum(log_softmax(x) *
+     * one_hot(labels), -1))) fused per row, and its gradient as the reference
+     * autograd builds it (neg, sum and mul backward, then log_softmax backward
+     * g - exp(out) * sum(g), autograd.cpp). Values are those of the unfused
+     * graph, operation for operation; see vkhip_node below. */
+    VKHIP_OP_CROSS_ENTROPY = 96,          /* src0 logits [N,C] f32 (unit-stride rows), src1 labels [N] i64 -> out [N] f32: -sum_c(ls*onehot) */
+    VKHIP_OP_CROSS_ENTROPY_BACKWARD = 97  /* src0 logits, src1 labels, src2 g [N] f32 -> out [N,C] f32: d(out)/d(logits) */
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */
@@ -302,6 +310,30 @@ int vkhip_event_destroy(void* event);
 int vkhip_event_record(void* event);
 /* Milliseconds between two recorded events; waits for `end` to complete. */
 int vkhip_event_elapsed(void* start, void* end, float* out_ms);
+
+/* ======================================================================== */
+/* Fused optimiser step                                                      */
+/* ======================================================================== */
+/* One parameter of an SGD step: `param` is updated in place, `grad` is
+ * contiguous, `velocity` is the momentum buffer (unused when momentum == 0).
+ * `first` = 1 on a parameter's first momentum step (no previous velocity). */
+typedef struct vkhip_sgd_param {
+    float* param;
+    const float* grad;
+    float* velocity;
+    uint64_t n;
+    int32_t first;
+    int32_t reserved;
+} vkhip_sgd_param;
+/* The whole SGD step of the reference optimiser (python/vkml/optim.py:
+ * 146-199: weight decay g' = g + p*wd, velocity v = m*v + g' (v = g' on the
+ * first step), Nesterov direction g' + m*v, p = p - lr*direction) for every
+ * parameter in ONE launch, instead of the reference's two ScaledAdd nodes and a
+ * copy per parameter (scaled_add.comp:41-66). Each expression is evaluated
+ * exactly as those nodes do it: two rounded products and one rounded add, no
+ * FMA, so the values are bit-identical to the unfused step. */
+int vkhip_sgd_step(const vkhip_sgd_param* params, size_t count, float lr, float momentum,
+                   float weight_decay, int nesterov);
 
 /* ======================================================================== */
 /* Observability: decision facts and per-dispatch timing                     */

@@ -319,3 +319,25 @@ class OracleBackend:
 
     def synchronize(self) -> None:
         pass
+
+    def sgd_step(self, entries, lr: float, momentum: float, weight_decay: float,
+                 nesterov: bool) -> None:
+        """The fused optimiser step on host memory, as the reference's
+        ScaledAdd nodes compute it (python/vkml/optim.py:146-199,
+        scaled_add.comp:41-66): each a*alpha + b*beta is two float32 products
+        and one float32 sum (numpy rounds each operation), products by 1.0
+        being exact."""
+        f32 = np.float32
+        for p_st, g_st, goff, v_st, voff, n, first in entries:
+            p = np.ctypeslib.as_array(ctypes.cast(p_st.ptr, ctypes.POINTER(ctypes.c_float)), (n,))
+            g = np.ctypeslib.as_array(ctypes.cast(g_st.ptr + goff, ctypes.POINTER(ctypes.c_float)),
+                                      (n,)).copy()
+            if weight_decay != 0.0:
+                g = g + p * f32(weight_decay)
+            direction = g
+            if momentum != 0.0:
+                v = np.ctypeslib.as_array(ctypes.cast(v_st.ptr + voff, ctypes.POINTER(ctypes.c_float)),
+                                          (n,))
+                v[...] = g if first else v * f32(momentum) + g
+                direction = g + v * f32(momentum) if nesterov else v
+            p[...] = p + direction * f32(-lr)

@@ -424,6 +424,47 @@ static int64_t tnumel(const vkhip_tensor* t) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Cross-entropy rows: the reference composition (src/api/ops.cpp:417-441)
+ * evaluated operation by operation, for the backend's fused
+ * VKHIP_OP_CROSS_ENTROPY[_BACKWARD] nodes:
+ *   ls     = log_softmax(x) per row (as or_softmax computes it)
+ *   onehot = (float)label == (float)c        (Cast, Equal with arange, Cast)
+ *   out    = -pairwise_c(ls * onehot)        (Mul, Sum over C, Neg)
+ * and the gradient the reference autograd builds for it, given g = dL/dout:
+ *   gl = (-g) * onehot                       (Neg, Sum and Mul backward)
+ *   dx = gl - expf(ls) * pairwise_c(gl)      (LogSoftmax backward)
+ * Rows are x + r*row_stride, C contiguous floats; labels[N] int64. */
+/* ------------------------------------------------------------------------ */
+void or_cross_entropy(const float* x, int64_t row_stride, const int64_t* labels, const float* g,
+                      float* out, int64_t rows, int64_t c, int backward, int threads) {
+#pragma omp parallel num_threads(nthreads(threads))
+    {
+        float* buf = (float*)malloc(sizeof(float) * (size_t)(2 * c + 1));
+        float* ls = buf + c;
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            const float* row = x + r * row_stride;
+            float peak = -INFINITY;
+            for (int64_t k = 0; k < c; ++k) peak = (peak < row[k]) ? row[k] : peak;
+            for (int64_t k = 0; k < c; ++k) buf[k] = expf(row[k] - peak);
+            const float ld = logf(pairwise(buf, 0, c));
+            for (int64_t k = 0; k < c; ++k) ls[k] = (row[k] - peak) - ld;
+            const float label = (float)labels[r];
+            if (!backward) {
+                for (int64_t k = 0; k < c; ++k) buf[k] = ls[k] * (label == (float)k ? 1.0f : 0.0f);
+                out[r] = -pairwise(buf, 0, c);
+            } else {
+                const float ng = -g[r];
+                for (int64_t k = 0; k < c; ++k) buf[k] = ng * (label == (float)k ? 1.0f : 0.0f);
+                const float total = pairwise(buf, 0, c);
+                for (int64_t k = 0; k < c; ++k) out[r * c + k] = buf[k] - expf(ls[k]) * total;
+            }
+        }
+        free(buf);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* or_compute: the CPU backend's compute(span<Node*>) loop over the same node
  * records the device backend takes (reference CpuBackend::compute,
  * src/backend/cpu/cpu_backend.cpp, which looks each op up in its kernel table,
@@ -553,6 +594,16 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 memcpy(&p, nd->params, sizeof p);
                 or_max_pool2d_backward((const float*)nd->src[0].data, (const float*)nd->src[1].data, (float*)o->data,
                                        (uint32_t)(o->ne[0] * o->ne[1]), (uint32_t)nd->src[0].ne[2], (uint32_t)nd->src[0].ne[3], &p, threads);
+                break;
+            }
+            case VKHIP_OP_CROSS_ENTROPY:
+            case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
+                const int back = nd->op == VKHIP_OP_CROSS_ENTROPY_BACKWARD;
+                if (nd->src[0].ndim != 2 || nd->src[0].nb[1] != 1) return VKHIP_ERR_UNSUPPORTED;
+                or_cross_entropy((const float*)nd->src[0].data, nd->src[0].nb[0],
+                                 (const int64_t*)nd->src[1].data,
+                                 back ? (const float*)nd->src[2].data : NULL, (float*)o->data,
+                                 nd->src[0].ne[0], nd->src[0].ne[1], back, threads);
                 break;
             }
             default: return VKHIP_ERR_UNSUPPORTED;

@@ -71,3 +71,31 @@ def hip():
     from vkml_amd.device import backend
 
     return backend()
+
+
+# ---- cross-entropy helpers shared by the host-core and device training tests ----
+
+def ce_loss_and_grad(backend, logits, labels, fused):
+    """cross_entropy's loss and logits gradient on `backend`, built as the
+    fused CROSS_ENTROPY nodes (fused=True) or as the reference composition."""
+    from vkml_amd import tensor as T
+
+    prev = T.FUSED_CROSS_ENTROPY
+    T.FUSED_CROSS_ENTROPY = fused
+    try:
+        x = T.tensor(logits, requires_grad=True, backend=backend)
+        loss = T.cross_entropy(x, T.tensor(labels, backend=backend))
+        loss.backward()
+        return loss.numpy(), x.grad.numpy()
+    finally:
+        T.FUSED_CROSS_ENTROPY = prev
+
+
+def ce_inputs(shape, seed):
+    rng = np.random.default_rng(seed)
+    logits = (rng.standard_normal(shape) * 3).astype(np.float32)
+    labels = rng.integers(0, shape[1], shape[0]).astype(np.int64)
+    labels[0] = shape[1] - 1
+    if shape[0] > 2:
+        labels[1] = shape[1]  # out of range: an all-zero one-hot row, as in the reference
+    return logits, labels

@@ -12,7 +12,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import SEED, gemm_tolerance, normwise_rel_err
+from conftest import SEED, ce_inputs, ce_loss_and_grad, gemm_tolerance, normwise_rel_err
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -109,3 +109,44 @@ def test_bias_gradient_reduce_is_bit_exact(backends):
     got = T.sum(T.tensor(x, backend=dev), [0, 2, 3]).numpy()
     want = T.sum(T.tensor(x, backend=cpu), [0, 2, 3]).numpy()
     assert got.tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("variant", [dict(momentum=0.9), dict(momentum=0.0),
+                                     dict(momentum=0.9, weight_decay=1e-2, nesterov=True)])
+def test_fused_sgd_on_device_is_bit_identical_to_the_oracle_graph(backends, variant):
+    """The device's one-launch SGD step against the reference's ScaledAdd graph
+    run by the CPU oracle: identical parameters, byte for byte, after 5 steps
+    over parameters of the BASELINE MLP's shapes."""
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED + 5)
+    shapes = [(128, 784), (128,), (10, 128), (10,)]
+    init = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    grads = [[rng.standard_normal(sh).astype(np.float32) for sh in shapes] for _ in range(5)]
+
+    def run(backend, fused):
+        params = [T.tensor(w, requires_grad=True, backend=backend) for w in init]
+        opt = optim.SGD(params, lr=0.1, fused=fused, **variant)
+        for step in grads:
+            for p, g in zip(params, step):
+                p.grad = T.tensor(g, backend=backend)
+            opt.step()
+        return [p.numpy() for p in params]
+
+    for a, b in zip(run(dev, True), run(cpu, False)):
+        assert a.tobytes() == b.tobytes()
+
+
+@pytest.mark.parametrize("shape", [(64, 10), (128, 100), (5, 37), (3, 2048), (7, 1), (33, 300),
+                                   (4096, 1000)])
+def test_fused_cross_entropy_on_device(backends, shape):
+    """Device CROSS_ENTROPY nodes: byte for byte the device's own unfused graph
+    (the log-softmax inside is the LOG_SOFTMAX kernel's arithmetic), and within
+    tolerance of the oracle's."""
+    dev, cpu = backends
+    logits, labels = ce_inputs(shape, shape[0] * 7 + shape[1])
+    fl, fg = ce_loss_and_grad(dev, logits, labels, True)
+    ul, ug = ce_loss_and_grad(dev, logits, labels, False)
+    assert fl.tobytes() == ul.tobytes() and fg.tobytes() == ug.tobytes()
+    ol, og = ce_loss_and_grad(cpu, logits, labels, True)
+    np.testing.assert_allclose(fl, ol, rtol=1e-5)
+    assert normwise_rel_err(fg, og) <= gemm_tolerance(shape[1])

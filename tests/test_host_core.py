@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import SEED
+from conftest import SEED, ce_inputs, ce_loss_and_grad
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -90,6 +90,79 @@ def test_sgd_momentum_matches_torch(cpu):
         tw.grad = torch.tensor(g)
         topt.step()
         np.testing.assert_allclose(p.numpy(), tw.detach().numpy(), rtol=1e-6, atol=1e-7)
+
+
+SGD_VARIANTS = [dict(momentum=0.0), dict(momentum=0.9), dict(momentum=0.9, weight_decay=1e-2),
+                dict(momentum=0.9, nesterov=True), dict(momentum=0.5, weight_decay=0.1, nesterov=True),
+                dict(momentum=0.0, weight_decay=1e-2)]
+
+
+def sgd_run(cpu, fused_flags, variant, steps=4):
+    rng = np.random.default_rng(11)
+    shapes = [(7, 5), (5,), (3, 4, 2)]
+    params = [T.tensor(rng.standard_normal(sh).astype(np.float32), requires_grad=True, backend=cpu)
+              for sh in shapes]
+    grads = [[rng.standard_normal(sh).astype(np.float32) for sh in shapes] for _ in range(steps)]
+    opt = optim.SGD(params, lr=0.05, **variant)
+    for k in range(steps):
+        opt.fused = fused_flags[k % len(fused_flags)]
+        for p, g in zip(params, grads[k]):
+            p.grad = T.tensor(g, backend=cpu)
+        opt.step()
+    return [p.numpy() for p in params], grads
+
+
+@pytest.mark.parametrize("variant", SGD_VARIANTS)
+def test_fused_sgd_step_is_bit_identical_to_the_node_graph(cpu, variant):
+    """One fused call per step against the reference's ScaledAdd graph, and a
+    run that alternates between the two (the velocity carries over)."""
+    nodes, _ = sgd_run(cpu, [False], variant)
+    fused, _ = sgd_run(cpu, [True], variant)
+    mixed, _ = sgd_run(cpu, [True, False], variant)
+    for a, b, c in zip(nodes, fused, mixed):
+        assert a.tobytes() == b.tobytes() == c.tobytes()
+
+
+@pytest.mark.parametrize("variant", SGD_VARIANTS)
+def test_sgd_variants_match_torch(cpu, variant):
+    got, grads = sgd_run(cpu, [True], variant)
+    rng = np.random.default_rng(11)
+    shapes = [(7, 5), (5,), (3, 4, 2)]
+    tp = [torch.tensor(rng.standard_normal(sh).astype(np.float32), requires_grad=True)
+          for sh in shapes]
+    topt = torch.optim.SGD(tp, lr=0.05, **variant)
+    for k in range(len(grads)):
+        for q, g in zip(tp, grads[k]):
+            q.grad = torch.tensor(g)
+        topt.step()
+    for a, q in zip(got, tp):
+        np.testing.assert_allclose(a, q.detach().numpy(), rtol=1e-6, atol=1e-7)
+
+
+CE_SHAPES = [(64, 10), (128, 100), (5, 37), (3, 2048), (7, 1), (33, 300)]
+
+
+@pytest.mark.parametrize("shape", CE_SHAPES)
+def test_fused_cross_entropy_is_bit_identical_to_the_node_graph(cpu, shape):
+    """The CROSS_ENTROPY / _BACKWARD nodes against the reference composition
+    (log_softmax, one-hot, mul, sum, neg, mean and their autograd) on the
+    oracle: same loss and same logits gradient, byte for byte."""
+    logits, labels = ce_inputs(shape, shape[0] * 1000 + shape[1])
+    fl, fg = ce_loss_and_grad(cpu, logits, labels, True)
+    gl, gg = ce_loss_and_grad(cpu, logits, labels, False)
+    assert fl.tobytes() == gl.tobytes() and fg.tobytes() == gg.tobytes()
+
+
+@pytest.mark.parametrize("shape", [(64, 10), (128, 100)])
+def test_fused_cross_entropy_matches_torch(cpu, shape):
+    logits, labels = ce_inputs(shape, 5)
+    labels[1] = 0  # torch rejects out-of-range labels
+    loss, grad = ce_loss_and_grad(cpu, logits, labels, True)
+    x = torch.tensor(logits.astype(np.float64), requires_grad=True)
+    ref = torch.nn.functional.cross_entropy(x, torch.tensor(labels))
+    ref.backward()
+    np.testing.assert_allclose(loss, ref.item(), rtol=1e-6)
+    np.testing.assert_allclose(grad, x.grad.numpy(), rtol=1e-5, atol=1e-7)
 
 
 def test_views_and_broadcast_resolve_by_aliasing(cpu):

@@ -29,6 +29,8 @@ OP = dict(
     NOT_EQUAL=27, NEG=28, EXP=35, LOG=36, RELU=43, SUM=47, MEAN=48, MAX=49, MIN=50, ARGMAX=52,
     ARGMIN=53, MATMUL=54, SOFTMAX=55, LOG_SOFTMAX=56, IM2COL=57, COL2IM=58, MAX_POOL2D=59,
     MAX_POOL2D_BACKWARD=60, WHERE=64,
+    # backend extensions (include/vkhip.h): the fused cross-entropy rows
+    CROSS_ENTROPY=96, CROSS_ENTROPY_BACKWARD=97,
 )
 
 
@@ -63,6 +65,11 @@ class Copy(ctypes.Structure):
     _fields_ = [("dst", c_void_p), ("src", c_void_p), ("nbytes", c_size_t)]
 
 
+class SgdParam(ctypes.Structure):
+    _fields_ = [("param", c_void_p), ("grad", c_void_p), ("velocity", c_void_p),
+                ("n", c_uint64), ("first", c_int32), ("reserved", c_int32)]
+
+
 class Decision(ctypes.Structure):
     _fields_ = [("site", c_char_p), ("op", c_char_p), ("chose", c_char_p),
                 ("instead_of", c_char_p), ("because", c_char_p), ("required", c_int64),
@@ -92,6 +99,7 @@ SIGNATURES = {
     "vkhip_free": (c_int, [c_void_p]),
     "vkhip_release_cached": (c_int, []),
     "vkhip_memory_stats": (c_int, [POINTER(c_size_t), POINTER(c_size_t)]),
+    "vkhip_sgd_step": (c_int, [POINTER(SgdParam), c_size_t, c_float, c_float, c_float, c_int]),
     "vkhip_subscribe_decisions": (c_int, [DECISION_FN, c_void_p]),
     "vkhip_set_profiling": (c_int, [c_int]),
     "vkhip_profile_read": (c_int, [POINTER(ProfileRecord), c_size_t, POINTER(c_size_t),

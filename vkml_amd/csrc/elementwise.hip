@@ -346,6 +346,72 @@ int launch_copy_bytes(void* dst, const void* src, size_t nbytes) {
     return VKHIP_OK;
 }
 
+// ---- fused SGD step ----------------------------------------------------------------
+// One launch updates up to kSgdBatch parameters: workgroup w belongs to the
+// parameter whose [block_start[i], block_start[i+1]) range holds w; each thread
+// updates 4 consecutive elements. Every expression is a scaled_add as the
+// reference optimiser builds it, a*alpha + b*beta with both products and the
+// sum rounded separately (multiplies by 1.0 are exact and left out).
+constexpr int kSgdBatch = 64;
+
+struct SgdBatch {
+    vkhip_sgd_param p[kSgdBatch];
+    uint32_t block_start[kSgdBatch + 1];
+    int32_t count;
+    float lr, momentum, weight_decay;
+    int32_t nesterov;
+};
+
+__global__ __launch_bounds__(256) void sgd_step_kernel(SgdBatch b) {
+    int i = 0;
+    while (i + 1 < b.count && blockIdx.x >= b.block_start[i + 1]) ++i;
+    const vkhip_sgd_param& q = b.p[i];
+    const uint64_t base = (static_cast<uint64_t>(blockIdx.x - b.block_start[i]) * 256 + threadIdx.x) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint64_t e = base + j;
+        if (e >= q.n) return;
+        const float p = q.param[e];
+        float g = q.grad[e];
+        if (b.weight_decay != 0.0f) g = __fadd_rn(g, __fmul_rn(p, b.weight_decay));
+        float dir = g;
+        if (b.momentum != 0.0f) {
+            const float v = q.first ? g : __fadd_rn(__fmul_rn(q.velocity[e], b.momentum), g);
+            q.velocity[e] = v;
+            dir = b.nesterov ? __fadd_rn(g, __fmul_rn(v, b.momentum)) : v;
+        }
+        q.param[e] = __fadd_rn(p, __fmul_rn(dir, -b.lr));
+    }
+}
+
+int launch_sgd_step(const vkhip_sgd_param* params, size_t count, float lr, float momentum,
+                    float weight_decay, int nesterov) {
+    for (size_t at = 0; at < count; at += kSgdBatch) {
+        SgdBatch b{};
+        b.count = static_cast<int32_t>(count - at < kSgdBatch ? count - at : kSgdBatch);
+        b.lr = lr;
+        b.momentum = momentum;
+        b.weight_decay = weight_decay;
+        b.nesterov = nesterov ? 1 : 0;
+        uint64_t blocks = 0;
+        for (int i = 0; i < b.count; ++i) {
+            const vkhip_sgd_param& q = params[at + i];
+            if (q.n && (!q.param || !q.grad || (momentum != 0.0f && !q.velocity)))
+                return fail(VKHIP_ERR_INVALID, "sgd_step: parameter %zu has a null buffer", at + i);
+            b.p[i] = q;
+            b.block_start[i] = static_cast<uint32_t>(blocks);
+            blocks += (q.n + 1023) / 1024;
+            if (blocks > 0x7fffffffull) return fail(VKHIP_ERR_UNSUPPORTED, "sgd_step: too many elements");
+        }
+        b.block_start[b.count] = static_cast<uint32_t>(blocks);
+        if (blocks == 0) continue;
+        hipLaunchKernelGGL(sgd_step_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                           ctx().stream, b);
+        VKHIP_LAUNCH_CHECK();
+    }
+    return VKHIP_OK;
+}
+
 }  // namespace vkhip
 
 extern "C" int vkhip_scaled_add(const float* a, const float* b, float* out, uint64_t n, float alpha,
@@ -369,4 +435,13 @@ extern "C" int vkhip_scaled_add(const float* a, const float* b, float* out, uint
     memcpy(nd.params, &alpha, sizeof alpha);
     memcpy(nd.params + sizeof alpha, &beta, sizeof beta);
     return vkhip::launch_elementwise(nd);
+}
+
+extern "C" int vkhip_sgd_step(const vkhip_sgd_param* params, size_t count, float lr,
+                              float momentum, float weight_decay, int nesterov) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("sgd_step");
+    if (count && !params) return vkhip::fail(VKHIP_ERR_INVALID, "sgd_step: null parameter list");
+    return vkhip::launch_sgd_step(params, count, lr, momentum, weight_decay, nesterov);
 }

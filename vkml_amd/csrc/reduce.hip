@@ -314,6 +314,109 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
     }
 }
 
+// ---- cross-entropy rows (fused) ------------------------------------------------
+// One wave per row of C <= 2048 logits. The log-softmax is computed exactly as
+// softmax_wave_rows_kernel<.., LOG = true> computes it (fmaxf peak, the same
+// exponential staged in the same pairwise tree, logf of the denominator,
+// ls = (x - peak) - log(denom)), so ls is bit-identical to the LOG_SOFTMAX
+// node's output. Forward: the one-hot row (float(label) == float(c)), the
+// rounded products ls*onehot, their pairwise sum over C (the SUM node's tree)
+// and its negation. Backward, given g = dL/d(out[r]): the reference autograd's
+// chain, neg (-g), sum and mul backward (gl = (-g) * onehot), log-softmax
+// backward gl - exp(ls) * pairwise_sum(gl) with the EXP node's expf.
+template <int E>
+__global__ __launch_bounds__(256) void cross_entropy_rows_kernel(
+    const float* __restrict__ logits, int64_t row_stride, const int64_t* __restrict__ labels,
+    const float* __restrict__ g_out, float* __restrict__ out, uint32_t rows, uint32_t n, int depth,
+    uint32_t sstride, int backward) {
+    extern __shared__ __attribute__((aligned(16))) float dyn[];
+    const int wave = threadIdx.x >> 6;
+    const int t = threadIdx.x & 63;
+    float* stage = dyn + wave * sstride;
+    uint32_t leaf_b = 0, leaf_e = 0;
+    if (static_cast<uint32_t>(t) < (1u << depth)) pairwise_leaf(n, depth, t, leaf_b, leaf_e);
+    for (uint32_t row = blockIdx.x * 4 + wave; row < rows; row += gridDim.x * 4) {
+        const float* rs = logits + static_cast<int64_t>(row) * row_stride;
+        float x[E];
+        bool keep[E];
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const uint32_t e = static_cast<uint32_t>(t) + 64u * i;
+            keep[i] = e < n;
+            x[i] = keep[i] ? rs[e] : 0.0f;
+        }
+        const float mx = wave_max(tree_peak<E>(x, keep));
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            x[i] = x[i] - mx;
+            if (keep[i]) stage[stage_index(t + 64u * i)] = softmax_exp(x[i]);
+        }
+        wave_lds_fence();
+        float v = leaf_e > leaf_b ? staged_leaf_sum(stage, leaf_b, leaf_e) : 0.0f;
+        const float denom = wave_sum_butterfly(v);
+        wave_lds_fence();
+        const float ld = logf(denom);
+        const float label = static_cast<float>(labels[row]);
+#pragma unroll
+        for (int i = 0; i < E; ++i) x[i] = x[i] - ld;  // log-softmax
+        if (!backward) {
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const uint32_t e = static_cast<uint32_t>(t) + 64u * i;
+                const float onehot = label == static_cast<float>(e) ? 1.0f : 0.0f;
+                if (keep[i]) stage[stage_index(e)] = __fmul_rn(x[i], onehot);
+            }
+            wave_lds_fence();
+            v = leaf_e > leaf_b ? staged_leaf_sum(stage, leaf_b, leaf_e) : 0.0f;
+            const float picked = wave_sum_butterfly(v);
+            wave_lds_fence();
+            if (t == 0) out[row] = -picked;
+        } else {
+            const float ng = -g_out[row];
+            float gl[E];
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const uint32_t e = static_cast<uint32_t>(t) + 64u * i;
+                gl[i] = __fmul_rn(ng, label == static_cast<float>(e) ? 1.0f : 0.0f);
+                if (keep[i]) stage[stage_index(e)] = gl[i];
+            }
+            wave_lds_fence();
+            v = leaf_e > leaf_b ? staged_leaf_sum(stage, leaf_b, leaf_e) : 0.0f;
+            const float total = wave_sum_butterfly(v);
+            wave_lds_fence();
+            float* ds = out + static_cast<uint64_t>(row) * n;
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const uint32_t e = static_cast<uint32_t>(t) + 64u * i;
+                if (keep[i]) ds[e] = __fsub_rn(gl[i], __fmul_rn(expf(x[i]), total));
+            }
+        }
+    }
+}
+
+int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t* labels,
+                         const float* g_out, float* out, uint32_t rows, uint32_t n, int backward) {
+    if (rows == 0) return VKHIP_OK;
+    if (n == 0 || n > 2048)
+        return fail(VKHIP_ERR_UNSUPPORTED, "cross_entropy: %u classes (1..2048 supported)", n);
+    const int depth = pairwise_depth(n);
+    const uint32_t ss = stage_stride(n);
+    const size_t lds = 4 * static_cast<size_t>(ss) * sizeof(float);
+    const uint32_t cus = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
+    const uint32_t want = ceil_div(rows, 4);
+    const uint32_t blocks = want < cus * 4 ? want : cus * 4;
+    void (*fn)(const float*, int64_t, const int64_t*, const float*, float*, uint32_t, uint32_t, int,
+               uint32_t, int);
+    if (n <= 64) fn = cross_entropy_rows_kernel<1>;
+    else if (n <= 256) fn = cross_entropy_rows_kernel<4>;
+    else if (n <= 1024) fn = cross_entropy_rows_kernel<16>;
+    else fn = cross_entropy_rows_kernel<32>;
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, ctx().stream, logits, row_stride, labels,
+                       g_out, out, rows, n, depth, ss, backward);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
 // ---- one thread per output: any layout ------------------------------------------------
 // The reduced elements of output o are at base(o) + lin_off(i, reduced). Sum and
 // mean walk the depth-D leaves in order and fold them with a carry stack (a

@@ -20,6 +20,8 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
 int launch_im2col(const float* src, const vkhip_operand& sd, float* dst, const vkhip_unfold& p);
 int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
                   const vkhip_unfold& p);
+int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t* labels,
+                         const float* g_out, float* out, uint32_t rows, uint32_t n, int backward);
 int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uint32_t out_h,
                       uint32_t out_w, const vkhip_unfold& p);
 int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_operand& sd,
@@ -203,6 +205,21 @@ static int supports_node(const vkhip_node& nd) {
         case VKHIP_OP_MAX_POOL2D:
             return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && nd.src[0].ndim == 4 &&
                    o.ndim == 4 && contiguous(o);
+        case VKHIP_OP_CROSS_ENTROPY:
+        case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
+            const vkhip_tensor& x = nd.src[0];
+            const vkhip_tensor& y = nd.src[1];
+            const bool back = nd.op == VKHIP_OP_CROSS_ENTROPY_BACKWARD;
+            if (nd.n_src != (back ? 3 : 2) || !is_f32(x) || x.ndim != 2 || x.nb[1] != 1 ||
+                x.ne[1] < 1 || x.ne[1] > 2048 || y.dtype != VKHIP_I64 || y.ndim != 1 ||
+                y.ne[0] != x.ne[0] || !contiguous(y) || !is_f32(o) || !contiguous(o))
+                return 0;
+            if (back)
+                return nd.src[2].ndim == 1 && nd.src[2].ne[0] == x.ne[0] && is_f32(nd.src[2]) &&
+                       contiguous(nd.src[2]) && o.ndim == 2 && o.ne[0] == x.ne[0] &&
+                       o.ne[1] == x.ne[1];
+            return o.ndim == 1 && o.ne[0] == x.ne[0];
+        }
         case VKHIP_OP_MAX_POOL2D_BACKWARD:
             return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
                    nd.src[0].ndim == 4 && contiguous(nd.src[0]) && nd.src[1].ndim == 4 &&
@@ -224,6 +241,8 @@ static const char* op_name(int op) {
         case VKHIP_OP_ARGMAX: return "argmax";
         case VKHIP_OP_MAX_POOL2D: return "max_pool2d";
         case VKHIP_OP_MAX_POOL2D_BACKWARD: return "max_pool2d_backward";
+        case VKHIP_OP_CROSS_ENTROPY: return "cross_entropy";
+        case VKHIP_OP_CROSS_ENTROPY_BACKWARD: return "cross_entropy_backward";
         case VKHIP_OP_MIN: return "min";
         case VKHIP_OP_ARGMIN: return "argmin";
         case VKHIP_OP_FULL: return "full";
@@ -305,6 +324,16 @@ static int compute_node(const vkhip_node& nd) {
             return launch_col2im(static_cast<const float*>(nd.src[0].data),
                                  static_cast<float*>(nd.out.data), static_cast<uint32_t>(nd.out.ne[0]),
                                  static_cast<uint32_t>(nd.out.ne[1]), p);
+        }
+        case VKHIP_OP_CROSS_ENTROPY:
+        case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
+            const bool back = nd.op == VKHIP_OP_CROSS_ENTROPY_BACKWARD;
+            return launch_cross_entropy(
+                static_cast<const float*>(nd.src[0].data), nd.src[0].nb[0],
+                static_cast<const int64_t*>(nd.src[1].data),
+                back ? static_cast<const float*>(nd.src[2].data) : nullptr,
+                static_cast<float*>(nd.out.data), static_cast<uint32_t>(nd.src[0].ne[0]),
+                static_cast<uint32_t>(nd.src[0].ne[1]), back ? 1 : 0);
         }
         case VKHIP_OP_MAX_POOL2D: {
             vkhip_unfold p;

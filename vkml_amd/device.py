@@ -40,7 +40,9 @@ def contiguous_strides(shape: Sequence[int]) -> tuple[int, ...]:
 
 
 class Buffer:
-    """One device allocation, freed stream-ordered when the last view dies."""
+    """One device allocation, returned to the backend's caches when the last
+    view dies (the backend's single stream orders every use, so this is safe
+    while work is in flight)."""
 
     __slots__ = ("ptr", "nbytes", "__weakref__")
 
@@ -50,14 +52,20 @@ class Buffer:
         check(lib.vkhip_alloc(max(int(nbytes), 0), byref(p)), "alloc")
         self.ptr = p.value or 0
         self.nbytes = int(nbytes)
+
+    def __del__(self):
         if self.ptr:
-            weakref.finalize(self, _free, self.ptr)
+            try:
+                _free(self.ptr)
+            except Exception:  # interpreter teardown: the backend is gone already
+                pass
+            self.ptr = 0
 
 
 def _free(ptr: int) -> None:
     b = _BACKEND
     if b is not None and b.alive:
-        b.lib.vkhip_free(c_void_p(ptr))
+        b.lib.vkhip_free(ptr)
 
 
 class DeviceArray:

@@ -123,6 +123,21 @@ class DeviceBackend:
     def compute(self, nodes, count: int) -> None:
         _lib.check(self.hip.lib.vkhip_compute(nodes, count), "compute")
 
+    def sgd_step(self, entries, lr: float, momentum: float, weight_decay: float,
+                 nesterov: bool) -> None:
+        """entries: (param storage, grad storage, grad offset bytes, velocity
+        storage or None, velocity offset bytes, element count, first) per
+        parameter; one launch."""
+        arr = (_lib.SgdParam * len(entries))()
+        for d, (p, g, goff, v, voff, n, first) in zip(arr, entries):
+            d.param = p.ptr
+            d.grad = g.ptr + goff
+            d.velocity = v.ptr + voff if v is not None else None
+            d.n = n
+            d.first = 1 if first else 0
+        _lib.check(self.hip.lib.vkhip_sgd_step(arr, len(entries), lr, momentum, weight_decay,
+                                               1 if nesterov else 0), "sgd_step")
+
     def synchronize(self) -> None:
         self.hip.synchronize()
 
@@ -612,10 +627,26 @@ def one_hot_f32(target: Tensor, classes: int) -> Tensor:
     return equal(target.to(np.float32).unsqueeze(-1), indices).to(np.float32)
 
 
+# The backends evaluate the per-row part of cross_entropy, -sum(log_softmax(x)
+# * one_hot, -1), as one CROSS_ENTROPY node and its gradient as one
+# CROSS_ENTROPY_BACKWARD node, operation for operation the values of the
+# reference graph below (one kernel each instead of ~8 nodes each way). False
+# builds the reference's node graph.
+FUSED_CROSS_ENTROPY = True
+
+
 def cross_entropy(logits: Tensor, target: Tensor) -> Tensor:
     """mean(-sum(log_softmax(logits) * one_hot, -1)) (reference ops.cpp:417-441)."""
     batched = logits.unsqueeze(0) if logits.ndim == 1 else logits
     labels = target.unsqueeze(0) if logits.ndim == 1 else target
+    if (FUSED_CROSS_ENTROPY and batched.ndim == 2 and batched.dtype == np.float32
+            and labels.dtype == np.int64 and labels.ndim == 1
+            and 1 <= batched.shape[1] <= 2048 and labels.shape[0] == batched.shape[0]):
+        x = batched.contiguous()
+        y = labels.contiguous()
+        node = Node(OP["CROSS_ENTROPY"], (x.shape[0],), np.float32, x.node.backend,
+                    [x.node, y.node], requires_grad=_grad_enabled and x.requires_grad)
+        return mean(Tensor(node))
     picked = sum(mul(log_softmax(batched, -1), one_hot_f32(labels, batched.shape[1])), [-1])
     return mean(neg(picked))
 
@@ -838,6 +869,10 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
             _accumulate(grads, a, matmul(grad, tb().transpose(-2, -1)))
         if b.requires_grad:
             _accumulate(grads, b, matmul(ta().transpose(-2, -1), grad))
+    elif op == OP["CROSS_ENTROPY"]:
+        g = Node(OP["CROSS_ENTROPY_BACKWARD"], a.shape, np.float32, a.backend,
+                 [a, b, grad.contiguous().node])
+        _accumulate(grads, a, Tensor(g))
     elif op == OP["MAX_POOL2D"]:
         inp = ta()
         n = Node(OP["MAX_POOL2D_BACKWARD"], inp.shape, inp.dtype, inp.node.backend,
