@@ -99,3 +99,27 @@ def ce_inputs(shape, seed):
     if shape[0] > 2:
         labels[1] = shape[1]  # out of range: an all-zero one-hot row, as in the reference
     return logits, labels
+
+
+# ---- the reference's known answers and fixtures (tests/golden) ----
+
+_GOLDEN = None
+
+
+def golden(name: str) -> dict:
+    """One entry of tests/golden/reference_fixtures.json, lists as float32
+    arrays (numbers stay numbers)."""
+    global _GOLDEN
+    if _GOLDEN is None:
+        import json
+
+        _GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_fixtures.json").read_text())
+
+    def conv(v):
+        if isinstance(v, list):
+            return np.array(v, np.float32)
+        if isinstance(v, dict):
+            return {k: conv(x) for k, x in v.items()}
+        return v
+
+    return {k: conv(v) for k, v in _GOLDEN[name].items()}

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from conftest import SEED, gemm_atol, gemm_tolerance, normwise_rel_err
+from conftest import SEED, gemm_atol, gemm_tolerance, golden, normwise_rel_err
 from vkml_amd import _lib, ops
 from vkml_amd.device import DeviceArray
 
@@ -49,19 +49,21 @@ def check_gemm(a: np.ndarray, b: np.ndarray, got: np.ndarray, want: np.ndarray |
 # ---------------------------------------------------------------------------
 
 def test_gemm_known_answer(hip):
-    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
-    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
-    np.testing.assert_array_equal(ops.matmul(dev(a), dev(b)).numpy(), [[58, 64], [139, 154]])
-    bt = np.array([[7, 9, 11], [8, 10, 12]], np.float32)
-    np.testing.assert_array_equal(ops.matmul(dev(a), dev(bt).T).numpy(), [[58, 64], [139, 154]])
+    """reference test_ops.cpp:266-280, 305-311."""
+    f = golden("matmul_2d")
+    np.testing.assert_array_equal(ops.matmul(dev(f["a"]), dev(f["b"])).numpy(), f["expected"])
+    t = golden("matmul_transposed_operand")
+    np.testing.assert_array_equal(ops.matmul(dev(t["a"]), dev(t["b_transposed"]).T).numpy(),
+                                  t["expected"])
+    bb = golden("matmul_batch_broadcast")
+    got = ops.matmul(dev(bb["a"][None]), dev(bb["b"][None]).broadcast_to((1, 2, 2, 2))).numpy()
+    np.testing.assert_array_equal(got[0], bb["expected"])
 
 
 def test_gemm_vector_rules(hip):
-    m = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
-    v = np.ones(3, np.float32)
-    u = np.ones(2, np.float32)
-    np.testing.assert_array_equal(ops.matmul(dev(m), dev(v)).numpy(), [6, 15])
-    np.testing.assert_array_equal(ops.matmul(dev(u), dev(m)).numpy(), [5, 7, 9])
+    f = golden("matmul_vector_rules")
+    np.testing.assert_array_equal(ops.matmul(dev(f["m"]), dev(f["v"])).numpy(), f["m_v"])
+    np.testing.assert_array_equal(ops.matmul(dev(f["u"]), dev(f["m"])).numpy(), f["u_m"])
 
 
 @pytest.mark.parametrize("size", [1, 2, 3, 7, 8, 15, 16, 31, 32, 63, 64, 127, 128, 255, 256, 257])
@@ -263,16 +265,7 @@ def test_softmax_parity(hip, shape, log):
         check_softmax(got, want, shape[1])
 
 
-STABILITY_INPUTS = {
-    "large positive": [[1000.0, 1001.0, 1002.0]],
-    "large negative": [[-1000.0, -1001.0, -1002.0]],
-    "mixed sign": [[-500.0, 0.0, 500.0]],
-    "identical": [[3.5] * 8],
-    "identical zeros": [[0.0] * 16],
-    "extreme spread": [[0.0, -300.0, -600.0, -900.0]],
-    "single element": [[42.0]],
-    "tiny magnitudes": [[1e-30, 2e-30, 3e-30]],
-}
+STABILITY_INPUTS = golden("softmax_stability_inputs")["inputs"]  # test_vulkan_kernels.py:808-817
 
 
 @pytest.mark.parametrize("name", list(STABILITY_INPUTS))

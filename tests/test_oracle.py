@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import oracle as O
-from conftest import SEED, gemm_atol, pairwise_gamma
+from conftest import SEED, gemm_atol, golden, pairwise_gamma
 
 
 def seq32(v: np.ndarray) -> np.float32:
@@ -102,26 +102,30 @@ def test_pairwise_within_backward_bound(n):
 
 def test_matmul_known_answer():
     """reference test_ops.cpp:266-272."""
-    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
-    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
-    np.testing.assert_array_equal(O.matmul(a, b), [[58, 64], [139, 154]])
+    f = golden("matmul_2d")
+    np.testing.assert_array_equal(O.matmul(f["a"], f["b"]), f["expected"])
 
 
 def test_matmul_transposed_operand_known_answer():
     """reference test_ops.cpp:274-280: b given as a transposed (strided) view."""
-    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
-    bt = np.array([[7, 9, 11], [8, 10, 12]], np.float32)
-    np.testing.assert_array_equal(O.matmul(a, bt.T), [[58, 64], [139, 154]])
+    f = golden("matmul_transposed_operand")
+    np.testing.assert_array_equal(O.matmul(f["a"], f["b_transposed"].T), f["expected"])
+
+
+def test_matmul_batch_broadcast_known_answer():
+    """reference test_ops.cpp:305-311: a [1,2,2] identity broadcast over the batch."""
+    f = golden("matmul_batch_broadcast")
+    b = np.broadcast_to(f["b"], f["a"].shape)
+    np.testing.assert_array_equal(O.matmul(f["a"], b), f["expected"])
 
 
 def test_matmul_vector_known_answers():
     """reference test_ops.cpp:282-293 (rank-1 promoted to a row / a column)."""
-    m = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
-    v = np.ones((3, 1), np.float32)
-    u = np.ones((1, 2), np.float32)
-    np.testing.assert_array_equal(O.matmul(m, v).ravel(), [6, 15])
-    np.testing.assert_array_equal(O.matmul(u, m).ravel(), [5, 7, 9])
-    np.testing.assert_array_equal(O.matmul(v.T, v).ravel(), [3])
+    f = golden("matmul_vector_rules")
+    m, v, u = f["m"], f["v"].reshape(3, 1), f["u"].reshape(1, 2)
+    np.testing.assert_array_equal(O.matmul(m, v).ravel(), f["m_v"])
+    np.testing.assert_array_equal(O.matmul(u, m).ravel(), f["u_m"])
+    np.testing.assert_array_equal(O.matmul(v.T, v).ravel(), [f["v_v"]])
 
 
 def test_matmul_products_are_rounded_then_pairwise_summed():
@@ -164,9 +168,9 @@ def test_matmul_threads_do_not_change_bits():
 
 def test_argmax_argmin_first_extremum_known_answer():
     """reference test_ops.cpp:225-231."""
-    a = np.array([[1, 5, 5], [4, 2, 4]], np.float32)
-    np.testing.assert_array_equal(O.argmax(a, 1), [1, 0])
-    np.testing.assert_array_equal(O.argmin(a, 1), [0, 1])
+    f = golden("argmax_first_extremum")
+    np.testing.assert_array_equal(O.argmax(f["a"], 1), f["argmax"])
+    np.testing.assert_array_equal(O.argmin(f["a"], 1), f["argmin"])
 
 
 def test_argmax_skips_nan_and_max_returns_it():
@@ -199,16 +203,7 @@ def test_max_min_are_exact_selections():
 # softmax (reference kernels_reduce.cpp:205-259)
 # ---------------------------------------------------------------------------
 
-STABILITY_INPUTS = {  # reference test_vulkan_kernels.py:808-817
-    "large positive": np.array([[1000.0, 1001.0, 1002.0]], dtype=np.float32),
-    "large negative": np.array([[-1000.0, -1001.0, -1002.0]], dtype=np.float32),
-    "mixed sign": np.array([[-500.0, 0.0, 500.0]], dtype=np.float32),
-    "identical": np.full((1, 8), 3.5, dtype=np.float32),
-    "identical zeros": np.zeros((1, 16), dtype=np.float32),
-    "extreme spread": np.array([[0.0, -300.0, -600.0, -900.0]], dtype=np.float32),
-    "single element": np.array([[42.0]], dtype=np.float32),
-    "tiny magnitudes": np.array([[1e-30, 2e-30, 3e-30]], dtype=np.float32),
-}
+STABILITY_INPUTS = golden("softmax_stability_inputs")["inputs"]  # test_vulkan_kernels.py:808-817
 
 
 @pytest.mark.parametrize("name", list(STABILITY_INPUTS))
@@ -224,13 +219,14 @@ def test_softmax_stability_vs_torch_float64(name, log):
 
 def test_softmax_known_answers():
     """reference test_ops.cpp:233-264."""
-    s = O.softmax(np.array([[1, 2, 3], [1, 2, 3]], np.float32), 1)
+    f = golden("softmax_shift_invariance")
+    s = O.softmax(f["rows"], 1)
     np.testing.assert_allclose(s.sum(1), 1.0, rtol=1e-6)
-    big = O.softmax(np.array([1000, 1001, 1002], np.float32), 0)
-    small = O.softmax(np.array([0, 1, 2], np.float32), 0)
-    np.testing.assert_allclose(big, small, atol=1e-6)
-    ls = O.log_softmax(np.array([0.0, -200.0, -400.0], np.float32), 0)
-    assert np.isfinite(ls).all() and abs(ls[2] + 400.0) <= 400.0 * 1e-4
+    big, small = O.softmax(f["big"], 0), O.softmax(f["small"], 0)
+    np.testing.assert_allclose(big, small, atol=f["tolerance"])
+    g = golden("log_softmax_finite")
+    ls = O.log_softmax(g["x"], 0)
+    assert np.isfinite(ls).all() and abs(ls[2] - g["third"]) <= abs(g["third"]) * g["epsilon"]
 
 
 def test_softmax_denominator_is_pairwise_and_strided_axes_work():
@@ -286,10 +282,11 @@ def test_col2im_is_the_adjoint_of_im2col(shape, kernel, stride, pad, dil):
 def test_col2im_fold_order_fixture():
     """reference test_vulkan_kernels.py:1342-1356: wide magnitudes expose the
     ascending (ki, kj) fold; interior positions get all nine contributions."""
-    vals = np.array([1e8, 1.0, -1e8, 1e-8, 1.0, -1.0, 1e7, 1.0, -1e7], np.float32)
-    cols = np.zeros((1, 9, 16), np.float32)
+    f = golden("col2im_fold_order")
+    vals = f["row_values"]
+    cols = np.zeros(tuple(int(e) for e in f["cols_shape"]), np.float32)
     cols[0, :, :] = vals[:, None]
-    got = O.col2im(cols, (4, 4), (3, 3), (1, 1), (1, 1))
+    got = O.col2im(cols, tuple(int(e) for e in f["image_hw"]), (3, 3), (1, 1), (1, 1))
     # Position (h, w) receives row ki*3+kj when the window at (h+1-ki, w+1-kj) exists.
     for h in range(4):
         for w in range(4):
@@ -328,9 +325,9 @@ def test_max_pool2d_and_backward_vs_torch(shape, kernel, stride, pad):
 
 def test_max_pool2d_tie_goes_to_the_first_maximum():
     """reference test_vulkan_kernels.py:1440-1452."""
-    x = np.array([[[[5.0, 5.0], [1.0, 2.0]]]], np.float32)
-    g = O.max_pool2d_backward(np.ones((1, 1, 1, 1), np.float32), x, (2, 2))
-    np.testing.assert_array_equal(g, [[[[1, 0], [0, 0]]]])
+    f = golden("max_pool2d_tie")
+    g = O.max_pool2d_backward(np.ones((1, 1, 1, 1), np.float32), f["x"], (2, 2))
+    np.testing.assert_array_equal(g, f["grad_of_sum"])
 
 
 def test_max_pool2d_pads_with_minus_infinity():
