@@ -238,6 +238,31 @@ def secondary(hip, ops, timer):
     bw("col2im_conv2", ms, byt)
     del imgs, cols, img_out
 
+    # convolution forward: one implicit-im2col GEMM against the reference
+    # lowering (im2col into a column matrix, then the batch-broadcast GEMM)
+    for name, (xs_shape, cout) in [("conv_128x64x32x32_c128", ((128, 64, 32, 32), 128)),
+                                   ("conv_cnn1_128x3x32x32_c64", ((128, 3, 32, 32), 64)),
+                                   ("conv_cnn2_128x64x16x16_c128", ((128, 64, 16, 16), 128))]:
+        n_, cin, h, w_ = xs_shape
+        x = DeviceArray.from_numpy(rng.standard_normal(xs_shape, dtype=np.float32))
+        wt = DeviceArray.from_numpy(rng.standard_normal((cout, cin, 3, 3), dtype=np.float32))
+        y = DeviceArray((n_, cout, h, w_), np.float32)
+        ck, L = cin * 9, h * w_
+        cols = DeviceArray((n_, ck, L), np.float32)
+        wf = wt.reshape(1, 1, cout, ck).broadcast_to((1, n_, cout, ck))
+        flops = 2.0 * n_ * cout * L * ck
+        ms_i = time_batch(lambda i: ops.conv2d(x, wt, 1, 1, out=y), timer, 20)
+
+        def explicit(i):
+            ops.im2col(x, 3, 1, 1, out=cols)
+            ops.matmul(wf, cols.reshape(1, n_, ck, L), out=y.reshape(1, n_, cout, L))
+
+        ms_e = time_batch(explicit, timer, 20)
+        out[name] = {"ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
+                     "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+                     "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
+        del x, wt, y, cols
+
     # softmax (read + write once), rotate past the MALL
     for shape, count in [((4096, 1000), 20), ((256, 32768), 10)]:
         xs = rotate(shape, count, lambda s: rng.standard_normal(s, dtype=np.float32) * 2)

@@ -132,7 +132,12 @@ enum vkhip_op {
      * g - exp(out) * sum(g), autograd.cpp). Values are those of the unfused
      * graph, operation for operation; see vkhip_node below. */
     VKHIP_OP_CROSS_ENTROPY = 96,          /* src0 logits [N,C] f32 (unit-stride rows), src1 labels [N] i64 -> out [N] f32: -sum_c(ls*onehot) */
-    VKHIP_OP_CROSS_ENTROPY_BACKWARD = 97  /* src0 logits, src1 labels, src2 g [N] f32 -> out [N,C] f32: d(out)/d(logits) */
+    VKHIP_OP_CROSS_ENTROPY_BACKWARD = 97, /* src0 logits, src1 labels, src2 g [N] f32 -> out [N,C] f32: d(out)/d(logits) */
+    /* src0 x [N,C,H,W], src1 weight [Cout,C,kh,kw] (C,kh,kw mergeable) or
+     * [Cout,C*kh*kw], params vkhip_unfold -> out [N,Cout,out_h,out_w]: the
+     * reference conv2d without bias (ops.cpp:662-705), im2col never written;
+     * bit-identical to IM2COL followed by MATMUL with the flat weight. */
+    VKHIP_OP_CONV2D = 98
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */
@@ -311,6 +316,16 @@ int vkhip_event_record(void* event);
 /* Milliseconds between two recorded events; waits for `end` to complete. */
 int vkhip_event_elapsed(void* start, void* end, float* out_ms);
 
+/* Convolution forward as one implicit-im2col GEMM per image:
+ * out[n] = w (Cout x C*kh*kw) @ cols(x[n]) with the cols matrix gathered from
+ * the image inside the GEMM's tile loads instead of materialised (the
+ * reference writes it: im2col then matmul, ops.cpp:662-705). x: [N,C,H,W] any
+ * strides; w: [Cout, C*kh*kw] as a rank-4 descriptor [1,1,Cout,CK]; out
+ * contiguous [N, Cout, out_h*out_w]. Same plan, tiles and MFMA order as
+ * vkhip_gemm on the materialised cols, hence the same bits. */
+int vkhip_conv2d(const float* x, const vkhip_operand* x_desc, const float* w,
+                 const vkhip_operand* w_desc, float* out, const vkhip_unfold* p);
+
 /* ======================================================================== */
 /* Fused optimiser step                                                      */
 /* ======================================================================== */
@@ -393,6 +408,12 @@ int vkhip_pairwise_leaf(uint32_t n, uint32_t leaf, uint32_t* out_depth, uint32_t
 /* n / d as the device kernels compute it (multiply-high by a precomputed
  * magic number; d = 0 returns 0xffffffff). */
 uint32_t vkhip_fast_divide(uint32_t n, uint32_t d);
+/* The implicit-im2col map the convolution GEMM gathers with: offset (in
+ * elements, from the image of one sample) of cols element (row, pos), given
+ * the image's channel/row/column strides x_strides[3], or -1 when it falls in
+ * the padding. */
+int vkhip_im2col_offset(const vkhip_unfold* p, uint32_t channels, const int64_t* x_strides,
+                        uint32_t row, uint32_t pos, int64_t* out_offset);
 
 #ifdef __cplusplus
 }

@@ -575,6 +575,26 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 or_im2col((const float*)nd->src[0].data, &s0, (float*)o->data, &p, threads);
                 break;
             }
+            case VKHIP_OP_CONV2D: {
+                /* The reference's conv2d graph (ops.cpp:662-705): im2col, then
+                 * flat_weight [Cout, C*kh*kw] @ cols [N, C*kh*kw, L] with the
+                 * weight broadcast over the batch. */
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                const vkhip_tensor* w = &nd->src[1];
+                const int64_t ck = w->ndim == 4 ? w->ne[1] * w->ne[2] * w->ne[3] : w->ne[1];
+                const int64_t L = o->ne[2] * o->ne[3];
+                float* cols = (float*)malloc(sizeof(float) * (size_t)(o->ne[0] * ck * L + 1));
+                if (!cols) return VKHIP_ERR_OOM;
+                or_im2col((const float*)nd->src[0].data, &s0, cols, &p, threads);
+                vkhip_operand wd = {{1, 1, (uint32_t)w->ne[0], (uint32_t)ck},
+                                    {0, 0, w->nb[0], w->ndim == 4 ? w->nb[3] : w->nb[1]}};
+                vkhip_operand cd = {{1, (uint32_t)o->ne[0], (uint32_t)ck, (uint32_t)L},
+                                    {0, ck * L, L, 1}};
+                or_matmul((const float*)w->data, &wd, cols, &cd, (float*)o->data, threads);
+                free(cols);
+                break;
+            }
             case VKHIP_OP_COL2IM: {
                 vkhip_unfold p;
                 memcpy(&p, nd->params, sizeof p);

@@ -91,6 +91,39 @@ def ce_loss_and_grad(backend, logits, labels, fused):
         T.FUSED_CROSS_ENTROPY = prev
 
 
+def conv_loss_and_grads(backend, x, w, bias, stride, pad, dil, implicit, x_grad=True):
+    """sum(conv2d(x, w, bias) * probe) and the gradients of x, w and bias on
+    `backend`, with conv2d built as one CONV2D node (implicit=True) or as the
+    reference's im2col + matmul graph. `probe` is a fixed pattern so every
+    output position carries a different weight into the gradients."""
+    from vkml_amd import tensor as T
+
+    prev = T.IMPLICIT_CONV
+    T.IMPLICIT_CONV = implicit
+    try:
+        xt = T.tensor(x, requires_grad=x_grad, backend=backend)
+        wt = T.tensor(w, requires_grad=True, backend=backend)
+        bt = T.tensor(bias, requires_grad=True, backend=backend)
+        out = T.conv2d(xt, wt, bt, stride, pad, dil)
+        probe = np.linspace(-1.0, 1.0, int(np.prod(out.shape)), dtype=np.float32)
+        loss = T.sum(out * T.tensor(probe.reshape(out.shape), backend=backend))
+        loss.backward()
+        return (out.numpy(), xt.grad.numpy() if x_grad else None, wt.grad.numpy(),
+                bt.grad.numpy())
+    finally:
+        T.IMPLICIT_CONV = prev
+
+
+CONV_GEOMETRIES = [  # (x shape, Cout, kernel, stride, pad, dilation)
+    ((2, 3, 5, 5), 4, (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 2, 6, 6), 3, (2, 2), (2, 2), (0, 0), (1, 1)),
+    ((2, 1, 7, 5), 2, (3, 2), (2, 1), (1, 0), (1, 1)),
+    ((1, 2, 5, 5), 5, (2, 2), (1, 1), (0, 0), (2, 2)),
+    ((3, 4, 9, 11), 6, (5, 3), (2, 3), (2, 1), (1, 2)),
+    ((2, 3, 8, 8), 8, (1, 1), (1, 1), (0, 0), (1, 1)),
+]
+
+
 def ce_inputs(shape, seed):
     rng = np.random.default_rng(seed)
     logits = (rng.standard_normal(shape) * 3).astype(np.float32)

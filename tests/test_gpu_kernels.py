@@ -228,6 +228,80 @@ def test_im2col_strided_input_view(hip):
     assert got.tobytes() == O.im2col(x, (3, 3), (2, 1), (1, 1), (1, 1)).tobytes()
 
 
+CONVS = [  # (x shape, Cout, kernel, stride, pad, dilation)
+    ((1, 1, 4, 4), 1, (2, 2), (1, 1), (0, 0), (1, 1)),
+    ((2, 3, 5, 5), 4, (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((2, 1, 7, 5), 2, (3, 2), (2, 1), (1, 0), (1, 1)),
+    ((1, 2, 5, 5), 5, (2, 2), (1, 1), (0, 0), (2, 2)),
+    ((3, 4, 9, 11), 6, (5, 3), (2, 3), (2, 1), (1, 2)),
+    ((2, 40, 20, 20), 70, (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 16, 64, 64), 32, (1, 1), (1, 1), (0, 0), (1, 1)),
+    ((4, 64, 16, 16), 128, (3, 3), (2, 2), (1, 1), (1, 1)),
+    # BASELINE config 4/5 layers at full batch: 128x128 tiles, 64x64 tiles and split-K
+    ((128, 3, 32, 32), 64, (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((128, 64, 32, 32), 64, (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((128, 64, 16, 16), 128, (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 64, 8, 8), 128, (3, 3), (1, 1), (1, 1), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONVS)
+def test_implicit_conv_is_bit_identical_to_im2col_then_gemm(hip, shape, cout, kernel, stride,
+                                                            pad, dil):
+    """vkhip_conv2d gathers the columns inside the GEMM's tile loads; with the
+    same plan and summation order its output equals the reference lowering
+    (im2col, then the batch-broadcast GEMM) bit for bit, and the oracle's to
+    the GEMM tolerance."""
+    rng = np.random.default_rng(SEED + shape[1])
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
+    got = ops.conv2d(dev(x), dev(w), stride, pad, dil).numpy()
+    cols = ops.im2col(dev(x), kernel, stride, pad, dil)
+    n, ck, L = cols.shape
+    wf = dev(w.reshape(1, 1, cout, ck)).broadcast_to((1, n, cout, ck))
+    want = ops.matmul(wf, cols.reshape(1, n, ck, L)).numpy().reshape(got.shape)
+    assert got.tobytes() == want.tobytes()
+    if n * cout * L * ck <= 1 << 27:
+        ref = O.matmul(np.broadcast_to(w.reshape(1, cout, ck), (n, cout, ck)),
+                       O.im2col(x, kernel, stride, pad, dil)).reshape(got.shape)
+        assert normwise_rel_err(got, ref) <= gemm_tolerance(ck)
+
+
+def test_implicit_conv_strided_image(hip):
+    """A channels-last image handed over as an NCHW view, and an image whose
+    batch stride leaves a gap between samples."""
+    rng = np.random.default_rng(SEED)
+    x = rng.uniform(-1, 1, (3, 6, 9, 7)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (5, 6, 3, 3)).astype(np.float32)
+    want = ops.conv2d(dev(x), dev(w), (2, 1), (1, 1), (1, 1)).numpy()
+    nhwc = dev(np.ascontiguousarray(np.transpose(x, (0, 2, 3, 1))))
+    view = _view(nhwc, (3, 6, 9, 7), (9 * 7 * 6, 1, 7 * 6, 6))
+    assert ops.conv2d(view, dev(w), (2, 1), (1, 1), (1, 1)).numpy().tobytes() == want.tobytes()
+    padded = np.zeros((3, 8, 9, 7), np.float32)
+    padded[:, :6] = x
+    gap = _view(dev(padded), (3, 6, 9, 7), (8 * 63, 63, 7, 1))
+    assert ops.conv2d(gap, dev(w), (2, 1), (1, 1), (1, 1)).numpy().tobytes() == want.tobytes()
+
+
+def test_implicit_conv_window_limit(hip):
+    """Windows of more than 63 elements are refused by the gather (the tensor
+    layer lowers them through im2col + matmul instead); 63 still works."""
+    rng = np.random.default_rng(SEED)
+    x = rng.uniform(-1, 1, (1, 2, 12, 12)).astype(np.float32)
+    with pytest.raises(Exception, match="window"):
+        ops.conv2d(dev(x), dev(np.ones((3, 2, 8, 8), np.float32)))
+    w = rng.uniform(-0.5, 0.5, (3, 2, 9, 7)).astype(np.float32)
+    got = ops.conv2d(dev(x), dev(w), 1, 2).numpy()
+    cols = ops.im2col(dev(x), (9, 7), 1, 2)
+    want = ops.matmul(dev(w.reshape(1, 1, 3, -1)).broadcast_to((1, 1, 3, 126)),
+                      cols.reshape(1, 1, 126, cols.shape[2])).numpy().reshape(got.shape)
+    assert got.tobytes() == want.tobytes()
+
+
+def _view(base: DeviceArray, shape, strides) -> DeviceArray:
+    return DeviceArray(shape, np.float32, strides=strides, buffer=base.buffer, offset=base.offset)
+
+
 def test_col2im_fold_order_fixture(hip):
     """reference test_col2im_fold_is_bit_reproducible (test_vulkan_kernels.py:1342-1356)."""
     vals = np.array([1e8, 1.0, -1e8, 1e-8, 1.0, -1.0, 1e7, 1.0, -1e7], np.float32)

@@ -12,7 +12,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import SEED, ce_inputs, ce_loss_and_grad, gemm_tolerance, normwise_rel_err
+from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads,
+                      gemm_tolerance, normwise_rel_err)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -101,6 +102,29 @@ def test_config4_conv_forward_dx_dw(backends, cin, cout):
     assert normwise_rel_err(res["dev"][2], res["cpu"][2]) <= gemm_tolerance(128 * 1024)
     # the bias gradient is a pure pairwise sum over axes {0, 2, 3}: bit-exact
     assert res["dev"][3].tobytes() == res["cpu"][3].tobytes()
+
+
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil",
+                         CONV_GEOMETRIES + [((128, 64, 16, 16), 128, (3, 3), (1, 1), (1, 1), (1, 1))])
+def test_conv_node_on_device_is_bit_identical_to_the_graph(backends, shape, cout, kernel, stride,
+                                                           pad, dil):
+    """On the device, conv2d as one CONV2D node (implicit-im2col GEMM) gives
+    the im2col + matmul graph's output and gradients bit for bit; against the
+    oracle both are within the GEMM tolerance."""
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED + 7)
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
+    node = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True)
+    graph = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=False)
+    for got, want in zip(node, graph):
+        assert got.tobytes() == want.tobytes()
+    if shape[0] <= 4:
+        ref = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True)
+        ck = shape[1] * kernel[0] * kernel[1]
+        for got, want, k in zip(node, ref, (ck, cout, shape[0] * node[0][0, 0].size, 1)):
+            assert normwise_rel_err(got, want) <= gemm_tolerance(max(k, 2))
 
 
 def test_bias_gradient_reduce_is_bit_exact(backends):

@@ -5,7 +5,7 @@ reference's rules. No device calls."""
 from __future__ import annotations
 
 import re
-from ctypes import byref, c_uint32
+from ctypes import byref, c_int64, c_uint32
 from pathlib import Path
 
 import numpy as np
@@ -154,3 +154,38 @@ def test_fast_divide_is_exact():
         for n in nums:
             n &= 0xFFFFFFFF
             assert lib.vkhip_fast_divide(n, d) == n // d, (n, d)
+
+
+@pytest.mark.parametrize("shape,kernel,stride,pad,dil", [
+    ((1, 1, 4, 4), (2, 2), (1, 1), (0, 0), (1, 1)),
+    ((1, 3, 5, 5), (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 2, 6, 6), (2, 2), (2, 2), (0, 0), (1, 1)),
+    ((1, 1, 7, 5), (3, 2), (2, 1), (1, 0), (1, 1)),
+    ((1, 2, 5, 5), (2, 2), (1, 1), (0, 0), (2, 2)),
+    ((1, 3, 9, 11), (5, 3), (2, 3), (2, 1), (1, 2)),
+])
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_implicit_im2col_map_matches_the_oracle_unfold(shape, kernel, stride, pad, dil, layout):
+    """The (row, pos) -> image offset map the convolution GEMM gathers with,
+    evaluated by the library's own host build of the device function, picks
+    exactly the oracle's im2col element for every column entry (0 where the
+    window covers padding), for a plain and a channels-last image layout."""
+    lib = _lib.load()
+    _, c, h, w = shape
+    img = np.arange(c * h * w, dtype=np.float32).reshape(c, h, w) + 1.0
+    strides = (h * w, w, 1) if layout == "nchw" else (1, w * c, c)
+    storage = np.zeros(c * h * w, np.float32)
+    for ci in range(c):
+        for y in range(h):
+            for xx in range(w):
+                storage[ci * strides[0] + y * strides[1] + xx * strides[2]] = img[ci, y, xx]
+    want = O.im2col(img[None], kernel, stride, pad, dil)[0]
+    u = _lib.unfold(kernel, stride, pad, dil, (h, w))
+    st = (c_int64 * 3)(*strides)
+    off = c_int64()
+    got = np.empty_like(want)
+    for row in range(want.shape[0]):
+        for pos in range(want.shape[1]):
+            assert lib.vkhip_im2col_offset(byref(u), c, st, row, pos, byref(off)) == 0
+            got[row, pos] = 0.0 if off.value < 0 else storage[off.value]
+    assert got.tobytes() == want.tobytes()

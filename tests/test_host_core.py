@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import SEED, ce_inputs, ce_loss_and_grad
+from conftest import CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -172,3 +172,27 @@ def test_views_and_broadcast_resolve_by_aliasing(cpu):
     np.testing.assert_array_equal((t + T.tensor(np.ones(4, np.float32), backend=cpu)).numpy(), a + 1)
     np.testing.assert_array_equal(T.sum(t, [0]).numpy(), a.sum(0))
     np.testing.assert_array_equal(T.matmul(t, t.T).numpy(), a @ a.T)
+
+
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONV_GEOMETRIES)
+def test_conv_node_matches_the_reference_graph(cpu, shape, cout, kernel, stride, pad, dil):
+    """conv2d as one CONV2D node gives the reference graph's (im2col + matmul)
+    output and x / weight / bias gradients bit for bit, and both agree with
+    torch's float64 convolution."""
+    rng = np.random.default_rng(SEED + 7)
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
+    node = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True)
+    graph = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=False)
+    for got, want in zip(node, graph):
+        assert got.tobytes() == want.tobytes()
+    xt = torch.tensor(x.astype(np.float64), requires_grad=True)
+    wt = torch.tensor(w.astype(np.float64), requires_grad=True)
+    bt = torch.tensor(bias.astype(np.float64), requires_grad=True)
+    out = torch.nn.functional.conv2d(xt, wt, bt, stride, pad, dil)
+    probe = torch.linspace(-1.0, 1.0, out.numel(), dtype=torch.float32).double().reshape(out.shape)
+    (out * probe).sum().backward()
+    np.testing.assert_allclose(node[0], out.detach().numpy(), rtol=1e-5, atol=1e-6)
+    for got, want in zip(node[1:], (xt.grad, wt.grad, bt.grad)):
+        np.testing.assert_allclose(got, want.numpy(), rtol=1e-4, atol=1e-5)

@@ -59,6 +59,8 @@ struct Unit {
 int cached_alloc(size_t nbytes, void** out);
 int cached_free(void* ptr);
 int release_cached();
+// Frees the cached implicit-im2col row tables (gemm.hip); before release_cached at shutdown.
+int release_conv_tables();
 void memory_stats(size_t* live, size_t* cached);
 
 #define VKHIP_HIP(expr)                                                                   \

@@ -21,6 +21,9 @@
 //     k is unchanged; only the order MFMA visits the k values differs.
 #include "common.h"
 
+#include <mutex>
+#include <vector>
+
 namespace vkhip {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -53,7 +56,83 @@ struct GemmArgs {
 //        (k-contiguous) or along rows.
 // GUARD = false is the interior fast path: the whole tile is in range, so no
 // per-element bounds checks are emitted.
-enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3 };
+enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4 };
+
+// The B operand of a convolution read straight from the image (implicit
+// im2col): element (row, pos) of image n's cols matrix [C*kh*kw, out_h*out_w]
+// is x[n, c, h, w] with row = c*kh*kw + ki*kw + kj, pos = oh*out_w + ow,
+// h = oh*stride_h - pad_h + ki*dil_h, w = ow*stride_w - pad_w + kj*dil_w, and
+// 0 outside the image (kernels_movement.cpp:438-483, the im2col kernel's map).
+struct Im2colB {
+    const float* x;  // image 0
+    int64_t sn;      // image (batch) stride in elements
+    // Within one image every offset fits 32 bits (checked by make_im2col).
+    int32_t sc, sh, sw;  // channel, row and column strides in elements
+    int32_t H, W, kh, kw, kk, strh, strw, padh, padw, dilh, dilw, ow;
+    FastDiv div_kk, div_kw, div_ow;  // by kh*kw, kw, out_w
+    const int32_t* rows;             // row table (see below)
+};
+
+// The map splits into a part that depends only on the output position (one
+// per lane, fixed for the whole kernel) and a part that depends only on the
+// cols row (the same for every lane of a wave in the loader below). Whether
+// an element is inside the image depends on the position and on the row's
+// window element r = ki*kw + kj only: each position keeps a bit mask over r
+// of the elements that fall in the padding.
+constexpr int kMaxWindow = 63;  // kh*kw; bit 63 marks rows past K
+
+struct ImgPos {
+    int32_t h0, w0;    // top-left image coordinate of the window
+    int32_t base;      // its offset (may lie outside the image)
+    uint64_t outside;  // bit r set: window element r lies in the padding
+};
+
+__host__ __device__ __forceinline__ ImgPos img_pos(const Im2colB& g, uint32_t pos, bool valid) {
+    const uint32_t oh = g.div_ow.div(pos);
+    const uint32_t ow = pos - oh * static_cast<uint32_t>(g.ow);
+    ImgPos p;
+    p.h0 = static_cast<int32_t>(oh) * g.strh - g.padh;
+    p.w0 = static_cast<int32_t>(ow) * g.strw - g.padw;
+    p.base = p.h0 * g.sh + p.w0 * g.sw;
+    p.outside = ~0ull;
+    if (valid) {
+        for (int ki = 0; ki < g.kh; ++ki) {
+            const bool row_in = static_cast<uint32_t>(p.h0 + ki * g.dilh) < static_cast<uint32_t>(g.H);
+            for (int kj = 0; kj < g.kw; ++kj) {
+                const bool in = row_in && static_cast<uint32_t>(p.w0 + kj * g.dilw) <
+                                              static_cast<uint32_t>(g.W);
+                if (in) p.outside &= ~(1ull << (ki * g.kw + kj));
+            }
+        }
+    }
+    return p;
+}
+
+// The row part of cols row `row` (channel c, window element ki, kj): its
+// offset and its window element.
+struct ImgRow {
+    int32_t off, r;
+};
+
+__host__ __device__ __forceinline__ ImgRow img_row(const Im2colB& g, uint32_t row) {
+    const uint32_t c = g.div_kk.div(row);
+    const uint32_t r = row - c * static_cast<uint32_t>(g.kk);
+    const uint32_t ki = g.div_kw.div(r);
+    const uint32_t kj = r - ki * static_cast<uint32_t>(g.kw);
+    ImgRow q;
+    q.off = static_cast<int32_t>(c) * g.sc + static_cast<int32_t>(ki) * g.dilh * g.sh +
+            static_cast<int32_t>(kj) * g.dilw * g.sw;
+    q.r = static_cast<int32_t>(r);
+    return q;
+}
+
+// The gather reads the row part from a table built once per geometry:
+// groups of 16 rows as {4*off[16], r[16]} (byte offsets), padded past K with
+// rows whose r = 63 is outside for every position, so the loader needs no K
+// bound. The table is read through the constant address space: a wave's rows
+// are uniform, so these are scalar loads.
+constexpr int kRowGroup = 16;
+typedef const int32_t __attribute__((address_space(4)))* RowTable;
 
 template <int R, int BK, int MODE>
 struct TileLoader {
@@ -129,8 +208,75 @@ struct TileLoader {
         }
     }
 
+    // The A operand of the convolution GEMM (k-contiguous weights, KCV with
+    // K a multiple of four, or KCS): out-of-range groups load a clamped
+    // in-range address and keep 0, so the loads need no branch and can be
+    // scheduled among the MFMAs.
+    __device__ __forceinline__ static void load_clamped(f32x4 (&v)[kRegs], const float* base,
+                                                        int64_t s_row, uint32_t row0, uint32_t rows,
+                                                        uint32_t k0, uint32_t kdim, int tid) {
+        static_assert(MODE == KCV || MODE == KCS, "k-contiguous operand");
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            int r, kq;
+            row_kq(tid + 256 * i, r, kq);
+            const uint32_t gr = row0 + r;
+            const uint32_t gk = k0 + 4 * kq;
+            const int64_t at = static_cast<int64_t>(gr) * s_row + gk;
+            if constexpr (MODE == KCV) {
+                const bool ok = gr < rows && gk < kdim;
+                const f32x4 t = *reinterpret_cast<const f32x4*>(base + (ok ? at : 0));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[i][j] = ok ? t[j] : 0.0f;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool ok = gr < rows && gk + j < kdim;
+                    const float t = base[ok ? at + j : 0];
+                    v[i][j] = ok ? t : 0.0f;
+                }
+            }
+        }
+    }
+
+    // IMG: lanes walk output positions, one tile row each (consecutive image
+    // addresses for unit stride), and a thread gathers kImgK consecutive k for
+    // its position. A wave's k rows are the same for all its lanes: their
+    // table entries are scalar loads. Per element a lane adds the row's
+    // offset to its position's and sets bit 31 when the element is in the
+    // padding; the buffer load returns 0 for such offsets (beyond the
+    // resource's 2^31-byte range), so there is no branch and no select. LDS
+    // receives the same [row][k] layout as every other mode.
+    static constexpr int kImgGroups = 256 / R;
+    static constexpr int kImgK = BK / kImgGroups;
+    __device__ __forceinline__ static void load_img(f32x4 (&v)[kRegs], __amdgpu_buffer_rsrc_t img,
+                                                    RowTable tab, int32_t base4, uint64_t outside,
+                                                    uint32_t k0, int tid) {
+        static_assert(R % 64 == 0 && kImgK % 4 == 0 && kImgK / 4 == kRegs &&
+                          kRowGroup % kImgK == 0, "IMG tile shape");
+        const uint32_t kb = k0 + kImgK * __builtin_amdgcn_readfirstlane(tid / R);
+        const RowTable t = tab + (kb / kRowGroup) * (2 * kRowGroup) + kb % kRowGroup;
+        int32_t off4[kImgK], r[kImgK];
+#pragma unroll
+        for (int j = 0; j < kImgK; ++j) {
+            off4[j] = t[j];
+            r[j] = t[kRowGroup + j];
+        }
+#pragma unroll
+        for (int j = 0; j < kImgK; ++j) {
+            const uint32_t pad = static_cast<uint32_t>(outside >> r[j]) & 1u;
+            const int32_t at = static_cast<int32_t>((pad << 31) | static_cast<uint32_t>(base4 + off4[j]));
+            v[j / 4][j % 4] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(img, at, 0, 0));
+        }
+    }
+
     __device__ __forceinline__ static void store(const f32x4 (&v)[kRegs], float* lds, int tid) {
-        if constexpr (MODE == RCV) {
+        if constexpr (MODE == IMG) {
+            const int r = tid % R, grp = tid / R;
+#pragma unroll
+            for (int q = 0; q < kRegs; ++q)
+                *reinterpret_cast<f32x4*>(lds + r * (BK + 4) + grp * kImgK + 4 * q) = v[q];
+        } else if constexpr (MODE == RCV) {
 #pragma unroll
             for (int tt = 0; tt < kTPT; ++tt) {
                 const int tile = tid + 256 * tt;
@@ -154,7 +300,7 @@ struct TileLoader {
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int AMODE, int BMODE>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_in) {
     static_assert((BM / WM) * (BN / WN) == 4, "four waves per workgroup");
     constexpr int LDK = BK + 4;
     constexpr int MI = WM / 32;
@@ -189,6 +335,22 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
     const uint32_t i0 = z / g.b1, i1 = z % g.b1;
     const float* abase = g.a + i0 * g.sa0 + i1 * g.sa1;
     const float* bbase = g.b + i0 * g.sb0 + i1 * g.sb1;
+    // Implicit im2col: this image as a buffer resource of 2^31 bytes (loads
+    // at offsets with bit 31 set return 0), the row table, and this lane's
+    // position.
+    const __amdgpu_buffer_rsrc_t img = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(im_in.x + static_cast<int64_t>(z) * im_in.sn), 0,
+        static_cast<int32_t>(0x80000000u), 0x00020000);
+    RowTable rows = nullptr;
+    int32_t base4 = 0;
+    uint64_t outside = 0;
+    if constexpr (BMODE == IMG) {
+        rows = (RowTable)im_in.rows;
+        const uint32_t pos = col0 + tid % BN;
+        const ImgPos at = img_pos(im_in, pos < g.n ? pos : 0u, pos < g.n);
+        base4 = at.base * 4;
+        outside = at.outside;
+    }
     float* cbase = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride +
                    static_cast<uint64_t>(z) * g.m * g.n;
 
@@ -207,7 +369,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 
     f32x4 ra[LA::kRegs], rb[LB::kRegs];
     auto load_tile = [&](uint32_t kt) {
-        if (rows_in && (kt + 1) * BK <= g.k) {
+        if constexpr (BMODE == IMG) {
+            LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
+            LB::load_img(rb, img, rows, base4, outside, kt * BK, tid);
+        } else if (rows_in && (kt + 1) * BK <= g.k) {
             LA::template load<false>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
             LB::template load<false>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
         } else {
@@ -227,7 +392,17 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
     for (uint32_t kt = kt0; kt < kt1; ++kt) {
         const int cur = (kt - kt0) & 1;
         const bool more = kt + 1 < kt1;
-        if (more) load_tile(kt + 1);
+        // The implicit-im2col loads have no branches: they are issued every
+        // iteration (the last one's are in range and unused) so that they sit
+        // in the same block as the MFMAs and interleave with them.
+        if constexpr (BMODE == IMG) {
+            load_tile(kt + 1);
+            // Keep every load of the next tile ahead of this tile's MFMAs, so
+            // that their latency hides behind all of them.
+            __builtin_amdgcn_sched_barrier(0);
+        } else if (more) {
+            load_tile(kt + 1);
+        }
         const float* As = lds[cur] + (wm0 + lrow) * LDK + kh * (BK / 2);
         const float* Bs = lds[cur] + BM * LDK + (wn0 + lrow) * LDK + kh * (BK / 2);
         // MFMA operands for step group q+1 are read from LDS while group q's
@@ -480,10 +655,10 @@ template <int BM, int BN, int WM, int WN, int AM>
 static void launch_b(const GemmArgs& g, dim3 grid, hipStream_t st, int bmode) {
     constexpr int BK = 32;
     switch (bmode) {
-        case KCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCV>), grid, dim3(256), 0, st, g); break;
-        case RCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, RCV>), grid, dim3(256), 0, st, g); break;
-        case KCS: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCS>), grid, dim3(256), 0, st, g); break;
-        default: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, RCS>), grid, dim3(256), 0, st, g); break;
+        case KCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCV>), grid, dim3(256), 0, st, g, Im2colB{}); break;
+        case RCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, RCV>), grid, dim3(256), 0, st, g, Im2colB{}); break;
+        case KCS: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCS>), grid, dim3(256), 0, st, g, Im2colB{}); break;
+        default: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, RCS>), grid, dim3(256), 0, st, g, Im2colB{}); break;
     }
 }
 
@@ -496,6 +671,21 @@ static int launch_tiles(const GemmArgs& g, uint32_t batch, uint32_t splits, int 
         case RCV: launch_b<BM, BN, WM, WN, RCV>(g, grid, st, bmode); break;
         case KCS: launch_b<BM, BN, WM, WN, KCS>(g, grid, st, bmode); break;
         default: launch_b<BM, BN, WM, WN, RCS>(g, grid, st, bmode); break;
+    }
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+template <int BM, int BN, int WM, int WN>
+static int launch_conv_tiles(const GemmArgs& g, const Im2colB& im, uint32_t batch, uint32_t splits,
+                             int amode) {
+    constexpr int BK = 32;
+    dim3 grid(g.tiles_m * g.tiles_n, splits, batch);
+    hipStream_t st = ctx().stream;
+    switch (amode) {
+        case KCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCV, IMG>), grid, dim3(256), 0, st, g, im); break;
+        case KCS: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCS, IMG>), grid, dim3(256), 0, st, g, im); break;
+        default: return fail(VKHIP_ERR_INVALID, "conv2d: weight load mode %d", amode);
     }
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
@@ -697,6 +887,214 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     return VKHIP_OK;
 }
 
+// Convolution forward, out[n] = W_flat (Cout x C*kh*kw) @ cols(x[n]) for every
+// image n, as the reference lowers conv2d (ops.cpp:662-705: im2col, then a
+// matmul with the flat weight broadcast over the batch), but with the cols
+// matrix never written: the B tiles are gathered from the image (Im2colB).
+// The plan, tiles, load order into LDS and MFMA sequence are those gemm()
+// uses for matmul(flat_weight, cols), so the result is bit-identical to it.
+// x: [N, C, H, W] (any strides); w: [Cout, C*kh*kw] as a rank-4 operand
+// [1, 1, Cout, CK]; out: contiguous [N, Cout, out_h*out_w].
+// ---- implicit-im2col row tables ----------------------------------------------
+
+__global__ __launch_bounds__(256) void conv_row_table_kernel(Im2colB im, int32_t* tab, uint32_t k,
+                                                              uint32_t rows) {
+    const uint32_t row = blockIdx.x * 256u + threadIdx.x;
+    if (row >= rows) return;
+    ImgRow q{0, kMaxWindow};
+    if (row < k) q = img_row(im, row);
+    int32_t* grp = tab + (row / kRowGroup) * (2 * kRowGroup) + row % kRowGroup;
+    grp[0] = q.off * 4;
+    grp[kRowGroup] = q.r;
+}
+
+// Tables depend on K, the window and the image strides only; the most recent
+// few are kept (device memory from the caching allocator, stream-ordered like
+// every other block) and released at shutdown.
+struct RowTableEntry {
+    uint32_t k, kh, kw;
+    int32_t dilh, dilw, sc, sh, sw;
+    int32_t* table;
+};
+static std::mutex g_tab_mu;
+static std::vector<RowTableEntry> g_tabs;
+constexpr size_t kMaxRowTables = 32;
+
+// Rows covered: every K-tile plus one, since the loader also reads the tile
+// after a partition's last.
+static int conv_row_table(Im2colB& im, uint32_t k) {
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    for (const RowTableEntry& e : g_tabs)
+        if (e.k == k && e.kh == static_cast<uint32_t>(im.kh) && e.kw == static_cast<uint32_t>(im.kw) &&
+            e.dilh == im.dilh && e.dilw == im.dilw && e.sc == im.sc && e.sh == im.sh && e.sw == im.sw) {
+            im.rows = e.table;
+            return VKHIP_OK;
+        }
+    const uint32_t rows = (ceil_div(k, 32u) + 1) * 32u;
+    void* p = nullptr;
+    int st = cached_alloc(static_cast<size_t>(rows) * 2 * sizeof(int32_t), &p);
+    if (st != VKHIP_OK) return st;
+    int32_t* table = static_cast<int32_t*>(p);
+    hipLaunchKernelGGL(conv_row_table_kernel, dim3(ceil_div(rows, 256u)), dim3(256), 0, ctx().stream,
+                       im, table, k, rows);
+    VKHIP_LAUNCH_CHECK();
+    if (g_tabs.size() == kMaxRowTables) {
+        st = cached_free(g_tabs.front().table);
+        g_tabs.erase(g_tabs.begin());
+        if (st != VKHIP_OK) return st;
+    }
+    g_tabs.push_back({k, static_cast<uint32_t>(im.kh), static_cast<uint32_t>(im.kw), im.dilh,
+                      im.dilw, im.sc, im.sh, im.sw, table});
+    im.rows = table;
+    return VKHIP_OK;
+}
+
+int release_conv_tables() {
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    int st = VKHIP_OK;
+    for (const RowTableEntry& e : g_tabs) {
+        const int rc = cached_free(e.table);
+        if (rc != VKHIP_OK) st = rc;
+    }
+    g_tabs.clear();
+    return st;
+}
+
+// Fills the image geometry of an implicit-im2col GEMM; the strides of one
+// image must be non-negative and every offset inside it must fit 32 bits.
+int make_im2col(const vkhip_unfold& p, uint32_t channels, const int64_t* strides, Im2colB& im) {
+    const int64_t oh = (static_cast<int64_t>(p.image_h) + 2 * p.pad_h -
+                        (static_cast<int64_t>(p.dilation_h) * (p.kernel_h - 1) + 1)) / p.stride_h + 1;
+    const int64_t ow = (static_cast<int64_t>(p.image_w) + 2 * p.pad_w -
+                        (static_cast<int64_t>(p.dilation_w) * (p.kernel_w - 1) + 1)) / p.stride_w + 1;
+    if (p.kernel_h <= 0 || p.kernel_w <= 0 || p.stride_h <= 0 || p.stride_w <= 0 ||
+        p.dilation_h <= 0 || p.dilation_w <= 0 || p.pad_h < 0 || p.pad_w < 0 || oh <= 0 || ow <= 0)
+        return fail(VKHIP_ERR_INVALID, "implicit im2col: invalid window geometry");
+    const int64_t sc = strides[0], sh = strides[1], sw = strides[2];
+    if (sc < 0 || sh < 0 || sw < 0)
+        return fail(VKHIP_ERR_UNSUPPORTED, "implicit im2col: negative image strides");
+    // The largest magnitude any intermediate offset reaches: window origins
+    // run from -pad to (out-1)*stride - pad, displacements up to dil*(k-1).
+    const int64_t reach_h = std::max<int64_t>(p.image_h, (oh - 1) * p.stride_h) + p.pad_h +
+                            static_cast<int64_t>(p.dilation_h) * p.kernel_h;
+    const int64_t reach_w = std::max<int64_t>(p.image_w, (ow - 1) * p.stride_w) + p.pad_w +
+                            static_cast<int64_t>(p.dilation_w) * p.kernel_w;
+    const int64_t reach = static_cast<int64_t>(channels + 1) * sc + reach_h * sh + reach_w * sw;
+    if (reach >= (int64_t{1} << 29))
+        return fail(VKHIP_ERR_UNSUPPORTED, "implicit im2col: one image spans 2^29 elements or more");
+    if (static_cast<int64_t>(p.kernel_h) * p.kernel_w > kMaxWindow)
+        return fail(VKHIP_ERR_UNSUPPORTED, "implicit im2col: window of more than %d elements",
+                    kMaxWindow);
+    im.sc = static_cast<int32_t>(sc);
+    im.sh = static_cast<int32_t>(sh);
+    im.sw = static_cast<int32_t>(sw);
+    im.H = p.image_h;
+    im.W = p.image_w;
+    im.kh = p.kernel_h;
+    im.kw = p.kernel_w;
+    im.kk = p.kernel_h * p.kernel_w;
+    im.strh = p.stride_h;
+    im.strw = p.stride_w;
+    im.padh = p.pad_h;
+    im.padw = p.pad_w;
+    im.dilh = p.dilation_h;
+    im.dilw = p.dilation_w;
+    im.ow = static_cast<int32_t>(ow);
+    im.div_kk = FastDiv(static_cast<uint32_t>(im.kk));
+    im.div_kw = FastDiv(static_cast<uint32_t>(im.kw));
+    im.div_ow = FastDiv(static_cast<uint32_t>(ow));
+    return VKHIP_OK;
+}
+
+int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
+                   const vkhip_operand& wd, float* out, const vkhip_unfold& p) {
+    if (p.kernel_h <= 0 || p.kernel_w <= 0 || p.stride_h <= 0 || p.stride_w <= 0 ||
+        p.dilation_h <= 0 || p.dilation_w <= 0 || p.pad_h < 0 || p.pad_w < 0)
+        return fail(VKHIP_ERR_INVALID, "conv2d: invalid window geometry");
+    if (static_cast<int64_t>(xd.ne[2]) != p.image_h || static_cast<int64_t>(xd.ne[3]) != p.image_w)
+        return fail(VKHIP_ERR_INVALID, "conv2d: image is %ux%u but the geometry says %dx%d",
+                    xd.ne[2], xd.ne[3], p.image_h, p.image_w);
+    const int64_t oh = (static_cast<int64_t>(p.image_h) + 2 * p.pad_h -
+                        (static_cast<int64_t>(p.dilation_h) * (p.kernel_h - 1) + 1)) / p.stride_h + 1;
+    const int64_t ow = (static_cast<int64_t>(p.image_w) + 2 * p.pad_w -
+                        (static_cast<int64_t>(p.dilation_w) * (p.kernel_w - 1) + 1)) / p.stride_w + 1;
+    if (oh <= 0 || ow <= 0) return fail(VKHIP_ERR_INVALID, "conv2d: window larger than padded image");
+    const uint64_t batch = static_cast<uint64_t>(xd.ne[0]);
+    const uint32_t channels = xd.ne[1];
+    const uint64_t ck = static_cast<uint64_t>(channels) * p.kernel_h * p.kernel_w;
+    if (wd.ne[0] != 1 || wd.ne[1] != 1 || static_cast<uint64_t>(wd.ne[3]) != ck)
+        return fail(VKHIP_ERR_INVALID, "conv2d: weight must be [Cout, C*kh*kw] with C*kh*kw = %llu",
+                    static_cast<unsigned long long>(ck));
+    const uint64_t L = static_cast<uint64_t>(oh) * ow;
+    if (L > 0xffffffffull || ck > 0xffffffffull || batch > 65535)
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d: extents too large");
+    const uint32_t m = wd.ne[2], n = static_cast<uint32_t>(L), k = static_cast<uint32_t>(ck);
+    if (batch == 0 || m == 0 || n == 0) return VKHIP_OK;
+    if (k == 0) {
+        VKHIP_HIP(hipMemsetAsync(out, 0, batch * m * n * sizeof(float), ctx().stream));
+        return VKHIP_OK;
+    }
+    uint32_t splits, chunk;
+    TileChoice tile;
+    gemm_plan(static_cast<uint32_t>(batch), m, n, k, 0, splits, chunk, tile);
+    publish("matmul.kernel", "conv2d", tile.bm == 128 ? "gemm_mfma_128x128_implicit_im2col"
+                                                      : "gemm_mfma_64x64_implicit_im2col",
+            "im2col_then_gemm", "the cols matrix is gathered from the image inside the GEMM",
+            static_cast<int64_t>(tile.tiles), ctx().ready ? ctx().caps.compute_units : 256);
+
+    GemmArgs g{};
+    g.a = w;
+    g.b = nullptr;
+    g.sa0 = 0;
+    g.sa1 = 0;
+    g.sam = wd.nb[2];
+    g.sak = wd.nb[3];
+    g.b1 = static_cast<uint32_t>(batch);
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.tiles_m = ceil_div(m, tile.bm);
+    g.tiles_n = ceil_div(n, tile.bn);
+    g.ktiles = ceil_div(k, 32);
+    g.chunk = chunk;
+    if (wd.nb[3] != 1 && k != 1)
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d: the weight rows must be contiguous");
+    g.sak = 1;
+    // 16-byte weight loads when every row starts 16-byte aligned and holds
+    // whole groups of four.
+    g.a_vec = reinterpret_cast<uintptr_t>(w) % 16 == 0 && g.sam % 4 == 0 && k % 4 == 0;
+
+    Im2colB im{};
+    const int geo = make_im2col(p, channels, xd.nb + 1, im);
+    if (geo != VKHIP_OK) return geo;
+    im.x = x;
+    im.sn = xd.nb[0];
+    {
+        const int rc = conv_row_table(im, k);
+        if (rc != VKHIP_OK) return rc;
+    }
+
+    const uint64_t out_elems = batch * m * n;
+    float* target = out;
+    if (splits > 1) {
+        float* ws = nullptr;
+        int st = workspace(out_elems * splits * sizeof(float), &ws);
+        if (st != VKHIP_OK) return st;
+        target = ws;
+        g.split_stride = out_elems;
+    }
+    g.c = target;
+    const int amode = g.a_vec ? KCV : KCS;
+    int st;
+    if (tile.bm == 128)
+        st = launch_conv_tiles<128, 128, 64, 64>(g, im, static_cast<uint32_t>(batch), splits, amode);
+    else
+        st = launch_conv_tiles<64, 64, 32, 32>(g, im, static_cast<uint32_t>(batch), splits, amode);
+    if (st != VKHIP_OK) return st;
+    if (splits > 1) return launch_split_k_reduce(target, out, out_elems, splits);
+    return VKHIP_OK;
+}
+
 }  // namespace vkhip
 
 // ---- C ABI -------------------------------------------------------------------
@@ -734,4 +1132,29 @@ extern "C" int vkhip_gemv(const float* a, int64_t lda, const float* x, int64_t i
     if (st != VKHIP_OK) return st;
     vkhip::Unit unit("gemv");
     return vkhip::launch_gemv(a, lda, x, incx, y, m, k);
+}
+
+extern "C" int vkhip_conv2d(const float* x, const vkhip_operand* x_desc, const float* w,
+                            const vkhip_operand* w_desc, float* out, const vkhip_unfold* p) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("conv2d");
+    if (!x_desc || !w_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d: null argument");
+    return vkhip::conv2d_forward(x, *x_desc, w, *w_desc, out, *p);
+}
+
+extern "C" int vkhip_im2col_offset(const vkhip_unfold* p, uint32_t channels, const int64_t* x_strides,
+                                   uint32_t row, uint32_t pos, int64_t* out_offset) {
+    if (!p || !x_strides || !out_offset) return vkhip::fail(VKHIP_ERR_INVALID, "im2col_offset: null argument");
+    vkhip::Im2colB im{};
+    const int st = vkhip::make_im2col(*p, channels, x_strides, im);
+    if (st != VKHIP_OK) return st;
+    // The loader's arithmetic: the table row's byte offset and window
+    // element against the position's padding mask.
+    const vkhip::ImgPos at = vkhip::img_pos(im, pos, true);
+    const vkhip::ImgRow q = vkhip::img_row(im, row);
+    const uint32_t pad = static_cast<uint32_t>(at.outside >> q.r) & 1u;
+    const uint32_t at4 = (pad << 31) | static_cast<uint32_t>(at.base * 4 + q.off * 4);
+    *out_offset = (at4 >> 31) ? -1 : static_cast<int64_t>(at4 / 4);
+    return VKHIP_OK;
 }

@@ -7,6 +7,7 @@
 // synchronise; frees are stream-ordered so memory still read by enqueued work
 // is not reused early (the reference retires frees behind its timeline,
 // vulkan_backend.cpp:921-984; hipFreeAsync gives that ordering directly).
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 
@@ -20,6 +21,8 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
 int launch_im2col(const float* src, const vkhip_operand& sd, float* dst, const vkhip_unfold& p);
 int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
                   const vkhip_unfold& p);
+int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
+                   const vkhip_operand& wd, float* out, const vkhip_unfold& p);
 int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t* labels,
                          const float* g_out, float* out, uint32_t rows, uint32_t n, int backward);
 int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uint32_t out_h,
@@ -205,6 +208,20 @@ static int supports_node(const vkhip_node& nd) {
         case VKHIP_OP_MAX_POOL2D:
             return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && nd.src[0].ndim == 4 &&
                    o.ndim == 4 && contiguous(o);
+        case VKHIP_OP_CONV2D: {
+            const vkhip_tensor& x = nd.src[0];
+            const vkhip_tensor& w = nd.src[1];
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            if (nd.n_src != 2 || !is_f32(x) || !is_f32(w) || !is_f32(o) || x.ndim != 4 ||
+                o.ndim != 4 || !contiguous(o) || o.ne[0] != x.ne[0] || o.ne[1] != w.ne[0] ||
+                static_cast<int64_t>(p.kernel_h) * p.kernel_w > 63)
+                return 0;
+            if (w.ndim == 4)  // [Cout, C, kh, kw] whose last three axes merge into contiguous rows
+                return w.ne[1] == x.ne[1] && w.nb[3] == 1 && w.nb[2] == w.ne[3] &&
+                       w.nb[1] == w.ne[2] * w.nb[2];
+            return w.ndim == 2 && w.nb[1] == 1;
+        }
         case VKHIP_OP_CROSS_ENTROPY:
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
             const vkhip_tensor& x = nd.src[0];
@@ -243,6 +260,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_MAX_POOL2D_BACKWARD: return "max_pool2d_backward";
         case VKHIP_OP_CROSS_ENTROPY: return "cross_entropy";
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: return "cross_entropy_backward";
+        case VKHIP_OP_CONV2D: return "conv2d";
         case VKHIP_OP_MIN: return "min";
         case VKHIP_OP_ARGMIN: return "argmin";
         case VKHIP_OP_FULL: return "full";
@@ -324,6 +342,37 @@ static int compute_node(const vkhip_node& nd) {
             return launch_col2im(static_cast<const float*>(nd.src[0].data),
                                  static_cast<float*>(nd.out.data), static_cast<uint32_t>(nd.out.ne[0]),
                                  static_cast<uint32_t>(nd.out.ne[1]), p);
+        }
+        case VKHIP_OP_CONV2D: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            const vkhip_tensor& w = nd.src[1];
+            const int64_t ck = w.ndim == 4 ? w.ne[1] * w.ne[2] * w.ne[3] : w.ne[1];
+            if (w.ndim == 4 && (w.ne[2] != p.kernel_h || w.ne[3] != p.kernel_w))
+                return fail(VKHIP_ERR_INVALID, "conv2d: weight window %lldx%lld, params %dx%d",
+                            static_cast<long long>(w.ne[2]), static_cast<long long>(w.ne[3]),
+                            p.kernel_h, p.kernel_w);
+            if (ck > 0xffffffffll) return fail(VKHIP_ERR_UNSUPPORTED, "conv2d: weight too large");
+            vkhip_operand wd;
+            wd.ne[0] = 1;
+            wd.ne[1] = 1;
+            wd.ne[2] = static_cast<uint32_t>(w.ne[0]);
+            wd.ne[3] = static_cast<uint32_t>(ck);
+            wd.nb[0] = 0;
+            wd.nb[1] = 0;
+            wd.nb[2] = w.nb[0];
+            wd.nb[3] = w.ndim == 4 ? w.nb[3] : w.nb[1];
+            const int64_t oh = (static_cast<int64_t>(p.image_h) + 2 * p.pad_h -
+                                (static_cast<int64_t>(p.dilation_h) * (p.kernel_h - 1) + 1)) / std::max(p.stride_h, 1) + 1;
+            const int64_t ow = (static_cast<int64_t>(p.image_w) + 2 * p.pad_w -
+                                (static_cast<int64_t>(p.dilation_w) * (p.kernel_w - 1) + 1)) / std::max(p.stride_w, 1) + 1;
+            if (nd.out.ne[2] != oh || nd.out.ne[3] != ow)
+                return fail(VKHIP_ERR_INVALID, "conv2d: output %lldx%lld, geometry gives %lldx%lld",
+                            static_cast<long long>(nd.out.ne[2]), static_cast<long long>(nd.out.ne[3]),
+                            static_cast<long long>(oh), static_cast<long long>(ow));
+            return conv2d_forward(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
+                                  static_cast<const float*>(w.data), wd,
+                                  static_cast<float*>(nd.out.data), p);
         }
         case VKHIP_OP_CROSS_ENTROPY:
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
@@ -418,6 +467,10 @@ extern "C" int vkhip_shutdown(void) {
         VKHIP_HIP(hipFreeAsync(c.ws, c.stream));
         c.ws = nullptr;
         c.ws_bytes = 0;
+    }
+    {
+        const int rc = vkhip::release_conv_tables();
+        if (rc != VKHIP_OK) return rc;
     }
     VKHIP_HIP(hipStreamSynchronize(c.stream));
     {

@@ -178,6 +178,38 @@ def col2im(cols: DeviceArray, image_hw, kernel, stride=1, padding=0, dilation=1,
     return out
 
 
+def conv2d(x: DeviceArray, weight: DeviceArray, stride=1, padding=0, dilation=1,
+           out: DeviceArray | None = None) -> DeviceArray:
+    """[N, C, H, W] * [Cout, C, kh, kw] (or the flat [Cout, C*kh*kw]) ->
+    [N, Cout, out_h, out_w]: the reference's im2col -> flat_weight @ cols
+    (ops.cpp:662-705) as one GEMM that gathers the columns straight from the
+    image, without materialising them. Windows of up to 63 elements (kh*kw);
+    larger ones raise the library's UNSUPPORTED error."""
+    _f32(x, "conv2d")
+    _f32(weight, "conv2d")
+    if x.ndim != 4 or weight.ndim != 4:
+        raise ValueError("conv2d expects an NCHW input and a [Cout, C, kh, kw] weight")
+    cout, cin, kh, kw = weight.shape
+    if cin != x.shape[1]:
+        raise ValueError(f"conv2d: weight has {cin} input channels, the image {x.shape[1]}")
+    if not weight.is_contiguous():
+        from .device import contiguous
+        weight = contiguous(weight)
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw = _pair(dilation)
+    n, _, h, w = x.shape
+    oh, ow = window_count(h, kh, sh, ph, dh), window_count(w, kw, sw, pw, dw)
+    if oh <= 0 or ow <= 0:
+        raise ValueError("conv2d: kernel larger than the padded image")
+    out = _out(out, (n, cout, oh, ow))
+    u = _lib.unfold((kh, kw), (sh, sw), (ph, pw), (dh, dw), (h, w))
+    wd = _lib.operand((cout, cin * kh * kw), (cin * kh * kw, 1))
+    check(_lib.load().vkhip_conv2d(c_void_p(x.ptr), byref(x.operand()), c_void_p(weight.ptr),
+                                   byref(wd), c_void_p(out.ptr), byref(u)), "conv2d")
+    return out
+
+
 # ---- softmax and reductions --------------------------------------------------------------
 
 def _axis4(x: DeviceArray, axis: int) -> int:

@@ -591,6 +591,15 @@ def col2im(cols: Tensor, image_hw, kernel, stride=1, padding=0, dilation=1) -> T
     return Tensor(node)
 
 
+# conv2d evaluates flat_weight @ im2col(x) as one CONV2D node: a GEMM that
+# gathers its columns from the image, bit-identical to the IM2COL + MATMUL
+# pair it replaces (the same GEMM plan and summation order) without writing
+# the C*kh*kw times larger column matrix. Its gradient is the reference
+# graph's, built from the same nodes. False builds the reference's graph.
+IMPLICIT_CONV = True
+IMPLICIT_CONV_MAX_WINDOW = 63  # kh*kw the device gather handles; larger windows use the graph
+
+
 def conv2d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padding=0,
            dilation=1) -> Tensor:
     """im2col -> flat_weight @ cols (batch-broadcast A) -> reshape -> + bias
@@ -598,11 +607,22 @@ def conv2d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padd
     stride, padding, dilation = map(_pair, (stride, padding, dilation))
     cout = weight.shape[0]
     kernel = (weight.shape[2], weight.shape[3])
-    cols = im2col(x, kernel, stride, padding, dilation)
     oh = window_count(x.shape[2], kernel[0], stride[0], padding[0], dilation[0])
     ow = window_count(x.shape[3], kernel[1], stride[1], padding[1], dilation[1])
-    flat_weight = weight.reshape(cout, cols.shape[1])
-    out = matmul(flat_weight, cols).reshape(x.shape[0], cout, oh, ow)
+    if (IMPLICIT_CONV and x.ndim == 4 and weight.ndim == 4 and x.dtype == np.float32
+            and weight.dtype == np.float32 and weight.shape[1] == x.shape[1]
+            and oh > 0 and ow > 0 and kernel[0] * kernel[1] <= IMPLICIT_CONV_MAX_WINDOW):
+        w = weight.contiguous()
+        node = Node(OP["CONV2D"], (x.shape[0], cout, oh, ow), np.float32, x.node.backend,
+                    [x.node, w.node],
+                    params=_unfold_params(kernel, stride, padding, dilation, x.shape[2:]),
+                    requires_grad=_grad_enabled and (x.requires_grad or w.requires_grad))
+        node.aux = (kernel, stride, padding, dilation, tuple(x.shape[2:]))
+        out = Tensor(node)
+    else:
+        cols = im2col(x, kernel, stride, padding, dilation)
+        flat_weight = weight.reshape(cout, cols.shape[1])
+        out = matmul(flat_weight, cols).reshape(x.shape[0], cout, oh, ow)
     if bias is not None:
         out = add(out, bias.reshape(cout, 1, 1))
     return out
@@ -869,6 +889,24 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
             _accumulate(grads, a, matmul(grad, tb().transpose(-2, -1)))
         if b.requires_grad:
             _accumulate(grads, b, matmul(ta().transpose(-2, -1), grad))
+    elif op == OP["CONV2D"]:
+        # The reference graph's gradients (ops.cpp:662-705 through the
+        # MATMUL, BROADCAST, RESHAPE and IM2COL rules): with the weight
+        # broadcast over the batch as flat4 [1, N, Cout, CK] and the columns
+        # as cols4 [1, N, CK, L], d(flat) = sum_n g4 @ cols4^T and
+        # d(x) = col2im(flat4^T @ g4).
+        kernel, stride, pad, dil, hw = node.aux
+        n_, cout, oh, ow = node.shape
+        ck = _numel(b.shape[1:])
+        g4 = grad.reshape(1, n_, cout, oh * ow)
+        if a.requires_grad:
+            flat4 = tb().reshape(cout, ck).broadcast_to((1, n_, cout, ck))
+            dcols = matmul(flat4.transpose(-2, -1), g4).reshape(n_, ck, oh * ow)
+            _accumulate(grads, a, col2im(dcols, hw, kernel, stride, pad, dil))
+        if b.requires_grad:
+            cols4 = im2col(ta(), kernel, stride, pad, dil).broadcast_to((1, n_, ck, oh * ow))
+            dflat = reduce_to_shape(matmul(g4, cols4.transpose(-2, -1)), (cout, ck))
+            _accumulate(grads, b, dflat.reshape(b.shape))
     elif op == OP["CROSS_ENTROPY"]:
         g = Node(OP["CROSS_ENTROPY_BACKWARD"], a.shape, np.float32, a.backend,
                  [a, b, grad.contiguous().node])
