@@ -207,6 +207,12 @@ WINDOWS = [  # reference test_vulkan_kernels.py:1303-1310
     ((128, 3, 32, 32), (3, 3), (1, 1), (1, 1), (1, 1)),
     ((128, 64, 32, 32), (3, 3), (1, 1), (1, 1), (1, 1)),
     ((128, 64, 16, 16), (3, 3), (1, 1), (1, 1), (1, 1)),
+    # several LDS-staged row blocks per plane (odd out_w, stride 2, dilation)
+    ((2, 3, 300, 300), (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 2, 200, 101), (3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 2, 301, 157), (5, 3), (2, 2), (2, 1), (1, 2)),
+    # rows too wide for the LDS tile: the per-row gather
+    ((1, 1, 3, 4000), (3, 3), (1, 1), (1, 1), (1, 1)),
 ]
 
 

@@ -11,6 +11,8 @@
 // is per-thread, so the per-element integer work is one divide by out_w (or W).
 #include "common.h"
 
+#include <algorithm>
+
 namespace vkhip {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -107,6 +109,80 @@ __global__ __launch_bounds__(256) void im2col_kernel(const float* __restrict__ s
     }
 }
 
+// The plane-staged im2col: one workgroup per (image plane, block of R output
+// rows). The input rows the block's windows touch are loaded once into LDS,
+// zero-padded, so each image element is read from memory once; then each
+// thread takes four consecutive positions and writes them for every window
+// offset (kh*kw cols rows), gathering from LDS. Measured on conv2
+// ([128,64,32,32] -> [128,576,1024]): 52 us (6.4 TB/s) against 79 us for the
+// per-row gather above, whose image re-reads through the caches (each element
+// nine times) held the writes back.
+constexpr uint32_t kIm2colTileBytes = 32768;
+
+template <bool NT>
+__global__ __launch_bounds__(256) void im2col_plane_kernel(const float* __restrict__ src, Op4 sd,
+                                                           float* __restrict__ dst, Geo g,
+                                                           uint32_t channels, uint32_t L,
+                                                           uint32_t rows_per_block, uint32_t rblocks,
+                                                           uint32_t in_rows, uint32_t pitch, int vec,
+                                                           FastDiv div_ow, FastDiv div_rb,
+                                                           FastDiv div_c, FastDiv div_pitch) {
+    extern __shared__ float tile[];
+    // Contiguous block ranges per XCD, so the blocks of one image stay in one L2.
+    uint32_t bid = blockIdx.x;
+    if ((gridDim.x & 7u) == 0) bid = (bid & 7u) * (gridDim.x >> 3) + (bid >> 3);
+    const uint32_t plane = div_rb.div(bid);  // n*C + c
+    const uint32_t rb = bid - plane * rblocks;
+    const uint32_t n = div_c.div(plane), c = plane - n * channels;
+    const int32_t oh0 = static_cast<int32_t>(rb * rows_per_block);
+    const int32_t h_first = oh0 * g.sh - g.ph;
+    const float* img = src + n * sd.nb[0] + c * sd.nb[1];
+    const uint32_t tile_n = in_rows * pitch;
+    for (uint32_t i = threadIdx.x; i < tile_n; i += 256) {
+        const uint32_t r = div_pitch.div(i), x = i - r * pitch;
+        const int32_t h = h_first + static_cast<int32_t>(r), w = static_cast<int32_t>(x) - g.pw;
+        const bool ok = static_cast<uint32_t>(h) < static_cast<uint32_t>(g.H) &&
+                        static_cast<uint32_t>(w) < static_cast<uint32_t>(g.W);
+        const float t = img[ok ? h * sd.nb[2] + w * sd.nb[3] : 0];
+        tile[i] = ok ? t : 0.0f;
+    }
+    __syncthreads();
+    const uint32_t rows_here = min(rows_per_block, static_cast<uint32_t>(g.out_h - oh0));
+    const uint32_t npos = rows_here * static_cast<uint32_t>(g.out_w);
+    const uint32_t kk = static_cast<uint32_t>(g.kh * g.kw);
+    float* out0 = dst + static_cast<uint64_t>(plane) * kk * L + static_cast<uint64_t>(oh0) * g.out_w;
+    for (uint32_t p0 = threadIdx.x * 4; p0 < npos; p0 += 1024) {
+        uint32_t at[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t p = min(p0 + j, npos - 1);
+            const uint32_t oh = div_ow.div(p), ow = p - oh * static_cast<uint32_t>(g.out_w);
+            at[j] = oh * g.sh * pitch + ow * g.sw;
+        }
+        for (uint32_t r = 0, ki = 0, kj = 0; r < kk; ++r) {
+            const uint32_t d = ki * g.dh * pitch + kj * g.dw;
+            f32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = tile[at[j] + d];
+            float* out = out0 + static_cast<uint64_t>(r) * L + p0;
+            if (vec && p0 + 3 < npos) {
+                if (NT)
+                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out));
+                else
+                    *reinterpret_cast<f32x4*>(out) = v;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (p0 + j < npos) out[j] = v[j];
+            }
+            if (++kj == static_cast<uint32_t>(g.kw)) {
+                kj = 0;
+                ++ki;
+            }
+        }
+    }
+}
+
 // Non-temporal stores for im2col's output (measured 3.8 vs 2.9 TB/s on conv2):
 // the cols tensor is streamed out once and read once by the GEMM after it.
 // VKHIP_NT_STORES=0 turns them off.
@@ -131,6 +207,38 @@ int launch_im2col(const float* src, const vkhip_operand& sd, float* dst, const v
     const uint64_t nrows = static_cast<uint64_t>(nb) * rows;
     if (nrows == 0 || L == 0) return VKHIP_OK;
     if (nrows > 0xffffffffull) return fail(VKHIP_ERR_UNSUPPORTED, "im2col: too many rows");
+    // Plane-staged when a block of output rows fits the LDS tile: R output
+    // rows need (R-1)*stride_h + (kh-1)*dil_h + 1 input rows of W + 2*pad_w.
+    {
+        const uint64_t pitch = static_cast<uint64_t>(g.W) + 2ull * g.pw;
+        const uint64_t halo = static_cast<uint64_t>(g.kh - 1) * g.dh + 1;
+        const uint64_t max_in_rows = kIm2colTileBytes / 4 / std::max<uint64_t>(pitch, 1);
+        uint64_t R = max_in_rows >= halo ? (max_in_rows - halo) / g.sh + 1 : 0;
+        R = std::min<uint64_t>(R, static_cast<uint64_t>(g.out_h));
+        // whole blocks of four positions keep the 16-byte stores aligned
+        while (R > 1 && (R * g.out_w) % 4 != 0 && R < static_cast<uint64_t>(g.out_h)) --R;
+        const uint64_t planes = static_cast<uint64_t>(nb) * ch;
+        if (R >= 1 && pitch * ((R - 1) * g.sh + halo) * 4 <= kIm2colTileBytes &&
+            planes * ceil_div(static_cast<uint64_t>(g.out_h), R) <= 0x7fffffffull) {
+            const uint32_t rblocks = static_cast<uint32_t>(ceil_div(static_cast<uint64_t>(g.out_h), R));
+            const uint32_t in_rows = static_cast<uint32_t>((R - 1) * g.sh + halo);
+            const int vec_plane = (L % 4 == 0) && ((R * g.out_w) % 4 == 0 || rblocks == 1) &&
+                                  (reinterpret_cast<uintptr_t>(dst) % 16 == 0);
+            const uint32_t blocks = static_cast<uint32_t>(planes * rblocks);
+            const size_t lds = static_cast<size_t>(in_rows) * pitch * 4;
+            auto kern = nt_stores() ? im2col_plane_kernel<true> : im2col_plane_kernel<false>;
+            hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, ctx().stream, src, to_op4(sd), dst, g,
+                               ch, L, static_cast<uint32_t>(R), rblocks, in_rows,
+                               static_cast<uint32_t>(pitch), vec_plane,
+                               FastDiv(static_cast<uint32_t>(g.out_w)), FastDiv(rblocks), FastDiv(ch),
+                               FastDiv(static_cast<uint32_t>(pitch)));
+            VKHIP_LAUNCH_CHECK();
+            publish("im2col.kernel", "im2col", "plane_staged", "row_gather",
+                    "the input rows of a block fit the LDS tile", static_cast<int64_t>(lds),
+                    kIm2colTileBytes);
+            return VKHIP_OK;
+        }
+    }
     const uint32_t pos_blocks = ceil_div(L, 1024);
     const uint64_t blocks = static_cast<uint64_t>(ceil_div(nrows, kIm2colRows)) * pos_blocks;
     if (blocks > 0x7fffffffu) return fail(VKHIP_ERR_UNSUPPORTED, "im2col: grid too large");
