@@ -137,7 +137,12 @@ enum vkhip_op {
      * [Cout,C*kh*kw], params vkhip_unfold -> out [N,Cout,out_h,out_w]: the
      * reference conv2d without bias (ops.cpp:662-705), im2col never written;
      * bit-identical to IM2COL followed by MATMUL with the flat weight. */
-    VKHIP_OP_CONV2D = 98
+    VKHIP_OP_CONV2D = 98,
+    /* src0 x [N,C,H,W], src1 grad [N,Cout,out_h,out_w] (positions unit-stride),
+     * params vkhip_unfold -> out [N,Cout,C*kh*kw]: per image grad @ im2col(x)^T,
+     * the conv2d weight gradient before its batch sum, bit-identical to IM2COL
+     * followed by MATMUL(grad, cols^T). */
+    VKHIP_OP_CONV2D_WEIGHT_GRAD = 99
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */
@@ -325,6 +330,16 @@ int vkhip_event_elapsed(void* start, void* end, float* out_ms);
  * vkhip_gemm on the materialised cols, hence the same bits. */
 int vkhip_conv2d(const float* x, const vkhip_operand* x_desc, const float* w,
                  const vkhip_operand* w_desc, float* out, const vkhip_unfold* p);
+/* The convolution weight gradient's per-image products without the cols
+ * matrix: out[n] = grad[n] (Cout x L) @ im2col(x[n])^T (L x C*kh*kw), the
+ * product the reference's conv2d backward takes on the materialised columns
+ * (matmul(grad, cols^T), autograd.cpp:548-553 over ops.cpp:662-705; the sum
+ * over n stays a separate reduction). x: [N,C,H,W] any strides; grad: rank-4
+ * [1, N, Cout, L] with unit stride along L; out contiguous [N, Cout, C*kh*kw].
+ * Same plan, K order and split-K fold as vkhip_gemm on the columns, hence the
+ * same bits. */
+int vkhip_conv2d_weight_grad(const float* x, const vkhip_operand* x_desc, const float* grad,
+                             const vkhip_operand* grad_desc, float* out, const vkhip_unfold* p);
 
 /* ======================================================================== */
 /* Fused optimiser step                                                      */

@@ -595,6 +595,26 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 free(cols);
                 break;
             }
+            case VKHIP_OP_CONV2D_WEIGHT_GRAD: {
+                /* The reference conv2d backward's weight product per image
+                 * (autograd.cpp:548-553 over ops.cpp:662-705): grad [N, Cout, L]
+                 * @ im2col(x)^T [N, L, C*kh*kw]; the batch sum is a separate node. */
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                const vkhip_tensor* g = &nd->src[1];
+                const int64_t L = g->ne[2] * g->ne[3];
+                const int64_t ck = o->ne[2];
+                float* cols = (float*)malloc(sizeof(float) * (size_t)(o->ne[0] * ck * L + 1));
+                if (!cols) return VKHIP_ERR_OOM;
+                or_im2col((const float*)nd->src[0].data, &s0, cols, &p, threads);
+                vkhip_operand gd = {{1, (uint32_t)g->ne[0], (uint32_t)g->ne[1], (uint32_t)L},
+                                    {0, g->nb[0], g->nb[1], 1}};
+                vkhip_operand cd = {{1, (uint32_t)o->ne[0], (uint32_t)L, (uint32_t)ck},
+                                    {0, ck * L, 1, L}};
+                or_matmul((const float*)g->data, &gd, cols, &cd, (float*)o->data, threads);
+                free(cols);
+                break;
+            }
             case VKHIP_OP_COL2IM: {
                 vkhip_unfold p;
                 memcpy(&p, nd->params, sizeof p);

@@ -273,6 +273,30 @@ def test_implicit_conv_is_bit_identical_to_im2col_then_gemm(hip, shape, cout, ke
         assert normwise_rel_err(got, ref) <= gemm_tolerance(ck)
 
 
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONVS)
+def test_implicit_weight_grad_is_bit_identical_to_gemm_on_cols(hip, shape, cout, kernel, stride,
+                                                               pad, dil):
+    """vkhip_conv2d_weight_grad gathers the transposed columns inside the GEMM;
+    its per-image products equal the reference lowering's matmul(grad,
+    im2col(x)^T) bit for bit (same plan, K order and split-K fold), and the
+    oracle's to the GEMM tolerance."""
+    rng = np.random.default_rng(SEED + 3 * shape[1])
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    cols = ops.im2col(dev(x), kernel, stride, pad, dil)
+    n, ck, L = cols.shape
+    oh = ops.window_count(shape[2], kernel[0], stride[0], pad[0], dil[0])
+    ow = ops.window_count(shape[3], kernel[1], stride[1], pad[1], dil[1])
+    g = rng.standard_normal((n, cout, oh, ow)).astype(np.float32)
+    got = ops.conv2d_weight_grad(dev(x), dev(g), kernel, stride, pad, dil).numpy()
+    want = ops.matmul(dev(g.reshape(1, n, cout, L)),
+                      cols.reshape(1, n, ck, L).transpose(-2, -1)).numpy().reshape(got.shape)
+    assert got.tobytes() == want.tobytes()
+    if n * cout * L * ck <= 1 << 27:
+        ref = O.matmul(g.reshape(n, cout, L),
+                       np.ascontiguousarray(np.swapaxes(O.im2col(x, kernel, stride, pad, dil), 1, 2)))
+        assert normwise_rel_err(got, ref) <= gemm_tolerance(L)
+
+
 def test_implicit_conv_strided_image(hip):
     """A channels-last image handed over as an NCHW view, and an image whose
     batch stride leaves a gap between samples."""

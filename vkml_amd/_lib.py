@@ -30,7 +30,7 @@ OP = dict(
     ARGMIN=53, MATMUL=54, SOFTMAX=55, LOG_SOFTMAX=56, IM2COL=57, COL2IM=58, MAX_POOL2D=59,
     MAX_POOL2D_BACKWARD=60, WHERE=64,
     # backend extensions (include/vkhip.h): the fused cross-entropy rows
-    CROSS_ENTROPY=96, CROSS_ENTROPY_BACKWARD=97, CONV2D=98,
+    CROSS_ENTROPY=96, CROSS_ENTROPY_BACKWARD=97, CONV2D=98, CONV2D_WEIGHT_GRAD=99,
 )
 
 
@@ -102,6 +102,7 @@ SIGNATURES = {
     "vkhip_sgd_step": (c_int, [POINTER(SgdParam), c_size_t, c_float, c_float, c_float, c_int]),
     "vkhip_conv2d": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand), c_void_p,
                              POINTER(Unfold)]),
+    "vkhip_conv2d_weight_grad": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand), c_void_p, POINTER(Unfold)]),
     "vkhip_im2col_offset": (c_int, [POINTER(Unfold), c_uint32, POINTER(c_int64), c_uint32, c_uint32,
                                     POINTER(c_int64)]),
     "vkhip_subscribe_decisions": (c_int, [DECISION_FN, c_void_p]),

@@ -56,7 +56,10 @@ struct GemmArgs {
 //        (k-contiguous) or along rows.
 // GUARD = false is the interior fast path: the whole tile is in range, so no
 // per-element bounds checks are emitted.
-enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4 };
+//   IMG  the B operand of a convolution, gathered from the image (below).
+//   IMGT the B operand of a convolution's weight gradient: the transposed
+//        cols matrix (k = output positions), gathered from the image.
+enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4, IMGT = 5 };
 
 // The B operand of a convolution read straight from the image (implicit
 // im2col): element (row, pos) of image n's cols matrix [C*kh*kw, out_h*out_w]
@@ -136,7 +139,7 @@ typedef const int32_t __attribute__((address_space(4)))* RowTable;
 
 template <int R, int BK, int MODE>
 struct TileLoader {
-    static constexpr bool KMAP = MODE == KCV || MODE == KCS;  // lanes walk k first
+    static constexpr bool KMAP = MODE == KCV || MODE == KCS || MODE == IMGT;  // lanes walk k first
     static constexpr int kGroups = R * BK / 4;
     static constexpr int kPer = kGroups / 256;
     static_assert(kGroups % 256 == 0, "tile must split evenly over 256 threads");
@@ -270,6 +273,66 @@ struct TileLoader {
         }
     }
 
+    // IMGT: element (row r, k = position p) of the transposed cols matrix,
+    // for the weight gradient's B operand. Lanes walk k first (a thread owns
+    // four consecutive positions, eight threads a 32-position row), each
+    // thread keeps kPer fixed rows for the whole kernel: their offsets and
+    // displacements are computed once (ImgRows); per K-tile a thread
+    // decomposes its four positions, and per element it adds, bounds-checks
+    // and loads without branching (bit 31 of a padded element's offset makes
+    // the buffer load return 0; so do positions past K and rows past N).
+    struct ImgRows {
+        int32_t off4[kPer], dh[kPer], dw[kPer];
+        bool valid[kPer];
+    };
+    __device__ __forceinline__ static void img_rows(ImgRows& rs, const Im2colB& im, uint32_t row0,
+                                                    uint32_t rows, int tid) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            int r, kq;
+            row_kq(tid + 256 * i, r, kq);
+            const uint32_t gr = row0 + r;
+            rs.valid[i] = gr < rows;
+            const ImgRow q = img_row(im, rs.valid[i] ? gr : 0u);
+            const uint32_t ki = im.div_kw.div(static_cast<uint32_t>(q.r));
+            rs.dh[i] = static_cast<int32_t>(ki) * im.dilh;
+            rs.dw[i] = (q.r - static_cast<int32_t>(ki) * im.kw) * im.dilw;
+            rs.off4[i] = q.off * 4;
+        }
+    }
+    __device__ __forceinline__ static void load_imgt(f32x4 (&v)[kRegs], __amdgpu_buffer_rsrc_t img,
+                                                     const Im2colB& im, const ImgRows& rs,
+                                                     uint32_t k0, uint32_t kdim, int tid) {
+        static_assert(KMAP && (256 % (BK / 4)) == 0, "IMGT lane map");
+        const uint32_t p0 = k0 + 4u * static_cast<uint32_t>(tid % (BK / 4));
+        uint32_t oh = im.div_ow.div(p0);
+        uint32_t ow = p0 - oh * static_cast<uint32_t>(im.ow);
+        int32_t h0[4], w0[4], base4[4];
+        bool pv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            pv[j] = p0 + j < kdim;
+            h0[j] = static_cast<int32_t>(oh) * im.strh - im.padh;
+            w0[j] = static_cast<int32_t>(ow) * im.strw - im.padw;
+            base4[j] = (h0[j] * im.sh + w0[j] * im.sw) * 4;
+            const bool wrap = ++ow == static_cast<uint32_t>(im.ow);
+            ow = wrap ? 0u : ow;
+            oh += wrap ? 1u : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool inside = pv[j] & rs.valid[i] &
+                                    (static_cast<uint32_t>(h0[j] + rs.dh[i]) < static_cast<uint32_t>(im.H)) &
+                                    (static_cast<uint32_t>(w0[j] + rs.dw[i]) < static_cast<uint32_t>(im.W));
+                const uint32_t at = (inside ? 0u : 0x80000000u) |
+                                    static_cast<uint32_t>(base4[j] + rs.off4[i]);
+                v[i][j] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(img, static_cast<int32_t>(at), 0, 0));
+            }
+    }
+
     __device__ __forceinline__ static void store(const f32x4 (&v)[kRegs], float* lds, int tid) {
         if constexpr (MODE == IMG) {
             const int r = tid % R, grp = tid / R;
@@ -351,6 +414,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         base4 = at.base * 4;
         outside = at.outside;
     }
+    typename LB::ImgRows trows;
+    if constexpr (BMODE == IMGT) LB::img_rows(trows, im_in, col0, g.n, tid);
     float* cbase = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride +
                    static_cast<uint64_t>(z) * g.m * g.n;
 
@@ -372,6 +437,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         if constexpr (BMODE == IMG) {
             LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
             LB::load_img(rb, img, rows, base4, outside, kt * BK, tid);
+        } else if constexpr (BMODE == IMGT) {
+            LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
+            LB::load_imgt(rb, img, im_in, trows, kt * BK, g.k, tid);
         } else if (rows_in && (kt + 1) * BK <= g.k) {
             LA::template load<false>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
             LB::template load<false>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
@@ -395,7 +463,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         // The implicit-im2col loads have no branches: they are issued every
         // iteration (the last one's are in range and unused) so that they sit
         // in the same block as the MFMAs and interleave with them.
-        if constexpr (BMODE == IMG) {
+        if constexpr (BMODE == IMG || BMODE == IMGT) {
             load_tile(kt + 1);
             // Keep every load of the next tile ahead of this tile's MFMAs, so
             // that their latency hides behind all of them.
@@ -676,16 +744,16 @@ static int launch_tiles(const GemmArgs& g, uint32_t batch, uint32_t splits, int 
     return VKHIP_OK;
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int BMODE>
 static int launch_conv_tiles(const GemmArgs& g, const Im2colB& im, uint32_t batch, uint32_t splits,
                              int amode) {
     constexpr int BK = 32;
     dim3 grid(g.tiles_m * g.tiles_n, splits, batch);
     hipStream_t st = ctx().stream;
     switch (amode) {
-        case KCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCV, IMG>), grid, dim3(256), 0, st, g, im); break;
-        case KCS: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCS, IMG>), grid, dim3(256), 0, st, g, im); break;
-        default: return fail(VKHIP_ERR_INVALID, "conv2d: weight load mode %d", amode);
+        case KCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCV, BMODE>), grid, dim3(256), 0, st, g, im); break;
+        case KCS: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCS, BMODE>), grid, dim3(256), 0, st, g, im); break;
+        default: return fail(VKHIP_ERR_INVALID, "conv2d: A operand load mode %d", amode);
     }
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
@@ -1087,14 +1155,92 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
     const int amode = g.a_vec ? KCV : KCS;
     int st;
     if (tile.bm == 128)
-        st = launch_conv_tiles<128, 128, 64, 64>(g, im, static_cast<uint32_t>(batch), splits, amode);
+        st = launch_conv_tiles<128, 128, 64, 64, IMG>(g, im, static_cast<uint32_t>(batch), splits, amode);
     else
-        st = launch_conv_tiles<64, 64, 32, 32>(g, im, static_cast<uint32_t>(batch), splits, amode);
+        st = launch_conv_tiles<64, 64, 32, 32, IMG>(g, im, static_cast<uint32_t>(batch), splits, amode);
     if (st != VKHIP_OK) return st;
     if (splits > 1) return launch_split_k_reduce(target, out, out_elems, splits);
     return VKHIP_OK;
 }
 
+
+// The weight gradient's per-image products, dW[n] = g[n] (Cout x L) @
+// im2col(x[n])^T (L x C*kh*kw), as one GEMM per image whose B operand is
+// gathered from the image (load mode IMGT): what the reference's conv2d
+// backward computes as matmul(grad, cols^T) on the materialised columns
+// (autograd.cpp:548-553 through ops.cpp:662-705), with the same plan, K order
+// and split-K fold, hence the same bits. x: [N,C,H,W] any strides; g: [N,
+// Cout, L] with unit position stride; out contiguous [N, Cout, C*kh*kw].
+int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
+                       const vkhip_operand& gd, float* out, const vkhip_unfold& p) {
+    if (static_cast<int64_t>(xd.ne[2]) != p.image_h || static_cast<int64_t>(xd.ne[3]) != p.image_w)
+        return fail(VKHIP_ERR_INVALID, "conv2d weight grad: image is %ux%u but the geometry says %dx%d",
+                    xd.ne[2], xd.ne[3], p.image_h, p.image_w);
+    Im2colB im{};
+    const int geo = make_im2col(p, xd.ne[1], xd.nb + 1, im);
+    if (geo != VKHIP_OK) return geo;
+    const int64_t oh = (static_cast<int64_t>(p.image_h) + 2 * p.pad_h -
+                        (static_cast<int64_t>(p.dilation_h) * (p.kernel_h - 1) + 1)) / p.stride_h + 1;
+    const uint64_t L = static_cast<uint64_t>(oh) * im.ow;
+    const uint64_t batch = xd.ne[0];
+    const uint64_t ck = static_cast<uint64_t>(xd.ne[1]) * p.kernel_h * p.kernel_w;
+    // gd: [1, N, Cout, L] (rank-4, right-aligned)
+    if (gd.ne[0] != 1 || gd.ne[1] != batch || static_cast<uint64_t>(gd.ne[3]) != L)
+        return fail(VKHIP_ERR_INVALID, "conv2d weight grad: gradient must be [N, Cout, %llu]",
+                    static_cast<unsigned long long>(L));
+    if (gd.nb[3] != 1 && L != 1)
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d weight grad: gradient positions must be contiguous");
+    if (L > 0xffffffffull || ck > 0xffffffffull || batch > 65535)
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d weight grad: extents too large");
+    const uint32_t m = gd.ne[2], n = static_cast<uint32_t>(ck), k = static_cast<uint32_t>(L);
+    if (batch == 0 || m == 0 || n == 0) return VKHIP_OK;
+    uint32_t splits, chunk;
+    TileChoice tile;
+    gemm_plan(static_cast<uint32_t>(batch), m, n, k, 0, splits, chunk, tile);
+    publish("matmul.kernel", "conv2d_weight_grad",
+            tile.bm == 128 ? "gemm_mfma_128x128_implicit_im2col_t" : "gemm_mfma_64x64_implicit_im2col_t",
+            "im2col_then_gemm", "the transposed cols matrix is gathered from the image inside the GEMM",
+            static_cast<int64_t>(tile.tiles), ctx().ready ? ctx().caps.compute_units : 256);
+    im.x = x;
+    im.sn = xd.nb[0];
+
+    GemmArgs g{};
+    g.a = gr;
+    g.b = nullptr;
+    g.sa0 = 0;
+    g.sa1 = gd.nb[1];
+    g.sam = gd.nb[2];
+    g.sak = 1;
+    g.b1 = static_cast<uint32_t>(batch);
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.tiles_m = ceil_div(m, tile.bm);
+    g.tiles_n = ceil_div(n, tile.bn);
+    g.ktiles = ceil_div(k, 32);
+    g.chunk = chunk;
+    g.a_vec = reinterpret_cast<uintptr_t>(gr) % 16 == 0 && g.sam % 4 == 0 && g.sa1 % 4 == 0 &&
+              k % 4 == 0;
+    const int amode = g.a_vec ? KCV : KCS;
+    const uint64_t out_elems = batch * m * n;
+    float* target = out;
+    if (splits > 1) {
+        float* ws = nullptr;
+        int st = workspace(out_elems * splits * sizeof(float), &ws);
+        if (st != VKHIP_OK) return st;
+        target = ws;
+    }
+    g.c = target;
+    g.split_stride = splits > 1 ? out_elems : 0;
+    int st;
+    if (tile.bm == 128)
+        st = launch_conv_tiles<128, 128, 64, 64, IMGT>(g, im, static_cast<uint32_t>(batch), splits, amode);
+    else
+        st = launch_conv_tiles<64, 64, 32, 32, IMGT>(g, im, static_cast<uint32_t>(batch), splits, amode);
+    if (st != VKHIP_OK) return st;
+    if (splits > 1) return launch_split_k_reduce(target, out, out_elems, splits);
+    return VKHIP_OK;
+}
 }  // namespace vkhip
 
 // ---- C ABI -------------------------------------------------------------------
@@ -1141,6 +1287,16 @@ extern "C" int vkhip_conv2d(const float* x, const vkhip_operand* x_desc, const f
     vkhip::Unit unit("conv2d");
     if (!x_desc || !w_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d: null argument");
     return vkhip::conv2d_forward(x, *x_desc, w, *w_desc, out, *p);
+}
+
+extern "C" int vkhip_conv2d_weight_grad(const float* x, const vkhip_operand* x_desc,
+                                        const float* grad, const vkhip_operand* grad_desc, float* out,
+                                        const vkhip_unfold* p) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("conv2d_weight_grad");
+    if (!x_desc || !grad_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d weight grad: null argument");
+    return vkhip::conv2d_weight_grad(x, *x_desc, grad, *grad_desc, out, *p);
 }
 
 extern "C" int vkhip_im2col_offset(const vkhip_unfold* p, uint32_t channels, const int64_t* x_strides,

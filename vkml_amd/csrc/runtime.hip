@@ -23,6 +23,8 @@ int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
                   const vkhip_unfold& p);
 int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
                    const vkhip_operand& wd, float* out, const vkhip_unfold& p);
+int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
+                       const vkhip_operand& gd, float* out, const vkhip_unfold& p);
 int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t* labels,
                          const float* g_out, float* out, uint32_t rows, uint32_t n, int backward);
 int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uint32_t out_h,
@@ -222,6 +224,17 @@ static int supports_node(const vkhip_node& nd) {
                        w.nb[1] == w.ne[2] * w.nb[2];
             return w.ndim == 2 && w.nb[1] == 1;
         }
+        case VKHIP_OP_CONV2D_WEIGHT_GRAD: {
+            const vkhip_tensor& x = nd.src[0];
+            const vkhip_tensor& gr = nd.src[1];
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return nd.n_src == 2 && is_f32(x) && is_f32(gr) && is_f32(o) && x.ndim == 4 &&
+                   gr.ndim == 4 && o.ndim == 3 && contiguous(o) && gr.ne[0] == x.ne[0] &&
+                   o.ne[0] == x.ne[0] && o.ne[1] == gr.ne[1] && gr.nb[3] == 1 &&
+                   gr.nb[2] == gr.ne[3] &&
+                   static_cast<int64_t>(p.kernel_h) * p.kernel_w <= 63;
+        }
         case VKHIP_OP_CROSS_ENTROPY:
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
             const vkhip_tensor& x = nd.src[0];
@@ -261,6 +274,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_CROSS_ENTROPY: return "cross_entropy";
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: return "cross_entropy_backward";
         case VKHIP_OP_CONV2D: return "conv2d";
+        case VKHIP_OP_CONV2D_WEIGHT_GRAD: return "conv2d_weight_grad";
         case VKHIP_OP_MIN: return "min";
         case VKHIP_OP_ARGMIN: return "argmin";
         case VKHIP_OP_FULL: return "full";
@@ -373,6 +387,29 @@ static int compute_node(const vkhip_node& nd) {
             return conv2d_forward(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
                                   static_cast<const float*>(w.data), wd,
                                   static_cast<float*>(nd.out.data), p);
+        }
+        case VKHIP_OP_CONV2D_WEIGHT_GRAD: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            const vkhip_tensor& gr = nd.src[1];
+            const int64_t L = gr.ne[2] * gr.ne[3];
+            const int64_t ck = nd.src[0].ne[1] * static_cast<int64_t>(p.kernel_h) * p.kernel_w;
+            if (nd.out.ne[2] != ck)
+                return fail(VKHIP_ERR_INVALID, "conv2d weight grad: output has %lld columns, want %lld",
+                            static_cast<long long>(nd.out.ne[2]), static_cast<long long>(ck));
+            if (L > 0xffffffffll) return fail(VKHIP_ERR_UNSUPPORTED, "conv2d weight grad: too many positions");
+            vkhip_operand gd;
+            gd.ne[0] = 1;
+            gd.ne[1] = static_cast<uint32_t>(gr.ne[0]);
+            gd.ne[2] = static_cast<uint32_t>(gr.ne[1]);
+            gd.ne[3] = static_cast<uint32_t>(L);
+            gd.nb[0] = 0;
+            gd.nb[1] = gr.nb[0];
+            gd.nb[2] = gr.nb[1];
+            gd.nb[3] = 1;
+            return conv2d_weight_grad(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
+                                      static_cast<const float*>(gr.data), gd,
+                                      static_cast<float*>(nd.out.data), p);
         }
         case VKHIP_OP_CROSS_ENTROPY:
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {

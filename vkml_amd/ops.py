@@ -210,6 +210,37 @@ def conv2d(x: DeviceArray, weight: DeviceArray, stride=1, padding=0, dilation=1,
     return out
 
 
+def conv2d_weight_grad(x: DeviceArray, grad: DeviceArray, kernel, stride=1, padding=0,
+                       dilation=1, out: DeviceArray | None = None) -> DeviceArray:
+    """Per-image weight-gradient products of a convolution, [N, Cout, C*kh*kw]
+    = grad [N, Cout, out_h, out_w] @ im2col(x)^T, without materialising the
+    columns (the reference's matmul(grad, cols^T) in conv2d's backward,
+    autograd.cpp:548-553 over ops.cpp:662-705); summing over N gives dW."""
+    _f32(x, "conv2d_weight_grad")
+    _f32(grad, "conv2d_weight_grad")
+    if x.ndim != 4 or grad.ndim != 4 or grad.shape[0] != x.shape[0]:
+        raise ValueError("conv2d_weight_grad expects an NCHW image and an [N, Cout, oh, ow] gradient")
+    kh, kw = _pair(kernel)
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw = _pair(dilation)
+    n, c, h, w = x.shape
+    oh, ow = window_count(h, kh, sh, ph, dh), window_count(w, kw, sw, pw, dw)
+    if grad.shape[2:] != (oh, ow):
+        raise ValueError(f"conv2d_weight_grad: gradient is {grad.shape[2:]}, geometry gives {(oh, ow)}")
+    if not grad.is_contiguous():
+        from .device import contiguous
+        grad = contiguous(grad)
+    cout = grad.shape[1]
+    out = _out(out, (n, cout, c * kh * kw))
+    u = _lib.unfold((kh, kw), (sh, sw), (ph, pw), (dh, dw), (h, w))
+    gd = _lib.operand((1, n, cout, oh * ow), (0, cout * oh * ow, oh * ow, 1))
+    check(_lib.load().vkhip_conv2d_weight_grad(c_void_p(x.ptr), byref(x.operand()),
+                                               c_void_p(grad.ptr), byref(gd), c_void_p(out.ptr),
+                                               byref(u)), "conv2d_weight_grad")
+    return out
+
+
 # ---- softmax and reductions --------------------------------------------------------------
 
 def _axis4(x: DeviceArray, axis: int) -> int:

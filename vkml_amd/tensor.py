@@ -894,7 +894,7 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         # MATMUL, BROADCAST, RESHAPE and IM2COL rules): with the weight
         # broadcast over the batch as flat4 [1, N, Cout, CK] and the columns
         # as cols4 [1, N, CK, L], d(flat) = sum_n g4 @ cols4^T and
-        # d(x) = col2im(flat4^T @ g4).
+        # d(x) = col2im(flat4^T @ g4), value for value.
         kernel, stride, pad, dil, hw = node.aux
         n_, cout, oh, ow = node.shape
         ck = _numel(b.shape[1:])
@@ -904,8 +904,13 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
             dcols = matmul(flat4.transpose(-2, -1), g4).reshape(n_, ck, oh * ow)
             _accumulate(grads, a, col2im(dcols, hw, kernel, stride, pad, dil))
         if b.requires_grad:
-            cols4 = im2col(ta(), kernel, stride, pad, dil).broadcast_to((1, n_, ck, oh * ow))
-            dflat = reduce_to_shape(matmul(g4, cols4.transpose(-2, -1)), (cout, ck))
+            # The per-image products g4 @ cols4^T as one CONV2D_WEIGHT_GRAD
+            # node (the columns gathered from the image, same bits), then
+            # the reference's batch sum.
+            wg = Node(OP["CONV2D_WEIGHT_GRAD"], (n_, cout, ck), np.float32, a.backend,
+                      [a, grad.contiguous().node], params=node.params)
+            prod = Tensor(wg).reshape(1, n_, cout, ck)
+            dflat = reduce_to_shape(prod, (cout, ck))
             _accumulate(grads, b, dflat.reshape(b.shape))
     elif op == OP["CROSS_ENTROPY"]:
         g = Node(OP["CROSS_ENTROPY_BACKWARD"], a.shape, np.float32, a.backend,
