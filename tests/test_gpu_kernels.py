@@ -165,7 +165,7 @@ def test_split_k_reduce_bit_exact(hip, splits):
 
 
 @pytest.mark.parametrize("m,k", [(1, 1), (7, 31), (64, 784), (129, 1000), (4096, 4096),
-                                 (300, 33)])
+                                 (300, 33), (9, 2500), (1, 3000), (4095, 2052)])
 def test_gemv_bit_exact(hip, m, k):
     """GEMV rounds each product and sums in the oracle's pairwise order."""
     rng = np.random.default_rng(SEED + m + k)
@@ -427,6 +427,8 @@ def test_softmax_non_last_axis(hip):
     ((4096, 64), [0]),          # strided column sums, split tree
     ((2, 3, 70001), [0, 2]),    # uneven tree over two strided axes
     ((50000, 3), [0]),          # three outputs, 128 subtrees of 390-391
+    ((7, 3000), [1]),           # two rows per workgroup, odd row count, uneven tree
+    ((6, 5, 2052), [2]),        # two rows per workgroup over two kept axes
     ((2, 3, 600000), [0, 2]),   # subtrees too long to stage: per-output workgroups
 ])
 def test_sum_mean_bit_exact(hip, shape, axes):

@@ -85,14 +85,18 @@ inline uint32_t ceil_div(uint64_t a, uint64_t b) { return static_cast<uint32_t>(
 
 // Offset (elements) of the `linear`-th element, row-major, of a rank-4
 // operand (reference linear_to_offset, src/backend/cpu/iterate.h:33-42).
-__device__ __forceinline__ int64_t lin_off4(uint64_t linear, const uint32_t ne[4],
+// `linear` < 2^32 at every caller (output counts are checked on the host),
+// so 32-bit division suffices; axes of extent 1 (the usual case) are skipped.
+__device__ __forceinline__ int64_t lin_off4(uint32_t linear, const uint32_t ne[4],
                                             const int64_t nb[4]) {
     int64_t off = 0;
 #pragma unroll
     for (int i = 3; i >= 0; --i) {
-        const uint64_t e = ne[i];
-        off += static_cast<int64_t>(linear % e) * nb[i];
-        linear /= e;
+        const uint32_t e = ne[i];
+        if (e == 1) continue;
+        const uint32_t q = linear / e;
+        off += static_cast<int64_t>(linear - q * e) * nb[i];
+        linear = q;
     }
     return off;
 }

@@ -495,7 +495,7 @@ __global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* _
                                                           void* __restrict__ dst) {
     const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (o >= n_out) return;
-    const float* base = src + lin_off4(o, kept.ne, kept.nb);
+    const float* base = src + lin_off4(static_cast<uint32_t>(o), kept.ne, kept.nb);
     if (op == VKHIP_REDUCE_SUM || op == VKHIP_REDUCE_MEAN) {
         float stack[kTallLevels];
 #pragma unroll
@@ -623,6 +623,55 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_sum_kernel(
     __syncthreads();
     float s = group_pairwise_sum<T>(stage, n, depth, t, scratch[slot]);
     if (live && t == 0) dst[o] = mean ? s / static_cast<float>(n) : s;
+}
+
+// GEMV rows of 2048 < k <= 4096 (at most 128 leaves): two rows per 256-thread
+// workgroup. x is loaded once for both rows, the rounded products of both are
+// staged, and then threads 0-127 sum row 0's leaves and 128-255 row 1's (the
+// one-row kernel leaves half the threads idle there). The per-row tree is
+// group_pairwise_sum<256>'s: leaf sums, the butterfly over each wave, then
+// the two waves' sums added and 0 + 0 added, as its four-wave butterfly does.
+// Measured on the 4096 x 4096 GEMV: 13.2 against 14.8 us.
+__global__ __launch_bounds__(256) void gemv2_rows_kernel(const float* __restrict__ a, int64_t lda,
+                                                         const float* __restrict__ xv,
+                                                         float* __restrict__ y, uint32_t m,
+                                                         uint32_t n, int depth, uint32_t sstride) {
+    extern __shared__ __attribute__((aligned(16))) float dyn[];
+    __shared__ float scratch[4];
+    const int t = threadIdx.x;
+    const uint32_t r0 = blockIdx.x * 2;
+    const bool live1 = r0 + 1 < m;
+    float w[16], x0[16], x1[16];
+    load_row<256, 4>(w, xv, n, t, true, 1);
+    load_row<256, 4>(x0, a + static_cast<int64_t>(r0) * lda, n, t, true, 1);
+    load_row<256, 4>(x1, a + static_cast<int64_t>(live1 ? r0 + 1 : r0) * lda, n, t, true, 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t e0 = 4u * (t + 256 * i);
+        if (e0 < n) {
+            f32x4 v0, v1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v0[j] = __fmul_rn(x0[4 * i + j], w[4 * i + j]);
+                v1[j] = __fmul_rn(x1[4 * i + j], w[4 * i + j]);
+            }
+            *reinterpret_cast<f32x4*>(dyn + stage_index(e0)) = v0;
+            *reinterpret_cast<f32x4*>(dyn + sstride + stage_index(e0)) = v1;
+        }
+    }
+    __syncthreads();
+    const int row = t >> 7, leaf = t & 127;
+    float v = 0.0f;
+    if (static_cast<uint32_t>(leaf) < (1u << depth))
+        v = staged_subtree_sum(dyn + row * sstride, n, depth, leaf, 1);
+    v = wave_sum_butterfly(v);
+    const int lane = t & 63, wave = t >> 6;
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    if (lane == 0 && (wave & 1) == 0) {
+        const uint32_t o = r0 + row;
+        if (o < m) y[o] = scratch[wave] + scratch[wave + 1] + (0.0f + 0.0f);
+    }
 }
 
 // Selections (max/min/argmax/argmin) over contiguous runs that fit the row
@@ -1196,8 +1245,8 @@ __global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restri
                                                            int log_mode, float* __restrict__ dst) {
     const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (o >= n_out) return;
-    const float* base = src + lin_off4(o, kept.ne, kept.nb);
-    float* obase = dst + lin_off4(o, okept.ne, okept.nb);
+    const float* base = src + lin_off4(static_cast<uint32_t>(o), kept.ne, kept.nb);
+    float* obase = dst + lin_off4(static_cast<uint32_t>(o), okept.ne, okept.nb);
     float peak = -__builtin_inff();
     for (uint32_t i = 0; i < n; ++i) peak = max_ignoring_nan(peak, base[rd.off(i)]);
     float stack[kTallLevels];
@@ -1346,6 +1395,13 @@ int launch_gemv_rows(const float* a, int64_t lda, const float* x, float* y, uint
     const int depth = pairwise_depth(k);
     const RowClass rc = row_class(k);
     hipStream_t st = ctx().stream;
+    if (vec && k > 2048 && k <= 4096 && m >= 2) {
+        const uint32_t ss = stage_stride(k);
+        hipLaunchKernelGGL(gemv2_rows_kernel, dim3(ceil_div(m, 2u)), dim3(256),
+                           2 * static_cast<size_t>(ss) * sizeof(float), st, a, lda, x, y, m, k, depth, ss);
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
     VKHIP_ROW_CLASSES(launch_sum_rows, a, kept, m, k, depth, 0, vec, y, st, x)
 }
 
