@@ -238,8 +238,9 @@ def secondary(hip, ops, timer):
     bw("col2im_conv2", ms, byt)
     del imgs, cols, img_out
 
-    # convolution forward: one implicit-im2col GEMM against the reference
-    # lowering (im2col into a column matrix, then the batch-broadcast GEMM)
+    # convolution forward and weight gradient: one implicit-im2col GEMM each,
+    # against the reference lowering (im2col into a column matrix, then the
+    # batch-broadcast GEMM)
     for name, (xs_shape, cout) in [("conv_128x64x32x32_c128", ((128, 64, 32, 32), 128)),
                                    ("conv_cnn1_128x3x32x32_c64", ((128, 3, 32, 32), 64)),
                                    ("conv_cnn2_128x64x16x16_c128", ((128, 64, 16, 16), 128))]:
@@ -261,14 +262,39 @@ def secondary(hip, ops, timer):
         out[name] = {"ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
                      "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
                      "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
-        del x, wt, y, cols
+        # the weight gradient's per-image products, grad @ im2col(x)^T
+        g = DeviceArray.from_numpy(rng.standard_normal((n_, cout, h, w_), dtype=np.float32))
+        wg = DeviceArray((n_, cout, ck), np.float32)
+        g4 = g.reshape(1, n_, cout, L)
+        colsT = cols.reshape(1, n_, ck, L).transpose(-2, -1)
+        ms_i = time_batch(lambda i: ops.conv2d_weight_grad(x, g, 3, 1, 1, out=wg), timer, 20)
 
-    # softmax (read + write once), rotate past the MALL
+        def explicit_wg(i):
+            ops.im2col(x, 3, 1, 1, out=cols)
+            ops.matmul(g4, colsT, out=wg.reshape(1, n_, cout, ck))
+
+        ms_e = time_batch(explicit_wg, timer, 20)
+        out[name.replace("conv_", "conv_wgrad_")] = {
+            "ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
+            "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+            "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
+        del x, wt, y, cols, g, wg
+
+    # softmax (read + write once), rotate past the MALL; each against the
+    # library's plain copy of the same bytes, the floor of a one-pass kernel
+    # at that size (launch ramp and drain included)
     for shape, count in [((4096, 1000), 20), ((256, 32768), 10)]:
         xs = rotate(shape, count, lambda s: rng.standard_normal(s, dtype=np.float32) * 2)
         ys = [DeviceArray(shape, np.float32) for _ in range(2)]
         ms = time_batch(lambda i: ops.softmax(xs[i % count], -1, out=ys[i % 2]), timer, 40)
-        bw(f"softmax_{shape[0]}x{shape[1]}", ms, 2 * shape[0] * shape[1] * 4)
+        name = f"softmax_{shape[0]}x{shape[1]}"
+        bw(name, ms, 2 * shape[0] * shape[1] * 4)
+        flat = [xv.reshape(shape[0] * shape[1]) for xv in xs]
+        yflat = [yv.reshape(shape[0] * shape[1]) for yv in ys]
+        ms_copy = time_batch(lambda i: hip.copy_device_to_device([(yflat[i % 2], flat[i % count])]),
+                             timer, 40)
+        out[name]["copy_same_bytes_ms"] = round(ms_copy, 5)
+        out[name]["frac_of_copy"] = round(ms_copy / ms, 4)
         del xs, ys
 
     # sum / max over the last axis of [8192, 4096] (134 MB read), 4 buffers
