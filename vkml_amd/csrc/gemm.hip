@@ -59,7 +59,11 @@ struct GemmArgs {
 //   IMG  the B operand of a convolution, gathered from the image (below).
 //   IMGT the B operand of a convolution's weight gradient: the transposed
 //        cols matrix (k = output positions), gathered from the image.
-enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4, IMGT = 5 };
+//   KCD  k-contiguous, 16-byte aligned, K a multiple of 4: loaded straight
+//        into LDS by buffer loads (no registers, no LDS stores), rows of BK
+//        floats whose 16-byte groups are XOR-swizzled by row (group g of row r
+//        at g ^ (r & 7)) so the MFMA operand reads stay conflict-free.
+enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4, IMGT = 5, KCD = 6 };
 
 // The B operand of a convolution read straight from the image (implicit
 // im2col): element (row, pos) of image n's cols matrix [C*kh*kw, out_h*out_w]
@@ -145,7 +149,7 @@ struct TileLoader {
     static_assert(kGroups % 256 == 0, "tile must split evenly over 256 threads");
     static constexpr int kTiles = R * BK / 16;        // 4x4 blocks
     static constexpr int kTPT = (kTiles + 255) / 256;  // blocks per thread
-    static constexpr int kRegs = MODE == RCV ? 4 * kTPT : kPer;
+    static constexpr int kRegs = MODE == RCV ? 4 * kTPT : (MODE == KCD ? 1 : kPer);
 
     __device__ __forceinline__ static void row_kq(int g, int& r, int& kq) {
         if (KMAP) {
@@ -208,6 +212,32 @@ struct TileLoader {
                     v[i] = t;
                 }
             }
+        }
+    }
+
+    // KCD: R rows x BK k as R*BK/4 16-byte slots; wave w's i-th load fills
+    // slots (4i + w)*64 .. +63 of the stage, one per lane, in order (the load
+    // writes lane l's 16 bytes at the instruction's LDS base + 16 l). Slot s
+    // holds row s / 8, k-group (s % 8) ^ (row & 7). Out-of-range groups read
+    // an offset past the buffer's range and land as zeros.
+    __device__ __forceinline__ static void load_direct(float* stage, __amdgpu_buffer_rsrc_t src,
+                                                       int64_t s_row, uint32_t row0, uint32_t rows,
+                                                       uint32_t k0, uint32_t kdim, int tid) {
+        static_assert(BK == 32 && (R * BK / 4) % 256 == 0, "KCD tile shape");
+        constexpr int kLoads = R * BK / 4 / 256;
+        const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int chunk = 4 * i + wave;
+            const int slot = chunk * 64 + lane;
+            const int r = slot >> 3;
+            const int grp = (slot & 7) ^ (r & 7);
+            const uint32_t gr = row0 + r, gk = k0 + 4 * grp;
+            const bool ok = gr < rows && gk < kdim;
+            const uint32_t off = ok ? static_cast<uint32_t>((static_cast<int64_t>(gr) * s_row + gk) * 4)
+                                    : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                src, (__attribute__((address_space(3))) void*)(stage + chunk * 256), 16, off, 0, 0, 0);
         }
     }
 
@@ -401,6 +431,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
     // Implicit im2col: this image as a buffer resource of 2^31 bytes (loads
     // at offsets with bit 31 set return 0), the row table, and this lane's
     // position.
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(abase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
     const __amdgpu_buffer_rsrc_t img = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(im_in.x + static_cast<int64_t>(z) * im_in.sn), 0,
         static_cast<int32_t>(0x80000000u), 0x00020000);
@@ -433,8 +465,15 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     f32x4 ra[LA::kRegs], rb[LB::kRegs];
-    auto load_tile = [&](uint32_t kt) {
-        if constexpr (BMODE == IMG) {
+    auto load_tile = [&](uint32_t kt, int dst) {
+        (void)dst;
+        if constexpr (AMODE == KCD) {
+            LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+            if (rows_in && (kt + 1) * BK <= g.k)
+                LB::template load<false>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
+            else
+                LB::template load<true>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
+        } else if constexpr (BMODE == IMG) {
             LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
             LB::load_img(rb, img, rows, base4, outside, kt * BK, tid);
         } else if constexpr (BMODE == IMGT) {
@@ -449,8 +488,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         }
     };
     if (kt0 < kt1) {
-        load_tile(kt0);
-        LA::store(ra, lds[0], tid);
+        load_tile(kt0, 0);
+        if constexpr (AMODE != KCD) LA::store(ra, lds[0], tid);
         LB::store(rb, lds[0] + BM * LDK, tid);
     }
     __syncthreads();
@@ -464,20 +503,26 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         // iteration (the last one's are in range and unused) so that they sit
         // in the same block as the MFMAs and interleave with them.
         if constexpr (BMODE == IMG || BMODE == IMGT) {
-            load_tile(kt + 1);
+            load_tile(kt + 1, cur ^ 1);
             // Keep every load of the next tile ahead of this tile's MFMAs, so
             // that their latency hides behind all of them.
             __builtin_amdgcn_sched_barrier(0);
         } else if (more) {
-            load_tile(kt + 1);
+            load_tile(kt + 1, cur ^ 1);
         }
-        const float* As = lds[cur] + (wm0 + lrow) * LDK + kh * (BK / 2);
+        // KCD rows are BK floats with swizzled groups: group kh*4 + q of row
+        // r sits at (kh*4 + q) ^ (r & 7); rows 32 apart share r & 7.
+        constexpr int APITCH = AMODE == KCD ? BK : LDK;
+        const float* As = lds[cur] + (wm0 + lrow) * APITCH + (AMODE == KCD ? 0 : kh * (BK / 2));
+        auto a_off = [&](int q) {
+            return AMODE == KCD ? 4 * ((kh * 4 + q) ^ (lrow & 7)) : 4 * q;
+        };
         const float* Bs = lds[cur] + BM * LDK + (wn0 + lrow) * LDK + kh * (BK / 2);
         // MFMA operands for step group q+1 are read from LDS while group q's
         // MFMAs run (two register sets).
         f32x4 av[2][MI], bv[2][NI];
 #pragma unroll
-        for (int i = 0; i < MI; ++i) av[0][i] = *reinterpret_cast<const f32x4*>(As + 32 * i * LDK);
+        for (int i = 0; i < MI; ++i) av[0][i] = *reinterpret_cast<const f32x4*>(As + 32 * i * APITCH + a_off(0));
 #pragma unroll
         for (int j = 0; j < NI; ++j) bv[0][j] = *reinterpret_cast<const f32x4*>(Bs + 32 * j * LDK);
 #pragma unroll
@@ -486,7 +531,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
             if (q + 1 < QN) {
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
-                    av[cb ^ 1][i] = *reinterpret_cast<const f32x4*>(As + 32 * i * LDK + 4 * (q + 1));
+                    av[cb ^ 1][i] = *reinterpret_cast<const f32x4*>(As + 32 * i * APITCH + a_off(q + 1));
 #pragma unroll
                 for (int j = 0; j < NI; ++j)
                     bv[cb ^ 1][j] = *reinterpret_cast<const f32x4*>(Bs + 32 * j * LDK + 4 * (q + 1));
@@ -513,7 +558,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
             }
         }
         if (more) {
-            LA::store(ra, lds[cur ^ 1], tid);
+            if constexpr (AMODE != KCD) LA::store(ra, lds[cur ^ 1], tid);
             LB::store(rb, lds[cur ^ 1] + BM * LDK, tid);
         }
         __syncthreads();
@@ -736,6 +781,7 @@ static int launch_tiles(const GemmArgs& g, uint32_t batch, uint32_t splits, int 
     hipStream_t st = ctx().stream;
     switch (amode) {
         case KCV: launch_b<BM, BN, WM, WN, KCV>(g, grid, st, bmode); break;
+        case KCD: launch_b<BM, BN, WM, WN, KCD>(g, grid, st, bmode); break;
         case RCV: launch_b<BM, BN, WM, WN, RCV>(g, grid, st, bmode); break;
         case KCS: launch_b<BM, BN, WM, WN, KCS>(g, grid, st, bmode); break;
         default: launch_b<BM, BN, WM, WN, RCS>(g, grid, st, bmode); break;
@@ -943,7 +989,12 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
         g.split_stride = out_elems;
     }
     g.c = target;
-    const int amode = akc ? (g.a_vec ? KCV : KCS) : (g.a_vec ? RCV : RCS);
+    int amode = akc ? (g.a_vec ? KCV : KCS) : (g.a_vec ? RCV : RCS);
+    // Straight-to-LDS A: unit k stride, K a multiple of four, and every byte
+    // offset of one batch's A within the buffer resource's 2^31 bytes.
+    if (amode == KCV && g.sak == 1 && k % 4 == 0 &&
+        ((static_cast<int64_t>(m) - 1) * g.sam + k) * 4 < (int64_t{1} << 31))
+        amode = KCD;
     const int bmode = bkc ? (g.b_vec ? KCV : KCS) : (g.b_vec ? RCV : RCS);
     int st;
     if (tile.bm == 128)
