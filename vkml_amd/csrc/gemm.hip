@@ -433,6 +433,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
     // position.
     const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(abase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(bbase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
     const __amdgpu_buffer_rsrc_t img = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(im_in.x + static_cast<int64_t>(z) * im_in.sn), 0,
         static_cast<int32_t>(0x80000000u), 0x00020000);
@@ -467,12 +469,22 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
     f32x4 ra[LA::kRegs], rb[LB::kRegs];
     auto load_tile = [&](uint32_t kt, int dst) {
         (void)dst;
-        if constexpr (AMODE == KCD) {
+        // (The order matters for the schedule: with A straight into LDS and
+        // B through registers, A's loads go first; measured 4% on NN.)
+        if constexpr (AMODE == KCD && BMODE != KCD) {
             LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
             if (rows_in && (kt + 1) * BK <= g.k)
                 LB::template load<false>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
             else
                 LB::template load<true>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
+        } else if constexpr (BMODE == KCD) {
+            if constexpr (AMODE == KCD)
+                LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+            else if (rows_in && (kt + 1) * BK <= g.k)
+                LA::template load<false>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
+            else
+                LA::template load<true>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
+            LB::load_direct(lds[dst] + BM * LDK, brsrc, g.sbn, col0, g.n, kt * BK, g.k, tid);
         } else if constexpr (BMODE == IMG) {
             LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
             LB::load_img(rb, img, rows, base4, outside, kt * BK, tid);
@@ -490,7 +502,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
     if (kt0 < kt1) {
         load_tile(kt0, 0);
         if constexpr (AMODE != KCD) LA::store(ra, lds[0], tid);
-        LB::store(rb, lds[0] + BM * LDK, tid);
+        if constexpr (BMODE != KCD) LB::store(rb, lds[0] + BM * LDK, tid);
     }
     __syncthreads();
 
@@ -517,14 +529,18 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         auto a_off = [&](int q) {
             return AMODE == KCD ? 4 * ((kh * 4 + q) ^ (lrow & 7)) : 4 * q;
         };
-        const float* Bs = lds[cur] + BM * LDK + (wn0 + lrow) * LDK + kh * (BK / 2);
+        constexpr int BPITCH = BMODE == KCD ? BK : LDK;
+        const float* Bs = lds[cur] + BM * LDK + (wn0 + lrow) * BPITCH + (BMODE == KCD ? 0 : kh * (BK / 2));
+        auto b_off = [&](int q) {
+            return BMODE == KCD ? 4 * ((kh * 4 + q) ^ (lrow & 7)) : 4 * q;
+        };
         // MFMA operands for step group q+1 are read from LDS while group q's
         // MFMAs run (two register sets).
         f32x4 av[2][MI], bv[2][NI];
 #pragma unroll
         for (int i = 0; i < MI; ++i) av[0][i] = *reinterpret_cast<const f32x4*>(As + 32 * i * APITCH + a_off(0));
 #pragma unroll
-        for (int j = 0; j < NI; ++j) bv[0][j] = *reinterpret_cast<const f32x4*>(Bs + 32 * j * LDK);
+        for (int j = 0; j < NI; ++j) bv[0][j] = *reinterpret_cast<const f32x4*>(Bs + 32 * j * BPITCH + b_off(0));
 #pragma unroll
         for (int q = 0; q < QN; ++q) {
             const int cb = q & 1;
@@ -534,7 +550,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
                     av[cb ^ 1][i] = *reinterpret_cast<const f32x4*>(As + 32 * i * APITCH + a_off(q + 1));
 #pragma unroll
                 for (int j = 0; j < NI; ++j)
-                    bv[cb ^ 1][j] = *reinterpret_cast<const f32x4*>(Bs + 32 * j * LDK + 4 * (q + 1));
+                    bv[cb ^ 1][j] = *reinterpret_cast<const f32x4*>(Bs + 32 * j * BPITCH + b_off(q + 1));
             }
 #pragma unroll
             for (int s = 0; s < 4; ++s)
@@ -559,7 +575,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         }
         if (more) {
             if constexpr (AMODE != KCD) LA::store(ra, lds[cur ^ 1], tid);
-            LB::store(rb, lds[cur ^ 1] + BM * LDK, tid);
+            if constexpr (BMODE != KCD) LB::store(rb, lds[cur ^ 1] + BM * LDK, tid);
         }
         __syncthreads();
     }
@@ -769,6 +785,7 @@ static void launch_b(const GemmArgs& g, dim3 grid, hipStream_t st, int bmode) {
     constexpr int BK = 32;
     switch (bmode) {
         case KCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCV>), grid, dim3(256), 0, st, g, Im2colB{}); break;
+        case KCD: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCD>), grid, dim3(256), 0, st, g, Im2colB{}); break;
         case RCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, RCV>), grid, dim3(256), 0, st, g, Im2colB{}); break;
         case KCS: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, KCS>), grid, dim3(256), 0, st, g, Im2colB{}); break;
         default: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AM, RCS>), grid, dim3(256), 0, st, g, Im2colB{}); break;
@@ -990,12 +1007,15 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     }
     g.c = target;
     int amode = akc ? (g.a_vec ? KCV : KCS) : (g.a_vec ? RCV : RCS);
-    // Straight-to-LDS A: unit k stride, K a multiple of four, and every byte
-    // offset of one batch's A within the buffer resource's 2^31 bytes.
+    // Straight-to-LDS operands: unit k stride, K a multiple of four, and every
+    // byte offset of one batch's operand within the buffer resource's 2^31 bytes.
     if (amode == KCV && g.sak == 1 && k % 4 == 0 &&
         ((static_cast<int64_t>(m) - 1) * g.sam + k) * 4 < (int64_t{1} << 31))
         amode = KCD;
-    const int bmode = bkc ? (g.b_vec ? KCV : KCS) : (g.b_vec ? RCV : RCS);
+    int bmode = bkc ? (g.b_vec ? KCV : KCS) : (g.b_vec ? RCV : RCS);
+    if (bmode == KCV && g.sbk == 1 && k % 4 == 0 &&
+        ((static_cast<int64_t>(n) - 1) * g.sbn + k) * 4 < (int64_t{1} << 31))
+        bmode = KCD;
     int st;
     if (tile.bm == 128)
         st = launch_tiles<128, 128, 64, 64>(g, static_cast<uint32_t>(batch), splits, amode, bmode);
