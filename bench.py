@@ -395,7 +395,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "gemm_mfma_kernel<128,128,32,64,64,6,1>",
+                     "kernel": "gemm_nn_direct_kernel",
                      "avg_launch_ms": round(avg_ms, 4), "min_launch_ms": round(min_ms, 4)},
     }
     if args.calibrate:

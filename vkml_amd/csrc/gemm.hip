@@ -595,6 +595,143 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         }
 }
 
+
+// ---- NN with both operands straight into LDS ----------------------------------
+// A (k-contiguous) lands in LDS as in load mode KCD. B (row-contiguous, NN)
+// lands as it lies in memory, BK rows of BN = 128 floats, which the MFMA's B
+// operand cannot read as four consecutive k. Instead a lane reads four
+// consecutive columns of one k row with one 16-byte LDS read and feeds them to
+// four MFMAs, the s-th of which computes the 32 x 32 block of columns
+// {4c + s : c < 32}: a wave owns 32 rows x 128 columns as four such strided
+// column sets. Each output element still accumulates the same k pairs in the
+// same order as the register-path kernel (step (q, st) adds k = 4q + st and
+// 16 + 4q + st), so the results are the same bits.
+__device__ __forceinline__ void load_b_rows_direct(float* stage, __amdgpu_buffer_rsrc_t src,
+                                                   int64_t s_k, uint32_t col0, uint32_t cols,
+                                                   uint32_t k0, uint32_t kdim, int tid) {
+    // 32 k rows x 32 groups of 4 columns = 1024 slots, four per thread.
+    const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int chunk = 4 * i + wave;
+        const int slot = chunk * 64 + lane;
+        const int r = slot >> 5, grp = slot & 31;
+        const uint32_t gk = k0 + r, gc = col0 + 4 * grp;
+        const bool ok = gk < kdim && gc < cols;
+        const uint32_t off = ok ? static_cast<uint32_t>((static_cast<int64_t>(gk) * s_k + gc) * 4)
+                                : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            src, (__attribute__((address_space(3))) void*)(stage + chunk * 256), 16, off, 0, 0, 0);
+    }
+}
+
+__global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
+    constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
+    using LA = TileLoader<BM, BK, KCD>;
+    __shared__ __attribute__((aligned(16))) float lds[2][BM * LDK + BK * BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = wave * 32;
+
+    const uint32_t ntiles = g.tiles_m * g.tiles_n;
+    uint32_t bid = blockIdx.x;
+    if ((ntiles & 7u) == 0) bid = (bid & 7u) * (ntiles >> 3) + (bid >> 3);
+    const uint32_t group_span = 8u * g.tiles_n;
+    const uint32_t first_m = (bid / group_span) * 8u;
+    const uint32_t gsize = min(g.tiles_m - first_m, 8u);
+    const uint32_t tm = first_m + (bid % group_span) % gsize;
+    const uint32_t tn = (bid % group_span) / gsize;
+    const uint32_t row0 = tm * BM;
+    const uint32_t col0 = tn * BN;
+
+    const uint32_t z = blockIdx.z;
+    const uint32_t i0 = z / g.b1, i1 = z % g.b1;
+    const float* abase = g.a + i0 * g.sa0 + i1 * g.sa1;
+    const float* bbase = g.b + i0 * g.sb0 + i1 * g.sb1;
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(abase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(bbase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    float* cbase = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride +
+                   static_cast<uint64_t>(z) * g.m * g.n;
+    const uint32_t kt0 = blockIdx.y * g.chunk;
+    const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[s][r] = 0.0f;
+
+    auto load_tile = [&](uint32_t kt, int dst) {
+        LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+        load_b_rows_direct(lds[dst] + BM * LDK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+    };
+    if (kt0 < kt1) load_tile(kt0, 0);
+    __syncthreads();
+
+    const int lrow = lane & 31;
+    const int kh = lane >> 5;
+    for (uint32_t kt = kt0; kt < kt1; ++kt) {
+        const int cur = (kt - kt0) & 1;
+        if (kt + 1 < kt1) load_tile(kt + 1, cur ^ 1);
+        const float* As = lds[cur] + (wm0 + lrow) * BK;
+        const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + 4 * lrow;
+        auto a_at = [&](int q) {
+            return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ (lrow & 7)));
+        };
+        auto b_at = [&](int q, int st) {
+            return *reinterpret_cast<const f32x4*>(Bs + (4 * q + st) * BN);
+        };
+        f32x4 av[2], bv[2][4];
+        av[0] = a_at(0);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) bv[0][st] = b_at(0, st);
+#pragma unroll
+        for (int q = 0; q < QN; ++q) {
+            const int cb = q & 1;
+            if (q + 1 < QN) {
+                av[cb ^ 1] = a_at(q + 1);
+#pragma unroll
+                for (int st = 0; st < 4; ++st) bv[cb ^ 1][st] = b_at(q + 1, st);
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    acc[s] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][st], bv[cb][st][s], acc[s],
+                                                                  0, 0, 0);
+            {
+                const int reads = (q + 1 < QN) ? 5 : 0;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    if (r < reads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // acc[s] register r of lane l: row 8*(r/4) + 4*(l/32) + r%4 of the wave's
+    // 32, column 4*(l%32) + s of the tile: four columns per lane are adjacent.
+    const uint32_t col = col0 + 4 * lrow;
+    if (col < g.n) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
+            if (row < g.m) {
+                f32x4 v;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) v[s] = acc[s][r];
+                *reinterpret_cast<f32x4*>(cbase + static_cast<uint64_t>(row) * g.n + col) = v;
+            }
+        }
+    }
+}
+
 // ---- split-K partial fold --------------------------------------------------
 // Per output: the binary-counter carry stack over the `splits` partial slices,
 // drained in ascending level order from 0.0 (reference
@@ -1017,6 +1154,18 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
         ((static_cast<int64_t>(n) - 1) * g.sbn + k) * 4 < (int64_t{1} << 31))
         bmode = KCD;
     int st;
+    // NN with both operands straight into LDS: 128x128 tiles, A in load mode
+    // KCD, B row-contiguous with 16-byte rows and N a multiple of four (a
+    // 16-byte group is wholly inside or outside), byte offsets within 2^31.
+    if (tile.bm == 128 && amode == KCD && bmode == RCV && g.sbn == 1 && n % 4 == 0 &&
+        g.sbk % 4 == 0 && ((static_cast<int64_t>(k) - 1) * g.sbk + n) * 4 < (int64_t{1} << 31) &&
+        reinterpret_cast<uintptr_t>(target) % 16 == 0) {
+        dim3 grid(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
+        hipLaunchKernelGGL(gemm_nn_direct_kernel, grid, dim3(256), 0, ctx().stream, g);
+        VKHIP_LAUNCH_CHECK();
+        if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
+        return VKHIP_OK;
+    }
     if (tile.bm == 128)
         st = launch_tiles<128, 128, 64, 64>(g, static_cast<uint32_t>(batch), splits, amode, bmode);
     else
