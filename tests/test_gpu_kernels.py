@@ -98,6 +98,33 @@ def test_gemm_config2_512_layouts(hip, layout):
     check_gemm(a, b, ops.matmul(da, db).numpy())
 
 
+LAYOUT_SHAPES = [  # (batch, m, n, k): 128x128 tiles, split-K, ragged edges, M or N not 4-aligned
+    (1, 2048, 2044, 100),
+    (4, 1020, 1024, 70),
+    (1, 256, 256, 16384),
+    (1, 2046, 2048, 67),
+    (1, 2048, 2047, 33),
+]
+
+
+@pytest.mark.parametrize("batch,m,n,k", LAYOUT_SHAPES)
+def test_gemm_layouts_give_the_same_bits(hip, batch, m, n, k):
+    """NN, NT, TN and TT of the same values take different loaders (straight to
+    LDS as k rows or as k-contiguous rows, or through registers) but accumulate
+    every output's k pairs in one order, so all four are the same bits."""
+    rng = np.random.default_rng(SEED + m + n + k)
+    a = rng.uniform(-2, 2, (batch, m, k)).astype(np.float32)
+    b = rng.uniform(-2, 2, (batch, k, n)).astype(np.float32)
+    outs = {}
+    for lay in ("nn", "nt", "tn", "tt"):
+        _, da = layout_view(a, lay[0] == "t")
+        _, db = layout_view(b, lay[1] == "t")
+        outs[lay] = ops.matmul(da, db).numpy()
+    check_gemm(a, b, outs["nn"])
+    for lay in ("nt", "tn", "tt"):
+        np.testing.assert_array_equal(outs[lay], outs["nn"], err_msg=lay)
+
+
 def test_gemm_batched_broadcast_conv_shape(hip):
     """conv2d's GEMM: flat weight [Cout, CK] broadcast (stride 0) over a batch
     of cols [N, CK, L], plus the dW (NT) and dcols (TN) products of backward."""

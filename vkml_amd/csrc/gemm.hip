@@ -625,6 +625,11 @@ __device__ __forceinline__ void load_b_rows_direct(float* stage, __amdgpu_buffer
     }
 }
 
+// ATR (TN): A is row-contiguous too ([k][m] in memory) and lands the same
+// way as B, BK rows of 128; a lane reads its row's one float of a k row per
+// MFMA step (the rows of a wave are contiguous, so the 32 lanes of a half
+// read 32 adjacent floats).
+template <bool ATR>
 __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
     constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
     using LA = TileLoader<BM, BK, KCD>;
@@ -666,7 +671,10 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
         for (int r = 0; r < 16; ++r) acc[s][r] = 0.0f;
 
     auto load_tile = [&](uint32_t kt, int dst) {
-        LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+        if constexpr (ATR)
+            load_b_rows_direct(lds[dst], arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
+        else
+            LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
         load_b_rows_direct(lds[dst] + BM * LDK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
     };
     if (kt0 < kt1) load_tile(kt0, 0);
@@ -677,10 +685,17 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
     for (uint32_t kt = kt0; kt < kt1; ++kt) {
         const int cur = (kt - kt0) & 1;
         if (kt + 1 < kt1) load_tile(kt + 1, cur ^ 1);
-        const float* As = lds[cur] + (wm0 + lrow) * BK;
+        const float* As = ATR ? lds[cur] + kh * 16 * BM + wm0 + lrow : lds[cur] + (wm0 + lrow) * BK;
         const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + 4 * lrow;
         auto a_at = [&](int q) {
-            return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ (lrow & 7)));
+            if constexpr (ATR) {
+                f32x4 v;
+#pragma unroll
+                for (int st = 0; st < 4; ++st) v[st] = As[(4 * q + st) * BM];
+                return v;
+            } else {
+                return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ (lrow & 7)));
+            }
         };
         auto b_at = [&](int q, int st) {
             return *reinterpret_cast<const f32x4*>(Bs + (4 * q + st) * BN);
@@ -1148,14 +1163,22 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
         ((static_cast<int64_t>(n) - 1) * g.sbn + k) * 4 < (int64_t{1} << 31))
         bmode = KCD;
     int st;
-    // NN with both operands straight into LDS: 128x128 tiles, A in load mode
-    // KCD, B row-contiguous with 16-byte rows and N a multiple of four (a
-    // 16-byte group is wholly inside or outside), byte offsets within 2^31.
-    if (tile.bm == 128 && amode == KCD && bmode == RCV && g.sbn == 1 && n % 4 == 0 &&
-        g.sbk % 4 == 0 && ((static_cast<int64_t>(k) - 1) * g.sbk + n) * 4 < (int64_t{1} << 31) &&
+    // NN and TN with both operands straight into LDS: 128x128 tiles, B
+    // row-contiguous with 16-byte rows and N a multiple of four (a 16-byte
+    // group is wholly inside or outside), A in load mode KCD (NN) or
+    // row-contiguous like B with M a multiple of four (TN), byte offsets
+    // within 2^31.
+    const bool b_rows = bmode == RCV && g.sbn == 1 && n % 4 == 0 && g.sbk % 4 == 0 &&
+                        ((static_cast<int64_t>(k) - 1) * g.sbk + n) * 4 < (int64_t{1} << 31);
+    const bool a_rows = amode == RCV && g.sam == 1 && m % 4 == 0 && g.sak % 4 == 0 &&
+                        ((static_cast<int64_t>(k) - 1) * g.sak + m) * 4 < (int64_t{1} << 31);
+    if (tile.bm == 128 && b_rows && (amode == KCD || a_rows) &&
         reinterpret_cast<uintptr_t>(target) % 16 == 0) {
         dim3 grid(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
-        hipLaunchKernelGGL(gemm_nn_direct_kernel, grid, dim3(256), 0, ctx().stream, g);
+        if (amode == KCD)
+            hipLaunchKernelGGL(gemm_nn_direct_kernel<false>, grid, dim3(256), 0, ctx().stream, g);
+        else
+            hipLaunchKernelGGL(gemm_nn_direct_kernel<true>, grid, dim3(256), 0, ctx().stream, g);
         VKHIP_LAUNCH_CHECK();
         if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
         return VKHIP_OK;
