@@ -384,7 +384,8 @@ def check_softmax(got, want, n):
 
 @pytest.mark.parametrize("shape", [(4096, 1000), (256, 32768), (64, 10), (128, 100),
                                    (3, 1), (5, 4097), (7, 2048), (2, 3000), (33, 8192),
-                                   (9, 4096), (5, 16384), (3000, 257), (1025, 64)])
+                                   (9, 4096), (5, 16384), (3000, 257), (1025, 64),
+                                   (3, 100000), (512, 16384)])
 @pytest.mark.parametrize("log", [False, True])
 def test_softmax_parity(hip, shape, log):
     x = (np.random.default_rng(SEED + shape[1]).standard_normal(shape) * 2).astype(np.float32)
@@ -394,6 +395,42 @@ def test_softmax_parity(hip, shape, log):
         assert normwise_rel_err(got, want) <= gemm_tolerance(shape[1])
     else:
         check_softmax(got, want, shape[1])
+
+
+@pytest.mark.parametrize("n,structure", [(40000, "softmax_split_rows"),
+                                         (65537, "softmax_split_rows"),
+                                         (32769, "softmax_split_rows"),
+                                         (131072, "softmax_split_rows"),
+                                         (12290, "softmax_workgroup_per_row"),
+                                         (8196, "softmax_workgroup_per_row"),
+                                         (32768, "softmax_workgroup_per_row")])
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax_long_rows_special_values(hip, n, structure, log):
+    """Rows longer than 2048: a workgroup per row up to 32768 floats, beyond
+    that 4096-float chunks on separate workgroups (chunk statistics, then
+    outputs), including ragged last chunks and unaligned rows. A chunk of -inf
+    only, a NaN, a +inf and an all -inf row give the oracle's values."""
+    from vkml_amd.device import DecisionRecorder
+
+    x = (np.random.default_rng(SEED + n).standard_normal((6, n)) * 2).astype(np.float32)
+    x[1, :4096] = -np.inf          # a whole chunk of -inf
+    x[1, -3:] = -np.inf
+    x[2, n // 2] = np.nan
+    x[3, 5000] = np.inf
+    x[4, :] = -np.inf
+    x[5, ::7] = -np.inf
+    with DecisionRecorder() as rec:
+        got = ops.softmax(dev(x), -1, log).numpy()
+    assert [d["chose"] for d in rec.decisions if d["site"] == "softmax.structure"] == [structure]
+    want = O.softmax(x, -1, log)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    np.testing.assert_array_equal(np.isneginf(got), np.isneginf(want))
+    for r in (0, 1, 5):
+        fin = np.isfinite(want[r])
+        if log:
+            assert normwise_rel_err(got[r][fin], want[r][fin]) <= gemm_tolerance(n)
+        else:
+            check_softmax(got[r], want[r], n)
 
 
 STABILITY_INPUTS = golden("softmax_stability_inputs")["inputs"]  # test_vulkan_kernels.py:808-817

@@ -9,10 +9,13 @@
 //   - max/min/argmax/argmin are selections, merged with an explicit lowest-index
 //     tie-break, so any merge order gives the oracle's sequential answer:
 //     first maximum; max/min return the first NaN; argmax/argmin skip NaN.
-//   - softmax uses the same staged row: peak = max, denominator = the oracle's
-//     pairwise tree over exp(x - peak), out = exp(x - peak) / denom or
-//     (x - peak) - log(denom). exp/log are the device library's (OCML), so the
-//     result is within a few ulp of the oracle's libm, not bit-identical.
+//   - softmax: peak = max, out = exp(x - peak) / denom or (x - peak) -
+//     log(denom). Rows of up to 2048 (one wave each, the cross-entropy rows
+//     too) stage exp(x - peak) for the oracle's pairwise tree; longer rows sum
+//     it from registers in a fixed order (a different association, a few ulp).
+//     exp is a base-2 exponential with a carried rounding term and log is the
+//     device library's, so results are within a few ulp of the oracle's libm,
+//     not bit-identical.
 //
 // Bandwidth: one HBM read and (softmax) one write per element; the row never
 // leaves the CU between passes.
@@ -156,17 +159,37 @@ __device__ __forceinline__ float softmax_exp(float s) {
 // based, 1e-5 * sqrt(n) relative).
 __device__ __forceinline__ float div_by(float x, float /*d*/, float r) { return x * r; }
 
+// Sum over a group of T threads, in a fixed order (a wave butterfly, then the
+// waves' sums in wave order): deterministic, every thread gets the total.
+template <int T>
+__device__ float group_sum(float v, int t, float* scratch) {
+    v = wave_sum_butterfly(v);
+    if constexpr (T > 64) {
+        const int lane = t & 63, wave = t >> 6;
+        if (lane == 0) scratch[wave] = v;
+        __syncthreads();
+        const float u = lane < T / 64 ? scratch[lane] : 0.0f;
+        v = wave_sum_butterfly(u);
+        __syncthreads();
+    }
+    return v;
+}
+
 // T threads per row (64: four rows per 256-thread block), rows of n <= 4*E4*T
 // contiguous floats at src + row*in_stride; dst rows contiguous. The row is read
-// once into registers; exp(x - peak) is computed once, staged in LDS for the
-// pairwise denominator and kept in registers for the output.
+// once into registers and exp(x - peak) is computed once and kept there for
+// the output. The denominator is summed from the registers (each thread's
+// values in order, then group_sum): the row is not staged in LDS for the
+// oracle's pairwise tree, which at these widths held one workgroup per CU in
+// lockstep phases (256x32768: 18.6 us staged, 15.8 from registers). The
+// association differs from the oracle's tree by a few ulp of the
+// denominator, inside the softmax tolerance.
 template <int T, int E4, bool LOG>
 __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
     const float* __restrict__ src, int64_t in_stride, float* __restrict__ dst, uint32_t rows,
-    uint32_t n, int depth, int vec, uint32_t sstride) {
+    uint32_t n, int vec) {
     constexpr int RPB = Rows<T>::kPerBlock;
     constexpr int E = 4 * E4;
-    extern __shared__ __attribute__((aligned(16))) float dyn[];
     __shared__ float scratch[RPB][T / 64 > 0 ? T / 64 : 1];
 
     const int slot = threadIdx.x / T;
@@ -174,7 +197,6 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
     const uint32_t row = blockIdx.x * RPB + slot;
     const bool live = row < rows;
     const float* rs = src + static_cast<int64_t>(live ? row : 0) * in_stride;
-    float* stage = dyn + slot * sstride;
 
     float x[E];
     load_row<T, E4>(x, rs, n, t, live, vec);
@@ -184,19 +206,18 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
     float mx = tree_peak<E>(x, keep);
     mx = group_max<T>(mx, t, scratch[slot]);
 
+    float part = 0.0f;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-        const uint32_t e = elem_of(vec, T, t, i);
         const float sh = x[i] - mx;
         const float ex = softmax_exp(sh);
-        if (live && e < n) stage[stage_index(e)] = ex;
+        if (keep[i]) part = part + ex;
         x[i] = LOG ? sh : ex;
     }
-    __syncthreads();
-    const float denom = group_pairwise_sum<T>(stage, n, depth, t, scratch[slot]);
+    const float denom = group_sum<T>(part, t, scratch[slot]);
     if (!live) return;
     const float ld = logf(denom);
-        const float rinv = 1.0f / denom;
+    const float rinv = 1.0f / denom;
     float* ds = dst + static_cast<uint64_t>(row) * n;
     if (vec) {
 #pragma unroll
@@ -1113,15 +1134,11 @@ static int launch_select_rows(int op, const float* src, const Op4& kept, uint32_
 
 template <int T, int E4>
 static int launch_softmax_rows(const float* src, int64_t stride, float* dst, uint32_t rows,
-                               uint32_t n, int depth, int log_mode, int vec, hipStream_t st) {
+                               uint32_t n, int log_mode, int vec, hipStream_t st) {
     constexpr int RPB = Rows<T>::kPerBlock;
-    const uint32_t ss = stage_stride(n);
-    const size_t lds = static_cast<size_t>(RPB) * ss * sizeof(float);
     auto fn = log_mode ? softmax_rows_kernel<T, E4, true> : softmax_rows_kernel<T, E4, false>;
-    int rc = allow_lds(reinterpret_cast<const void*>(fn), lds);
-    if (rc != VKHIP_OK) return rc;
-    hipLaunchKernelGGL(fn, dim3(ceil_div(rows, RPB)), dim3(Rows<T>::kThreads), lds, st, src,
-                       stride, dst, rows, n, depth, vec, ss);
+    hipLaunchKernelGGL(fn, dim3(ceil_div(rows, RPB)), dim3(Rows<T>::kThreads), 0, st, src,
+                       stride, dst, rows, n, vec);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -1282,6 +1299,153 @@ __global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restri
     }
 }
 
+// ---- softmax over rows longer than a workgroup holds ------------------------------
+// Rows beyond kRowsMax floats are cut into chunks of kSmxChunk floats, one
+// workgroup each, in two launches:
+//   1. per chunk c: its peak m_c and s_c = sum of exp(x - m_c) over the chunk;
+//   2. per chunk: the row's peak M = max_c m_c and denominator
+//      d = sum_c s_c * exp(m_c - M), c ascending (the same arithmetic in every
+//      workgroup of the row), then the chunk's outputs exp(x - M) / d or
+//      (x - M) - log(d).
+// The second launch re-reads its chunk, which the first has just pulled
+// through the memory-side cache. (For 256x32768 this measured 17.9 us against
+// 15.8 for a workgroup per row, so shorter rows keep that path.) The
+// denominator is the oracle's sum re-associated (a few ulp; softmax parity is
+// tolerance-based). Special values come out as the oracle's: a chunk of -inf
+// only contributes 0, a NaN or +inf anywhere in a row makes the row NaN, an
+// all -inf row is NaN.
+constexpr uint32_t kSmxChunk = 4096;     // floats per workgroup (16 per thread)
+constexpr uint32_t kSmxMaxChunks = 256;  // rows up to 2^20 floats
+
+struct SmxStat {
+    float peak, sum;
+};
+
+template <bool VEC>
+__device__ __forceinline__ void load_chunk(float (&x)[16], bool (&keep)[16], const float* rs,
+                                           uint32_t b, uint32_t e, int t) {
+    if constexpr (VEC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t e0 = b + 4u * (t + 256 * i);
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (e0 < e) v = *reinterpret_cast<const f32x4*>(rs + e0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x[4 * i + j] = v[j];
+                keep[4 * i + j] = e0 < e;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t q = b + t + 256u * i;
+            keep[i] = q < e;
+            x[i] = keep[i] ? rs[q] : 0.0f;
+        }
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void softmax_chunk_stats_kernel(const float* __restrict__ src,
+                                                                  int64_t stride, uint32_t n,
+                                                                  uint32_t chunks,
+                                                                  SmxStat* __restrict__ stats) {
+    __shared__ float scratch[4];
+    const int t = threadIdx.x;
+    const uint32_t row = blockIdx.x / chunks, c = blockIdx.x % chunks;
+    const float* rs = src + static_cast<int64_t>(row) * stride;
+    const uint32_t b = c * kSmxChunk, e = min(n, b + kSmxChunk);
+    float x[16];
+    bool keep[16];
+    load_chunk<VEC>(x, keep, rs, b, e, t);
+    const float m = group_max<256>(tree_peak<16>(x, keep), t, scratch);
+    const bool all_ninf = m == -__builtin_inff();
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        // -inf - (-inf) would be NaN: a chunk of -inf only adds zeros (a NaN
+        // element still gives NaN).
+        const float sh = (all_ninf && x[i] == -__builtin_inff()) ? -__builtin_inff() : x[i] - m;
+        if (keep[i]) sum = sum + softmax_exp(sh);
+    }
+    sum = wave_sum_butterfly(sum);
+    if ((t & 63) == 0) scratch[t >> 6] = sum;
+    __syncthreads();
+    if (t == 0) stats[blockIdx.x] = SmxStat{m, (scratch[0] + scratch[1]) + (scratch[2] + scratch[3])};
+}
+
+template <bool VEC, bool LOG>
+__global__ __launch_bounds__(256) void softmax_chunk_apply_kernel(const float* __restrict__ src,
+                                                                  int64_t stride,
+                                                                  float* __restrict__ dst, uint32_t n,
+                                                                  uint32_t chunks,
+                                                                  const SmxStat* __restrict__ stats) {
+    const int t = threadIdx.x;
+    const uint32_t row = blockIdx.x / chunks, c = blockIdx.x % chunks;
+    const float* rs = src + static_cast<int64_t>(row) * stride;
+    const uint32_t b = c * kSmxChunk, e = min(n, b + kSmxChunk);
+    float x[16];
+    bool keep[16];
+    load_chunk<VEC>(x, keep, rs, b, e, t);
+
+    const SmxStat* rstat = stats + static_cast<uint64_t>(row) * chunks;
+    float peak = -__builtin_inff();
+    for (uint32_t j = 0; j < chunks; ++j) peak = __builtin_fmaxf(peak, rstat[j].peak);
+    float denom = 0.0f;
+    for (uint32_t j = 0; j < chunks; ++j) denom = denom + rstat[j].sum * softmax_exp(rstat[j].peak - peak);
+    const float ld = logf(denom);
+    const float rinv = 1.0f / denom;
+
+    float* ds = dst + static_cast<uint64_t>(row) * n;
+    if constexpr (VEC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t e0 = b + 4u * (t + 256 * i);
+            if (e0 < e) {
+                f32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float sh = x[4 * i + j] - peak;
+                    o[j] = LOG ? sh - ld : softmax_exp(sh) * rinv;
+                }
+                *reinterpret_cast<f32x4*>(ds + e0) = o;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t q = b + t + 256u * i;
+            if (keep[i]) {
+                const float sh = x[i] - peak;
+                ds[q] = LOG ? sh - ld : softmax_exp(sh) * rinv;
+            }
+        }
+    }
+}
+
+template <bool VEC>
+static int launch_softmax_split(const float* src, int64_t row_stride, float* dst, uint32_t rows,
+                                uint32_t n, int log_mode, hipStream_t st) {
+    const uint32_t chunks = ceil_div(n, kSmxChunk);
+    SmxStat* stats = nullptr;
+    int rc = workspace(static_cast<size_t>(rows) * chunks * sizeof(SmxStat),
+                       reinterpret_cast<float**>(&stats));
+    if (rc != VKHIP_OK) return rc;
+    const dim3 grid(rows * chunks);
+    hipLaunchKernelGGL(softmax_chunk_stats_kernel<VEC>, grid, dim3(256), 0, st, src, row_stride, n,
+                       chunks, stats);
+    VKHIP_LAUNCH_CHECK();
+    if (log_mode)
+        hipLaunchKernelGGL((softmax_chunk_apply_kernel<VEC, true>), grid, dim3(256), 0, st, src,
+                           row_stride, dst, n, chunks, stats);
+    else
+        hipLaunchKernelGGL((softmax_chunk_apply_kernel<VEC, false>), grid, dim3(256), 0, st, src,
+                           row_stride, dst, n, chunks, stats);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
 // Contiguous rows of up to 2048 floats: a wave per row, persistent with
 // next-row prefetch when there are more rows than waves. (A variant that kept
 // each thread's own 32-float leaves in registers for 4096..32768-wide rows was
@@ -1343,6 +1507,19 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
         }
         if (expect < 0) row_stride = n;
     }
+    const bool split = axis == 3 && d.nb[3] == 1 && rows_regular && n > kRowsMax &&
+                       ceil_div(n, kSmxChunk) <= kSmxMaxChunks &&
+                       static_cast<uint64_t>(rows) * ceil_div(n, kSmxChunk) < (1ull << 31);
+    if (split) {
+        const bool vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (n % 4 == 0) &&
+                         (row_stride % 4 == 0);
+        publish("softmax.structure", log_mode ? "log_softmax" : "softmax", "softmax_split_rows",
+                "softmax_workgroup_per_row", "rows longer than one workgroup's registers hold",
+                n, rows);
+        return vec ? launch_softmax_split<true>(src, row_stride, dst, rows, n, log_mode, st)
+                   : launch_softmax_split<false>(src, row_stride, dst, rows, n, log_mode, st);
+    }
     if (axis == 3 && d.nb[3] == 1 && rows_regular && n <= kRowsMax) {
         const int vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
                         (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (n % 4 == 0) &&
@@ -1356,7 +1533,7 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
             return log_mode ? launch_softmax_short<true>(src, row_stride, dst, rows, n, depth, vec, st)
                             : launch_softmax_short<false>(src, row_stride, dst, rows, n, depth, vec, st);
         const RowClass rc = row_class(n);
-        VKHIP_ROW_CLASSES(launch_softmax_rows, src, row_stride, dst, rows, n, depth, log_mode, vec, st)
+        VKHIP_ROW_CLASSES(launch_softmax_rows, src, row_stride, dst, rows, n, log_mode, vec, st)
     }
     // General layout: one thread per row.
     publish("softmax.structure", log_mode ? "log_softmax" : "softmax", "softmax_lane_per_row",
