@@ -654,6 +654,38 @@ def test_caching_allocator_reuses_and_accounts(hip):
     assert lib.vkhip_free(c_void_p(0x1000)) == _lib.ERR_INVALID
 
 
+@pytest.mark.parametrize("sizes", [[1 << 10, 3 << 20, 5 << 20, 7, 4 << 20, 1 << 22, 333],
+                                   [13 << 20, 9 << 20, 17 << 20, 20 << 20]])
+def test_host_copies_through_staging_slots(hip, sizes):
+    """vkhip_copy_from_host returns once the caller's bytes are copied (small
+    uploads go through pinned slots whose DMA is still queued): overwriting the
+    host buffer right away must not change what lands on the device, uploads
+    queued behind a running kernel land after it, and a ring's worth of
+    uploads (chunked, reusing slots) and the direct path above it all arrive."""
+    from ctypes import c_void_p
+
+    lib = _lib.load()
+    rng = np.random.default_rng(SEED + 91)
+    devs, wants = [], []
+    big = dev(rng.standard_normal((4096, 4096)).astype(np.float32))
+    for nbytes in sizes:
+        n = nbytes // 4 + 1
+        x = rng.standard_normal(n).astype(np.float32)
+        d = DeviceArray((n,), np.float32)
+        ops.matmul(big, big)  # keep the stream busy while the upload is queued
+        assert lib.vkhip_copy_from_host(c_void_p(d.ptr), x.ctypes.data_as(c_void_p), x.nbytes) == 0
+        wants.append(x.copy())
+        x[:] = -1.0  # the caller's buffer is free once the call returns
+        devs.append(d)
+    for d, want in zip(devs, wants):
+        assert d.numpy().tobytes() == want.tobytes()
+    # Small downloads through a slot, back to back.
+    for d, want in zip(devs, wants):
+        head = np.empty(min(want.size, 1000), np.float32)
+        assert lib.vkhip_copy_to_host(head.ctypes.data_as(c_void_p), c_void_p(d.ptr), head.nbytes) == 0
+        assert head.tobytes() == want[:head.size].tobytes()
+
+
 def test_decision_facts_join_profile_records(hip):
     """Decision facts name the kernel each op chose with the numbers behind it,
     and their dispatch ids join with the per-unit timing records (reference

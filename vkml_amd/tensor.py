@@ -931,9 +931,23 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         raise NotImplementedError(f"no gradient rule for op {op}")
 
 
+# Backward flushes the gradients built so far after the first rule it applies
+# and then after every BACKWARD_FLUSH_EVERY rules, so the device starts on the
+# forward pass (which the first gradient needs) while the host is still
+# building the rest of the backward graph. Only nodes the final flush would
+# compute anyway are computed, each once, so the results are the same; 0 turns
+# it off (one flush at the end, as the reference does). Graphs whose
+# uncomputed nodes hold less than BACKWARD_FLUSH_MIN_BYTES are flushed once at
+# the end: their device work is shorter than a flush's host cost (the config-1
+# MLP step: 0.50 ms with one flush, 0.54 with early ones; the config-5 CNN step
+# 1.57 -> 1.29 ms with them).
+BACKWARD_FLUSH_EVERY = 8
+BACKWARD_FLUSH_MIN_BYTES = 8 << 20
+
+
 def backward(root: Tensor, seed: Tensor | None = None) -> None:
-    """Reverse-mode pass from `root`; leaf gradients are realised in ONE flush
-    (reference autograd.cpp:588-673)."""
+    """Reverse-mode pass from `root`; leaf gradients are realised in one final
+    flush (reference autograd.cpp:588-673), after the early flushes above."""
     if not root.requires_grad:
         raise RuntimeError("backward() called on a tensor that does not require grad")
     if seed is None:
@@ -942,12 +956,25 @@ def backward(root: Tensor, seed: Tensor | None = None) -> None:
         seed = ones(root.shape, root.dtype, root.node.backend)
     order = _autograd_order(root.node)
     grads = {id(root.node): (root.node, seed)}
+    every = 0
+    if BACKWARD_FLUSH_EVERY > 0:
+        pending = 0
+        for node in order:
+            if not node.computed:
+                pending += _numel(node.shape) * node.itemsize
+                if pending >= BACKWARD_FLUSH_MIN_BYTES:
+                    every = BACKWARD_FLUSH_EVERY
+                    break
     with no_grad():
+        applied = 0
         for node in reversed(order):
             entry = grads.get(id(node))
             if entry is None or node.op in LEAF_OPS:
                 continue
             _apply_backward(node, entry[1], grads)
+            if every and applied % every == 0:
+                realize([grads[id(s)][1] for s in node.src if id(s) in grads])
+            applied += 1
         totals, leaves = [], []
         for node in order:
             if node.op not in LEAF_OPS or not node.requires_grad:
