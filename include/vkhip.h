@@ -230,6 +230,9 @@ int vkhip_free(void* ptr);
 int vkhip_release_cached(void);
 /* Bytes handed out and not freed, and bytes held in the caches. */
 int vkhip_memory_stats(size_t* bytes_in_use, size_t* bytes_cached);
+/* Returns once the host bytes are copied (uploads up to 16 MB through pinned
+ * staging slots, the DMA queued on the stream before any later work): the
+ * caller may reuse host_src at once (backend.h copy_from_host). */
 int vkhip_copy_from_host(void* dst, const void* host_src, size_t nbytes);
 int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes); /* synchronises */
 /* One unit of work for several disjoint copies (backend.h:83-108). */
