@@ -152,6 +152,17 @@ def test_gemm_large_k_cancellation(hip):
     assert np.max(np.abs(got - exact)) <= gemm_atol(a, b)
 
 
+def test_gemm_empty_k_writes_zeros(hip):
+    """K == 0: every output is an empty sum, 0 (the reference's CPU loop), written
+    by a fill kernel over whatever the output buffer held."""
+    for a_shape, b_shape in (((5, 0), (0, 7)), ((2, 3, 0), (2, 0, 4))):
+        out_shape = a_shape[:-1] + b_shape[-1:]
+        out = dev(np.full(out_shape, np.nan, np.float32))
+        got = ops.matmul(dev(np.zeros(a_shape, np.float32)), dev(np.zeros(b_shape, np.float32)),
+                         out=out).numpy()
+        assert got.shape == out_shape and not np.signbit(got).any() and (got == 0).all()
+
+
 def test_gemm_is_deterministic(hip):
     rng = np.random.default_rng(SEED + 33)
     a, b = dev(rng.uniform(-2, 2, (64, 128)).astype(np.float32)), \

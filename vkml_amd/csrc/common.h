@@ -55,6 +55,9 @@ struct Unit {
     Unit& operator=(const Unit&) = delete;
 };
 
+// Zero-fill of `count` floats on the backend stream (elementwise.hip).
+int launch_zero_f32(float* dst, uint64_t count);
+
 // The caching allocator behind vkhip_alloc / vkhip_free (allocator.hip).
 int cached_alloc(size_t nbytes, void** out);
 int cached_free(void* ptr);

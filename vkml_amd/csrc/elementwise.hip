@@ -326,6 +326,25 @@ __global__ __launch_bounds__(256) void copy16_kernel(const f32x4_t* __restrict__
         dst[i] = src[i];
 }
 
+// Zero-fill of `count` floats: a kernel rather than hipMemsetAsync, so the
+// launch sequence stays free of memset nodes when a caller captures the stream
+// into a graph.
+__global__ __launch_bounds__(256) void zero_f32_kernel(float* __restrict__ dst, uint64_t count) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride)
+        dst[i] = 0.0f;
+}
+
+int launch_zero_f32(float* dst, uint64_t count) {
+    if (count == 0) return VKHIP_OK;
+    const uint64_t want = (count + 255) / 256;
+    const uint32_t blocks = static_cast<uint32_t>(want < 65536 ? want : 65536);
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(blocks), dim3(256), 0, ctx().stream, dst, count);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
 int launch_copy_bytes(void* dst, const void* src, size_t nbytes) {
     if (nbytes == 0) return VKHIP_OK;
     hipStream_t st = ctx().stream;

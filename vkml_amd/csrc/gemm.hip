@@ -1076,8 +1076,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     const int kernel = opts ? opts->kernel : VKHIP_GEMM_AUTO;
     const int32_t split_req = opts ? opts->split_k : 0;
     if (k == 0) {
-        VKHIP_HIP(hipMemsetAsync(c, 0, batch * m * n * sizeof(float), ctx().stream));
-        return VKHIP_OK;
+        return launch_zero_f32(c, batch * m * n);
     }
 
     // GEMV: an N == 1 product with a unit-stride K axis of A is a bandwidth
@@ -1336,8 +1335,7 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
     const uint32_t m = wd.ne[2], n = static_cast<uint32_t>(L), k = static_cast<uint32_t>(ck);
     if (batch == 0 || m == 0 || n == 0) return VKHIP_OK;
     if (k == 0) {
-        VKHIP_HIP(hipMemsetAsync(out, 0, batch * m * n * sizeof(float), ctx().stream));
-        return VKHIP_OK;
+        return launch_zero_f32(out, batch * m * n);
     }
     uint32_t splits, chunk;
     TileChoice tile;
