@@ -60,11 +60,15 @@ class no_grad:
 
 
 def contiguous_strides(shape: Sequence[int]) -> tuple[int, ...]:
-    out, s = [], 1
-    for e in reversed(list(shape)):
-        out.append(s)
-        s *= int(e)
-    return tuple(reversed(out))
+    n = len(shape)
+    if n == 0:
+        return ()
+    out = [1] * n
+    s = 1
+    for i in range(n - 1, 0, -1):
+        s *= int(shape[i])
+        out[i - 1] = s
+    return tuple(out)
 
 
 def _numel(shape) -> int:
@@ -159,14 +163,14 @@ def default_backend():
 class Node:
     __slots__ = ("op", "shape", "strides", "dtype", "src", "params", "view_src", "view_offset",
                  "storage", "offset", "computed", "requires_grad", "grad", "backend", "aux",
-                 "__weakref__")
+                 "rec", "__weakref__")
 
     def __init__(self, op, shape, dtype, backend, src=(), params=b"", requires_grad=False,
                  strides=None):
         self.op = op
-        self.shape = tuple(int(e) for e in shape)
+        self.shape = tuple(map(int, shape))
         self.strides = tuple(strides) if strides is not None else contiguous_strides(self.shape)
-        self.dtype = np.dtype(dtype)
+        self.dtype = dtype if isinstance(dtype, np.dtype) else np.dtype(dtype)
         self.src = list(src)
         self.params = params
         self.view_src = None
@@ -178,6 +182,7 @@ class Node:
         self.grad = None
         self.backend = backend
         self.aux = None  # op-specific host data (permutation, axis, ...)
+        self.rec = None  # packed tensor fields, cached once the storage is bound
 
     @property
     def is_view(self) -> bool:
@@ -685,9 +690,16 @@ assert _NODE_RECORD.size == ctypes.sizeof(_lib.NodeDesc)
 
 
 def _tensor_fields(n: Node) -> tuple:
-    pad = _PADS[len(n.shape)]
-    data = n.storage.ptr + n.offset * n.dtype.itemsize if n.storage is not None else 0
-    return (data, _VK_DTYPE[n.dtype], len(n.shape)) + n.shape + pad + n.strides + pad
+    """The vkhip_tensor fields of a node with bound storage, cached on the node
+    (storage, offset and strides only change through assign(), which clears it)."""
+    rec = n.rec
+    if rec is None:
+        pad = _PADS[len(n.shape)]
+        if n.storage is None:
+            return (0, _VK_DTYPE[n.dtype], len(n.shape)) + n.shape + pad + n.strides + pad
+        data = n.storage.ptr + n.offset * n.dtype.itemsize
+        rec = n.rec = (data, _VK_DTYPE[n.dtype], len(n.shape)) + n.shape + pad + n.strides + pad
+    return rec
 
 
 def realize(tensors: Iterable[Tensor]) -> None:
@@ -702,19 +714,23 @@ def realize(tensors: Iterable[Tensor]) -> None:
     order: list[Node] = []
     seen: set[int] = set()
     stack = list(reversed(roots))
+    push, pop, mark, emit = stack.append, stack.pop, seen.add, order.append
     while stack:
         node = stack[-1]
         nid = id(node)
         if nid in seen:
-            stack.pop()
+            pop()
             continue
-        waiting = [c for c in node.src if not c.computed and id(c) not in seen]
+        waiting = False
+        for c in reversed(node.src):
+            if not c.computed and id(c) not in seen:
+                push(c)
+                waiting = True
         if waiting:
-            stack.extend(reversed(waiting))
             continue
-        stack.pop()
-        seen.add(nid)
-        order.append(node)
+        pop()
+        mark(nid)
+        emit(node)
     by_backend: dict[int, list[Node]] = {}
     backends = {}
     for node in order:
@@ -731,16 +747,17 @@ def realize(tensors: Iterable[Tensor]) -> None:
         by_backend.setdefault(id(node.backend), []).append(node)
         backends[id(node.backend)] = node.backend
     size = _NODE_RECORD.size
+    pack = _NODE_RECORD.pack_into
     for key, nodes in by_backend.items():
         buf = bytearray(size * len(nodes))
         for k, node in enumerate(nodes):
             src = node.src
-            fields = [node.op, len(src)]
-            fields += _tensor_fields(node)
-            for j in range(3):
-                fields += _tensor_fields(src[j]) if j < len(src) else _NO_TENSOR
-            fields.append(node.params or b"")
-            _NODE_RECORD.pack_into(buf, k * size, *fields)
+            ns = len(src)
+            pack(buf, k * size, node.op, ns, *_tensor_fields(node),
+                 *(_tensor_fields(src[0]) if ns > 0 else _NO_TENSOR),
+                 *(_tensor_fields(src[1]) if ns > 1 else _NO_TENSOR),
+                 *(_tensor_fields(src[2]) if ns > 2 else _NO_TENSOR),
+                 node.params or b"")
         arr = (_lib.NodeDesc * len(nodes)).from_buffer(buf)
         backends[key].compute(arr, len(nodes))
         for node in nodes:
@@ -755,6 +772,7 @@ def assign(params: Sequence[Tensor], values: Sequence[Tensor]) -> None:
         p.node.storage = v.node.storage
         p.node.offset = v.node.offset
         p.node.strides = v.node.strides
+        p.node.rec = None
         p.node.computed = True
 
 
