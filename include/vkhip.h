@@ -142,7 +142,12 @@ enum vkhip_op {
      * params vkhip_unfold -> out [N,Cout,C*kh*kw]: per image grad @ im2col(x)^T,
      * the conv2d weight gradient before its batch sum, bit-identical to IM2COL
      * followed by MATMUL(grad, cols^T). */
-    VKHIP_OP_CONV2D_WEIGHT_GRAD = 99
+    VKHIP_OP_CONV2D_WEIGHT_GRAD = 99,
+    /* src0 x, src1 g (the relu's input and the gradient of its output, same
+     * extents as out) -> out = x <= 0 ? +0 : g: the reference relu gradient
+     * where(less_equal(x, zeros_like(x)), zeros_like(g), g) (autograd.cpp:397-408)
+     * as one node, value for value (a NaN x passes g through). */
+    VKHIP_OP_RELU_BACKWARD = 100
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */

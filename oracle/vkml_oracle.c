@@ -539,6 +539,16 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                     ((uint8_t*)o->data)[i] = (uint8_t)compare_f(nd->op, x[lin_off(i, s0.ne, s0.nb)], y[lin_off(i, s1.ne, s1.nb)]);
                 break;
             }
+            case VKHIP_OP_RELU_BACKWARD: {
+                /* where(less_equal(x, zeros_like(x)), zeros_like(g), g), autograd.cpp:397-408 */
+                const float* x = (const float*)nd->src[0].data;
+                const float* g = (const float*)nd->src[1].data;
+                for (int64_t i = 0; i < n; ++i) {
+                    const float xv = x[lin_off(i, s0.ne, s0.nb)];
+                    ((float*)o->data)[i] = compare_f(VKHIP_OP_LESS_EQUAL, xv, 0.0f) ? 0.0f : g[lin_off(i, s1.ne, s1.nb)];
+                }
+                break;
+            }
             case VKHIP_OP_WHERE: {
                 const uint8_t* c = (const uint8_t*)nd->src[0].data;
                 const float* x = (const float*)nd->src[1].data;

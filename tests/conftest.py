@@ -114,6 +114,35 @@ def conv_loss_and_grads(backend, x, w, bias, stride, pad, dil, implicit, x_grad=
         T.IMPLICIT_CONV = prev
 
 
+def relu_inputs(shape, seed):
+    """x and the output gradient g for the relu gradient, with NaN, +-0, +-inf
+    in both (the select must pass NaN x through and keep g's bits)."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(shape).astype(np.float32)
+    g = rng.standard_normal(shape).astype(np.float32)
+    flat_x, flat_g = x.reshape(-1), g.reshape(-1)
+    specials = np.array([np.nan, 0.0, -0.0, np.inf, -np.inf, 1e-45, -1e-45], np.float32)
+    k = min(flat_x.size, specials.size)
+    flat_x[:k] = specials[:k]
+    flat_g[1:1 + k] = specials[:k][: max(0, min(k, flat_g.size - 1))]
+    return x, g
+
+
+def relu_grad(backend, x, g, fused):
+    """d(relu(x))/dx applied to g on `backend`, as the RELU_BACKWARD node
+    (fused=True) or as the reference's where/less_equal/zeros_like nodes."""
+    from vkml_amd import tensor as T
+
+    prev = T.FUSED_RELU_BACKWARD
+    T.FUSED_RELU_BACKWARD = fused
+    try:
+        xt = T.tensor(x, requires_grad=True, backend=backend)
+        T.backward(T.relu(xt), T.tensor(g, backend=backend))
+        return xt.grad.numpy()
+    finally:
+        T.FUSED_RELU_BACKWARD = prev
+
+
 CONV_GEOMETRIES = [  # (x shape, Cout, kernel, stride, pad, dilation)
     ((2, 3, 5, 5), 4, (3, 3), (1, 1), (1, 1), (1, 1)),
     ((1, 2, 6, 6), 3, (2, 2), (2, 2), (0, 0), (1, 1)),

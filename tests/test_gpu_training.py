@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads,
-                      gemm_tolerance, normwise_rel_err)
+                      gemm_tolerance, normwise_rel_err, relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -174,3 +174,15 @@ def test_fused_cross_entropy_on_device(backends, shape):
     ol, og = ce_loss_and_grad(cpu, logits, labels, True)
     np.testing.assert_allclose(fl, ol, rtol=1e-5)
     assert normwise_rel_err(fg, og) <= gemm_tolerance(shape[1])
+
+
+@pytest.mark.parametrize("shape", [(5, 7), (2, 3, 4, 5), (128, 64, 32, 32), (127, 3, 5), (1,)])
+def test_fused_relu_backward_on_device(backends, shape):
+    """Device RELU_BACKWARD: byte for byte the device's where/less_equal graph
+    and the oracle's node (a select: exact), NaN/+-0/+-inf included; the
+    vector path (contiguous, a multiple of 4) and the generic one both run."""
+    dev, cpu = backends
+    x, g = relu_inputs(shape, 29 + len(shape))
+    fused = relu_grad(dev, x, g, True)
+    assert fused.tobytes() == relu_grad(dev, x, g, False).tobytes()
+    assert fused.tobytes() == relu_grad(cpu, x, g, True).tobytes()

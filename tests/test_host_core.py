@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads
+from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads,
+                      relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -151,6 +152,19 @@ def test_fused_cross_entropy_is_bit_identical_to_the_node_graph(cpu, shape):
     fl, fg = ce_loss_and_grad(cpu, logits, labels, True)
     gl, gg = ce_loss_and_grad(cpu, logits, labels, False)
     assert fl.tobytes() == gl.tobytes() and fg.tobytes() == gg.tobytes()
+
+
+@pytest.mark.parametrize("shape", [(5, 7), (2, 3, 4, 5), (128, 256), (1,)])
+def test_fused_relu_backward_is_bit_identical_to_the_node_graph(cpu, shape):
+    """The RELU_BACKWARD node against the reference's where(less_equal(x, 0),
+    zeros, g) on the oracle, byte for byte, NaN/+-0/+-inf included; and the
+    values torch's relu gradient gives on numbers (NaN x passes g through)."""
+    x, g = relu_inputs(shape, 17 + len(shape))
+    fused = relu_grad(cpu, x, g, True)
+    graph = relu_grad(cpu, x, g, False)
+    assert fused.tobytes() == graph.tobytes()
+    want = np.where(x <= 0, np.float32(0.0), g)
+    assert fused.tobytes() == want.astype(np.float32).tobytes()
 
 
 @pytest.mark.parametrize("shape", [(64, 10), (128, 100)])

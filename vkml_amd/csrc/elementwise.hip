@@ -148,6 +148,11 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EwArgs a) {
                 store_out(a, i, x <= 0.0f ? 0.0f : x);
                 break;
             }
+            case VKHIP_OP_RELU_BACKWARD: {
+                const float x = load_f(a.s[0], i, k);
+                store_out(a, i, x <= 0.0f ? 0.0f : load_f(a.s[1], i, k));
+                break;
+            }
             case VKHIP_OP_ADD: store_out(a, i, __fadd_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
             case VKHIP_OP_SUB: store_out(a, i, __fsub_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
             case VKHIP_OP_MUL: store_out(a, i, __fmul_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
@@ -223,6 +228,7 @@ __global__ __launch_bounds__(256) void elementwise_f32_vec_kernel(int op, const 
                 r[j] = __fadd_rn(__fmul_rn(a[j], alpha), __fmul_rn(b[j], beta));
                 break;
             case VKHIP_OP_RELU: r[j] = a[j] <= 0.0f ? 0.0f : a[j]; break;
+            case VKHIP_OP_RELU_BACKWARD: r[j] = a[j] <= 0.0f ? 0.0f : b[j]; break;
             case VKHIP_OP_NEG: r[j] = -a[j]; break;
             default: r[j] = a[j]; break;  // contiguous copy
         }
@@ -274,7 +280,7 @@ int launch_elementwise(const vkhip_node& nd) {
     const int op = nd.op;
     const bool vec_op = op == VKHIP_OP_ADD || op == VKHIP_OP_SUB || op == VKHIP_OP_MUL ||
                         op == VKHIP_OP_SCALED_ADD || op == VKHIP_OP_RELU || op == VKHIP_OP_NEG ||
-                        op == VKHIP_OP_CONTIGUOUS;
+                        op == VKHIP_OP_CONTIGUOUS || op == VKHIP_OP_RELU_BACKWARD;
     if (vec_op && n % 4 == 0 && nd.out.dtype == VKHIP_F32) {
         bool ok = reinterpret_cast<uintptr_t>(nd.out.data) % 16 == 0;
         for (int s = 0; s < nd.n_src && ok; ++s)

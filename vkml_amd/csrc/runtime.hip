@@ -140,6 +140,7 @@ static bool is_elementwise(int op) {
         case VKHIP_OP_SCALED_ADD: case VKHIP_OP_MAXIMUM: case VKHIP_OP_MINIMUM:
         case VKHIP_OP_EQUAL: case VKHIP_OP_LESS: case VKHIP_OP_GREATER: case VKHIP_OP_LESS_EQUAL:
         case VKHIP_OP_GREATER_EQUAL: case VKHIP_OP_NOT_EQUAL: case VKHIP_OP_WHERE:
+        case VKHIP_OP_RELU_BACKWARD:
             return true;
         default: return false;
     }
@@ -177,6 +178,7 @@ static int supports_node(const vkhip_node& nd) {
         case VKHIP_OP_SCALED_ADD:
         case VKHIP_OP_MAXIMUM:
         case VKHIP_OP_MINIMUM:
+        case VKHIP_OP_RELU_BACKWARD:
             return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]);
         case VKHIP_OP_EQUAL:
         case VKHIP_OP_LESS:
@@ -286,6 +288,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_EXP: return "exp";
         case VKHIP_OP_LOG: return "log";
         case VKHIP_OP_RELU: return "relu";
+        case VKHIP_OP_RELU_BACKWARD: return "relu_backward";
         case VKHIP_OP_ADD: return "add";
         case VKHIP_OP_SUB: return "sub";
         case VKHIP_OP_MUL: return "mul";

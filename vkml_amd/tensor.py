@@ -353,7 +353,10 @@ class Tensor:
         return _view(BROADCAST, self, dims, strides, 0)
 
     def contiguous(self) -> "Tensor":
-        if self.node.is_contiguous() and not self.node.is_view:
+        """Self when the layout is already contiguous, a view included (its data
+        pointer carries the offset), else a CONTIGUOUS copy (reference
+        tensor.cpp:287-299)."""
+        if self.node.is_contiguous():
             return self
         return _unary(OP["CONTIGUOUS"], self)
 
@@ -659,6 +662,13 @@ def one_hot_f32(target: Tensor, classes: int) -> Tensor:
 # builds the reference's node graph.
 FUSED_CROSS_ENTROPY = True
 
+# The relu gradient where(less_equal(x, zeros_like(x)), zeros_like(g), g)
+# (reference autograd.cpp:397-408) as one RELU_BACKWARD node: x <= 0 ? +0 : g,
+# the same values (a select, no arithmetic) from one pass over x and g instead
+# of four kernels and two materialised zero tensors. False builds the
+# reference's nodes.
+FUSED_RELU_BACKWARD = True
+
 
 def cross_entropy(logits: Tensor, target: Tensor) -> Tensor:
     """mean(-sum(log_softmax(logits) * one_hot, -1)) (reference ops.cpp:417-441)."""
@@ -880,7 +890,13 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
     elif op == OP["LOG"]:
         _accumulate(grads, a, grad / ta())
     elif op == OP["RELU"]:
-        _accumulate(grads, a, where(less_equal(ta(), zeros_like(ta())), zeros_like(grad), grad))
+        if FUSED_RELU_BACKWARD:
+            x = ta()
+            g = grad if grad.shape == x.shape else grad.broadcast_to(x.shape)
+            rb = Node(OP["RELU_BACKWARD"], x.shape, np.float32, x.node.backend, [x.node, g.node])
+            _accumulate(grads, a, Tensor(rb))
+        else:
+            _accumulate(grads, a, where(less_equal(ta(), zeros_like(ta())), zeros_like(grad), grad))
     elif op in (OP["SUM"], OP["MEAN"]):
         mask, keepdim = node.aux
         src_dims = list(a.shape)
