@@ -505,6 +505,11 @@ def test_softmax_non_last_axis(hip):
     ((7, 3000), [1]),           # two rows per workgroup, odd row count, uneven tree
     ((6, 5, 2052), [2]),        # two rows per workgroup over two kept axes
     ((2, 3, 600000), [0, 2]),   # subtrees too long to stage: per-output workgroups
+    ((256, 100), [0]),          # strided, 8 pairwise leaves: a wave per leaf
+    ((100, 77), [0]),           # 4 uneven leaves
+    ((33, 5), [0]),             # 2 leaves of 16 and 17
+    ((128, 9216), [0]),         # many outputs, 4 leaves each
+    ((3, 50, 7), [0, 1]),       # 150 over two strided axes, 8 leaves
 ])
 def test_sum_mean_bit_exact(hip, shape, axes):
     x = (np.random.default_rng(SEED).standard_normal(shape) * 10).astype(np.float32)

@@ -510,6 +510,61 @@ static Reader single_reader(int64_t step) {
     return r;
 }
 
+// Sum/mean with few pairwise leaves per output (n_red <= 256: at most 8
+// leaves of <= 32): a workgroup of 64 x L threads covers 64 consecutive
+// outputs, wave w summing leaf w of each (its <= 32 loads in flight at once,
+// lanes on consecutive outputs), and lane o of wave 0 then folds the L leaf
+// sums in the order the one-thread carry stack of reduce_tall_kernel folds
+// them. Same association, so the same bits, in one memory round trip instead
+// of one per leaf.
+template <int L>
+__global__ __launch_bounds__(64 * L) void reduce_tall_leaves_kernel(
+    const float* __restrict__ src, Op4 kept, Reader rd, uint32_t n_out, uint32_t n_red, int mean,
+    float* __restrict__ dst) {
+    static_assert(L == 2 || L == 4 || L == 8, "leaves per output");
+    constexpr int D = L == 2 ? 1 : L == 4 ? 2 : 3;
+    __shared__ float part[L][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t o = blockIdx.x * 64u + lane;
+    if (o < n_out) {
+        const float* base = src + lin_off4(o, kept.ne, kept.nb);
+        uint32_t b, e;
+        pairwise_leaf(n_red, D, static_cast<uint32_t>(w), b, e);
+        float v[32];
+#pragma unroll
+        for (int r = 0; r < 32; ++r) v[r] = b + r < e ? base[rd.off(b + r)] : 0.0f;
+        float s = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 32; ++r)
+            if (b + r < e) s = s + v[r];
+        part[w][lane] = s;
+    }
+    __syncthreads();
+    if (w != 0 || o >= n_out) return;
+    float stack[D + 1];
+#pragma unroll
+    for (int l = 0; l <= D; ++l) stack[l] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        float s = part[j][lane];
+        bool carry = true;
+#pragma unroll
+        for (int l = 0; l <= D; ++l) {
+            if (carry) {
+                if ((j >> l) & 1) {
+                    s = stack[l] + s;
+                } else {
+                    stack[l] = s;
+                    carry = false;
+                }
+            }
+        }
+    }
+    float total = stack[D];
+    if (mean) total = total / static_cast<float>(n_red);
+    dst[o] = total;
+}
+
 __global__ __launch_bounds__(256) void reduce_tall_kernel(int op, const float* __restrict__ src,
                                                           Op4 kept, Reader rd, uint64_t n_out,
                                                           uint32_t n_red, int depth,
@@ -1243,6 +1298,25 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
         hipLaunchKernelGGL(reduce_wide_strided_kernel<256>, dim3(n_out), dim3(256), 0, st, src,
                            kept, rd, n_red, depth, op == VKHIP_REDUCE_MEAN ? 1 : 0,
                            static_cast<float*>(dst));
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
+    if (sum_op && depth >= 1 && depth <= 3 && n_out < (1ull << 32) - 64) {
+        publish("reduce.structure", rname, "reduce_wave_per_leaf", "reduce_lane_per_output",
+                "the reduced elements are strided, at most 8 pairwise leaves per output",
+                n_red, n_out);
+        const dim3 grid(ceil_div(n_out, 64));
+        const int mean = op == VKHIP_REDUCE_MEAN ? 1 : 0;
+        float* out = static_cast<float*>(dst);
+        if (depth == 1)
+            hipLaunchKernelGGL(reduce_tall_leaves_kernel<2>, grid, dim3(128), 0, st, src, kept, rd,
+                               n_out, n_red, mean, out);
+        else if (depth == 2)
+            hipLaunchKernelGGL(reduce_tall_leaves_kernel<4>, grid, dim3(256), 0, st, src, kept, rd,
+                               n_out, n_red, mean, out);
+        else
+            hipLaunchKernelGGL(reduce_tall_leaves_kernel<8>, grid, dim3(512), 0, st, src, kept, rd,
+                               n_out, n_red, mean, out);
         VKHIP_LAUNCH_CHECK();
         return VKHIP_OK;
     }
