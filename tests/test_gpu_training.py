@@ -186,3 +186,22 @@ def test_fused_relu_backward_on_device(backends, shape):
     fused = relu_grad(dev, x, g, True)
     assert fused.tobytes() == relu_grad(dev, x, g, False).tobytes()
     assert fused.tobytes() == relu_grad(cpu, x, g, True).tobytes()
+
+
+@pytest.mark.parametrize("xs,ys", [((128, 64, 32, 32), (64, 1, 1)), ((128, 256), (256,)),
+                                   ((4, 6, 8), (4, 1, 1)), ((2, 3, 4, 5), (3, 1, 1)),
+                                   ((5, 12), (12,)), ((7, 3), (3,)), ((2, 3, 8), (2, 1, 8)),
+                                   ((3, 4, 4), (1, 4, 1)), ((6, 10), (6, 1))])
+def test_broadcast_binary_ops_on_device(backends, xs, ys):
+    """add/sub/mul with a broadcast second operand (the bias adds: a value per
+    channel over H*W runs, or a row of features repeated over the batch) take
+    a vector path where the layout allows and the generic one elsewhere; every
+    result is the oracle's, bit for bit."""
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED + len(xs) * 10 + len(ys))
+    x = rng.standard_normal(xs).astype(np.float32)
+    y = rng.standard_normal(ys).astype(np.float32)
+    for op in (T.add, T.sub, T.mul):
+        got = op(T.tensor(x, backend=dev), T.tensor(y, backend=dev)).numpy()
+        want = op(T.tensor(x, backend=cpu), T.tensor(y, backend=cpu)).numpy()
+        assert got.tobytes() == want.tobytes(), op.__name__

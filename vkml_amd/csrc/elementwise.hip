@@ -236,6 +236,48 @@ __global__ __launch_bounds__(256) void elementwise_f32_vec_kernel(int op, const 
     reinterpret_cast<f32x4*>(out)[i] = r;
 }
 
+// Binary f32 ops whose second operand is broadcast in one of the two shapes
+// bias adds take, with 16-byte loads and stores of the first operand and the
+// output (both contiguous):
+//   PERIODIC: y repeats with period `inner` (y's trailing axes contiguous, its
+//             leading axes broadcast): y index = i % inner, e.g. [N,F] + [F];
+//   RUNS:     y is constant over runs of `inner` elements (its trailing axes
+//             broadcast) and indexed by the run number through the leading
+//             axes' strides `lead`, e.g. [N,C,H,W] + [C,1,1].
+// inner is a multiple of 4, so a thread's four elements share one run (RUNS)
+// or read four consecutive y values (PERIODIC).
+template <bool RUNS>
+__global__ __launch_bounds__(256) void elementwise_bcast_vec_kernel(
+    int op, const float* __restrict__ x, const float* __restrict__ y, float* __restrict__ out,
+    uint64_t n4, uint32_t inner, FastDiv div_inner, Op4 lead) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const uint64_t e0 = 4 * i;
+    const f32x4 a = reinterpret_cast<const f32x4*>(x)[i];
+    f32x4 b;
+    if constexpr (RUNS) {
+        const uint32_t run = div_inner.div(static_cast<uint32_t>(e0));
+        const float v = y[lin_off4(run, lead.ne, lead.nb)];
+        b = f32x4{v, v, v, v};
+    } else {
+        const uint32_t q = div_inner.div(static_cast<uint32_t>(e0));
+        const uint32_t r = static_cast<uint32_t>(e0) - q * inner;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = y[r + j];
+    }
+    f32x4 res;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        switch (op) {
+            case VKHIP_OP_ADD: res[j] = __fadd_rn(a[j], b[j]); break;
+            case VKHIP_OP_SUB: res[j] = __fsub_rn(a[j], b[j]); break;
+            default: res[j] = __fmul_rn(a[j], b[j]); break;
+        }
+    }
+    reinterpret_cast<f32x4*>(out)[i] = res;
+}
+
 static bool is_contig(const vkhip_tensor& t) {
     int64_t expect = 1;
     for (int i = t.ndim - 1; i >= 0; --i) {
@@ -294,6 +336,66 @@ int launch_elementwise(const vkhip_node& nd) {
                                static_cast<float*>(nd.out.data), n4, ab[0], ab[1]);
             VKHIP_LAUNCH_CHECK();
             return VKHIP_OK;
+        }
+    }
+    // Broadcast second operand of a bias add (see elementwise_bcast_vec_kernel).
+    if ((op == VKHIP_OP_ADD || op == VKHIP_OP_SUB || op == VKHIP_OP_MUL) && nd.n_src == 2 &&
+        n % 4 == 0 && n < (1ull << 32) && nd.out.dtype == VKHIP_F32 &&
+        nd.src[0].dtype == VKHIP_F32 && nd.src[1].dtype == VKHIP_F32 &&
+        is_contig(nd.src[0]) && tnumel(nd.src[0]) == n &&
+        reinterpret_cast<uintptr_t>(nd.out.data) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(nd.src[0].data) % 16 == 0) {
+        const vkhip_tensor& y = nd.src[1];
+        // Trailing axes where y is broadcast (stride 0), then where it is
+        // contiguous; extent-1 axes are skipped.
+        int axis = y.ndim - 1;
+        uint64_t zero_run = 1, contig_run = 1;
+        while (axis >= 0 && (y.ne[axis] == 1 || y.nb[axis] == 0)) zero_run *= y.ne[axis--];
+        const int lead_end = axis;  // axes [0, lead_end] remain
+        if (zero_run > 1 && zero_run % 4 == 0 && lead_end >= 0) {
+            // RUNS: y indexed by the run number through its leading axes.
+            Op4 lead{};
+            for (int i = 0; i < 4; ++i) {
+                lead.ne[i] = 1;
+                lead.nb[i] = 0;
+            }
+            const int pad = 3 - lead_end;
+            bool fits = pad >= 0;
+            for (int i = 0; i <= lead_end && fits; ++i) {
+                lead.ne[pad + i] = static_cast<uint32_t>(y.ne[i]);
+                lead.nb[pad + i] = y.nb[i];
+            }
+            if (fits) {
+                const uint64_t n4 = n / 4;
+                hipLaunchKernelGGL(elementwise_bcast_vec_kernel<true>, dim3(ceil_div(n4, 256)),
+                                   dim3(256), 0, st, op, static_cast<const float*>(nd.src[0].data),
+                                   static_cast<const float*>(y.data), static_cast<float*>(nd.out.data),
+                                   n4, static_cast<uint32_t>(zero_run),
+                                   FastDiv(static_cast<uint32_t>(zero_run)), lead);
+                VKHIP_LAUNCH_CHECK();
+                return VKHIP_OK;
+            }
+        }
+        if (zero_run == 1) {
+            // PERIODIC: a contiguous trailing block of y, broadcast over the rest.
+            axis = y.ndim - 1;
+            while (axis >= 0 && (y.ne[axis] == 1 || static_cast<uint64_t>(y.nb[axis]) == contig_run)) {
+                contig_run *= y.ne[axis];
+                --axis;
+            }
+            bool rest_broadcast = true;
+            for (int i = 0; i <= axis; ++i)
+                if (y.ne[i] != 1 && y.nb[i] != 0) rest_broadcast = false;
+            if (rest_broadcast && contig_run % 4 == 0 && contig_run < n) {
+                const uint64_t n4 = n / 4;
+                hipLaunchKernelGGL(elementwise_bcast_vec_kernel<false>, dim3(ceil_div(n4, 256)),
+                                   dim3(256), 0, st, op, static_cast<const float*>(nd.src[0].data),
+                                   static_cast<const float*>(y.data), static_cast<float*>(nd.out.data),
+                                   n4, static_cast<uint32_t>(contig_run),
+                                   FastDiv(static_cast<uint32_t>(contig_run)), Op4{});
+                VKHIP_LAUNCH_CHECK();
+                return VKHIP_OK;
+            }
         }
     }
     EwArgs a{};
