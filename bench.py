@@ -191,7 +191,10 @@ def secondary(hip, ops, timer):
                      "frac_of_hbm": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4)}
 
     # GEMM variants (compute-bound: no rotation)
-    for name, (m, n, k), lay in [("gemm_nt_4096", (4096, 4096, 4096), "nt"),
+    for name, (m, n, k), lay in [("gemm_512", (512, 512, 512), "nn"),
+                                 ("gemm_1024", (1024, 1024, 1024), "nn"),
+                                 ("gemm_2048", (2048, 2048, 2048), "nn"),
+                                 ("gemm_nt_4096", (4096, 4096, 4096), "nt"),
                                  ("gemm_tn_4096", (4096, 4096, 4096), "tn"),
                                  ("gemm_8192x1024x4096", (8192, 1024, 4096), "nn"),
                                  ("gemm_8192", (8192, 8192, 8192), "nn"),
