@@ -750,6 +750,50 @@ __global__ __launch_bounds__(256) void gemv2_rows_kernel(const float* __restrict
     }
 }
 
+// Row sums of 2048 < n <= 4096 over evenly spaced rows: two rows per
+// 256-thread workgroup, the gemv2_rows_kernel arrangement without the vector.
+// Threads 0-127 sum row 0's leaves and 128-255 row 1's; the final
+// (w0 + w1) + (0 + 0) is what group_pairwise_sum<256> computes for one row
+// (its upper two waves hold no leaves), so the bits are the one-row kernel's.
+// More rows in flight per CU: [8192, 4096] 24.0 -> 23.4 us.
+__global__ __launch_bounds__(256) void sum2_rows_kernel(const float* __restrict__ a, int64_t lda,
+                                                        float* __restrict__ y, uint32_t m,
+                                                        uint32_t n, int depth, uint32_t sstride, int mean) {
+    extern __shared__ __attribute__((aligned(16))) float dyn[];
+    __shared__ float scratch[4];
+    const int t = threadIdx.x;
+    const uint32_t r0 = blockIdx.x * 2;
+    const bool live1 = r0 + 1 < m;
+    float x0[16], x1[16];
+    load_row<256, 4>(x0, a + static_cast<int64_t>(r0) * lda, n, t, true, 1);
+    load_row<256, 4>(x1, a + static_cast<int64_t>(live1 ? r0 + 1 : r0) * lda, n, t, true, 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t e0 = 4u * (t + 256 * i);
+        if (e0 < n) {
+            f32x4 v0, v1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { v0[j] = x0[4 * i + j]; v1[j] = x1[4 * i + j]; }
+            *reinterpret_cast<f32x4*>(dyn + stage_index(e0)) = v0;
+            *reinterpret_cast<f32x4*>(dyn + sstride + stage_index(e0)) = v1;
+        }
+    }
+    __syncthreads();
+    const int row = t >> 7, leaf = t & 127;
+    float v = 0.0f;
+    if (static_cast<uint32_t>(leaf) < (1u << depth))
+        v = staged_subtree_sum(dyn + row * sstride, n, depth, leaf, 1);
+    v = wave_sum_butterfly(v);
+    const int lane = t & 63, wave = t >> 6;
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    if (lane == 0 && (wave & 1) == 0) {
+        const uint32_t o = r0 + row;
+        const float s = scratch[wave] + scratch[wave + 1] + (0.0f + 0.0f);
+        if (o < m) y[o] = mean ? s / static_cast<float>(n) : s;
+    }
+}
+
 // Selections (max/min/argmax/argmin) over contiguous runs that fit the row
 // classes: the thread's elements are loaded up front, scanned in index order,
 // then merged across threads with the lowest-index tie-break.
@@ -1250,6 +1294,15 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
             const int mean = op == VKHIP_REDUCE_MEAN;
             float* out = static_cast<float*>(dst);
             const RowClass rc = row_class(n_red);
+            if (vec && n_red > 2048 && n_red <= 4096 && n_out >= 2 && kept.ne[0] == 1 &&
+                kept.ne[1] == 1 && kept.ne[2] == 1) {
+                const uint32_t ss = stage_stride(n_red);
+                hipLaunchKernelGGL(sum2_rows_kernel, dim3(ceil_div(n_out, 2u)), dim3(256),
+                                   2 * static_cast<size_t>(ss) * sizeof(float), st, src, kept.nb[3],
+                                   out, n_out, n_red, depth, ss, mean);
+                VKHIP_LAUNCH_CHECK();
+                return VKHIP_OK;
+            }
             VKHIP_ROW_CLASSES(launch_sum_rows, src, kept, n_out, n_red, depth, mean, vec, out, st,
                               nullptr)
         }
