@@ -1035,9 +1035,15 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
     chunk = ktiles > 0 ? ktiles : 1;
     const uint32_t req = split_request > 1 ? static_cast<uint32_t>(split_request) : 0u;
     bool want_split = false;
+    // 64x64 tiles at one workgroup per CU hide little latency (1024x1024x2048:
+    // 69 TFLOP/s); when 128x128 tiles split K into partitions of at least 16
+    // K-tiles instead, those run faster (86). With 8 K-tiles per partition
+    // the 64x64 tiles still win (1024^3: 69 against 67).
+    const bool deep_split = t64 < 2ull * cu && !narrow &&
+                            ktiles / ((cu + t128 - 1) / t128) >= 16;
     if (t128 >= cu && !narrow) {
         tile = {128, 128, "128x128 tiles give every CU a workgroup"};
-    } else if (t64 >= cu) {
+    } else if (t64 >= cu && !deep_split) {
         tile = {64, 64, narrow ? "128x128 tiles would pad the output by more than 25%"
                                : "only 64x64 tiles give every CU a workgroup"};
     } else {
