@@ -1035,19 +1035,28 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
     chunk = ktiles > 0 ? ktiles : 1;
     const uint32_t req = split_request > 1 ? static_cast<uint32_t>(split_request) : 0u;
     bool want_split = false;
-    // 64x64 tiles at one workgroup per CU hide little latency (1024x1024x2048:
-    // 69 TFLOP/s); when 128x128 tiles split K into partitions of at least 16
-    // K-tiles instead, those run faster (86). With 8 K-tiles per partition
-    // the 64x64 tiles still win (1024^3: 69 against 67).
-    const bool deep_split = t64 < 2ull * cu && !narrow &&
-                            ktiles / ((cu + t128 - 1) / t128) >= 16;
+    // 64x64 tiles run two workgroups per CU. At one workgroup per CU they hide
+    // little latency (1024x1024x2048: 69 TFLOP/s), and a short last round
+    // (under 60% of its slots filled) idles most CUs (1536^3: 73); 128x128
+    // tiles that split K into partitions of at least 16 K-tiles run those
+    // faster (86 and 89), provided, for the second case, the partitions give
+    // at least 1.5 workgroups per CU (1536x1536x4096 as 288 partitions: 71,
+    // against 77 on 64x64 tiles). With 8 K-tiles per partition the 64x64
+    // tiles still win (1024^3: 69 against 67).
+    const uint64_t slots64 = 2ull * cu;
+    const bool poor64 = t64 * 10 < ((t64 + slots64 - 1) / slots64) * slots64 * 6;
+    const uint64_t target128 = (cu + t128 - 1) / t128;
+    uint64_t c128 = 1;
+    while (c128 * 2 <= ktiles / target128) c128 *= 2;
+    const uint64_t parts128 = t128 * ((ktiles + c128 - 1) / c128);
+    const bool deep_split = !narrow && ktiles / target128 >= 16 &&
+                            (t64 < slots64 || (poor64 && 2 * parts128 >= 3ull * cu));
     if (t128 >= cu && !narrow) {
         tile = {128, 128, "128x128 tiles give every CU a workgroup"};
     } else if (t64 >= cu && !deep_split) {
         tile = {64, 64, narrow ? "128x128 tiles would pad the output by more than 25%"
                                : "only 64x64 tiles give every CU a workgroup"};
     } else {
-        const uint64_t target128 = (cu + t128 - 1) / t128;
         tile = (!narrow && ktiles / target128 >= 8)
                    ? TileChoice{128, 128, "too few output tiles: K split over 128x128 tiles"}
                    : TileChoice{64, 64, "too few output tiles: K split over 64x64 tiles"};
