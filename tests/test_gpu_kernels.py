@@ -104,6 +104,9 @@ LAYOUT_SHAPES = [  # (batch, m, n, k): 128x128 tiles, split-K, ragged edges, M o
     (1, 256, 256, 16384),
     (1, 2046, 2048, 67),
     (1, 2048, 2047, 33),
+    (1, 1024, 1024, 256),   # 64x64 tiles, one workgroup per CU
+    (2, 1000, 1020, 100),   # 64x64 tiles, ragged edges
+    (1, 1022, 1024, 64),    # 64x64 tiles, M not 4-aligned (TN through registers)
 ]
 
 

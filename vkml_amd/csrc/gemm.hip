@@ -741,6 +741,130 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
     }
 }
 
+// 64x64 tiles with both operands straight into LDS, for outputs that give
+// each CU only a workgroup or two of 64x64 tiles. Rows of k (B, and A in TN)
+// land as 32 rows of 64 floats; A in NN lands KCD-swizzled. Four waves: two
+// row groups of 32 x two strided column sets {2c + s}, one MFMA chain each,
+// a lane reading one float of a k row per step. Same k order per output as
+// the register-path 64x64 kernel, so the same bits.
+template <int COLS>
+__device__ __forceinline__ void load_rows_direct(float* stage, __amdgpu_buffer_rsrc_t src, int64_t s_k,
+                                                 uint32_t col0, uint32_t cols, uint32_t k0,
+                                                 uint32_t kdim, int tid) {
+    constexpr int G = COLS / 4;  // 16-byte groups per k row
+    const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int i = 0; i < 32 * G / 256; ++i) {
+        const int chunk = 4 * i + wave;
+        const int slot = chunk * 64 + lane;
+        const int r = slot / G, grp = slot % G;
+        const uint32_t gk = k0 + r, gc = col0 + 4 * grp;
+        const bool ok = gk < kdim && gc < cols;
+        const uint32_t off = ok ? static_cast<uint32_t>((static_cast<int64_t>(gk) * s_k + gc) * 4)
+                                : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            src, (__attribute__((address_space(3))) void*)(stage + chunk * 256), 16, off, 0, 0, 0);
+    }
+}
+
+template <bool ATR>
+__global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
+    constexpr int BM = 64, BN = 64, BK = 32, QN = BK / 8;
+    using LA = TileLoader<BM, BK, KCD>;
+    __shared__ __attribute__((aligned(16))) float lds[2][BM * BK + BK * BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = (wave & 1) * 32;
+    const int s0 = wave >> 1;
+
+    const uint32_t ntiles = g.tiles_m * g.tiles_n;
+    uint32_t bid = blockIdx.x;
+    if ((ntiles & 7u) == 0) bid = (bid & 7u) * (ntiles >> 3) + (bid >> 3);
+    const uint32_t group_span = 8u * g.tiles_n;
+    const uint32_t first_m = (bid / group_span) * 8u;
+    const uint32_t gsize = min(g.tiles_m - first_m, 8u);
+    const uint32_t tm = first_m + (bid % group_span) % gsize;
+    const uint32_t tn = (bid % group_span) / gsize;
+    const uint32_t row0 = tm * BM;
+    const uint32_t col0 = tn * BN;
+
+    const uint32_t z = blockIdx.z;
+    const uint32_t i0 = z / g.b1, i1 = z % g.b1;
+    const float* abase = g.a + i0 * g.sa0 + i1 * g.sa1;
+    const float* bbase = g.b + i0 * g.sb0 + i1 * g.sb1;
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(abase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(bbase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    float* cbase = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride +
+                   static_cast<uint64_t>(z) * g.m * g.n;
+    const uint32_t kt0 = blockIdx.y * g.chunk;
+    const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+    auto load_tile = [&](uint32_t kt, int dst) {
+        if constexpr (ATR)
+            load_rows_direct<BM>(lds[dst], arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
+        else
+            LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+        load_rows_direct<BN>(lds[dst] + BM * BK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+    };
+    if (kt0 < kt1) load_tile(kt0, 0);
+    __syncthreads();
+
+    const int lrow = lane & 31;
+    const int kh = lane >> 5;
+    for (uint32_t kt = kt0; kt < kt1; ++kt) {
+        const int cur = (kt - kt0) & 1;
+        if (kt + 1 < kt1) load_tile(kt + 1, cur ^ 1);
+        const float* As = ATR ? lds[cur] + kh * 16 * BM + wm0 + lrow : lds[cur] + (wm0 + lrow) * BK;
+        const float* Bs = lds[cur] + BM * BK + kh * 16 * BN + 2 * lrow + s0;
+        auto a_at = [&](int q) {
+            if constexpr (ATR) {
+                f32x4 v;
+#pragma unroll
+                for (int st = 0; st < 4; ++st) v[st] = As[(4 * q + st) * BM];
+                return v;
+            } else {
+                return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ (lrow & 7)));
+            }
+        };
+        f32x4 av[2], bv[2];
+        av[0] = a_at(0);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) bv[0][st] = Bs[st * BN];
+#pragma unroll
+        for (int q = 0; q < QN; ++q) {
+            const int cb = q & 1;
+            if (q + 1 < QN) {
+                av[cb ^ 1] = a_at(q + 1);
+#pragma unroll
+                for (int st = 0; st < 4; ++st) bv[cb ^ 1][st] = Bs[(4 * (q + 1) + st) * BN];
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][st], bv[cb][st], acc, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    // acc register r of lane l: row 8*(r/4) + 4*(l/32) + r%4 of the wave's 32,
+    // column 2*(l%32) + s0 of the tile.
+    const uint32_t col = col0 + 2 * lrow + s0;
+    if (col < g.n) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
+            if (row < g.m) cbase[static_cast<uint64_t>(row) * g.n + col] = acc[r];
+        }
+    }
+}
+
 // ---- split-K partial fold --------------------------------------------------
 // Per output: the binary-counter carry stack over the `splits` partial slices,
 // drained in ascending level order from 0.0 (reference
@@ -1193,6 +1317,16 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
             hipLaunchKernelGGL(gemm_nn_direct_kernel<false>, grid, dim3(256), 0, ctx().stream, g);
         else
             hipLaunchKernelGGL(gemm_nn_direct_kernel<true>, grid, dim3(256), 0, ctx().stream, g);
+        VKHIP_LAUNCH_CHECK();
+        if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
+        return VKHIP_OK;
+    }
+    if (tile.bm == 64 && b_rows && (amode == KCD || a_rows)) {
+        dim3 grid(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
+        if (amode == KCD)
+            hipLaunchKernelGGL(gemm_direct64_kernel<false>, grid, dim3(256), 0, ctx().stream, g);
+        else
+            hipLaunchKernelGGL(gemm_direct64_kernel<true>, grid, dim3(256), 0, ctx().stream, g);
         VKHIP_LAUNCH_CHECK();
         if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
         return VKHIP_OK;
