@@ -757,3 +757,33 @@ def test_errors_are_reported_not_crashed(hip):
     code = lib.vkhip_gemm(c_void_p(a.ptr), byref(d), c_void_p(b.ptr), byref(e), c_void_p(a.ptr),
                           None)
     assert code == _lib.ERR_INVALID and b"inner dimensions" in lib.vkhip_last_error()
+
+
+def test_host_provided_stream(hip):
+    """vkhip_set_stream: work (an upload through the staging slots, a GEMM, a
+    softmax and a download) runs on a stream the host hands over, here one
+    made with hipStreamCreate (default priority), in order and with the
+    results of the backend's own stream; vkhip_set_stream(NULL) returns to it."""
+    import ctypes
+
+    hiprt = ctypes.CDLL("libamdhip64.so")
+    rng = np.random.default_rng(SEED + 93)
+    a = rng.standard_normal((300, 200)).astype(np.float32)
+    b = rng.standard_normal((200, 100)).astype(np.float32)
+    want = ops.matmul(dev(a), dev(b)).numpy()
+    want_sm = ops.softmax(dev(want), -1).numpy()
+    own = hip.stream_handle()
+    side = ctypes.c_void_p()
+    assert hiprt.hipStreamCreate(ctypes.byref(side)) == 0 and side.value
+    try:
+        hip.set_stream(side.value)
+        assert hip.stream_handle() == side.value
+        got = ops.matmul(dev(a), dev(b))
+        got_sm = ops.softmax(got, -1).numpy()
+        assert got.numpy().tobytes() == want.tobytes()
+        assert got_sm.tobytes() == want_sm.tobytes()
+    finally:
+        hip.set_stream(None)
+        assert hiprt.hipStreamDestroy(side) == 0
+    assert hip.stream_handle() == own
+    assert ops.matmul(dev(a), dev(b)).numpy().tobytes() == want.tobytes()

@@ -283,6 +283,14 @@ class HipBackend:
             if n.value < 1024:
                 return out
 
+    def set_stream(self, stream_handle: int | None) -> None:
+        """Launch on a stream the host provides (None: the backend's own);
+        the current stream is synchronised first (vkhip_set_stream)."""
+        check(self.lib.vkhip_set_stream(c_void_p(stream_handle or None)), "set_stream")
+
+    def stream_handle(self) -> int:
+        return self.lib.vkhip_get_stream() or 0
+
 
 class DecisionRecorder:
     """Collects the backend's decision facts while active:
@@ -312,12 +320,6 @@ class DecisionRecorder:
     def __exit__(self, *exc):
         backend().lib.vkhip_subscribe_decisions(_lib.DECISION_FN(0), None)
         return False
-
-    def set_stream(self, stream_handle: int | None) -> None:
-        check(self.lib.vkhip_set_stream(c_void_p(stream_handle or None)), "set_stream")
-
-    def stream_handle(self) -> int:
-        return self.lib.vkhip_get_stream() or 0
 
 
 class Event:
