@@ -787,3 +787,21 @@ def test_host_provided_stream(hip):
         assert hiprt.hipStreamDestroy(side) == 0
     assert hip.stream_handle() == own
     assert ops.matmul(dev(a), dev(b)).numpy().tobytes() == want.tobytes()
+
+
+def test_copy_device_to_device_batch(hip):
+    """vkhip_copy_device_to_device: several disjoint copies as one unit of work,
+    16-byte multiples (the copy kernel) and odd sizes (the runtime's
+    copy), byte for byte; mismatched or strided pairs are refused on the host."""
+    rng = np.random.default_rng(SEED + 95)
+    srcs = [rng.standard_normal(n).astype(np.float32) for n in (4096, 1001, 37, 1 << 20)]
+    src_d = [dev(x) for x in srcs]
+    dst_d = [DeviceArray((x.size,), np.float32) for x in srcs]
+    hip.copy_device_to_device(list(zip(dst_d, src_d)))
+    for d, x in zip(dst_d, srcs):
+        assert d.numpy().tobytes() == x.tobytes()
+    with pytest.raises(ValueError):
+        hip.copy_device_to_device([(DeviceArray((10,), np.float32), dev(np.zeros(11, np.float32)))])
+    with pytest.raises(ValueError):
+        m = dev(np.zeros((4, 6), np.float32))
+        hip.copy_device_to_device([(DeviceArray((6, 4), np.float32), m.transpose(0, 1))])

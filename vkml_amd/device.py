@@ -247,8 +247,16 @@ class HipBackend:
         return src.numpy()
 
     def copy_device_to_device(self, copies) -> None:
-        """copies: iterable of (dst DeviceArray, src DeviceArray) pairs of equal byte size."""
-        cs = [_lib.Copy(d.ptr, s.ptr, d.nbytes_dense()) for d, s in copies]
+        """copies: iterable of (dst DeviceArray, src DeviceArray) pairs, both
+        contiguous and of equal byte size (the reference BufferCopy's bytes)."""
+        cs = []
+        for d, s in copies:
+            if not (d.is_contiguous() and s.is_contiguous()):
+                raise ValueError("copy_device_to_device: both arrays must be contiguous")
+            if d.nbytes_dense() != s.nbytes_dense():
+                raise ValueError(f"copy_device_to_device: {s.nbytes_dense()} source bytes for "
+                                 f"{d.nbytes_dense()} destination bytes")
+            cs.append(_lib.Copy(d.ptr, s.ptr, d.nbytes_dense()))
         if cs:
             check(self.lib.vkhip_copy_device_to_device((_lib.Copy * len(cs))(*cs), len(cs)),
                   "copy_device_to_device")
