@@ -805,3 +805,30 @@ def test_copy_device_to_device_batch(hip):
     with pytest.raises(ValueError):
         m = dev(np.zeros((4, 6), np.float32))
         hip.copy_device_to_device([(DeviceArray((6, 4), np.float32), m.transpose(0, 1))])
+
+
+def test_supports_predicate_and_unsupported_compute(hip):
+    """vkhip_supports reports exactly the implemented (op, dtype) set: a float
+    relu node is supported, an op this backend lacks and a relu over int64
+    are not, and vkhip_compute refuses such a node with ERR_UNSUPPORTED and a
+    message instead of running anything (the reference executor's rule: no
+    fallback, executor.cpp:107-124)."""
+    x = dev(np.arange(8, dtype=np.float32) - 4)
+    out = DeviceArray((8,), np.float32)
+
+    def node(op, dtype):
+        nd = _lib.NodeDesc()
+        nd.op, nd.n_src = op, 1
+        for t, arr in ((nd.out, out), (nd.src[0], x)):
+            t.data, t.dtype, t.ndim = arr.ptr, dtype, 1
+            t.ne[0], t.nb[0] = 8, 1
+        return nd
+
+    relu = node(_lib.OP["RELU"], _lib.F32)
+    assert hip.supports(relu)
+    hip.compute(relu)
+    assert out.numpy().tobytes() == np.maximum(np.arange(8, dtype=np.float32) - 4, 0).tobytes()
+    for bad in (node(1, _lib.F32), node(_lib.OP["RELU"], _lib.I64)):
+        assert not hip.supports(bad)
+        with pytest.raises(_lib.NotImplementedOnDevice):
+            hip.compute(bad)
