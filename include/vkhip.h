@@ -193,7 +193,12 @@ typedef struct vkhip_copy {
 enum vkhip_gemm_kernel {
     VKHIP_GEMM_AUTO = 0,   /* MFMA tiles, split-K / GEMV by the planner */
     VKHIP_GEMM_MFMA = 1,   /* MFMA tiles, never GEMV */
-    VKHIP_GEMM_GEMV = 2    /* force the GEMV path (N == 1 or M == 1 only) */
+    VKHIP_GEMM_GEMV = 2,   /* force the GEMV path (N == 1 or M == 1 only) */
+    /* the comparison arm: each product rounded, the K products summed in the
+     * CPU oracle's pairwise order, so C is the oracle's bit for bit (the role
+     * of the reference's gemm_naive.comp:56-101, VKML_GEMM_KERNEL=naive,
+     * vulkan_backend.cpp:2158-2161). Vector ALU, not matrix cores: slow. */
+    VKHIP_GEMM_EXACT = 3
 };
 typedef struct vkhip_gemm_opts {
     int32_t kernel;        /* vkhip_gemm_kernel */
@@ -416,6 +421,34 @@ int vkhip_set_profiling(int enabled);
  * of records dropped since the last read. */
 int vkhip_profile_read(vkhip_profile_record* out, size_t capacity, size_t* count,
                        uint64_t* dropped);
+
+/* ======================================================================== */
+/* Recorded programs: replay of a step whose graph repeats                   */
+/* ======================================================================== */
+/* No single counterpart in the reference; it is the "record once, re-submit"
+ * model the reference measured for its submission path
+ * (docs/adr/0012-asynchronous-submission.md section 2) applied to the host
+ * cost docs/SMALL-STEP-LATENCY.md:44-51 names. While a program records, every
+ * vkhip_compute, vkhip_sgd_step and vkhip_copy_device_to_device call runs as
+ * usual and is also appended to it with its arguments (node records byte for
+ * byte); host copies are not recorded. Replaying enqueues the same calls in
+ * the same order with the same device pointers, so the caller keeps every
+ * buffer the recorded calls touched alive and in place, and uploads new inputs
+ * into the recorded input buffers before each run. A replayed SGD step
+ * continues from the recorded step's velocity (its first-step flags are
+ * recorded as 0). One program records at a time. */
+typedef struct vkhip_program vkhip_program;
+int vkhip_program_begin(void);
+int vkhip_program_end(vkhip_program** out);
+/* use_graph != 0: the first run captures the replayed launches into a HIP
+ * graph on the backend stream (not while profiling is on), later runs launch
+ * the graph; the backend stream must then stay the same. use_graph == 0
+ * replays call by call. */
+int vkhip_program_run(vkhip_program* program, int use_graph);
+/* Waits for a captured graph to finish, then frees the program. */
+int vkhip_program_destroy(vkhip_program* program);
+int vkhip_program_info(const vkhip_program* program, size_t* calls, size_t* nodes,
+                       int* has_graph);
 
 /* ======================================================================== */
 /* Host-side planning helpers (callable without a GPU)                       */

@@ -320,6 +320,12 @@ class OracleBackend:
     def synchronize(self) -> None:
         pass
 
+    def copy(self, copies) -> None:
+        """copy_device_to_device on host memory: (dst storage, dst offset
+        bytes, src storage, src offset bytes, nbytes) per pair."""
+        for dst, doff, src, soff, nbytes in copies:
+            ctypes.memmove(dst.ptr + doff, src.ptr + soff, nbytes)
+
     def sgd_step(self, entries, lr: float, momentum: float, weight_decay: float,
                  nesterov: bool) -> None:
         """The fused optimiser step on host memory, as the reference's

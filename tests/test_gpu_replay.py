@@ -1,0 +1,93 @@
+"""Recorded programs (vkhip_program_*) and CapturedStep: a training step
+recorded once and replayed, call by call or as one HIP graph, gives the same
+bits as running the step eagerly, step after step (BASELINE configs 1 and 5).
+
+Between replays the test runs eager work of its own and synchronises, and it
+checks every replay against the eager trajectory, not only the last."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import SEED, config5_model
+from vkml_amd import nn, optim
+from vkml_amd import tensor as T
+
+pytestmark = pytest.mark.gpu
+
+
+def _mlp(backend):
+    nn.manual_seed(SEED)
+    return nn.Sequential(nn.Flatten(), nn.Linear(784, 128, backend=backend), nn.ReLU(),
+                         nn.Linear(128, 10, backend=backend))
+
+
+CONFIGS = {
+    "mlp": (_mlp, (64, 1, 28, 28), (0.0, 1.0), 10, 0.1),
+    "cnn": (config5_model, (128, 3, 32, 32), (-1.0, 1.0), 100, 0.01),
+}
+
+
+def _batches(config, steps):
+    _, shape, (lo, hi), classes, _ = CONFIGS[config]
+    rng = np.random.default_rng(SEED + 31)
+    return [(rng.uniform(lo, hi, shape).astype(np.float32),
+             rng.integers(0, classes, shape[0]).astype(np.int64)) for _ in range(steps)]
+
+
+def _step_fn(model, opt):
+    def fn(x, y):
+        opt.zero_grad()
+        loss = nn.cross_entropy(model(x), y)
+        loss.backward()
+        opt.step()
+        return loss
+    return fn
+
+
+@pytest.mark.parametrize("graph", [False, True], ids=["replay", "graph"])
+@pytest.mark.parametrize("config", ["mlp", "cnn"])
+def test_replayed_steps_are_the_eager_steps_bit_for_bit(config, graph):
+    dev = T.default_backend()
+    make, _, _, _, lr = CONFIGS[config]
+    batches = _batches(config, 8)
+
+    model_e = make(dev)
+    opt_e = optim.SGD(model_e.parameters(), lr=lr, momentum=0.9)
+    fn_e = _step_fn(model_e, opt_e)
+    eager = []
+    for x, y in batches:
+        eager.append(np.float32(fn_e(T.tensor(x, backend=dev), T.tensor(y, backend=dev)).item()))
+
+    model_c = make(dev)
+    opt_c = optim.SGD(model_c.parameters(), lr=lr, momentum=0.9)
+    step = T.CapturedStep(_step_fn(model_c, opt_c), *batches[0], graph=graph)
+    got = [np.float32(step.first[0])]
+    probe = T.tensor(np.ones((256, 256), np.float32), backend=dev)
+    for i, (x, y) in enumerate(batches[1:]):
+        got.append(np.float32(step(x, y)[0]))
+        # the program's own eager work and a synchronisation between replays
+        s = T.sum(T.matmul(probe, probe)).item()
+        assert s == 256.0 ** 3
+        assert got[-1].tobytes() == eager[i + 1].tobytes(), f"replay {i + 1}"
+    assert np.array(got).tobytes() == np.array(eager).tobytes()
+    info = step.info()
+    assert info["nodes"] > 0 and info["graph"] == graph
+    for pe, pc in zip(model_e.parameters(), model_c.parameters()):
+        assert pe.numpy().tobytes() == pc.numpy().tobytes()
+    step.close()
+
+
+def test_captured_step_checks_its_inputs():
+    dev = T.default_backend()
+    model = _mlp(dev)
+    opt = optim.SGD(model.parameters(), lr=0.1)
+    (x, y), = _batches("mlp", 1)
+    step = T.CapturedStep(_step_fn(model, opt), x, y)
+    with pytest.raises(ValueError):
+        step(x[:32], y[:32])
+    with pytest.raises(ValueError):
+        step(x)
+    step.close()
+    with pytest.raises(RuntimeError):
+        step(x, y)

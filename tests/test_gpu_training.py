@@ -1,10 +1,10 @@
 """Whole training steps on the device against the same graph on the CPU oracle.
 
-BASELINE config 1 (MNIST-shaped MLP, 100 SGD-momentum steps) must keep every
-step's loss within 1e-4 of the oracle's; config 5 (CIFAR-100-shaped CNN) is run
-at full batch for a few steps (the oracle needs ~10 s per full step) and at a
-reduced batch for more; config 4's conv layers are checked forward, dX and dW at
-full shape. The graph, the initial weights and the data are identical on both
+BASELINE config 1 (MNIST-shaped MLP, 100 SGD-momentum steps) and config 5
+(CIFAR-100-shaped CNN, batch 128, 100 steps) must keep every step's loss within
+1e-4 of the oracle's (config 5 against the oracle's committed trajectory, plus
+live comparisons of a few steps); config 4's conv layers are checked forward,
+dX and dW at full shape. The graph, the initial weights and the data are identical on both
 sides; only the backend executing the nodes differs.
 """
 from __future__ import annotations
@@ -12,8 +12,9 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads,
-                      gemm_tolerance, normwise_rel_err, relu_grad, relu_inputs)
+from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad,
+                      config5_golden_losses, config5_train, conv_loss_and_grads, gemm_tolerance,
+                      normwise_rel_err, relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -76,6 +77,27 @@ def test_config5_cnn_loss_drift(backends, batch, steps):
     got = train(cnn(dev), dev, batches, lr=0.01)
     want = train(cnn(cpu), cpu, batches, lr=0.01)
     drift = np.abs(got - want)
+    assert drift.max() <= 1e-4, f"max loss drift {drift.max():.3g} at step {drift.argmax()}"
+
+
+@pytest.mark.timeout(300)
+def test_config5_cnn_fast_path_tracks_the_oracle(backends):
+    """BASELINE config 5 at full batch (128), a fresh batch each step, on the
+    default (matrix-core) numerics against the CPU oracle's trajectory (the
+    committed fixture tests/golden/config5_cnn_losses.json, about 6 minutes
+    of oracle work, written by tests/golden/make_config5_losses.py and
+    re-derived live for its first steps by tests/test_config5_fixture.py).
+    The first 15 steps stay within 1e-4. Later steps separate: this loop's
+    trajectory is chaotic (max-pool and ReLU switch on rounding-level
+    differences), so GEMM accumulation order alone, or a 1-ulp difference in
+    one exponential, grows to ~1e-3 by step ~80; the 100-step bar is met in
+    the exact numerics mode (test_config5_exact_numerics_100_steps)."""
+    dev, _ = backends
+    got = config5_train(dev, steps=15)
+    want = config5_golden_losses()[:15]
+    drift = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    print(f"config5 fast path, 15 steps: max drift {drift.max():.3g} at step {drift.argmax()}",
+          flush=True)
     assert drift.max() <= 1e-4, f"max loss drift {drift.max():.3g} at step {drift.argmax()}"
 
 

@@ -189,3 +189,104 @@ def test_implicit_im2col_map_matches_the_oracle_unfold(shape, kernel, stride, pa
             assert lib.vkhip_im2col_offset(byref(u), c, st, row, pos, byref(off)) == 0
             got[row, pos] = 0.0 if off.value < 0 else storage[off.value]
     assert got.tobytes() == want.tobytes()
+
+
+# ---- node extent checks (vkhip_supports is host-only: no device needed) ----
+
+def _tensor(shape, dtype=_lib.F32, strides=None, data=0x1000):
+    t = _lib.TensorDesc()
+    t.data = data
+    t.dtype = dtype
+    t.ndim = len(shape)
+    if strides is None:
+        strides, s = [], 1
+        for e in reversed(shape):
+            strides.insert(0, s)
+            s *= e
+    for i, (e, st) in enumerate(zip(shape, strides)):
+        t.ne[i] = e
+        t.nb[i] = st
+    return t
+
+
+def _node(op, out, srcs, params=b""):
+    nd = _lib.NodeDesc()
+    nd.op = _lib.OP[op]
+    nd.n_src = len(srcs)
+    nd.out = out
+    for i, s in enumerate(srcs):
+        nd.src[i] = s
+    for i, b in enumerate(params):
+        nd.params[i] = b
+    return nd
+
+
+def _unfold_bytes(k, s, p, d, hw):
+    u = _lib.unfold((k, k), (s, s), (p, p), (d, d), hw)
+    return bytes(u)
+
+
+def _mask(*axes):
+    return int(sum(1 << a for a in axes)).to_bytes(4, "little")
+
+
+# (name, well-formed node, malformed variants): every malformed node must be
+# refused before any launch, because the kernels size their reads and writes
+# from params and the operands, not from the output tensor.
+def _extent_cases():
+    conv = _unfold_bytes(3, 1, 1, 1, (8, 8))
+    return [
+        ("matmul", _node("MATMUL", _tensor((4, 5)), [_tensor((4, 3)), _tensor((3, 5))]),
+         [_node("MATMUL", _tensor((4, 6)), [_tensor((4, 3)), _tensor((3, 5))]),
+          _node("MATMUL", _tensor((5, 5)), [_tensor((4, 3)), _tensor((3, 5))]),
+          _node("MATMUL", _tensor((4, 5)), [_tensor((4, 3)), _tensor((2, 5))]),
+          _node("MATMUL", _tensor((2, 4, 5)), [_tensor((3, 4, 3)), _tensor((3, 5))]),
+          _node("MATMUL", _tensor((3, 4, 5)), [_tensor((2, 4, 3)), _tensor((3, 3, 5))])]),
+        ("matmul_batch", _node("MATMUL", _tensor((2, 3, 4, 5)),
+                               [_tensor((2, 1, 4, 3)), _tensor((1, 3, 3, 5))]), []),
+        ("softmax", _node("SOFTMAX", _tensor((6, 7)), [_tensor((6, 7))], (1).to_bytes(4, "little")),
+         [_node("SOFTMAX", _tensor((6, 8)), [_tensor((6, 7))], (1).to_bytes(4, "little")),
+          _node("LOG_SOFTMAX", _tensor((42,)), [_tensor((6, 7))], (1).to_bytes(4, "little"))]),
+        ("sum", _node("SUM", _tensor((6,)), [_tensor((6, 7))], _mask(1)),
+         [_node("SUM", _tensor((7,)), [_tensor((6, 7))], _mask(1)),
+          _node("SUM", _tensor((6,)), [_tensor((6, 7))], _mask(1, 2))]),
+        ("argmax", _node("ARGMAX", _tensor((7,), _lib.I64), [_tensor((6, 7))], _mask(0)),
+         [_node("ARGMAX", _tensor((6,), _lib.I64), [_tensor((6, 7))], _mask(0))]),
+        ("im2col", _node("IM2COL", _tensor((2, 27, 64)), [_tensor((2, 3, 8, 8))], conv),
+         [_node("IM2COL", _tensor((2, 27, 63)), [_tensor((2, 3, 8, 8))], conv),
+          _node("IM2COL", _tensor((2, 26, 64)), [_tensor((2, 3, 8, 8))], conv),
+          _node("IM2COL", _tensor((1, 27, 64)), [_tensor((2, 3, 8, 8))], conv),
+          _node("IM2COL", _tensor((2, 27, 64)), [_tensor((2, 3, 8, 9))], conv)]),
+        ("col2im", _node("COL2IM", _tensor((2, 3, 8, 8)), [_tensor((2, 27, 64))], conv),
+         [_node("COL2IM", _tensor((2, 3, 8, 7)), [_tensor((2, 27, 64))], conv),
+          _node("COL2IM", _tensor((2, 4, 8, 8)), [_tensor((2, 27, 64))], conv),
+          _node("COL2IM", _tensor((2, 3, 8, 8)), [_tensor((2, 27, 60))], conv),
+          _node("COL2IM", _tensor((3, 3, 8, 8)), [_tensor((2, 27, 64))], conv)]),
+        ("max_pool2d", _node("MAX_POOL2D", _tensor((2, 3, 4, 4)), [_tensor((2, 3, 8, 8))],
+                             _unfold_bytes(2, 2, 0, 1, (8, 8))),
+         [_node("MAX_POOL2D", _tensor((2, 3, 4, 5)), [_tensor((2, 3, 8, 8))],
+                _unfold_bytes(2, 2, 0, 1, (8, 8))),
+          _node("MAX_POOL2D", _tensor((2, 3, 4, 4)), [_tensor((2, 3, 8, 9))],
+                _unfold_bytes(2, 2, 0, 1, (8, 8)))]),
+        ("max_pool2d_backward", _node("MAX_POOL2D_BACKWARD", _tensor((2, 3, 8, 8)),
+                                      [_tensor((2, 3, 4, 4)), _tensor((2, 3, 8, 8))],
+                                      _unfold_bytes(2, 2, 0, 1, (8, 8))),
+         [_node("MAX_POOL2D_BACKWARD", _tensor((2, 3, 8, 8)),
+                [_tensor((2, 3, 4, 3)), _tensor((2, 3, 8, 8))], _unfold_bytes(2, 2, 0, 1, (8, 8))),
+          _node("MAX_POOL2D_BACKWARD", _tensor((2, 3, 8, 4)),
+                [_tensor((2, 3, 4, 4)), _tensor((2, 3, 8, 8))], _unfold_bytes(2, 2, 0, 1, (8, 8)))]),
+    ]
+
+
+@pytest.mark.parametrize("case", _extent_cases(), ids=lambda c: c[0])
+def test_supports_refuses_nodes_whose_extents_disagree(case):
+    """A node whose output (or col2im source) extents disagree with what its
+    params and operands imply is not supported, so compute() refuses it with
+    VKHIP_ERR_INVALID before any launch instead of writing out of bounds."""
+    from ctypes import byref as ref
+
+    lib = _lib.load()
+    name, good, bad = case
+    assert lib.vkhip_supports(ref(good)) == 1, (name, lib.vkhip_last_error())
+    for i, nd in enumerate(bad):
+        assert lib.vkhip_supports(ref(nd)) == 0, f"{name}: malformed variant {i} accepted"

@@ -258,3 +258,34 @@ def test_early_backward_flushes_give_the_same_training_steps(cpu, every):
     losses, params, calls = run(every)
     assert losses == want_losses and params == want_params
     assert calls > base_calls
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_pre_step_alias_sees_the_update_on_both_sgd_paths(cpu, fused):
+    """assign() copies into the parameter's storage, as the reference's
+    assign does (copy_device_to_device, python/vkml/__init__.py:153-165), and
+    the fused step updates in place: a detach() taken before step() sees the
+    new values on both paths, and both paths give the same bits."""
+    rng = np.random.default_rng(SEED + 11)
+    w = rng.standard_normal((6, 5)).astype(np.float32)
+    g = rng.standard_normal((6, 5)).astype(np.float32)
+    results = {}
+    for path in (fused, not fused):
+        p = T.tensor(w, requires_grad=True, backend=cpu)
+        alias = p.detach()
+        opt = optim.SGD([p], lr=0.1, momentum=0.9, fused=path)
+        for _ in range(2):
+            p.grad = T.tensor(g, backend=cpu)
+            opt.step()
+        results[path] = p.numpy()
+        assert alias.numpy().tobytes() == results[path].tobytes()
+        assert results[path].tobytes() != w.tobytes()
+    assert results[True].tobytes() == results[False].tobytes()
+
+
+def test_assign_checks_its_pairs(cpu):
+    a = T.tensor(np.zeros((2, 3), np.float32), backend=cpu)
+    with pytest.raises(ValueError):
+        T.assign([a], [])
+    with pytest.raises(ValueError):
+        T.assign([a], [T.tensor(np.zeros((3, 2), np.float32), backend=cpu)])

@@ -20,7 +20,7 @@ F32, F16, I32, I64, BOOL = 0, 1, 2, 3, 4
 
 REDUCE_SUM, REDUCE_MEAN, REDUCE_MAX, REDUCE_MIN, REDUCE_ARGMAX, REDUCE_ARGMIN = range(6)
 
-GEMM_AUTO, GEMM_MFMA, GEMM_GEMV = 0, 1, 2
+GEMM_AUTO, GEMM_MFMA, GEMM_GEMV, GEMM_EXACT = 0, 1, 2, 3
 
 # vkml::OpKind ordinals (include/vkml/graph/op.h:30-139) for the supported subset.
 OP = dict(
@@ -118,6 +118,12 @@ SIGNATURES = {
     "vkhip_compute": (c_int, [POINTER(NodeDesc), c_size_t]),
     "vkhip_gemm": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand), c_void_p,
                            POINTER(GemmOpts)]),
+    "vkhip_program_begin": (c_int, []),
+    "vkhip_program_end": (c_int, [POINTER(c_void_p)]),
+    "vkhip_program_run": (c_int, [c_void_p, c_int]),
+    "vkhip_program_destroy": (c_int, [c_void_p]),
+    "vkhip_program_info": (c_int, [c_void_p, POINTER(c_size_t), POINTER(c_size_t),
+                                   POINTER(c_int)]),
     "vkhip_gemm_plan": (c_int, [c_uint32, c_uint32, c_uint32, c_uint32, c_int32,
                                 POINTER(c_uint32), POINTER(c_uint32)]),
     "vkhip_split_k_reduce": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32]),

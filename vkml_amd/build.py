@@ -26,7 +26,8 @@ LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libvkhip.so"
 OBJDIR = ROOT / "_build" / "vkhip"
 
-SOURCES = ["runtime.hip", "allocator.hip", "observe.hip", "gemm.hip", "movement.hip", "reduce.hip", "elementwise.hip"]
+SOURCES = ["runtime.hip", "allocator.hip", "observe.hip", "program.hip", "gemm.hip", "movement.hip",
+           "reduce.hip", "elementwise.hip"]
 
 
 def hipcc() -> str:

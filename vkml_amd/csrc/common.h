@@ -31,6 +31,13 @@ struct Context {
     // (reference grows its own the same way, vulkan_backend.cpp:899-919).
     float* ws = nullptr;
     size_t ws_bytes = 0;
+    int ws_pins = 0;               // captured graphs holding the workspace blocks
+    void* ws_retired[64] = {};     // blocks replaced while pinned, freed at the last unpin
+    int ws_retired_count = 0;
+    // GEMM kernel selection for MATMUL nodes, from VKHIP_GEMM_KERNEL at init
+    // ("exact" | "mfma" | unset/"auto"), as the reference's VKML_GEMM_KERNEL
+    // selects its GEMM for every matmul in the process (vulkan_backend.cpp:2158-2172).
+    int node_gemm_kernel = VKHIP_GEMM_AUTO;
 };
 
 Context& ctx();
@@ -40,6 +47,24 @@ int require_ready();
 
 // Workspace of at least `bytes` on the current stream.
 int workspace(size_t bytes, float** out);
+// While pinned (a captured HIP graph holds the current blocks), a workspace
+// that must grow gets a new block and keeps the old one until the last pin
+// goes, and the implicit-im2col row tables are not evicted.
+int pin_workspaces(int delta);
+bool workspaces_pinned();
+
+// Recorded programs (program.hip): the calls that enqueue work on tensors
+// note themselves after they succeed; no-ops unless a program is recording.
+bool program_recording();
+void program_note_compute(const vkhip_node* nodes, size_t n);
+void program_note_sgd(const vkhip_sgd_param* params, size_t count, float lr, float momentum,
+                      float weight_decay, int nesterov);
+void program_note_copy(const vkhip_copy* copies, size_t n);
+// Per-unit event timing is on (observe.hip).
+bool profiling_on();
+
+int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd, float* c,
+         const vkhip_gemm_opts* opts);
 
 // Decision facts and units of work (observe.hip). A unit is a node of
 // vkhip_compute or one per-op entry call; decisions published inside it carry

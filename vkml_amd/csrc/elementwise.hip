@@ -570,5 +570,7 @@ extern "C" int vkhip_sgd_step(const vkhip_sgd_param* params, size_t count, float
     if (st != VKHIP_OK) return st;
     vkhip::Unit unit("sgd_step");
     if (count && !params) return vkhip::fail(VKHIP_ERR_INVALID, "sgd_step: null parameter list");
-    return vkhip::launch_sgd_step(params, count, lr, momentum, weight_decay, nesterov);
+    st = vkhip::launch_sgd_step(params, count, lr, momentum, weight_decay, nesterov);
+    if (st == VKHIP_OK) vkhip::program_note_sgd(params, count, lr, momentum, weight_decay, nesterov);
+    return st;
 }

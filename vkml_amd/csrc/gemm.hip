@@ -1008,6 +1008,107 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ a, 
     if (lane == 0) y[row] = v;
 }
 
+// ---- exact GEMM (comparison arm) --------------------------------------------
+// C[b, i, j] = the CPU oracle's sum for that output, bit for bit: each product
+// a[i,k] * b[k,j] rounded to f32 on its own (no FMA), the K products summed
+// in the oracle's pairwise order (reference matmul_impl,
+// kernels_matmul.cpp:34-87, over pairwise_sum, reduce.h:55-72). The role of
+// the reference's gemm_naive.comp:56-101, the arm selected with
+// VKML_GEMM_KERNEL=naive (vulkan_backend.cpp:2158-2161) to check the fast
+// kernels against: here the fast kernels accumulate in the matrix cores'
+// order, so this arm is what reproduces the oracle exactly.
+//
+// A workgroup owns a 32 x 32 output tile, a thread 2 x 2 outputs (rows ty and
+// ty + 16, columns tx and tx + 16). The K axis is walked leaf by leaf in the
+// pairwise tree's depth-D layout (pairwise_leaf): the leaf's A and B slices
+// (at most 32 k each) are staged in LDS through the operands' strides, each
+// thread sums its outputs' rounded products over the leaf sequentially from
+// 0.0, and pushes each leaf sum onto a per-output carry stack; 2^D pushes of
+// a complete tree leave the balanced fold of the leaves on top, which is the
+// oracle's recursion (empty leaves carry +0.0, exact).
+constexpr int kExactTile = 32;
+constexpr int kExactLevels = 28;  // 2^27 leaves of 32 cover every 32-bit K
+
+__device__ __forceinline__ void exact_push(float (&stack)[kExactLevels], uint32_t count,
+                                           float block) {
+    bool carry = true;
+#pragma unroll
+    for (int l = 0; l < kExactLevels; ++l) {
+        if (carry) {
+            if ((count >> l) & 1u) {
+                block = __fadd_rn(stack[l], block);
+            } else {
+                stack[l] = block;
+                carry = false;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void gemm_exact_kernel(GemmArgs g, int depth) {
+    __shared__ float As[kExactTile][kExactTile + 1];  // [row][k]
+    __shared__ float Bs[kExactTile][kExactTile + 1];  // [k][col]
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const uint32_t tm = blockIdx.x / g.tiles_n, tn = blockIdx.x - tm * g.tiles_n;
+    const uint32_t row0 = tm * kExactTile, col0 = tn * kExactTile;
+    const uint32_t bz = blockIdx.z;
+    const uint32_t i0 = bz / g.b1, i1 = bz - i0 * g.b1;
+    const float* a = g.a + static_cast<int64_t>(i0) * g.sa0 + static_cast<int64_t>(i1) * g.sa1;
+    const float* b = g.b + static_cast<int64_t>(i0) * g.sb0 + static_cast<int64_t>(i1) * g.sb1;
+    float stack[4][kExactLevels];
+#pragma unroll
+    for (int o = 0; o < 4; ++o)
+#pragma unroll
+        for (int l = 0; l < kExactLevels; ++l) stack[o][l] = 0.0f;
+    const uint32_t leaves = 1u << depth;
+    for (uint32_t leaf = 0; leaf < leaves; ++leaf) {
+        uint32_t kb, ke;
+        pairwise_leaf(g.k, depth, leaf, kb, ke);
+        const uint32_t len = ke - kb;
+        if (len > 0) {
+            // stage A[row0 .. +32][kb .. ke) and B[kb .. ke)[col0 .. +32], zeros outside
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int idx = tid + 256 * q;
+                const int r = idx >> 5, kk = idx & 31;
+                const uint32_t gr = row0 + r;
+                As[r][kk] = (gr < g.m && static_cast<uint32_t>(kk) < len)
+                                ? a[static_cast<int64_t>(gr) * g.sam + static_cast<int64_t>(kb + kk) * g.sak]
+                                : 0.0f;
+                const int bk = idx >> 5, c = idx & 31;
+                const uint32_t gc = col0 + c;
+                Bs[bk][c] = (gc < g.n && static_cast<uint32_t>(bk) < len)
+                                ? b[static_cast<int64_t>(kb + bk) * g.sbk + static_cast<int64_t>(gc) * g.sbn]
+                                : 0.0f;
+            }
+        }
+        __syncthreads();
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t kk = 0; kk < len; ++kk) {
+            const float a0 = As[ty][kk], a1 = As[ty + 16][kk];
+            const float b0 = Bs[kk][tx], b1 = Bs[kk][tx + 16];
+            acc[0] = __fadd_rn(acc[0], __fmul_rn(a0, b0));
+            acc[1] = __fadd_rn(acc[1], __fmul_rn(a0, b1));
+            acc[2] = __fadd_rn(acc[2], __fmul_rn(a1, b0));
+            acc[3] = __fadd_rn(acc[3], __fmul_rn(a1, b1));
+        }
+#pragma unroll
+        for (int o = 0; o < 4; ++o) exact_push(stack[o], leaf, acc[o]);
+        __syncthreads();
+    }
+    float* c = g.c + static_cast<uint64_t>(bz) * g.m * g.n;
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+        const uint32_t gr = row0 + ty + 16 * (o >> 1), gc = col0 + tx + 16 * (o & 1);
+        float v = 0.0f;
+#pragma unroll
+        for (int l = 0; l < kExactLevels; ++l)
+            if (l == depth) v = stack[o][l];
+        if (gr < g.m && gc < g.n) c[static_cast<uint64_t>(gr) * g.n + gc] = v;
+    }
+}
+
 // ---- planning ---------------------------------------------------------------
 
 // Split-K plan (reference plan_split_k, vulkan_backend.cpp:596-647), restated
@@ -1197,6 +1298,39 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
     return VKHIP_OK;
 }
 
+static int launch_gemm_exact(const float* a, const vkhip_operand& ad, const float* b,
+                             const vkhip_operand& bd, float* c, uint32_t batch, uint32_t b1,
+                             uint32_t m, uint32_t n, uint32_t k) {
+    GemmArgs g{};
+    g.a = a;
+    g.b = b;
+    g.c = c;
+    g.sa0 = ad.ne[0] == 1 ? 0 : ad.nb[0];
+    g.sa1 = ad.ne[1] == 1 ? 0 : ad.nb[1];
+    g.sam = ad.nb[2];
+    g.sak = ad.nb[3];
+    g.sb0 = bd.ne[0] == 1 ? 0 : bd.nb[0];
+    g.sb1 = bd.ne[1] == 1 ? 0 : bd.nb[1];
+    g.sbk = bd.nb[2];
+    g.sbn = bd.nb[3];
+    g.b1 = b1;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.tiles_m = ceil_div(m, kExactTile);
+    g.tiles_n = ceil_div(n, kExactTile);
+    const uint64_t tiles = static_cast<uint64_t>(g.tiles_m) * g.tiles_n;
+    if (tiles > 0x7fffffffull)
+        return fail(VKHIP_ERR_UNSUPPORTED, "exact gemm: %llu output tiles",
+                    static_cast<unsigned long long>(tiles));
+    const int depth = pairwise_depth(k);
+    if (depth >= kExactLevels) return fail(VKHIP_ERR_UNSUPPORTED, "exact gemm: K=%u too deep", k);
+    hipLaunchKernelGGL(gemm_exact_kernel, dim3(static_cast<uint32_t>(tiles), 1, batch), dim3(256), 0,
+                       ctx().stream, g, depth);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
 int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd,
          float* c, const vkhip_gemm_opts* opts) {
     const uint32_t b0 = ad.ne[0] > bd.ne[0] ? ad.ne[0] : bd.ne[0];
@@ -1229,6 +1363,13 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     }
     if (kernel == VKHIP_GEMM_GEMV)
         return fail(VKHIP_ERR_UNSUPPORTED, "gemv requested for a %ux%ux%u problem", m, n, k);
+    if (kernel == VKHIP_GEMM_EXACT) {
+        publish("matmul.kernel", "matmul", "gemm_exact", "gemm_mfma", "exact arm requested",
+                static_cast<int64_t>(k), static_cast<int64_t>(m) * n);
+        return launch_gemm_exact(a, ad, b, bd, c, static_cast<uint32_t>(batch), b1, m, n, k);
+    }
+    if (kernel != VKHIP_GEMM_AUTO && kernel != VKHIP_GEMM_MFMA)
+        return fail(VKHIP_ERR_INVALID, "gemm: unknown kernel selection %d", kernel);
 
     uint32_t splits, chunk;
     TileChoice tile;
@@ -1284,20 +1425,29 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     float* target = c;
     if (splits > 1) {
         float* ws = nullptr;
-        int st = workspace(out_elems * splits * sizeof(float), &ws);
-        if (st != VKHIP_OK) return st;
+        const size_t need = out_elems * splits * sizeof(float);
+        {
+            int st = workspace(need, &ws);
+            if (st != VKHIP_OK) return st;
+        }
         target = ws;
         g.split_stride = out_elems;
     }
     g.c = target;
     int amode = akc ? (g.a_vec ? KCV : KCS) : (g.a_vec ? RCV : RCS);
+    // The buffer-load paths (straight-to-LDS operands and the direct kernels)
+    // address an operand by unsigned 32-bit byte offsets from its base, so
+    // they take operands whose strides are all non-negative; a negative
+    // stride (a reversed view) stays on the pointer loads.
+    const bool a_fwd = g.sa0 >= 0 && g.sa1 >= 0 && g.sam >= 0 && g.sak >= 0;
+    const bool b_fwd = g.sb0 >= 0 && g.sb1 >= 0 && g.sbk >= 0 && g.sbn >= 0;
     // Straight-to-LDS operands: unit k stride, K a multiple of four, and every
     // byte offset of one batch's operand within the buffer resource's 2^31 bytes.
-    if (amode == KCV && g.sak == 1 && k % 4 == 0 &&
+    if (a_fwd && amode == KCV && g.sak == 1 && k % 4 == 0 &&
         ((static_cast<int64_t>(m) - 1) * g.sam + k) * 4 < (int64_t{1} << 31))
         amode = KCD;
     int bmode = bkc ? (g.b_vec ? KCV : KCS) : (g.b_vec ? RCV : RCS);
-    if (bmode == KCV && g.sbk == 1 && k % 4 == 0 &&
+    if (b_fwd && bmode == KCV && g.sbk == 1 && k % 4 == 0 &&
         ((static_cast<int64_t>(n) - 1) * g.sbn + k) * 4 < (int64_t{1} << 31))
         bmode = KCD;
     int st;
@@ -1306,9 +1456,9 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     // group is wholly inside or outside), A in load mode KCD (NN) or
     // row-contiguous like B with M a multiple of four (TN), byte offsets
     // within 2^31.
-    const bool b_rows = bmode == RCV && g.sbn == 1 && n % 4 == 0 && g.sbk % 4 == 0 &&
+    const bool b_rows = b_fwd && bmode == RCV && g.sbn == 1 && n % 4 == 0 && g.sbk % 4 == 0 &&
                         ((static_cast<int64_t>(k) - 1) * g.sbk + n) * 4 < (int64_t{1} << 31);
-    const bool a_rows = amode == RCV && g.sam == 1 && m % 4 == 0 && g.sak % 4 == 0 &&
+    const bool a_rows = a_fwd && amode == RCV && g.sam == 1 && m % 4 == 0 && g.sak % 4 == 0 &&
                         ((static_cast<int64_t>(k) - 1) * g.sak + m) * 4 < (int64_t{1} << 31);
     if (tile.bm == 128 && b_rows && (amode == KCD || a_rows) &&
         reinterpret_cast<uintptr_t>(target) % 16 == 0) {
@@ -1391,7 +1541,9 @@ static int conv_row_table(Im2colB& im, uint32_t k) {
     hipLaunchKernelGGL(conv_row_table_kernel, dim3(ceil_div(rows, 256u)), dim3(256), 0, ctx().stream,
                        im, table, k, rows);
     VKHIP_LAUNCH_CHECK();
-    if (g_tabs.size() == kMaxRowTables) {
+    // (a captured HIP graph may address every cached table: none is evicted
+    // while graphs hold the workspaces)
+    if (g_tabs.size() >= kMaxRowTables && !workspaces_pinned()) {
         st = cached_free(g_tabs.front().table);
         g_tabs.erase(g_tabs.begin());
         if (st != VKHIP_OK) return st;

@@ -139,6 +139,10 @@ extern "C" int vkhip_subscribe_decisions(vkhip_decision_fn fn, void* user) {
     return VKHIP_OK;
 }
 
+namespace vkhip {
+bool profiling_on() { return obs().profiling.load(std::memory_order_relaxed); }
+}  // namespace vkhip
+
 extern "C" int vkhip_set_profiling(int enabled) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;

@@ -15,9 +15,7 @@
 
 namespace vkhip {
 
-// Launchers defined in the kernel translation units.
-int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd, float* c,
-         const vkhip_gemm_opts* opts);
+// Launchers defined in the kernel translation units (gemm() in common.h).
 int launch_im2col(const float* src, const vkhip_operand& sd, float* dst, const vkhip_unfold& p);
 int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
                   const vkhip_unfold& p);
@@ -59,6 +57,7 @@ Context& ctx() {
 }
 
 static std::mutex g_mu;  // guards init/shutdown/workspace (reference allocation-map mutex)
+
 static int release_stage_slots();  // pinned upload/download slots, below
 
 int require_ready() {
@@ -71,7 +70,15 @@ int workspace(size_t bytes, float** out) {
     std::lock_guard<std::mutex> lk(g_mu);
     Context& c = ctx();
     if (c.ws_bytes < bytes) {
-        if (c.ws) VKHIP_HIP(hipFreeAsync(c.ws, c.stream));
+        if (c.ws && c.ws_pins > 0) {
+            // a captured graph still addresses this block: keep it
+            if (c.ws_retired_count == static_cast<int>(sizeof c.ws_retired / sizeof c.ws_retired[0]))
+                return fail(VKHIP_ERR_UNSUPPORTED,
+                            "workspace: too many blocks held by captured graphs (destroy some programs)");
+            c.ws_retired[c.ws_retired_count++] = c.ws;
+        } else if (c.ws) {
+            VKHIP_HIP(hipFreeAsync(c.ws, c.stream));
+        }
         c.ws = nullptr;
         c.ws_bytes = 0;
         void* p = nullptr;
@@ -82,6 +89,24 @@ int workspace(size_t bytes, float** out) {
     }
     *out = c.ws;
     return VKHIP_OK;
+}
+
+int pin_workspaces(int delta) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Context& c = ctx();
+    c.ws_pins += delta;
+    if (c.ws_pins < 0) c.ws_pins = 0;
+    if (c.ws_pins == 0 && c.ws_retired_count > 0) {
+        for (int i = 0; i < c.ws_retired_count; ++i)
+            if (c.ready) VKHIP_HIP(hipFreeAsync(c.ws_retired[i], c.stream));
+        c.ws_retired_count = 0;
+    }
+    return VKHIP_OK;
+}
+
+bool workspaces_pinned() {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return ctx().ws_pins > 0;
 }
 
 // ---- node -> descriptor helpers ------------------------------------------------
@@ -261,6 +286,138 @@ static int supports_node(const vkhip_node& nd) {
     }
 }
 
+static const char* op_name(int op);
+
+static int64_t window_span(int64_t extent, int k, int s, int pad, int dil) {
+    if (k <= 0 || s <= 0 || dil <= 0 || pad < 0) return -1;
+    return (extent + 2LL * pad - (static_cast<int64_t>(dil) * (k - 1) + 1)) / s + 1;
+}
+
+static int64_t tensor_numel(const vkhip_tensor& t) {
+    int64_t n = 1;
+    for (int i = 0; i < t.ndim; ++i) n *= t.ne[i];
+    return n;
+}
+
+// The extents a node's params and operands imply for its output (and, for
+// col2im, its source). The kernels size their writes and reads from params
+// and operand descriptors, so a node whose tensors disagree with them is
+// refused here instead of reading or writing out of bounds. Returns VKHIP_OK
+// or VKHIP_ERR_INVALID with the message set.
+static int check_extents(const vkhip_node& nd) {
+    const vkhip_tensor& o = nd.out;
+    if (nd.n_src < 0 || nd.n_src > 3) return fail(VKHIP_ERR_INVALID, "node with %d sources", nd.n_src);
+    if (!fits32(o)) return fail(VKHIP_ERR_INVALID, "%s: output rank or extents out of range", op_name(nd.op));
+    for (int s = 0; s < nd.n_src; ++s)
+        if (!fits32(nd.src[s]))
+            return fail(VKHIP_ERR_INVALID, "%s: source %d rank or extents out of range", op_name(nd.op), s);
+    switch (nd.op) {
+        case VKHIP_OP_MATMUL: {
+            if (nd.n_src != 2 || nd.src[0].ndim < 2 || nd.src[1].ndim < 2 || o.ndim < 2)
+                return fail(VKHIP_ERR_INVALID, "matmul: operands and output need rank >= 2");
+            const vkhip_operand a = to_operand(nd.src[0]), b = to_operand(nd.src[1]);
+            const vkhip_operand c = to_operand(o);
+            if (a.ne[3] != b.ne[2])
+                return fail(VKHIP_ERR_INVALID, "matmul: inner extents %u and %u disagree", a.ne[3], b.ne[2]);
+            const uint32_t want[4] = {std::max(a.ne[0], b.ne[0]), std::max(a.ne[1], b.ne[1]), a.ne[2],
+                                      b.ne[3]};
+            for (int i = 0; i < 4; ++i)
+                if (c.ne[i] != want[i] || (i < 2 && ((a.ne[i] != 1 && a.ne[i] != want[i]) ||
+                                                     (b.ne[i] != 1 && b.ne[i] != want[i]))))
+                    return fail(VKHIP_ERR_INVALID,
+                                "matmul: output [%u,%u,%u,%u] disagrees with the operands' [%u,%u,%u,%u]",
+                                c.ne[0], c.ne[1], c.ne[2], c.ne[3], want[0], want[1], want[2], want[3]);
+            return VKHIP_OK;
+        }
+        case VKHIP_OP_SOFTMAX:
+        case VKHIP_OP_LOG_SOFTMAX:
+            if (nd.n_src != 1 || o.ndim != nd.src[0].ndim)
+                return fail(VKHIP_ERR_INVALID, "softmax: output rank differs from the source's");
+            for (int i = 0; i < o.ndim; ++i)
+                if (o.ne[i] != nd.src[0].ne[i])
+                    return fail(VKHIP_ERR_INVALID, "softmax: output extents differ from the source's");
+            return VKHIP_OK;
+        case VKHIP_OP_SUM:
+        case VKHIP_OP_MEAN:
+        case VKHIP_OP_MAX:
+        case VKHIP_OP_MIN:
+        case VKHIP_OP_ARGMAX:
+        case VKHIP_OP_ARGMIN: {
+            if (nd.n_src != 1) return fail(VKHIP_ERR_INVALID, "reduction: one source expected");
+            uint32_t mask;
+            memcpy(&mask, nd.params, sizeof mask);
+            const vkhip_tensor& s = nd.src[0];
+            if (s.ndim < 0 || s.ndim > 4 || (mask >> std::max(s.ndim, 0)) != 0)
+                return fail(VKHIP_ERR_INVALID, "reduction: axes mask 0x%x outside rank %d", mask, s.ndim);
+            if (mask == 0) mask = s.ndim <= 0 ? 0u : (1u << s.ndim) - 1u;
+            int64_t kept = 1;
+            for (int i = 0; i < s.ndim; ++i)
+                if (!((mask >> i) & 1u)) kept *= s.ne[i];
+            if (tensor_numel(o) != kept)
+                return fail(VKHIP_ERR_INVALID, "reduction: output holds %lld values, the kept axes give %lld",
+                            static_cast<long long>(tensor_numel(o)), static_cast<long long>(kept));
+            return VKHIP_OK;
+        }
+        case VKHIP_OP_IM2COL:
+        case VKHIP_OP_COL2IM: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            const int64_t oh = window_span(p.image_h, p.kernel_h, p.stride_h, p.pad_h, p.dilation_h);
+            const int64_t ow = window_span(p.image_w, p.kernel_w, p.stride_w, p.pad_w, p.dilation_w);
+            if (oh <= 0 || ow <= 0 || p.image_h < 0 || p.image_w < 0)
+                return fail(VKHIP_ERR_INVALID, "%s: invalid window geometry", op_name(nd.op));
+            const bool fwd = nd.op == VKHIP_OP_IM2COL;
+            const vkhip_tensor& img = fwd ? nd.src[0] : o;
+            const vkhip_tensor& cols = fwd ? o : nd.src[0];
+            if (nd.n_src != 1 || img.ndim != 4 || cols.ndim != 3)
+                return fail(VKHIP_ERR_INVALID, "%s: image rank 4 and columns rank 3 expected", op_name(nd.op));
+            const int64_t rows = img.ne[1] * static_cast<int64_t>(p.kernel_h) * p.kernel_w;
+            if (img.ne[2] != p.image_h || img.ne[3] != p.image_w || cols.ne[0] != img.ne[0] ||
+                cols.ne[1] != rows || cols.ne[2] != oh * ow)
+                return fail(VKHIP_ERR_INVALID,
+                            "%s: columns [%lld,%lld,%lld] and image [%lld,%lld,%lld,%lld] disagree with "
+                            "the window geometry (want [%lld,%lld,%lld], image %dx%d)",
+                            op_name(nd.op), static_cast<long long>(cols.ne[0]),
+                            static_cast<long long>(cols.ne[1]), static_cast<long long>(cols.ne[2]),
+                            static_cast<long long>(img.ne[0]), static_cast<long long>(img.ne[1]),
+                            static_cast<long long>(img.ne[2]), static_cast<long long>(img.ne[3]),
+                            static_cast<long long>(img.ne[0]), static_cast<long long>(rows),
+                            static_cast<long long>(oh * ow), p.image_h, p.image_w);
+            return VKHIP_OK;
+        }
+        case VKHIP_OP_MAX_POOL2D: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            const int64_t oh = window_span(p.image_h, p.kernel_h, p.stride_h, p.pad_h, p.dilation_h);
+            const int64_t ow = window_span(p.image_w, p.kernel_w, p.stride_w, p.pad_w, p.dilation_w);
+            const vkhip_tensor& x = nd.src[0];
+            if (nd.n_src != 1 || x.ndim != 4 || o.ndim != 4 || oh <= 0 || ow <= 0 ||
+                x.ne[2] != p.image_h || x.ne[3] != p.image_w || o.ne[0] != x.ne[0] ||
+                o.ne[1] != x.ne[1] || o.ne[2] != oh || o.ne[3] != ow)
+                return fail(VKHIP_ERR_INVALID, "max_pool2d: input/output extents disagree with the window geometry");
+            return VKHIP_OK;
+        }
+        case VKHIP_OP_MAX_POOL2D_BACKWARD: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            const int64_t oh = window_span(p.image_h, p.kernel_h, p.stride_h, p.pad_h, p.dilation_h);
+            const int64_t ow = window_span(p.image_w, p.kernel_w, p.stride_w, p.pad_w, p.dilation_w);
+            const vkhip_tensor& g = nd.src[0];
+            const vkhip_tensor& x = nd.src[1];
+            if (nd.n_src != 2 || g.ndim != 4 || x.ndim != 4 || o.ndim != 4 || oh <= 0 || ow <= 0 ||
+                x.ne[2] != p.image_h || x.ne[3] != p.image_w || g.ne[0] != x.ne[0] ||
+                g.ne[1] != x.ne[1] || g.ne[2] != oh || g.ne[3] != ow)
+                return fail(VKHIP_ERR_INVALID,
+                            "max_pool2d_backward: gradient/input extents disagree with the window geometry");
+            for (int i = 0; i < 4; ++i)
+                if (o.ne[i] != x.ne[i])
+                    return fail(VKHIP_ERR_INVALID, "max_pool2d_backward: output shape differs from the input's");
+            return VKHIP_OK;
+        }
+        default: return VKHIP_OK;  // elementwise (same extents: supports_node), conv, cross-entropy
+    }
+}
+
 static const char* op_name(int op) {
     switch (op) {
         case VKHIP_OP_MATMUL: return "matmul";
@@ -309,6 +466,10 @@ static const char* op_name(int op) {
 
 static int compute_node(const vkhip_node& nd) {
     Unit unit(op_name(nd.op));
+    {
+        const int rc = check_extents(nd);
+        if (rc != VKHIP_OK) return rc;
+    }
     if (!supports_node(nd))
         return fail(VKHIP_ERR_UNSUPPORTED, "vkhip: %s (op %d) is not supported for these dtypes/layout",
                     op_name(nd.op), nd.op);
@@ -316,9 +477,10 @@ static int compute_node(const vkhip_node& nd) {
         case VKHIP_OP_MATMUL: {
             const vkhip_operand a = to_operand(nd.src[0]);
             const vkhip_operand b = to_operand(nd.src[1]);
+            const vkhip_gemm_opts opts{ctx().node_gemm_kernel, 0};
             return gemm(static_cast<const float*>(nd.src[0].data), a,
                         static_cast<const float*>(nd.src[1].data), b,
-                        static_cast<float*>(nd.out.data), nullptr);
+                        static_cast<float*>(nd.out.data), &opts);
         }
         case VKHIP_OP_SUM:
         case VKHIP_OP_MEAN:
@@ -486,6 +648,11 @@ extern "C" int vkhip_init(int device) {
     VKHIP_HIP(hipStreamCreateWithFlags(&c.own_stream, hipStreamNonBlocking));
     c.stream = c.own_stream;
     c.device = device;
+    c.node_gemm_kernel = VKHIP_GEMM_AUTO;
+    if (const char* sel = getenv("VKHIP_GEMM_KERNEL")) {
+        if (strcmp(sel, "exact") == 0) c.node_gemm_kernel = VKHIP_GEMM_EXACT;
+        else if (strcmp(sel, "mfma") == 0) c.node_gemm_kernel = VKHIP_GEMM_MFMA;
+    }
     memset(&c.caps, 0, sizeof c.caps);
     snprintf(c.caps.name, sizeof c.caps.name, "%s", prop.name);
     c.caps.device_index = device;
@@ -509,6 +676,9 @@ extern "C" int vkhip_shutdown(void) {
         c.ws = nullptr;
         c.ws_bytes = 0;
     }
+    for (int i = 0; i < c.ws_retired_count; ++i) VKHIP_HIP(hipFreeAsync(c.ws_retired[i], c.stream));
+    c.ws_retired_count = 0;
+    c.ws_pins = 0;
     {
         const int rc = vkhip::release_conv_tables();
         if (rc != VKHIP_OK) return rc;
@@ -685,15 +855,17 @@ extern "C" int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes
     return VKHIP_OK;
 }
 
+namespace vkhip {
+int copy_pairs(const vkhip_copy* copies, size_t n);
+}
+
 extern "C" int vkhip_copy_device_to_device(const vkhip_copy* copies, size_t n) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
-    vkhip::Unit unit("copy_device_to_device");
-    for (size_t i = 0; i < n; ++i) {
-        st = vkhip::launch_copy_bytes(copies[i].dst, copies[i].src, copies[i].nbytes);
-        if (st != VKHIP_OK) return st;
-    }
-    return VKHIP_OK;
+    if (n && !copies) return fail(VKHIP_ERR_INVALID, "copy_device_to_device: null copy list");
+    st = vkhip::copy_pairs(copies, n);
+    if (st == VKHIP_OK) vkhip::program_note_copy(copies, n);
+    return st;
 }
 
 extern "C" int vkhip_synchronize(void) {
@@ -706,17 +878,35 @@ extern "C" int vkhip_synchronize(void) {
 // ---- compute -------------------------------------------------------------------------
 
 extern "C" int vkhip_supports(const vkhip_node* node) {
-    return node ? vkhip::supports_node(*node) : 0;
+    return node && vkhip::check_extents(*node) == VKHIP_OK ? vkhip::supports_node(*node) : 0;
 }
+
+namespace vkhip {
+int compute_nodes(const vkhip_node* nodes, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const int st = compute_node(nodes[i]);
+        if (st != VKHIP_OK) return st;
+    }
+    return VKHIP_OK;
+}
+
+int copy_pairs(const vkhip_copy* copies, size_t n) {
+    Unit unit("copy_device_to_device");
+    for (size_t i = 0; i < n; ++i) {
+        const int st = launch_copy_bytes(copies[i].dst, copies[i].src, copies[i].nbytes);
+        if (st != VKHIP_OK) return st;
+    }
+    return VKHIP_OK;
+}
+}  // namespace vkhip
 
 extern "C" int vkhip_compute(const vkhip_node* nodes, size_t n) {
     int st = vkhip::require_ready();
     if (st != VKHIP_OK) return st;
-    for (size_t i = 0; i < n; ++i) {
-        st = vkhip::compute_node(nodes[i]);
-        if (st != VKHIP_OK) return st;
-    }
-    return VKHIP_OK;
+    if (n && !nodes) return fail(VKHIP_ERR_INVALID, "compute: null node span");
+    st = vkhip::compute_nodes(nodes, n);
+    if (st == VKHIP_OK) vkhip::program_note_compute(nodes, n);
+    return st;
 }
 
 extern "C" int vkhip_max_pool2d(const float* src, float* dst, uint32_t planes, uint32_t out_h,

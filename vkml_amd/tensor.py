@@ -109,7 +109,10 @@ class DeviceBackend:
     def alloc(self, nbytes: int):
         from .device import Buffer
 
-        return Buffer(max(int(nbytes), 4))
+        buf = Buffer(max(int(nbytes), 4))
+        if _KEEP is not None:
+            _KEEP.append(buf)
+        return buf
 
     def upload(self, storage, offset_bytes: int, arr: np.ndarray) -> None:
         arr = np.ascontiguousarray(arr)
@@ -133,6 +136,8 @@ class DeviceBackend:
         storage or None, velocity offset bytes, element count, first) per
         parameter; one launch."""
         arr = (_lib.SgdParam * len(entries))()
+        if _KEEP is not None:
+            _KEEP.extend(x for e in entries for x in (e[0], e[1], e[3]) if x is not None)
         for d, (p, g, goff, v, voff, n, first) in zip(arr, entries):
             d.param = p.ptr
             d.grad = g.ptr + goff
@@ -142,11 +147,26 @@ class DeviceBackend:
         _lib.check(self.hip.lib.vkhip_sgd_step(arr, len(entries), lr, momentum, weight_decay,
                                                1 if nesterov else 0), "sgd_step")
 
+    def copy(self, copies) -> None:
+        """copies: (dst storage, dst offset bytes, src storage, src offset
+        bytes, nbytes); one unit of work (Backend::copy_device_to_device)."""
+        cs = (_lib.Copy * len(copies))()
+        if _KEEP is not None:
+            _KEEP.extend(x for c in copies for x in (c[0], c[2]))
+        for d, (dst, doff, src, soff, nbytes) in zip(cs, copies):
+            d.dst, d.src, d.nbytes = dst.ptr + doff, src.ptr + soff, nbytes
+        _lib.check(self.hip.lib.vkhip_copy_device_to_device(cs, len(copies)),
+                   "copy_device_to_device")
+
     def synchronize(self) -> None:
         self.hip.synchronize()
 
 
 _DEFAULT_BACKEND = None
+
+# While a CapturedStep records, every device buffer its calls touch is kept
+# here (see CapturedStep): the replay addresses them by pointer.
+_KEEP: list | None = None
 
 
 def default_backend():
@@ -769,21 +789,137 @@ def realize(tensors: Iterable[Tensor]) -> None:
                  *(_tensor_fields(src[2]) if ns > 2 else _NO_TENSOR),
                  node.params or b"")
         arr = (_lib.NodeDesc * len(nodes)).from_buffer(buf)
+        if _KEEP is not None:
+            _KEEP.extend(x.storage for node in nodes for x in (node, *node.src) if x is not None)
         backends[key].compute(arr, len(nodes))
         for node in nodes:
             node.computed = True
 
 
 def assign(params: Sequence[Tensor], values: Sequence[Tensor]) -> None:
-    """Rebind each parameter to its new value's storage (reference
-    python/vkml/__init__.py assign, which becomes copy_device_to_device)."""
+    """Copy each value into its parameter's storage, as one unit of work
+    (reference python/vkml/__init__.py:153-165, which becomes one
+    copy_device_to_device over the pairs). Every alias of a parameter (a
+    detach() or view taken earlier) then sees the new values, as it does in
+    the reference and under the fused SGD step, which updates in place. A
+    parameter without bound contiguous storage of its own is bound to the
+    value's storage instead."""
+    params, values = list(params), list(values)
+    if len(params) != len(values):
+        raise ValueError(f"assign: {len(params)} destinations but {len(values)} sources")
     realize(values)
+    copies = {}
     for p, v in zip(params, values):
-        p.node.storage = v.node.storage
-        p.node.offset = v.node.offset
-        p.node.strides = v.node.strides
-        p.node.rec = None
-        p.node.computed = True
+        if p.shape != v.shape or p.dtype != v.dtype:
+            raise ValueError(f"assign: {v.shape} {v.dtype} into {p.shape} {p.dtype}")
+        pn, vn = p.node, v.node
+        if (pn.storage is not None and pn.computed and pn.is_contiguous() and vn.is_contiguous()
+                and pn.backend is vn.backend and pn.storage is not vn.storage):
+            nbytes = _numel(pn.shape) * pn.itemsize
+            if nbytes:
+                copies.setdefault(id(pn.backend), (pn.backend, []))[1].append(
+                    (pn.storage, pn.offset * pn.itemsize, vn.storage, vn.offset * vn.itemsize,
+                     nbytes))
+            continue
+        pn.storage = vn.storage
+        pn.offset = vn.offset
+        pn.strides = vn.strides
+        pn.rec = None
+        pn.computed = True
+    for backend, pairs in copies.values():
+        backend.copy(pairs)
+
+
+class CapturedStep:
+    """A step (forward, backward, optimiser) recorded once and replayed.
+
+    The Python host core costs several microseconds per node to build, order
+    and pack a graph, which at the BASELINE training shapes is more than the
+    device work of a step (reference docs/SMALL-STEP-LATENCY.md:44-51 measures
+    the same gap for its own host). When a step's graph repeats, only its
+    inputs change: `CapturedStep(fn, *example_inputs)` runs `fn` once on device
+    tensors holding the example inputs while the backend records every
+    compute, SGD and copy call it makes (vkhip_program_begin/end), and each
+    later `step(*arrays)` uploads the arrays into those same input tensors,
+    replays the recorded calls from C (`vkhip_program_run`) and downloads
+    `fn`'s outputs. With graph=True the replay is captured into a HIP graph on
+    its first run and launched as one unit afterwards.
+
+    Contract (that of any recorded replay): `fn` builds the same graph every
+    call (same shapes and control flow, nothing decided from device values,
+    step-varying data only through its arguments); hyper-parameters are those
+    of the recording (an optimiser's lr and momentum included); the recording
+    step is a real step (it updates the parameters) and every replay continues
+    from the state the previous one left. Every device buffer the recorded
+    calls touch is held by this object until `close()`, so replays never write
+    into memory handed out elsewhere. The recording returns what the eager
+    step would; replays return the same bits an eager step would (tested).
+    """
+
+    def __init__(self, fn, *example_inputs, graph: bool = False, backend=None):
+        global _KEEP
+        from .device import backend as hip_backend
+
+        self.backend = backend or default_backend()
+        if not isinstance(self.backend, DeviceBackend):
+            raise TypeError("CapturedStep replays device work: it needs the HIP device backend")
+        self.lib = hip_backend().lib
+        self.graph = bool(graph)
+        self.inputs = [Tensor.from_numpy(np.asarray(a), backend=self.backend) for a in example_inputs]
+        self._program = None
+        if _KEEP is not None:
+            raise RuntimeError("CapturedStep: another step is being recorded")
+        keep: list = [t.node.storage for t in self.inputs]
+        _KEEP = keep
+        try:
+            _lib.check(self.lib.vkhip_program_begin(), "program_begin")
+            try:
+                out = fn(*self.inputs)
+                out = list(out) if isinstance(out, (tuple, list)) else [out]
+                self.outputs = [t if t.node.is_contiguous() else t.contiguous() for t in out]
+                realize(self.outputs)
+            finally:
+                prog = ctypes.c_void_p()
+                code = self.lib.vkhip_program_end(ctypes.byref(prog))
+                self._program = prog.value
+            _lib.check(code, "program_end")
+        finally:
+            _KEEP = None
+        keep.extend(t.node.storage for t in self.outputs)
+        self._keep = keep
+        self.first = [t.numpy() for t in self.outputs]
+
+    def info(self) -> dict:
+        calls, nodes, has_graph = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int()
+        _lib.check(self.lib.vkhip_program_info(self._program, ctypes.byref(calls), ctypes.byref(nodes),
+                                               ctypes.byref(has_graph)), "program_info")
+        return {"calls": calls.value, "nodes": nodes.value, "graph": bool(has_graph.value)}
+
+    def __call__(self, *arrays) -> list:
+        if self._program is None:
+            raise RuntimeError("CapturedStep: closed")
+        if len(arrays) != len(self.inputs):
+            raise ValueError(f"CapturedStep: {len(arrays)} inputs, recorded with {len(self.inputs)}")
+        for t, a in zip(self.inputs, arrays):
+            a = np.asarray(a)
+            if a.shape != t.shape or a.dtype != t.dtype:
+                raise ValueError(f"CapturedStep: input {a.shape} {a.dtype}, recorded {t.shape} {t.dtype}")
+            host = a.view(np.uint8) if a.dtype == np.bool_ else a
+            self.backend.upload(t.node.storage, t.node.offset * t.node.itemsize, host)
+        _lib.check(self.lib.vkhip_program_run(self._program, 1 if self.graph else 0), "program_run")
+        return [t.numpy() for t in self.outputs]
+
+    def close(self) -> None:
+        if self._program is not None:
+            _lib.check(self.lib.vkhip_program_destroy(self._program), "program_destroy")
+            self._program = None
+            self._keep = []
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter teardown
+            pass
 
 
 # ---------------------------------------------------------------------------
