@@ -270,6 +270,21 @@ int vkhip_gemm(const float* a, const vkhip_operand* a_desc,
                const float* b, const vkhip_operand* b_desc,
                float* c, const vkhip_gemm_opts* opts);
 
+/* vkhip_gemm that allocates nothing. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, plan, kernels and bits as vkhip_gemm; the split-K partials go to
+ * a fixed per-device scratch array of VKHIP_GEMM_NOALLOC_SCRATCH_BYTES that
+ * the library holds until the process ends, instead of the workspace
+ * vkhip_gemm grows. A product whose planned split needs more than that is
+ * refused with VKHIP_ERR_INVALID (nothing is launched). Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race on it. No profile record is taken for these calls. */
+#define VKHIP_GEMM_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)
+int vkhip_gemm_noalloc(const float* a, const vkhip_operand* a_desc,
+                       const float* b, const vkhip_operand* b_desc,
+                       float* c, const vkhip_gemm_opts* opts);
+
 /* The split-K plan the AUTO path would use for this problem
  * (reference plan_split_k, vulkan_backend.cpp:596-647). Writes splits (1 =
  * no split) and chunk (K-tiles per partition, a power of two). */

@@ -118,6 +118,8 @@ SIGNATURES = {
     "vkhip_compute": (c_int, [POINTER(NodeDesc), c_size_t]),
     "vkhip_gemm": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand), c_void_p,
                            POINTER(GemmOpts)]),
+    "vkhip_gemm_noalloc": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand),
+                                   c_void_p, POINTER(GemmOpts)]),
     "vkhip_program_begin": (c_int, []),
     "vkhip_program_end": (c_int, [POINTER(c_void_p)]),
     "vkhip_program_run": (c_int, [c_void_p, c_int]),

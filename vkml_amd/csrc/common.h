@@ -34,6 +34,9 @@ struct Context {
     int ws_pins = 0;               // captured graphs holding the workspace blocks
     void* ws_retired[64] = {};     // blocks replaced while pinned, freed at the last unpin
     int ws_retired_count = 0;
+    // Device address of this device's fixed scratch array (runtime.hip), from
+    // hipGetSymbolAddress at init; null if it could not be resolved.
+    float* scratch = nullptr;
     // GEMM kernel selection for MATMUL nodes, from VKHIP_GEMM_KERNEL at init
     // ("exact" | "mfma" | unset/"auto"), as the reference's VKML_GEMM_KERNEL
     // selects its GEMM for every matmul in the process (vulkan_backend.cpp:2158-2172).
@@ -63,8 +66,15 @@ void program_note_copy(const vkhip_copy* copies, size_t n);
 // Per-unit event timing is on (observe.hip).
 bool profiling_on();
 
+// A caller-fixed split-K workspace (the allocation-free GEMM entry point's
+// per-device scratch array): gemm() uses it instead of growing workspace()
+// and refuses a plan that needs more than `bytes`.
+struct FixedScratch {
+    float* ptr;
+    size_t bytes;
+};
 int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd, float* c,
-         const vkhip_gemm_opts* opts);
+         const vkhip_gemm_opts* opts, const FixedScratch* scratch = nullptr);
 
 // Decision facts and units of work (observe.hip). A unit is a node of
 // vkhip_compute or one per-op entry call; decisions published inside it carry

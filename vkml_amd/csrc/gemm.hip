@@ -1332,7 +1332,7 @@ static int launch_gemm_exact(const float* a, const vkhip_operand& ad, const floa
 }
 
 int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd,
-         float* c, const vkhip_gemm_opts* opts) {
+         float* c, const vkhip_gemm_opts* opts, const FixedScratch* scratch) {
     const uint32_t b0 = ad.ne[0] > bd.ne[0] ? ad.ne[0] : bd.ne[0];
     const uint32_t b1 = ad.ne[1] > bd.ne[1] ? ad.ne[1] : bd.ne[1];
     const uint32_t m = ad.ne[2], k = ad.ne[3], n = bd.ne[3];
@@ -1426,7 +1426,15 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     if (splits > 1) {
         float* ws = nullptr;
         const size_t need = out_elems * splits * sizeof(float);
-        {
+        if (scratch) {
+            if (need > scratch->bytes)
+                return fail(VKHIP_ERR_INVALID,
+                            "matmul %ux%ux%u (batch %llu) splits K into %u partitions whose partials "
+                            "need %zu bytes; the allocation-free entry point's scratch holds %zu",
+                            m, n, k, static_cast<unsigned long long>(batch), splits, need,
+                            scratch->bytes);
+            ws = scratch->ptr;
+        } else {
             int st = workspace(need, &ws);
             if (st != VKHIP_OK) return st;
         }
@@ -1787,6 +1795,19 @@ extern "C" int vkhip_gemm(const float* a, const vkhip_operand* a_desc, const flo
     vkhip::Unit unit("matmul");
     if (!a_desc || !b_desc) return vkhip::fail(VKHIP_ERR_INVALID, "gemm: null descriptor");
     return vkhip::gemm(a, *a_desc, b, *b_desc, c, opts);
+}
+
+extern "C" int vkhip_gemm_noalloc(const float* a, const vkhip_operand* a_desc, const float* b,
+                                  const vkhip_operand* b_desc, float* c,
+                                  const vkhip_gemm_opts* opts) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!a_desc || !b_desc) return vkhip::fail(VKHIP_ERR_INVALID, "gemm_noalloc: null descriptor");
+    if (!vkhip::ctx().scratch)
+        return vkhip::fail(VKHIP_ERR_UNSUPPORTED, "gemm_noalloc: no scratch array on device %d",
+                           vkhip::ctx().device);
+    const vkhip::FixedScratch fixed{vkhip::ctx().scratch, VKHIP_GEMM_NOALLOC_SCRATCH_BYTES};
+    return vkhip::gemm(a, *a_desc, b, *b_desc, c, opts, &fixed);
 }
 
 extern "C" int vkhip_gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,

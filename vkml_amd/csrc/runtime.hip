@@ -58,6 +58,30 @@ Context& ctx() {
 
 static std::mutex g_mu;  // guards init/shutdown/workspace (reference allocation-map mutex)
 
+// ---- fixed scratch of the allocation-free GEMM entry point ----------------------
+// vkhip_gemm_noalloc keeps its split-K partials here instead of in the grown
+// workspace. Every GPU the library runs on holds its own copy of this array
+// until the process ends, at its own address. In host code `scratch` is a
+// host-side stand-in, not a device address: its device address comes from
+// hipGetSymbolAddress, once per device at vkhip_init with that device current,
+// and only that address is handed to kernels. Nothing here needs to start at
+// zero: every partition writes its whole slice before the fold reads it.
+constexpr size_t kScratchBytes = VKHIP_GEMM_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxScratchDevices = 64;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+static float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+static int resolve_scratch(int device) {
+    if (device < 0 || device >= kMaxScratchDevices) return VKHIP_OK;  // entry point unavailable
+    if (g_scratch_ptr[device]) return VKHIP_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return fail(VKHIP_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d failed: %s", device,
+                    hipGetErrorString(e));
+    g_scratch_ptr[device] = static_cast<float*>(p);
+    return VKHIP_OK;
+}
 static int release_stage_slots();  // pinned upload/download slots, below
 
 int require_ready() {
@@ -645,9 +669,14 @@ extern "C" int vkhip_init(int device) {
     VKHIP_HIP(hipDeviceGetDefaultMemPool(&pool, device));
     uint64_t keep = ~0ull;
     VKHIP_HIP(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep));
+    {
+        const int rc = vkhip::resolve_scratch(device);
+        if (rc != VKHIP_OK) return rc;
+    }
     VKHIP_HIP(hipStreamCreateWithFlags(&c.own_stream, hipStreamNonBlocking));
     c.stream = c.own_stream;
     c.device = device;
+    c.scratch = device < vkhip::kMaxScratchDevices ? vkhip::g_scratch_ptr[device] : nullptr;
     c.node_gemm_kernel = VKHIP_GEMM_AUTO;
     if (const char* sel = getenv("VKHIP_GEMM_KERNEL")) {
         if (strcmp(sel, "exact") == 0) c.node_gemm_kernel = VKHIP_GEMM_EXACT;
@@ -695,6 +724,7 @@ extern "C" int vkhip_shutdown(void) {
     VKHIP_HIP(hipStreamDestroy(c.own_stream));
     c.own_stream = nullptr;
     c.stream = nullptr;
+    c.scratch = nullptr;
     c.ready = false;
     return VKHIP_OK;
 }
