@@ -438,6 +438,27 @@ int vkhip_profile_read(vkhip_profile_record* out, size_t capacity, size_t* count
                        uint64_t* dropped);
 
 /* ======================================================================== */
+/* Numerics mode                                                              */
+/* ======================================================================== */
+/* FAST (default): matrix-core GEMMs and convolutions, hardware-assisted
+ * exp/log; within the north star's tolerances of the CPU oracle (GEMM and
+ * softmax 1e-5*sqrt(K)), bit-exact everywhere else. EXACT: every node the
+ * CPU oracle's bits: GEMMs (AUTO selection) and convolutions on the exact arm
+ * (VKHIP_GEMM_EXACT's arithmetic, convolution columns gathered from the
+ * image), softmax / log-softmax / cross-entropy / exp / log with the oracle's
+ * exp and log methods (vkhip_exact_math) and true division. The role of the
+ * reference's precise comparison arms (gemm_naive.comp:56-101 with
+ * VKML_GEMM_KERNEL=naive, vulkan_backend.cpp:2158-2172), extended to the
+ * transcendentals so whole training runs can be compared bit for bit. Applies
+ * to work enqueued after the call; VKHIP_NUMERICS=exact sets it at init. */
+enum vkhip_numerics {
+    VKHIP_NUMERICS_FAST = 0,
+    VKHIP_NUMERICS_EXACT = 1
+};
+int vkhip_set_numerics(int mode);
+int vkhip_get_numerics(void);
+
+/* ======================================================================== */
 /* Recorded programs: replay of a step whose graph repeats                   */
 /* ======================================================================== */
 /* No single counterpart in the reference; it is the "record once, re-submit"
@@ -476,6 +497,12 @@ int vkhip_program_info(const vkhip_program* program, size_t* calls, size_t* node
  * adjacent-first reproduces the oracle's additions. */
 int vkhip_pairwise_leaf(uint32_t n, uint32_t leaf, uint32_t* out_depth, uint32_t* out_begin,
                         uint32_t* out_end);
+/* The exact numerics mode's exp (log_mode 0) or log (log_mode 1) of n host
+ * floats, evaluated on the host by the same source the device kernels use:
+ * double-precision Cody-Waite/Taylor exp and atanh-series log, bit for bit
+ * the CPU oracle's (which fixes the reference's unpinned std::exp/std::log,
+ * kernels_reduce.cpp:227-243, to these methods). */
+int vkhip_exact_math(const float* host_x, float* host_y, size_t n, int log_mode);
 /* n / d as the device kernels compute it (multiply-high by a precomputed
  * magic number; d = 0 returns 0xffffffff). */
 uint32_t vkhip_fast_divide(uint32_t n, uint32_t d);

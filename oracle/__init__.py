@@ -70,6 +70,7 @@ def load():
                                           c_uint32, P(Unfold), c_int]),
         "or_split_k_fold": (None, [c_void_p, c_void_p, c_uint64, c_uint32]),
         "or_compute": (c_int, [c_void_p, ctypes.c_size_t, c_int]),
+        "or_exp_vec": (None, [c_void_p, c_void_p, c_int64, c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -263,6 +264,22 @@ def max_pool2d_backward(grad, x, kernel, stride=None, padding=0, threads=None) -
     load().or_max_pool2d_backward(_ptr(grad), _ptr(x), _ptr(out), n * c, grad.shape[2],
                                   grad.shape[3], byref(u), threads or default_threads())
     return out
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """The oracle's exp on float32 values (the method in vkml_oracle.c or_expf)."""
+    x = np.ascontiguousarray(_f32(x))
+    y = np.empty_like(x)
+    load().or_exp_vec(_ptr(x), _ptr(y), x.size, 0)
+    return y
+
+
+def logf(x: np.ndarray) -> np.ndarray:
+    """The oracle's log on float32 values (vkml_oracle.c or_logf)."""
+    x = np.ascontiguousarray(_f32(x))
+    y = np.empty_like(x)
+    load().or_exp_vec(_ptr(x), _ptr(y), x.size, 1)
+    return y
 
 
 def split_k_fold(ws: np.ndarray, splits: int) -> np.ndarray:

@@ -49,6 +49,71 @@ static float pairwise(const float* v, int64_t begin, int64_t end) {
 
 float or_pairwise_sum(const float* v, int64_t n) { return pairwise(v, 0, n); }
 
+/* ------------------------------------------------------------------------ */
+/* exp and log. The reference calls std::exp / std::log on float
+ * (kernels_reduce.cpp:227-243), i.e. the platform libm, whose results the
+ * reference does not pin (glibc's expf/logf are within 0.502 ulp and miss the
+ * correctly rounded value for ~1e-4 / ~1e-3 of inputs). The oracle fixes
+ * them to named methods evaluated in IEEE double, so the device's exact
+ * numerics mode can reproduce them bit for bit:
+ *   exp: Cody-Waite reduction x = k ln2 + r, |r| <= ln2/2 (ln2 as two
+ *        doubles, fused multiply-adds), Taylor polynomial of e^r to degree 13
+ *        (Horner), times 2^k;
+ *   log: x = m 2^e, m in [sqrt(1/2), sqrt(2)), s = (m-1)/(m+1),
+ *        log m = 2 atanh s = 2s(1 + s^2/3 + ... + s^24/25), plus e ln2.
+ * Each is the correctly rounded float except within ~2^-27 ulp of a rounding
+ * midpoint (pinned against mpmath in tests/test_oracle.py). */
+/* ------------------------------------------------------------------------ */
+float or_logf(float xf);
+
+float or_expf(float xf) {
+    if (xf != xf) return xf + xf;
+    if (xf > 89.0f) return INFINITY;
+    if (xf < -104.0f) return 0.0f;
+    const double x = xf;
+    const double kd = rint(x * 0x1.71547652b82fep+0);
+    double r = fma(-kd, 0x1.62e42fefa39efp-1, x);
+    r = fma(-kd, 0x1.abc9e3b39803fp-56, r);
+    static const double c[] = {0x1.6124613a86d09p-33, 0x1.1eed8eff8d898p-29, 0x1.ae64567f544e4p-26,
+                               0x1.27e4fb7789f5cp-22, 0x1.71de3a556c734p-19, 0x1.a01a01a01a01ap-16,
+                               0x1.a01a01a01a01ap-13, 0x1.6c16c16c16c17p-10, 0x1.1111111111111p-7,
+                               0x1.5555555555555p-5,  0x1.5555555555555p-3,  0x1.0000000000000p-1,
+                               1.0, 1.0};
+    double p = c[0];
+    for (int i = 1; i < 14; ++i) p = fma(p, r, c[i]);
+    return (float)ldexp(p, (int)kd);
+}
+
+void or_exp_vec(const float* x, float* y, int64_t n, int log_mode) {
+    for (int64_t i = 0; i < n; ++i) y[i] = log_mode ? or_logf(x[i]) : or_expf(x[i]);
+}
+
+float or_logf(float xf) {
+    if (xf != xf) return xf + xf;
+    if (xf < 0.0f) return NAN;
+    if (xf == 0.0f) return -INFINITY;
+    if (xf == INFINITY) return xf;
+    int e = 0;
+    double m = frexp((double)xf, &e);
+    if (m < 0x1.6a09e667f3bcdp-1) {
+        m = m + m;
+        e -= 1;
+    }
+    const double f = m - 1.0;
+    const double s = f / (2.0 + f);
+    const double z = s * s;
+    static const double c[] = {0x1.47ae147ae147bp-5, 0x1.642c8590b2164p-5, 0x1.8618618618618p-5,
+                               0x1.af286bca1af28p-5, 0x1.e1e1e1e1e1e1ep-5, 0x1.1111111111111p-4,
+                               0x1.3b13b13b13b14p-4, 0x1.745d1745d1746p-4, 0x1.c71c71c71c71cp-4,
+                               0x1.2492492492492p-3, 0x1.999999999999ap-3, 0x1.5555555555555p-2};
+    double w = c[0];
+    for (int i = 1; i < 12; ++i) w = fma(w, z, c[i]);
+    const double t = s + s;
+    const double lm = fma(t * z, w, t);
+    const double ed = (double)e;
+    return (float)fma(ed, 0x1.62e42fefa39efp-1, fma(ed, 0x1.abc9e3b39803fp-56, lm));
+}
+
 /* Offset (elements) of the `linear`-th element in row-major order of a
  * rank-4 descriptor: reference linear_to_offset, src/backend/cpu/iterate.h:33-42. */
 static int64_t lin_off(int64_t linear, const uint32_t ne[4], const int64_t nb[4]) {
@@ -206,12 +271,12 @@ void or_softmax(const float* in, const vkhip_operand* d, float* out, int axis, i
                 const float v = base[lin_off(k, rne, rnb)];
                 peak = (peak < v) ? v : peak; /* std::max(peak, v) */
             }
-            for (int64_t k = 0; k < n_axis; ++k) ex[k] = expf(base[lin_off(k, rne, rnb)] - peak);
+            for (int64_t k = 0; k < n_axis; ++k) ex[k] = or_expf(base[lin_off(k, rne, rnb)] - peak);
             const float denom = pairwise(ex, 0, n_axis);
-            const float ld = logf(denom);
+            const float ld = or_logf(denom);
             for (int64_t k = 0; k < n_axis; ++k) {
                 const float shifted = base[lin_off(k, rne, rnb)] - peak;
-                obase[lin_off(k, orne, ornb)] = log_softmax ? shifted - ld : expf(shifted) / denom;
+                obase[lin_off(k, orne, ornb)] = log_softmax ? shifted - ld : or_expf(shifted) / denom;
             }
         }
         free(ex);
@@ -378,8 +443,8 @@ void or_split_k_fold(const float* ws, float* dst, uint64_t ne, uint32_t splits) 
 static float unary_f(int op, float x) {
     switch (op) {
         case VKHIP_OP_NEG: return -x;
-        case VKHIP_OP_EXP: return expf(x);
-        case VKHIP_OP_LOG: return logf(x);
+        case VKHIP_OP_EXP: return or_expf(x);
+        case VKHIP_OP_LOG: return or_logf(x);
         case VKHIP_OP_RELU: return x <= 0.0f ? 0.0f : x; /* NaN propagates, k_relu */
         case VKHIP_OP_CONTIGUOUS: return x;
         default: return NAN;
@@ -446,8 +511,8 @@ void or_cross_entropy(const float* x, int64_t row_stride, const int64_t* labels,
             const float* row = x + r * row_stride;
             float peak = -INFINITY;
             for (int64_t k = 0; k < c; ++k) peak = (peak < row[k]) ? row[k] : peak;
-            for (int64_t k = 0; k < c; ++k) buf[k] = expf(row[k] - peak);
-            const float ld = logf(pairwise(buf, 0, c));
+            for (int64_t k = 0; k < c; ++k) buf[k] = or_expf(row[k] - peak);
+            const float ld = or_logf(pairwise(buf, 0, c));
             for (int64_t k = 0; k < c; ++k) ls[k] = (row[k] - peak) - ld;
             const float label = (float)labels[r];
             if (!backward) {
@@ -457,7 +522,7 @@ void or_cross_entropy(const float* x, int64_t row_stride, const int64_t* labels,
                 const float ng = -g[r];
                 for (int64_t k = 0; k < c; ++k) buf[k] = ng * (label == (float)k ? 1.0f : 0.0f);
                 const float total = pairwise(buf, 0, c);
-                for (int64_t k = 0; k < c; ++k) out[r * c + k] = buf[k] - expf(ls[k]) * total;
+                for (int64_t k = 0; k < c; ++k) out[r * c + k] = buf[k] - or_expf(ls[k]) * total;
             }
         }
         free(buf);

@@ -373,3 +373,87 @@ def test_split_fold_non_power_of_two_chunks_break_identity():
         folded = O.split_k_fold(np.array(parts, np.float32), len(parts))
         mismatches += folded.tobytes() != O.split_k_fold(vals, 97).tobytes()
     assert mismatches > 15
+
+
+# ---- the oracle's exp and log (vkml_oracle.c or_expf / or_logf) ----
+
+def _cr_float(fn, xs):
+    """Correctly rounded float32 of fn over float32 inputs, from mpmath at 100
+    bits (the double rounding through float64 is below 2^-47 relative)."""
+    import mpmath
+
+    mpmath.mp.prec = 100
+    out = np.empty(len(xs), np.float32)
+    with np.errstate(over="ignore"):
+        for i, x in enumerate(xs):
+            out[i] = np.float32(float(fn(mpmath.mpf(float(x)))))
+    return out
+
+
+def _exp_inputs():
+    rng = np.random.default_rng(SEED + 101)
+    special = np.array([0.0, -0.0, 1.0, -1.0, 88.72283, 88.72284, 89.0, -87.33654, -87.3366,
+                        -100.0, -103.97, -103.98, -104.0, 1e-8, -1e-8, 0.5, -0.5, 0.34657359,
+                        -0.34657359, 0.34657362, 20.0, -20.0], np.float32)
+    return np.concatenate([special, rng.uniform(-104, 89, 3000).astype(np.float32),
+                           rng.uniform(-20, 0, 3000).astype(np.float32),
+                           rng.uniform(-1e-3, 1e-3, 500).astype(np.float32)])
+
+
+def _log_inputs():
+    rng = np.random.default_rng(SEED + 102)
+    special = np.array([1.0, 2.0, 0.5, np.float32(np.sqrt(0.5)), np.float32(np.sqrt(2.0)),
+                        1.0000001, 0.99999994, 1e-45, 1e-40, 1.1754944e-38, 3.4028235e38, 10.0,
+                        100.0, 4.6, 12800.0], np.float32)
+    return np.concatenate([special, np.exp(rng.uniform(-100, 88, 3000)).astype(np.float32),
+                           rng.uniform(0.5, 2.0, 3000).astype(np.float32),
+                           (1 + rng.uniform(-1e-4, 1e-4, 500)).astype(np.float32)])
+
+
+def test_oracle_exp_is_correctly_rounded():
+    """The oracle fixes the reference's unpinned std::exp (platform libm,
+    kernels_reduce.cpp:227-243) to a Cody-Waite + degree-13 Taylor method in
+    double: against mpmath it must be the correctly rounded float on every
+    sampled input, subnormal results and overflow to +inf included. A dropped
+    polynomial term, a wrong ln2 split or a bad reduction breaks this."""
+    import mpmath
+
+    x = _exp_inputs()
+    got = O.expf(x)
+    want = _cr_float(mpmath.exp, x)
+    bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} mismatches, e.g. x={x[bad[:3]]} got {got[bad[:3]]} want {want[bad[:3]]}"
+    assert np.isposinf(O.expf(np.array([89.5, np.inf], np.float32))).all()
+    assert (O.expf(np.array([-104.5, -np.inf], np.float32)) == 0).all()
+    assert np.isnan(O.expf(np.array([np.nan], np.float32))).all()
+
+
+def test_oracle_log_is_correctly_rounded():
+    import mpmath
+
+    x = _log_inputs()
+    got = O.logf(x)
+    want = _cr_float(mpmath.log, x)
+    bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} mismatches, e.g. x={x[bad[:3]]} got {got[bad[:3]]} want {want[bad[:3]]}"
+    sp = O.logf(np.array([0.0, -0.0, -1.0, np.inf, np.nan, 1.0], np.float32))
+    assert np.isneginf(sp[0]) and np.isneginf(sp[1]) and np.isnan(sp[2]) and np.isposinf(sp[3])
+    assert np.isnan(sp[4]) and sp[5] == 0.0 and not np.signbit(sp[5])
+
+
+def test_device_source_exp_log_match_the_oracle():
+    """libvkhip's exact-numerics exp/log (the source the device kernels use,
+    evaluated on the host through vkhip_exact_math) against the oracle's, bit
+    for bit, on a dense sweep of the softmax and log domains."""
+    from vkml_amd import _lib
+
+    lib = _lib.load()
+    rng = np.random.default_rng(SEED + 103)
+    for log_mode, x in ((0, np.concatenate([np.linspace(-104, 89, 400_001, dtype=np.float32),
+                                            rng.uniform(-30, 0, 400_000).astype(np.float32)])),
+                        (1, np.concatenate([np.exp(np.linspace(-103, 88, 400_001)).astype(np.float32),
+                                            rng.uniform(1e-3, 1e3, 400_000).astype(np.float32)]))):
+        y = np.empty_like(x)
+        assert lib.vkhip_exact_math(x.ctypes.data, y.ctypes.data, x.size, log_mode) == 0
+        want = O.logf(x) if log_mode else O.expf(x)
+        assert y.tobytes() == want.tobytes()

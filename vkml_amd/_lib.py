@@ -22,6 +22,8 @@ REDUCE_SUM, REDUCE_MEAN, REDUCE_MAX, REDUCE_MIN, REDUCE_ARGMAX, REDUCE_ARGMIN = 
 
 GEMM_AUTO, GEMM_MFMA, GEMM_GEMV, GEMM_EXACT = 0, 1, 2, 3
 
+NUMERICS_FAST, NUMERICS_EXACT = 0, 1
+
 # vkml::OpKind ordinals (include/vkml/graph/op.h:30-139) for the supported subset.
 OP = dict(
     FULL=2, ARANGE=3, CONTIGUOUS=11, CAST=12, ADD=14, SUB=15, MUL=16, SCALED_ADD=17, DIV=18,
@@ -120,6 +122,8 @@ SIGNATURES = {
                            POINTER(GemmOpts)]),
     "vkhip_gemm_noalloc": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand),
                                    c_void_p, POINTER(GemmOpts)]),
+    "vkhip_set_numerics": (c_int, [c_int]),
+    "vkhip_get_numerics": (c_int, []),
     "vkhip_program_begin": (c_int, []),
     "vkhip_program_end": (c_int, [POINTER(c_void_p)]),
     "vkhip_program_run": (c_int, [c_void_p, c_int]),
@@ -144,6 +148,7 @@ SIGNATURES = {
     "vkhip_event_record": (c_int, [c_void_p]),
     "vkhip_event_elapsed": (c_int, [c_void_p, c_void_p, POINTER(c_float)]),
     "vkhip_fast_divide": (c_uint32, [c_uint32, c_uint32]),
+    "vkhip_exact_math": (c_int, [c_void_p, c_void_p, c_size_t, c_int]),
     "vkhip_pairwise_leaf": (c_int, [c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_uint32),
                                     POINTER(c_uint32)]),
 }

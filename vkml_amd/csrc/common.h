@@ -41,6 +41,10 @@ struct Context {
     // ("exact" | "mfma" | unset/"auto"), as the reference's VKML_GEMM_KERNEL
     // selects its GEMM for every matmul in the process (vulkan_backend.cpp:2158-2172).
     int node_gemm_kernel = VKHIP_GEMM_AUTO;
+    // VKHIP_NUMERICS_EXACT (vkhip_set_numerics, or VKHIP_NUMERICS=exact at
+    // init): GEMMs and convolutions on the exact arm, the shared exp/log and
+    // true division in softmax, log-softmax, cross-entropy, exp and log.
+    int exact_math = 0;
 };
 
 Context& ctx();
@@ -302,6 +306,81 @@ __device__ __forceinline__ float staged_subtree_sum(const float* st, uint32_t n,
     for (int l = 0; l < 9; ++l)
         if ((1u << l) == per) v = stack[l];
     return v;
+}
+
+// ---- exp and log shared with the CPU oracle (the exact numerics mode) ---------
+// The reference's CPU softmax calls the platform libm (std::exp / std::log,
+// kernels_reduce.cpp:227-243), whose float results are not pinned (glibc's
+// expf and logf are within 0.502 ulp and differ from the correctly rounded
+// value for about 1e-4 / 1e-3 of inputs). In the exact numerics mode the
+// device and the oracle (oracle/vkml_oracle.c) evaluate both with the same
+// sequence of IEEE double operations, so they agree bit for bit by
+// construction, and each result is the correctly rounded float except when
+// exp(x) or log(x) lies within ~2^-27 ulp of a rounding midpoint:
+//   exp: Cody-Waite reduction x = k ln2 + r (|r| <= ln2/2, ln2 split in two
+//        doubles, fused multiply-adds), the Taylor polynomial of e^r to degree
+//        13 in Horner form (truncation below 2^-52), scaled by 2^k;
+//   log: x = m 2^e with m in [sqrt(1/2), sqrt(2)), s = (m - 1) / (m + 1)
+//        (m - 1 and m + 1 exact), log m = 2 atanh s = 2s (1 + s^2/3 + s^4/5
+//        + ... + s^24/25) (truncation below 2^-60), plus e ln2.
+// Results below 2^-150 are +0, above FLT_MAX +inf; log(0) = -inf, log of a
+// negative number or NaN is NaN.
+__host__ __device__ inline float exact_expf(float xf) {
+    if (xf != xf) return xf + xf;
+    if (xf > 89.0f) return __builtin_inff();
+    if (xf < -104.0f) return 0.0f;
+    const double x = xf;
+    const double kd = __builtin_rint(x * 0x1.71547652b82fep+0);
+    double r = __builtin_fma(-kd, 0x1.62e42fefa39efp-1, x);
+    r = __builtin_fma(-kd, 0x1.abc9e3b39803fp-56, r);
+    double p = 0x1.6124613a86d09p-33;
+    p = __builtin_fma(p, r, 0x1.1eed8eff8d898p-29);
+    p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);
+    p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);
+    p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);
+    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);
+    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);
+    p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);
+    p = __builtin_fma(p, r, 0x1.1111111111111p-7);
+    p = __builtin_fma(p, r, 0x1.5555555555555p-5);
+    p = __builtin_fma(p, r, 0x1.5555555555555p-3);
+    p = __builtin_fma(p, r, 0x1.0000000000000p-1);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    return static_cast<float>(__builtin_ldexp(p, static_cast<int>(kd)));
+}
+
+__host__ __device__ inline float exact_logf(float xf) {
+    if (xf != xf) return xf + xf;
+    if (xf < 0.0f) return __builtin_nanf("");
+    if (xf == 0.0f) return -__builtin_inff();
+    if (xf == __builtin_inff()) return xf;
+    int e = 0;
+    double m = __builtin_frexp(static_cast<double>(xf), &e);  // m in [0.5, 1), exact
+    if (m < 0x1.6a09e667f3bcdp-1) {
+        m = m + m;
+        e -= 1;
+    }
+    const double f = m - 1.0;  // exact: m has at most 24 significant bits
+    const double s = f / (2.0 + f);
+    const double z = s * s;
+    double w = 0x1.47ae147ae147bp-5;
+    w = __builtin_fma(w, z, 0x1.642c8590b2164p-5);
+    w = __builtin_fma(w, z, 0x1.8618618618618p-5);
+    w = __builtin_fma(w, z, 0x1.af286bca1af28p-5);
+    w = __builtin_fma(w, z, 0x1.e1e1e1e1e1e1ep-5);
+    w = __builtin_fma(w, z, 0x1.1111111111111p-4);
+    w = __builtin_fma(w, z, 0x1.3b13b13b13b14p-4);
+    w = __builtin_fma(w, z, 0x1.745d1745d1746p-4);
+    w = __builtin_fma(w, z, 0x1.c71c71c71c71cp-4);
+    w = __builtin_fma(w, z, 0x1.2492492492492p-3);
+    w = __builtin_fma(w, z, 0x1.999999999999ap-3);
+    w = __builtin_fma(w, z, 0x1.5555555555555p-2);
+    const double t = s + s;
+    const double lm = __builtin_fma(t * z, w, t);
+    const double ed = static_cast<double>(e);
+    const double y = __builtin_fma(ed, 0x1.62e42fefa39efp-1, __builtin_fma(ed, 0x1.abc9e3b39803fp-56, lm));
+    return static_cast<float>(y);
 }
 
 // ---- butterflies across a wave of 64 ----------------------------------------

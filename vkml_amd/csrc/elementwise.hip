@@ -40,6 +40,7 @@ struct EwArgs {
     uint32_t ne[4];
     FastDiv dv[3];  // by ne[3], ne[2], ne[1]
     int32_t wide;
+    int32_t exact;  // exact numerics mode: the oracle's exp and log
 };
 
 // Coordinates of output element i (computed once, shared by every source).
@@ -141,8 +142,16 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EwArgs a) {
                     store_out(a, i, load_f(a.s[0], i, k));
                 break;
             case VKHIP_OP_NEG: store_out(a, i, -load_f(a.s[0], i, k)); break;
-            case VKHIP_OP_EXP: store_out(a, i, expf(load_f(a.s[0], i, k))); break;
-            case VKHIP_OP_LOG: store_out(a, i, logf(load_f(a.s[0], i, k))); break;
+            case VKHIP_OP_EXP: {
+                const float x = load_f(a.s[0], i, k);
+                store_out(a, i, a.exact ? exact_expf(x) : expf(x));
+                break;
+            }
+            case VKHIP_OP_LOG: {
+                const float x = load_f(a.s[0], i, k);
+                store_out(a, i, a.exact ? exact_logf(x) : logf(x));
+                break;
+            }
             case VKHIP_OP_RELU: {
                 const float x = load_f(a.s[0], i, k);
                 store_out(a, i, x <= 0.0f ? 0.0f : x);
@@ -401,6 +410,7 @@ int launch_elementwise(const vkhip_node& nd) {
     EwArgs a{};
     a.op = op;
     a.out_dtype = nd.out.dtype;
+    a.exact = ctx().exact_math;
     a.out = nd.out.data;
     a.n = n;
     for (int s = 0; s < nd.n_src && s < 3; ++s) a.s[s] = make_src(nd.src[s]);

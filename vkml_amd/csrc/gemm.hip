@@ -1045,7 +1045,37 @@ __device__ __forceinline__ void exact_push(float (&stack)[kExactLevels], uint32_
     }
 }
 
-__global__ __launch_bounds__(256) void gemm_exact_kernel(GemmArgs g, int depth) {
+// Convolution operands of the exact arm: element (row, pos) of image n's
+// columns, row = c*kh*kw + ki*kw + kj, pos = oh*out_w + ow, is x[n, c, h, w]
+// with h = oh*stride_h - pad_h + ki*dil_h, w = ow*stride_w - pad_w + kj*dil_w,
+// or 0 outside the image (kernels_movement.cpp:438-483). B_IMG: B = the
+// columns (forward: k = row, col = pos); B_IMGT: B = their transpose (weight
+// gradient: k = pos, col = row).
+enum ExactB { B_PTR = 0, B_IMG = 1, B_IMGT = 2 };
+struct ExactImg {
+    const float* x;
+    int64_t sn, sc, sh, sw;  // image strides (elements)
+    int32_t H, W, kh, kw, out_w;
+    int32_t st_h, st_w, pad_h, pad_w, dil_h, dil_w;
+    uint32_t rows, positions;  // C*kh*kw, out_h*out_w
+    FastDiv by_kk, by_kw, by_ow;
+};
+
+__device__ __forceinline__ float exact_img_value(const ExactImg& im, const float* xn, uint32_t row,
+                                                 uint32_t pos) {
+    if (row >= im.rows || pos >= im.positions) return 0.0f;
+    const uint32_t c = im.by_kk.div(row);
+    const uint32_t rem = row - c * static_cast<uint32_t>(im.kh * im.kw);
+    const uint32_t ki = im.by_kw.div(rem), kj = rem - ki * static_cast<uint32_t>(im.kw);
+    const uint32_t oh = im.by_ow.div(pos), ow = pos - oh * static_cast<uint32_t>(im.out_w);
+    const int64_t h = static_cast<int64_t>(oh) * im.st_h - im.pad_h + static_cast<int64_t>(ki) * im.dil_h;
+    const int64_t w = static_cast<int64_t>(ow) * im.st_w - im.pad_w + static_cast<int64_t>(kj) * im.dil_w;
+    if (h < 0 || h >= im.H || w < 0 || w >= im.W) return 0.0f;
+    return xn[static_cast<int64_t>(c) * im.sc + h * im.sh + w * im.sw];
+}
+
+template <int BMODE>
+__global__ __launch_bounds__(256) void gemm_exact_kernel(GemmArgs g, int depth, ExactImg im) {
     __shared__ float As[kExactTile][kExactTile + 1];  // [row][k]
     __shared__ float Bs[kExactTile][kExactTile + 1];  // [k][col]
     const int tid = threadIdx.x;
@@ -1056,6 +1086,7 @@ __global__ __launch_bounds__(256) void gemm_exact_kernel(GemmArgs g, int depth) 
     const uint32_t i0 = bz / g.b1, i1 = bz - i0 * g.b1;
     const float* a = g.a + static_cast<int64_t>(i0) * g.sa0 + static_cast<int64_t>(i1) * g.sa1;
     const float* b = g.b + static_cast<int64_t>(i0) * g.sb0 + static_cast<int64_t>(i1) * g.sb1;
+    const float* xn = BMODE == B_PTR ? nullptr : im.x + static_cast<int64_t>(bz) * im.sn;
     float stack[4][kExactLevels];
 #pragma unroll
     for (int o = 0; o < 4; ++o)
@@ -1078,9 +1109,14 @@ __global__ __launch_bounds__(256) void gemm_exact_kernel(GemmArgs g, int depth) 
                                 : 0.0f;
                 const int bk = idx >> 5, c = idx & 31;
                 const uint32_t gc = col0 + c;
-                Bs[bk][c] = (gc < g.n && static_cast<uint32_t>(bk) < len)
-                                ? b[static_cast<int64_t>(kb + bk) * g.sbk + static_cast<int64_t>(gc) * g.sbn]
-                                : 0.0f;
+                const bool in = gc < g.n && static_cast<uint32_t>(bk) < len;
+                if constexpr (BMODE == B_PTR)
+                    Bs[bk][c] = in ? b[static_cast<int64_t>(kb + bk) * g.sbk + static_cast<int64_t>(gc) * g.sbn]
+                                   : 0.0f;
+                else if constexpr (BMODE == B_IMG)
+                    Bs[bk][c] = in ? exact_img_value(im, xn, kb + bk, gc) : 0.0f;
+                else
+                    Bs[bk][c] = in ? exact_img_value(im, xn, gc, kb + bk) : 0.0f;
             }
         }
         __syncthreads();
@@ -1298,6 +1334,26 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
     return VKHIP_OK;
 }
 
+static int launch_exact(GemmArgs& g, uint32_t batch, int bmode, const ExactImg& im) {
+    g.tiles_m = ceil_div(g.m, kExactTile);
+    g.tiles_n = ceil_div(g.n, kExactTile);
+    const uint64_t tiles = static_cast<uint64_t>(g.tiles_m) * g.tiles_n;
+    if (tiles > 0x7fffffffull)
+        return fail(VKHIP_ERR_UNSUPPORTED, "exact gemm: %llu output tiles",
+                    static_cast<unsigned long long>(tiles));
+    const int depth = pairwise_depth(g.k);
+    if (depth >= kExactLevels) return fail(VKHIP_ERR_UNSUPPORTED, "exact gemm: K=%u too deep", g.k);
+    const dim3 grid(static_cast<uint32_t>(tiles), 1, batch);
+    if (bmode == B_IMG)
+        hipLaunchKernelGGL(gemm_exact_kernel<B_IMG>, grid, dim3(256), 0, ctx().stream, g, depth, im);
+    else if (bmode == B_IMGT)
+        hipLaunchKernelGGL(gemm_exact_kernel<B_IMGT>, grid, dim3(256), 0, ctx().stream, g, depth, im);
+    else
+        hipLaunchKernelGGL(gemm_exact_kernel<B_PTR>, grid, dim3(256), 0, ctx().stream, g, depth, im);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
 static int launch_gemm_exact(const float* a, const vkhip_operand& ad, const float* b,
                              const vkhip_operand& bd, float* c, uint32_t batch, uint32_t b1,
                              uint32_t m, uint32_t n, uint32_t k) {
@@ -1317,17 +1373,39 @@ static int launch_gemm_exact(const float* a, const vkhip_operand& ad, const floa
     g.m = m;
     g.n = n;
     g.k = k;
-    g.tiles_m = ceil_div(m, kExactTile);
-    g.tiles_n = ceil_div(n, kExactTile);
-    const uint64_t tiles = static_cast<uint64_t>(g.tiles_m) * g.tiles_n;
-    if (tiles > 0x7fffffffull)
-        return fail(VKHIP_ERR_UNSUPPORTED, "exact gemm: %llu output tiles",
-                    static_cast<unsigned long long>(tiles));
-    const int depth = pairwise_depth(k);
-    if (depth >= kExactLevels) return fail(VKHIP_ERR_UNSUPPORTED, "exact gemm: K=%u too deep", k);
-    hipLaunchKernelGGL(gemm_exact_kernel, dim3(static_cast<uint32_t>(tiles), 1, batch), dim3(256), 0,
-                       ctx().stream, g, depth);
-    VKHIP_LAUNCH_CHECK();
+    return launch_exact(g, batch, B_PTR, ExactImg{});
+}
+
+// The exact arm's image geometry for a convolution (see ExactImg).
+static int exact_img(const vkhip_unfold& p, const float* x, const vkhip_operand& xd, ExactImg& im) {
+    const int64_t oh = (static_cast<int64_t>(p.image_h) + 2 * p.pad_h -
+                        (static_cast<int64_t>(p.dilation_h) * (p.kernel_h - 1) + 1)) / p.stride_h + 1;
+    const int64_t ow = (static_cast<int64_t>(p.image_w) + 2 * p.pad_w -
+                        (static_cast<int64_t>(p.dilation_w) * (p.kernel_w - 1) + 1)) / p.stride_w + 1;
+    const uint64_t rows = static_cast<uint64_t>(xd.ne[1]) * p.kernel_h * p.kernel_w;
+    if (oh <= 0 || ow <= 0 || rows > 0xffffffffull || static_cast<uint64_t>(oh) * ow > 0xffffffffull)
+        return fail(VKHIP_ERR_INVALID, "exact conv: invalid geometry");
+    im.x = x;
+    im.sn = xd.nb[0];
+    im.sc = xd.nb[1];
+    im.sh = xd.nb[2];
+    im.sw = xd.nb[3];
+    im.H = p.image_h;
+    im.W = p.image_w;
+    im.kh = p.kernel_h;
+    im.kw = p.kernel_w;
+    im.out_w = static_cast<int32_t>(ow);
+    im.st_h = p.stride_h;
+    im.st_w = p.stride_w;
+    im.pad_h = p.pad_h;
+    im.pad_w = p.pad_w;
+    im.dil_h = p.dilation_h;
+    im.dil_w = p.dilation_w;
+    im.rows = static_cast<uint32_t>(rows);
+    im.positions = static_cast<uint32_t>(oh * ow);
+    im.by_kk = FastDiv(static_cast<uint32_t>(p.kernel_h * p.kernel_w));
+    im.by_kw = FastDiv(static_cast<uint32_t>(p.kernel_w));
+    im.by_ow = FastDiv(static_cast<uint32_t>(ow));
     return VKHIP_OK;
 }
 
@@ -1346,7 +1424,8 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     if (batch == 0 || m == 0 || n == 0) return VKHIP_OK;
     if (batch > 65535) return fail(VKHIP_ERR_UNSUPPORTED, "matmul batch %llu > 65535",
                                    static_cast<unsigned long long>(batch));
-    const int kernel = opts ? opts->kernel : VKHIP_GEMM_AUTO;
+    int kernel = opts ? opts->kernel : VKHIP_GEMM_AUTO;
+    if (kernel == VKHIP_GEMM_AUTO && ctx().exact_math) kernel = VKHIP_GEMM_EXACT;
     const int32_t split_req = opts ? opts->split_k : 0;
     if (k == 0) {
         return launch_zero_f32(c, batch * m * n);
@@ -1646,6 +1725,28 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
     if (k == 0) {
         return launch_zero_f32(out, batch * m * n);
     }
+    if (ctx().exact_math) {
+        // the exact arm with the columns gathered from the image: the oracle's
+        // im2col + matmul, bit for bit
+        publish("matmul.kernel", "conv2d", "gemm_exact_implicit_im2col", "gemm_mfma_implicit_im2col",
+                "exact numerics mode", static_cast<int64_t>(k), static_cast<int64_t>(m) * n);
+        if (wd.nb[3] != 1 && k != 1)
+            return fail(VKHIP_ERR_UNSUPPORTED, "conv2d: the weight rows must be contiguous");
+        ExactImg im{};
+        const int geo = exact_img(p, x, xd, im);
+        if (geo != VKHIP_OK) return geo;
+        GemmArgs g{};
+        g.a = w;
+        g.b = x;
+        g.sam = wd.nb[2];
+        g.sak = 1;
+        g.b1 = static_cast<uint32_t>(batch);
+        g.m = m;
+        g.n = n;
+        g.k = k;
+        g.c = out;
+        return launch_exact(g, static_cast<uint32_t>(batch), B_IMG, im);
+    }
     uint32_t splits, chunk;
     TileChoice tile;
     gemm_plan(static_cast<uint32_t>(batch), m, n, k, 0, splits, chunk, tile);
@@ -1738,6 +1839,28 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
         return fail(VKHIP_ERR_UNSUPPORTED, "conv2d weight grad: extents too large");
     const uint32_t m = gd.ne[2], n = static_cast<uint32_t>(ck), k = static_cast<uint32_t>(L);
     if (batch == 0 || m == 0 || n == 0) return VKHIP_OK;
+    if (ctx().exact_math) {
+        // the exact arm with the transposed columns gathered from the image:
+        // the oracle's matmul(grad, im2col(x)^T), bit for bit
+        publish("matmul.kernel", "conv2d_weight_grad", "gemm_exact_implicit_im2col_t",
+                "gemm_mfma_implicit_im2col_t", "exact numerics mode", static_cast<int64_t>(k),
+                static_cast<int64_t>(m) * n);
+        ExactImg im{};
+        const int geo = exact_img(p, x, xd, im);
+        if (geo != VKHIP_OK) return geo;
+        GemmArgs g{};
+        g.a = gr;
+        g.b = x;
+        g.sa1 = gd.nb[1];
+        g.sam = gd.nb[2];
+        g.sak = gd.nb[3];
+        g.b1 = static_cast<uint32_t>(batch);
+        g.m = m;
+        g.n = n;
+        g.k = k;
+        g.c = out;
+        return launch_exact(g, static_cast<uint32_t>(batch), B_IMGT, im);
+    }
     uint32_t splits, chunk;
     TileChoice tile;
     gemm_plan(static_cast<uint32_t>(batch), m, n, k, 0, splits, chunk, tile);

@@ -345,7 +345,7 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
 // and its negation. Backward, given g = dL/d(out[r]): the reference autograd's
 // chain, neg (-g), sum and mul backward (gl = (-g) * onehot), log-softmax
 // backward gl - exp(ls) * pairwise_sum(gl) with the EXP node's expf.
-template <int E>
+template <int E, bool EXACT>
 __global__ __launch_bounds__(256) void cross_entropy_rows_kernel(
     const float* __restrict__ logits, int64_t row_stride, const int64_t* __restrict__ labels,
     const float* __restrict__ g_out, float* __restrict__ out, uint32_t rows, uint32_t n, int depth,
@@ -370,13 +370,13 @@ __global__ __launch_bounds__(256) void cross_entropy_rows_kernel(
 #pragma unroll
         for (int i = 0; i < E; ++i) {
             x[i] = x[i] - mx;
-            if (keep[i]) stage[stage_index(t + 64u * i)] = softmax_exp(x[i]);
+            if (keep[i]) stage[stage_index(t + 64u * i)] = EXACT ? exact_expf(x[i]) : softmax_exp(x[i]);
         }
         wave_lds_fence();
         float v = leaf_e > leaf_b ? staged_leaf_sum(stage, leaf_b, leaf_e) : 0.0f;
         const float denom = wave_sum_butterfly(v);
         wave_lds_fence();
-        const float ld = logf(denom);
+        const float ld = EXACT ? exact_logf(denom) : logf(denom);
         const float label = static_cast<float>(labels[row]);
 #pragma unroll
         for (int i = 0; i < E; ++i) x[i] = x[i] - ld;  // log-softmax
@@ -409,7 +409,7 @@ __global__ __launch_bounds__(256) void cross_entropy_rows_kernel(
 #pragma unroll
             for (int i = 0; i < E; ++i) {
                 const uint32_t e = static_cast<uint32_t>(t) + 64u * i;
-                if (keep[i]) ds[e] = __fsub_rn(gl[i], __fmul_rn(expf(x[i]), total));
+                if (keep[i]) ds[e] = __fsub_rn(gl[i], __fmul_rn(EXACT ? exact_expf(x[i]) : expf(x[i]), total));
             }
         }
     }
@@ -428,10 +428,11 @@ int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t*
     const uint32_t blocks = want < cus * 4 ? want : cus * 4;
     void (*fn)(const float*, int64_t, const int64_t*, const float*, float*, uint32_t, uint32_t, int,
                uint32_t, int);
-    if (n <= 64) fn = cross_entropy_rows_kernel<1>;
-    else if (n <= 256) fn = cross_entropy_rows_kernel<4>;
-    else if (n <= 1024) fn = cross_entropy_rows_kernel<16>;
-    else fn = cross_entropy_rows_kernel<32>;
+    const bool ex = ctx().exact_math != 0;
+    if (n <= 64) fn = ex ? cross_entropy_rows_kernel<1, true> : cross_entropy_rows_kernel<1, false>;
+    else if (n <= 256) fn = ex ? cross_entropy_rows_kernel<4, true> : cross_entropy_rows_kernel<4, false>;
+    else if (n <= 1024) fn = ex ? cross_entropy_rows_kernel<16, true> : cross_entropy_rows_kernel<16, false>;
+    else fn = ex ? cross_entropy_rows_kernel<32, true> : cross_entropy_rows_kernel<32, false>;
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, ctx().stream, logits, row_stride, labels,
                        g_out, out, rows, n, depth, ss, backward);
     VKHIP_LAUNCH_CHECK();
@@ -1383,6 +1384,7 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
 
 // ---- softmax host side ------------------------------------------------------------
 
+template <bool EXACT>
 __global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restrict__ src, Op4 kept,
                                                            Reader rd, Op4 okept, Reader ord,
                                                            uint64_t n_out, uint32_t n, int depth,
@@ -1401,7 +1403,10 @@ __global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restri
         uint32_t b, e;
         pairwise_leaf(n, depth, j, b, e);
         float s = 0.0f;
-        for (uint32_t q = b; q < e; ++q) s = s + softmax_exp(base[rd.off(q)] - peak);
+        for (uint32_t q = b; q < e; ++q) {
+            const float sh = base[rd.off(q)] - peak;
+            s = s + (EXACT ? exact_expf(sh) : softmax_exp(sh));
+        }
         bool carry = true;
 #pragma unroll
         for (int l = 0; l < kTallLevels; ++l) {
@@ -1419,10 +1424,10 @@ __global__ __launch_bounds__(256) void softmax_tall_kernel(const float* __restri
 #pragma unroll
     for (int l = 0; l < kTallLevels; ++l)
         if (l == depth) denom = stack[l];
-    const float ld = logf(denom);
+    const float ld = EXACT ? exact_logf(denom) : logf(denom);
     for (uint32_t i = 0; i < n; ++i) {
         const float sh = base[rd.off(i)] - peak;
-        obase[ord.off(i)] = log_mode ? sh - ld : softmax_exp(sh) / denom;
+        obase[ord.off(i)] = log_mode ? sh - ld : (EXACT ? exact_expf(sh) : softmax_exp(sh)) / denom;
     }
 }
 
@@ -1616,6 +1621,27 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
     const uint32_t rows = static_cast<uint32_t>(n_out64);
     hipStream_t st = ctx().stream;
     const int depth = pairwise_depth(n);
+    if (ctx().exact_math) {
+        // Exact numerics: one thread per row for every layout, the oracle's
+        // sequence (peak, the pairwise sum of exp over the row, log of it or
+        // a true division) with the oracle's exp and log.
+        publish("softmax.structure", log_mode ? "log_softmax" : "softmax", "softmax_exact_lane_per_row",
+                "softmax_wave_per_row", "exact numerics mode", n, rows);
+        vkhip_operand od;
+        int64_t s = 1;
+        for (int i = 3; i >= 0; --i) {
+            od.ne[i] = d.ne[i];
+            od.nb[i] = s;
+            s *= d.ne[i];
+        }
+        Op4 okept, ored;
+        split_axes(od, 1u << axis, okept, ored);
+        hipLaunchKernelGGL(softmax_tall_kernel<true>, dim3(ceil_div(rows, 256)), dim3(256), 0, st, src,
+                           kept, single_reader(d.nb[axis]), okept, single_reader(od.nb[axis]), n_out64,
+                           n, depth, log_mode, dst);
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
     // Fast path: softmax over the innermost, unit-stride axis, rows evenly spaced.
     int64_t row_stride = 0;
     bool rows_regular = true;
@@ -1676,8 +1702,8 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
     split_axes(od, 1u << axis, okept, ored);
     const Reader rd = single_reader(d.nb[axis]);
     const Reader ord = single_reader(od.nb[axis]);
-    hipLaunchKernelGGL(softmax_tall_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, st, src, kept,
-                       rd, okept, ord, n_out64, n, depth, log_mode, dst);
+    hipLaunchKernelGGL(softmax_tall_kernel<false>, dim3(ceil_div(rows, 256)), dim3(256), 0, st, src,
+                       kept, rd, okept, ord, n_out64, n, depth, log_mode, dst);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }

@@ -678,6 +678,9 @@ extern "C" int vkhip_init(int device) {
     c.device = device;
     c.scratch = device < vkhip::kMaxScratchDevices ? vkhip::g_scratch_ptr[device] : nullptr;
     c.node_gemm_kernel = VKHIP_GEMM_AUTO;
+    c.exact_math = 0;
+    if (const char* sel = getenv("VKHIP_NUMERICS"))
+        if (strcmp(sel, "exact") == 0) c.exact_math = 1;
     if (const char* sel = getenv("VKHIP_GEMM_KERNEL")) {
         if (strcmp(sel, "exact") == 0) c.node_gemm_kernel = VKHIP_GEMM_EXACT;
         else if (strcmp(sel, "mfma") == 0) c.node_gemm_kernel = VKHIP_GEMM_MFMA;
@@ -750,6 +753,19 @@ extern "C" int vkhip_set_stream(void* stream) {
 }
 
 extern "C" void* vkhip_get_stream(void) { return ctx().stream; }
+
+extern "C" int vkhip_set_numerics(int mode) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (mode != VKHIP_NUMERICS_FAST && mode != VKHIP_NUMERICS_EXACT)
+        return fail(VKHIP_ERR_INVALID, "set_numerics: unknown mode %d", mode);
+    ctx().exact_math = mode == VKHIP_NUMERICS_EXACT ? 1 : 0;
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_get_numerics(void) {
+    return ctx().exact_math ? VKHIP_NUMERICS_EXACT : VKHIP_NUMERICS_FAST;
+}
 
 // ---- memory ----------------------------------------------------------------------------
 
@@ -1009,6 +1025,13 @@ extern "C" int vkhip_event_elapsed(void* start, void* end, float* out_ms) {
 }
 
 // ---- host-side planning helpers (no device needed) -----------------------------------
+
+extern "C" int vkhip_exact_math(const float* host_x, float* host_y, size_t n, int log_mode) {
+    if (n && (!host_x || !host_y)) return fail(VKHIP_ERR_INVALID, "exact_math: null array");
+    for (size_t i = 0; i < n; ++i)
+        host_y[i] = log_mode ? vkhip::exact_logf(host_x[i]) : vkhip::exact_expf(host_x[i]);
+    return VKHIP_OK;
+}
 
 extern "C" uint32_t vkhip_fast_divide(uint32_t n, uint32_t d) {
     return d == 0 ? 0xffffffffu : vkhip::FastDiv(d).div(n);

@@ -217,6 +217,16 @@ class HipBackend:
     def capabilities(self) -> _lib.Caps:
         return self.caps
 
+    # numerics mode (vkhip_set_numerics): "fast" or "exact"
+    def set_numerics(self, mode: str) -> None:
+        codes = {"fast": _lib.NUMERICS_FAST, "exact": _lib.NUMERICS_EXACT}
+        if mode not in codes:
+            raise ValueError(f"numerics mode {mode!r}: 'fast' or 'exact'")
+        check(self.lib.vkhip_set_numerics(codes[mode]), "set_numerics")
+
+    def numerics(self) -> str:
+        return "exact" if self.lib.vkhip_get_numerics() == _lib.NUMERICS_EXACT else "fast"
+
     # Backend::allocator
     def allocate(self, shape, dtype=np.float32) -> DeviceArray:
         return DeviceArray(shape, dtype)
