@@ -21,7 +21,7 @@ timed steps are meant to see the sustained clock. The secondary cases are each
 queued behind ~25 ms of GEMM for the same reason.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--warmup-seconds S]
-       [--no-secondary] [--no-cpu-baseline]
+       [--no-secondary] [--no-cpu-baseline] [--case NAME[,NAME] [--no-gate]]
 """
 from __future__ import annotations
 
@@ -56,6 +56,12 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="target CPU work for the baseline sample")
+    p.add_argument("--case", default="",
+                   help="run only these secondary cases (comma-separated names) and print them; "
+                        "the headline, training and CPU lines are skipped (profiling runs)")
+    p.add_argument("--no-gate", action="store_true",
+                   help="do not queue the ~25 ms of GEMM before each timed batch (profiling runs: "
+                        "counters then see the case's kernels only)")
     p.add_argument("--calibrate", action="store_true",
                    help="also run the plain 16-byte copy kernel 5x over 256 MiB (the byte-counter "
                         "calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
@@ -72,6 +78,7 @@ class Timer:
 
 
 _GATE = None
+_GATE_ON = True
 
 
 def gate(launches: int = 24):
@@ -82,6 +89,8 @@ def gate(launches: int = 24):
     from vkml_amd import ops
     from vkml_amd.device import DeviceArray
 
+    if not _GATE_ON:
+        return
     if _GATE is None:
         a = DeviceArray.from_numpy(np.ones((4096, 4096), np.float32))
         _GATE = (a, DeviceArray((4096, 4096), np.float32))
@@ -269,144 +278,196 @@ def cpu_baseline(args):
             "lines": lines}
 
 
-def secondary(hip, ops, timer):
-    """The other hot-path kernels at BASELINE shapes: mean per-launch time of
-    back-to-back launches into preallocated outputs."""
+# ---- secondary cases ------------------------------------------------------------
+# Each case measures one hot-path kernel family at its BASELINE shape and adds
+# its entries to `out`. `python bench.py --case NAME[,NAME]` runs only the
+# named cases (the profiling runs behind profiles/ use this with rocprofv3).
+
+def _rotate(rng, shape, count, scale=1.0):
     from vkml_amd.device import DeviceArray
 
-    rng = np.random.default_rng(7)
-    out = {}
+    return [DeviceArray.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+            for _ in range(count)]
 
-    def rotate(shape, count, gen=lambda s: rng.standard_normal(s, dtype=np.float32)):
-        return [DeviceArray.from_numpy(gen(shape)) for _ in range(count)]
 
-    def bw(name, ms, byt):
-        out[name] = {"ms": round(ms, 5), "gbs": round(byt / ms / 1e6, 1),
-                     "frac_of_hbm": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4)}
+def _bw(out, name, ms, byt):
+    out[name] = {"ms": round(ms, 5), "gbs": round(byt / ms / 1e6, 1),
+                 "frac_of_hbm": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4)}
 
-    # GEMM variants (compute-bound: no rotation)
-    for name, (m, n, k), lay in [("gemm_512", (512, 512, 512), "nn"),
-                                 ("gemm_1024", (1024, 1024, 1024), "nn"),
-                                 ("gemm_2048", (2048, 2048, 2048), "nn"),
-                                 ("gemm_nt_4096", (4096, 4096, 4096), "nt"),
-                                 ("gemm_tn_4096", (4096, 4096, 4096), "tn"),
-                                 ("gemm_8192x1024x4096", (8192, 1024, 4096), "nn"),
-                                 ("gemm_8192", (8192, 8192, 8192), "nn"),
-                                 ("splitk_256x256x65536", (256, 256, 65536), "nn"),
-                                 ("wgrad_128x784x16384", (128, 784, 16384), "nn")]:
-        a = DeviceArray.from_numpy(rng.standard_normal((m, k) if lay[0] == "n" else (k, m),
-                                                       dtype=np.float32))
-        b = DeviceArray.from_numpy(rng.standard_normal((k, n) if lay[1] == "n" else (n, k),
-                                                       dtype=np.float32))
-        av = a if lay[0] == "n" else a.T
-        bv = b if lay[1] == "n" else b.T
-        c = DeviceArray((m, n), np.float32)
-        ms = time_batch(lambda i: ops.matmul(av, bv, out=c), timer, 10 if m * n * k > 2**36 else 20)
-        splits, _ = ops.gemm_plan(1, m, n, k)
-        tf = 2.0 * m * n * k / ms / 1e9
-        out[name] = {"ms": round(ms, 5), "tflops": round(tf, 2),
-                     "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "splits": splits}
-        del a, b, c
 
-    # Practical HBM ceiling: the library's plain 16-byte copy, 4 x 256 MiB buffers
+GEMM_CASES = {"gemm_512": ((512, 512, 512), "nn"), "gemm_1024": ((1024, 1024, 1024), "nn"),
+              "gemm_2048": ((2048, 2048, 2048), "nn"), "gemm_nn_4096": ((4096, 4096, 4096), "nn"),
+              "gemm_nt_4096": ((4096, 4096, 4096), "nt"), "gemm_tn_4096": ((4096, 4096, 4096), "tn"),
+              "gemm_8192x1024x4096": ((8192, 1024, 4096), "nn"), "gemm_8192": ((8192, 8192, 8192), "nn"),
+              "splitk_256x256x65536": ((256, 256, 65536), "nn"),
+              "wgrad_128x784x16384": ((128, 784, 16384), "nn")}
+
+
+def case_gemm(name, hip, ops, timer, rng, out):
+    """GEMM variants (compute-bound: no rotation)."""
+    from vkml_amd.device import DeviceArray
+
+    (m, n, k), lay = GEMM_CASES[name]
+    a = DeviceArray.from_numpy(rng.standard_normal((m, k) if lay[0] == "n" else (k, m), dtype=np.float32))
+    b = DeviceArray.from_numpy(rng.standard_normal((k, n) if lay[1] == "n" else (n, k), dtype=np.float32))
+    av = a if lay[0] == "n" else a.T
+    bv = b if lay[1] == "n" else b.T
+    c = DeviceArray((m, n), np.float32)
+    ms = time_batch(lambda i: ops.matmul(av, bv, out=c), timer, 10 if m * n * k > 2**36 else 20)
+    splits, _ = ops.gemm_plan(1, m, n, k)
+    tf = 2.0 * m * n * k / ms / 1e9
+    out[name] = {"ms": round(ms, 5), "tflops": round(tf, 2),
+                 "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "splits": splits}
+
+
+def case_copy(name, hip, ops, timer, rng, out):
+    """Practical HBM ceiling: the library's plain 16-byte copy, 4 x 256 MiB."""
+    from vkml_amd.device import DeviceArray
+
     bufs = [DeviceArray((64 << 20,), np.float32) for _ in range(4)]
-    ms = time_batch(lambda i: hip.copy_device_to_device([(bufs[(i + 1) % 4], bufs[i % 4])]),
-                    timer, 20)
-    bw("copy_256MiB", ms, 2 * (64 << 20) * 4)
-    del bufs
+    ms = time_batch(lambda i: hip.copy_device_to_device([(bufs[(i + 1) % 4], bufs[i % 4])]), timer, 20)
+    _bw(out, name, ms, 2 * (64 << 20) * 4)
 
-    # GEMV 4096x4096 . 4096 (bandwidth): rotate 8 matrices (512 MB)
-    mats = rotate((4096, 4096), 8)
+
+def case_gemv(name, hip, ops, timer, rng, out):
+    """GEMV 4096x4096 . 4096 (bandwidth): 8 rotated matrices (512 MB)."""
+    from vkml_amd.device import DeviceArray
+
+    mats = _rotate(rng, (4096, 4096), 8)
     x = DeviceArray.from_numpy(rng.standard_normal(4096, dtype=np.float32))
     y = DeviceArray((4096,), np.float32)
     ms = time_batch(lambda i: ops.gemv(mats[i % 8], x, out=y), timer, 40)
-    bw("gemv_4096", ms, 4096 * 4096 * 4 + 4096 * 4 * 2)
-    del mats
+    _bw(out, name, ms, 4096 * 4096 * 4 + 4096 * 4 * 2)
 
-    # im2col / col2im conv2 [128,64,32,32] <-> [128,576,1024] (335.5 MB each way)
-    imgs = rotate((128, 64, 32, 32), 2)
+
+def case_im2col_col2im(name, hip, ops, timer, rng, out):
+    """im2col / col2im conv2 [128,64,32,32] <-> [128,576,1024] (335.5 MB each way)."""
+    from vkml_amd.device import DeviceArray
+
+    imgs = _rotate(rng, (128, 64, 32, 32), 2)
     cols = [ops.im2col(im, 3, 1, 1) for im in imgs]
     img_out = DeviceArray((128, 64, 32, 32), np.float32)
     hip.synchronize()
     byt = 128 * 64 * 32 * 32 * 4 + 128 * 576 * 1024 * 4
-    ms = time_batch(lambda i: ops.im2col(imgs[i % 2], 3, 1, 1, out=cols[(i + 1) % 2]), timer, 20)
-    bw("im2col_conv2", ms, byt)
-    ms = time_batch(lambda i: ops.col2im(cols[i % 2], (32, 32), 3, 1, 1, out=img_out), timer, 20)
-    bw("col2im_conv2", ms, byt)
-    del imgs, cols, img_out
+    if name in ("im2col_conv2", "im2col_col2im"):
+        ms = time_batch(lambda i: ops.im2col(imgs[i % 2], 3, 1, 1, out=cols[(i + 1) % 2]), timer, 20)
+        _bw(out, "im2col_conv2", ms, byt)
+    if name in ("col2im_conv2", "im2col_col2im"):
+        ms = time_batch(lambda i: ops.col2im(cols[i % 2], (32, 32), 3, 1, 1, out=img_out), timer, 20)
+        _bw(out, "col2im_conv2", ms, byt)
 
-    # convolution forward and weight gradient: one implicit-im2col GEMM each,
-    # against the reference lowering (im2col into a column matrix, then the
-    # batch-broadcast GEMM)
-    for name, (xs_shape, cout) in [("conv_128x64x32x32_c128", ((128, 64, 32, 32), 128)),
-                                   ("conv_cnn1_128x3x32x32_c64", ((128, 3, 32, 32), 64)),
-                                   ("conv_cnn2_128x64x16x16_c128", ((128, 64, 16, 16), 128))]:
-        n_, cin, h, w_ = xs_shape
-        x = DeviceArray.from_numpy(rng.standard_normal(xs_shape, dtype=np.float32))
-        wt = DeviceArray.from_numpy(rng.standard_normal((cout, cin, 3, 3), dtype=np.float32))
-        y = DeviceArray((n_, cout, h, w_), np.float32)
-        ck, L = cin * 9, h * w_
-        cols = DeviceArray((n_, ck, L), np.float32)
-        wf = wt.reshape(1, 1, cout, ck).broadcast_to((1, n_, cout, ck))
-        flops = 2.0 * n_ * cout * L * ck
-        ms_i = time_batch(lambda i: ops.conv2d(x, wt, 1, 1, out=y), timer, 20)
 
-        def explicit(i):
-            ops.im2col(x, 3, 1, 1, out=cols)
-            ops.matmul(wf, cols.reshape(1, n_, ck, L), out=y.reshape(1, n_, cout, L))
+CONV_CASES = {"conv_128x64x32x32_c128": ((128, 64, 32, 32), 128),
+              "conv_cnn1_128x3x32x32_c64": ((128, 3, 32, 32), 64),
+              "conv_cnn2_128x64x16x16_c128": ((128, 64, 16, 16), 128)}
 
-        ms_e = time_batch(explicit, timer, 20)
-        out[name] = {"ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
-                     "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
-                     "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
-        # the weight gradient's per-image products, grad @ im2col(x)^T
-        g = DeviceArray.from_numpy(rng.standard_normal((n_, cout, h, w_), dtype=np.float32))
-        wg = DeviceArray((n_, cout, ck), np.float32)
-        g4 = g.reshape(1, n_, cout, L)
-        colsT = cols.reshape(1, n_, ck, L).transpose(-2, -1)
-        ms_i = time_batch(lambda i: ops.conv2d_weight_grad(x, g, 3, 1, 1, out=wg), timer, 20)
 
-        def explicit_wg(i):
-            ops.im2col(x, 3, 1, 1, out=cols)
-            ops.matmul(g4, colsT, out=wg.reshape(1, n_, cout, ck))
+def case_conv(name, hip, ops, timer, rng, out):
+    """Convolution forward and weight gradient: one implicit-im2col GEMM each,
+    against the reference lowering (im2col into a column matrix, then the
+    batch-broadcast GEMM)."""
+    from vkml_amd.device import DeviceArray
 
-        ms_e = time_batch(explicit_wg, timer, 20)
-        out[name.replace("conv_", "conv_wgrad_")] = {
-            "ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
-            "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
-            "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
-        del x, wt, y, cols, g, wg
+    xs_shape, cout = CONV_CASES[name]
+    n_, cin, h, w_ = xs_shape
+    x = DeviceArray.from_numpy(rng.standard_normal(xs_shape, dtype=np.float32))
+    wt = DeviceArray.from_numpy(rng.standard_normal((cout, cin, 3, 3), dtype=np.float32))
+    y = DeviceArray((n_, cout, h, w_), np.float32)
+    ck, L = cin * 9, h * w_
+    cols = DeviceArray((n_, ck, L), np.float32)
+    wf = wt.reshape(1, 1, cout, ck).broadcast_to((1, n_, cout, ck))
+    flops = 2.0 * n_ * cout * L * ck
+    ms_i = time_batch(lambda i: ops.conv2d(x, wt, 1, 1, out=y), timer, 20)
 
-    # softmax (read + write once), rotate past the MALL; each against the
-    # library's plain copy of the same bytes, the floor of a one-pass kernel
-    # at that size (launch ramp and drain included)
-    for shape, count in [((4096, 1000), 20), ((256, 32768), 10)]:
-        xs = rotate(shape, count, lambda s: rng.standard_normal(s, dtype=np.float32) * 2)
-        ys = [DeviceArray(shape, np.float32) for _ in range(2)]
-        ms = time_batch(lambda i: ops.softmax(xs[i % count], -1, out=ys[i % 2]), timer, 40)
-        name = f"softmax_{shape[0]}x{shape[1]}"
-        bw(name, ms, 2 * shape[0] * shape[1] * 4)
-        flat = [xv.reshape(shape[0] * shape[1]) for xv in xs]
-        yflat = [yv.reshape(shape[0] * shape[1]) for yv in ys]
-        ms_copy = time_batch(lambda i: hip.copy_device_to_device([(yflat[i % 2], flat[i % count])]),
-                             timer, 40)
-        out[name]["copy_same_bytes_ms"] = round(ms_copy, 5)
-        out[name]["frac_of_copy"] = round(ms_copy / ms, 4)
-        del xs, ys
+    def explicit(i):
+        ops.im2col(x, 3, 1, 1, out=cols)
+        ops.matmul(wf, cols.reshape(1, n_, ck, L), out=y.reshape(1, n_, cout, L))
 
-    # sum / max over the last axis of [8192, 4096] (134 MB read), 4 buffers
-    xs = rotate((8192, 4096), 4)
+    ms_e = time_batch(explicit, timer, 20)
+    out[name] = {"ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
+                 "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+                 "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
+    g = DeviceArray.from_numpy(rng.standard_normal((n_, cout, h, w_), dtype=np.float32))
+    wg = DeviceArray((n_, cout, ck), np.float32)
+    g4 = g.reshape(1, n_, cout, L)
+    colsT = cols.reshape(1, n_, ck, L).transpose(-2, -1)
+    ms_i = time_batch(lambda i: ops.conv2d_weight_grad(x, g, 3, 1, 1, out=wg), timer, 20)
+
+    def explicit_wg(i):
+        ops.im2col(x, 3, 1, 1, out=cols)
+        ops.matmul(g4, colsT, out=wg.reshape(1, n_, cout, ck))
+
+    ms_e = time_batch(explicit_wg, timer, 20)
+    out[name.replace("conv_", "conv_wgrad_")] = {
+        "ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
+        "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+        "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
+
+
+SOFTMAX_CASES = {"softmax_4096x1000": ((4096, 1000), 20), "softmax_256x32768": ((256, 32768), 10)}
+
+
+def case_softmax(name, hip, ops, timer, rng, out):
+    """Softmax (read + write once), rotated past the MALL, against the
+    library's plain copy of the same bytes (the floor of a one-pass kernel at
+    that size, launch ramp and drain included)."""
+    from vkml_amd.device import DeviceArray
+
+    shape, count = SOFTMAX_CASES[name]
+    xs = _rotate(rng, shape, count, 2.0)
+    ys = [DeviceArray(shape, np.float32) for _ in range(2)]
+    ms = time_batch(lambda i: ops.softmax(xs[i % count], -1, out=ys[i % 2]), timer, 40)
+    _bw(out, name, ms, 2 * shape[0] * shape[1] * 4)
+    flat = [xv.reshape(shape[0] * shape[1]) for xv in xs]
+    yflat = [yv.reshape(shape[0] * shape[1]) for yv in ys]
+    ms_copy = time_batch(lambda i: hip.copy_device_to_device([(yflat[i % 2], flat[i % count])]),
+                         timer, 40)
+    out[name]["copy_same_bytes_ms"] = round(ms_copy, 5)
+    out[name]["frac_of_copy"] = round(ms_copy / ms, 4)
+
+
+def case_reduce(name, hip, ops, timer, rng, out):
+    """sum / max over the last axis of [8192, 4096] (134 MB read), 4 buffers."""
+    from vkml_amd.device import DeviceArray
+
+    xs = _rotate(rng, (8192, 4096), 4)
     r = DeviceArray((8192,), np.float32)
-    for name, fn in [("sum_8192x4096", ops.sum), ("max_8192x4096", ops.amax)]:
-        ms = time_batch(lambda i: fn(xs[i % 4], [1], out=r), timer, 20)
-        bw(name, ms, 8192 * 4096 * 4 + 8192 * 4)
-    del xs
+    fns = {"sum_8192x4096": ops.sum, "max_8192x4096": ops.amax}
+    for key, fn in fns.items():
+        if name in (key, "reduce_8192x4096"):
+            ms = time_batch(lambda i: fn(xs[i % 4], [1], out=r), timer, 20)
+            _bw(out, key, ms, 8192 * 4096 * 4 + 8192 * 4)
+
+
+CASES = {**{k: case_gemm for k in GEMM_CASES}, "copy_256MiB": case_copy, "gemv_4096": case_gemv,
+         "im2col_conv2": case_im2col_col2im, "col2im_conv2": case_im2col_col2im,
+         **{k: case_conv for k in CONV_CASES}, **{k: case_softmax for k in SOFTMAX_CASES},
+         "sum_8192x4096": case_reduce, "max_8192x4096": case_reduce}
+DEFAULT_RUN = [k for k in GEMM_CASES if k != "gemm_nn_4096"] + [
+    "copy_256MiB", "gemv_4096", "im2col_col2im", *CONV_CASES, *SOFTMAX_CASES, "reduce_8192x4096"]
+CASES["im2col_col2im"] = case_im2col_col2im
+CASES["reduce_8192x4096"] = case_reduce
+
+
+def secondary(hip, ops, timer, names=None):
+    """The other hot-path kernels at BASELINE shapes: mean per-launch time of
+    back-to-back launches into preallocated outputs."""
+    rng = np.random.default_rng(7)
+    out = {}
+    for name in names or DEFAULT_RUN:
+        if name not in CASES:
+            raise SystemExit(f"unknown case {name!r}; known: {sorted(CASES)}")
+        CASES[name](name, hip, ops, timer, rng, out)
     return out
 
 
-def training_steps(steps_mlp: int = 100, steps_cnn: int = 20):
+def training_steps(steps_mlp: int = 100, steps_cnn: int = 50):
     """BASELINE configs 1 and 5 as training loops on the device: steps/s over
-    the timed steps (graph build + flushes + the loss read each step)."""
+    the timed steps, each step's loss read back to the host. Three ways to run
+    the same step: "eager" (the host core builds, orders and packs the graph
+    every step), "replay" (the step recorded once, its compute/SGD calls
+    replayed from C, vkhip_program_run) and "graph" (the replay captured once
+    into a HIP graph); all three give the same bits (tests/test_gpu_replay.py)."""
     from vkml_amd import nn, optim
     from vkml_amd import tensor as T
 
@@ -423,28 +484,45 @@ def training_steps(steps_mlp: int = 100, steps_cnn: int = 20):
             (128, 3, 32, 32), 100, 0.01, steps_cnn, (-1.0, 1.0)),
     }
     for name, (make, shape, classes, lr, steps, (lo, hi)) in configs.items():
-        nn.manual_seed(20260726)
-        model = make()
-        opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
         data = [(rng.uniform(lo, hi, shape).astype(np.float32),
                  rng.integers(0, classes, shape[0]).astype(np.int64)) for _ in range(4)]
+        out = {}
+        for mode in ("eager", "replay", "graph"):
+            nn.manual_seed(20260726)
+            model = make()
+            opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
 
-        def step(i):
-            x, y = data[i % 4]
-            opt.zero_grad()
-            loss = nn.cross_entropy(model(T.tensor(x)), T.tensor(y))
-            loss.backward()
-            opt.step()
-            return loss.item()
+            def fn(x, y):
+                opt.zero_grad()
+                loss = nn.cross_entropy(model(x), y)
+                loss.backward()
+                opt.step()
+                return loss
 
-        for i in range(3):
-            step(i)
-        t0 = time.perf_counter()
-        for i in range(steps):
-            last = step(i)
-        dt = time.perf_counter() - t0
-        res[name] = {"steps": steps, "ms_per_step": round(dt * 1e3 / steps, 3),
-                     "steps_per_s": round(steps / dt, 2), "last_loss": round(last, 5)}
+            if mode == "eager":
+                def step(i):
+                    x, y = data[i % 4]
+                    return fn(T.tensor(x), T.tensor(y)).item()
+            else:
+                captured = T.CapturedStep(fn, *data[0], graph=(mode == "graph"))
+
+                def step(i):
+                    return float(captured(*data[i % 4])[0])
+            # the recording is step 0 of the replayed runs: every mode then
+            # takes the same steps on the same batches, and reports the same
+            # last loss
+            for i in range(0 if mode == "eager" else 1, 3):
+                step(i)
+            t0 = time.perf_counter()
+            for i in range(3, 3 + steps):
+                last = step(i)
+            dt = time.perf_counter() - t0
+            out[mode] = {"ms_per_step": round(dt * 1e3 / steps, 4),
+                         "steps_per_s": round(steps / dt, 2), "last_loss": round(last, 5)}
+            if mode != "eager":
+                out[mode].update(captured.info())
+                captured.close()
+        res[name] = {"steps": steps, **out}
     return res
 
 
@@ -472,6 +550,12 @@ def main():
 
     hip = backend()
     timer = Timer()
+    if args.case:
+        global _GATE_ON
+        _GATE_ON = not args.no_gate
+        names = [c for c in args.case.split(",") if c]
+        print(json.dumps({"cases": secondary(hip, ops, timer, names), "gate": _GATE_ON}), flush=True)
+        return
     value, ms_step, avg_ms, achieved, min_ms, warm = gemm_headline(args, hip, ops, timer)
     result = {
         "metric": METRIC,
