@@ -101,12 +101,13 @@ def plan(batch, m, n, k, split=0):
 
 
 def test_split_k_plan_rules():
-    """The split-K plan: power-of-two chunk, workspace <= 64 MiB, OFF never
-    splits, a forced request gets the largest power-of-two chunk giving at
-    least that many partitions (reference plan_split_k,
+    """The split-K plan: equal chunks of K-tiles, workspace <= 64 MiB, OFF
+    never splits, a forced request gets the largest power-of-two chunk giving
+    at least that many partitions (reference plan_split_k,
     vulkan_backend.cpp:596-647); AUTO splits exactly when neither 128x128 nor
-    64x64 output tiles give each of the 256 CUs a workgroup, aiming at about
-    one workgroup per CU (the rule restated for MI355X)."""
+    64x64 output tiles give each of the 256 CUs a workgroup, and then takes as
+    many partitions as fit one round of one workgroup per CU (the rule
+    restated for MI355X)."""
     # the GEMM sweep's square sizes down to 1024^3 and 8192x1024x4096 fill the
     # machine with 128x128 or 64x64 tiles: no split
     assert plan(1, 4096, 4096, 4096) == (1, 128)
@@ -119,11 +120,16 @@ def test_split_k_plan_rules():
     for m, n, k in [(256, 256, 65536), (128, 784, 16384), (64, 128, 784), (128, 1024, 576)]:
         splits, chunk = plan(1, m, n, k)
         ktiles = -(-k // 32)
-        assert splits > 1 and chunk >= 2 and chunk & (chunk - 1) == 0
+        assert splits > 1 and chunk >= 2
         assert splits == -(-ktiles // chunk)
         assert m * n * splits * 4 <= 64 << 20
         tiles = -(-m // 64) * -(-n // 64)
         assert tiles * splits >= min(512, tiles * (ktiles // 2)) // 2
+    # one round of 256 workgroups: 4 tiles x 64, 7 tiles x 35 (15 K-tiles each)
+    assert plan(1, 256, 256, 65536) == (64, 32)
+    assert plan(1, 128, 784, 16384) == (35, 15)
+    # more than half a round of tiles (144 at 1536^3): power-of-two chunk
+    assert plan(1, 1536, 1536, 1536) == (3, 16)
     # a batched conv GEMM has tiles enough
     assert plan(128, 128, 1024, 576)[0] == 1
     # OFF

@@ -42,7 +42,40 @@ struct GemmArgs {
     uint32_t chunk;              // K-tiles per split partition
     uint64_t split_stride;       // elements between partition slices of c
     uint32_t a_vec, b_vec;       // 16-byte loads along k are legal
+    uint32_t flat_splits;        // > 0: split grid launched flat, grid.x = tiles * flat_splits
 };
+
+// Output tile (tm, tn) and K partition of this workgroup.
+//  - Unsplit grids (blockIdx.x = tile): the hardware deals workgroups to the
+//    8 XCDs round-robin, so the tile index is remapped to give each XCD a
+//    contiguous tile range, walked in groups of 8 tile-rows for L2 reuse.
+//  - Split grids launched flat (flat_splits > 0, grid.x = tiles * partitions):
+//    the workgroups one XCD receives (linear id % 8) take a contiguous range
+//    of (partition, tile) pairs, so the tiles of one partition, which read the
+//    same K slices of A and B, share that XCD's L2 instead of each fetching
+//    them from memory.
+//  - Otherwise blockIdx.y is the partition.
+// Which workgroup computes what never changes what it computes: same bits.
+__device__ __forceinline__ void tile_of(const GemmArgs& g, uint32_t& tm, uint32_t& tn,
+                                        uint32_t& split) {
+    const uint32_t ntiles = g.tiles_m * g.tiles_n;
+    uint32_t bid = blockIdx.x;
+    split = blockIdx.y;
+    if (g.flat_splits) {
+        const uint32_t total = ntiles * g.flat_splits;
+        const uint32_t xcd = bid & 7u, slot = bid >> 3, q = total >> 3, r = total & 7u;
+        const uint32_t v = xcd * q + min(xcd, r) + slot;
+        split = v / ntiles;
+        bid = v - split * ntiles;
+    } else if ((ntiles & 7u) == 0) {
+        bid = (bid & 7u) * (ntiles >> 3) + (bid >> 3);
+    }
+    const uint32_t group_span = 8u * g.tiles_n;
+    const uint32_t first_m = (bid / group_span) * 8u;
+    const uint32_t gsize = min(g.tiles_m - first_m, 8u);
+    tm = first_m + (bid % group_span) % gsize;
+    tn = (bid % group_span) / gsize;
+}
 
 // Loads one BK-deep tile of an operand (rows x BK) into registers as groups of
 // four consecutive k, then stores each group to LDS [row][k] as 16 bytes.
@@ -413,14 +446,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
     // Tile order: contiguous tile ranges per XCD (workgroups are dealt to the
     // 8 XCDs round-robin), and within a range, groups of 8 tile-rows so that
     // co-resident tiles share A and B panels in that XCD's L2.
-    const uint32_t ntiles = g.tiles_m * g.tiles_n;
-    uint32_t bid = blockIdx.x;
-    if ((ntiles & 7u) == 0) bid = (bid & 7u) * (ntiles >> 3) + (bid >> 3);
-    const uint32_t group_span = 8u * g.tiles_n;
-    const uint32_t first_m = (bid / group_span) * 8u;
-    const uint32_t gsize = min(g.tiles_m - first_m, 8u);
-    const uint32_t tm = first_m + (bid % group_span) % gsize;
-    const uint32_t tn = (bid % group_span) / gsize;
+    uint32_t tm, tn, split;
+    tile_of(g, tm, tn, split);
     const uint32_t row0 = tm * BM;
     const uint32_t col0 = tn * BN;
 
@@ -450,10 +477,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
     }
     typename LB::ImgRows trows;
     if constexpr (BMODE == IMGT) LB::img_rows(trows, im_in, col0, g.n, tid);
-    float* cbase = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride +
+    float* cbase = g.c + static_cast<uint64_t>(split) * g.split_stride +
                    static_cast<uint64_t>(z) * g.m * g.n;
 
-    const uint32_t kt0 = blockIdx.y * g.chunk;
+    const uint32_t kt0 = split * g.chunk;
     const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
     // Whole tile inside M x N: K-tiles that are also inside K load unguarded.
     const bool rows_in = row0 + BM <= g.m && col0 + BN <= g.n;
@@ -640,14 +667,8 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
     const int wave = tid >> 6;
     const int wm0 = wave * 32;
 
-    const uint32_t ntiles = g.tiles_m * g.tiles_n;
-    uint32_t bid = blockIdx.x;
-    if ((ntiles & 7u) == 0) bid = (bid & 7u) * (ntiles >> 3) + (bid >> 3);
-    const uint32_t group_span = 8u * g.tiles_n;
-    const uint32_t first_m = (bid / group_span) * 8u;
-    const uint32_t gsize = min(g.tiles_m - first_m, 8u);
-    const uint32_t tm = first_m + (bid % group_span) % gsize;
-    const uint32_t tn = (bid % group_span) / gsize;
+    uint32_t tm, tn, split;
+    tile_of(g, tm, tn, split);
     const uint32_t row0 = tm * BM;
     const uint32_t col0 = tn * BN;
 
@@ -659,9 +680,9 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
         const_cast<float*>(abase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
     const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(bbase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
-    float* cbase = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride +
+    float* cbase = g.c + static_cast<uint64_t>(split) * g.split_stride +
                    static_cast<uint64_t>(z) * g.m * g.n;
-    const uint32_t kt0 = blockIdx.y * g.chunk;
+    const uint32_t kt0 = split * g.chunk;
     const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
 
     f32x16 acc[4];
@@ -779,14 +800,8 @@ __global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
     const int wm0 = (wave & 1) * 32;
     const int s0 = wave >> 1;
 
-    const uint32_t ntiles = g.tiles_m * g.tiles_n;
-    uint32_t bid = blockIdx.x;
-    if ((ntiles & 7u) == 0) bid = (bid & 7u) * (ntiles >> 3) + (bid >> 3);
-    const uint32_t group_span = 8u * g.tiles_n;
-    const uint32_t first_m = (bid / group_span) * 8u;
-    const uint32_t gsize = min(g.tiles_m - first_m, 8u);
-    const uint32_t tm = first_m + (bid % group_span) % gsize;
-    const uint32_t tn = (bid % group_span) / gsize;
+    uint32_t tm, tn, split;
+    tile_of(g, tm, tn, split);
     const uint32_t row0 = tm * BM;
     const uint32_t col0 = tn * BN;
 
@@ -798,9 +813,9 @@ __global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
         const_cast<float*>(abase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
     const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(bbase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
-    float* cbase = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride +
+    float* cbase = g.c + static_cast<uint64_t>(split) * g.split_stride +
                    static_cast<uint64_t>(z) * g.m * g.n;
-    const uint32_t kt0 = blockIdx.y * g.chunk;
+    const uint32_t kt0 = split * g.chunk;
     const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
 
     f32x16 acc;
@@ -1148,30 +1163,46 @@ __global__ __launch_bounds__(256) void gemm_exact_kernel(GemmArgs g, int depth, 
 // ---- planning ---------------------------------------------------------------
 
 // Split-K plan (reference plan_split_k, vulkan_backend.cpp:596-647), restated
-// for MI355X. Kept from the reference: the partition chunk is a power of two of
-// K-tiles, a forced request gets the largest power-of-two chunk that still
-// yields at least that many partitions, the partial workspace is capped at
-// 64 MiB, and the fold of the partials is the carry stack. Changed: the
-// reference's profitability rule (split iff K-tiles >= output tiles, at most
-// 16 partitions, chunk >= 4) was fitted on a 36-CU RDNA1 part. Here the caller
-// splits only products whose output tiles cannot give every one of the 256 CUs
-// a workgroup; the target is ceil(CUs / tiles) partitions, capped at 256, with
-// a chunk of at least two K-tiles.
+// for MI355X. Kept from the reference: every partition but the last covers the
+// same chunk of K-tiles, a forced request gets the largest power-of-two chunk
+// that still yields at least that many partitions, the partial workspace is
+// capped at 64 MiB, and the fold of the partials is the carry stack (so the
+// result is bit-stable for a given plan). Changed: the reference's
+// profitability rule (split iff K-tiles >= output tiles, at most 16
+// partitions, power-of-two chunk >= 4) was fitted on a 36-CU RDNA1 part. Here
+// the caller splits only products whose output tiles cannot give every one of
+// the 256 CUs a workgroup; AUTO takes floor(CUs / tiles) partitions (at most
+// 256) and the chunk that covers K in that many, at least two K-tiles, when
+// that is two or more; products with more than half a round of tiles keep a
+// power-of-two chunk giving ceil(CUs / tiles) partitions.
 static void plan_split_k(uint32_t tiles, uint32_t ktiles, uint64_t out_elems, uint32_t slots,
                          uint32_t requested, uint32_t& splits, uint32_t& chunk) {
     splits = 1;
     chunk = ktiles;
     if (ktiles < 2 || tiles == 0) return;
-    uint32_t target = requested;
-    if (target == 0) {
-        if (tiles >= slots) return;
-        target = (slots + tiles - 1) / tiles;
-        if (target < 2) target = 2;
-        if (target > 256) target = 256;
-    }
     uint32_t c = 1;
-    while (c * 2 <= ktiles / target) c *= 2;
-    if (c < 2 && requested == 0) c = 2;
+    if (requested == 0) {
+        // AUTO: as many partitions as keep the whole grid in one round of one
+        // workgroup per CU (a second, partial round would cost a whole
+        // partition's time), with equal chunks of K-tiles: 128x784x16384 (7
+        // tiles) runs 35 partitions of 15 K-tiles in one round, not 64 of 8
+        // in 1.75 rounds.
+        if (tiles >= slots) return;
+        if (2 * tiles <= slots) {
+            uint32_t target = slots / tiles;
+            if (target > 256) target = 256;
+            c = (ktiles + target - 1) / target;
+        } else {
+            // more than half a round of tiles: no split fits one round; the
+            // largest power-of-two chunk giving ceil(CUs / tiles) partitions,
+            // as measured for 1536^3 (3 partitions of 16 K-tiles)
+            const uint32_t target = (slots + tiles - 1) / tiles;
+            while (c * 2 <= ktiles / target) c *= 2;
+        }
+        if (c < 2) c = 2;
+    } else {
+        while (c * 2 <= ktiles / requested) c *= 2;
+    }
     if (c >= ktiles) return;
     const uint32_t s = (ktiles + c - 1) / c;
     if (s < 2 || s > 511) return;
@@ -1547,9 +1578,14 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
                         ((static_cast<int64_t>(k) - 1) * g.sbk + n) * 4 < (int64_t{1} << 31);
     const bool a_rows = a_fwd && amode == RCV && g.sam == 1 && m % 4 == 0 && g.sak % 4 == 0 &&
                         ((static_cast<int64_t>(k) - 1) * g.sak + m) * 4 < (int64_t{1} << 31);
+    // Split direct launches run flat, partitions grouped per XCD (tile_of).
+    const uint64_t flat = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
+    if (splits > 1 && flat <= 0x7fffffffull) g.flat_splits = splits;
+    const dim3 dgrid = g.flat_splits ? dim3(static_cast<uint32_t>(flat), 1, static_cast<uint32_t>(batch))
+                                     : dim3(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
     if (tile.bm == 128 && b_rows && (amode == KCD || a_rows) &&
         reinterpret_cast<uintptr_t>(target) % 16 == 0) {
-        dim3 grid(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
+        const dim3 grid = dgrid;
         if (amode == KCD)
             hipLaunchKernelGGL(gemm_nn_direct_kernel<false>, grid, dim3(256), 0, ctx().stream, g);
         else
@@ -1559,7 +1595,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
         return VKHIP_OK;
     }
     if (tile.bm == 64 && b_rows && (amode == KCD || a_rows)) {
-        dim3 grid(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
+        const dim3 grid = dgrid;
         if (amode == KCD)
             hipLaunchKernelGGL(gemm_direct64_kernel<false>, grid, dim3(256), 0, ctx().stream, g);
         else
@@ -1568,6 +1604,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
         if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
         return VKHIP_OK;
     }
+    g.flat_splits = 0;  // the register-path kernel takes the partition from blockIdx.y
     if (tile.bm == 128)
         st = launch_tiles<128, 128, 64, 64>(g, static_cast<uint32_t>(batch), splits, amode, bmode);
     else
