@@ -461,7 +461,14 @@ def secondary(hip, ops, timer, names=None):
     return out
 
 
-def training_steps(steps_mlp: int = 100, steps_cnn: int = 50):
+def case_training(name, hip, ops, timer, rng, out):
+    """One training config (config 1 "train_mlp" or config 5 "train_cnn") in
+    the three ways training_steps runs it."""
+    only = {"train_mlp": "mlp_784_128_10_b64", "train_cnn": "cifar_cnn_b128"}[name]
+    out.update(training_steps(only=only))
+
+
+def training_steps(steps_mlp: int = 100, steps_cnn: int = 50, only: str | None = None):
     """BASELINE configs 1 and 5 as training loops on the device: steps/s over
     the timed steps, each step's loss read back to the host. Three ways to run
     the same step: "eager" (the host core builds, orders and packs the graph
@@ -484,6 +491,8 @@ def training_steps(steps_mlp: int = 100, steps_cnn: int = 50):
             (128, 3, 32, 32), 100, 0.01, steps_cnn, (-1.0, 1.0)),
     }
     for name, (make, shape, classes, lr, steps, (lo, hi)) in configs.items():
+        if only is not None and name != only:
+            continue
         data = [(rng.uniform(lo, hi, shape).astype(np.float32),
                  rng.integers(0, classes, shape[0]).astype(np.int64)) for _ in range(4)]
         out = {}
@@ -524,6 +533,10 @@ def training_steps(steps_mlp: int = 100, steps_cnn: int = 50):
                 captured.close()
         res[name] = {"steps": steps, **out}
     return res
+
+
+CASES["train_mlp"] = case_training
+CASES["train_cnn"] = case_training
 
 
 def read_traffic(args):
