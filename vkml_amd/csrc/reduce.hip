@@ -227,7 +227,7 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
                 f32x4 o;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) o[j] = LOG ? x[4 * i + j] - ld : div_by(x[4 * i + j], denom, rinv);
-                *reinterpret_cast<f32x4*>(ds + e0) = o;
+                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(ds + e0));
             }
         }
     } else {
@@ -322,7 +322,7 @@ __global__ __launch_bounds__(256) void softmax_wave_rows_kernel(
                     f32x4 o;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) o[j] = LOG ? x[4 * i + j] - ld : div_by(x[4 * i + j], denom, rinv);
-                    *reinterpret_cast<f32x4*>(ds + e0) = o;
+                    __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(ds + e0));
                 }
             }
         } else {
@@ -1541,7 +1541,7 @@ __global__ __launch_bounds__(256) void softmax_chunk_apply_kernel(const float* _
                     const float sh = x[4 * i + j] - peak;
                     o[j] = LOG ? sh - ld : softmax_exp(sh) * rinv;
                 }
-                *reinterpret_cast<f32x4*>(ds + e0) = o;
+                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(ds + e0));
             }
         }
     } else {
