@@ -402,6 +402,21 @@ def case_conv(name, hip, ops, timer, rng, out):
         "ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
         "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
         "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
+    # dW itself (summed over the batch): the per-image products followed by
+    # the batch SUM (the reference graph's two nodes) against one product
+    # with the batch folded into K
+    dw = DeviceArray((cout, ck), np.float32)
+
+    def per_image_then_sum(i):
+        ops.conv2d_weight_grad(x, g, 3, 1, 1, out=wg)
+        ops.sum(wg, [0], out=dw)
+
+    ms_s = time_batch(per_image_then_sum, timer, 20)
+    ms_f = time_batch(lambda i: ops.conv2d_weight_grad_sum(x, g, 3, 1, 1, out=dw), timer, 20)
+    out[name.replace("conv_", "conv_dw_")] = {
+        "ms": round(ms_f, 5), "tflops": round(flops / ms_f / 1e9, 2),
+        "frac_of_peak": round(flops / ms_f / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+        "per_image_then_sum_ms": round(ms_s, 5), "speedup_vs_per_image": round(ms_s / ms_f, 3)}
 
 
 SOFTMAX_CASES = {"softmax_4096x1000": ((4096, 1000), 20), "softmax_256x32768": ((256, 32768), 10)}

@@ -147,7 +147,14 @@ enum vkhip_op {
      * extents as out) -> out = x <= 0 ? +0 : g: the reference relu gradient
      * where(less_equal(x, zeros_like(x)), zeros_like(g), g) (autograd.cpp:397-408)
      * as one node, value for value (a NaN x passes g through). */
-    VKHIP_OP_RELU_BACKWARD = 100
+    VKHIP_OP_RELU_BACKWARD = 100,
+    /* src0 x [N,C,H,W], src1 grad [N,Cout,out_h,out_w] (positions unit-stride),
+     * params vkhip_unfold -> out [Cout, C*kh*kw]: the conv2d weight gradient
+     * summed over the batch, the value of CONV2D_WEIGHT_GRAD followed by the
+     * batch SUM. FAST numerics fold the batch into the product's K axis (no
+     * intermediate, within the GEMM tolerance of the graph); EXACT numerics
+     * give the graph's bits. */
+    VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM = 101
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */
@@ -368,6 +375,16 @@ int vkhip_conv2d(const float* x, const vkhip_operand* x_desc, const float* w,
  * same bits. */
 int vkhip_conv2d_weight_grad(const float* x, const vkhip_operand* x_desc, const float* grad,
                              const vkhip_operand* grad_desc, float* out, const vkhip_unfold* p);
+
+/* The weight gradient summed over the batch (VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM):
+ * out [Cout, C*kh*kw] contiguous = sum_n grad[n] @ im2col(x[n])^T, what the
+ * reference's conv2d backward computes as the per-image products followed by
+ * the broadcast adjoint's batch sum (autograd.cpp:548-553, :84-116). grad as
+ * for vkhip_conv2d_weight_grad. FAST numerics with out_h*out_w a multiple of
+ * 32: one product with the batch folded into K. Otherwise the per-image
+ * products and the batch sum (the graph's bits). */
+int vkhip_conv2d_weight_grad_sum(const float* x, const vkhip_operand* x_desc, const float* grad,
+                                 const vkhip_operand* grad_desc, float* out, const vkhip_unfold* p);
 
 /* ======================================================================== */
 /* Fused optimiser step                                                      */

@@ -690,6 +690,32 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 free(cols);
                 break;
             }
+            case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: {
+                /* The same per-image products, then the broadcast adjoint's
+                 * batch sum (autograd.cpp:84-116): the graph's value, per
+                 * element the pairwise sum over the N images. */
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                const vkhip_tensor* g = &nd->src[1];
+                const int64_t N = g->ne[0], cout = g->ne[1];
+                const int64_t L = g->ne[2] * g->ne[3];
+                const int64_t ck = o->ne[1];
+                float* cols = (float*)malloc(sizeof(float) * (size_t)(N * ck * L + 1));
+                float* per = (float*)malloc(sizeof(float) * (size_t)(N * cout * ck + 1));
+                if (!cols || !per) { free(cols); free(per); return VKHIP_ERR_OOM; }
+                or_im2col((const float*)nd->src[0].data, &s0, cols, &p, threads);
+                vkhip_operand gd = {{1, (uint32_t)N, (uint32_t)cout, (uint32_t)L},
+                                    {0, g->nb[0], g->nb[1], 1}};
+                vkhip_operand cd = {{1, (uint32_t)N, (uint32_t)L, (uint32_t)ck},
+                                    {0, ck * L, 1, L}};
+                or_matmul((const float*)g->data, &gd, cols, &cd, per, threads);
+                vkhip_operand pd = {{1, (uint32_t)N, (uint32_t)cout, (uint32_t)ck},
+                                    {0, cout * ck, ck, 1}};
+                or_reduce(VKHIP_REDUCE_SUM, per, &pd, 0x2u, o->data, threads);
+                free(cols);
+                free(per);
+                break;
+            }
             case VKHIP_OP_COL2IM: {
                 vkhip_unfold p;
                 memcpy(&p, nd->params, sizeof p);

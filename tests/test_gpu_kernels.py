@@ -338,6 +338,50 @@ def test_implicit_weight_grad_is_bit_identical_to_gemm_on_cols(hip, shape, cout,
         assert normwise_rel_err(got, ref) <= gemm_tolerance(L)
 
 
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil",
+                         CONVS + [((8, 16, 16, 16), 24, (3, 3), (1, 1), (1, 1), (1, 1)),
+                                  ((3, 5, 12, 16), 7, (5, 5), (1, 1), (2, 2), (1, 1))])
+def test_weight_grad_sum_is_the_batch_sum_of_the_products(hip, shape, cout, kernel, stride, pad,
+                                                          dil):
+    """vkhip_conv2d_weight_grad_sum: with out_h*out_w a multiple of 32 the batch
+    is folded into the product's K axis (K = N*out_h*out_w) -- within the GEMM
+    tolerance for that K of the per-image products + batch sum and of the
+    oracle, whose graph it replaces; otherwise it runs that graph and gives
+    its bits."""
+    rng = np.random.default_rng(SEED + 5 * shape[1])
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    n = shape[0]
+    oh = ops.window_count(shape[2], kernel[0], stride[0], pad[0], dil[0])
+    ow = ops.window_count(shape[3], kernel[1], stride[1], pad[1], dil[1])
+    L = oh * ow
+    g = rng.standard_normal((n, cout, oh, ow)).astype(np.float32)
+    print(f"weight_grad_sum x={shape} cout={cout} L={L}", flush=True)
+    got = ops.conv2d_weight_grad_sum(dev(x), dev(g), kernel, stride, pad, dil).numpy()
+    per = ops.conv2d_weight_grad(dev(x), dev(g), kernel, stride, pad, dil)
+    want = ops.sum(per, [0]).numpy()
+    ck = shape[1] * kernel[0] * kernel[1]
+    assert got.shape == (cout, ck)
+    if L % 32:
+        assert got.tobytes() == want.tobytes()
+    else:
+        assert normwise_rel_err(got, want) <= gemm_tolerance(n * L)
+    if n * cout * L * ck <= 1 << 27:
+        cols = np.ascontiguousarray(np.swapaxes(O.im2col(x, kernel, stride, pad, dil), 1, 2))
+        ref = O.sum(O.matmul(g.reshape(n, cout, L), cols), [0])
+        assert normwise_rel_err(got, ref) <= gemm_tolerance(n * L)
+
+
+def test_weight_grad_sum_edges(hip):
+    """An empty batch gives zeros; a gradient of the wrong extent is refused."""
+    x = np.ones((0, 2, 8, 8), np.float32)
+    g = np.ones((0, 3, 8, 8), np.float32)
+    got = ops.conv2d_weight_grad_sum(dev(x), dev(g), 3, 1, 1).numpy()
+    assert got.shape == (3, 18) and not got.any()
+    x = np.ones((2, 2, 8, 8), np.float32)
+    with pytest.raises(ValueError):
+        ops.conv2d_weight_grad_sum(dev(x), dev(np.ones((2, 3, 7, 8), np.float32)), 3, 1, 1)
+
+
 def test_implicit_conv_strided_image(hip):
     """A channels-last image handed over as an NCHW view, and an image whose
     batch stride leaves a gap between samples."""

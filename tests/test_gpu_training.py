@@ -132,16 +132,26 @@ def test_conv_node_on_device_is_bit_identical_to_the_graph(backends, shape, cout
                                                            pad, dil):
     """On the device, conv2d as one CONV2D node (implicit-im2col GEMM) gives
     the im2col + matmul graph's output and gradients bit for bit; against the
-    oracle both are within the GEMM tolerance."""
+    oracle both are within the GEMM tolerance. With the weight gradient as one
+    batch-summed node (the batch folded into the product's K axis when
+    out_h*out_w is a multiple of 32) the output, dX and bias gradient keep
+    those bits and dW is within the GEMM tolerance for K = N*out_h*out_w."""
     dev, cpu = backends
     rng = np.random.default_rng(SEED + 7)
     x = rng.uniform(-1, 1, shape).astype(np.float32)
     w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
     bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
-    node = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True)
+    node = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True, fold=False)
     graph = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=False)
     for got, want in zip(node, graph):
         assert got.tobytes() == want.tobytes()
+    folded = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True, fold=True)
+    for i in (0, 1, 3):
+        assert folded[i].tobytes() == graph[i].tobytes()
+    positions = node[0][0, 0].size
+    assert normwise_rel_err(folded[2], graph[2]) <= gemm_tolerance(shape[0] * positions)
+    if positions % 32:
+        assert folded[2].tobytes() == graph[2].tobytes()
     if shape[0] <= 4:
         ref = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True)
         ck = shape[1] * kernel[0] * kernel[1]

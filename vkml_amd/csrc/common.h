@@ -29,8 +29,10 @@ struct Context {
     vkhip_caps caps{};
     // Split-K partials workspace, grown on demand and released stream-ordered
     // (reference grows its own the same way, vulkan_backend.cpp:899-919).
-    float* ws = nullptr;
-    size_t ws_bytes = 0;
+    // slot 0: split-K partials and reduction partials; slot 1: a node's own
+    // temporaries (which may hold data across a GEMM that uses slot 0)
+    float* ws[2] = {nullptr, nullptr};
+    size_t ws_bytes[2] = {0, 0};
     int ws_pins = 0;               // captured graphs holding the workspace blocks
     void* ws_retired[64] = {};     // blocks replaced while pinned, freed at the last unpin
     int ws_retired_count = 0;
@@ -52,8 +54,12 @@ Context& ctx();
 // Returns VKHIP_OK or a failure code with the message set.
 int require_ready();
 
-// Workspace of at least `bytes` on the current stream.
-int workspace(size_t bytes, float** out);
+// Workspace of at least `bytes` on the current stream (slot 0; slot 1 is
+// node_temporary's).
+int workspace(size_t bytes, float** out, int slot = 0);
+// A node's temporary of at least `bytes` (workspace slot 1): valid until the
+// next node that asks for one; work using it is ordered on the stream.
+inline int node_temporary(size_t bytes, float** out) { return workspace(bytes, out, 1); }
 // While pinned (a captured HIP graph holds the current blocks), a workspace
 // that must grow gets a new block and keeps the old one until the last pin
 // goes, and the implicit-im2col row tables are not evicted.

@@ -96,7 +96,11 @@ __device__ __forceinline__ void tile_of(const GemmArgs& g, uint32_t& tm, uint32_
 //        into LDS by buffer loads (no registers, no LDS stores), rows of BK
 //        floats whose 16-byte groups are XOR-swizzled by row (group g of row r
 //        at g ^ (r & 7)) so the MFMA operand reads stay conflict-free.
-enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4, IMGT = 5, KCD = 6 };
+//   IMGTB the weight gradient summed over the batch: IMGT with the batch
+//        folded into K (k = n * L + position, L a multiple of BK), as B of one
+//        product [Cout, N*L] x [N*L, C*kh*kw] (a kernel-level mode: the tile
+//        loader is IMGT's, given image n's resource and positions per K-tile).
+enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4, IMGT = 5, KCD = 6, IMGTB = 7 };
 
 // The B operand of a convolution read straight from the image (implicit
 // im2col): element (row, pos) of image n's cols matrix [C*kh*kw, out_h*out_w]
@@ -111,6 +115,8 @@ struct Im2colB {
     int32_t H, W, kh, kw, kk, strh, strw, padh, padw, dilh, dilw, ow;
     FastDiv div_kk, div_kw, div_ow;  // by kh*kw, kw, out_w
     const int32_t* rows;             // row table (see below)
+    uint32_t L, images;              // IMGTB: positions per image, images
+    FastDiv div_L;                   // IMGTB: by L
 };
 
 // The map splits into a part that depends only on the output position (one
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
     constexpr int NI = WN / 32;
     constexpr int QN = BK / 8;  // groups of four MFMA k-steps per K-tile
     using LA = TileLoader<BM, BK, AMODE>;
-    using LB = TileLoader<BN, BK, BMODE>;
+    using LB = TileLoader<BN, BK, BMODE == IMGTB ? IMGT : BMODE>;
 
     __shared__ __attribute__((aligned(16))) float lds[2][(BM + BN) * LDK];
 
@@ -476,7 +482,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         outside = at.outside;
     }
     typename LB::ImgRows trows;
-    if constexpr (BMODE == IMGT) LB::img_rows(trows, im_in, col0, g.n, tid);
+    if constexpr (BMODE == IMGT || BMODE == IMGTB) LB::img_rows(trows, im_in, col0, g.n, tid);
     float* cbase = g.c + static_cast<uint64_t>(split) * g.split_stride +
                    static_cast<uint64_t>(z) * g.m * g.n;
 
@@ -518,6 +524,21 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         } else if constexpr (BMODE == IMGT) {
             LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
             LB::load_imgt(rb, img, im_in, trows, kt * BK, g.k, tid);
+        } else if constexpr (BMODE == IMGTB) {
+            // K-tile kt is positions p0 .. p0 + BK - 1 of image n (L is a
+            // multiple of BK). The tile after the last, loaded and unused,
+            // stays on the last image with positions past L: every load then
+            // reads in range or returns 0.
+            const uint32_t k0 = kt * BK;
+            uint32_t n = im_in.div_L.div(k0);
+            n = n < im_in.images ? n : im_in.images - 1u;
+            const uint32_t p0 = k0 - n * im_in.L;
+            LA::load_clamped(ra, abase + static_cast<int64_t>(n) * g.sa1, g.sam, row0, g.m, p0, im_in.L,
+                             tid);
+            const __amdgpu_buffer_rsrc_t imgn = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(im_in.x + static_cast<int64_t>(n) * im_in.sn), 0,
+                static_cast<int32_t>(0x80000000u), 0x00020000);
+            LB::load_imgt(rb, imgn, im_in, trows, p0, im_in.L, tid);
         } else if (rows_in && (kt + 1) * BK <= g.k) {
             LA::template load<false>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
             LB::template load<false>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
@@ -541,7 +562,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         // The implicit-im2col loads have no branches: they are issued every
         // iteration (the last one's are in range and unused) so that they sit
         // in the same block as the MFMAs and interleave with them.
-        if constexpr (BMODE == IMG || BMODE == IMGT) {
+        if constexpr (BMODE == IMG || BMODE == IMGT || BMODE == IMGTB) {
             load_tile(kt + 1, cur ^ 1);
             // Keep every load of the next tile ahead of this tile's MFMAs, so
             // that their latency hides behind all of them.
@@ -1945,6 +1966,115 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
     if (splits > 1) return launch_split_k_reduce(target, out, out_elems, splits);
     return VKHIP_OK;
 }
+
+int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst);
+
+// The weight gradient summed over the batch, out [Cout, C*kh*kw] = sum_n
+// grad[n] @ im2col(x[n])^T: the reference graph's per-image products and
+// batch sum (autograd.cpp:548-553 over ops.cpp:662-705, then the broadcast
+// adjoint sum, autograd.cpp:84-116).
+//  - FAST numerics with L = out_h*out_w a multiple of 32: ONE product with the
+//    batch folded into K (k = n*L + position), [Cout, N*L] x [N*L, C*kh*kw],
+//    the columns gathered from each image (load mode IMGTB), split-K planned
+//    like any product: no [N, Cout, C*kh*kw] intermediate and no separate
+//    batch sum. Its K order differs from the graph's (within the GEMM
+//    tolerance, not the same bits).
+//  - EXACT numerics, or L not a multiple of 32: the per-image products
+//    (conv2d_weight_grad, exact in the exact mode) into a node temporary,
+//    then the batch sum's pairwise reduction: the graph's bits.
+int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* gr,
+                           const vkhip_operand& gd, float* out, const vkhip_unfold& p) {
+    if (static_cast<int64_t>(xd.ne[2]) != p.image_h || static_cast<int64_t>(xd.ne[3]) != p.image_w)
+        return fail(VKHIP_ERR_INVALID, "conv2d weight grad sum: image is %ux%u but the geometry says %dx%d",
+                    xd.ne[2], xd.ne[3], p.image_h, p.image_w);
+    Im2colB im{};
+    const int geo = make_im2col(p, xd.ne[1], xd.nb + 1, im);
+    if (geo != VKHIP_OK) return geo;
+    const int64_t oh = (static_cast<int64_t>(p.image_h) + 2 * p.pad_h -
+                        (static_cast<int64_t>(p.dilation_h) * (p.kernel_h - 1) + 1)) / p.stride_h + 1;
+    const uint64_t L = static_cast<uint64_t>(oh) * im.ow;
+    const uint64_t batch = xd.ne[0];
+    const uint64_t ck = static_cast<uint64_t>(xd.ne[1]) * p.kernel_h * p.kernel_w;
+    const uint32_t cout = gd.ne[2];
+    if (gd.ne[0] != 1 || gd.ne[1] != batch || static_cast<uint64_t>(gd.ne[3]) != L)
+        return fail(VKHIP_ERR_INVALID, "conv2d weight grad sum: gradient must be [N, Cout, %llu]",
+                    static_cast<unsigned long long>(L));
+    if (gd.nb[3] != 1 && L != 1)
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d weight grad sum: gradient positions must be contiguous");
+    if (cout == 0 || ck == 0) return VKHIP_OK;
+    if (batch == 0 || L == 0) return launch_zero_f32(out, static_cast<uint64_t>(cout) * ck);
+    const uint64_t k64 = batch * L;
+    if (ctx().exact_math || L % 32 != 0 || k64 > 0xffffffffull || ck > 0xffffffffull) {
+        publish("matmul.kernel", "conv2d_weight_grad_sum", "per_image_products_then_batch_sum",
+                "batch_folded_into_k", ctx().exact_math ? "exact numerics mode"
+                                                        : "positions per image not a multiple of 32",
+                static_cast<int64_t>(L), static_cast<int64_t>(batch));
+        float* tmp = nullptr;
+        const uint64_t per = static_cast<uint64_t>(cout) * ck;
+        int st = node_temporary(batch * per * sizeof(float), &tmp);
+        if (st != VKHIP_OK) return st;
+        st = conv2d_weight_grad(x, xd, gr, gd, tmp, p);
+        if (st != VKHIP_OK) return st;
+        vkhip_operand td;
+        td.ne[0] = 1;
+        td.ne[1] = static_cast<uint32_t>(batch);
+        td.ne[2] = cout;
+        td.ne[3] = static_cast<uint32_t>(ck);
+        td.nb[0] = 0;
+        td.nb[1] = static_cast<int64_t>(per);
+        td.nb[2] = static_cast<int64_t>(ck);
+        td.nb[3] = 1;
+        return launch_reduce(VKHIP_REDUCE_SUM, tmp, td, 0x2u, out);
+    }
+    const uint32_t m = cout, n = static_cast<uint32_t>(ck), k = static_cast<uint32_t>(k64);
+    uint32_t splits, chunk;
+    TileChoice tile;
+    gemm_plan(1, m, n, k, 0, splits, chunk, tile);
+    publish("matmul.kernel", "conv2d_weight_grad_sum",
+            tile.bm == 128 ? "gemm_mfma_128x128_batch_folded" : "gemm_mfma_64x64_batch_folded",
+            "per_image_products_then_batch_sum", "the batch folded into K: one product, no intermediate",
+            static_cast<int64_t>(tile.tiles), static_cast<int64_t>(splits));
+    im.x = x;
+    im.sn = xd.nb[0];
+    im.L = static_cast<uint32_t>(L);
+    im.images = static_cast<uint32_t>(batch);
+    im.div_L = FastDiv(static_cast<uint32_t>(L));
+
+    GemmArgs g{};
+    g.a = gr;
+    g.b = x;
+    g.sa1 = gd.nb[1];  // image stride of the gradient
+    g.sam = gd.nb[2];
+    g.sak = 1;
+    g.b1 = 1;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.tiles_m = ceil_div(m, tile.bm);
+    g.tiles_n = ceil_div(n, tile.bn);
+    g.ktiles = ceil_div(k, 32);
+    g.chunk = chunk;
+    g.a_vec = reinterpret_cast<uintptr_t>(gr) % 16 == 0 && g.sam % 4 == 0 && g.sa1 % 4 == 0;
+    const int amode = g.a_vec ? KCV : KCS;
+    const uint64_t out_elems = static_cast<uint64_t>(m) * n;
+    float* target = out;
+    if (splits > 1) {
+        float* ws = nullptr;
+        int st = workspace(out_elems * splits * sizeof(float), &ws);
+        if (st != VKHIP_OK) return st;
+        target = ws;
+    }
+    g.c = target;
+    g.split_stride = splits > 1 ? out_elems : 0;
+    int st;
+    if (tile.bm == 128)
+        st = launch_conv_tiles<128, 128, 64, 64, IMGTB>(g, im, 1, splits, amode);
+    else
+        st = launch_conv_tiles<64, 64, 32, 32, IMGTB>(g, im, 1, splits, amode);
+    if (st != VKHIP_OK) return st;
+    if (splits > 1) return launch_split_k_reduce(target, out, out_elems, splits);
+    return VKHIP_OK;
+}
 }  // namespace vkhip
 
 // ---- C ABI -------------------------------------------------------------------
@@ -2014,6 +2144,16 @@ extern "C" int vkhip_conv2d_weight_grad(const float* x, const vkhip_operand* x_d
     vkhip::Unit unit("conv2d_weight_grad");
     if (!x_desc || !grad_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d weight grad: null argument");
     return vkhip::conv2d_weight_grad(x, *x_desc, grad, *grad_desc, out, *p);
+}
+
+extern "C" int vkhip_conv2d_weight_grad_sum(const float* x, const vkhip_operand* x_desc,
+                                            const float* grad, const vkhip_operand* grad_desc,
+                                            float* out, const vkhip_unfold* p) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("conv2d_weight_grad_sum");
+    if (!x_desc || !grad_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d_weight_grad_sum: null argument");
+    return vkhip::conv2d_weight_grad_sum(x, *x_desc, grad, *grad_desc, out, *p);
 }
 
 extern "C" int vkhip_im2col_offset(const vkhip_unfold* p, uint32_t channels, const int64_t* x_strides,

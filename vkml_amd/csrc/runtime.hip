@@ -23,6 +23,8 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
                    const vkhip_operand& wd, float* out, const vkhip_unfold& p);
 int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
                        const vkhip_operand& gd, float* out, const vkhip_unfold& p);
+int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* gr,
+                           const vkhip_operand& gd, float* out, const vkhip_unfold& p);
 int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t* labels,
                          const float* g_out, float* out, uint32_t rows, uint32_t n, int backward);
 int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uint32_t out_h,
@@ -90,28 +92,29 @@ int require_ready() {
     return VKHIP_OK;
 }
 
-int workspace(size_t bytes, float** out) {
+int workspace(size_t bytes, float** out, int slot) {
     std::lock_guard<std::mutex> lk(g_mu);
     Context& c = ctx();
-    if (c.ws_bytes < bytes) {
-        if (c.ws && c.ws_pins > 0) {
+    if (slot < 0 || slot > 1) return fail(VKHIP_ERR_INVALID, "workspace: slot %d", slot);
+    if (c.ws_bytes[slot] < bytes) {
+        if (c.ws[slot] && c.ws_pins > 0) {
             // a captured graph still addresses this block: keep it
             if (c.ws_retired_count == static_cast<int>(sizeof c.ws_retired / sizeof c.ws_retired[0]))
                 return fail(VKHIP_ERR_UNSUPPORTED,
                             "workspace: too many blocks held by captured graphs (destroy some programs)");
-            c.ws_retired[c.ws_retired_count++] = c.ws;
-        } else if (c.ws) {
-            VKHIP_HIP(hipFreeAsync(c.ws, c.stream));
+            c.ws_retired[c.ws_retired_count++] = c.ws[slot];
+        } else if (c.ws[slot]) {
+            VKHIP_HIP(hipFreeAsync(c.ws[slot], c.stream));
         }
-        c.ws = nullptr;
-        c.ws_bytes = 0;
+        c.ws[slot] = nullptr;
+        c.ws_bytes[slot] = 0;
         void* p = nullptr;
         if (hipMallocAsync(&p, bytes, c.stream) != hipSuccess)
-            return fail(VKHIP_ERR_OOM, "split-K workspace of %zu bytes could not be allocated", bytes);
-        c.ws = static_cast<float*>(p);
-        c.ws_bytes = bytes;
+            return fail(VKHIP_ERR_OOM, "workspace of %zu bytes could not be allocated", bytes);
+        c.ws[slot] = static_cast<float*>(p);
+        c.ws_bytes[slot] = bytes;
     }
-    *out = c.ws;
+    *out = c.ws[slot];
     return VKHIP_OK;
 }
 
@@ -287,6 +290,16 @@ static int supports_node(const vkhip_node& nd) {
                    gr.nb[2] == gr.ne[3] &&
                    static_cast<int64_t>(p.kernel_h) * p.kernel_w <= 63;
         }
+        case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: {
+            const vkhip_tensor& x = nd.src[0];
+            const vkhip_tensor& gr = nd.src[1];
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return nd.n_src == 2 && is_f32(x) && is_f32(gr) && is_f32(o) && x.ndim == 4 &&
+                   gr.ndim == 4 && o.ndim == 2 && contiguous(o) && gr.ne[0] == x.ne[0] &&
+                   o.ne[0] == gr.ne[1] && gr.nb[3] == 1 && gr.nb[2] == gr.ne[3] &&
+                   static_cast<int64_t>(p.kernel_h) * p.kernel_w <= 63;
+        }
         case VKHIP_OP_CROSS_ENTROPY:
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
             const vkhip_tensor& x = nd.src[0];
@@ -459,6 +472,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: return "cross_entropy_backward";
         case VKHIP_OP_CONV2D: return "conv2d";
         case VKHIP_OP_CONV2D_WEIGHT_GRAD: return "conv2d_weight_grad";
+        case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: return "conv2d_weight_grad_sum";
         case VKHIP_OP_MIN: return "min";
         case VKHIP_OP_ARGMIN: return "argmin";
         case VKHIP_OP_FULL: return "full";
@@ -601,6 +615,29 @@ static int compute_node(const vkhip_node& nd) {
                                       static_cast<const float*>(gr.data), gd,
                                       static_cast<float*>(nd.out.data), p);
         }
+        case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            const vkhip_tensor& gr = nd.src[1];
+            const int64_t L = gr.ne[2] * gr.ne[3];
+            const int64_t ck = nd.src[0].ne[1] * static_cast<int64_t>(p.kernel_h) * p.kernel_w;
+            if (nd.out.ne[1] != ck)
+                return fail(VKHIP_ERR_INVALID, "conv2d weight grad sum: output has %lld columns, want %lld",
+                            static_cast<long long>(nd.out.ne[1]), static_cast<long long>(ck));
+            if (L > 0xffffffffll) return fail(VKHIP_ERR_UNSUPPORTED, "conv2d weight grad sum: too many positions");
+            vkhip_operand gd;
+            gd.ne[0] = 1;
+            gd.ne[1] = static_cast<uint32_t>(gr.ne[0]);
+            gd.ne[2] = static_cast<uint32_t>(gr.ne[1]);
+            gd.ne[3] = static_cast<uint32_t>(L);
+            gd.nb[0] = 0;
+            gd.nb[1] = gr.nb[0];
+            gd.nb[2] = gr.nb[1];
+            gd.nb[3] = 1;
+            return conv2d_weight_grad_sum(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
+                                          static_cast<const float*>(gr.data), gd,
+                                          static_cast<float*>(nd.out.data), p);
+        }
         case VKHIP_OP_CROSS_ENTROPY:
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
             const bool back = nd.op == VKHIP_OP_CROSS_ENTROPY_BACKWARD;
@@ -703,10 +740,10 @@ extern "C" int vkhip_shutdown(void) {
     std::lock_guard<std::mutex> lk(vkhip::g_mu);
     vkhip::Context& c = ctx();
     if (!c.ready) return VKHIP_OK;
-    if (c.ws) {
-        VKHIP_HIP(hipFreeAsync(c.ws, c.stream));
-        c.ws = nullptr;
-        c.ws_bytes = 0;
+    for (int slot = 0; slot < 2; ++slot) {
+        if (c.ws[slot]) VKHIP_HIP(hipFreeAsync(c.ws[slot], c.stream));
+        c.ws[slot] = nullptr;
+        c.ws_bytes[slot] = 0;
     }
     for (int i = 0; i < c.ws_retired_count; ++i) VKHIP_HIP(hipFreeAsync(c.ws_retired[i], c.stream));
     c.ws_retired_count = 0;

@@ -241,6 +241,39 @@ def conv2d_weight_grad(x: DeviceArray, grad: DeviceArray, kernel, stride=1, padd
     return out
 
 
+def conv2d_weight_grad_sum(x: DeviceArray, grad: DeviceArray, kernel, stride=1, padding=0,
+                           dilation=1, out: DeviceArray | None = None) -> DeviceArray:
+    """The convolution's weight gradient summed over the batch, [Cout, C*kh*kw]
+    = sum_n grad[n] @ im2col(x[n])^T: conv2d's backward for the weight
+    (autograd.cpp:548-553) followed by the broadcast adjoint's batch sum
+    (autograd.cpp:84-116). Fast numerics with out_h*out_w a multiple of 32 run
+    one product with the batch folded into K; otherwise the per-image products
+    and the batch sum."""
+    _f32(x, "conv2d_weight_grad_sum")
+    _f32(grad, "conv2d_weight_grad_sum")
+    if x.ndim != 4 or grad.ndim != 4 or grad.shape[0] != x.shape[0]:
+        raise ValueError("conv2d_weight_grad_sum expects an NCHW image and an [N, Cout, oh, ow] gradient")
+    kh, kw = _pair(kernel)
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw = _pair(dilation)
+    n, c, h, w = x.shape
+    oh, ow = window_count(h, kh, sh, ph, dh), window_count(w, kw, sw, pw, dw)
+    if grad.shape[2:] != (oh, ow):
+        raise ValueError(f"conv2d_weight_grad_sum: gradient is {grad.shape[2:]}, geometry gives {(oh, ow)}")
+    if not grad.is_contiguous():
+        from .device import contiguous
+        grad = contiguous(grad)
+    cout = grad.shape[1]
+    out = _out(out, (cout, c * kh * kw))
+    u = _lib.unfold((kh, kw), (sh, sw), (ph, pw), (dh, dw), (h, w))
+    gd = _lib.operand((1, n, cout, oh * ow), (0, cout * oh * ow, oh * ow, 1))
+    check(_lib.load().vkhip_conv2d_weight_grad_sum(c_void_p(x.ptr), byref(x.operand()),
+                                                   c_void_p(grad.ptr), byref(gd), c_void_p(out.ptr),
+                                                   byref(u)), "conv2d_weight_grad_sum")
+    return out
+
+
 # ---- softmax and reductions --------------------------------------------------------------
 
 def _axis4(x: DeviceArray, axis: int) -> int:

@@ -956,6 +956,14 @@ def _accumulate(grads: dict, node: Node, g: Tensor) -> None:
         grads[key] = (node, g)
 
 
+# The conv2d weight gradient as one CONV2D_WEIGHT_GRAD_SUM node (True) or as
+# CONV2D_WEIGHT_GRAD per image followed by the batch SUM node, the reference
+# graph's shape (False). The oracle gives both the same bits; the device's
+# fast numerics fold the batch into the product's K axis for the former,
+# which stays within the GEMM tolerance of the graph, not bit-identical.
+FOLD_CONV_WEIGHT_GRAD = True
+
+
 def reduce_to_shape(g: Tensor, target_dims) -> Tensor:
     """Sums g down to target_dims, undoing a broadcast (autograd.cpp:84-116)."""
     gd = list(g.shape)
@@ -1074,13 +1082,21 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
             dcols = matmul(flat4.transpose(-2, -1), g4).reshape(n_, ck, oh * ow)
             _accumulate(grads, a, col2im(dcols, hw, kernel, stride, pad, dil))
         if b.requires_grad:
-            # The per-image products g4 @ cols4^T as one CONV2D_WEIGHT_GRAD
-            # node (the columns gathered from the image, same bits), then
-            # the reference's batch sum.
-            wg = Node(OP["CONV2D_WEIGHT_GRAD"], (n_, cout, ck), np.float32, a.backend,
-                      [a, grad.contiguous().node], params=node.params)
-            prod = Tensor(wg).reshape(1, n_, cout, ck)
-            dflat = reduce_to_shape(prod, (cout, ck))
+            if FOLD_CONV_WEIGHT_GRAD:
+                # sum_n g4 @ cols4^T as one node: the device folds the batch
+                # into the product's K axis (no [N, Cout, CK] intermediate);
+                # the oracle computes the per-image products and batch sum.
+                wg = Node(OP["CONV2D_WEIGHT_GRAD_SUM"], (cout, ck), np.float32, a.backend,
+                          [a, grad.contiguous().node], params=node.params)
+                dflat = Tensor(wg)
+            else:
+                # The per-image products g4 @ cols4^T as one CONV2D_WEIGHT_GRAD
+                # node (the columns gathered from the image, same bits), then
+                # the reference's batch sum.
+                wg = Node(OP["CONV2D_WEIGHT_GRAD"], (n_, cout, ck), np.float32, a.backend,
+                          [a, grad.contiguous().node], params=node.params)
+                prod = Tensor(wg).reshape(1, n_, cout, ck)
+                dflat = reduce_to_shape(prod, (cout, ck))
             _accumulate(grads, b, dflat.reshape(b.shape))
     elif op == OP["CROSS_ENTROPY"]:
         g = Node(OP["CROSS_ENTROPY_BACKWARD"], a.shape, np.float32, a.backend,
