@@ -417,6 +417,20 @@ def case_conv(name, hip, ops, timer, rng, out):
         "ms": round(ms_f, 5), "tflops": round(flops / ms_f / 1e9, 2),
         "frac_of_peak": round(flops / ms_f / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
         "per_image_then_sum_ms": round(ms_s, 5), "speedup_vs_per_image": round(ms_s / ms_f, 3)}
+    # dX: the reference graph's TN product into the column matrix and col2im,
+    # against one convolution of the gradient with the flipped weight
+    dx = DeviceArray(xs_shape, np.float32)
+
+    def tn_then_col2im(i):
+        ops.matmul(wf.transpose(-2, -1), g4, out=cols.reshape(1, n_, ck, L))
+        ops.col2im(cols, (h, w_), 3, 1, 1, out=dx)
+
+    ms_t = time_batch(tn_then_col2im, timer, 20)
+    ms_f = time_batch(lambda i: ops.conv2d_input_grad(g, wt, (h, w_), 1, 1, out=dx), timer, 20)
+    out[name.replace("conv_", "conv_dx_")] = {
+        "ms": round(ms_f, 5), "tflops": round(flops / ms_f / 1e9, 2),
+        "frac_of_peak": round(flops / ms_f / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+        "tn_then_col2im_ms": round(ms_t, 5), "speedup_vs_tn_col2im": round(ms_t / ms_f, 3)}
 
 
 SOFTMAX_CASES = {"softmax_4096x1000": ((4096, 1000), 20), "softmax_256x32768": ((256, 32768), 10)}

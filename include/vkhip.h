@@ -154,7 +154,16 @@ enum vkhip_op {
      * batch SUM. FAST numerics fold the batch into the product's K axis (no
      * intermediate, within the GEMM tolerance of the graph); EXACT numerics
      * give the graph's bits. */
-    VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM = 101
+    VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM = 101,
+    /* src0 grad [N,Cout,out_h,out_w] (positions unit-stride), src1 weight
+     * [Cout,C,kh,kw] or [Cout,C*kh*kw] (rows contiguous), params the forward's
+     * vkhip_unfold -> out [N,C,H,W] contiguous: the conv2d input gradient,
+     * the value of col2im(flat_weight^T @ grad). FAST numerics with unit
+     * strides compute it as one convolution of grad with the flipped,
+     * transposed weight when C >= 32 (no column matrix; within the GEMM
+     * tolerance of the graph); otherwise the TN product and col2im (the
+     * graph's bits). */
+    VKHIP_OP_CONV2D_INPUT_GRAD = 102
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */
@@ -383,6 +392,17 @@ int vkhip_conv2d_weight_grad(const float* x, const vkhip_operand* x_desc, const 
  * for vkhip_conv2d_weight_grad. FAST numerics with out_h*out_w a multiple of
  * 32: one product with the batch folded into K. Otherwise the per-image
  * products and the batch sum (the graph's bits). */
+/* The convolution input gradient (VKHIP_OP_CONV2D_INPUT_GRAD): out [N,C,H,W]
+ * contiguous = col2im(flat_weight^T @ grad[n]), what the reference's conv2d
+ * backward computes for x through the matmul and im2col adjoints
+ * (autograd.cpp:548-553, ops.cpp:662-705). grad: rank-4 [N, Cout, out_h,
+ * out_w] with unit position strides; w: [1,1,Cout,C*kh*kw] rows contiguous;
+ * p: the forward's geometry. FAST numerics with unit strides,
+ * dilation*(k-1) >= pad and C >= 32: one implicit-im2col convolution of grad
+ * with the weight flipped and transposed (pad dilation*(k-1) - pad).
+ * Otherwise the TN product into a column matrix, then col2im. */
+int vkhip_conv2d_input_grad(const float* grad, const vkhip_operand* grad_desc, const float* w,
+                            const vkhip_operand* w_desc, float* out, const vkhip_unfold* p);
 int vkhip_conv2d_weight_grad_sum(const float* x, const vkhip_operand* x_desc, const float* grad,
                                  const vkhip_operand* grad_desc, float* out, const vkhip_unfold* p);
 

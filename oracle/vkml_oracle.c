@@ -690,6 +690,29 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 free(cols);
                 break;
             }
+            case VKHIP_OP_CONV2D_INPUT_GRAD: {
+                /* The reference conv2d backward's input gradient
+                 * (autograd.cpp:548-553 over ops.cpp:662-705): the TN product
+                 * flat_weight^T [C*kh*kw, Cout] @ grad[n] [Cout, L] into the
+                 * column matrix, then col2im (the im2col adjoint). */
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                const vkhip_tensor* g = &nd->src[0];
+                const vkhip_tensor* w = &nd->src[1];
+                const int64_t N = g->ne[0], cout = g->ne[1];
+                const int64_t L = g->ne[2] * g->ne[3];
+                const int64_t ck = o->ne[1] * (int64_t)p.kernel_h * p.kernel_w;
+                float* cols = (float*)malloc(sizeof(float) * (size_t)(N * ck * L + 1));
+                if (!cols) return VKHIP_ERR_OOM;
+                vkhip_operand ad = {{1, (uint32_t)N, (uint32_t)ck, (uint32_t)cout},
+                                    {0, 0, 1, w->nb[0]}};
+                vkhip_operand bd = {{1, (uint32_t)N, (uint32_t)cout, (uint32_t)L},
+                                    {0, g->nb[0], g->nb[1], 1}};
+                or_matmul((const float*)w->data, &ad, (const float*)g->data, &bd, cols, threads);
+                or_col2im(cols, (float*)o->data, (uint32_t)N, (uint32_t)o->ne[1], &p, threads);
+                free(cols);
+                break;
+            }
             case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: {
                 /* The same per-image products, then the broadcast adjoint's
                  * batch sum (autograd.cpp:84-116): the graph's value, per

@@ -91,20 +91,25 @@ def ce_loss_and_grad(backend, logits, labels, fused):
         T.FUSED_CROSS_ENTROPY = prev
 
 
-def conv_loss_and_grads(backend, x, w, bias, stride, pad, dil, implicit, x_grad=True, fold=None):
+def conv_loss_and_grads(backend, x, w, bias, stride, pad, dil, implicit, x_grad=True, fold=None,
+                        fused_dx=None):
     """sum(conv2d(x, w, bias) * probe) and the gradients of x, w and bias on
     `backend`, with conv2d built as one CONV2D node (implicit=True) or as the
     reference's im2col + matmul graph. `probe` is a fixed pattern so every
     output position carries a different weight into the gradients. `fold`
     overrides FOLD_CONV_WEIGHT_GRAD (the weight gradient as one batch-summed
-    node, or per-image node + batch SUM) when not None."""
+    node, or per-image node + batch SUM) and `fused_dx` FUSED_CONV_INPUT_GRAD
+    (the input gradient as one node, or TN product + COL2IM) when not None."""
     from vkml_amd import tensor as T
 
     prev = T.IMPLICIT_CONV
     prev_fold = T.FOLD_CONV_WEIGHT_GRAD
+    prev_dx = T.FUSED_CONV_INPUT_GRAD
     T.IMPLICIT_CONV = implicit
     if fold is not None:
         T.FOLD_CONV_WEIGHT_GRAD = fold
+    if fused_dx is not None:
+        T.FUSED_CONV_INPUT_GRAD = fused_dx
     try:
         xt = T.tensor(x, requires_grad=x_grad, backend=backend)
         wt = T.tensor(w, requires_grad=True, backend=backend)
@@ -118,6 +123,7 @@ def conv_loss_and_grads(backend, x, w, bias, stride, pad, dil, implicit, x_grad=
     finally:
         T.IMPLICIT_CONV = prev
         T.FOLD_CONV_WEIGHT_GRAD = prev_fold
+        T.FUSED_CONV_INPUT_GRAD = prev_dx
 
 
 def relu_inputs(shape, seed):

@@ -371,6 +371,44 @@ def test_weight_grad_sum_is_the_batch_sum_of_the_products(hip, shape, cout, kern
         assert normwise_rel_err(got, ref) <= gemm_tolerance(n * L)
 
 
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil",
+                         CONVS + [((8, 16, 16, 16), 24, (3, 3), (1, 1), (1, 1), (1, 1)),
+                                  ((2, 3, 9, 9), 4, (3, 3), (1, 1), (3, 3), (1, 1)),
+                                  ((3, 5, 12, 16), 7, (5, 5), (1, 1), (2, 2), (1, 1)),
+                                  ((2, 40, 12, 10), 16, (5, 3), (1, 1), (2, 1), (1, 2)),
+                                  ((2, 32, 8, 8), 8, (1, 1), (1, 1), (0, 0), (1, 1))])
+def test_input_grad_matches_the_tn_product_and_col2im(hip, shape, cout, kernel, stride, pad, dil):
+    """vkhip_conv2d_input_grad against the reference lowering on the device
+    (the TN product flat_weight^T @ grad into columns, then col2im) and the
+    oracle: unit strides with pad <= dilation*(k-1) run the convolution of the
+    gradient with the flipped, transposed weight (within the GEMM tolerance
+    for K = Cout*kh*kw) when there are at least 32 input channels; other
+    geometries run that lowering and give its bits."""
+    rng = np.random.default_rng(SEED + 7 * shape[1])
+    n, c, h, w = shape
+    oh = ops.window_count(h, kernel[0], stride[0], pad[0], dil[0])
+    ow = ops.window_count(w, kernel[1], stride[1], pad[1], dil[1])
+    g = rng.standard_normal((n, cout, oh, ow)).astype(np.float32)
+    wt = rng.uniform(-0.5, 0.5, (cout, c) + kernel).astype(np.float32)
+    print(f"input_grad x={shape} cout={cout} k={kernel} s={stride} p={pad} d={dil}", flush=True)
+    got = ops.conv2d_input_grad(dev(g), dev(wt), (h, w), stride, pad, dil).numpy()
+    ck, L = c * kernel[0] * kernel[1], oh * ow
+    wf = dev(wt.reshape(1, 1, cout, ck)).broadcast_to((1, n, cout, ck))
+    dcols = ops.matmul(wf.transpose(-2, -1), dev(g.reshape(1, n, cout, L))).reshape(n, ck, L)
+    want = ops.col2im(dcols, (h, w), kernel, stride, pad, dil).numpy()
+    fused = (stride == (1, 1) and all(d * (k - 1) >= p for d, k, p in zip(dil, kernel, pad))
+             and c >= 32)
+    if fused:
+        assert normwise_rel_err(got, want) <= gemm_tolerance(cout * kernel[0] * kernel[1])
+    else:
+        assert got.tobytes() == want.tobytes()
+    if n * cout * L * ck <= 1 << 27:
+        cols = O.matmul(np.ascontiguousarray(np.broadcast_to(wt.reshape(cout, ck).T, (n, ck, cout))),
+                        g.reshape(n, cout, L))
+        ref = O.col2im(cols, (h, w), kernel, stride, pad, dil)
+        assert normwise_rel_err(got, ref) <= gemm_tolerance(cout * kernel[0] * kernel[1])
+
+
 def test_weight_grad_sum_edges(hip):
     """An empty batch gives zeros; a gradient of the wrong extent is refused."""
     x = np.ones((0, 2, 8, 8), np.float32)

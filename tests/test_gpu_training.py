@@ -134,24 +134,33 @@ def test_conv_node_on_device_is_bit_identical_to_the_graph(backends, shape, cout
     the im2col + matmul graph's output and gradients bit for bit; against the
     oracle both are within the GEMM tolerance. With the weight gradient as one
     batch-summed node (the batch folded into the product's K axis when
-    out_h*out_w is a multiple of 32) the output, dX and bias gradient keep
-    those bits and dW is within the GEMM tolerance for K = N*out_h*out_w."""
+    out_h*out_w is a multiple of 32) and the input gradient as one node (a
+    convolution of the gradient for unit strides) the output and bias
+    gradient keep those bits, dW is within the GEMM tolerance for
+    K = N*out_h*out_w and dX for K = Cout*kh*kw."""
     dev, cpu = backends
     rng = np.random.default_rng(SEED + 7)
     x = rng.uniform(-1, 1, shape).astype(np.float32)
     w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
     bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
-    node = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True, fold=False)
+    node = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True, fold=False,
+                               fused_dx=False)
     graph = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=False)
     for got, want in zip(node, graph):
         assert got.tobytes() == want.tobytes()
-    folded = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True, fold=True)
-    for i in (0, 1, 3):
+    folded = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True, fold=True,
+                                 fused_dx=True)
+    for i in (0, 3):
         assert folded[i].tobytes() == graph[i].tobytes()
     positions = node[0][0, 0].size
     assert normwise_rel_err(folded[2], graph[2]) <= gemm_tolerance(shape[0] * positions)
     if positions % 32:
         assert folded[2].tobytes() == graph[2].tobytes()
+    window = kernel[0] * kernel[1]
+    assert normwise_rel_err(folded[1], graph[1]) <= gemm_tolerance(cout * window)
+    if (stride != (1, 1) or any(d * (k - 1) < p for d, k, p in zip(dil, kernel, pad))
+            or shape[1] < 32):
+        assert folded[1].tobytes() == graph[1].tobytes()
     if shape[0] <= 4:
         ref = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True)
         ck = shape[1] * kernel[0] * kernel[1]

@@ -192,19 +192,22 @@ def test_views_and_broadcast_resolve_by_aliasing(cpu):
 def test_conv_node_matches_the_reference_graph(cpu, shape, cout, kernel, stride, pad, dil):
     """conv2d as one CONV2D node gives the reference graph's (im2col + matmul)
     output and x / weight / bias gradients bit for bit, with the weight
-    gradient as per-image products + batch SUM or as one batch-summed node,
-    and both agree with torch's float64 convolution."""
+    gradient as per-image products + batch SUM or as one batch-summed node and
+    the input gradient as TN product + col2im or as one node, and both agree with torch's float64 convolution."""
     rng = np.random.default_rng(SEED + 7)
     x = rng.uniform(-1, 1, shape).astype(np.float32)
     w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
     bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
-    node = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True, fold=False)
-    folded = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True, fold=True)
+    node = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True, fold=False,
+                               fused_dx=False)
+    folded = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True, fold=True,
+                                 fused_dx=True)
     graph = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=False)
     for got, want in zip(node, graph):
         assert got.tobytes() == want.tobytes()
     # the batch-summed weight-gradient node is the per-image products and the
-    # batch SUM on the oracle: the same bits
+    # batch SUM on the oracle, the input-gradient node the TN product and
+    # col2im: the same bits
     for got, want in zip(folded, graph):
         assert got.tobytes() == want.tobytes()
     xt = torch.tensor(x.astype(np.float64), requires_grad=True)

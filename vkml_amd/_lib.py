@@ -33,7 +33,7 @@ OP = dict(
     MAX_POOL2D_BACKWARD=60, WHERE=64,
     # backend extensions (include/vkhip.h): the fused cross-entropy rows
     CROSS_ENTROPY=96, CROSS_ENTROPY_BACKWARD=97, CONV2D=98, CONV2D_WEIGHT_GRAD=99,
-    RELU_BACKWARD=100, CONV2D_WEIGHT_GRAD_SUM=101,
+    RELU_BACKWARD=100, CONV2D_WEIGHT_GRAD_SUM=101, CONV2D_INPUT_GRAD=102,
 )
 
 
@@ -106,6 +106,8 @@ SIGNATURES = {
     "vkhip_conv2d": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand), c_void_p,
                              POINTER(Unfold)]),
     "vkhip_conv2d_weight_grad": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand), c_void_p, POINTER(Unfold)]),
+    "vkhip_conv2d_input_grad": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand), c_void_p,
+                                        POINTER(Unfold)]),
     "vkhip_conv2d_weight_grad_sum": (c_int, [c_void_p, POINTER(Operand), c_void_p, POINTER(Operand), c_void_p,
                                              POINTER(Unfold)]),
     "vkhip_im2col_offset": (c_int, [POINTER(Unfold), c_uint32, POINTER(c_int64), c_uint32, c_uint32,

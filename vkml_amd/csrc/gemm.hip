@@ -1968,6 +1968,7 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
 }
 
 int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst);
+int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels, const vkhip_unfold& p);
 
 // The weight gradient summed over the batch, out [Cout, C*kh*kw] = sum_n
 // grad[n] @ im2col(x[n])^T: the reference graph's per-image products and
@@ -2075,6 +2076,128 @@ int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float*
     if (splits > 1) return launch_split_k_reduce(target, out, out_elems, splits);
     return VKHIP_OK;
 }
+
+// The flipped, transposed weight of the input gradient's convolution:
+// wt[c][o*kk + (kk - 1 - r)] = w[o][c*kk + r] (kk = kh*kw window elements,
+// r = ki*kw + kj, so kk - 1 - r is the window rotated by 180 degrees).
+__global__ void conv_weight_flip_kernel(const float* __restrict__ w, int64_t s_out,
+                                        float* __restrict__ wt, uint32_t channels, uint32_t cout,
+                                        uint32_t kk) {
+    const uint64_t total = static_cast<uint64_t>(channels) * cout * kk;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t row = static_cast<uint64_t>(cout) * kk;
+        const uint32_t c = static_cast<uint32_t>(i / row);
+        const uint32_t rest = static_cast<uint32_t>(i - c * row);
+        const uint32_t o = rest / kk;
+        const uint32_t r = kk - 1 - (rest - o * kk);
+        wt[i] = w[static_cast<int64_t>(o) * s_out + static_cast<int64_t>(c) * kk + r];
+    }
+}
+
+// Input gradient of conv2d (forward geometry p, weight rows [Cout, C*kh*kw]
+// contiguous with row stride w_row). With unit strides the column adjoint
+// col2im(W^T @ g) equals the convolution of g with the 180-degree rotated,
+// channel-transposed window under pad' = dilation*(k-1) - pad: dX[c][h][w] =
+// sum_{o,ki,kj} W[o][c][ki][kj] g[o][h + pad - ki*d][w + pad - kj*d], and
+// with ki' = kh-1-ki the row offset is h - pad' + ki'*d. That runs as the
+// implicit-im2col conv kernel on g (no column matrix, no col2im pass), in a
+// different summation order than the graph (within the GEMM tolerance for
+// K = Cout*kh*kw). Exact numerics, other strides or pad > dilation*(k-1) run
+// the graph: the TN product into a column matrix, then col2im.
+int conv2d_input_grad(const float* gr, const vkhip_operand& gd, const float* w, int64_t w_row,
+                      uint32_t channels, float* out, const vkhip_unfold& p) {
+    if (p.kernel_h <= 0 || p.kernel_w <= 0 || p.stride_h <= 0 || p.stride_w <= 0 ||
+        p.dilation_h <= 0 || p.dilation_w <= 0 || p.pad_h < 0 || p.pad_w < 0 || p.image_h < 0 ||
+        p.image_w < 0)
+        return fail(VKHIP_ERR_INVALID, "conv2d input grad: invalid window geometry");
+    const int64_t oh = (static_cast<int64_t>(p.image_h) + 2 * p.pad_h -
+                        (static_cast<int64_t>(p.dilation_h) * (p.kernel_h - 1) + 1)) / p.stride_h + 1;
+    const int64_t ow = (static_cast<int64_t>(p.image_w) + 2 * p.pad_w -
+                        (static_cast<int64_t>(p.dilation_w) * (p.kernel_w - 1) + 1)) / p.stride_w + 1;
+    if (oh <= 0 || ow <= 0) return fail(VKHIP_ERR_INVALID, "conv2d input grad: window larger than padded image");
+    if (static_cast<int64_t>(gd.ne[2]) != oh || static_cast<int64_t>(gd.ne[3]) != ow)
+        return fail(VKHIP_ERR_INVALID, "conv2d input grad: gradient is %ux%u, the geometry gives %lldx%lld",
+                    gd.ne[2], gd.ne[3], static_cast<long long>(oh), static_cast<long long>(ow));
+    if (gd.nb[3] != 1 || gd.nb[2] != static_cast<int64_t>(ow))
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d input grad: gradient positions must be contiguous");
+    const uint32_t batch = gd.ne[0], cout = gd.ne[1];
+    const uint32_t kk = static_cast<uint32_t>(p.kernel_h * p.kernel_w);
+    const uint64_t ck = static_cast<uint64_t>(channels) * kk;
+    const uint64_t L = static_cast<uint64_t>(oh) * ow;
+    const uint64_t image = static_cast<uint64_t>(p.image_h) * p.image_w;
+    if (batch == 0 || channels == 0 || image == 0) return VKHIP_OK;
+    if (cout == 0) return launch_zero_f32(out, static_cast<uint64_t>(batch) * channels * image);
+    const int pad2h = p.dilation_h * (p.kernel_h - 1) - p.pad_h;
+    const int pad2w = p.dilation_w * (p.kernel_w - 1) - p.pad_w;
+    // The convolution's output rows are the C input channels: under 32 they
+    // fill too little of a 64-row tile (C = 3: 0.3x the TN product + col2im).
+    const bool geometry = p.stride_h == 1 && p.stride_w == 1 && pad2h >= 0 && pad2w >= 0 &&
+                          kk <= 63 && static_cast<uint64_t>(cout) * kk <= 0xffffffffull;
+    const bool fused = !ctx().exact_math && geometry && channels >= 32;
+    publish("conv.input_grad", "conv2d_input_grad",
+            fused ? "implicit_conv_of_grad_with_flipped_weight" : "tn_product_then_col2im",
+            fused ? "tn_product_then_col2im" : "implicit_conv_of_grad_with_flipped_weight",
+            fused ? "unit strides: the column adjoint is a convolution"
+                  : (ctx().exact_math ? "exact numerics mode"
+                                      : (geometry ? "fewer than 32 input channels"
+                                                  : "strided or over-padded window")),
+            static_cast<int64_t>(channels), 32);
+    if (fused) {
+        const uint64_t wt_elems = static_cast<uint64_t>(channels) * cout * kk;
+        float* wt = nullptr;
+        int st = node_temporary(wt_elems * sizeof(float), &wt);
+        if (st != VKHIP_OK) return st;
+        const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((wt_elems + 255) / 256, 4096));
+        hipLaunchKernelGGL(conv_weight_flip_kernel, dim3(blocks), dim3(256), 0, ctx().stream, w, w_row,
+                           wt, channels, cout, kk);
+        VKHIP_LAUNCH_CHECK();
+        vkhip_unfold q = p;
+        q.stride_h = 1;
+        q.stride_w = 1;
+        q.pad_h = pad2h;
+        q.pad_w = pad2w;
+        q.image_h = static_cast<int32_t>(oh);
+        q.image_w = static_cast<int32_t>(ow);
+        vkhip_operand wd;
+        wd.ne[0] = 1;
+        wd.ne[1] = 1;
+        wd.ne[2] = channels;
+        wd.ne[3] = cout * kk;
+        wd.nb[0] = 0;
+        wd.nb[1] = 0;
+        wd.nb[2] = static_cast<int64_t>(cout) * kk;
+        wd.nb[3] = 1;
+        return conv2d_forward(gr, gd, wt, wd, out, q);
+    }
+    if (ck > 0xffffffffull || L > 0xffffffffull)
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d input grad: extents too large");
+    float* cols = nullptr;
+    int st = node_temporary(static_cast<uint64_t>(batch) * ck * L * sizeof(float), &cols);
+    if (st != VKHIP_OK) return st;
+    // flat_weight^T broadcast over the batch @ grad: the graph's MATMUL node
+    vkhip_operand ad, bd;
+    ad.ne[0] = 1;
+    ad.ne[1] = batch;
+    ad.ne[2] = static_cast<uint32_t>(ck);
+    ad.ne[3] = cout;
+    ad.nb[0] = 0;
+    ad.nb[1] = 0;
+    ad.nb[2] = 1;
+    ad.nb[3] = w_row;
+    bd.ne[0] = 1;
+    bd.ne[1] = batch;
+    bd.ne[2] = cout;
+    bd.ne[3] = static_cast<uint32_t>(L);
+    bd.nb[0] = 0;
+    bd.nb[1] = gd.nb[0];
+    bd.nb[2] = gd.nb[1];
+    bd.nb[3] = 1;
+    const vkhip_gemm_opts opts{ctx().node_gemm_kernel, 0};
+    st = gemm(w, ad, gr, bd, cols, &opts);
+    if (st != VKHIP_OK) return st;
+    return launch_col2im(cols, out, batch, channels, p);
+}
 }  // namespace vkhip
 
 // ---- C ABI -------------------------------------------------------------------
@@ -2144,6 +2267,22 @@ extern "C" int vkhip_conv2d_weight_grad(const float* x, const vkhip_operand* x_d
     vkhip::Unit unit("conv2d_weight_grad");
     if (!x_desc || !grad_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d weight grad: null argument");
     return vkhip::conv2d_weight_grad(x, *x_desc, grad, *grad_desc, out, *p);
+}
+
+extern "C" int vkhip_conv2d_input_grad(const float* grad, const vkhip_operand* grad_desc,
+                                       const float* w, const vkhip_operand* w_desc, float* out,
+                                       const vkhip_unfold* p) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    vkhip::Unit unit("conv2d_input_grad");
+    if (!grad_desc || !w_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d_input_grad: null argument");
+    const int64_t kk = static_cast<int64_t>(p->kernel_h) * p->kernel_w;
+    if (kk <= 0 || w_desc->ne[0] != 1 || w_desc->ne[1] != 1 || w_desc->ne[2] != grad_desc->ne[1] ||
+        w_desc->ne[3] % kk != 0 || (w_desc->nb[3] != 1 && w_desc->ne[3] > 1) || w_desc->nb[2] < 0)
+        return vkhip::fail(VKHIP_ERR_INVALID,
+                           "conv2d_input_grad: weight must be [1,1,Cout,C*kh*kw] with contiguous rows");
+    return vkhip::conv2d_input_grad(grad, *grad_desc, w, w_desc->nb[2],
+                                    static_cast<uint32_t>(w_desc->ne[3] / kk), out, *p);
 }
 
 extern "C" int vkhip_conv2d_weight_grad_sum(const float* x, const vkhip_operand* x_desc,

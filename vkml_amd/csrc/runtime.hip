@@ -25,6 +25,8 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
                        const vkhip_operand& gd, float* out, const vkhip_unfold& p);
 int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* gr,
                            const vkhip_operand& gd, float* out, const vkhip_unfold& p);
+int conv2d_input_grad(const float* gr, const vkhip_operand& gd, const float* w, int64_t w_row,
+                      uint32_t channels, float* out, const vkhip_unfold& p);
 int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t* labels,
                          const float* g_out, float* out, uint32_t rows, uint32_t n, int backward);
 int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uint32_t out_h,
@@ -290,6 +292,22 @@ static int supports_node(const vkhip_node& nd) {
                    gr.nb[2] == gr.ne[3] &&
                    static_cast<int64_t>(p.kernel_h) * p.kernel_w <= 63;
         }
+        case VKHIP_OP_CONV2D_INPUT_GRAD: {
+            const vkhip_tensor& gr = nd.src[0];
+            const vkhip_tensor& w = nd.src[1];
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            if (nd.n_src != 2 || !is_f32(gr) || !is_f32(w) || !is_f32(o) || gr.ndim != 4 ||
+                o.ndim != 4 || !contiguous(o) || o.ne[0] != gr.ne[0] || w.ne[0] != gr.ne[1] ||
+                gr.nb[3] != 1 || gr.nb[2] != gr.ne[3] || o.ne[2] != p.image_h || o.ne[3] != p.image_w ||
+                static_cast<int64_t>(p.kernel_h) * p.kernel_w > 63)
+                return 0;
+            if (w.ndim == 4)
+                return w.ne[1] == o.ne[1] && w.ne[2] == p.kernel_h && w.ne[3] == p.kernel_w &&
+                       w.nb[3] == 1 && w.nb[2] == w.ne[3] && w.nb[1] == w.ne[2] * w.nb[2];
+            return w.ndim == 2 && w.nb[1] == 1 &&
+                   w.ne[1] == o.ne[1] * static_cast<int64_t>(p.kernel_h) * p.kernel_w;
+        }
         case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: {
             const vkhip_tensor& x = nd.src[0];
             const vkhip_tensor& gr = nd.src[1];
@@ -473,6 +491,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_CONV2D: return "conv2d";
         case VKHIP_OP_CONV2D_WEIGHT_GRAD: return "conv2d_weight_grad";
         case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: return "conv2d_weight_grad_sum";
+        case VKHIP_OP_CONV2D_INPUT_GRAD: return "conv2d_input_grad";
         case VKHIP_OP_MIN: return "min";
         case VKHIP_OP_ARGMIN: return "argmin";
         case VKHIP_OP_FULL: return "full";
@@ -614,6 +633,15 @@ static int compute_node(const vkhip_node& nd) {
             return conv2d_weight_grad(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
                                       static_cast<const float*>(gr.data), gd,
                                       static_cast<float*>(nd.out.data), p);
+        }
+        case VKHIP_OP_CONV2D_INPUT_GRAD: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            if (nd.out.ne[1] > 0xffffffffll || nd.src[0].ne[0] > 0xffffffffll || nd.src[0].ne[1] > 0xffffffffll)
+                return fail(VKHIP_ERR_UNSUPPORTED, "conv2d input grad: extents too large");
+            return conv2d_input_grad(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
+                                     static_cast<const float*>(nd.src[1].data), nd.src[1].nb[0],
+                                     static_cast<uint32_t>(nd.out.ne[1]), static_cast<float*>(nd.out.data), p);
         }
         case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: {
             vkhip_unfold p;

@@ -241,6 +241,41 @@ def conv2d_weight_grad(x: DeviceArray, grad: DeviceArray, kernel, stride=1, padd
     return out
 
 
+def conv2d_input_grad(grad: DeviceArray, weight: DeviceArray, image_hw, stride=1, padding=0,
+                      dilation=1, out: DeviceArray | None = None) -> DeviceArray:
+    """The convolution's input gradient [N, C, H, W] = col2im(flat_weight^T @
+    grad[n]): conv2d's backward for x (autograd.cpp:548-553 through the matmul
+    and im2col adjoints, ops.cpp:662-705). Fast numerics with unit strides run
+    one convolution of grad with the flipped, transposed weight; otherwise the
+    TN product and col2im."""
+    _f32(grad, "conv2d_input_grad")
+    _f32(weight, "conv2d_input_grad")
+    if grad.ndim != 4 or weight.ndim != 4 or grad.shape[1] != weight.shape[0]:
+        raise ValueError("conv2d_input_grad expects an [N, Cout, oh, ow] gradient and a [Cout, C, kh, kw] weight")
+    cout, c, kh, kw = weight.shape
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw = _pair(dilation)
+    h, w = _pair(image_hw)
+    oh, ow = window_count(h, kh, sh, ph, dh), window_count(w, kw, sw, pw, dw)
+    if grad.shape[2:] != (oh, ow):
+        raise ValueError(f"conv2d_input_grad: gradient is {grad.shape[2:]}, geometry gives {(oh, ow)}")
+    if not grad.is_contiguous():
+        from .device import contiguous
+        grad = contiguous(grad)
+    if not weight.is_contiguous():
+        from .device import contiguous
+        weight = contiguous(weight)
+    n = grad.shape[0]
+    out = _out(out, (n, c, h, w))
+    u = _lib.unfold((kh, kw), (sh, sw), (ph, pw), (dh, dw), (h, w))
+    wd = _lib.operand((1, 1, cout, c * kh * kw), (0, 0, c * kh * kw, 1))
+    check(_lib.load().vkhip_conv2d_input_grad(c_void_p(grad.ptr), byref(grad.operand()),
+                                              c_void_p(weight.ptr), byref(wd), c_void_p(out.ptr),
+                                              byref(u)), "conv2d_input_grad")
+    return out
+
+
 def conv2d_weight_grad_sum(x: DeviceArray, grad: DeviceArray, kernel, stride=1, padding=0,
                            dilation=1, out: DeviceArray | None = None) -> DeviceArray:
     """The convolution's weight gradient summed over the batch, [Cout, C*kh*kw]

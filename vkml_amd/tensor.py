@@ -963,6 +963,13 @@ def _accumulate(grads: dict, node: Node, g: Tensor) -> None:
 # which stays within the GEMM tolerance of the graph, not bit-identical.
 FOLD_CONV_WEIGHT_GRAD = True
 
+# The conv2d input gradient as one CONV2D_INPUT_GRAD node (True) or as the
+# reference graph's TN product and COL2IM (False). The oracle gives both the
+# same bits; the device's fast numerics run the node, for unit strides, as a
+# convolution of the gradient with the flipped, transposed weight (within the
+# GEMM tolerance of the graph).
+FUSED_CONV_INPUT_GRAD = True
+
 
 def reduce_to_shape(g: Tensor, target_dims) -> Tensor:
     """Sums g down to target_dims, undoing a broadcast (autograd.cpp:84-116)."""
@@ -1078,9 +1085,18 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         ck = _numel(b.shape[1:])
         g4 = grad.reshape(1, n_, cout, oh * ow)
         if a.requires_grad:
-            flat4 = tb().reshape(cout, ck).broadcast_to((1, n_, cout, ck))
-            dcols = matmul(flat4.transpose(-2, -1), g4).reshape(n_, ck, oh * ow)
-            _accumulate(grads, a, col2im(dcols, hw, kernel, stride, pad, dil))
+            if FUSED_CONV_INPUT_GRAD:
+                # col2im(flat^T @ g4) as one node: with unit strides the device
+                # runs it as a convolution of the gradient with the flipped,
+                # transposed weight (no column matrix); the oracle computes
+                # the product and col2im.
+                dx = Node(OP["CONV2D_INPUT_GRAD"], a.shape, np.float32, a.backend,
+                          [grad.contiguous().node, b], params=node.params)
+                _accumulate(grads, a, Tensor(dx))
+            else:
+                flat4 = tb().reshape(cout, ck).broadcast_to((1, n_, cout, ck))
+                dcols = matmul(flat4.transpose(-2, -1), g4).reshape(n_, ck, oh * ow)
+                _accumulate(grads, a, col2im(dcols, hw, kernel, stride, pad, dil))
         if b.requires_grad:
             if FOLD_CONV_WEIGHT_GRAD:
                 # sum_n g4 @ cols4^T as one node: the device folds the batch
