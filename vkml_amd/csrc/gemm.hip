@@ -783,6 +783,165 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
     }
 }
 
+// The convolution weight gradient's product grad (Cout x K) @ cols^T (K x
+// C*kh*kw) with both operands straight into LDS, in gemm_nn_direct_kernel's
+// layouts (A KCD-swizzled [128 rows][32 k], B [32 k][128 columns]) and MFMA
+// order, so the same bits as that product on the materialised columns.
+//   A = grad rows, k-contiguous within one image.
+//   B = the transposed columns gathered from the image. Row k of a K-tile is
+//     one output position p, the same for the whole wave, so one single-float
+//     LDS-direct load brings 64 consecutive columns j (one per lane) of that
+//     position: x[n][c(j)][h(p) + dh(j)][w(p) + dw(j)]. A lane's two columns
+//     (offset, dh, dw) are fixed for the kernel; the position part is scalar.
+//     Padding, columns past C*kh*kw and positions past L read at an offset
+//     with bit 31 set, which the 2^31-byte buffer resource returns as 0.
+// FOLD: K = N*L with the batch folded in (L a multiple of 32, so each K-tile
+// lies in image kt*32 / L): the weight gradient summed over the batch in one
+// product. Otherwise K = L and the image is blockIdx.z (per-image products).
+template <bool FOLD>
+__global__ __launch_bounds__(256) void conv_wgrad_direct_kernel(GemmArgs g, Im2colB im) {
+    constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
+    using LA = TileLoader<BM, BK, KCD>;
+    __shared__ __attribute__((aligned(16))) float lds[2][BM * LDK + BK * BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm0 = wave * 32;
+
+    uint32_t tm, tn, split;
+    tile_of(g, tm, tn, split);
+    const uint32_t row0 = tm * BM;
+    const uint32_t col0 = tn * BN;
+    const uint32_t z = blockIdx.z;
+    float* cbase = g.c + static_cast<uint64_t>(split) * g.split_stride +
+                   static_cast<uint64_t>(z) * g.m * g.n;
+    const uint32_t kt0 = split * g.chunk;
+    const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
+    const uint32_t L = FOLD ? im.L : g.k;
+
+    // this lane's two columns j = col0 + 64 h + lane
+    int32_t joff4[2], jdh[2], jdw[2];
+    bool jok[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t j = col0 + 64 * h + lane;
+        jok[h] = j < g.n;
+        const ImgRow q = img_row(im, jok[h] ? j : 0u);
+        const uint32_t ki = im.div_kw.div(static_cast<uint32_t>(q.r));
+        jdh[h] = static_cast<int32_t>(ki) * im.dilh;
+        jdw[h] = (q.r - static_cast<int32_t>(ki) * im.kw) * im.dilw;
+        joff4[h] = q.off * 4;
+    }
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[s][r] = 0.0f;
+
+    auto load_tile = [&](uint32_t kt, int dst) {
+        const uint32_t k0 = kt * BK;
+        uint32_t n = z, p0 = k0;
+        if constexpr (FOLD) {
+            n = im.div_L.div(k0);
+            p0 = k0 - n * L;
+        }
+        const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(g.a + static_cast<int64_t>(n) * g.sa1), 0,
+            static_cast<int32_t>(0x80000000u), 0x00020000);
+        LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, p0, L, tid);
+        const __amdgpu_buffer_rsrc_t img = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(im.x + static_cast<int64_t>(n) * im.sn), 0,
+            static_cast<int32_t>(0x80000000u), 0x00020000);
+        // wave w fills k rows 8w .. 8w + 7, two loads of 64 columns per row
+        uint32_t p = p0 + 8 * wave;
+        uint32_t oh = im.div_ow.div(p);
+        uint32_t ow = p - oh * static_cast<uint32_t>(im.ow);
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const bool pok = p < L;
+            const int32_t h0 = static_cast<int32_t>(oh) * im.strh - im.padh;
+            const int32_t w0 = static_cast<int32_t>(ow) * im.strw - im.padw;
+            const int32_t base4 = (h0 * im.sh + w0 * im.sw) * 4;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const bool inside = pok & jok[h] &
+                                    (static_cast<uint32_t>(h0 + jdh[h]) < static_cast<uint32_t>(im.H)) &
+                                    (static_cast<uint32_t>(w0 + jdw[h]) < static_cast<uint32_t>(im.W));
+                const uint32_t off = inside ? static_cast<uint32_t>(base4 + joff4[h]) : 0x80000000u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    img,
+                    (__attribute__((address_space(3))) void*)(lds[dst] + BM * LDK + (8 * wave + rr) * BN +
+                                                              64 * h),
+                    4, off, 0, 0, 0);
+            }
+            ++p;
+            ++ow;
+            const bool wrap = ow == static_cast<uint32_t>(im.ow);
+            ow = wrap ? 0u : ow;
+            oh += wrap ? 1u : 0u;
+        }
+    };
+    if (kt0 < kt1) load_tile(kt0, 0);
+    __syncthreads();
+
+    const int lrow = lane & 31;
+    const int kh = lane >> 5;
+    for (uint32_t kt = kt0; kt < kt1; ++kt) {
+        const int cur = (kt - kt0) & 1;
+        if (kt + 1 < kt1) load_tile(kt + 1, cur ^ 1);
+        const float* As = lds[cur] + (wm0 + lrow) * BK;
+        const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + 4 * lrow;
+        auto a_at = [&](int q) {
+            return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ (lrow & 7)));
+        };
+        auto b_at = [&](int q, int st) {
+            return *reinterpret_cast<const f32x4*>(Bs + (4 * q + st) * BN);
+        };
+        f32x4 av[2], bv[2][4];
+        av[0] = a_at(0);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) bv[0][st] = b_at(0, st);
+#pragma unroll
+        for (int q = 0; q < QN; ++q) {
+            const int cb = q & 1;
+            if (q + 1 < QN) {
+                av[cb ^ 1] = a_at(q + 1);
+#pragma unroll
+                for (int st = 0; st < 4; ++st) bv[cb ^ 1][st] = b_at(q + 1, st);
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    acc[s] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][st], bv[cb][st][s], acc[s],
+                                                                  0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    const uint32_t col = col0 + 4 * lrow;
+    if (col < g.n) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
+            if (row < g.m) {
+                f32x4 v;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) v[s] = acc[s][r];
+                if (g.n % 4 == 0) {
+                    *reinterpret_cast<f32x4*>(cbase + static_cast<uint64_t>(row) * g.n + col) = v;
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        if (col + s < g.n) cbase[static_cast<uint64_t>(row) * g.n + col + s] = v[s];
+                }
+            }
+        }
+    }
+}
+
 // 64x64 tiles with both operands straight into LDS, for outputs that give
 // each CU only a workgroup or two of 64x64 tiles. Rows of k (B, and A in TN)
 // land as 32 rows of 64 floats; A in NN lands KCD-swizzled. Four waves: two
@@ -1874,6 +2033,15 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
 // (autograd.cpp:548-553 through ops.cpp:662-705), with the same plan, K order
 // and split-K fold, hence the same bits. x: [N,C,H,W] any strides; g: [N,
 // Cout, L] with unit position stride; out contiguous [N, Cout, C*kh*kw].
+// Whether conv_wgrad_direct_kernel takes a weight-gradient product: 128x128
+// tiles, the gradient rows 16-byte aligned with whole groups of four
+// positions, and every byte offset of one image's gradient within 2^31.
+static bool wgrad_direct_fits(const GemmArgs& g, uint32_t positions, const float* target) {
+    return reinterpret_cast<uintptr_t>(g.a) % 16 == 0 && reinterpret_cast<uintptr_t>(target) % 16 == 0 &&
+           g.sam >= 0 && g.sa1 >= 0 && g.sam % 4 == 0 && g.sa1 % 4 == 0 && positions % 4 == 0 &&
+           ((static_cast<int64_t>(g.m) - 1) * g.sam + positions) * 4 < (int64_t{1} << 31);
+}
+
 int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
                        const vkhip_operand& gd, float* out, const vkhip_unfold& p) {
     if (static_cast<int64_t>(xd.ne[2]) != p.image_h || static_cast<int64_t>(xd.ne[3]) != p.image_w)
@@ -1958,7 +2126,16 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
     g.c = target;
     g.split_stride = splits > 1 ? out_elems : 0;
     int st;
-    if (tile.bm == 128)
+    if (tile.bm == 128 && wgrad_direct_fits(g, k, target)) {
+        // both operands straight into LDS (same bits as the register path)
+        const uint64_t flat = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
+        g.flat_splits = splits > 1 && flat <= 0x7fffffffull ? splits : 0;
+        const dim3 grid = g.flat_splits ? dim3(static_cast<uint32_t>(flat), 1, static_cast<uint32_t>(batch))
+                                        : dim3(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
+        hipLaunchKernelGGL(conv_wgrad_direct_kernel<false>, grid, dim3(256), 0, ctx().stream, g, im);
+        VKHIP_LAUNCH_CHECK();
+        st = VKHIP_OK;
+    } else if (tile.bm == 128)
         st = launch_conv_tiles<128, 128, 64, 64, IMGT>(g, im, static_cast<uint32_t>(batch), splits, amode);
     else
         st = launch_conv_tiles<64, 64, 32, 32, IMGT>(g, im, static_cast<uint32_t>(batch), splits, amode);
@@ -2068,7 +2245,15 @@ int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float*
     g.c = target;
     g.split_stride = splits > 1 ? out_elems : 0;
     int st;
-    if (tile.bm == 128)
+    if (tile.bm == 128 && wgrad_direct_fits(g, static_cast<uint32_t>(L), target)) {
+        const uint64_t flat = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
+        g.flat_splits = splits > 1 && flat <= 0x7fffffffull ? splits : 0;
+        const dim3 grid = g.flat_splits ? dim3(static_cast<uint32_t>(flat), 1, 1)
+                                        : dim3(g.tiles_m * g.tiles_n, splits, 1);
+        hipLaunchKernelGGL(conv_wgrad_direct_kernel<true>, grid, dim3(256), 0, ctx().stream, g, im);
+        VKHIP_LAUNCH_CHECK();
+        st = VKHIP_OK;
+    } else if (tile.bm == 128)
         st = launch_conv_tiles<128, 128, 64, 64, IMGTB>(g, im, 1, splits, amode);
     else
         st = launch_conv_tiles<64, 64, 32, 32, IMGTB>(g, im, 1, splits, amode);
