@@ -783,23 +783,29 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
     }
 }
 
-// The convolution weight gradient's product grad (Cout x K) @ cols^T (K x
-// C*kh*kw) with both operands straight into LDS, in gemm_nn_direct_kernel's
-// layouts (A KCD-swizzled [128 rows][32 k], B [32 k][128 columns]) and MFMA
-// order, so the same bits as that product on the materialised columns.
-//   A = grad rows, k-contiguous within one image.
-//   B = the transposed columns gathered from the image. Row k of a K-tile is
-//     one output position p, the same for the whole wave, so one single-float
-//     LDS-direct load brings 64 consecutive columns j (one per lane) of that
-//     position: x[n][c(j)][h(p) + dh(j)][w(p) + dw(j)]. A lane's two columns
-//     (offset, dh, dw) are fixed for the kernel; the position part is scalar.
-//     Padding, columns past C*kh*kw and positions past L read at an offset
-//     with bit 31 set, which the 2^31-byte buffer resource returns as 0.
-// FOLD: K = N*L with the batch folded in (L a multiple of 32, so each K-tile
-// lies in image kt*32 / L): the weight gradient summed over the batch in one
-// product. Otherwise K = L and the image is blockIdx.z (per-image products).
-template <bool FOLD>
-__global__ __launch_bounds__(256) void conv_wgrad_direct_kernel(GemmArgs g, Im2colB im) {
+// The convolution weight gradient's products with both operands straight into
+// LDS, in gemm_nn_direct_kernel's layouts (A KCD-swizzled [128 rows][32 k],
+// B [32 k][128 columns]) and MFMA order, so the same bits as that kernel on
+// the materialised columns:
+//   CD_WGRAD      out[n] = grad[n] (Cout x L) @ cols(x[n])^T: k = position p,
+//                 B column = window row j (channel, window element).
+//   CD_WGRAD_FOLD the same summed over n, one product with K = N*L (L a
+//                 multiple of 32, so each K-tile lies in image kt*32 / L).
+// A is the gradient rows of one image, k-contiguous. B is gathered by
+// single-float LDS-direct loads: row k of a K-tile is one position for the
+// whole wave, so one load brings 64 consecutive B columns (one per lane) of
+// it. An element is x[n][c][h][w] at h = sh_k + fh_lane, w = sw_k + fw_lane,
+// offset so_k + fo_lane: the position part is scalar, the window-row part
+// fixed for the kernel (a lane owns two columns), both from the im2col map
+// (kernels_movement.cpp:438-483). Padding, columns past N and positions past
+// L read at an offset with bit 31 set, which the 2^31-byte buffer resource
+// returns as 0. (The forward's B operand gathered this way -- k = window row,
+// a lane owning two positions -- measured slower than the register-path
+// IMG loader: [128,64,32,32] -> 128 channels 0.199 -> 0.215 ms.)
+enum ConvDirect { CD_WGRAD = 1, CD_WGRAD_FOLD = 2 };
+
+template <int CD>
+__global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im) {
     constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
     using LA = TileLoader<BM, BK, KCD>;
     __shared__ __attribute__((aligned(16))) float lds[2][BM * LDK + BK * BN];
@@ -818,20 +824,21 @@ __global__ __launch_bounds__(256) void conv_wgrad_direct_kernel(GemmArgs g, Im2c
                    static_cast<uint64_t>(z) * g.m * g.n;
     const uint32_t kt0 = split * g.chunk;
     const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
-    const uint32_t L = FOLD ? im.L : g.k;
+    // K of one image (A's k extent per image)
+    const uint32_t kimg = CD == CD_WGRAD_FOLD ? im.L : g.k;
 
-    // this lane's two columns j = col0 + 64 h + lane
-    int32_t joff4[2], jdh[2], jdw[2];
-    bool jok[2];
+    // this lane's two B columns j = col0 + 64 h + lane: channel and window element
+    int32_t fo4[2], fh[2], fw[2];
+    bool fok[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint32_t j = col0 + 64 * h + lane;
-        jok[h] = j < g.n;
-        const ImgRow q = img_row(im, jok[h] ? j : 0u);
+        fok[h] = j < g.n;
+        const ImgRow q = img_row(im, fok[h] ? j : 0u);
         const uint32_t ki = im.div_kw.div(static_cast<uint32_t>(q.r));
-        jdh[h] = static_cast<int32_t>(ki) * im.dilh;
-        jdw[h] = (q.r - static_cast<int32_t>(ki) * im.kw) * im.dilw;
-        joff4[h] = q.off * 4;
+        fh[h] = static_cast<int32_t>(ki) * im.dilh;
+        fw[h] = (q.r - static_cast<int32_t>(ki) * im.kw) * im.dilw;
+        fo4[h] = q.off * 4;
     }
 
     f32x16 acc[4];
@@ -842,45 +849,51 @@ __global__ __launch_bounds__(256) void conv_wgrad_direct_kernel(GemmArgs g, Im2c
 
     auto load_tile = [&](uint32_t kt, int dst) {
         const uint32_t k0 = kt * BK;
-        uint32_t n = z, p0 = k0;
-        if constexpr (FOLD) {
-            n = im.div_L.div(k0);
-            p0 = k0 - n * L;
-        }
-        const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(g.a + static_cast<int64_t>(n) * g.sa1), 0,
-            static_cast<int32_t>(0x80000000u), 0x00020000);
-        LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, p0, L, tid);
-        const __amdgpu_buffer_rsrc_t img = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(im.x + static_cast<int64_t>(n) * im.sn), 0,
-            static_cast<int32_t>(0x80000000u), 0x00020000);
-        // wave w fills k rows 8w .. 8w + 7, two loads of 64 columns per row
-        uint32_t p = p0 + 8 * wave;
-        uint32_t oh = im.div_ow.div(p);
-        uint32_t ow = p - oh * static_cast<uint32_t>(im.ow);
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-            const bool pok = p < L;
-            const int32_t h0 = static_cast<int32_t>(oh) * im.strh - im.padh;
-            const int32_t w0 = static_cast<int32_t>(ow) * im.strw - im.padw;
-            const int32_t base4 = (h0 * im.sh + w0 * im.sw) * 4;
+        // one B row of the K-tile: its scalar part, then the two loads
+        auto gather_row = [&](__amdgpu_buffer_rsrc_t img, int rr, bool kok, int32_t sh_k, int32_t sw_k,
+                              int32_t so4_k) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const bool inside = pok & jok[h] &
-                                    (static_cast<uint32_t>(h0 + jdh[h]) < static_cast<uint32_t>(im.H)) &
-                                    (static_cast<uint32_t>(w0 + jdw[h]) < static_cast<uint32_t>(im.W));
-                const uint32_t off = inside ? static_cast<uint32_t>(base4 + joff4[h]) : 0x80000000u;
+                const bool inside = kok & fok[h] &
+                                    (static_cast<uint32_t>(sh_k + fh[h]) < static_cast<uint32_t>(im.H)) &
+                                    (static_cast<uint32_t>(sw_k + fw[h]) < static_cast<uint32_t>(im.W));
+                const uint32_t off =
+                    inside ? static_cast<uint32_t>(so4_k) + static_cast<uint32_t>(fo4[h]) : 0x80000000u;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     img,
                     (__attribute__((address_space(3))) void*)(lds[dst] + BM * LDK + (8 * wave + rr) * BN +
                                                               64 * h),
                     4, off, 0, 0, 0);
             }
-            ++p;
-            ++ow;
-            const bool wrap = ow == static_cast<uint32_t>(im.ow);
-            ow = wrap ? 0u : ow;
-            oh += wrap ? 1u : 0u;
+        };
+        {
+            uint32_t n = z, p0 = k0;
+            if constexpr (CD == CD_WGRAD_FOLD) {
+                n = im.div_L.div(k0);
+                p0 = k0 - n * kimg;
+            }
+            const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(g.a + static_cast<int64_t>(n) * g.sa1), 0,
+                static_cast<int32_t>(0x80000000u), 0x00020000);
+            LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, p0, kimg, tid);
+            const __amdgpu_buffer_rsrc_t img = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(im.x + static_cast<int64_t>(n) * im.sn), 0,
+                static_cast<int32_t>(0x80000000u), 0x00020000);
+            // wave w gathers positions p0 + 8w .. + 7, walked incrementally
+            uint32_t p = p0 + 8 * wave;
+            uint32_t oh = im.div_ow.div(p);
+            uint32_t ow = p - oh * static_cast<uint32_t>(im.ow);
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                const int32_t h0 = static_cast<int32_t>(oh) * im.strh - im.padh;
+                const int32_t w0 = static_cast<int32_t>(ow) * im.strw - im.padw;
+                gather_row(img, rr, p < kimg, h0, w0, (h0 * im.sh + w0 * im.sw) * 4);
+                ++p;
+                ++ow;
+                const bool wrap = ow == static_cast<uint32_t>(im.ow);
+                ow = wrap ? 0u : ow;
+                oh += wrap ? 1u : 0u;
+            }
         }
     };
     if (kt0 < kt1) load_tile(kt0, 0);
@@ -2033,7 +2046,7 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
 // (autograd.cpp:548-553 through ops.cpp:662-705), with the same plan, K order
 // and split-K fold, hence the same bits. x: [N,C,H,W] any strides; g: [N,
 // Cout, L] with unit position stride; out contiguous [N, Cout, C*kh*kw].
-// Whether conv_wgrad_direct_kernel takes a weight-gradient product: 128x128
+// Whether conv_direct_kernel takes a weight-gradient product: 128x128
 // tiles, the gradient rows 16-byte aligned with whole groups of four
 // positions, and every byte offset of one image's gradient within 2^31.
 static bool wgrad_direct_fits(const GemmArgs& g, uint32_t positions, const float* target) {
@@ -2132,7 +2145,7 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
         g.flat_splits = splits > 1 && flat <= 0x7fffffffull ? splits : 0;
         const dim3 grid = g.flat_splits ? dim3(static_cast<uint32_t>(flat), 1, static_cast<uint32_t>(batch))
                                         : dim3(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
-        hipLaunchKernelGGL(conv_wgrad_direct_kernel<false>, grid, dim3(256), 0, ctx().stream, g, im);
+        hipLaunchKernelGGL(conv_direct_kernel<CD_WGRAD>, grid, dim3(256), 0, ctx().stream, g, im);
         VKHIP_LAUNCH_CHECK();
         st = VKHIP_OK;
     } else if (tile.bm == 128)
@@ -2250,7 +2263,7 @@ int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float*
         g.flat_splits = splits > 1 && flat <= 0x7fffffffull ? splits : 0;
         const dim3 grid = g.flat_splits ? dim3(static_cast<uint32_t>(flat), 1, 1)
                                         : dim3(g.tiles_m * g.tiles_n, splits, 1);
-        hipLaunchKernelGGL(conv_wgrad_direct_kernel<true>, grid, dim3(256), 0, ctx().stream, g, im);
+        hipLaunchKernelGGL(conv_direct_kernel<CD_WGRAD_FOLD>, grid, dim3(256), 0, ctx().stream, g, im);
         VKHIP_LAUNCH_CHECK();
         st = VKHIP_OK;
     } else if (tile.bm == 128)
