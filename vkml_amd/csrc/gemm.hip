@@ -95,12 +95,20 @@ __device__ __forceinline__ void tile_of(const GemmArgs& g, uint32_t& tm, uint32_
 //   KCD  k-contiguous, 16-byte aligned, K a multiple of 4: loaded straight
 //        into LDS by buffer loads (no registers, no LDS stores), rows of BK
 //        floats whose 16-byte groups are XOR-swizzled by row (group g of row r
-//        at g ^ (r & 7)) so the MFMA operand reads stay conflict-free.
+//        at g ^ kcd_swizzle(r)) so the MFMA operand reads stay conflict-free.
 //   IMGTB the weight gradient summed over the batch: IMGT with the batch
 //        folded into K (k = n * L + position, L a multiple of BK), as B of one
 //        product [Cout, N*L] x [N*L, C*kh*kw] (a kernel-level mode: the tile
 //        loader is IMGT's, given image n's resource and positions per K-tile).
 enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4, IMGT = 5, KCD = 6, IMGTB = 7 };
+
+// The KCD row swizzle. A 16-byte LDS read is served 16 lanes per pass over
+// 64 banks (256 bytes); the sixteen rows of a pass (BK = 32 floats = 128
+// bytes each) fall on two bank halves by row parity, so the eight rows of one
+// parity must take eight distinct groups: bits 1..3 of the row. (Bits 0..2
+// gave rows r and r + 8 the same banks: two-way conflicts on every operand
+// read, 1/6 of the LDS cycles by SQ_LDS_BANK_CONFLICT.)
+__host__ __device__ constexpr int kcd_swizzle(int row) { return (row >> 1) & 7; }
 
 // The B operand of a convolution read straight from the image (implicit
 // im2col): element (row, pos) of image n's cols matrix [C*kh*kw, out_h*out_w]
@@ -257,7 +265,7 @@ struct TileLoader {
     // KCD: R rows x BK k as R*BK/4 16-byte slots; wave w's i-th load fills
     // slots (4i + w)*64 .. +63 of the stage, one per lane, in order (the load
     // writes lane l's 16 bytes at the instruction's LDS base + 16 l). Slot s
-    // holds row s / 8, k-group (s % 8) ^ (row & 7). Out-of-range groups read
+    // holds row s / 8, k-group (s % 8) ^ kcd_swizzle(row). Out-of-range groups read
     // an offset past the buffer's range and land as zeros.
     __device__ __forceinline__ static void load_direct(float* stage, __amdgpu_buffer_rsrc_t src,
                                                        int64_t s_row, uint32_t row0, uint32_t rows,
@@ -270,7 +278,7 @@ struct TileLoader {
             const int chunk = 4 * i + wave;
             const int slot = chunk * 64 + lane;
             const int r = slot >> 3;
-            const int grp = (slot & 7) ^ (r & 7);
+            const int grp = (slot & 7) ^ kcd_swizzle(r);
             const uint32_t gr = row0 + r, gk = k0 + 4 * grp;
             const bool ok = gr < rows && gk < kdim;
             const uint32_t off = ok ? static_cast<uint32_t>((static_cast<int64_t>(gr) * s_row + gk) * 4)
@@ -571,16 +579,16 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
             load_tile(kt + 1, cur ^ 1);
         }
         // KCD rows are BK floats with swizzled groups: group kh*4 + q of row
-        // r sits at (kh*4 + q) ^ (r & 7); rows 32 apart share r & 7.
+        // r sits at (kh*4 + q) ^ kcd_swizzle(r); rows 32 apart share it.
         constexpr int APITCH = AMODE == KCD ? BK : LDK;
         const float* As = lds[cur] + (wm0 + lrow) * APITCH + (AMODE == KCD ? 0 : kh * (BK / 2));
         auto a_off = [&](int q) {
-            return AMODE == KCD ? 4 * ((kh * 4 + q) ^ (lrow & 7)) : 4 * q;
+            return AMODE == KCD ? 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)) : 4 * q;
         };
         constexpr int BPITCH = BMODE == KCD ? BK : LDK;
         const float* Bs = lds[cur] + BM * LDK + (wn0 + lrow) * BPITCH + (BMODE == KCD ? 0 : kh * (BK / 2));
         auto b_off = [&](int q) {
-            return BMODE == KCD ? 4 * ((kh * 4 + q) ^ (lrow & 7)) : 4 * q;
+            return BMODE == KCD ? 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)) : 4 * q;
         };
         // MFMA operands for step group q+1 are read from LDS while group q's
         // MFMAs run (two register sets).
@@ -736,7 +744,7 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
                 for (int st = 0; st < 4; ++st) v[st] = As[(4 * q + st) * BM];
                 return v;
             } else {
-                return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ (lrow & 7)));
+                return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)));
             }
         };
         auto b_at = [&](int q, int st) {
@@ -907,7 +915,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
         const float* As = lds[cur] + (wm0 + lrow) * BK;
         const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + 4 * lrow;
         auto a_at = [&](int q) {
-            return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ (lrow & 7)));
+            return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)));
         };
         auto b_at = [&](int q, int st) {
             return *reinterpret_cast<const f32x4*>(Bs + (4 * q + st) * BN);
@@ -1039,7 +1047,7 @@ __global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
                 for (int st = 0; st < 4; ++st) v[st] = As[(4 * q + st) * BM];
                 return v;
             } else {
-                return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ (lrow & 7)));
+                return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)));
             }
         };
         f32x4 av[2], bv[2];
