@@ -720,12 +720,52 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[s][r] = 0.0f;
 
+    // The eight straight-to-LDS loads of a K-tile (four of A, four of B; the
+    // slot maps of LA::load_direct and load_b_rows_direct) at per-lane byte
+    // offsets fixed for the kernel, rows or columns past the operand at bit
+    // 31 (read as zeros), plus the K-tile's part as the scalar offset: per
+    // load one M0 write and the load, against eight address instructions
+    // recomputed per K-tile. A last K-tile that K does not fill takes the
+    // checked loaders.
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t voa[4], vob[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int slot = (4 * i + wv) * 64 + lane;
+        if constexpr (ATR) {
+            const uint32_t gc = row0 + 4 * (slot & 31);
+            voa[i] = gc < g.m ? static_cast<uint32_t>(((slot >> 5) * g.sak + gc) * 4) : 0x80000000u;
+        } else {
+            const int r = slot >> 3;
+            const uint32_t gr = row0 + r;
+            voa[i] = gr < g.m ? static_cast<uint32_t>((gr * g.sam + 4 * ((slot & 7) ^ kcd_swizzle(r))) * 4)
+                              : 0x80000000u;
+        }
+        const uint32_t gc = col0 + 4 * (slot & 31);
+        vob[i] = gc < g.n ? static_cast<uint32_t>(((slot >> 5) * g.sbk + gc) * 4) : 0x80000000u;
+    }
+    const uint32_t a_step = static_cast<uint32_t>((ATR ? g.sak : 1) * BK * 4);
+    const uint32_t b_step = static_cast<uint32_t>(g.sbk * BK * 4);
     auto load_tile = [&](uint32_t kt, int dst) {
-        if constexpr (ATR)
-            load_b_rows_direct(lds[dst], arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
-        else
-            LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
-        load_b_rows_direct(lds[dst] + BM * LDK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+        if ((kt + 1) * BK > g.k) {
+            if constexpr (ATR)
+                load_b_rows_direct(lds[dst], arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
+            else
+                LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+            load_b_rows_direct(lds[dst] + BM * LDK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+            return;
+        }
+        const uint32_t sa = kt * a_step, sb = kt * b_step;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                arsrc, (__attribute__((address_space(3))) void*)(lds[dst] + (4 * i + wv) * 256), 16, voa[i],
+                sa, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                brsrc, (__attribute__((address_space(3))) void*)(lds[dst] + BM * LDK + (4 * i + wv) * 256), 16,
+                vob[i], sb, 0, 0);
     };
     if (kt0 < kt1) load_tile(kt0, 0);
     __syncthreads();
