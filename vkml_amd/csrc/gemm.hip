@@ -439,6 +439,51 @@ struct TileLoader {
     }
 };
 
+// Straight-to-LDS loads with their addresses computed once per kernel. A
+// lane's byte offset within the operand is fixed for the whole K loop except
+// for the K-tile's part, which is the same for every lane and goes in the
+// loads' scalar offset: per load one M0 write and the load. Rows or columns
+// past the operand get bit 31 in the fixed offset and read as zeros. The K
+// bound is not checked: a last K-tile that K does not fill takes the checked
+// loaders (TileLoader::load_direct, load_b_rows_direct, load_rows_direct),
+// which fill the same LDS slots.
+//   kcd_offsets   KCD slots (k-contiguous rows of BK = 32, swizzled), R rows;
+//                 the K-tile part is k0 * 4 bytes.
+//   rows_offsets  rows of k, COLS columns each (B in NN, A in TN); the K-tile
+//                 part is k0 * s_k * 4 bytes.
+template <int R>
+__device__ __forceinline__ void kcd_offsets(uint32_t (&vo)[R / 32], int wv, int lane, int64_t s_row,
+                                            uint32_t row0, uint32_t rows) {
+#pragma unroll
+    for (int i = 0; i < R / 32; ++i) {
+        const int slot = (4 * i + wv) * 64 + lane;
+        const int r = slot >> 3;
+        const uint32_t gr = row0 + r;
+        vo[i] = gr < rows ? static_cast<uint32_t>((gr * s_row + 4 * ((slot & 7) ^ kcd_swizzle(r))) * 4)
+                          : 0x80000000u;
+    }
+}
+template <int COLS>
+__device__ __forceinline__ void rows_offsets(uint32_t (&vo)[COLS / 32], int wv, int lane, int64_t s_k,
+                                             uint32_t col0, uint32_t cols) {
+    constexpr int G = COLS / 4;  // 16-byte groups per k row
+#pragma unroll
+    for (int i = 0; i < COLS / 32; ++i) {
+        const int slot = (4 * i + wv) * 64 + lane;
+        const uint32_t gc = col0 + 4 * (slot % G);
+        vo[i] = gc < cols ? static_cast<uint32_t>(((slot / G) * s_k + gc) * 4) : 0x80000000u;
+    }
+}
+// Issues the loads: load i fills the 64-lane block (4 i + wave) of the stage.
+template <int N>
+__device__ __forceinline__ void issue_direct(float* stage, __amdgpu_buffer_rsrc_t src, const uint32_t* vo,
+                                             int wv, uint32_t soff) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            src, (__attribute__((address_space(3))) void*)(stage + (4 * i + wv) * 256), 16, vo[i], soff, 0, 0);
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int AMODE, int BMODE>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_in) {
     static_assert((BM / WM) * (BN / WN) == 4, "four waves per workgroup");
@@ -507,25 +552,46 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+    // KCD operands: offsets computed once (kcd_offsets)
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t voa[AMODE == KCD ? BM / 32 : 1], vob[BMODE == KCD ? BN / 32 : 1];
+    if constexpr (AMODE == KCD) kcd_offsets<BM>(voa, wv, lane, g.sam, row0, g.m);
+    if constexpr (BMODE == KCD) kcd_offsets<BN>(vob, wv, lane, g.sbn, col0, g.n);
+    auto a_direct = [&](uint32_t kt, int dst) {
+        if constexpr (AMODE == KCD) {
+            if ((kt + 1) * BK <= g.k)
+                issue_direct<BM / 32>(lds[dst], arsrc, voa, wv, kt * BK * 4);
+            else
+                LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+        }
+    };
+    auto b_direct = [&](uint32_t kt, int dst) {
+        if constexpr (BMODE == KCD) {
+            if ((kt + 1) * BK <= g.k)
+                issue_direct<BN / 32>(lds[dst] + BM * LDK, brsrc, vob, wv, kt * BK * 4);
+            else
+                LB::load_direct(lds[dst] + BM * LDK, brsrc, g.sbn, col0, g.n, kt * BK, g.k, tid);
+        }
+    };
     f32x4 ra[LA::kRegs], rb[LB::kRegs];
     auto load_tile = [&](uint32_t kt, int dst) {
         (void)dst;
         // (The order matters for the schedule: with A straight into LDS and
         // B through registers, A's loads go first; measured 4% on NN.)
         if constexpr (AMODE == KCD && BMODE != KCD) {
-            LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+            a_direct(kt, dst);
             if (rows_in && (kt + 1) * BK <= g.k)
                 LB::template load<false>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
             else
                 LB::template load<true>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
         } else if constexpr (BMODE == KCD) {
             if constexpr (AMODE == KCD)
-                LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+                a_direct(kt, dst);
             else if (rows_in && (kt + 1) * BK <= g.k)
                 LA::template load<false>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
             else
                 LA::template load<true>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
-            LB::load_direct(lds[dst] + BM * LDK, brsrc, g.sbn, col0, g.n, kt * BK, g.k, tid);
+            b_direct(kt, dst);
         } else if constexpr (BMODE == IMG) {
             LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
             LB::load_img(rb, img, rows, base4, outside, kt * BK, tid);
@@ -720,30 +786,15 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[s][r] = 0.0f;
 
-    // The eight straight-to-LDS loads of a K-tile (four of A, four of B; the
-    // slot maps of LA::load_direct and load_b_rows_direct) at per-lane byte
-    // offsets fixed for the kernel, rows or columns past the operand at bit
-    // 31 (read as zeros), plus the K-tile's part as the scalar offset: per
-    // load one M0 write and the load, against eight address instructions
-    // recomputed per K-tile. A last K-tile that K does not fill takes the
-    // checked loaders.
+    // The K-tile's eight straight-to-LDS loads (four of A, four of B) with
+    // their offsets computed once (kcd_offsets / rows_offsets).
     const int wv = __builtin_amdgcn_readfirstlane(wave);
     uint32_t voa[4], vob[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int slot = (4 * i + wv) * 64 + lane;
-        if constexpr (ATR) {
-            const uint32_t gc = row0 + 4 * (slot & 31);
-            voa[i] = gc < g.m ? static_cast<uint32_t>(((slot >> 5) * g.sak + gc) * 4) : 0x80000000u;
-        } else {
-            const int r = slot >> 3;
-            const uint32_t gr = row0 + r;
-            voa[i] = gr < g.m ? static_cast<uint32_t>((gr * g.sam + 4 * ((slot & 7) ^ kcd_swizzle(r))) * 4)
-                              : 0x80000000u;
-        }
-        const uint32_t gc = col0 + 4 * (slot & 31);
-        vob[i] = gc < g.n ? static_cast<uint32_t>(((slot >> 5) * g.sbk + gc) * 4) : 0x80000000u;
-    }
+    if constexpr (ATR)
+        rows_offsets<BM>(voa, wv, lane, g.sak, row0, g.m);
+    else
+        kcd_offsets<BM>(voa, wv, lane, g.sam, row0, g.m);
+    rows_offsets<BN>(vob, wv, lane, g.sbk, col0, g.n);
     const uint32_t a_step = static_cast<uint32_t>((ATR ? g.sak : 1) * BK * 4);
     const uint32_t b_step = static_cast<uint32_t>(g.sbk * BK * 4);
     auto load_tile = [&](uint32_t kt, int dst) {
@@ -755,17 +806,8 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
             load_b_rows_direct(lds[dst] + BM * LDK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
             return;
         }
-        const uint32_t sa = kt * a_step, sb = kt * b_step;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                arsrc, (__attribute__((address_space(3))) void*)(lds[dst] + (4 * i + wv) * 256), 16, voa[i],
-                sa, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                brsrc, (__attribute__((address_space(3))) void*)(lds[dst] + BM * LDK + (4 * i + wv) * 256), 16,
-                vob[i], sb, 0, 0);
+        issue_direct<BM / 32>(lds[dst], arsrc, voa, wv, kt * a_step);
+        issue_direct<BN / 32>(lds[dst] + BM * LDK, brsrc, vob, wv, kt * b_step);
     };
     if (kt0 < kt1) load_tile(kt0, 0);
     __syncthreads();
@@ -889,6 +931,9 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
         fo4[h] = q.off * 4;
     }
 
+    uint32_t voa[BM / 32];
+    kcd_offsets<BM>(voa, wave, lane, g.sam, row0, g.m);
+
     f32x16 acc[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
@@ -923,7 +968,10 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
             const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(g.a + static_cast<int64_t>(n) * g.sa1), 0,
                 static_cast<int32_t>(0x80000000u), 0x00020000);
-            LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, p0, kimg, tid);
+            if (p0 + BK <= kimg)
+                issue_direct<BM / 32>(lds[dst], arsrc, voa, wave, p0 * 4);
+            else
+                LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, p0, kimg, tid);
             const __amdgpu_buffer_rsrc_t img = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(im.x + static_cast<int64_t>(n) * im.sn), 0,
                 static_cast<int32_t>(0x80000000u), 0x00020000);
@@ -1063,12 +1111,26 @@ __global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t voa[2], vob[2];
+    if constexpr (ATR)
+        rows_offsets<BM>(voa, wv, lane, g.sak, row0, g.m);
+    else
+        kcd_offsets<BM>(voa, wv, lane, g.sam, row0, g.m);
+    rows_offsets<BN>(vob, wv, lane, g.sbk, col0, g.n);
+    const uint32_t a_step = static_cast<uint32_t>((ATR ? g.sak : 1) * BK * 4);
+    const uint32_t b_step = static_cast<uint32_t>(g.sbk * BK * 4);
     auto load_tile = [&](uint32_t kt, int dst) {
-        if constexpr (ATR)
-            load_rows_direct<BM>(lds[dst], arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
-        else
-            LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
-        load_rows_direct<BN>(lds[dst] + BM * BK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+        if ((kt + 1) * BK > g.k) {
+            if constexpr (ATR)
+                load_rows_direct<BM>(lds[dst], arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
+            else
+                LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+            load_rows_direct<BN>(lds[dst] + BM * BK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+            return;
+        }
+        issue_direct<BM / 32>(lds[dst], arsrc, voa, wv, kt * a_step);
+        issue_direct<BN / 32>(lds[dst] + BM * BK, brsrc, vob, wv, kt * b_step);
     };
     if (kt0 < kt1) load_tile(kt0, 0);
     __syncthreads();
