@@ -549,6 +549,19 @@ uint32_t vkhip_fast_divide(uint32_t n, uint32_t d);
  * the padding. */
 int vkhip_im2col_offset(const vkhip_unfold* p, uint32_t channels, const int64_t* x_strides,
                         uint32_t row, uint32_t pos, int64_t* out_offset);
+/* The same map as the weight-gradient gather computes it (the transposed
+ * columns gathered by LDS-direct loads: a window row's fixed part plus a
+ * position's part, bounds-tested): offset of cols element (row, pos) or -1. */
+int vkhip_im2col_offset_t(const vkhip_unfold* p, uint32_t channels, const int64_t* x_strides,
+                          uint32_t row, uint32_t pos, int64_t* out_offset);
+/* Byte offset the straight-to-LDS (KCD) loader reads for 16-byte slot `slot`
+ * of a stage of an operand with row stride s_row (elements), rows from row0,
+ * K-tile k0 of kdim; 0x80000000 when the row or k-group is past the operand
+ * (read as zeros). The loader requires kdim a multiple of four and 16-byte
+ * aligned rows; tests replay it to check every access is aligned and inside
+ * the operand. */
+uint32_t vkhip_kcd_slot_offset(uint32_t slot, int64_t s_row, uint32_t row0, uint32_t rows,
+                               uint32_t k0, uint32_t kdim);
 
 #ifdef __cplusplus
 }

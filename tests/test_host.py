@@ -171,12 +171,16 @@ def test_fast_divide_is_exact():
     ((1, 3, 9, 11), (5, 3), (2, 3), (2, 1), (1, 2)),
 ])
 @pytest.mark.parametrize("layout", ["nchw", "nhwc"])
-def test_implicit_im2col_map_matches_the_oracle_unfold(shape, kernel, stride, pad, dil, layout):
-    """The (row, pos) -> image offset map the convolution GEMM gathers with,
-    evaluated by the library's own host build of the device function, picks
-    exactly the oracle's im2col element for every column entry (0 where the
-    window covers padding), for a plain and a channels-last image layout."""
+@pytest.mark.parametrize("gather", ["vkhip_im2col_offset", "vkhip_im2col_offset_t"])
+def test_implicit_im2col_map_matches_the_oracle_unfold(shape, kernel, stride, pad, dil, layout, gather):
+    """The (row, pos) -> image offset maps the convolution GEMMs gather with
+    (the forward's register-path loader; the weight gradient's LDS-direct
+    loader), evaluated by the library's own host build of the device
+    functions, pick exactly the oracle's im2col element for every column
+    entry (0 where the window covers padding), for a plain and a channels-last
+    image layout."""
     lib = _lib.load()
+    offset_of = getattr(lib, gather)
     _, c, h, w = shape
     img = np.arange(c * h * w, dtype=np.float32).reshape(c, h, w) + 1.0
     strides = (h * w, w, 1) if layout == "nchw" else (1, w * c, c)
@@ -192,9 +196,52 @@ def test_implicit_im2col_map_matches_the_oracle_unfold(shape, kernel, stride, pa
     got = np.empty_like(want)
     for row in range(want.shape[0]):
         for pos in range(want.shape[1]):
-            assert lib.vkhip_im2col_offset(byref(u), c, st, row, pos, byref(off)) == 0
+            assert offset_of(byref(u), c, st, row, pos, byref(off)) == 0
             got[row, pos] = 0.0 if off.value < 0 else storage[off.value]
     assert got.tobytes() == want.tobytes()
+
+
+def _kcd_stage_accesses(lib, rows_tile, s_row, row0, rows, k0, kdim):
+    """Every (LDS float index, byte offset) a KCD stage of `rows_tile` rows
+    loads, from the library's host build of the loader's slot map."""
+    out = []
+    for slot in range(rows_tile * 8):
+        off = lib.vkhip_kcd_slot_offset(slot, s_row, row0, rows, k0, kdim)
+        out.append((4 * slot, None if off & 0x80000000 else off))
+    return out
+
+
+@pytest.mark.parametrize("cout,k", [(4, 27), (64, 27), (2, 18), (6, 45), (64, 576), (128, 1152),
+                                    (5, 8), (128, 784)])
+def test_kcd_loader_stays_inside_the_operand_when_its_conditions_hold(cout, k):
+    """The straight-to-LDS (KCD) loader's accesses for a [Cout, K] weight
+    operand, replayed on the host from the library's own slot map over every
+    K-tile and row tile: each 16-byte stage slot is written once, inside the
+    stage. With K a multiple of four (the condition the kernels launch it
+    under) every load is 16-byte aligned and inside the operand. With K not a
+    multiple of four -- the convolution weights' A operand of CIFAR conv1 and
+    of the first conv test geometry, K = 3*3*3 = 27 -- loads start at
+    addresses that are not 16-byte aligned and the last row's last group
+    reads past the operand's end: what a conv kernel loading its weights this
+    way did before it ended in a GPU memory fault, and why conv2d_forward only
+    takes the straight-to-LDS paths when K % 4 == 0."""
+    lib = _lib.load()
+    nbytes = cout * k * 4
+    misaligned = overrun = 0
+    for rows_tile in (64, 128):
+        for row0 in range(0, cout, rows_tile):
+            for k0 in range(0, k, 32):
+                acc = _kcd_stage_accesses(lib, rows_tile, k, row0, cout, k0, k)
+                assert sorted(i for i, _ in acc) == list(range(0, rows_tile * 32, 4))
+                for _, off in acc:
+                    if off is None:
+                        continue
+                    misaligned += off % 16 != 0
+                    overrun += off + 16 > nbytes
+    if k % 4 == 0:
+        assert misaligned == 0 and overrun == 0
+    else:
+        assert misaligned > 0 and overrun > 0
 
 
 # ---- node extent checks (vkhip_supports is host-only: no device needed) ----

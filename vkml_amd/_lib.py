@@ -112,6 +112,9 @@ SIGNATURES = {
                                              POINTER(Unfold)]),
     "vkhip_im2col_offset": (c_int, [POINTER(Unfold), c_uint32, POINTER(c_int64), c_uint32, c_uint32,
                                     POINTER(c_int64)]),
+    "vkhip_im2col_offset_t": (c_int, [POINTER(Unfold), c_uint32, POINTER(c_int64), c_uint32, c_uint32,
+                                      POINTER(c_int64)]),
+    "vkhip_kcd_slot_offset": (c_uint32, [c_uint32, c_int64, c_uint32, c_uint32, c_uint32, c_uint32]),
     "vkhip_subscribe_decisions": (c_int, [DECISION_FN, c_void_p]),
     "vkhip_set_profiling": (c_int, [c_int]),
     "vkhip_profile_read": (c_int, [POINTER(ProfileRecord), c_size_t, POINTER(c_size_t),

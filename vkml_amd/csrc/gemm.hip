@@ -110,6 +110,18 @@ enum LoadMode { KCV = 0, RCV = 1, KCS = 2, RCS = 3, IMG = 4, IMGT = 5, KCD = 6, 
 // read, 1/6 of the LDS cycles by SQ_LDS_BANK_CONFLICT.)
 __host__ __device__ constexpr int kcd_swizzle(int row) { return (row >> 1) & 7; }
 
+// The byte offset a KCD loader reads for 16-byte slot `slot` of a stage (row
+// slot / 8, k-group (slot % 8) ^ kcd_swizzle(row)), or bit 31 (read as 0) for
+// a row or k-group past the operand. The loader needs K a multiple of four
+// (a group inside K is inside the row) and 16-byte aligned rows.
+__host__ __device__ __forceinline__ uint32_t kcd_slot_offset(int slot, int64_t s_row, uint32_t row0,
+                                                            uint32_t rows, uint32_t k0, uint32_t kdim) {
+    const int r = slot >> 3;
+    const uint32_t gr = row0 + r, gk = k0 + 4 * ((slot & 7) ^ kcd_swizzle(r));
+    return gr < rows && gk < kdim ? static_cast<uint32_t>((static_cast<int64_t>(gr) * s_row + gk) * 4)
+                                  : 0x80000000u;
+}
+
 // The B operand of a convolution read straight from the image (implicit
 // im2col): element (row, pos) of image n's cols matrix [C*kh*kw, out_h*out_w]
 // is x[n, c, h, w] with row = c*kh*kw + ki*kw + kj, pos = oh*out_w + ow,
@@ -276,13 +288,7 @@ struct TileLoader {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
             const int chunk = 4 * i + wave;
-            const int slot = chunk * 64 + lane;
-            const int r = slot >> 3;
-            const int grp = (slot & 7) ^ kcd_swizzle(r);
-            const uint32_t gr = row0 + r, gk = k0 + 4 * grp;
-            const bool ok = gr < rows && gk < kdim;
-            const uint32_t off = ok ? static_cast<uint32_t>((static_cast<int64_t>(gr) * s_row + gk) * 4)
-                                    : 0x80000000u;
+            const uint32_t off = kcd_slot_offset(chunk * 64 + lane, s_row, row0, rows, k0, kdim);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 src, (__attribute__((address_space(3))) void*)(stage + chunk * 256), 16, off, 0, 0, 0);
         }
@@ -455,13 +461,7 @@ template <int R>
 __device__ __forceinline__ void kcd_offsets(uint32_t (&vo)[R / 32], int wv, int lane, int64_t s_row,
                                             uint32_t row0, uint32_t rows) {
 #pragma unroll
-    for (int i = 0; i < R / 32; ++i) {
-        const int slot = (4 * i + wv) * 64 + lane;
-        const int r = slot >> 3;
-        const uint32_t gr = row0 + r;
-        vo[i] = gr < rows ? static_cast<uint32_t>((gr * s_row + 4 * ((slot & 7) ^ kcd_swizzle(r))) * 4)
-                          : 0x80000000u;
-    }
+    for (int i = 0; i < R / 32; ++i) vo[i] = kcd_slot_offset((4 * i + wv) * 64 + lane, s_row, row0, rows, 0, ~0u);
 }
 template <int COLS>
 __device__ __forceinline__ void rows_offsets(uint32_t (&vo)[COLS / 32], int wv, int lane, int64_t s_k,
@@ -873,6 +873,43 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
     }
 }
 
+// The weight-gradient gather's address arithmetic (conv_direct_kernel), also
+// built for the host so tests replay it (vkhip_im2col_offset_t). Column j of
+// the transposed columns (a window row: channel, window element) contributes
+// a fixed offset and displacement; a position contributes the window's origin;
+// an element is inside when both displacements land in the image.
+struct GatherCol {
+    int32_t fo4, fh, fw;  // 4 * offset, row and column displacement
+    bool ok;              // j < C*kh*kw
+};
+__host__ __device__ __forceinline__ GatherCol gather_col(const Im2colB& im, uint32_t j, uint32_t ncols) {
+    GatherCol c;
+    c.ok = j < ncols;
+    const ImgRow q = img_row(im, c.ok ? j : 0u);
+    const uint32_t ki = im.div_kw.div(static_cast<uint32_t>(q.r));
+    c.fh = static_cast<int32_t>(ki) * im.dilh;
+    c.fw = (q.r - static_cast<int32_t>(ki) * im.kw) * im.dilw;
+    c.fo4 = q.off * 4;
+    return c;
+}
+struct GatherPos {
+    int32_t sh, sw, so4;  // window origin row, column and 4 * its offset
+};
+__host__ __device__ __forceinline__ GatherPos gather_pos(const Im2colB& im, uint32_t oh, uint32_t ow) {
+    GatherPos q;
+    q.sh = static_cast<int32_t>(oh) * im.strh - im.padh;
+    q.sw = static_cast<int32_t>(ow) * im.strw - im.padw;
+    q.so4 = (q.sh * im.sh + q.sw * im.sw) * 4;
+    return q;
+}
+// byte offset of the element in the image, or bit 31 (read as 0)
+__host__ __device__ __forceinline__ uint32_t gather_offset(const Im2colB& im, const GatherCol& c,
+                                                           int32_t sh, int32_t sw, int32_t so4, bool kok) {
+    const bool inside = kok & c.ok & (static_cast<uint32_t>(sh + c.fh) < static_cast<uint32_t>(im.H)) &
+                        (static_cast<uint32_t>(sw + c.fw) < static_cast<uint32_t>(im.W));
+    return inside ? static_cast<uint32_t>(so4) + static_cast<uint32_t>(c.fo4) : 0x80000000u;
+}
+
 // The convolution weight gradient's products with both operands straight into
 // LDS, in gemm_nn_direct_kernel's layouts (A KCD-swizzled [128 rows][32 k],
 // B [32 k][128 columns]) and MFMA order, so the same bits as that kernel on
@@ -918,18 +955,9 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
     const uint32_t kimg = CD == CD_WGRAD_FOLD ? im.L : g.k;
 
     // this lane's two B columns j = col0 + 64 h + lane: channel and window element
-    int32_t fo4[2], fh[2], fw[2];
-    bool fok[2];
+    GatherCol col_of[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t j = col0 + 64 * h + lane;
-        fok[h] = j < g.n;
-        const ImgRow q = img_row(im, fok[h] ? j : 0u);
-        const uint32_t ki = im.div_kw.div(static_cast<uint32_t>(q.r));
-        fh[h] = static_cast<int32_t>(ki) * im.dilh;
-        fw[h] = (q.r - static_cast<int32_t>(ki) * im.kw) * im.dilw;
-        fo4[h] = q.off * 4;
-    }
+    for (int h = 0; h < 2; ++h) col_of[h] = gather_col(im, col0 + 64 * h + lane, g.n);
 
     uint32_t voa[BM / 32];
     kcd_offsets<BM>(voa, wave, lane, g.sam, row0, g.m);
@@ -947,11 +975,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
                               int32_t so4_k) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const bool inside = kok & fok[h] &
-                                    (static_cast<uint32_t>(sh_k + fh[h]) < static_cast<uint32_t>(im.H)) &
-                                    (static_cast<uint32_t>(sw_k + fw[h]) < static_cast<uint32_t>(im.W));
-                const uint32_t off =
-                    inside ? static_cast<uint32_t>(so4_k) + static_cast<uint32_t>(fo4[h]) : 0x80000000u;
+                const uint32_t off = gather_offset(im, col_of[h], sh_k, sw_k, so4_k, kok);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     img,
                     (__attribute__((address_space(3))) void*)(lds[dst] + BM * LDK + (8 * wave + rr) * BN +
@@ -981,9 +1005,8 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
             uint32_t ow = p - oh * static_cast<uint32_t>(im.ow);
 #pragma unroll
             for (int rr = 0; rr < 8; ++rr) {
-                const int32_t h0 = static_cast<int32_t>(oh) * im.strh - im.padh;
-                const int32_t w0 = static_cast<int32_t>(ow) * im.strw - im.padw;
-                gather_row(img, rr, p < kimg, h0, w0, (h0 * im.sh + w0 * im.sw) * 4);
+                const GatherPos q = gather_pos(im, oh, ow);
+                gather_row(img, rr, p < kimg, q.sh, q.sw, q.so4);
                 ++p;
                 ++ow;
                 const bool wrap = ow == static_cast<uint32_t>(im.ow);
@@ -2601,6 +2624,28 @@ extern "C" int vkhip_conv2d_weight_grad_sum(const float* x, const vkhip_operand*
     vkhip::Unit unit("conv2d_weight_grad_sum");
     if (!x_desc || !grad_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d_weight_grad_sum: null argument");
     return vkhip::conv2d_weight_grad_sum(x, *x_desc, grad, *grad_desc, out, *p);
+}
+
+extern "C" uint32_t vkhip_kcd_slot_offset(uint32_t slot, int64_t s_row, uint32_t row0, uint32_t rows,
+                                          uint32_t k0, uint32_t kdim) {
+    return vkhip::kcd_slot_offset(static_cast<int>(slot), s_row, row0, rows, k0, kdim);
+}
+
+extern "C" int vkhip_im2col_offset_t(const vkhip_unfold* p, uint32_t channels, const int64_t* x_strides,
+                                     uint32_t row, uint32_t pos, int64_t* out_offset) {
+    if (!p || !x_strides || !out_offset) return vkhip::fail(VKHIP_ERR_INVALID, "im2col_offset_t: null argument");
+    vkhip::Im2colB im{};
+    const int st = vkhip::make_im2col(*p, channels, x_strides, im);
+    if (st != VKHIP_OK) return st;
+    // The weight-gradient gather's arithmetic (conv_direct_kernel): the
+    // window row's fixed part, the position's scalar part, the bounds test.
+    const uint32_t ncols = channels * static_cast<uint32_t>(p->kernel_h * p->kernel_w);
+    const vkhip::GatherCol c = vkhip::gather_col(im, row, ncols);
+    const uint32_t oh = im.div_ow.div(pos);
+    const vkhip::GatherPos q = vkhip::gather_pos(im, oh, pos - oh * static_cast<uint32_t>(im.ow));
+    const uint32_t at4 = vkhip::gather_offset(im, c, q.sh, q.sw, q.so4, true);
+    *out_offset = (at4 >> 31) ? -1 : static_cast<int64_t>(at4 / 4);
+    return VKHIP_OK;
 }
 
 extern "C" int vkhip_im2col_offset(const vkhip_unfold* p, uint32_t channels, const int64_t* x_strides,
