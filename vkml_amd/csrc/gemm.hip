@@ -578,7 +578,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         (void)dst;
         // (The order matters for the schedule: with A straight into LDS and
         // B through registers, A's loads go first; measured 4% on NN.)
-        if constexpr (AMODE == KCD && BMODE != KCD) {
+        constexpr bool kImgB = BMODE == IMG || BMODE == IMGT || BMODE == IMGTB;
+        if constexpr (AMODE == KCD && BMODE != KCD && !kImgB) {
             a_direct(kt, dst);
             if (rows_in && (kt + 1) * BK <= g.k)
                 LB::template load<false>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
@@ -593,12 +594,19 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
                 LA::template load<true>(ra, abase, g.sam, g.sak, row0, g.m, kt * BK, g.k, tid);
             b_direct(kt, dst);
         } else if constexpr (BMODE == IMG) {
-            LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
+            if constexpr (AMODE == KCD)
+                a_direct(kt, dst);
+            else
+                LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
             LB::load_img(rb, img, rows, base4, outside, kt * BK, tid);
         } else if constexpr (BMODE == IMGT) {
-            LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
+            if constexpr (AMODE == KCD)
+                a_direct(kt, dst);
+            else
+                LA::load_clamped(ra, abase, g.sam, row0, g.m, kt * BK, g.k, tid);
             LB::load_imgt(rb, img, im_in, trows, kt * BK, g.k, tid);
         } else if constexpr (BMODE == IMGTB) {
+            static_assert(AMODE != KCD, "IMGTB switches image per K-tile: A on the register path");
             // K-tile kt is positions p0 .. p0 + BK - 1 of image n (L is a
             // multiple of BK). The tile after the last, loaded and unused,
             // stays on the last image with positions past L: every load then
@@ -1580,6 +1588,12 @@ static int launch_conv_tiles(const GemmArgs& g, const Im2colB& im, uint32_t batc
     switch (amode) {
         case KCV: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCV, BMODE>), grid, dim3(256), 0, st, g, im); break;
         case KCS: hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCS, BMODE>), grid, dim3(256), 0, st, g, im); break;
+        case KCD:
+            if constexpr (BMODE != IMGTB) {
+                hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, KCD, BMODE>), grid, dim3(256), 0, st, g, im);
+                break;
+            }
+            return fail(VKHIP_ERR_INVALID, "conv2d: the batch-folded product takes no straight-to-LDS A");
         default: return fail(VKHIP_ERR_INVALID, "conv2d: A operand load mode %d", amode);
     }
     VKHIP_LAUNCH_CHECK();
@@ -2160,7 +2174,12 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
         g.split_stride = out_elems;
     }
     g.c = target;
-    const int amode = g.a_vec ? KCV : KCS;
+    // The weights or gradient rows straight into LDS when the KCD loader's
+    // conditions hold (K a multiple of four, 16-byte aligned rows: a_vec;
+    // byte offsets within 2^31), else through registers.
+    const bool a_kcd = g.a_vec && g.sam >= 0 &&
+                       ((static_cast<int64_t>(m) - 1) * g.sam + k) * 4 < (int64_t{1} << 31);
+    const int amode = a_kcd ? KCD : (g.a_vec ? KCV : KCS);
     int st;
     if (tile.bm == 128)
         st = launch_conv_tiles<128, 128, 64, 64, IMG>(g, im, static_cast<uint32_t>(batch), splits, amode);
@@ -2260,7 +2279,12 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
     g.chunk = chunk;
     g.a_vec = reinterpret_cast<uintptr_t>(gr) % 16 == 0 && g.sam % 4 == 0 && g.sa1 % 4 == 0 &&
               k % 4 == 0;
-    const int amode = g.a_vec ? KCV : KCS;
+    // The weights or gradient rows straight into LDS when the KCD loader's
+    // conditions hold (K a multiple of four, 16-byte aligned rows: a_vec;
+    // byte offsets within 2^31), else through registers.
+    const bool a_kcd = g.a_vec && g.sam >= 0 &&
+                       ((static_cast<int64_t>(m) - 1) * g.sam + k) * 4 < (int64_t{1} << 31);
+    const int amode = a_kcd ? KCD : (g.a_vec ? KCV : KCS);
     const uint64_t out_elems = batch * m * n;
     float* target = out;
     if (splits > 1) {
