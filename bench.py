@@ -338,6 +338,11 @@ def case_gemv(name, hip, ops, timer, rng, out):
     y = DeviceArray((4096,), np.float32)
     ms = time_batch(lambda i: ops.gemv(mats[i % 8], x, out=y), timer, 40)
     _bw(out, name, ms, 4096 * 4096 * 4 + 4096 * 4 * 2)
+    # the floor of one launch that reads these bytes: the library's row sum of
+    # the same rotated matrices (the same reads, no vector, no products)
+    ms_sum = time_batch(lambda i: ops.sum(mats[i % 8], [1], out=y), timer, 40)
+    out[name]["row_sum_same_matrix_ms"] = round(ms_sum, 5)
+    out[name]["frac_of_row_sum"] = round(ms_sum / ms, 4)
 
 
 def case_im2col_col2im(name, hip, ops, timer, rng, out):

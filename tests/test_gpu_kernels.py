@@ -889,6 +889,23 @@ def test_copy_device_to_device_batch(hip):
         hip.copy_device_to_device([(DeviceArray((6, 4), np.float32), m.transpose(0, 1))])
 
 
+@pytest.mark.parametrize("shape,perm", [((8192, 256), (1, 0)), ((256, 100), (1, 0)), ((65, 130), (1, 0)),
+                                        ((3, 100, 37), (0, 2, 1)), ((2, 3, 65, 130), (0, 1, 3, 2)),
+                                        ((2, 3, 5, 7), (1, 0, 3, 2)), ((1, 64), (1, 0))])
+def test_contiguous_of_a_transposed_view_is_the_values(hip, shape, perm):
+    """CONTIGUOUS of views whose last two axes are transposed (the tiled
+    transpose path; the weight gradients of x @ w.T arrive this way) and of
+    other permutations: the values, byte for byte."""
+    from vkml_amd.device import contiguous
+
+    x = np.random.default_rng(SEED + 96).standard_normal(shape).astype(np.float32)
+    base = dev(x)
+    d = DeviceArray([base.shape[p] for p in perm], np.float32, [base.strides[p] for p in perm],
+                    base.buffer, base.offset)
+    got = contiguous(d).numpy()
+    assert got.tobytes() == np.ascontiguousarray(np.transpose(x, perm)).tobytes()
+
+
 def test_supports_predicate_and_unsupported_compute(hip):
     """vkhip_supports reports exactly the implemented (op, dtype) set: a float
     relu node is supported, an op this backend lacks and a relu over int64

@@ -318,6 +318,37 @@ static Src make_src(const vkhip_tensor& t) {
     return s;
 }
 
+// Materialising a transposed view: out [B0, B1, R, C] contiguous from a
+// source whose element (b0, b1, r, c) sits at b0*s0 + b1*s1 + r + c*sc (unit
+// stride down the rows: a transpose of the last two axes, as autograd's
+// weight gradients of x @ w.T arrive). 64x64 tiles through LDS so that both
+// the reads (along r) and the writes (along c) are contiguous; the generic
+// strided copy reads a 4-byte element per cache line.
+__global__ __launch_bounds__(256) void transpose_copy_kernel(const float* __restrict__ src, int64_t s0,
+                                                             int64_t s1, int64_t sc,
+                                                             float* __restrict__ dst, uint32_t b1n,
+                                                             uint32_t R, uint32_t C, uint32_t tiles_c) {
+    __shared__ float tile[64][65];
+    const uint32_t t = threadIdx.x;
+    const uint32_t tr = blockIdx.x / tiles_c, tc = blockIdx.x - tr * tiles_c;
+    const uint32_t r0 = tr * 64, c0 = tc * 64;
+    const uint32_t b = blockIdx.y, b0 = b / b1n, b1 = b - b0 * b1n;
+    const float* sp = src + static_cast<int64_t>(b0) * s0 + static_cast<int64_t>(b1) * s1;
+    float* dp = dst + static_cast<uint64_t>(b) * R * C;
+    const uint32_t lr = t & 63, lc = t >> 6;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t c = c0 + lc + 4 * i, r = r0 + lr;
+        if (c < C && r < R) tile[lc + 4 * i][lr] = sp[static_cast<int64_t>(c) * sc + r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t r = r0 + lc + 4 * i, c = c0 + lr;
+        if (c < C && r < R) dp[static_cast<uint64_t>(r) * C + c] = tile[lr][lc + 4 * i];
+    }
+}
+
 int launch_elementwise(const vkhip_node& nd) {
     const uint64_t n = tnumel(nd.out);
     if (n == 0) return VKHIP_OK;
@@ -345,6 +376,37 @@ int launch_elementwise(const vkhip_node& nd) {
                                static_cast<float*>(nd.out.data), n4, ab[0], ab[1]);
             VKHIP_LAUNCH_CHECK();
             return VKHIP_OK;
+        }
+    }
+    // A transposed view made contiguous (transpose_copy_kernel).
+    if (op == VKHIP_OP_CONTIGUOUS && nd.out.dtype == VKHIP_F32 && nd.src[0].dtype == VKHIP_F32 &&
+        nd.out.ndim >= 2 && nd.out.ndim <= 4 && is_contig(nd.out)) {
+        const vkhip_tensor& x = nd.src[0];
+        const int d = x.ndim;
+        const int64_t R = x.ne[d - 2], C = x.ne[d - 1];
+        if (x.nb[d - 2] == 1 && x.nb[d - 1] != 1 && C > 1 && R > 1 && R < (1ll << 31) && C < (1ll << 31)) {
+            int64_t b0n = 1, b1n = 1, s0 = 0, s1 = 0;
+            if (d == 3) {
+                b1n = x.ne[0];
+                s1 = x.nb[0];
+            } else if (d == 4) {
+                b0n = x.ne[0];
+                s0 = x.nb[0];
+                b1n = x.ne[1];
+                s1 = x.nb[1];
+            }
+            const uint32_t tiles_c = static_cast<uint32_t>((C + 63) / 64);
+            const uint64_t tiles = static_cast<uint64_t>(tiles_c) * ((R + 63) / 64);
+            if (tiles <= 0x7fffffffull && b0n * b1n <= 65535) {
+                hipLaunchKernelGGL(transpose_copy_kernel, dim3(static_cast<uint32_t>(tiles),
+                                                               static_cast<uint32_t>(b0n * b1n)),
+                                   dim3(256), 0, st, static_cast<const float*>(x.data), s0, s1,
+                                   x.nb[d - 1], static_cast<float*>(nd.out.data),
+                                   static_cast<uint32_t>(b1n), static_cast<uint32_t>(R),
+                                   static_cast<uint32_t>(C), tiles_c);
+                VKHIP_LAUNCH_CHECK();
+                return VKHIP_OK;
+            }
         }
     }
     // Broadcast second operand of a bias add (see elementwise_bcast_vec_kernel).
