@@ -1048,7 +1048,7 @@ constexpr uint32_t kSubtreeMax = 8192;  // elements one workgroup stages
 
 __global__ __launch_bounds__(256) void reduce_subtree_kernel(const float* __restrict__ src,
                                                              Op4 kept, Reader rd, uint32_t n,
-                                                             int depth, int split,
+                                                             int depth, int split, int vec,
                                                              float* __restrict__ partial) {
     __shared__ __attribute__((aligned(16))) float stage[(kSubtreeMax + 4 * (kSubtreeMax / 32) + 3) & ~3u];
     __shared__ float scratch[4];
@@ -1058,16 +1058,38 @@ __global__ __launch_bounds__(256) void reduce_subtree_kernel(const float* __rest
     pairwise_leaf(n, split, j, b, e);
     const uint32_t m = e - b;
     constexpr int kBatch = kSubtreeMax / 256;
-    float v[kBatch];
+    if (vec && (b & 3u) == 0) {
+        // Runs of four consecutive reduced elements are adjacent and 16-byte
+        // aligned (host-checked): one offset and one 16-byte load per four,
+        // staged as one 16-byte store (stage_index keeps groups of four).
+        f32x4_t v[kBatch / 4];
 #pragma unroll
-    for (int r = 0; r < kBatch; ++r) {
-        const uint32_t i = threadIdx.x + 256u * r;
-        v[r] = i < m ? base[rd.off(b + i)] : 0.0f;
-    }
+        for (int r = 0; r < kBatch / 4; ++r) {
+            const uint32_t i = 4u * (threadIdx.x + 256u * r);
+            if (i + 3 < m) {
+                v[r] = *reinterpret_cast<const f32x4_t*>(base + rd.off(b + i));
+            } else {
 #pragma unroll
-    for (int r = 0; r < kBatch; ++r) {
-        const uint32_t i = threadIdx.x + 256u * r;
-        if (i < m) stage[stage_index(i)] = v[r];
+                for (int q = 0; q < 4; ++q) v[r][q] = i + q < m ? base[rd.off(b + i + q)] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kBatch / 4; ++r) {
+            const uint32_t i = 4u * (threadIdx.x + 256u * r);
+            if (i < m) *reinterpret_cast<f32x4_t*>(stage + stage_index(i)) = v[r];
+        }
+    } else {
+        float v[kBatch];
+#pragma unroll
+        for (int r = 0; r < kBatch; ++r) {
+            const uint32_t i = threadIdx.x + 256u * r;
+            v[r] = i < m ? base[rd.off(b + i)] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < kBatch; ++r) {
+            const uint32_t i = threadIdx.x + 256u * r;
+            if (i < m) stage[stage_index(i)] = v[r];
+        }
     }
     __syncthreads();
     const float sum = group_pairwise_sum<256>(stage, m, depth - split, threadIdx.x, scratch);
@@ -1086,17 +1108,28 @@ __global__ __launch_bounds__(256) void reduce_subtree_fold_kernel(const float* _
 #pragma unroll
     for (int l = 0; l < 8; ++l) stack[l] = 0.0f;
     const uint32_t parts = 1u << split;
-    for (uint32_t j = 0; j < parts; ++j) {
-        float sv = partial[static_cast<uint64_t>(j) * n_out + o];
-        bool carry = true;
+    // The partials of a group of eight are loaded before any is pushed, so
+    // their latencies overlap (one dependent load per push took ~5 us for 16).
+    for (uint32_t j0 = 0; j0 < parts; j0 += 8) {
+        float pv[8];
 #pragma unroll
-        for (int l = 0; l < 8; ++l) {
-            if (carry) {
-                if ((j >> l) & 1u) {
-                    sv = stack[l] + sv;
-                } else {
-                    stack[l] = sv;
-                    carry = false;
+        for (int q = 0; q < 8; ++q)
+            pv[q] = j0 + q < parts ? partial[static_cast<uint64_t>(j0 + q) * n_out + o] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t j = j0 + q;
+            if (j >= parts) break;
+            float sv = pv[q];
+            bool carry = true;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                if (carry) {
+                    if ((j >> l) & 1u) {
+                        sv = stack[l] + sv;
+                    } else {
+                        stack[l] = sv;
+                        carry = false;
+                    }
                 }
             }
         }
@@ -1336,8 +1369,18 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
             float* part = nullptr;
             int rc = workspace((static_cast<size_t>(n_out) << split) * sizeof(float), &part);
             if (rc != VKHIP_OK) return rc;
+            // 16-byte loads: the innermost reduced axis contiguous in groups of
+            // four, every other stride and the base 16-byte aligned.
+            bool vec4 = reinterpret_cast<uintptr_t>(src) % 16 == 0;
+            if (rd.naxes == 1) {
+                vec4 = vec4 && rd.nb_outer == 1;
+            } else {
+                vec4 = vec4 && rd.nb[0] == 1 && rd.ne[0] % 4 == 0 && rd.nb_outer % 4 == 0;
+                for (int a = 1; a + 1 < rd.naxes; ++a) vec4 = vec4 && rd.nb[a] % 4 == 0;
+            }
+            for (int a = 0; a < 4; ++a) vec4 = vec4 && (kept.ne[a] == 1 || kept.nb[a] % 4 == 0);
             hipLaunchKernelGGL(reduce_subtree_kernel, dim3(1u << split, n_out), dim3(256), 0, st,
-                               src, kept, rd, n_red, depth, split, part);
+                               src, kept, rd, n_red, depth, split, vec4 ? 1 : 0, part);
             VKHIP_LAUNCH_CHECK();
             hipLaunchKernelGGL(reduce_subtree_fold_kernel, dim3(ceil_div(n_out, 256)), dim3(256), 0,
                                st, part, n_out, split, n_red, op == VKHIP_REDUCE_MEAN ? 1 : 0,
