@@ -163,7 +163,14 @@ enum vkhip_op {
      * transposed weight when C >= 32 (no column matrix; within the GEMM
      * tolerance of the graph); otherwise the TN product and col2im (the
      * graph's bits). */
-    VKHIP_OP_CONV2D_INPUT_GRAD = 102
+    VKHIP_OP_CONV2D_INPUT_GRAD = 102,
+    /* CONV2D with the bias add and ReLU that follow it in a conv layer: src0
+     * x, src1 w (as CONV2D), src2 bias [Cout] or [Cout,1,1] (any stride along
+     * channels) -> out = relu(conv2d(x, w) + bias[c]), where relu(v) = v <= 0
+     * ? 0 : v: the values of the CONV2D, ADD (bias broadcast) and RELU nodes
+     * it replaces, bit for bit, without writing and re-reading the two
+     * intermediates. */
+    VKHIP_OP_CONV2D_BIAS_RELU = 103
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */

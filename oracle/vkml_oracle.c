@@ -650,10 +650,12 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 or_im2col((const float*)nd->src[0].data, &s0, (float*)o->data, &p, threads);
                 break;
             }
-            case VKHIP_OP_CONV2D: {
+            case VKHIP_OP_CONV2D:
+            case VKHIP_OP_CONV2D_BIAS_RELU: {
                 /* The reference's conv2d graph (ops.cpp:662-705): im2col, then
                  * flat_weight [Cout, C*kh*kw] @ cols [N, C*kh*kw, L] with the
-                 * weight broadcast over the batch. */
+                 * weight broadcast over the batch; for CONV2D_BIAS_RELU then
+                 * the bias ADD (broadcast over N, H, W) and k_relu. */
                 vkhip_unfold p;
                 memcpy(&p, nd->params, sizeof p);
                 const vkhip_tensor* w = &nd->src[1];
@@ -668,6 +670,15 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                                     {0, ck * L, L, 1}};
                 or_matmul((const float*)w->data, &wd, cols, &cd, (float*)o->data, threads);
                 free(cols);
+                if (nd->op == VKHIP_OP_CONV2D_BIAS_RELU) {
+                    const float* bias = (const float*)nd->src[2].data;
+                    const int64_t bs = nd->src[2].nb[0], cout = o->ne[1];
+                    float* y = (float*)o->data;
+                    for (int64_t i = 0; i < o->ne[0] * cout * L; ++i) {
+                        const float v = y[i] + bias[((i / L) % cout) * bs];
+                        y[i] = unary_f(VKHIP_OP_RELU, v);
+                    }
+                }
                 break;
             }
             case VKHIP_OP_CONV2D_WEIGHT_GRAD: {

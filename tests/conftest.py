@@ -126,6 +126,28 @@ def conv_loss_and_grads(backend, x, w, bias, stride, pad, dil, implicit, x_grad=
         T.FUSED_CONV_INPUT_GRAD = prev_dx
 
 
+def conv_relu_loss_and_grads(backend, x, w, bias, stride, pad, dil, fused):
+    """sum(relu(conv2d(x, w, bias)) * probe) and the gradients of x, w and bias,
+    with relu(conv + bias) built as one CONV2D_BIAS_RELU node (fused) or as
+    the CONV2D, ADD and RELU nodes."""
+    from vkml_amd import tensor as T
+
+    prev = T.FUSED_CONV_EPILOGUE
+    T.FUSED_CONV_EPILOGUE = fused
+    try:
+        xt = T.tensor(x, requires_grad=True, backend=backend)
+        wt = T.tensor(w, requires_grad=True, backend=backend)
+        bt = T.tensor(bias, requires_grad=True, backend=backend)
+        out = T.relu(T.conv2d(xt, wt, bt, stride, pad, dil))
+        assert (out.node.op == T.OP["CONV2D_BIAS_RELU"]) == fused
+        probe = np.linspace(-1.0, 1.0, int(np.prod(out.shape)), dtype=np.float32)
+        loss = T.sum(out * T.tensor(probe.reshape(out.shape), backend=backend))
+        loss.backward()
+        return out.numpy(), xt.grad.numpy(), wt.grad.numpy(), bt.grad.numpy()
+    finally:
+        T.FUSED_CONV_EPILOGUE = prev
+
+
 def relu_inputs(shape, seed):
     """x and the output gradient g for the relu gradient, with NaN, +-0, +-inf
     in both (the select must pass NaN x through and keep g's bits)."""

@@ -13,7 +13,8 @@ import pytest
 
 import oracle as O
 from conftest import (CONFIG5_STEPS, CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad,
-                      config5_golden_losses, config5_train, conv_loss_and_grads)
+                      config5_golden_losses, config5_train, conv_loss_and_grads,
+                      conv_relu_loss_and_grads)
 from oracle import OracleBackend
 from vkml_amd import _lib, nn, ops, optim
 from vkml_amd import tensor as T
@@ -98,6 +99,21 @@ def test_exact_convolution_is_the_oracle(exact, cpu, shape, cout, kernel, stride
     bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
     dev = conv_loss_and_grads(exact, x, w, bias, stride, pad, dil, implicit=True)
     ref = conv_loss_and_grads(cpu, x, w, bias, stride, pad, dil, implicit=True)
+    for got, want in zip(dev, ref):
+        assert got.tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil",
+                         CONV_GEOMETRIES + [((16, 64, 16, 16), 32, (3, 3), (1, 1), (1, 1), (1, 1))])
+def test_exact_conv_bias_relu_is_the_oracle(exact, cpu, shape, cout, kernel, stride, pad, dil):
+    """The CONV2D_BIAS_RELU node on the exact arm (bias and ReLU applied after
+    the exact product) and its gradients: the oracle's bits."""
+    rng = np.random.default_rng(SEED + 19)
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
+    dev = conv_relu_loss_and_grads(exact, x, w, bias, stride, pad, dil, True)
+    ref = conv_relu_loss_and_grads(cpu, x, w, bias, stride, pad, dil, True)
     for got, want in zip(dev, ref):
         assert got.tobytes() == want.tobytes()
 

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad,
-                      config5_golden_losses, config5_train, conv_loss_and_grads, gemm_tolerance,
+                      config5_golden_losses, config5_train, conv_loss_and_grads, conv_relu_loss_and_grads,
+                      gemm_tolerance,
                       normwise_rel_err, relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
@@ -166,6 +167,28 @@ def test_conv_node_on_device_is_bit_identical_to_the_graph(backends, shape, cout
         ck = shape[1] * kernel[0] * kernel[1]
         for got, want, k in zip(node, ref, (ck, cout, shape[0] * node[0][0, 0].size, 1)):
             assert normwise_rel_err(got, want) <= gemm_tolerance(max(k, 2))
+
+
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil",
+                         CONV_GEOMETRIES + [((128, 64, 16, 16), 128, (3, 3), (1, 1), (1, 1), (1, 1)),
+                                            ((128, 3, 32, 32), 64, (3, 3), (1, 1), (1, 1), (1, 1)),
+                                            ((1, 64, 8, 8), 128, (3, 3), (1, 1), (1, 1), (1, 1))])
+def test_conv_bias_relu_node_on_device_is_the_three_nodes(backends, shape, cout, kernel, stride, pad,
+                                                          dil):
+    """On the device, relu(conv2d(x, w, bias)) as one CONV2D_BIAS_RELU node
+    (bias and ReLU in the conv kernel's epilogue, or in a pass after the
+    split-K fold: the last geometry splits) gives the CONV2D + ADD + RELU
+    graph's output and gradients bit for bit."""
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED + 13)
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
+    print(f"conv_bias_relu x={shape} cout={cout} k={kernel}", flush=True)
+    fused = conv_relu_loss_and_grads(dev, x, w, bias, stride, pad, dil, True)
+    graph = conv_relu_loss_and_grads(dev, x, w, bias, stride, pad, dil, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
 
 
 def test_bias_gradient_reduce_is_bit_exact(backends):

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads,
+                      conv_relu_loss_and_grads,
                       relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
@@ -186,6 +187,23 @@ def test_views_and_broadcast_resolve_by_aliasing(cpu):
     np.testing.assert_array_equal((t + T.tensor(np.ones(4, np.float32), backend=cpu)).numpy(), a + 1)
     np.testing.assert_array_equal(T.sum(t, [0]).numpy(), a.sum(0))
     np.testing.assert_array_equal(T.matmul(t, t.T).numpy(), a @ a.T)
+
+
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONV_GEOMETRIES)
+def test_conv_bias_relu_node_is_the_three_nodes(cpu, shape, cout, kernel, stride, pad, dil):
+    """relu(conv2d(x, w, bias)) as one CONV2D_BIAS_RELU node gives the CONV2D +
+    ADD + RELU graph's output and gradients bit for bit on the oracle (its
+    relu gradient taken from the output), including NaN and signed-zero
+    pre-activations."""
+    rng = np.random.default_rng(SEED + 11)
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    x.reshape(-1)[:3] = [np.nan, -0.0, 0.0]
+    w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, cout).astype(np.float32)
+    fused = conv_relu_loss_and_grads(cpu, x, w, bias, stride, pad, dil, True)
+    graph = conv_relu_loss_and_grads(cpu, x, w, bias, stride, pad, dil, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
 
 
 @pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONV_GEOMETRIES)

@@ -43,6 +43,12 @@ struct GemmArgs {
     uint64_t split_stride;       // elements between partition slices of c
     uint32_t a_vec, b_vec;       // 16-byte loads along k are legal
     uint32_t flat_splits;        // > 0: split grid launched flat, grid.x = tiles * flat_splits
+    // Convolution epilogue (unsplit register-path conv kernel only): out =
+    // acc + bias[row * bias_stride] when bias is set, then relu (x <= 0 ? 0 :
+    // x) when relu is set -- the ADD and RELU nodes' arithmetic.
+    const float* bias;
+    int64_t bias_stride;
+    uint32_t relu;
 };
 
 // Output tile (tm, tn) and K partition of this workgroup.
@@ -638,6 +644,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
 
     const int lrow = lane & 31;
     const int kh = lane >> 5;
+    const bool single_tile = kt0 + 1 >= kt1;
     for (uint32_t kt = kt0; kt < kt1; ++kt) {
         const int cur = (kt - kt0) & 1;
         const bool more = kt + 1 < kt1;
@@ -645,10 +652,15 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
         // iteration (the last one's are in range and unused) so that they sit
         // in the same block as the MFMAs and interleave with them.
         if constexpr (BMODE == IMG || BMODE == IMGT || BMODE == IMGTB) {
-            load_tile(kt + 1, cur ^ 1);
-            // Keep every load of the next tile ahead of this tile's MFMAs, so
-            // that their latency hides behind all of them.
-            __builtin_amdgcn_sched_barrier(0);
+            // (A workgroup with a single K-tile -- K <= 32, as a 3-channel
+            // 3x3 convolution's 27 -- has no next tile to load or wait for.)
+            if (single_tile) {
+            } else {
+                load_tile(kt + 1, cur ^ 1);
+                // Keep every load of the next tile ahead of this tile's MFMAs,
+                // so that their latency hides behind all of them.
+                __builtin_amdgcn_sched_barrier(0);
+            }
         } else if (more) {
             load_tile(kt + 1, cur ^ 1);
         }
@@ -720,7 +732,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t row = row0 + wm0 + 32 * i + 8 * (r / 4) + 4 * kh + (r % 4);
-                if (row < g.m && col < g.n) cbase[static_cast<uint64_t>(row) * g.n + col] = acc[i][j][r];
+                float v = acc[i][j][r];
+                if constexpr (BMODE == IMG) {
+                    if (g.bias) v = v + g.bias[static_cast<int64_t>(row < g.m ? row : 0) * g.bias_stride];
+                    if (g.relu) v = v <= 0.0f ? 0.0f : v;
+                }
+                if (row < g.m && col < g.n) cbase[static_cast<uint64_t>(row) * g.n + col] = v;
             }
         }
 }
@@ -2075,8 +2092,40 @@ int make_im2col(const vkhip_unfold& p, uint32_t channels, const int64_t* strides
     return VKHIP_OK;
 }
 
+// The conv epilogue as its own pass, for plans whose kernel cannot apply it
+// (split-K partitions, the exact arm): out[n][c][p] = relu(out + bias[c]).
+__global__ __launch_bounds__(256) void conv_bias_relu_kernel(float* __restrict__ out, uint64_t total,
+                                                             FastDiv div_l, uint32_t cout,
+                                                             const float* __restrict__ bias,
+                                                             int64_t bias_stride, uint32_t relu) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        // i / L within 2^32 (checked by the caller), its channel is that mod Cout
+        const uint32_t c = div_l.div(static_cast<uint32_t>(i)) % cout;
+        float v = out[i];
+        if (bias) v = v + bias[static_cast<int64_t>(c) * bias_stride];
+        if (relu) v = v <= 0.0f ? 0.0f : v;
+        out[i] = v;
+    }
+}
+
+static int launch_conv_epilogue(float* out, uint64_t total, uint32_t positions, uint32_t cout,
+                                const float* bias, int64_t bias_stride, bool relu) {
+    if (!bias && !relu) return VKHIP_OK;
+    if (total == 0) return VKHIP_OK;
+    if (total > 0xffffffffull)
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d epilogue: output of %llu elements",
+                    static_cast<unsigned long long>(total));
+    const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((total + 255) / 256, 65536));
+    hipLaunchKernelGGL(conv_bias_relu_kernel, dim3(blocks), dim3(256), 0, ctx().stream, out, total,
+                       FastDiv(positions), cout, bias, bias_stride, relu ? 1u : 0u);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
 int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
-                   const vkhip_operand& wd, float* out, const vkhip_unfold& p) {
+                   const vkhip_operand& wd, float* out, const vkhip_unfold& p, const float* bias,
+                   int64_t bias_stride, bool relu) {
     if (p.kernel_h <= 0 || p.kernel_w <= 0 || p.stride_h <= 0 || p.stride_w <= 0 ||
         p.dilation_h <= 0 || p.dilation_w <= 0 || p.pad_h < 0 || p.pad_w < 0)
         return fail(VKHIP_ERR_INVALID, "conv2d: invalid window geometry");
@@ -2100,7 +2149,9 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
     const uint32_t m = wd.ne[2], n = static_cast<uint32_t>(L), k = static_cast<uint32_t>(ck);
     if (batch == 0 || m == 0 || n == 0) return VKHIP_OK;
     if (k == 0) {
-        return launch_zero_f32(out, batch * m * n);
+        const int st = launch_zero_f32(out, batch * m * n);
+        if (st != VKHIP_OK) return st;
+        return launch_conv_epilogue(out, batch * m * n, n, m, bias, bias_stride, relu);
     }
     if (ctx().exact_math) {
         // the exact arm with the columns gathered from the image: the oracle's
@@ -2122,7 +2173,9 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
         g.n = n;
         g.k = k;
         g.c = out;
-        return launch_exact(g, static_cast<uint32_t>(batch), B_IMG, im);
+        const int st = launch_exact(g, static_cast<uint32_t>(batch), B_IMG, im);
+        if (st != VKHIP_OK) return st;
+        return launch_conv_epilogue(out, batch * m * n, n, m, bias, bias_stride, relu);
     }
     uint32_t splits, chunk;
     TileChoice tile;
@@ -2174,6 +2227,11 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
         g.split_stride = out_elems;
     }
     g.c = target;
+    if (splits == 1) {  // the kernel applies the epilogue (split plans: after the fold)
+        g.bias = bias;
+        g.bias_stride = bias_stride;
+        g.relu = relu ? 1u : 0u;
+    }
     // The weights or gradient rows straight into LDS when the KCD loader's
     // conditions hold (K a multiple of four, 16-byte aligned rows: a_vec;
     // byte offsets within 2^31), else through registers.
@@ -2186,7 +2244,11 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
     else
         st = launch_conv_tiles<64, 64, 32, 32, IMG>(g, im, static_cast<uint32_t>(batch), splits, amode);
     if (st != VKHIP_OK) return st;
-    if (splits > 1) return launch_split_k_reduce(target, out, out_elems, splits);
+    if (splits > 1) {
+        st = launch_split_k_reduce(target, out, out_elems, splits);
+        if (st != VKHIP_OK) return st;
+        return launch_conv_epilogue(out, out_elems, n, m, bias, bias_stride, relu);
+    }
     return VKHIP_OK;
 }
 
@@ -2523,7 +2585,7 @@ int conv2d_input_grad(const float* gr, const vkhip_operand& gd, const float* w, 
         wd.nb[1] = 0;
         wd.nb[2] = static_cast<int64_t>(cout) * kk;
         wd.nb[3] = 1;
-        return conv2d_forward(gr, gd, wt, wd, out, q);
+        return conv2d_forward(gr, gd, wt, wd, out, q, nullptr, 0, false);
     }
     if (ck > 0xffffffffull || L > 0xffffffffull)
         return fail(VKHIP_ERR_UNSUPPORTED, "conv2d input grad: extents too large");
@@ -2611,7 +2673,7 @@ extern "C" int vkhip_conv2d(const float* x, const vkhip_operand* x_desc, const f
     if (st != VKHIP_OK) return st;
     vkhip::Unit unit("conv2d");
     if (!x_desc || !w_desc || !p) return vkhip::fail(VKHIP_ERR_INVALID, "conv2d: null argument");
-    return vkhip::conv2d_forward(x, *x_desc, w, *w_desc, out, *p);
+    return vkhip::conv2d_forward(x, *x_desc, w, *w_desc, out, *p, nullptr, 0, false);
 }
 
 extern "C" int vkhip_conv2d_weight_grad(const float* x, const vkhip_operand* x_desc,

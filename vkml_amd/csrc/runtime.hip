@@ -20,7 +20,8 @@ int launch_im2col(const float* src, const vkhip_operand& sd, float* dst, const v
 int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
                   const vkhip_unfold& p);
 int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
-                   const vkhip_operand& wd, float* out, const vkhip_unfold& p);
+                   const vkhip_operand& wd, float* out, const vkhip_unfold& p, const float* bias,
+                   int64_t bias_stride, bool relu);
 int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
                        const vkhip_operand& gd, float* out, const vkhip_unfold& p);
 int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* gr,
@@ -267,12 +268,20 @@ static int supports_node(const vkhip_node& nd) {
         case VKHIP_OP_MAX_POOL2D:
             return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && nd.src[0].ndim == 4 &&
                    o.ndim == 4 && contiguous(o);
-        case VKHIP_OP_CONV2D: {
+        case VKHIP_OP_CONV2D:
+        case VKHIP_OP_CONV2D_BIAS_RELU: {
             const vkhip_tensor& x = nd.src[0];
             const vkhip_tensor& w = nd.src[1];
             vkhip_unfold p;
             memcpy(&p, nd.params, sizeof p);
-            if (nd.n_src != 2 || !is_f32(x) || !is_f32(w) || !is_f32(o) || x.ndim != 4 ||
+            if (nd.op == VKHIP_OP_CONV2D_BIAS_RELU) {
+                // the bias: [Cout] or [Cout, 1, 1], any stride along channels
+                const vkhip_tensor& b = nd.src[2];
+                if (nd.n_src != 3 || !is_f32(b) || b.ndim < 1 || b.ne[0] != w.ne[0]) return 0;
+                for (int i = 1; i < b.ndim; ++i)
+                    if (b.ne[i] != 1) return 0;
+            }
+            if (nd.n_src != (nd.op == VKHIP_OP_CONV2D ? 2 : 3) || !is_f32(x) || !is_f32(w) || !is_f32(o) || x.ndim != 4 ||
                 o.ndim != 4 || !contiguous(o) || o.ne[0] != x.ne[0] || o.ne[1] != w.ne[0] ||
                 static_cast<int64_t>(p.kernel_h) * p.kernel_w > 63)
                 return 0;
@@ -492,6 +501,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_CONV2D_WEIGHT_GRAD: return "conv2d_weight_grad";
         case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: return "conv2d_weight_grad_sum";
         case VKHIP_OP_CONV2D_INPUT_GRAD: return "conv2d_input_grad";
+        case VKHIP_OP_CONV2D_BIAS_RELU: return "conv2d_bias_relu";
         case VKHIP_OP_MIN: return "min";
         case VKHIP_OP_ARGMIN: return "argmin";
         case VKHIP_OP_FULL: return "full";
@@ -580,7 +590,8 @@ static int compute_node(const vkhip_node& nd) {
                                  static_cast<float*>(nd.out.data), static_cast<uint32_t>(nd.out.ne[0]),
                                  static_cast<uint32_t>(nd.out.ne[1]), p);
         }
-        case VKHIP_OP_CONV2D: {
+        case VKHIP_OP_CONV2D:
+        case VKHIP_OP_CONV2D_BIAS_RELU: {
             vkhip_unfold p;
             memcpy(&p, nd.params, sizeof p);
             const vkhip_tensor& w = nd.src[1];
@@ -607,9 +618,12 @@ static int compute_node(const vkhip_node& nd) {
                 return fail(VKHIP_ERR_INVALID, "conv2d: output %lldx%lld, geometry gives %lldx%lld",
                             static_cast<long long>(nd.out.ne[2]), static_cast<long long>(nd.out.ne[3]),
                             static_cast<long long>(oh), static_cast<long long>(ow));
+            const bool fused = nd.op == VKHIP_OP_CONV2D_BIAS_RELU;
             return conv2d_forward(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
                                   static_cast<const float*>(w.data), wd,
-                                  static_cast<float*>(nd.out.data), p);
+                                  static_cast<float*>(nd.out.data), p,
+                                  fused ? static_cast<const float*>(nd.src[2].data) : nullptr,
+                                  fused ? nd.src[2].nb[0] : 0, fused);
         }
         case VKHIP_OP_CONV2D_WEIGHT_GRAD: {
             vkhip_unfold p;

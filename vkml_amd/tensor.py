@@ -477,7 +477,34 @@ def greater_equal(a, b): return _binary(OP["GREATER_EQUAL"], a, b, np.bool_)
 def neg(a): return _unary(OP["NEG"], a)
 def exp(a): return _unary(OP["EXP"], a)
 def log(a): return _unary(OP["LOG"], a)
-def relu(a): return _unary(OP["RELU"], a)
+def relu(a):
+    if FUSED_CONV_EPILOGUE:
+        fused = _conv_bias_relu(a)
+        if fused is not None:
+            return fused
+    return _unary(OP["RELU"], a)
+
+
+def _conv_bias_relu(t: Tensor):
+    """relu(conv2d(x, w) + bias) as one CONV2D_BIAS_RELU node when t is the
+    ADD of a CONV2D node and its bias broadcast from [Cout, 1, 1] (what
+    conv2d(x, w, bias) builds), else None. The CONV2D and ADD nodes stay in
+    the graph: computed only if something else needs them."""
+    n = t.node
+    if n.op != OP["ADD"] or n.dtype != np.float32 or len(n.src) != 2:
+        return None
+    conv, bb = n.src
+    if conv.op != OP["CONV2D"] or bb.op != BROADCAST or len(conv.src) != 2:
+        return None
+    bias3 = bb.src[0]
+    cout = conv.shape[1]
+    if tuple(bias3.shape) != (cout, 1, 1) or bias3.dtype != np.float32:
+        return None
+    node = Node(OP["CONV2D_BIAS_RELU"], conv.shape, np.float32, conv.backend,
+                [conv.src[0], conv.src[1], bias3], params=conv.params,
+                requires_grad=n.requires_grad)
+    node.aux = conv.aux
+    return Tensor(node)
 
 
 def scaled_add(a: Tensor, b: Tensor, alpha: float, beta: float) -> Tensor:
@@ -970,6 +997,11 @@ FOLD_CONV_WEIGHT_GRAD = True
 # GEMM tolerance of the graph).
 FUSED_CONV_INPUT_GRAD = True
 
+# relu(conv2d(x, w, bias)) as one CONV2D_BIAS_RELU node (the conv kernel adds
+# the bias and applies the ReLU in its epilogue; the same values as the
+# CONV2D, ADD and RELU nodes, bit for bit, on the device and the oracle).
+FUSED_CONV_EPILOGUE = True
+
 
 def reduce_to_shape(g: Tensor, target_dims) -> Tensor:
     """Sums g down to target_dims, undoing a broadcast (autograd.cpp:84-116)."""
@@ -988,6 +1020,50 @@ def reduce_to_shape(g: Tensor, target_dims) -> Tensor:
             axes.append(i)
     r = sum(g, axes, keepdim=True) if axes else g
     return r.reshape(target_dims)
+
+
+def _conv2d_backward(node: Node, a: Node, b: Node, grad: Tensor, grads: dict) -> None:
+    """The CONV2D gradient rule (shared with CONV2D_BIAS_RELU); a = x, b = w."""
+    tb = lambda: Tensor(b)  # noqa: E731
+    # The reference graph's gradients (ops.cpp:662-705 through the
+    # MATMUL, BROADCAST, RESHAPE and IM2COL rules): with the weight
+    # broadcast over the batch as flat4 [1, N, Cout, CK] and the columns
+    # as cols4 [1, N, CK, L], d(flat) = sum_n g4 @ cols4^T and
+    # d(x) = col2im(flat4^T @ g4), value for value.
+    kernel, stride, pad, dil, hw = node.aux
+    n_, cout, oh, ow = node.shape
+    ck = _numel(b.shape[1:])
+    g4 = grad.reshape(1, n_, cout, oh * ow)
+    if a.requires_grad:
+        if FUSED_CONV_INPUT_GRAD:
+            # col2im(flat^T @ g4) as one node: with unit strides the device
+            # runs it as a convolution of the gradient with the flipped,
+            # transposed weight (no column matrix); the oracle computes
+            # the product and col2im.
+            dx = Node(OP["CONV2D_INPUT_GRAD"], a.shape, np.float32, a.backend,
+                      [grad.contiguous().node, b], params=node.params)
+            _accumulate(grads, a, Tensor(dx))
+        else:
+            flat4 = tb().reshape(cout, ck).broadcast_to((1, n_, cout, ck))
+            dcols = matmul(flat4.transpose(-2, -1), g4).reshape(n_, ck, oh * ow)
+            _accumulate(grads, a, col2im(dcols, hw, kernel, stride, pad, dil))
+    if b.requires_grad:
+        if FOLD_CONV_WEIGHT_GRAD:
+            # sum_n g4 @ cols4^T as one node: the device folds the batch
+            # into the product's K axis (no [N, Cout, CK] intermediate);
+            # the oracle computes the per-image products and batch sum.
+            wg = Node(OP["CONV2D_WEIGHT_GRAD_SUM"], (cout, ck), np.float32, a.backend,
+                      [a, grad.contiguous().node], params=node.params)
+            dflat = Tensor(wg)
+        else:
+            # The per-image products g4 @ cols4^T as one CONV2D_WEIGHT_GRAD
+            # node (the columns gathered from the image, same bits), then
+            # the reference's batch sum.
+            wg = Node(OP["CONV2D_WEIGHT_GRAD"], (n_, cout, ck), np.float32, a.backend,
+                      [a, grad.contiguous().node], params=node.params)
+            prod = Tensor(wg).reshape(1, n_, cout, ck)
+            dflat = reduce_to_shape(prod, (cout, ck))
+        _accumulate(grads, b, dflat.reshape(b.shape))
 
 
 def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
@@ -1074,46 +1150,22 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
             _accumulate(grads, a, matmul(grad, tb().transpose(-2, -1)))
         if b.requires_grad:
             _accumulate(grads, b, matmul(ta().transpose(-2, -1), grad))
+    elif op == OP["CONV2D_BIAS_RELU"]:
+        # relu(conv + bias): the RELU rule (the fused relu gradient, here from
+        # the output y: y <= 0 exactly where the pre-activation z <= 0, and a
+        # NaN z leaves y NaN, so the select is the one on z), the ADD/BROADCAST
+        # rules for the bias (its broadcast adjoint: the sum over N, H, W), then
+        # the CONV2D rule with that gradient.
+        g = grad if grad.shape == out.shape else grad.broadcast_to(out.shape)
+        dz = Tensor(Node(OP["RELU_BACKWARD"], out.shape, np.float32, out.node.backend,
+                         [node, g.node]))
+        bias3 = node.src[2]
+        if bias3.requires_grad:
+            _accumulate(grads, bias3, reduce_to_shape(dz, bias3.shape))
+        if a.requires_grad or b.requires_grad:
+            _conv2d_backward(node, a, b, dz, grads)
     elif op == OP["CONV2D"]:
-        # The reference graph's gradients (ops.cpp:662-705 through the
-        # MATMUL, BROADCAST, RESHAPE and IM2COL rules): with the weight
-        # broadcast over the batch as flat4 [1, N, Cout, CK] and the columns
-        # as cols4 [1, N, CK, L], d(flat) = sum_n g4 @ cols4^T and
-        # d(x) = col2im(flat4^T @ g4), value for value.
-        kernel, stride, pad, dil, hw = node.aux
-        n_, cout, oh, ow = node.shape
-        ck = _numel(b.shape[1:])
-        g4 = grad.reshape(1, n_, cout, oh * ow)
-        if a.requires_grad:
-            if FUSED_CONV_INPUT_GRAD:
-                # col2im(flat^T @ g4) as one node: with unit strides the device
-                # runs it as a convolution of the gradient with the flipped,
-                # transposed weight (no column matrix); the oracle computes
-                # the product and col2im.
-                dx = Node(OP["CONV2D_INPUT_GRAD"], a.shape, np.float32, a.backend,
-                          [grad.contiguous().node, b], params=node.params)
-                _accumulate(grads, a, Tensor(dx))
-            else:
-                flat4 = tb().reshape(cout, ck).broadcast_to((1, n_, cout, ck))
-                dcols = matmul(flat4.transpose(-2, -1), g4).reshape(n_, ck, oh * ow)
-                _accumulate(grads, a, col2im(dcols, hw, kernel, stride, pad, dil))
-        if b.requires_grad:
-            if FOLD_CONV_WEIGHT_GRAD:
-                # sum_n g4 @ cols4^T as one node: the device folds the batch
-                # into the product's K axis (no [N, Cout, CK] intermediate);
-                # the oracle computes the per-image products and batch sum.
-                wg = Node(OP["CONV2D_WEIGHT_GRAD_SUM"], (cout, ck), np.float32, a.backend,
-                          [a, grad.contiguous().node], params=node.params)
-                dflat = Tensor(wg)
-            else:
-                # The per-image products g4 @ cols4^T as one CONV2D_WEIGHT_GRAD
-                # node (the columns gathered from the image, same bits), then
-                # the reference's batch sum.
-                wg = Node(OP["CONV2D_WEIGHT_GRAD"], (n_, cout, ck), np.float32, a.backend,
-                          [a, grad.contiguous().node], params=node.params)
-                prod = Tensor(wg).reshape(1, n_, cout, ck)
-                dflat = reduce_to_shape(prod, (cout, ck))
-            _accumulate(grads, b, dflat.reshape(b.shape))
+        _conv2d_backward(node, a, b, grad, grads)
     elif op == OP["CROSS_ENTROPY"]:
         g = Node(OP["CROSS_ENTROPY_BACKWARD"], a.shape, np.float32, a.backend,
                  [a, b, grad.contiguous().node])
