@@ -170,7 +170,11 @@ enum vkhip_op {
      * ? 0 : v: the values of the CONV2D, ADD (bias broadcast) and RELU nodes
      * it replaces, bit for bit, without writing and re-reading the two
      * intermediates. */
-    VKHIP_OP_CONV2D_BIAS_RELU = 103
+    VKHIP_OP_CONV2D_BIAS_RELU = 103,
+    /* relu(src0 + src1), sources with the output's extents (broadcast axes
+     * stride 0) as for ADD: the ADD and RELU nodes' values in one pass
+     * (a Linear layer's bias add and activation). */
+    VKHIP_OP_ADD_RELU = 104
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */

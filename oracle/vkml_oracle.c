@@ -454,6 +454,10 @@ static float unary_f(int op, float x) {
 static float binary_f(int op, float x, float y, float alpha, float beta) {
     switch (op) {
         case VKHIP_OP_ADD: return x + y;
+        case VKHIP_OP_ADD_RELU: {
+            const float v = x + y;
+            return v <= 0.0f ? 0.0f : v; /* k_add then k_relu */
+        }
         case VKHIP_OP_SUB: return x - y;
         case VKHIP_OP_MUL: return x * y;
         case VKHIP_OP_DIV: return x / y;
@@ -586,7 +590,7 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 for (int64_t i = 0; i < n; ++i) ((float*)o->data)[i] = unary_f(nd->op, x[lin_off(i, s0.ne, s0.nb)]);
                 break;
             }
-            case VKHIP_OP_ADD: case VKHIP_OP_SUB: case VKHIP_OP_MUL: case VKHIP_OP_DIV:
+            case VKHIP_OP_ADD: case VKHIP_OP_ADD_RELU: case VKHIP_OP_SUB: case VKHIP_OP_MUL: case VKHIP_OP_DIV:
             case VKHIP_OP_SCALED_ADD: case VKHIP_OP_MAXIMUM: case VKHIP_OP_MINIMUM: {
                 float ab[2] = {1.0f, 1.0f};
                 memcpy(ab, nd->params, sizeof ab);

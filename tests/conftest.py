@@ -148,6 +148,51 @@ def conv_relu_loss_and_grads(backend, x, w, bias, stride, pad, dil, fused):
         T.FUSED_CONV_EPILOGUE = prev
 
 
+GRAPH_REWRITES = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU",
+                  "FUSED_CONV_EPILOGUE", "FUSED_CONV_INPUT_GRAD", "FOLD_CONV_WEIGHT_GRAD")
+
+
+def train_with_rewrites(backend, model_fn, batches, enabled, lr=0.1, momentum=0.9,
+                        rewrites=GRAPH_REWRITES):
+    """Losses and final parameters of SGD-momentum steps over `batches` with
+    the tensor layer's graph rewrites in `rewrites` switched on or off."""
+    from vkml_amd import nn, optim
+    from vkml_amd import tensor as T
+
+    saved = {r: getattr(T, r) for r in rewrites}
+    try:
+        for r in rewrites:
+            setattr(T, r, enabled)
+        model = model_fn(backend)
+        opt = optim.SGD(model.parameters(), lr=lr, momentum=momentum)
+        losses = []
+        for x, y in batches:
+            opt.zero_grad()
+            loss = nn.cross_entropy(model(T.tensor(x, backend=backend)), T.tensor(y, backend=backend))
+            loss.backward()
+            opt.step()
+            losses.append(np.float32(loss.item()))
+        return np.array(losses), [p.numpy() for p in model.parameters()]
+    finally:
+        for r, v in saved.items():
+            setattr(T, r, v)
+
+
+def mlp_model(backend):
+    """Config 1's MLP: Flatten, Linear(784,128), ReLU, Linear(128,10)."""
+    from vkml_amd import nn
+
+    nn.manual_seed(SEED)
+    return nn.Sequential(nn.Flatten(), nn.Linear(784, 128, backend=backend), nn.ReLU(),
+                         nn.Linear(128, 10, backend=backend))
+
+
+def mlp_batches(steps, batch=64):
+    rng = np.random.default_rng(SEED + 3)
+    return [(rng.uniform(0, 1, (batch, 1, 28, 28)).astype(np.float32),
+             rng.integers(0, 10, batch).astype(np.int64)) for _ in range(steps)]
+
+
 def relu_inputs(shape, seed):
     """x and the output gradient g for the relu gradient, with NaN, +-0, +-inf
     in both (the select must pass NaN x through and keep g's bits)."""

@@ -13,8 +13,8 @@ import numpy as np
 import pytest
 
 from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad,
-                      config5_golden_losses, config5_train, conv_loss_and_grads, conv_relu_loss_and_grads,
-                      gemm_tolerance,
+                      config5_batches, config5_golden_losses, config5_model, config5_train, conv_loss_and_grads,
+                      conv_relu_loss_and_grads, gemm_tolerance, mlp_batches, mlp_model, train_with_rewrites,
                       normwise_rel_err, relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
@@ -189,6 +189,27 @@ def test_conv_bias_relu_node_on_device_is_the_three_nodes(backends, shape, cout,
     graph = conv_relu_loss_and_grads(dev, x, w, bias, stride, pad, dil, False)
     for got, want in zip(fused, graph):
         assert got.tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("model", ["mlp", "cnn"])
+def test_exact_graph_rewrites_keep_the_device_bits(backends, model):
+    """On the device, the graph rewrites that compute the same arithmetic
+    (constant folding, weight gradients in the weight's layout, fused
+    add+relu and conv+bias+relu) leave every loss and parameter of
+    SGD-momentum training bit for bit unchanged: config 1's MLP for 10 steps,
+    config 5's CNN at batch 128 for 3 steps."""
+    dev, _ = backends
+    rewrites = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU", "FUSED_CONV_EPILOGUE")
+    if model == "mlp":
+        fn, batches = mlp_model, mlp_batches(10)
+    else:
+        fn, batches = config5_model, list(config5_batches(3, 128))
+    print(f"rewrites {model}", flush=True)
+    on = train_with_rewrites(dev, fn, batches, True, rewrites=rewrites)
+    off = train_with_rewrites(dev, fn, batches, False, rewrites=rewrites)
+    assert on[0].tobytes() == off[0].tobytes()
+    for a, b in zip(on[1], off[1]):
+        assert a.tobytes() == b.tobytes()
 
 
 def test_bias_gradient_reduce_is_bit_exact(backends):

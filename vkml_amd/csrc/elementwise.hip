@@ -163,6 +163,11 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EwArgs a) {
                 break;
             }
             case VKHIP_OP_ADD: store_out(a, i, __fadd_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
+            case VKHIP_OP_ADD_RELU: {
+                const float v = __fadd_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k));
+                store_out(a, i, v <= 0.0f ? 0.0f : v);
+                break;
+            }
             case VKHIP_OP_SUB: store_out(a, i, __fsub_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
             case VKHIP_OP_MUL: store_out(a, i, __fmul_rn(load_f(a.s[0], i, k), load_f(a.s[1], i, k))); break;
             case VKHIP_OP_DIV: store_out(a, i, load_f(a.s[0], i, k) / load_f(a.s[1], i, k)); break;
@@ -231,6 +236,11 @@ __global__ __launch_bounds__(256) void elementwise_f32_vec_kernel(int op, const 
     for (int j = 0; j < 4; ++j) {
         switch (op) {
             case VKHIP_OP_ADD: r[j] = __fadd_rn(a[j], b[j]); break;
+            case VKHIP_OP_ADD_RELU: {
+                const float v = __fadd_rn(a[j], b[j]);
+                r[j] = v <= 0.0f ? 0.0f : v;
+                break;
+            }
             case VKHIP_OP_SUB: r[j] = __fsub_rn(a[j], b[j]); break;
             case VKHIP_OP_MUL: r[j] = __fmul_rn(a[j], b[j]); break;
             case VKHIP_OP_SCALED_ADD:
@@ -280,6 +290,11 @@ __global__ __launch_bounds__(256) void elementwise_bcast_vec_kernel(
     for (int j = 0; j < 4; ++j) {
         switch (op) {
             case VKHIP_OP_ADD: res[j] = __fadd_rn(a[j], b[j]); break;
+            case VKHIP_OP_ADD_RELU: {
+                const float v = __fadd_rn(a[j], b[j]);
+                res[j] = v <= 0.0f ? 0.0f : v;
+                break;
+            }
             case VKHIP_OP_SUB: res[j] = __fsub_rn(a[j], b[j]); break;
             default: res[j] = __fmul_rn(a[j], b[j]); break;
         }
@@ -360,7 +375,7 @@ int launch_elementwise(const vkhip_node& nd) {
 
     // Vector fast path: f32, everything contiguous and 16-byte aligned.
     const int op = nd.op;
-    const bool vec_op = op == VKHIP_OP_ADD || op == VKHIP_OP_SUB || op == VKHIP_OP_MUL ||
+    const bool vec_op = op == VKHIP_OP_ADD || op == VKHIP_OP_ADD_RELU || op == VKHIP_OP_SUB || op == VKHIP_OP_MUL ||
                         op == VKHIP_OP_SCALED_ADD || op == VKHIP_OP_RELU || op == VKHIP_OP_NEG ||
                         op == VKHIP_OP_CONTIGUOUS || op == VKHIP_OP_RELU_BACKWARD;
     if (vec_op && n % 4 == 0 && nd.out.dtype == VKHIP_F32) {
@@ -410,7 +425,8 @@ int launch_elementwise(const vkhip_node& nd) {
         }
     }
     // Broadcast second operand of a bias add (see elementwise_bcast_vec_kernel).
-    if ((op == VKHIP_OP_ADD || op == VKHIP_OP_SUB || op == VKHIP_OP_MUL) && nd.n_src == 2 &&
+    if ((op == VKHIP_OP_ADD || op == VKHIP_OP_ADD_RELU || op == VKHIP_OP_SUB || op == VKHIP_OP_MUL) &&
+        nd.n_src == 2 &&
         n % 4 == 0 && n < (1ull << 32) && nd.out.dtype == VKHIP_F32 &&
         nd.src[0].dtype == VKHIP_F32 && nd.src[1].dtype == VKHIP_F32 &&
         is_contig(nd.src[0]) && tnumel(nd.src[0]) == n &&

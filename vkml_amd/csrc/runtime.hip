@@ -192,6 +192,7 @@ static bool is_elementwise(int op) {
         case VKHIP_OP_FULL: case VKHIP_OP_ARANGE: case VKHIP_OP_CONTIGUOUS: case VKHIP_OP_CAST:
         case VKHIP_OP_NEG: case VKHIP_OP_EXP: case VKHIP_OP_LOG: case VKHIP_OP_RELU:
         case VKHIP_OP_ADD: case VKHIP_OP_SUB: case VKHIP_OP_MUL: case VKHIP_OP_DIV:
+        case VKHIP_OP_ADD_RELU:
         case VKHIP_OP_SCALED_ADD: case VKHIP_OP_MAXIMUM: case VKHIP_OP_MINIMUM:
         case VKHIP_OP_EQUAL: case VKHIP_OP_LESS: case VKHIP_OP_GREATER: case VKHIP_OP_LESS_EQUAL:
         case VKHIP_OP_GREATER_EQUAL: case VKHIP_OP_NOT_EQUAL: case VKHIP_OP_WHERE:
@@ -227,6 +228,7 @@ static int supports_node(const vkhip_node& nd) {
         case VKHIP_OP_LOG:
         case VKHIP_OP_RELU: return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]);
         case VKHIP_OP_ADD:
+        case VKHIP_OP_ADD_RELU:
         case VKHIP_OP_SUB:
         case VKHIP_OP_MUL:
         case VKHIP_OP_DIV:
@@ -514,6 +516,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_RELU: return "relu";
         case VKHIP_OP_RELU_BACKWARD: return "relu_backward";
         case VKHIP_OP_ADD: return "add";
+        case VKHIP_OP_ADD_RELU: return "add_relu";
         case VKHIP_OP_SUB: return "sub";
         case VKHIP_OP_MUL: return "mul";
         case VKHIP_OP_DIV: return "div";

@@ -378,6 +378,10 @@ class Tensor:
         tensor.cpp:287-299)."""
         if self.node.is_contiguous():
             return self
+        if FOLD_CONSTANTS and not self.requires_grad:
+            v = _full_value(self)
+            if v is not None:
+                return full(self.shape, float(v), np.float32, self.node.backend)
         return _unary(OP["CONTIGUOUS"], self)
 
     def to(self, dtype) -> "Tensor":
@@ -441,6 +445,42 @@ def arange(start: float, stop: float, step: float = 1.0, dtype=np.float32, backe
                        params=_params(("d", float(start)), ("d", float(step)))))
 
 
+# Arithmetic on FULL constants is evaluated on the host (IEEE single
+# precision, as the oracle and the device compute it) and a view of a constant
+# made contiguous is a new constant: the seed, 1/count and broadcast chain of
+# a mean's gradient is then one FULL node instead of four launches.
+FOLD_CONSTANTS = True
+
+# The gradient of a weight used as w.T in a product (nn.Linear) computed in
+# w's layout (grad^T @ x) rather than as (x^T @ grad)^T then copied: the same
+# values (see the MATMUL rule).
+WEIGHT_GRAD_IN_PLACE_LAYOUT = True
+
+
+def _transposed_matrix_source(b: "Node"):
+    """w when node b is the view w.T of a 2-D w that requires grad, else None."""
+    if (b.op == PERMUTE and len(b.shape) == 2 and b.aux is not None and list(b.aux) == [1, 0]
+            and b.view_src is not None and b.view_src.requires_grad and b.view_src.dtype == np.float32):
+        return b.view_src
+    return None
+_FOLDABLE = {OP["ADD"]: np.add, OP["SUB"]: np.subtract, OP["MUL"]: np.multiply,
+             OP["DIV"]: np.divide}
+
+
+def _full_value(t: "Tensor"):
+    """The value of an uncomputed float32 FULL constant, or of a view of one
+    (a broadcast or reshape of it), else None."""
+    n = t.node
+    while n.view_src is not None and n.op in (RESHAPE, BROADCAST, UNSQUEEZE):
+        n = n.view_src
+    if (n.op != FULL or n.computed or n.dtype != np.float32 or n.requires_grad
+            or len(n.params) < 8):
+        return None
+    import struct
+
+    return np.float32(struct.unpack_from("<d", n.params, 0)[0])
+
+
 def _scalar_like(peer: Tensor, value) -> Tensor:
     if isinstance(value, Tensor):
         return value
@@ -454,6 +494,12 @@ def _binary(op, a: Tensor, b, out_dtype=None, params=b"") -> Tensor:
     bb = b if b.shape == dims else b.broadcast_to(dims)
     out_dtype = np.dtype(out_dtype or a.dtype)
     rg = _grad_enabled and (a.requires_grad or b.requires_grad) and out_dtype == np.float32
+    if FOLD_CONSTANTS and not rg and op in _FOLDABLE and out_dtype == np.float32:
+        va, vb = _full_value(a), _full_value(b)
+        if va is not None and vb is not None:
+            with np.errstate(all="ignore"):
+                r = _FOLDABLE[op](va, vb)
+            return full(dims, float(np.float32(r)), np.float32, a.node.backend)
     return Tensor(Node(op, dims, out_dtype, a.node.backend, [ba.node, bb.node], params=params,
                        requires_grad=rg))
 
@@ -482,6 +528,11 @@ def relu(a):
         fused = _conv_bias_relu(a)
         if fused is not None:
             return fused
+    if FUSED_ADD_RELU and a.node.op == OP["ADD"] and a.dtype == np.float32 and len(a.node.src) == 2:
+        # relu(x + y) as one ADD_RELU node over the ADD's sources (the ADD
+        # stays in the graph, computed only if something else needs it)
+        return Tensor(Node(OP["ADD_RELU"], a.shape, np.float32, a.node.backend, list(a.node.src),
+                           requires_grad=a.node.requires_grad))
     return _unary(OP["RELU"], a)
 
 
@@ -1002,6 +1053,10 @@ FUSED_CONV_INPUT_GRAD = True
 # CONV2D, ADD and RELU nodes, bit for bit, on the device and the oracle).
 FUSED_CONV_EPILOGUE = True
 
+# relu(a + b) as one ADD_RELU node (a Linear layer's bias add and activation):
+# the ADD and RELU nodes' values in one pass.
+FUSED_ADD_RELU = True
+
 
 def reduce_to_shape(g: Tensor, target_dims) -> Tensor:
     """Sums g down to target_dims, undoing a broadcast (autograd.cpp:84-116)."""
@@ -1149,7 +1204,25 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         if a.requires_grad:
             _accumulate(grads, a, matmul(grad, tb().transpose(-2, -1)))
         if b.requires_grad:
-            _accumulate(grads, b, matmul(ta().transpose(-2, -1), grad))
+            w = _transposed_matrix_source(b) if WEIGHT_GRAD_IN_PLACE_LAYOUT else None
+            if w is not None:
+                # b = w^T (x @ w.T, a Linear layer): d(w) = grad^T @ a is the
+                # transpose of d(w^T) = a^T @ grad -- the same products summed
+                # in the same k order under a plan symmetric in M and N -- in
+                # w's own layout, so no transposing copy follows.
+                _accumulate(grads, w, matmul(grad.transpose(-2, -1), ta()))
+            else:
+                _accumulate(grads, b, matmul(ta().transpose(-2, -1), grad))
+    elif op == OP["ADD_RELU"]:
+        # the RELU rule (the mask from the output, as for CONV2D_BIAS_RELU)
+        # then the ADD rule: the same gradient to both sources
+        g = grad if grad.shape == out.shape else grad.broadcast_to(out.shape)
+        dz = Tensor(Node(OP["RELU_BACKWARD"], out.shape, np.float32, out.node.backend,
+                         [node, g.node]))
+        if a.requires_grad:
+            _accumulate(grads, a, dz)
+        if b.requires_grad:
+            _accumulate(grads, b, dz)
     elif op == OP["CONV2D_BIAS_RELU"]:
         # relu(conv + bias): the RELU rule (the fused relu gradient, here from
         # the output y: y <= 0 exactly where the pre-activation z <= 0, and a
