@@ -107,6 +107,8 @@ LAYOUT_SHAPES = [  # (batch, m, n, k): 128x128 tiles, split-K, ragged edges, M o
     (1, 1024, 1024, 256),   # 64x64 tiles, one workgroup per CU
     (2, 1000, 1020, 100),   # 64x64 tiles, ragged edges
     (1, 1022, 1024, 64),    # 64x64 tiles, M not 4-aligned (TN through registers)
+    (1, 384, 256, 24000),   # paired partitions (84), two per direct workgroup
+    (1, 256, 384, 30000),   # paired partitions, odd count (79): the last pair is one
 ]
 
 
@@ -197,10 +199,13 @@ def test_split_k_config3_parity_and_bit_stability(hip, m, n, k):
     assert normwise_rel_err(forced, unsplit) <= gemm_tolerance(k)
 
 
-@pytest.mark.parametrize("splits", [1, 2, 3, 4, 7, 16, 33, 128])
-def test_split_k_reduce_bit_exact(hip, splits):
-    rng = np.random.default_rng(splits)
-    ws = (rng.standard_normal(splits * 1000 + 0) * 1e3).astype(np.float32)
+@pytest.mark.parametrize("splits", [1, 2, 3, 4, 7, 16, 17, 33, 35, 64, 128, 511])
+@pytest.mark.parametrize("ne", [1000, 1001])
+def test_split_k_reduce_bit_exact(hip, splits, ne):
+    """Every partition count (chunked groups plus a remainder) and both the
+    16-byte (ne % 4 == 0) and the scalar loads give the oracle's fold."""
+    rng = np.random.default_rng(splits + ne)
+    ws = (rng.standard_normal(splits * ne) * 1e3).astype(np.float32)
     got = ops.split_k_reduce(dev(ws), splits).numpy()
     assert got.tobytes() == O.split_k_fold(ws, splits).tobytes()
 

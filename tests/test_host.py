@@ -125,9 +125,14 @@ def test_split_k_plan_rules():
         assert m * n * splits * 4 <= 64 << 20
         tiles = -(-m // 64) * -(-n // 64)
         assert tiles * splits >= min(512, tiles * (ktiles // 2)) // 2
-    # one round of 256 workgroups: 4 tiles x 64, 7 tiles x 35 (15 K-tiles each)
-    assert plan(1, 256, 256, 65536) == (64, 32)
-    assert plan(1, 128, 784, 16384) == (35, 15)
+    # one round of 256 workgroups, then twice the partitions for pairs (two K
+    # streams per workgroup) when each keeps >= 8 K-tiles and the pairs still
+    # fit one round: 4 tiles x 64 -> 128 partitions of 16 K-tiles (64 pairs
+    # per tile); 7 tiles x 35 -> 64 partitions of 8 (32 pairs per tile)
+    assert plan(1, 256, 256, 65536) == (128, 16)
+    assert plan(1, 128, 784, 16384) == (64, 8)
+    # partitions that would drop below 8 K-tiles stay one per workgroup
+    assert plan(1, 256, 256, 16384) == (64, 8)
     # more than half a round of tiles (144 at 1536^3): power-of-two chunk
     assert plan(1, 1536, 1536, 1536) == (3, 16)
     # a batched conv GEMM has tiles enough

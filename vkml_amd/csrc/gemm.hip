@@ -43,6 +43,7 @@ struct GemmArgs {
     uint64_t split_stride;       // elements between partition slices of c
     uint32_t a_vec, b_vec;       // 16-byte loads along k are legal
     uint32_t flat_splits;        // > 0: split grid launched flat, grid.x = tiles * flat_splits
+    uint32_t pairs;              // paired direct kernel: partition pairs per tile
     // Convolution epilogue (unsplit register-path conv kernel only): out =
     // acc + bias[row * bias_stride] when bias is set, then relu (x <= 0 ? 0 :
     // x) when relu is set -- the ADD and RELU nodes' arithmetic.
@@ -776,21 +777,38 @@ __device__ __forceinline__ void load_b_rows_direct(float* stage, __amdgpu_buffer
 // way as B, BK rows of 128; a lane reads its row's one float of a k row per
 // MFMA step (the rows of a wave are contiguous, so the 32 lanes of a half
 // read 32 adjacent floats).
-template <bool ATR>
-__global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
+//
+// PAIR: two groups of four waves, each with its own LDS double
+// buffer, computing the K partitions 2q and 2q+1 of one tile side by side:
+// two independent K streams per CU when the grid gives each CU one
+// workgroup. Group 1 hands its accumulators to group 0 through LDS and the
+// workgroup writes partial(2q) + partial(2q+1), the node the carry-stack fold
+// forms first from those two partials (fp addition commutes), so folding the
+// g.pairs pair sums gives the bits of folding all the partitions' partials.
+// When the partition count is odd the last pair's second group has no K
+// range: its sum is the last partial plus +0.0, which folds to the same bits
+// (the fold's drain adds the lone last partial to 0.0 first; every later sum
+// is the same). With one pair the fold's drain (0.0 + the pair sum) is applied
+// here and the result is the output.
+template <bool ATR, bool PAIR>
+__global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmArgs g) {
     constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
+    constexpr int NG = PAIR ? 2 : 1;  // K streams (groups of four waves)
     using LA = TileLoader<BM, BK, KCD>;
-    __shared__ __attribute__((aligned(16))) float lds[2][BM * LDK + BK * BN];
+    __shared__ __attribute__((aligned(16))) float lds_all[NG][2][BM * LDK + BK * BN];
 
-    const int tid = threadIdx.x;
+    const int tid = PAIR ? threadIdx.x & 255 : threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm0 = wave * 32;
+    const int grp = PAIR ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 8) : 0;
+    auto& lds = lds_all[grp];
 
     uint32_t tm, tn, split;
     tile_of(g, tm, tn, split);
     const uint32_t row0 = tm * BM;
     const uint32_t col0 = tn * BN;
+    const uint32_t part = PAIR ? 2 * split + grp : split;  // this group's K partition
 
     const uint32_t z = blockIdx.z;
     const uint32_t i0 = z / g.b1, i1 = z % g.b1;
@@ -802,8 +820,11 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
         const_cast<float*>(bbase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
     float* cbase = g.c + static_cast<uint64_t>(split) * g.split_stride +
                    static_cast<uint64_t>(z) * g.m * g.n;
-    const uint32_t kt0 = split * g.chunk;
+    const uint32_t kt0 = min(g.ktiles, part * g.chunk);
     const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
+    // Both groups of a pair run the steps of the pair's first (never
+    // shorter) partition; a group past its own range only joins the barriers.
+    const uint32_t steps = PAIR ? min(g.ktiles - 2 * split * g.chunk, g.chunk) : kt1 - kt0;
 
     f32x16 acc[4];
 #pragma unroll
@@ -839,8 +860,13 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
 
     const int lrow = lane & 31;
     const int kh = lane >> 5;
-    for (uint32_t kt = kt0; kt < kt1; ++kt) {
-        const int cur = (kt - kt0) & 1;
+    for (uint32_t it = 0; it < steps; ++it) {
+        const uint32_t kt = kt0 + it;
+        if (PAIR && kt >= kt1) {
+            __syncthreads();
+            continue;
+        }
+        const int cur = it & 1;
         if (kt + 1 < kt1) load_tile(kt + 1, cur ^ 1);
         const float* As = ATR ? lds[cur] + kh * 16 * BM + wm0 + lrow : lds[cur] + (wm0 + lrow) * BK;
         const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + 4 * lrow;
@@ -879,6 +905,29 @@ __global__ __launch_bounds__(256) void gemm_nn_direct_kernel(GemmArgs g) {
                                                                   0, 0, 0);
         }
         __syncthreads();
+    }
+
+    if constexpr (PAIR) {
+        // Group 1's accumulators through its own (now idle) LDS stages, one
+        // float per lane per register, lanes consecutive: no bank conflicts.
+        float* xch = &lds_all[1][0][0];
+        const int wv4 = __builtin_amdgcn_readfirstlane(wave);
+        if (grp == 1) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) xch[((wv4 * 4 + s) * 16 + r) * 64 + lane] = acc[s][r];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+        const bool final = g.pairs == 1;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float v = acc[s][r] + xch[((wv4 * 4 + s) * 16 + r) * 64 + lane];
+                acc[s][r] = final ? 0.0f + v : v;
+            }
     }
 
     // acc[s] register r of lane l: row 8*(r/4) + 4*(l/32) + r%4 of the wave's
@@ -1254,61 +1303,76 @@ __device__ __forceinline__ void carry_push(float (&stack)[kSplitLevels], uint32_
     }
 }
 
-// G threads per output. With G == 1 a thread folds all `splits` partials.
-// With G > 1 (splits a power of two) thread g folds the block of per =
-// splits/G consecutive partials starting at g*per, which the carry stack
-// leaves as one balanced subtree at level log2(per); the G subtrees then meet
-// in a balanced tree and the drain adds it to 0.0 - the same association as
-// one thread pushing all partials. Partials are read eight at a time so the
-// loads overlap; outputs are consecutive across lanes, so loads coalesce.
-template <int G>
+// G thread groups per block of 256 / G consecutive outputs. The host picks the
+// chunk C, the smallest power of two with ceil(splits / C) <= G. Groups
+// g < nchunks = splits / C fold the consecutive partials [g*C, (g+1)*C),
+// which the carry stack leaves as one balanced subtree at level log2(C);
+// group nchunks folds the rem = splits % C trailing partials into a carry
+// stack of levels below log2(C) and drains it (0.0 + its lowest level + ...).
+// The drain of the whole stack takes those low levels first, so group 0
+// continues that total with the carry stack of the nchunks chunk values,
+// whose levels are log2(C) and up: the same association as one thread
+// pushing all partials and draining from 0.0. With C a template constant
+// every push position is known at compile time, so the pushes compile to
+// straight-line adds. Partials are read eight at a time so the loads overlap;
+// outputs are consecutive across the lanes of a group, so loads coalesce.
+// (Measured on 64 x 65536 partials: 8 groups 3.0 us; 16 groups 4.4 us and 32
+// groups 11.9 us, where group 0's combine grows; 16-byte loads of four
+// outputs per lane 3.75 us.)
+template <int G, int C>
 __global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __restrict__ ws,
                                                              float* __restrict__ dst, uint64_t ne,
-                                                             uint32_t splits) {
+                                                             uint32_t splits, uint32_t nchunks) {
     constexpr int kOuts = 256 / G;
+    constexpr int kChunkLevel = C >= 64 ? 6 : C >= 32 ? 5 : C >= 16 ? 4 : C >= 8 ? 3 : C >= 4 ? 2 : C >= 2 ? 1 : 0;
+    static_assert((1 << kChunkLevel) == C && kChunkLevel < kSplitLevels, "chunk is a power of two");
     __shared__ float part[G][kOuts];
     const int g = threadIdx.x / kOuts, o = threadIdx.x % kOuts;
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * kOuts + o;
     const bool live = i < ne;
-    const uint32_t per = splits / G;
-    const float* src = ws + static_cast<uint64_t>(g) * per * ne + (live ? i : 0);
-    float stack[kSplitLevels];
+    const uint32_t rem = splits - nchunks * C;
+    const bool chunk = static_cast<uint32_t>(g) < nchunks;
+    float val = 0.0f;
+    if (live && (chunk || (static_cast<uint32_t>(g) == nchunks && rem != 0))) {
+        const uint32_t count = chunk ? C : rem;
+        const float* src = ws + static_cast<uint64_t>(g) * C * ne + i;
+        float stack[kSplitLevels];
 #pragma unroll
-    for (int l = 0; l < kSplitLevels; ++l) stack[l] = 0.0f;
-    if (live) {
-        for (uint32_t s0 = 0; s0 < per; s0 += 8) {
+        for (int l = 0; l < kSplitLevels; ++l) stack[l] = 0.0f;
+#pragma unroll
+        for (int s0 = 0; s0 < C; s0 += 8) {
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                v[j] = s0 + j < per ? src[static_cast<uint64_t>(s0 + j) * ne] : 0.0f;
+            for (int j = 0; j < 8 && s0 + j < C; ++j)
+                if (static_cast<uint32_t>(s0 + j) < count) v[j] = src[static_cast<uint64_t>(s0 + j) * ne];
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (s0 + j < per) carry_push(stack, s0 + j, v[j]);
+            for (int j = 0; j < 8 && s0 + j < C; ++j)
+                if (static_cast<uint32_t>(s0 + j) < count) carry_push(stack, s0 + j, v[j]);
+        }
+        if (chunk) {
+            val = stack[kChunkLevel];
+        } else {
+#pragma unroll
+            for (int l = 0; l < kChunkLevel; ++l)
+                if ((rem >> l) & 1u) val = val + stack[l];
         }
     }
-    if constexpr (G == 1) {
-        float total = 0.0f;
+    part[g][o] = val;
+    __syncthreads();
+    if (g != 0 || !live) return;
+    // The remainder's drained total (0.0 when rem == 0) continues with the
+    // chunk values' carry stack, drained from its lowest level.
+    float total = rem != 0 ? part[nchunks][o] : 0.0f;
+    float chunks[kSplitLevels];
 #pragma unroll
-        for (int l = 0; l < kSplitLevels; ++l)
-            if ((per >> l) & 1u) total = total + stack[l];
-        if (live) dst[i] = total;
-    } else {
-        float mine = 0.0f;
+    for (int l = 0; l < kSplitLevels; ++l) chunks[l] = 0.0f;
 #pragma unroll
-        for (int l = 0; l < kSplitLevels; ++l)
-            if ((1u << l) == per) mine = stack[l];
-        part[g][o] = mine;
-        __syncthreads();
-        if (g != 0 || !live) return;
-        float v[G];
+    for (int j = 0; j < G; ++j)
+        if (static_cast<uint32_t>(j) < nchunks) carry_push(chunks, j, part[j][o]);
 #pragma unroll
-        for (int j = 0; j < G; ++j) v[j] = part[j][o];
-#pragma unroll
-        for (int w = 1; w < G; w <<= 1)
-#pragma unroll
-            for (int j = 0; j + w < G; j += 2 * w) v[j] = v[j] + v[j + w];
-        dst[i] = 0.0f + v[0];
-    }
+    for (int l = 0; l < kSplitLevels; ++l)
+        if ((nchunks >> l) & 1u) total = total + chunks[l];
+    dst[i] = total;
 }
 
 // ---- GEMV -------------------------------------------------------------------
@@ -1567,6 +1631,7 @@ struct TileChoice {
     int bm, bn;
     const char* why = "";   // the reason, for the matmul.kernel decision fact
     uint64_t tiles = 0;     // output tiles of this tiling
+    bool pair = false;      // partitions planned for pairs (two per workgroup)
 };
 
 template <int BM, int BN, int WM, int WN, int AM>
@@ -1617,21 +1682,37 @@ static int launch_conv_tiles(const GemmArgs& g, const Im2colB& im, uint32_t batc
     return VKHIP_OK;
 }
 
+template <int G, int C>
+static void launch_split_k_fold(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
+    hipLaunchKernelGGL((split_k_reduce_kernel<G, C>), dim3(ceil_div(ne, 256 / G)), dim3(256), 0,
+                       ctx().stream, ws, dst, ne, splits, splits / C);
+}
+
 int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
     if (ne == 0) return VKHIP_OK;
     if (splits == 0 || splits >= (1u << kSplitLevels))
         return fail(VKHIP_ERR_INVALID, "split-K reduce: %u partitions outside 1..%u", splits,
                     (1u << kSplitLevels) - 1);
-    const bool pow2 = (splits & (splits - 1)) == 0;
-    if (pow2 && splits >= 8)
-        hipLaunchKernelGGL(split_k_reduce_kernel<8>, dim3(ceil_div(ne, 32)), dim3(256), 0,
-                           ctx().stream, ws, dst, ne, splits);
-    else if (pow2 && splits >= 2)
-        hipLaunchKernelGGL(split_k_reduce_kernel<2>, dim3(ceil_div(ne, 128)), dim3(256), 0,
-                           ctx().stream, ws, dst, ne, splits);
-    else
-        hipLaunchKernelGGL(split_k_reduce_kernel<1>, dim3(ceil_div(ne, 256)), dim3(256), 0,
-                           ctx().stream, ws, dst, ne, splits);
+    // Groups: 8, or the power of two at or above a smaller partition count
+    // (no idle groups); chunk: the smallest power of two that leaves at most
+    // that many groups busy (64 for 511 partitions).
+    if (splits <= 2) {
+        launch_split_k_fold<2, 1>(ws, dst, ne, splits);
+    } else if (splits <= 4) {
+        launch_split_k_fold<4, 1>(ws, dst, ne, splits);
+    } else {
+        uint32_t chunk = 1;
+        while (ceil_div(splits, chunk) > 8) chunk *= 2;
+        switch (chunk) {
+            case 1: launch_split_k_fold<8, 1>(ws, dst, ne, splits); break;
+            case 2: launch_split_k_fold<8, 2>(ws, dst, ne, splits); break;
+            case 4: launch_split_k_fold<8, 4>(ws, dst, ne, splits); break;
+            case 8: launch_split_k_fold<8, 8>(ws, dst, ne, splits); break;
+            case 16: launch_split_k_fold<8, 16>(ws, dst, ne, splits); break;
+            case 32: launch_split_k_fold<8, 32>(ws, dst, ne, splits); break;
+            default: launch_split_k_fold<8, 64>(ws, dst, ne, splits); break;
+        }
+    }
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -1718,6 +1799,24 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
     if (tiles > 0xffffffffull) return VKHIP_OK;
     plan_split_k(static_cast<uint32_t>(tiles), ktiles, static_cast<uint64_t>(m) * n * batch, cu,
                  req, splits, chunk);
+    // A split over 128x128 tiles that gives each CU at most one workgroup is
+    // planned with twice the partitions instead, run as pairs by the direct
+    // kernel (two K streams per workgroup, gemm_nn_direct_kernel<.., true>),
+    // when every partition keeps at least 8 K-tiles and the pairs still fit
+    // one workgroup per CU: 256x256x65536 as 128 partitions in 64 pairs runs
+    // 74.8 us against 78.6 as 64 partitions. Other kernels run the same plan
+    // unpaired (NT 256x256x65536: 81.2 us against 80.3), so every layout
+    // keeps the same partitions and the same bits.
+    if (req == 0 && tile.bm == 128 && tiles * splits <= cu) {
+        uint32_t s2 = 1, c2 = ktiles;
+        plan_split_k(static_cast<uint32_t>(tiles), ktiles, static_cast<uint64_t>(m) * n * batch,
+                     2 * cu, 0, s2, c2);
+        if (s2 > splits && c2 >= 8 && tiles * ((s2 + 1) / 2) <= cu) {
+            splits = s2;
+            chunk = c2;
+            tile.pair = true;
+        }
+    }
     if (splits == 1) chunk = ktiles > 0 ? ktiles : 1;
     return VKHIP_OK;
 }
@@ -1889,26 +1988,6 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
                   : (g.sbn == 1 && aligned(b, g.sb0, g.sb1, g.sbk));
 
     const uint64_t out_elems = batch * m * n;
-    float* target = c;
-    if (splits > 1) {
-        float* ws = nullptr;
-        const size_t need = out_elems * splits * sizeof(float);
-        if (scratch) {
-            if (need > scratch->bytes)
-                return fail(VKHIP_ERR_INVALID,
-                            "matmul %ux%ux%u (batch %llu) splits K into %u partitions whose partials "
-                            "need %zu bytes; the allocation-free entry point's scratch holds %zu",
-                            m, n, k, static_cast<unsigned long long>(batch), splits, need,
-                            scratch->bytes);
-            ws = scratch->ptr;
-        } else {
-            int st = workspace(need, &ws);
-            if (st != VKHIP_OK) return st;
-        }
-        target = ws;
-        g.split_stride = out_elems;
-    }
-    g.c = target;
     int amode = akc ? (g.a_vec ? KCV : KCS) : (g.a_vec ? RCV : RCS);
     // The buffer-load paths (straight-to-LDS operands and the direct kernels)
     // address an operand by unsigned 32-bit byte offsets from its base, so
@@ -1935,18 +2014,62 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
                         ((static_cast<int64_t>(k) - 1) * g.sbk + n) * 4 < (int64_t{1} << 31);
     const bool a_rows = a_fwd && amode == RCV && g.sam == 1 && m % 4 == 0 && g.sak % 4 == 0 &&
                         ((static_cast<int64_t>(k) - 1) * g.sak + m) * 4 < (int64_t{1} << 31);
+    // The paired direct kernel writes one slice per pair of partitions (none
+    // for a single pair); every other kernel one per partition.
+    const bool direct128 = tile.bm == 128 && b_rows && (amode == KCD || a_rows);
+    const bool paired = direct128 && tile.pair && splits >= 2 && reinterpret_cast<uintptr_t>(c) % 16 == 0;
+    const uint32_t slices = paired ? (splits + 1) / 2 : splits;
+    float* target = c;
+    if (slices > 1) {
+        float* ws = nullptr;
+        const size_t need = out_elems * slices * sizeof(float);
+        if (scratch) {
+            if (need > scratch->bytes)
+                return fail(VKHIP_ERR_INVALID,
+                            "matmul %ux%ux%u (batch %llu) splits K into %u partitions whose partials "
+                            "need %zu bytes; the allocation-free entry point's scratch holds %zu",
+                            m, n, k, static_cast<unsigned long long>(batch), splits, need,
+                            scratch->bytes);
+            ws = scratch->ptr;
+        } else {
+            const int wst = workspace(need, &ws);
+            if (wst != VKHIP_OK) return wst;
+        }
+        target = ws;
+        g.split_stride = out_elems;
+    }
+    g.c = target;
     // Split direct launches run flat, partitions grouped per XCD (tile_of).
     const uint64_t flat = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
     if (splits > 1 && flat <= 0x7fffffffull) g.flat_splits = splits;
     const dim3 dgrid = g.flat_splits ? dim3(static_cast<uint32_t>(flat), 1, static_cast<uint32_t>(batch))
                                      : dim3(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
-    if (tile.bm == 128 && b_rows && (amode == KCD || a_rows) &&
-        reinterpret_cast<uintptr_t>(target) % 16 == 0) {
+    // (paired: c is 16-byte aligned, and so is the workspace)
+    if (paired || (direct128 && reinterpret_cast<uintptr_t>(target) % 16 == 0)) {
+        if (paired) {
+            g.pairs = slices;
+            dim3 grid(g.tiles_m * g.tiles_n, 1, static_cast<uint32_t>(batch));
+            if (g.pairs == 1) {
+                g.flat_splits = 0;
+            } else {
+                const uint64_t pflat = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * g.pairs;
+                g.flat_splits = pflat <= 0x7fffffffull ? g.pairs : 0;
+                grid = g.flat_splits ? dim3(static_cast<uint32_t>(pflat), 1, static_cast<uint32_t>(batch))
+                                     : dim3(g.tiles_m * g.tiles_n, g.pairs, static_cast<uint32_t>(batch));
+            }
+            if (amode == KCD)
+                hipLaunchKernelGGL((gemm_nn_direct_kernel<false, true>), grid, dim3(512), 0, ctx().stream, g);
+            else
+                hipLaunchKernelGGL((gemm_nn_direct_kernel<true, true>), grid, dim3(512), 0, ctx().stream, g);
+            VKHIP_LAUNCH_CHECK();
+            if (g.pairs > 1) return launch_split_k_reduce(target, c, out_elems, g.pairs);
+            return VKHIP_OK;
+        }
         const dim3 grid = dgrid;
         if (amode == KCD)
-            hipLaunchKernelGGL(gemm_nn_direct_kernel<false>, grid, dim3(256), 0, ctx().stream, g);
+            hipLaunchKernelGGL((gemm_nn_direct_kernel<false, false>), grid, dim3(256), 0, ctx().stream, g);
         else
-            hipLaunchKernelGGL(gemm_nn_direct_kernel<true>, grid, dim3(256), 0, ctx().stream, g);
+            hipLaunchKernelGGL((gemm_nn_direct_kernel<true, false>), grid, dim3(256), 0, ctx().stream, g);
         VKHIP_LAUNCH_CHECK();
         if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
         return VKHIP_OK;
