@@ -754,16 +754,18 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
 // column sets. Each output element still accumulates the same k pairs in the
 // same order as the register-path kernel (step (q, st) adds k = 4q + st and
 // 16 + 4q + st), so the results are the same bits.
+template <int COLS = 128>
 __device__ __forceinline__ void load_b_rows_direct(float* stage, __amdgpu_buffer_rsrc_t src,
                                                    int64_t s_k, uint32_t col0, uint32_t cols,
                                                    uint32_t k0, uint32_t kdim, int tid) {
-    // 32 k rows x 32 groups of 4 columns = 1024 slots, four per thread.
+    // 32 k rows x COLS/4 groups of 4 columns = 8 COLS slots, COLS/32 per thread.
+    constexpr int G = COLS / 4;
     const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < COLS / 32; ++i) {
         const int chunk = 4 * i + wave;
         const int slot = chunk * 64 + lane;
-        const int r = slot >> 5, grp = slot & 31;
+        const int r = slot / G, grp = slot % G;
         const uint32_t gk = k0 + r, gc = col0 + 4 * grp;
         const bool ok = gk < kdim && gc < cols;
         const uint32_t off = ok ? static_cast<uint32_t>((static_cast<int64_t>(gk) * s_k + gc) * 4)
@@ -790,9 +792,18 @@ __device__ __forceinline__ void load_b_rows_direct(float* stage, __amdgpu_buffer
 // (the fold's drain adds the lone last partial to 0.0 first; every later sum
 // is the same). With one pair the fold's drain (0.0 + the pair sum) is applied
 // here and the result is the output.
-template <bool ATR, bool PAIR>
+//
+// BN = 64: 128x64 tiles, a lane's two adjacent columns per k row (one 8-byte
+// LDS read) feeding two MFMAs over the column sets {2c + s}. Twice the tiles
+// of 128x128, so a grid that gives each CU one 128x128 workgroup gives it
+// two independent ones; each output takes the same MFMAs in the same order,
+// so the same bits as 128x128.
+template <bool ATR, bool PAIR, int BN = 128>
 __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmArgs g) {
-    constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
+    static_assert(BN == 128 || (BN == 64 && !PAIR), "128x128 tiles, or unpaired 128x64");
+    constexpr int BM = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
+    constexpr int NS = BN / 32;  // column sets: adjacent columns per lane
+    using BV = float __attribute__((ext_vector_type(NS)));
     constexpr int NG = PAIR ? 2 : 1;  // K streams (groups of four waves)
     using LA = TileLoader<BM, BK, KCD>;
     __shared__ __attribute__((aligned(16))) float lds_all[NG][2][BM * LDK + BK * BN];
@@ -826,16 +837,16 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
     // shorter) partition; a group past its own range only joins the barriers.
     const uint32_t steps = PAIR ? min(g.ktiles - 2 * split * g.chunk, g.chunk) : kt1 - kt0;
 
-    f32x16 acc[4];
+    f32x16 acc[NS];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[s][r] = 0.0f;
 
     // The K-tile's eight straight-to-LDS loads (four of A, four of B) with
     // their offsets computed once (kcd_offsets / rows_offsets).
     const int wv = __builtin_amdgcn_readfirstlane(wave);
-    uint32_t voa[4], vob[4];
+    uint32_t voa[4], vob[BN / 32];
     if constexpr (ATR)
         rows_offsets<BM>(voa, wv, lane, g.sak, row0, g.m);
     else
@@ -849,7 +860,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
                 load_b_rows_direct(lds[dst], arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
             else
                 LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
-            load_b_rows_direct(lds[dst] + BM * LDK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+            load_b_rows_direct<BN>(lds[dst] + BM * LDK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
             return;
         }
         issue_direct<BM / 32>(lds[dst], arsrc, voa, wv, kt * a_step);
@@ -869,7 +880,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
         const int cur = it & 1;
         if (kt + 1 < kt1) load_tile(kt + 1, cur ^ 1);
         const float* As = ATR ? lds[cur] + kh * 16 * BM + wm0 + lrow : lds[cur] + (wm0 + lrow) * BK;
-        const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + 4 * lrow;
+        const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + NS * lrow;
         auto a_at = [&](int q) {
             if constexpr (ATR) {
                 f32x4 v;
@@ -880,12 +891,11 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
                 return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)));
             }
         };
-        auto b_at = [&](int q, int st) {
-            return *reinterpret_cast<const f32x4*>(Bs + (4 * q + st) * BN);
-        };
+        auto b_at = [&](int q, int st) { return *reinterpret_cast<const BV*>(Bs + (4 * q + st) * BN); };
         // (Left to the compiler's scheduler: the MFMA/read interleave the
         // register-path kernel imposes measured 1-3% slower here.)
-        f32x4 av[2], bv[2][4];
+        f32x4 av[2];
+        BV bv[2][4];
         av[0] = a_at(0);
 #pragma unroll
         for (int st = 0; st < 4; ++st) bv[0][st] = b_at(0, st);
@@ -900,7 +910,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
 #pragma unroll
             for (int st = 0; st < 4; ++st)
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
+                for (int s = 0; s < NS; ++s)
                     acc[s] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][st], bv[cb][st][s], acc[s],
                                                                   0, 0, 0);
         }
@@ -931,17 +941,18 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
     }
 
     // acc[s] register r of lane l: row 8*(r/4) + 4*(l/32) + r%4 of the wave's
-    // 32, column 4*(l%32) + s of the tile: four columns per lane are adjacent.
-    const uint32_t col = col0 + 4 * lrow;
+    // 32, column NS*(l%32) + s of the tile: a lane's NS columns are adjacent
+    // (N is a multiple of four, so they are in or out together).
+    const uint32_t col = col0 + NS * lrow;
     if (col < g.n) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
             if (row < g.m) {
-                f32x4 v;
+                BV v;
 #pragma unroll
-                for (int s = 0; s < 4; ++s) v[s] = acc[s][r];
-                *reinterpret_cast<f32x4*>(cbase + static_cast<uint64_t>(row) * g.n + col) = v;
+                for (int s = 0; s < NS; ++s) v[s] = acc[s][r];
+                *reinterpret_cast<BV*>(cbase + static_cast<uint64_t>(row) * g.n + col) = v;
             }
         }
     }
@@ -2063,6 +2074,35 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
                 hipLaunchKernelGGL((gemm_nn_direct_kernel<true, true>), grid, dim3(512), 0, ctx().stream, g);
             VKHIP_LAUNCH_CHECK();
             if (g.pairs > 1) return launch_split_k_reduce(target, c, out_elems, g.pairs);
+            return VKHIP_OK;
+        }
+        // 128x64 tiles when the last round of 128x128 workgroups would leave
+        // more of the machine idle: workgroups resident per CU are two of
+        // 128x128 (70 KB of LDS each) or three of 128x64 (53 KB), and a
+        // 128x64 tile does 0.94x the work per CU-second (4096^3: 130 against
+        // 138 TFLOP/s), so the fill of the launch's rounds decides:
+        //   fill = workgroups / (rounds * slots), 128x64's scaled by 0.94.
+        // Measured: 3072^3 90 -> 119 TFLOP/s, 2304^3 90 -> 112, 2048x3072x2048
+        // 105 -> 127, 2048^3 121 -> 125; 4096^3, 8192x1024x4096, 2560^3 and
+        // 4096x2048x2048 keep 128x128 (128x64 measured 3-7% slower there).
+        const uint64_t cus = ctx().ready ? static_cast<uint64_t>(ctx().caps.compute_units) : 256u;
+        const uint64_t w128 = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits * batch;
+        const uint64_t w64 = static_cast<uint64_t>(g.tiles_m) * ceil_div(n, 64) * splits * batch;
+        auto fill = [](uint64_t wgs, uint64_t slots) {
+            return static_cast<double>(wgs) / static_cast<double>((wgs + slots - 1) / slots * slots);
+        };
+        if (0.94 * fill(w64, 3 * cus) > fill(w128, 2 * cus)) {
+            g.tiles_n = ceil_div(n, 64);
+            const uint64_t f64 = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
+            g.flat_splits = (splits > 1 && f64 <= 0x7fffffffull) ? splits : 0;
+            const dim3 grid = g.flat_splits ? dim3(static_cast<uint32_t>(f64), 1, static_cast<uint32_t>(batch))
+                                            : dim3(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
+            if (amode == KCD)
+                hipLaunchKernelGGL((gemm_nn_direct_kernel<false, false, 64>), grid, dim3(256), 0, ctx().stream, g);
+            else
+                hipLaunchKernelGGL((gemm_nn_direct_kernel<true, false, 64>), grid, dim3(256), 0, ctx().stream, g);
+            VKHIP_LAUNCH_CHECK();
+            if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
             return VKHIP_OK;
         }
         const dim3 grid = dgrid;
