@@ -174,7 +174,13 @@ enum vkhip_op {
     /* relu(src0 + src1), sources with the output's extents (broadcast axes
      * stride 0) as for ADD: the ADD and RELU nodes' values in one pass
      * (a Linear layer's bias add and activation). */
-    VKHIP_OP_ADD_RELU = 104
+    VKHIP_OP_ADD_RELU = 104,
+    /* MAX_POOL2D_BACKWARD followed by the RELU_BACKWARD of the relu that
+     * produced the pool's input: src0 g [N,C,out_h,out_w], src1 x [N,C,H,W]
+     * (the pool's input, the relu's output), params vkhip_unfold as for
+     * MAX_POOL2D_BACKWARD -> out = x <= 0 ? +0 : max_pool2d_backward(g, x):
+     * the two nodes' values (selects only), in one pass that reads x once. */
+    VKHIP_OP_MAX_POOL2D_BACKWARD_RELU = 105
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */

@@ -768,11 +768,19 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 if (st != VKHIP_OK) return st;
                 break;
             }
-            case VKHIP_OP_MAX_POOL2D_BACKWARD: {
+            case VKHIP_OP_MAX_POOL2D_BACKWARD:
+            case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU: {
                 vkhip_unfold p;
                 memcpy(&p, nd->params, sizeof p);
                 or_max_pool2d_backward((const float*)nd->src[0].data, (const float*)nd->src[1].data, (float*)o->data,
                                        (uint32_t)(o->ne[0] * o->ne[1]), (uint32_t)nd->src[0].ne[2], (uint32_t)nd->src[0].ne[3], &p, threads);
+                if (nd->op == VKHIP_OP_MAX_POOL2D_BACKWARD_RELU) {
+                    /* the relu gradient on the pool's input, as VKHIP_OP_RELU_BACKWARD */
+                    const float* x = (const float*)nd->src[1].data;
+                    float* out = (float*)o->data;
+                    for (int64_t i = 0; i < n; ++i)
+                        if (compare_f(VKHIP_OP_LESS_EQUAL, x[i], 0.0f)) out[i] = 0.0f;
+                }
                 break;
             }
             case VKHIP_OP_CROSS_ENTROPY:

@@ -148,8 +148,42 @@ def conv_relu_loss_and_grads(backend, x, w, bias, stride, pad, dil, fused):
         T.FUSED_CONV_EPILOGUE = prev
 
 
+def relu_pool_loss_and_grad(backend, x, kernel, stride, pad, fused):
+    """sum(max_pool2d(relu(x)) * probe) and the gradient of x, with the relu
+    and pool gradients built as one MAX_POOL2D_BACKWARD_RELU node (fused) or
+    as MAX_POOL2D_BACKWARD and RELU_BACKWARD."""
+    from vkml_amd import tensor as T
+
+    prev = T.FUSED_POOL_RELU_GRAD
+    T.FUSED_POOL_RELU_GRAD = fused
+    try:
+        xt = T.tensor(x, requires_grad=True, backend=backend)
+        out = T.max_pool2d(T.relu(xt), kernel, stride, pad)
+        probe = np.linspace(-1.0, 1.0, int(np.prod(out.shape)), dtype=np.float32)
+        loss = T.sum(out * T.tensor(probe.reshape(out.shape), backend=backend))
+        loss.backward()
+        want = T.OP["MAX_POOL2D_BACKWARD_RELU"] if fused else T.OP["RELU_BACKWARD"]
+        assert xt.grad.node.op == want
+        return out.numpy(), xt.grad.numpy()
+    finally:
+        T.FUSED_POOL_RELU_GRAD = prev
+
+
+# (shape, kernel, stride, padding): the 2x2 tiling kernel and the general one
+POOL_GEOMETRIES = [((2, 3, 8, 8), 2, 2, 0), ((2, 3, 7, 9), 3, 2, 1), ((1, 2, 6, 6), 3, 1, 1)]
+
+
+def pool_relu_input(shape, seed):
+    """Uniform values with ties, NaN, signed zeros and negatives."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-3, 4, shape).astype(np.float32) * np.float32(0.5)
+    x.reshape(-1)[:4] = [np.nan, -0.0, 0.0, -1.0]
+    return x
+
+
 GRAPH_REWRITES = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU",
-                  "FUSED_CONV_EPILOGUE", "FUSED_CONV_INPUT_GRAD", "FOLD_CONV_WEIGHT_GRAD")
+                  "FUSED_CONV_EPILOGUE", "FUSED_CONV_INPUT_GRAD", "FOLD_CONV_WEIGHT_GRAD",
+                  "FUSED_POOL_RELU_GRAD")
 
 
 def train_with_rewrites(backend, model_fn, batches, enabled, lr=0.1, momentum=0.9,

@@ -15,7 +15,8 @@ import pytest
 from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad,
                       config5_batches, config5_golden_losses, config5_model, config5_train, conv_loss_and_grads,
                       conv_relu_loss_and_grads, gemm_tolerance, mlp_batches, mlp_model, train_with_rewrites,
-                      normwise_rel_err, relu_grad, relu_inputs)
+                      normwise_rel_err, relu_grad, relu_inputs, POOL_GEOMETRIES, pool_relu_input,
+                      relu_pool_loss_and_grad)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -191,15 +192,33 @@ def test_conv_bias_relu_node_on_device_is_the_three_nodes(backends, shape, cout,
         assert got.tobytes() == want.tobytes()
 
 
+@pytest.mark.parametrize("shape,kernel,stride,pad",
+                         POOL_GEOMETRIES + [((128, 64, 32, 32), 2, 2, 0), ((128, 128, 16, 16), 2, 2, 0)])
+def test_pool_relu_gradient_node_on_device(backends, shape, kernel, stride, pad):
+    """On the device, the relu gradient of max_pool2d(relu(x)) as one
+    MAX_POOL2D_BACKWARD_RELU node gives the oracle's bits and the device's own
+    two-node graph's, through the 2x2 tiling kernel and the general one."""
+    dev, cpu = backends
+    x = pool_relu_input(shape, SEED + 14)
+    print(f"pool_relu x={shape} k={kernel} s={stride} p={pad}", flush=True)
+    fused = relu_pool_loss_and_grad(dev, x, kernel, stride, pad, True)
+    graph = relu_pool_loss_and_grad(dev, x, kernel, stride, pad, False)
+    want = relu_pool_loss_and_grad(cpu, x, kernel, stride, pad, True)
+    for got, two, ref in zip(fused, graph, want):
+        assert got.tobytes() == two.tobytes()
+        assert got.tobytes() == ref.tobytes()
+
+
 @pytest.mark.parametrize("model", ["mlp", "cnn"])
 def test_exact_graph_rewrites_keep_the_device_bits(backends, model):
     """On the device, the graph rewrites that compute the same arithmetic
     (constant folding, weight gradients in the weight's layout, fused
-    add+relu and conv+bias+relu) leave every loss and parameter of
+    add+relu, conv+bias+relu and pool+relu gradients) leave every loss and parameter of
     SGD-momentum training bit for bit unchanged: config 1's MLP for 10 steps,
     config 5's CNN at batch 128 for 3 steps."""
     dev, _ = backends
-    rewrites = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU", "FUSED_CONV_EPILOGUE")
+    rewrites = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU", "FUSED_CONV_EPILOGUE",
+                "FUSED_POOL_RELU_GRAD")
     if model == "mlp":
         fn, batches = mlp_model, mlp_batches(10)
     else:

@@ -11,7 +11,7 @@ import torch
 
 from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads,
                       config5_batches, config5_model, conv_relu_loss_and_grads, mlp_batches, mlp_model,
-                      train_with_rewrites,
+                      train_with_rewrites, POOL_GEOMETRIES, pool_relu_input, relu_pool_loss_and_grad,
                       relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
@@ -206,6 +206,21 @@ def test_graph_rewrites_keep_the_oracle_bits(cpu, model):
     assert on[0].tobytes() == off[0].tobytes()
     for a, b in zip(on[1], off[1]):
         assert a.tobytes() == b.tobytes()
+
+
+@pytest.mark.parametrize("shape,kernel,stride,pad", POOL_GEOMETRIES)
+def test_pool_relu_gradient_node_is_the_two_nodes(cpu, shape, kernel, stride, pad):
+    """The relu gradient of max_pool2d(relu(x)) as one MAX_POOL2D_BACKWARD_RELU
+    node gives the MAX_POOL2D_BACKWARD + RELU_BACKWARD graph's bits on the
+    oracle, with ties (first maximum), NaN, signed zeros and negatives."""
+    x = pool_relu_input(shape, SEED + 12)
+    fused = relu_pool_loss_and_grad(cpu, x, kernel, stride, pad, True)
+    graph = relu_pool_loss_and_grad(cpu, x, kernel, stride, pad, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
+    # and the mask is the relu's: x <= 0 gets +0 whatever the pool routed there
+    g = fused[1]
+    assert np.all(g[x <= 0] == 0) and not np.any(np.signbit(g[x <= 0]))
 
 
 @pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONV_GEOMETRIES)

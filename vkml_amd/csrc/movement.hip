@@ -507,7 +507,9 @@ __global__ __launch_bounds__(256) void max_pool2d_kernel(const float* __restrict
 // grad: contiguous [N, C, out_h, out_w]; src: [N, C, H, W] with strides sd;
 // dst contiguous [N, C, H, W]. Pull: each input position adds, in ascending
 // window order, the gradient of every window whose first maximum it is
-// (kernels_movement.cpp:620-680).
+// (kernels_movement.cpp:620-680). RELU: then the gradient of the relu that
+// produced src, src <= 0 ? +0 : that value (a NaN src passes it through).
+template <bool RELU>
 __global__ __launch_bounds__(256) void max_pool2d_backward_kernel(
     const float* __restrict__ grad, const float* __restrict__ src, Op4 sd, float* __restrict__ dst,
     Geo g, uint32_t channels, uint32_t blocks_per_plane) {
@@ -534,6 +536,7 @@ __global__ __launch_bounds__(256) void max_pool2d_backward_kernel(
                 acc = acc + gp[oh * g.out_w + ow];
         }
     }
+    if (RELU && pl[h * sd.nb[2] + x * sd.nb[3]] <= 0.0f) acc = 0.0f;
     dst[static_cast<uint64_t>(plane) * hw + idx] = acc;
 }
 
@@ -578,7 +581,9 @@ __global__ __launch_bounds__(256) void max_pool2x2_kernel(const float* __restric
 // Backward of the same tiling: every input position lies in exactly one
 // window, so the pull of the general kernel reduces to 0 + g at the window's
 // first maximum and +0 elsewhere (0 + g also turns a -0 gradient into +0, as
-// the pull's accumulator does).
+// the pull's accumulator does). RELU: masked by src <= 0 as above, from the
+// src values already loaded for the window scan.
+template <bool RELU>
 __global__ __launch_bounds__(256) void max_pool2x2_backward_kernel(
     const float* __restrict__ grad, const float* __restrict__ src, float* __restrict__ dst,
     uint32_t W, FastDiv pairs_per_row, uint32_t total) {
@@ -602,6 +607,13 @@ __global__ __launch_bounds__(256) void max_pool2x2_backward_kernel(
     top[3] = a1 == 1 ? g1 : 0.0f;
     bot[2] = a1 == 2 ? g1 : 0.0f;
     bot[3] = a1 == 3 ? g1 : 0.0f;
+    if (RELU) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (t[i] <= 0.0f) top[i] = 0.0f;
+            if (u[i] <= 0.0f) bot[i] = 0.0f;
+        }
+    }
     *reinterpret_cast<f32x4_t*>(dst + base) = top;
     *reinterpret_cast<f32x4_t*>(dst + base + W) = bot;
 }
@@ -681,7 +693,8 @@ int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uin
 }
 
 int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_operand& sd,
-                               float* dst, uint32_t out_h, uint32_t out_w, const vkhip_unfold& p) {
+                               float* dst, uint32_t out_h, uint32_t out_w, const vkhip_unfold& p,
+                               bool relu) {
     Geo g;
     int st = make_geo(p, g);
     if (st != VKHIP_OK) return st;
@@ -703,7 +716,7 @@ int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_
     if (tiled) {
         const uint64_t total = planes * out_h * out_w / 2;
         if (total <= 0xffffffffull) {
-            hipLaunchKernelGGL(max_pool2x2_backward_kernel,
+            hipLaunchKernelGGL(relu ? max_pool2x2_backward_kernel<true> : max_pool2x2_backward_kernel<false>,
                                dim3(ceil_div(static_cast<uint32_t>(total), 256)), dim3(256), 0,
                                ctx().stream, grad, src, dst, static_cast<uint32_t>(g.W),
                                FastDiv(out_w / 2), static_cast<uint32_t>(total));
@@ -712,8 +725,9 @@ int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_
         }
     }
     const uint32_t bpp = ceil_div(hw, 256);
-    hipLaunchKernelGGL(max_pool2d_backward_kernel, dim3(static_cast<uint32_t>(planes * bpp)),
-                       dim3(256), 0, ctx().stream, grad, src, to_op4(sd), dst, g, sd.ne[1], bpp);
+    hipLaunchKernelGGL(relu ? max_pool2d_backward_kernel<true> : max_pool2d_backward_kernel<false>,
+                       dim3(static_cast<uint32_t>(planes * bpp)), dim3(256), 0, ctx().stream, grad,
+                       src, to_op4(sd), dst, g, sd.ne[1], bpp);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }

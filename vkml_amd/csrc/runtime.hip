@@ -33,7 +33,8 @@ int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t*
 int launch_max_pool2d(const float* src, const vkhip_operand& sd, float* dst, uint32_t out_h,
                       uint32_t out_w, const vkhip_unfold& p);
 int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_operand& sd,
-                               float* dst, uint32_t out_h, uint32_t out_w, const vkhip_unfold& p);
+                               float* dst, uint32_t out_h, uint32_t out_w, const vkhip_unfold& p,
+                               bool relu);
 int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axis, int log_mode);
 int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst);
 int launch_elementwise(const vkhip_node& nd);
@@ -345,6 +346,7 @@ static int supports_node(const vkhip_node& nd) {
             return o.ndim == 1 && o.ne[0] == x.ne[0];
         }
         case VKHIP_OP_MAX_POOL2D_BACKWARD:
+        case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU:
             return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
                    nd.src[0].ndim == 4 && contiguous(nd.src[0]) && nd.src[1].ndim == 4 &&
                    o.ndim == 4 && contiguous(o);
@@ -463,7 +465,8 @@ static int check_extents(const vkhip_node& nd) {
                 return fail(VKHIP_ERR_INVALID, "max_pool2d: input/output extents disagree with the window geometry");
             return VKHIP_OK;
         }
-        case VKHIP_OP_MAX_POOL2D_BACKWARD: {
+        case VKHIP_OP_MAX_POOL2D_BACKWARD:
+        case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU: {
             vkhip_unfold p;
             memcpy(&p, nd.params, sizeof p);
             const int64_t oh = window_span(p.image_h, p.kernel_h, p.stride_h, p.pad_h, p.dilation_h);
@@ -497,6 +500,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_ARGMAX: return "argmax";
         case VKHIP_OP_MAX_POOL2D: return "max_pool2d";
         case VKHIP_OP_MAX_POOL2D_BACKWARD: return "max_pool2d_backward";
+        case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU: return "max_pool2d_backward_relu";
         case VKHIP_OP_CROSS_ENTROPY: return "cross_entropy";
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: return "cross_entropy_backward";
         case VKHIP_OP_CONV2D: return "conv2d";
@@ -703,7 +707,8 @@ static int compute_node(const vkhip_node& nd) {
                                      static_cast<uint32_t>(nd.out.ne[2]),
                                      static_cast<uint32_t>(nd.out.ne[3]), p);
         }
-        case VKHIP_OP_MAX_POOL2D_BACKWARD: {
+        case VKHIP_OP_MAX_POOL2D_BACKWARD:
+        case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU: {
             vkhip_unfold p;
             memcpy(&p, nd.params, sizeof p);
             for (int i = 0; i < 4; ++i)
@@ -714,7 +719,8 @@ static int compute_node(const vkhip_node& nd) {
             return launch_max_pool2d_backward(
                 static_cast<const float*>(nd.src[0].data), static_cast<const float*>(nd.src[1].data),
                 to_operand(nd.src[1]), static_cast<float*>(nd.out.data),
-                static_cast<uint32_t>(nd.src[0].ne[2]), static_cast<uint32_t>(nd.src[0].ne[3]), p);
+                static_cast<uint32_t>(nd.src[0].ne[2]), static_cast<uint32_t>(nd.src[0].ne[3]), p,
+                nd.op == VKHIP_OP_MAX_POOL2D_BACKWARD_RELU);
         }
         default: return launch_elementwise(nd);
     }
@@ -1069,7 +1075,7 @@ extern "C" int vkhip_max_pool2d_backward(const float* grad, const float* src, fl
         d.nb[i] = s;
         s *= ne[i];
     }
-    return vkhip::launch_max_pool2d_backward(grad, src, d, dst, out_h, out_w, *p);
+    return vkhip::launch_max_pool2d_backward(grad, src, d, dst, out_h, out_w, *p, false);
 }
 
 // ---- timing ------------------------------------------------------------------------------

@@ -458,7 +458,13 @@ WEIGHT_GRAD_IN_PLACE_LAYOUT = True
 
 
 def _transposed_matrix_source(b: "Node"):
-    """w when node b is the view w.T of a 2-D w that requires grad, else None."""
+    """w when node b is the view w.T of a 2-D w that requires grad, or the
+    matmul lowering's rank-4 broadcast of that view (leading axes of 1), else
+    None."""
+    while (b.op == BROADCAST and b.view_src is not None and len(b.view_src.shape) == 2
+           and len(b.shape) == 4 and tuple(b.shape[:2]) == (1, 1)
+           and tuple(b.shape[2:]) == tuple(b.view_src.shape)):
+        b = b.view_src
     if (b.op == PERMUTE and len(b.shape) == 2 and b.aux is not None and list(b.aux) == [1, 0]
             and b.view_src is not None and b.view_src.requires_grad and b.view_src.dtype == np.float32):
         return b.view_src
@@ -766,6 +772,28 @@ FUSED_CROSS_ENTROPY = True
 # of four kernels and two materialised zero tensors. False builds the
 # reference's nodes.
 FUSED_RELU_BACKWARD = True
+
+# A relu gradient whose incoming gradient is that of a max-pool over the
+# relu's output (conv -> relu -> pool) as one MAX_POOL2D_BACKWARD_RELU node:
+# the pool's gradient routed to each window's first maximum, then masked by
+# the pool's input <= 0, the values of the two nodes (selects only) in one
+# pass. False keeps MAX_POOL2D_BACKWARD and RELU_BACKWARD.
+FUSED_POOL_RELU_GRAD = True
+
+
+def _relu_grad(mask_src: "Node", y: "Node", g: "Tensor") -> "Tensor":
+    """RELU_BACKWARD(mask_src, g), where mask_src is the relu's input or its
+    output y (relu(v) <= 0 exactly where v <= 0; a NaN stays NaN, so both
+    masks select alike). When g is the not yet computed gradient of a max-pool
+    whose input is y, and y feeds nothing else (else g would be a sum), one
+    MAX_POOL2D_BACKWARD_RELU node over the pool gradient's sources instead."""
+    gn = g.node
+    if (FUSED_POOL_RELU_GRAD and gn.op == OP["MAX_POOL2D_BACKWARD"] and not gn.computed
+            and gn.src[1] is y):
+        return Tensor(Node(OP["MAX_POOL2D_BACKWARD_RELU"], gn.shape, np.float32, gn.backend,
+                           list(gn.src), params=gn.params))
+    return Tensor(Node(OP["RELU_BACKWARD"], mask_src.shape, np.float32, mask_src.backend,
+                       [mask_src, gn]))
 
 
 def cross_entropy(logits: Tensor, target: Tensor) -> Tensor:
@@ -1175,8 +1203,7 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         if FUSED_RELU_BACKWARD:
             x = ta()
             g = grad if grad.shape == x.shape else grad.broadcast_to(x.shape)
-            rb = Node(OP["RELU_BACKWARD"], x.shape, np.float32, x.node.backend, [x.node, g.node])
-            _accumulate(grads, a, Tensor(rb))
+            _accumulate(grads, a, _relu_grad(x.node, node, g))
         else:
             _accumulate(grads, a, where(less_equal(ta(), zeros_like(ta())), zeros_like(grad), grad))
     elif op in (OP["SUM"], OP["MEAN"]):
@@ -1210,15 +1237,14 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
                 # transpose of d(w^T) = a^T @ grad -- the same products summed
                 # in the same k order under a plan symmetric in M and N -- in
                 # w's own layout, so no transposing copy follows.
-                _accumulate(grads, w, matmul(grad.transpose(-2, -1), ta()))
+                _accumulate(grads, w, matmul(grad.transpose(-2, -1), ta()).reshape(w.shape))
             else:
                 _accumulate(grads, b, matmul(ta().transpose(-2, -1), grad))
     elif op == OP["ADD_RELU"]:
         # the RELU rule (the mask from the output, as for CONV2D_BIAS_RELU)
         # then the ADD rule: the same gradient to both sources
         g = grad if grad.shape == out.shape else grad.broadcast_to(out.shape)
-        dz = Tensor(Node(OP["RELU_BACKWARD"], out.shape, np.float32, out.node.backend,
-                         [node, g.node]))
+        dz = _relu_grad(node, node, g)
         if a.requires_grad:
             _accumulate(grads, a, dz)
         if b.requires_grad:
@@ -1230,8 +1256,7 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         # rules for the bias (its broadcast adjoint: the sum over N, H, W), then
         # the CONV2D rule with that gradient.
         g = grad if grad.shape == out.shape else grad.broadcast_to(out.shape)
-        dz = Tensor(Node(OP["RELU_BACKWARD"], out.shape, np.float32, out.node.backend,
-                         [node, g.node]))
+        dz = _relu_grad(node, node, g)
         bias3 = node.src[2]
         if bias3.requires_grad:
             _accumulate(grads, bias3, reduce_to_shape(dz, bias3.shape))
