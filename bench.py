@@ -508,7 +508,11 @@ def training_steps(steps_mlp: int = 100, steps_cnn: int = 50, only: str | None =
     the same step: "eager" (the host core builds, orders and packs the graph
     every step), "replay" (the step recorded once, its compute/SGD calls
     replayed from C, vkhip_program_run) and "graph" (the replay captured once
-    into a HIP graph); all three give the same bits (tests/test_gpu_replay.py)."""
+    into a HIP graph); all three give the same bits (tests/test_gpu_replay.py).
+    "graph_queued" is "graph" with the loss read back after the last timed
+    step only: every step still uploads its batch and runs the whole forward,
+    backward and update, but the host queues the next step instead of waiting
+    on each loss, so the device runs the steps back to back."""
     from vkml_amd import nn, optim
     from vkml_amd import tensor as T
 
@@ -530,7 +534,7 @@ def training_steps(steps_mlp: int = 100, steps_cnn: int = 50, only: str | None =
         data = [(rng.uniform(lo, hi, shape).astype(np.float32),
                  rng.integers(0, classes, shape[0]).astype(np.int64)) for _ in range(4)]
         out = {}
-        for mode in ("eager", "replay", "graph"):
+        for mode in ("eager", "replay", "graph", "graph_queued"):
             nn.manual_seed(20260726)
             model = make()
             opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
@@ -547,18 +551,26 @@ def training_steps(steps_mlp: int = 100, steps_cnn: int = 50, only: str | None =
                     x, y = data[i % 4]
                     return fn(T.tensor(x), T.tensor(y)).item()
             else:
-                captured = T.CapturedStep(fn, *data[0], graph=(mode == "graph"))
+                captured = T.CapturedStep(fn, *data[0], graph=mode.startswith("graph"))
+                queued = mode == "graph_queued"
 
                 def step(i):
-                    return float(captured(*data[i % 4])[0])
+                    out = captured(*data[i % 4], read=not queued)
+                    return None if out is None else float(out[0])
+            # (queued: the last loss is read after the timed loop's final
+            # step, inside the timed region)
             # the recording is step 0 of the replayed runs: every mode then
             # takes the same steps on the same batches, and reports the same
             # last loss
             for i in range(0 if mode == "eager" else 1, 3):
                 step(i)
+            if mode == "graph_queued":
+                captured.outputs_now()  # the warm-up steps are done
             t0 = time.perf_counter()
             for i in range(3, 3 + steps):
                 last = step(i)
+            if mode == "graph_queued":
+                last = float(captured.outputs_now()[0])
             dt = time.perf_counter() - t0
             out[mode] = {"ms_per_step": round(dt * 1e3 / steps, 4),
                          "steps_per_s": round(steps / dt, 2), "last_loss": round(last, 5)}

@@ -180,7 +180,14 @@ enum vkhip_op {
      * (the pool's input, the relu's output), params vkhip_unfold as for
      * MAX_POOL2D_BACKWARD -> out = x <= 0 ? +0 : max_pool2d_backward(g, x):
      * the two nodes' values (selects only), in one pass that reads x once. */
-    VKHIP_OP_MAX_POOL2D_BACKWARD_RELU = 105
+    VKHIP_OP_MAX_POOL2D_BACKWARD_RELU = 105,
+    /* MATMUL with the bias add (and ReLU) of a Linear layer: src0, src1 as
+     * MATMUL, src2 bias [N] (any stride), params uint32 relu -> out =
+     * relu?(src0 @ src1 + bias[col]), relu(v) = v <= 0 ? 0 : v: the values of
+     * the MATMUL, ADD (bias broadcast over rows) and RELU nodes it replaces,
+     * the epilogue applied where the split-K partials are folded (or in a
+     * pass after an unsplit product). */
+    VKHIP_OP_MATMUL_BIAS = 106
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */

@@ -640,6 +640,22 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
             case VKHIP_OP_MATMUL:
                 or_matmul((const float*)nd->src[0].data, &s0, (const float*)nd->src[1].data, &s1, (float*)o->data, threads);
                 break;
+            case VKHIP_OP_MATMUL_BIAS: {
+                /* MATMUL, then the ADD of the bias broadcast over rows and the
+                 * RELU (relu flag in params), element by element in f32 */
+                uint32_t relu;
+                memcpy(&relu, nd->params, sizeof relu);
+                or_matmul((const float*)nd->src[0].data, &s0, (const float*)nd->src[1].data, &s1, (float*)o->data, threads);
+                const float* bias = (const float*)nd->src[2].data;
+                const int64_t ncols = o->ne[o->ndim - 1], bs = nd->src[2].nb[0];
+                float* out = (float*)o->data;
+                for (int64_t i = 0; i < n; ++i) {
+                    float v = out[i] + bias[(i % ncols) * bs];
+                    if (relu) v = unary_f(VKHIP_OP_RELU, v);
+                    out[i] = v;
+                }
+                break;
+            }
             case VKHIP_OP_SOFTMAX: case VKHIP_OP_LOG_SOFTMAX: {
                 int32_t axis;
                 memcpy(&axis, nd->params, sizeof axis);

@@ -169,6 +169,35 @@ def relu_pool_loss_and_grad(backend, x, kernel, stride, pad, fused):
         T.FUSED_POOL_RELU_GRAD = prev
 
 
+def linear_loss_and_grads(backend, x, w, bias, relu, fused):
+    """sum(relu?(x @ w.T + bias) * probe) and the gradients of x, w and bias,
+    with the product, bias add and relu built as one MATMUL_BIAS node (fused)
+    or as the MATMUL, ADD and RELU nodes."""
+    from vkml_amd import tensor as T
+
+    prev = T.FUSED_LINEAR_BIAS
+    T.FUSED_LINEAR_BIAS = fused
+    try:
+        xt = T.tensor(x, requires_grad=True, backend=backend)
+        wt = T.tensor(w, requires_grad=True, backend=backend)
+        bt = T.tensor(bias, requires_grad=True, backend=backend)
+        out = T.matmul(xt, wt.transpose(-2, -1)) + bt
+        if relu:
+            out = T.relu(out)
+        assert (out.node.view_src is not None and out.node.view_src.op == T.OP["MATMUL_BIAS"]) == fused
+        probe = np.linspace(-1.0, 1.0, int(np.prod(out.shape)), dtype=np.float32)
+        loss = T.sum(out * T.tensor(probe.reshape(out.shape), backend=backend))
+        loss.backward()
+        return out.numpy(), xt.grad.numpy(), wt.grad.numpy(), bt.grad.numpy()
+    finally:
+        T.FUSED_LINEAR_BIAS = prev
+
+
+# (rows, in, out): split-K folds (the epilogue in the fold) and unsplit products
+LINEAR_SHAPES = [(64, 784, 128), (64, 128, 10), (128, 8192, 256), (128, 256, 100), (512, 64, 4096),
+                 (3, 5, 7)]
+
+
 # (shape, kernel, stride, padding): the 2x2 tiling kernel and the general one
 POOL_GEOMETRIES = [((2, 3, 8, 8), 2, 2, 0), ((2, 3, 7, 9), 3, 2, 1), ((1, 2, 6, 6), 3, 1, 1)]
 
@@ -183,7 +212,7 @@ def pool_relu_input(shape, seed):
 
 GRAPH_REWRITES = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU",
                   "FUSED_CONV_EPILOGUE", "FUSED_CONV_INPUT_GRAD", "FOLD_CONV_WEIGHT_GRAD",
-                  "FUSED_POOL_RELU_GRAD")
+                  "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS")
 
 
 def train_with_rewrites(backend, model_fn, batches, enabled, lr=0.1, momentum=0.9,

@@ -78,6 +78,32 @@ def test_replayed_steps_are_the_eager_steps_bit_for_bit(config, graph):
     step.close()
 
 
+@pytest.mark.parametrize("graph", [False, True], ids=["replay", "graph"])
+@pytest.mark.parametrize("config", ["mlp", "cnn"])
+def test_queued_steps_are_the_read_back_steps(config, graph):
+    """Replays queued without reading the loss (read=False: the next step's
+    uploads wait only for their staging slots) end in the same parameters and
+    last loss as replays that read every loss back."""
+    dev = T.default_backend()
+    make, _, _, _, lr = CONFIGS[config]
+    batches = _batches(config, 10)
+    finals = []
+    for queued in (False, True):
+        model = make(dev)
+        opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
+        step = T.CapturedStep(_step_fn(model, opt), *batches[0], graph=graph)
+        last = None
+        for x, y in batches[1:]:
+            out = step(x, y, read=not queued)
+            last = out[0] if out is not None else None
+        if queued:
+            assert last is None
+            last = step.outputs_now()[0]
+        finals.append((np.asarray(last).tobytes(), [p.numpy().tobytes() for p in model.parameters()]))
+        step.close()
+    assert finals[0] == finals[1]
+
+
 def test_captured_step_checks_its_inputs():
     dev = T.default_backend()
     model = _mlp(dev)

@@ -16,7 +16,7 @@ from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad,
                       config5_batches, config5_golden_losses, config5_model, config5_train, conv_loss_and_grads,
                       conv_relu_loss_and_grads, gemm_tolerance, mlp_batches, mlp_model, train_with_rewrites,
                       normwise_rel_err, relu_grad, relu_inputs, POOL_GEOMETRIES, pool_relu_input,
-                      relu_pool_loss_and_grad)
+                      relu_pool_loss_and_grad, LINEAR_SHAPES, linear_loss_and_grads)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -192,6 +192,24 @@ def test_conv_bias_relu_node_on_device_is_the_three_nodes(backends, shape, cout,
         assert got.tobytes() == want.tobytes()
 
 
+@pytest.mark.parametrize("relu", [False, True])
+@pytest.mark.parametrize("rows,fan_in,fan_out", LINEAR_SHAPES)
+def test_linear_bias_node_on_device(backends, rows, fan_in, fan_out, relu):
+    """On the device, x @ w.T + bias (then relu) as one MATMUL_BIAS node (the
+    epilogue in the split-K fold, or a pass after an unsplit product) gives the
+    device's MATMUL + ADD (+ RELU) graph bit for bit."""
+    dev, _ = backends
+    rng = np.random.default_rng(SEED + 16)
+    x = rng.uniform(-1, 1, (rows, fan_in)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (fan_out, fan_in)).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, fan_out).astype(np.float32)
+    print(f"linear_bias {rows}x{fan_in}->{fan_out} relu={relu}", flush=True)
+    fused = linear_loss_and_grads(dev, x, w, bias, relu, True)
+    graph = linear_loss_and_grads(dev, x, w, bias, relu, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
+
+
 @pytest.mark.parametrize("shape,kernel,stride,pad",
                          POOL_GEOMETRIES + [((128, 64, 32, 32), 2, 2, 0), ((128, 128, 16, 16), 2, 2, 0)])
 def test_pool_relu_gradient_node_on_device(backends, shape, kernel, stride, pad):
@@ -213,12 +231,12 @@ def test_pool_relu_gradient_node_on_device(backends, shape, kernel, stride, pad)
 def test_exact_graph_rewrites_keep_the_device_bits(backends, model):
     """On the device, the graph rewrites that compute the same arithmetic
     (constant folding, weight gradients in the weight's layout, fused
-    add+relu, conv+bias+relu and pool+relu gradients) leave every loss and parameter of
+    add+relu, conv+bias+relu, pool+relu gradients and Linear bias epilogues) leave every loss and parameter of
     SGD-momentum training bit for bit unchanged: config 1's MLP for 10 steps,
     config 5's CNN at batch 128 for 3 steps."""
     dev, _ = backends
     rewrites = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU", "FUSED_CONV_EPILOGUE",
-                "FUSED_POOL_RELU_GRAD")
+                "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS")
     if model == "mlp":
         fn, batches = mlp_model, mlp_batches(10)
     else:

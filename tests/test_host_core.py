@@ -12,6 +12,7 @@ import torch
 from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads,
                       config5_batches, config5_model, conv_relu_loss_and_grads, mlp_batches, mlp_model,
                       train_with_rewrites, POOL_GEOMETRIES, pool_relu_input, relu_pool_loss_and_grad,
+                      LINEAR_SHAPES, linear_loss_and_grads,
                       relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
@@ -206,6 +207,21 @@ def test_graph_rewrites_keep_the_oracle_bits(cpu, model):
     assert on[0].tobytes() == off[0].tobytes()
     for a, b in zip(on[1], off[1]):
         assert a.tobytes() == b.tobytes()
+
+
+@pytest.mark.parametrize("relu", [False, True])
+@pytest.mark.parametrize("rows,fan_in,fan_out", LINEAR_SHAPES[:2] + LINEAR_SHAPES[-1:])
+def test_linear_bias_node_is_the_three_nodes(cpu, rows, fan_in, fan_out, relu):
+    """x @ w.T + bias (then relu) as one MATMUL_BIAS node gives the MATMUL +
+    ADD (+ RELU) graph's output and gradients bit for bit on the oracle."""
+    rng = np.random.default_rng(SEED + 15)
+    x = rng.uniform(-1, 1, (rows, fan_in)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, (fan_out, fan_in)).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, fan_out).astype(np.float32)
+    fused = linear_loss_and_grads(cpu, x, w, bias, relu, True)
+    graph = linear_loss_and_grads(cpu, x, w, bias, relu, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
 
 
 @pytest.mark.parametrize("shape,kernel,stride,pad", POOL_GEOMETRIES)

@@ -83,8 +83,16 @@ struct FixedScratch {
     float* ptr;
     size_t bytes;
 };
+// A product's column epilogue: out[.., col] = relu?(out + bias[col * bias_stride]),
+// the values of the ADD of a bias broadcast over rows and the RELU after it.
+struct GemmEpilogue {
+    const float* bias;
+    int64_t bias_stride;
+    bool relu;
+};
 int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd, float* c,
-         const vkhip_gemm_opts* opts, const FixedScratch* scratch = nullptr);
+         const vkhip_gemm_opts* opts, const FixedScratch* scratch = nullptr,
+         const GemmEpilogue* epi = nullptr);
 
 // Decision facts and units of work (observe.hip). A unit is a node of
 // vkhip_compute or one per-op entry call; decisions published inside it carry

@@ -1330,10 +1330,20 @@ __device__ __forceinline__ void carry_push(float (&stack)[kSplitLevels], uint32_
 // (Measured on 64 x 65536 partials: 8 groups 3.0 us; 16 groups 4.4 us and 32
 // groups 11.9 us, where group 0's combine grows; 16-byte loads of four
 // outputs per lane 3.75 us.)
+// An epilogue (bias != null) adds bias[(i % ncols) * bias_stride] to the
+// folded value and then applies relu (v <= 0 ? 0 : v) when asked: the ADD and
+// RELU nodes' arithmetic on the product's output.
+struct FoldEpilogue {
+    const float* bias;
+    int64_t bias_stride;
+    uint32_t ncols, relu;
+};
+
 template <int G, int C>
 __global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __restrict__ ws,
                                                              float* __restrict__ dst, uint64_t ne,
-                                                             uint32_t splits, uint32_t nchunks) {
+                                                             uint32_t splits, uint32_t nchunks,
+                                                             FoldEpilogue epi) {
     constexpr int kOuts = 256 / G;
     constexpr int kChunkLevel = C >= 64 ? 6 : C >= 32 ? 5 : C >= 16 ? 4 : C >= 8 ? 3 : C >= 4 ? 2 : C >= 2 ? 1 : 0;
     static_assert((1 << kChunkLevel) == C && kChunkLevel < kSplitLevels, "chunk is a power of two");
@@ -1383,7 +1393,21 @@ __global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __rest
 #pragma unroll
     for (int l = 0; l < kSplitLevels; ++l)
         if ((nchunks >> l) & 1u) total = total + chunks[l];
+    if (epi.bias) {
+        total = total + epi.bias[static_cast<int64_t>(i % epi.ncols) * epi.bias_stride];
+        if (epi.relu) total = total <= 0.0f ? 0.0f : total;
+    }
     dst[i] = total;
+}
+
+// The same epilogue over an unsplit product's output, in place.
+__global__ __launch_bounds__(256) void bias_cols_kernel(float* __restrict__ c, uint64_t ne,
+                                                        FoldEpilogue epi) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= ne) return;
+    float v = c[i] + epi.bias[static_cast<int64_t>(i % epi.ncols) * epi.bias_stride];
+    if (epi.relu) v = v <= 0.0f ? 0.0f : v;
+    c[i] = v;
 }
 
 // ---- GEMV -------------------------------------------------------------------
@@ -1694,12 +1718,14 @@ static int launch_conv_tiles(const GemmArgs& g, const Im2colB& im, uint32_t batc
 }
 
 template <int G, int C>
-static void launch_split_k_fold(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
+static void launch_split_k_fold(const float* ws, float* dst, uint64_t ne, uint32_t splits,
+                                const FoldEpilogue& epi) {
     hipLaunchKernelGGL((split_k_reduce_kernel<G, C>), dim3(ceil_div(ne, 256 / G)), dim3(256), 0,
-                       ctx().stream, ws, dst, ne, splits, splits / C);
+                       ctx().stream, ws, dst, ne, splits, splits / C, epi);
 }
 
-int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
+int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits,
+                          const FoldEpilogue& epi) {
     if (ne == 0) return VKHIP_OK;
     if (splits == 0 || splits >= (1u << kSplitLevels))
         return fail(VKHIP_ERR_INVALID, "split-K reduce: %u partitions outside 1..%u", splits,
@@ -1708,22 +1734,38 @@ int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t spl
     // (no idle groups); chunk: the smallest power of two that leaves at most
     // that many groups busy (64 for 511 partitions).
     if (splits <= 2) {
-        launch_split_k_fold<2, 1>(ws, dst, ne, splits);
+        launch_split_k_fold<2, 1>(ws, dst, ne, splits, epi);
     } else if (splits <= 4) {
-        launch_split_k_fold<4, 1>(ws, dst, ne, splits);
+        launch_split_k_fold<4, 1>(ws, dst, ne, splits, epi);
     } else {
         uint32_t chunk = 1;
         while (ceil_div(splits, chunk) > 8) chunk *= 2;
         switch (chunk) {
-            case 1: launch_split_k_fold<8, 1>(ws, dst, ne, splits); break;
-            case 2: launch_split_k_fold<8, 2>(ws, dst, ne, splits); break;
-            case 4: launch_split_k_fold<8, 4>(ws, dst, ne, splits); break;
-            case 8: launch_split_k_fold<8, 8>(ws, dst, ne, splits); break;
-            case 16: launch_split_k_fold<8, 16>(ws, dst, ne, splits); break;
-            case 32: launch_split_k_fold<8, 32>(ws, dst, ne, splits); break;
-            default: launch_split_k_fold<8, 64>(ws, dst, ne, splits); break;
+            case 1: launch_split_k_fold<8, 1>(ws, dst, ne, splits, epi); break;
+            case 2: launch_split_k_fold<8, 2>(ws, dst, ne, splits, epi); break;
+            case 4: launch_split_k_fold<8, 4>(ws, dst, ne, splits, epi); break;
+            case 8: launch_split_k_fold<8, 8>(ws, dst, ne, splits, epi); break;
+            case 16: launch_split_k_fold<8, 16>(ws, dst, ne, splits, epi); break;
+            case 32: launch_split_k_fold<8, 32>(ws, dst, ne, splits, epi); break;
+            default: launch_split_k_fold<8, 64>(ws, dst, ne, splits, epi); break;
         }
     }
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
+    return launch_split_k_reduce(ws, dst, ne, splits, FoldEpilogue{nullptr, 0, 1, 0});
+}
+
+static FoldEpilogue fold_epilogue(const GemmEpilogue* epi, uint32_t ncols) {
+    if (!epi || !epi->bias) return FoldEpilogue{nullptr, 0, 1, 0};
+    return FoldEpilogue{epi->bias, epi->bias_stride, ncols, epi->relu ? 1u : 0u};
+}
+
+static int launch_bias_cols(float* c, uint64_t ne, const FoldEpilogue& epi) {
+    if (ne == 0 || !epi.bias) return VKHIP_OK;
+    hipLaunchKernelGGL(bias_cols_kernel, dim3(ceil_div(ne, 256)), dim3(256), 0, ctx().stream, c, ne, epi);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }
@@ -1907,8 +1949,9 @@ static int exact_img(const vkhip_unfold& p, const float* x, const vkhip_operand&
     return VKHIP_OK;
 }
 
-int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd,
-         float* c, const vkhip_gemm_opts* opts, const FixedScratch* scratch) {
+static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd,
+                     float* c, const vkhip_gemm_opts* opts, const FixedScratch* scratch,
+                     const FoldEpilogue& fe, bool* fused) {
     const uint32_t b0 = ad.ne[0] > bd.ne[0] ? ad.ne[0] : bd.ne[0];
     const uint32_t b1 = ad.ne[1] > bd.ne[1] ? ad.ne[1] : bd.ne[1];
     const uint32_t m = ad.ne[2], k = ad.ne[3], n = bd.ne[3];
@@ -2073,7 +2116,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
             else
                 hipLaunchKernelGGL((gemm_nn_direct_kernel<true, true>), grid, dim3(512), 0, ctx().stream, g);
             VKHIP_LAUNCH_CHECK();
-            if (g.pairs > 1) return launch_split_k_reduce(target, c, out_elems, g.pairs);
+            if (g.pairs > 1) { *fused = true; return launch_split_k_reduce(target, c, out_elems, g.pairs, fe); }
             return VKHIP_OK;
         }
         // 128x64 tiles when the last round of 128x128 workgroups would leave
@@ -2102,7 +2145,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
             else
                 hipLaunchKernelGGL((gemm_nn_direct_kernel<true, false, 64>), grid, dim3(256), 0, ctx().stream, g);
             VKHIP_LAUNCH_CHECK();
-            if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
+            if (splits > 1) { *fused = true; return launch_split_k_reduce(target, c, out_elems, splits, fe); }
             return VKHIP_OK;
         }
         const dim3 grid = dgrid;
@@ -2111,7 +2154,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
         else
             hipLaunchKernelGGL((gemm_nn_direct_kernel<true, false>), grid, dim3(256), 0, ctx().stream, g);
         VKHIP_LAUNCH_CHECK();
-        if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
+        if (splits > 1) { *fused = true; return launch_split_k_reduce(target, c, out_elems, splits, fe); }
         return VKHIP_OK;
     }
     if (tile.bm == 64 && b_rows && (amode == KCD || a_rows)) {
@@ -2121,7 +2164,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
         else
             hipLaunchKernelGGL(gemm_direct64_kernel<true>, grid, dim3(256), 0, ctx().stream, g);
         VKHIP_LAUNCH_CHECK();
-        if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
+        if (splits > 1) { *fused = true; return launch_split_k_reduce(target, c, out_elems, splits, fe); }
         return VKHIP_OK;
     }
     g.flat_splits = 0;  // the register-path kernel takes the partition from blockIdx.y
@@ -2130,8 +2173,20 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     else
         st = launch_tiles<64, 64, 32, 32>(g, static_cast<uint32_t>(batch), splits, amode, bmode);
     if (st != VKHIP_OK) return st;
-    if (splits > 1) return launch_split_k_reduce(target, c, out_elems, splits);
+    if (splits > 1) { *fused = true; return launch_split_k_reduce(target, c, out_elems, splits, fe); }
     return VKHIP_OK;
+}
+
+int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd, float* c,
+         const vkhip_gemm_opts* opts, const FixedScratch* scratch, const GemmEpilogue* epi) {
+    const FoldEpilogue fe = fold_epilogue(epi, bd.ne[3]);
+    bool fused = false;
+    const int st = gemm_core(a, ad, b, bd, c, opts, scratch, fe, &fused);
+    if (st != VKHIP_OK || !fe.bias || fused) return st;
+    // no split (or the GEMV, the exact arm, K == 0): the epilogue as a pass
+    const uint64_t rows = static_cast<uint64_t>(std::max(ad.ne[0], bd.ne[0])) *
+                          std::max(ad.ne[1], bd.ne[1]) * ad.ne[2];
+    return launch_bias_cols(c, rows * bd.ne[3], fe);
 }
 
 // Convolution forward, out[n] = W_flat (Cout x C*kh*kw) @ cols(x[n]) for every

@@ -258,6 +258,10 @@ static int supports_node(const vkhip_node& nd) {
         case VKHIP_OP_MATMUL:
             return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
                    contiguous(o) && nd.src[0].ndim >= 2 && nd.src[1].ndim >= 2;
+        case VKHIP_OP_MATMUL_BIAS:
+            return nd.n_src == 3 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
+                   is_f32(nd.src[2]) && contiguous(o) && nd.src[0].ndim >= 2 && nd.src[1].ndim >= 2 &&
+                   o.ndim >= 2 && nd.src[2].ndim == 1 && nd.src[2].ne[0] == o.ne[o.ndim - 1];
         case VKHIP_OP_SOFTMAX:
         case VKHIP_OP_LOG_SOFTMAX:
             return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && contiguous(o) &&
@@ -380,9 +384,14 @@ static int check_extents(const vkhip_node& nd) {
         if (!fits32(nd.src[s]))
             return fail(VKHIP_ERR_INVALID, "%s: source %d rank or extents out of range", op_name(nd.op), s);
     switch (nd.op) {
-        case VKHIP_OP_MATMUL: {
-            if (nd.n_src != 2 || nd.src[0].ndim < 2 || nd.src[1].ndim < 2 || o.ndim < 2)
+        case VKHIP_OP_MATMUL:
+        case VKHIP_OP_MATMUL_BIAS: {
+            if (nd.n_src != (nd.op == VKHIP_OP_MATMUL ? 2 : 3) || nd.src[0].ndim < 2 ||
+                nd.src[1].ndim < 2 || o.ndim < 2)
                 return fail(VKHIP_ERR_INVALID, "matmul: operands and output need rank >= 2");
+            if (nd.op == VKHIP_OP_MATMUL_BIAS &&
+                (nd.src[2].ndim != 1 || nd.src[2].ne[0] != o.ne[o.ndim - 1]))
+                return fail(VKHIP_ERR_INVALID, "matmul_bias: the bias needs one value per output column");
             const vkhip_operand a = to_operand(nd.src[0]), b = to_operand(nd.src[1]);
             const vkhip_operand c = to_operand(o);
             if (a.ne[3] != b.ne[2])
@@ -490,6 +499,7 @@ static int check_extents(const vkhip_node& nd) {
 static const char* op_name(int op) {
     switch (op) {
         case VKHIP_OP_MATMUL: return "matmul";
+        case VKHIP_OP_MATMUL_BIAS: return "matmul_bias";
         case VKHIP_OP_SOFTMAX: return "softmax";
         case VKHIP_OP_LOG_SOFTMAX: return "log_softmax";
         case VKHIP_OP_IM2COL: return "im2col";
@@ -548,13 +558,21 @@ static int compute_node(const vkhip_node& nd) {
         return fail(VKHIP_ERR_UNSUPPORTED, "vkhip: %s (op %d) is not supported for these dtypes/layout",
                     op_name(nd.op), nd.op);
     switch (nd.op) {
-        case VKHIP_OP_MATMUL: {
+        case VKHIP_OP_MATMUL:
+        case VKHIP_OP_MATMUL_BIAS: {
             const vkhip_operand a = to_operand(nd.src[0]);
             const vkhip_operand b = to_operand(nd.src[1]);
             const vkhip_gemm_opts opts{ctx().node_gemm_kernel, 0};
+            GemmEpilogue epi{nullptr, 0, false};
+            if (nd.op == VKHIP_OP_MATMUL_BIAS) {
+                uint32_t relu;
+                memcpy(&relu, nd.params, sizeof relu);
+                epi = GemmEpilogue{static_cast<const float*>(nd.src[2].data), nd.src[2].nb[0], relu != 0};
+            }
             return gemm(static_cast<const float*>(nd.src[0].data), a,
                         static_cast<const float*>(nd.src[1].data), b,
-                        static_cast<float*>(nd.out.data), &opts);
+                        static_cast<float*>(nd.out.data), &opts, nullptr,
+                        nd.op == VKHIP_OP_MATMUL_BIAS ? &epi : nullptr);
         }
         case VKHIP_OP_SUM:
         case VKHIP_OP_MEAN:

@@ -457,6 +457,23 @@ FOLD_CONSTANTS = True
 WEIGHT_GRAD_IN_PLACE_LAYOUT = True
 
 
+def _matmul_backward(a: "Node", b: "Node", grad: "Tensor", grads: dict) -> None:
+    """The MATMUL rule: d(a) = grad @ b^T, d(b) = a^T @ grad (reference
+    autograd.cpp), d(b) taken in w's layout when b is a Linear weight's w.T."""
+    if a.requires_grad:
+        _accumulate(grads, a, matmul(grad, Tensor(b).transpose(-2, -1)))
+    if b.requires_grad:
+        w = _transposed_matrix_source(b) if WEIGHT_GRAD_IN_PLACE_LAYOUT else None
+        if w is not None:
+            # b = w^T (x @ w.T, a Linear layer): d(w) = grad^T @ a is the
+            # transpose of d(w^T) = a^T @ grad -- the same products summed
+            # in the same k order under a plan symmetric in M and N -- in
+            # w's own layout, so no transposing copy follows.
+            _accumulate(grads, w, matmul(grad.transpose(-2, -1), Tensor(a)).reshape(w.shape))
+        else:
+            _accumulate(grads, b, matmul(Tensor(a).transpose(-2, -1), grad))
+
+
 def _transposed_matrix_source(b: "Node"):
     """w when node b is the view w.T of a 2-D w that requires grad, or the
     matmul lowering's rank-4 broadcast of that view (leading axes of 1), else
@@ -493,7 +510,46 @@ def _scalar_like(peer: Tensor, value) -> Tensor:
     return full((), float(value), peer.dtype, peer.node.backend)
 
 
+# A Linear layer's matmul(x, w.T) + bias (and the ReLU after it) as one
+# MATMUL_BIAS node: the bias add (and relu) applied where the product's split-K
+# partials are folded, the values of the MATMUL, ADD and RELU nodes. False
+# builds those nodes.
+FUSED_LINEAR_BIAS = True
+
+
+def _matmul_bias(a: Tensor, b: Tensor, relu: bool):
+    """matmul(...) + b as one MATMUL_BIAS node when a is the (reshaped) output
+    of a not yet computed MATMUL and b a float32 vector with one value per
+    output column; relu=True instead turns such a node (a, as the reshape of a
+    MATMUL_BIAS without relu) into one with it. Else None. The replaced nodes
+    stay in the graph, computed only if something else needs them."""
+    if not FUSED_LINEAR_BIAS or a.dtype != np.float32:
+        return None
+    v = a.node
+    if v.op != RESHAPE or v.view_src is None or v.view_src.computed:
+        return None
+    mm = v.view_src
+    if relu:
+        if mm.op != OP["MATMUL_BIAS"] or mm.aux:
+            return None
+        srcs = list(mm.src)
+    else:
+        if (mm.op != OP["MATMUL"] or not isinstance(b, Tensor) or b.ndim != 1 or b.dtype != np.float32
+                or b.shape[0] != mm.shape[-1] or a.shape[-1] != b.shape[0]):
+            return None
+        srcs = [mm.src[0], mm.src[1], b.node]
+    node = Node(OP["MATMUL_BIAS"], mm.shape, np.float32, mm.backend, srcs,
+                params=_params(("I", 1 if relu else 0)),
+                requires_grad=_grad_enabled and any(s.requires_grad for s in srcs))
+    node.aux = bool(relu)
+    return Tensor(node).reshape(a.shape)
+
+
 def _binary(op, a: Tensor, b, out_dtype=None, params=b"") -> Tensor:
+    if op == OP["ADD"] and FUSED_LINEAR_BIAS:
+        fused = _matmul_bias(a, b, False)
+        if fused is not None:
+            return fused
     b = _scalar_like(a, b)
     dims = broadcast_dims(a.shape, b.shape)
     ba = a if a.shape == dims else a.broadcast_to(dims)
@@ -532,6 +588,10 @@ def log(a): return _unary(OP["LOG"], a)
 def relu(a):
     if FUSED_CONV_EPILOGUE:
         fused = _conv_bias_relu(a)
+        if fused is not None:
+            return fused
+    if FUSED_LINEAR_BIAS:
+        fused = _matmul_bias(a, None, True)
         if fused is not None:
             return fused
     if FUSED_ADD_RELU and a.node.op == OP["ADD"] and a.dtype == np.float32 and len(a.node.src) == 2:
@@ -1001,7 +1061,12 @@ class CapturedStep:
                                                ctypes.byref(has_graph)), "program_info")
         return {"calls": calls.value, "nodes": nodes.value, "graph": bool(has_graph.value)}
 
-    def __call__(self, *arrays) -> list:
+    def __call__(self, *arrays, read: bool = True):
+        """Uploads `arrays`, replays the step and returns `fn`'s outputs as
+        host arrays. read=False returns None without waiting for the device:
+        the next call's uploads are stream-ordered after this replay (their
+        pinned staging slots are reused only once their copies are done), so
+        steps queue back to back; `outputs()` reads the latest step's."""
         if self._program is None:
             raise RuntimeError("CapturedStep: closed")
         if len(arrays) != len(self.inputs):
@@ -1013,6 +1078,10 @@ class CapturedStep:
             host = a.view(np.uint8) if a.dtype == np.bool_ else a
             self.backend.upload(t.node.storage, t.node.offset * t.node.itemsize, host)
         _lib.check(self.lib.vkhip_program_run(self._program, 1 if self.graph else 0), "program_run")
+        return self.outputs_now() if read else None
+
+    def outputs_now(self) -> list:
+        """`fn`'s outputs of the latest replay, as host arrays (waits for it)."""
         return [t.numpy() for t in self.outputs]
 
     def close(self) -> None:
@@ -1228,18 +1297,17 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         total = sum(grad, [node.aux], keepdim=True)
         _accumulate(grads, a, sub(grad, exp(out) * total.broadcast_to(a.shape)))
     elif op == OP["MATMUL"]:
-        if a.requires_grad:
-            _accumulate(grads, a, matmul(grad, tb().transpose(-2, -1)))
-        if b.requires_grad:
-            w = _transposed_matrix_source(b) if WEIGHT_GRAD_IN_PLACE_LAYOUT else None
-            if w is not None:
-                # b = w^T (x @ w.T, a Linear layer): d(w) = grad^T @ a is the
-                # transpose of d(w^T) = a^T @ grad -- the same products summed
-                # in the same k order under a plan symmetric in M and N -- in
-                # w's own layout, so no transposing copy follows.
-                _accumulate(grads, w, matmul(grad.transpose(-2, -1), ta()).reshape(w.shape))
-            else:
-                _accumulate(grads, b, matmul(ta().transpose(-2, -1), grad))
+        _matmul_backward(a, b, grad, grads)
+    elif op == OP["MATMUL_BIAS"]:
+        # the RELU rule (the mask from the output, as for CONV2D_BIAS_RELU)
+        # when the node has one, the ADD/BROADCAST rules for the bias (the sum
+        # over rows), then the MATMUL rule with that gradient
+        g = grad if grad.shape == out.shape else grad.broadcast_to(out.shape)
+        dz = _relu_grad(node, node, g) if node.aux else g
+        bias = node.src[2]
+        if bias.requires_grad:
+            _accumulate(grads, bias, reduce_to_shape(dz.reshape((-1, bias.shape[0])), bias.shape))
+        _matmul_backward(a, b, dz, grads)
     elif op == OP["ADD_RELU"]:
         # the RELU rule (the mask from the output, as for CONV2D_BIAS_RELU)
         # then the ADD rule: the same gradient to both sources
