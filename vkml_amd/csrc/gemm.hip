@@ -2715,19 +2715,18 @@ int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float*
 // The flipped, transposed weight of the input gradient's convolution:
 // wt[c][o*kk + (kk - 1 - r)] = w[o][c*kk + r] (kk = kh*kw window elements,
 // r = ki*kw + kj, so kk - 1 - r is the window rotated by 180 degrees).
+// One thread per element of wt (fewer than 2^32, checked by the host), the
+// index split by multiply-high divisions.
 __global__ void conv_weight_flip_kernel(const float* __restrict__ w, int64_t s_out,
-                                        float* __restrict__ wt, uint32_t channels, uint32_t cout,
-                                        uint32_t kk) {
-    const uint64_t total = static_cast<uint64_t>(channels) * cout * kk;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-        const uint64_t row = static_cast<uint64_t>(cout) * kk;
-        const uint32_t c = static_cast<uint32_t>(i / row);
-        const uint32_t rest = static_cast<uint32_t>(i - c * row);
-        const uint32_t o = rest / kk;
-        const uint32_t r = kk - 1 - (rest - o * kk);
-        wt[i] = w[static_cast<int64_t>(o) * s_out + static_cast<int64_t>(c) * kk + r];
-    }
+                                        float* __restrict__ wt, uint32_t total, FastDiv div_row,
+                                        FastDiv div_kk) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= total) return;
+    const uint32_t c = div_row.div(i);
+    const uint32_t rest = i - c * div_row.d;
+    const uint32_t o = div_kk.div(rest);
+    const uint32_t r = div_kk.d - 1 - (rest - o * div_kk.d);
+    wt[i] = w[static_cast<int64_t>(o) * s_out + static_cast<int64_t>(c) * div_kk.d + r];
 }
 
 // Input gradient of conv2d (forward geometry p, weight rows [Cout, C*kh*kw]
@@ -2783,9 +2782,12 @@ int conv2d_input_grad(const float* gr, const vkhip_operand& gd, const float* w, 
         float* wt = nullptr;
         int st = node_temporary(wt_elems * sizeof(float), &wt);
         if (st != VKHIP_OK) return st;
-        const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((wt_elems + 255) / 256, 4096));
-        hipLaunchKernelGGL(conv_weight_flip_kernel, dim3(blocks), dim3(256), 0, ctx().stream, w, w_row,
-                           wt, channels, cout, kk);
+        if (wt_elems >= (uint64_t{1} << 32))
+            return fail(VKHIP_ERR_UNSUPPORTED, "conv2d input grad: %llu weight elements",
+                        static_cast<unsigned long long>(wt_elems));
+        hipLaunchKernelGGL(conv_weight_flip_kernel, dim3(ceil_div(wt_elems, 256)), dim3(256), 0,
+                           ctx().stream, w, w_row, wt, static_cast<uint32_t>(wt_elems),
+                           FastDiv(cout * kk), FastDiv(kk));
         VKHIP_LAUNCH_CHECK();
         vkhip_unfold q = p;
         q.stride_h = 1;
