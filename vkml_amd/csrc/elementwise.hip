@@ -577,25 +577,54 @@ struct SgdBatch {
     int32_t nesterov;
 };
 
+// One parameter element's update (torch.optim.SGD's order of operations).
+__device__ __forceinline__ void sgd_update(float& p, float g, float& v, bool first, const SgdBatch& b) {
+    if (b.weight_decay != 0.0f) g = __fadd_rn(g, __fmul_rn(p, b.weight_decay));
+    float dir = g;
+    if (b.momentum != 0.0f) {
+        v = first ? g : __fadd_rn(__fmul_rn(v, b.momentum), g);
+        dir = b.nesterov ? __fadd_rn(g, __fmul_rn(v, b.momentum)) : v;
+    }
+    p = __fadd_rn(p, __fmul_rn(dir, -b.lr));
+}
+
+// Four consecutive elements per thread: one 16-byte load and store per
+// buffer when the parameter's buffers are 16-byte aligned and the four are
+// in range, else element by element.
 __global__ __launch_bounds__(256) void sgd_step_kernel(SgdBatch b) {
     int i = 0;
     while (i + 1 < b.count && blockIdx.x >= b.block_start[i + 1]) ++i;
     const vkhip_sgd_param& q = b.p[i];
     const uint64_t base = (static_cast<uint64_t>(blockIdx.x - b.block_start[i]) * 256 + threadIdx.x) * 4;
+    if (base >= q.n) return;
+    const bool mom = b.momentum != 0.0f;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(q.param) | reinterpret_cast<uintptr_t>(q.grad) |
+                           (mom ? reinterpret_cast<uintptr_t>(q.velocity) : 0)) & 15) == 0;
+    if (aligned && base + 4 <= q.n) {
+        f32x4_t p = *reinterpret_cast<const f32x4_t*>(q.param + base);
+        const f32x4_t g = *reinterpret_cast<const f32x4_t*>(q.grad + base);
+        f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (mom && !q.first) v = *reinterpret_cast<const f32x4_t*>(q.velocity + base);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float pj = p[j], vj = v[j];
+            sgd_update(pj, g[j], vj, q.first, b);
+            p[j] = pj;
+            v[j] = vj;
+        }
+        if (mom) *reinterpret_cast<f32x4_t*>(q.velocity + base) = v;
+        *reinterpret_cast<f32x4_t*>(q.param + base) = p;
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint64_t e = base + j;
         if (e >= q.n) return;
-        const float p = q.param[e];
-        float g = q.grad[e];
-        if (b.weight_decay != 0.0f) g = __fadd_rn(g, __fmul_rn(p, b.weight_decay));
-        float dir = g;
-        if (b.momentum != 0.0f) {
-            const float v = q.first ? g : __fadd_rn(__fmul_rn(q.velocity[e], b.momentum), g);
-            q.velocity[e] = v;
-            dir = b.nesterov ? __fadd_rn(g, __fmul_rn(v, b.momentum)) : v;
-        }
-        q.param[e] = __fadd_rn(p, __fmul_rn(dir, -b.lr));
+        float p = q.param[e];
+        float v = mom && !q.first ? q.velocity[e] : 0.0f;
+        sgd_update(p, q.grad[e], v, q.first, b);
+        if (mom) q.velocity[e] = v;
+        q.param[e] = p;
     }
 }
 
