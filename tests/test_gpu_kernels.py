@@ -109,6 +109,7 @@ LAYOUT_SHAPES = [  # (batch, m, n, k): 128x128 tiles, split-K, ragged edges, M o
     (1, 1022, 1024, 64),    # 64x64 tiles, M not 4-aligned (TN through registers)
     (1, 384, 256, 24000),   # paired partitions (84), two per direct workgroup
     (1, 256, 384, 30000),   # paired partitions, odd count (79): the last pair is one
+    (3, 128, 256, 40000),   # paired partitions over a batch (84 per tile)
 ]
 
 

@@ -1949,6 +1949,12 @@ static int exact_img(const vkhip_unfold& p, const float* x, const vkhip_operand&
     return VKHIP_OK;
 }
 
+// How full a launch's rounds keep the machine: workgroups / (rounds * slots),
+// slots = the workgroups resident at once.
+static double round_fill(uint64_t wgs, uint64_t slots) {
+    return static_cast<double>(wgs) / static_cast<double>((wgs + slots - 1) / slots * slots);
+}
+
 static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd,
                      float* c, const vkhip_gemm_opts* opts, const FixedScratch* scratch,
                      const FoldEpilogue& fe, bool* fused) {
@@ -2131,10 +2137,7 @@ static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, co
         const uint64_t cus = ctx().ready ? static_cast<uint64_t>(ctx().caps.compute_units) : 256u;
         const uint64_t w128 = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits * batch;
         const uint64_t w64 = static_cast<uint64_t>(g.tiles_m) * ceil_div(n, 64) * splits * batch;
-        auto fill = [](uint64_t wgs, uint64_t slots) {
-            return static_cast<double>(wgs) / static_cast<double>((wgs + slots - 1) / slots * slots);
-        };
-        if (0.94 * fill(w64, 3 * cus) > fill(w128, 2 * cus)) {
+        if (0.94 * round_fill(w64, 3 * cus) > round_fill(w128, 2 * cus)) {
             g.tiles_n = ceil_div(n, 64);
             const uint64_t f64 = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
             g.flat_splits = (splits > 1 && f64 <= 0x7fffffffull) ? splits : 0;
@@ -2457,7 +2460,19 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
                        ((static_cast<int64_t>(m) - 1) * g.sam + k) * 4 < (int64_t{1} << 31);
     const int amode = a_kcd ? KCD : (g.a_vec ? KCV : KCS);
     int st;
-    if (tile.bm == 128)
+    // 128x64 tiles when their rounds fill the machine better (two workgroups
+    // per CU either way: 70 and 55 KB of LDS; 0.94 for the narrower tile's
+    // work per CU-second, as for the GEMM): the CIFAR conv2 layer's 256 tiles
+    // of 128x128 give each CU one workgroup, 512 of 128x64 two (0.0556 ->
+    // 0.0493 ms); [128,64,32,32] -> 128 keeps 128x128 (0.172 against 0.190).
+    // Tile width never changes the bits.
+    const uint64_t cus = ctx().ready ? static_cast<uint64_t>(ctx().caps.compute_units) : 256u;
+    const uint64_t w128 = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits * batch;
+    const uint64_t w64 = static_cast<uint64_t>(g.tiles_m) * ceil_div(n, 64) * splits * batch;
+    if (tile.bm == 128 && 0.94 * round_fill(w64, 2 * cus) > round_fill(w128, 2 * cus)) {
+        g.tiles_n = ceil_div(n, 64);
+        st = launch_conv_tiles<128, 64, 64, 32, IMG>(g, im, static_cast<uint32_t>(batch), splits, amode);
+    } else if (tile.bm == 128)
         st = launch_conv_tiles<128, 128, 64, 64, IMG>(g, im, static_cast<uint32_t>(batch), splits, amode);
     else
         st = launch_conv_tiles<64, 64, 32, 32, IMG>(g, im, static_cast<uint32_t>(batch), splits, amode);
