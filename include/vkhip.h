@@ -187,7 +187,13 @@ enum vkhip_op {
      * the MATMUL, ADD (bias broadcast over rows) and RELU nodes it replaces,
      * the epilogue applied where the split-K partials are folded (or in a
      * pass after an unsplit product). */
-    VKHIP_OP_MATMUL_BIAS = 106
+    VKHIP_OP_MATMUL_BIAS = 106,
+    /* MATMUL followed by the RELU_BACKWARD it feeds: src0, src1 as MATMUL,
+     * src2 x with the output's extents (contiguous; the relu's input or
+     * output) -> out = x <= 0 ? +0 : src0 @ src1 (a NaN x passes the product):
+     * the two nodes' values, the select applied where the split-K partials
+     * are folded (or in a pass after an unsplit product). */
+    VKHIP_OP_MATMUL_RELU_BACKWARD = 107
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */

@@ -656,6 +656,15 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 }
                 break;
             }
+            case VKHIP_OP_MATMUL_RELU_BACKWARD: {
+                /* MATMUL, then RELU_BACKWARD(x = src2 (contiguous), g = product) */
+                or_matmul((const float*)nd->src[0].data, &s0, (const float*)nd->src[1].data, &s1, (float*)o->data, threads);
+                const float* x = (const float*)nd->src[2].data;
+                float* out = (float*)o->data;
+                for (int64_t i = 0; i < n; ++i)
+                    if (compare_f(VKHIP_OP_LESS_EQUAL, x[i], 0.0f)) out[i] = 0.0f;
+                break;
+            }
             case VKHIP_OP_SOFTMAX: case VKHIP_OP_LOG_SOFTMAX: {
                 int32_t axis;
                 memcpy(&axis, nd->params, sizeof axis);

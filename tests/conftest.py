@@ -193,6 +193,43 @@ def linear_loss_and_grads(backend, x, w, bias, relu, fused):
         T.FUSED_LINEAR_BIAS = prev
 
 
+def mlp2_loss_and_grads(backend, x, w1, b1, w2, fused):
+    """sum((relu(x @ w1.T + b1) @ w2.T) * probe) and the gradients of x, w1,
+    b1 and w2, with the hidden relu's gradient built as one
+    MATMUL_RELU_BACKWARD node over the second layer's input-gradient product
+    (fused) or as MATMUL then RELU_BACKWARD."""
+    from vkml_amd import tensor as T
+
+    prev = T.FUSED_MATMUL_RELU_GRAD
+    T.FUSED_MATMUL_RELU_GRAD = fused
+    try:
+        xt = T.tensor(x, requires_grad=True, backend=backend)
+        w1t = T.tensor(w1, requires_grad=True, backend=backend)
+        b1t = T.tensor(b1, requires_grad=True, backend=backend)
+        w2t = T.tensor(w2, requires_grad=True, backend=backend)
+        h = T.relu(T.matmul(xt, w1t.transpose(-2, -1)) + b1t)
+        out = T.matmul(h, w2t.transpose(-2, -1))
+        probe = np.linspace(-1.0, 1.0, int(np.prod(out.shape)), dtype=np.float32)
+        loss = T.sum(out * T.tensor(probe.reshape(out.shape), backend=backend))
+        loss.backward()
+        # the bias gradient sums the relu gradient: find that node below it
+        ops, n = [], b1t.grad.node
+        for _ in range(6):
+            ops.append(n.op)
+            n = n.view_src if n.view_src is not None else (n.src[0] if n.src else None)
+            if n is None:
+                break
+        want = T.OP["MATMUL_RELU_BACKWARD"] if fused else T.OP["RELU_BACKWARD"]
+        assert want in ops, ops
+        return out.numpy(), xt.grad.numpy(), w1t.grad.numpy(), b1t.grad.numpy(), w2t.grad.numpy()
+    finally:
+        T.FUSED_MATMUL_RELU_GRAD = prev
+
+
+# (rows, in, hidden, out): the hidden layer's input-gradient product split or not
+MLP2_SHAPES = [(64, 784, 128, 10), (128, 8192, 256, 100), (5, 7, 9, 3)]
+
+
 # (rows, in, out): split-K folds (the epilogue in the fold) and unsplit products
 LINEAR_SHAPES = [(64, 784, 128), (64, 128, 10), (128, 8192, 256), (128, 256, 100), (512, 64, 4096),
                  (3, 5, 7)]
@@ -212,7 +249,7 @@ def pool_relu_input(shape, seed):
 
 GRAPH_REWRITES = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU",
                   "FUSED_CONV_EPILOGUE", "FUSED_CONV_INPUT_GRAD", "FOLD_CONV_WEIGHT_GRAD",
-                  "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS")
+                  "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD")
 
 
 def train_with_rewrites(backend, model_fn, batches, enabled, lr=0.1, momentum=0.9,

@@ -16,7 +16,8 @@ from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad,
                       config5_batches, config5_golden_losses, config5_model, config5_train, conv_loss_and_grads,
                       conv_relu_loss_and_grads, gemm_tolerance, mlp_batches, mlp_model, train_with_rewrites,
                       normwise_rel_err, relu_grad, relu_inputs, POOL_GEOMETRIES, pool_relu_input,
-                      relu_pool_loss_and_grad, LINEAR_SHAPES, linear_loss_and_grads)
+                      relu_pool_loss_and_grad, LINEAR_SHAPES, linear_loss_and_grads, MLP2_SHAPES,
+                      mlp2_loss_and_grads)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -192,6 +193,24 @@ def test_conv_bias_relu_node_on_device_is_the_three_nodes(backends, shape, cout,
         assert got.tobytes() == want.tobytes()
 
 
+@pytest.mark.parametrize("rows,fan_in,hidden,fan_out", MLP2_SHAPES)
+def test_matmul_relu_gradient_node_on_device(backends, rows, fan_in, hidden, fan_out):
+    """On the device, the hidden relu's gradient as one MATMUL_RELU_BACKWARD
+    node (the select in the split-K fold or a pass after an unsplit product)
+    gives the device's MATMUL + RELU_BACKWARD graph bit for bit."""
+    dev, _ = backends
+    rng = np.random.default_rng(SEED + 18)
+    x = rng.uniform(-1, 1, (rows, fan_in)).astype(np.float32)
+    w1 = rng.uniform(-0.5, 0.5, (hidden, fan_in)).astype(np.float32)
+    b1 = rng.uniform(-0.5, 0.5, hidden).astype(np.float32)
+    w2 = rng.uniform(-0.5, 0.5, (fan_out, hidden)).astype(np.float32)
+    print(f"matmul_relu_grad {rows}x{fan_in}->{hidden}->{fan_out}", flush=True)
+    fused = mlp2_loss_and_grads(dev, x, w1, b1, w2, True)
+    graph = mlp2_loss_and_grads(dev, x, w1, b1, w2, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
+
+
 @pytest.mark.parametrize("relu", [False, True])
 @pytest.mark.parametrize("rows,fan_in,fan_out", LINEAR_SHAPES)
 def test_linear_bias_node_on_device(backends, rows, fan_in, fan_out, relu):
@@ -236,7 +255,7 @@ def test_exact_graph_rewrites_keep_the_device_bits(backends, model):
     config 5's CNN at batch 128 for 3 steps."""
     dev, _ = backends
     rewrites = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU", "FUSED_CONV_EPILOGUE",
-                "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS")
+                "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD")
     if model == "mlp":
         fn, batches = mlp_model, mlp_batches(10)
     else:

@@ -12,7 +12,7 @@ import torch
 from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_loss_and_grads,
                       config5_batches, config5_model, conv_relu_loss_and_grads, mlp_batches, mlp_model,
                       train_with_rewrites, POOL_GEOMETRIES, pool_relu_input, relu_pool_loss_and_grad,
-                      LINEAR_SHAPES, linear_loss_and_grads,
+                      LINEAR_SHAPES, linear_loss_and_grads, MLP2_SHAPES, mlp2_loss_and_grads,
                       relu_grad, relu_inputs)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
@@ -207,6 +207,22 @@ def test_graph_rewrites_keep_the_oracle_bits(cpu, model):
     assert on[0].tobytes() == off[0].tobytes()
     for a, b in zip(on[1], off[1]):
         assert a.tobytes() == b.tobytes()
+
+
+@pytest.mark.parametrize("rows,fan_in,hidden,fan_out", [MLP2_SHAPES[0], MLP2_SHAPES[-1]])
+def test_matmul_relu_gradient_node_is_the_two_nodes(cpu, rows, fan_in, hidden, fan_out):
+    """The hidden relu's gradient of relu(x @ w1.T + b1) @ w2.T as one
+    MATMUL_RELU_BACKWARD node gives the MATMUL + RELU_BACKWARD graph's bits on
+    the oracle (values, with negatives and zeros in the hidden layer)."""
+    rng = np.random.default_rng(SEED + 17)
+    x = rng.uniform(-1, 1, (rows, fan_in)).astype(np.float32)
+    w1 = rng.uniform(-0.5, 0.5, (hidden, fan_in)).astype(np.float32)
+    b1 = rng.uniform(-0.5, 0.5, hidden).astype(np.float32)
+    w2 = rng.uniform(-0.5, 0.5, (fan_out, hidden)).astype(np.float32)
+    fused = mlp2_loss_and_grads(cpu, x, w1, b1, w2, True)
+    graph = mlp2_loss_and_grads(cpu, x, w1, b1, w2, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
 
 
 @pytest.mark.parametrize("relu", [False, True])

@@ -83,12 +83,15 @@ struct FixedScratch {
     float* ptr;
     size_t bytes;
 };
-// A product's column epilogue: out[.., col] = relu?(out + bias[col * bias_stride]),
-// the values of the ADD of a bias broadcast over rows and the RELU after it.
+// A product's epilogue: out[.., col] = relu?(out + bias[col * bias_stride]),
+// the values of the ADD of a bias broadcast over rows and the RELU after it;
+// or, with mask set (laid out as the output), out = mask <= 0 ? +0 : out, the
+// relu gradient of a relu whose output gradient is the product.
 struct GemmEpilogue {
     const float* bias;
     int64_t bias_stride;
     bool relu;
+    const float* mask = nullptr;
 };
 int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_operand& bd, float* c,
          const vkhip_gemm_opts* opts, const FixedScratch* scratch = nullptr,

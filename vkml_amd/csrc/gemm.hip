@@ -29,6 +29,27 @@ namespace vkhip {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// An epilogue adds bias[(i % ncols) * bias_stride] to the folded value and
+// then applies relu (v <= 0 ? 0 : v) when asked -- the ADD and RELU nodes'
+// arithmetic on the product's output -- or (mask != null) takes the relu
+// gradient mask[i] <= 0 ? +0 : v, mask laid out as the output (RELU_BACKWARD
+// with the product as its incoming gradient; a NaN mask passes v).
+struct FoldEpilogue {
+    const float* bias;
+    int64_t bias_stride;
+    uint32_t ncols, relu;
+    const float* mask;
+};
+
+__device__ __forceinline__ float apply_epilogue(const FoldEpilogue& epi, uint64_t i, float v) {
+    if (epi.bias) {
+        v = v + epi.bias[static_cast<int64_t>(i % epi.ncols) * epi.bias_stride];
+        if (epi.relu) v = v <= 0.0f ? 0.0f : v;
+    }
+    if (epi.mask && epi.mask[i] <= 0.0f) v = 0.0f;
+    return v;
+}
+
 struct GemmArgs {
     const float* a;
     const float* b;
@@ -50,7 +71,17 @@ struct GemmArgs {
     const float* bias;
     int64_t bias_stride;
     uint32_t relu;
+    // A product's epilogue (MATMUL_BIAS, MATMUL_RELU_BACKWARD) applied by the
+    // kernel that writes the output (unsplit plans; split plans: the fold).
+    FoldEpilogue epi;
 };
+
+// The product epilogue at output (z, row, col), when the launch has one.
+__device__ __forceinline__ float product_epilogue(const GemmArgs& g, uint32_t z, uint32_t row,
+                                                  uint32_t col, float v) {
+    if (!g.epi.bias && !g.epi.mask) return v;
+    return apply_epilogue(g.epi, (static_cast<uint64_t>(z) * g.m + row) * g.n + col, v);
+}
 
 // Output tile (tm, tn) and K partition of this workgroup.
 //  - Unsplit grids (blockIdx.x = tile): the hardware deals workgroups to the
@@ -738,7 +769,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
                     if (g.bias) v = v + g.bias[static_cast<int64_t>(row < g.m ? row : 0) * g.bias_stride];
                     if (g.relu) v = v <= 0.0f ? 0.0f : v;
                 }
-                if (row < g.m && col < g.n) cbase[static_cast<uint64_t>(row) * g.n + col] = v;
+                if (row < g.m && col < g.n)
+                    cbase[static_cast<uint64_t>(row) * g.n + col] = product_epilogue(g, z, row, col, v);
             }
         }
 }
@@ -951,7 +983,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
             if (row < g.m) {
                 BV v;
 #pragma unroll
-                for (int s = 0; s < NS; ++s) v[s] = acc[s][r];
+                for (int s = 0; s < NS; ++s) v[s] = product_epilogue(g, z, row, col + s, acc[s][r]);
                 *reinterpret_cast<BV*>(cbase + static_cast<uint64_t>(row) * g.n + col) = v;
             }
         }
@@ -1286,7 +1318,7 @@ __global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
-            if (row < g.m) cbase[static_cast<uint64_t>(row) * g.n + col] = acc[r];
+            if (row < g.m) cbase[static_cast<uint64_t>(row) * g.n + col] = product_epilogue(g, z, row, col, acc[r]);
         }
     }
 }
@@ -1330,15 +1362,6 @@ __device__ __forceinline__ void carry_push(float (&stack)[kSplitLevels], uint32_
 // (Measured on 64 x 65536 partials: 8 groups 3.0 us; 16 groups 4.4 us and 32
 // groups 11.9 us, where group 0's combine grows; 16-byte loads of four
 // outputs per lane 3.75 us.)
-// An epilogue (bias != null) adds bias[(i % ncols) * bias_stride] to the
-// folded value and then applies relu (v <= 0 ? 0 : v) when asked: the ADD and
-// RELU nodes' arithmetic on the product's output.
-struct FoldEpilogue {
-    const float* bias;
-    int64_t bias_stride;
-    uint32_t ncols, relu;
-};
-
 template <int G, int C>
 __global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __restrict__ ws,
                                                              float* __restrict__ dst, uint64_t ne,
@@ -1393,11 +1416,7 @@ __global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __rest
 #pragma unroll
     for (int l = 0; l < kSplitLevels; ++l)
         if ((nchunks >> l) & 1u) total = total + chunks[l];
-    if (epi.bias) {
-        total = total + epi.bias[static_cast<int64_t>(i % epi.ncols) * epi.bias_stride];
-        if (epi.relu) total = total <= 0.0f ? 0.0f : total;
-    }
-    dst[i] = total;
+    dst[i] = apply_epilogue(epi, i, total);
 }
 
 // The same epilogue over an unsplit product's output, in place.
@@ -1405,9 +1424,7 @@ __global__ __launch_bounds__(256) void bias_cols_kernel(float* __restrict__ c, u
                                                         FoldEpilogue epi) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= ne) return;
-    float v = c[i] + epi.bias[static_cast<int64_t>(i % epi.ncols) * epi.bias_stride];
-    if (epi.relu) v = v <= 0.0f ? 0.0f : v;
-    c[i] = v;
+    c[i] = apply_epilogue(epi, i, c[i]);
 }
 
 // ---- GEMV -------------------------------------------------------------------
@@ -1755,16 +1772,16 @@ int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t spl
 }
 
 int launch_split_k_reduce(const float* ws, float* dst, uint64_t ne, uint32_t splits) {
-    return launch_split_k_reduce(ws, dst, ne, splits, FoldEpilogue{nullptr, 0, 1, 0});
+    return launch_split_k_reduce(ws, dst, ne, splits, FoldEpilogue{nullptr, 0, 1, 0, nullptr});
 }
 
 static FoldEpilogue fold_epilogue(const GemmEpilogue* epi, uint32_t ncols) {
-    if (!epi || !epi->bias) return FoldEpilogue{nullptr, 0, 1, 0};
-    return FoldEpilogue{epi->bias, epi->bias_stride, ncols, epi->relu ? 1u : 0u};
+    if (!epi || (!epi->bias && !epi->mask)) return FoldEpilogue{nullptr, 0, 1, 0, nullptr};
+    return FoldEpilogue{epi->bias, epi->bias_stride, ncols, epi->relu ? 1u : 0u, epi->mask};
 }
 
 static int launch_bias_cols(float* c, uint64_t ne, const FoldEpilogue& epi) {
-    if (ne == 0 || !epi.bias) return VKHIP_OK;
+    if (ne == 0 || (!epi.bias && !epi.mask)) return VKHIP_OK;
     hipLaunchKernelGGL(bias_cols_kernel, dim3(ceil_div(ne, 256)), dim3(256), 0, ctx().stream, c, ne, epi);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
@@ -2099,6 +2116,10 @@ static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, co
         g.split_stride = out_elems;
     }
     g.c = target;
+    if (slices == 1 && (fe.bias || fe.mask)) {  // the kernel writes the output: its epilogue
+        g.epi = fe;
+        *fused = true;
+    }
     // Split direct launches run flat, partitions grouped per XCD (tile_of).
     const uint64_t flat = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
     if (splits > 1 && flat <= 0x7fffffffull) g.flat_splits = splits;
@@ -2185,7 +2206,7 @@ int gemm(const float* a, const vkhip_operand& ad, const float* b, const vkhip_op
     const FoldEpilogue fe = fold_epilogue(epi, bd.ne[3]);
     bool fused = false;
     const int st = gemm_core(a, ad, b, bd, c, opts, scratch, fe, &fused);
-    if (st != VKHIP_OK || !fe.bias || fused) return st;
+    if (st != VKHIP_OK || (!fe.bias && !fe.mask) || fused) return st;
     // no split (or the GEMV, the exact arm, K == 0): the epilogue as a pass
     const uint64_t rows = static_cast<uint64_t>(std::max(ad.ne[0], bd.ne[0])) *
                           std::max(ad.ne[1], bd.ne[1]) * ad.ne[2];

@@ -262,6 +262,15 @@ static int supports_node(const vkhip_node& nd) {
             return nd.n_src == 3 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
                    is_f32(nd.src[2]) && contiguous(o) && nd.src[0].ndim >= 2 && nd.src[1].ndim >= 2 &&
                    o.ndim >= 2 && nd.src[2].ndim == 1 && nd.src[2].ne[0] == o.ne[o.ndim - 1];
+        case VKHIP_OP_MATMUL_RELU_BACKWARD: {
+            if (!(nd.n_src == 3 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
+                  is_f32(nd.src[2]) && contiguous(o) && contiguous(nd.src[2]) && nd.src[0].ndim >= 2 &&
+                  nd.src[1].ndim >= 2 && o.ndim >= 2 && nd.src[2].ndim == o.ndim))
+                return 0;
+            for (int i = 0; i < o.ndim; ++i)
+                if (nd.src[2].ne[i] != o.ne[i]) return 0;
+            return 1;
+        }
         case VKHIP_OP_SOFTMAX:
         case VKHIP_OP_LOG_SOFTMAX:
             return nd.n_src == 1 && is_f32(o) && is_f32(nd.src[0]) && contiguous(o) &&
@@ -385,10 +394,17 @@ static int check_extents(const vkhip_node& nd) {
             return fail(VKHIP_ERR_INVALID, "%s: source %d rank or extents out of range", op_name(nd.op), s);
     switch (nd.op) {
         case VKHIP_OP_MATMUL:
-        case VKHIP_OP_MATMUL_BIAS: {
+        case VKHIP_OP_MATMUL_BIAS:
+        case VKHIP_OP_MATMUL_RELU_BACKWARD: {
             if (nd.n_src != (nd.op == VKHIP_OP_MATMUL ? 2 : 3) || nd.src[0].ndim < 2 ||
                 nd.src[1].ndim < 2 || o.ndim < 2)
                 return fail(VKHIP_ERR_INVALID, "matmul: operands and output need rank >= 2");
+            if (nd.op == VKHIP_OP_MATMUL_RELU_BACKWARD) {
+                bool same = nd.src[2].ndim == o.ndim;
+                for (int i = 0; same && i < o.ndim; ++i) same = nd.src[2].ne[i] == o.ne[i];
+                if (!same)
+                    return fail(VKHIP_ERR_INVALID, "matmul_relu_backward: the mask's extents differ from the output's");
+            }
             if (nd.op == VKHIP_OP_MATMUL_BIAS &&
                 (nd.src[2].ndim != 1 || nd.src[2].ne[0] != o.ne[o.ndim - 1]))
                 return fail(VKHIP_ERR_INVALID, "matmul_bias: the bias needs one value per output column");
@@ -500,6 +516,7 @@ static const char* op_name(int op) {
     switch (op) {
         case VKHIP_OP_MATMUL: return "matmul";
         case VKHIP_OP_MATMUL_BIAS: return "matmul_bias";
+        case VKHIP_OP_MATMUL_RELU_BACKWARD: return "matmul_relu_backward";
         case VKHIP_OP_SOFTMAX: return "softmax";
         case VKHIP_OP_LOG_SOFTMAX: return "log_softmax";
         case VKHIP_OP_IM2COL: return "im2col";
@@ -559,7 +576,8 @@ static int compute_node(const vkhip_node& nd) {
                     op_name(nd.op), nd.op);
     switch (nd.op) {
         case VKHIP_OP_MATMUL:
-        case VKHIP_OP_MATMUL_BIAS: {
+        case VKHIP_OP_MATMUL_BIAS:
+        case VKHIP_OP_MATMUL_RELU_BACKWARD: {
             const vkhip_operand a = to_operand(nd.src[0]);
             const vkhip_operand b = to_operand(nd.src[1]);
             const vkhip_gemm_opts opts{ctx().node_gemm_kernel, 0};
@@ -568,11 +586,13 @@ static int compute_node(const vkhip_node& nd) {
                 uint32_t relu;
                 memcpy(&relu, nd.params, sizeof relu);
                 epi = GemmEpilogue{static_cast<const float*>(nd.src[2].data), nd.src[2].nb[0], relu != 0};
+            } else if (nd.op == VKHIP_OP_MATMUL_RELU_BACKWARD) {
+                epi.mask = static_cast<const float*>(nd.src[2].data);
             }
             return gemm(static_cast<const float*>(nd.src[0].data), a,
                         static_cast<const float*>(nd.src[1].data), b,
                         static_cast<float*>(nd.out.data), &opts, nullptr,
-                        nd.op == VKHIP_OP_MATMUL_BIAS ? &epi : nullptr);
+                        nd.op == VKHIP_OP_MATMUL ? nullptr : &epi);
         }
         case VKHIP_OP_SUM:
         case VKHIP_OP_MEAN:

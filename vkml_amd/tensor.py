@@ -840,18 +840,35 @@ FUSED_RELU_BACKWARD = True
 # pass. False keeps MAX_POOL2D_BACKWARD and RELU_BACKWARD.
 FUSED_POOL_RELU_GRAD = True
 
+# A relu gradient whose incoming gradient is a product (a Linear layer's input
+# gradient, grad @ w, feeding the relu before it) as one MATMUL_RELU_BACKWARD
+# node: the select applied where the product's split-K partials are folded.
+# False keeps MATMUL and RELU_BACKWARD.
+FUSED_MATMUL_RELU_GRAD = True
+
 
 def _relu_grad(mask_src: "Node", y: "Node", g: "Tensor") -> "Tensor":
     """RELU_BACKWARD(mask_src, g), where mask_src is the relu's input or its
     output y (relu(v) <= 0 exactly where v <= 0; a NaN stays NaN, so both
     masks select alike). When g is the not yet computed gradient of a max-pool
     whose input is y, and y feeds nothing else (else g would be a sum), one
-    MAX_POOL2D_BACKWARD_RELU node over the pool gradient's sources instead."""
+    MAX_POOL2D_BACKWARD_RELU node over the pool gradient's sources instead;
+    when g is (a reshape of) a not yet computed product, one
+    MATMUL_RELU_BACKWARD node over its operands."""
     gn = g.node
     if (FUSED_POOL_RELU_GRAD and gn.op == OP["MAX_POOL2D_BACKWARD"] and not gn.computed
             and gn.src[1] is y):
         return Tensor(Node(OP["MAX_POOL2D_BACKWARD_RELU"], gn.shape, np.float32, gn.backend,
                            list(gn.src), params=gn.params))
+    mm = gn
+    while mm.op == RESHAPE and mm.view_src is not None:
+        mm = mm.view_src
+    if (FUSED_MATMUL_RELU_GRAD and mm.op == OP["MATMUL"] and not mm.computed
+            and mask_src.is_contiguous() and _numel(mm.shape) == _numel(mask_src.shape)):
+        mask = Tensor(mask_src).reshape(mm.shape)
+        node = Node(OP["MATMUL_RELU_BACKWARD"], mm.shape, np.float32, mm.backend,
+                    [mm.src[0], mm.src[1], mask.node])
+        return Tensor(node).reshape(g.shape)
     return Tensor(Node(OP["RELU_BACKWARD"], mask_src.shape, np.float32, mask_src.backend,
                        [mask_src, gn]))
 
