@@ -133,6 +133,9 @@ def test_split_k_plan_rules():
     assert plan(1, 128, 784, 16384) == (64, 8)
     # partitions that would drop below 8 K-tiles stay one per workgroup
     assert plan(1, 256, 256, 16384) == (64, 8)
+    # K of 4 K-tiles or fewer is never split (the fold would cost more)
+    assert plan(1, 64, 10, 128)[0] == 1 and plan(1, 128, 256, 100)[0] == 1
+    assert plan(1, 128, 100, 256)[0] > 1
     # more than half a round of tiles (144 at 1536^3): power-of-two chunk
     assert plan(1, 1536, 1536, 1536) == (3, 16)
     # a batched conv GEMM has tiles enough

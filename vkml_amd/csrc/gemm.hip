@@ -1649,6 +1649,11 @@ static void plan_split_k(uint32_t tiles, uint32_t ktiles, uint64_t out_elems, ui
     if (ktiles < 2 || tiles == 0) return;
     uint32_t c = 1;
     if (requested == 0) {
+        // AUTO never splits K of 4 K-tiles or fewer: the fold's launch costs
+        // more than the partitions save (64x10x128 6.3 us unsplit against 6.7
+        // as 2 partitions, 128x256x100 5.8 against 6.7; 8 K-tiles split into 4
+        // still win, 128x100x256 6.7 against 7.9).
+        if (ktiles <= 4) return;
         // AUTO: as many partitions as keep the whole grid in one round of one
         // workgroup per CU (a second, partial round would cost a whole
         // partition's time), with equal chunks of K-tiles: 128x784x16384 (7
