@@ -331,7 +331,7 @@ __global__ __launch_bounds__(256) void col2im_staged_kernel(const float* __restr
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t i = threadIdx.x + 256u * r;
-            if (i < nv) v[r] = s4[i];
+            if (i < nv) v[r] = __builtin_nontemporal_load(s4 + i);
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {

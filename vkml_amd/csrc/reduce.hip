@@ -104,8 +104,14 @@ struct Rows {
 };
 
 // Loads this thread's share of a contiguous row: float4 groups 4*(t + T*i)
-// (vec) or elements t + T*i (scalar), i < E4 (vec) / 4*E4 (scalar).
-template <int T, int E4>
+// (vec) or elements t + T*i (scalar), i < E4 (vec) / 4*E4 (scalar). The
+// 16-byte loads are non-temporal (STREAM) for data each workgroup reads once:
+// a read-only probe over 67 / 134 MB measured 11.0-11.2 / 20.3-20.6 us with
+// them against 11.7 / 22.2 us with ordinary loads. A vector that every
+// workgroup reads again (the GEMV's x) keeps ordinary loads. (Loads issued
+// unconditionally at clamped addresses, then zeroed, measured slower for the
+// softmax rows, 7.6 -> 9.6 us at [4096, 1000], and equal for max.)
+template <int T, int E4, bool STREAM = true>
 __device__ __forceinline__ void load_row(float (&x)[4 * E4], const float* rs, uint32_t n, int t,
                                          bool live, int vec) {
     if (vec) {
@@ -113,7 +119,10 @@ __device__ __forceinline__ void load_row(float (&x)[4 * E4], const float* rs, ui
         for (int i = 0; i < E4; ++i) {
             const uint32_t e0 = 4u * (t + T * i);
             f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (live && e0 < n) v = *reinterpret_cast<const f32x4*>(rs + e0);
+            if (live && e0 < n) {
+                const f32x4* p = reinterpret_cast<const f32x4*>(rs + e0);
+                v = STREAM ? __builtin_nontemporal_load(p) : *p;
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) x[4 * i + j] = v[j];
         }
@@ -124,6 +133,20 @@ __device__ __forceinline__ void load_row(float (&x)[4 * E4], const float* rs, ui
             x[i] = (live && e < n) ? rs[e] : 0.0f;
         }
     }
+}
+
+// load_row for a row that fills every slot (n == 4 * E4 * T, 16-byte
+// aligned): no bounds tests, so every load is issued before the first wait.
+template <int T, int E4>
+__device__ __forceinline__ void load_row_full(float (&x)[4 * E4], const float* rs, int t) {
+    f32x4 v[E4];
+#pragma unroll
+    for (int i = 0; i < E4; ++i)
+        v[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rs) + t + T * i);
+#pragma unroll
+    for (int i = 0; i < E4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[4 * i + j] = v[i][j];
 }
 
 __device__ __forceinline__ uint32_t elem_of(int vec, int T, int t, int i) {
@@ -675,7 +698,7 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_sum_kernel(
     load_row<T, E4>(x, rs, n, t, live, vec);
     if constexpr (PROD) {
         float w[4 * E4];
-        load_row<T, E4>(w, xv, n, t, live, vec);
+        load_row<T, E4, false>(w, xv, n, t, live, vec);
 #pragma unroll
         for (int i = 0; i < 4 * E4; ++i) x[i] = __fmul_rn(x[i], w[i]);
     }
@@ -702,35 +725,76 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_sum_kernel(
     if (live && t == 0) dst[o] = mean ? s / static_cast<float>(n) : s;
 }
 
-// GEMV rows of 2048 < k <= 4096 (at most 128 leaves): two rows per 256-thread
-// workgroup. x is loaded once for both rows, the rounded products of both are
-// staged, and then threads 0-127 sum row 0's leaves and 128-255 row 1's (the
-// one-row kernel leaves half the threads idle there). The per-row tree is
-// group_pairwise_sum<256>'s: leaf sums, the butterfly over each wave, then
-// the two waves' sums added and 0 + 0 added, as its four-wave butterfly does.
-// Measured on the 4096 x 4096 GEMV: 13.2 against 14.8 us.
-__global__ __launch_bounds__(256) void gemv2_rows_kernel(const float* __restrict__ a, int64_t lda,
-                                                         const float* __restrict__ xv,
-                                                         float* __restrict__ y, uint32_t m,
-                                                         uint32_t n, int depth, uint32_t sstride) {
+// Row sums (PROD = false) and GEMV rows (PROD = true: the rounded products
+// x[k] * A[row, k]) for 2048 < n <= 4096 (at most 128 leaves), two rows per
+// 256-thread workgroup: both rows are staged, then threads 0-127 sum row 0's
+// leaves and 128-255 row 1's (one row per workgroup leaves half the threads
+// idle in the tree). The per-row tree is group_pairwise_sum<256>'s: leaf sums,
+// the butterfly over each wave, then the two waves' sums added and 0 + 0
+// added, as its four-wave butterfly does (its upper two waves hold no leaves),
+// so the bits are the one-row kernel's. Measured (4096 x 4096 GEMV / [8192,
+// 4096] sum): 12.8 / 22.2 us, against 14.8 / 24.0 with one row per
+// workgroup; a persistent grid of four workgroups per CU that issues its next
+// pair's loads while the current pair's tree runs measured 13.4 / 23.8.
+//
+// FULL: n == 4096, every leaf 32 whole floats (leaf j = [32 j, 32 j + 32)),
+// so the loads need no bounds and a thread's leaf needs no range walk.
+template <bool PROD, bool FULL>
+__global__ __launch_bounds__(256) void rows2_sum_kernel(const float* __restrict__ a, int64_t lda,
+                                                        const float* __restrict__ xv,
+                                                        float* __restrict__ y, uint32_t m,
+                                                        uint32_t n, int depth, uint32_t sstride,
+                                                        int mean) {
     extern __shared__ __attribute__((aligned(16))) float dyn[];
     __shared__ float scratch[4];
+    if constexpr (FULL) n = 4096u;
+    sstride &= ~3u;  // a multiple of four floats (stage_stride): 16-byte LDS stores for row 1
     const int t = threadIdx.x;
     const uint32_t r0 = blockIdx.x * 2;
     const bool live1 = r0 + 1 < m;
     float w[16], x0[16], x1[16];
-    load_row<256, 4>(w, xv, n, t, true, 1);
-    load_row<256, 4>(x0, a + static_cast<int64_t>(r0) * lda, n, t, true, 1);
-    load_row<256, 4>(x1, a + static_cast<int64_t>(live1 ? r0 + 1 : r0) * lda, n, t, true, 1);
+    const float* a0 = a + static_cast<int64_t>(r0) * lda;
+    const float* a1 = a + static_cast<int64_t>(live1 ? r0 + 1 : r0) * lda;
+    if constexpr (FULL) {
+        // Unconditional loads, the matrix rows' first: bounds tests around
+        // each load had the compiler wait for earlier loads between them.
+        f32x4 v0[4], v1[4], vw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v0[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a0) + t + 256 * i);
+            v1[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a1) + t + 256 * i);
+        }
+        if constexpr (PROD) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vw[i] = reinterpret_cast<const f32x4*>(xv)[t + 256 * i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x0[4 * i + j] = v0[i][j];
+                x1[4 * i + j] = v1[i][j];
+                if constexpr (PROD) w[4 * i + j] = vw[i][j];
+            }
+    } else {
+        if constexpr (PROD) load_row<256, 4, false>(w, xv, n, t, true, 1);
+        load_row<256, 4>(x0, a0, n, t, true, 1);
+        load_row<256, 4>(x1, a1, n, t, true, 1);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t e0 = 4u * (t + 256 * i);
-        if (e0 < n) {
+        if (FULL || e0 < n) {
             f32x4 v0, v1;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                v0[j] = __fmul_rn(x0[4 * i + j], w[4 * i + j]);
-                v1[j] = __fmul_rn(x1[4 * i + j], w[4 * i + j]);
+                if constexpr (PROD) {
+                    v0[j] = __fmul_rn(x0[4 * i + j], w[4 * i + j]);
+                    v1[j] = __fmul_rn(x1[4 * i + j], w[4 * i + j]);
+                } else {
+                    v0[j] = x0[4 * i + j];
+                    v1[j] = x1[4 * i + j];
+                }
             }
             *reinterpret_cast<f32x4*>(dyn + stage_index(e0)) = v0;
             *reinterpret_cast<f32x4*>(dyn + sstride + stage_index(e0)) = v1;
@@ -739,50 +803,9 @@ __global__ __launch_bounds__(256) void gemv2_rows_kernel(const float* __restrict
     __syncthreads();
     const int row = t >> 7, leaf = t & 127;
     float v = 0.0f;
-    if (static_cast<uint32_t>(leaf) < (1u << depth))
-        v = staged_subtree_sum(dyn + row * sstride, n, depth, leaf, 1);
-    v = wave_sum_butterfly(v);
-    const int lane = t & 63, wave = t >> 6;
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    if (lane == 0 && (wave & 1) == 0) {
-        const uint32_t o = r0 + row;
-        if (o < m) y[o] = scratch[wave] + scratch[wave + 1] + (0.0f + 0.0f);
-    }
-}
-
-// Row sums of 2048 < n <= 4096 over evenly spaced rows: two rows per
-// 256-thread workgroup, the gemv2_rows_kernel arrangement without the vector.
-// Threads 0-127 sum row 0's leaves and 128-255 row 1's; the final
-// (w0 + w1) + (0 + 0) is what group_pairwise_sum<256> computes for one row
-// (its upper two waves hold no leaves), so the bits are the one-row kernel's.
-// More rows in flight per CU: [8192, 4096] 24.0 -> 23.4 us.
-__global__ __launch_bounds__(256) void sum2_rows_kernel(const float* __restrict__ a, int64_t lda,
-                                                        float* __restrict__ y, uint32_t m,
-                                                        uint32_t n, int depth, uint32_t sstride, int mean) {
-    extern __shared__ __attribute__((aligned(16))) float dyn[];
-    __shared__ float scratch[4];
-    const int t = threadIdx.x;
-    const uint32_t r0 = blockIdx.x * 2;
-    const bool live1 = r0 + 1 < m;
-    float x0[16], x1[16];
-    load_row<256, 4>(x0, a + static_cast<int64_t>(r0) * lda, n, t, true, 1);
-    load_row<256, 4>(x1, a + static_cast<int64_t>(live1 ? r0 + 1 : r0) * lda, n, t, true, 1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t e0 = 4u * (t + 256 * i);
-        if (e0 < n) {
-            f32x4 v0, v1;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { v0[j] = x0[4 * i + j]; v1[j] = x1[4 * i + j]; }
-            *reinterpret_cast<f32x4*>(dyn + stage_index(e0)) = v0;
-            *reinterpret_cast<f32x4*>(dyn + sstride + stage_index(e0)) = v1;
-        }
-    }
-    __syncthreads();
-    const int row = t >> 7, leaf = t & 127;
-    float v = 0.0f;
-    if (static_cast<uint32_t>(leaf) < (1u << depth))
+    if constexpr (FULL)
+        v = staged_leaf_sum(dyn + row * sstride, 32u * leaf, 32u * leaf + 32u);
+    else if (static_cast<uint32_t>(leaf) < (1u << depth))
         v = staged_subtree_sum(dyn + row * sstride, n, depth, leaf, 1);
     v = wave_sum_butterfly(v);
     const int lane = t & 63, wave = t >> 6;
@@ -791,7 +814,7 @@ __global__ __launch_bounds__(256) void sum2_rows_kernel(const float* __restrict_
     if (lane == 0 && (wave & 1) == 0) {
         const uint32_t o = r0 + row;
         const float s = scratch[wave] + scratch[wave + 1] + (0.0f + 0.0f);
-        if (o < m) y[o] = mean ? s / static_cast<float>(n) : s;
+        if (o < m) y[o] = (!PROD && mean) ? s / static_cast<float>(n) : s;
     }
 }
 
@@ -851,7 +874,11 @@ __device__ __forceinline__ Sel sel_merge_t(Sel a, Sel b) {
 // row if there is one, else the first of the extreme values (which fixes the
 // sign of a zero maximum); argmax/argmin skip NaN and return the lowest index
 // of a strict improvement, 0 when nothing improves on the initial +-inf.
-template <int T, int E4, int OP>
+//
+// FULL: every row fills the thread slots exactly (vec, n == 4 * E4 * T), so
+// the loads are unconditional and all issued before the first wait
+// ([8192, 4096] max: 22.3 -> 21.9-22.2 us).
+template <int T, int E4, int OP, bool FULL>
 __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kernel(
     const float* __restrict__ src, Op4 kept, uint32_t n_out, uint32_t n, int vec,
     void* __restrict__ dst) {
@@ -867,7 +894,10 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kern
     const bool live = o < n_out;
     const float* rs = src + (live ? lin_off4(o, kept.ne, kept.nb) : 0);
     float x[4 * E4];
-    load_row<T, E4>(x, rs, n, t, live, vec);
+    if constexpr (FULL)
+        load_row_full<T, E4>(x, rs, t);
+    else
+        load_row<T, E4>(x, rs, n, t, live, vec);
     // One candidate per thread, scanned in increasing index order. For value
     // ops a NaN outranks every number and the first one stays; the first
     // element is taken even when it equals the initial +-inf.
@@ -875,9 +905,9 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void reduce_rows_select_reg_kern
     uint32_t bi = kNone;
 #pragma unroll
     for (int i = 0; i < 4 * E4; ++i) {
-        const uint32_t e = elem_of(vec, T, t, i);
+        const uint32_t e = FULL ? 4u * (t + T * (i / 4)) + (i % 4) : elem_of(vec, T, t, i);
         const float v = x[i];
-        const bool valid = live && e < n;
+        const bool valid = live && (FULL || e < n);
         const bool improves = is_max ? v > bv : v < bv;
         bool better;
         if constexpr (value_op) {
@@ -1236,26 +1266,26 @@ static int launch_sum_rows(const float* src, const Op4& kept, uint32_t n_out, ui
     return VKHIP_OK;
 }
 
-template <int T, int E4>
-static int launch_select_rows(int op, const float* src, const Op4& kept, uint32_t n_out,
-                              uint32_t n, int vec, void* out, hipStream_t st) {
+template <int T, int E4, bool FULL>
+static int launch_select_rows_as(int op, const float* src, const Op4& kept, uint32_t n_out,
+                                 uint32_t n, int vec, void* out, hipStream_t st) {
     constexpr int RPB = Rows<T>::kPerBlock;
     const dim3 grid(ceil_div(n_out, RPB)), block(Rows<T>::kThreads);
     switch (op) {
         case VKHIP_REDUCE_MAX:
-            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_MAX>), grid,
+            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_MAX, FULL>), grid,
                                block, 0, st, src, kept, n_out, n, vec, out);
             break;
         case VKHIP_REDUCE_MIN:
-            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_MIN>), grid,
+            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_MIN, FULL>), grid,
                                block, 0, st, src, kept, n_out, n, vec, out);
             break;
         case VKHIP_REDUCE_ARGMAX:
-            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_ARGMAX>), grid,
+            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_ARGMAX, FULL>), grid,
                                block, 0, st, src, kept, n_out, n, vec, out);
             break;
         case VKHIP_REDUCE_ARGMIN:
-            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_ARGMIN>), grid,
+            hipLaunchKernelGGL((reduce_rows_select_reg_kernel<T, E4, VKHIP_REDUCE_ARGMIN, FULL>), grid,
                                block, 0, st, src, kept, n_out, n, vec, out);
             break;
         default:
@@ -1263,6 +1293,14 @@ static int launch_select_rows(int op, const float* src, const Op4& kept, uint32_
     }
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
+}
+
+template <int T, int E4>
+static int launch_select_rows(int op, const float* src, const Op4& kept, uint32_t n_out,
+                              uint32_t n, int vec, void* out, hipStream_t st) {
+    if (vec && n == 4u * E4 * T)
+        return launch_select_rows_as<T, E4, true>(op, src, kept, n_out, n, vec, out, st);
+    return launch_select_rows_as<T, E4, false>(op, src, kept, n_out, n, vec, out, st);
 }
 
 template <int T, int E4>
@@ -1331,9 +1369,10 @@ int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mas
             if (vec && n_red > 2048 && n_red <= 4096 && n_out >= 2 && kept.ne[0] == 1 &&
                 kept.ne[1] == 1 && kept.ne[2] == 1) {
                 const uint32_t ss = stage_stride(n_red);
-                hipLaunchKernelGGL(sum2_rows_kernel, dim3(ceil_div(n_out, 2u)), dim3(256),
+                auto* kern = n_red == 4096 ? rows2_sum_kernel<false, true> : rows2_sum_kernel<false, false>;
+                hipLaunchKernelGGL(kern, dim3(ceil_div(n_out, 2u)), dim3(256),
                                    2 * static_cast<size_t>(ss) * sizeof(float), st, src, kept.nb[3],
-                                   out, n_out, n_red, depth, ss, mean);
+                                   nullptr, out, n_out, n_red, depth, ss, mean);
                 VKHIP_LAUNCH_CHECK();
                 return VKHIP_OK;
             }
@@ -1770,8 +1809,9 @@ int launch_gemv_rows(const float* a, int64_t lda, const float* x, float* y, uint
     hipStream_t st = ctx().stream;
     if (vec && k > 2048 && k <= 4096 && m >= 2) {
         const uint32_t ss = stage_stride(k);
-        hipLaunchKernelGGL(gemv2_rows_kernel, dim3(ceil_div(m, 2u)), dim3(256),
-                           2 * static_cast<size_t>(ss) * sizeof(float), st, a, lda, x, y, m, k, depth, ss);
+        auto* kern = k == 4096 ? rows2_sum_kernel<true, true> : rows2_sum_kernel<true, false>;
+        hipLaunchKernelGGL(kern, dim3(ceil_div(m, 2u)), dim3(256),
+                           2 * static_cast<size_t>(ss) * sizeof(float), st, a, lda, x, y, m, k, depth, ss, 0);
         VKHIP_LAUNCH_CHECK();
         return VKHIP_OK;
     }
