@@ -461,6 +461,21 @@ def _view(base: DeviceArray, shape, strides) -> DeviceArray:
     return DeviceArray(shape, np.float32, strides=strides, buffer=base.buffer, offset=base.offset)
 
 
+@pytest.mark.parametrize("shape", [(3, 5, 7, 8), (2, 2, 3, 4), (1, 3, 5, 64), (1, 1, 4, 256),
+                                   (2, 2, 5, 12), (5, 3, 9, 16)])
+def test_col2im_3x3_same_size_bit_exact(hip, shape):
+    """3x3 / stride 1 / padding 1 col2im over arbitrary columns (not an im2col
+    image): neighbouring pixels' terms, the image border, signed zeros and
+    partial waves; widths 4..256 take the register kernel, 12 the staged one."""
+    n, c, h, w = shape
+    rng = np.random.default_rng(SEED + h * w)
+    cols = rng.standard_normal((n, c * 9, h * w)).astype(np.float32)
+    cols[..., ::7] = -0.0
+    cols[0, :, 1] = np.float32(1e8) * np.sign(rng.standard_normal(c * 9)).astype(np.float32)
+    got = ops.col2im(dev(cols), (h, w), (3, 3), (1, 1), (1, 1)).numpy()
+    assert got.tobytes() == O.col2im(cols, (h, w), (3, 3), (1, 1), (1, 1)).tobytes()
+
+
 def test_col2im_fold_order_fixture(hip):
     """reference test_col2im_fold_is_bit_reproducible (test_vulkan_kernels.py:1342-1356)."""
     vals = np.array([1e8, 1.0, -1e8, 1e-8, 1.0, -1.0, 1e7, 1.0, -1e7], np.float32)

@@ -408,6 +408,72 @@ __global__ __launch_bounds__(256) void col2im_staged_kernel(const float* __restr
     }
 }
 
+// col2im of a 3x3 window, stride 1, padding 1, dilation 1, out = H x W with
+// W a multiple of four and Q = W / 4 dividing 64 (the config geometries).
+// Thread (plane, h, q) owns output pixels w = 4q .. 4q + 3 of row h. The
+// columns it needs from window row ki all lie in output row oh = h + 1 - ki,
+// at ow = w + 1 - kj: for each of the nine cols rows it loads the aligned
+// float4 at [oh][4q .. 4q + 3] (every cols element is loaded by exactly one
+// thread, 16-byte loads coalesced along the row), and the two values just
+// outside it (kj = 0 needs [4q + 4], kj = 2 needs [4q - 1]) come from the
+// neighbouring lanes of the same row (0 at the image border). No LDS, so
+// occupancy is not held to four planes per CU as in the staged kernel.
+// Each pixel adds its nine terms in ascending (ki, kj) from +0.0, an absent
+// term as +0.0: the sum is never -0.0, so adding +0.0 changes nothing and the
+// result is the pull's bits (kernels_movement.cpp:500-542).
+__global__ __launch_bounds__(256) void col2im_3x3_kernel(const float* __restrict__ cols,
+                                                         float* __restrict__ dst, uint32_t H,
+                                                         uint32_t W, uint64_t total, FastDiv div_q,
+                                                         FastDiv div_h) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const bool live = i < total;
+    const uint32_t Q = W >> 2;
+    const uint64_t ii = live ? i : 0;
+    // i = (plane * H + h) * Q + q; total < 2^32 (checked by the launcher)
+    const uint32_t row = div_q.div(static_cast<uint32_t>(ii));
+    const uint32_t q = static_cast<uint32_t>(ii) - row * Q;
+    const uint32_t plane = div_h.div(row);
+    const uint32_t h = row - plane * H;
+    const uint64_t L = static_cast<uint64_t>(H) * W;
+    const float* cb = cols + static_cast<uint64_t>(plane) * 9u * L + 4u * q;
+    f32x4 v[9];
+#pragma unroll
+    for (int ki = 0; ki < 3; ++ki) {
+        const int32_t oh = static_cast<int32_t>(h) + 1 - ki;
+        const bool ok = live && oh >= 0 && oh < static_cast<int32_t>(H);
+        const uint64_t off = ok ? static_cast<uint64_t>(oh) * W : 0u;
+#pragma unroll
+        for (int kj = 0; kj < 3; ++kj) {
+            const f32x4 t = __builtin_nontemporal_load(
+                reinterpret_cast<const f32x4*>(cb + static_cast<uint64_t>(ki * 3 + kj) * L + off));
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            v[ki * 3 + kj] = ok ? t : z;
+        }
+    }
+    float nxt[3], prv[3];  // [4q + 4] of window (ki, 0); [4q - 1] of window (ki, 2)
+#pragma unroll
+    for (int ki = 0; ki < 3; ++ki) {
+        const float a = __shfl_down(v[ki * 3][0], 1);
+        const float b = __shfl_up(v[ki * 3 + 2][3], 1);
+        nxt[ki] = q + 1 < Q ? a : 0.0f;
+        prv[ki] = q > 0 ? b : 0.0f;
+    }
+    f32x4 acc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float s = 0.0f;
+#pragma unroll
+        for (int ki = 0; ki < 3; ++ki) {
+            s = s + (j < 3 ? v[ki * 3][j + 1] : nxt[ki]);  // kj = 0: ow = w + 1
+            s = s + v[ki * 3 + 1][j];                       // kj = 1: ow = w
+            s = s + (j > 0 ? v[ki * 3 + 2][j - 1] : prv[ki]);  // kj = 2: ow = w - 1
+        }
+        acc[j] = s;
+    }
+    if (live)
+        __builtin_nontemporal_store(acc, reinterpret_cast<f32x4*>(dst + static_cast<uint64_t>(row) * W + 4u * q));
+}
+
 int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
                   const vkhip_unfold& p) {
     Geo g;
@@ -417,6 +483,23 @@ int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels,
     if (planes == 0 || g.H == 0 || g.W == 0) return VKHIP_OK;
     const uint64_t L = static_cast<uint64_t>(g.out_h) * g.out_w;
     const uint64_t plane_floats = L * g.kh * g.kw;
+    // 3x3, stride 1, padding 1 (same-size output), rows of whole float4s
+    // whose lanes stay inside one wave: the register kernel above.
+    const uint64_t q_total = planes * static_cast<uint64_t>(g.H) * (g.W / 4);
+    if (g.kh == 3 && g.kw == 3 && g.sh == 1 && g.sw == 1 && g.dh == 1 && g.dw == 1 && g.ph == 1 &&
+        g.pw == 1 && g.out_h == g.H && g.out_w == g.W && g.W % 4 == 0 && 64 % (g.W / 4) == 0 &&
+        reinterpret_cast<uintptr_t>(cols) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0 &&
+        planes * 9 * L < (1ull << 40) && q_total + 255 < (1ull << 32)) {
+        publish("col2im.kernel", "col2im", "col2im_3x3", "col2im_staged",
+                "3x3 window, stride 1, padding 1, rows of whole float4s",
+                static_cast<int64_t>(g.W), 4);
+        hipLaunchKernelGGL(col2im_3x3_kernel, dim3(static_cast<uint32_t>((q_total + 255) / 256)),
+                           dim3(256), 0, ctx().stream, cols, dst, static_cast<uint32_t>(g.H),
+                           static_cast<uint32_t>(g.W), q_total,
+                           FastDiv(static_cast<uint32_t>(g.W / 4)), FastDiv(static_cast<uint32_t>(g.H)));
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
     const bool staged = plane_floats * sizeof(float) <= 65536 && planes <= 0x7fffffffull;
     publish("col2im.kernel", "col2im", staged ? "col2im_staged" : "col2im_direct",
             staged ? "col2im_direct" : "col2im_staged",
