@@ -322,6 +322,14 @@ def relu_grad(backend, x, g, fused):
         T.FUSED_RELU_BACKWARD = prev
 
 
+def small_window(shape, cout, kernel, L):
+    """Whether a weight gradient runs conv_wgrad_small_kernel: C*kh*kw <= 32,
+    Cout <= 64, whole 32-position K-tiles per image and an image of at most
+    8192 floats (staged in LDS)."""
+    ck = shape[1] * kernel[0] * kernel[1]
+    return ck <= 32 and cout <= 64 and L % 32 == 0 and shape[1] * shape[2] * shape[3] <= 8192
+
+
 CONV_GEOMETRIES = [  # (x shape, Cout, kernel, stride, pad, dilation)
     ((2, 3, 5, 5), 4, (3, 3), (1, 1), (1, 1), (1, 1)),
     ((1, 2, 6, 6), 3, (2, 2), (2, 2), (0, 0), (1, 1)),

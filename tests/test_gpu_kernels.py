@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from conftest import SEED, gemm_atol, gemm_tolerance, golden, normwise_rel_err
+from conftest import SEED, gemm_atol, gemm_tolerance, golden, normwise_rel_err, small_window
 from vkml_amd import _lib, ops
 from vkml_amd.device import DeviceArray
 
@@ -320,13 +320,23 @@ def test_implicit_conv_is_bit_identical_to_im2col_then_gemm(hip, shape, cout, ke
         assert normwise_rel_err(got, ref) <= gemm_tolerance(ck)
 
 
-@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONVS)
+SMALL_WINDOW_CONVS = [  # conv_wgrad_small_kernel geometries beyond CONVS' 3-channel layer
+    ((4, 2, 16, 16), 5, (3, 3), (2, 2), (1, 1), (1, 1)),
+    ((2, 2, 16, 16), 3, (3, 3), (1, 1), (2, 2), (2, 2)),
+    ((3, 1, 32, 32), 40, (5, 5), (1, 1), (2, 2), (1, 1)),
+    ((2, 8, 9, 9), 64, (2, 2), (1, 1), (0, 0), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONVS + SMALL_WINDOW_CONVS)
 def test_implicit_weight_grad_is_bit_identical_to_gemm_on_cols(hip, shape, cout, kernel, stride,
                                                                pad, dil):
     """vkhip_conv2d_weight_grad gathers the transposed columns inside the GEMM;
     its per-image products equal the reference lowering's matmul(grad,
     im2col(x)^T) bit for bit (same plan, K order and split-K fold), and the
-    oracle's to the GEMM tolerance."""
+    oracle's to the GEMM tolerance. Small windows (C*kh*kw <= 32) run the
+    image-staged kernel instead: within the GEMM tolerance of the lowering,
+    and the same bits on a second run."""
     rng = np.random.default_rng(SEED + 3 * shape[1])
     x = rng.uniform(-1, 1, shape).astype(np.float32)
     cols = ops.im2col(dev(x), kernel, stride, pad, dil)
@@ -334,10 +344,16 @@ def test_implicit_weight_grad_is_bit_identical_to_gemm_on_cols(hip, shape, cout,
     oh = ops.window_count(shape[2], kernel[0], stride[0], pad[0], dil[0])
     ow = ops.window_count(shape[3], kernel[1], stride[1], pad[1], dil[1])
     g = rng.standard_normal((n, cout, oh, ow)).astype(np.float32)
+    print(f"weight_grad x={shape} cout={cout} k={kernel} s={stride} p={pad} d={dil}", flush=True)
     got = ops.conv2d_weight_grad(dev(x), dev(g), kernel, stride, pad, dil).numpy()
     want = ops.matmul(dev(g.reshape(1, n, cout, L)),
                       cols.reshape(1, n, ck, L).transpose(-2, -1)).numpy().reshape(got.shape)
-    assert got.tobytes() == want.tobytes()
+    if small_window(shape, cout, kernel, L):
+        assert normwise_rel_err(got, want) <= gemm_tolerance(L)
+        again = ops.conv2d_weight_grad(dev(x), dev(g), kernel, stride, pad, dil).numpy()
+        assert got.tobytes() == again.tobytes()
+    else:
+        assert got.tobytes() == want.tobytes()
     if n * cout * L * ck <= 1 << 27:
         ref = O.matmul(g.reshape(n, cout, L),
                        np.ascontiguousarray(np.swapaxes(O.im2col(x, kernel, stride, pad, dil), 1, 2)))
@@ -345,8 +361,10 @@ def test_implicit_weight_grad_is_bit_identical_to_gemm_on_cols(hip, shape, cout,
 
 
 @pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil",
-                         CONVS + [((8, 16, 16, 16), 24, (3, 3), (1, 1), (1, 1), (1, 1)),
-                                  ((3, 5, 12, 16), 7, (5, 5), (1, 1), (2, 2), (1, 1))])
+                         CONVS + SMALL_WINDOW_CONVS +
+                         [((8, 16, 16, 16), 24, (3, 3), (1, 1), (1, 1), (1, 1)),
+                          ((3, 5, 12, 16), 7, (5, 5), (1, 1), (2, 2), (1, 1)),
+                          ((600, 1, 8, 8), 6, (3, 3), (1, 1), (1, 1), (1, 1))])
 def test_weight_grad_sum_is_the_batch_sum_of_the_products(hip, shape, cout, kernel, stride, pad,
                                                           dil):
     """vkhip_conv2d_weight_grad_sum: with out_h*out_w a multiple of 32 the batch

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from conftest import SEED, gemm_tolerance, normwise_rel_err
+from conftest import SEED, gemm_tolerance, normwise_rel_err, small_window
 from vkml_amd import ops
 from vkml_amd import tensor as T
 from vkml_amd.device import DeviceArray
@@ -55,8 +55,9 @@ def conv_cases(count: int):
 def test_random_conv_forward_and_weight_grad_match_the_lowering(hip, shape, cout, kernel, stride,
                                                                 pad, dil):
     """Implicit-im2col forward and weight gradient against im2col + GEMM on
-    the device (bit for bit) and the oracle (GEMM tolerance), and the device
-    im2col against the oracle's (bit for bit)."""
+    the device (bit for bit; small-window weight gradients within the GEMM
+    tolerance) and the oracle (GEMM tolerance), and the device im2col against
+    the oracle's (bit for bit)."""
     rng = np.random.default_rng(SEED + sum(shape) + cout)
     x = rng.uniform(-1, 1, shape).astype(np.float32)
     w = rng.uniform(-0.5, 0.5, (cout, shape[1]) + kernel).astype(np.float32)
@@ -74,7 +75,10 @@ def test_random_conv_forward_and_weight_grad_match_the_lowering(hip, shape, cout
     dw = ops.conv2d_weight_grad(dev(x), dev(g), kernel, stride, pad, dil).numpy()
     want_dw = ops.matmul(dev(g.reshape(1, n, cout, L)),
                          cols.reshape(1, n, ck, L).transpose(-2, -1)).numpy().reshape(dw.shape)
-    assert dw.tobytes() == want_dw.tobytes()
+    if small_window(shape, cout, kernel, L):  # its own fixed summation order
+        assert normwise_rel_err(dw, want_dw) <= gemm_tolerance(L)
+    else:
+        assert dw.tobytes() == want_dw.tobytes()
 
 
 def reduce_cases(count: int):

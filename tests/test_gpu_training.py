@@ -12,7 +12,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad,
+from conftest import (CONV_GEOMETRIES, SEED, small_window, ce_inputs, ce_loss_and_grad,
                       config5_batches, config5_golden_losses, config5_model, config5_train, conv_loss_and_grads,
                       conv_relu_loss_and_grads, gemm_tolerance, mlp_batches, mlp_model, train_with_rewrites,
                       normwise_rel_err, relu_grad, relu_inputs, POOL_GEOMETRIES, pool_relu_input,
@@ -149,13 +149,17 @@ def test_conv_node_on_device_is_bit_identical_to_the_graph(backends, shape, cout
     node = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True, fold=False,
                                fused_dx=False)
     graph = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=False)
-    for got, want in zip(node, graph):
-        assert got.tobytes() == want.tobytes()
+    positions = node[0][0, 0].size
+    for i, (got, want) in enumerate(zip(node, graph)):
+        if i == 2 and small_window(shape, cout, kernel, positions):
+            # the small-window weight gradient sums in its own (fixed) order
+            assert normwise_rel_err(got, want) <= gemm_tolerance(positions)
+        else:
+            assert got.tobytes() == want.tobytes()
     folded = conv_loss_and_grads(dev, x, w, bias, stride, pad, dil, implicit=True, fold=True,
                                  fused_dx=True)
     for i in (0, 3):
         assert folded[i].tobytes() == graph[i].tobytes()
-    positions = node[0][0, 0].size
     assert normwise_rel_err(folded[2], graph[2]) <= gemm_tolerance(shape[0] * positions)
     if positions % 32:
         assert folded[2].tobytes() == graph[2].tobytes()

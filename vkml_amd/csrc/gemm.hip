@@ -2370,6 +2370,236 @@ static int launch_conv_epilogue(float* out, uint64_t total, uint32_t positions, 
     return VKHIP_OK;
 }
 
+// ---- weight gradient of a small window (C*kh*kw <= 32, Cout <= 64) ----------
+// The 3-channel first layer's product, [Cout, L] x [L, 27] per image, pads a
+// GEMM tile to 6-10% use, and its K (positions) is all there is: the layer is
+// bound by the gradient's bytes, not by the matrix cores. Here a workgroup of
+// eight waves takes a run of K-tiles (32 positions each) of one image, which
+// it first stages whole in LDS (padded pitches, stage_image; at most 8192
+// floats); each wave
+// owns consecutive K-tiles and both 32-row blocks of Cout: its A operand is
+// the gradient rows read straight into registers (16 consecutive positions
+// per lane, four 16-byte loads), its B operand the columns' window element of
+// that position read from the staged image (0 in the padding or past C*kh*kw),
+// shared by the two blocks' MFMAs. Each wave's partial keeps the MFMA order of
+// the GEMM kernels over its K-tiles; the eight partials are summed in LDS as a
+// balanced tree over consecutive waves ((w0+w1)+(w2+w3))+((w4+w5)+(w6+w7)).
+//   FOLD = false: one workgroup per image, out[n] = its sum.
+//   FOLD = true:  the batch-summed gradient with K = N*L: workgroup b takes
+//                 K-tiles [b*kpw, (b+1)*kpw) (within one image) and writes
+//                 partial b; the split-K carry-stack fold sums the partials.
+// Deterministic for a given shape (fixed partition and summation order);
+// within the GEMM tolerance of the lowering, not its bits.
+constexpr int kSmallWgradWaves = 8;
+constexpr int kSmallWgradLds = 8192;  // floats: the staged image, then 4 wave partials
+
+// Image n into LDS as [C][H][W] with a row pitch of `wp` and a channel pitch
+// of `cp` floats (element (c, h, w) at c*cp + h*wp + w). The pitches spread a
+// window's elements over the LDS banks: for a 3x3 window over three channels
+// the 27 elements one position reads land on 27 distinct banks (wp = 4 mod 64
+// gives rows 0, 36 and 72 = 8; cp = 16 mod 64 moves channels by 16 banks).
+// Eight loads per thread are issued before their LDS stores, so a stage of up
+// to 8 * blockDim elements waits for memory once.
+struct StagePitch {
+    int32_t wp, cp;
+    FastDiv div_hw, div_w;  // by H*W and W
+};
+__host__ inline StagePitch stage_pitch(int H, int W) {
+    StagePitch s;
+    s.wp = ((W + 3) & ~3) + 4;
+    const int plane = H * s.wp;
+    s.cp = ((plane + 47) / 64) * 64 + 16;  // the first value >= plane that is 16 mod 64
+    s.div_hw = FastDiv(static_cast<uint32_t>(H * W));
+    s.div_w = FastDiv(static_cast<uint32_t>(W));
+    return s;
+}
+__host__ inline uint64_t stage_floats(const StagePitch& s, int chans) {
+    return static_cast<uint64_t>(chans) * static_cast<uint64_t>(s.cp);
+}
+__device__ __forceinline__ void stage_image(float* lds, const Im2colB& im, uint32_t n, uint32_t elems,
+                                            const StagePitch& sp) {
+    const float* xn = im.x + static_cast<int64_t>(n) * im.sn;
+    for (uint32_t e0 = threadIdx.x; e0 < elems; e0 += 8 * blockDim.x) {
+        float v[8];
+        int32_t at[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t e = e0 + u * blockDim.x;
+            const uint32_t ec = e < elems ? e : 0u;
+            const uint32_t c = sp.div_hw.div(ec), r = ec - c * sp.div_hw.d, h = sp.div_w.div(r),
+                           w = r - h * sp.div_w.d;
+            v[u] = xn[static_cast<int32_t>(c) * im.sc + static_cast<int32_t>(h) * im.sh +
+                      static_cast<int32_t>(w) * im.sw];
+            at[u] = static_cast<int32_t>(c) * sp.cp + static_cast<int32_t>(h) * sp.wp + static_cast<int32_t>(w);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (e0 + u * blockDim.x < elems) lds[at[u]] = v[u];
+    }
+}
+
+template <bool FOLD>
+__global__ __launch_bounds__(64 * kSmallWgradWaves) void conv_wgrad_small_kernel(GemmArgs g, Im2colB im,
+                                                                                 uint32_t kpw,
+                                                                                 uint32_t per_wave,
+                                                                                 StagePitch sp) {
+    __shared__ __attribute__((aligned(16))) float lds[kSmallWgradLds];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, kh = lane >> 5;
+    const uint32_t tpi = im.L / 32;  // K-tiles per image
+    const uint32_t first = blockIdx.x * kpw;
+    const uint32_t n = FOLD ? first / tpi : blockIdx.x;
+    const uint32_t t0 = FOLD ? first - n * tpi : 0u;
+    const int chans = static_cast<int>(g.n) / im.kk;
+
+    // this lane's column j = lrow: channel c, window element (ki, kj); its
+    // element of position (oh, ow) is at off + oh*strh*wp + ow*strw when
+    // inside the image
+    const uint32_t j = static_cast<uint32_t>(lrow);
+    const bool jok = j < g.n;
+    const uint32_t jc = jok ? j : 0u;
+    const uint32_t c = jc / static_cast<uint32_t>(im.kk);
+    const uint32_t r = jc - c * static_cast<uint32_t>(im.kk);
+    const uint32_t ki = r / static_cast<uint32_t>(im.kw), kj = r - ki * static_cast<uint32_t>(im.kw);
+    const int fh = jok ? static_cast<int>(ki) * im.dilh - im.padh : -(1 << 28);
+    const int fw = static_cast<int>(kj) * im.dilw - im.padw;
+    const int off = static_cast<int>(c) * sp.cp + fh * sp.wp + fw;
+    const int sth = im.strh * sp.wp;
+
+    // the gradient rows of this lane in the two Cout blocks (rows past Cout
+    // read the last row: their outputs are never stored)
+    const float* gn = g.a + static_cast<int64_t>(n) * g.sa1;
+    const float* arow0 = gn + static_cast<int64_t>(min(static_cast<uint32_t>(lrow), g.m - 1)) * g.sam + 16 * kh;
+    const float* arow1 = gn + static_cast<int64_t>(min(static_cast<uint32_t>(32 + lrow), g.m - 1)) * g.sam + 16 * kh;
+
+    f32x16 acc0, acc1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        acc0[i] = 0.0f;
+        acc1[i] = 0.0f;
+    }
+    const uint32_t w0 = t0 + static_cast<uint32_t>(wave) * per_wave;
+    const uint32_t w1 = min(t0 + kpw, w0 + per_wave);
+    // The gradient rows of K-tile t go one tile ahead of its MFMAs (the first
+    // tile's ahead of the image staging), so their memory latency overlaps.
+    f32x4 a0[4], a1[4];
+    auto load_a = [&](uint32_t t) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            a0[q] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(arow0 + t * 32 + 4 * q));
+            a1[q] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(arow1 + t * 32 + 4 * q));
+        }
+    };
+    if (w0 < w1) load_a(w0);
+    stage_image(lds, im, n, static_cast<uint32_t>(chans * im.H * im.W), sp);
+    __syncthreads();
+    for (uint32_t t = w0; t < w1; ++t) {
+        const uint32_t p0 = t * 32;
+        f32x4 c0[4], c1[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            c0[q] = a0[q];
+            c1[q] = a1[q];
+        }
+        if (t + 1 < w1) load_a(t + 1);
+        // the window element of positions p0 + 16*kh + i, i = 0..15
+        const uint32_t p = p0 + 16 * kh;
+        uint32_t oh = im.div_ow.div(p);
+        uint32_t ow = p - oh * static_cast<uint32_t>(im.ow);
+        float bv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int h = static_cast<int>(oh) * im.strh + fh, w = static_cast<int>(ow) * im.strw + fw;
+            const bool in = (static_cast<uint32_t>(h) < static_cast<uint32_t>(im.H)) &
+                            (static_cast<uint32_t>(w) < static_cast<uint32_t>(im.W));
+            const float v = lds[in ? off + static_cast<int>(oh) * sth + static_cast<int>(ow) * im.strw : 0];
+            bv[i] = in ? v : 0.0f;
+            if (++ow == static_cast<uint32_t>(im.ow)) {
+                ow = 0;
+                ++oh;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(c0[q][st], bv[4 * q + st], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(c1[q][st], bv[4 * q + st], acc1, 0, 0, 0);
+            }
+    }
+
+    // balanced tree over consecutive waves: at step s the wave w with
+    // w % 2s == s hands its partial to w - s, which adds it to its own
+    __syncthreads();  // every wave is done with the staged image
+#pragma unroll
+    for (int s = 1; s < kSmallWgradWaves; s *= 2) {
+        float* slot = lds + (wave / (2 * s)) * 2048;
+        if ((wave & (2 * s - 1)) == s) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                slot[i * 64 + lane] = acc0[i];
+                slot[1024 + i * 64 + lane] = acc1[i];
+            }
+        }
+        __syncthreads();
+        if ((wave & (2 * s - 1)) == 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                acc0[i] = acc0[i] + slot[i * 64 + lane];
+                acc1[i] = acc1[i] + slot[1024 + i * 64 + lane];
+            }
+        }
+        __syncthreads();
+    }
+    if (wave != 0 || !jok) return;
+    // register i of lane l: row 8*(i/4) + 4*(l/32) + i%4 of its block, column l%32
+    float* dst = g.c + static_cast<uint64_t>(blockIdx.x) * g.m * g.n;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t row = 8 * (i / 4) + 4 * kh + (i % 4);
+        if (row < g.m) dst[static_cast<uint64_t>(row) * g.n + j] = acc0[i];
+        if (row + 32 < g.m) dst[static_cast<uint64_t>(row + 32) * g.n + j] = acc1[i];
+    }
+}
+
+// Whether conv_wgrad_small_kernel takes a weight gradient: C*kh*kw <= 32,
+// Cout <= 64, whole K-tiles per image, the image fits the stage, and the
+// gradient rows are 16-byte aligned.
+static bool wgrad_small_fits(const float* gr, const vkhip_operand& gd, uint64_t ck, uint32_t cout,
+                             uint64_t L, const Im2colB& im, uint32_t chans) {
+    return ck >= 1 && ck <= 32 && cout >= 1 && cout <= 64 && L % 32 == 0 && L >= 32 &&
+           L <= 0x7fffffffull &&
+           stage_floats(stage_pitch(im.H, im.W), static_cast<int>(chans)) <= static_cast<uint64_t>(kSmallWgradLds) &&
+           reinterpret_cast<uintptr_t>(gr) % 16 == 0 && gd.nb[1] >= 0 && gd.nb[2] >= 0 &&
+           gd.nb[1] % 4 == 0 && gd.nb[2] % 4 == 0;
+}
+
+// Launch: FOLD writes `parts` partials of Cout*ck floats to `ws`, else out
+// [N][Cout][ck] directly.
+static int launch_wgrad_small(bool fold, const float* gr, const vkhip_operand& gd, Im2colB im,
+                              uint32_t cout, uint32_t ck, uint32_t batch, uint32_t kpw, float* dst) {
+    GemmArgs g{};
+    g.a = gr;
+    g.sa1 = gd.nb[1];
+    g.sam = gd.nb[2];
+    g.m = cout;
+    g.n = ck;
+    g.c = dst;
+    const uint32_t tpi = im.L / 32;
+    const uint32_t per_wave = ceil_div(kpw, static_cast<uint32_t>(kSmallWgradWaves));
+    const uint32_t blocks = fold ? static_cast<uint32_t>(static_cast<uint64_t>(batch) * tpi / kpw) : batch;
+    const StagePitch sp = stage_pitch(im.H, im.W);
+    if (fold)
+        hipLaunchKernelGGL(conv_wgrad_small_kernel<true>, dim3(blocks), dim3(64 * kSmallWgradWaves), 0,
+                           ctx().stream, g, im, kpw, per_wave, sp);
+    else
+        hipLaunchKernelGGL(conv_wgrad_small_kernel<false>, dim3(blocks), dim3(64 * kSmallWgradWaves), 0,
+                           ctx().stream, g, im, kpw, per_wave, sp);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
 int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
                    const vkhip_operand& wd, float* out, const vkhip_unfold& p, const float* bias,
                    int64_t bias_stride, bool relu) {
@@ -2573,6 +2803,16 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
         g.c = out;
         return launch_exact(g, static_cast<uint32_t>(batch), B_IMGT, im);
     }
+    if (wgrad_small_fits(gr, gd, ck, m, L, im, xd.ne[1])) {
+        publish("matmul.kernel", "conv2d_weight_grad", "conv_wgrad_small_window",
+                "gemm_mfma_implicit_im2col_t", "C*kh*kw <= 32: the image staged in LDS, one workgroup per image",
+                static_cast<int64_t>(batch), static_cast<int64_t>(ck));
+        im.x = x;
+        im.sn = xd.nb[0];
+        im.L = static_cast<uint32_t>(L);
+        return launch_wgrad_small(false, gr, gd, im, m, n, static_cast<uint32_t>(batch),
+                                  static_cast<uint32_t>(L / 32), out);
+    }
     uint32_t splits, chunk;
     TileChoice tile;
     gemm_plan(static_cast<uint32_t>(batch), m, n, k, 0, splits, chunk, tile);
@@ -2694,6 +2934,33 @@ int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float*
         td.nb[2] = static_cast<int64_t>(ck);
         td.nb[3] = 1;
         return launch_reduce(VKHIP_REDUCE_SUM, tmp, td, 0x2u, out);
+    }
+    if (wgrad_small_fits(gr, gd, ck, cout, L, im, xd.ne[1])) {
+        // K-tiles per workgroup: an image's, halved (keeping whole K-tiles
+        // per wave) while that leaves fewer than 256 workgroups; at most 511
+        // partials for the fold
+        const uint32_t tpi = static_cast<uint32_t>(L / 32);
+        uint32_t kpw = tpi;
+        while (kpw % 2 == 0 && kpw >= 2 * kSmallWgradWaves && batch * tpi / kpw < 256) kpw /= 2;
+        const uint64_t parts = batch * tpi / kpw;
+        if (parts <= 511) {
+            publish("matmul.kernel", "conv2d_weight_grad_sum", "conv_wgrad_small_window_folded",
+                    "batch_folded_into_k", "C*kh*kw <= 32: the image staged in LDS, partials per K range",
+                    static_cast<int64_t>(parts), static_cast<int64_t>(ck));
+            im.x = x;
+            im.sn = xd.nb[0];
+            im.L = static_cast<uint32_t>(L);
+            const uint64_t out_elems = static_cast<uint64_t>(cout) * ck;
+            float* target = out;
+            if (parts > 1) {
+                const int st = workspace(out_elems * parts * sizeof(float), &target);
+                if (st != VKHIP_OK) return st;
+            }
+            const int st = launch_wgrad_small(true, gr, gd, im, cout, static_cast<uint32_t>(ck),
+                                              static_cast<uint32_t>(batch), kpw, target);
+            if (st != VKHIP_OK || parts == 1) return st;
+            return launch_split_k_reduce(target, out, out_elems, static_cast<uint32_t>(parts));
+        }
     }
     const uint32_t m = cout, n = static_cast<uint32_t>(ck), k = static_cast<uint32_t>(k64);
     uint32_t splits, chunk;
