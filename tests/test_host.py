@@ -128,11 +128,14 @@ def test_split_k_plan_rules():
     # one round of 256 workgroups, then twice the partitions for pairs (two K
     # streams per workgroup) when each keeps >= 8 K-tiles and the pairs still
     # fit one round: 4 tiles x 64 -> 128 partitions of 16 K-tiles (64 pairs
-    # per tile); 7 tiles x 35 -> 64 partitions of 8 (32 pairs per tile)
+    # per tile); unless 128x64 tiles, three workgroups per CU, promise less
+    # matrix-core time: 13 such tiles x 57 partitions of 9 K-tiles for
+    # 128x784x16384 (784 columns pad to 832 instead of 896)
     assert plan(1, 256, 256, 65536) == (128, 16)
-    assert plan(1, 128, 784, 16384) == (64, 8)
-    # partitions that would drop below 8 K-tiles stay one per workgroup
-    assert plan(1, 256, 256, 16384) == (64, 8)
+    assert plan(1, 128, 784, 16384) == (57, 9)
+    # partitions below 8 K-tiles are not paired: 8 tiles of 128x64 x 86
+    # partitions of 6 against 4 tiles x 64 unpaired partitions of 8
+    assert plan(1, 256, 256, 16384) == (86, 6)
     # K of 4 K-tiles or fewer is never split (the fold would cost more)
     assert plan(1, 64, 10, 128)[0] == 1 and plan(1, 128, 256, 100)[0] == 1
     assert plan(1, 128, 100, 256)[0] > 1

@@ -1827,7 +1827,7 @@ int launch_gemv(const float* a, int64_t lda, const float* x, int64_t incx, float
 //    partitions of 64x64 tiles), else with 64x64 tiles (512^3: 11 us as 4
 //    partitions, 16 us as 8).
 int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_request,
-              uint32_t& splits, uint32_t& chunk, TileChoice& tile) {
+              uint32_t& splits, uint32_t& chunk, TileChoice& tile, bool narrow_split = false) {
     constexpr uint32_t BK = 32;
     const uint32_t cu = ctx().ready ? static_cast<uint32_t>(ctx().caps.compute_units) : 256u;
     const uint64_t t128 = static_cast<uint64_t>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
@@ -1886,7 +1886,29 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
         uint32_t s2 = 1, c2 = ktiles;
         plan_split_k(static_cast<uint32_t>(tiles), ktiles, static_cast<uint64_t>(m) * n * batch,
                      2 * cu, 0, s2, c2);
-        if (s2 > splits && c2 >= 8 && tiles * ((s2 + 1) / 2) <= cu) {
+        const bool pair_ok = s2 > splits && c2 >= 8 && tiles * ((s2 + 1) / 2) <= cu;
+        // gemm()'s direct kernels also run 128x64 tiles, three workgroups per
+        // CU (narrow_split): a split over those pads N less (784 columns: 832
+        // against 896) and fills three slots per CU instead of one paired
+        // workgroup. Taken when its estimated matrix-core time per CU is
+        // lower: 128x64 K-tiles per CU over the fraction of the time the
+        // matrix cores do useful work, fold included (paired 128x128 0.75,
+        // unpaired one workgroup per CU 0.60, three 128x64 per CU 0.75; the
+        // last from 128x784x16384 as 57 partitions of 9 K-tiles, 39.9 us
+        // against 44.8 as 32 pairs of 8, and 256x256x65536 as 94 partitions
+        // of 22, 79.8 us against 78.3 as 64 pairs of 16, which stays paired).
+        const uint64_t t6 = static_cast<uint64_t>(ceil_div(m, 128)) * ceil_div(n, 64) * batch;
+        uint32_t s3 = 1, c3 = ktiles;
+        if (narrow_split && t6 <= 0xffffffffull)
+            plan_split_k(static_cast<uint32_t>(t6), ktiles, static_cast<uint64_t>(m) * n * batch, 3 * cu, 0,
+                         s3, c3);
+        const double cost_now = pair_ok ? 4.0 * c2 / 0.75 : 2.0 * chunk / 0.60;
+        const uint64_t rounds3 = (t6 * s3 + 3ull * cu - 1) / (3ull * cu);
+        const double cost3 = static_cast<double>(rounds3) * 3.0 * c3 / 0.75;
+        if (narrow_split && s3 > 1 && c3 >= 4 && cost3 < cost_now) {
+            splits = s3;
+            chunk = c3;
+        } else if (pair_ok) {
             splits = s2;
             chunk = c2;
             tile.pair = true;
@@ -2021,7 +2043,7 @@ static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, co
 
     uint32_t splits, chunk;
     TileChoice tile;
-    gemm_plan(static_cast<uint32_t>(batch), m, n, k, split_req, splits, chunk, tile);
+    gemm_plan(static_cast<uint32_t>(batch), m, n, k, split_req, splits, chunk, tile, true);
     {
         const int64_t cus = ctx().ready ? ctx().caps.compute_units : 256;
         publish("matmul.kernel", "matmul", tile.bm == 128 ? "gemm_mfma_128x128" : "gemm_mfma_64x64",
@@ -3172,7 +3194,7 @@ extern "C" int vkhip_gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t 
                                int32_t split_request, uint32_t* out_splits, uint32_t* out_chunk) {
     uint32_t s, c;
     vkhip::TileChoice t;
-    vkhip::gemm_plan(batch, m, n, k, split_request, s, c, t);
+    vkhip::gemm_plan(batch, m, n, k, split_request, s, c, t, true);
     if (out_splits) *out_splits = s;
     if (out_chunk) *out_chunk = c;
     return VKHIP_OK;
