@@ -1048,9 +1048,13 @@ __host__ __device__ __forceinline__ uint32_t gather_offset(const Im2colB& im, co
 // IMG loader: [128,64,32,32] -> 128 channels 0.199 -> 0.215 ms.)
 enum ConvDirect { CD_WGRAD = 1, CD_WGRAD_FOLD = 2 };
 
-template <int CD>
+template <int CD, int BN = 128>
 __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im) {
-    constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
+    static_assert(BN == 128 || BN == 64, "128x128 or 128x64 tiles");
+    constexpr int BM = 128, BK = 32, LDK = BK + 4, QN = BK / 8;
+    constexpr int NS = BN / 32;  // column sets: adjacent columns per lane
+    constexpr int NH = BN / 64;  // gathered B columns per lane
+    using BV = float __attribute__((ext_vector_type(NS)));
     using LA = TileLoader<BM, BK, KCD>;
     __shared__ __attribute__((aligned(16))) float lds[2][BM * LDK + BK * BN];
 
@@ -1071,17 +1075,17 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
     // K of one image (A's k extent per image)
     const uint32_t kimg = CD == CD_WGRAD_FOLD ? im.L : g.k;
 
-    // this lane's two B columns j = col0 + 64 h + lane: channel and window element
-    GatherCol col_of[2];
+    // this lane's B columns j = col0 + 64 h + lane: channel and window element
+    GatherCol col_of[NH];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) col_of[h] = gather_col(im, col0 + 64 * h + lane, g.n);
+    for (int h = 0; h < NH; ++h) col_of[h] = gather_col(im, col0 + 64 * h + lane, g.n);
 
     uint32_t voa[BM / 32];
     kcd_offsets<BM>(voa, wave, lane, g.sam, row0, g.m);
 
-    f32x16 acc[4];
+    f32x16 acc[NS];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[s][r] = 0.0f;
 
@@ -1091,7 +1095,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
         auto gather_row = [&](__amdgpu_buffer_rsrc_t img, int rr, bool kok, int32_t sh_k, int32_t sw_k,
                               int32_t so4_k) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < NH; ++h) {
                 const uint32_t off = gather_offset(im, col_of[h], sh_k, sw_k, so4_k, kok);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     img,
@@ -1141,14 +1145,13 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
         const int cur = (kt - kt0) & 1;
         if (kt + 1 < kt1) load_tile(kt + 1, cur ^ 1);
         const float* As = lds[cur] + (wm0 + lrow) * BK;
-        const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + 4 * lrow;
+        const float* Bs = lds[cur] + BM * LDK + kh * 16 * BN + NS * lrow;
         auto a_at = [&](int q) {
             return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)));
         };
-        auto b_at = [&](int q, int st) {
-            return *reinterpret_cast<const f32x4*>(Bs + (4 * q + st) * BN);
-        };
-        f32x4 av[2], bv[2][4];
+        auto b_at = [&](int q, int st) { return *reinterpret_cast<const BV*>(Bs + (4 * q + st) * BN); };
+        f32x4 av[2];
+        BV bv[2][4];
         av[0] = a_at(0);
 #pragma unroll
         for (int st = 0; st < 4; ++st) bv[0][st] = b_at(0, st);
@@ -1163,27 +1166,27 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(GemmArgs g, Im2colB im
 #pragma unroll
             for (int st = 0; st < 4; ++st)
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
+                for (int s = 0; s < NS; ++s)
                     acc[s] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][st], bv[cb][st][s], acc[s],
                                                                   0, 0, 0);
         }
         __syncthreads();
     }
 
-    const uint32_t col = col0 + 4 * lrow;
+    const uint32_t col = col0 + NS * lrow;
     if (col < g.n) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
             if (row < g.m) {
-                f32x4 v;
+                BV v;
 #pragma unroll
-                for (int s = 0; s < 4; ++s) v[s] = acc[s][r];
-                if (g.n % 4 == 0) {
-                    *reinterpret_cast<f32x4*>(cbase + static_cast<uint64_t>(row) * g.n + col) = v;
+                for (int s = 0; s < NS; ++s) v[s] = acc[s][r];
+                if (g.n % NS == 0) {
+                    *reinterpret_cast<BV*>(cbase + static_cast<uint64_t>(row) * g.n + col) = v;
                 } else {
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
+                    for (int s = 0; s < NS; ++s)
                         if (col + s < g.n) cbase[static_cast<uint64_t>(row) * g.n + col + s] = v[s];
                 }
             }
@@ -2771,6 +2774,17 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
 // (autograd.cpp:548-553 through ops.cpp:662-705), with the same plan, K order
 // and split-K fold, hence the same bits. x: [N,C,H,W] any strides; g: [N,
 // Cout, L] with unit position stride; out contiguous [N, Cout, C*kh*kw].
+// Whether conv_direct_kernel runs 128x64 tiles: the rule gemm() applies to
+// its direct kernels (three 128x64 workgroups per CU against two 128x128,
+// 0.94 for the narrower tile's work per CU-second, the fill of the launch's
+// rounds deciding). The tile width does not change the bits.
+static bool wgrad_narrow_tiles(const GemmArgs& g, uint32_t splits, uint64_t batch) {
+    const uint64_t cus = ctx().ready ? static_cast<uint64_t>(ctx().caps.compute_units) : 256u;
+    const uint64_t w128 = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits * batch;
+    const uint64_t w64 = static_cast<uint64_t>(g.tiles_m) * ceil_div(g.n, 64u) * splits * batch;
+    return 0.94 * round_fill(w64, 3 * cus) > round_fill(w128, 2 * cus);
+}
+
 // Whether conv_direct_kernel takes a weight-gradient product: 128x128
 // tiles, the gradient rows 16-byte aligned with whole groups of four
 // positions, and every byte offset of one image's gradient within 2^31.
@@ -2880,12 +2894,18 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
     g.split_stride = splits > 1 ? out_elems : 0;
     int st;
     if (tile.bm == 128 && wgrad_direct_fits(g, k, target)) {
-        // both operands straight into LDS (same bits as the register path)
+        // both operands straight into LDS (same bits as the register path);
+        // 128x64 tiles when their rounds fill the machine better (as in gemm())
+        const bool narrow = wgrad_narrow_tiles(g, splits, batch);
+        if (narrow) g.tiles_n = ceil_div(n, 64u);
         const uint64_t flat = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
         g.flat_splits = splits > 1 && flat <= 0x7fffffffull ? splits : 0;
         const dim3 grid = g.flat_splits ? dim3(static_cast<uint32_t>(flat), 1, static_cast<uint32_t>(batch))
                                         : dim3(g.tiles_m * g.tiles_n, splits, static_cast<uint32_t>(batch));
-        hipLaunchKernelGGL(conv_direct_kernel<CD_WGRAD>, grid, dim3(256), 0, ctx().stream, g, im);
+        if (narrow)
+            hipLaunchKernelGGL((conv_direct_kernel<CD_WGRAD, 64>), grid, dim3(256), 0, ctx().stream, g, im);
+        else
+            hipLaunchKernelGGL((conv_direct_kernel<CD_WGRAD, 128>), grid, dim3(256), 0, ctx().stream, g, im);
         VKHIP_LAUNCH_CHECK();
         st = VKHIP_OK;
     } else if (tile.bm == 128)
@@ -2987,7 +3007,7 @@ int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float*
     const uint32_t m = cout, n = static_cast<uint32_t>(ck), k = static_cast<uint32_t>(k64);
     uint32_t splits, chunk;
     TileChoice tile;
-    gemm_plan(1, m, n, k, 0, splits, chunk, tile);
+    gemm_plan(1, m, n, k, 0, splits, chunk, tile, true);
     publish("matmul.kernel", "conv2d_weight_grad_sum",
             tile.bm == 128 ? "gemm_mfma_128x128_batch_folded" : "gemm_mfma_64x64_batch_folded",
             "per_image_products_then_batch_sum", "the batch folded into K: one product, no intermediate",
@@ -3026,11 +3046,16 @@ int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float*
     g.split_stride = splits > 1 ? out_elems : 0;
     int st;
     if (tile.bm == 128 && wgrad_direct_fits(g, static_cast<uint32_t>(L), target)) {
+        const bool narrow = wgrad_narrow_tiles(g, splits, 1);
+        if (narrow) g.tiles_n = ceil_div(n, 64u);
         const uint64_t flat = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * splits;
         g.flat_splits = splits > 1 && flat <= 0x7fffffffull ? splits : 0;
         const dim3 grid = g.flat_splits ? dim3(static_cast<uint32_t>(flat), 1, 1)
                                         : dim3(g.tiles_m * g.tiles_n, splits, 1);
-        hipLaunchKernelGGL(conv_direct_kernel<CD_WGRAD_FOLD>, grid, dim3(256), 0, ctx().stream, g, im);
+        if (narrow)
+            hipLaunchKernelGGL((conv_direct_kernel<CD_WGRAD_FOLD, 64>), grid, dim3(256), 0, ctx().stream, g, im);
+        else
+            hipLaunchKernelGGL((conv_direct_kernel<CD_WGRAD_FOLD, 128>), grid, dim3(256), 0, ctx().stream, g, im);
         VKHIP_LAUNCH_CHECK();
         st = VKHIP_OK;
     } else if (tile.bm == 128)
