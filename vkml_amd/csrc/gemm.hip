@@ -769,8 +769,15 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
                     if (g.bias) v = v + g.bias[static_cast<int64_t>(row < g.m ? row : 0) * g.bias_stride];
                     if (g.relu) v = v <= 0.0f ? 0.0f : v;
                 }
-                if (row < g.m && col < g.n)
-                    cbase[static_cast<uint64_t>(row) * g.n + col] = product_epilogue(g, z, row, col, v);
+                if (row < g.m && col < g.n) {
+                    float* at = cbase + static_cast<uint64_t>(row) * g.n + col;
+                    // convolution outputs stream past the L2 (non-temporal):
+                    // they are read next by another kernel, not by this one
+                    if constexpr (BMODE == IMG)
+                        __builtin_nontemporal_store(product_epilogue(g, z, row, col, v), at);
+                    else
+                        *at = product_epilogue(g, z, row, col, v);
+                }
             }
         }
 }

@@ -697,8 +697,10 @@ __global__ __launch_bounds__(256) void max_pool2x2_backward_kernel(
             if (u[i] <= 0.0f) bot[i] = 0.0f;
         }
     }
-    *reinterpret_cast<f32x4_t*>(dst + base) = top;
-    *reinterpret_cast<f32x4_t*>(dst + base + W) = bot;
+    // the image gradient streams past the L2 (non-temporal): the next
+    // kernels read it, this one never does
+    __builtin_nontemporal_store(top, reinterpret_cast<f32x4_t*>(dst + base));
+    __builtin_nontemporal_store(bot, reinterpret_cast<f32x4_t*>(dst + base + W));
 }
 
 // The 2x2 fast path applies to contiguous planes whose width is a multiple of
