@@ -533,6 +533,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
     using LB = TileLoader<BN, BK, BMODE == IMGTB ? IMGT : BMODE>;
 
     __shared__ __attribute__((aligned(16))) float lds[2][(BM + BN) * LDK];
+    // the convolution epilogue's bias rows, read before the K loop so their
+    // latency hides behind it
+    __shared__ float bias_rows[BMODE == IMG ? BM : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -667,6 +670,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
             LB::template load<true>(rb, bbase, g.sbn, g.sbk, col0, g.n, kt * BK, g.k, tid);
         }
     };
+    if constexpr (BMODE == IMG) {
+        if (g.bias && tid < BM) {
+            const uint32_t row = row0 + tid;
+            bias_rows[tid] = g.bias[static_cast<int64_t>(row < g.m ? row : 0) * g.bias_stride];
+        }
+    }
     if (kt0 < kt1) {
         load_tile(kt0, 0);
         if constexpr (AMODE != KCD) LA::store(ra, lds[0], tid);
@@ -766,7 +775,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
                 const uint32_t row = row0 + wm0 + 32 * i + 8 * (r / 4) + 4 * kh + (r % 4);
                 float v = acc[i][j][r];
                 if constexpr (BMODE == IMG) {
-                    if (g.bias) v = v + g.bias[static_cast<int64_t>(row < g.m ? row : 0) * g.bias_stride];
+                    if (g.bias) v = v + bias_rows[row - row0];
                     if (g.relu) v = v <= 0.0f ? 0.0f : v;
                 }
                 if (row < g.m && col < g.n) {
