@@ -1000,7 +1000,9 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
                 BV v;
 #pragma unroll
                 for (int s = 0; s < NS; ++s) v[s] = product_epilogue(g, z, row, col + s, acc[s][r]);
-                *reinterpret_cast<BV*>(cbase + static_cast<uint64_t>(row) * g.n + col) = v;
+                // streamed past the L2 (non-temporal): outputs and split-K
+                // partials are read by later kernels, never by this one
+                __builtin_nontemporal_store(v, reinterpret_cast<BV*>(cbase + static_cast<uint64_t>(row) * g.n + col));
             }
         }
     }
