@@ -497,87 +497,135 @@ def secondary(hip, ops, timer, names=None):
 
 def case_training(name, hip, ops, timer, rng, out):
     """One training config (config 1 "train_mlp" or config 5 "train_cnn") in
-    the three ways training_steps runs it."""
-    only = {"train_mlp": "mlp_784_128_10_b64", "train_cnn": "cifar_cnn_b128"}[name]
+    every mode training_steps runs."""
+    only = {"train_mlp": 1, "train_cnn": 5}[name]
     out.update(training_steps(only=only))
 
 
-def training_steps(steps_mlp: int = 100, steps_cnn: int = 50, only: str | None = None):
-    """BASELINE configs 1 and 5 as training loops on the device: steps/s over
-    the timed steps, each step's loss read back to the host. Three ways to run
-    the same step: "eager" (the host core builds, orders and packs the graph
-    every step), "replay" (the step recorded once, its compute/SGD calls
-    replayed from C, vkhip_program_run) and "graph" (the replay captured once
-    into a HIP graph); all three give the same bits (tests/test_gpu_replay.py).
-    "graph_queued" is "graph" with the loss read back after the last timed
-    step only: every step still uploads its batch and runs the whole forward,
-    backward and update, but the host queues the next step instead of waiting
-    on each loss, so the device runs the steps back to back."""
+TRAIN_MODES = ("dropin", "eager", "replay", "graph", "graph_queued", "exact")
+
+
+def _streams():
+    """tests/golden/streams.py: the configs' seeded data streams, models and
+    the committed CPU-oracle trajectories the parity tests compare against."""
+    golden = ROOT / "tests" / "golden"
+    if str(golden) not in sys.path:
+        sys.path.insert(0, str(golden))
+    import streams
+
+    return streams
+
+
+def training_steps(only: int | None = None, modes=TRAIN_MODES):
+    """BASELINE configs 1 and 5 as training loops on the device, on the very
+    streams the parity tests check (tests/golden/streams.py: 100 steps, a
+    fresh seeded batch per step, all generated before the timed loop), each
+    mode from freshly initialised weights:
+
+      dropin        the reference's node graph only (tensor.reference_graph(),
+                    SGD(fused=False)), built and flushed every step: what
+                    vkML's executor would hand a drop-in HipBackend::compute
+      eager         the host core's rewritten graph, built every step
+      replay        the step recorded once, its calls replayed from C
+      graph         the replay captured once into a HIP graph
+      graph_queued  "graph" with no per-step loss read-back: the host queues
+                    step after step, the last loss is read inside the timed
+                    region
+      exact         "replay" in the exact numerics mode (vkhip_set_numerics):
+                    every node the oracle's bits
+
+    Step 0 (the recording, for the replayed modes) is untimed; steps 1-99 are
+    timed by wall clock, each step uploading its batch and (but for
+    graph_queued) reading its loss back. Every mode reports its largest loss
+    drift over the 100 steps from the committed oracle trajectory
+    (tests/golden/config*_losses.json) and the step where it occurs;
+    graph_queued reads only its last loss, which must be the graph mode's
+    bits, and reports the graph mode's drift. `oracle_libm_drift` is the
+    distance between the oracle trajectory with its named exp/log and with
+    the platform libm's (the reference's std::exp / std::log): how far two
+    valid builds of the reference's own CPU arithmetic separate."""
     from vkml_amd import nn, optim
     from vkml_amd import tensor as T
 
+    S = _streams()
+    hip = T.default_backend().hip
     res = {}
-    rng = np.random.default_rng(20260726)
-    configs = {
-        "mlp_784_128_10_b64": (lambda: nn.Sequential(nn.Flatten(), nn.Linear(784, 128), nn.ReLU(),
-                                                      nn.Linear(128, 10)),
-                               (64, 1, 28, 28), 10, 0.1, steps_mlp, (0.0, 1.0)),
-        "cifar_cnn_b128": (lambda: nn.Sequential(
-            nn.Conv2d(3, 64, 3, padding=1), nn.ReLU(), nn.MaxPool2d(2),
-            nn.Conv2d(64, 128, 3, padding=1), nn.ReLU(), nn.MaxPool2d(2), nn.Flatten(),
-            nn.Linear(8192, 256), nn.ReLU(), nn.Linear(256, 100)),
-            (128, 3, 32, 32), 100, 0.01, steps_cnn, (-1.0, 1.0)),
-    }
-    for name, (make, shape, classes, lr, steps, (lo, hi)) in configs.items():
-        if only is not None and name != only:
+    for num, cfg in S.CONFIGS.items():
+        if only is not None and num != only:
             continue
-        data = [(rng.uniform(lo, hi, shape).astype(np.float32),
-                 rng.integers(0, classes, shape[0]).astype(np.int64)) for _ in range(4)]
-        out = {}
-        for mode in ("eager", "replay", "graph", "graph_queued"):
-            nn.manual_seed(20260726)
-            model = make()
-            opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
+        data = list(S.batches(cfg))
+        want = S.oracle_losses(cfg)
+        envelope, env_step = S.max_drift(want, S.oracle_losses(cfg, libm=True))
+        entry = {"steps": cfg.steps, "timed_steps": cfg.steps - 1, "stream": "tests/golden/streams.py",
+                 "oracle_fixture": S.fixture_path(cfg).name,
+                 "oracle_libm_drift": envelope, "oracle_libm_drift_step": env_step}
+        for mode in modes:
+            nn.manual_seed(cfg.model_seed)
+            ref_ctx = T.reference_graph() if mode == "dropin" else None
+            if mode == "exact":
+                hip.set_numerics("exact")
+            try:
+                if ref_ctx:
+                    ref_ctx.__enter__()
+                model = S.model(cfg)
+                opt = optim.SGD(model.parameters(), lr=cfg.lr, momentum=cfg.momentum,
+                                fused=mode != "dropin")
 
-            def fn(x, y):
-                opt.zero_grad()
-                loss = nn.cross_entropy(model(x), y)
-                loss.backward()
-                opt.step()
-                return loss
+                def fn(x, y):
+                    opt.zero_grad()
+                    loss = nn.cross_entropy(model(x), y)
+                    loss.backward()
+                    opt.step()
+                    return loss
 
-            if mode == "eager":
-                def step(i):
-                    x, y = data[i % 4]
-                    return fn(T.tensor(x), T.tensor(y)).item()
+                losses = []
+                captured = None
+                if mode in ("dropin", "eager"):
+                    def step(i):
+                        x, y = data[i]
+                        return fn(T.tensor(x), T.tensor(y)).item()
+                    losses.append(step(0))
+                else:
+                    captured = T.CapturedStep(fn, *data[0], graph=mode.startswith("graph"))
+                    losses.append(float(captured.first[0]))
+                    queued = mode == "graph_queued"
+
+                    def step(i):
+                        out = captured(*data[i], read=not queued)
+                        return None if out is None else float(out[0])
+                hip.synchronize()
+                t0 = time.perf_counter()
+                for i in range(1, cfg.steps):
+                    losses.append(step(i))
+                if mode == "graph_queued":
+                    losses[-1] = float(captured.outputs_now()[0])
+                dt = time.perf_counter() - t0
+            finally:
+                if ref_ctx:
+                    ref_ctx.__exit__(None, None, None)
+                if mode == "exact":
+                    hip.set_numerics("fast")
+            timed = cfg.steps - 1
+            out = {"ms_per_step": round(dt * 1e3 / timed, 4), "steps_per_s": round(timed / dt, 2),
+                   "last_loss": losses[-1]}
+            if mode == "graph_queued":
+                same = np.float32(losses[-1]).tobytes() == np.float32(entry["graph"]["last_loss"]).tobytes()
+                out["last_loss_same_bits_as_graph"] = bool(same)
+                out["max_loss_drift_vs_oracle"] = entry["graph"]["max_loss_drift_vs_oracle"] if same else None
+                out["drift_from"] = "graph (same steps; last loss checked bit for bit)"
             else:
-                captured = T.CapturedStep(fn, *data[0], graph=mode.startswith("graph"))
-                queued = mode == "graph_queued"
-
-                def step(i):
-                    out = captured(*data[i % 4], read=not queued)
-                    return None if out is None else float(out[0])
-            # (queued: the last loss is read after the timed loop's final
-            # step, inside the timed region)
-            # the recording is step 0 of the replayed runs: every mode then
-            # takes the same steps on the same batches, and reports the same
-            # last loss
-            for i in range(0 if mode == "eager" else 1, 3):
-                step(i)
-            if mode == "graph_queued":
-                captured.outputs_now()  # the warm-up steps are done
-            t0 = time.perf_counter()
-            for i in range(3, 3 + steps):
-                last = step(i)
-            if mode == "graph_queued":
-                last = float(captured.outputs_now()[0])
-            dt = time.perf_counter() - t0
-            out[mode] = {"ms_per_step": round(dt * 1e3 / steps, 4),
-                         "steps_per_s": round(steps / dt, 2), "last_loss": round(last, 5)}
-            if mode != "eager":
-                out[mode].update(captured.info())
+                got = np.array(losses, np.float32)
+                d, at = S.max_drift(got, want)
+                out["max_loss_drift_vs_oracle"] = d
+                out["max_drift_step"] = at
+                out["steps_within_1e-4"] = int(np.argmax(np.abs(got.astype(np.float64) - want) > 1e-4)) \
+                    if d > 1e-4 else cfg.steps
+                out["bit_identical_steps"] = int(np.sum(got.view(np.uint32) == want.view(np.uint32)))
+            if captured is not None:
+                out.update(captured.info())
                 captured.close()
-        res[name] = {"steps": steps, **out}
+            entry[mode] = out
+        res[cfg.key] = entry
     return res
 
 

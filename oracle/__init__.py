@@ -71,6 +71,8 @@ def load():
         "or_split_k_fold": (None, [c_void_p, c_void_p, c_uint64, c_uint32]),
         "or_compute": (c_int, [c_void_p, ctypes.c_size_t, c_int]),
         "or_exp_vec": (None, [c_void_p, c_void_p, c_int64, c_int]),
+        "or_set_libm_math": (None, [c_int]),
+        "or_get_libm_math": (c_int, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -280,6 +282,24 @@ def logf(x: np.ndarray) -> np.ndarray:
     y = np.empty_like(x)
     load().or_exp_vec(_ptr(x), _ptr(y), x.size, 1)
     return y
+
+
+class libm_math:
+    """Context manager: inside it the oracle's exp and log (softmax,
+    log-softmax, cross-entropy, EXP/LOG nodes) call the platform libm's expf /
+    logf, as the reference's std::exp / std::log on float do
+    (kernels_reduce.cpp:233,240; kernels_elementwise.cpp:192,196), instead of
+    the named correctly rounded methods. Used to measure the spread between two
+    valid builds of the reference's CPU arithmetic; not for parity fixtures."""
+
+    def __enter__(self):
+        self._prev = load().or_get_libm_math()
+        load().or_set_libm_math(1)
+        return self
+
+    def __exit__(self, *exc):
+        load().or_set_libm_math(self._prev)
+        return False
 
 
 def split_k_fold(ws: np.ndarray, splits: int) -> np.ndarray:

@@ -62,11 +62,24 @@ float or_pairwise_sum(const float* v, int64_t n) { return pairwise(v, 0, n); }
  *   log: x = m 2^e, m in [sqrt(1/2), sqrt(2)), s = (m-1)/(m+1),
  *        log m = 2 atanh s = 2s(1 + s^2/3 + ... + s^24/25), plus e ln2.
  * Each is the correctly rounded float except within ~2^-27 ulp of a rounding
- * midpoint (pinned against mpmath in tests/test_oracle.py). */
+ * midpoint (pinned against mpmath in tests/test_oracle.py).
+ *
+ * or_set_libm_math(1) switches both to the platform libm's expf / logf, which
+ * is what the reference's std::exp / std::log on float call: the oracle then
+ * runs the reference's CPU arithmetic as built against this libm. It exists
+ * to measure how far two equally valid exp/log choices move a whole training
+ * trajectory; parity fixtures use the named methods (the default). */
 /* ------------------------------------------------------------------------ */
 float or_logf(float xf);
 
+static int or_libm_math = 0;
+
+void or_set_libm_math(int on) { or_libm_math = on != 0; }
+
+int or_get_libm_math(void) { return or_libm_math; }
+
 float or_expf(float xf) {
+    if (or_libm_math) return expf(xf);
     if (xf != xf) return xf + xf;
     if (xf > 89.0f) return INFINITY;
     if (xf < -104.0f) return 0.0f;
@@ -89,6 +102,7 @@ void or_exp_vec(const float* x, float* y, int64_t n, int log_mode) {
 }
 
 float or_logf(float xf) {
+    if (or_libm_math) return logf(xf);
     if (xf != xf) return xf + xf;
     if (xf < 0.0f) return NAN;
     if (xf == 0.0f) return -INFINITY;

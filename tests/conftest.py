@@ -374,59 +374,36 @@ def golden(name: str) -> dict:
     return {k: conv(v) for k, v in _GOLDEN[name].items()}
 
 
-# ---- BASELINE config 5 (CIFAR-100-shaped CNN) training trajectory ----
+# ---- BASELINE configs 1 and 5: the training streams (tests/golden/streams.py) ----
 
-CONFIG5_STEPS = 100
-CONFIG5_BATCH = 128
-CONFIG5_LR = 0.01
-CONFIG5_MOMENTUM = 0.9
-CONFIG5_LOSSES = Path(__file__).parent / "golden" / "config5_cnn_losses.json"
+sys.path.insert(0, str(Path(__file__).parent / "golden"))
+import streams  # noqa: E402
+
+CONFIG5_STEPS = streams.CONFIG5.steps
+CONFIG5_BATCH = streams.CONFIG5.batch
+CONFIG5_LR = streams.CONFIG5.lr
+CONFIG5_MOMENTUM = streams.CONFIG5.momentum
+CONFIG5_LOSSES = streams.fixture_path(streams.CONFIG5)
 
 
 def config5_model(backend):
     """conv(3->64,3x3)-ReLU-pool, conv(64->128,3x3)-ReLU-pool, flatten,
     Linear(8192,256)-ReLU, Linear(256,100), Kaiming-uniform from SEED."""
-    from vkml_amd import nn
-
-    nn.manual_seed(SEED)
-    return nn.Sequential(
-        nn.Conv2d(3, 64, 3, padding=1, backend=backend), nn.ReLU(), nn.MaxPool2d(2),
-        nn.Conv2d(64, 128, 3, padding=1, backend=backend), nn.ReLU(), nn.MaxPool2d(2),
-        nn.Flatten(), nn.Linear(8192, 256, backend=backend), nn.ReLU(),
-        nn.Linear(256, 100, backend=backend))
+    return streams.model(streams.CONFIG5, backend)
 
 
 def config5_batches(steps: int = CONFIG5_STEPS, batch: int = CONFIG5_BATCH):
     """A fresh batch per step, x ~ U[-1, 1) [batch, 3, 32, 32] and labels
-    uniform in [0, 100), from one seeded generator (generated lazily)."""
-    rng = np.random.default_rng(SEED + batch)
-    for _ in range(steps):
-        yield (rng.uniform(-1, 1, (batch, 3, 32, 32)).astype(np.float32),
-               rng.integers(0, 100, batch).astype(np.int64))
+    uniform in [0, 100), from one generator seeded SEED + batch."""
+    return streams.batches(streams.CONFIG5, steps, batch)
 
 
 def config5_train(backend, steps: int = CONFIG5_STEPS, batch: int = CONFIG5_BATCH) -> np.ndarray:
     """Per-step losses (float32) of config 5's SGD-momentum loop on `backend`."""
-    from vkml_amd import nn, optim
-    from vkml_amd import tensor as T
-
-    model = config5_model(backend)
-    opt = optim.SGD(model.parameters(), lr=CONFIG5_LR, momentum=CONFIG5_MOMENTUM)
-    losses = []
-    for x, y in config5_batches(steps, batch):
-        opt.zero_grad()
-        loss = nn.cross_entropy(model(T.tensor(x, backend=backend)), T.tensor(y, backend=backend))
-        loss.backward()
-        opt.step()
-        losses.append(loss.item())
-    return np.array(losses, np.float32)
+    return streams.train(streams.CONFIG5, backend, steps, batch)
 
 
 def config5_golden_losses() -> np.ndarray:
     """The oracle's 100-step config-5 trajectory, written by
-    tests/golden/make_config5_losses.py (float32 bit patterns)."""
-    import json
-
-    data = json.loads(CONFIG5_LOSSES.read_text())
-    bits = np.array([int(h, 16) for h in data["losses_f32_bits"]], np.uint32)
-    return bits.view(np.float32)
+    tests/golden/make_training_losses.py (float32 bit patterns)."""
+    return streams.oracle_losses(streams.CONFIG5)

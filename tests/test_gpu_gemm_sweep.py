@@ -133,6 +133,9 @@ EXACT_CASES = [  # (A shape, B shape): 2-D, ragged, K not a multiple of 32, batc
     ((33, 1000), (1000, 65)), ((128, 4097), (4097, 40)), ((3, 48), (48, 5)), ((70, 33), (33, 70)),
     ((2, 3, 17, 100), (3, 100, 9)), ((4, 64, 27), (27, 96)), ((256, 256), (256, 256)),
     ((16, 65536), (65536, 8)),
+    # config 5's Linear(8192, 256) forward: 8 output tiles, K split into 64
+    # subtrees folded by the carry stack
+    ((128, 8192), (8192, 256)),
 ]
 
 

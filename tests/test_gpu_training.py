@@ -83,25 +83,48 @@ def test_config5_cnn_loss_drift(backends, batch, steps):
     assert drift.max() <= 1e-4, f"max loss drift {drift.max():.3g} at step {drift.argmax()}"
 
 
+# How far the fast numerics may move config 5's 100-step trajectory, as a
+# multiple of how far the reference's own CPU arithmetic moves it between two
+# valid libm builds (the oracle with its named, correctly rounded exp/log
+# against the oracle with glibc's expf/logf: tests/golden/config5_cnn_losses
+# and config5_cnn_losses_libm). Both trajectories are the reference's CPU
+# algorithm; the fast path differs from either by GEMM accumulation order
+# (within 1e-5*sqrt(K) per product) and <= 2-ulp transcendentals.
+FAST_PATH_ENVELOPE_FACTOR = 2.0
+
+
 @pytest.mark.timeout(300)
 def test_config5_cnn_fast_path_tracks_the_oracle(backends):
-    """BASELINE config 5 at full batch (128), a fresh batch each step, on the
-    default (matrix-core) numerics against the CPU oracle's trajectory (the
-    committed fixture tests/golden/config5_cnn_losses.json, about 6 minutes
-    of oracle work, written by tests/golden/make_config5_losses.py and
-    re-derived live for its first steps by tests/test_config5_fixture.py).
-    The first 15 steps stay within 1e-4. Later steps separate: this loop's
-    trajectory is chaotic (max-pool and ReLU switch on rounding-level
-    differences), so GEMM accumulation order alone, or a 1-ulp difference in
-    one exponential, grows to ~1e-3 by step ~80; the 100-step bar is met in
-    the exact numerics mode (test_config5_exact_numerics_100_steps)."""
+    """BASELINE config 5 at full batch (128), a fresh batch each step, all 100
+    steps on the default (matrix-core) numerics against the CPU oracle's
+    committed trajectory (tests/golden/config5_cnn_losses.json, written by
+    tests/golden/make_training_losses.py and re-derived live for its first
+    steps by tests/test_training_fixtures.py).
+
+    The loop is chaotic at the rounding level (max-pool window choices and
+    ReLU signs switch on last-bit differences): the oracle itself, with only
+    its exp/log swapped for glibc's (1-ulp differences in ~1e-3 of the calls),
+    agrees bit for bit for 11 steps, leaves 1e-4 at step 24 and is 1.8e-3
+    off at step 86 (tests/test_training_fixtures.py pins these). So:
+      - the first 15 steps stay within the north star's 1e-4;
+      - all 100 stay within FAST_PATH_ENVELOPE_FACTOR times that
+        oracle-against-oracle spread.
+    The north star's 1e-4 for all 100 steps is met bit for bit by the exact
+    numerics mode (test_config5_exact_numerics_100_steps)."""
+    import streams as S
+
     dev, _ = backends
-    got = config5_train(dev, steps=15)
-    want = config5_golden_losses()[:15]
+    got = config5_train(dev)
+    want = config5_golden_losses()
+    envelope, env_at = S.max_drift(want, S.oracle_losses(S.CONFIG5, libm=True))
     drift = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    print(f"config5 fast path, 15 steps: max drift {drift.max():.3g} at step {drift.argmax()}",
-          flush=True)
-    assert drift.max() <= 1e-4, f"max loss drift {drift.max():.3g} at step {drift.argmax()}"
+    print(f"config5 fast path, 100 steps: max drift {drift.max():.3g} at step {drift.argmax()}; "
+          f"first 15 steps {drift[:15].max():.3g}; oracle named-vs-libm envelope {envelope:.3g} "
+          f"(step {env_at}); ratio {drift.max() / envelope:.3g}", flush=True)
+    assert drift[:15].max() <= 1e-4, f"max loss drift {drift[:15].max():.3g} at step {drift[:15].argmax()}"
+    assert drift.max() <= FAST_PATH_ENVELOPE_FACTOR * envelope, \
+        f"max loss drift {drift.max():.3g} at step {drift.argmax()} against envelope {envelope:.3g}"
+    assert got[-1] < got[0] + 0.05  # training does not diverge
 
 
 @pytest.mark.timeout(900)
@@ -270,6 +293,40 @@ def test_exact_graph_rewrites_keep_the_device_bits(backends, model):
     assert on[0].tobytes() == off[0].tobytes()
     for a, b in zip(on[1], off[1]):
         assert a.tobytes() == b.tobytes()
+
+
+@pytest.mark.parametrize("rows", [16384, 65536])
+def test_weight_grad_layout_rewrite_keeps_bits_at_split_shapes(backends, rows):
+    """A Linear(784, 128) weight gradient over 16384 and 65536 batch rows:
+    the K-dominant products BASELINE config 3 names (128 x 784 x 16384). The
+    device plans 128 x 784 and 784 x 128 over that K with different split-K
+    partitions, so the in-place layout (g^T @ x) is not the reference
+    layout's (x^T @ g)^T bits there; the host core must then keep the
+    reference layout. The weight gradient is the same bytes with the rewrite
+    on and off."""
+    dev, _ = backends
+    from vkml_amd import ops
+
+    assert ops.gemm_plan(1, 128, 784, rows) != ops.gemm_plan(1, 784, 128, rows)
+    rng = np.random.default_rng(SEED + rows)
+    x = rng.standard_normal((rows, 784)).astype(np.float32)
+    g = rng.standard_normal((rows, 128)).astype(np.float32)
+    saved = T.WEIGHT_GRAD_IN_PLACE_LAYOUT
+    grads = []
+    try:
+        for flag in (True, False):
+            T.WEIGHT_GRAD_IN_PLACE_LAYOUT = flag
+            nn.manual_seed(SEED)
+            lin = nn.Linear(784, 128, bias=False, backend=dev)
+            y = lin(T.tensor(x, backend=dev))
+            y.backward(T.tensor(g, backend=dev))
+            grads.append(lin.weight.grad.numpy())
+    finally:
+        T.WEIGHT_GRAD_IN_PLACE_LAYOUT = saved
+    assert grads[0].tobytes() == grads[1].tobytes()
+    # and both are the product within the GEMM bar (float64 check on rows)
+    want = (g.astype(np.float64).T @ x.astype(np.float64))
+    assert normwise_rel_err(grads[0], want) <= gemm_tolerance(rows)
 
 
 def test_bias_gradient_reduce_is_bit_exact(backends):

@@ -209,6 +209,61 @@ def test_graph_rewrites_keep_the_oracle_bits(cpu, model):
         assert a.tobytes() == b.tobytes()
 
 
+class _RecordingOracle(OracleBackend):
+    """The oracle backend, noting the op of every node it is handed."""
+
+    def __init__(self):
+        super().__init__()
+        self.ops = []
+        self.flushes = 0
+
+    def compute(self, nodes, count: int) -> None:
+        self.ops.extend(int(nodes[i].op) for i in range(count))
+        self.flushes += 1
+        super().compute(nodes, count)
+
+
+@pytest.mark.parametrize("model", ["mlp", "cnn"])
+def test_reference_graph_hands_the_backend_reference_nodes_only(model):
+    """Inside tensor.reference_graph() (and with SGD(fused=False)) a training
+    step reaches the backend as the reference executor's node stream: every
+    node a reference OpKind (ordinals below 96; the backend-extension nodes
+    start there), im2col/col2im for convolutions, and the same losses and
+    parameters, bit for bit, as the rewritten graph."""
+    fn, batches = (mlp_model, mlp_batches(2)) if model == "mlp" else \
+        (config5_model, list(config5_batches(2, 4)))
+    res = {}
+    for ref in (True, False):
+        be = _RecordingOracle()
+        net = fn(be)
+        opt = optim.SGD(net.parameters(), lr=0.1, momentum=0.9, fused=not ref)
+        losses = []
+        for x, y in batches:
+            ctx = T.reference_graph() if ref else None
+            if ctx:
+                ctx.__enter__()
+            try:
+                opt.zero_grad()
+                loss = nn.cross_entropy(net(T.tensor(x, backend=be)), T.tensor(y, backend=be))
+                loss.backward()
+                opt.step()
+                losses.append(np.float32(loss.item()))
+            finally:
+                if ctx:
+                    ctx.__exit__(None, None, None)
+        res[ref] = (np.array(losses), [p.numpy() for p in net.parameters()], be)
+    ops_ref = set(res[True][2].ops)
+    assert max(ops_ref) < 96, sorted(o for o in ops_ref if o >= 96)
+    assert max(set(res[False][2].ops)) >= 96  # the rewritten graph does use extension nodes
+    if model == "cnn":
+        assert T.OP["IM2COL"] in ops_ref and T.OP["COL2IM"] in ops_ref
+    # the switches are restored on exit
+    assert T.IMPLICIT_CONV and T.FUSED_CROSS_ENTROPY and T.BACKWARD_FLUSH_EVERY > 0
+    assert res[True][0].tobytes() == res[False][0].tobytes()
+    for a, b in zip(res[True][1], res[False][1]):
+        assert a.tobytes() == b.tobytes()
+
+
 @pytest.mark.parametrize("rows,fan_in,hidden,fan_out", [MLP2_SHAPES[0], MLP2_SHAPES[-1]])
 def test_matmul_relu_gradient_node_is_the_two_nodes(cpu, rows, fan_in, hidden, fan_out):
     """The hidden relu's gradient of relu(x @ w1.T + b1) @ w2.T as one

@@ -1648,6 +1648,162 @@ __global__ __launch_bounds__(256) void gemm_exact_kernel(GemmArgs g, int depth, 
     }
 }
 
+// The exact arm's throughput kernel: the same sums as gemm_exact_kernel (each
+// product rounded on its own, each leaf summed sequentially from 0.0, leaf sums
+// folded by a carry stack), register-blocked the way the reference's default
+// gemm_reg.comp:108-274 is, but for wave64 and a 16-lane-wide VALU:
+//  - a 64 x 64 output tile per 256-thread workgroup, thread (tx, ty) owning
+//    rows 4ty..4ty+3 and columns 4tx..4tx+3 (16 outputs);
+//  - a leaf's A slice is staged k-major ([k][row]) and B's [k][col], so every
+//    multiply-add step reads its 4 A and 4 B values as two 16-byte LDS reads
+//    (one per 16 rounded multiplies and 16 rounded adds; a wave's A read is 4
+//    broadcast addresses, its B read 256 contiguous bytes);
+//  - the next leaf's operands are loaded into registers while the current
+//    leaf is summed, and stored to the other LDS buffer after it (one barrier
+//    per leaf);
+//  - the carry stack holds LV levels per output, LV >= depth + 1 chosen at
+//    launch from K (the reference sizes its stack from K too,
+//    gemm_reg.comp:14-29), instead of enough levels for any 32-bit K.
+// Staging reads follow the operands' unit stride: along k (a_kfast / b_kfast)
+// or along the rows / columns.
+constexpr int kExact4Ld = 68;  // LDS row pitch in floats (16-byte aligned rows)
+
+template <int LV>
+__device__ __forceinline__ void exact_push_lv(float (&stack)[LV], uint32_t count, float block) {
+    bool carry = true;
+#pragma unroll
+    for (int l = 0; l < LV; ++l) {
+        if (carry) {
+            if ((count >> l) & 1u) {
+                block = __fadd_rn(stack[l], block);
+            } else {
+                stack[l] = block;
+                carry = false;
+            }
+        }
+    }
+}
+
+template <int BMODE>
+__device__ __forceinline__ void exact4_load(const GemmArgs& g, const ExactImg& im, const float* a,
+                                            const float* b, const float* xn, uint32_t row0,
+                                            uint32_t col0, uint32_t kb, uint32_t len, int tid,
+                                            bool a_kfast, bool b_kfast, float (&va)[8],
+                                            float (&vb)[8]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int idx = tid + 256 * q;
+        const int r = a_kfast ? (idx >> 5) : (idx & 63);
+        const int kk = a_kfast ? (idx & 31) : (idx >> 6);
+        const uint32_t gr = row0 + r;
+        va[q] = (gr < g.m && static_cast<uint32_t>(kk) < len)
+                    ? a[static_cast<int64_t>(gr) * g.sam + static_cast<int64_t>(kb + kk) * g.sak]
+                    : 0.0f;
+        const int c = b_kfast ? (idx >> 5) : (idx & 63);
+        const int bk = b_kfast ? (idx & 31) : (idx >> 6);
+        const uint32_t gc = col0 + c;
+        const bool in = gc < g.n && static_cast<uint32_t>(bk) < len;
+        if constexpr (BMODE == B_PTR)
+            vb[q] = in ? b[static_cast<int64_t>(kb + bk) * g.sbk + static_cast<int64_t>(gc) * g.sbn] : 0.0f;
+        else if constexpr (BMODE == B_IMG)
+            vb[q] = in ? exact_img_value(im, xn, kb + bk, gc) : 0.0f;
+        else
+            vb[q] = in ? exact_img_value(im, xn, gc, kb + bk) : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void exact4_store(float (*As)[kExact4Ld], float (*Bs)[kExact4Ld], int tid,
+                                             bool a_kfast, bool b_kfast, const float (&va)[8],
+                                             const float (&vb)[8]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int idx = tid + 256 * q;
+        const int r = a_kfast ? (idx >> 5) : (idx & 63);
+        const int kk = a_kfast ? (idx & 31) : (idx >> 6);
+        As[kk][r] = va[q];
+        const int c = b_kfast ? (idx >> 5) : (idx & 63);
+        const int bk = b_kfast ? (idx & 31) : (idx >> 6);
+        Bs[bk][c] = vb[q];
+    }
+}
+
+// Split over the K axis (blockIdx.y = s of 2^slog): a product with too few
+// output tiles to fill the machine gives each split the complete subtree of
+// 2^(depth - slog) consecutive leaves starting at leaf s * 2^(depth - slog),
+// and writes that subtree's sum to slice s of g.c (split_stride apart). The
+// carry-stack fold of the 2^slog slices (split_k_reduce_kernel) is then the
+// tree's upper levels, so the result is the unsplit product's bits.
+template <int BMODE, int LV>
+__global__ __launch_bounds__(256) void gemm_exact4_kernel(GemmArgs g, int depth, ExactImg im,
+                                                          int a_kfast_i, int b_kfast_i, int slog) {
+    __shared__ __align__(16) float As[2][32][kExact4Ld];  // [buffer][k][row]
+    __shared__ __align__(16) float Bs[2][32][kExact4Ld];  // [buffer][k][col]
+    const bool a_kfast = a_kfast_i != 0, b_kfast = b_kfast_i != 0;
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const uint32_t tm = blockIdx.x / g.tiles_n, tn = blockIdx.x - tm * g.tiles_n;
+    const uint32_t row0 = tm * 64u, col0 = tn * 64u;
+    const uint32_t bz = blockIdx.z;
+    const uint32_t i0 = bz / g.b1, i1 = bz - i0 * g.b1;
+    const float* a = g.a + static_cast<int64_t>(i0) * g.sa0 + static_cast<int64_t>(i1) * g.sa1;
+    const float* b = g.b + static_cast<int64_t>(i0) * g.sb0 + static_cast<int64_t>(i1) * g.sb1;
+    const float* xn = BMODE == B_PTR ? nullptr : im.x + static_cast<int64_t>(bz) * im.sn;
+    float stack[16][LV];
+#pragma unroll
+    for (int o = 0; o < 16; ++o)
+#pragma unroll
+        for (int l = 0; l < LV; ++l) stack[o][l] = 0.0f;
+    const int ldepth = depth - slog;  // depth of this split's subtree
+    const uint32_t leaves = 1u << ldepth;
+    const uint32_t first = blockIdx.y << ldepth;
+    float va[8], vb[8];
+    uint32_t kb, ke;
+    pairwise_leaf(g.k, depth, first, kb, ke);
+    exact4_load<BMODE>(g, im, a, b, xn, row0, col0, kb, ke - kb, tid, a_kfast, b_kfast, va, vb);
+    exact4_store(As[0], Bs[0], tid, a_kfast, b_kfast, va, vb);
+    __syncthreads();
+    for (uint32_t leaf = 0; leaf < leaves; ++leaf) {
+        const int cur = leaf & 1;
+        const uint32_t len = ke - kb;
+        uint32_t nkb = 0, nke = 0;
+        if (leaf + 1 < leaves) {
+            pairwise_leaf(g.k, depth, first + leaf + 1, nkb, nke);
+            exact4_load<BMODE>(g, im, a, b, xn, row0, col0, nkb, nke - nkb, tid, a_kfast, b_kfast, va, vb);
+        }
+        float acc[16];
+#pragma unroll
+        for (int o = 0; o < 16; ++o) acc[o] = 0.0f;
+        for (uint32_t kk = 0; kk < len; ++kk) {
+            const f32x4 av = *reinterpret_cast<const f32x4*>(&As[cur][kk][4 * ty]);
+            const f32x4 bv = *reinterpret_cast<const f32x4*>(&Bs[cur][kk][4 * tx]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[4 * i + j] = __fadd_rn(acc[4 * i + j], __fmul_rn(av[i], bv[j]));
+        }
+#pragma unroll
+        for (int o = 0; o < 16; ++o) exact_push_lv<LV>(stack[o], leaf, acc[o]);
+        if (leaf + 1 < leaves) exact4_store(As[cur ^ 1], Bs[cur ^ 1], tid, a_kfast, b_kfast, va, vb);
+        kb = nkb;
+        ke = nke;
+        __syncthreads();
+    }
+    float* c = g.c + static_cast<uint64_t>(blockIdx.y) * g.split_stride + static_cast<uint64_t>(bz) * g.m * g.n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t gr = row0 + 4 * ty + i;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t gc = col0 + 4 * tx + j;
+            float v = 0.0f;
+#pragma unroll
+            for (int l = 0; l < LV; ++l)
+                if (l == ldepth) v = stack[4 * i + j][l];
+            if (gr < g.m && gc < g.n) c[static_cast<uint64_t>(gr) * g.n + gc] = v;
+        }
+    }
+}
+
 // ---- planning ---------------------------------------------------------------
 
 // Split-K plan (reference plan_split_k, vulkan_backend.cpp:596-647), restated
@@ -1918,6 +2074,11 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
         // last from 128x784x16384 as 57 partitions of 9 K-tiles, 39.9 us
         // against 44.8 as 32 pairs of 8, and 256x256x65536 as 94 partitions
         // of 22, 79.8 us against 78.3 as 64 pairs of 16, which stays paired).
+        // (This tile count, unlike the rest of the plan, depends on which
+        // operand is A: M x N and N x M may get different partitions, and so
+        // different bits. vkhip_gemm_plan exposes the plan so that a caller
+        // that swaps the operands, as the host core's in-place weight
+        // gradient does, can check that both orientations agree.)
         const uint64_t t6 = static_cast<uint64_t>(ceil_div(m, 128)) * ceil_div(n, 64) * batch;
         uint32_t s3 = 1, c3 = ktiles;
         if (narrow_split && t6 <= 0xffffffffull)
@@ -1939,7 +2100,87 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
     return VKHIP_OK;
 }
 
-static int launch_exact(GemmArgs& g, uint32_t batch, int bmode, const ExactImg& im) {
+template <int BMODE, int LV>
+static void launch_exact4_lv(const GemmArgs& g, uint32_t batch, int depth, const ExactImg& im,
+                             int a_kfast, int b_kfast, int slog) {
+    const dim3 grid(g.tiles_m * g.tiles_n, 1u << slog, batch);
+    hipLaunchKernelGGL((gemm_exact4_kernel<BMODE, LV>), grid, dim3(256), 0, ctx().stream, g, depth, im,
+                       a_kfast, b_kfast, slog);
+}
+
+template <int BMODE>
+static void launch_exact4(const GemmArgs& g, uint32_t batch, int depth, const ExactImg& im, int a_kfast,
+                          int b_kfast, int slog) {
+    const int ldepth = depth - slog;  // the stack holds levels 0..ldepth
+    if (ldepth < 4)
+        launch_exact4_lv<BMODE, 4>(g, batch, depth, im, a_kfast, b_kfast, slog);
+    else if (ldepth < 6)
+        launch_exact4_lv<BMODE, 6>(g, batch, depth, im, a_kfast, b_kfast, slog);
+    else if (ldepth < 9)
+        launch_exact4_lv<BMODE, 9>(g, batch, depth, im, a_kfast, b_kfast, slog);
+    else
+        launch_exact4_lv<BMODE, 13>(g, batch, depth, im, a_kfast, b_kfast, slog);
+}
+
+// Deepest K the register-blocked exact kernel takes (its largest stack has 13
+// levels: K up to 2^12 leaves of 32 = 131072); deeper K runs gemm_exact_kernel.
+constexpr int kExact4MaxDepth = 12;
+
+// K-splits of the exact arm for a product of `tiles` 64x64 output tiles (all
+// batches) and pairwise depth `depth`: 2^slog complete subtrees, enough to
+// give the 256 CUs two workgroups each, each subtree keeping at least two
+// leaves; 0 when the tiles fill the machine already.
+static int exact_split_log(uint64_t tiles, int depth, uint64_t out_elems) {
+    const uint64_t cu = ctx().ready ? static_cast<uint64_t>(ctx().caps.compute_units) : 256u;
+    int slog = 0;
+    while (slog + 1 < depth && (tiles << (slog + 1)) <= 2 * cu && slog + 1 <= 8 &&
+           (out_elems << (slog + 1)) * sizeof(float) <= (64ull << 20))
+        ++slog;
+    return slog;
+}
+
+// ws: the caller's partial workspace (nullptr: the backend's own, grown on
+// demand), of ws_bytes bytes.
+static int launch_exact(GemmArgs& g, uint32_t batch, int bmode, const ExactImg& im,
+                        float* ws = nullptr, size_t ws_bytes = 0, bool may_split = false) {
+    const int depth4 = pairwise_depth(g.k);
+    if (depth4 <= kExact4MaxDepth) {
+        g.tiles_m = ceil_div(g.m, 64u);
+        g.tiles_n = ceil_div(g.n, 64u);
+        const uint64_t tiles4 = static_cast<uint64_t>(g.tiles_m) * g.tiles_n;
+        if (tiles4 > 0x7fffffffull)
+            return fail(VKHIP_ERR_UNSUPPORTED, "exact gemm: %llu output tiles",
+                        static_cast<unsigned long long>(tiles4));
+        // stage along whichever axis of each operand is unit-stride
+        const int a_kfast = g.sak == 1 || g.sam != 1;
+        const int b_kfast = bmode == B_IMGT || (bmode == B_PTR && (g.sbk == 1 || g.sbn != 1));
+        const uint64_t out_elems = static_cast<uint64_t>(batch) * g.m * g.n;
+        const int slog = may_split ? exact_split_log(tiles4 * batch, depth4, out_elems) : 0;
+        float* c = g.c;
+        if (slog > 0) {
+            const size_t need = (out_elems << slog) * sizeof(float);
+            if (ws == nullptr) {
+                const int wst = workspace(need, &ws);
+                if (wst != VKHIP_OK) return wst;
+            } else if (need > ws_bytes) {
+                return fail(VKHIP_ERR_INVALID,
+                            "exact matmul %ux%ux%u (batch %u) splits K into %d subtrees whose partials "
+                            "need %zu bytes; the allocation-free entry point's scratch holds %zu",
+                            g.m, g.n, g.k, batch, 1 << slog, need, ws_bytes);
+            }
+            g.c = ws;
+            g.split_stride = out_elems;
+        }
+        if (bmode == B_IMG)
+            launch_exact4<B_IMG>(g, batch, depth4, im, a_kfast, b_kfast, slog);
+        else if (bmode == B_IMGT)
+            launch_exact4<B_IMGT>(g, batch, depth4, im, a_kfast, b_kfast, slog);
+        else
+            launch_exact4<B_PTR>(g, batch, depth4, im, a_kfast, b_kfast, slog);
+        VKHIP_LAUNCH_CHECK();
+        if (slog > 0) return launch_split_k_reduce(ws, c, out_elems, 1u << slog);
+        return VKHIP_OK;
+    }
     g.tiles_m = ceil_div(g.m, kExactTile);
     g.tiles_n = ceil_div(g.n, kExactTile);
     const uint64_t tiles = static_cast<uint64_t>(g.tiles_m) * g.tiles_n;
@@ -1961,7 +2202,8 @@ static int launch_exact(GemmArgs& g, uint32_t batch, int bmode, const ExactImg& 
 
 static int launch_gemm_exact(const float* a, const vkhip_operand& ad, const float* b,
                              const vkhip_operand& bd, float* c, uint32_t batch, uint32_t b1,
-                             uint32_t m, uint32_t n, uint32_t k) {
+                             uint32_t m, uint32_t n, uint32_t k, float* ws = nullptr,
+                             size_t ws_bytes = 0) {
     GemmArgs g{};
     g.a = a;
     g.b = b;
@@ -1978,7 +2220,7 @@ static int launch_gemm_exact(const float* a, const vkhip_operand& ad, const floa
     g.m = m;
     g.n = n;
     g.k = k;
-    return launch_exact(g, batch, B_PTR, ExactImg{});
+    return launch_exact(g, batch, B_PTR, ExactImg{}, ws, ws_bytes, true);
 }
 
 // The exact arm's image geometry for a convolution (see ExactImg).
@@ -2057,7 +2299,8 @@ static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, co
     if (kernel == VKHIP_GEMM_EXACT) {
         publish("matmul.kernel", "matmul", "gemm_exact", "gemm_mfma", "exact arm requested",
                 static_cast<int64_t>(k), static_cast<int64_t>(m) * n);
-        return launch_gemm_exact(a, ad, b, bd, c, static_cast<uint32_t>(batch), b1, m, n, k);
+        return launch_gemm_exact(a, ad, b, bd, c, static_cast<uint32_t>(batch), b1, m, n, k,
+                                 scratch ? scratch->ptr : nullptr, scratch ? scratch->bytes : 0);
     }
     if (kernel != VKHIP_GEMM_AUTO && kernel != VKHIP_GEMM_MFMA)
         return fail(VKHIP_ERR_INVALID, "gemm: unknown kernel selection %d", kernel);

@@ -105,6 +105,7 @@ class DeviceBackend:
         from .device import backend
 
         self.hip = backend(index)
+        self._plans = {}
 
     def alloc(self, nbytes: int):
         from .device import Buffer
@@ -146,6 +147,20 @@ class DeviceBackend:
             d.first = 1 if first else 0
         _lib.check(self.hip.lib.vkhip_sgd_step(arr, len(entries), lr, momentum, weight_decay,
                                                1 if nesterov else 0), "sgd_step")
+
+    def transposed_plans_agree(self, batch: int, m: int, n: int, k: int) -> bool:
+        """Whether the M x N and N x M products over the same K get the same
+        split-K plan, and so the same bits for the same products (the
+        library's kernels sum each output's K range in an order only the
+        plan's (splits, chunk) decides)."""
+        key = (batch, m, n, k)
+        hit = self._plans.get(key)
+        if hit is None:
+            from . import ops
+
+            hit = ops.gemm_plan(batch, m, n, k) == ops.gemm_plan(batch, n, m, k)
+            self._plans[key] = hit
+        return hit
 
     def copy(self, copies) -> None:
         """copies: (dst storage, dst offset bytes, src storage, src offset
@@ -453,7 +468,8 @@ FOLD_CONSTANTS = True
 
 # The gradient of a weight used as w.T in a product (nn.Linear) computed in
 # w's layout (grad^T @ x) rather than as (x^T @ grad)^T then copied: the same
-# values (see the MATMUL rule).
+# values (see the MATMUL rule), applied where the backend plans both
+# orientations of the product alike.
 WEIGHT_GRAD_IN_PLACE_LAYOUT = True
 
 
@@ -464,11 +480,19 @@ def _matmul_backward(a: "Node", b: "Node", grad: "Tensor", grads: dict) -> None:
         _accumulate(grads, a, matmul(grad, Tensor(b).transpose(-2, -1)))
     if b.requires_grad:
         w = _transposed_matrix_source(b) if WEIGHT_GRAD_IN_PLACE_LAYOUT else None
+        if w is not None and len(w.shape) == 2:
+            # the backend's product plan must not depend on the orientation
+            # (the device's narrow split-K plan can: 128 x 784 and 784 x 128
+            # over K = 16384 split K differently)
+            agree = getattr(w.backend, "transposed_plans_agree", None)
+            batch = int(np.prod(a.shape[:-2], dtype=np.int64)) if len(a.shape) > 2 else 1
+            if agree is not None and not agree(batch, w.shape[0], w.shape[1], a.shape[-2]):
+                w = None
         if w is not None:
             # b = w^T (x @ w.T, a Linear layer): d(w) = grad^T @ a is the
             # transpose of d(w^T) = a^T @ grad -- the same products summed
-            # in the same k order under a plan symmetric in M and N -- in
-            # w's own layout, so no transposing copy follows.
+            # in the same k order under the same plan -- in w's own layout,
+            # so no transposing copy follows.
             _accumulate(grads, w, matmul(grad.transpose(-2, -1), Tensor(a)).reshape(w.shape))
         else:
             _accumulate(grads, b, matmul(Tensor(a).transpose(-2, -1), grad))
@@ -1380,6 +1404,39 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
 # 1.57 -> 1.29 ms with them).
 BACKWARD_FLUSH_EVERY = 8
 BACKWARD_FLUSH_MIN_BYTES = 8 << 20
+
+
+# Every switch above that makes the host core build something other than the
+# reference's node graph: a rewrite, a fused node, an implicit convolution, an
+# early flush. Each computes the reference nodes' values (tested per switch);
+# together off, a step's graph is the one vkML's own executor hands its
+# backend (src/dispatch/executor.cpp:90-154), node for node, every node a
+# reference OpKind.
+REFERENCE_GRAPH_SWITCHES = {
+    "FOLD_CONSTANTS": False, "WEIGHT_GRAD_IN_PLACE_LAYOUT": False, "FUSED_LINEAR_BIAS": False,
+    "IMPLICIT_CONV": False, "FUSED_CROSS_ENTROPY": False, "FUSED_RELU_BACKWARD": False,
+    "FUSED_POOL_RELU_GRAD": False, "FUSED_MATMUL_RELU_GRAD": False, "FOLD_CONV_WEIGHT_GRAD": False,
+    "FUSED_CONV_INPUT_GRAD": False, "FUSED_CONV_EPILOGUE": False, "FUSED_ADD_RELU": False,
+    "BACKWARD_FLUSH_EVERY": 0,
+}
+
+
+class reference_graph:
+    """Context manager: graphs built inside it use the reference's OpKind
+    nodes only (REFERENCE_GRAPH_SWITCHES), flushed once per realise, as the
+    reference's executor would hand them to a drop-in HipBackend::compute.
+    (An optimiser built with SGD(fused=False) keeps its step in ScaledAdd
+    nodes as well.)"""
+
+    def __enter__(self):
+        mod = globals()
+        self._saved = {k: mod[k] for k in REFERENCE_GRAPH_SWITCHES}
+        mod.update(REFERENCE_GRAPH_SWITCHES)
+        return self
+
+    def __exit__(self, *exc):
+        globals().update(self._saved)
+        return False
 
 
 def backward(root: Tensor, seed: Tensor | None = None) -> None:
