@@ -39,6 +39,10 @@ sys.path.insert(0, str(ROOT))
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
+# fp32 VALU rate for rounded multiplies and adds issued separately (no FMA, no
+# packed fp32): 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz, one FLOP per lane-op.
+# The exact arm rounds every product and sum on its own, so this is its roof.
+VALU_FP32_SEPARATE_TFLOPS = 39.3
 METRIC = "fp32 GEMM TFLOP/s @4096³ (% fp32 MFMA peak); im2col/softmax GB/s; steps/s"
 
 
@@ -223,6 +227,13 @@ def cpu_baseline(args):
     red = rng.standard_normal((1024, 4096)).astype(np.float32)
     mlp_x = rng.uniform(0, 1, (64, 1, 28, 28)).astype(np.float32)
     mlp_y = rng.integers(0, 10, 64).astype(np.int64)
+    sk_b = rng.standard_normal((65536, 256), dtype=np.float32)
+    gv_a = rng.standard_normal((4096, 4096), dtype=np.float32)
+    gv_x = rng.standard_normal((4096, 1), dtype=np.float32)
+    cols = O.im2col(img, 3, 1, 1)
+    wide = (rng.standard_normal((16, 32768)) * 2).astype(np.float32)
+    S = _streams()
+    cnn_x, cnn_y = next(S.batches(S.CONFIG5, 1, 8))
     for threads in sorted({1, threads_all}):
         # GEMM 4096^3 on a row sample sized to ~1/3 of the budget
         probe_rows = max(threads, 4)
@@ -265,6 +276,42 @@ def cpu_baseline(args):
         dt = _timed(mlp_step, per_case, 3)
         line("mlp_784_128_10_b64_step", 1.0 / dt, "steps/s", threads,
              f"whole step, best {dt * 1e3:.2f} ms")
+        # split-K shape 256x256x65536 on a row sample (the oracle has no split:
+        # one pairwise sum per output)
+        sk_rows = max(threads, 8)
+        sk_a = rng.standard_normal((sk_rows, 65536), dtype=np.float32)
+        dt = _timed(lambda: O.matmul(sk_a, sk_b, threads=threads), per_case, 1)
+        line("splitk_256x256x65536", 2.0 * sk_rows * 256 * 65536 / dt / 1e9, "GFLOP/s", threads,
+             f"{sk_rows} of 256 rows, best {dt:.2f} s")
+        # GEMV 4096x4096 . 4096 (read the matrix once)
+        dt = _timed(lambda: O.matmul(gv_a, gv_x, threads=threads), per_case, 2)
+        line("gemv_4096", (gv_a.nbytes + 2 * 4096 * 4) / dt / 1e9, "GB/s", threads,
+             f"whole problem, best {dt * 1e3:.1f} ms")
+        # col2im conv2 geometry on 8 of 128 images (read cols + write image)
+        dt = _timed(lambda: O.col2im(cols, (32, 32), 3, 1, 1, threads=threads), per_case, 2)
+        line("col2im_conv2", (cols.nbytes + img.nbytes) / dt / 1e9, "GB/s", threads,
+             f"8 of 128 images, best {dt * 1e3:.1f} ms")
+        # softmax [256, 32768] on 16 of the 256 rows
+        dt = _timed(lambda: O.softmax(wide, -1, threads=threads), per_case, 2)
+        line("softmax_256x32768", 2 * wide.nbytes / dt / 1e9, "GB/s", threads,
+             f"16 of 256 rows, best {dt * 1e3:.1f} ms")
+        # one config-5 CNN training step at batch 8 (the whole network, a
+        # sixteenth of the batch): steps/s at batch 8 and, labelled, the
+        # batch-128 rate it implies (the step's work is linear in the batch)
+        nn.manual_seed(S.CONFIG5.model_seed)
+        cnn = S.model(S.CONFIG5, be)
+        copt = optim.SGD(cnn.parameters(), lr=S.CONFIG5.lr, momentum=S.CONFIG5.momentum)
+
+        def cnn_step():
+            copt.zero_grad()
+            loss = nn.cross_entropy(cnn(T.tensor(cnn_x, backend=be)), T.tensor(cnn_y, backend=be))
+            loss.backward()
+            copt.step()
+            loss.item()
+
+        dt = _timed(cnn_step, per_case, 2)
+        line("cifar_cnn_b128_step", 8.0 / 128.0 / dt, "steps/s", threads,
+             f"batch 8 of 128 (extrapolated linearly to 128), best {dt * 1e3:.1f} ms per batch-8 step")
 
     head = next(l for l in lines if l["case"].startswith("gemm") and l["cores"] == threads_all)
     return {"value": round(head["value"] / 1e3, 6), "unit": "TFLOP/s", "cores": threads_all,
@@ -318,6 +365,23 @@ def case_gemm(name, hip, ops, timer, rng, out):
     tf = 2.0 * m * n * k / ms / 1e9
     out[name] = {"ms": round(ms, 5), "tflops": round(tf, 2),
                  "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "splits": splits}
+
+
+def case_gemm_exact(name, hip, ops, timer, rng, out):
+    """The exact arm (VKHIP_GEMM_EXACT: the oracle's bits) at 4096^3 NN, against
+    the VALU rate of separately rounded multiplies and adds."""
+    from vkml_amd import _lib
+    from vkml_amd.device import DeviceArray
+
+    m = n = k = 4096
+    a = DeviceArray.from_numpy(rng.standard_normal((m, k), dtype=np.float32))
+    b = DeviceArray.from_numpy(rng.standard_normal((k, n), dtype=np.float32))
+    c = DeviceArray((m, n), np.float32)
+    ms = time_batch(lambda i: ops.matmul(a, b, kernel=_lib.GEMM_EXACT, out=c), timer, 3, warmup=1)
+    tf = 2.0 * m * n * k / ms / 1e9
+    out[name] = {"ms": round(ms, 4), "tflops": round(tf, 2),
+                 "frac_of_valu_separate": round(tf / VALU_FP32_SEPARATE_TFLOPS, 4),
+                 "frac_of_mfma_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
 
 
 def case_copy(name, hip, ops, timer, rng, out):
@@ -375,6 +439,19 @@ def case_conv(name, hip, ops, timer, rng, out):
 
     xs_shape, cout = CONV_CASES[name]
     n_, cin, h, w_ = xs_shape
+
+    def roof(entry, flops, byt, ms):
+        """frac_of_roofline: the larger of the two floors (MFMA FLOP, HBM
+        bytes read + written once) over the measured time; `bound` names it."""
+        t_flop = flops / (MFMA_FP32_PEAK_TFLOPS * 1e9)
+        t_byte = byt / (HBM_PEAK_GBS * 1e6)
+        entry["algorithmic_bytes"] = int(byt)
+        entry["bound"] = "hbm" if t_byte > t_flop else "mfma"
+        entry["frac_of_roofline"] = round(max(t_flop, t_byte) / ms, 4)
+        entry["floor_us"] = round(max(t_flop, t_byte) * 1e3, 3)
+
+    x_bytes, y_bytes = 4 * n_ * cin * h * w_, 4 * n_ * cout * h * w_
+    w_bytes = 4 * cout * cin * 9
     x = DeviceArray.from_numpy(rng.standard_normal(xs_shape, dtype=np.float32))
     wt = DeviceArray.from_numpy(rng.standard_normal((cout, cin, 3, 3), dtype=np.float32))
     y = DeviceArray((n_, cout, h, w_), np.float32)
@@ -392,6 +469,7 @@ def case_conv(name, hip, ops, timer, rng, out):
     out[name] = {"ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
                  "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
                  "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
+    roof(out[name], flops, x_bytes + w_bytes + y_bytes, ms_i)
     g = DeviceArray.from_numpy(rng.standard_normal((n_, cout, h, w_), dtype=np.float32))
     wg = DeviceArray((n_, cout, ck), np.float32)
     g4 = g.reshape(1, n_, cout, L)
@@ -407,6 +485,8 @@ def case_conv(name, hip, ops, timer, rng, out):
         "ms": round(ms_i, 5), "tflops": round(flops / ms_i / 1e9, 2),
         "frac_of_peak": round(flops / ms_i / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
         "explicit_ms": round(ms_e, 5), "speedup_vs_explicit": round(ms_e / ms_i, 3)}
+    roof(out[name.replace("conv_", "conv_wgrad_")], flops,
+         x_bytes + y_bytes + 4 * n_ * cout * cin * 9, ms_i)
     # dW itself (summed over the batch): the per-image products followed by
     # the batch SUM (the reference graph's two nodes) against one product
     # with the batch folded into K
@@ -422,6 +502,7 @@ def case_conv(name, hip, ops, timer, rng, out):
         "ms": round(ms_f, 5), "tflops": round(flops / ms_f / 1e9, 2),
         "frac_of_peak": round(flops / ms_f / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
         "per_image_then_sum_ms": round(ms_s, 5), "speedup_vs_per_image": round(ms_s / ms_f, 3)}
+    roof(out[name.replace("conv_", "conv_dw_")], flops, x_bytes + y_bytes + w_bytes, ms_f)
     # dX: the reference graph's TN product into the column matrix and col2im,
     # against one convolution of the gradient with the flipped weight
     dx = DeviceArray(xs_shape, np.float32)
@@ -436,6 +517,7 @@ def case_conv(name, hip, ops, timer, rng, out):
         "ms": round(ms_f, 5), "tflops": round(flops / ms_f / 1e9, 2),
         "frac_of_peak": round(flops / ms_f / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
         "tn_then_col2im_ms": round(ms_t, 5), "speedup_vs_tn_col2im": round(ms_t / ms_f, 3)}
+    roof(out[name.replace("conv_", "conv_dx_")], flops, y_bytes + w_bytes + x_bytes, ms_f)
 
 
 SOFTMAX_CASES = {"softmax_4096x1000": ((4096, 1000), 20), "softmax_256x32768": ((256, 32768), 10)}
@@ -473,12 +555,13 @@ def case_reduce(name, hip, ops, timer, rng, out):
             _bw(out, key, ms, 8192 * 4096 * 4 + 8192 * 4)
 
 
-CASES = {**{k: case_gemm for k in GEMM_CASES}, "copy_256MiB": case_copy, "gemv_4096": case_gemv,
+CASES = {**{k: case_gemm for k in GEMM_CASES}, "gemm_exact_4096": case_gemm_exact,
+         "copy_256MiB": case_copy, "gemv_4096": case_gemv,
          "im2col_conv2": case_im2col_col2im, "col2im_conv2": case_im2col_col2im,
          **{k: case_conv for k in CONV_CASES}, **{k: case_softmax for k in SOFTMAX_CASES},
          "sum_8192x4096": case_reduce, "max_8192x4096": case_reduce}
 DEFAULT_RUN = [k for k in GEMM_CASES if k != "gemm_nn_4096"] + [
-    "copy_256MiB", "gemv_4096", "im2col_col2im", *CONV_CASES, *SOFTMAX_CASES, "reduce_8192x4096"]
+    "gemm_exact_4096", "copy_256MiB", "gemv_4096", "im2col_col2im", *CONV_CASES, *SOFTMAX_CASES, "reduce_8192x4096"]
 CASES["im2col_col2im"] = case_im2col_col2im
 CASES["reduce_8192x4096"] = case_reduce
 
