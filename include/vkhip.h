@@ -394,6 +394,10 @@ int vkhip_event_destroy(void* event);
 int vkhip_event_record(void* event);
 /* Milliseconds between two recorded events; waits for `end` to complete. */
 int vkhip_event_elapsed(void* start, void* end, float* out_ms);
+/* Waits on the host until `event` (recorded) has completed. No counterpart in
+ * the reference (its host reads synchronise, tensor.cpp:178-200); for callers
+ * that queue work without reading it back and bound how far ahead they run. */
+int vkhip_event_synchronize(void* event);
 
 /* Convolution forward as one implicit-im2col GEMM per image:
  * out[n] = w (Cout x C*kh*kw) @ cols(x[n]) with the cols matrix gathered from

@@ -437,3 +437,24 @@ def test_assign_checks_its_pairs(cpu):
         T.assign([a], [])
     with pytest.raises(ValueError):
         T.assign([a], [T.tensor(np.zeros((3, 2), np.float32), backend=cpu)])
+
+
+@pytest.mark.parametrize("fused", ["FUSED_ADD_RELU", "FUSED_CONV_EPILOGUE"])
+def test_fused_relu_nodes_follow_no_grad(cpu, fused):
+    """relu() under no_grad on an ADD (or conv + bias ADD) built with grad
+    enabled gives a node that does not require grad, as the unfused RELU
+    does (the fused node takes requires_grad from the grad mode too)."""
+    rng = np.random.default_rng(SEED + 31)
+    w = T.tensor(rng.standard_normal((4, 3, 3, 3)).astype(np.float32), requires_grad=True, backend=cpu)
+    b = T.tensor(rng.standard_normal(4).astype(np.float32), requires_grad=True, backend=cpu)
+    x = T.tensor(rng.standard_normal((2, 3, 8, 8)).astype(np.float32), backend=cpu)
+    if fused == "FUSED_ADD_RELU":
+        pre = x.reshape(2, 192) + T.tensor(rng.standard_normal(192).astype(np.float32),
+                                            requires_grad=True, backend=cpu)
+    else:
+        pre = T.conv2d(x, w, b, 1, 1)
+    assert pre.requires_grad
+    with T.no_grad():
+        out = T.relu(pre)
+    assert not out.requires_grad
+    assert T.relu(pre).requires_grad

@@ -155,6 +155,7 @@ SIGNATURES = {
     "vkhip_event_destroy": (c_int, [c_void_p]),
     "vkhip_event_record": (c_int, [c_void_p]),
     "vkhip_event_elapsed": (c_int, [c_void_p, c_void_p, POINTER(c_float)]),
+    "vkhip_event_synchronize": (c_int, [c_void_p]),
     "vkhip_fast_divide": (c_uint32, [c_uint32, c_uint32]),
     "vkhip_exact_math": (c_int, [c_void_p, c_void_p, c_size_t, c_int]),
     "vkhip_pairwise_leaf": (c_int, [c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_uint32),

@@ -2761,9 +2761,11 @@ __global__ __launch_bounds__(64 * kSmallWgradWaves) void conv_wgrad_small_kernel
     const uint32_t c = jc / static_cast<uint32_t>(im.kk);
     const uint32_t r = jc - c * static_cast<uint32_t>(im.kk);
     const uint32_t ki = r / static_cast<uint32_t>(im.kw), kj = r - ki * static_cast<uint32_t>(im.kw);
-    const int fh = jok ? static_cast<int>(ki) * im.dilh - im.padh : -(1 << 28);
+    // (lanes past C*kh*kw get a row far above the image, so that their 'in'
+    // test fails; their offset is not formed from it)
+    const int fh = jok ? static_cast<int>(ki) * im.dilh - im.padh : -(1 << 20);
     const int fw = static_cast<int>(kj) * im.dilw - im.padw;
-    const int off = static_cast<int>(c) * sp.cp + fh * sp.wp + fw;
+    const int off = jok ? static_cast<int>(c) * sp.cp + fh * sp.wp + fw : 0;
     const int sth = im.strh * sp.wp;
 
     // the gradient rows of this lane in the two Cout blocks (rows past Cout

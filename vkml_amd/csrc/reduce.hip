@@ -262,6 +262,104 @@ __global__ __launch_bounds__(Rows<T>::kThreads) void softmax_rows_kernel(
     }
 }
 
+// ---- softmax, one workgroup per long row, one pass of statistics ---------------------
+// For rows of 1024 threads x 32 floats (up to 32768 elements, e.g. [256, 32768],
+// one row per CU): the row's peak and its sum of exponentials are reduced as
+// one (peak, sum) pair instead of a peak reduction followed by a sum reduction.
+// Each thread sums exp(x - m_t) against its own peak m_t; pairs combine as
+// (max(m1, m2), s1 e^(m1 - M) + s2 e^(m2 - M)); the outputs are
+// exp(x - m_t) * (e^(m_t - M) / S) (softmax) or x - M - log(S) (log-softmax):
+// one block-level exchange and one barrier fewer between the row's loads and
+// its stores. The rescaling adds a few roundings (within the fast numerics'
+// 1e-5*sqrt(n)); the exact numerics mode has its own kernels. Special values:
+// a thread whose elements are all -inf contributes (-inf, 0) and outputs 0; a
+// +inf or NaN anywhere makes the sum, and so the row, NaN, as the oracle's.
+__device__ __forceinline__ void pair_combine(float& m, float& s, float m2, float s2) {
+    const float M = __builtin_fmaxf(m, m2);
+    const float a = m == M ? 1.0f : softmax_exp(m - M);
+    const float b = m2 == M ? 1.0f : softmax_exp(m2 - M);
+    s = s * a + s2 * b;
+    m = M;
+}
+
+__device__ __forceinline__ void wave_pair(float& m, float& s) {
+    pair_combine(m, s, wave_partner<1>(m), wave_partner<1>(s));
+    pair_combine(m, s, wave_partner<2>(m), wave_partner<2>(s));
+    pair_combine(m, s, wave_partner<4>(m), wave_partner<4>(s));
+    pair_combine(m, s, wave_partner<8>(m), wave_partner<8>(s));
+    pair_combine(m, s, wave_partner<16>(m), wave_partner<16>(s));
+    const float m0 = lane_value(m, 0), s0 = lane_value(s, 0);
+    const float m1 = lane_value(m, 32), s1 = lane_value(s, 32);
+    m = m0;
+    s = s0;
+    pair_combine(m, s, m1, s1);
+}
+
+template <int E4, bool LOG>
+__global__ __launch_bounds__(1024) void softmax_online_rows_kernel(const float* __restrict__ src,
+                                                                   int64_t in_stride,
+                                                                   float* __restrict__ dst,
+                                                                   uint32_t rows, uint32_t n) {
+    constexpr int T = 1024, E = 4 * E4;
+    __shared__ float sm[T / 64], ss[T / 64];
+    const int t = threadIdx.x;
+    const uint32_t row = blockIdx.x;
+    const float* rs = src + static_cast<int64_t>(row) * in_stride;
+    float x[E];
+    load_row<T, E4>(x, rs, n, t, true, 1);
+    bool keep[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) keep[i] = elem_of(1, T, t, i) < n;
+    const float mt = tree_peak<E>(x, keep);
+    const float mref = mt == -__builtin_inff() ? 0.0f : mt;  // an all -inf share sums to 0
+    float e[E];
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        e[i] = softmax_exp(x[i] - mref);
+        if (keep[i]) part = part + e[i];
+    }
+    float m = mt, s = part;
+    wave_pair(m, s);
+    const int lane = t & 63, wave = t >> 6;
+    if (lane == 0) {
+        sm[wave] = m;
+        ss[wave] = s;
+    }
+    __syncthreads();
+    float M = lane < T / 64 ? sm[lane] : -__builtin_inff();
+    float S = lane < T / 64 ? ss[lane] : 0.0f;
+    wave_pair(M, S);
+    float* ds = dst + static_cast<uint64_t>(row) * n;
+    if constexpr (LOG) {
+        const float ld = logf(S);
+#pragma unroll
+        for (int i = 0; i < E4; ++i) {
+            const uint32_t e0 = 4u * (t + T * i);
+            if (e0 < n) {
+                f32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] = (x[4 * i + j] - M) - ld;
+                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(ds + e0));
+            }
+        }
+    } else {
+        // this thread's factor e^(m_t - M) / S (0 for an all -inf share)
+        const float f = mt == -__builtin_inff() ? 0.0f : (mt == M ? 1.0f : softmax_exp(mt - M));
+        const float scale = f * (1.0f / S);
+#pragma unroll
+        for (int i = 0; i < E4; ++i) {
+            const uint32_t e0 = 4u * (t + T * i);
+            if (e0 < n) {
+                f32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] = e[4 * i + j] * scale;
+                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(ds + e0));
+            }
+        }
+    }
+}
+
 // ---- softmax, one wave per row, persistent with prefetch -------------------------------
 // Rows of n <= 16*E4 (E4 float4 per lane) contiguous floats. Each wave walks
 // rows row0, row0 + stride, ... and issues the next row's loads before it
@@ -1307,6 +1405,14 @@ template <int T, int E4>
 static int launch_softmax_rows(const float* src, int64_t stride, float* dst, uint32_t rows,
                                uint32_t n, int log_mode, int vec, hipStream_t st) {
     constexpr int RPB = Rows<T>::kPerBlock;
+    if constexpr (T == 1024) {
+        if (vec) {  // one (peak, sum) reduction per row
+            auto fo = log_mode ? softmax_online_rows_kernel<E4, true> : softmax_online_rows_kernel<E4, false>;
+            hipLaunchKernelGGL(fo, dim3(rows), dim3(1024), 0, st, src, stride, dst, rows, n);
+            VKHIP_LAUNCH_CHECK();
+            return VKHIP_OK;
+        }
+    }
     auto fn = log_mode ? softmax_rows_kernel<T, E4, true> : softmax_rows_kernel<T, E4, false>;
     hipLaunchKernelGGL(fn, dim3(ceil_div(rows, RPB)), dim3(Rows<T>::kThreads), 0, st, src,
                        stride, dst, rows, n, vec);

@@ -355,6 +355,10 @@ class Event:
         check(backend().lib.vkhip_event_record(c_void_p(self.handle)), "event_record")
         return self
 
+    def synchronize(self) -> None:
+        """Waits on the host until the recorded event has completed."""
+        check(backend().lib.vkhip_event_synchronize(c_void_p(self.handle)), "event_synchronize")
+
     def elapsed_ms(self, end: "Event") -> float:
         ms = ctypes.c_float()
         check(backend().lib.vkhip_event_elapsed(c_void_p(self.handle), c_void_p(end.handle),
