@@ -1448,6 +1448,153 @@ __global__ __launch_bounds__(256) void bias_cols_kernel(float* __restrict__ c, u
     c[i] = apply_epilogue(epi, i, c[i]);
 }
 
+// ---- split-K products folded inside the workgroup ----------------------------
+// A product whose plan splits K into S = 2..4 partitions (512^3: 4 of 4
+// K-tiles; a Linear(256, 100) layer at batch 128: 4 of 2) ran as the split
+// kernel writing S partial slices and split_k_reduce_kernel folding them: two
+// launches, the second bound by its launch and the partials' round trip
+// (10.4 us at 512^3 for 1.7 us of matrix-core work). Here a workgroup owns a
+// 32 x 32 output tile and one wave per partition: wave p stages its own
+// K-tiles [p*chunk, min((p+1)*chunk, ktiles)) in LDS (its K-slices of A and
+// B, zero outside the operands, with waits within the wave only) and runs the
+// 16 MFMA steps per K-tile that every kernel here runs (step t pairs k = t and
+// k = 16 + t), from 0, so its partial is the split kernel's. The S partials
+// then go through LDS and are folded per output exactly as the fold kernel
+// folds them (carry stack in partition order, drained from 0.0), with the
+// same epilogue: the product's bits, in one launch.
+constexpr int kWgFoldLdk = 33;  // LDS pitch of a staged 32 x 32 slice
+
+template <int S, int KT>
+__global__ __launch_bounds__(64 * S) void gemm_wgfold_kernel(GemmArgs g, FoldEpilogue epi, int a_kfast,
+                                                             int b_kfast) {
+    // KT: K-tiles per partition, all of whose operand slices a wave loads
+    // into registers before its first MFMA (16-byte loads for a k-contiguous
+    // A and an n-contiguous B, the NN layout; elements otherwise)
+    __shared__ float stage[S][2][32 * kWgFoldLdk];  // per wave: A [row][k], B [col][k]
+    __shared__ float parts[S][16][64];
+    const int lane = threadIdx.x & 63;
+    const int p = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lrow = lane & 31, kh = lane >> 5;
+    const uint32_t tm = blockIdx.x / g.tiles_n, tn = blockIdx.x - tm * g.tiles_n;
+    const uint32_t row0 = 32u * tm, col0 = 32u * tn;
+    const uint32_t z = blockIdx.z;
+    const uint32_t i0 = z / g.b1, i1 = z - i0 * g.b1;
+    const float* a = g.a + static_cast<int64_t>(i0) * g.sa0 + static_cast<int64_t>(i1) * g.sa1;
+    const float* b = g.b + static_cast<int64_t>(i0) * g.sb0 + static_cast<int64_t>(i1) * g.sb1;
+    float* As = stage[p][0];
+    float* Bs = stage[p][1];
+    const uint32_t kt0 = static_cast<uint32_t>(p) * g.chunk;
+    const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
+    // the vector path: lane l loads row/k-row l/8 + 8q, 4 floats at 4*(l%8)
+    const bool vec = g.a_vec && g.b_vec && g.sak == 1 && g.sbn == 1;
+    float va[KT][16], vb[KT][16];
+#pragma unroll
+    for (int u = 0; u < KT; ++u) {
+        const uint32_t k0 = 32u * (kt0 + u);
+        const bool live = kt0 + u < kt1;
+        if (vec) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t rr = static_cast<uint32_t>(lane / 8 + 8 * q), c4 = 4u * (lane % 8);
+                const uint32_t gr = row0 + rr, gk = k0 + c4;
+                f32x4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (live && gr < g.m && gk + 3 < g.k)
+                    x = *reinterpret_cast<const f32x4*>(a + static_cast<int64_t>(gr) * g.sam + gk);
+                else if (live && gr < g.m)
+                    for (int j = 0; j < 4; ++j)
+                        if (gk + j < g.k) x[j] = a[static_cast<int64_t>(gr) * g.sam + gk + j];
+                const uint32_t gbk = k0 + rr, gc = col0 + c4;
+                f32x4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (live && gbk < g.k && gc + 3 < g.n)
+                    y = *reinterpret_cast<const f32x4*>(b + static_cast<int64_t>(gbk) * g.sbk + gc);
+                else if (live && gbk < g.k)
+                    for (int j = 0; j < 4; ++j)
+                        if (gc + j < g.n) y[j] = b[static_cast<int64_t>(gbk) * g.sbk + gc + j];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    va[u][4 * q + j] = x[j];
+                    vb[u][4 * q + j] = y[j];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t rr = a_kfast ? static_cast<uint32_t>(2 * i + kh) : static_cast<uint32_t>(lrow);
+                const uint32_t kk = a_kfast ? static_cast<uint32_t>(lrow) : static_cast<uint32_t>(2 * i + kh);
+                const uint32_t gr = row0 + rr, gk = k0 + kk;
+                va[u][i] = (live && gr < g.m && gk < g.k)
+                               ? a[static_cast<int64_t>(gr) * g.sam + static_cast<int64_t>(gk) * g.sak]
+                               : 0.0f;
+                const uint32_t cc = b_kfast ? static_cast<uint32_t>(2 * i + kh) : static_cast<uint32_t>(lrow);
+                const uint32_t bk = b_kfast ? static_cast<uint32_t>(lrow) : static_cast<uint32_t>(2 * i + kh);
+                const uint32_t gc = col0 + cc, gbk = k0 + bk;
+                vb[u][i] = (live && gc < g.n && gbk < g.k)
+                               ? b[static_cast<int64_t>(gbk) * g.sbk + static_cast<int64_t>(gc) * g.sbn]
+                               : 0.0f;
+            }
+        }
+    }
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < KT; ++u) {
+        if (kt0 + u >= kt1) break;
+        // (a wave's LDS operations complete in issue order; the fences keep
+        // the compiler from moving this K-tile's stores above the previous
+        // K-tile's reads, or its reads above these stores)
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+        if (vec) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int rr = lane / 8 + 8 * q, c = 4 * (lane % 8) + j;
+                    As[rr * kWgFoldLdk + c] = va[u][4 * q + j];  // A[row rr][k c]
+                    Bs[c * kWgFoldLdk + rr] = vb[u][4 * q + j];  // B[k rr][col c] as [col][k]
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int rr = a_kfast ? 2 * i + kh : lrow, kk = a_kfast ? lrow : 2 * i + kh;
+                As[rr * kWgFoldLdk + kk] = va[u][i];
+                const int cc = b_kfast ? 2 * i + kh : lrow, bk = b_kfast ? lrow : 2 * i + kh;
+                Bs[cc * kWgFoldLdk + bk] = vb[u][i];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[lrow * kWgFoldLdk + 16 * kh + t],
+                                                       Bs[lrow * kWgFoldLdk + 16 * kh + t], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) parts[p][r][lane] = acc[r];
+    __syncthreads();
+    // fold: output (r, l) of the tile, r = 0..15 register, l = lane
+    float* cz = g.c + static_cast<uint64_t>(z) * g.m * g.n;
+    for (int e = static_cast<int>(threadIdx.x); e < 1024; e += 64 * S) {
+        const int r = e >> 6, l = e & 63;
+        const uint32_t row = row0 + 8 * (r / 4) + 4 * (l >> 5) + (r % 4);
+        const uint32_t col = col0 + (l & 31);
+        float stack[kSplitLevels];
+#pragma unroll
+        for (int lv = 0; lv < kSplitLevels; ++lv) stack[lv] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < S; ++q) carry_push(stack, static_cast<uint32_t>(q), parts[q][r][l]);
+        float total = 0.0f;
+#pragma unroll
+        for (int lv = 0; lv < kSplitLevels; ++lv)
+            if ((static_cast<uint32_t>(S) >> lv) & 1u) total = total + stack[lv];
+        if (row < g.m && col < g.n) {
+            const uint64_t i = (static_cast<uint64_t>(z) * g.m + row) * g.n + col;
+            cz[static_cast<uint64_t>(row) * g.n + col] = apply_epilogue(epi, i, total);
+        }
+    }
+}
+
 // ---- GEMV -------------------------------------------------------------------
 // y[row] = sum_k A[row,k] * x[k]: one wave per row. The row is streamed once
 // with 16-byte loads into LDS, products are rounded to f32 separately (no FMA,
@@ -2399,6 +2546,31 @@ static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, co
     // for a single pair); every other kernel one per partition.
     const bool direct128 = tile.bm == 128 && b_rows && (amode == KCD || a_rows);
     const bool paired = direct128 && tile.pair && splits >= 2 && reinterpret_cast<uintptr_t>(c) % 16 == 0;
+    // Two to four partitions on 64x64 tiles: one launch, the partials folded
+    // inside the workgroup (gemm_wgfold_kernel), the same bits.
+    if (splits >= 2 && splits <= 4 && chunk <= 4 && tile.bm == 64 && !tile.pair) {
+        g.tiles_m = ceil_div(m, 32u);
+        g.tiles_n = ceil_div(n, 32u);
+        const uint64_t t32 = static_cast<uint64_t>(g.tiles_m) * g.tiles_n;
+        if (t32 <= 0x7fffffffull) {
+            g.c = c;
+            const int akf = g.sak == 1 || g.sam != 1;
+            const int bkf = g.sbk == 1 || g.sbn != 1;
+            const dim3 grid(static_cast<uint32_t>(t32), 1, static_cast<uint32_t>(batch));
+#define VKHIP_WGF(SS, KT) \
+    hipLaunchKernelGGL((gemm_wgfold_kernel<SS, KT>), grid, dim3(64 * SS), 0, ctx().stream, g, fe, akf, bkf)
+#define VKHIP_WGF_S(KT) \
+    do { if (splits == 2) VKHIP_WGF(2, KT); else if (splits == 3) VKHIP_WGF(3, KT); else VKHIP_WGF(4, KT); } while (0)
+            if (chunk <= 2) VKHIP_WGF_S(2); else VKHIP_WGF_S(4);
+#undef VKHIP_WGF_S
+#undef VKHIP_WGF
+            VKHIP_LAUNCH_CHECK();
+            *fused = true;
+            return VKHIP_OK;
+        }
+        g.tiles_m = ceil_div(m, tile.bm);
+        g.tiles_n = ceil_div(n, tile.bn);
+    }
     const uint32_t slices = paired ? (splits + 1) / 2 : splits;
     float* target = c;
     if (slices > 1) {
