@@ -66,6 +66,9 @@ def parse():
     p.add_argument("--no-gate", action="store_true",
                    help="do not queue the ~25 ms of GEMM before each timed batch (profiling runs: "
                         "counters then see the case's kernels only)")
+    p.add_argument("--train-modes", default="",
+                   help="training modes the train_mlp / train_cnn cases run (comma-separated; default "
+                        "all: dropin,eager,replay,graph,graph_queued,exact), for profiling one mode")
     p.add_argument("--calibrate", action="store_true",
                    help="also run the plain 16-byte copy kernel 5x over 256 MiB (the byte-counter "
                         "calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
@@ -582,7 +585,14 @@ def case_training(name, hip, ops, timer, rng, out):
     """One training config (config 1 "train_mlp" or config 5 "train_cnn") in
     every mode training_steps runs."""
     only = {"train_mlp": 1, "train_cnn": 5}[name]
-    out.update(training_steps(only=only))
+    modes = tuple(m for m in _TRAIN_MODES_ARG.split(",") if m) or TRAIN_MODES
+    unknown = set(modes) - set(TRAIN_MODES)
+    if unknown:
+        raise SystemExit(f"unknown training modes {sorted(unknown)}; known: {TRAIN_MODES}")
+    out.update(training_steps(only=only, modes=modes))
+
+
+_TRAIN_MODES_ARG = ""
 
 
 TRAIN_MODES = ("dropin", "eager", "replay", "graph", "graph_queued", "exact")
@@ -691,7 +701,10 @@ def training_steps(only: int | None = None, modes=TRAIN_MODES):
             timed = cfg.steps - 1
             out = {"ms_per_step": round(dt * 1e3 / timed, 4), "steps_per_s": round(timed / dt, 2),
                    "last_loss": losses[-1]}
-            if mode == "graph_queued":
+            if mode == "graph_queued" and "graph" not in entry:
+                out["max_loss_drift_vs_oracle"] = None
+                out["drift_from"] = "graph mode not run"
+            elif mode == "graph_queued":
                 same = np.float32(losses[-1]).tobytes() == np.float32(entry["graph"]["last_loss"]).tobytes()
                 out["last_loss_same_bits_as_graph"] = bool(same)
                 out["max_loss_drift_vs_oracle"] = entry["graph"]["max_loss_drift_vs_oracle"] if same else None
@@ -741,8 +754,9 @@ def main():
     hip = backend()
     timer = Timer()
     if args.case:
-        global _GATE_ON
+        global _GATE_ON, _TRAIN_MODES_ARG
         _GATE_ON = not args.no_gate
+        _TRAIN_MODES_ARG = args.train_modes
         names = [c for c in args.case.split(",") if c]
         print(json.dumps({"cases": secondary(hip, ops, timer, names), "gate": _GATE_ON}), flush=True)
         return

@@ -200,6 +200,52 @@ def test_split_k_config3_parity_and_bit_stability(hip, m, n, k):
     assert normwise_rel_err(forced, unsplit) <= gemm_tolerance(k)
 
 
+def _carry_fold_f32(parts):
+    """The split-K fold of partials in partition order: binary-counter carry
+    stack (block + stack[l]), drained from 0.0 in ascending level order
+    (gemm_split_k_reduce.comp:48-85), in float32."""
+    stack = {}
+    for count, v in enumerate(parts):
+        block, lvl = v, 0
+        while (count >> lvl) & 1:
+            block = (block + stack[lvl]).astype(np.float32)
+            lvl += 1
+        stack[lvl] = block
+    total = np.zeros_like(parts[0])
+    for lvl in sorted(stack):
+        if (len(parts) >> lvl) & 1:
+            total = (total + stack[lvl]).astype(np.float32)
+    return total
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 512, 512), (384, 512, 500), (320, 288, 230), (256, 256, 200)])
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+def test_workgroup_folded_split_k_is_the_fold_of_its_partitions(hip, m, n, k, layout):
+    """Products whose plan splits K into 2-4 partitions of at most 4 K-tiles
+    run one launch that folds the partitions' partials in LDS. Their result
+    is, bit for bit, the carry-stack fold of the device's own products over
+    each partition's K range (each of at most 4 K-tiles, never split, so the
+    same MFMA sequence from 0), in NN (16-byte staging) and NT (element
+    staging), ragged K included."""
+    splits, chunk = ops.gemm_plan(1, m, n, k)
+    assert 2 <= splits <= 4 and chunk <= 4, (splits, chunk)
+    rng = np.random.default_rng(SEED + m + n + k)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    b = rng.standard_normal((k, n), dtype=np.float32)
+
+    def prod(x, y):
+        dy = dev(y) if layout == "nn" else dev(np.ascontiguousarray(y.T)).transpose(-2, -1)
+        return ops.matmul(dev(x), dy).numpy()
+
+    full = prod(a, b)
+    parts = []
+    for p in range(splits):
+        k0, k1 = 32 * chunk * p, min(k, 32 * chunk * (p + 1))
+        parts.append(prod(np.ascontiguousarray(a[:, k0:k1]), np.ascontiguousarray(b[k0:k1])))
+    assert full.tobytes() == _carry_fold_f32(parts).tobytes()
+    assert normwise_rel_err(full, O.matmul(a, b)) <= gemm_tolerance(k)
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 4, 7, 16, 17, 33, 35, 64, 128, 511])
 @pytest.mark.parametrize("ne", [1000, 1001])
 def test_split_k_reduce_bit_exact(hip, splits, ne):
