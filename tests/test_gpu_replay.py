@@ -104,6 +104,40 @@ def test_queued_steps_are_the_read_back_steps(config, graph):
     assert finals[0] == finals[1]
 
 
+@pytest.mark.parametrize("graph", [False, True], ids=["replay", "graph"])
+@pytest.mark.parametrize("config", ["mlp", "cnn"])
+def test_resident_inputs_and_device_loss_log_are_the_host_steps(config, graph):
+    """Batches resident in HBM (DeviceArray inputs, copied on the device) and
+    every step's loss kept in a device log (outputs_to, read once at the end,
+    steps queued with read=False) give the losses and parameters of replays
+    fed from host arrays that read every loss back."""
+    from vkml_amd.device import DeviceArray
+
+    dev = T.default_backend()
+    make, _, _, _, lr = CONFIGS[config]
+    batches = _batches(config, 8)
+    runs = []
+    for resident in (False, True):
+        model = make(dev)
+        opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
+        step = T.CapturedStep(_step_fn(model, opt), *batches[0], graph=graph)
+        losses = [np.float32(step.first[0])]
+        if resident:
+            feed = [(DeviceArray.from_numpy(x), DeviceArray.from_numpy(y)) for x, y in batches]
+            shape = step.outputs[0].shape
+            log = DeviceArray((len(batches),) + tuple(shape), np.float32)
+            for i in range(1, len(batches)):
+                assert step(*feed[i], read=False) is None
+                step.outputs_to(DeviceArray(shape, np.float32, None, log.buffer, offset=i))
+            losses += list(log.numpy().reshape(len(batches))[1:])
+        else:
+            losses += [np.float32(step(x, y)[0]) for x, y in batches[1:]]
+        runs.append((np.array(losses, np.float32).tobytes(),
+                     [p.numpy().tobytes() for p in model.parameters()]))
+        step.close()
+    assert runs[0] == runs[1]
+
+
 def test_captured_step_checks_its_inputs():
     dev = T.default_backend()
     model = _mlp(dev)
@@ -114,6 +148,13 @@ def test_captured_step_checks_its_inputs():
         step(x[:32], y[:32])
     with pytest.raises(ValueError):
         step(x)
+    from vkml_amd.device import DeviceArray
+    with pytest.raises(ValueError):  # a device input of another shape
+        step(DeviceArray.from_numpy(x[:32]), y)
+    with pytest.raises(ValueError):  # a non-contiguous device input
+        step(DeviceArray.from_numpy(np.ascontiguousarray(x.transpose(0, 1, 3, 2))).transpose(-2, -1), y)
+    with pytest.raises(ValueError):  # a loss destination of the wrong size
+        step.outputs_to(DeviceArray((2,), np.float32))
     step.close()
     with pytest.raises(RuntimeError):
         step(x, y)

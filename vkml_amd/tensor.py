@@ -1110,11 +1110,16 @@ class CapturedStep:
     queue_depth = 2
 
     def __call__(self, *arrays, read: bool = True):
-        """Uploads `arrays`, replays the step and returns `fn`'s outputs as
-        host arrays. read=False returns None without waiting for the step:
-        the next call's uploads are stream-ordered after this replay, so steps
+        """Copies `arrays` into the recorded inputs, replays the step and
+        returns `fn`'s outputs as host arrays. An input is a host array
+        (uploaded through the pinned staging slots) or a contiguous
+        DeviceArray of the recorded shape and dtype (copied on the device,
+        stream-ordered: a data set kept resident in HBM feeds its steps with no
+        host copy). read=False returns None without waiting for the step: the
+        next call's copies are stream-ordered after this replay, so steps
         queue back to back, at most `queue_depth` of them in flight (the call
-        first waits for the oldest); `outputs_now()` reads the latest step's."""
+        first waits for the oldest); `outputs_now()` reads the latest step's
+        outputs and `outputs_to()` copies them on the device."""
         if self._program is None:
             raise RuntimeError("CapturedStep: closed")
         if not read:
@@ -1127,12 +1132,25 @@ class CapturedStep:
                 self._events[self._queued % self.queue_depth].synchronize()
         if len(arrays) != len(self.inputs):
             raise ValueError(f"CapturedStep: {len(arrays)} inputs, recorded with {len(self.inputs)}")
+        from .device import DeviceArray
+
+        device_copies = []
         for t, a in zip(self.inputs, arrays):
+            if isinstance(a, DeviceArray):
+                if a.shape != t.shape or a.dtype != t.dtype or not a.is_contiguous():
+                    raise ValueError(f"CapturedStep: device input {a.shape} {a.dtype} (contiguous: "
+                                     f"{a.is_contiguous()}), recorded {t.shape} {t.dtype}")
+                dst = t.node.storage.ptr + t.node.offset * t.node.itemsize
+                device_copies.append(_lib.Copy(dst, a.ptr, a.nbytes_dense()))
+                continue
             a = np.asarray(a)
             if a.shape != t.shape or a.dtype != t.dtype:
                 raise ValueError(f"CapturedStep: input {a.shape} {a.dtype}, recorded {t.shape} {t.dtype}")
             host = a.view(np.uint8) if a.dtype == np.bool_ else a
             self.backend.upload(t.node.storage, t.node.offset * t.node.itemsize, host)
+        if device_copies:
+            _lib.check(self.lib.vkhip_copy_device_to_device(
+                (_lib.Copy * len(device_copies))(*device_copies), len(device_copies)), "copy_device_to_device")
         _lib.check(self.lib.vkhip_program_run(self._program, 1 if self.graph else 0), "program_run")
         if read:
             self._queued = 0
@@ -1144,6 +1162,23 @@ class CapturedStep:
     def outputs_now(self) -> list:
         """`fn`'s outputs of the latest replay, as host arrays (waits for it)."""
         return [t.numpy() for t in self.outputs]
+
+    def outputs_to(self, *dsts) -> None:
+        """Copies `fn`'s outputs of the latest replay into the DeviceArrays
+        `dsts` (one per output, contiguous, same byte size), on the device and
+        stream-ordered after the replay: a queued loop keeps, say, every
+        step's loss in a device log and reads the log once."""
+        if len(dsts) != len(self.outputs):
+            raise ValueError(f"CapturedStep: {len(dsts)} destinations for {len(self.outputs)} outputs")
+        copies = []
+        for d, t in zip(dsts, self.outputs):
+            nbytes = t.numel() * t.node.itemsize
+            if not d.is_contiguous() or d.nbytes_dense() != nbytes:
+                raise ValueError(f"CapturedStep: destination of {d.nbytes_dense()} bytes for an output "
+                                 f"of {nbytes}")
+            copies.append(_lib.Copy(d.ptr, t.node.storage.ptr + t.node.offset * t.node.itemsize, nbytes))
+        _lib.check(self.lib.vkhip_copy_device_to_device((_lib.Copy * len(copies))(*copies), len(copies)),
+                   "copy_device_to_device")
 
     def close(self) -> None:
         if self._program is not None:
