@@ -688,6 +688,23 @@ def test_sum_mean_bit_exact(hip, shape, axes):
     assert ops.mean(d, axes).numpy().tobytes() == O.mean(x, axes).tobytes()
 
 
+def test_split_tree_sums_back_to_back(hip):
+    """Split-tree reductions (subtree partials, then their balanced fold)
+    interleaved with different output and subtree counts (64 x 16, 128 x 4,
+    3 x 128, 200 x 4 partials) share the reduction workspace; every result
+    stays the oracle's bits."""
+    rng = np.random.default_rng(SEED + 5)
+    cases = [((128, 64, 32, 32), [0, 2, 3]), ((128, 128, 16, 16), [0, 2, 3]), ((50000, 3), [0]),
+             ((4096, 64), [0]), ((16, 200, 8, 32), [0, 2, 3])]
+    xs = [(rng.standard_normal(shape) * 4).astype(np.float32) for shape, _ in cases]
+    ds = [dev(x) for x in xs]
+    want = [O.sum(x, axes).tobytes() for x, (_, axes) in zip(xs, cases)]
+    for rep in range(3):
+        for i in (0, 2, 1, 4, 3, 0, 0, 1):
+            got = ops.sum(ds[i], cases[i][1]).numpy().tobytes()
+            assert got == want[i], f"repeat {rep}, case {cases[i][0]}"
+
+
 @pytest.mark.parametrize("shape,axis", [((8192, 4096), 1), ((1024, 1024), 1), ((64, 10), 1),
                                         ((100, 37), 0), ((3, 5000), 1)])
 def test_max_min_argmax_exact(hip, shape, axis):
