@@ -27,7 +27,7 @@ LIB = LIBDIR / "libvkhip.so"
 OBJDIR = ROOT / "_build" / "vkhip"
 
 SOURCES = ["runtime.hip", "allocator.hip", "observe.hip", "program.hip", "gemm.hip", "movement.hip",
-           "reduce.hip", "elementwise.hip"]
+           "reduce.hip", "elementwise.hip", "conv_small.hip"]
 
 
 def hipcc() -> str:
@@ -51,8 +51,14 @@ def compile_flags() -> list[str]:
     ]
 
 
+# Per-source additions: the small-window convolution kernels keep their MFMA
+# accumulators in VGPRs, which their epilogues read with plain VALU
+# instructions (from AGPRs each value would first be copied out).
+FILE_FLAGS = {"conv_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path, obj: Path, verbose: bool) -> tuple[Path, str]:
-    cmd = [hipcc(), *compile_flags(), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *compile_flags(), *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = res.stdout + res.stderr
     # hipcc's host pass does not know the packed-fp32 feature and says so; that

@@ -1,0 +1,23 @@
+// Small-window convolutions (conv_small.hip): layers whose window holds at
+// most 32 elements (C*kh*kw <= 32) and whose output has at most 64 channels,
+// the 3-channel first layer of configs 4/5. Internal to the library.
+#pragma once
+
+#include "common.h"
+
+namespace vkhip {
+
+// Whether win_conv_forward takes this forward convolution (oh x ow outputs
+// per image, weights [Cout][C*kh*kw] described by wd).
+bool win_fwd_fits(const vkhip_operand& xd, const vkhip_unfold& pr, uint32_t channels, uint64_t ck,
+                  uint32_t cout, const vkhip_operand& wd, uint32_t oh, uint32_t ow);
+
+// out[n][co][p] = relu?(sum_j w[co][j] * window_j(x[n], p) + bias[co]): the
+// implicit-im2col GEMM's bits (same K pairing and order), plus the epilogue's
+// one rounded add.
+int win_conv_forward(const float* x, const vkhip_operand& xd, const float* w, const vkhip_operand& wd,
+                     float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
+                     uint32_t ck, uint32_t oh, uint32_t ow, const float* bias, int64_t bias_stride,
+                     bool relu);
+
+}  // namespace vkhip

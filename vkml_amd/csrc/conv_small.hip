@@ -1,0 +1,352 @@
+// Small-window convolutions on gfx950 (CDNA4): layers whose window holds at
+// most 32 elements (C*kh*kw <= 32) and whose output has at most 64 channels.
+// CIFAR's first layer, [128,3,32,32] -> 64 channels with a 3x3 window (27
+// elements), is the case in configs 4 and 5 (reference: conv2d,
+// src/api/ops.cpp:662-705, im2col then flat_weight @ cols).
+//
+// Such a layer is one K-tile of a product: 27 of the 32 k of one MFMA chain.
+// Its cost is HBM traffic (the forward writes a 33.5 MB output from a 1.6 MB
+// image) and the issue slots around the matrix core, not the matrix core
+// itself, so these kernels are laid out for few VALU instructions per output.
+//
+// Forward (win_fwd_kernel). A workgroup of four waves takes 4*BPW consecutive
+// 32-position blocks of one image. It stages the input rows those blocks read,
+// zero-bordered by the padding, in LDS, followed by a zero region as long as
+// one channel's rows: window elements past K read there, so the gather needs
+// neither a bounds check nor a select. Each wave computes every output
+// channel (at most 64) of its blocks, with the weights in registers for the
+// whole launch. Step t pairs window elements t and 16 + t (lanes 0-31 and
+// 32-63), the pairing and order of the GEMM kernels' K-tiles, and the
+// accumulator starts at zero: every output is the implicit-im2col GEMM's
+// value bit for bit, then the epilogue's bias add and ReLU, one rounding each,
+// as the graph's ADD and RELU nodes. The accumulator layout puts 32
+// consecutive positions of one channel in the 32 lanes of a half-wave, so
+// each store instruction writes two whole 128-byte rows; the stores are
+// non-temporal buffer stores whose row offset is a scalar operand. (Measured
+// at CIFAR conv1: 9.7 us, against 29 us for the transposed layout whose lanes
+// each store four positions as one 16-byte non-temporal store -- 64 partial
+// lines per instruction -- and 13.2 us for the same with ordinary stores.)
+#include "conv_small.h"
+
+#include <algorithm>
+
+namespace vkhip {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kWinWaves = 4;            // waves per workgroup
+constexpr int kWinThreads = 64 * kWinWaves;
+constexpr int kWinLdsFloats = 16384;    // dynamic LDS per workgroup: 64 KB
+constexpr int kWinWpitch = 33;          // weight row pitch in LDS (odd: lanes on distinct banks)
+
+struct WinFwd {
+    const float* x;
+    int64_t sn, sc, sh, sw;  // image strides (elements)
+    const float* w;          // [Cout][K], row stride wrow, k stride 1
+    int64_t wrow;
+    const float* bias;       // null: no bias
+    int64_t bias_stride;
+    float* out;              // [N][Cout][L] contiguous
+    int32_t C, H, W, padh, padw, strh, strw, OW;
+    int32_t Wp, rows, plane, stage;  // staged rows per channel, plane = rows * Wp, stage = C * plane
+    uint32_t cout, K, L, nblk, wg_per_image;
+    FastDiv div_ow;
+    int32_t sc4, sh4;                // channel and row strides in bytes
+    int32_t q4, r4;                  // 4 = q4 * rows + r4
+    int32_t wave_c[4], wave_r[4];    // staged row w: channel and padded row
+    int32_t offs[32];  // window element j's offset in the stage; j >= K: the zero region
+};
+
+// T: 32-channel tiles (1 or 2); BPW: blocks per wave; RELU: the epilogue's
+// ReLU; FULL: Cout = 32*T and L % 32 == 0 (every store unconditional).
+// Without a bias the epilogue adds +0, which leaves every value's bits as
+// they are: a chain that starts from +0 never ends at -0.
+template <int T, int BPW, bool RELU, bool FULL>
+__global__ __launch_bounds__(kWinThreads) void win_fwd_kernel(WinFwd p) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, kh = lane >> 5;
+    const uint32_t n = blockIdx.y;
+    const uint32_t b0 = blockIdx.x * static_cast<uint32_t>(kWinWaves * BPW);
+    float* img = smem;                                    // [C][rows][Wp], then `plane` zeros
+    float* wts = smem + ((p.stage + p.plane + 3) & ~3);   // [64][kWinWpitch]
+    int32_t* offs_l = reinterpret_cast<int32_t*>(wts + 64 * kWinWpitch);  // [32]
+    float* bias_l = wts + 64 * kWinWpitch + 32;  // [64]
+    const int32_t row_a = static_cast<int32_t>(p.div_ow.div(32u * b0)) * p.strh;
+
+    // The set-up's global loads in one batch. Buffer loads return 0 past the
+    // resource (offsets with bit 31 set): the padding columns and the weight
+    // slots past K or Cout are loaded as zeros without a select.
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.x + static_cast<int64_t>(n) * p.sn), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.w), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    // weights: thread slot e = tid + 256u is channel (tid >> 5) + 8u, element tid & 31
+    const uint32_t wj = static_cast<uint32_t>(tid) & 31u, wc = static_cast<uint32_t>(tid) >> 5;
+    const uint32_t wvoff = wj < p.K ? (wc * static_cast<uint32_t>(p.wrow) + wj) * 4u : 0x80000000u;
+    float we[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        uint32_t voff = wvoff + static_cast<uint32_t>(u) * (32u * static_cast<uint32_t>(p.wrow));
+        if (8u * u + 8u > p.cout) voff = wc + 8u * u < p.cout ? voff : 0x80000000u;
+        we[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, static_cast<int32_t>(voff), 0, 0));
+    }
+    const int32_t my_off = p.offs[lane & 31];
+    // staged rows: wave-uniform row (channel c, padded row rr), lane = padded column
+    const int32_t nrows = p.C * p.rows;
+    const int w_in = lane - p.padw;
+    const bool col_in = lane < p.Wp && static_cast<uint32_t>(w_in) < static_cast<uint32_t>(p.W);
+    const uint32_t xvoff = col_in ? static_cast<uint32_t>(w_in) * static_cast<uint32_t>(p.sw) * 4u : 0x80000000u;
+    // row wave + 4u is channel c, padded row rr, walked incrementally
+    // (4 = q4 * rows + r4)
+    constexpr int U = 16;  // staged rows per wave at most (the launch checks C * rows <= 64)
+    float sv[U];
+    int32_t c = p.wave_c[wave], rr = p.wave_r[wave];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        sv[u] = 0.0f;
+        if (wave + kWinWaves * u >= nrows) break;
+        {
+            const int32_t h = row_a + rr - p.padh;
+            if (static_cast<uint32_t>(h) < static_cast<uint32_t>(p.H))
+                sv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                      xr, static_cast<int32_t>(xvoff), c * p.sc4 + h * p.sh4, 0));
+        }
+        rr += p.r4;
+        c += p.q4;
+        if (rr >= p.rows) {
+            rr -= p.rows;
+            ++c;
+        }
+    }
+
+    // LDS: the zero region, the weights, the window offsets, the staged rows.
+    for (int e = tid; e < p.plane; e += kWinThreads) img[p.stage + e] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) wts[(wc + 8u * u) * kWinWpitch + wj] = we[u];
+    if (tid < 32) offs_l[tid] = my_off;
+    if (tid < 64) bias_l[tid] = p.bias && static_cast<uint32_t>(tid) < p.cout ? p.bias[tid * p.bias_stride] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int32_t row = wave + kWinWaves * u;
+        if (row >= nrows) break;
+        if (lane < p.Wp) img[row * p.Wp + lane] = sv[u];
+    }
+    __syncthreads();
+
+    // This lane's weights (B: window element t + 16*kh of channel 32i + lrow,
+    // zero past K or Cout) and window offsets.
+    const float* wl = wts + lrow * kWinWpitch + 16 * kh;
+    float bw[T][16];
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) bw[i][t] = wl[i * 32 * kWinWpitch + t];
+    int32_t off[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) off[t] = offs_l[16 * kh + t];
+    float bv[T][16];  // the bias of channel 32i + 8(r/4) + 4kh + r%4
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bv[i][r] = bias_l[32 * i + 8 * (r / 4) + 4 * kh + r % 4];
+    // every set-up read lands before the first block's chain starts
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    const __amdgpu_buffer_rsrc_t outr = __builtin_amdgcn_make_buffer_rsrc(
+        p.out + static_cast<uint64_t>(n) * p.cout * p.L, 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+
+    // Block u of this wave is b0 + wave + 4u. Blocks are software-pipelined:
+    // block u's MFMA chain is issued before block u-1's epilogue, so that one
+    // wave keeps the matrix core busy while its previous outputs are biased,
+    // rectified and stored. Blocks past the image (a partial last workgroup)
+    // are computed on clamped positions and not stored.
+    auto gather = [&](uint32_t b, float (&av)[16]) {
+        const uint32_t pos = 32u * min(b, p.nblk - 1u) + lrow;
+        const uint32_t pc = FULL ? pos : min(pos, p.L - 1u);
+        const uint32_t oh = p.div_ow.div(pc), ow = pc - oh * static_cast<uint32_t>(p.OW);
+        const int32_t base = (static_cast<int32_t>(oh) * p.strh - row_a) * p.Wp + static_cast<int32_t>(ow) * p.strw;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) av[t] = img[base + off[t]];
+    };
+    auto chain = [&](const float (&av)[16], v16f (&acc)[T]) {
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+#pragma unroll
+            for (int i = 0; i < T; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(bw[i][t], av[t], acc[i], 0, 0, 0);
+    };
+    // lane (lrow, kh) holds channel 32i + 8(r/4) + 4kh + r%4 of position
+    // 32b + lrow in acc[i][r]: each store instruction writes two whole
+    // 128-byte rows of 32 positions
+    auto epilogue = [&](uint32_t b, const v16f (&acc)[T]) {
+        if (!FULL && b >= p.nblk) return;
+        const uint32_t pos = 32u * b + lrow;
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            const uint32_t voff = (pos + (32u * i + 4u * kh) * p.L) * 4u;
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float x = acc[i][r] + bv[i][r];
+                if (RELU) x = x <= 0.0f ? 0.0f : x;
+                v[r] = x;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t co = 32u * i + 8u * (r / 4) + 4u * kh + r % 4;
+                if (FULL || (co < p.cout && pos < p.L))
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v[r]), outr, static_cast<int32_t>(voff),
+                                                          static_cast<int32_t>((8 * (r / 4) + r % 4) * p.L * 4u), 2);
+            }
+        }
+    };
+    const uint32_t bw0 = b0 + static_cast<uint32_t>(wave);
+    v16f acc[2][T];
+    float av[2][16];
+    gather(bw0, av[0]);
+#pragma unroll
+    for (int u = 0; u < BPW; ++u) {
+        // the next block's window values are read while this block's chain runs
+        if (u + 1 < BPW) gather(bw0 + kWinWaves * (u + 1), av[(u + 1) & 1]);
+        chain(av[u & 1], acc[u & 1]);
+        if (u > 0) epilogue(bw0 + kWinWaves * (u - 1), acc[(u - 1) & 1]);
+    }
+    epilogue(bw0 + kWinWaves * (BPW - 1), acc[(BPW - 1) & 1]);
+}
+
+// Padded input rows per channel that the most demanding workgroup of
+// `bpw`-block waves reads.
+int32_t win_rows(uint32_t L, uint32_t ow, int32_t strh, int32_t kh, int32_t dilh, int32_t hp, uint32_t bpw) {
+    const uint32_t span = 32u * kWinWaves * bpw;
+    int32_t rows = 1;
+    for (uint32_t first = 0; first < L; first += span) {
+        const uint32_t last = std::min(L, first + span) - 1u;
+        rows = std::max(rows, static_cast<int32_t>(last / ow - first / ow) * strh + (kh - 1) * dilh + 1);
+    }
+    return std::min(rows, hp);
+}
+
+// LDS floats of a workgroup: the staged rows, the zero region, the weights,
+// the window offsets.
+size_t win_lds_floats(int32_t channels, int32_t rows, int32_t wp) {
+    return ((static_cast<size_t>(channels + 1) * rows * wp + 3) & ~size_t(3)) + 64 * kWinWpitch + 32 + 64;
+}
+
+// Blocks per wave. One, with four waves per SIMD resident: the other
+// waves' chains hide each wave's set-up and store waits. Measured at CIFAR
+// conv1 (all bit-identical): 9.6 us at one block per wave, 15.0 us at two
+// and 12.8 us at four (the pipelined loop below, 2 or 1 waves per SIMD).
+constexpr uint32_t kWinBpw = 1;
+
+}  // namespace
+
+bool win_fwd_fits(const vkhip_operand& xd, const vkhip_unfold& pr, uint32_t channels, uint64_t ck,
+                  uint32_t cout, const vkhip_operand& wd, uint32_t oh, uint32_t ow) {
+    const int64_t hp = static_cast<int64_t>(pr.image_h) + 2 * pr.pad_h;
+    const int64_t wp = static_cast<int64_t>(pr.image_w) + 2 * pr.pad_w;
+    const uint64_t L = static_cast<uint64_t>(oh) * ow;
+    if (!(ck >= 1 && ck <= 32 && cout >= 1 && cout <= 64 && (wd.nb[3] == 1 || ck == 1) && wp <= 64 &&
+          hp <= 0x7fffffff && L >= 1 && L <= 0x7fffffffull && ow >= 1 && channels >= 1))
+        return false;
+    // 32-bit byte offsets below bit 31 for the image and the weights (buffer loads)
+    if (xd.nb[1] < 0 || xd.nb[2] < 0 || xd.nb[3] < 0 || wd.nb[2] < 0) return false;
+    const int64_t span = (static_cast<int64_t>(channels) - 1) * xd.nb[1] +
+                         (static_cast<int64_t>(pr.image_h) - 1) * xd.nb[2] +
+                         (static_cast<int64_t>(pr.image_w) - 1) * xd.nb[3] + 1;
+    const int64_t wspan = (static_cast<int64_t>(cout) - 1) * wd.nb[2] + static_cast<int64_t>(ck) + 8 * wd.nb[2];
+    if (span > (int64_t(1) << 28) || wspan > (int64_t(1) << 28) || static_cast<uint64_t>(cout) * L > (1ull << 28))
+        return false;
+    const int32_t rows = win_rows(static_cast<uint32_t>(L), ow, pr.stride_h, pr.kernel_h, pr.dilation_h,
+                                  static_cast<int32_t>(hp), kWinBpw);
+    return static_cast<int64_t>(channels) * rows <= 16 * kWinWaves &&
+           win_lds_floats(static_cast<int32_t>(channels), rows, static_cast<int32_t>(wp)) <= kWinLdsFloats;
+}
+
+int win_conv_forward(const float* x, const vkhip_operand& xd, const float* w, const vkhip_operand& wd,
+                     float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
+                     uint32_t ck, uint32_t oh, uint32_t ow, const float* bias, int64_t bias_stride,
+                     bool relu) {
+    WinFwd p{};
+    p.x = x;
+    p.sn = xd.nb[0];
+    p.sc = xd.nb[1];
+    p.sh = xd.nb[2];
+    p.sw = xd.nb[3];
+    p.w = w;
+    p.wrow = wd.nb[2];
+    p.bias = bias;
+    p.bias_stride = bias_stride;
+    p.out = out;
+    p.C = static_cast<int32_t>(channels);
+    p.H = pr.image_h;
+    p.W = pr.image_w;
+    p.padh = pr.pad_h;
+    p.padw = pr.pad_w;
+    p.strh = pr.stride_h;
+    p.strw = pr.stride_w;
+    p.OW = static_cast<int32_t>(ow);
+    p.Wp = pr.image_w + 2 * pr.pad_w;
+    const int32_t hp = pr.image_h + 2 * pr.pad_h;
+    p.cout = cout;
+    p.K = ck;
+    p.L = oh * ow;
+    p.nblk = (p.L + 31u) / 32u;
+    p.div_ow = FastDiv(ow);
+    constexpr uint32_t bpw = kWinBpw;
+    p.rows = win_rows(p.L, ow, p.strh, pr.kernel_h, pr.dilation_h, hp, bpw);
+    p.plane = p.rows * p.Wp;
+    p.stage = p.C * p.plane;
+    p.sc4 = static_cast<int32_t>(xd.nb[1] * 4);
+    p.sh4 = static_cast<int32_t>(xd.nb[2] * 4);
+    p.q4 = kWinWaves / p.rows;
+    p.r4 = kWinWaves % p.rows;
+    for (int w = 0; w < kWinWaves; ++w) {
+        p.wave_c[w] = w / p.rows;
+        p.wave_r[w] = w % p.rows;
+    }
+    const int32_t kk = pr.kernel_h * pr.kernel_w;
+    for (uint32_t j = 0; j < 32; ++j) {
+        if (j >= ck) {
+            p.offs[j] = p.stage;
+            continue;
+        }
+        const int32_t c = static_cast<int32_t>(j) / kk, r = static_cast<int32_t>(j) % kk;
+        const int32_t ki = r / pr.kernel_w, kj = r % pr.kernel_w;
+        p.offs[j] = c * p.plane + ki * pr.dilation_h * p.Wp + kj * pr.dilation_w;
+    }
+    const size_t lds = win_lds_floats(p.C, p.rows, p.Wp);
+    if (p.C * p.rows > 16 * kWinWaves || lds > kWinLdsFloats)
+        return fail(VKHIP_ERR_INVALID, "conv2d: staged rows exceed the small-window stage");
+    p.wg_per_image = (p.nblk + kWinWaves * bpw - 1) / (kWinWaves * bpw);
+    if (batch > 65535)
+        return fail(VKHIP_ERR_UNSUPPORTED, "conv2d: batch %u above the grid's 65535", batch);
+    const bool two = cout > 32;
+    const bool full = cout == (two ? 64u : 32u) && p.L % 32 == 0;
+    const dim3 g(p.wg_per_image, batch), blk(kWinThreads);
+    const size_t bytes = lds * sizeof(float);
+#define VKHIP_WINF(T, B, R, F) hipLaunchKernelGGL((win_fwd_kernel<T, B, R, F>), g, blk, bytes, ctx().stream, p)
+#define VKHIP_WINF_F(T, B, R)                                             \
+    do {                                                                  \
+        if (full) VKHIP_WINF(T, B, R, true); else VKHIP_WINF(T, B, R, false); \
+    } while (0)
+#define VKHIP_WINF_R(T, B)                                                \
+    do {                                                                  \
+        if (relu) VKHIP_WINF_F(T, B, true); else VKHIP_WINF_F(T, B, false);   \
+    } while (0)
+    static_assert(kWinBpw == 1, "instantiate the launch for other blocks per wave");
+    if (two) VKHIP_WINF_R(2, 1); else VKHIP_WINF_R(1, 1);
+#undef VKHIP_WINF_R
+#undef VKHIP_WINF_F
+#undef VKHIP_WINF
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+}  // namespace vkhip

@@ -20,6 +20,7 @@
 //     of the tile, so each lane's k values are contiguous in LDS. The sum over
 //     k is unchanged; only the order MFMA visits the k values differs.
 #include "common.h"
+#include "conv_small.h"
 
 #include <mutex>
 #include <vector>
@@ -3077,20 +3078,10 @@ static int launch_wgrad_small(bool fold, const float* gr, const vkhip_operand& g
     return VKHIP_OK;
 }
 
-// ---- small-window convolution forward -----------------------------------------
-// A convolution whose window holds at most 32 elements (C*kh*kw <= 32: CIFAR's
-// 3-channel 3x3 layer has 27) and at most 64 output channels is a product with
-// one K-tile: every output is 16 MFMA steps, and the layer is bound by writing
-// its output (33.5 MB at [128,3,32,32] -> 64, against 1.6 MB of image). This
-// kernel stages one image, zero-bordered by the padding, in LDS, keeps the
-// weights in registers for the whole launch, and walks 32-position blocks:
-// per block a wave gathers each lane's 16 window values from LDS (no bounds
-// checks: the border holds the padding's zeros), runs the 16 steps for each
-// 32-channel tile, adds the bias, applies the ReLU and streams the 32 x 32
-// outputs to memory (non-temporal). Step t pairs window elements t and 16 + t
-// (lanes 0-31 and 32-63), the pairing and order of every GEMM kernel's K-tile
-// here, so the outputs are the implicit-im2col GEMM's (and the im2col +
-// matmul graph's) bits.
+// ---- small-window convolution staging ---------------------------------------
+// The image geometry and LDS staging shared by the small-window weight-gradient
+// kernels below (windows of at most 32 elements, at most 64 output channels;
+// the forward of such layers runs win_fwd_kernel, conv_small.hip).
 constexpr int kSmallFwdLds = 8192;  // floats of staged (zero-bordered) image
 
 struct SmallConvFwd {
@@ -3147,193 +3138,6 @@ __device__ __forceinline__ void stage_store(float* lds, const float (&v)[U], con
         if (e < staged) lds[e] = v[u];
     }
     if (tid == 0) lds[staged] = 0.0f;
-}
-
-// One wave per 32-position block and 32-channel tile: few registers per wave
-// (16 weights, 16 window values, one accumulator), so that six or more waves
-// per SIMD keep the output streaming. A workgroup of 4 blocks x T tiles (T
-// waves per block) stages the input rows its blocks read in dynamic LDS:
-// [C][p.rows][Wp] then one zero, followed by the weights and the bias.
-// U: staged rows per wave (at most); FLAT: weights [Cout][K] contiguous,
-// 16-byte aligned, Cout*K % 4 == 0; FULL: Cout = 32*T and whole blocks of
-// positions (L % 32 == 0), so that every store is unconditional (measured
-// 1.3 us of the CIFAR conv1 layer's 14.3 go to the branches around guarded
-// stores).
-template <int T, int U, bool FLAT, bool FULL>
-__global__ __launch_bounds__(256 * T) void conv_small_fwd_kernel(SmallConvFwd p) {
-    extern __shared__ __attribute__((aligned(16))) float smem[];
-    constexpr int NW = 4 * T;  // waves
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lrow = lane & 31, kh = lane >> 5;
-    const int tile = T == 2 ? (wave & 1) : 0;
-    const int wblk = T == 2 ? (wave >> 1) : wave;
-    const uint32_t n = blockIdx.x / p.wg_per_image;
-    const uint32_t part = blockIdx.x - n * p.wg_per_image;
-    const uint32_t b0 = part * p.blocks_per_wg;
-    const uint32_t b1 = min(p.nblk, b0 + p.blocks_per_wg);
-    const int32_t zslot = p.C * p.plane;         // the staged zero
-    float* img = smem;
-    float* wts = smem + ((zslot + 4) & ~3);      // [co][j], pitch wpitch (16-byte aligned)
-    float* bias_rows = wts + 64 * 33;
-    int32_t* offs = reinterpret_cast<int32_t*>(bias_rows + 64);
-    // the padded input rows this workgroup's outputs read: from output row
-    // oh_a's window top, p.rows of them per channel
-    const uint32_t oh_a = p.div_ow.div(32u * b0);
-    const int32_t row_a = static_cast<int32_t>(oh_a) * p.strh;
-
-    // every global load of the set-up in one batch: the weights, the window
-    // offsets, the bias and the staged rows. Weights stored [Cout][K]
-    // contiguously are copied as they lie (16-byte loads) and read with
-    // pitch K (odd pitches keep the lanes' reads on distinct banks);
-    // otherwise element by element into a pitch of 33.
-    const uint32_t wpitch = FLAT ? p.K : 33u;
-    constexpr int WV = 2 / T;  // 16-byte weight loads per thread (512 of them at most)
-    f32x4 wv[WV];
-    if constexpr (FLAT) {
-        const uint32_t n4 = p.cout * p.K / 4;
-#pragma unroll
-        for (int u = 0; u < WV; ++u) {
-            const uint32_t e = static_cast<uint32_t>(tid) + 64u * NW * u;
-            wv[u] = reinterpret_cast<const f32x4*>(p.w)[e < n4 ? e : 0u];
-        }
-    }
-    const int32_t my_off = p.offs[tid & 31];
-    // (no branch around the bias load: with no bias it reads a weight and
-    // discards it, so the loads stay one batch)
-    const float* bsrc = p.bias ? p.bias : p.w;
-    const int64_t bstride = p.bias ? p.bias_stride : 0;
-    const float bload = bsrc[static_cast<int64_t>(min(static_cast<uint32_t>(tid & 63), p.cout - 1u)) * bstride];
-    const float my_bias = p.bias ? bload : 0.0f;
-    // staged rows: wave w takes rows w, w + NW, ... of the C * p.rows, lane =
-    // padded column (Wp <= 64); the row's channel and padded row index are
-    // wave-uniform, the clamped rows past the end are loaded and not stored
-    const float* xn = p.x + static_cast<int64_t>(n) * p.sn;
-    const int32_t nrows = p.C * p.rows;
-    const int w_in = lane - p.padw;
-    const bool col_in = lane < p.Wp && static_cast<uint32_t>(w_in) < static_cast<uint32_t>(p.W);
-    const int wcl = min(max(w_in, 0), p.W - 1);
-    float sv[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int32_t row = min(wave + NW * u, nrows - 1);
-        const int32_t c = row / p.rows, rr = row - c * p.rows;
-        const int32_t h = row_a + rr - p.padh;
-        const bool in = col_in && static_cast<uint32_t>(h) < static_cast<uint32_t>(p.H);
-        const int32_t hcl = min(max(h, 0), p.H - 1);
-        const float x = xn[static_cast<int64_t>(c) * p.sc + static_cast<int64_t>(hcl) * p.sh +
-                           static_cast<int64_t>(wcl) * p.sw];
-        sv[u] = in ? x : 0.0f;
-    }
-    if constexpr (FLAT) {
-        const uint32_t n4 = p.cout * p.K / 4;
-#pragma unroll
-        for (int u = 0; u < WV; ++u) {
-            const uint32_t e = static_cast<uint32_t>(tid) + 64u * NW * u;
-            if (e < n4) reinterpret_cast<f32x4*>(wts)[e] = wv[u];
-        }
-    } else {
-        for (uint32_t e = tid; e < p.cout * 32u; e += 64u * NW) {
-            const uint32_t co = e >> 5, j = e & 31;
-            if (j < p.K) wts[co * 33 + j] = p.w[static_cast<int64_t>(co) * p.wrow + j];
-        }
-    }
-    if (tid < 32) offs[tid] = static_cast<uint32_t>(tid) < p.K ? my_off : -1;
-    if (tid < 64) bias_rows[tid] = static_cast<uint32_t>(tid) < p.cout ? my_bias : 0.0f;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int32_t row = wave + NW * u;
-        if (row < nrows && lane < p.Wp) {
-            const int32_t c = row / p.rows, rr = row - c * p.rows;
-            img[c * p.plane + rr * p.Wp + lane] = sv[u];
-        }
-    }
-    if (tid == 0) img[zslot] = 0.0f;
-    __syncthreads();
-
-    // this lane's weights (its tile's channel lrow) and window offsets for the
-    // 16 steps (window element j = t + 16*kh; past K: weight 0 and the zero)
-    const uint32_t co_l = 32u * tile + lrow;
-    float a[16];
-    int32_t off[16];
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        const uint32_t j = static_cast<uint32_t>(t + 16 * kh);
-        off[t] = offs[j];
-        const bool in = co_l < p.cout && j < p.K;
-        const float w = wts[(in ? co_l : 0u) * wpitch + (in ? j : 0u)];
-        a[t] = in ? w : 0.0f;
-    }
-    const bool full = p.cout >= 32u * (tile + 1);
-    const bool has_bias = p.bias != nullptr, relu = p.relu != 0;
-    float* outn = p.out + static_cast<uint64_t>(n) * p.cout * p.L + static_cast<uint64_t>(32u * tile) * p.L;
-    // the wave's blocks: b0 + wblk, + 4, ...; the stores of one block drain
-    // while the next block gathers and multiplies
-    for (uint32_t b = b0 + static_cast<uint32_t>(wblk); b < b1; b += 4) {
-        const uint32_t pos = 32u * b + lrow;
-        const bool valid = pos < p.L;
-        const uint32_t pc = valid ? pos : 0u;
-        const uint32_t oh = p.div_ow.div(pc), ow = pc - oh * static_cast<uint32_t>(p.OW);
-        const int32_t base = (static_cast<int32_t>(oh) * p.strh - row_a) * p.Wp + static_cast<int32_t>(ow) * p.strw;
-        float bv[16];
-#pragma unroll
-        for (int t = 0; t < 16; ++t) bv[t] = img[off[t] >= 0 ? base + off[t] : zslot];
-        f32x16 acc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], bv[t], acc, 0, 0, 0);
-        // epilogue: the bias add and the ReLU (uniform choices), row
-        // 8(r/4) + 4kh + r%4 of the lane's column of this tile
-        const uint32_t loff = 4u * kh * p.L + pos;
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-            const f32x4 bq = *reinterpret_cast<const f32x4*>(&bias_rows[32 * tile + 8 * g4 + 4 * kh]);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float v = acc[4 * g4 + q];
-                if (has_bias) v = v + bq[q];
-                if (relu) v = v <= 0.0f ? 0.0f : v;
-                const uint32_t rowu = 8u * g4 + q;
-                if (FULL || (valid && (full || 32u * tile + rowu + 4u * kh < p.cout)))
-                    __builtin_nontemporal_store(v, outn + static_cast<uint64_t>(rowu) * p.L + loff);
-            }
-        }
-    }
-}
-
-// Blocks of 32 positions per workgroup of conv_small_fwd_kernel: 16, four
-// per wave, so that each wave's stores of one block drain while it computes the
-// next (CIFAR conv1: 16 output rows of an image per workgroup, 256 workgroups).
-constexpr uint32_t kSmallFwdBlocks = 16;
-
-// Padded input rows per channel that the most demanding workgroup of
-// conv_small_fwd_kernel reads.
-static int32_t conv_small_fwd_rows(uint32_t L, uint32_t ow, int32_t strh, int32_t kh, int32_t dilh,
-                                   int32_t hp) {
-    int32_t rows = 1;
-    for (uint32_t first = 0; first < L; first += 32u * kSmallFwdBlocks) {
-        const uint32_t last = std::min(L, first + 32u * kSmallFwdBlocks) - 1u;
-        rows = std::max(rows, static_cast<int32_t>(last / ow - first / ow) * strh + (kh - 1) * dilh + 1);
-    }
-    return std::min(rows, hp);
-}
-
-// Whether conv_small_fwd_kernel takes a forward convolution (see above): a
-// window of at most 32 elements, at most 64 output channels, padded rows of
-// at most 64 columns (one per lane) and at most 16 staged rows per wave.
-static bool conv_small_fwd_fits(const vkhip_unfold& pr, uint32_t channels, uint64_t ck, uint32_t cout,
-                                const vkhip_operand& wd, uint32_t L, uint32_t ow) {
-    const int64_t hp = static_cast<int64_t>(pr.image_h) + 2 * pr.pad_h;
-    const int64_t wp = static_cast<int64_t>(pr.image_w) + 2 * pr.pad_w;
-    if (!(ck >= 1 && ck <= 32 && cout >= 1 && cout <= 64 && (wd.nb[3] == 1 || ck == 1) && wp <= 64 &&
-          hp <= 0x7fffffff && L >= 1 && ow >= 1))
-        return false;
-    const int64_t rows = conv_small_fwd_rows(L, ow, pr.stride_h, pr.kernel_h, pr.dilation_h,
-                                             static_cast<int32_t>(hp));
-    const int64_t waves = cout > 32 ? 8 : 4;
-    return static_cast<int64_t>(channels) * rows <= 16 * waves &&
-           static_cast<int64_t>(channels) * rows * wp + 1 < kSmallFwdLds;
 }
 
 // ---- small-window convolution weight gradient, summed over the batch ----------
@@ -3542,60 +3346,6 @@ static int launch_conv_wgrad_stream(SmallConvFwd p, const float* gr, const vkhip
     return VKHIP_OK;
 }
 
-static int launch_conv_small_fwd(const float* x, const vkhip_operand& xd, const float* w,
-                                 const vkhip_operand& wd, float* out, const vkhip_unfold& pr,
-                                 uint32_t batch, uint32_t channels, uint32_t cout, uint32_t ck,
-                                 uint32_t oh, uint32_t ow, const float* bias, int64_t bias_stride,
-                                 bool relu) {
-    SmallConvFwd p = small_conv_geometry(x, xd, pr, channels, cout, ck, oh, ow);
-    p.w = w;
-    p.wrow = wd.nb[2];
-    p.w_flat4 = (p.wrow == static_cast<int64_t>(ck) || cout == 1) && (static_cast<uint64_t>(cout) * ck) % 4 == 0 &&
-                reinterpret_cast<uintptr_t>(w) % 16 == 0;
-    p.bias = bias;
-    p.bias_stride = bias_stride;
-    p.relu = relu ? 1u : 0u;
-    p.out = out;
-    // Each workgroup stages only the input rows its blocks read.
-    p.blocks_per_wg = kSmallFwdBlocks;
-    p.wg_per_image = ceil_div(p.nblk, p.blocks_per_wg);
-    p.rows = conv_small_fwd_rows(p.L, ow, p.strh, pr.kernel_h, p.dilh, p.Hp);
-    p.plane = p.rows * p.Wp;
-    for (uint32_t j = 0; j < 32; ++j) {
-        const uint32_t jc = j < ck ? j : 0u;
-        const uint32_t c = jc / static_cast<uint32_t>(p.kk), r = jc % static_cast<uint32_t>(p.kk);
-        const uint32_t ki = r / static_cast<uint32_t>(p.kw), kj = r % static_cast<uint32_t>(p.kw);
-        p.offs[j] = static_cast<int32_t>(c) * p.plane + static_cast<int32_t>(ki) * p.dilh * p.Wp +
-                    static_cast<int32_t>(kj) * p.dilw;
-    }
-    if (p.C * p.plane >= kSmallFwdLds)
-        return fail(VKHIP_ERR_INVALID, "conv2d: staged rows exceed the stage");
-    const uint64_t grid = static_cast<uint64_t>(batch) * p.wg_per_image;
-    if (grid > 0x7fffffffull) return fail(VKHIP_ERR_UNSUPPORTED, "conv2d: %llu workgroups",
-                                          static_cast<unsigned long long>(grid));
-    const uint32_t tiles = cout > 32 ? 2u : 1u;
-    const uint32_t rounds = ceil_div(static_cast<uint32_t>(p.C * p.rows), 4u * tiles);  // staged rows per wave
-    // dynamic LDS: the staged rows and their zero (rounded to 16 bytes), the
-    // weights (64 x 33), the bias (64) and the offsets (32)
-    const size_t lds = (static_cast<size_t>((p.C * p.plane + 4) & ~3) + 64 * 33 + 64 + 32) * sizeof(float);
-    const bool full = cout == 32u * tiles && p.L % 32 == 0;
-#define VKHIP_SFW(T, U, F, FU) \
-    hipLaunchKernelGGL((conv_small_fwd_kernel<T, U, F, FU>), dim3(static_cast<uint32_t>(grid)), dim3(256 * T), lds, ctx().stream, p)
-#define VKHIP_SFW_U(T, F, FU) \
-    do { if (rounds <= 8) VKHIP_SFW(T, 8, F, FU); else VKHIP_SFW(T, 16, F, FU); } while (0)
-    if (p.w_flat4 && full) {
-        if (tiles == 2) VKHIP_SFW_U(2, true, true); else VKHIP_SFW_U(1, true, true);
-    } else if (p.w_flat4) {
-        if (tiles == 2) VKHIP_SFW_U(2, true, false); else VKHIP_SFW_U(1, true, false);
-    } else {
-        if (tiles == 2) VKHIP_SFW_U(2, false, false); else VKHIP_SFW_U(1, false, false);
-    }
-#undef VKHIP_SFW_U
-#undef VKHIP_SFW
-    VKHIP_LAUNCH_CHECK();
-    return VKHIP_OK;
-}
-
 int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
                    const vkhip_operand& wd, float* out, const vkhip_unfold& p, const float* bias,
                    int64_t bias_stride, bool relu) {
@@ -3650,13 +3400,12 @@ int conv2d_forward(const float* x, const vkhip_operand& xd, const float* w,
         if (st != VKHIP_OK) return st;
         return launch_conv_epilogue(out, batch * m * n, n, m, bias, bias_stride, relu);
     }
-    if (conv_small_fwd_fits(p, channels, k, m, wd, static_cast<uint32_t>(oh * ow), static_cast<uint32_t>(ow))) {
-        publish("matmul.kernel", "conv2d", "conv_small_fwd", "gemm_mfma_implicit_im2col",
+    if (win_fwd_fits(xd, p, channels, k, m, wd, static_cast<uint32_t>(oh), static_cast<uint32_t>(ow))) {
+        publish("matmul.kernel", "conv2d", "win_fwd", "gemm_mfma_implicit_im2col",
                 "a window of at most 32 elements and at most 64 output channels: one K-tile per output",
                 static_cast<int64_t>(k), static_cast<int64_t>(m));
-        return launch_conv_small_fwd(x, xd, w, wd, out, p, static_cast<uint32_t>(batch), channels, m, k,
-                                     static_cast<uint32_t>(oh), static_cast<uint32_t>(ow), bias,
-                                     bias_stride, relu);
+        return win_conv_forward(x, xd, w, wd, out, p, static_cast<uint32_t>(batch), channels, m, k,
+                                static_cast<uint32_t>(oh), static_cast<uint32_t>(ow), bias, bias_stride, relu);
     }
     uint32_t splits, chunk;
     TileChoice tile;
