@@ -341,6 +341,10 @@ CONVS = [  # (x shape, Cout, kernel, stride, pad, dilation)
     ((128, 64, 32, 32), 64, (3, 3), (1, 1), (1, 1), (1, 1)),
     ((128, 64, 16, 16), 128, (3, 3), (1, 1), (1, 1), (1, 1)),
     ((1, 64, 8, 8), 128, (3, 3), (1, 1), (1, 1), (1, 1)),
+    # the small-window forward with whole blocks but fewer than a workgroup's
+    # four: the blocks past the image compute and must not store
+    ((3, 8, 8, 8), 32, (1, 1), (1, 1), (0, 0), (1, 1)),
+    ((2, 3, 8, 12), 64, (3, 3), (1, 1), (1, 1), (1, 1)),
 ]
 
 

@@ -20,4 +20,15 @@ int win_conv_forward(const float* x, const vkhip_operand& xd, const float* w, co
                      uint32_t ck, uint32_t oh, uint32_t ow, const float* bias, int64_t bias_stride,
                      bool relu);
 
+// Whether win_conv_weight_grad_sum takes this batch-summed weight gradient
+// (gradient [N][Cout][oh*ow] described by gd).
+bool win_wgrad_fits(const float* g, const vkhip_operand& gd, const vkhip_operand& xd, const vkhip_unfold& pr,
+                    uint32_t channels, uint64_t ck, uint32_t cout, uint64_t batch, uint32_t oh, uint32_t ow);
+
+// dW[co][j] = sum over n, p of g[n][co][p] * window_j(x[n], p), one launch
+// (the partials folded inside it, in a fixed order).
+int win_conv_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* g, const vkhip_operand& gd,
+                             float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
+                             uint32_t ck, uint32_t oh, uint32_t ow);
+
 }  // namespace vkhip

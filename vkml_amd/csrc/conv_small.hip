@@ -60,7 +60,8 @@ struct WinFwd {
 };
 
 // T: 32-channel tiles (1 or 2); BPW: blocks per wave; RELU: the epilogue's
-// ReLU; FULL: Cout = 32*T and L % 32 == 0 (every store unconditional).
+// ReLU; FULL: Cout = 32*T and L % 32 == 0 (every store of a block inside the
+// image unconditional).
 // Without a bias the epilogue adds +0, which leaves every value's bits as
 // they are: a chain that starts from +0 never ends at -0.
 template <int T, int BPW, bool RELU, bool FULL>
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(kWinThreads) void win_fwd_kernel(WinFwd p) {
     // 32b + lrow in acc[i][r]: each store instruction writes two whole
     // 128-byte rows of 32 positions
     auto epilogue = [&](uint32_t b, const v16f (&acc)[T]) {
-        if (!FULL && b >= p.nblk) return;
+        if (b >= p.nblk) return;  // the last workgroup of an image may run past its blocks
         const uint32_t pos = 32u * b + lrow;
 #pragma unroll
         for (int i = 0; i < T; ++i) {
@@ -221,10 +222,9 @@ __global__ __launch_bounds__(kWinThreads) void win_fwd_kernel(WinFwd p) {
     epilogue(bw0 + kWinWaves * (BPW - 1), acc[(BPW - 1) & 1]);
 }
 
-// Padded input rows per channel that the most demanding workgroup of
-// `bpw`-block waves reads.
-int32_t win_rows(uint32_t L, uint32_t ow, int32_t strh, int32_t kh, int32_t dilh, int32_t hp, uint32_t bpw) {
-    const uint32_t span = 32u * kWinWaves * bpw;
+// Padded input rows per channel that the most demanding workgroup reads when
+// each workgroup takes `span` consecutive positions of an image.
+int32_t win_rows(uint32_t L, uint32_t ow, int32_t strh, int32_t kh, int32_t dilh, int32_t hp, uint32_t span) {
     int32_t rows = 1;
     for (uint32_t first = 0; first < L; first += span) {
         const uint32_t last = std::min(L, first + span) - 1u;
@@ -264,7 +264,7 @@ bool win_fwd_fits(const vkhip_operand& xd, const vkhip_unfold& pr, uint32_t chan
     if (span > (int64_t(1) << 28) || wspan > (int64_t(1) << 28) || static_cast<uint64_t>(cout) * L > (1ull << 28))
         return false;
     const int32_t rows = win_rows(static_cast<uint32_t>(L), ow, pr.stride_h, pr.kernel_h, pr.dilation_h,
-                                  static_cast<int32_t>(hp), kWinBpw);
+                                  static_cast<int32_t>(hp), 32u * kWinWaves * kWinBpw);
     return static_cast<int64_t>(channels) * rows <= 16 * kWinWaves &&
            win_lds_floats(static_cast<int32_t>(channels), rows, static_cast<int32_t>(wp)) <= kWinLdsFloats;
 }
@@ -300,7 +300,7 @@ int win_conv_forward(const float* x, const vkhip_operand& xd, const float* w, co
     p.nblk = (p.L + 31u) / 32u;
     p.div_ow = FastDiv(ow);
     constexpr uint32_t bpw = kWinBpw;
-    p.rows = win_rows(p.L, ow, p.strh, pr.kernel_h, pr.dilation_h, hp, bpw);
+    p.rows = win_rows(p.L, ow, p.strh, pr.kernel_h, pr.dilation_h, hp, 32u * kWinWaves * bpw);
     p.plane = p.rows * p.Wp;
     p.stage = p.C * p.plane;
     p.sc4 = static_cast<int32_t>(xd.nb[1] * 4);
@@ -345,6 +345,392 @@ int win_conv_forward(const float* x, const vkhip_operand& xd, const float* w, co
 #undef VKHIP_WINF_R
 #undef VKHIP_WINF_F
 #undef VKHIP_WINF
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
+
+
+// ---- weight gradient summed over the batch ------------------------------------
+// dW[co][j] = sum over images n and positions p of g[n][co][p] * window element
+// j of image n at p (reference: the per-image products matmul(grad, cols^T)
+// and the broadcast adjoint's batch sum, autograd.cpp:548-553 and :84-116).
+// At CIFAR conv1 the product is [64 x 27] with K = 128 x 1024 positions: it is
+// bound by reading the 33.5 MB gradient once.
+//
+// win_wgrad_kernel: a workgroup of four waves takes CH chunks of 64 positions
+// of one image (512 positions at CIFAR conv1: 256 workgroups). It stages the
+// input rows those positions read once (as the forward does, with the zero
+// region for window elements past K), and streams the gradient through a ring
+// of registers D chunks ahead: each chunk is loaded with 16-byte loads of
+// whole 256-byte channel rows (16 consecutive lanes on consecutive
+// addresses), and written to one of two LDS buffers in a swizzled layout (the
+// 16-byte group p of channel co sits at co*16 + (p ^ (co % 16))), from which a
+// lane of the product reads its channel's four consecutive positions without
+// bank conflicts. Chunk c + 1 is written and read into registers while chunk
+// c's MFMAs run. The product is channels x window elements with the positions
+// as K: lanes 0-31 and 32-63 take positions p and p + 4 of each 8-position
+// group, four steps per 16-byte read; even and odd steps accumulate
+// separately (two chains per tile) and are added at the end. The four waves'
+// sums are added in wave order through LDS, and the workgroup's [64 x 32]
+// partial goes to the workspace.
+//
+// Measured at CIFAR conv1: 16.4 us with the fold (against 21.3 for the
+// per-workgroup streamed kernel it replaces and 30.5 for the per-image
+// products and batch sum). The loads alone, in this pattern at one workgroup
+// per CU, take 7.7 us; the 33.5 MB read linearly by many workgroups 5.9 us.
+//
+// The 256 workgroup partials are folded by win_fold_kernel in a second
+// launch: each output's partials in workgroup order, as 16 runs added in
+// parallel and then in run order. (Folding inside the same launch -- the last
+// workgroup of each group of 16 adding the group's partials, the last group
+// adding the group sums, ordered by device-scope atomic counts -- measured 29
+// us: its tail is six dependent round trips to the level all XCDs share;
+// device-scope fences, which write back the L2, made it 109 us.) Fixed orders
+// throughout: the result is the same bits on every run, within the GEMM
+// tolerance of the per-image graph.
+namespace {
+
+constexpr uint32_t kWgMaxParts = 512;  // workgroup partials at most (the fold's 16 runs of 32)
+
+struct WinWgrad {
+    const float* x;
+    int64_t sn;                // image stride (elements)
+    int32_t sc4, sh4, sw4;     // channel, row and column strides of the image (bytes)
+    const float* g;
+    int64_t gsn;               // gradient image stride (elements)
+    int32_t gsc;               // gradient channel stride (elements; rows 16-byte aligned)
+    float* part;               // [nwg][2048] workgroup partials (output co * 32 + j)
+    float* out;                // [Cout][K]
+    int32_t C, H, W, padh, padw, strh, strw, OW, Wp, rows, plane, stage;
+    uint32_t cout, K, L, wg_per_image, nwg;
+    FastDiv div_ow;
+    int32_t q_step, r_step;            // waves = q_step * rows + r_step
+    int32_t wave_c[8], wave_r[8];      // staged row w: channel and padded row
+    int32_t offs[32];
+};
+
+template <int T, int NW, int CH, int D>
+__global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    constexpr int NT = 64 * NW;        // threads
+    constexpr int PC = 16 * NW;        // positions per chunk: 16 per wave
+    constexpr int G = PC / 4;          // 16-byte position groups per channel row of a chunk
+    constexpr int CF = 64 * PC;        // floats per chunk buffer
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, kh = lane >> 5;
+    const uint32_t n = blockIdx.y;
+    const uint32_t pos0 = blockIdx.x * static_cast<uint32_t>(PC * CH);  // first position of the workgroup
+    float* img = smem;                                          // [C][rows][Wp], then `plane` zeros
+    float* gbuf = smem + ((p.stage + p.plane + 3) & ~3);        // 2 x [64 x PC] swizzled
+    int32_t* offs_l = reinterpret_cast<int32_t*>(gbuf + 2 * CF);
+    const int32_t row_a = static_cast<int32_t>(p.div_ow.div(pos0)) * p.strh;
+
+    // Gradient chunk c: 64 * G 16-byte slots, thread tid loads slots tid + NT u:
+    // channel s / G, position group s % G, stored at group (s % G) ^ (channel
+    // % 16) of the channel's row. Channels past Cout load zeros.
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.g + static_cast<int64_t>(n) * p.gsn), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    uint32_t goff[4];
+    int32_t gdst[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t sl = static_cast<uint32_t>(tid) + NT * u, co = sl / G, grp = sl % G;
+        goff[u] = co < p.cout ? (co * static_cast<uint32_t>(p.gsc) + pos0 + 4u * grp) * 4u : 0x80000000u;
+        gdst[u] = static_cast<int32_t>(co * G + (grp ^ (co & 15u))) * 4;
+    }
+    v4f ring[D][4];
+    auto load_chunk = [&](int c, v4f (&r)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            r[u] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                               gr, static_cast<int32_t>(goff[u]), c * PC * 4, 0));
+    };
+    auto store_chunk = [&](int buf, const v4f (&r)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) *reinterpret_cast<v4f*>(gbuf + buf * CF + gdst[u]) = r[u];
+    };
+    // The input rows of the workgroup's positions, staged as the forward does.
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.x + static_cast<int64_t>(n) * p.sn), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    const int32_t my_off = p.offs[lane & 31];
+    const int32_t nrows = p.C * p.rows;
+    const int w_in = lane - p.padw;
+    const bool col_in = lane < p.Wp && static_cast<uint32_t>(w_in) < static_cast<uint32_t>(p.W);
+    const uint32_t xvoff = col_in ? static_cast<uint32_t>(w_in) * static_cast<uint32_t>(p.sw4) : 0x80000000u;
+    constexpr int U = 64 / NW;
+    float sv[U];
+    {
+        int32_t c = p.wave_c[wave], rr = p.wave_r[wave];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            sv[u] = 0.0f;
+            if (wave + NW * u >= nrows) break;
+            const int32_t h = row_a + rr - p.padh;
+            if (static_cast<uint32_t>(h) < static_cast<uint32_t>(p.H))
+                sv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                      xr, static_cast<int32_t>(xvoff), c * p.sc4 + h * p.sh4, 0));
+            rr += p.r_step;
+            c += p.q_step;
+            if (rr >= p.rows) {
+                rr -= p.rows;
+                ++c;
+            }
+        }
+    }
+    // the first D chunks' loads go out behind the image's
+#pragma unroll
+    for (int c = 0; c < D && c < CH; ++c) load_chunk(c, ring[c]);
+    for (int e = tid; e < p.plane; e += NT) img[p.stage + e] = 0.0f;
+    if (tid < 32) offs_l[tid] = my_off;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int32_t row = wave + NW * u;
+        if (row >= nrows) break;
+        if (lane < p.Wp) img[row * p.Wp + lane] = sv[u];
+    }
+    store_chunk(0, ring[0]);
+    __syncthreads();
+    const int32_t off = offs_l[lrow];  // this lane's window element (B column lrow)
+
+    // A chunk's operands of this wave: its 16 positions are the 4-position
+    // groups 8gg + 4kh (gg = 0, 1); a[gg][i] = 4 positions of channel 32i +
+    // lrow, b[gg][q] = window element lrow at the lane's position q.
+    struct Ops {
+        v4f a[2][T];
+        float b[2][4];
+    };
+    auto read_ops = [&](int c, Ops& o) {
+        const float* gb = gbuf + (c & 1) * CF;
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+            const uint32_t grp = 4u * wave + 2u * gg + kh;
+#pragma unroll
+            for (int i = 0; i < T; ++i) {
+                const uint32_t co = 32u * i + lrow;
+                o.a[gg][i] = *reinterpret_cast<const v4f*>(gb + (co * G + (grp ^ (co & 15u))) * 4u);
+            }
+            const uint32_t pp = pos0 + PC * c + 4u * grp;  // this lane's first position
+            const uint32_t oh = p.div_ow.div(pp), ow = pp - oh * static_cast<uint32_t>(p.OW);
+            const int32_t base = (static_cast<int32_t>(oh) * p.strh - row_a) * p.Wp +
+                                 static_cast<int32_t>(ow) * p.strw + off;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o.b[gg][q] = img[base + q * p.strw];
+        }
+    };
+    v16f acc[2][T];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[e][i][r] = 0.0f;
+    auto mfma_ops = [&](const Ops& o) {
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < T; ++i)
+                    acc[q & 1][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[gg][i][q], o.b[gg][q], acc[q & 1][i], 0, 0, 0);
+    };
+
+    // Chunk c + 1 is written to LDS and read into registers while chunk c's
+    // MFMAs run. Buffer (c + 1) & 1 last held chunk c - 1, whose reads ended
+    // before the previous barrier.
+    Ops ops[2];
+    read_ops(0, ops[0]);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        if (c + D < CH) load_chunk(c + D, ring[c % D]);  // its slot's data is in LDS already
+        if (c + 1 < CH) {
+            store_chunk((c + 1) & 1, ring[(c + 1) % D]);
+            __syncthreads();
+            read_ops(c + 1, ops[(c + 1) & 1]);
+        }
+        mfma_ops(ops[c & 1]);
+    }
+    __syncthreads();  // every wave is done with the chunk buffers
+
+    // The waves' sums in wave order, through the (now idle) gradient buffers.
+    float* red = gbuf;  // [NW][T][16][64] <= 2 chunk buffers
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[((wave * T + i) * 16 + r) * 64 + lane] = acc[0][i][r] + acc[1][i][r];
+    __syncthreads();
+    const uint32_t wg = n * p.wg_per_image + blockIdx.x;
+    float* mine = p.part + static_cast<uint64_t>(wg) * 2048u;
+    // output o = co * 32 + j of the partial; lane l of register r of tile i
+    // holds co = 32i + 8(r/4) + 4(l/32) + r%4, j = l%32
+#pragma unroll
+    for (int k = 0; k < 2048 / NT; ++k) {
+        const uint32_t o = static_cast<uint32_t>(tid) + NT * k, co = o >> 5, j = o & 31u;
+        if (co >= 32u * T) break;
+        const uint32_t i = co >> 5, rem = co & 31u, r = 4u * (rem >> 3) + (rem & 3u), l = j + 32u * ((rem >> 2) & 1u);
+        float v = red[((0 * T + i) * 16 + r) * 64 + l];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v = v + red[((w * T + i) * 16 + r) * 64 + l];
+        mine[o] = v;
+    }
+}
+
+// dW[co][j] = the sum of the `parts` workgroup partials of output o = co*32 + j
+// ([parts][2048] at part), in partial order: 16 threads per output, each
+// adding a run of at most 16 consecutive partials, then the 16 run sums in run
+// order (at most 32 per run). A workgroup takes 16 outputs.
+__global__ __launch_bounds__(256) void win_fold_kernel(const float* __restrict__ part, uint32_t parts,
+                                                       float* __restrict__ out, uint32_t cout, uint32_t K) {
+    __shared__ float runs[16][17];
+    const int tid = threadIdx.x, oi = tid & 15, run = tid >> 4;
+    const uint32_t o = blockIdx.x * 16u + oi;
+    const uint32_t per = (parts + 15u) / 16u, first = run * per;
+    float x[32];
+#pragma unroll
+    for (int w = 0; w < 32; ++w) {
+        const uint32_t q = first + w;
+        x[w] = part[static_cast<uint64_t>(q < parts && static_cast<uint32_t>(w) < per ? q : 0u) * 2048u + o];
+    }
+    float v = 0.0f;
+    bool any = false;
+#pragma unroll
+    for (int w = 0; w < 32; ++w) {
+        const bool in = static_cast<uint32_t>(w) < per && first + w < parts;
+        const float t = any ? v + x[w] : x[w];
+        v = in ? t : v;
+        any = any || in;
+    }
+    runs[run][oi] = v;
+    __syncthreads();
+    if (tid < 16) {
+        float s = runs[0][tid];
+        for (uint32_t r = 1; r < 16 && r * per < parts; ++r) s = s + runs[r][tid];
+        const uint32_t oo = blockIdx.x * 16u + tid, co = oo >> 5, j = oo & 31u;
+        if (co < cout && j < K) out[co * K + j] = s;
+    }
+}
+
+// Positions per workgroup: the largest of 512, 256, 128, 64 that divides an
+// image's positions and leaves at most kWgMaxParts workgroups; 0 if none does.
+uint32_t win_wgrad_span(uint64_t batch, uint32_t L) {
+    for (uint32_t span = 512; span >= 64; span /= 2)
+        if (L % span == 0 && batch * (L / span) <= kWgMaxParts) return span;
+    return 0;
+}
+
+// Waves per workgroup: four, chunks of 64 positions (measured at CIFAR conv1:
+// 16.4 us with the fold, against 17.3 us for eight waves and chunks of 128).
+constexpr uint32_t kWgWaves = 4;
+
+constexpr int kWgLdsFloats = 24576;  // dynamic LDS of the weight-gradient kernel: 96 KB
+
+// LDS floats: the staged rows and zero region, two chunk buffers, the offsets.
+size_t win_wgrad_lds(int32_t channels, int32_t plane, uint32_t waves) {
+    return ((static_cast<size_t>(channels + 1) * plane + 3) & ~size_t(3)) + 2 * 64 * 16 * waves + 32;
+}
+
+}  // namespace
+
+bool win_wgrad_fits(const float* g, const vkhip_operand& gd, const vkhip_operand& xd, const vkhip_unfold& pr,
+                    uint32_t channels, uint64_t ck, uint32_t cout, uint64_t batch, uint32_t oh, uint32_t ow) {
+    const int64_t hp = static_cast<int64_t>(pr.image_h) + 2 * pr.pad_h;
+    const int64_t wp = static_cast<int64_t>(pr.image_w) + 2 * pr.pad_w;
+    const uint64_t L = static_cast<uint64_t>(oh) * ow;
+    if (!(ck >= 1 && ck <= 32 && cout >= 1 && cout <= 64 && wp <= 64 && hp <= 0x7fffffff && channels >= 1 &&
+          L >= 64 && L % 64 == 0 && ow % 4 == 0 && L <= (1u << 24) && batch >= 1 && batch <= 65535))
+        return false;
+    // 16-byte aligned gradient rows of contiguous positions, 32-bit byte offsets
+    if (reinterpret_cast<uintptr_t>(g) % 16 != 0 || gd.nb[3] != 1 || gd.nb[1] < 0 || gd.nb[2] < 0 ||
+        gd.nb[1] % 4 != 0 || gd.nb[2] % 4 != 0 || (static_cast<int64_t>(cout) - 1) * gd.nb[2] + L > (int64_t(1) << 28))
+        return false;
+    if (xd.nb[1] < 0 || xd.nb[2] < 0 || xd.nb[3] < 0) return false;
+    const int64_t xspan = (static_cast<int64_t>(channels) - 1) * xd.nb[1] +
+                          (static_cast<int64_t>(pr.image_h) - 1) * xd.nb[2] +
+                          (static_cast<int64_t>(pr.image_w) - 1) * xd.nb[3] + 1;
+    if (xspan > (int64_t(1) << 28)) return false;
+    const uint32_t span = win_wgrad_span(batch, static_cast<uint32_t>(L));
+    if (span == 0) return false;
+    const uint32_t waves = kWgWaves;
+    const int32_t r2 = win_rows(static_cast<uint32_t>(L), ow, pr.stride_h, pr.kernel_h, pr.dilation_h,
+                                static_cast<int32_t>(hp), span);
+    const size_t lds = win_wgrad_lds(static_cast<int32_t>(channels), r2 * static_cast<int32_t>(wp), waves);
+    return static_cast<int64_t>(channels) * r2 <= 64 && lds <= kWgLdsFloats;
+}
+
+int win_conv_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* g, const vkhip_operand& gd,
+                             float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
+                             uint32_t ck, uint32_t oh, uint32_t ow) {
+    WinWgrad p{};
+    p.x = x;
+    p.sn = xd.nb[0];
+    p.sc4 = static_cast<int32_t>(xd.nb[1] * 4);
+    p.sh4 = static_cast<int32_t>(xd.nb[2] * 4);
+    p.sw4 = static_cast<int32_t>(xd.nb[3] * 4);
+    p.g = g;
+    p.gsn = gd.nb[1];
+    p.gsc = static_cast<int32_t>(gd.nb[2]);
+    p.out = out;
+    p.C = static_cast<int32_t>(channels);
+    p.H = pr.image_h;
+    p.W = pr.image_w;
+    p.padh = pr.pad_h;
+    p.padw = pr.pad_w;
+    p.strh = pr.stride_h;
+    p.strw = pr.stride_w;
+    p.OW = static_cast<int32_t>(ow);
+    p.Wp = pr.image_w + 2 * pr.pad_w;
+    const int32_t hp = pr.image_h + 2 * pr.pad_h;
+    p.cout = cout;
+    p.K = ck;
+    p.L = oh * ow;
+    p.div_ow = FastDiv(ow);
+    const uint32_t span = win_wgrad_span(batch, p.L);
+    if (span == 0) return fail(VKHIP_ERR_INVALID, "conv2d weight grad sum: no span for %u positions", p.L);
+    const uint32_t waves = kWgWaves, ch = span / (16u * waves);
+    p.rows = win_rows(p.L, ow, p.strh, pr.kernel_h, pr.dilation_h, hp, span);
+    p.plane = p.rows * p.Wp;
+    p.stage = p.C * p.plane;
+    p.q_step = static_cast<int32_t>(waves) / p.rows;
+    p.r_step = static_cast<int32_t>(waves) % p.rows;
+    for (int w = 0; w < 8; ++w) {
+        p.wave_c[w] = w / p.rows;
+        p.wave_r[w] = w % p.rows;
+    }
+    const int32_t kk = pr.kernel_h * pr.kernel_w;
+    for (uint32_t j = 0; j < 32; ++j) {
+        if (j >= ck) {
+            p.offs[j] = p.stage;
+            continue;
+        }
+        const int32_t c = static_cast<int32_t>(j) / kk, r = static_cast<int32_t>(j) % kk;
+        const int32_t ki = r / pr.kernel_w, kj = r % pr.kernel_w;
+        p.offs[j] = c * p.plane + ki * pr.dilation_h * p.Wp + kj * pr.dilation_w;
+    }
+    p.wg_per_image = p.L / span;
+    p.nwg = batch * p.wg_per_image;
+    const size_t lds = win_wgrad_lds(p.C, p.plane, waves);
+    if (p.C * p.rows > 64 || lds > kWgLdsFloats || p.nwg > kWgMaxParts)
+        return fail(VKHIP_ERR_INVALID, "conv2d weight grad sum: the small-window plan does not fit");
+    const int st = workspace(static_cast<size_t>(p.nwg) * 2048u * sizeof(float), &p.part);
+    if (st != VKHIP_OK) return st;
+    const dim3 grid(p.wg_per_image, batch);
+    const size_t bytes = lds * sizeof(float);
+    const bool two = cout > 32;
+#define VKHIP_WGR(T, NW, CH, D) \
+    hipLaunchKernelGGL((win_wgrad_kernel<T, NW, CH, D>), grid, dim3(64 * NW), bytes, ctx().stream, p)
+#define VKHIP_WGR_CH(T)                                          \
+    do {                                                         \
+        static_assert(kWgWaves == 4, "instantiate other wave counts"); \
+        if (ch == 8) VKHIP_WGR(T, 4, 8, 4);                      \
+        else if (ch == 4) VKHIP_WGR(T, 4, 4, 3);                 \
+        else if (ch == 2) VKHIP_WGR(T, 4, 2, 2);                 \
+        else VKHIP_WGR(T, 4, 1, 1);                              \
+    } while (0)
+    if (two) VKHIP_WGR_CH(2); else VKHIP_WGR_CH(1);
+#undef VKHIP_WGR_CH
+#undef VKHIP_WGR
+    VKHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(win_fold_kernel, dim3(two ? 128 : 64), dim3(256), 0, ctx().stream, p.part, p.nwg, out, cout, ck);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }

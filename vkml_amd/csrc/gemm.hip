@@ -3705,6 +3705,16 @@ int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float*
         td.nb[3] = 1;
         return launch_reduce(VKHIP_REDUCE_SUM, tmp, td, 0x2u, out);
     }
+    {
+        const uint32_t ohw = static_cast<uint32_t>(L / static_cast<uint64_t>(im.ow));
+        if (win_wgrad_fits(gr, gd, xd, p, xd.ne[1], ck, cout, batch, ohw, static_cast<uint32_t>(im.ow))) {
+            publish("matmul.kernel", "conv2d_weight_grad_sum", "win_wgrad", "conv_wgrad_small_window_folded",
+                    "C*kh*kw <= 32: the gradient streamed once, partials folded in the same launch",
+                    static_cast<int64_t>(L), static_cast<int64_t>(ck));
+            return win_conv_weight_grad_sum(x, xd, gr, gd, out, p, static_cast<uint32_t>(batch), xd.ne[1], cout,
+                                            static_cast<uint32_t>(ck), ohw, static_cast<uint32_t>(im.ow));
+        }
+    }
     uint64_t stream_parts = 0;
     const uint32_t stream_bpw = wgrad_stream_fits(gr, gd, p, xd.ne[1], ck, cout, L)
                                     ? wgrad_stream_bpw(batch, static_cast<uint32_t>(L / 32), stream_parts)
