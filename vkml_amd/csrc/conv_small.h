@@ -25,10 +25,21 @@ int win_conv_forward(const float* x, const vkhip_operand& xd, const float* w, co
 bool win_wgrad_fits(const float* g, const vkhip_operand& gd, const vkhip_operand& xd, const vkhip_unfold& pr,
                     uint32_t channels, uint64_t ck, uint32_t cout, uint64_t batch, uint32_t oh, uint32_t ow);
 
-// dW[co][j] = sum over n, p of g[n][co][p] * window_j(x[n], p), one launch
-// (the partials folded inside it, in a fixed order).
+// dW[co][j] = sum over n, p of g[n][co][p] * window_j(x[n], p): workgroup
+// partials, then their fold in a fixed order (two launches).
 int win_conv_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* g, const vkhip_operand& gd,
                              float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
                              uint32_t ck, uint32_t oh, uint32_t ow);
+
+// Whether win_conv_input_grad takes this input gradient (unit strides, C*kh*kw
+// <= 32, Cout <= 128).
+bool win_dx_fits(const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout, uint32_t oh, uint32_t ow);
+
+// dX = col2im(flat_weight^T @ grad) in one launch, the reference lowering's
+// bits; grad [N][Cout][oh][ow] with contiguous positions, the flat weight
+// [Cout][C*kh*kw] with row stride w_row.
+int win_conv_input_grad(const float* g, const vkhip_operand& gd, const float* w, int64_t w_row, float* out,
+                        const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout, uint32_t oh,
+                        uint32_t ow);
 
 }  // namespace vkhip

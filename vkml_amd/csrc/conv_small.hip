@@ -735,4 +735,205 @@ int win_conv_weight_grad_sum(const float* x, const vkhip_operand& xd, const floa
     return VKHIP_OK;
 }
 
+
+// ---- input gradient of a thin layer ----------------------------------------------
+// dX = col2im(flat_weight^T @ grad) (reference: conv2d's backward through the
+// im2col node, autograd.cpp:548-553 and ops.cpp:514-541). With C*kh*kw <= 32
+// the column matrix has at most 32 rows (27 at CIFAR conv1, 14 MB), and a
+// convolution of the gradient with the flipped weight would have C = 3 output
+// rows on a 32-row MFMA tile. win_dx_kernel instead computes the columns
+// Z = W^T g for the rows of positions a band of dX rows reads (one MFMA tile
+// of rows: the window elements; positions in blocks of 32; K = Cout in K-tiles
+// of 32 with step t pairing k and 16 + t, the GEMM kernels' chain: Z is the TN
+// product's bits) into LDS, and folds them there in col2im's order (for ki,
+// for kj, ascending, from 0): dX is the reference lowering's bits, with no 14
+// MB column matrix written and read back. The band's halo rows of Z are
+// computed by both bands that read them.
+namespace {
+
+struct WinDx {
+    const float* g;
+    int64_t gsn;                // gradient image stride (elements)
+    int32_t gsc4;               // gradient channel stride (bytes)
+    const float* w;             // flat weight [Cout][K], row stride wrow
+    int32_t wrow4;              // (bytes)
+    float* out;                 // dX [N][C][H][W] contiguous
+    int32_t C, H, W, OH, OW, kh, kw, padh, padw, dilh, dilw;
+    uint32_t cout, K, R, zpitch;  // dX rows per workgroup, Z row pitch in LDS (floats)
+    FastDiv div_w, div_rw;      // by W, by R * W
+};
+
+template <int KT, int NW>
+__global__ __launch_bounds__(64 * NW) void win_dx_kernel(WinDx p) {
+    extern __shared__ __attribute__((aligned(16))) float zl[];  // [32 window elements][zpitch]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, kh = lane >> 5;
+    const uint32_t n = blockIdx.y;
+    const int32_t h0 = static_cast<int32_t>(blockIdx.x * p.R);
+    const int32_t h1 = min(h0 + static_cast<int32_t>(p.R), p.H);
+    // the gradient rows the band's windows reach
+    const int32_t zr0 = max(h0 + p.padh - (p.kh - 1) * p.dilh, 0);
+    const int32_t zr1 = min(h1 - 1 + p.padh, p.OH - 1);
+    const uint32_t zp0 = static_cast<uint32_t>(zr0) * p.OW;
+    const uint32_t npos = zr1 >= zr0 ? static_cast<uint32_t>(zr1 - zr0 + 1) * p.OW : 0u;
+    const uint32_t nzb = (npos + 31u) / 32u;
+    const uint32_t L = static_cast<uint32_t>(p.OH * p.OW);
+
+    // A = W^T: lane (window element lrow, kh) holds W[32kt + t + 16kh][lrow];
+    // zero past Cout or K (the GEMM's padding)
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.w), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    float a[KT][16];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const uint32_t co = 32u * kt + t + 16u * kh;
+            const uint32_t off = co < p.cout && static_cast<uint32_t>(lrow) < p.K
+                                     ? co * static_cast<uint32_t>(p.wrow4) + 4u * lrow
+                                     : 0x80000000u;
+            a[kt][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, static_cast<int32_t>(off), 0, 0));
+        }
+    // B = g: lane (position lrow of the block, kh) holds g[32kt + t + 16kh][p]
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.g + static_cast<int64_t>(n) * p.gsn), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    auto load_b = [&](uint32_t zb, float (&b)[KT][16]) {
+        const uint32_t pos = zp0 + 32u * zb + lrow;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const uint32_t co = 32u * kt + t + 16u * kh;
+                const uint32_t off = co < p.cout && pos < L ? co * static_cast<uint32_t>(p.gsc4) + 4u * pos : 0x80000000u;
+                b[kt][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(gr, static_cast<int32_t>(off), 0, 0));
+            }
+    };
+    // Z block zb into LDS: lane (position lrow, kh) holds window element
+    // 8(r/4) + 4kh + r%4 in acc[r]
+    auto z_block = [&](uint32_t zb, const float (&b)[KT][16]) {
+        v16f acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kt][t], b[kt][t], acc, 0, 0, 0);
+        const uint32_t col = 32u * zb + lrow;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) zl[(8 * (r / 4) + 4 * kh + r % 4) * p.zpitch + col] = acc[r];
+    };
+    // blocks wave + NW i: each round loads MB blocks' B, all before the first
+    // of their MFMAs (three blocks while they fit the registers of two waves
+    // per SIMD)
+    constexpr int MB = KT <= 2 ? 3 : 1;
+    for (uint32_t zb0 = static_cast<uint32_t>(wave); zb0 < nzb; zb0 += NW * MB) {
+        float bs[MB][KT][16];
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            if (zb0 + NW * i < nzb) load_b(zb0 + NW * i, bs[i]);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            if (zb0 + NW * i < nzb) z_block(zb0 + NW * i, bs[i]);
+    }
+    __syncthreads();
+
+    // col2im of the band from LDS: dX[c][h][x] = sum over the window elements
+    // that hit it, for ki, for kj, from 0
+    // (o walks C x R x W; the last band of an image may hold fewer than R rows)
+    const uint32_t rows = static_cast<uint32_t>(h1 - h0), total = static_cast<uint32_t>(p.C) * p.R * p.W;
+    for (uint32_t o = static_cast<uint32_t>(tid); o < total; o += 64u * NW) {
+        const uint32_t c = p.div_rw.div(o), rem = o - c * p.R * p.W;
+        const uint32_t hh = p.div_w.div(rem), x = rem - hh * p.W;
+        if (hh >= rows) continue;
+        const int32_t h = h0 + static_cast<int32_t>(hh);
+        float accv = 0.0f;
+        for (int ki = 0; ki < p.kh; ++ki) {
+            const int32_t oh = h + p.padh - ki * p.dilh;
+            if (oh < 0 || oh >= p.OH) continue;
+            const float* zrow = zl + static_cast<uint32_t>((static_cast<int32_t>(c) * p.kh + ki) * p.kw) * p.zpitch +
+                                static_cast<uint32_t>(oh) * p.OW - zp0;
+            for (int kj = 0; kj < p.kw; ++kj) {
+                const int32_t ow = static_cast<int32_t>(x) + p.padw - kj * p.dilw;
+                if (ow < 0 || ow >= p.OW) continue;
+                accv += zrow[kj * p.zpitch + ow];
+            }
+        }
+        p.out[((static_cast<uint64_t>(n) * p.C + c) * p.H + h) * p.W + x] = accv;
+    }
+}
+
+// Z row pitch (floats) for npos positions: whole 32-position blocks, then
+// 8 mod 16 so that the two half-waves' rows (4 apart) sit on different banks.
+uint32_t win_dx_pitch(uint32_t npos) {
+    uint32_t pitch = (npos + 31u) / 32u * 32u;
+    while (pitch % 16u != 8u) ++pitch;
+    return pitch;
+}
+
+// dX rows per workgroup: the largest of 16, 8, 4, 2, 1 whose Z band fits the
+// LDS and that gives at least 256 workgroups (or 1). (At CIFAR conv1, 16 rows:
+// 15.3 us; 8 rows, 512 workgroups, 19.7 us.)
+uint32_t win_dx_rows(uint32_t batch, int32_t H, int32_t OH, int32_t OW, int32_t kh, int32_t dilh) {
+    for (uint32_t R = 16; R >= 1; R /= 2) {
+        const uint32_t zrows = std::min<uint32_t>(R + (kh - 1) * dilh, OH);
+        const uint64_t floats = 32ull * win_dx_pitch(zrows * static_cast<uint32_t>(OW));
+        const uint64_t wgs = static_cast<uint64_t>(batch) * ((static_cast<uint32_t>(H) + R - 1) / R);
+        if (floats <= 24576 && (wgs >= 256 || R == 1)) return R;
+    }
+    return 0;
+}
+
+}  // namespace
+
+bool win_dx_fits(const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout, uint32_t oh, uint32_t ow) {
+    const uint64_t ck = static_cast<uint64_t>(channels) * pr.kernel_h * pr.kernel_w;
+    if (!(pr.stride_h == 1 && pr.stride_w == 1 && ck >= 1 && ck <= 32 && cout >= 1 && cout <= 128 && batch >= 1 &&
+          batch <= 65535 && pr.image_h >= 1 && pr.image_w >= 1 &&
+          static_cast<uint64_t>(oh) * ow * 4ull * cout < (1ull << 31)))
+        return false;
+    return win_dx_rows(batch, pr.image_h, static_cast<int32_t>(oh), static_cast<int32_t>(ow), pr.kernel_h,
+                       pr.dilation_h) != 0;
+}
+
+int win_conv_input_grad(const float* g, const vkhip_operand& gd, const float* w, int64_t w_row, float* out,
+                        const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout, uint32_t oh,
+                        uint32_t ow) {
+    WinDx p{};
+    p.g = g;
+    p.gsn = gd.nb[0];
+    p.gsc4 = static_cast<int32_t>(gd.nb[1] * 4);
+    p.w = w;
+    p.wrow4 = static_cast<int32_t>(w_row * 4);
+    p.out = out;
+    p.C = static_cast<int32_t>(channels);
+    p.H = pr.image_h;
+    p.W = pr.image_w;
+    p.OH = static_cast<int32_t>(oh);
+    p.OW = static_cast<int32_t>(ow);
+    p.kh = pr.kernel_h;
+    p.kw = pr.kernel_w;
+    p.padh = pr.pad_h;
+    p.padw = pr.pad_w;
+    p.dilh = pr.dilation_h;
+    p.dilw = pr.dilation_w;
+    p.cout = cout;
+    p.K = channels * pr.kernel_h * pr.kernel_w;
+    p.R = win_dx_rows(batch, pr.image_h, p.OH, p.OW, pr.kernel_h, pr.dilation_h);
+    if (p.R == 0) return fail(VKHIP_ERR_INVALID, "conv2d input grad: the small-window band does not fit");
+    const uint32_t zrows = std::min<uint32_t>(p.R + (pr.kernel_h - 1) * pr.dilation_h, oh);
+    p.zpitch = win_dx_pitch(zrows * ow);
+    p.div_w = FastDiv(static_cast<uint32_t>(pr.image_w));
+    p.div_rw = FastDiv(p.R * static_cast<uint32_t>(pr.image_w));
+    const dim3 grid((static_cast<uint32_t>(pr.image_h) + p.R - 1) / p.R, batch);
+    const size_t bytes = 32ull * p.zpitch * sizeof(float);
+    const uint32_t kt = (cout + 31u) / 32u;
+    // eight waves (two per SIMD): 15.3 us at CIFAR conv1, against 19.5 us for four
+    if (kt == 1) hipLaunchKernelGGL((win_dx_kernel<1, 8>), grid, dim3(512), bytes, ctx().stream, p);
+    else if (kt == 2) hipLaunchKernelGGL((win_dx_kernel<2, 8>), grid, dim3(512), bytes, ctx().stream, p);
+    else if (kt == 3) hipLaunchKernelGGL((win_dx_kernel<3, 8>), grid, dim3(512), bytes, ctx().stream, p);
+    else hipLaunchKernelGGL((win_dx_kernel<4, 8>), grid, dim3(512), bytes, ctx().stream, p);
+    VKHIP_LAUNCH_CHECK();
+    return VKHIP_OK;
+}
 }  // namespace vkhip

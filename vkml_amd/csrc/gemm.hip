@@ -3884,6 +3884,14 @@ int conv2d_input_grad(const float* gr, const vkhip_operand& gd, const float* w, 
     const bool geometry = p.stride_h == 1 && p.stride_w == 1 && pad2h >= 0 && pad2w >= 0 &&
                           kk <= 63 && static_cast<uint64_t>(cout) * kk <= 0xffffffffull;
     const bool fused = !ctx().exact_math && geometry && channels >= 32;
+    if (!ctx().exact_math && ctx().node_gemm_kernel != VKHIP_GEMM_EXACT && ck <= 32 &&
+        win_dx_fits(p, batch, channels, cout, static_cast<uint32_t>(oh), static_cast<uint32_t>(ow))) {
+        publish("conv.input_grad", "conv2d_input_grad", "columns_in_lds_then_col2im", "tn_product_then_col2im",
+                "C*kh*kw <= 32: the column matrix of a band of rows held in LDS, the lowering's bits",
+                static_cast<int64_t>(ck), 32);
+        return win_conv_input_grad(gr, gd, w, w_row, out, p, batch, channels, cout, static_cast<uint32_t>(oh),
+                                   static_cast<uint32_t>(ow));
+    }
     publish("conv.input_grad", "conv2d_input_grad",
             fused ? "implicit_conv_of_grad_with_flipped_weight" : "tn_product_then_col2im",
             fused ? "tn_product_then_col2im" : "implicit_conv_of_grad_with_flipped_weight",
