@@ -33,7 +33,8 @@ int win_conv_weight_grad_sum(const float* x, const vkhip_operand& xd, const floa
 
 // Whether win_conv_input_grad takes this input gradient (unit strides, C*kh*kw
 // <= 32, Cout <= 128).
-bool win_dx_fits(const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout, uint32_t oh, uint32_t ow);
+bool win_dx_fits(const vkhip_operand& gd, int64_t w_row, const vkhip_unfold& pr, uint32_t batch, uint32_t channels,
+                 uint32_t cout, uint32_t oh, uint32_t ow);
 
 // dX = col2im(flat_weight^T @ grad) in one launch, the reference lowering's
 // bits; grad [N][Cout][oh][ow] with contiguous positions, the flat weight

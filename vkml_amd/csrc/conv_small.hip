@@ -886,12 +886,18 @@ uint32_t win_dx_rows(uint32_t batch, int32_t H, int32_t OH, int32_t OW, int32_t 
 
 }  // namespace
 
-bool win_dx_fits(const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout, uint32_t oh, uint32_t ow) {
+bool win_dx_fits(const vkhip_operand& gd, int64_t w_row, const vkhip_unfold& pr, uint32_t batch, uint32_t channels,
+                 uint32_t cout, uint32_t oh, uint32_t ow) {
     const uint64_t ck = static_cast<uint64_t>(channels) * pr.kernel_h * pr.kernel_w;
     if (!(pr.stride_h == 1 && pr.stride_w == 1 && ck >= 1 && ck <= 32 && cout >= 1 && cout <= 128 && batch >= 1 &&
-          batch <= 65535 && pr.image_h >= 1 && pr.image_w >= 1 &&
-          static_cast<uint64_t>(oh) * ow * 4ull * cout < (1ull << 31)))
+          batch <= 65535 && pr.image_h >= 1 && pr.image_w >= 1))
         return false;
+    // 32-bit byte offsets within an image's gradient: channel stride x Cout + positions
+    const uint64_t L = static_cast<uint64_t>(oh) * ow;
+    if (gd.nb[1] < 0 || (static_cast<uint64_t>(cout) - 1) * static_cast<uint64_t>(gd.nb[1]) + L > (1ull << 29))
+        return false;
+    // and within the weight: row stride x Cout
+    if (w_row < 0 || (static_cast<uint64_t>(cout) - 1) * static_cast<uint64_t>(w_row) + ck > (1ull << 29)) return false;
     return win_dx_rows(batch, pr.image_h, static_cast<int32_t>(oh), static_cast<int32_t>(ow), pr.kernel_h,
                        pr.dilation_h) != 0;
 }

@@ -3885,7 +3885,7 @@ int conv2d_input_grad(const float* gr, const vkhip_operand& gd, const float* w, 
                           kk <= 63 && static_cast<uint64_t>(cout) * kk <= 0xffffffffull;
     const bool fused = !ctx().exact_math && geometry && channels >= 32;
     if (!ctx().exact_math && ctx().node_gemm_kernel != VKHIP_GEMM_EXACT && ck <= 32 &&
-        win_dx_fits(p, batch, channels, cout, static_cast<uint32_t>(oh), static_cast<uint32_t>(ow))) {
+        win_dx_fits(gd, w_row, p, batch, channels, cout, static_cast<uint32_t>(oh), static_cast<uint32_t>(ow))) {
         publish("conv.input_grad", "conv2d_input_grad", "columns_in_lds_then_col2im", "tn_product_then_col2im",
                 "C*kh*kw <= 32: the column matrix of a band of rows held in LDS, the lowering's bits",
                 static_cast<int64_t>(ck), 32);
