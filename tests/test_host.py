@@ -104,16 +104,24 @@ def test_split_k_plan_rules():
     """The split-K plan: equal chunks of K-tiles, workspace <= 64 MiB, OFF
     never splits, a forced request gets the largest power-of-two chunk giving
     at least that many partitions (reference plan_split_k,
-    vulkan_backend.cpp:596-647); AUTO splits exactly when neither 128x128 nor
-    64x64 output tiles give each of the 256 CUs a workgroup, and then takes as
+    vulkan_backend.cpp:596-647); AUTO splits K in two when 64x64 tiles are
+    exactly one round of one workgroup per CU, and otherwise exactly when
+    neither 128x128 nor 64x64 output tiles give each of the 256 CUs a
+    workgroup, and then takes as
     many partitions as fit one round of one workgroup per CU (the rule
     restated for MI355X)."""
-    # the GEMM sweep's square sizes down to 1024^3 and 8192x1024x4096 fill the
+    # the GEMM sweep's square sizes down to 2048^3 and 8192x1024x4096 fill the
     # machine with 128x128 or 64x64 tiles: no split
     assert plan(1, 4096, 4096, 4096) == (1, 128)
     assert plan(1, 8192, 1024, 4096)[0] == 1
     assert plan(1, 2048, 2048, 2048)[0] == 1
-    assert plan(1, 1024, 1024, 1024)[0] == 1
+    # exactly one round of 64x64 tiles with K >= 16 K-tiles: two partitions
+    # (run as the two halves of one workgroup); fewer K-tiles, or batches,
+    # stay unsplit
+    assert plan(1, 1024, 1024, 1024) == (2, 16)
+    assert plan(1, 1024, 1024, 1056) == (2, 17)
+    assert plan(1, 1024, 1024, 480)[0] == 1
+    assert plan(2, 1024, 512, 1024)[0] == 1
     # 512^3: 64 tiles of 64x64 -> four partitions of four K-tiles
     assert plan(1, 512, 512, 512) == (4, 4)
     # the skinny K-dominant BASELINE shapes and the small MLP/conv GEMMs split

@@ -1239,11 +1239,18 @@ __device__ __forceinline__ void load_rows_direct(float* stage, __amdgpu_buffer_r
     }
 }
 
-template <bool ATR>
+//
+// G K-tiles per stage: the loads of the next stage are issued before the
+// current stage's MFMAs and complete at the barrier that ends it, so a stage
+// of G = 4 (64 MFMAs per wave, 128 KB of LDS for the two stages) covers the
+// memory latency that a single K-tile (16 MFMAs) leaves exposed at one
+// workgroup per CU. The tiles of a stage run in K order: the same chain, the
+// same bits for every G.
+template <bool ATR, int G>
 __global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
-    constexpr int BM = 64, BN = 64, BK = 32, QN = BK / 8;
+    constexpr int BM = 64, BN = 64, BK = 32, QN = BK / 8, TILE = BM * BK + BK * BN;
     using LA = TileLoader<BM, BK, KCD>;
-    __shared__ __attribute__((aligned(16))) float lds[2][BM * BK + BK * BN];
+    __shared__ __attribute__((aligned(16))) float lds[2][G * TILE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1282,53 +1289,63 @@ __global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
     rows_offsets<BN>(vob, wv, lane, g.sbk, col0, g.n);
     const uint32_t a_step = static_cast<uint32_t>((ATR ? g.sak : 1) * BK * 4);
     const uint32_t b_step = static_cast<uint32_t>(g.sbk * BK * 4);
-    auto load_tile = [&](uint32_t kt, int dst) {
+    auto load_tile = [&](uint32_t kt, float* dst) {
         if ((kt + 1) * BK > g.k) {
             if constexpr (ATR)
-                load_rows_direct<BM>(lds[dst], arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
+                load_rows_direct<BM>(dst, arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
             else
-                LA::load_direct(lds[dst], arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
-            load_rows_direct<BN>(lds[dst] + BM * BK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+                LA::load_direct(dst, arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+            load_rows_direct<BN>(dst + BM * BK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
             return;
         }
-        issue_direct<BM / 32>(lds[dst], arsrc, voa, wv, kt * a_step);
-        issue_direct<BN / 32>(lds[dst] + BM * BK, brsrc, vob, wv, kt * b_step);
+        issue_direct<BM / 32>(dst, arsrc, voa, wv, kt * a_step);
+        issue_direct<BN / 32>(dst + BM * BK, brsrc, vob, wv, kt * b_step);
     };
-    if (kt0 < kt1) load_tile(kt0, 0);
+    auto load_stage = [&](uint32_t kt, int buf) {
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+            if (kt + j < kt1) load_tile(kt + j, lds[buf] + j * TILE);
+    };
+    if (kt0 < kt1) load_stage(kt0, 0);
     __syncthreads();
 
     const int lrow = lane & 31;
     const int kh = lane >> 5;
-    for (uint32_t kt = kt0; kt < kt1; ++kt) {
-        const int cur = (kt - kt0) & 1;
-        if (kt + 1 < kt1) load_tile(kt + 1, cur ^ 1);
-        const float* As = ATR ? lds[cur] + kh * 16 * BM + wm0 + lrow : lds[cur] + (wm0 + lrow) * BK;
-        const float* Bs = lds[cur] + BM * BK + kh * 16 * BN + 2 * lrow + s0;
-        auto a_at = [&](int q) {
-            if constexpr (ATR) {
-                f32x4 v;
+    for (uint32_t kt = kt0; kt < kt1; kt += G) {
+        const int cur = ((kt - kt0) / G) & 1;
+        if (kt + G < kt1) load_stage(kt + G, cur ^ 1);
 #pragma unroll
-                for (int st = 0; st < 4; ++st) v[st] = As[(4 * q + st) * BM];
-                return v;
-            } else {
-                return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)));
+        for (int j = 0; j < G; ++j) {
+            if (j > 0 && kt + j >= kt1) break;
+            const float* tl = lds[cur] + j * TILE;
+            const float* As = ATR ? tl + kh * 16 * BM + wm0 + lrow : tl + (wm0 + lrow) * BK;
+            const float* Bs = tl + BM * BK + kh * 16 * BN + 2 * lrow + s0;
+            auto a_at = [&](int q) {
+                if constexpr (ATR) {
+                    f32x4 v;
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) v[st] = As[(4 * q + st) * BM];
+                    return v;
+                } else {
+                    return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)));
+                }
+            };
+            f32x4 av[2], bv[2];
+            av[0] = a_at(0);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) bv[0][st] = Bs[st * BN];
+#pragma unroll
+            for (int q = 0; q < QN; ++q) {
+                const int cb = q & 1;
+                if (q + 1 < QN) {
+                    av[cb ^ 1] = a_at(q + 1);
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) bv[cb ^ 1][st] = Bs[(4 * (q + 1) + st) * BN];
+                }
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][st], bv[cb][st], acc, 0, 0, 0);
             }
-        };
-        f32x4 av[2], bv[2];
-        av[0] = a_at(0);
-#pragma unroll
-        for (int st = 0; st < 4; ++st) bv[0][st] = Bs[st * BN];
-#pragma unroll
-        for (int q = 0; q < QN; ++q) {
-            const int cb = q & 1;
-            if (q + 1 < QN) {
-                av[cb ^ 1] = a_at(q + 1);
-#pragma unroll
-                for (int st = 0; st < 4; ++st) bv[cb ^ 1][st] = Bs[(4 * (q + 1) + st) * BN];
-            }
-#pragma unroll
-            for (int st = 0; st < 4; ++st)
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][st], bv[cb][st], acc, 0, 0, 0);
         }
         __syncthreads();
     }
@@ -1589,6 +1606,158 @@ __global__ __launch_bounds__(64 * S) void gemm_wgfold_kernel(GemmArgs g, FoldEpi
 #pragma unroll
         for (int lv = 0; lv < kSplitLevels; ++lv)
             if ((static_cast<uint32_t>(S) >> lv) & 1u) total = total + stack[lv];
+        if (row < g.m && col < g.n) {
+            const uint64_t i = (static_cast<uint64_t>(z) * g.m + row) * g.n + col;
+            cz[static_cast<uint64_t>(row) * g.n + col] = apply_epilogue(epi, i, total);
+        }
+    }
+}
+
+// ---- two K partitions of a 64x64 tile in one workgroup -------------------------
+// One round of 64x64 tiles (one workgroup per CU) gives each SIMD one wave and
+// one MFMA chain (1024^3 unsplit: matrix cores 54% busy). The plan splits K in
+// two there, and this kernel
+// runs both partitions of a tile as the two halves of one workgroup: waves
+// 0-3 partition 0, waves 4-7 partition 1, each half staging its own K-tiles
+// straight into LDS and each wave running gemm_direct64_kernel's quarter and
+// step order, from 0, so every partial is the split kernel's; two chains per
+// SIMD. Partition 1 then hands its partials to partition 0 through LDS, which
+// folds each output as split_k_reduce_kernel folds two slices (carry stack in
+// partition order, drained from 0.0) and applies the same epilogue: the split
+// plan's bits in one launch, with no workspace. G K-tiles per stage per
+// partition (128 KB of LDS at G = 2). Measured 1024^3: 58% of peak, the
+// matrix cores waiting on the stages' loads (41% of wave cycles) rather than
+// on the chains.
+template <bool ATR, int G>
+__global__ __launch_bounds__(512) void gemm_pair64_kernel(GemmArgs g, FoldEpilogue epi) {
+    constexpr int BM = 64, BN = 64, BK = 32, QN = BK / 8, TILE = BM * BK + BK * BN;
+    using LA = TileLoader<BM, BK, KCD>;
+    __shared__ __attribute__((aligned(16))) float lds[2][2][G * TILE];  // [buffer][partition]
+
+    const int tid = threadIdx.x & 255;  // within the partition's half
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int part = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 8));
+    const int wm0 = (wave & 1) * 32;
+    const int s0 = wave >> 1;
+
+    uint32_t tm, tn, split;
+    tile_of(g, tm, tn, split);
+    const uint32_t row0 = tm * BM;
+    const uint32_t col0 = tn * BN;
+
+    const uint32_t z = blockIdx.z;
+    const uint32_t i0 = z / g.b1, i1 = z % g.b1;
+    const float* abase = g.a + i0 * g.sa0 + i1 * g.sa1;
+    const float* bbase = g.b + i0 * g.sb0 + i1 * g.sb1;
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(abase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(bbase), 0, static_cast<int32_t>(0x80000000u), 0x00020000);
+    const uint32_t kt0 = static_cast<uint32_t>(part) * g.chunk;
+    const uint32_t kt1 = min(g.ktiles, kt0 + g.chunk);
+    const uint32_t stages = (g.chunk + G - 1) / G;  // the same count for both halves (barriers)
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t voa[2], vob[2];
+    if constexpr (ATR)
+        rows_offsets<BM>(voa, wv, lane, g.sak, row0, g.m);
+    else
+        kcd_offsets<BM>(voa, wv, lane, g.sam, row0, g.m);
+    rows_offsets<BN>(vob, wv, lane, g.sbk, col0, g.n);
+    const uint32_t a_step = static_cast<uint32_t>((ATR ? g.sak : 1) * BK * 4);
+    const uint32_t b_step = static_cast<uint32_t>(g.sbk * BK * 4);
+    auto load_tile = [&](uint32_t kt, float* dst) {
+        if ((kt + 1) * BK > g.k) {
+            if constexpr (ATR)
+                load_rows_direct<BM>(dst, arsrc, g.sak, row0, g.m, kt * BK, g.k, tid);
+            else
+                LA::load_direct(dst, arsrc, g.sam, row0, g.m, kt * BK, g.k, tid);
+            load_rows_direct<BN>(dst + BM * BK, brsrc, g.sbk, col0, g.n, kt * BK, g.k, tid);
+            return;
+        }
+        issue_direct<BM / 32>(dst, arsrc, voa, wv, kt * a_step);
+        issue_direct<BN / 32>(dst + BM * BK, brsrc, vob, wv, kt * b_step);
+    };
+    auto load_stage = [&](uint32_t kt, int buf) {
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+            if (kt + j < kt1) load_tile(kt + j, lds[buf][part] + j * TILE);
+    };
+    if (kt0 < kt1) load_stage(kt0, 0);
+    __syncthreads();
+
+    const int lrow = lane & 31;
+    const int kh = lane >> 5;
+    for (uint32_t s = 0; s < stages; ++s) {
+        const uint32_t kt = kt0 + s * G;
+        const int cur = s & 1;
+        if (kt + G < kt1) load_stage(kt + G, cur ^ 1);
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            if (kt + j >= kt1) break;
+            const float* tl = lds[cur][part] + j * TILE;
+            const float* As = ATR ? tl + kh * 16 * BM + wm0 + lrow : tl + (wm0 + lrow) * BK;
+            const float* Bs = tl + BM * BK + kh * 16 * BN + 2 * lrow + s0;
+            auto a_at = [&](int q) {
+                if constexpr (ATR) {
+                    f32x4 v;
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) v[st] = As[(4 * q + st) * BM];
+                    return v;
+                } else {
+                    return *reinterpret_cast<const f32x4*>(As + 4 * ((kh * 4 + q) ^ kcd_swizzle(lrow)));
+                }
+            };
+            f32x4 av[2], bv[2];
+            av[0] = a_at(0);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) bv[0][st] = Bs[st * BN];
+#pragma unroll
+            for (int q = 0; q < QN; ++q) {
+                const int cb = q & 1;
+                if (q + 1 < QN) {
+                    av[cb ^ 1] = a_at(q + 1);
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) bv[cb ^ 1][st] = Bs[(4 * (q + 1) + st) * BN];
+                }
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cb][st], bv[cb][st], acc, 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    // The last stage issued no loads and ended at a barrier: the stage
+    // buffers are free for partition 1's partials (4 waves x 16 x 64 floats).
+    float* parts = &lds[0][0][0];
+    if (part == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) parts[(wave * 16 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (part == 1) return;
+    // acc register r of lane l: row 8*(r/4) + 4*(l/32) + r%4 of the wave's 32,
+    // column 2*(l%32) + s0 of the tile.
+    const uint32_t col = col0 + 2 * lrow + s0;
+    float* cz = g.c + static_cast<uint64_t>(z) * g.m * g.n;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        float stack[kSplitLevels];
+#pragma unroll
+        for (int lv = 0; lv < kSplitLevels; ++lv) stack[lv] = 0.0f;
+        carry_push(stack, 0u, acc[r]);
+        carry_push(stack, 1u, parts[(wave * 16 + r) * 64 + lane]);
+        float total = 0.0f;
+#pragma unroll
+        for (int lv = 0; lv < kSplitLevels; ++lv)
+            if ((2u >> lv) & 1u) total = total + stack[lv];
+        const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
         if (row < g.m && col < g.n) {
             const uint64_t i = (static_cast<uint64_t>(z) * g.m + row) * g.n + col;
             cz[static_cast<uint64_t>(row) * g.n + col] = apply_epilogue(epi, i, total);
@@ -2207,6 +2376,16 @@ int gemm_plan(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, int32_t split_
     }
     tile.tiles = tile.bm == 128 ? t128 : t64;
     if (split_request == 1) return VKHIP_OK;  // OFF
+    // Exactly one round of 64x64 tiles (one workgroup per CU) and K of at
+    // least 16 K-tiles: two partitions, which gemm()'s direct path runs as the
+    // two halves of one workgroup (gemm_pair64_kernel: two MFMA chains per
+    // SIMD: 1024^3 23.2-24.0 us, against 24.1-25.6 unsplit; 128x128 or
+    // 128x64 tiles in four partitions plus the fold ran 35.6).
+    if (!want_split && req == 0 && tile.bm == 64 && t64 == cu && batch == 1 && ktiles >= 16) {
+        splits = 2;
+        chunk = (ktiles + 1) / 2;
+        return VKHIP_OK;
+    }
     if (!want_split && req == 0) return VKHIP_OK;
     const uint64_t tiles = tile.bm == 128 ? t128 : t64;
     if (tiles > 0xffffffffull) return VKHIP_OK;
@@ -2576,6 +2755,23 @@ static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, co
         g.tiles_m = ceil_div(m, tile.bm);
         g.tiles_n = ceil_div(n, tile.bn);
     }
+    // Two partitions of a 64x64 tile grid that is one round of one workgroup
+    // per CU: both in one workgroup, folded there (gemm_pair64_kernel).
+    {
+        const uint64_t cus = ctx().ready ? static_cast<uint64_t>(ctx().caps.compute_units) : 256u;
+        const uint64_t t64n = static_cast<uint64_t>(g.tiles_m) * g.tiles_n * batch;
+        if (splits == 2 && tile.bm == 64 && !tile.pair && t64n <= cus && b_rows && (amode == KCD || a_rows)) {
+            g.c = c;
+            g.flat_splits = 0;
+            const dim3 grid(g.tiles_m * g.tiles_n, 1, static_cast<uint32_t>(batch));
+            void (*kern)(GemmArgs, FoldEpilogue) = amode == KCD ? gemm_pair64_kernel<false, 2>
+                                                                : gemm_pair64_kernel<true, 2>;
+            hipLaunchKernelGGL(kern, grid, dim3(512), 0, ctx().stream, g, fe);
+            VKHIP_LAUNCH_CHECK();
+            *fused = true;
+            return VKHIP_OK;
+        }
+    }
     const uint32_t slices = paired ? (splits + 1) / 2 : splits;
     float* target = c;
     if (slices > 1) {
@@ -2664,10 +2860,14 @@ static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, co
     }
     if (tile.bm == 64 && b_rows && (amode == KCD || a_rows)) {
         const dim3 grid = dgrid;
-        if (amode == KCD)
-            hipLaunchKernelGGL(gemm_direct64_kernel<false>, grid, dim3(256), 0, ctx().stream, g);
-        else
-            hipLaunchKernelGGL(gemm_direct64_kernel<true>, grid, dim3(256), 0, ctx().stream, g);
+        // Four K-tiles per stage when the grid is one round of one workgroup
+        // per CU (its 128 KB of LDS allow no second); one K-tile per stage
+        // otherwise, where two workgroups per CU hide each other's waits.
+        const uint64_t cus = ctx().ready ? static_cast<uint64_t>(ctx().caps.compute_units) : 256u;
+        const bool staged = static_cast<uint64_t>(grid.x) * grid.y * grid.z <= cus && chunk >= 8;
+        void (*kern)(GemmArgs) = amode == KCD ? (staged ? gemm_direct64_kernel<false, 4> : gemm_direct64_kernel<false, 1>)
+                                              : (staged ? gemm_direct64_kernel<true, 4> : gemm_direct64_kernel<true, 1>);
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx().stream, g);
         VKHIP_LAUNCH_CHECK();
         if (splits > 1) { *fused = true; return launch_split_k_reduce(target, c, out_elems, splits, fe); }
         return VKHIP_OK;
