@@ -619,7 +619,9 @@ def training_steps(only: int | None = None, modes=TRAIN_MODES):
                     SGD(fused=False)), built and flushed every step: what
                     vkML's executor would hand a drop-in HipBackend::compute
       eager         the host core's rewritten graph, built every step
-      replay        the step recorded once, its calls replayed from C
+      replay        the step recorded once, its calls replayed from C; each
+                    call uploads the next batch on the copy stream while its
+                    step runs (CapturedStep prefetch), and reads its loss back
       graph         the replay captured once into a HIP graph
       graph_queued  "graph" with no per-step loss read-back: the host queues
                     step after step, the last loss is read inside the timed
@@ -702,11 +704,16 @@ def training_steps(only: int | None = None, modes=TRAIN_MODES):
                             captured.outputs_to(DeviceArray(loss_t.shape, np.float32, None, log.buffer,
                                                             offset=i * max(loss_t.numel(), 1)))
                     else:
+                        ahead = not mode.startswith("resident")  # host batches: upload i + 1 during step i
+
                         def step(i):
-                            out = captured(*feed[i], read=not queued)
+                            nxt = feed[i + 1] if ahead and i + 1 < cfg.steps else None
+                            out = captured(*feed[i], read=not queued, prefetch=nxt)
                             return None if out is None else float(out[0])
                 hip.synchronize()
                 t0 = time.perf_counter()
+                if captured is not None and not mode.startswith("resident"):
+                    captured.prefetch(*feed[1])
                 for i in range(1, cfg.steps):
                     losses.append(step(i))
                 if mode == "graph_queued":

@@ -291,6 +291,21 @@ int vkhip_memory_stats(size_t* bytes_in_use, size_t* bytes_cached);
  * caller may reuse host_src at once (backend.h copy_from_host). */
 int vkhip_copy_from_host(void* dst, const void* host_src, size_t nbytes);
 int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes); /* synchronises */
+/* An upload queued ahead of the stream's work. No counterpart in the
+ * reference (its uploads are ordered with its compute queue, backend.h
+ * copy_from_host); for a training loop that uploads batch i + 1 while the
+ * device runs step i: the separate transfer queue its asynchronous-submission
+ * design leaves out (docs/adr/0012-asynchronous-submission.md:223-224), on
+ * a HIP stream and events instead of semaphores. The bytes go through the
+ * pinned staging slots (at most 32 MB) and return to the caller as
+ * vkhip_copy_from_host's do; their DMAs run on a second stream that first
+ * waits for `after` (an event recorded on the backend stream once it no
+ * longer reads dst; null: no wait), and `done` is recorded behind them.
+ * The backend stream must wait for `done` (vkhip_stream_wait_event) before it
+ * reads dst. */
+int vkhip_copy_from_host_async(void* dst, const void* host_src, size_t nbytes, void* after, void* done);
+/* Later work on the backend stream waits (on the device) for `event`. */
+int vkhip_stream_wait_event(void* event);
 /* One unit of work for several disjoint copies (backend.h:83-108). */
 int vkhip_copy_device_to_device(const vkhip_copy* copies, size_t n);
 int vkhip_synchronize(void);

@@ -138,6 +138,52 @@ def test_resident_inputs_and_device_loss_log_are_the_host_steps(config, graph):
     assert runs[0] == runs[1]
 
 
+@pytest.mark.parametrize("graph", [False, True], ids=["replay", "graph"])
+@pytest.mark.parametrize("config", ["mlp", "cnn"])
+def test_prefetched_uploads_are_the_plain_uploads(config, graph):
+    """Each call uploading the next batch on the copy stream (prefetch=) while
+    its own step runs gives the losses and parameters of calls that upload
+    their own batch: read back every step, queued (read=False), and with a
+    prefetch the next call does not use (other array objects: they are
+    uploaded instead). The host arrays are overwritten right after each
+    prefetch: the bytes were copied when the call returned."""
+    dev = T.default_backend()
+    make, _, _, _, lr = CONFIGS[config]
+    batches = _batches(config, 9)
+    runs = []
+    for variant in ("plain", "prefetch", "prefetch_queued"):
+        model = make(dev)
+        opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
+        step = T.CapturedStep(_step_fn(model, opt), *batches[0], graph=graph)
+        losses = [np.float32(step.first[0])]
+        if variant == "plain":
+            losses += [np.float32(step(x, y)[0]) for x, y in batches[1:]]
+        else:
+            queued = variant == "prefetch_queued"
+            feed = [(x.copy(), y.copy()) for x, y in batches]
+            step.prefetch(*feed[1])
+            for i in range(1, len(feed)):
+                x, y = feed[i]
+                if i == 4:  # a fresh copy of the batch: the staged one is not used
+                    x, y = batches[i][0].copy(), batches[i][1].copy()
+                nxt = feed[i + 1] if i + 1 < len(feed) else None
+                out = step(x, y, read=not queued, prefetch=nxt)
+                if nxt is not None:  # scribble over the host bytes just staged
+                    nxt[0][...] = 7.0
+                    nxt[1][...] = 0
+                    feed[i + 1] = nxt
+                if queued:
+                    assert out is None
+                    losses.append(np.float32(step.outputs_now()[0]))
+                else:
+                    losses.append(np.float32(out[0]))
+        runs.append((np.array(losses, np.float32).tobytes(),
+                     [p.numpy().tobytes() for p in model.parameters()]))
+        step.close()
+    assert runs[1] == runs[0]
+    assert runs[2] == runs[0]
+
+
 def test_captured_step_checks_its_inputs():
     dev = T.default_backend()
     model = _mlp(dev)
@@ -155,6 +201,10 @@ def test_captured_step_checks_its_inputs():
         step(DeviceArray.from_numpy(np.ascontiguousarray(x.transpose(0, 1, 3, 2))).transpose(-2, -1), y)
     with pytest.raises(ValueError):  # a loss destination of the wrong size
         step.outputs_to(DeviceArray((2,), np.float32))
+    with pytest.raises(ValueError):  # a prefetch of another shape
+        step.prefetch(x[:32], y[:32])
+    with pytest.raises(ValueError):  # prefetch takes host arrays
+        step.prefetch(DeviceArray.from_numpy(x), y)
     step.close()
     with pytest.raises(RuntimeError):
         step(x, y)

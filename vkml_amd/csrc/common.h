@@ -26,6 +26,9 @@ struct Context {
     int device = -1;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;  // where launches go: own_stream or a host-provided one
+    // Uploads queued ahead of the stream's work (vkhip_copy_from_host_async),
+    // created on first use, default priority.
+    hipStream_t copy_stream = nullptr;
     vkhip_caps caps{};
     // Split-K partials workspace, grown on demand and released stream-ordered
     // (reference grows its own the same way, vulkan_backend.cpp:899-919).

@@ -842,6 +842,11 @@ extern "C" int vkhip_shutdown(void) {
         if (rc != VKHIP_OK) return rc;
     }
     VKHIP_HIP(hipStreamSynchronize(c.stream));
+    if (c.copy_stream) {
+        VKHIP_HIP(hipStreamSynchronize(c.copy_stream));
+        VKHIP_HIP(hipStreamDestroy(c.copy_stream));
+        c.copy_stream = nullptr;
+    }
     {
         const int rc = vkhip::release_stage_slots();
         if (rc != VKHIP_OK) return rc;
@@ -1010,6 +1015,47 @@ extern "C" int vkhip_copy_from_host(void* dst, const void* host_src, size_t nbyt
         VKHIP_HIP(hipEventRecord(slot->done, ctx().stream));
         slot->pending = true;
     }
+    return VKHIP_OK;
+}
+
+// Uploads ahead of the stream: the same pinned slots, the DMAs on a second
+// stream that waits only for `after` (the event the stream recorded once it no
+// longer reads dst), so a training loop copies batch i + 1 on the host and over
+// PCIe while the device runs step i; `done` is recorded behind the DMAs for the
+// stream to wait on (vkhip_stream_wait_event) before it reads dst.
+extern "C" int vkhip_copy_from_host_async(void* dst, const void* host_src, size_t nbytes, void* after,
+                                          void* done) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!done) return fail(VKHIP_ERR_INVALID, "copy_from_host_async: null completion event");
+    if (nbytes && (!dst || !host_src)) return fail(VKHIP_ERR_INVALID, "copy_from_host_async: null pointer");
+    if (nbytes > vkhip::kStagedMax)
+        return fail(VKHIP_ERR_UNSUPPORTED, "copy_from_host_async: %zu bytes exceed the %zu bytes of staging slots",
+                    nbytes, vkhip::kStagedMax);
+    vkhip::Context& c = ctx();
+    if (!c.copy_stream) VKHIP_HIP(hipStreamCreateWithFlags(&c.copy_stream, hipStreamNonBlocking));
+    if (after) VKHIP_HIP(hipStreamWaitEvent(c.copy_stream, static_cast<hipEvent_t>(after), 0));
+    std::lock_guard<std::mutex> lk(vkhip::g_stage_mu);
+    for (size_t off = 0; off < nbytes; off += vkhip::kStageSlotBytes) {
+        const size_t chunk = std::min(vkhip::kStageSlotBytes, nbytes - off);
+        vkhip::StageSlot* slot = nullptr;
+        st = vkhip::next_stage_slot(&slot);
+        if (st != VKHIP_OK) return st;
+        memcpy(slot->host, static_cast<const char*>(host_src) + off, chunk);
+        VKHIP_HIP(hipMemcpyAsync(static_cast<char*>(dst) + off, slot->host, chunk, hipMemcpyHostToDevice,
+                                 c.copy_stream));
+        VKHIP_HIP(hipEventRecord(slot->done, c.copy_stream));
+        slot->pending = true;
+    }
+    VKHIP_HIP(hipEventRecord(static_cast<hipEvent_t>(done), c.copy_stream));
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_stream_wait_event(void* event) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!event) return fail(VKHIP_ERR_INVALID, "stream_wait_event: null event");
+    VKHIP_HIP(hipStreamWaitEvent(ctx().stream, static_cast<hipEvent_t>(event), 0));
     return VKHIP_OK;
 }
 

@@ -1109,7 +1109,7 @@ class CapturedStep:
     # launches the next step.
     queue_depth = 2
 
-    def __call__(self, *arrays, read: bool = True):
+    def __call__(self, *arrays, read: bool = True, prefetch=None):
         """Copies `arrays` into the recorded inputs, replays the step and
         returns `fn`'s outputs as host arrays. An input is a host array
         (uploaded through the pinned staging slots) or a contiguous
@@ -1119,7 +1119,16 @@ class CapturedStep:
         next call's copies are stream-ordered after this replay, so steps
         queue back to back, at most `queue_depth` of them in flight (the call
         first waits for the oldest); `outputs_now()` reads the latest step's
-        outputs and `outputs_to()` copies them on the device."""
+        outputs and `outputs_to()` copies them on the device.
+
+        prefetch: the next call's host arrays. They are uploaded, once this
+        step is queued, into device staging buffers on the backend's copy
+        stream (vkhip_copy_from_host_async), so the host copy and the DMA of
+        batch i + 1 overlap step i on the device (and this call's read-back);
+        the next call given those same array objects copies them from the
+        staging buffers on the device instead of uploading them. The arrays
+        must not change in between (the host bytes are copied at once, so a
+        change would be ignored, not raced)."""
         if self._program is None:
             raise RuntimeError("CapturedStep: closed")
         if not read:
@@ -1134,7 +1143,20 @@ class CapturedStep:
             raise ValueError(f"CapturedStep: {len(arrays)} inputs, recorded with {len(self.inputs)}")
         from .device import DeviceArray
 
+        staged = getattr(self, "_staged", None)
+        self._staged = None
+        if staged is not None and (len(staged[0]) != len(arrays) or
+                                   any(a is not b for a, b in zip(arrays, staged[0]))):
+            staged = None  # prefetched arrays not the ones given: upload these
         device_copies = []
+        if staged is not None:
+            k = staged[1]
+            _lib.check(self.lib.vkhip_stream_wait_event(ctypes.c_void_p(self._stage_ready[k].handle)),
+                       "stream_wait_event")
+            for t, buf in zip(self.inputs, self._stage_bufs[k]):
+                dst = t.node.storage.ptr + t.node.offset * t.node.itemsize
+                device_copies.append(_lib.Copy(dst, buf.ptr, buf.nbytes_dense()))
+            arrays = ()
         for t, a in zip(self.inputs, arrays):
             if isinstance(a, DeviceArray):
                 if a.shape != t.shape or a.dtype != t.dtype or not a.is_contiguous():
@@ -1151,13 +1173,49 @@ class CapturedStep:
         if device_copies:
             _lib.check(self.lib.vkhip_copy_device_to_device(
                 (_lib.Copy * len(device_copies))(*device_copies), len(device_copies)), "copy_device_to_device")
+        if staged is not None:
+            self._stage_free[staged[1]].record()  # the staging buffers may be refilled after this
         _lib.check(self.lib.vkhip_program_run(self._program, 1 if self.graph else 0), "program_run")
+        if prefetch is not None:
+            self.prefetch(*prefetch)
         if read:
             self._queued = 0
             return self.outputs_now()
         self._events[self._queued % self.queue_depth].record()
         self._queued += 1
         return None
+
+    def prefetch(self, *arrays) -> None:
+        """Uploads host `arrays` (the next call's inputs) into the staging
+        buffer set that the latest call did not use, on the copy stream, ahead
+        of the work queued so far: the copy stream waits for that set's last
+        device copy out (its `free` event), then `ready` is recorded behind the
+        DMAs. The next call given these same array objects reads them from
+        there (see __call__)."""
+        from .device import DeviceArray, Event
+
+        if self._program is None:
+            raise RuntimeError("CapturedStep: closed")
+        if len(arrays) != len(self.inputs) or any(isinstance(a, DeviceArray) for a in arrays):
+            raise ValueError("CapturedStep: prefetch takes one host array per recorded input")
+        if not hasattr(self, "_stage_bufs"):
+            self._stage_bufs = [[DeviceArray(t.shape, np.uint8 if t.dtype == np.bool_ else t.dtype)
+                                 for t in self.inputs] for _ in range(2)]
+            self._stage_ready = [Event(), Event()]
+            self._stage_free = [Event().record(), Event().record()]
+            self._stage_next = 0
+        k = self._stage_next
+        self._stage_next ^= 1
+        for t, a, buf in zip(self.inputs, arrays, self._stage_bufs[k]):
+            a = np.ascontiguousarray(a)
+            if a.shape != t.shape or a.dtype != t.dtype:
+                raise ValueError(f"CapturedStep: prefetch {a.shape} {a.dtype}, recorded {t.shape} {t.dtype}")
+            host = a.view(np.uint8) if a.dtype == np.bool_ else a
+            _lib.check(self.lib.vkhip_copy_from_host_async(
+                ctypes.c_void_p(buf.ptr), host.ctypes.data_as(ctypes.c_void_p), host.nbytes,
+                ctypes.c_void_p(self._stage_free[k].handle), ctypes.c_void_p(self._stage_ready[k].handle)),
+                "copy_from_host_async")
+        self._staged = (arrays, k)
 
     def outputs_now(self) -> list:
         """`fn`'s outputs of the latest replay, as host arrays (waits for it)."""
