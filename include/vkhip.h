@@ -193,7 +193,20 @@ enum vkhip_op {
      * output) -> out = x <= 0 ? +0 : src0 @ src1 (a NaN x passes the product):
      * the two nodes' values, the select applied where the split-K partials
      * are folded (or in a pass after an unsplit product). */
-    VKHIP_OP_MATMUL_RELU_BACKWARD = 107
+    VKHIP_OP_MATMUL_RELU_BACKWARD = 107,
+    /* The weight and bias gradients of a conv layer y = relu(conv2d(x, w) +
+     * bias) whose output feeds a 2x2, stride-2 max-pool, from the pool's
+     * output gradient: src0 x [N,C,H,W], src1 y [N,Cout,oh,ow] (contiguous),
+     * src2 gp [N,Cout,oh/2,ow/2] (contiguous), params the conv's
+     * vkhip_unfold -> out [Cout*C*kh*kw + Cout] contiguous: the weight
+     * gradient [Cout, C*kh*kw] then the bias gradient [Cout], the values of
+     * MAX_POOL2D_BACKWARD_RELU(gp, y) = dz, CONV2D_WEIGHT_GRAD_SUM(x, dz) and
+     * SUM(dz, axes 0, 2, 3) that it replaces (the backward of conv2d's bias
+     * add, the relu and the pool, autograd.cpp:84-116 and :397-408, and the
+     * pool's adjoint). FAST numerics where the small-window kernel takes the
+     * layer form dz in the kernel without writing it: the replaced nodes'
+     * fast-path bits; otherwise those nodes in turn. */
+    VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD = 108
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */

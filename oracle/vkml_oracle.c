@@ -553,6 +553,28 @@ void or_cross_entropy(const float* x, int64_t row_stride, const int64_t* labels,
  * src/backend/cpu/cpu_backend.cpp, which looks each op up in its kernel table,
  * kernels.h:15-24). Host pointers. Returns a vkhip_status. */
 /* ------------------------------------------------------------------------ */
+/* The conv2d weight gradient summed over the batch: the per-image products
+ * g[n] [Cout, L] @ im2col(x[n])^T [L, ck], then the broadcast adjoint's batch
+ * sum (autograd.cpp:548-553 and :84-116): the graph's value, per element the
+ * pairwise sum over the N images. g: [N, Cout, L] with image stride gsn and
+ * channel stride gsc (positions contiguous). */
+static int weight_grad_sum(const float* x, const vkhip_operand* xd, const float* g, int64_t N, int64_t cout,
+                           int64_t L, int64_t gsn, int64_t gsc, int64_t ck, const vkhip_unfold* p, float* out,
+                           int threads) {
+    float* cols = (float*)malloc(sizeof(float) * (size_t)(N * ck * L + 1));
+    float* per = (float*)malloc(sizeof(float) * (size_t)(N * cout * ck + 1));
+    if (!cols || !per) { free(cols); free(per); return VKHIP_ERR_OOM; }
+    or_im2col(x, xd, cols, p, threads);
+    vkhip_operand gd = {{1, (uint32_t)N, (uint32_t)cout, (uint32_t)L}, {0, gsn, gsc, 1}};
+    vkhip_operand cd = {{1, (uint32_t)N, (uint32_t)L, (uint32_t)ck}, {0, ck * L, 1, L}};
+    or_matmul(g, &gd, cols, &cd, per, threads);
+    vkhip_operand pd = {{1, (uint32_t)N, (uint32_t)cout, (uint32_t)ck}, {0, cout * ck, ck, 1}};
+    or_reduce(VKHIP_REDUCE_SUM, per, &pd, 0x2u, out, threads);
+    free(cols);
+    free(per);
+    return VKHIP_OK;
+}
+
 int or_compute(const vkhip_node* nodes, size_t count, int threads) {
     for (size_t ni = 0; ni < count; ++ni) {
         const vkhip_node* nd = &nodes[ni];
@@ -768,29 +790,45 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 break;
             }
             case VKHIP_OP_CONV2D_WEIGHT_GRAD_SUM: {
-                /* The same per-image products, then the broadcast adjoint's
-                 * batch sum (autograd.cpp:84-116): the graph's value, per
-                 * element the pairwise sum over the N images. */
                 vkhip_unfold p;
                 memcpy(&p, nd->params, sizeof p);
                 const vkhip_tensor* g = &nd->src[1];
-                const int64_t N = g->ne[0], cout = g->ne[1];
-                const int64_t L = g->ne[2] * g->ne[3];
-                const int64_t ck = o->ne[1];
-                float* cols = (float*)malloc(sizeof(float) * (size_t)(N * ck * L + 1));
-                float* per = (float*)malloc(sizeof(float) * (size_t)(N * cout * ck + 1));
-                if (!cols || !per) { free(cols); free(per); return VKHIP_ERR_OOM; }
-                or_im2col((const float*)nd->src[0].data, &s0, cols, &p, threads);
-                vkhip_operand gd = {{1, (uint32_t)N, (uint32_t)cout, (uint32_t)L},
-                                    {0, g->nb[0], g->nb[1], 1}};
-                vkhip_operand cd = {{1, (uint32_t)N, (uint32_t)L, (uint32_t)ck},
-                                    {0, ck * L, 1, L}};
-                or_matmul((const float*)g->data, &gd, cols, &cd, per, threads);
-                vkhip_operand pd = {{1, (uint32_t)N, (uint32_t)cout, (uint32_t)ck},
-                                    {0, cout * ck, ck, 1}};
-                or_reduce(VKHIP_REDUCE_SUM, per, &pd, 0x2u, o->data, threads);
-                free(cols);
-                free(per);
+                const int st = weight_grad_sum((const float*)nd->src[0].data, &s0, (const float*)g->data, g->ne[0],
+                                               g->ne[1], g->ne[2] * g->ne[3], g->nb[0], g->nb[1], o->ne[1], &p,
+                                               (float*)o->data, threads);
+                if (st != VKHIP_OK) return st;
+                break;
+            }
+            case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: {
+                /* The nodes it stands for, in turn: dz = the pool's adjoint
+                 * over y (2x2 windows, stride 2) masked by the relu
+                 * (MAX_POOL2D_BACKWARD_RELU), the batch-summed weight
+                 * gradient of dz (CONV2D_WEIGHT_GRAD_SUM) and the bias
+                 * gradient, dz summed over N, oh, ow (the broadcast adjoint,
+                 * autograd.cpp:84-116). */
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                const vkhip_tensor* y = &nd->src[1];
+                const int64_t N = y->ne[0], cout = y->ne[1], L = y->ne[2] * y->ne[3];
+                const int64_t ck = nd->src[0].ne[1] * (int64_t)p.kernel_h * p.kernel_w;
+                float* dz = (float*)malloc(sizeof(float) * (size_t)(N * cout * L + 1));
+                if (!dz) return VKHIP_ERR_OOM;
+                vkhip_unfold pp = {2, 2, 2, 2, 0, 0, 1, 1, (int32_t)y->ne[2], (int32_t)y->ne[3]};
+                or_max_pool2d_backward((const float*)nd->src[2].data, (const float*)y->data, dz, (uint32_t)(N * cout),
+                                       (uint32_t)nd->src[2].ne[2], (uint32_t)nd->src[2].ne[3], &pp, threads);
+                const float* yv = (const float*)y->data;
+                for (int64_t i = 0; i < N * cout * L; ++i)
+                    if (compare_f(VKHIP_OP_LESS_EQUAL, yv[i], 0.0f)) dz[i] = 0.0f;
+                float* out = (float*)o->data;
+                int st = weight_grad_sum((const float*)nd->src[0].data, &s0, dz, N, cout, L, cout * L, L, ck, &p,
+                                         out, threads);
+                if (st == VKHIP_OK) {
+                    vkhip_operand rd = {{(uint32_t)N, (uint32_t)cout, (uint32_t)y->ne[2], (uint32_t)y->ne[3]},
+                                        {cout * L, L, y->ne[3], 1}};
+                    or_reduce(VKHIP_REDUCE_SUM, dz, &rd, 0xDu, out + cout * ck, threads);
+                }
+                free(dz);
+                if (st != VKHIP_OK) return st;
                 break;
             }
             case VKHIP_OP_COL2IM: {

@@ -169,6 +169,46 @@ def relu_pool_loss_and_grad(backend, x, kernel, stride, pad, fused):
         T.FUSED_POOL_RELU_GRAD = prev
 
 
+def conv_pool_loss_and_grads(backend, x, w, bias, fused):
+    """sum(max_pool2d(relu(conv2d(x, w, bias, pad 1)), 2) * probe) with x
+    needing no gradient, and the weight and bias gradients: built as one
+    CONV2D_POOL_WEIGHT_BIAS_GRAD node (fused) or as MAX_POOL2D_BACKWARD_RELU,
+    CONV2D_WEIGHT_GRAD_SUM and the bias's SUM."""
+    from vkml_amd import tensor as T
+
+    prev = T.FUSED_CONV_POOL_GRAD
+    T.FUSED_CONV_POOL_GRAD = fused
+    try:
+        xt = T.tensor(x, backend=backend)
+        wt = T.tensor(w, requires_grad=True, backend=backend)
+        bt = T.tensor(bias, requires_grad=True, backend=backend)
+        out = T.max_pool2d(T.relu(T.conv2d(xt, wt, bt, 1, 1, 1)), 2)
+        probe = np.linspace(-1.0, 1.0, int(np.prod(out.shape)), dtype=np.float32)
+        loss = T.sum(out * T.tensor(probe.reshape(out.shape), backend=backend))
+        loss.backward()
+        src = wt.grad.node
+        while src.view_src is not None:
+            src = src.view_src
+        assert (src.op == T.OP["CONV2D_POOL_WEIGHT_BIAS_GRAD"]) == fused
+        return out.numpy(), wt.grad.numpy(), bt.grad.numpy()
+    finally:
+        T.FUSED_CONV_POOL_GRAD = prev
+
+
+def conv_pool_node(backend, x, y, gp, kernel, pad):
+    """The CONV2D_POOL_WEIGHT_BIAS_GRAD node alone over given x, y and gp
+    (unit stride and dilation): its [Cout*C*kh*kw + Cout] output."""
+    from vkml_amd import tensor as T
+
+    n_, c, h, w_ = x.shape
+    cout = y.shape[1]
+    ck = c * kernel[0] * kernel[1]
+    xt, yt, gt = (T.tensor(a, backend=backend) for a in (x, y, gp))
+    node = T.Node(T.OP["CONV2D_POOL_WEIGHT_BIAS_GRAD"], (cout * ck + cout,), np.float32, xt.node.backend,
+                  [xt.node, yt.node, gt.node], params=T._unfold_params(kernel, (1, 1), pad, (1, 1), (h, w_)))
+    return T.Tensor(node).numpy()
+
+
 def linear_loss_and_grads(backend, x, w, bias, relu, fused):
     """sum(relu?(x @ w.T + bias) * probe) and the gradients of x, w and bias,
     with the product, bias add and relu built as one MATMUL_BIAS node (fused)
@@ -249,7 +289,8 @@ def pool_relu_input(shape, seed):
 
 GRAPH_REWRITES = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU",
                   "FUSED_CONV_EPILOGUE", "FUSED_CONV_INPUT_GRAD", "FOLD_CONV_WEIGHT_GRAD",
-                  "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD")
+                  "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD",
+                  "FUSED_CONV_POOL_GRAD")
 
 
 def train_with_rewrites(backend, model_fn, batches, enabled, lr=0.1, momentum=0.9,

@@ -17,7 +17,7 @@ from conftest import (CONV_GEOMETRIES, SEED, small_window, ce_inputs, ce_loss_an
                       conv_relu_loss_and_grads, gemm_tolerance, mlp_batches, mlp_model, train_with_rewrites,
                       normwise_rel_err, relu_grad, relu_inputs, POOL_GEOMETRIES, pool_relu_input,
                       relu_pool_loss_and_grad, LINEAR_SHAPES, linear_loss_and_grads, MLP2_SHAPES,
-                      mlp2_loss_and_grads)
+                      mlp2_loss_and_grads, conv_pool_loss_and_grads, conv_pool_node)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -273,16 +273,55 @@ def test_pool_relu_gradient_node_on_device(backends, shape, kernel, stride, pad)
         assert got.tobytes() == ref.tobytes()
 
 
+# The CIFAR conv1 layer (the fused kernel), row widths 16 and 8 (fused, the
+# fewest spans it takes), and two it leaves to the three nodes (width 12; a
+# batch whose positions are no power of two).
+CONV_POOL_DEVICE_LAYERS = [((128, 3, 32, 32), 64), ((4, 3, 16, 16), 16), ((8, 3, 8, 8), 32),
+                           ((3, 4, 10, 12), 8), ((3, 3, 8, 8), 4)]
+
+
+@pytest.mark.parametrize("shape,cout", CONV_POOL_DEVICE_LAYERS)
+def test_conv_pool_gradient_node_on_device(backends, shape, cout):
+    """On the device, the weight and bias gradients of
+    max_pool2d(relu(conv2d(x, w, bias))) as one CONV2D_POOL_WEIGHT_BIAS_GRAD
+    node give the bits of the device's own MAX_POOL2D_BACKWARD_RELU +
+    CONV2D_WEIGHT_GRAD_SUM + SUM graph (pool windows with ties, pre-activations
+    on 0). The node alone over the same x, y and pool gradient: the bias
+    gradient is the oracle's bits (the pairwise tree's order), the weight
+    gradient within the GEMM bar over K = N*oh*ow."""
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED + 23)
+    x = rng.integers(-1, 2, shape).astype(np.float32)
+    w = (rng.integers(-1, 2, (cout, shape[1], 3, 3)) * 0.5).astype(np.float32)
+    bias = (rng.integers(-1, 2, cout) * 0.5).astype(np.float32)
+    print(f"conv_pool x={shape} cout={cout}", flush=True)
+    fused = conv_pool_loss_and_grads(dev, x, w, bias, True)
+    graph = conv_pool_loss_and_grads(dev, x, w, bias, False)
+    for got, two in zip(fused, graph):
+        assert got.tobytes() == two.tobytes()
+    n_, c, h, w_ = shape
+    xr = rng.uniform(-1, 1, shape).astype(np.float32)
+    y = pool_relu_input((n_, cout, h, w_), SEED + 24)
+    y = np.where(np.isnan(y), y, y + rng.uniform(0, 0.25, y.shape).astype(np.float32) * (y > 0))
+    gp = rng.standard_normal((n_, cout, h // 2, w_ // 2)).astype(np.float32)
+    got = conv_pool_node(dev, xr, y, gp, (3, 3), (1, 1))
+    want = conv_pool_node(cpu, xr, y, gp, (3, 3), (1, 1))
+    nw = cout * c * 9
+    assert got[nw:].tobytes() == want[nw:].tobytes()
+    assert normwise_rel_err(got[:nw], want[:nw]) <= gemm_tolerance(n_ * h * w_)
+
+
 @pytest.mark.parametrize("model", ["mlp", "cnn"])
 def test_exact_graph_rewrites_keep_the_device_bits(backends, model):
     """On the device, the graph rewrites that compute the same arithmetic
     (constant folding, weight gradients in the weight's layout, fused
-    add+relu, conv+bias+relu, pool+relu gradients and Linear bias epilogues) leave every loss and parameter of
+    add+relu, conv+bias+relu, pool+relu gradients, the conv layer's pool-fed
+    weight and bias gradients and Linear bias epilogues) leave every loss and parameter of
     SGD-momentum training bit for bit unchanged: config 1's MLP for 10 steps,
     config 5's CNN at batch 128 for 3 steps."""
     dev, _ = backends
     rewrites = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU", "FUSED_CONV_EPILOGUE",
-                "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD")
+                "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD", "FUSED_CONV_POOL_GRAD")
     if model == "mlp":
         fn, batches = mlp_model, mlp_batches(10)
     else:

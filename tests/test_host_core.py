@@ -13,7 +13,7 @@ from conftest import (CONV_GEOMETRIES, SEED, ce_inputs, ce_loss_and_grad, conv_l
                       config5_batches, config5_model, conv_relu_loss_and_grads, mlp_batches, mlp_model,
                       train_with_rewrites, POOL_GEOMETRIES, pool_relu_input, relu_pool_loss_and_grad,
                       LINEAR_SHAPES, linear_loss_and_grads, MLP2_SHAPES, mlp2_loss_and_grads,
-                      relu_grad, relu_inputs)
+                      relu_grad, relu_inputs, conv_pool_loss_and_grads)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -308,6 +308,57 @@ def test_pool_relu_gradient_node_is_the_two_nodes(cpu, shape, kernel, stride, pa
     # and the mask is the relu's: x <= 0 gets +0 whatever the pool routed there
     g = fused[1]
     assert np.all(g[x <= 0] == 0) and not np.any(np.signbit(g[x <= 0]))
+
+
+CONV_POOL_LAYERS = [((2, 3, 8, 8), 4), ((1, 2, 6, 10), 3), ((3, 1, 4, 4), 5)]
+
+
+def conv_pool_operands(shape, cout, seed):
+    """Small integers and halves: the conv outputs tie inside pool windows and
+    sit exactly on the relu's 0."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-1, 2, shape).astype(np.float32)
+    w = (rng.integers(-1, 2, (cout, shape[1], 3, 3)) * 0.5).astype(np.float32)
+    bias = (rng.integers(-1, 2, cout) * 0.5).astype(np.float32)
+    return x, w, bias
+
+
+@pytest.mark.parametrize("shape,cout", CONV_POOL_LAYERS)
+def test_conv_pool_gradient_node_is_the_three_nodes(cpu, shape, cout):
+    """The weight and bias gradients of max_pool2d(relu(conv2d(x, w, bias)))
+    with x needing none, as one CONV2D_POOL_WEIGHT_BIAS_GRAD node, give the
+    MAX_POOL2D_BACKWARD_RELU + CONV2D_WEIGHT_GRAD_SUM + SUM graph's bits on the
+    oracle, with ties in the pool windows and pre-activations on 0."""
+    x, w, bias = conv_pool_operands(shape, cout, SEED + 21)
+    fused = conv_pool_loss_and_grads(cpu, x, w, bias, True)
+    graph = conv_pool_loss_and_grads(cpu, x, w, bias, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
+    assert np.any(bias != 0) and np.any(fused[2] != 0)
+
+
+def test_conv_pool_gradient_rewrite_needs_its_pattern(cpu):
+    """No fused node when the image needs its gradient, or the pool is not 2x2
+    at stride 2: the three nodes stay."""
+    from vkml_amd import tensor as T
+
+    x, w, bias = conv_pool_operands((2, 3, 8, 8), 4, SEED + 22)
+
+    def weight_grad_source(x_grad, kernel, stride):
+        xt = T.tensor(x, requires_grad=x_grad, backend=cpu)
+        wt = T.tensor(w, requires_grad=True, backend=cpu)
+        bt = T.tensor(bias, requires_grad=True, backend=cpu)
+        out = T.max_pool2d(T.relu(T.conv2d(xt, wt, bt, 1, 1, 1)), kernel, stride)
+        T.sum(out).backward()
+        src = wt.grad.node
+        while src.view_src is not None:
+            src = src.view_src
+        return src.op
+
+    assert weight_grad_source(False, 2, 2) == T.OP["CONV2D_POOL_WEIGHT_BIAS_GRAD"]
+    assert weight_grad_source(True, 2, 2) == T.OP["CONV2D_WEIGHT_GRAD_SUM"]
+    assert weight_grad_source(False, 2, 1) == T.OP["CONV2D_WEIGHT_GRAD_SUM"]
+    assert weight_grad_source(False, 3, 2) == T.OP["CONV2D_WEIGHT_GRAD_SUM"]
 
 
 @pytest.mark.parametrize("shape,cout,kernel,stride,pad,dil", CONV_GEOMETRIES)

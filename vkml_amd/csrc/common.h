@@ -33,9 +33,11 @@ struct Context {
     // Split-K partials workspace, grown on demand and released stream-ordered
     // (reference grows its own the same way, vulkan_backend.cpp:899-919).
     // slot 0: split-K partials and reduction partials; slot 1: a node's own
-    // temporaries (which may hold data across a GEMM that uses slot 0)
-    float* ws[2] = {nullptr, nullptr};
-    size_t ws_bytes[2] = {0, 0};
+    // temporaries (which may hold data across a GEMM that uses slot 0);
+    // slot 2: a fused node's intermediate, held across the nodes it runs
+    // (which may use slots 0 and 1)
+    float* ws[3] = {nullptr, nullptr, nullptr};
+    size_t ws_bytes[3] = {0, 0, 0};
     int ws_pins = 0;               // captured graphs holding the workspace blocks
     void* ws_retired[64] = {};     // blocks replaced while pinned, freed at the last unpin
     int ws_retired_count = 0;
@@ -63,6 +65,8 @@ int workspace(size_t bytes, float** out, int slot = 0);
 // A node's temporary of at least `bytes` (workspace slot 1): valid until the
 // next node that asks for one; work using it is ordered on the stream.
 inline int node_temporary(size_t bytes, float** out) { return workspace(bytes, out, 1); }
+// A fused node's intermediate (workspace slot 2): valid until the next call.
+inline int fused_intermediate(size_t bytes, float** out) { return workspace(bytes, out, 2); }
 // While pinned (a captured HIP graph holds the current blocks), a workspace
 // that must grow gets a new block and keeps the old one until the last pin
 // goes, and the implicit-im2col row tables are not evicted.
@@ -439,6 +443,20 @@ __device__ __forceinline__ float wave_sum_butterfly(float v) {
     v = v + wave_partner<8>(v);
     v = v + wave_partner<16>(v);
     return lane_value(v, 0) + lane_value(v, 32);
+}
+
+// The window scan of a 2x2 max-pool: strict '>' from -inf over a, b, c, d in
+// that order (window positions (0,0), (0,1), (1,0), (1,1)); the offset of the
+// first maximum, -1 if none wins (all -inf or NaN). Shared by the pool kernels
+// and the fused pool-gradient weight-gradient kernel, so both pick alike.
+__device__ __forceinline__ int32_t argmax4(float a, float b, float c, float d) {
+    float best = -__builtin_inff();
+    int32_t off = -1;
+    if (a > best) { best = a; off = 0; }
+    if (b > best) { best = b; off = 1; }
+    if (c > best) { best = c; off = 2; }
+    if (d > best) { best = d; off = 3; }
+    return off;
 }
 
 }  // namespace vkhip

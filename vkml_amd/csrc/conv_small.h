@@ -31,6 +31,26 @@ int win_conv_weight_grad_sum(const float* x, const vkhip_operand& xd, const floa
                              float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
                              uint32_t ck, uint32_t oh, uint32_t ow);
 
+// Whether win_conv_pool_weight_bias_grad takes this layer: y [N][Cout][oh][ow]
+// (described by yd as the gradient is for win_wgrad_fits) and its 2x2,
+// stride-2 max-pool's output gradient gp (image and channel strides gpsn,
+// gpsc; rows contiguous), with ow in {4, 8, 16, 32}, oh even, N*oh*ow a power
+// of two.
+bool win_pool_wgrad_fits(const float* y, const vkhip_operand& yd, const float* gp, int64_t gpsn, int64_t gpsc,
+                         const vkhip_operand& xd, const vkhip_unfold& pr, uint32_t channels, uint64_t ck,
+                         uint32_t cout, uint64_t batch, uint32_t oh, uint32_t ow);
+
+// The conv layer's weight and bias gradients from its pool's output gradient:
+// dz = the max-pool backward of gp over y masked by the relu (y <= 0 -> 0),
+// formed in the kernel and never written; out [Cout][K] = the batch-summed
+// weight gradient of dz (win_conv_weight_grad_sum's bits) and bias_out[Cout]
+// = the sum of dz over N, oh, ow in the pairwise tree's order (the
+// reduction's bits). Two launches.
+int win_conv_pool_weight_bias_grad(const float* x, const vkhip_operand& xd, const float* y, const vkhip_operand& yd,
+                                   const float* gp, int64_t gpsn, int64_t gpsc, float* out, float* bias_out,
+                                   const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
+                                   uint32_t ck, uint32_t oh, uint32_t ow);
+
 // Whether win_conv_input_grad takes this input gradient (unit strides, C*kh*kw
 // <= 32, Cout <= 128).
 bool win_dx_fits(const vkhip_operand& gd, int64_t w_row, const vkhip_unfold& pr, uint32_t batch, uint32_t channels,

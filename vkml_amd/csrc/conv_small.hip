@@ -33,6 +33,7 @@
 namespace vkhip {
 namespace {
 
+typedef float v2f __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -401,6 +402,13 @@ struct WinWgrad {
     int32_t gsc;               // gradient channel stride (elements; rows 16-byte aligned)
     float* part;               // [nwg][2048] workgroup partials (output co * 32 + j)
     float* out;                // [Cout][K]
+    // GM = 1: g is the pool's input y (the layer's relu output) and the
+    // gradient is that of a 2x2, stride-2 max-pool of y given the pool's
+    // output gradient gp [N][Cout][oh/2][ow/2] (rows contiguous).
+    const float* gp;
+    int64_t gpsn;              // pool gradient image stride (elements)
+    int32_t gpsc;              // pool gradient channel stride (elements, even)
+    float* bpart;              // GM = 1: [nwg][64] the bias gradient's span sums
     int32_t C, H, W, padh, padw, strh, strw, OW, Wp, rows, plane, stage;
     uint32_t cout, K, L, wg_per_image, nwg;
     FastDiv div_ow;
@@ -409,8 +417,9 @@ struct WinWgrad {
     int32_t offs[32];
 };
 
-template <int T, int NW, int CH, int D>
+template <int T, int NW, int CH, int D, int GM>
 __global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
+    static_assert(GM == 0 || (NW == 4 && (CH & (CH - 1)) == 0), "pool-gradient chunks: 64 positions");
     extern __shared__ __attribute__((aligned(16))) float smem[];
     constexpr int NT = 64 * NW;        // threads
     constexpr int PC = 16 * NW;        // positions per chunk: 16 per wave
@@ -439,16 +448,83 @@ __global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
         goff[u] = co < p.cout ? (co * static_cast<uint32_t>(p.gsc) + pos0 + 4u * grp) * 4u : 0x80000000u;
         gdst[u] = static_cast<int32_t>(co * G + (grp ^ (co & 15u))) * 4;
     }
+    // GM = 1: the chunk's gradient from the pool. A chunk (64 positions) is
+    // 64 / OW whole row pairs, i.e. 512 blocks of 2 rows x 4 positions (two
+    // pool windows); thread tid takes blocks tid and tid + 256: channel s / 8,
+    // block s % 8 = row pair rp and column group cg. Each block loads y's two
+    // rows (16 bytes each) and the two windows' pool gradients (8 bytes), and
+    // stores the max-pool backward with the relu mask (the values of
+    // max_pool2x2_backward_kernel<true>) as the two 16-byte groups of its rows.
+    const __amdgpu_buffer_rsrc_t pr_ = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(GM == 1 ? p.gp + static_cast<int64_t>(n) * p.gpsn : p.g), 0,
+        static_cast<int32_t>(0x80000000u), 0x00020000);
+    uint32_t poff[2] = {0u, 0u}, row2 = 0u;
+    int32_t pdst[2][2] = {{0, 0}, {0, 0}};
+    if constexpr (GM == 1) {
+        const uint32_t qw = static_cast<uint32_t>(p.OW) / 4u;
+        row2 = static_cast<uint32_t>(p.OW) * 4u;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t sl = static_cast<uint32_t>(tid) + NT * u, co = sl >> 3, b = sl & 7u;
+            const uint32_t rp = b / qw, cg = b - rp * qw;
+            const uint32_t at = 2u * rp * static_cast<uint32_t>(p.OW) + 4u * cg;  // block's first position in the chunk
+            goff[u] = co < p.cout ? (co * static_cast<uint32_t>(p.gsc) + pos0 + at) * 4u : 0x80000000u;
+            poff[u] = co < p.cout ? (co * static_cast<uint32_t>(p.gpsc) + pos0 / 4u + rp * (p.OW / 2u) + 2u * cg) * 4u
+                                  : 0x80000000u;
+            const uint32_t gtop = at / 4u, gbot = gtop + qw;
+            pdst[u][0] = static_cast<int32_t>(co * G + (gtop ^ (co & 15u))) * 4;
+            pdst[u][1] = static_cast<int32_t>(co * G + (gbot ^ (co & 15u))) * 4;
+        }
+    }
     v4f ring[D][4];
-    auto load_chunk = [&](int c, v4f (&r)[4]) {
+    v2f pring[D][2];
+    auto load_chunk = [&](int c, v4f (&r)[4], v2f (&pg)[2]) {
+        if constexpr (GM == 1) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            r[u] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                                               gr, static_cast<int32_t>(goff[u]), c * PC * 4, 0));
+            for (int u = 0; u < 2; ++u) {
+                r[2 * u] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       gr, static_cast<int32_t>(goff[u]), c * PC * 4, 0));
+                r[2 * u + 1] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           gr, static_cast<int32_t>(goff[u] + row2), c * PC * 4, 0));
+                pg[u] = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(
+                                                    pr_, static_cast<int32_t>(poff[u]), c * PC, 0));
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                r[u] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   gr, static_cast<int32_t>(goff[u]), c * PC * 4, 0));
+        }
     };
-    auto store_chunk = [&](int buf, const v4f (&r)[4]) {
+    auto store_chunk = [&](int buf, const v4f (&r)[4], const v2f (&pg)[2]) {
+        if constexpr (GM == 1) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) *reinterpret_cast<v4f*>(gbuf + buf * CF + gdst[u]) = r[u];
+            for (int u = 0; u < 2; ++u) {
+                const v4f t = r[2 * u], b = r[2 * u + 1];
+                const int32_t a0 = argmax4(t[0], t[1], b[0], b[1]);
+                const int32_t a1 = argmax4(t[2], t[3], b[2], b[3]);
+                const float g0 = 0.0f + pg[u][0], g1 = 0.0f + pg[u][1];
+                v4f top, bot;
+                top[0] = a0 == 0 ? g0 : 0.0f;
+                top[1] = a0 == 1 ? g0 : 0.0f;
+                bot[0] = a0 == 2 ? g0 : 0.0f;
+                bot[1] = a0 == 3 ? g0 : 0.0f;
+                top[2] = a1 == 0 ? g1 : 0.0f;
+                top[3] = a1 == 1 ? g1 : 0.0f;
+                bot[2] = a1 == 2 ? g1 : 0.0f;
+                bot[3] = a1 == 3 ? g1 : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (t[i] <= 0.0f) top[i] = 0.0f;
+                    if (b[i] <= 0.0f) bot[i] = 0.0f;
+                }
+                *reinterpret_cast<v4f*>(gbuf + buf * CF + pdst[u][0]) = top;
+                *reinterpret_cast<v4f*>(gbuf + buf * CF + pdst[u][1]) = bot;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) *reinterpret_cast<v4f*>(gbuf + buf * CF + gdst[u]) = r[u];
+        }
     };
     // The input rows of the workgroup's positions, staged as the forward does.
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -480,7 +556,7 @@ __global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
     }
     // the first D chunks' loads go out behind the image's
 #pragma unroll
-    for (int c = 0; c < D && c < CH; ++c) load_chunk(c, ring[c]);
+    for (int c = 0; c < D && c < CH; ++c) load_chunk(c, ring[c], pring[c]);
     for (int e = tid; e < p.plane; e += NT) img[p.stage + e] = 0.0f;
     if (tid < 32) offs_l[tid] = my_off;
 #pragma unroll
@@ -489,9 +565,39 @@ __global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
         if (row >= nrows) break;
         if (lane < p.Wp) img[row * p.Wp + lane] = sv[u];
     }
-    store_chunk(0, ring[0]);
+    store_chunk(0, ring[0], pring[0]);
     __syncthreads();
     const int32_t off = offs_l[lrow];  // this lane's window element (B column lrow)
+
+    // GM = 1, the bias gradient: the sum over the workgroup's span of each
+    // channel's gradient as the oracle's pairwise tree takes it (the span is
+    // an aligned power-of-two subtree): leaves of 32 positions summed in order
+    // from +0, adjacent leaves and then pairs added level by level. A chunk
+    // holds two leaves per channel; half the threads (waves 0-1 for even
+    // chunks, 2-3 for odd ones) sum one leaf each from the chunk buffer, and
+    // the even lane keeps the pair's sum in bl[c][co].
+    float* bl = reinterpret_cast<float*>(offs_l + 32);  // [CH][64]
+    auto leaves = [&](int c) {
+        if constexpr (GM == 1) {
+            const int t = (tid + 128 * (c & 1)) & 255;
+            if (t < 128) {
+                const uint32_t co = static_cast<uint32_t>(t) >> 1, j = static_cast<uint32_t>(t) & 1u;
+                const float* gb = gbuf + (c & 1) * CF;
+                float sum = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t grp = 8u * j + k;
+                    const v4f v = *reinterpret_cast<const v4f*>(gb + (co * G + (grp ^ (co & 15u))) * 4u);
+                    sum = sum + v[0];
+                    sum = sum + v[1];
+                    sum = sum + v[2];
+                    sum = sum + v[3];
+                }
+                const float other = wave_partner<1>(sum);
+                if (j == 0) bl[c * 64 + co] = sum + other;
+            }
+        }
+    };
 
     // A chunk's operands of this wave: its 16 positions are the 4-position
     // groups 8gg + 4kh (gg = 0, 1); a[gg][i] = 4 positions of channel 32i +
@@ -540,13 +646,15 @@ __global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
     // before the previous barrier.
     Ops ops[2];
     read_ops(0, ops[0]);
+    leaves(0);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-        if (c + D < CH) load_chunk(c + D, ring[c % D]);  // its slot's data is in LDS already
+        if (c + D < CH) load_chunk(c + D, ring[c % D], pring[c % D]);  // its slot's data is in LDS already
         if (c + 1 < CH) {
-            store_chunk((c + 1) & 1, ring[(c + 1) % D]);
+            store_chunk((c + 1) & 1, ring[(c + 1) % D], pring[(c + 1) % D]);
             __syncthreads();
             read_ops(c + 1, ops[(c + 1) & 1]);
+            leaves(c + 1);
         }
         mfma_ops(ops[c & 1]);
     }
@@ -560,6 +668,19 @@ __global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
         for (int r = 0; r < 16; ++r) red[((wave * T + i) * 16 + r) * 64 + lane] = acc[0][i][r] + acc[1][i][r];
     __syncthreads();
     const uint32_t wg = n * p.wg_per_image + blockIdx.x;
+    if constexpr (GM == 1) {
+        // the chunk pairs' sums up the balanced tree: the span's sum
+        if (tid < 64) {
+            float v[CH];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) v[c] = bl[c * 64 + tid];
+#pragma unroll
+            for (int w = 1; w < CH; w *= 2)
+#pragma unroll
+                for (int i = 0; i + w < CH; i += 2 * w) v[i] = v[i] + v[i + w];
+            p.bpart[static_cast<uint64_t>(wg) * 64u + tid] = v[0];
+        }
+    }
     float* mine = p.part + static_cast<uint64_t>(wg) * 2048u;
     // output o = co * 32 + j of the partial; lane l of register r of tile i
     // holds co = 32i + 8(r/4) + 4(l/32) + r%4, j = l%32
@@ -579,10 +700,59 @@ __global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
 // ([parts][2048] at part), in partial order: 16 threads per output, each
 // adding a run of at most 16 consecutive partials, then the 16 run sums in run
 // order (at most 32 per run). A workgroup takes 16 outputs.
+//
+// With bpart (the pool-gradient kernel's span sums, [parts][64], parts a power
+// of two >= 4), the last workgroup folds the bias gradient into bout[Cout]:
+// per channel the balanced pairwise tree over the span sums, as four runs of
+// parts / 4 consecutive sums (a binary-counter carry stack over each, which
+// for a power-of-two count is the balanced tree) and then (run 0 + run 1) +
+// (run 2 + run 3).
 __global__ __launch_bounds__(256) void win_fold_kernel(const float* __restrict__ part, uint32_t parts,
-                                                       float* __restrict__ out, uint32_t cout, uint32_t K) {
+                                                       float* __restrict__ out, uint32_t cout, uint32_t K,
+                                                       const float* __restrict__ bpart, float* __restrict__ bout) {
     __shared__ float runs[16][17];
     const int tid = threadIdx.x, oi = tid & 15, run = tid >> 4;
+    if (bpart != nullptr && blockIdx.x == gridDim.x - 1) {
+        __shared__ float bruns[4][64];
+        const int co = tid & 63, br = tid >> 6;
+        const uint32_t per = parts / 4u;
+        float stack[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) stack[l] = 0.0f;
+        for (uint32_t i0 = 0; i0 < per; i0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = i0 + u < per ? bpart[static_cast<uint64_t>(br * per + i0 + u) * 64u + co] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (i0 + u >= per) break;
+                const uint32_t count = i0 + u;
+                float b = v[u];
+                bool carry = true;
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    if (carry) {
+                        if ((count >> l) & 1u) {
+                            b = stack[l] + b;
+                        } else {
+                            stack[l] = b;
+                            carry = false;
+                        }
+                    }
+                }
+            }
+        }
+        float r = 0.0f;
+#pragma unroll
+        for (int l = 0; l < 8; ++l)
+            if (per == (1u << l)) r = stack[l];
+        bruns[br][co] = r;
+        __syncthreads();
+        if (tid < 64 && static_cast<uint32_t>(tid) < cout)
+            bout[tid] = (bruns[0][tid] + bruns[1][tid]) + (bruns[2][tid] + bruns[3][tid]);
+        return;
+    }
     const uint32_t o = blockIdx.x * 16u + oi;
     const uint32_t per = (parts + 15u) / 16u, first = run * per;
     float x[32];
@@ -624,12 +794,27 @@ constexpr uint32_t kWgWaves = 4;
 
 constexpr int kWgLdsFloats = 24576;  // dynamic LDS of the weight-gradient kernel: 96 KB
 
-// LDS floats: the staged rows and zero region, two chunk buffers, the offsets.
+// LDS floats: the staged rows and zero region, two chunk buffers, the offsets
+// and the pool-gradient kernel's chunk pair sums (8 chunks x 64 channels).
 size_t win_wgrad_lds(int32_t channels, int32_t plane, uint32_t waves) {
-    return ((static_cast<size_t>(channels + 1) * plane + 3) & ~size_t(3)) + 2 * 64 * 16 * waves + 32;
+    return ((static_cast<size_t>(channels + 1) * plane + 3) & ~size_t(3)) + 2 * 64 * 16 * waves + 32 + 512;
 }
 
+// The pool-gradient variant's arguments (GM = 1).
+struct WinPoolGrad {
+    const float* gp;  // [N][Cout][oh/2][ow/2]
+    int64_t gpsn, gpsc;
+    float* bias_out;  // [Cout]
+};
+
+
 }  // namespace
+
+// The batch-summed weight gradient's two launches (pool: the pool-gradient
+// variant with the bias gradient).
+static int win_weight_grad_launch(const float* x, const vkhip_operand& xd, const float* g, const vkhip_operand& gd,
+                                  float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels,
+                                  uint32_t cout, uint32_t ck, uint32_t oh, uint32_t ow, const WinPoolGrad* pool);
 
 bool win_wgrad_fits(const float* g, const vkhip_operand& gd, const vkhip_operand& xd, const vkhip_unfold& pr,
                     uint32_t channels, uint64_t ck, uint32_t cout, uint64_t batch, uint32_t oh, uint32_t ow) {
@@ -660,6 +845,38 @@ bool win_wgrad_fits(const float* g, const vkhip_operand& gd, const vkhip_operand
 int win_conv_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* g, const vkhip_operand& gd,
                              float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
                              uint32_t ck, uint32_t oh, uint32_t ow) {
+    return win_weight_grad_launch(x, xd, g, gd, out, pr, batch, channels, cout, ck, oh, ow, nullptr);
+}
+
+bool win_pool_wgrad_fits(const float* y, const vkhip_operand& yd, const float* gp, int64_t gpsn, int64_t gpsc,
+                         const vkhip_operand& xd, const vkhip_unfold& pr, uint32_t channels, uint64_t ck,
+                         uint32_t cout, uint64_t batch, uint32_t oh, uint32_t ow) {
+    if (!win_wgrad_fits(y, yd, xd, pr, channels, ck, cout, batch, oh, ow)) return false;
+    // chunks of whole row pairs, a power-of-two reduction (so every span is an
+    // aligned subtree of the pairwise tree) and at least four spans
+    const uint64_t L = static_cast<uint64_t>(oh) * ow;
+    const uint64_t total = batch * L;
+    if (!(ow == 4 || ow == 8 || ow == 16 || ow == 32) || oh % 2 != 0 || (total & (total - 1)) != 0) return false;
+    const uint32_t span = win_wgrad_span(batch, static_cast<uint32_t>(L));
+    if (span == 0 || total / span < 4) return false;
+    // 8-byte pool-gradient pairs, rows contiguous, 32-bit byte offsets
+    if (reinterpret_cast<uintptr_t>(gp) % 8 != 0 || gpsc % 2 != 0 || gpsc < static_cast<int64_t>(L / 4) ||
+        gpsn < 0 || (static_cast<int64_t>(cout) - 1) * gpsc + static_cast<int64_t>(L / 4) > (int64_t(1) << 28))
+        return false;
+    return true;
+}
+
+int win_conv_pool_weight_bias_grad(const float* x, const vkhip_operand& xd, const float* y, const vkhip_operand& yd,
+                                   const float* gp, int64_t gpsn, int64_t gpsc, float* out, float* bias_out,
+                                   const vkhip_unfold& pr, uint32_t batch, uint32_t channels, uint32_t cout,
+                                   uint32_t ck, uint32_t oh, uint32_t ow) {
+    const WinPoolGrad pool{gp, gpsn, gpsc, bias_out};
+    return win_weight_grad_launch(x, xd, y, yd, out, pr, batch, channels, cout, ck, oh, ow, &pool);
+}
+
+static int win_weight_grad_launch(const float* x, const vkhip_operand& xd, const float* g, const vkhip_operand& gd,
+                                  float* out, const vkhip_unfold& pr, uint32_t batch, uint32_t channels,
+                                  uint32_t cout, uint32_t ck, uint32_t oh, uint32_t ow, const WinPoolGrad* pool) {
     WinWgrad p{};
     p.x = x;
     p.sn = xd.nb[0];
@@ -711,26 +928,41 @@ int win_conv_weight_grad_sum(const float* x, const vkhip_operand& xd, const floa
     const size_t lds = win_wgrad_lds(p.C, p.plane, waves);
     if (p.C * p.rows > 64 || lds > kWgLdsFloats || p.nwg > kWgMaxParts)
         return fail(VKHIP_ERR_INVALID, "conv2d weight grad sum: the small-window plan does not fit");
-    const int st = workspace(static_cast<size_t>(p.nwg) * 2048u * sizeof(float), &p.part);
+    const size_t part_floats = static_cast<size_t>(p.nwg) * (2048u + (pool ? 64u : 0u));
+    const int st = workspace(part_floats * sizeof(float), &p.part);
     if (st != VKHIP_OK) return st;
+    if (pool) {
+        p.gp = pool->gp;
+        p.gpsn = pool->gpsn;
+        p.gpsc = static_cast<int32_t>(pool->gpsc);
+        p.bpart = p.part + static_cast<size_t>(p.nwg) * 2048u;
+        if ((p.nwg & (p.nwg - 1)) != 0 || p.nwg < 4 || (ch & (ch - 1)) != 0 || 2 * p.OW > 64 || 64 % (2 * p.OW) != 0)
+            return fail(VKHIP_ERR_INVALID, "conv2d pool weight grad: the small-window plan does not fit");
+    }
     const dim3 grid(p.wg_per_image, batch);
     const size_t bytes = lds * sizeof(float);
     const bool two = cout > 32;
-#define VKHIP_WGR(T, NW, CH, D) \
-    hipLaunchKernelGGL((win_wgrad_kernel<T, NW, CH, D>), grid, dim3(64 * NW), bytes, ctx().stream, p)
-#define VKHIP_WGR_CH(T)                                          \
+#define VKHIP_WGR(T, NW, CH, D, GM) \
+    hipLaunchKernelGGL((win_wgrad_kernel<T, NW, CH, D, GM>), grid, dim3(64 * NW), bytes, ctx().stream, p)
+#define VKHIP_WGR_CH(T, GM)                                      \
     do {                                                         \
         static_assert(kWgWaves == 4, "instantiate other wave counts"); \
-        if (ch == 8) VKHIP_WGR(T, 4, 8, 4);                      \
-        else if (ch == 4) VKHIP_WGR(T, 4, 4, 3);                 \
-        else if (ch == 2) VKHIP_WGR(T, 4, 2, 2);                 \
-        else VKHIP_WGR(T, 4, 1, 1);                              \
+        if (ch == 8) VKHIP_WGR(T, 4, 8, 4, GM);                  \
+        else if (ch == 4) VKHIP_WGR(T, 4, 4, 3, GM);             \
+        else if (ch == 2) VKHIP_WGR(T, 4, 2, 2, GM);             \
+        else VKHIP_WGR(T, 4, 1, 1, GM);                          \
     } while (0)
-    if (two) VKHIP_WGR_CH(2); else VKHIP_WGR_CH(1);
+    if (pool) {
+        if (two) VKHIP_WGR_CH(2, 1); else VKHIP_WGR_CH(1, 1);
+    } else {
+        if (two) VKHIP_WGR_CH(2, 0); else VKHIP_WGR_CH(1, 0);
+    }
 #undef VKHIP_WGR_CH
 #undef VKHIP_WGR
     VKHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(win_fold_kernel, dim3(two ? 128 : 64), dim3(256), 0, ctx().stream, p.part, p.nwg, out, cout, ck);
+    const uint32_t fold_wgs = (two ? 128u : 64u) + (pool ? 1u : 0u);
+    hipLaunchKernelGGL(win_fold_kernel, dim3(fold_wgs), dim3(256), 0, ctx().stream, p.part, p.nwg, out, cout, ck,
+                       pool ? p.bpart : nullptr, pool ? pool->bias_out : nullptr);
     VKHIP_LAUNCH_CHECK();
     return VKHIP_OK;
 }

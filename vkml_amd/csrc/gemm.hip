@@ -3847,6 +3847,89 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
 
 int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst);
 int launch_col2im(const float* cols, float* dst, uint32_t n, uint32_t channels, const vkhip_unfold& p);
+int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_operand& sd, float* dst,
+                               uint32_t out_h, uint32_t out_w, const vkhip_unfold& p, bool relu);
+int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* gr, const vkhip_operand& gd,
+                           float* out, const vkhip_unfold& p);
+
+// The weight and bias gradients of a conv layer whose output y = relu(conv2d(x,
+// w) + bias) feeds a 2x2, stride-2 max-pool, from the pool's output gradient gp
+// (VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD): out = [Cout*C*kh*kw weight
+// gradient, Cout bias gradient], the values of the MAX_POOL2D_BACKWARD_RELU,
+// CONV2D_WEIGHT_GRAD_SUM and SUM (over N, oh, ow) nodes it replaces. yd, gpd:
+// [N, Cout, oh, ow] and [N, Cout, oh/2, ow/2] (to_operand's rank-4 layout).
+//  - FAST numerics where the small-window kernel takes the layer: one pass
+//    over y and gp that forms the relu-masked pool gradient in the kernel
+//    (never written) and sums both gradients (win_conv_pool_weight_bias_grad):
+//    the replaced nodes' bits on the fast path.
+//  - Otherwise those nodes in turn, the pool gradient in the fused
+//    intermediate.
+int conv2d_pool_weight_bias_grad(const float* x, const vkhip_operand& xd, const float* y, const vkhip_operand& yd,
+                                 const float* gp, const vkhip_operand& gpd, float* out, const vkhip_unfold& p) {
+    const uint32_t batch = yd.ne[0], cout = yd.ne[1], oh = yd.ne[2], ow = yd.ne[3];
+    const uint64_t L = static_cast<uint64_t>(oh) * ow;
+    const uint64_t ck = static_cast<uint64_t>(xd.ne[1]) * p.kernel_h * p.kernel_w;
+    if (gpd.ne[0] != batch || gpd.ne[1] != cout || gpd.ne[2] != oh / 2 || gpd.ne[3] != ow / 2 || xd.ne[0] != batch)
+        return fail(VKHIP_ERR_INVALID, "conv2d pool weight grad: pool gradient [%u,%u,%u,%u] does not pool [%u,%u,%u,%u]",
+                    gpd.ne[0], gpd.ne[1], gpd.ne[2], gpd.ne[3], batch, cout, oh, ow);
+    float* bias_out = out + static_cast<uint64_t>(cout) * ck;
+    vkhip_operand gyd;  // y as a gradient operand [1, N, Cout, L]
+    gyd.ne[0] = 1;
+    gyd.ne[1] = batch;
+    gyd.ne[2] = cout;
+    gyd.ne[3] = static_cast<uint32_t>(L);
+    gyd.nb[0] = 0;
+    gyd.nb[1] = yd.nb[0];
+    gyd.nb[2] = yd.nb[1];
+    gyd.nb[3] = 1;
+    const bool y_rows = yd.nb[3] == 1 && yd.nb[2] == static_cast<int64_t>(ow);
+    const bool gp_rows = gpd.nb[3] == 1 && gpd.nb[2] == static_cast<int64_t>(ow / 2);
+    if (!ctx().exact_math && y_rows && gp_rows && L <= 0xffffffffull &&
+        win_pool_wgrad_fits(y, gyd, gp, gpd.nb[0], gpd.nb[1], xd, p, xd.ne[1], ck, cout, batch, oh, ow)) {
+        publish("matmul.kernel", "conv2d_pool_weight_bias_grad", "win_wgrad_pool", "pool_backward_then_products",
+                "C*kh*kw <= 32: the relu-masked pool gradient formed in the weight-gradient kernel",
+                static_cast<int64_t>(L), static_cast<int64_t>(ck));
+        return win_conv_pool_weight_bias_grad(x, xd, y, gyd, gp, gpd.nb[0], gpd.nb[1], out, bias_out, p, batch,
+                                              xd.ne[1], cout, static_cast<uint32_t>(ck), oh, ow);
+    }
+    publish("matmul.kernel", "conv2d_pool_weight_bias_grad", "pool_backward_then_products", "win_wgrad_pool",
+            ctx().exact_math ? "exact numerics mode" : "the layer does not fit the small-window kernel",
+            static_cast<int64_t>(L), static_cast<int64_t>(ck));
+    const uint64_t dz_elems = static_cast<uint64_t>(batch) * cout * L;
+    float* dz = nullptr;
+    int st = fused_intermediate(dz_elems * sizeof(float), &dz);
+    if (st != VKHIP_OK) return st;
+    vkhip_unfold pp{};
+    pp.kernel_h = pp.kernel_w = 2;
+    pp.stride_h = pp.stride_w = 2;
+    pp.pad_h = pp.pad_w = 0;
+    pp.dilation_h = pp.dilation_w = 1;
+    pp.image_h = static_cast<int32_t>(oh);
+    pp.image_w = static_cast<int32_t>(ow);
+    st = launch_max_pool2d_backward(gp, y, yd, dz, gpd.ne[2], gpd.ne[3], pp, true);
+    if (st != VKHIP_OK) return st;
+    vkhip_operand dgd;  // dz as the gradient operand [1, N, Cout, L]
+    dgd.ne[0] = 1;
+    dgd.ne[1] = batch;
+    dgd.ne[2] = cout;
+    dgd.ne[3] = static_cast<uint32_t>(L);
+    dgd.nb[0] = 0;
+    dgd.nb[1] = static_cast<int64_t>(cout) * static_cast<int64_t>(L);
+    dgd.nb[2] = static_cast<int64_t>(L);
+    dgd.nb[3] = 1;
+    st = conv2d_weight_grad_sum(x, xd, dz, dgd, out, p);
+    if (st != VKHIP_OK) return st;
+    vkhip_operand rd;  // dz [N, Cout, oh, ow], summed over axes 0, 2, 3
+    rd.ne[0] = batch;
+    rd.ne[1] = cout;
+    rd.ne[2] = oh;
+    rd.ne[3] = ow;
+    rd.nb[0] = dgd.nb[1];
+    rd.nb[1] = static_cast<int64_t>(L);
+    rd.nb[2] = static_cast<int64_t>(ow);
+    rd.nb[3] = 1;
+    return launch_reduce(VKHIP_REDUCE_SUM, dz, rd, 0xDu, bias_out);
+}
 
 // The weight gradient summed over the batch, out [Cout, C*kh*kw] = sum_n
 // grad[n] @ im2col(x[n])^T: the reference graph's per-image products and

@@ -628,18 +628,9 @@ __global__ __launch_bounds__(256) void max_pool2d_backward_kernel(
 // 2*oh and 2*oh + 1, columns 4j..4j+3) cover both. Output row r of the flat
 // [planes*out_h, out_w] output reads input rows 2r and 2r + 1 of the flat
 // [planes*H, W] input. The window scan is window_argmax's: strict '>' from
-// -inf in the order (0,0), (0,1), (1,0), (1,1); no winner (all -inf or NaN)
-// gives -1, and the forward then takes the first position, as the general
-// kernel does.
-__device__ __forceinline__ int32_t argmax4(float a, float b, float c, float d) {
-    float best = -__builtin_inff();
-    int32_t off = -1;
-    if (a > best) { best = a; off = 0; }
-    if (b > best) { best = b; off = 1; }
-    if (c > best) { best = c; off = 2; }
-    if (d > best) { best = d; off = 3; }
-    return off;
-}
+// -inf in the order (0,0), (0,1), (1,0), (1,1) (argmax4, common.h); no winner
+// (all -inf or NaN) gives -1, and the forward then takes the first position, as
+// the general kernel does.
 
 __device__ __forceinline__ float pick4(int32_t off, float a, float b, float c, float d) {
     return off == 1 ? b : off == 2 ? c : off == 3 ? d : a;

@@ -26,6 +26,8 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
                        const vkhip_operand& gd, float* out, const vkhip_unfold& p);
 int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* gr,
                            const vkhip_operand& gd, float* out, const vkhip_unfold& p);
+int conv2d_pool_weight_bias_grad(const float* x, const vkhip_operand& xd, const float* y, const vkhip_operand& yd,
+                                 const float* gp, const vkhip_operand& gpd, float* out, const vkhip_unfold& p);
 int conv2d_input_grad(const float* gr, const vkhip_operand& gd, const float* w, int64_t w_row,
                       uint32_t channels, float* out, const vkhip_unfold& p);
 int launch_cross_entropy(const float* logits, int64_t row_stride, const int64_t* labels,
@@ -99,7 +101,7 @@ int require_ready() {
 int workspace(size_t bytes, float** out, int slot) {
     std::lock_guard<std::mutex> lk(g_mu);
     Context& c = ctx();
-    if (slot < 0 || slot > 1) return fail(VKHIP_ERR_INVALID, "workspace: slot %d", slot);
+    if (slot < 0 || slot > 2) return fail(VKHIP_ERR_INVALID, "workspace: slot %d", slot);
     if (c.ws_bytes[slot] < bytes) {
         if (c.ws[slot] && c.ws_pins > 0) {
             // a captured graph still addresses this block: keep it
@@ -343,6 +345,16 @@ static int supports_node(const vkhip_node& nd) {
                    o.ne[0] == gr.ne[1] && gr.nb[3] == 1 && gr.nb[2] == gr.ne[3] &&
                    static_cast<int64_t>(p.kernel_h) * p.kernel_w <= 63;
         }
+        case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: {
+            const vkhip_tensor& x = nd.src[0];
+            const vkhip_tensor& y = nd.src[1];
+            const vkhip_tensor& gp = nd.src[2];
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return nd.n_src == 3 && is_f32(x) && is_f32(y) && is_f32(gp) && is_f32(o) && x.ndim == 4 &&
+                   y.ndim == 4 && gp.ndim == 4 && contiguous(y) && contiguous(gp) && o.ndim == 1 && contiguous(o) &&
+                   static_cast<int64_t>(p.kernel_h) * p.kernel_w <= 63;
+        }
         case VKHIP_OP_CROSS_ENTROPY:
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
             const vkhip_tensor& x = nd.src[0];
@@ -478,6 +490,24 @@ static int check_extents(const vkhip_node& nd) {
                             static_cast<long long>(oh * ow), p.image_h, p.image_w);
             return VKHIP_OK;
         }
+        case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            const int64_t oh = window_span(p.image_h, p.kernel_h, p.stride_h, p.pad_h, p.dilation_h);
+            const int64_t ow = window_span(p.image_w, p.kernel_w, p.stride_w, p.pad_w, p.dilation_w);
+            const vkhip_tensor& x = nd.src[0];
+            const vkhip_tensor& y = nd.src[1];
+            const vkhip_tensor& gp = nd.src[2];
+            if (nd.n_src != 3 || x.ndim != 4 || y.ndim != 4 || gp.ndim != 4 || o.ndim != 1 || oh <= 0 || ow <= 0 ||
+                x.ne[2] != p.image_h || x.ne[3] != p.image_w || y.ne[0] != x.ne[0] || y.ne[2] != oh ||
+                y.ne[3] != ow || gp.ne[0] != y.ne[0] || gp.ne[1] != y.ne[1] || gp.ne[2] != oh / 2 ||
+                gp.ne[3] != ow / 2 ||
+                o.ne[0] != y.ne[1] * (x.ne[1] * static_cast<int64_t>(p.kernel_h) * p.kernel_w + 1))
+                return fail(VKHIP_ERR_INVALID,
+                            "conv2d_pool_weight_bias_grad: image, layer output, pool gradient and output extents "
+                            "disagree with the window geometry");
+            return VKHIP_OK;
+        }
         case VKHIP_OP_MAX_POOL2D: {
             vkhip_unfold p;
             memcpy(&p, nd.params, sizeof p);
@@ -528,6 +558,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_MAX_POOL2D: return "max_pool2d";
         case VKHIP_OP_MAX_POOL2D_BACKWARD: return "max_pool2d_backward";
         case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU: return "max_pool2d_backward_relu";
+        case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: return "conv2d_pool_weight_bias_grad";
         case VKHIP_OP_CROSS_ENTROPY: return "cross_entropy";
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: return "cross_entropy_backward";
         case VKHIP_OP_CONV2D: return "conv2d";
@@ -725,6 +756,14 @@ static int compute_node(const vkhip_node& nd) {
                                           static_cast<const float*>(gr.data), gd,
                                           static_cast<float*>(nd.out.data), p);
         }
+        case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return conv2d_pool_weight_bias_grad(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
+                                                static_cast<const float*>(nd.src[1].data), to_operand(nd.src[1]),
+                                                static_cast<const float*>(nd.src[2].data), to_operand(nd.src[2]),
+                                                static_cast<float*>(nd.out.data), p);
+        }
         case VKHIP_OP_CROSS_ENTROPY:
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: {
             const bool back = nd.op == VKHIP_OP_CROSS_ENTROPY_BACKWARD;
@@ -829,7 +868,7 @@ extern "C" int vkhip_shutdown(void) {
     std::lock_guard<std::mutex> lk(vkhip::g_mu);
     vkhip::Context& c = ctx();
     if (!c.ready) return VKHIP_OK;
-    for (int slot = 0; slot < 2; ++slot) {
+    for (int slot = 0; slot < 3; ++slot) {
         if (c.ws[slot]) VKHIP_HIP(hipFreeAsync(c.ws[slot], c.stream));
         c.ws[slot] = nullptr;
         c.ws_bytes[slot] = 0;

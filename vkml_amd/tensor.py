@@ -864,6 +864,16 @@ FUSED_RELU_BACKWARD = True
 # pass. False keeps MAX_POOL2D_BACKWARD and RELU_BACKWARD.
 FUSED_POOL_RELU_GRAD = True
 
+# The weight and bias gradients of a conv layer (conv2d with bias, relu, then a
+# 2x2 stride-2 max-pool) whose input needs no gradient, as one
+# CONV2D_POOL_WEIGHT_BIAS_GRAD node over the image, the layer's output and the
+# pool's output gradient, in place of MAX_POOL2D_BACKWARD_RELU,
+# CONV2D_WEIGHT_GRAD_SUM and the bias's SUM: on the device the relu-masked pool
+# gradient is formed inside the weight-gradient kernel (never written) and the
+# bias gradient summed there in the pairwise tree's order; the nodes' values.
+# False keeps the three nodes.
+FUSED_CONV_POOL_GRAD = True
+
 # A relu gradient whose incoming gradient is a product (a Linear layer's input
 # gradient, grad @ w, feeding the relu before it) as one MATMUL_RELU_BACKWARD
 # node: the select applied where the product's split-K partials are folded.
@@ -1372,6 +1382,30 @@ def _conv2d_backward(node: Node, a: Node, b: Node, grad: Tensor, grads: dict) ->
         _accumulate(grads, b, dflat.reshape(b.shape))
 
 
+def _conv_pool_grads(node: Node, a: Node, b: Node, bias3: Node, dz: Tensor, grads: dict) -> bool:
+    """The weight and bias gradients of the CONV2D_BIAS_RELU `node` as one
+    CONV2D_POOL_WEIGHT_BIAS_GRAD node when dz is the MAX_POOL2D_BACKWARD_RELU
+    of a 2x2, stride-2 pool over the node's output, both gradients are wanted
+    and the image's is not (else dz is needed anyway): the weight gradient and
+    the bias gradient are views of its output. Returns whether it did."""
+    pn = dz.node
+    if not (FUSED_CONV_POOL_GRAD and FOLD_CONV_WEIGHT_GRAD and pn.op == OP["MAX_POOL2D_BACKWARD_RELU"]
+            and not pn.computed and b.requires_grad and bias3.requires_grad and not a.requires_grad):
+        return False
+    gp, y = pn.src
+    n_, cout, oh, ow = node.shape
+    if y is not node or pn.params != _unfold_params((2, 2), (2, 2), (0, 0), (1, 1), (oh, ow)):
+        return False
+    ck = _numel(b.shape[1:])
+    out = Tensor(Node(OP["CONV2D_POOL_WEIGHT_BIAS_GRAD"], (cout * ck + cout,), np.float32, a.backend,
+                      [a, y, Tensor(gp).contiguous().node], params=node.params))
+    dflat = _view(RESHAPE, out, (cout, ck), (ck, 1), 0)
+    dbias = _view(RESHAPE, out, (cout,), (1,), cout * ck)
+    _accumulate(grads, b, dflat.reshape(b.shape))
+    _accumulate(grads, bias3, dbias.reshape(bias3.shape))
+    return True
+
+
 def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
     op = node.op
     a = node.src[0] if node.src else None
@@ -1480,6 +1514,8 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         g = grad if grad.shape == out.shape else grad.broadcast_to(out.shape)
         dz = _relu_grad(node, node, g)
         bias3 = node.src[2]
+        if _conv_pool_grads(node, a, b, bias3, dz, grads):
+            return
         if bias3.requires_grad:
             _accumulate(grads, bias3, reduce_to_shape(dz, bias3.shape))
         if a.requires_grad or b.requires_grad:
@@ -1530,7 +1566,7 @@ REFERENCE_GRAPH_SWITCHES = {
     "IMPLICIT_CONV": False, "FUSED_CROSS_ENTROPY": False, "FUSED_RELU_BACKWARD": False,
     "FUSED_POOL_RELU_GRAD": False, "FUSED_MATMUL_RELU_GRAD": False, "FOLD_CONV_WEIGHT_GRAD": False,
     "FUSED_CONV_INPUT_GRAD": False, "FUSED_CONV_EPILOGUE": False, "FUSED_ADD_RELU": False,
-    "BACKWARD_FLUSH_EVERY": 0,
+    "FUSED_CONV_POOL_GRAD": False, "BACKWARD_FLUSH_EVERY": 0,
 }
 
 
