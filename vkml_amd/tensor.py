@@ -1134,11 +1134,11 @@ class CapturedStep:
         prefetch: the next call's host arrays. They are uploaded, once this
         step is queued, into device staging buffers on the backend's copy
         stream (vkhip_copy_from_host_async), so the host copy and the DMA of
-        batch i + 1 overlap step i on the device (and this call's read-back);
-        the next call given those same array objects copies them from the
-        staging buffers on the device instead of uploading them. The arrays
-        must not change in between (the host bytes are copied at once, so a
-        change would be ignored, not raced)."""
+        batch i + 1 overlap step i on the device, and copied on the device into
+        the recorded inputs right behind this step: the next call given those
+        same array objects replays at once (any other arrays are uploaded over
+        them, as usual). The host bytes are copied when this call returns, so
+        a later change to the arrays is not seen."""
         if self._program is None:
             raise RuntimeError("CapturedStep: closed")
         if not read:
@@ -1155,18 +1155,9 @@ class CapturedStep:
 
         staged = getattr(self, "_staged", None)
         self._staged = None
-        if staged is not None and (len(staged[0]) != len(arrays) or
-                                   any(a is not b for a, b in zip(arrays, staged[0]))):
-            staged = None  # prefetched arrays not the ones given: upload these
+        if staged is not None and len(staged) == len(arrays) and all(a is b for a, b in zip(arrays, staged)):
+            arrays = ()  # prefetched: already copied into the inputs, stream-ordered
         device_copies = []
-        if staged is not None:
-            k = staged[1]
-            _lib.check(self.lib.vkhip_stream_wait_event(ctypes.c_void_p(self._stage_ready[k].handle)),
-                       "stream_wait_event")
-            for t, buf in zip(self.inputs, self._stage_bufs[k]):
-                dst = t.node.storage.ptr + t.node.offset * t.node.itemsize
-                device_copies.append(_lib.Copy(dst, buf.ptr, buf.nbytes_dense()))
-            arrays = ()
         for t, a in zip(self.inputs, arrays):
             if isinstance(a, DeviceArray):
                 if a.shape != t.shape or a.dtype != t.dtype or not a.is_contiguous():
@@ -1183,8 +1174,6 @@ class CapturedStep:
         if device_copies:
             _lib.check(self.lib.vkhip_copy_device_to_device(
                 (_lib.Copy * len(device_copies))(*device_copies), len(device_copies)), "copy_device_to_device")
-        if staged is not None:
-            self._stage_free[staged[1]].record()  # the staging buffers may be refilled after this
         _lib.check(self.lib.vkhip_program_run(self._program, 1 if self.graph else 0), "program_run")
         if prefetch is not None:
             self.prefetch(*prefetch)
@@ -1196,12 +1185,13 @@ class CapturedStep:
         return None
 
     def prefetch(self, *arrays) -> None:
-        """Uploads host `arrays` (the next call's inputs) into the staging
-        buffer set that the latest call did not use, on the copy stream, ahead
-        of the work queued so far: the copy stream waits for that set's last
-        device copy out (its `free` event), then `ready` is recorded behind the
-        DMAs. The next call given these same array objects reads them from
-        there (see __call__)."""
+        """Uploads host `arrays` (the next call's inputs) into one of two
+        staging buffer sets on the copy stream, ahead of the work queued so
+        far (the copy stream waits only for that set's last device copy out,
+        its `free` event, and records `ready` behind the DMAs), then queues on
+        the backend stream, behind that work, the wait for `ready` and the
+        device copy into the recorded inputs. The next call given these same
+        array objects replays without uploading (see __call__)."""
         from .device import DeviceArray, Event
 
         if self._program is None:
@@ -1225,7 +1215,17 @@ class CapturedStep:
                 ctypes.c_void_p(buf.ptr), host.ctypes.data_as(ctypes.c_void_p), host.nbytes,
                 ctypes.c_void_p(self._stage_free[k].handle), ctypes.c_void_p(self._stage_ready[k].handle)),
                 "copy_from_host_async")
-        self._staged = (arrays, k)
+        # Behind the work queued so far (this step's replay included), the
+        # stream waits for the DMAs and copies the staged batch into the
+        # recorded inputs; the staging set is free again after that copy.
+        _lib.check(self.lib.vkhip_stream_wait_event(ctypes.c_void_p(self._stage_ready[k].handle)),
+                   "stream_wait_event")
+        copies = [_lib.Copy(t.node.storage.ptr + t.node.offset * t.node.itemsize, buf.ptr, buf.nbytes_dense())
+                  for t, buf in zip(self.inputs, self._stage_bufs[k])]
+        _lib.check(self.lib.vkhip_copy_device_to_device((_lib.Copy * len(copies))(*copies), len(copies)),
+                   "copy_device_to_device")
+        self._stage_free[k].record()
+        self._staged = arrays
 
     def outputs_now(self) -> list:
         """`fn`'s outputs of the latest replay, as host arrays (waits for it)."""
