@@ -987,10 +987,13 @@ def test_host_provided_stream(hip):
 
 def test_copy_device_to_device_batch(hip):
     """vkhip_copy_device_to_device: several disjoint copies as one unit of work,
-    16-byte multiples (the copy kernel) and odd sizes (the runtime's
-    copy), byte for byte; mismatched or strided pairs are refused on the host."""
+    16-byte multiples and odd sizes, batched up to eight pairs per launch
+    (twelve pairs here: two launches; 1001 floats is past the batch's 4 KB of
+    byte copies and goes alone, as do 64 MB and more), byte for byte;
+    mismatched or strided pairs are refused on the host."""
     rng = np.random.default_rng(SEED + 95)
-    srcs = [rng.standard_normal(n).astype(np.float32) for n in (4096, 1001, 37, 1 << 20)]
+    sizes = (4096, 1001, 37, 1 << 20, 1, 3, 256, 1023, 5, (16 << 20) + 4, 8, 12)
+    srcs = [rng.standard_normal(n).astype(np.float32) for n in sizes]
     src_d = [dev(x) for x in srcs]
     dst_d = [DeviceArray((x.size,), np.float32) for x in srcs]
     hip.copy_device_to_device(list(zip(dst_d, src_d)))

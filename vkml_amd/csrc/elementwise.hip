@@ -541,6 +541,73 @@ int launch_zero_f32(float* dst, uint64_t count) {
     return VKHIP_OK;
 }
 
+// Several disjoint copies in one launch (a training step's batch and labels):
+// workgroup w copies 256 units of the pair whose [block_start[i],
+// block_start[i+1]) range holds w; a unit is 16 bytes for a pair whose
+// addresses and size are 16-byte multiples, else one byte.
+constexpr int kCopyBatch = 8;
+struct CopyBatch {
+    const unsigned char* src[kCopyBatch];
+    unsigned char* dst[kCopyBatch];
+    uint64_t units[kCopyBatch];
+    uint32_t block_start[kCopyBatch + 1];
+    uint32_t vec;  // bit i: pair i copies 16-byte units
+    int n;
+};
+
+__global__ __launch_bounds__(256) void copy_batch_kernel(CopyBatch b) {
+    const uint32_t w = blockIdx.x;
+    int i = 0;
+    while (i + 1 < b.n && w >= b.block_start[i + 1]) ++i;
+    const uint64_t u = static_cast<uint64_t>(w - b.block_start[i]) * 256u + threadIdx.x;
+    if (u >= b.units[i]) return;
+    if ((b.vec >> i) & 1u)
+        reinterpret_cast<f32x4_t*>(b.dst[i])[u] = reinterpret_cast<const f32x4_t*>(b.src[i])[u];
+    else
+        b.dst[i][u] = b.src[i][u];
+}
+
+int launch_copy_bytes(void* dst, const void* src, size_t nbytes);
+
+// Copies the pairs: those of up to 64 MB (byte copies: 4 KB) in batches of
+// kCopyBatch per launch, any other alone.
+int launch_copy_pairs(const vkhip_copy* copies, size_t n) {
+    CopyBatch b{};
+    uint32_t blocks = 0;
+    auto flush = [&]() -> int {
+        if (b.n == 0) return VKHIP_OK;
+        b.block_start[b.n] = blocks;
+        hipLaunchKernelGGL(copy_batch_kernel, dim3(blocks), dim3(256), 0, ctx().stream, b);
+        VKHIP_LAUNCH_CHECK();
+        b = CopyBatch{};
+        blocks = 0;
+        return VKHIP_OK;
+    };
+    for (size_t k = 0; k < n; ++k) {
+        const vkhip_copy& c = copies[k];
+        if (c.nbytes == 0) continue;
+        const bool vec = reinterpret_cast<uintptr_t>(c.dst) % 16 == 0 && reinterpret_cast<uintptr_t>(c.src) % 16 == 0 &&
+                         c.nbytes % 16 == 0;
+        if (vec ? c.nbytes > (size_t{64} << 20) : c.nbytes > 4096) {
+            const int st = launch_copy_bytes(c.dst, c.src, c.nbytes);
+            if (st != VKHIP_OK) return st;
+            continue;
+        }
+        const uint64_t units = vec ? c.nbytes / 16 : c.nbytes;
+        b.src[b.n] = static_cast<const unsigned char*>(c.src);
+        b.dst[b.n] = static_cast<unsigned char*>(c.dst);
+        b.units[b.n] = units;
+        b.block_start[b.n] = blocks;
+        if (vec) b.vec |= 1u << b.n;
+        blocks += static_cast<uint32_t>((units + 255) / 256);
+        if (++b.n == kCopyBatch) {
+            const int st = flush();
+            if (st != VKHIP_OK) return st;
+        }
+    }
+    return flush();
+}
+
 int launch_copy_bytes(void* dst, const void* src, size_t nbytes) {
     if (nbytes == 0) return VKHIP_OK;
     hipStream_t st = ctx().stream;

@@ -41,6 +41,7 @@ int launch_softmax(const float* src, const vkhip_operand& d, float* dst, int axi
 int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst);
 int launch_elementwise(const vkhip_node& nd);
 int launch_copy_bytes(void* dst, const void* src, size_t nbytes);
+int launch_copy_pairs(const vkhip_copy* copies, size_t n);
 
 static thread_local char g_last_error[512] = "";
 
@@ -1155,11 +1156,7 @@ int compute_nodes(const vkhip_node* nodes, size_t n) {
 
 int copy_pairs(const vkhip_copy* copies, size_t n) {
     Unit unit("copy_device_to_device");
-    for (size_t i = 0; i < n; ++i) {
-        const int st = launch_copy_bytes(copies[i].dst, copies[i].src, copies[i].nbytes);
-        if (st != VKHIP_OK) return st;
-    }
-    return VKHIP_OK;
+    return launch_copy_pairs(copies, n);
 }
 }  // namespace vkhip
 
