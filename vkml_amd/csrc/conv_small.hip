@@ -702,55 +702,65 @@ __global__ __launch_bounds__(64 * NW) void win_wgrad_kernel(WinWgrad p) {
 // order (at most 32 per run). A workgroup takes 16 outputs.
 //
 // With bpart (the pool-gradient kernel's span sums, [parts][64], parts a power
-// of two >= 4), the last workgroup folds the bias gradient into bout[Cout]:
-// per channel the balanced pairwise tree over the span sums, as four runs of
-// parts / 4 consecutive sums (a binary-counter carry stack over each, which
-// for a power-of-two count is the balanced tree) and then (run 0 + run 1) +
-// (run 2 + run 3).
+// of two >= 4), the last four workgroups fold the bias gradient into
+// bout[Cout], 16 channels each: per channel the balanced pairwise tree over
+// the span sums, as R = min(16, parts) runs of parts / R consecutive sums (a
+// binary-counter carry stack over each, which for a power-of-two count is the
+// balanced tree), then the R run sums level by level.
 __global__ __launch_bounds__(256) void win_fold_kernel(const float* __restrict__ part, uint32_t parts,
                                                        float* __restrict__ out, uint32_t cout, uint32_t K,
                                                        const float* __restrict__ bpart, float* __restrict__ bout) {
     __shared__ float runs[16][17];
     const int tid = threadIdx.x, oi = tid & 15, run = tid >> 4;
-    if (bpart != nullptr && blockIdx.x == gridDim.x - 1) {
-        __shared__ float bruns[4][64];
-        const int co = tid & 63, br = tid >> 6;
-        const uint32_t per = parts / 4u;
-        float stack[8];
+    if (bpart != nullptr && blockIdx.x >= gridDim.x - 4) {
+        const uint32_t co = (blockIdx.x - (gridDim.x - 4)) * 16u + static_cast<uint32_t>(oi);
+        const uint32_t nr = parts < 16u ? parts : 16u, per = parts / nr;
+        float r = 0.0f;
+        if (static_cast<uint32_t>(run) < nr) {
+            float stack[6];
 #pragma unroll
-        for (int l = 0; l < 8; ++l) stack[l] = 0.0f;
-        for (uint32_t i0 = 0; i0 < per; i0 += 8) {
-            float v[8];
+            for (int l = 0; l < 6; ++l) stack[l] = 0.0f;
+            for (uint32_t i0 = 0; i0 < per; i0 += 8) {
+                float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                v[u] = i0 + u < per ? bpart[static_cast<uint64_t>(br * per + i0 + u) * 64u + co] : 0.0f;
+                for (int u = 0; u < 8; ++u)
+                    v[u] = i0 + u < per ? bpart[static_cast<uint64_t>(run * per + i0 + u) * 64u + co] : 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (i0 + u >= per) break;
-                const uint32_t count = i0 + u;
-                float b = v[u];
-                bool carry = true;
+                for (int u = 0; u < 8; ++u) {
+                    if (i0 + u >= per) break;
+                    const uint32_t count = i0 + u;
+                    float b = v[u];
+                    bool carry = true;
 #pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    if (carry) {
-                        if ((count >> l) & 1u) {
-                            b = stack[l] + b;
-                        } else {
-                            stack[l] = b;
-                            carry = false;
+                    for (int l = 0; l < 6; ++l) {
+                        if (carry) {
+                            if ((count >> l) & 1u) {
+                                b = stack[l] + b;
+                            } else {
+                                stack[l] = b;
+                                carry = false;
+                            }
                         }
                     }
                 }
             }
-        }
-        float r = 0.0f;
 #pragma unroll
-        for (int l = 0; l < 8; ++l)
-            if (per == (1u << l)) r = stack[l];
-        bruns[br][co] = r;
+            for (int l = 0; l < 6; ++l)
+                if (per == (1u << l)) r = stack[l];
+        }
+        runs[run][oi] = r;
         __syncthreads();
-        if (tid < 64 && static_cast<uint32_t>(tid) < cout)
-            bout[tid] = (bruns[0][tid] + bruns[1][tid]) + (bruns[2][tid] + bruns[3][tid]);
+        if (tid < 16) {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = runs[i][tid];
+#pragma unroll
+            for (int w = 1; w < 16; w *= 2)
+#pragma unroll
+                for (int i = 0; i + w < 16; i += 2 * w)
+                    if (static_cast<uint32_t>(i + w) < nr) v[i] = v[i] + v[i + w];
+            if (co < cout) bout[co] = v[0];
+        }
         return;
     }
     const uint32_t o = blockIdx.x * 16u + oi;
@@ -960,7 +970,7 @@ static int win_weight_grad_launch(const float* x, const vkhip_operand& xd, const
 #undef VKHIP_WGR_CH
 #undef VKHIP_WGR
     VKHIP_LAUNCH_CHECK();
-    const uint32_t fold_wgs = (two ? 128u : 64u) + (pool ? 1u : 0u);
+    const uint32_t fold_wgs = (two ? 128u : 64u) + (pool ? 4u : 0u);
     hipLaunchKernelGGL(win_fold_kernel, dim3(fold_wgs), dim3(256), 0, ctx().stream, p.part, p.nwg, out, cout, ck,
                        pool ? p.bpart : nullptr, pool ? pool->bias_out : nullptr);
     VKHIP_LAUNCH_CHECK();
