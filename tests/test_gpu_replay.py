@@ -184,6 +184,34 @@ def test_prefetched_uploads_are_the_plain_uploads(config, graph):
     assert runs[2] == runs[0]
 
 
+def test_constant_nodes_replay_only_while_nothing_else_writes_them():
+    """A recorded constant (FULL) that no other recorded call writes keeps its
+    recorded value and is left out of replays; one that another call
+    overwrites (here a device copy into it) is recomputed every replay, so
+    every replay sees the constant again."""
+    dev = T.default_backend()
+    x0 = np.arange(8, dtype=np.float32)
+
+    def kept(x):
+        return x + T.full((8,), 3.0, backend=dev)
+
+    def overwritten(x):
+        c = T.full((8,), 3.0, backend=dev)
+        y = x + c
+        T.realize([y])
+        T.assign([c], [y])  # c's buffer now holds x + 3
+        return y
+
+    for fn in (kept, overwritten):
+        step = T.CapturedStep(fn, x0)
+        assert step.first[0].tobytes() == (x0 + 3).tobytes()
+        for i in range(1, 4):
+            x = x0 * i
+            got = step(x)[0]
+            assert got.tobytes() == (x + np.float32(3)).tobytes(), (fn.__name__, i)
+        step.close()
+
+
 def test_captured_step_checks_its_inputs():
     dev = T.default_backend()
     model = _mlp(dev)

@@ -145,11 +145,75 @@ extern "C" int vkhip_program_begin(void) {
     return VKHIP_OK;
 }
 
+namespace vkhip {
+namespace {
+
+// Bytes [lo, hi) a tensor's elements occupy (strides may be negative or 0).
+struct Span {
+    uintptr_t lo, hi;
+};
+
+Span tensor_span(const vkhip_tensor& t) {
+    const int64_t item = t.dtype == VKHIP_I64 ? 8 : t.dtype == VKHIP_BOOL ? 1 : t.dtype == VKHIP_F16 ? 2 : 4;
+    int64_t lo = 0, hi = 0;
+    for (int i = 0; i < t.ndim; ++i) {
+        if (t.ne[i] <= 0) return {0, 0};
+        const int64_t reach = (t.ne[i] - 1) * t.nb[i];
+        if (reach < 0) lo += reach; else hi += reach;
+    }
+    const uintptr_t base = reinterpret_cast<uintptr_t>(t.data);
+    return {base + static_cast<uintptr_t>(lo * item), base + static_cast<uintptr_t>((hi + 1) * item)};
+}
+
+bool overlaps(const Span& a, const Span& b) { return a.lo < b.hi && b.lo < a.hi; }
+
+// Constant nodes (FULL, ARANGE: no sources, the value in their params) whose
+// output no other recorded call writes keep the value the recording wrote,
+// since a program holds every buffer it touches: replays leave them out (the
+// seed and 1/count of a mean's gradient, say, one launch per step).
+void drop_constant_nodes(vkhip_program& p) {
+    std::vector<Span> writes;
+    std::vector<size_t> own;  // per node, in call order: its output's index in writes
+    for (const vkhip_program::Call& c : p.calls) {
+        for (const vkhip_node& nd : c.nodes) {
+            own.push_back(writes.size());
+            writes.push_back(tensor_span(nd.out));
+        }
+        for (const vkhip_sgd_param& sp : c.sgd) {
+            const uintptr_t pa = reinterpret_cast<uintptr_t>(sp.param), va = reinterpret_cast<uintptr_t>(sp.velocity);
+            writes.push_back({pa, pa + sp.n * sizeof(float)});
+            if (sp.velocity) writes.push_back({va, va + sp.n * sizeof(float)});
+        }
+        for (const vkhip_copy& cp : c.copies) {
+            const uintptr_t d = reinterpret_cast<uintptr_t>(cp.dst);
+            writes.push_back({d, d + cp.nbytes});
+        }
+    }
+    size_t k = 0;
+    for (vkhip_program::Call& c : p.calls) {
+        std::vector<vkhip_node> kept;
+        for (const vkhip_node& nd : c.nodes) {
+            const size_t mine = own[k++];
+            bool constant = (nd.op == VKHIP_OP_FULL || nd.op == VKHIP_OP_ARANGE) && nd.n_src == 0;
+            const Span s = writes[mine];
+            for (size_t w = 0; constant && w < writes.size(); ++w)
+                if (w != mine && overlaps(s, writes[w])) constant = false;
+            if (!constant) kept.push_back(nd);
+        }
+        p.node_count -= c.nodes.size() - kept.size();
+        c.nodes.swap(kept);
+    }
+}
+
+}  // namespace
+}  // namespace vkhip
+
 extern "C" int vkhip_program_end(vkhip_program** out) {
     if (!out) return fail(VKHIP_ERR_INVALID, "program_end: null output");
     std::lock_guard<std::mutex> lk(vkhip::g_prog_mu);
     *out = nullptr;
     if (!vkhip::g_recording) return fail(VKHIP_ERR_INVALID, "program_end: not recording");
+    vkhip::drop_constant_nodes(*vkhip::g_recording);
     *out = vkhip::g_recording;
     vkhip::g_recording = nullptr;
     return VKHIP_OK;
