@@ -621,7 +621,9 @@ def training_steps(only: int | None = None, modes=TRAIN_MODES):
       eager         the host core's rewritten graph, built every step
       replay        the step recorded once, its calls replayed from C; each
                     call uploads the next batch on the copy stream while its
-                    step runs (CapturedStep prefetch), and reads its loss back
+                    step runs (CapturedStep prefetch; the stream's batches in
+                    pinned host memory, which the DMA reads in place), and
+                    reads its loss back
       graph         the replay captured once into a HIP graph
       graph_queued  "graph" with no per-step loss read-back: the host queues
                     step after step, the last loss is read inside the timed
@@ -648,7 +650,7 @@ def training_steps(only: int | None = None, modes=TRAIN_MODES):
     valid builds of the reference's own CPU arithmetic separate."""
     from vkml_amd import nn, optim
     from vkml_amd import tensor as T
-    from vkml_amd.device import DeviceArray
+    from vkml_amd.device import DeviceArray, pinned_copy
 
     S = _streams()
     hip = T.default_backend().hip
@@ -659,6 +661,7 @@ def training_steps(only: int | None = None, modes=TRAIN_MODES):
         data = list(S.batches(cfg))
         want = S.oracle_losses(cfg)
         envelope, env_step = S.max_drift(want, S.oracle_losses(cfg, libm=True))
+        pinned = None
         entry = {"steps": cfg.steps, "timed_steps": cfg.steps - 1, "stream": "tests/golden/streams.py",
                  "oracle_fixture": S.fixture_path(cfg).name,
                  "oracle_libm_drift": envelope, "oracle_libm_drift_step": env_step}
@@ -692,7 +695,11 @@ def training_steps(only: int | None = None, modes=TRAIN_MODES):
                     captured = T.CapturedStep(fn, *data[0], graph=mode.startswith("graph"))
                     losses.append(float(captured.first[0]))
                     queued = mode == "graph_queued"
-                    feed = data
+                    # host-fed modes read their batches from pinned host memory, as a
+                    # data loader with pinned buffers fills them (the DMA reads them in place)
+                    if pinned is None:
+                        pinned = [(pinned_copy(x), pinned_copy(y)) for x, y in data]
+                    feed = pinned
                     if mode.startswith("resident"):
                         feed = [(DeviceArray.from_numpy(x), DeviceArray.from_numpy(y)) for x, y in data]
                     if mode == "resident_queued":

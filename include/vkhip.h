@@ -304,6 +304,11 @@ int vkhip_memory_stats(size_t* bytes_in_use, size_t* bytes_cached);
  * caller may reuse host_src at once (backend.h copy_from_host). */
 int vkhip_copy_from_host(void* dst, const void* host_src, size_t nbytes);
 int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes); /* synchronises */
+/* Pinned host memory (no counterpart in the reference, whose uploads stage
+ * through its own buffers): for a data loader that fills its batches where
+ * the DMA can read them. vkhip_host_free waits for the device first. */
+int vkhip_host_alloc(size_t nbytes, void** out_ptr);
+int vkhip_host_free(void* ptr);
 /* An upload queued ahead of the stream's work. No counterpart in the
  * reference (its uploads are ordered with its compute queue, backend.h
  * copy_from_host); for a training loop that uploads batch i + 1 while the
@@ -311,7 +316,9 @@ int vkhip_copy_to_host(void* host_dst, const void* src, size_t nbytes); /* synch
  * design leaves out (docs/adr/0012-asynchronous-submission.md:223-224), on
  * a HIP stream and events instead of semaphores. The bytes go through the
  * pinned staging slots (at most 32 MB) and return to the caller as
- * vkhip_copy_from_host's do; their DMAs run on a second stream that first
+ * vkhip_copy_from_host's do -- except bytes inside a vkhip_host_alloc block,
+ * which the DMA reads in place: the caller keeps them unchanged until `done`
+ * has completed. The DMAs run on a second stream that first
  * waits for `after` (an event recorded on the backend stream once it no
  * longer reads dst; null: no wait), and `done` is recorded behind them.
  * The backend stream must wait for `done` (vkhip_stream_wait_event) before it

@@ -145,13 +145,16 @@ def test_prefetched_uploads_are_the_plain_uploads(config, graph):
     its own step runs gives the losses and parameters of calls that upload
     their own batch: read back every step, queued (read=False), and with a
     prefetch the next call does not use (other array objects: they are
-    uploaded instead). The host arrays are overwritten right after each
-    prefetch: the bytes were copied when the call returned."""
+    uploaded instead), and from pinned host arrays (vkhip_host_alloc), which the
+    DMA reads in place. The pageable host arrays are overwritten right after
+    each prefetch: their bytes were copied when the call returned."""
     dev = T.default_backend()
     make, _, _, _, lr = CONFIGS[config]
     batches = _batches(config, 9)
     runs = []
-    for variant in ("plain", "prefetch", "prefetch_queued"):
+    from vkml_amd.device import pinned_copy
+
+    for variant in ("plain", "prefetch", "prefetch_queued", "prefetch_pinned"):
         model = make(dev)
         opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
         step = T.CapturedStep(_step_fn(model, opt), *batches[0], graph=graph)
@@ -160,7 +163,9 @@ def test_prefetched_uploads_are_the_plain_uploads(config, graph):
             losses += [np.float32(step(x, y)[0]) for x, y in batches[1:]]
         else:
             queued = variant == "prefetch_queued"
-            feed = [(x.copy(), y.copy()) for x, y in batches]
+            pinned = variant == "prefetch_pinned"
+            # pinned batches are read by the DMA in place (no scribbling there)
+            feed = [(pinned_copy(x), pinned_copy(y)) if pinned else (x.copy(), y.copy()) for x, y in batches]
             step.prefetch(*feed[1])
             for i in range(1, len(feed)):
                 x, y = feed[i]
@@ -168,10 +173,9 @@ def test_prefetched_uploads_are_the_plain_uploads(config, graph):
                     x, y = batches[i][0].copy(), batches[i][1].copy()
                 nxt = feed[i + 1] if i + 1 < len(feed) else None
                 out = step(x, y, read=not queued, prefetch=nxt)
-                if nxt is not None:  # scribble over the host bytes just staged
+                if nxt is not None and not pinned:  # scribble over the host bytes just staged
                     nxt[0][...] = 7.0
                     nxt[1][...] = 0
-                    feed[i + 1] = nxt
                 if queued:
                     assert out is None
                     losses.append(np.float32(step.outputs_now()[0]))
@@ -182,6 +186,7 @@ def test_prefetched_uploads_are_the_plain_uploads(config, graph):
         step.close()
     assert runs[1] == runs[0]
     assert runs[2] == runs[0]
+    assert runs[3] == runs[0]
 
 
 def test_constant_nodes_replay_only_while_nothing_else_writes_them():

@@ -122,6 +122,8 @@ SIGNATURES = {
                                    POINTER(c_uint64)]),
     "vkhip_copy_from_host": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vkhip_copy_from_host_async": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "vkhip_host_alloc": (c_int, [c_size_t, POINTER(c_void_p)]),
+    "vkhip_host_free": (c_int, [c_void_p]),
     "vkhip_stream_wait_event": (c_int, [c_void_p]),
     "vkhip_copy_to_host": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vkhip_copy_device_to_device": (c_int, [POINTER(Copy), c_size_t]),

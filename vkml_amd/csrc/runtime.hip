@@ -9,6 +9,7 @@
 // vulkan_backend.cpp:921-984; hipFreeAsync gives that ordering directly).
 #include <algorithm>
 #include <cstring>
+#include <map>
 #include <mutex>
 
 #include "common.h"
@@ -1058,6 +1059,55 @@ extern "C" int vkhip_copy_from_host(void* dst, const void* host_src, size_t nbyt
     return VKHIP_OK;
 }
 
+// Pinned host buffers handed out by vkhip_host_alloc: an upload ahead of the
+// stream from inside one is DMA'd from there, without the staging copy.
+namespace vkhip {
+static std::mutex g_host_mu;
+static std::map<uintptr_t, size_t> g_host_blocks;  // start -> bytes
+
+static bool in_host_block(const void* p, size_t nbytes) {
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    auto it = g_host_blocks.upper_bound(a);
+    if (it == g_host_blocks.begin()) return false;
+    --it;
+    return a >= it->first && a + nbytes <= it->first + it->second;
+}
+}  // namespace vkhip
+
+extern "C" int vkhip_host_alloc(size_t nbytes, void** out) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!out) return fail(VKHIP_ERR_INVALID, "host_alloc: null output");
+    *out = nullptr;
+    if (nbytes == 0) return VKHIP_OK;
+    void* p = nullptr;
+    if (hipHostMalloc(&p, nbytes, hipHostMallocDefault) != hipSuccess || !p)
+        return fail(VKHIP_ERR_OOM, "host_alloc: %zu bytes of pinned host memory could not be allocated", nbytes);
+    std::lock_guard<std::mutex> lk(vkhip::g_host_mu);
+    vkhip::g_host_blocks[reinterpret_cast<uintptr_t>(p)] = nbytes;
+    *out = p;
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_host_free(void* p) {
+    if (!p) return VKHIP_OK;
+    {
+        std::lock_guard<std::mutex> lk(vkhip::g_host_mu);
+        auto it = vkhip::g_host_blocks.find(reinterpret_cast<uintptr_t>(p));
+        if (it == vkhip::g_host_blocks.end())
+            return fail(VKHIP_ERR_INVALID, "host_free: %p was not handed out by vkhip_host_alloc", p);
+        vkhip::g_host_blocks.erase(it);
+    }
+    // a DMA may still read it: free only once the device is done
+    if (ctx().ready) {
+        VKHIP_HIP(hipStreamSynchronize(ctx().stream));
+        if (ctx().copy_stream) VKHIP_HIP(hipStreamSynchronize(ctx().copy_stream));
+    }
+    VKHIP_HIP(hipHostFree(p));
+    return VKHIP_OK;
+}
+
 // Uploads ahead of the stream: the same pinned slots, the DMAs on a second
 // stream that waits only for `after` (the event the stream recorded once it no
 // longer reads dst), so a training loop copies batch i + 1 on the host and over
@@ -1075,6 +1125,12 @@ extern "C" int vkhip_copy_from_host_async(void* dst, const void* host_src, size_
     vkhip::Context& c = ctx();
     if (!c.copy_stream) VKHIP_HIP(hipStreamCreateWithFlags(&c.copy_stream, hipStreamNonBlocking));
     if (after) VKHIP_HIP(hipStreamWaitEvent(c.copy_stream, static_cast<hipEvent_t>(after), 0));
+    if (nbytes && vkhip::in_host_block(host_src, nbytes)) {
+        // pinned by vkhip_host_alloc: the DMA reads the caller's bytes
+        VKHIP_HIP(hipMemcpyAsync(dst, host_src, nbytes, hipMemcpyHostToDevice, c.copy_stream));
+        VKHIP_HIP(hipEventRecord(static_cast<hipEvent_t>(done), c.copy_stream));
+        return VKHIP_OK;
+    }
     std::lock_guard<std::mutex> lk(vkhip::g_stage_mu);
     for (size_t off = 0; off < nbytes; off += vkhip::kStageSlotBytes) {
         const size_t chunk = std::min(vkhip::kStageSlotBytes, nbytes - off);

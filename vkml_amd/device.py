@@ -68,6 +68,53 @@ def _free(ptr: int) -> None:
         b.lib.vkhip_free(ptr)
 
 
+class PinnedArray(np.ndarray):
+    """A host array in pinned memory (vkhip_host_alloc), for batches that a
+    data loader fills where the DMA reads them: an upload ahead of the stream
+    (vkhip_copy_from_host_async, CapturedStep.prefetch) reads it in place
+    instead of copying it into a staging slot first. Keep its values
+    unchanged until the step that consumes the upload has run."""
+
+    _block = None
+
+
+class _HostBlock:
+    __slots__ = ("ptr", "__weakref__")
+
+    def __init__(self, nbytes: int):
+        p = c_void_p()
+        check(backend().lib.vkhip_host_alloc(max(int(nbytes), 1), byref(p)), "host_alloc")
+        self.ptr = p.value or 0
+
+    def __del__(self):
+        b = _BACKEND
+        if self.ptr and b is not None and b.alive:
+            try:
+                b.lib.vkhip_host_free(c_void_p(self.ptr))
+            except Exception:  # interpreter teardown
+                pass
+        self.ptr = 0
+
+
+def pinned_empty(shape, dtype=np.float32) -> PinnedArray:
+    """An uninitialised PinnedArray of `shape` and `dtype`."""
+    dt = np.dtype(dtype)
+    count = int(np.prod(shape)) if len(tuple(shape)) else 1
+    block = _HostBlock(count * dt.itemsize)
+    raw = (ctypes.c_uint8 * max(count * dt.itemsize, 1)).from_address(block.ptr)
+    arr = np.frombuffer(raw, dtype=dt, count=count).reshape(shape).view(PinnedArray)
+    arr._block = block
+    return arr
+
+
+def pinned_copy(a) -> PinnedArray:
+    """A PinnedArray holding a copy of `a`."""
+    a = np.asarray(a)
+    out = pinned_empty(a.shape, a.dtype)
+    out[...] = a
+    return out
+
+
 class DeviceArray:
     """A strided view over a Buffer: extents, element strides, dtype, offset."""
 
