@@ -771,6 +771,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const uint32_t col = col0 + wn0 + 32 * j + lrow;
+            // every epilogue load (a mask) before the first store: the
+            // compiler cannot tell the output from the mask, and interleaved
+            // it waits out one load round trip per store
+            float vo[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t row = row0 + wm0 + 32 * i + 8 * (r / 4) + 4 * kh + (r % 4);
@@ -779,14 +783,19 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g, Im2colB im_i
                     if (g.bias) v = v + bias_rows[row - row0];
                     if (g.relu) v = v <= 0.0f ? 0.0f : v;
                 }
+                vo[r] = row < g.m && col < g.n ? product_epilogue(g, z, row, col, v) : v;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = row0 + wm0 + 32 * i + 8 * (r / 4) + 4 * kh + (r % 4);
                 if (row < g.m && col < g.n) {
                     float* at = cbase + static_cast<uint64_t>(row) * g.n + col;
                     // convolution outputs stream past the L2 (non-temporal):
                     // they are read next by another kernel, not by this one
                     if constexpr (BMODE == IMG)
-                        __builtin_nontemporal_store(product_epilogue(g, z, row, col, v), at);
+                        __builtin_nontemporal_store(vo[r], at);
                     else
-                        *at = product_epilogue(g, z, row, col, v);
+                        *at = vo[r];
                 }
             }
         }
@@ -994,17 +1003,23 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void gemm_nn_direct_kernel(GemmAr
     // (N is a multiple of four, so they are in or out together).
     const uint32_t col = col0 + NS * lrow;
     if (col < g.n) {
+        // the epilogue's loads (a mask) before the first store (see
+        // gemm_mfma_kernel)
+        BV vo[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
-            if (row < g.m) {
-                BV v;
 #pragma unroll
-                for (int s = 0; s < NS; ++s) v[s] = product_epilogue(g, z, row, col + s, acc[s][r]);
-                // streamed past the L2 (non-temporal): outputs and split-K
-                // partials are read by later kernels, never by this one
-                __builtin_nontemporal_store(v, reinterpret_cast<BV*>(cbase + static_cast<uint64_t>(row) * g.n + col));
-            }
+            for (int s = 0; s < NS; ++s)
+                vo[r][s] = row < g.m ? product_epilogue(g, z, row, col + s, acc[s][r]) : acc[s][r];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
+            // streamed past the L2 (non-temporal): outputs and split-K
+            // partials are read by later kernels, never by this one
+            if (row < g.m)
+                __builtin_nontemporal_store(vo[r], reinterpret_cast<BV*>(cbase + static_cast<uint64_t>(row) * g.n + col));
         }
     }
 }
@@ -1354,10 +1369,18 @@ __global__ __launch_bounds__(256) void gemm_direct64_kernel(GemmArgs g) {
     // column 2*(l%32) + s0 of the tile.
     const uint32_t col = col0 + 2 * lrow + s0;
     if (col < g.n) {
+        // the epilogue's loads (a mask) before the first store (see
+        // gemm_mfma_kernel)
+        float vo[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
-            if (row < g.m) cbase[static_cast<uint64_t>(row) * g.n + col] = product_epilogue(g, z, row, col, acc[r]);
+            vo[r] = row < g.m ? product_epilogue(g, z, row, col, acc[r]) : acc[r];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
+            if (row < g.m) cbase[static_cast<uint64_t>(row) * g.n + col] = vo[r];
         }
     }
 }
@@ -1746,6 +1769,7 @@ __global__ __launch_bounds__(512) void gemm_pair64_kernel(GemmArgs g, FoldEpilog
     // column 2*(l%32) + s0 of the tile.
     const uint32_t col = col0 + 2 * lrow + s0;
     float* cz = g.c + static_cast<uint64_t>(z) * g.m * g.n;
+    float vo[16];  // every epilogue load (a mask) before the first store
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         float stack[kSplitLevels];
@@ -1758,10 +1782,14 @@ __global__ __launch_bounds__(512) void gemm_pair64_kernel(GemmArgs g, FoldEpilog
         for (int lv = 0; lv < kSplitLevels; ++lv)
             if ((2u >> lv) & 1u) total = total + stack[lv];
         const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
-        if (row < g.m && col < g.n) {
-            const uint64_t i = (static_cast<uint64_t>(z) * g.m + row) * g.n + col;
-            cz[static_cast<uint64_t>(row) * g.n + col] = apply_epilogue(epi, i, total);
-        }
+        vo[r] = row < g.m && col < g.n
+                    ? apply_epilogue(epi, (static_cast<uint64_t>(z) * g.m + row) * g.n + col, total)
+                    : total;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t row = row0 + wm0 + 8 * (r / 4) + 4 * kh + (r % 4);
+        if (row < g.m && col < g.n) cz[static_cast<uint64_t>(row) * g.n + col] = vo[r];
     }
 }
 
