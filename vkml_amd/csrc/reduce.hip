@@ -295,7 +295,9 @@ __device__ __forceinline__ void wave_pair(float& m, float& s) {
     pair_combine(m, s, m1, s1);
 }
 
-template <int E4, bool LOG>
+// FULL: the row fills every thread's E elements (n == 4 * E4 * 1024): no
+// per-element bounds (about a tenth of the kernel's VALU instructions).
+template <int E4, bool LOG, bool FULL>
 __global__ __launch_bounds__(1024) void softmax_online_rows_kernel(const float* __restrict__ src,
                                                                    int64_t in_stride,
                                                                    float* __restrict__ dst,
@@ -305,11 +307,15 @@ __global__ __launch_bounds__(1024) void softmax_online_rows_kernel(const float* 
     const int t = threadIdx.x;
     const uint32_t row = blockIdx.x;
     const float* rs = src + static_cast<int64_t>(row) * in_stride;
+    if constexpr (FULL) n = 4u * E4 * T;
     float x[E];
-    load_row<T, E4>(x, rs, n, t, true, 1);
+    if constexpr (FULL)
+        load_row_full<T, E4>(x, rs, t);
+    else
+        load_row<T, E4>(x, rs, n, t, true, 1);
     bool keep[E];
 #pragma unroll
-    for (int i = 0; i < E; ++i) keep[i] = elem_of(1, T, t, i) < n;
+    for (int i = 0; i < E; ++i) keep[i] = FULL || elem_of(1, T, t, i) < n;
     const float mt = tree_peak<E>(x, keep);
     const float mref = mt == -__builtin_inff() ? 0.0f : mt;  // an all -inf share sums to 0
     float e[E];
@@ -1407,7 +1413,9 @@ static int launch_softmax_rows(const float* src, int64_t stride, float* dst, uin
     constexpr int RPB = Rows<T>::kPerBlock;
     if constexpr (T == 1024) {
         if (vec) {  // one (peak, sum) reduction per row
-            auto fo = log_mode ? softmax_online_rows_kernel<E4, true> : softmax_online_rows_kernel<E4, false>;
+            const bool full = n == 4u * E4 * 1024u;
+            auto fo = log_mode ? (full ? softmax_online_rows_kernel<E4, true, true> : softmax_online_rows_kernel<E4, true, false>)
+                               : (full ? softmax_online_rows_kernel<E4, false, true> : softmax_online_rows_kernel<E4, false, false>);
             hipLaunchKernelGGL(fo, dim3(rows), dim3(1024), 0, st, src, stride, dst, rows, n);
             VKHIP_LAUNCH_CHECK();
             return VKHIP_OK;
