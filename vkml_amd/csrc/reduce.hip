@@ -162,8 +162,11 @@ __device__ __forceinline__ uint32_t elem_of(int vec, int T, int t, int i) {
 // 2^(t + r) = 2^t (1 + r ln 2) to within (r ln 2)^2 / 2 < 2^-41 for |r| < 2^-20.
 // The result is within about 2 ulp of exp(s) (against ~1 for the general expf,
 // in a third of the instructions: the softmax kernels are instruction-bound at
-// 32768-wide rows). Shifts below -150 (and -inf) give 0; the general expf keeps
-// subnormal results down to -103.97, a difference of less than 2^-126.
+// 32768-wide rows). Shifts below -150 give 0 (2^t rounds to 0 there); the
+// general expf keeps subnormal results down to -103.97, a difference of less
+// than 2^-126. s = -inf: 2^t = 0 and r is NaN, which the maximum with -1 (an
+// IEEE maxNum: the non-NaN operand) replaces, so the result is +0; for any
+// finite s, |r ln 2| < 2^-20 and the maximum leaves it as it is.
 __device__ __forceinline__ float softmax_exp(float s) {
     constexpr float kL2eHi = 1.44269502162933349609375f;
     constexpr float kL2eLo = 1.925963033500011e-08f;
@@ -171,8 +174,7 @@ __device__ __forceinline__ float softmax_exp(float s) {
     const float t = s * kL2eHi;
     const float r = __builtin_fmaf(s, kL2eLo, __builtin_fmaf(s, kL2eHi, -t));
     const float e = __builtin_amdgcn_exp2f(t);
-    const float v = __builtin_fmaf(e, r * kLn2, e);
-    return t < -150.0f ? 0.0f : v;
+    return __builtin_fmaf(e, __builtin_fmaxf(r * kLn2, -1.0f), e);
 }
 
 // ---- softmax over contiguous rows ------------------------------------------------
