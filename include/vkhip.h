@@ -206,7 +206,16 @@ enum vkhip_op {
      * pool's adjoint). FAST numerics where the small-window kernel takes the
      * layer form dz in the kernel without writing it: the replaced nodes'
      * fast-path bits; otherwise those nodes in turn. */
-    VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD = 108
+    VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD = 108,
+    /* MAX_POOL2D_BACKWARD_RELU of 2x2 windows at stride 2 with the bias
+     * gradient of the conv layer whose relu output the pool read: src0 g
+     * [N,C,H/2,W/2], src1 y [N,C,H,W] (both contiguous), params the pool's
+     * vkhip_unfold (2x2, stride 2, no padding) -> out [N*C*H*W + C]
+     * contiguous: the pool gradient dz (105's values) then SUM(dz, axes 0, 2,
+     * 3), the broadcast adjoint of the layer's bias (autograd.cpp:84-116), in
+     * the pairwise tree's order; one pass over dz where the planes allow it
+     * (rows of 16 or 32, power-of-two extents). */
+    VKHIP_OP_MAX_POOL2D_BACKWARD_RELU_BIAS = 109
 };
 
 /* ---- a tensor as a node sees it (vkml::Node shape + storage) ------------ */

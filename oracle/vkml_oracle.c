@@ -799,6 +799,25 @@ int or_compute(const vkhip_node* nodes, size_t count, int threads) {
                 if (st != VKHIP_OK) return st;
                 break;
             }
+            case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU_BIAS: {
+                /* The nodes it stands for: dz = MAX_POOL2D_BACKWARD_RELU (2x2
+                 * windows at stride 2), then the bias gradient, dz summed
+                 * over N, H, W (the broadcast adjoint, autograd.cpp:84-116). */
+                vkhip_unfold p;
+                memcpy(&p, nd->params, sizeof p);
+                const vkhip_tensor* y = &nd->src[1];
+                const int64_t N = y->ne[0], C = y->ne[1], plane = y->ne[2] * y->ne[3];
+                float* out = (float*)o->data;
+                or_max_pool2d_backward((const float*)nd->src[0].data, (const float*)y->data, out, (uint32_t)(N * C),
+                                       (uint32_t)nd->src[0].ne[2], (uint32_t)nd->src[0].ne[3], &p, threads);
+                const float* yv = (const float*)y->data;
+                for (int64_t i = 0; i < N * C * plane; ++i)
+                    if (compare_f(VKHIP_OP_LESS_EQUAL, yv[i], 0.0f)) out[i] = 0.0f;
+                vkhip_operand rd = {{(uint32_t)N, (uint32_t)C, (uint32_t)y->ne[2], (uint32_t)y->ne[3]},
+                                    {C * plane, plane, y->ne[3], 1}};
+                or_reduce(VKHIP_REDUCE_SUM, out, &rd, 0xDu, out + N * C * plane, threads);
+                break;
+            }
             case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: {
                 /* The nodes it stands for, in turn: dz = the pool's adjoint
                  * over y (2x2 windows, stride 2) masked by the relu

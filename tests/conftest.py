@@ -195,6 +195,32 @@ def conv_pool_loss_and_grads(backend, x, w, bias, fused):
         T.FUSED_CONV_POOL_GRAD = prev
 
 
+def pool_bias_loss_and_grads(backend, x, w, bias, fused):
+    """sum(max_pool2d(relu(conv2d(x, w, bias, pad 1)), 2) * probe) with x
+    needing its gradient: the x, weight and bias gradients, the bias's built as
+    one MAX_POOL2D_BACKWARD_RELU_BIAS node with the pool gradient (fused) or as
+    MAX_POOL2D_BACKWARD_RELU and SUM."""
+    from vkml_amd import tensor as T
+
+    prev = T.FUSED_POOL_BIAS_GRAD
+    T.FUSED_POOL_BIAS_GRAD = fused
+    try:
+        xt = T.tensor(x, requires_grad=True, backend=backend)
+        wt = T.tensor(w, requires_grad=True, backend=backend)
+        bt = T.tensor(bias, requires_grad=True, backend=backend)
+        out = T.max_pool2d(T.relu(T.conv2d(xt, wt, bt, 1, 1, 1)), 2)
+        probe = np.linspace(-1.0, 1.0, int(np.prod(out.shape)), dtype=np.float32)
+        loss = T.sum(out * T.tensor(probe.reshape(out.shape), backend=backend))
+        loss.backward()
+        src = bt.grad.node
+        while src.view_src is not None:
+            src = src.view_src
+        assert (src.op == T.OP["MAX_POOL2D_BACKWARD_RELU_BIAS"]) == fused
+        return out.numpy(), xt.grad.numpy(), wt.grad.numpy(), bt.grad.numpy()
+    finally:
+        T.FUSED_POOL_BIAS_GRAD = prev
+
+
 def conv_pool_node(backend, x, y, gp, kernel, pad):
     """The CONV2D_POOL_WEIGHT_BIAS_GRAD node alone over given x, y and gp
     (unit stride and dilation): its [Cout*C*kh*kw + Cout] output."""
@@ -290,7 +316,7 @@ def pool_relu_input(shape, seed):
 GRAPH_REWRITES = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU",
                   "FUSED_CONV_EPILOGUE", "FUSED_CONV_INPUT_GRAD", "FOLD_CONV_WEIGHT_GRAD",
                   "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD",
-                  "FUSED_CONV_POOL_GRAD")
+                  "FUSED_CONV_POOL_GRAD", "FUSED_POOL_BIAS_GRAD")
 
 
 def train_with_rewrites(backend, model_fn, batches, enabled, lr=0.1, momentum=0.9,

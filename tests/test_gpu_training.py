@@ -17,7 +17,7 @@ from conftest import (CONV_GEOMETRIES, SEED, small_window, ce_inputs, ce_loss_an
                       conv_relu_loss_and_grads, gemm_tolerance, mlp_batches, mlp_model, train_with_rewrites,
                       normwise_rel_err, relu_grad, relu_inputs, POOL_GEOMETRIES, pool_relu_input,
                       relu_pool_loss_and_grad, LINEAR_SHAPES, linear_loss_and_grads, MLP2_SHAPES,
-                      mlp2_loss_and_grads, conv_pool_loss_and_grads, conv_pool_node)
+                      mlp2_loss_and_grads, conv_pool_loss_and_grads, conv_pool_node, pool_bias_loss_and_grads)
 from oracle import OracleBackend
 from vkml_amd import nn, optim
 from vkml_amd import tensor as T
@@ -311,6 +311,41 @@ def test_conv_pool_gradient_node_on_device(backends, shape, cout):
     assert normwise_rel_err(got[:nw], want[:nw]) <= gemm_tolerance(n_ * h * w_)
 
 
+# CIFAR conv2's layer (the plane-sum kernel, rows of 16), rows of 32, and one
+# it leaves to the pool backward and the reduction (rows of 10).
+POOL_BIAS_DEVICE_LAYERS = [((128, 64, 16, 16), 128), ((4, 3, 32, 32), 8), ((3, 4, 6, 10), 5)]
+
+
+@pytest.mark.parametrize("shape,cout", POOL_BIAS_DEVICE_LAYERS)
+def test_pool_bias_gradient_node_on_device(backends, shape, cout):
+    """On the device, a conv layer's bias gradient taken with its relu-masked
+    pool gradient as one MAX_POOL2D_BACKWARD_RELU_BIAS node gives the device's
+    own MAX_POOL2D_BACKWARD_RELU + SUM graph bit for bit (image, weight and
+    bias gradients), and the node alone over the same pool gradient and layer
+    output gives the oracle's bits, pool gradient and bias gradient both."""
+    dev, cpu = backends
+    rng = np.random.default_rng(SEED + 26)
+    x = rng.integers(-1, 2, shape).astype(np.float32)
+    w = (rng.integers(-1, 2, (cout, shape[1], 3, 3)) * 0.5).astype(np.float32)
+    bias = (rng.integers(-1, 2, cout) * 0.5).astype(np.float32)
+    print(f"pool_bias x={shape} cout={cout}", flush=True)
+    fused = pool_bias_loss_and_grads(dev, x, w, bias, True)
+    graph = pool_bias_loss_and_grads(dev, x, w, bias, False)
+    for got, two in zip(fused, graph):
+        assert got.tobytes() == two.tobytes()
+    n_, _, h, w_ = shape
+    y = pool_relu_input((n_, cout, h, w_), SEED + 27)
+    gp = rng.standard_normal((n_, cout, h // 2, w_ // 2)).astype(np.float32)
+
+    def node(backend):
+        yt, gt = T.tensor(y, backend=backend), T.tensor(gp, backend=backend)
+        out = T.Node(T.OP["MAX_POOL2D_BACKWARD_RELU_BIAS"], (y.size + cout,), np.float32, yt.node.backend,
+                     [gt.node, yt.node], params=T._unfold_params((2, 2), (2, 2), (0, 0), (1, 1), (h, w_)))
+        return T.Tensor(out).numpy()
+
+    assert node(dev).tobytes() == node(cpu).tobytes()
+
+
 @pytest.mark.parametrize("model", ["mlp", "cnn"])
 def test_exact_graph_rewrites_keep_the_device_bits(backends, model):
     """On the device, the graph rewrites that compute the same arithmetic
@@ -321,7 +356,8 @@ def test_exact_graph_rewrites_keep_the_device_bits(backends, model):
     config 5's CNN at batch 128 for 3 steps."""
     dev, _ = backends
     rewrites = ("FOLD_CONSTANTS", "WEIGHT_GRAD_IN_PLACE_LAYOUT", "FUSED_ADD_RELU", "FUSED_CONV_EPILOGUE",
-                "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD", "FUSED_CONV_POOL_GRAD")
+                "FUSED_POOL_RELU_GRAD", "FUSED_LINEAR_BIAS", "FUSED_MATMUL_RELU_GRAD", "FUSED_CONV_POOL_GRAD",
+                "FUSED_POOL_BIAS_GRAD")
     if model == "mlp":
         fn, batches = mlp_model, mlp_batches(10)
     else:

@@ -337,6 +337,22 @@ def test_conv_pool_gradient_node_is_the_three_nodes(cpu, shape, cout):
     assert np.any(bias != 0) and np.any(fused[2] != 0)
 
 
+@pytest.mark.parametrize("shape,cout", [((2, 3, 16, 16), 4), ((1, 2, 6, 10), 3), ((2, 2, 32, 32), 2)])
+def test_pool_bias_gradient_node_is_the_two_nodes(cpu, shape, cout):
+    """A conv layer's bias gradient taken with its relu-masked pool gradient as
+    one MAX_POOL2D_BACKWARD_RELU_BIAS node (the image needing its gradient)
+    gives the MAX_POOL2D_BACKWARD_RELU + SUM graph's bits on the oracle, for
+    the image, weight and bias gradients, with ties and pre-activations on 0."""
+    from conftest import pool_bias_loss_and_grads
+
+    x, w, bias = conv_pool_operands(shape, cout, SEED + 25)
+    fused = pool_bias_loss_and_grads(cpu, x, w, bias, True)
+    graph = pool_bias_loss_and_grads(cpu, x, w, bias, False)
+    for got, want in zip(fused, graph):
+        assert got.tobytes() == want.tobytes()
+    assert np.any(fused[3] != 0)
+
+
 def test_conv_pool_gradient_rewrite_needs_its_pattern(cpu):
     """No fused node when the image needs its gradient, or the pool is not 2x2
     at stride 2: the three nodes stay."""

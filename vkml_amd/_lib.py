@@ -35,6 +35,7 @@ OP = dict(
     CROSS_ENTROPY=96, CROSS_ENTROPY_BACKWARD=97, CONV2D=98, CONV2D_WEIGHT_GRAD=99,
     RELU_BACKWARD=100, CONV2D_WEIGHT_GRAD_SUM=101, CONV2D_INPUT_GRAD=102, CONV2D_BIAS_RELU=103, ADD_RELU=104,
     MAX_POOL2D_BACKWARD_RELU=105, MATMUL_BIAS=106, MATMUL_RELU_BACKWARD=107, CONV2D_POOL_WEIGHT_BIAS_GRAD=108,
+    MAX_POOL2D_BACKWARD_RELU_BIAS=109,
 )
 
 

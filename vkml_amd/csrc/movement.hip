@@ -808,6 +808,218 @@ int launch_max_pool2d_backward(const float* grad, const float* src, const vkhip_
     return VKHIP_OK;
 }
 
+// ---- the relu-masked pool gradient with each plane's sum (a conv layer's bias
+// gradient) ----------------------------------------------------------------------
+// MAX_POOL2D_BACKWARD_RELU's values for 2x2 windows at stride 2 over planes of
+// rows W = 16 or 32, H = 2P rows, plus for every plane the sum of those values
+// in the pairwise tree's order. A workgroup takes RP = 1024 / W consecutive row
+// pairs; W / 4 lanes share one (each the 4 positions 4j..4j+3 of both rows: two
+// windows, the tiled kernel's selects, 16-byte loads and stores on consecutive
+// addresses), and put its values in LDS. Thread t < RP then sums row pair t in
+// position order from +0 (one 32-position leaf for W = 16, two for W = 32),
+// and the P row pairs of a plane, adjacent lanes, add their sums level by level
+// (xor butterflies: a balanced tree, every lane ends with the same value). With
+// the planes' positions a power of two the plane is an aligned subtree of the
+// reduction over N, H, W; plane_sums_fold_kernel then adds each channel's
+// planes as a balanced tree over the images.
+template <int W, int P>
+__global__ __launch_bounds__(256) void max_pool2x2_backward_relu_sums_kernel(
+    const float* __restrict__ grad, const float* __restrict__ src, float* __restrict__ dst,
+    float* __restrict__ psum) {
+    static_assert((W == 16 || W == 32) && P >= 1 && P <= 32 && (P & (P - 1)) == 0, "row pairs per plane");
+    constexpr int L4 = W / 4;           // lanes per row pair
+    constexpr int RP = 256 / L4;        // row pairs per workgroup
+    constexpr int PITCH = 2 * W + 4;    // LDS floats per row pair (16-byte rows, spread banks)
+    static_assert(P <= RP, "a plane's row pairs in one workgroup");
+    __shared__ __attribute__((aligned(16))) float vals[RP * PITCH];
+    const int t = threadIdx.x, rp = t / L4, j = t % L4;
+    const uint64_t q = static_cast<uint64_t>(blockIdx.x) * RP + rp;  // global row pair
+    const uint64_t base = q * (2 * W) + 4 * j;
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src + base);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + base + W);
+    const float2 g = *reinterpret_cast<const float2*>(grad + q * (W / 2) + 2 * j);
+    const int32_t a0 = argmax4(a[0], a[1], b[0], b[1]);
+    const int32_t a1 = argmax4(a[2], a[3], b[2], b[3]);
+    const float g0 = 0.0f + g.x, g1 = 0.0f + g.y;
+    f32x4_t top, bot;
+    top[0] = a0 == 0 ? g0 : 0.0f;
+    top[1] = a0 == 1 ? g0 : 0.0f;
+    bot[0] = a0 == 2 ? g0 : 0.0f;
+    bot[1] = a0 == 3 ? g0 : 0.0f;
+    top[2] = a1 == 0 ? g1 : 0.0f;
+    top[3] = a1 == 1 ? g1 : 0.0f;
+    bot[2] = a1 == 2 ? g1 : 0.0f;
+    bot[3] = a1 == 3 ? g1 : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (a[i] <= 0.0f) top[i] = 0.0f;
+        if (b[i] <= 0.0f) bot[i] = 0.0f;
+    }
+    __builtin_nontemporal_store(top, reinterpret_cast<f32x4_t*>(dst + base));
+    __builtin_nontemporal_store(bot, reinterpret_cast<f32x4_t*>(dst + base + W));
+    *reinterpret_cast<f32x4_t*>(vals + rp * PITCH + 4 * j) = top;
+    *reinterpret_cast<f32x4_t*>(vals + rp * PITCH + W + 4 * j) = bot;
+    __syncthreads();
+    if (t >= 64) return;  // wave 0 sums (RP <= 64 row pairs), whole waves leave
+    float sum = 0.0f;
+    if (t < RP) {
+        const float* r = vals + t * PITCH;
+        float leaf0 = 0.0f, leaf1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < W / 4; ++i) {
+            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(r + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) leaf0 = leaf0 + v[k];
+        }
+        float& second = W == 16 ? leaf0 : leaf1;
+#pragma unroll
+        for (int i = 0; i < W / 4; ++i) {
+            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(r + W + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) second = second + v[k];
+        }
+        sum = W == 16 ? leaf0 : leaf0 + leaf1;
+    }
+    if constexpr (P >= 2) sum = sum + wave_partner<1>(sum);
+    if constexpr (P >= 4) sum = sum + wave_partner<2>(sum);
+    if constexpr (P >= 8) sum = sum + wave_partner<4>(sum);
+    if constexpr (P >= 16) sum = sum + wave_partner<8>(sum);
+    if constexpr (P >= 32) sum = sum + wave_partner<16>(sum);
+    if (t < RP && t % P == 0) psum[(static_cast<uint64_t>(blockIdx.x) * RP + t) / P] = sum;
+}
+
+// Per channel c, the balanced pairwise tree over the images of the plane sums
+// psum[n * C + c] (N a power of two): 16 channels per workgroup, R = min(16, N)
+// runs of N / R consecutive images each (a binary-counter carry stack, which
+// for a power-of-two count is the balanced tree), then the runs level by level.
+__global__ __launch_bounds__(256) void plane_sums_fold_kernel(const float* __restrict__ psum, uint32_t n,
+                                                              uint32_t channels, float* __restrict__ out) {
+    __shared__ float runs[16][17];
+    const int tid = threadIdx.x, cl = tid & 15, run = tid >> 4;
+    const uint32_t c = blockIdx.x * 16u + static_cast<uint32_t>(cl);
+    const uint32_t nr = n < 16u ? n : 16u, per = n / nr;
+    float r = 0.0f;
+    if (static_cast<uint32_t>(run) < nr && c < channels) {
+        float stack[13];
+#pragma unroll
+        for (int l = 0; l < 13; ++l) stack[l] = 0.0f;
+        for (uint32_t i0 = 0; i0 < per; i0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                v[k] = i0 + k < per ? psum[static_cast<uint64_t>(run * per + i0 + k) * channels + c] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (i0 + k >= per) break;
+                const uint32_t count = i0 + k;
+                float b = v[k];
+                bool carry = true;
+#pragma unroll
+                for (int l = 0; l < 13; ++l) {
+                    if (carry) {
+                        if ((count >> l) & 1u) {
+                            b = stack[l] + b;
+                        } else {
+                            stack[l] = b;
+                            carry = false;
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int l = 0; l < 13; ++l)
+            if (per == (1u << l)) r = stack[l];
+    }
+    runs[run][cl] = r;
+    __syncthreads();
+    if (tid < 16 && c < channels) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = runs[i][tid];
+#pragma unroll
+        for (int w = 1; w < 16; w *= 2)
+#pragma unroll
+            for (int i = 0; i + w < 16; i += 2 * w)
+                if (static_cast<uint32_t>(i + w) < nr) v[i] = v[i] + v[i + w];
+        out[c] = v[0];
+    }
+}
+
+int launch_reduce(int op, const float* src, const vkhip_operand& d, uint32_t mask, void* dst);
+
+// MAX_POOL2D_BACKWARD_RELU of 2x2 windows at stride 2 into dst [N,C,H,W], and
+// dst's sum over N, H, W into bias_out [C] (the pairwise tree's bits): the
+// kernel above and the fold where they apply (rows of 16 or 32, 2 to 64 rows,
+// N*H*W a power of two, contiguous 16-byte aligned operands), else the pool
+// backward and the reduction in turn.
+int launch_max_pool2x2_backward_relu_sums(const float* grad, const float* src, const vkhip_operand& sd,
+                                          float* dst, float* bias_out) {
+    const uint32_t N = sd.ne[0], C = sd.ne[1], H = sd.ne[2], Wd = sd.ne[3];
+    const uint64_t hw = static_cast<uint64_t>(H) * Wd, total = static_cast<uint64_t>(N) * hw;
+    const bool contiguous = sd.nb[3] == 1 && sd.nb[2] == static_cast<int64_t>(Wd) &&
+                            sd.nb[1] == static_cast<int64_t>(hw) && (N == 1 || sd.nb[0] == static_cast<int64_t>(C * hw));
+    const auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const uint32_t P = H / 2;
+    const uint64_t pairs = static_cast<uint64_t>(N) * C * P;
+    const bool fits = (Wd == 16 || Wd == 32) && H % 2 == 0 && P >= 1 && P <= 32 && (P & (P - 1)) == 0 &&
+                      (total & (total - 1)) == 0 && (N & (N - 1)) == 0 && contiguous && al(grad) && al(src) &&
+                      al(dst) && pairs % 64 == 0 && pairs <= 0xffffffffull && C > 0;
+    publish("max_pool2d.kernel", "max_pool2d_backward_relu_sums", fits ? "pool2x2_relu_plane_sums" : "pool_backward_then_sum",
+            fits ? "pool_backward_then_sum" : "pool2x2_relu_plane_sums",
+            fits ? "rows of 16 or 32 and power-of-two extents: the sums in the pool kernel"
+                 : "the plane sums need rows of 16 or 32 and power-of-two extents",
+            static_cast<int64_t>(Wd), static_cast<int64_t>(H));
+    if (fits) {
+        float* psum = nullptr;
+        const int st = workspace(static_cast<size_t>(N) * C * sizeof(float), &psum);
+        if (st != VKHIP_OK) return st;
+        const uint32_t per_wg = 1024u / Wd;  // row pairs per workgroup (pairs is a multiple of 64)
+        const dim3 grid(static_cast<uint32_t>(pairs / per_wg));
+#define VKHIP_PRS(WW, PP) \
+    hipLaunchKernelGGL((max_pool2x2_backward_relu_sums_kernel<WW, PP>), grid, dim3(256), 0, ctx().stream, grad, src, dst, \
+                       psum)
+#define VKHIP_PRS_P(WW)                                                                                        \
+    do {                                                                                                      \
+        switch (P) {                                                                                          \
+            case 1: VKHIP_PRS(WW, 1); break;                                                                  \
+            case 2: VKHIP_PRS(WW, 2); break;                                                                  \
+            case 4: VKHIP_PRS(WW, 4); break;                                                                  \
+            case 8: VKHIP_PRS(WW, 8); break;                                                                  \
+            case 16: VKHIP_PRS(WW, 16); break;                                                                \
+            default: VKHIP_PRS(WW, 32); break;                                                                \
+        }                                                                                                     \
+    } while (0)
+        if (Wd == 16) VKHIP_PRS_P(16); else VKHIP_PRS_P(32);
+#undef VKHIP_PRS_P
+#undef VKHIP_PRS
+        VKHIP_LAUNCH_CHECK();
+        hipLaunchKernelGGL(plane_sums_fold_kernel, dim3(ceil_div(C, 16u)), dim3(256), 0, ctx().stream, psum, N, C,
+                           bias_out);
+        VKHIP_LAUNCH_CHECK();
+        return VKHIP_OK;
+    }
+    vkhip_unfold pp{};
+    pp.kernel_h = pp.kernel_w = 2;
+    pp.stride_h = pp.stride_w = 2;
+    pp.dilation_h = pp.dilation_w = 1;
+    pp.image_h = static_cast<int32_t>(H);
+    pp.image_w = static_cast<int32_t>(Wd);
+    int st = launch_max_pool2d_backward(grad, src, sd, dst, H / 2, Wd / 2, pp, true);
+    if (st != VKHIP_OK) return st;
+    vkhip_operand dd;
+    dd.ne[0] = N;
+    dd.ne[1] = C;
+    dd.ne[2] = H;
+    dd.ne[3] = Wd;
+    dd.nb[0] = static_cast<int64_t>(C * hw);
+    dd.nb[1] = static_cast<int64_t>(hw);
+    dd.nb[2] = Wd;
+    dd.nb[3] = 1;
+    return launch_reduce(VKHIP_REDUCE_SUM, dst, dd, 0xDu, bias_out);
+}
+
+
 }  // namespace vkhip
 
 extern "C" int vkhip_im2col(const float* src, const vkhip_operand* src_desc, float* dst,

@@ -27,6 +27,8 @@ int conv2d_weight_grad(const float* x, const vkhip_operand& xd, const float* gr,
                        const vkhip_operand& gd, float* out, const vkhip_unfold& p);
 int conv2d_weight_grad_sum(const float* x, const vkhip_operand& xd, const float* gr,
                            const vkhip_operand& gd, float* out, const vkhip_unfold& p);
+int launch_max_pool2x2_backward_relu_sums(const float* grad, const float* src, const vkhip_operand& sd,
+                                          float* dst, float* bias_out);
 int conv2d_pool_weight_bias_grad(const float* x, const vkhip_operand& xd, const float* y, const vkhip_operand& yd,
                                  const float* gp, const vkhip_operand& gpd, float* out, const vkhip_unfold& p);
 int conv2d_input_grad(const float* gr, const vkhip_operand& gd, const float* w, int64_t w_row,
@@ -377,6 +379,14 @@ static int supports_node(const vkhip_node& nd) {
             return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) &&
                    nd.src[0].ndim == 4 && contiguous(nd.src[0]) && nd.src[1].ndim == 4 &&
                    o.ndim == 4 && contiguous(o);
+        case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU_BIAS: {
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            return nd.n_src == 2 && is_f32(o) && is_f32(nd.src[0]) && is_f32(nd.src[1]) && nd.src[0].ndim == 4 &&
+                   contiguous(nd.src[0]) && nd.src[1].ndim == 4 && contiguous(nd.src[1]) && o.ndim == 1 &&
+                   contiguous(o) && p.kernel_h == 2 && p.kernel_w == 2 && p.stride_h == 2 && p.stride_w == 2 &&
+                   p.pad_h == 0 && p.pad_w == 0 && p.dilation_h == 1 && p.dilation_w == 1;
+        }
         default: return 0;
     }
 }
@@ -492,6 +502,20 @@ static int check_extents(const vkhip_node& nd) {
                             static_cast<long long>(oh * ow), p.image_h, p.image_w);
             return VKHIP_OK;
         }
+        case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU_BIAS: {
+            const vkhip_tensor& g = nd.src[0];
+            const vkhip_tensor& y = nd.src[1];
+            vkhip_unfold p;
+            memcpy(&p, nd.params, sizeof p);
+            if (nd.n_src != 2 || g.ndim != 4 || y.ndim != 4 || o.ndim != 1 || y.ne[2] != p.image_h ||
+                y.ne[3] != p.image_w || y.ne[2] % 2 != 0 || y.ne[3] % 2 != 0 || g.ne[0] != y.ne[0] ||
+                g.ne[1] != y.ne[1] || g.ne[2] != y.ne[2] / 2 || g.ne[3] != y.ne[3] / 2 ||
+                o.ne[0] != y.ne[0] * y.ne[1] * y.ne[2] * y.ne[3] + y.ne[1])
+                return fail(VKHIP_ERR_INVALID,
+                            "max_pool2d_backward_relu_bias: gradient, pool input and output extents disagree "
+                            "with 2x2 windows at stride 2 over even extents");
+            return VKHIP_OK;
+        }
         case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: {
             vkhip_unfold p;
             memcpy(&p, nd.params, sizeof p);
@@ -561,6 +585,7 @@ static const char* op_name(int op) {
         case VKHIP_OP_MAX_POOL2D_BACKWARD: return "max_pool2d_backward";
         case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU: return "max_pool2d_backward_relu";
         case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: return "conv2d_pool_weight_bias_grad";
+        case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU_BIAS: return "max_pool2d_backward_relu_bias";
         case VKHIP_OP_CROSS_ENTROPY: return "cross_entropy";
         case VKHIP_OP_CROSS_ENTROPY_BACKWARD: return "cross_entropy_backward";
         case VKHIP_OP_CONV2D: return "conv2d";
@@ -757,6 +782,13 @@ static int compute_node(const vkhip_node& nd) {
             return conv2d_weight_grad_sum(static_cast<const float*>(nd.src[0].data), to_operand(nd.src[0]),
                                           static_cast<const float*>(gr.data), gd,
                                           static_cast<float*>(nd.out.data), p);
+        }
+        case VKHIP_OP_MAX_POOL2D_BACKWARD_RELU_BIAS: {
+            const vkhip_tensor& y = nd.src[1];
+            float* out = static_cast<float*>(nd.out.data);
+            return launch_max_pool2x2_backward_relu_sums(static_cast<const float*>(nd.src[0].data),
+                                                         static_cast<const float*>(y.data), to_operand(y), out,
+                                                         out + y.ne[0] * y.ne[1] * y.ne[2] * y.ne[3]);
         }
         case VKHIP_OP_CONV2D_POOL_WEIGHT_BIAS_GRAD: {
             vkhip_unfold p;

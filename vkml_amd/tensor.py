@@ -874,6 +874,14 @@ FUSED_POOL_RELU_GRAD = True
 # False keeps the three nodes.
 FUSED_CONV_POOL_GRAD = True
 
+# A conv layer's bias gradient, when its relu-masked pool gradient is one
+# MAX_POOL2D_BACKWARD_RELU node of 2x2 windows at stride 2, as one
+# MAX_POOL2D_BACKWARD_RELU_BIAS node whose output holds the pool gradient and
+# the bias gradient (both views of it): the device sums each plane of the pool
+# gradient while it writes it, in the pairwise tree's order, instead of a
+# reduction re-reading it. False keeps the pool gradient and the bias's SUM.
+FUSED_POOL_BIAS_GRAD = True
+
 # A relu gradient whose incoming gradient is a product (a Linear layer's input
 # gradient, grad @ w, feeding the relu before it) as one MATMUL_RELU_BACKWARD
 # node: the select applied where the product's split-K partials are folded.
@@ -1406,6 +1414,28 @@ def _conv_pool_grads(node: Node, a: Node, b: Node, bias3: Node, dz: Tensor, grad
     return True
 
 
+def _pool_relu_bias_grad(dz: Tensor, bias3: Node, grads: dict):
+    """When dz is an uncomputed MAX_POOL2D_BACKWARD_RELU of 2x2 windows at
+    stride 2 (over a conv layer's relu output), one MAX_POOL2D_BACKWARD_RELU_BIAS
+    node in its place: the bias gradient (dz summed over N, H, W) is accumulated
+    from its output's tail and the returned view of its head is dz."""
+    pn = dz.node
+    if not (FUSED_POOL_BIAS_GRAD and pn.op == OP["MAX_POOL2D_BACKWARD_RELU"] and not pn.computed):
+        return None
+    y = pn.src[1]
+    if len(y.shape) != 4:
+        return None
+    n_, c, h, w = y.shape
+    if h % 2 or w % 2 or pn.params != _unfold_params((2, 2), (2, 2), (0, 0), (1, 1), (h, w)):
+        return None
+    total = n_ * c * h * w
+    out = Tensor(Node(OP["MAX_POOL2D_BACKWARD_RELU_BIAS"], (total + c,), np.float32, pn.backend, list(pn.src),
+                      params=pn.params))
+    dbias = _view(RESHAPE, out, (c,), (1,), total)
+    _accumulate(grads, bias3, dbias.reshape(bias3.shape))
+    return _view(RESHAPE, out, tuple(y.shape), contiguous_strides(y.shape), 0)
+
+
 def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
     op = node.op
     a = node.src[0] if node.src else None
@@ -1517,7 +1547,11 @@ def _apply_backward(node: Node, grad: Tensor, grads: dict) -> None:
         if _conv_pool_grads(node, a, b, bias3, dz, grads):
             return
         if bias3.requires_grad:
-            _accumulate(grads, bias3, reduce_to_shape(dz, bias3.shape))
+            with_bias = _pool_relu_bias_grad(dz, bias3, grads)
+            if with_bias is not None:
+                dz = with_bias
+            else:
+                _accumulate(grads, bias3, reduce_to_shape(dz, bias3.shape))
         if a.requires_grad or b.requires_grad:
             _conv2d_backward(node, a, b, dz, grads)
     elif op == OP["CONV2D"]:
@@ -1566,7 +1600,7 @@ REFERENCE_GRAPH_SWITCHES = {
     "IMPLICIT_CONV": False, "FUSED_CROSS_ENTROPY": False, "FUSED_RELU_BACKWARD": False,
     "FUSED_POOL_RELU_GRAD": False, "FUSED_MATMUL_RELU_GRAD": False, "FOLD_CONV_WEIGHT_GRAD": False,
     "FUSED_CONV_INPUT_GRAD": False, "FUSED_CONV_EPILOGUE": False, "FUSED_ADD_RELU": False,
-    "FUSED_CONV_POOL_GRAD": False, "BACKWARD_FLUSH_EVERY": 0,
+    "FUSED_CONV_POOL_GRAD": False, "FUSED_POOL_BIAS_GRAD": False, "BACKWARD_FLUSH_EVERY": 0,
 }
 
 
