@@ -591,15 +591,32 @@ int vkhip_get_numerics(void);
 typedef struct vkhip_program vkhip_program;
 int vkhip_program_begin(void);
 int vkhip_program_end(vkhip_program** out);
-/* use_graph != 0: the first run captures the replayed launches into a HIP
- * graph on the backend stream (not while profiling is on), later runs launch
- * the graph; the backend stream must then stay the same. use_graph == 0
- * replays call by call. */
+/* use_graph bit 0 set: the first run captures the replayed launches into a
+ * HIP graph on the backend stream (not while profiling is on), later runs
+ * launch the graph; the backend stream must then stay the same. Bit 0 clear:
+ * a plain run, call by call; bit 1 (2) then marks a run whose outputs the
+ * caller will not read, which skips the early-output copy below. */
 int vkhip_program_run(vkhip_program* program, int use_graph);
 /* Waits for a captured graph to finish, then frees the program. */
 int vkhip_program_destroy(vkhip_program* program);
 int vkhip_program_info(const vkhip_program* program, size_t* calls, size_t* nodes,
                        int* has_graph);
+/* Early outputs (no counterpart in the reference; the step-latency target of
+ * docs/SMALL-STEP-LATENCY.md:44-51 for a host that reads each step's loss).
+ * Declares the program's outputs as n device spans (src, nbytes; dst unused),
+ * at most 4096 bytes in all, before its first run. The recorded units (a
+ * node, an SGD call, a copy call) are reordered once: each unit that the
+ * outputs depend on moves ahead of later-recorded units it shares no buffer
+ * hazard with (read/write, write/read, write/write of the bytes their tensors
+ * span), so the values of every unit are unchanged. Each plain run (use_graph
+ * == 0) then copies the outputs into pinned host memory right behind their
+ * last writer and records an event there. Graph runs do not. */
+int vkhip_program_set_outputs(vkhip_program* program, const vkhip_copy* outputs, size_t n);
+/* Waits for the latest plain run's outputs (not for the rest of its step)
+ * and copies their bytes, in declaration order, to host_dst (nbytes: their
+ * total). VKHIP_ERR_INVALID when no outputs are declared or the latest run
+ * was a graph run or none. */
+int vkhip_program_read_outputs(vkhip_program* program, void* host_dst, size_t nbytes);
 
 /* ======================================================================== */
 /* Host-side planning helpers (callable without a GPU)                       */

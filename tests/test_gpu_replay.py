@@ -189,6 +189,48 @@ def test_prefetched_uploads_are_the_plain_uploads(config, graph):
     assert runs[3] == runs[0]
 
 
+@pytest.mark.parametrize("config", ["mlp", "cnn"])
+def test_early_outputs_are_the_step_end_outputs(config):
+    """A plain replay's outputs read back early (vkhip_program_set_outputs: the
+    units the loss depends on hoisted ahead of the backward pass and update,
+    the bytes copied to pinned memory behind their last writer, the read
+    waiting for that copy only) are the bytes the whole step leaves in the
+    output tensor, and the reordering changes no unit's values: every loss
+    and the final parameters equal those of replays read after the step ends,
+    with the same node count. Graph replays declare no early outputs."""
+    import ctypes
+
+    from vkml_amd import _lib
+
+    dev = T.default_backend()
+    make, _, _, _, lr = CONFIGS[config]
+    batches = _batches(config, 7)
+    runs, infos = [], []
+    for early in (False, True):
+        model = make(dev)
+        opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
+        step = T.CapturedStep(_step_fn(model, opt), *batches[0], early_outputs=early)
+        losses = [np.float32(step.first[0])]
+        for x, y in batches[1:]:
+            out = step(x, y)
+            if early:  # read before the step's end; the step's end leaves the same bytes
+                assert out[0].tobytes() == step.outputs_now()[0].tobytes()
+            losses.append(np.float32(out[0]))
+        runs.append((np.array(losses, np.float32).tobytes(), [p.numpy().tobytes() for p in model.parameters()]))
+        infos.append(step.info()["nodes"])
+        step.close()
+    assert runs[1] == runs[0]
+    assert infos[1] == infos[0]
+    model = make(dev)
+    opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
+    step = T.CapturedStep(_step_fn(model, opt), *batches[0], graph=True)
+    step(*batches[1])
+    buf = np.empty(4, np.uint8)
+    assert step.lib.vkhip_program_read_outputs(step._program, buf.ctypes.data_as(ctypes.c_void_p), 4) \
+        == _lib.ERR_INVALID
+    step.close()
+
+
 def test_constant_nodes_replay_only_while_nothing_else_writes_them():
     """A recorded constant (FULL) that no other recorded call writes keeps its
     recorded value and is left out of replays; one that another call

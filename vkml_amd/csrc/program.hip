@@ -26,6 +26,7 @@
 // step instead of one per kernel. While a graph exists the backend keeps the
 // workspace blocks it captured (a workspace that grows later gets a new block;
 // the captured one is freed when the last graph is destroyed).
+#include <cstring>
 #include <memory>
 #include <mutex>
 #include <vector>
@@ -54,6 +55,16 @@ struct vkhip_program {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     hipStream_t graph_stream = nullptr;
+    // Early outputs: the declared device spans are copied into `out_host`
+    // (pinned, device-visible at `out_dev`) behind calls[out_after - 1] of each
+    // plain run, and `out_event` is recorded there.
+    std::vector<vkhip_copy> outputs;
+    void* out_host = nullptr;
+    void* out_dev = nullptr;
+    size_t out_bytes = 0;
+    size_t out_after = 0;
+    hipEvent_t out_event = nullptr;
+    bool out_ready = false;  // the latest run was a plain run that recorded out_event
 };
 
 namespace vkhip {
@@ -103,8 +114,14 @@ void program_note_copy(const vkhip_copy* copies, size_t n) {
 int compute_nodes(const vkhip_node* nodes, size_t n);  // runtime.hip
 int copy_pairs(const vkhip_copy* copies, size_t n);     // runtime.hip
 
-static int replay(const vkhip_program& p) {
-    for (const vkhip_program::Call& c : p.calls) {
+static int replay(const vkhip_program& p, bool early_outputs) {
+    for (size_t k = 0; k < p.calls.size(); ++k) {
+        if (early_outputs && k == p.out_after) {
+            int st = copy_pairs(p.outputs.data(), p.outputs.size());
+            if (st != VKHIP_OK) return st;
+            VKHIP_HIP(hipEventRecord(p.out_event, ctx().stream));
+        }
+        const vkhip_program::Call& c = p.calls[k];
         int st = VKHIP_OK;
         switch (c.kind) {
             case vkhip_program::kCompute: st = compute_nodes(c.nodes.data(), c.nodes.size()); break;
@@ -115,6 +132,11 @@ static int replay(const vkhip_program& p) {
             case vkhip_program::kCopy: st = copy_pairs(c.copies.data(), c.copies.size()); break;
         }
         if (st != VKHIP_OK) return st;
+    }
+    if (early_outputs && p.out_after == p.calls.size()) {
+        const int st = copy_pairs(p.outputs.data(), p.outputs.size());
+        if (st != VKHIP_OK) return st;
+        VKHIP_HIP(hipEventRecord(p.out_event, ctx().stream));
     }
     return VKHIP_OK;
 }
@@ -226,6 +248,7 @@ extern "C" int vkhip_program_run(vkhip_program* p, int use_graph) {
     if (vkhip::program_recording())
         return fail(VKHIP_ERR_INVALID, "program_run: cannot replay while recording");
     hipStream_t stream = ctx().stream;
+    p->out_ready = false;
     if (p->exec) {
         if (stream != p->graph_stream)
             return fail(VKHIP_ERR_INVALID, "program_run: the backend stream changed since the graph was captured");
@@ -233,14 +256,19 @@ extern "C" int vkhip_program_run(vkhip_program* p, int use_graph) {
         return VKHIP_OK;
     }
     vkhip::ReplayScope scope;
-    if (!use_graph) return vkhip::replay(*p);
+    if (!(use_graph & 1)) {
+        const bool early = !p->outputs.empty() && !(use_graph & 2);
+        st = vkhip::replay(*p, early);
+        p->out_ready = early && st == VKHIP_OK;
+        return st;
+    }
     // First graph run: capture the replayed launches, then launch the graph.
     // Profiling records events per unit of work, which a capture must not do.
-    if (vkhip::profiling_on()) return vkhip::replay(*p);
+    if (vkhip::profiling_on()) return vkhip::replay(*p, false);
     st = vkhip::pin_workspaces(+1);
     if (st != VKHIP_OK) return st;
     VKHIP_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
-    st = vkhip::replay(*p);
+    st = vkhip::replay(*p, false);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(stream, &graph);
     if (st != VKHIP_OK || e != hipSuccess) {
@@ -275,6 +303,13 @@ extern "C" int vkhip_program_destroy(vkhip_program* p) {
         const int rc = vkhip::pin_workspaces(-1);
         if (st == VKHIP_OK) st = rc;
     }
+    if (p->out_event) {
+        // a plain run may still be copying into the pinned block
+        if (ctx().ready && hipEventSynchronize(p->out_event) != hipSuccess && st == VKHIP_OK)
+            st = fail(VKHIP_ERR_DEVICE, "program_destroy: output event synchronisation failed");
+        (void)hipEventDestroy(p->out_event);
+    }
+    if (p->out_host) (void)hipHostFree(p->out_host);
     delete p;
     return st;
 }
@@ -285,5 +320,168 @@ extern "C" int vkhip_program_info(const vkhip_program* p, size_t* calls, size_t*
     if (calls) *calls = p->calls.size();
     if (nodes) *nodes = p->node_count;
     if (has_graph) *has_graph = p->exec ? 1 : 0;
+    return VKHIP_OK;
+}
+
+namespace vkhip {
+namespace {
+
+// A recorded unit (one node, one SGD call or one copy call) with the byte
+// spans it reads and writes.
+struct Unit {
+    vkhip_program::Call call;
+    std::vector<Span> reads, writes;
+};
+
+bool any_overlap(const std::vector<Span>& a, const std::vector<Span>& b) {
+    for (const Span& x : a)
+        for (const Span& y : b)
+            if (overlaps(x, y)) return true;
+    return false;
+}
+
+// Two units may trade places unless one writes bytes the other reads or writes.
+bool hazard(const Unit& a, const Unit& b) {
+    return any_overlap(a.writes, b.reads) || any_overlap(a.writes, b.writes) || any_overlap(a.reads, b.writes);
+}
+
+std::vector<Unit> units_of(const vkhip_program& p) {
+    std::vector<Unit> units;
+    for (const vkhip_program::Call& c : p.calls) {
+        if (c.kind == vkhip_program::kCompute) {
+            for (const vkhip_node& nd : c.nodes) {
+                Unit u;
+                u.call.kind = vkhip_program::kCompute;
+                u.call.nodes.push_back(nd);
+                for (int i = 0; i < nd.n_src && i < 3; ++i) u.reads.push_back(tensor_span(nd.src[i]));
+                u.writes.push_back(tensor_span(nd.out));
+                units.push_back(std::move(u));
+            }
+            continue;
+        }
+        Unit u;
+        u.call = c;
+        for (const vkhip_sgd_param& sp : c.sgd) {
+            const uintptr_t pa = reinterpret_cast<uintptr_t>(sp.param), ga = reinterpret_cast<uintptr_t>(sp.grad),
+                            va = reinterpret_cast<uintptr_t>(sp.velocity), nb = sp.n * sizeof(float);
+            u.reads.push_back({ga, ga + nb});
+            u.writes.push_back({pa, pa + nb});
+            if (sp.velocity) u.writes.push_back({va, va + nb});
+        }
+        for (const vkhip_copy& cp : c.copies) {
+            const uintptr_t d = reinterpret_cast<uintptr_t>(cp.dst), sa = reinterpret_cast<uintptr_t>(cp.src);
+            u.reads.push_back({sa, sa + cp.nbytes});
+            u.writes.push_back({d, d + cp.nbytes});
+        }
+        units.push_back(std::move(u));
+    }
+    return units;
+}
+
+// Moves the units the outputs depend on ahead of the later-recorded units they
+// have no hazard with, keeping their own order, and regroups consecutive nodes
+// into compute calls, ending a call at the last unit that writes an output.
+// Returns the number of calls up to and including that unit.
+size_t hoist_outputs(vkhip_program& p, const std::vector<Span>& outs) {
+    std::vector<Unit> units = units_of(p);
+    const size_t n = units.size();
+    // The dependence cone: walking back from the end, a unit that writes bytes
+    // the outputs (or a unit already in the cone) read joins it.
+    std::vector<char> cone(n, 0);
+    std::vector<Span> needed = outs;
+    for (size_t i = n; i-- > 0;) {
+        if (!any_overlap(units[i].writes, needed)) continue;
+        cone[i] = 1;
+        needed.insert(needed.end(), units[i].reads.begin(), units[i].reads.end());
+    }
+    for (size_t i = 0; i < n; ++i) {
+        if (!cone[i]) continue;
+        size_t j = i;
+        while (j > 0 && !cone[j - 1] && !hazard(units[j - 1], units[j])) {
+            std::swap(units[j - 1], units[j]);
+            std::swap(cone[j - 1], cone[j]);
+            --j;
+        }
+    }
+    size_t last = 0;  // one past the last unit that writes an output
+    for (size_t i = 0; i < n; ++i)
+        if (any_overlap(units[i].writes, outs)) last = i + 1;
+    std::vector<vkhip_program::Call> calls;
+    size_t after = 0;
+    for (size_t i = 0; i < n; ++i) {
+        Unit& u = units[i];
+        const bool join = u.call.kind == vkhip_program::kCompute && !calls.empty() &&
+                          calls.back().kind == vkhip_program::kCompute && i != last;
+        if (join)
+            calls.back().nodes.push_back(u.call.nodes[0]);
+        else
+            calls.push_back(std::move(u.call));
+        if (i + 1 == last) after = calls.size();
+    }
+    p.calls.swap(calls);
+    return after;
+}
+
+}  // namespace
+}  // namespace vkhip
+
+extern "C" int vkhip_program_set_outputs(vkhip_program* p, const vkhip_copy* outputs, size_t n) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!p || (n && !outputs)) return fail(VKHIP_ERR_INVALID, "program_set_outputs: null argument");
+    if (!p->outputs.empty()) return fail(VKHIP_ERR_INVALID, "program_set_outputs: outputs already declared");
+    if (p->exec) return fail(VKHIP_ERR_INVALID, "program_set_outputs: the program has a captured graph");
+    if (n == 0) return VKHIP_OK;
+    constexpr size_t kMaxOutputBytes = 4096;
+    size_t total = 0;
+    std::vector<vkhip::Span> spans;
+    for (size_t i = 0; i < n; ++i) {
+        if (!outputs[i].src || outputs[i].nbytes == 0)
+            return fail(VKHIP_ERR_INVALID, "program_set_outputs: output %zu is empty", i);
+        total += outputs[i].nbytes;
+        const uintptr_t a = reinterpret_cast<uintptr_t>(outputs[i].src);
+        spans.push_back({a, a + outputs[i].nbytes});
+    }
+    if (total > kMaxOutputBytes)
+        return fail(VKHIP_ERR_INVALID, "program_set_outputs: %zu bytes of outputs (at most %zu)", total,
+                    kMaxOutputBytes);
+    void* host = nullptr;
+    void* dev = nullptr;
+    if (hipHostMalloc(&host, total, hipHostMallocDefault) != hipSuccess || !host)
+        return fail(VKHIP_ERR_OOM, "program_set_outputs: %zu bytes of pinned memory", total);
+    hipEvent_t ev = nullptr;
+    if (hipHostGetDevicePointer(&dev, host, 0) != hipSuccess ||
+        hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+        (void)hipHostFree(host);
+        return fail(VKHIP_ERR_DEVICE, "program_set_outputs: pinned block or event could not be set up");
+    }
+    std::lock_guard<std::mutex> lk(vkhip::g_prog_mu);
+    p->out_after = vkhip::hoist_outputs(*p, spans);
+    size_t off = 0;
+    for (size_t i = 0; i < n; ++i) {
+        vkhip_copy c = outputs[i];
+        c.dst = static_cast<unsigned char*>(dev) + off;
+        off += c.nbytes;
+        p->outputs.push_back(c);
+    }
+    p->out_host = host;
+    p->out_dev = dev;
+    p->out_bytes = total;
+    p->out_event = ev;
+    p->out_ready = false;
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_program_read_outputs(vkhip_program* p, void* host_dst, size_t nbytes) {
+    int st = vkhip::require_ready();
+    if (st != VKHIP_OK) return st;
+    if (!p || !host_dst) return fail(VKHIP_ERR_INVALID, "program_read_outputs: null argument");
+    if (p->outputs.empty() || !p->out_ready)
+        return fail(VKHIP_ERR_INVALID, "program_read_outputs: no plain run with declared outputs");
+    if (nbytes != p->out_bytes)
+        return fail(VKHIP_ERR_INVALID, "program_read_outputs: %zu bytes asked, the outputs hold %zu", nbytes,
+                    p->out_bytes);
+    VKHIP_HIP(hipEventSynchronize(p->out_event));
+    memcpy(host_dst, p->out_host, nbytes);
     return VKHIP_OK;
 }

@@ -1081,7 +1081,7 @@ class CapturedStep:
     step would; replays return the same bits an eager step would (tested).
     """
 
-    def __init__(self, fn, *example_inputs, graph: bool = False, backend=None):
+    def __init__(self, fn, *example_inputs, graph: bool = False, backend=None, early_outputs: bool = True):
         global _KEEP
         from .device import backend as hip_backend
 
@@ -1113,6 +1113,22 @@ class CapturedStep:
         keep.extend(t.node.storage for t in self.outputs)
         self._keep = keep
         self.first = [t.numpy() for t in self.outputs]
+        # Plain replays (graph=False) hand their outputs back from pinned host
+        # memory once the units the outputs depend on have run, not after the
+        # whole step (vkhip_program_set_outputs hoists those units, a loss's
+        # forward tail, ahead of the backward pass): the host reads step i's
+        # loss and queues step i + 1 while step i's backward pass and update
+        # still run, so the device does not idle between steps.
+        self._early = None
+        if early_outputs and not self.graph and self.outputs:
+            spans = [(t.node.storage.ptr + t.node.offset * t.node.itemsize, t.numel() * t.node.itemsize)
+                     for t in self.outputs]
+            total = int(np.sum([n for _, n in spans]))  # this module's sum() is the tensor reduction
+            if all(n > 0 for _, n in spans) and total <= 4096:
+                copies = [_lib.Copy(None, ptr, n) for ptr, n in spans]
+                _lib.check(self.lib.vkhip_program_set_outputs(self._program, (_lib.Copy * len(copies))(*copies),
+                                                              len(copies)), "program_set_outputs")
+                self._early = np.empty(total, np.uint8)
 
     def info(self) -> dict:
         calls, nodes, has_graph = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int()
@@ -1182,12 +1198,26 @@ class CapturedStep:
         if device_copies:
             _lib.check(self.lib.vkhip_copy_device_to_device(
                 (_lib.Copy * len(device_copies))(*device_copies), len(device_copies)), "copy_device_to_device")
-        _lib.check(self.lib.vkhip_program_run(self._program, 1 if self.graph else 0), "program_run")
+        mode = 1 if self.graph else 0 if read else 2  # 2: a plain run nobody reads early
+        _lib.check(self.lib.vkhip_program_run(self._program, mode), "program_run")
         if prefetch is not None:
             self.prefetch(*prefetch)
         if read:
             self._queued = 0
-            return self.outputs_now()
+            if self._early is None:
+                return self.outputs_now()
+            _lib.check(self.lib.vkhip_program_read_outputs(
+                self._program, self._early.ctypes.data_as(ctypes.c_void_p), self._early.nbytes),
+                "program_read_outputs")
+            outs, off = [], 0
+            for t in self.outputs:
+                n = t.node
+                size = t.numel() * n.itemsize
+                host = self._early[off:off + size].view(np.uint8 if n.dtype == np.bool_ else n.dtype)
+                host = host.reshape(n.shape).copy()
+                outs.append(host.astype(np.bool_) if n.dtype == np.bool_ else host)
+                off += size
+            return outs
         self._events[self._queued % self.queue_depth].record()
         self._queued += 1
         return None
