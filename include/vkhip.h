@@ -621,6 +621,13 @@ int vkhip_program_read_outputs(vkhip_program* program, void* host_dst, size_t nb
 /* ======================================================================== */
 /* Host-side planning helpers (callable without a GPU)                       */
 /* ======================================================================== */
+/* The order vkhip_program_set_outputs gives n recorded node records (each a
+ * unit reading its sources' and writing its output's byte spans) for the
+ * declared outputs: order[i] is the recorded index of the i-th node to run,
+ * and *out_after the number of nodes after which the outputs are final. No
+ * device is touched (pointers are compared, never dereferenced). */
+int vkhip_program_output_order(const vkhip_node* nodes, size_t n, const vkhip_copy* outputs,
+                               size_t n_outputs, size_t* order, size_t* out_after);
 /* Geometry of the CPU oracle's pairwise-summation tree (reference
  * pairwise_sum, src/backend/cpu/reduce.h:55-72) as the device kernels lay it
  * out: depth D and the element range [begin, end) of depth-D leaf `leaf`

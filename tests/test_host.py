@@ -4,6 +4,7 @@ bit-exact kernel uses, the split-K plan) agrees with the oracle and the
 reference's rules. No device calls."""
 from __future__ import annotations
 
+import ctypes
 import re
 from ctypes import byref, c_int64, c_uint32
 from pathlib import Path
@@ -362,3 +363,83 @@ def test_supports_refuses_nodes_whose_extents_disagree(case):
     assert lib.vkhip_supports(ref(good)) == 1, (name, lib.vkhip_last_error())
     for i, nd in enumerate(bad):
         assert lib.vkhip_supports(ref(nd)) == 0, f"{name}: malformed variant {i} accepted"
+
+
+def _vec_node(op, out_addr, srcs, n=64):
+    """A node record over fake device addresses: f32 vectors of n elements
+    (the planner compares byte spans and never dereferences them)."""
+    nd = _lib.NodeDesc()
+    nd.op = op
+
+    def desc(t, addr):
+        t.data = addr
+        t.dtype = 0
+        t.ndim = 1
+        t.ne[0] = n
+        t.nb[0] = 1
+
+    desc(nd.out, out_addr)
+    nd.n_src = len(srcs)
+    for i, a in enumerate(srcs):
+        desc(nd.src[i], a)
+    return nd
+
+
+def _output_order(nodes, outputs):
+    lib = _lib.load()
+    arr = (_lib.NodeDesc * len(nodes))(*nodes)
+    outs = (_lib.Copy * len(outputs))(*[_lib.Copy(None, a, n) for a, n in outputs])
+    order = (ctypes.c_size_t * len(nodes))()
+    after = ctypes.c_size_t()
+    assert lib.vkhip_program_output_order(arr, len(nodes), outs, len(outputs), order,
+                                          ctypes.byref(after)) == 0
+    return list(order), after.value
+
+
+def test_program_output_order_hoists_the_output_cone_within_hazards():
+    """vkhip_program_set_outputs' reordering, on node records over fake
+    addresses: the units the output depends on (a loss row node and its mean)
+    move ahead of later-recorded units they share no bytes with, keep their own
+    order, and stop behind the writer of what they read; a unit that writes
+    bytes they read (WAR), reads bytes they write (RAW the other way) or writes
+    the same bytes (WAW) is not passed. `after` counts the units that run before
+    the outputs are final."""
+    B = 1 << 20  # spans of 256 bytes, far apart
+    X, LOGITS, G1, G2, ROWS, LOSS, W, OTHER = (B * (i + 1) for i in range(8))
+    fwd = _vec_node(54, LOGITS, [X, W])          # logits = f(x, w)
+    bwd1 = _vec_node(97, G1, [LOGITS, X])        # gradient chain reads logits
+    bwd2 = _vec_node(54, G2, [G1, X])
+    upd = _vec_node(17, W, [W, G2])              # the update writes w
+    rows = _vec_node(96, ROWS, [LOGITS, X])      # the loss rows
+    mean = _vec_node(48, LOSS, [ROWS])           # the output
+    order, after = _output_order([fwd, bwd1, bwd2, upd, rows, mean], [(LOSS, 4)])
+    assert order == [0, 4, 5, 1, 2, 3] and after == 3
+
+    # The update overwrites the logits' buffer (a WAR hazard for the loss rows): no move.
+    upd_war = _vec_node(17, LOGITS, [LOGITS, G2])
+    order, after = _output_order([fwd, bwd1, bwd2, upd_war, rows, mean], [(LOSS, 4)])
+    assert order == [0, 1, 2, 3, 4, 5] and after == 6
+
+    # A unit reading the bytes the loss rows write (they hold an older value
+    # there) keeps the rows behind it; the mean stays behind the rows.
+    reader = _vec_node(54, OTHER, [ROWS, X])
+    order, after = _output_order([fwd, bwd1, reader, bwd2, rows, mean], [(LOSS, 4)])
+    assert order == [0, 1, 2, 4, 5, 3] and after == 5
+
+    # A unit writing part of the bytes the loss rows write (WAW), where the
+    # mean reads only the other part (so that unit stays out of the cone), is
+    # not passed either.
+    half = _vec_node(54, ROWS + 128, [G1, X], n=32)
+    mean32 = _vec_node(48, LOSS, [ROWS], n=32)
+    order, after = _output_order([fwd, bwd1, half, bwd2, rows, mean32], [(LOSS, 4)])
+    assert order == [0, 1, 2, 4, 5, 3] and after == 5
+
+    # Another writer of the output's bytes joins the cone: the cone keeps its
+    # order, so the output is final behind the last writer.
+    seed = _vec_node(2, LOSS, [])
+    order, after = _output_order([fwd, bwd1, seed, bwd2, rows, mean], [(LOSS, 4)])
+    assert order == [0, 2, 4, 5, 1, 3] and after == 4
+
+    # An output nothing writes is final before the first unit.
+    order, after = _output_order([fwd, bwd1], [(OTHER, 4)])
+    assert order == [0, 1] and after == 0

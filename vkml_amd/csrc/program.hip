@@ -328,7 +328,7 @@ namespace {
 
 // A recorded unit (one node, one SGD call or one copy call) with the byte
 // spans it reads and writes.
-struct Unit {
+struct RecordedUnit {
     vkhip_program::Call call;
     std::vector<Span> reads, writes;
 };
@@ -341,16 +341,16 @@ bool any_overlap(const std::vector<Span>& a, const std::vector<Span>& b) {
 }
 
 // Two units may trade places unless one writes bytes the other reads or writes.
-bool hazard(const Unit& a, const Unit& b) {
+bool hazard(const RecordedUnit& a, const RecordedUnit& b) {
     return any_overlap(a.writes, b.reads) || any_overlap(a.writes, b.writes) || any_overlap(a.reads, b.writes);
 }
 
-std::vector<Unit> units_of(const vkhip_program& p) {
-    std::vector<Unit> units;
+std::vector<RecordedUnit> units_of(const vkhip_program& p) {
+    std::vector<RecordedUnit> units;
     for (const vkhip_program::Call& c : p.calls) {
         if (c.kind == vkhip_program::kCompute) {
             for (const vkhip_node& nd : c.nodes) {
-                Unit u;
+                RecordedUnit u;
                 u.call.kind = vkhip_program::kCompute;
                 u.call.nodes.push_back(nd);
                 for (int i = 0; i < nd.n_src && i < 3; ++i) u.reads.push_back(tensor_span(nd.src[i]));
@@ -359,7 +359,7 @@ std::vector<Unit> units_of(const vkhip_program& p) {
             }
             continue;
         }
-        Unit u;
+        RecordedUnit u;
         u.call = c;
         for (const vkhip_sgd_param& sp : c.sgd) {
             const uintptr_t pa = reinterpret_cast<uintptr_t>(sp.param), ga = reinterpret_cast<uintptr_t>(sp.grad),
@@ -378,12 +378,12 @@ std::vector<Unit> units_of(const vkhip_program& p) {
     return units;
 }
 
-// Moves the units the outputs depend on ahead of the later-recorded units they
-// have no hazard with, keeping their own order, and regroups consecutive nodes
-// into compute calls, ending a call at the last unit that writes an output.
-// Returns the number of calls up to and including that unit.
-size_t hoist_outputs(vkhip_program& p, const std::vector<Span>& outs) {
-    std::vector<Unit> units = units_of(p);
+// The order in which `units` run when each unit the outputs depend on moves
+// ahead of the later-recorded units it has no hazard with, keeping the order
+// among those units: `order[i]` is the recorded index of the i-th unit to
+// run. Returns one past the position of the last unit that writes an output
+// (0 when none does): the outputs are final behind that many units.
+size_t output_order(const std::vector<RecordedUnit>& units, const std::vector<Span>& outs, std::vector<size_t>& order) {
     const size_t n = units.size();
     // The dependence cone: walking back from the end, a unit that writes bytes
     // the outputs (or a unit already in the cone) read joins it.
@@ -394,22 +394,33 @@ size_t hoist_outputs(vkhip_program& p, const std::vector<Span>& outs) {
         cone[i] = 1;
         needed.insert(needed.end(), units[i].reads.begin(), units[i].reads.end());
     }
+    order.resize(n);
+    for (size_t i = 0; i < n; ++i) order[i] = i;
     for (size_t i = 0; i < n; ++i) {
-        if (!cone[i]) continue;
+        if (!cone[order[i]]) continue;
         size_t j = i;
-        while (j > 0 && !cone[j - 1] && !hazard(units[j - 1], units[j])) {
-            std::swap(units[j - 1], units[j]);
-            std::swap(cone[j - 1], cone[j]);
+        while (j > 0 && !cone[order[j - 1]] && !hazard(units[order[j - 1]], units[order[j]])) {
+            std::swap(order[j - 1], order[j]);
             --j;
         }
     }
-    size_t last = 0;  // one past the last unit that writes an output
+    size_t last = 0;
     for (size_t i = 0; i < n; ++i)
-        if (any_overlap(units[i].writes, outs)) last = i + 1;
+        if (any_overlap(units[order[i]].writes, outs)) last = i + 1;
+    return last;
+}
+
+// Reorders the program's units by output_order and regroups consecutive
+// nodes into compute calls, ending a call at the last unit that writes an
+// output. Returns the number of calls up to and including that unit.
+size_t hoist_outputs(vkhip_program& p, const std::vector<Span>& outs) {
+    std::vector<RecordedUnit> units = units_of(p);
+    std::vector<size_t> order;
+    const size_t last = output_order(units, outs, order);
     std::vector<vkhip_program::Call> calls;
     size_t after = 0;
-    for (size_t i = 0; i < n; ++i) {
-        Unit& u = units[i];
+    for (size_t i = 0; i < order.size(); ++i) {
+        RecordedUnit& u = units[order[i]];
         const bool join = u.call.kind == vkhip_program::kCompute && !calls.empty() &&
                           calls.back().kind == vkhip_program::kCompute && i != last;
         if (join)
@@ -483,5 +494,29 @@ extern "C" int vkhip_program_read_outputs(vkhip_program* p, void* host_dst, size
                     p->out_bytes);
     VKHIP_HIP(hipEventSynchronize(p->out_event));
     memcpy(host_dst, p->out_host, nbytes);
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_program_output_order(const vkhip_node* nodes, size_t n, const vkhip_copy* outputs,
+                                          size_t n_outputs, size_t* order, size_t* out_after) {
+    if ((n && (!nodes || !order)) || (n_outputs && !outputs) || !out_after)
+        return fail(VKHIP_ERR_INVALID, "program_output_order: null argument");
+    std::vector<vkhip::RecordedUnit> units;
+    for (size_t i = 0; i < n; ++i) {
+        vkhip::RecordedUnit u;
+        u.call.kind = vkhip_program::kCompute;
+        u.call.nodes.push_back(nodes[i]);
+        for (int k = 0; k < nodes[i].n_src && k < 3; ++k) u.reads.push_back(vkhip::tensor_span(nodes[i].src[k]));
+        u.writes.push_back(vkhip::tensor_span(nodes[i].out));
+        units.push_back(std::move(u));
+    }
+    std::vector<vkhip::Span> spans;
+    for (size_t i = 0; i < n_outputs; ++i) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(outputs[i].src);
+        spans.push_back({a, a + outputs[i].nbytes});
+    }
+    std::vector<size_t> ord;
+    *out_after = vkhip::output_order(units, spans, ord);
+    for (size_t i = 0; i < n; ++i) order[i] = ord[i];
     return VKHIP_OK;
 }
