@@ -612,6 +612,18 @@ int vkhip_program_info(const vkhip_program* program, size_t* calls, size_t* node
  * == 0) then copies the outputs into pinned host memory right behind their
  * last writer and records an event there. Graph runs do not. */
 int vkhip_program_set_outputs(vkhip_program* program, const vkhip_copy* outputs, size_t n);
+/* Input rebinding (no counterpart in the reference). Points the program's
+ * recorded input span [recorded, recorded + nbytes) at `now` for the plain
+ * runs enqueued after the call: every pointer field of the recorded calls
+ * (node tensors, SGD parameters, copies) that lay inside the span when it was
+ * first bound is moved to the same offset from `now`; now == recorded
+ * restores it. A host then feeds a step from a batch already in device
+ * memory (a resident data set, a staging buffer a DMA filled) without copying
+ * it into the recorded input; the bytes at `now` must stay unchanged until
+ * the runs that read them have finished. VKHIP_ERR_INVALID once the program
+ * has a captured graph, for a span a recorded call writes, or for a span
+ * overlapping another bound span. */
+int vkhip_program_bind_input(vkhip_program* program, const void* recorded, const void* now, size_t nbytes);
 /* Waits for the latest plain run's outputs (not for the rest of its step)
  * and copies their bytes, in declaration order, to host_dst (nbytes: their
  * total). VKHIP_ERR_INVALID when no outputs are declared or the latest run

@@ -231,6 +231,41 @@ def test_early_outputs_are_the_step_end_outputs(config):
     step.close()
 
 
+def test_device_inputs_are_read_in_place_and_written_spans_refuse_binding():
+    """A plain replay given DeviceArray inputs points its recorded inputs at
+    them (vkhip_program_bind_input) instead of copying them in: the losses and
+    parameters are those of host uploads, the recorded input tensors keep the
+    recording's batch, a later host upload rebinds the recorded inputs, and a
+    span a recorded call writes (the loss output) refuses a binding."""
+    import ctypes
+
+    from vkml_amd import _lib
+    from vkml_amd.device import DeviceArray
+
+    dev = T.default_backend()
+    make, _, _, _, lr = CONFIGS["mlp"]
+    batches = _batches("mlp", 6)
+    runs = []
+    for feed in ("host", "device"):
+        model = make(dev)
+        opt = optim.SGD(model.parameters(), lr=lr, momentum=0.9)
+        step = T.CapturedStep(_step_fn(model, opt), *batches[0])
+        losses = [np.float32(step.first[0])]
+        for i, (x, y) in enumerate(batches[1:]):
+            if feed == "device" and i != 2:  # call 3 uploads from the host between device calls
+                x, y = DeviceArray.from_numpy(x), DeviceArray.from_numpy(y)
+            losses.append(np.float32(step(x, y)[0]))
+        if feed == "device":
+            assert step.inputs[0].numpy().tobytes() == batches[3][0].tobytes()  # the last host upload
+            out = step.outputs[0]
+            ptr = out.node.storage.ptr + out.node.offset * out.node.itemsize
+            assert step.lib.vkhip_program_bind_input(step._program, ctypes.c_void_p(ptr), ctypes.c_void_p(ptr),
+                                                     4) == _lib.ERR_INVALID
+        runs.append((np.array(losses, np.float32).tobytes(), [p.numpy().tobytes() for p in model.parameters()]))
+        step.close()
+    assert runs[1] == runs[0]
+
+
 def test_constant_nodes_replay_only_while_nothing_else_writes_them():
     """A recorded constant (FULL) that no other recorded call writes keeps its
     recorded value and is left out of replays; one that another call

@@ -145,6 +145,7 @@ SIGNATURES = {
                                    POINTER(c_int)]),
     "vkhip_program_set_outputs": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vkhip_program_read_outputs": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "vkhip_program_bind_input": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
     "vkhip_program_output_order": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, POINTER(c_size_t),
                                            POINTER(c_size_t)]),
     "vkhip_gemm_plan": (c_int, [c_uint32, c_uint32, c_uint32, c_uint32, c_int32,

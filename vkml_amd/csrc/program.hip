@@ -65,6 +65,18 @@ struct vkhip_program {
     size_t out_after = 0;
     hipEvent_t out_event = nullptr;
     bool out_ready = false;  // the latest run was a plain run that recorded out_event
+    // Input bindings: each recorded pointer field that lies in a bound input
+    // span, with its offset there; vkhip_program_bind_input rewrites them.
+    struct Site {
+        void** slot;
+        uintptr_t offset;
+    };
+    struct Binding {
+        uintptr_t recorded;
+        size_t nbytes;
+        std::vector<Site> sites;
+    };
+    std::vector<Binding> bindings;
 };
 
 namespace vkhip {
@@ -441,6 +453,7 @@ extern "C" int vkhip_program_set_outputs(vkhip_program* p, const vkhip_copy* out
     if (st != VKHIP_OK) return st;
     if (!p || (n && !outputs)) return fail(VKHIP_ERR_INVALID, "program_set_outputs: null argument");
     if (!p->outputs.empty()) return fail(VKHIP_ERR_INVALID, "program_set_outputs: outputs already declared");
+    if (!p->bindings.empty()) return fail(VKHIP_ERR_INVALID, "program_set_outputs: inputs already bound");
     if (p->exec) return fail(VKHIP_ERR_INVALID, "program_set_outputs: the program has a captured graph");
     if (n == 0) return VKHIP_OK;
     constexpr size_t kMaxOutputBytes = 4096;
@@ -518,5 +531,52 @@ extern "C" int vkhip_program_output_order(const vkhip_node* nodes, size_t n, con
     std::vector<size_t> ord;
     *out_after = vkhip::output_order(units, spans, ord);
     for (size_t i = 0; i < n; ++i) order[i] = ord[i];
+    return VKHIP_OK;
+}
+
+extern "C" int vkhip_program_bind_input(vkhip_program* p, const void* recorded, const void* now, size_t nbytes) {
+    if (!p || !recorded || !now || nbytes == 0) return fail(VKHIP_ERR_INVALID, "program_bind_input: null argument");
+    if (p->exec) return fail(VKHIP_ERR_INVALID, "program_bind_input: the program has a captured graph");
+    const uintptr_t r = reinterpret_cast<uintptr_t>(recorded);
+    vkhip_program::Binding* b = nullptr;
+    for (vkhip_program::Binding& x : p->bindings) {
+        if (x.recorded == r && x.nbytes == nbytes) b = &x;
+        else if (x.recorded < r + nbytes && r < x.recorded + x.nbytes)
+            return fail(VKHIP_ERR_INVALID, "program_bind_input: span overlaps another bound input");
+    }
+    if (!b) {
+        // First binding of this span: find every pointer field inside it.
+        // A span some recorded call writes is not an input: refused.
+        vkhip_program::Binding nb;
+        nb.recorded = r;
+        nb.nbytes = nbytes;
+        bool written = false;
+        auto note = [&](void** slot, bool write) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(*slot);
+            if (a < r || a >= r + nbytes) return;
+            nb.sites.push_back({slot, a - r});
+            written = written || write;
+        };
+        for (vkhip_program::Call& c : p->calls) {
+            for (vkhip_node& nd : c.nodes) {
+                note(&nd.out.data, true);
+                for (int i = 0; i < nd.n_src && i < 3; ++i) note(&nd.src[i].data, false);
+            }
+            for (vkhip_sgd_param& sp : c.sgd) {
+                note(reinterpret_cast<void**>(&sp.param), true);
+                note(reinterpret_cast<void**>(const_cast<float**>(&sp.grad)), false);
+                note(reinterpret_cast<void**>(&sp.velocity), true);
+            }
+            for (vkhip_copy& cp : c.copies) {
+                note(&cp.dst, true);
+                note(const_cast<void**>(&cp.src), false);
+            }
+        }
+        if (written) return fail(VKHIP_ERR_INVALID, "program_bind_input: a recorded call writes the span");
+        p->bindings.push_back(std::move(nb));
+        b = &p->bindings.back();
+    }
+    const uintptr_t base = reinterpret_cast<uintptr_t>(now);
+    for (const vkhip_program::Site& site : b->sites) *site.slot = reinterpret_cast<void*>(base + site.offset);
     return VKHIP_OK;
 }

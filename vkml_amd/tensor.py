@@ -1161,8 +1161,14 @@ class CapturedStep:
         batch i + 1 overlap step i on the device, and copied on the device into
         the recorded inputs right behind this step: the next call given those
         same array objects replays at once (any other arrays are uploaded over
-        them, as usual). The host bytes are copied when this call returns, so
-        a later change to the arrays is not seen."""
+        them, as usual). The host bytes are
+        copied when this call returns, so a later change to the arrays is not
+        seen.
+
+        A plain replay (graph=False) also reads a DeviceArray input in place
+        (vkhip_program_bind_input points the recorded input at it): its bytes
+        must stay unchanged until the step has run, and the recorded input
+        tensor then no longer holds the latest batch."""
         if self._program is None:
             raise RuntimeError("CapturedStep: closed")
         if not read:
@@ -1182,18 +1188,20 @@ class CapturedStep:
         if staged is not None and len(staged) == len(arrays) and all(a is b for a, b in zip(arrays, staged)):
             arrays = ()  # prefetched: already copied into the inputs, stream-ordered
         device_copies = []
-        for t, a in zip(self.inputs, arrays):
+        for i, (t, a) in enumerate(zip(self.inputs, arrays)):
+            rec = t.node.storage.ptr + t.node.offset * t.node.itemsize
             if isinstance(a, DeviceArray):
                 if a.shape != t.shape or a.dtype != t.dtype or not a.is_contiguous():
                     raise ValueError(f"CapturedStep: device input {a.shape} {a.dtype} (contiguous: "
                                      f"{a.is_contiguous()}), recorded {t.shape} {t.dtype}")
-                dst = t.node.storage.ptr + t.node.offset * t.node.itemsize
-                device_copies.append(_lib.Copy(dst, a.ptr, a.nbytes_dense()))
+                if not self._bind(i, a.ptr):  # read in place, or copied into the recorded input
+                    device_copies.append(_lib.Copy(rec, a.ptr, a.nbytes_dense()))
                 continue
             a = np.asarray(a)
             if a.shape != t.shape or a.dtype != t.dtype:
                 raise ValueError(f"CapturedStep: input {a.shape} {a.dtype}, recorded {t.shape} {t.dtype}")
             host = a.view(np.uint8) if a.dtype == np.bool_ else a
+            self._bind(i, rec)
             self.backend.upload(t.node.storage, t.node.offset * t.node.itemsize, host)
         if device_copies:
             _lib.check(self.lib.vkhip_copy_device_to_device(
@@ -1221,6 +1229,37 @@ class CapturedStep:
         self._events[self._queued % self.queue_depth].record()
         self._queued += 1
         return None
+
+    def _binding_state(self) -> None:
+        if not hasattr(self, "_bound"):  # every input at its recorded address, rebindable unless a graph
+            self._bound = [t.node.storage.ptr + t.node.offset * t.node.itemsize for t in self.inputs]
+            self._bindable = [not self.graph] * len(self.inputs)
+
+    def _bind(self, i: int, ptr: int) -> bool:
+        """Points recorded input i at device address `ptr` for the plain runs
+        that follow (vkhip_program_bind_input); False where the program cannot
+        be rebound (a graph, or a recorded call writes the input), the caller
+        then copies into the recorded input (which this leaves bound)."""
+        t = self.inputs[i]
+        self._binding_state()
+        if not self._bindable[i]:
+            return False
+        if self._bound[i] == ptr:
+            return True
+        rec = t.node.storage.ptr + t.node.offset * t.node.itemsize
+        code = self.lib.vkhip_program_bind_input(self._program, ctypes.c_void_p(rec), ctypes.c_void_p(ptr),
+                                                 t.numel() * t.node.itemsize)
+        if code == _lib.ERR_INVALID:
+            self._bindable[i] = False
+            if self._bound[i] != rec:
+                _lib.check(self.lib.vkhip_program_bind_input(self._program, ctypes.c_void_p(rec),
+                                                             ctypes.c_void_p(rec), t.numel() * t.node.itemsize),
+                           "program_bind_input")
+                self._bound[i] = rec
+            return False
+        _lib.check(code, "program_bind_input")
+        self._bound[i] = ptr
+        return True
 
     def prefetch(self, *arrays) -> None:
         """Uploads host `arrays` (the next call's inputs) into one of two
@@ -1256,10 +1295,16 @@ class CapturedStep:
         # Behind the work queued so far (this step's replay included), the
         # stream waits for the DMAs and copies the staged batch into the
         # recorded inputs; the staging set is free again after that copy.
+        # (Reading the staging set in place instead, its inputs rebound to it,
+        # measured slower for config 5's replay, 0.348 against 0.341-0.345
+        # ms/step: the first convolution then reads the batch cold.)
         _lib.check(self.lib.vkhip_stream_wait_event(ctypes.c_void_p(self._stage_ready[k].handle)),
                    "stream_wait_event")
+        self._binding_state()
         copies = [_lib.Copy(t.node.storage.ptr + t.node.offset * t.node.itemsize, buf.ptr, buf.nbytes_dense())
                   for t, buf in zip(self.inputs, self._stage_bufs[k])]
+        for i, t in enumerate(self.inputs):
+            self._bind(i, t.node.storage.ptr + t.node.offset * t.node.itemsize)
         _lib.check(self.lib.vkhip_copy_device_to_device((_lib.Copy * len(copies))(*copies), len(copies)),
                    "copy_device_to_device")
         self._stage_free[k].record()
