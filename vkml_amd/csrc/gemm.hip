@@ -2890,12 +2890,14 @@ static int gemm_core(const float* a, const vkhip_operand& ad, const float* b, co
         const dim3 grid = dgrid;
         // Four K-tiles per stage when the grid is one round of one workgroup
         // per CU (its 128 KB of LDS allow no second); one K-tile per stage
-        // otherwise, where two workgroups per CU hide each other's waits. A
-        // short chunk (2-7 K-tiles: a Linear layer's gradients at batch 128)
-        // then loads in one or two stages instead of one load latency per
-        // K-tile.
+        // otherwise, where two workgroups per CU hide each other's waits. With
+        // A straight to LDS (NN), a short chunk (2-7 K-tiles: a Linear layer's
+        // input gradient at batch 128) loads in one or two stages as well
+        // (config 5's fc2 input gradient 13.0 -> 12.4 us); with A transposed
+        // the four-tile stage made the fc2 weight gradient slower (5.9 -> 8.5).
         const uint64_t cus = ctx().ready ? static_cast<uint64_t>(ctx().caps.compute_units) : 256u;
-        const bool staged = static_cast<uint64_t>(grid.x) * grid.y * grid.z <= cus && chunk >= 2;
+        const bool staged = static_cast<uint64_t>(grid.x) * grid.y * grid.z <= cus &&
+                            (chunk >= 8 || (chunk >= 2 && amode == KCD));
         void (*kern)(GemmArgs) = amode == KCD ? (staged ? gemm_direct64_kernel<false, 4> : gemm_direct64_kernel<false, 1>)
                                               : (staged ? gemm_direct64_kernel<true, 4> : gemm_direct64_kernel<true, 1>);
         hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx().stream, g);
