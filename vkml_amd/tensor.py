@@ -1230,6 +1230,10 @@ class CapturedStep:
         self._queued += 1
         return None
 
+    def _recorded_ptr(self, i: int) -> int:
+        t = self.inputs[i]
+        return t.node.storage.ptr + t.node.offset * t.node.itemsize
+
     def _binding_state(self) -> None:
         if not hasattr(self, "_bound"):  # every input at its recorded address, rebindable unless a graph
             self._bound = [t.node.storage.ptr + t.node.offset * t.node.itemsize for t in self.inputs]
@@ -1281,32 +1285,38 @@ class CapturedStep:
             self._stage_ready = [Event(), Event()]
             self._stage_free = [Event().record(), Event().record()]
             self._stage_next = 0
+            # per staging set, built once: its buffers' addresses, its events'
+            # handles and the device copies into the recorded inputs
+            self._stage_args = []
+            for k in range(2):
+                copies = [_lib.Copy(t.node.storage.ptr + t.node.offset * t.node.itemsize, buf.ptr, buf.nbytes_dense())
+                          for t, buf in zip(self.inputs, self._stage_bufs[k])]
+                self._stage_args.append(([ctypes.c_void_p(buf.ptr) for buf in self._stage_bufs[k]],
+                                         ctypes.c_void_p(self._stage_free[k].handle),
+                                         ctypes.c_void_p(self._stage_ready[k].handle),
+                                         (_lib.Copy * len(copies))(*copies), len(copies)))
         k = self._stage_next
         self._stage_next ^= 1
-        for t, a, buf in zip(self.inputs, arrays, self._stage_bufs[k]):
+        dsts, free, ready, copies, ncopies = self._stage_args[k]
+        for t, a, dst in zip(self.inputs, arrays, dsts):
             a = np.ascontiguousarray(a)
             if a.shape != t.shape or a.dtype != t.dtype:
                 raise ValueError(f"CapturedStep: prefetch {a.shape} {a.dtype}, recorded {t.shape} {t.dtype}")
             host = a.view(np.uint8) if a.dtype == np.bool_ else a
-            _lib.check(self.lib.vkhip_copy_from_host_async(
-                ctypes.c_void_p(buf.ptr), host.ctypes.data_as(ctypes.c_void_p), host.nbytes,
-                ctypes.c_void_p(self._stage_free[k].handle), ctypes.c_void_p(self._stage_ready[k].handle)),
-                "copy_from_host_async")
+            _lib.check(self.lib.vkhip_copy_from_host_async(dst, ctypes.c_void_p(host.ctypes.data), host.nbytes,
+                                                           free, ready), "copy_from_host_async")
         # Behind the work queued so far (this step's replay included), the
         # stream waits for the DMAs and copies the staged batch into the
         # recorded inputs; the staging set is free again after that copy.
         # (Reading the staging set in place instead, its inputs rebound to it,
         # measured slower for config 5's replay, 0.348 against 0.341-0.345
         # ms/step: the first convolution then reads the batch cold.)
-        _lib.check(self.lib.vkhip_stream_wait_event(ctypes.c_void_p(self._stage_ready[k].handle)),
-                   "stream_wait_event")
+        _lib.check(self.lib.vkhip_stream_wait_event(ready), "stream_wait_event")
         self._binding_state()
-        copies = [_lib.Copy(t.node.storage.ptr + t.node.offset * t.node.itemsize, buf.ptr, buf.nbytes_dense())
-                  for t, buf in zip(self.inputs, self._stage_bufs[k])]
         for i, t in enumerate(self.inputs):
-            self._bind(i, t.node.storage.ptr + t.node.offset * t.node.itemsize)
-        _lib.check(self.lib.vkhip_copy_device_to_device((_lib.Copy * len(copies))(*copies), len(copies)),
-                   "copy_device_to_device")
+            if self._bound[i] != self._recorded_ptr(i):
+                self._bind(i, self._recorded_ptr(i))
+        _lib.check(self.lib.vkhip_copy_device_to_device(copies, ncopies), "copy_device_to_device")
         self._stage_free[k].record()
         self._staged = arrays
 
